@@ -1,0 +1,222 @@
+/* sc_handoff.h - the C-ABI of the MI355X prefill->decode cache handoff.
+ *
+ * One shared library, libsc_handoff.so, built for gfx950.  Every entry point is `extern "C"`, takes plain
+ * pointers and sizes, returns an int status (SC_OK == 0) and never lets a C++ exception cross the ABI; the
+ * message of the last failure on the calling thread is `sc_last_error()`.
+ *
+ * Status classes follow the reference's restore contract (include/strata/core/conversation_snapshot.hpp:103-108):
+ *   SC_EINVAL  the request was refused BEFORE any device work was enqueued; nothing was written
+ *              (the reference's `ConversationRestore::invalid`, conversation_state.cpp:474);
+ *   SC_EHIP    a HIP call failed after work may have been enqueued: destination state is undefined
+ *              (the reference's `transfer_failed`, conversation_state.cpp:478-504; fatal to that slot).
+ *
+ * Layouts (all device memory unless a name says host):
+ *   prefill K/V   [T][n_head_kv][head_dim]         f16 (or f32, rounded RNE to f16 as kv_append does)
+ *   prefill rec   [HV][S][S] f32                  head-major recurrent state of one GDN layer
+ *   prefill conv  [rows][C] f32 (row stride ld)   the conv input rows; the history is the last 3 rows
+ *   decode K/V    [page][n_head_kv][page_size][head_dim] f16 through a page table
+ *                 (include/strata/core/layer.hpp:204-205; identity when the table is NULL = kv_mode 0)
+ *   decode GDN    one row per GDN layer: (S, HV, S) f32 recurrence then [C][d_conv-1] f32 history
+ *                 (src/core/session.cpp:156-162, src/kernels/cuda/gdn.cu:75)
+ *   image         the park image / transfer buffer: the blobs of a SavedConversation in the wire codec's
+ *                 blob-pool order, each 64-byte aligned (src/core/conversation_wire.cpp:400-437):
+ *                 for each QSA layer K then V (the first ceil(T/page_size)*page_size cells, as
+ *                 conversation_kv_save copies them, src/core/conversation_snapshot.cpp:40-49,157-171),
+ *                 then the GDN rows (conversation_checkpoint_save, src/core/conversation_state.cpp:233-235).
+ */
+#ifndef SC_HANDOFF_H
+#define SC_HANDOFF_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    SC_OK = 0,
+    SC_EINVAL = 1,   /* refused before any write */
+    SC_EHIP = 2,     /* HIP failure after work may have been enqueued (transfer_failed) */
+    SC_ENOMEM = 3,   /* an allocation the call needed failed; nothing was written */
+    SC_ERANGE = 4    /* a size is beyond what the entry point supports; nothing was written */
+};
+
+enum { SC_DTYPE_F16 = 0, SC_DTYPE_F32 = 1 };
+
+/* Blob kinds of the image (one row each in the image layout). */
+enum { SC_BLOB_K = 1, SC_BLOB_V = 2, SC_BLOB_GDN = 3 };
+
+/* The subset of strata::core::ModelGeometry (include/strata/core/layout.hpp:27-59) the path depends on, plus
+ * the page granule of strata::kernels::QsaShapes (include/strata/kernels/qsa.hpp:113, page_size = 4). */
+typedef struct sc_geometry {
+    int64_t n_layers;          /* layout.hpp:29 */
+    int64_t qsa_interval;      /* layout.hpp:30: layer % qsa_interval == qsa_interval - 1 is full attention */
+    int64_t n_head_kv;         /* layout.hpp:42 */
+    int64_t head_dim;          /* layout.hpp:43; a multiple of 8 (16-byte rows) */
+    int64_t page_size;         /* qsa.hpp:113 */
+    int64_t ssm_state_size;    /* S, layout.hpp:33 */
+    int64_t ssm_k_heads;       /* layout.hpp:34 */
+    int64_t ssm_v_heads;       /* HV, layout.hpp:35 */
+    int64_t ssm_d_conv;        /* layout.hpp:36: the history keeps d_conv - 1 = 3 rows */
+    int64_t ssm_conv_channels; /* C, layout.hpp:37 */
+    int64_t idx_key_dim;       /* layout.hpp:45 */
+} sc_geometry;
+
+/* The carve source: one prefilled sequence (or one appended chunk of it) in the prefill layout.
+ * The pointer arrays are HOST arrays of DEVICE pointers, one entry per QSA / GDN layer in layer order. */
+typedef struct sc_prefill_view {
+    int64_t tokens;               /* T: prefill token t lands in decode cell pos0 + t */
+    int64_t pos0;                 /* first decode cell written (kv_append's pos0, src/prefill/kernels.cu:570-573) */
+    int32_t kv_dtype;             /* SC_DTYPE_F16 (a pure permutation) or SC_DTYPE_F32 (RNE to f16) */
+    int32_t with_gdn;             /* 0: K/V only (an appended chunk); 1: carve the GDN state too */
+    const void* const* k;         /* [n_qsa] -> [T][n_head_kv][head_dim] */
+    const void* const* v;         /* [n_qsa] */
+    const float* const* rec;      /* [n_gdn] -> [HV][S][S] */
+    const float* const* conv;     /* [n_gdn] -> [conv_rows][C] conv input rows (row stride conv_ld floats) */
+    int64_t conv_rows;            /* rows in each conv source; fewer than 3 keeps older history rows
+                                     (gdn_conv_hist_kernel, src/prefill/kernels.cu:219-228) */
+    int64_t conv_ld;              /* row stride of the conv source in floats (>= C) */
+} sc_prefill_view;
+
+/* The decode slot: the device pointers of a strata::core::SessionState's state for one sequence
+ * (include/strata/core/session.hpp:30-60 and QsaState, include/strata/core/layer.hpp:203-225). */
+typedef struct sc_decode_slot {
+    int64_t n_pages;                    /* physical pages in each K/V pool */
+    int64_t max_cells;                  /* logical capacity in cells (n_pages * page_size for identity) */
+    uint16_t* const* k_pool;            /* [n_qsa] -> [n_pages][n_head_kv][page_size][head_dim] f16 */
+    uint16_t* const* v_pool;            /* [n_qsa] */
+    const int32_t* const* page_table;   /* NULL, or [n_qsa] device tables logical page -> physical page;
+                                           a NULL entry is the identity table (kv_mode 0) */
+    float* gdn_state;                   /* n_gdn rows of sc_gdn_row_floats() floats (session.hpp:34) */
+} sc_decode_slot;
+
+/* One row of an image layout. */
+typedef struct sc_image_blob {
+    int32_t kind;     /* SC_BLOB_K, SC_BLOB_V, SC_BLOB_GDN */
+    int32_t layer;    /* QSA ordinal for K/V, -1 for the GDN blob */
+    uint64_t offset;  /* from the image start, a multiple of 64 */
+    uint64_t bytes;
+} sc_image_blob;
+
+typedef struct sc_plan sc_plan;   /* a device-resident handoff table plus its launch shape */
+
+/* ---- errors ---------------------------------------------------------------------------------------------- */
+
+/* The message of the last failure on this thread ("" after a success).  Messages of refusals carry the
+ * reference's prefix "conversation snapshot: " where the reference has the same refusal
+ * (src/core/conversation_state.cpp:21-24). */
+const char* sc_last_error(void);
+/* Library version, e.g. "sc_handoff 0.1 gfx950". */
+const char* sc_version(void);
+
+/* ---- geometry and layout arithmetic (host only, no HIP call) ----------------------------------------------- */
+
+/* QSA and GDN layer counts: n_layers / qsa_interval and the rest (layout.hpp:57-58). */
+int64_t sc_n_qsa_layers(const sc_geometry* g);
+int64_t sc_n_gdn_layers(const sc_geometry* g);
+/* Floats of one GDN row: S*HV*S + C*(d_conv-1) (conversation_state.cpp:186-189, session.cpp:160-161). */
+int64_t sc_gdn_row_floats(const sc_geometry* g);
+/* Cells a park copies for `tokens`: ceil(tokens/page_size)*page_size (conversation_snapshot.cpp:40). */
+int64_t sc_kv_cells(const sc_geometry* g, int64_t tokens);
+/* Payload bytes of one handoff of `tokens` tokens: K+V of every QSA layer over sc_kv_cells() cells plus every
+ * GDN row.  The figure behind the bench's GB/s. */
+uint64_t sc_payload_bytes(const sc_geometry* g, int64_t tokens);
+/* The image layout for `tokens`.  With blobs == NULL only *n_blobs and *total_bytes are written.
+ * Replaces the byte accounting of conversation_kv_bytes / conversation_snapshot_bytes
+ * (include/strata/core/conversation_snapshot.hpp:13,87-88) for the K/V + GDN payload. */
+int sc_image_layout(const sc_geometry* g, int64_t tokens, sc_image_blob* blobs, int64_t* n_blobs,
+                    uint64_t* total_bytes);
+
+/* ---- plans: the device-resident handoff table ---------------------------------------------------------------- */
+
+/* Fused carve -> scatter: prefill layout straight into the decode slot, one launch for every layer.
+ * Replaces kv_append (include/strata/prefill/kernels.hpp:81-83, src/prefill/kernels.cu:560-625) and
+ * gdn_conv_hist (src/prefill/kernels.cu:219-228) as the writers of the decode layout, plus the GDN row
+ * placement of src/prefill/prefill.cpp:1282-1283.  Validates extents against the slot first. */
+int sc_plan_carve(const sc_geometry* g, const sc_prefill_view* src, const sc_decode_slot* dst, sc_plan** out);
+/* Pass 1 of the two-pass handoff: carve into a transfer buffer laid out as the image for src->tokens
+ * (pos0 must be 0).  The transfer buffer is what a park writes and what crosses to another instance. */
+int sc_plan_gather(const sc_geometry* g, const sc_prefill_view* src, void* image, uint64_t image_bytes,
+                   sc_plan** out);
+/* Pass 2: an image of `tokens` tokens into a decode slot through its page tables.  With identity tables it
+ * is the device-side twin of conversation_kv_restore + conversation_checkpoint_restore's GDN copy
+ * (conversation_snapshot.cpp:196-204, conversation_state.cpp:251), and of kv_stage_from_host
+ * (src/kernels/cuda/kv_stream.cu:244-252) for paged pools. */
+int sc_plan_scatter(const sc_geometry* g, const void* image, uint64_t image_bytes, int64_t tokens,
+                    const sc_decode_slot* dst, sc_plan** out);
+/* The inverse: a decode slot's first sc_kv_cells(tokens) cells and its GDN rows into an image, through the
+ * page tables.  The device half of conversation_kv_save (conversation_snapshot.cpp:139-173) for paged pools. */
+int sc_plan_capture(const sc_geometry* g, const sc_decode_slot* src, int64_t tokens, void* image,
+                    uint64_t image_bytes, sc_plan** out);
+/* Enqueue the plan on `stream` (a hipStream_t; NULL is the null stream).  Asynchronous. */
+int sc_plan_launch(const sc_plan* plan, void* stream);
+/* Algorithmic payload bytes the plan moves (each read once and written once). */
+uint64_t sc_plan_payload_bytes(const sc_plan* plan);
+/* Workgroups the launch uses (0 = the library's default); for launch-shape sweeps. */
+int sc_plan_set_grid(sc_plan* plan, int64_t workgroups);
+/* Frees the device table.  The caller must not destroy a plan whose launch has not completed. */
+int sc_plan_destroy(sc_plan* plan);
+
+/* ---- park / resume: slot <-> pinned host image ----------------------------------------------------------------- */
+
+/* Park: copy a decode slot (identity page tables) into a pinned host image of sc_image_layout(tokens), with
+ * hipMemcpyAsync on `stream`, one copy per blob; records `done` (a hipEvent_t, may be NULL) after the last.
+ * Replaces conversation_kv_save's synchronous per-16-MiB cudaMemcpy loop (conversation_snapshot.cpp:105-113,
+ * 160-171) and conversation_checkpoint_save's GDN copy (conversation_state.cpp:235). */
+int sc_park_async(const sc_geometry* g, const sc_decode_slot* slot, int64_t tokens, void* host_image,
+                  uint64_t image_bytes, void* stream, void* done);
+/* Resume: the inverse, H2D.  Replaces conversation_kv_restore (conversation_snapshot.cpp:196-204) and
+ * conversation_checkpoint_restore's GDN copy (conversation_state.cpp:251). */
+int sc_resume_async(const sc_geometry* g, const void* host_image, uint64_t image_bytes, int64_t tokens,
+                    const sc_decode_slot* slot, void* stream, void* done);
+
+/* ---- runtime plumbing the C++ host layer calls instead of HIP ---------------------------------------------------- */
+
+int sc_device_alloc(void** ptr, uint64_t bytes);
+int sc_device_free(void* ptr);
+/* Pinned host memory (hipHostMalloc): the park pool. */
+int sc_host_alloc(void** ptr, uint64_t bytes);
+int sc_host_free(void* ptr);
+/* hipMemcpyAsync(hipMemcpyDefault) on `stream`. */
+int sc_copy_async(void* dst, const void* src, uint64_t bytes, void* stream);
+/* A device-side fill of `bytes` bytes with `value` by a small kernel (never a memset node). */
+int sc_fill_bytes_async(void* dst, uint8_t value, uint64_t bytes, void* stream);
+int sc_stream_create(void** stream);     /* non-blocking, default priority */
+int sc_stream_destroy(void* stream);
+int sc_stream_sync(void* stream);
+int sc_device_sync(void);
+int sc_event_create(void** event);
+int sc_event_destroy(void* event);
+int sc_event_record(void* event, void* stream);
+int sc_event_sync(void* event);
+int sc_event_elapsed_ms(void* start, void* end, float* ms);
+/* The stream waits for the event (hipStreamWaitEvent). */
+int sc_stream_wait_event(void* stream, void* event);
+
+/* Host-link probe: pinned `bytes` x `iters` hipMemcpyAsync per direction, after one warm-up copy; the method of
+ * probe_pcie_h2d_gbps (src/program/generate.cpp:1133-1161) applied to both directions. */
+int sc_probe_link(uint64_t bytes, int iters, double* h2d_gbps, double* d2h_gbps);
+
+/* ---- synthetic inputs (bench and tests; not on the handoff path) ---------------------------------------------- */
+
+/* Counter-based fills, bit-identical to the host generator of the test oracle:
+ *   element i of stream s under seed: u64 = mix(seed, s, i) (SplitMix64 finaliser, see the source);
+ *   uniform f16:  u = (u64 >> 40) * 2^-24;  x = lo + (hi - lo) * u  in f32, then RNE to f16;
+ *   normal f32:   (sum of twelve 24-bit uniforms) - 6, an Irwin-Hall(12) value with mean 0 and variance 1,
+ *                 formed in integers so host and device produce the same bits. */
+int sc_fill_uniform_f16(uint16_t* dst, uint64_t n, float lo, float hi, uint64_t seed, uint64_t stream_id,
+                        void* stream);
+int sc_fill_uniform_f32(float* dst, uint64_t n, float lo, float hi, uint64_t seed, uint64_t stream_id,
+                        void* stream);
+int sc_fill_normal_f32(float* dst, uint64_t n, uint64_t seed, uint64_t stream_id, void* stream);
+
+/* A synthetic decode step for overlap measurements: every workgroup reads its share of `n_bytes` bytes of K/V
+ * at `kv` and folds them into one u32 per workgroup in `sink` (so the reads cannot be elided).  It stands in
+ * for the attention reading the slot that keeps decoding while others park or resume. */
+int sc_decode_probe(const void* kv, uint64_t n_bytes, uint32_t* sink, int64_t workgroups, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SC_HANDOFF_H */

@@ -1,0 +1,312 @@
+/* sc_oracle.c - CPU restatement of the reference's prefill->decode cache handoff.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg load this
+ * library, and only as the checker or the timed CPU baseline.  The product (libsc_handoff.so) never links,
+ * loads or calls it, and has no CPU fallback.
+ *
+ * Every function names the reference code it restates.  Pinning (what each one is checked against, so that a
+ * dropped term, a wrong index or a transposed operand fails a test):
+ *   sco_f16_bits            the reference's numpy-generated f32->f16 vectors (src/kernels/qsa_oracle_vectors.inc,
+ *                           committed as tests/golden/f16_oracle_vectors.json) and numpy astype(float16)
+ *   sco_kv_append           numpy reshape/transpose of [T][H][D] into [page][H][ps][D] and the two rival layouts of
+ *                           src/kernels/qsa_parity.cpp:489-497, which must differ
+ *   sco_rec_carve           numpy transpose(1, 0, 2) and the fused_gdn.cu:31-33 index form
+ *   sco_conv_hist           numpy qkv[T-3:T].T, and the T < 3 cases against an explicit history shift
+ *   sco_image_layout        the published payload totals (59 899 904 / 884 342 784 / 3 300 261 888 bytes)
+ *                           and the closed forms cells = ceil(T/4)*4, data = cells*H*D*2
+ *   sco_park / sco_resume   A/B/A round trips and byte accounting
+ *   sco_fnv1a64             textbook FNV-1a 64 vectors with the standard basis; the reference's seed on empty input
+ *   sco_fill_*              the device generators of libsc_handoff.so, bit for bit (GPU tests), and moments
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* Same field order as sc_geometry (include/sc_handoff.h) and strata::core::ModelGeometry's subset. */
+typedef struct sco_geometry {
+    int64_t n_layers, qsa_interval, n_head_kv, head_dim, page_size;
+    int64_t ssm_state_size, ssm_k_heads, ssm_v_heads, ssm_d_conv, ssm_conv_channels, idx_key_dim;
+} sco_geometry;
+
+/* ---- synthetic inputs ----------------------------------------------------------------------------------------- */
+
+uint64_t sco_mix64(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+uint64_t sco_synth_key(uint64_t seed, uint64_t sid) { return sco_mix64(seed ^ sco_mix64(sid + 0x9E3779B97F4A7C15ull)); }
+
+static uint64_t draw(uint64_t key, uint64_t i) { return sco_mix64(key + (i + 1) * 0x9E3779B97F4A7C15ull); }
+
+/* ---- f32 -> f16 ------------------------------------------------------------------------------------------------ */
+
+/* Round to nearest even, from the IEEE-754 binary16 definition.  NaN -> sign|0x7C00|0x200 and finite overflow ->
+ * infinity, the conventions of include/strata/kernels/f16_bits.hpp:37-70 (the reference's decode-side
+ * converter).  Written as exact rational rounding on the mantissa as an integer: the value is m * 2^(e-23);
+ * the f16 result keeps floor(m / 2^k) with k = 13 for normals and k = 14 - e16 in the subnormal range. */
+uint16_t sco_f16_bits(uint32_t x) {
+    const uint32_t sign = (x >> 16) & 0x8000u;
+    const int e8 = (int) ((x >> 23) & 0xFFu);
+    uint32_t m = x & 0x7FFFFFu;
+    if (e8 == 0xFF) return (uint16_t) (sign | 0x7C00u | (m ? 0x200u : 0u));
+    if (e8 == 0) return (uint16_t) sign;             /* f32 subnormals are far below the f16 range: +-0 */
+    m |= 0x800000u;                                   /* value = m * 2^(e8 - 150) */
+    const int e16 = e8 - 127 + 15;                    /* biased f16 exponent if normal */
+    int k = e16 >= 1 ? 13 : 14 - e16;                 /* mantissa bits dropped */
+    if (k > 24) return (uint16_t) sign;               /* below half the smallest subnormal */
+    uint32_t q = m >> k;
+    const uint32_t rem = m - (q << k), half = 1u << (k - 1);
+    if (rem > half || (rem == half && (q & 1u))) ++q;
+    /* q counts units of the last place: 2^(e16-25) for normals (with the implicit bit at 2^10), 2^-24 below */
+    uint32_t bits;
+    if (e16 >= 1) {
+        uint32_t e = (uint32_t) e16;
+        if (q == 0x800u) { q = 0x400u; ++e; }        /* rounding carried into the next binade */
+        if (e >= 31) return (uint16_t) (sign | 0x7C00u);
+        bits = (e << 10) | (q & 0x3FFu);
+    } else {
+        bits = q;                                     /* q == 0x400 is the smallest normal, encoded the same way */
+    }
+    return (uint16_t) (sign | bits);
+}
+
+void sco_f16_from_f32(const float* src, uint16_t* dst, uint64_t n) {
+    for (uint64_t i = 0; i < n; ++i) {
+        uint32_t x;
+        memcpy(&x, &src[i], 4);
+        dst[i] = sco_f16_bits(x);
+    }
+}
+
+void sco_fill_uniform_f32(float* dst, uint64_t n, float lo, float hi, uint64_t seed, uint64_t sid) {
+    const uint64_t key = sco_synth_key(seed, sid);
+    const float span = hi - lo;
+    for (uint64_t i = 0; i < n; ++i) {
+        const float u = (float) (uint32_t) (draw(key, i) >> 40) * 0x1p-24f;
+        dst[i] = fmaf(span, u, lo);
+    }
+}
+
+void sco_fill_uniform_f16(uint16_t* dst, uint64_t n, float lo, float hi, uint64_t seed, uint64_t sid) {
+    const uint64_t key = sco_synth_key(seed, sid);
+    const float span = hi - lo;
+    for (uint64_t i = 0; i < n; ++i) {
+        const float u = (float) (uint32_t) (draw(key, i) >> 40) * 0x1p-24f;
+        const float x = fmaf(span, u, lo);
+        uint32_t b;
+        memcpy(&b, &x, 4);
+        dst[i] = sco_f16_bits(b);
+    }
+}
+
+/* Irwin-Hall(12) - 6: mean 0, variance 1, formed in integers so every platform gets the same bits. */
+void sco_fill_normal_f32(float* dst, uint64_t n, uint64_t seed, uint64_t sid) {
+    const uint64_t key = sco_synth_key(seed, sid);
+    for (uint64_t i = 0; i < n; ++i) {
+        int64_t sum = 0;
+        for (int k = 0; k < 6; ++k) {
+            const uint64_t x = draw(key, i * 6 + (uint64_t) k);
+            sum += (int64_t) (x >> 40) + (int64_t) ((x >> 16) & 0xFFFFFFull);
+        }
+        dst[i] = (float) (int32_t) (sum - ((int64_t) 6 << 24)) * 0x1p-24f;
+    }
+}
+
+/* ---- the carve -------------------------------------------------------------------------------------------------- */
+
+/* kv_append (src/prefill/kernels.cu:560-601, launched at :618-625): token t of kv head h, element d, goes to cell
+ * pos = pos0 + t at pool[((table[pos/ps] * H + h) * ps + pos % ps) * D + d]; a page that is not resident
+ * (negative entry) is skipped, as kernels.cu:577 skips it.  `src` is f16 bits (dtype 0) or f32 (dtype 1, rounded
+ * to f16 as kernels.cu:575 rounds it).  Entries at or past n_pages are skipped too (the device never writes past
+ * its pool). */
+void sco_kv_append(const void* src, int dtype, int64_t T, int64_t pos0, const int32_t* table, int64_t n_pages,
+                   int64_t H, int64_t D, int64_t ps, uint16_t* pool) {
+    for (int64_t t = 0; t < T; ++t)
+        for (int64_t h = 0; h < H; ++h) {
+            const int64_t pos = pos0 + t;
+            const int64_t page = table ? (int64_t) table[pos / ps] : pos / ps;
+            if (page < 0 || page >= n_pages) continue;
+            const int64_t row = (page * H + h) * ps + pos % ps;
+            for (int64_t d = 0; d < D; ++d) {
+                const int64_t i = (t * H + h) * D + d;
+                uint16_t v;
+                if (dtype == 0) {
+                    v = ((const uint16_t*) src)[i];
+                } else {
+                    uint32_t b;
+                    memcpy(&b, (const float*) src + i, 4);
+                    v = sco_f16_bits(b);
+                }
+                pool[row * D + d] = v;
+            }
+        }
+}
+
+/* The recurrence: element (i, h, j) of a head-major [HV][S][S] prefill image goes to i*HV*S + h*S + j, the
+ * (S, HV, S) layout with j fastest that src/kernels/cuda/gdn.cu:75 and fused_gdn.cu:31-33 read and write. */
+void sco_rec_carve(const float* src, int64_t S, int64_t HV, float* dst) {
+    for (int64_t h = 0; h < HV; ++h)
+        for (int64_t i = 0; i < S; ++i)
+            for (int64_t j = 0; j < S; ++j) dst[(i * HV + h) * S + j] = src[(h * S + i) * S + j];
+}
+
+/* gdn_conv_hist_kernel (src/prefill/kernels.cu:219-228): after a chunk of `rows` input rows [rows][C] (row stride
+ * ld), history slot k (of nhist) is input row rows - nhist + k, or - for a chunk shorter than the history - the
+ * previous history's slot k + rows, read before any slot is overwritten.  A fresh sequence's previous history is
+ * zero (session_zero / qsa_state_zero, include/strata/core/session.hpp:104, layer.hpp:306). */
+void sco_conv_hist(float* hist, const float* qkv, int64_t rows, int64_t ld, int64_t C, int64_t nhist, int fresh) {
+    float v[8];
+    for (int64_t c = 0; c < C; ++c) {
+        for (int64_t k = 0; k < nhist; ++k) {
+            const int64_t t = rows - nhist + k;
+            v[k] = t >= 0 ? qkv[t * ld + c] : fresh ? 0.0f : hist[c * nhist + (t + nhist)];
+        }
+        for (int64_t k = 0; k < nhist; ++k) hist[c * nhist + k] = v[k];
+    }
+}
+
+/* ---- the image: a SavedConversation's K/V + GDN payload in blob-pool order ------------------------------------ */
+
+typedef struct sco_blob {
+    int32_t kind, layer;   /* 1 K, 2 V, 3 GDN */
+    uint64_t offset, bytes;
+} sco_blob;
+
+static int64_t n_qsa(const sco_geometry* g) { return g->n_layers / g->qsa_interval; }
+static int64_t n_gdn(const sco_geometry* g) { return g->n_layers - n_qsa(g); }
+int64_t sco_gdn_row_floats(const sco_geometry* g) {
+    return g->ssm_state_size * g->ssm_v_heads * g->ssm_state_size + g->ssm_conv_channels * (g->ssm_d_conv - 1);
+}
+/* conversation_snapshot.cpp:40: the page-granular extent a park copies. */
+int64_t sco_cells(const sco_geometry* g, int64_t tokens) {
+    return (tokens + g->page_size - 1) / g->page_size * g->page_size;
+}
+
+static uint64_t align64(uint64_t x) { return (x + 63) / 64 * 64; }
+
+/* Blob order of the wire codec's pool (src/core/conversation_wire.cpp:400-437): every KV record's buffers in
+ * kv order (k then v; f16 has no scale buffers), then the live checkpoint's gdn buffer; 64-byte aligned.
+ * Sizes: data = cells * n_head_kv * head_dim * 2 (conversation_snapshot.cpp:40-49); gdn = n_gdn rows of
+ * (S*HV*S + C*(d_conv-1)) floats (conversation_state.cpp:186-189). Returns the blob count. */
+int64_t sco_image_layout(const sco_geometry* g, int64_t tokens, sco_blob* out, uint64_t* total) {
+    const uint64_t kv = (uint64_t) sco_cells(g, tokens) * (uint64_t) g->n_head_kv * (uint64_t) g->head_dim * 2;
+    uint64_t at = 0;
+    int64_t n = 0;
+    for (int64_t j = 0; j < n_qsa(g); ++j)
+        for (int kind = 1; kind <= 2; ++kind) {
+            at = align64(at);
+            if (out) { out[n].kind = kind; out[n].layer = (int32_t) j; out[n].offset = at; out[n].bytes = kv; }
+            ++n;
+            at += kv;
+        }
+    if (n_gdn(g) > 0) {
+        const uint64_t bytes = (uint64_t) n_gdn(g) * (uint64_t) sco_gdn_row_floats(g) * 4;
+        at = align64(at);
+        if (out) { out[n].kind = 3; out[n].layer = -1; out[n].offset = at; out[n].bytes = bytes; }
+        ++n;
+        at += bytes;
+    }
+    if (total) *total = align64(at);
+    return n;
+}
+
+/* conversation_kv_save (src/core/conversation_snapshot.cpp:139-173) for identity-layout f16 pools: each buffer's
+ * first `data` bytes, which are the first cells/ps pages; plus conversation_checkpoint_save's gdn copy
+ * (conversation_state.cpp:233-235).  Host pointers; gaps in the image are zeroed. */
+void sco_park(const sco_geometry* g, int64_t tokens, const uint16_t* const* k_pool, const uint16_t* const* v_pool,
+              const float* gdn_state, uint8_t* image) {
+    sco_blob blobs[4096];
+    uint64_t total = 0;
+    const int64_t n = sco_image_layout(g, tokens, blobs, &total);
+    memset(image, 0, total);
+    for (int64_t b = 0; b < n; ++b) {
+        const void* from = blobs[b].kind == 3 ? (const void*) gdn_state
+                         : blobs[b].kind == 1 ? (const void*) k_pool[blobs[b].layer] : (const void*) v_pool[blobs[b].layer];
+        memcpy(image + blobs[b].offset, from, blobs[b].bytes);
+    }
+}
+
+/* conversation_kv_restore (conversation_snapshot.cpp:196-204) + conversation_checkpoint_restore's gdn copy
+ * (conversation_state.cpp:251): the inverse of sco_park. */
+void sco_resume(const sco_geometry* g, int64_t tokens, const uint8_t* image, uint16_t* const* k_pool,
+                uint16_t* const* v_pool, float* gdn_state) {
+    sco_blob blobs[4096];
+    uint64_t total = 0;
+    const int64_t n = sco_image_layout(g, tokens, blobs, &total);
+    for (int64_t b = 0; b < n; ++b) {
+        void* to = blobs[b].kind == 3 ? (void*) gdn_state
+                 : blobs[b].kind == 1 ? (void*) k_pool[blobs[b].layer] : (void*) v_pool[blobs[b].layer];
+        memcpy(to, image + blobs[b].offset, blobs[b].bytes);
+    }
+}
+
+/* ---- FNV-1a 64 ----------------------------------------------------------------------------------------------- */
+
+/* src/core/pinned.cu:594-601: xor the byte, then multiply by the 64-bit FNV prime.  The reference seeds every call
+ * with 1469598103934665603 = 0x14650fb0739d0383 (conversation_snapshot.cpp:225, conversation_wire.hpp:196), not
+ * the textbook basis 0xcbf29ce484222325; callers pass the seed. */
+uint64_t sco_fnv1a64(const uint8_t* p, uint64_t n, uint64_t seed) {
+    uint64_t h = seed;
+    for (uint64_t i = 0; i < n; ++i) {
+        h ^= p[i];
+        h *= 1099511628211ull;
+    }
+    return h;
+}
+
+/* ---- the whole handoff, as the CPU would do it --------------------------------------------------------------- */
+
+/* The fused carve of one sequence into a decode slot (identity or paged pools), host pointers: what
+ * sc_plan_carve computes.  Layer arrays are in QSA / GDN order. */
+void sco_handoff_carve(const sco_geometry* g, int64_t T, int64_t pos0, int dtype, const void* const* k_src,
+                       const void* const* v_src, int with_gdn, const float* const* rec_src,
+                       const float* const* conv_src, int64_t conv_rows, int64_t conv_ld,
+                       uint16_t* const* k_pool, uint16_t* const* v_pool, const int32_t* const* tables,
+                       int64_t n_pages, float* gdn_state) {
+    for (int64_t j = 0; j < n_qsa(g); ++j) {
+        const int32_t* table = tables ? tables[j] : NULL;
+        sco_kv_append(k_src[j], dtype, T, pos0, table, n_pages, g->n_head_kv, g->head_dim, g->page_size, k_pool[j]);
+        sco_kv_append(v_src[j], dtype, T, pos0, table, n_pages, g->n_head_kv, g->head_dim, g->page_size, v_pool[j]);
+    }
+    if (!with_gdn) return;
+    const int64_t row = sco_gdn_row_floats(g), S = g->ssm_state_size, HV = g->ssm_v_heads;
+    for (int64_t i = 0; i < n_gdn(g); ++i) {
+        float* base = gdn_state + i * row;
+        sco_rec_carve(rec_src[i], S, HV, base);
+        sco_conv_hist(base + S * HV * S, conv_src[i], conv_rows, conv_ld, g->ssm_conv_channels, g->ssm_d_conv - 1,
+                      pos0 == 0);
+    }
+}
+
+/* The reference's host-side handoff of an already-parked image, restated as the CPU baseline:
+ *   save    - conversation_kv_save's copy into 16 MiB segments (include/strata/core/conversation_buffer.hpp:18,
+ *             conversation_snapshot.cpp:160-171): one segment buffer per <=16 MiB piece of each blob;
+ *   encode  - the wire codec's blob pool with FNV-1a over every written byte (conversation_wire.cpp:400-480);
+ *   decode  - copy out of the payload into fresh segments and re-check the hash (conversation_wire.cpp:694-754,
+ *             handoff.cpp:1133-1136);
+ *   restore - conversation_kv_restore's copy back into the slot (conversation_snapshot.cpp:196-204).
+ * `slot_src` and `slot_dst` are contiguous images of the slot's payload (as sco_park lays it out); `scratch`
+ * must hold 3 * image bytes.  Returns the payload hash (the caller compares encode and decode hashes through
+ * the return values of two calls, or trusts the internal check: a mismatch returns 0). */
+uint64_t sco_cpu_handoff(const uint8_t* slot_src, uint8_t* slot_dst, uint64_t bytes, uint8_t* scratch) {
+    const uint64_t seg = 16ull << 20;
+    const uint64_t seed = 1469598103934665603ull;
+    uint8_t* saved = scratch;
+    uint8_t* wire = scratch + bytes;
+    uint8_t* decoded = scratch + 2 * bytes;
+    for (uint64_t at = 0; at < bytes; at += seg) memcpy(saved + at, slot_src + at, bytes - at < seg ? bytes - at : seg);
+    uint64_t h_enc = seed;
+    for (uint64_t at = 0; at < bytes; at += seg) {
+        const uint64_t n = bytes - at < seg ? bytes - at : seg;
+        memcpy(wire + at, saved + at, n);
+        h_enc = sco_fnv1a64(wire + at, n, h_enc);
+    }
+    const uint64_t h_dec = sco_fnv1a64(wire, bytes, seed);
+    if (h_dec != h_enc) return 0;
+    for (uint64_t at = 0; at < bytes; at += seg) memcpy(decoded + at, wire + at, bytes - at < seg ? bytes - at : seg);
+    for (uint64_t at = 0; at < bytes; at += seg) memcpy(slot_dst + at, decoded + at, bytes - at < seg ? bytes - at : seg);
+    return h_enc;
+}

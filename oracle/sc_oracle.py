@@ -1,0 +1,220 @@
+"""ctypes binding of the CPU oracle (oracle/sc_oracle.c).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg, as the
+checker or the timed CPU baseline.  The product never imports it.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+import numpy as np
+
+_HERE = Path(__file__).resolve().parent
+_LIB_PATH = _HERE / "liboracle.so"
+if not _LIB_PATH.exists():
+    raise ImportError(f"the oracle is not built ({_LIB_PATH}); run __graft_entry__.build() first")
+lib = C.CDLL(str(_LIB_PATH))
+
+REFERENCE_FNV_SEED = 1469598103934665603   # 0x14650fb0739d0383, every call site of the reference
+TEXTBOOK_FNV_BASIS = 0xCBF29CE484222325
+
+
+class Geometry(C.Structure):
+    _fields_ = [(name, C.c_int64) for name in (
+        "n_layers", "qsa_interval", "n_head_kv", "head_dim", "page_size", "ssm_state_size", "ssm_k_heads",
+        "ssm_v_heads", "ssm_d_conv", "ssm_conv_channels", "idx_key_dim")]
+
+
+class Blob(C.Structure):
+    _fields_ = [("kind", C.c_int32), ("layer", C.c_int32), ("offset", C.c_uint64), ("bytes", C.c_uint64)]
+
+
+_P = C.c_void_p
+_I64, _U64 = C.c_int64, C.c_uint64
+_G = C.POINTER(Geometry)
+for _name, _res, _args in (
+    ("sco_mix64", _U64, [_U64]),
+    ("sco_synth_key", _U64, [_U64, _U64]),
+    ("sco_f16_bits", C.c_uint16, [C.c_uint32]),
+    ("sco_f16_from_f32", None, [_P, _P, _U64]),
+    ("sco_fill_uniform_f32", None, [_P, _U64, C.c_float, C.c_float, _U64, _U64]),
+    ("sco_fill_uniform_f16", None, [_P, _U64, C.c_float, C.c_float, _U64, _U64]),
+    ("sco_fill_normal_f32", None, [_P, _U64, _U64, _U64]),
+    ("sco_kv_append", None, [_P, C.c_int, _I64, _I64, _P, _I64, _I64, _I64, _I64, _P]),
+    ("sco_rec_carve", None, [_P, _I64, _I64, _P]),
+    ("sco_conv_hist", None, [_P, _P, _I64, _I64, _I64, _I64, C.c_int]),
+    ("sco_gdn_row_floats", _I64, [_G]),
+    ("sco_cells", _I64, [_G, _I64]),
+    ("sco_image_layout", _I64, [_G, _I64, C.POINTER(Blob), C.POINTER(_U64)]),
+    ("sco_park", None, [_G, _I64, C.POINTER(_P), C.POINTER(_P), _P, _P]),
+    ("sco_resume", None, [_G, _I64, _P, C.POINTER(_P), C.POINTER(_P), _P]),
+    ("sco_fnv1a64", _U64, [_P, _U64, _U64]),
+    ("sco_handoff_carve", None, [_G, _I64, _I64, C.c_int, C.POINTER(_P), C.POINTER(_P), C.c_int, C.POINTER(_P),
+                                 C.POINTER(_P), _I64, _I64, C.POINTER(_P), C.POINTER(_P), C.POINTER(_P), _I64, _P]),
+    ("sco_cpu_handoff", _U64, [_P, _P, _U64, _P]),
+):
+    _fn = getattr(lib, _name)
+    _fn.restype = _res
+    _fn.argtypes = _args
+
+
+def geometry_from(geo) -> Geometry:
+    """Copy any object with the sc_geometry fields (e.g. the product binding's Geometry)."""
+    return Geometry(*[getattr(geo, f) for f, _ in Geometry._fields_])
+
+
+def _ptr(a: np.ndarray) -> int:
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data
+
+
+def _parr(arrays) -> C.Array:
+    arr = (C.c_void_p * max(len(arrays), 1))()
+    for i, a in enumerate(arrays):
+        arr[i] = None if a is None else _ptr(a)
+    return arr
+
+
+# ---- generators --------------------------------------------------------------------------------------------------
+
+def fill_uniform_f16(n: int, lo: float, hi: float, seed: int, sid: int) -> np.ndarray:
+    out = np.empty(max(n, 1), dtype=np.uint16)
+    lib.sco_fill_uniform_f16(_ptr(out), n, lo, hi, seed, sid)
+    return out[:n]
+
+
+def fill_uniform_f32(n: int, lo: float, hi: float, seed: int, sid: int) -> np.ndarray:
+    out = np.empty(max(n, 1), dtype=np.float32)
+    lib.sco_fill_uniform_f32(_ptr(out), n, lo, hi, seed, sid)
+    return out[:n]
+
+
+def fill_normal_f32(n: int, seed: int, sid: int) -> np.ndarray:
+    out = np.empty(max(n, 1), dtype=np.float32)
+    lib.sco_fill_normal_f32(_ptr(out), n, seed, sid)
+    return out[:n]
+
+
+def f16_bits(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, dtype=np.uint16)
+    lib.sco_f16_from_f32(_ptr(x), _ptr(out), x.size)
+    return out
+
+
+# ---- carve pieces ----------------------------------------------------------------------------------------------------
+
+def kv_append(src: np.ndarray, T: int, pos0: int, table, n_pages: int, H: int, D: int, ps: int,
+              pool: np.ndarray) -> None:
+    src = np.ascontiguousarray(src)
+    dtype = 0 if src.dtype == np.uint16 else 1
+    tab = None if table is None else np.ascontiguousarray(table, dtype=np.int32)
+    lib.sco_kv_append(_ptr(src), dtype, T, pos0, None if tab is None else _ptr(tab), n_pages, H, D, ps, _ptr(pool))
+
+
+def rec_carve(src: np.ndarray, S: int, HV: int) -> np.ndarray:
+    src = np.ascontiguousarray(src, dtype=np.float32)
+    out = np.empty(S * HV * S, dtype=np.float32)
+    lib.sco_rec_carve(_ptr(src), S, HV, _ptr(out))
+    return out
+
+
+def conv_hist(hist: np.ndarray, qkv: np.ndarray, rows: int, ld: int, C_: int, nhist: int, fresh: bool) -> None:
+    qkv = np.ascontiguousarray(qkv, dtype=np.float32)
+    lib.sco_conv_hist(_ptr(hist), _ptr(qkv) if qkv.size else None, rows, ld, C_, nhist, int(fresh))
+
+
+def image_layout(geo, tokens: int) -> tuple[list[tuple[int, int, int, int]], int]:
+    g = geometry_from(geo)
+    blobs = (Blob * 4096)()
+    total = _U64()
+    n = lib.sco_image_layout(C.byref(g), tokens, blobs, C.byref(total))
+    return [(b.kind, b.layer, b.offset, b.bytes) for b in blobs[:n]], int(total.value)
+
+
+def fnv1a64(data: bytes | np.ndarray, seed: int = REFERENCE_FNV_SEED) -> int:
+    a = np.frombuffer(bytes(data), dtype=np.uint8) if not isinstance(data, np.ndarray) else \
+        np.ascontiguousarray(data).view(np.uint8).reshape(-1)
+    return int(lib.sco_fnv1a64(_ptr(a) if a.size else None, a.size, seed))
+
+
+# ---- whole handoff -------------------------------------------------------------------------------------------------
+
+def expected_slot(geo, inputs: dict, slot_cells: int, pos0: int = 0, tables=None, n_pages: int | None = None,
+                  initial: dict | None = None, with_gdn: bool = True) -> dict:
+    """The decode slot after the fused carve of `inputs` (as PrefillBuffers.host() returns them), starting from
+    `initial` (default: zeros) - the oracle of sc_plan_carve."""
+    g = geometry_from(geo)
+    n_pages = n_pages if n_pages is not None else (slot_cells + g.page_size - 1) // g.page_size
+    out = new_state(geo, n_pages, initial)
+    carve_into(geo, inputs, out, n_pages, pos0, tables, with_gdn)
+    return out
+
+
+def new_state(geo, n_pages: int, initial: dict | None = None) -> dict:
+    """A host decode slot (Slot.host_state() keys): zeros, or a copy of `initial`."""
+    g = geometry_from(geo)
+    n_qsa = g.n_layers // g.qsa_interval
+    n_gdn = g.n_layers - n_qsa
+    ps, H, D = g.page_size, g.n_head_kv, g.head_dim
+    row = int(lib.sco_gdn_row_floats(C.byref(g)))
+    out = {}
+    for j in range(n_qsa):
+        for name in ("k", "v"):
+            key = f"{name}{j}"
+            out[key] = (initial[key].copy() if initial else np.zeros((n_pages, H, ps, D), dtype=np.uint16))
+            out[key] = np.ascontiguousarray(out[key].reshape(n_pages, H, ps, D))
+    if n_gdn:
+        out["gdn"] = initial["gdn"].copy() if initial else np.zeros((n_gdn, row), dtype=np.float32)
+        out["gdn"] = np.ascontiguousarray(out["gdn"].reshape(n_gdn, row))
+    return out
+
+
+def carve_into(geo, inputs: dict, out: dict, n_pages: int, pos0: int = 0, tables=None, with_gdn: bool = True) -> None:
+    """The fused carve of `inputs` into the host slot `out`, in place (sco_handoff_carve)."""
+    g = geometry_from(geo)
+    n_qsa = g.n_layers // g.qsa_interval
+    n_gdn = g.n_layers - n_qsa
+    T = inputs["tokens"]
+    ks = [np.ascontiguousarray(a) for a in inputs["k"]]
+    vs = [np.ascontiguousarray(a) for a in inputs["v"]]
+    recs = [np.ascontiguousarray(a, dtype=np.float32) for a in inputs["rec"]]
+    convs = [np.ascontiguousarray(a, dtype=np.float32) for a in inputs["conv"]]
+    dtype = 0 if (ks and ks[0].dtype == np.uint16) else 1
+    tabs = None
+    if tables is not None:
+        tabs = [None if t is None else np.ascontiguousarray(t, dtype=np.int32) for t in tables]
+    kp = _parr([out[f"k{j}"] for j in range(n_qsa)])
+    vp = _parr([out[f"v{j}"] for j in range(n_qsa)])
+    lib.sco_handoff_carve(C.byref(g), T, pos0, dtype, _parr(ks), _parr(vs), int(with_gdn), _parr(recs),
+                          _parr(convs), inputs["conv_rows"], g.ssm_conv_channels, kp, vp,
+                          _parr(tabs) if tabs is not None else None, n_pages,
+                          _ptr(out["gdn"]) if n_gdn else None)
+
+
+def park(geo, tokens: int, state: dict) -> np.ndarray:
+    """The image sc_park_async writes for a slot (identity pools) in `state` (Slot.host_state() keys)."""
+    g = geometry_from(geo)
+    n_qsa = g.n_layers // g.qsa_interval
+    _, total = image_layout(geo, tokens)
+    image = np.empty(max(total, 1), dtype=np.uint8)
+    ks = [np.ascontiguousarray(state[f"k{j}"]) for j in range(n_qsa)]
+    vs = [np.ascontiguousarray(state[f"v{j}"]) for j in range(n_qsa)]
+    gdn = np.ascontiguousarray(state["gdn"]) if "gdn" in state else None
+    lib.sco_park(C.byref(g), tokens, _parr(ks), _parr(vs), None if gdn is None else _ptr(gdn), _ptr(image))
+    return image[:total]
+
+
+def resume(geo, tokens: int, image: np.ndarray, state: dict) -> None:
+    g = geometry_from(geo)
+    n_qsa = g.n_layers // g.qsa_interval
+    ks = [state[f"k{j}"] for j in range(n_qsa)]
+    vs = [state[f"v{j}"] for j in range(n_qsa)]
+    gdn = state.get("gdn")
+    lib.sco_resume(C.byref(g), tokens, _ptr(np.ascontiguousarray(image)), _parr(ks), _parr(vs),
+                   None if gdn is None else _ptr(gdn))
+
+
+def cpu_handoff(src: np.ndarray, dst: np.ndarray, scratch: np.ndarray) -> int:
+    return int(lib.sco_cpu_handoff(_ptr(src), _ptr(dst), src.size, _ptr(scratch)))

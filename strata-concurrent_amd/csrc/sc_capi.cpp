@@ -1,0 +1,700 @@
+// sc_capi.cpp - the extern "C" layer of libsc_handoff.so (declared in include/sc_handoff.h).
+//
+// Every entry point validates its whole request on the host before the first HIP call, so a refusal
+// (SC_EINVAL / SC_ERANGE) has enqueued nothing and written nothing - the reference's "invalid images are
+// rejected before any CUDA call/write" contract (include/strata/core/conversation_snapshot.hpp:104-105).  A HIP
+// failure after that point is SC_EHIP: the destination may be partly written, as the reference's
+// `transfer_failed` (conversation_snapshot.hpp:103-108).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+#include <cstring>
+#include <exception>
+#include <limits>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "../../include/sc_handoff.h"
+#include "sc_internal.hpp"
+
+namespace sc {
+hipError_t launch_move(const MoveRow* rows, int n_rows, const MoveGeo& geo, uint64_t n_tiles, int64_t grid,
+                       hipStream_t stream);
+hipError_t launch_fill_uniform_f16(uint16_t* dst, uint64_t n, float lo, float hi, uint64_t seed, uint64_t sid,
+                                   hipStream_t stream);
+hipError_t launch_fill_uniform_f32(float* dst, uint64_t n, float lo, float hi, uint64_t seed, uint64_t sid,
+                                   hipStream_t stream);
+hipError_t launch_fill_normal_f32(float* dst, uint64_t n, uint64_t seed, uint64_t sid, hipStream_t stream);
+hipError_t launch_fill_bytes(void* dst, uint8_t value, uint64_t n, hipStream_t stream);
+hipError_t launch_decode_probe(const void* kv, uint64_t n_bytes, uint32_t* sink, int64_t workgroups,
+                               hipStream_t stream);
+
+static uint64_t host_mix64(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+// The key of synthetic stream `sid` under `seed`; element i of the stream is mix64(key + (i + 1) * golden).
+uint64_t synth_key(uint64_t seed, uint64_t sid) { return host_mix64(seed ^ host_mix64(sid + 0x9E3779B97F4A7C15ull)); }
+}  // namespace sc
+
+struct sc_plan {
+    sc::MoveRow* rows_dev = nullptr;
+    int n_rows = 0;
+    sc::MoveGeo geo{};
+    uint64_t n_tiles = 0;
+    uint64_t payload = 0;
+    int64_t grid = 0;
+};
+
+namespace {
+
+thread_local std::string g_error;
+
+int ok() {
+    g_error.clear();
+    return SC_OK;
+}
+int fail(int code, const std::string& message) {
+    g_error = message;
+    return code;
+}
+int snapshot_fail(const char* message) { return fail(SC_EINVAL, std::string("conversation snapshot: ") + message); }
+int hip_fail(hipError_t e, const char* what) {
+    return fail(SC_EHIP, std::string("sc_handoff ") + what + ": " + hipGetErrorString(e));
+}
+
+constexpr uint64_t kBlobAlign = 64;   // the wire codec's blob-pool alignment (conversation_wire.hpp:68-70)
+uint64_t round_up(uint64_t x, uint64_t a) { return (x + a - 1) / a * a; }
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+struct Geo {
+    int64_t n_qsa = 0, n_gdn = 0, H = 0, D = 0, ps = 0, S = 0, HV = 0, C = 0, hist = 0;
+    uint64_t row_bytes = 0, page_bytes = 0, gdn_row_bytes = 0, rec_bytes = 0;
+};
+
+bool geometry(const sc_geometry* g, Geo& o, std::string& why) {
+    if (!g) { why = "missing geometry"; return false; }
+    if (g->n_layers < 0 || g->qsa_interval < 1 || g->n_head_kv < 1 || g->head_dim < 1 || g->page_size < 1 ||
+        g->ssm_state_size < 1 || g->ssm_v_heads < 1 || g->ssm_conv_channels < 1 || g->ssm_d_conv < 2) {
+        why = "invalid model geometry";
+        return false;
+    }
+    if (g->n_head_kv > 4096 || g->head_dim > (1 << 20) || g->page_size > (1 << 20) || g->ssm_state_size > 65536 ||
+        g->ssm_v_heads > 65536 || g->ssm_conv_channels > (int64_t(1) << 30) || g->n_layers > 100000) {
+        why = "model geometry beyond the supported range";
+        return false;
+    }
+    o.n_qsa = g->n_layers / g->qsa_interval;
+    o.n_gdn = g->n_layers - o.n_qsa;
+    o.H = g->n_head_kv; o.D = g->head_dim; o.ps = g->page_size;
+    o.S = g->ssm_state_size; o.HV = g->ssm_v_heads; o.C = g->ssm_conv_channels; o.hist = g->ssm_d_conv - 1;
+    if ((o.D * 2) % 16) { why = "head_dim must make 16-byte rows (a multiple of 8)"; return false; }
+    if ((o.S * 4) % 16) { why = "ssm_state_size must make 16-byte rows (a multiple of 4)"; return false; }
+    if (o.hist > sc::kMaxHist) { why = "ssm_d_conv beyond the supported history"; return false; }
+    o.row_bytes = uint64_t(o.D) * 2;
+    o.page_bytes = uint64_t(o.H) * uint64_t(o.ps) * o.row_bytes;
+    o.rec_bytes = uint64_t(o.S) * uint64_t(o.HV) * uint64_t(o.S) * 4;
+    o.gdn_row_bytes = o.rec_bytes + uint64_t(o.C) * uint64_t(o.hist) * 4;
+    return true;
+}
+
+int64_t cells_of(const Geo& g, int64_t tokens) { return (tokens + g.ps - 1) / g.ps * g.ps; }
+
+struct Blob {
+    int32_t kind, layer;
+    uint64_t offset, bytes;
+};
+
+// K then V of every QSA layer, then the GDN rows; each blob on a 64-byte boundary.
+std::vector<Blob> image_blobs(const Geo& g, int64_t tokens, uint64_t& total) {
+    std::vector<Blob> out;
+    const uint64_t kv = uint64_t(cells_of(g, tokens)) * uint64_t(g.H) * g.row_bytes;
+    uint64_t at = 0;
+    for (int64_t j = 0; j < g.n_qsa; ++j)
+        for (int32_t kind : {SC_BLOB_K, SC_BLOB_V}) {
+            at = round_up(at, kBlobAlign);
+            out.push_back({kind, int32_t(j), at, kv});
+            at += kv;
+        }
+    if (g.n_gdn > 0) {
+        at = round_up(at, kBlobAlign);
+        out.push_back({SC_BLOB_GDN, -1, at, uint64_t(g.n_gdn) * g.gdn_row_bytes});
+        at += uint64_t(g.n_gdn) * g.gdn_row_bytes;
+    }
+    total = round_up(at, kBlobAlign);
+    return out;
+}
+
+// Zero rows for the gaps between blobs (and after the last), so an image is fully deterministic.
+void gap_rows(const std::vector<Blob>& blobs, uint64_t total, uint8_t* image, std::vector<sc::MoveRow>& rows) {
+    uint64_t at = 0;
+    auto gap = [&](uint64_t end) {
+        if (end > at) {
+            sc::MoveRow r{};
+            r.kind = sc::kZero; r.dst = image + at; r.n = (end - at) / 16;
+            if (r.n) rows.push_back(r);
+        }
+    };
+    for (const Blob& b : blobs) { gap(b.offset); at = b.offset + b.bytes; }
+    gap(total);
+}
+
+sc::MoveGeo move_geo(const Geo& g) {
+    sc::MoveGeo m{};
+    m.row_chunks = sc::make_fastdiv(uint32_t(g.row_bytes / 16));
+    m.heads = sc::make_fastdiv(uint32_t(g.H));
+    m.page_size = sc::make_fastdiv(uint32_t(g.ps));
+    m.rec_chunks = sc::make_fastdiv(uint32_t(g.S * 4 / 16));
+    m.v_heads = sc::make_fastdiv(uint32_t(g.HV));
+    m.page_chunks = sc::make_fastdiv(uint32_t(g.page_bytes / 16));
+    m.state = uint32_t(g.S);
+    return m;
+}
+
+constexpr uint64_t kMaxRowChunks = uint64_t(1) << 31;
+
+// Assigns tile ranges, uploads the table and fills the plan.  The only HIP calls a plan builder makes.
+int finish_plan(std::vector<sc::MoveRow>& rows, const Geo& g, uint64_t payload, sc_plan** out) {
+    if (rows.size() > 1024) return fail(SC_ERANGE, "sc_handoff: more than 1024 handoff table rows in one plan");
+    uint64_t tiles = 0;
+    for (auto& r : rows) {
+        if (r.n >= kMaxRowChunks) return fail(SC_ERANGE, "sc_handoff: a handoff table row beyond 2^31 chunks");
+        r.tile0 = tiles;
+        tiles += r.kind == sc::kConv ? (r.n + sc::kConvTileChannels - 1) / sc::kConvTileChannels
+                                     : (r.n + sc::kTileChunks - 1) / sc::kTileChunks;
+    }
+    // rows that move nothing still own an (empty) tile range; the kernel never visits them
+    sc_plan* p = new (std::nothrow) sc_plan();
+    if (!p) return fail(SC_ENOMEM, "sc_handoff: plan allocation failed");
+    p->n_rows = int(rows.size());
+    p->geo = move_geo(g);
+    p->n_tiles = tiles;
+    p->payload = payload;
+    int device = 0, cus = 0;
+    hipError_t e = hipGetDevice(&device);
+    if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
+    if (e != hipSuccess) { delete p; return hip_fail(e, "device query"); }
+    p->grid = int64_t(std::max(cus, 1)) * 8;
+    if (rows.empty()) {   // an empty handoff (0 tokens, no running state) is a valid no-op
+        *out = p;
+        return ok();
+    }
+    e = hipMalloc(reinterpret_cast<void**>(&p->rows_dev), rows.size() * sizeof(sc::MoveRow));
+    if (e != hipSuccess) { delete p; return fail(SC_ENOMEM, std::string("sc_handoff: table allocation: ") + hipGetErrorString(e)); }
+    e = hipMemcpy(p->rows_dev, rows.data(), rows.size() * sizeof(sc::MoveRow), hipMemcpyHostToDevice);
+    if (e != hipSuccess) { (void) hipFree(p->rows_dev); delete p; return hip_fail(e, "table upload"); }
+    *out = p;
+    return ok();
+}
+
+bool slot_identity(const sc_decode_slot* s, int64_t n_qsa) {
+    if (!s->page_table) return true;
+    for (int64_t j = 0; j < n_qsa; ++j)
+        if (s->page_table[j]) return false;
+    return true;
+}
+
+// Checks the slot can hold `cells` cells (from cell 0) and that its buffers are present and aligned.
+int check_slot(const Geo& g, const sc_decode_slot* s, int64_t cells_end, bool need_gdn) {
+    if (!s) return snapshot_fail("missing decode slot");
+    if (s->n_pages < 0 || s->max_cells < 0 || cells_end > s->max_cells)
+        return snapshot_fail("invalid K/V extent");
+    if (g.n_qsa > 0) {
+        if (!s->k_pool || !s->v_pool) return snapshot_fail("missing target state buffer");
+        const bool identity = slot_identity(s, g.n_qsa);
+        if (identity && s->max_cells > s->n_pages * g.ps) return snapshot_fail("invalid K/V extent");
+        for (int64_t j = 0; j < g.n_qsa; ++j) {
+            if (!s->k_pool[j] || !s->v_pool[j]) return snapshot_fail("missing target state buffer");
+            if (!aligned16(s->k_pool[j]) || !aligned16(s->v_pool[j]))
+                return fail(SC_EINVAL, "sc_handoff: K/V pools must be 16-byte aligned");
+        }
+    }
+    if (need_gdn && g.n_gdn > 0) {
+        if (!s->gdn_state) return snapshot_fail("missing running-state buffer");
+        if (!aligned16(s->gdn_state) || g.gdn_row_bytes % 16)
+            return fail(SC_EINVAL, "sc_handoff: GDN rows must be 16-byte aligned multiples of 16 bytes");
+    }
+    return SC_OK;
+}
+
+int check_view(const Geo& g, const sc_prefill_view* v) {
+    if (!v) return snapshot_fail("missing prefill view");
+    if (v->tokens < 0 || v->pos0 < 0 || v->tokens > (int64_t(1) << 30) || v->pos0 > (int64_t(1) << 30))
+        return snapshot_fail("invalid K/V extent");
+    if (v->kv_dtype != SC_DTYPE_F16 && v->kv_dtype != SC_DTYPE_F32)
+        return fail(SC_EINVAL, "sc_handoff: unsupported prefill K/V dtype");
+    if (g.n_qsa > 0 && v->tokens > 0) {
+        if (!v->k || !v->v) return snapshot_fail("missing prefill K/V");
+        for (int64_t j = 0; j < g.n_qsa; ++j) {
+            if (!v->k[j] || !v->v[j]) return snapshot_fail("missing prefill K/V");
+            if (!aligned16(v->k[j]) || !aligned16(v->v[j]))
+                return fail(SC_EINVAL, "sc_handoff: prefill K/V must be 16-byte aligned");
+        }
+    }
+    if (v->with_gdn && g.n_gdn > 0) {
+        if (!v->rec || !v->conv) return snapshot_fail("missing prefill running state");
+        if (v->conv_rows < 0 || v->conv_ld < g.C) return snapshot_fail("invalid conv source extent");
+        for (int64_t i = 0; i < g.n_gdn; ++i) {
+            if (!v->rec[i] || (!v->conv[i] && v->conv_rows > 0)) return snapshot_fail("missing prefill running state");
+            if (!aligned16(v->rec[i])) return fail(SC_EINVAL, "sc_handoff: recurrent state must be 16-byte aligned");
+        }
+    }
+    return SC_OK;
+}
+
+void kv_rows(const Geo& g, const sc_prefill_view* v, int64_t j, uint16_t* kdst, uint16_t* vdst,
+             const int32_t* table, int64_t phys_pages, int64_t virtual_cells, std::vector<sc::MoveRow>& rows) {
+    const uint64_t row_chunks = g.row_bytes / 16;
+    const void* srcs[2] = {v->k[j], v->v[j]};
+    uint16_t* dsts[2] = {kdst, vdst};
+    for (int a = 0; a < 2; ++a) {
+        sc::MoveRow r{};
+        r.kind = v->kv_dtype == SC_DTYPE_F16 ? sc::kKv16 : sc::kKv32;
+        r.src = static_cast<const uint8_t*>(srcs[a]);
+        r.dst = reinterpret_cast<uint8_t*>(dsts[a]);
+        r.table = table;
+        r.pos0 = v->pos0;
+        r.ld = phys_pages;
+        // `virtual_cells` > tokens: the rows of cells [tokens, virtual_cells) are written as zeros (image tails)
+        const int64_t rows_n = std::max(v->tokens, virtual_cells) * g.H;
+        r.aux = int32_t(v->tokens);
+        r.n = uint64_t(rows_n) * row_chunks;
+        if (r.n) rows.push_back(r);
+    }
+}
+
+void gdn_rows(const Geo& g, const sc_prefill_view* v, float* gdn, std::vector<sc::MoveRow>& rows) {
+    const uint64_t row_floats = g.gdn_row_bytes / 4;
+    for (int64_t i = 0; i < g.n_gdn; ++i) {
+        float* base = gdn + uint64_t(i) * row_floats;
+        sc::MoveRow rec{};
+        rec.kind = sc::kRec;
+        rec.src = reinterpret_cast<const uint8_t*>(v->rec[i]);
+        rec.dst = reinterpret_cast<uint8_t*>(base);
+        rec.n = uint64_t(g.S) * uint64_t(g.HV) * uint64_t(g.S * 4 / 16);
+        rows.push_back(rec);
+        sc::MoveRow conv{};
+        conv.kind = sc::kConv;
+        conv.aux = int32_t(g.hist) | (v->pos0 == 0 ? 0x100 : 0);   // a fresh sequence's older history is zero
+        conv.src = reinterpret_cast<const uint8_t*>(v->conv[i]);
+        conv.dst = reinterpret_cast<uint8_t*>(base + g.rec_bytes / 4);
+        conv.n = uint64_t(g.C);
+        conv.pos0 = v->conv_rows;
+        conv.ld = v->conv_ld;
+        rows.push_back(conv);
+    }
+}
+
+uint64_t kv_payload(const Geo& g, int64_t tokens) { return uint64_t(tokens) * uint64_t(g.H) * g.row_bytes * 2 * uint64_t(g.n_qsa); }
+
+template <class F>
+int guarded(F&& f) {
+    try {
+        return f();
+    } catch (const std::bad_alloc&) {
+        return fail(SC_ENOMEM, "sc_handoff: host allocation failed");
+    } catch (const std::exception& e) {
+        return fail(SC_EINVAL, std::string("sc_handoff: ") + e.what());
+    } catch (...) {
+        return fail(SC_EINVAL, "sc_handoff: unknown failure");
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* sc_last_error(void) { return g_error.c_str(); }
+const char* sc_version(void) { return "sc_handoff 0.1 gfx950"; }
+
+int64_t sc_n_qsa_layers(const sc_geometry* g) { return g && g->qsa_interval > 0 ? g->n_layers / g->qsa_interval : 0; }
+int64_t sc_n_gdn_layers(const sc_geometry* g) { return g ? g->n_layers - sc_n_qsa_layers(g) : 0; }
+int64_t sc_gdn_row_floats(const sc_geometry* g) {
+    Geo o;
+    std::string why;
+    return geometry(g, o, why) ? int64_t(o.gdn_row_bytes / 4) : 0;
+}
+int64_t sc_kv_cells(const sc_geometry* g, int64_t tokens) {
+    Geo o;
+    std::string why;
+    return geometry(g, o, why) && tokens >= 0 ? cells_of(o, tokens) : -1;
+}
+uint64_t sc_payload_bytes(const sc_geometry* g, int64_t tokens) {
+    Geo o;
+    std::string why;
+    if (!geometry(g, o, why) || tokens < 0) return 0;
+    return kv_payload(o, cells_of(o, tokens)) + uint64_t(o.n_gdn) * o.gdn_row_bytes;
+}
+
+int sc_image_layout(const sc_geometry* g, int64_t tokens, sc_image_blob* blobs, int64_t* n_blobs,
+                    uint64_t* total_bytes) {
+    return guarded([&] {
+        Geo o;
+        std::string why;
+        if (!geometry(g, o, why)) return snapshot_fail(why.c_str());
+        if (tokens < 0 || tokens > (int64_t(1) << 30)) return snapshot_fail("invalid K/V extent");
+        uint64_t total = 0;
+        const auto list = image_blobs(o, tokens, total);
+        if (blobs)
+            for (size_t i = 0; i < list.size(); ++i)
+                blobs[i] = sc_image_blob{list[i].kind, list[i].layer, list[i].offset, list[i].bytes};
+        if (n_blobs) *n_blobs = int64_t(list.size());
+        if (total_bytes) *total_bytes = total;
+        return ok();
+    });
+}
+
+int sc_plan_carve(const sc_geometry* g, const sc_prefill_view* src, const sc_decode_slot* dst, sc_plan** out) {
+    return guarded([&] {
+        if (!out) return fail(SC_EINVAL, "sc_handoff: missing plan output");
+        Geo o;
+        std::string why;
+        if (!geometry(g, o, why)) return snapshot_fail(why.c_str());
+        int rc = check_view(o, src);
+        if (rc) return rc;
+        rc = check_slot(o, dst, src->pos0 + src->tokens, src->with_gdn != 0);
+        if (rc) return rc;
+        std::vector<sc::MoveRow> rows;
+        for (int64_t j = 0; j < o.n_qsa; ++j) {
+            const int32_t* table = dst->page_table ? dst->page_table[j] : nullptr;
+            kv_rows(o, src, j, dst->k_pool[j], dst->v_pool[j], table, dst->n_pages, 0, rows);
+        }
+        uint64_t payload = kv_payload(o, src->tokens);
+        if (src->with_gdn) {
+            gdn_rows(o, src, dst->gdn_state, rows);
+            payload += uint64_t(o.n_gdn) * o.gdn_row_bytes;
+        }
+        return finish_plan(rows, o, payload, out);
+    });
+}
+
+int sc_plan_gather(const sc_geometry* g, const sc_prefill_view* src, void* image, uint64_t image_bytes,
+                   sc_plan** out) {
+    return guarded([&] {
+        if (!out) return fail(SC_EINVAL, "sc_handoff: missing plan output");
+        Geo o;
+        std::string why;
+        if (!geometry(g, o, why)) return snapshot_fail(why.c_str());
+        int rc = check_view(o, src);
+        if (rc) return rc;
+        if (src->pos0 != 0) return snapshot_fail("an image starts at cell 0");
+        if (!src->with_gdn && o.n_gdn > 0) return snapshot_fail("an image carries the running state");
+        uint64_t total = 0;
+        const auto blobs = image_blobs(o, src->tokens, total);
+        if (!image || image_bytes < total) return snapshot_fail("transfer buffer smaller than the image");
+        if (!aligned16(image)) return fail(SC_EINVAL, "sc_handoff: transfer buffer must be 16-byte aligned");
+        if (o.gdn_row_bytes % 16) return fail(SC_EINVAL, "sc_handoff: GDN rows must be multiples of 16 bytes");
+        uint8_t* base = static_cast<uint8_t*>(image);
+        const int64_t cells = cells_of(o, src->tokens);
+        std::vector<sc::MoveRow> rows;
+        size_t b = 0;
+        for (int64_t j = 0; j < o.n_qsa; ++j, b += 2)
+            kv_rows(o, src, j, reinterpret_cast<uint16_t*>(base + blobs[b].offset),
+                    reinterpret_cast<uint16_t*>(base + blobs[b + 1].offset), nullptr, cells / o.ps, cells, rows);
+        if (o.n_gdn > 0) gdn_rows(o, src, reinterpret_cast<float*>(base + blobs[b].offset), rows);
+        gap_rows(blobs, total, base, rows);
+        return finish_plan(rows, o, kv_payload(o, cells) + uint64_t(o.n_gdn) * o.gdn_row_bytes, out);
+    });
+}
+
+static int page_plan(const sc_geometry* g, const void* image, uint64_t image_bytes, int64_t tokens,
+                     const sc_decode_slot* slot, bool scatter, sc_plan** out) {
+    if (!out) return fail(SC_EINVAL, "sc_handoff: missing plan output");
+    Geo o;
+    std::string why;
+    if (!geometry(g, o, why)) return snapshot_fail(why.c_str());
+    if (tokens < 0 || tokens > (int64_t(1) << 30)) return snapshot_fail("invalid K/V extent");
+    const int64_t cells = cells_of(o, tokens);
+    int rc = check_slot(o, slot, cells, true);
+    if (rc) return rc;
+    uint64_t total = 0;
+    const auto blobs = image_blobs(o, tokens, total);
+    if (!image || image_bytes < total) return snapshot_fail("invalid K/V payload size");
+    if (!aligned16(image)) return fail(SC_EINVAL, "sc_handoff: image must be 16-byte aligned");
+    uint8_t* base = const_cast<uint8_t*>(static_cast<const uint8_t*>(image));
+    std::vector<sc::MoveRow> rows;
+    const uint64_t pages = uint64_t(cells / o.ps);
+    size_t b = 0;
+    for (int64_t j = 0; j < o.n_qsa; ++j, b += 2) {
+        uint16_t* pools[2] = {slot->k_pool[j], slot->v_pool[j]};
+        for (int a = 0; a < 2; ++a) {
+            sc::MoveRow r{};
+            r.kind = scatter ? sc::kPagesScatter : sc::kPagesGather;
+            uint8_t* img = base + blobs[b + a].offset;
+            r.src = scatter ? img : reinterpret_cast<const uint8_t*>(pools[a]);
+            r.dst = scatter ? reinterpret_cast<uint8_t*>(pools[a]) : img;
+            r.table = slot->page_table ? slot->page_table[j] : nullptr;
+            r.n = pages * (o.page_bytes / 16);
+            r.ld = slot->n_pages;
+            if (r.n) rows.push_back(r);
+        }
+    }
+    if (o.n_gdn > 0) {
+        sc::MoveRow r{};
+        r.kind = sc::kCopy;
+        uint8_t* img = base + blobs[b].offset;
+        r.src = scatter ? img : reinterpret_cast<const uint8_t*>(slot->gdn_state);
+        r.dst = scatter ? reinterpret_cast<uint8_t*>(slot->gdn_state) : img;
+        r.n = uint64_t(o.n_gdn) * o.gdn_row_bytes / 16;
+        rows.push_back(r);
+    }
+    if (!scatter) gap_rows(blobs, total, base, rows);
+    return finish_plan(rows, o, kv_payload(o, cells) + uint64_t(o.n_gdn) * o.gdn_row_bytes, out);
+}
+
+int sc_plan_scatter(const sc_geometry* g, const void* image, uint64_t image_bytes, int64_t tokens,
+                    const sc_decode_slot* dst, sc_plan** out) {
+    return guarded([&] { return page_plan(g, image, image_bytes, tokens, dst, true, out); });
+}
+
+int sc_plan_capture(const sc_geometry* g, const sc_decode_slot* src, int64_t tokens, void* image,
+                    uint64_t image_bytes, sc_plan** out) {
+    return guarded([&] { return page_plan(g, image, image_bytes, tokens, src, false, out); });
+}
+
+int sc_plan_launch(const sc_plan* plan, void* stream) {
+    if (!plan) return fail(SC_EINVAL, "sc_handoff: missing plan");
+    const hipError_t e = sc::launch_move(plan->rows_dev, plan->n_rows, plan->geo, plan->n_tiles, plan->grid,
+                                         static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? ok() : hip_fail(e, "move launch");
+}
+
+uint64_t sc_plan_payload_bytes(const sc_plan* plan) { return plan ? plan->payload : 0; }
+
+int sc_plan_set_grid(sc_plan* plan, int64_t workgroups) {
+    if (!plan || workgroups < 0 || workgroups > (int64_t(1) << 30)) return fail(SC_EINVAL, "sc_handoff: invalid grid");
+    if (workgroups == 0) {
+        int device = 0, cus = 0;
+        if (hipGetDevice(&device) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
+            return fail(SC_EHIP, "sc_handoff: device query failed");
+        workgroups = int64_t(std::max(cus, 1)) * 8;
+    }
+    plan->grid = workgroups;
+    return ok();
+}
+
+int sc_plan_destroy(sc_plan* plan) {
+    if (!plan) return ok();
+    const hipError_t e = plan->rows_dev ? hipFree(plan->rows_dev) : hipSuccess;
+    delete plan;
+    return e == hipSuccess ? ok() : hip_fail(e, "table free");
+}
+
+// ---- park / resume --------------------------------------------------------------------------------------------
+
+static int dma_image(const sc_geometry* g, const sc_decode_slot* slot, int64_t tokens, uint8_t* host,
+                     uint64_t image_bytes, bool park, void* stream, void* done) {
+    Geo o;
+    std::string why;
+    if (!geometry(g, o, why)) return snapshot_fail(why.c_str());
+    if (tokens < 0 || tokens > (int64_t(1) << 30)) return snapshot_fail("invalid K/V extent");
+    const int64_t cells = cells_of(o, tokens);
+    int rc = check_slot(o, slot, cells, true);
+    if (rc) return rc;
+    if (!slot_identity(slot, o.n_qsa))
+        return fail(SC_EINVAL, "sc_handoff: park/resume copies identity-layout pools; capture a paged slot first");
+    uint64_t total = 0;
+    const auto blobs = image_blobs(o, tokens, total);
+    if (!host || image_bytes < total) return snapshot_fail("invalid K/V payload size");
+    if (park) {
+        // the gaps between blobs are never copied; clear them so the image is deterministic
+        uint64_t at = 0;
+        for (const Blob& b : blobs) {
+            if (b.offset > at) std::memset(host + at, 0, b.offset - at);
+            at = b.offset + b.bytes;
+        }
+        if (total > at) std::memset(host + at, 0, total - at);
+    }
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    size_t b = 0;
+    for (int64_t j = 0; j < o.n_qsa; ++j, b += 2) {
+        uint16_t* pools[2] = {slot->k_pool[j], slot->v_pool[j]};
+        for (int a = 0; a < 2; ++a) {
+            const Blob& blob = blobs[b + a];
+            if (!blob.bytes) continue;
+            const hipError_t e = park ? hipMemcpyAsync(host + blob.offset, pools[a], blob.bytes, hipMemcpyDeviceToHost, s)
+                                      : hipMemcpyAsync(pools[a], host + blob.offset, blob.bytes, hipMemcpyHostToDevice, s);
+            if (e != hipSuccess) return hip_fail(e, park ? "park copy" : "resume copy");
+        }
+    }
+    if (o.n_gdn > 0) {
+        const Blob& blob = blobs[b];
+        const hipError_t e = park ? hipMemcpyAsync(host + blob.offset, slot->gdn_state, blob.bytes, hipMemcpyDeviceToHost, s)
+                                  : hipMemcpyAsync(slot->gdn_state, host + blob.offset, blob.bytes, hipMemcpyHostToDevice, s);
+        if (e != hipSuccess) return hip_fail(e, park ? "park copy" : "resume copy");
+    }
+    if (done) {
+        const hipError_t e = hipEventRecord(static_cast<hipEvent_t>(done), s);
+        if (e != hipSuccess) return hip_fail(e, "event record");
+    }
+    return ok();
+}
+
+int sc_park_async(const sc_geometry* g, const sc_decode_slot* slot, int64_t tokens, void* host_image,
+                  uint64_t image_bytes, void* stream, void* done) {
+    return guarded([&] { return dma_image(g, slot, tokens, static_cast<uint8_t*>(host_image), image_bytes, true, stream, done); });
+}
+
+int sc_resume_async(const sc_geometry* g, const void* host_image, uint64_t image_bytes, int64_t tokens,
+                    const sc_decode_slot* slot, void* stream, void* done) {
+    return guarded([&] {
+        return dma_image(g, slot, tokens, const_cast<uint8_t*>(static_cast<const uint8_t*>(host_image)), image_bytes,
+                         false, stream, done);
+    });
+}
+
+// ---- plumbing --------------------------------------------------------------------------------------------------
+
+#define SC_HIP(call, what)                                    \
+    do {                                                      \
+        const hipError_t e_ = (call);                         \
+        if (e_ != hipSuccess) return hip_fail(e_, what);      \
+    } while (0)
+
+int sc_device_alloc(void** ptr, uint64_t bytes) {
+    if (!ptr) return fail(SC_EINVAL, "sc_handoff: missing pointer");
+    const hipError_t e = hipMalloc(ptr, bytes ? bytes : 16);
+    return e == hipSuccess ? ok() : fail(SC_ENOMEM, std::string("sc_handoff: device allocation: ") + hipGetErrorString(e));
+}
+int sc_device_free(void* ptr) {
+    SC_HIP(hipFree(ptr), "device free");
+    return ok();
+}
+int sc_host_alloc(void** ptr, uint64_t bytes) {
+    if (!ptr) return fail(SC_EINVAL, "sc_handoff: missing pointer");
+    const hipError_t e = hipHostMalloc(ptr, bytes ? bytes : 16, hipHostMallocDefault);
+    return e == hipSuccess ? ok() : fail(SC_ENOMEM, std::string("sc_handoff: pinned allocation: ") + hipGetErrorString(e));
+}
+int sc_host_free(void* ptr) {
+    SC_HIP(hipHostFree(ptr), "pinned free");
+    return ok();
+}
+int sc_copy_async(void* dst, const void* src, uint64_t bytes, void* stream) {
+    if (!bytes) return ok();
+    if (!dst || !src) return fail(SC_EINVAL, "sc_handoff: missing copy buffer");
+    SC_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDefault, static_cast<hipStream_t>(stream)), "copy");
+    return ok();
+}
+int sc_fill_bytes_async(void* dst, uint8_t value, uint64_t bytes, void* stream) {
+    if (!bytes) return ok();
+    if (!dst) return fail(SC_EINVAL, "sc_handoff: missing fill buffer");
+    SC_HIP(sc::launch_fill_bytes(dst, value, bytes, static_cast<hipStream_t>(stream)), "fill");
+    return ok();
+}
+int sc_stream_create(void** stream) {
+    if (!stream) return fail(SC_EINVAL, "sc_handoff: missing stream");
+    hipStream_t s = nullptr;
+    SC_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "stream create");
+    *stream = s;
+    return ok();
+}
+int sc_stream_destroy(void* stream) {
+    SC_HIP(hipStreamDestroy(static_cast<hipStream_t>(stream)), "stream destroy");
+    return ok();
+}
+int sc_stream_sync(void* stream) {
+    SC_HIP(hipStreamSynchronize(static_cast<hipStream_t>(stream)), "stream sync");
+    return ok();
+}
+int sc_device_sync(void) {
+    SC_HIP(hipDeviceSynchronize(), "device sync");
+    return ok();
+}
+int sc_event_create(void** event) {
+    if (!event) return fail(SC_EINVAL, "sc_handoff: missing event");
+    hipEvent_t ev = nullptr;
+    SC_HIP(hipEventCreate(&ev), "event create");
+    *event = ev;
+    return ok();
+}
+int sc_event_destroy(void* event) {
+    SC_HIP(hipEventDestroy(static_cast<hipEvent_t>(event)), "event destroy");
+    return ok();
+}
+int sc_event_record(void* event, void* stream) {
+    SC_HIP(hipEventRecord(static_cast<hipEvent_t>(event), static_cast<hipStream_t>(stream)), "event record");
+    return ok();
+}
+int sc_event_sync(void* event) {
+    SC_HIP(hipEventSynchronize(static_cast<hipEvent_t>(event)), "event sync");
+    return ok();
+}
+int sc_event_elapsed_ms(void* start, void* end, float* ms) {
+    if (!ms) return fail(SC_EINVAL, "sc_handoff: missing output");
+    SC_HIP(hipEventElapsedTime(ms, static_cast<hipEvent_t>(start), static_cast<hipEvent_t>(end)), "event elapsed");
+    return ok();
+}
+int sc_stream_wait_event(void* stream, void* event) {
+    SC_HIP(hipStreamWaitEvent(static_cast<hipStream_t>(stream), static_cast<hipEvent_t>(event), 0), "stream wait");
+    return ok();
+}
+
+int sc_probe_link(uint64_t bytes, int iters, double* h2d_gbps, double* d2h_gbps) {
+    if (!bytes || iters < 1 || !h2d_gbps || !d2h_gbps) return fail(SC_EINVAL, "sc_handoff: invalid probe request");
+    void* h = nullptr;
+    void* d = nullptr;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    hipStream_t s = nullptr;
+    int rc = SC_OK;
+    auto cleanup = [&] {
+        if (e0) (void) hipEventDestroy(e0);
+        if (e1) (void) hipEventDestroy(e1);
+        if (s) (void) hipStreamDestroy(s);
+        if (d) (void) hipFree(d);
+        if (h) (void) hipHostFree(h);
+    };
+    hipError_t e = hipHostMalloc(&h, bytes, hipHostMallocDefault);
+    if (e == hipSuccess) e = hipMalloc(&d, bytes);
+    if (e == hipSuccess) e = hipEventCreate(&e0);
+    if (e == hipSuccess) e = hipEventCreate(&e1);
+    if (e == hipSuccess) e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
+    if (e != hipSuccess) { cleanup(); return hip_fail(e, "probe setup"); }
+    std::memset(h, 0, bytes);   // fault the pages in before timing
+    for (int dir = 0; dir < 2 && rc == SC_OK; ++dir) {
+        const hipMemcpyKind kind = dir == 0 ? hipMemcpyHostToDevice : hipMemcpyDeviceToHost;
+        void* to = dir == 0 ? d : h;
+        const void* from = dir == 0 ? h : d;
+        float ms = 0.f;
+        e = hipMemcpyAsync(to, from, bytes, kind, s);   // warm-up: context up, copy engine primed
+        if (e == hipSuccess) e = hipEventRecord(e0, s);
+        for (int i = 0; i < iters && e == hipSuccess; ++i) e = hipMemcpyAsync(to, from, bytes, kind, s);
+        if (e == hipSuccess) e = hipEventRecord(e1, s);
+        if (e == hipSuccess) e = hipEventSynchronize(e1);
+        if (e == hipSuccess) e = hipEventElapsedTime(&ms, e0, e1);
+        if (e != hipSuccess) { rc = hip_fail(e, "probe copy"); break; }
+        const double gbps = ms > 0.f ? double(bytes) * iters / (double(ms) * 1e-3) / 1e9 : -1.0;
+        (dir == 0 ? *h2d_gbps : *d2h_gbps) = gbps;
+    }
+    cleanup();
+    return rc == SC_OK ? ok() : rc;
+}
+
+int sc_fill_uniform_f16(uint16_t* dst, uint64_t n, float lo, float hi, uint64_t seed, uint64_t stream_id,
+                        void* stream) {
+    if (n && !dst) return fail(SC_EINVAL, "sc_handoff: missing fill buffer");
+    SC_HIP(sc::launch_fill_uniform_f16(dst, n, lo, hi, seed, stream_id, static_cast<hipStream_t>(stream)), "fill");
+    return ok();
+}
+int sc_fill_uniform_f32(float* dst, uint64_t n, float lo, float hi, uint64_t seed, uint64_t stream_id,
+                        void* stream) {
+    if (n && !dst) return fail(SC_EINVAL, "sc_handoff: missing fill buffer");
+    SC_HIP(sc::launch_fill_uniform_f32(dst, n, lo, hi, seed, stream_id, static_cast<hipStream_t>(stream)), "fill");
+    return ok();
+}
+int sc_fill_normal_f32(float* dst, uint64_t n, uint64_t seed, uint64_t stream_id, void* stream) {
+    if (n && !dst) return fail(SC_EINVAL, "sc_handoff: missing fill buffer");
+    SC_HIP(sc::launch_fill_normal_f32(dst, n, seed, stream_id, static_cast<hipStream_t>(stream)), "fill");
+    return ok();
+}
+int sc_decode_probe(const void* kv, uint64_t n_bytes, uint32_t* sink, int64_t workgroups, void* stream) {
+    if (!kv || !sink || workgroups <= 0 || workgroups > (int64_t(1) << 20) || (n_bytes % 16))
+        return fail(SC_EINVAL, "sc_handoff: invalid decode probe request");
+    SC_HIP(sc::launch_decode_probe(kv, n_bytes, sink, workgroups, static_cast<hipStream_t>(stream)), "decode probe");
+    return ok();
+}
+
+}  // extern "C"

@@ -1,0 +1,76 @@
+// sc_internal.hpp - the handoff table's row format and the launch geometry, shared by the host plan builder
+// (sc_capi.cpp) and the move kernel (sc_kernels.hip).
+//
+// The handoff table is one row per moved blob.  Every row describes a flat space of 16-byte CHUNKS (or, for
+// the conv history, of channels) and a closed-form address map from a chunk index to its source and
+// destination byte offsets.  A launch walks the concatenation of all rows in TILES of kTileChunks chunks, so
+// one launch moves every layer of a handoff whatever the mix of kinds.
+#pragma once
+
+#include <cstdint>
+
+namespace sc {
+
+constexpr int kThreads = 256;            // one workgroup = 4 wave64
+constexpr int kChunksPerThread = 4;      // 16-byte chunks in flight per thread per tile
+constexpr int kTileChunks = kThreads * kChunksPerThread;   // 1024 chunks = 16 KiB per tile
+constexpr int kConvTileChannels = 512;   // channels per conv-history tile (LDS-staged transpose)
+constexpr int kMaxHist = 4;              // d_conv - 1 rows of history the conv tile supports
+
+// Row kinds.
+enum MoveKind : int32_t {
+    kKv16 = 1,          // prefill K or V rows [T][H][D] f16 -> paged pool rows (page table, pos0)
+    kKv32 = 2,          // the same from f32 rows, rounded to f16 (round to nearest even)
+    kRec = 3,           // recurrence [HV][S][S] -> (S, HV, S)
+    kConv = 4,          // conv input rows [rows][C] -> history [C][hist] (LDS-staged transpose)
+    kPagesScatter = 5,  // contiguous pages -> pool pages through the page table
+    kPagesGather = 6,   // pool pages through the page table -> contiguous pages
+    kCopy = 7,          // contiguous 16-byte chunks
+    kZero = 8,          // zero-fill 16-byte chunks (padding and stale-cell tails of an image)
+};
+
+// Division by a runtime constant d >= 1 for 32-bit numerators: q = (umulhi(n, m) + n) >> s with
+// s = ceil(log2 d), m = floor(2^32 * (2^s - d) / d) + 1 (the round-up method of Granlund and Montgomery,
+// "Division by invariant integers using multiplication", PLDI 1994).  The sum is formed in 64 bits.
+struct FastDiv {
+    uint32_t d = 1, m = 1, s = 0;
+};
+
+inline FastDiv make_fastdiv(uint32_t d) {
+    FastDiv f;
+    f.d = d;
+    uint32_t s = 0;
+    while ((uint64_t(1) << s) < d) ++s;
+    f.s = s;
+    f.m = uint32_t(((uint64_t(1) << 32) * ((uint64_t(1) << s) - d)) / d + 1);
+    return f;
+}
+
+// One row of the handoff table (device-resident, 64 bytes).
+struct MoveRow {
+    int32_t kind;
+    int32_t aux;            // kKv*: source tokens (rows past them are zero-filled); kConv: history rows
+                            // (d_conv - 1) | 0x100 when the sequence is fresh (older history reads as zero)
+    uint64_t tile0;         // first global tile of this row
+    const uint8_t* src;
+    uint8_t* dst;
+    const int32_t* table;   // page table (destination side for kKv*/kPagesScatter, source side for kPagesGather)
+    uint64_t n;             // chunks (kKv*, kRec, kPages*, kCopy, kZero) or channels (kConv)
+    int64_t pos0;           // kKv*: first decode cell; kConv: rows available in the source
+    int64_t ld;             // kConv: source row stride in floats; kKv*, kPages*: physical pages in the pool
+};
+static_assert(sizeof(MoveRow) == 64, "handoff table rows are 64 bytes");
+
+// Geometry every row of one plan shares.
+struct MoveGeo {
+    FastDiv row_chunks;     // chunks per 512-byte-class row: D*2/16 (K/V) ...
+    FastDiv heads;          // n_head_kv
+    FastDiv page_size;      // cells per page
+    FastDiv rec_chunks;     // S*4/16
+    FastDiv v_heads;        // HV
+    FastDiv page_chunks;    // chunks per page: H*ps*D*2/16
+    uint32_t state;         // S
+    uint32_t pad;
+};
+
+}  // namespace sc

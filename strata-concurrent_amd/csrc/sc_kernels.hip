@@ -1,0 +1,365 @@
+// sc_kernels.hip - the CDNA4 (gfx950) kernels of the prefill->decode cache handoff.
+//
+// All of it is data movement, so every kernel here is bounded by HBM bandwidth, not by the matrix cores:
+//   * sc_move_kernel  - walks a handoff table (sc_internal.hpp) in 16 KiB tiles.  Every K/V, recurrence, page
+//                       and copy row moves whole 16-byte chunks: 64 lanes x 16 B = 1 KiB per wave instruction,
+//                       and a 512-byte pool row is one contiguous run on both sides, so both the loads and the
+//                       stores are fully coalesced without LDS.  The conv history is the one real transpose
+//                       ([rows][C] -> [C][3], 4-byte granules) and goes through LDS.
+//   * fill / generator kernels for synthetic inputs, and the decode probe used to measure overlap.
+//
+// The K/V address map is the reference's kv_append (src/prefill/kernels.cu:567-573): prefill token t of kv head
+// h goes to cell pos0 + t, i.e. pool row (table[cell / ps] * H + h) * ps + cell % ps; a negative table entry is
+// a page that is not resident and is skipped, as kv_append skips it (kernels.cu:577).  The recurrence map is
+// the (S, HV, S) layout of src/kernels/cuda/gdn.cu:75 (element (i, h, j) at i*HV*S + h*S + j), taken from a
+// head-major [HV][S][S] prefill image.  The history map is gdn_conv_hist_kernel (kernels.cu:219-228).
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "sc_internal.hpp"
+
+namespace sc {
+namespace {
+
+__device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv& f) {
+    const uint32_t hi = __umulhi(n, f.m);
+    return uint32_t((uint64_t(hi) + uint64_t(n)) >> f.s);
+}
+
+using u32x4 = __attribute__((ext_vector_type(4))) uint32_t;
+
+// Every buffer the handoff touches is global memory: say so, so the 16-byte accesses are global_load/store_dwordx4
+// rather than flat ones that also arbitrate for LDS.
+using gu32x4 = __attribute__((address_space(1))) u32x4;
+__device__ __forceinline__ u32x4 ld16(const uint8_t* p) { return *(const gu32x4*) (p); }
+__device__ __forceinline__ void st16(uint8_t* p, u32x4 v) { *(gu32x4*) (p) = v; }
+
+// IEEE-754 binary32 -> binary16, round to nearest even, as raw bits.  Finite values too large for f16 become
+// infinities, an f32 infinity stays one and a NaN becomes a quiet NaN (sign | 0x7C00 | 0x200), the convention
+// of the reference's f16_from_f32 (include/strata/kernels/f16_bits.hpp:37-70).  Written from the format
+// definition: keep 10 mantissa bits, round on the 13 dropped bits with ties to even, and in the subnormal range
+// shift the restored implicit bit right so the rounding point moves with the exponent.
+__device__ __forceinline__ uint32_t f16_bits_rne(uint32_t x) {
+    const uint32_t sign = (x >> 16) & 0x8000u;
+    const uint32_t e8 = (x >> 23) & 0xFFu;
+    uint32_t man = x & 0x7FFFFFu;
+    if (e8 == 0xFFu) return sign | 0x7C00u | (man ? 0x200u : 0u);
+    const int e = int(e8) - 112;   // rebias 127 -> 15
+    if (e >= 31) return sign | 0x7C00u;
+    if (e <= 0) {
+        if (e < -10) return sign;
+        man |= 0x800000u;
+        const uint32_t sh = uint32_t(14 - e);
+        uint32_t h = man >> sh;
+        const uint32_t rem = man & ((1u << sh) - 1u), half = 1u << (sh - 1);
+        h += (rem > half || (rem == half && (h & 1u))) ? 1u : 0u;
+        return sign | h;
+    }
+    uint32_t h = sign | (uint32_t(e) << 10) | (man >> 13);
+    const uint32_t rem = man & 0x1FFFu;
+    h += (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) ? 1u : 0u;
+    return h;
+}
+
+// Pool byte offset of (cell, head) for a K/V row; -1 when the page is not resident or out of the pool.
+__device__ __forceinline__ int64_t pool_row(const MoveRow& r, const MoveGeo& g, uint32_t src_row) {
+    const uint32_t t = fdiv(src_row, g.heads);
+    const uint32_t h = src_row - t * g.heads.d;
+    const int64_t cell = r.pos0 + int64_t(t);
+    const uint32_t page = fdiv(uint32_t(cell), g.page_size);
+    const uint32_t in_page = uint32_t(cell) - page * g.page_size.d;
+    int64_t phys = r.table ? int64_t(r.table[page]) : int64_t(page);
+    if (phys < 0 || phys >= r.ld) return -1;
+    return (phys * g.heads.d + h) * g.page_size.d + in_page;
+}
+
+__device__ void tile_kv16(const MoveRow& r, const MoveGeo& g, uint64_t local) {
+    const uint32_t row_bytes = g.row_chunks.d * 16u;
+    u32x4 v[kChunksPerThread];
+    uint32_t q[kChunksPerThread];
+#pragma unroll
+    for (int j = 0; j < kChunksPerThread; ++j) {
+        q[j] = uint32_t(local * kTileChunks) + uint32_t(j * kThreads) + threadIdx.x;
+        if (q[j] >= r.n) continue;
+        // rows past the source's tokens (an image's stale-cell tail) are written as zeros
+        const uint32_t t = fdiv(fdiv(q[j], g.row_chunks), g.heads);
+        v[j] = t < uint32_t(r.aux) ? ld16(r.src + uint64_t(q[j]) * 16u) : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int j = 0; j < kChunksPerThread; ++j) {
+        if (q[j] >= r.n) continue;
+        const uint32_t row = fdiv(q[j], g.row_chunks);
+        const uint32_t ch = q[j] - row * g.row_chunks.d;
+        const int64_t prow = pool_row(r, g, row);
+        if (prow >= 0) st16(r.dst + uint64_t(prow) * row_bytes + ch * 16u, v[j]);
+    }
+}
+
+__device__ void tile_kv32(const MoveRow& r, const MoveGeo& g, uint64_t local) {
+    const uint32_t row_bytes = g.row_chunks.d * 16u;
+#pragma unroll
+    for (int j = 0; j < kChunksPerThread; ++j) {
+        const uint32_t q = uint32_t(local * kTileChunks) + uint32_t(j * kThreads) + threadIdx.x;
+        if (q >= r.n) continue;
+        const uint32_t row = fdiv(q, g.row_chunks);
+        u32x4 o = {0u, 0u, 0u, 0u};
+        if (fdiv(row, g.heads) < uint32_t(r.aux)) {
+            // destination chunk q holds 8 halves = 32 source bytes at q * 32
+            const u32x4 a = ld16(r.src + uint64_t(q) * 32u);
+            const u32x4 b = ld16(r.src + uint64_t(q) * 32u + 16u);
+            o.x = f16_bits_rne(a.x) | (f16_bits_rne(a.y) << 16);
+            o.y = f16_bits_rne(a.z) | (f16_bits_rne(a.w) << 16);
+            o.z = f16_bits_rne(b.x) | (f16_bits_rne(b.y) << 16);
+            o.w = f16_bits_rne(b.z) | (f16_bits_rne(b.w) << 16);
+        }
+        const uint32_t ch = q - row * g.row_chunks.d;
+        const int64_t prow = pool_row(r, g, row);
+        if (prow >= 0) st16(r.dst + uint64_t(prow) * row_bytes + ch * 16u, o);
+    }
+}
+
+// Destination rows (i, h) of the (S, HV, S) recurrence, S*4 bytes each, read from head-major row h*S + i.
+__device__ void tile_rec(const MoveRow& r, const MoveGeo& g, uint64_t local) {
+    const uint32_t row_bytes = g.rec_chunks.d * 16u;
+    u32x4 v[kChunksPerThread];
+    uint32_t q[kChunksPerThread];
+#pragma unroll
+    for (int j = 0; j < kChunksPerThread; ++j) {
+        q[j] = uint32_t(local * kTileChunks) + uint32_t(j * kThreads) + threadIdx.x;
+        if (q[j] >= r.n) continue;
+        const uint32_t row = fdiv(q[j], g.rec_chunks);
+        const uint32_t ch = q[j] - row * g.rec_chunks.d;
+        const uint32_t i = fdiv(row, g.v_heads);
+        const uint32_t h = row - i * g.v_heads.d;
+        v[j] = ld16(r.src + (uint64_t(h) * g.state + i) * row_bytes + ch * 16u);
+    }
+#pragma unroll
+    for (int j = 0; j < kChunksPerThread; ++j)
+        if (q[j] < r.n) st16(r.dst + uint64_t(q[j]) * 16u, v[j]);
+}
+
+// Whole pages between a contiguous run and a paged pool.
+__device__ void tile_pages(const MoveRow& r, const MoveGeo& g, uint64_t local, bool scatter) {
+    const uint64_t page_bytes = uint64_t(g.page_chunks.d) * 16u;
+    u32x4 v[kChunksPerThread];
+    int64_t dst_off[kChunksPerThread];
+#pragma unroll
+    for (int j = 0; j < kChunksPerThread; ++j) {
+        dst_off[j] = -1;
+        const uint32_t q = uint32_t(local * kTileChunks) + uint32_t(j * kThreads) + threadIdx.x;
+        if (q >= r.n) continue;
+        const uint32_t page = fdiv(q, g.page_chunks);
+        const uint32_t ch = q - page * g.page_chunks.d;
+        const int64_t phys = r.table ? int64_t(r.table[page]) : int64_t(page);
+        if (phys < 0 || phys >= r.ld) continue;
+        const uint64_t pooled = uint64_t(phys) * page_bytes + ch * 16u;
+        const uint64_t packed = uint64_t(page) * page_bytes + ch * 16u;
+        v[j] = ld16(r.src + (scatter ? packed : pooled));
+        dst_off[j] = int64_t(scatter ? pooled : packed);
+    }
+#pragma unroll
+    for (int j = 0; j < kChunksPerThread; ++j)
+        if (dst_off[j] >= 0) st16(r.dst + dst_off[j], v[j]);
+}
+
+__device__ void tile_copy(const MoveRow& r, uint64_t local, bool zero) {
+    u32x4 v[kChunksPerThread];
+    uint64_t q[kChunksPerThread];
+#pragma unroll
+    for (int j = 0; j < kChunksPerThread; ++j) {
+        q[j] = local * kTileChunks + uint64_t(j * kThreads) + threadIdx.x;
+        if (q[j] < r.n) v[j] = zero ? u32x4{0u, 0u, 0u, 0u} : ld16(r.src + q[j] * 16u);
+    }
+#pragma unroll
+    for (int j = 0; j < kChunksPerThread; ++j)
+        if (q[j] < r.n) st16(r.dst + q[j] * 16u, v[j]);
+}
+
+// The conv history: channels [c0, c0 + kConvTileChannels) of history rows k = 0..hist-1, which are source rows
+// rows - hist + k.  For a source shorter than the history the older rows come from the previous history (read
+// before any of it is overwritten), or are zero for a fresh sequence, whose state starts zeroed.  Staged through
+// LDS so both the row reads and the interleaved [C][hist] writes are contiguous across lanes.
+__device__ void tile_conv(const MoveRow& r, uint64_t local, float (*lds)[kConvTileChannels]) {
+    const int hist = r.aux & 0xFF;
+    const bool fresh = ((r.aux >> 8) & 1) != 0;
+    const int64_t C = int64_t(r.n);
+    const int64_t c0 = int64_t(local) * kConvTileChannels;
+    const int64_t nc = C - c0 < kConvTileChannels ? C - c0 : kConvTileChannels;
+    const float* src = reinterpret_cast<const float*>(r.src);
+    float* dst = reinterpret_cast<float*>(r.dst);
+    for (int k = 0; k < hist; ++k) {
+        const int64_t t = r.pos0 - hist + k;
+        for (int64_t c = threadIdx.x; c < nc; c += kThreads)
+            lds[k][c] = t >= 0 ? src[t * r.ld + c0 + c] : fresh ? 0.0f : dst[(c0 + c) * hist + (t + hist)];
+    }
+    __syncthreads();
+    const int64_t n_out = nc * hist;
+    for (int64_t o = threadIdx.x; o < n_out; o += kThreads) {
+        const int64_t c = o / hist;
+        dst[c0 * hist + o] = lds[o - c * hist][c];
+    }
+    __syncthreads();
+}
+
+__device__ __forceinline__ int find_row(const uint64_t* tile0, int n_rows, uint64_t tile) {
+    int lo = 0, hi = n_rows - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (tile0[mid] <= tile) lo = mid; else hi = mid - 1;
+    }
+    return lo;
+}
+
+constexpr int kLdsRows = 1024;
+
+__global__ void __launch_bounds__(kThreads) sc_move_kernel(const MoveRow* __restrict__ rows, int n_rows,
+                                                            MoveGeo geo, uint64_t n_tiles) {
+    __shared__ uint64_t s_tile0[kLdsRows];
+    __shared__ float s_conv[kMaxHist][kConvTileChannels];
+    for (int i = threadIdx.x; i < n_rows; i += kThreads) s_tile0[i] = rows[i].tile0;
+    __syncthreads();
+    int cur = -1;
+    MoveRow r{};
+    for (uint64_t tile = blockIdx.x; tile < n_tiles; tile += gridDim.x) {
+        const int k = __builtin_amdgcn_readfirstlane(find_row(s_tile0, n_rows, tile));
+        if (k != cur) { cur = k; r = rows[k]; }
+        const uint64_t local = tile - r.tile0;
+        switch (r.kind) {
+            case kKv16: tile_kv16(r, geo, local); break;
+            case kKv32: tile_kv32(r, geo, local); break;
+            case kRec: tile_rec(r, geo, local); break;
+            case kConv: tile_conv(r, local, s_conv); break;
+            case kPagesScatter: tile_pages(r, geo, local, true); break;
+            case kPagesGather: tile_pages(r, geo, local, false); break;
+            case kCopy: tile_copy(r, local, false); break;
+            case kZero: tile_copy(r, local, true); break;
+            default: break;
+        }
+    }
+}
+
+// ---- synthetic inputs ----------------------------------------------------------------------------------------
+
+__device__ __forceinline__ uint64_t mix64(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+// Draw i of the stream keyed by `key` (SplitMix64 advanced i + 1 steps from the key).
+__device__ __forceinline__ uint64_t draw(uint64_t key, uint64_t i) { return mix64(key + (i + 1) * 0x9E3779B97F4A7C15ull); }
+
+__global__ void fill_uniform_f16_kernel(uint16_t* dst, uint64_t n, float lo, float span, uint64_t key) {
+    for (uint64_t i = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += uint64_t(gridDim.x) * blockDim.x) {
+        const float u = float(uint32_t(draw(key, i) >> 40)) * 0x1p-24f;
+        const float x = __builtin_fmaf(span, u, lo);
+        dst[i] = uint16_t(f16_bits_rne(__float_as_uint(x)));
+    }
+}
+
+__global__ void fill_uniform_f32_kernel(float* dst, uint64_t n, float lo, float span, uint64_t key) {
+    for (uint64_t i = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += uint64_t(gridDim.x) * blockDim.x) {
+        const float u = float(uint32_t(draw(key, i) >> 40)) * 0x1p-24f;
+        dst[i] = __builtin_fmaf(span, u, lo);
+    }
+}
+
+__global__ void fill_normal_f32_kernel(float* dst, uint64_t n, uint64_t key) {
+    for (uint64_t i = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += uint64_t(gridDim.x) * blockDim.x) {
+        int64_t sum = 0;
+#pragma unroll
+        for (int k = 0; k < 6; ++k) {
+            const uint64_t x = draw(key, i * 6 + k);
+            sum += int64_t(x >> 40) + int64_t((x >> 16) & 0xFFFFFFull);
+        }
+        dst[i] = float(int32_t(sum - (int64_t(6) << 24))) * 0x1p-24f;
+    }
+}
+
+__global__ void fill_bytes_kernel(uint8_t* dst, uint8_t value, uint64_t n) {
+    const uint64_t stride = uint64_t(gridDim.x) * blockDim.x;
+    const uint64_t head = (16u - (reinterpret_cast<uintptr_t>(dst) & 15u)) & 15u;
+    const uint64_t pre = head < n ? head : n;
+    const uint64_t gid = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (gid < pre) dst[gid] = value;
+    const uint64_t body = (n - pre) / 16;
+    const uint32_t w = uint32_t(value) * 0x01010101u;
+    const u32x4 v = {w, w, w, w};
+    for (uint64_t i = gid; i < body; i += stride) st16(dst + pre + i * 16, v);
+    const uint64_t tail0 = pre + body * 16;
+    for (uint64_t i = tail0 + gid; i < n; i += stride) dst[i] = value;
+}
+
+// Reads its share of the K/V bytes and folds them into one word per workgroup.
+__global__ void __launch_bounds__(kThreads) decode_probe_kernel(const uint8_t* kv, uint64_t n16, uint32_t* sink) {
+    uint32_t acc = 0;
+    for (uint64_t i = uint64_t(blockIdx.x) * kThreads + threadIdx.x; i < n16; i += uint64_t(gridDim.x) * kThreads) {
+        const u32x4 v = ld16(kv + i * 16);
+        acc ^= v.x ^ (v.y * 3u) ^ (v.z * 5u) ^ (v.w * 7u);
+    }
+    for (int o = 32; o > 0; o >>= 1) acc ^= __shfl_xor(acc, o);
+    __shared__ uint32_t s[kThreads / 64];
+    if ((threadIdx.x & 63) == 0) s[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) sink[blockIdx.x] = s[0] ^ s[1] ^ s[2] ^ s[3];
+}
+
+}  // namespace
+
+// ---- launchers (host) ------------------------------------------------------------------------------------------
+
+hipError_t launch_move(const MoveRow* rows, int n_rows, const MoveGeo& geo, uint64_t n_tiles, int64_t grid,
+                       hipStream_t stream) {
+    if (n_tiles == 0) return hipSuccess;
+    if (n_rows <= 0 || n_rows > kLdsRows) return hipErrorInvalidValue;
+    const uint64_t g = uint64_t(grid) < n_tiles ? uint64_t(grid) : n_tiles;
+    hipLaunchKernelGGL(sc_move_kernel, dim3(unsigned(g)), dim3(kThreads), 0, stream, rows, n_rows, geo, n_tiles);
+    return hipGetLastError();
+}
+
+static unsigned fill_grid(uint64_t n) {
+    const uint64_t b = (n + 255) / 256;
+    return unsigned(b < 8192 ? (b ? b : 1) : 8192);
+}
+
+uint64_t synth_key(uint64_t seed, uint64_t stream_id);
+
+hipError_t launch_fill_uniform_f16(uint16_t* dst, uint64_t n, float lo, float hi, uint64_t seed, uint64_t sid,
+                                   hipStream_t stream) {
+    if (!n) return hipSuccess;
+    hipLaunchKernelGGL(fill_uniform_f16_kernel, dim3(fill_grid(n)), dim3(256), 0, stream, dst, n, lo, hi - lo,
+                       synth_key(seed, sid));
+    return hipGetLastError();
+}
+
+hipError_t launch_fill_uniform_f32(float* dst, uint64_t n, float lo, float hi, uint64_t seed, uint64_t sid,
+                                   hipStream_t stream) {
+    if (!n) return hipSuccess;
+    hipLaunchKernelGGL(fill_uniform_f32_kernel, dim3(fill_grid(n)), dim3(256), 0, stream, dst, n, lo, hi - lo,
+                       synth_key(seed, sid));
+    return hipGetLastError();
+}
+
+hipError_t launch_fill_normal_f32(float* dst, uint64_t n, uint64_t seed, uint64_t sid, hipStream_t stream) {
+    if (!n) return hipSuccess;
+    hipLaunchKernelGGL(fill_normal_f32_kernel, dim3(fill_grid(n)), dim3(256), 0, stream, dst, n,
+                       synth_key(seed, sid));
+    return hipGetLastError();
+}
+
+hipError_t launch_fill_bytes(void* dst, uint8_t value, uint64_t n, hipStream_t stream) {
+    if (!n) return hipSuccess;
+    hipLaunchKernelGGL(fill_bytes_kernel, dim3(fill_grid(n / 16 + 16)), dim3(256), 0, stream,
+                       static_cast<uint8_t*>(dst), value, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_decode_probe(const void* kv, uint64_t n_bytes, uint32_t* sink, int64_t workgroups,
+                               hipStream_t stream) {
+    if (workgroups <= 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(decode_probe_kernel, dim3(unsigned(workgroups)), dim3(kThreads), 0, stream,
+                       static_cast<const uint8_t*>(kv), n_bytes / 16, sink);
+    return hipGetLastError();
+}
+
+}  // namespace sc

@@ -1,0 +1,109 @@
+"""The C-ABI library on the CPU: it loads, exports every entry point include/sc_handoff.h declares, and its host
+logic (layout arithmetic, refusals before any HIP call) matches the oracle and the reference's error contract.
+No test here makes a compute call: there is no GPU in this container."""
+import ctypes as C
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+
+
+def declared_symbols():
+    text = (ROOT / "include" / "sc_handoff.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(sc_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol(sc):
+    names = declared_symbols()
+    assert len(names) >= 30
+    for name in names:
+        assert hasattr(sc.lib, name), name
+    assert set(names) == set(sc.EXPORTS)
+
+
+def test_version(sc):
+    assert sc.lib.sc_version().decode().startswith("sc_handoff")
+
+
+def test_layout_arithmetic_matches_oracle(sc, oracle):
+    for kw in ({}, dict(n_layers=16), dict(ssm_v_heads=48, ssm_conv_channels=10240), dict(page_size=1)):
+        geo = sc.geometry(**kw)
+        for tokens in (0, 1, 3, 4, 5, 4096, 32768, 131071):
+            blobs, total = sc.image_layout(geo, tokens)
+            want, want_total = oracle.image_layout(geo, tokens)
+            assert total == want_total
+            assert [(b.kind, b.layer, b.offset, b.bytes) for b in blobs] == want
+            assert sc.payload_bytes(geo, tokens) == sum(b[3] for b in want)
+            assert sc.lib.sc_kv_cells(C.byref(geo), tokens) == oracle.lib.sco_cells(oracle.geometry_from(geo), tokens)
+        assert sc.lib.sc_gdn_row_floats(C.byref(geo)) == geo.gdn_row_floats
+        assert sc.lib.sc_n_qsa_layers(C.byref(geo)) == geo.n_layers // 4
+
+
+def _fake_slot(sc, geo, max_cells, n_pages):
+    # host addresses stand in for device pointers: every request below is refused before any HIP call
+    fake = 1 << 40
+    ks = (C.c_void_p * geo.n_qsa)(*[fake + 0x1000 * j for j in range(geo.n_qsa)])
+    vs = (C.c_void_p * geo.n_qsa)(*[fake + 0x100000 + 0x1000 * j for j in range(geo.n_qsa)])
+    slot = sc.DecodeSlot(n_pages=n_pages, max_cells=max_cells, k_pool=C.cast(ks, C.POINTER(C.c_void_p)),
+                         v_pool=C.cast(vs, C.POINTER(C.c_void_p)), page_table=None, gdn_state=fake + 0x200000)
+    return slot, (ks, vs)
+
+
+def _fake_view(sc, geo, tokens, pos0=0):
+    fake = 1 << 41
+    arr = lambda n, base: (C.c_void_p * max(n, 1))(*[base + 0x1000 * i for i in range(n)])
+    k, v, r, c = arr(geo.n_qsa, fake), arr(geo.n_qsa, fake + 1 << 30), arr(geo.n_gdn, fake + 2 << 30), \
+        arr(geo.n_gdn, fake + 3 << 30)
+    cast = lambda a: C.cast(a, C.POINTER(C.c_void_p))
+    view = sc.PrefillView(tokens=tokens, pos0=pos0, kv_dtype=0, with_gdn=1, k=cast(k), v=cast(v), rec=cast(r),
+                          conv=cast(c), conv_rows=3, conv_ld=geo.ssm_conv_channels)
+    return view, (k, v, r, c)
+
+
+@pytest.mark.parametrize("case", ["past_capacity", "pool_too_small", "bad_dtype", "missing_pool", "bad_geometry",
+                                  "short_conv_ld", "misaligned"])
+def test_carve_refusals_before_any_hip_call(sc, case):
+    geo = sc.geometry(n_layers=8)
+    slot, keep1 = _fake_slot(sc, geo, max_cells=64, n_pages=16)
+    view, keep2 = _fake_view(sc, geo, tokens=60)
+    if case == "past_capacity":
+        view.pos0 = 8                      # 8 + 60 > 64 cells
+    elif case == "pool_too_small":
+        slot.n_pages = 8                   # identity pools hold 32 cells < max_cells
+    elif case == "bad_dtype":
+        view.kv_dtype = 7
+    elif case == "missing_pool":
+        keep1[0][1] = None
+    elif case == "bad_geometry":
+        geo.head_dim = 12                  # 24-byte rows
+    elif case == "short_conv_ld":
+        view.conv_ld = geo.ssm_conv_channels - 1
+    elif case == "misaligned":
+        keep2[0][0] = (1 << 41) + 8
+    h = C.c_void_p()
+    rc = sc.lib.sc_plan_carve(C.byref(geo), C.byref(view), C.byref(slot), C.byref(h))
+    assert rc == sc.SC_EINVAL
+    assert h.value is None
+    msg = sc.last_error()
+    assert msg.startswith("conversation snapshot:") or msg.startswith("sc_handoff:")
+
+
+def test_image_refusals(sc):
+    geo = sc.geometry(n_layers=8)
+    slot, keep = _fake_slot(sc, geo, max_cells=64, n_pages=16)
+    _, total = sc.image_layout(geo, 60)
+    h = C.c_void_p()
+    # an image smaller than the layout is refused, the reference's "invalid K/V payload size"
+    assert sc.lib.sc_plan_scatter(C.byref(geo), 1 << 40, total - 64, 60, C.byref(slot), C.byref(h)) == sc.SC_EINVAL
+    assert "invalid K/V payload size" in sc.last_error()
+    # more tokens than the slot holds
+    assert sc.lib.sc_plan_scatter(C.byref(geo), 1 << 40, 1 << 40, 65, C.byref(slot), C.byref(h)) == sc.SC_EINVAL
+    assert sc.last_error() == "conversation snapshot: invalid K/V extent"
+    # park of a paged slot needs a capture first
+    tab = (C.c_void_p * 2)(1 << 42, None)
+    slot.page_table = C.cast(tab, C.POINTER(C.c_void_p))
+    assert sc.lib.sc_park_async(C.byref(geo), C.byref(slot), 60, 1 << 40, total, None, None) == sc.SC_EINVAL
+    assert "identity-layout" in sc.last_error()
