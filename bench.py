@@ -46,10 +46,9 @@ def cpu_model() -> str:
 def time_launches(plan, stream, steps: int, warmup: int, sc) -> tuple[float, list[float]]:
     """Warm up, then time exactly `steps` launches: total wall (ms) bracketed by synchronizes, and per-launch
     durations from event pairs recorded on the launch stream."""
-    import torch
     for _ in range(warmup):
         plan.launch(stream)
-    torch.cuda.synchronize()
+    sc.device_sync()
     starts = [sc.Event() for _ in range(steps)]
     ends = [sc.Event() for _ in range(steps)]
     t0 = time.perf_counter()
@@ -57,7 +56,7 @@ def time_launches(plan, stream, steps: int, warmup: int, sc) -> tuple[float, lis
         starts[i].record(stream)
         plan.launch(stream)
         ends[i].record(stream)
-    torch.cuda.synchronize()
+    sc.device_sync()
     wall_ms = (time.perf_counter() - t0) * 1e3
     per = [s.elapsed_ms(e) for s, e in zip(starts, ends)]
     return wall_ms, per
@@ -130,11 +129,12 @@ def main() -> int:
               "the handoff's sharding across GPUs is a design note, not a measured path", file=sys.stderr)
         return 2
 
-    import torch
     import sc_handoff as sc
 
-    torch.cuda.set_device(0)
-    stream = torch.cuda.current_stream()
+    if sc.device_count() < 1:
+        print("bench.py: no HIP device visible", file=sys.stderr)
+        return 1
+    stream = sc.Stream()   # every timed launch and its events go on this one non-blocking stream
     geo_kw = dict(n_layers=48, qsa_interval=4, n_head_kv=2, head_dim=256, page_size=4, ssm_state_size=128,
                   ssm_k_heads=16, ssm_v_heads=32, ssm_d_conv=4, ssm_conv_channels=8192, idx_key_dim=128)
     geo = sc.geometry(**geo_kw)
@@ -144,7 +144,7 @@ def main() -> int:
     log(f"config 3: {T} tokens, payload {P} B; generating inputs on the device")
     case = sc.SyntheticCase(geo, tokens=T, seed=0x5EED)
     slot = case.new_slot(max_cells=T)
-    torch.cuda.synchronize()
+    sc.device_sync()
     plan = sc.plan_carve(geo, case.prefill, slot)
     if args.grid:
         plan.set_grid(args.grid)
@@ -176,13 +176,13 @@ def main() -> int:
 
     # two-pass gather -> scatter through a transfer buffer (the cross-instance path)
     _, total = sc.image_layout(geo, T)
-    image = torch.empty(total, dtype=torch.uint8, device="cuda:0")
-    gather = sc.plan_gather(geo, case.prefill, image.data_ptr(), total)
-    scatter = sc.plan_scatter(geo, image.data_ptr(), total, T, slot)
+    image = sc.DeviceBuffer(total, "uint8")
+    gather = sc.plan_gather(geo, case.prefill, image.ptr, total)
+    scatter = sc.plan_scatter(geo, image.ptr, total, T, slot)
     for _ in range(2):
         gather.launch(stream)
         scatter.launch(stream)
-    torch.cuda.synchronize()
+    sc.device_sync()
     e = [sc.Event() for _ in range(3)]
     reps = 5
     g_ms = s_ms = 0.0
@@ -230,7 +230,7 @@ def main() -> int:
                   "pinned 256 MiB x 4 per direction"}
     log(f"park {pk:.1f} ms, resume {rs:.1f} ms; link d2h {d2h:.1f} GB/s, h2d {h2d:.1f} GB/s")
     host.free()
-    del image
+    image.free()
 
     # p50 latency of the 32K handoff (config 2): first enqueue to completion event
     TL = args.latency_tokens
@@ -238,10 +238,10 @@ def main() -> int:
     case_l = sc.SyntheticCase(geo, tokens=TL, seed=0x5EED + 1)
     slot_l = case_l.new_slot(max_cells=TL)
     plan_l = sc.plan_carve(geo, case_l.prefill, slot_l)
-    torch.cuda.synchronize()
+    sc.device_sync()
     for _ in range(3):
         plan_l.launch(stream)
-    torch.cuda.synchronize()
+    sc.device_sync()
     lat = []
     a, b = sc.Event(), sc.Event()
     for _ in range(args.latency_reps):

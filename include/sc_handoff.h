@@ -173,6 +173,8 @@ int sc_resume_async(const sc_geometry* g, const void* host_image, uint64_t image
 
 /* ---- runtime plumbing the C++ host layer calls instead of HIP ---------------------------------------------------- */
 
+/* Number of visible HIP devices (0 and SC_EHIP when the runtime finds none). */
+int sc_device_count(int* count);
 int sc_device_alloc(void** ptr, uint64_t bytes);
 int sc_device_free(void* ptr);
 /* Pinned host memory (hipHostMalloc): the park pool. */

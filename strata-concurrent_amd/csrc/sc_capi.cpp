@@ -555,6 +555,12 @@ int sc_resume_async(const sc_geometry* g, const void* host_image, uint64_t image
         if (e_ != hipSuccess) return hip_fail(e_, what);      \
     } while (0)
 
+int sc_device_count(int* count) {
+    if (!count) return fail(SC_EINVAL, "sc_handoff: missing output");
+    *count = 0;
+    SC_HIP(hipGetDeviceCount(count), "device count");
+    return ok();
+}
 int sc_device_alloc(void** ptr, uint64_t bytes) {
     if (!ptr) return fail(SC_EINVAL, "sc_handoff: missing pointer");
     const hipError_t e = hipMalloc(ptr, bytes ? bytes : 16);

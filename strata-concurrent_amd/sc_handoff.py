@@ -1,8 +1,8 @@
 """Python binding of libsc_handoff.so (include/sc_handoff.h) over ctypes, plus device-buffer helpers.
 
-PyTorch provides device memory and streams here and nothing else: every byte of the handoff is moved by the
-library's own HIP kernels and copies.  Importing this module loads the built library and fails loudly when it is
-missing - there is no fallback.
+Device memory, streams and events come from the library itself (hipMalloc / hipStreamCreate through its C-ABI), so
+a process that uses this module runs exactly one HIP runtime - the one the library links, as a C++ engine would.
+Importing this module loads the built library and fails loudly when it is missing: there is no fallback.
 """
 from __future__ import annotations
 
@@ -86,6 +86,7 @@ _SIGS = {
     "sc_plan_destroy": (C.c_int, [_P]),
     "sc_park_async": (C.c_int, [_GEO, C.POINTER(DecodeSlot), _I64, _P, _U64, _P, _P]),
     "sc_resume_async": (C.c_int, [_GEO, _P, _U64, _I64, C.POINTER(DecodeSlot), _P, _P]),
+    "sc_device_count": (C.c_int, [C.POINTER(C.c_int)]),
     "sc_device_alloc": (C.c_int, [C.POINTER(_P), _U64]),
     "sc_device_free": (C.c_int, [_P]),
     "sc_host_alloc": (C.c_int, [C.POINTER(_P), _U64]),
@@ -160,13 +161,75 @@ def _ptrs(values) -> C.Array:
 
 
 def _stream(stream) -> int | None:
-    """A raw hipStream_t from a torch stream, an int handle, or None (torch's current stream)."""
-    if stream is None:
-        import torch
-        return torch.cuda.current_stream().cuda_stream
-    if isinstance(stream, int):
+    """A raw hipStream_t: None is the null stream; a Stream or any object with a `handle`."""
+    if stream is None or isinstance(stream, int):
         return stream
-    return stream.cuda_stream
+    return stream.handle
+
+
+def device_count() -> int:
+    n = C.c_int(0)
+    return n.value if lib.sc_device_count(C.byref(n)) == SC_OK else 0
+
+
+def device_sync() -> None:
+    check(lib.sc_device_sync(), "sc_device_sync")
+
+
+class DeviceBuffer:
+    """Device memory from the library (hipMalloc): a pointer, a dtype and a shape, nothing more."""
+
+    def __init__(self, shape, dtype):
+        import numpy as np
+        self.shape = tuple(int(x) for x in (shape if isinstance(shape, (tuple, list)) else (shape,)))
+        self.dtype = np.dtype(dtype)
+        self.nbytes = int(np.prod(self.shape, dtype=np.int64)) * self.dtype.itemsize
+        p = C.c_void_p()
+        check(lib.sc_device_alloc(C.byref(p), max(self.nbytes, 16)), "sc_device_alloc")
+        self.ptr = p.value
+
+    def data_ptr(self) -> int:
+        return self.ptr
+
+    def numel(self) -> int:
+        return self.nbytes // self.dtype.itemsize
+
+    def offset(self, index: int) -> int:
+        """Address of flat element `index`."""
+        return self.ptr + index * self.dtype.itemsize
+
+    def fill(self, value: int, stream=None) -> None:
+        fill_bytes(self.ptr, value, self.nbytes, stream)
+
+    def numpy(self, count: int | None = None, start: int = 0):
+        """Synchronously copy elements [start, start + count) (default: all) to a new host array."""
+        import numpy as np
+        n = self.numel() - start if count is None else count
+        out = np.empty(max(n, 1), dtype=self.dtype)
+        if n:
+            check(lib.sc_copy_async(out.ctypes.data, self.offset(start), n * self.dtype.itemsize, None), "copy")
+            device_sync()
+        out = out[:n]
+        return out.reshape(self.shape) if count is None and start == 0 else out
+
+    def upload(self, array, start: int = 0) -> None:
+        import numpy as np
+        a = np.ascontiguousarray(array, dtype=self.dtype).reshape(-1)
+        if a.size:
+            check(lib.sc_copy_async(self.offset(start), a.ctypes.data, a.nbytes, None), "copy")
+            device_sync()
+
+    def free(self) -> None:
+        if self.ptr:
+            check(lib.sc_device_free(self.ptr), "sc_device_free")
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            if self.ptr:
+                lib.sc_device_free(self.ptr)
+        except Exception:
+            pass
 
 
 class Plan:
@@ -199,7 +262,7 @@ class Plan:
             pass
 
 
-# ---- device buffers (torch tensors as plain device memory) --------------------------------------------------------
+# ---- device buffers of the two layouts ------------------------------------------------------------------------------
 
 
 @dataclass
@@ -227,29 +290,15 @@ class PrefillBuffers:
         return view, (ks, vs, rs, cs)
 
     def host(self) -> dict:
-        """The inputs read back to numpy (K/V as raw f16 bits)."""
-        import numpy as np
-        out = {}
-        for name, ts in (("k", self.k), ("v", self.v)):
-            out[name] = [_host_bits(t) for t in ts]
-        out["rec"] = [t.cpu().numpy() for t in self.rec]
-        out["conv"] = [t.cpu().numpy() for t in self.conv]
-        out["tokens"] = self.tokens
-        out["conv_rows"] = self.conv_rows
-        out["kv_dtype"] = self.kv_dtype
-        return out
-
-
-def _host_bits(t):
-    import torch
-    if t.dtype == torch.float16:
-        return t.view(torch.int16).cpu().numpy().view("uint16")
-    return t.cpu().numpy()
+        """The inputs read back to numpy (K/V as raw f16 bits, or f32)."""
+        return {"k": [t.numpy() for t in self.k], "v": [t.numpy() for t in self.v],
+                "rec": [t.numpy() for t in self.rec], "conv": [t.numpy() for t in self.conv],
+                "tokens": self.tokens, "conv_rows": self.conv_rows, "kv_dtype": self.kv_dtype}
 
 
 @dataclass
 class Slot:
-    """A decode slot: per QSA layer K/V pools [n_pages][H][ps][D] f16, optional page tables, and the GDN rows."""
+    """A decode slot: per QSA layer K/V pools [n_pages][H][ps][D] f16 bits, optional page tables, the GDN rows."""
     geo: Geometry
     n_pages: int
     max_cells: int
@@ -269,30 +318,46 @@ class Slot:
                           page_table=C.cast(ts, C.POINTER(C.c_void_p)) if ts is not None else None,
                           gdn_state=self.gdn.data_ptr() if self.gdn is not None else None)
 
+    def buffers(self) -> list:
+        return [*self.k_pool, *self.v_pool, *([self.gdn] if self.gdn is not None else [])]
+
+    def fill(self, value: int) -> None:
+        for b in self.buffers():
+            b.fill(value)
+
     def host_state(self) -> dict:
-        import numpy as np
-        out = {}
-        for j, t in enumerate(self.k_pool):
-            out[f"k{j}"] = _host_bits(t)
-        for j, t in enumerate(self.v_pool):
-            out[f"v{j}"] = _host_bits(t)
+        out = {f"k{j}": t.numpy() for j, t in enumerate(self.k_pool)}
+        out.update({f"v{j}": t.numpy() for j, t in enumerate(self.v_pool)})
         if self.gdn is not None:
-            out["gdn"] = self.gdn.cpu().numpy()
+            out["gdn"] = self.gdn.numpy()
         return out
 
 
-def new_slot(geo: Geometry, max_cells: int, device="cuda:0", n_pages: int | None = None, tables=None,
-             fill: int = 0) -> Slot:
-    import torch
+def new_slot(geo: Geometry, max_cells: int, n_pages: int | None = None, tables=None, fill: int = 0) -> Slot:
     ps = geo.page_size
     n_pages = n_pages if n_pages is not None else (max_cells + ps - 1) // ps
     shape = (n_pages, geo.n_head_kv, ps, geo.head_dim)
-    k = [torch.empty(shape, dtype=torch.float16, device=device) for _ in range(geo.n_qsa)]
-    v = [torch.empty(shape, dtype=torch.float16, device=device) for _ in range(geo.n_qsa)]
-    gdn = torch.empty((geo.n_gdn, geo.gdn_row_floats), dtype=torch.float32, device=device) if geo.n_gdn else None
-    for t in [*k, *v, *([gdn] if gdn is not None else [])]:
-        fill_bytes(t.data_ptr(), fill, t.numel() * t.element_size())
-    return Slot(geo, n_pages, max_cells, k, v, gdn, tables)
+    k = [DeviceBuffer(shape, "uint16") for _ in range(geo.n_qsa)]
+    v = [DeviceBuffer(shape, "uint16") for _ in range(geo.n_qsa)]
+    gdn = DeviceBuffer((geo.n_gdn, geo.gdn_row_floats), "float32") if geo.n_gdn else None
+    slot = Slot(geo, n_pages, max_cells, k, v, gdn, tables)
+    slot.fill(fill)
+    return slot
+
+
+def device_tables(tables) -> list | None:
+    """Upload host page tables (one int32 array per QSA layer, or None for identity)."""
+    if tables is None:
+        return None
+    out = []
+    for t in tables:
+        if t is None:
+            out.append(None)
+            continue
+        b = DeviceBuffer(len(t), "int32")
+        b.upload(t)
+        out.append(b)
+    return out
 
 
 def fill_bytes(ptr: int, value: int, nbytes: int, stream=None) -> None:
@@ -306,32 +371,31 @@ def sid_rec(i: int) -> int: return 5000 + i
 def sid_conv(i: int) -> int: return 9000 + i
 
 
-def synthetic_prefill(geo: Geometry, tokens: int, seed: int, device="cuda:0", kv_dtype: int = SC_DTYPE_F16,
-                      conv_rows: int | None = None) -> PrefillBuffers:
+def synthetic_prefill(geo: Geometry, tokens: int, seed: int, kv_dtype: int = SC_DTYPE_F16,
+                      conv_rows: int | None = None, stream=None) -> PrefillBuffers:
     """K/V ~ U[-4, 4] (f16, or f32 when kv_dtype is F32), recurrence and conv rows ~ N(0, 1) (Irwin-Hall 12),
     generated on the device by the library's counter-based generators."""
-    import torch
     H, D = geo.n_head_kv, geo.head_dim
     S, HV, Cc = geo.ssm_state_size, geo.ssm_v_heads, geo.ssm_conv_channels
     conv_rows = min(tokens, geo.ssm_d_conv - 1) if conv_rows is None else conv_rows
-    stream = _stream(None)
+    s = _stream(stream)
     ks, vs, recs, convs = [], [], [], []
-    kv_t = torch.float16 if kv_dtype == SC_DTYPE_F16 else torch.float32
     for j in range(geo.n_qsa):
         for lst, sid in ((ks, sid_k(j)), (vs, sid_v(j))):
-            t = torch.empty((max(tokens, 1), H, D), dtype=kv_t, device=device)
             n = tokens * H * D
             if kv_dtype == SC_DTYPE_F16:
-                check(lib.sc_fill_uniform_f16(t.data_ptr(), n, -4.0, 4.0, seed, sid, stream), "fill")
+                t = DeviceBuffer((max(tokens, 1), H, D), "uint16")
+                check(lib.sc_fill_uniform_f16(t.ptr, n, -4.0, 4.0, seed, sid, s), "fill")
             else:
-                check(lib.sc_fill_uniform_f32(t.data_ptr(), n, -4.0, 4.0, seed, sid, stream), "fill")
+                t = DeviceBuffer((max(tokens, 1), H, D), "float32")
+                check(lib.sc_fill_uniform_f32(t.ptr, n, -4.0, 4.0, seed, sid, s), "fill")
             lst.append(t)
     for i in range(geo.n_gdn):
-        r = torch.empty((HV, S, S), dtype=torch.float32, device=device)
-        check(lib.sc_fill_normal_f32(r.data_ptr(), r.numel(), seed, sid_rec(i), stream), "fill")
+        r = DeviceBuffer((HV, S, S), "float32")
+        check(lib.sc_fill_normal_f32(r.ptr, r.numel(), seed, sid_rec(i), s), "fill")
         recs.append(r)
-        c = torch.empty((max(conv_rows, 1), Cc), dtype=torch.float32, device=device)
-        check(lib.sc_fill_normal_f32(c.data_ptr(), conv_rows * Cc, seed, sid_conv(i), stream), "fill")
+        c = DeviceBuffer((max(conv_rows, 1), Cc), "float32")
+        check(lib.sc_fill_normal_f32(c.ptr, conv_rows * Cc, seed, sid_conv(i), s), "fill")
         convs.append(c)
     return PrefillBuffers(geo, tokens, ks, vs, recs, convs, conv_rows, kv_dtype)
 
@@ -339,18 +403,17 @@ def synthetic_prefill(geo: Geometry, tokens: int, seed: int, device="cuda:0", kv
 class SyntheticCase:
     """A seeded prefill sequence on the device plus the helpers smoke() and the tests use."""
 
-    def __init__(self, geo: Geometry, tokens: int, seed: int, device="cuda:0", kv_dtype: int = SC_DTYPE_F16):
-        self.geo, self.tokens, self.seed, self.device = geo, tokens, seed, device
-        self.prefill = synthetic_prefill(geo, tokens, seed, device, kv_dtype)
+    def __init__(self, geo: Geometry, tokens: int, seed: int, kv_dtype: int = SC_DTYPE_F16):
+        self.geo, self.tokens, self.seed = geo, tokens, seed
+        self.prefill = synthetic_prefill(geo, tokens, seed, kv_dtype)
 
     def new_slot(self, max_cells: int, **kw) -> Slot:
-        return new_slot(self.geo, max_cells, self.device, **kw)
+        return new_slot(self.geo, max_cells, **kw)
 
     def carve_into(self, slot: Slot, pos0: int = 0, stream=None) -> None:
         plan = plan_carve(self.geo, self.prefill, slot, pos0)
         plan.launch(stream)
-        import torch
-        torch.cuda.synchronize()
+        device_sync()
         plan.destroy()
 
     def host_inputs(self) -> dict:

@@ -19,17 +19,17 @@ TOY = dict(n_layers=16)   # config 1: 4 QSA + 12 GDN layers at the configs' per-
 
 
 def _sync():
-    import torch
-    torch.cuda.synchronize()
+    import sc_handoff
+    sc_handoff.device_sync()
 
 
 def _device_u8(nbytes):
-    import torch
-    return torch.empty(max(nbytes, 16), dtype=torch.uint8, device="cuda:0")
+    import sc_handoff
+    return sc_handoff.DeviceBuffer(max(nbytes, 16), "uint8")
 
 
-def _tables(kind, n_qsa, n_pages, device="cuda:0"):
-    import torch
+def _tables(kind, n_qsa, n_pages):
+    import sc_handoff
     if kind == "identity":
         return None, None
     if kind == "reversed":
@@ -41,8 +41,7 @@ def _tables(kind, n_qsa, n_pages, device="cuda:0"):
         t = np.random.default_rng(n_pages).permutation(n_pages).astype(np.int32)
     else:
         raise ValueError(kind)
-    dev = [torch.from_numpy(t).to(device) for _ in range(n_qsa)]
-    return dev, [t] * n_qsa
+    return sc_handoff.device_tables([t] * n_qsa), [t] * n_qsa
 
 
 def _compare(want, got):
@@ -58,19 +57,16 @@ def _compare(want, got):
 
 @pytest.mark.parametrize("n", [1, 1000, 4097, 1 << 20])
 def test_device_generators_match_oracle(sc, oracle, cuda, n):
-    import torch
-    stream = torch.cuda.current_stream().cuda_stream
-    a = torch.empty(n, dtype=torch.float16, device=cuda)
-    sc.check(sc.lib.sc_fill_uniform_f16(a.data_ptr(), n, -4.0, 4.0, 0x5EED, 17, stream), "fill")
-    b = torch.empty(n, dtype=torch.float32, device=cuda)
-    sc.check(sc.lib.sc_fill_normal_f32(b.data_ptr(), n, 0x5EED, 18, stream), "fill")
-    c = torch.empty(n, dtype=torch.float32, device=cuda)
-    sc.check(sc.lib.sc_fill_uniform_f32(c.data_ptr(), n, -4.0, 4.0, 99, 3, stream), "fill")
+    a = sc.DeviceBuffer(n, "uint16")
+    sc.check(sc.lib.sc_fill_uniform_f16(a.ptr, n, -4.0, 4.0, 0x5EED, 17, None), "fill")
+    b = sc.DeviceBuffer(n, "float32")
+    sc.check(sc.lib.sc_fill_normal_f32(b.ptr, n, 0x5EED, 18, None), "fill")
+    c = sc.DeviceBuffer(n, "float32")
+    sc.check(sc.lib.sc_fill_uniform_f32(c.ptr, n, -4.0, 4.0, 99, 3, None), "fill")
     _sync()
-    assert np.array_equal(a.view(torch.int16).cpu().numpy().view(np.uint16),
-                          oracle.fill_uniform_f16(n, -4.0, 4.0, 0x5EED, 17))
-    assert np.array_equal(b.cpu().numpy().view(np.uint32), oracle.fill_normal_f32(n, 0x5EED, 18).view(np.uint32))
-    assert np.array_equal(c.cpu().numpy().view(np.uint32), oracle.fill_uniform_f32(n, -4.0, 4.0, 99, 3).view(np.uint32))
+    assert np.array_equal(a.numpy(), oracle.fill_uniform_f16(n, -4.0, 4.0, 0x5EED, 17))
+    assert np.array_equal(b.numpy().view(np.uint32), oracle.fill_normal_f32(n, 0x5EED, 18).view(np.uint32))
+    assert np.array_equal(c.numpy().view(np.uint32), oracle.fill_uniform_f32(n, -4.0, 4.0, 99, 3).view(np.uint32))
 
 
 # ---- the fused carve -> scatter, every byte against the oracle -----------------------------------------------------
@@ -135,7 +131,7 @@ def test_gather_then_scatter(sc, oracle, cuda, tokens, table):
     case = sc.SyntheticCase(geo, tokens=tokens, seed=tokens)
     _, total = sc.image_layout(geo, tokens)
     image = _device_u8(total)
-    sc.fill_bytes(image.data_ptr(), 0xEE, image.numel())
+    image.fill(0xEE)
     gather = sc.plan_gather(geo, case.prefill, image.data_ptr(), total)
     gather.launch()
     _sync()
@@ -143,7 +139,7 @@ def test_gather_then_scatter(sc, oracle, cuda, tokens, table):
     cells = geo.cells(tokens)
     expected = oracle.expected_slot(geo, case.host_inputs(), slot_cells=cells)
     want_image = oracle.park(geo, tokens, expected)
-    got_image = image[:total].cpu().numpy()
+    got_image = image.numpy(total)
     assert np.array_equal(got_image, want_image)
     # scatter into a decode slot (possibly paged) == the fused carve into the same kind of slot
     max_cells = cells + 8
@@ -171,7 +167,7 @@ def test_capture_reads_through_the_page_table(sc, oracle, cuda, table):
     case.carve_into(slot)
     _, total = sc.image_layout(geo, tokens)
     image = _device_u8(total)
-    sc.fill_bytes(image.data_ptr(), 0x11, image.numel())
+    image.fill(0x11)
     plan = sc.plan_capture(geo, slot, tokens, image.data_ptr(), total)
     plan.launch()
     _sync()
@@ -185,7 +181,7 @@ def test_capture_reads_through_the_page_table(sc, oracle, cuda, table):
             continue
         order = np.arange(cells // geo.page_size) if host_tabs is None else host_tabs[0][: cells // geo.page_size]
         logical[key] = np.ascontiguousarray(pool[order])
-    assert np.array_equal(image[:total].cpu().numpy(), oracle.park(geo, tokens, logical))
+    assert np.array_equal(image.numpy(total), oracle.park(geo, tokens, logical))
 
 
 # ---- park / resume: pinned host RAM on a side stream ---------------------------------------------------------------
@@ -206,7 +202,7 @@ def test_park_resume_round_trip(sc, oracle, cuda):
     state = slot.host_state()
     assert np.array_equal(host.numpy(), oracle.park(geo, tokens, state))
     fresh = case.new_slot(max_cells=4096, fill=0x5A)
-    _sync()   # the fill ran on torch's stream; the side stream does not wait for it
+    _sync()   # the fill ran on the null stream; the non-blocking side stream does not wait for it
     sc.resume_async(geo, host.ptr, total, tokens, fresh, stream=side, done=done.handle)
     done.sync()
     got = fresh.host_state()
@@ -244,38 +240,41 @@ def test_refusal_writes_nothing(sc, cuda):
 
 # ---- full-depth configs: size-independent properties ----------------------------------------------------------------
 
-def _sampled_rows_check(sc, oracle, geo, case, slot, n_samples=2048, seed=0):
-    """Sampled K/V rows and recurrence rows sit where the reference's closed forms put them; the whole conv history
-    of every GDN layer matches the oracle."""
-    import torch
+def _sampled_rows_check(sc, oracle, geo, case, slot, n_samples=4096, seed=0):
+    """Sampled K/V rows and recurrence rows sit where the reference's closed forms put them (kv_append's row for
+    cell t of head h: page t // ps, in-page t % ps; the recurrence's (i, h) row of (S, HV, S)); the whole conv
+    history of every GDN layer matches the oracle."""
     rng = np.random.default_rng(seed)
     T, H, ps, S, HV = case.tokens, geo.n_head_kv, geo.page_size, geo.ssm_state_size, geo.ssm_v_heads
-    for _ in range(4):
-        j = int(rng.integers(geo.n_qsa))
-        t = torch.from_numpy(rng.integers(0, T, size=n_samples)).to("cuda:0")
-        h = torch.from_numpy(rng.integers(0, H, size=n_samples)).to("cuda:0")
+    for j in rng.choice(geo.n_qsa, size=3, replace=False):
+        t = rng.integers(0, T, size=n_samples)
+        h = rng.integers(0, H, size=n_samples)
         for src, pool in ((case.prefill.k[j], slot.k_pool[j]), (case.prefill.v[j], slot.v_pool[j])):
-            want = src[t, h].cpu()
-            got = pool[t // ps, h, t % ps].cpu()          # kv_append's row for cell t (identity table)
-            assert torch.equal(want.view(torch.int16), got.view(torch.int16))
-    for _ in range(4):
-        g = int(rng.integers(geo.n_gdn))
-        i = torch.from_numpy(rng.integers(0, S, size=n_samples)).to("cuda:0")
-        hv = torch.from_numpy(rng.integers(0, HV, size=n_samples)).to("cuda:0")
-        rec = slot.gdn[g, : S * HV * S].view(S, HV, S)
-        assert torch.equal(case.prefill.rec[g][hv, i].view(torch.int32), rec[i, hv].view(torch.int32))
+            src_h, pool_h = src.numpy(), pool.numpy()
+            assert np.array_equal(src_h[t, h], pool_h[t // ps, h, t % ps])
+    for g in rng.choice(geo.n_gdn, size=4, replace=False):
+        i = rng.integers(0, S, size=n_samples)
+        hv = rng.integers(0, HV, size=n_samples)
+        rec = slot.gdn.numpy(S * HV * S, int(g) * geo.gdn_row_floats).reshape(S, HV, S)
+        src = case.prefill.rec[g].numpy()
+        assert np.array_equal(src[hv, i].view(np.uint32), rec[i, hv].view(np.uint32))
     Cc, nh = geo.ssm_conv_channels, geo.ssm_d_conv - 1
+    gdn = slot.gdn.numpy()
     for g in range(geo.n_gdn):
         hist = np.zeros((Cc, nh), dtype=np.float32)
-        oracle.conv_hist(hist, case.prefill.conv[g].cpu().numpy(), case.prefill.conv_rows, Cc, Cc, nh, True)
-        got = slot.gdn[g, S * HV * S:].cpu().numpy()
-        assert np.array_equal(got.view(np.uint32), hist.reshape(-1).view(np.uint32))
+        oracle.conv_hist(hist, case.prefill.conv[g].numpy(), case.prefill.conv_rows, Cc, Cc, nh, True)
+        assert np.array_equal(gdn[g, S * HV * S:].view(np.uint32), hist.reshape(-1).view(np.uint32))
+
+
+def _equal_buffers(a_list, b_list):
+    for a, b in zip(a_list, b_list):
+        assert a.nbytes == b.nbytes
+        assert np.array_equal(a.numpy().view(np.uint8), b.numpy().view(np.uint8))
 
 
 @pytest.mark.parametrize("tokens", [32768, 131072])
 def test_full_depth_properties(sc, oracle, cuda, tokens):
     """Configs 2 and 3: 48 layers (12 QSA, 36 GDN) at 32K and 128K tokens."""
-    import torch
     geo = sc.geometry()
     case = sc.SyntheticCase(geo, tokens=tokens, seed=0x5EED + tokens)
     fused = case.new_slot(max_cells=tokens)
@@ -285,29 +284,23 @@ def test_full_depth_properties(sc, oracle, cuda, tokens):
     _, total = sc.image_layout(geo, tokens)
     assert total == sc.payload_bytes(geo, tokens)
     image = _device_u8(total)
-    gather = sc.plan_gather(geo, case.prefill, image.data_ptr(), total)
+    gather = sc.plan_gather(geo, case.prefill, image.ptr, total)
     gather.launch()
     two_pass = case.new_slot(max_cells=tokens, fill=0x33)
-    scatter = sc.plan_scatter(geo, image.data_ptr(), total, tokens, two_pass)
+    scatter = sc.plan_scatter(geo, image.ptr, total, tokens, two_pass)
     scatter.launch()
     _sync()
-    for a, b in zip(fused.k_pool + fused.v_pool + [fused.gdn], two_pass.k_pool + two_pass.v_pool + [two_pass.gdn]):
-        assert torch.equal(a.view(torch.uint8), b.view(torch.uint8))
-    # park -> resume round trip through pinned host memory
+    _equal_buffers(fused.buffers(), two_pass.buffers())
+    # park -> resume round trip through pinned host memory on a side stream
     host = sc.PinnedBuffer(total)
     side = sc.Stream()
     done = sc.Event()
     sc.park_async(geo, fused, tokens, host.ptr, total, stream=side, done=done.handle)
     done.sync()
-    back = torch.from_numpy(host.numpy()).to("cuda:0")
-    assert torch.equal(back, image[:total])          # the parked image is the gathered transfer buffer
-    del back
-    sc.fill_bytes(two_pass.gdn.data_ptr(), 0, two_pass.gdn.numel() * 4)
-    for t in two_pass.k_pool + two_pass.v_pool:
-        sc.fill_bytes(t.data_ptr(), 0, t.numel() * 2)
+    assert np.array_equal(host.numpy(), image.numpy(total))   # the parked image is the gathered transfer buffer
+    two_pass.fill(0)
     _sync()
     sc.resume_async(geo, host.ptr, total, tokens, two_pass, stream=side, done=done.handle)
     done.sync()
-    for a, b in zip(fused.k_pool + fused.v_pool + [fused.gdn], two_pass.k_pool + two_pass.v_pool + [two_pass.gdn]):
-        assert torch.equal(a.view(torch.uint8), b.view(torch.uint8))
+    _equal_buffers(fused.buffers(), two_pass.buffers())
     host.free()
