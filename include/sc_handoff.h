@@ -171,10 +171,41 @@ int sc_park_async(const sc_geometry* g, const sc_decode_slot* slot, int64_t toke
 int sc_resume_async(const sc_geometry* g, const void* host_image, uint64_t image_bytes, int64_t tokens,
                     const sc_decode_slot* slot, void* stream, void* done);
 
+/* ---- block movers of streamed and ring K/V layers ---------------------------------------------------------------- */
+
+/* The per-block byte runs of up to four pool arrays: block b of array i is bytes [b*len[i], (b+1)*len[i]) of
+ * src[i] (the host copy, a device-mapped pinned pointer) and of dst[i] (the VRAM slots).  The reference's `Runs`
+ * (src/kernels/cuda/kv_stream.cu:26-55): f16 K and V; int8 codes and scales; q4 codes. */
+typedef struct sc_kv_runs {
+    const void* src[4];
+    void* dst[4];
+    uint64_t len[4];
+    int32_t n;
+} sc_kv_runs;
+
+/* Blocks [b0, b1) of the host copy into ring slots b % n_slots, as hipMemcpyAsync runs up to the ring's end.
+ * Replaces kv_ring_restore (include/strata/kernels/kv_stream.hpp:78-81, src/kernels/cuda/kv_stream.cu:231-242). */
+int sc_kv_ring_restore(const sc_kv_runs* runs, int64_t b0, int64_t b1, int64_t n_slots, void* stream);
+/* The first n_blocks blocks of the host copy into an identity-layout pool.  Replaces kv_stage_from_host
+ * (kv_stream.hpp:83-86, kv_stream.cu:244-252). */
+int sc_kv_stage_from_host(const sc_kv_runs* runs, int64_t n_blocks, void* stream);
+/* The static ring table block -> block % n_slots.  Replaces kv_ring_table (kv_stream.hpp:75-76, kv_stream.cu:226-229). */
+int sc_kv_ring_table(int32_t* page_table, int64_t n_blocks, int64_t n_slots, void* stream);
+/* Evicts every block of a streamed layer: page table -1, slots free (block -1, stamp -1, ref 0), the 16 control
+ * ints zero.  Replaces kv_stream_reset (kv_stream.hpp:65-66, kv_stream.cu:173-182,199-202). */
+int sc_kv_stream_reset(int32_t* page_table, int64_t n_blocks, int32_t* slot_block, int32_t* slot_stamp,
+                       int32_t* slot_ref, int64_t n_slots, int32_t* ctl, void* stream);
+/* Bytes of one block (page) of K and V together.  Replaces kv_block_bytes (kv_stream.hpp:95-96). */
+uint64_t sc_kv_block_bytes(int64_t n_head_kv, int64_t head_dim, int64_t page_size, int32_t format);
+
 /* ---- runtime plumbing the C++ host layer calls instead of HIP ---------------------------------------------------- */
 
 /* Number of visible HIP devices (0 and SC_EHIP when the runtime finds none). */
 int sc_device_count(int* count);
+/* The calling thread's current device, and making one current (hipGetDevice / hipSetDevice): what a layer-split
+ * caller's OnDevice scope (include/strata/core/on_device.hpp:10-20) needs. */
+int sc_get_device(int* device);
+int sc_set_device(int device);
 int sc_device_alloc(void** ptr, uint64_t bytes);
 int sc_device_free(void* ptr);
 /* Pinned host memory (hipHostMalloc): the park pool. */

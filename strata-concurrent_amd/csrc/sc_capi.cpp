@@ -30,6 +30,9 @@ hipError_t launch_fill_normal_f32(float* dst, uint64_t n, uint64_t seed, uint64_
 hipError_t launch_fill_bytes(void* dst, uint8_t value, uint64_t n, hipStream_t stream);
 hipError_t launch_decode_probe(const void* kv, uint64_t n_bytes, uint32_t* sink, int64_t workgroups,
                                hipStream_t stream);
+hipError_t launch_stream_reset(int32_t* table, int64_t n_blocks, int32_t* slot_block, int32_t* slot_stamp,
+                               int32_t* slot_ref, int64_t n_slots, int32_t* ctl, hipStream_t stream);
+hipError_t launch_ring_table(int32_t* table, int64_t n_blocks, int64_t n_slots, hipStream_t stream);
 
 static uint64_t host_mix64(uint64_t z) {
     z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
@@ -496,6 +499,12 @@ int sc_plan_destroy(sc_plan* plan) {
     return e == hipSuccess ? ok() : hip_fail(e, "table free");
 }
 
+#define SC_HIP(call, what)                                    \
+    do {                                                      \
+        const hipError_t e_ = (call);                         \
+        if (e_ != hipSuccess) return hip_fail(e_, what);      \
+    } while (0)
+
 // ---- park / resume --------------------------------------------------------------------------------------------
 
 static int dma_image(const sc_geometry* g, const sc_decode_slot* slot, int64_t tokens, uint8_t* host,
@@ -559,18 +568,81 @@ int sc_resume_async(const sc_geometry* g, const void* host_image, uint64_t image
     });
 }
 
-// ---- plumbing --------------------------------------------------------------------------------------------------
+// ---- block movers ----------------------------------------------------------------------------------------------
 
-#define SC_HIP(call, what)                                    \
-    do {                                                      \
-        const hipError_t e_ = (call);                         \
-        if (e_ != hipSuccess) return hip_fail(e_, what);      \
-    } while (0)
+static int check_runs(const sc_kv_runs* r) {
+    if (!r || r->n < 1 || r->n > 4) return fail(SC_EINVAL, "sc_handoff: invalid block runs");
+    for (int a = 0; a < r->n; ++a)
+        if (!r->src[a] || !r->dst[a] || !r->len[a]) return fail(SC_EINVAL, "sc_handoff: invalid block runs");
+    return SC_OK;
+}
+
+int sc_kv_ring_restore(const sc_kv_runs* runs, int64_t b0, int64_t b1, int64_t n_slots, void* stream) {
+    if (int rc = check_runs(runs)) return rc;
+    if (b0 < 0 || b1 < b0 || n_slots < 1) return fail(SC_EINVAL, "sc_handoff: invalid ring range");
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    for (int64_t b = b0; b < b1;) {
+        const int64_t slot = b % n_slots, run = std::min<int64_t>(b1 - b, n_slots - slot);   // up to the ring's end
+        for (int a = 0; a < runs->n; ++a) {
+            const uint64_t len = runs->len[a];
+            const hipError_t e = hipMemcpyAsync(static_cast<uint8_t*>(runs->dst[a]) + uint64_t(slot) * len,
+                                                static_cast<const uint8_t*>(runs->src[a]) + uint64_t(b) * len,
+                                                uint64_t(run) * len, hipMemcpyDefault, s);
+            if (e != hipSuccess) return hip_fail(e, "ring restore");
+        }
+        b += run;
+    }
+    return ok();
+}
+
+int sc_kv_stage_from_host(const sc_kv_runs* runs, int64_t n_blocks, void* stream) {
+    if (n_blocks <= 0) return ok();
+    if (int rc = check_runs(runs)) return rc;
+    for (int a = 0; a < runs->n; ++a) {
+        const hipError_t e = hipMemcpyAsync(runs->dst[a], runs->src[a], uint64_t(n_blocks) * runs->len[a],
+                                            hipMemcpyDefault, static_cast<hipStream_t>(stream));
+        if (e != hipSuccess) return hip_fail(e, "stage");
+    }
+    return ok();
+}
+
+int sc_kv_ring_table(int32_t* page_table, int64_t n_blocks, int64_t n_slots, void* stream) {
+    if (n_blocks < 0 || n_slots < 1 || (n_blocks && !page_table)) return fail(SC_EINVAL, "sc_handoff: invalid ring table");
+    SC_HIP(sc::launch_ring_table(page_table, n_blocks, n_slots, static_cast<hipStream_t>(stream)), "ring table");
+    return ok();
+}
+
+int sc_kv_stream_reset(int32_t* page_table, int64_t n_blocks, int32_t* slot_block, int32_t* slot_stamp,
+                       int32_t* slot_ref, int64_t n_slots, int32_t* ctl, void* stream) {
+    if (n_blocks < 0 || n_slots < 0 || !page_table || !slot_block || !slot_stamp || !slot_ref || !ctl)
+        return fail(SC_EINVAL, "sc_handoff: invalid streaming map");
+    SC_HIP(sc::launch_stream_reset(page_table, n_blocks, slot_block, slot_stamp, slot_ref, n_slots, ctl,
+                                   static_cast<hipStream_t>(stream)), "stream reset");
+    return ok();
+}
+
+uint64_t sc_kv_block_bytes(int64_t n_head_kv, int64_t head_dim, int64_t page_size, int32_t format) {
+    const uint64_t rows = uint64_t(n_head_kv) * uint64_t(page_size);
+    if (format == 2) return rows * uint64_t(head_dim / 32) * 18 * 2;                       // q4_0: 18 B per 32
+    if (format == 1) return rows * uint64_t(head_dim) * 2 + rows * uint64_t(head_dim / 64) * 2 * 2;   // int8 + scales
+    return rows * uint64_t(head_dim) * 2 * 2;                                                 // f16 K and V
+}
+
+// ---- plumbing --------------------------------------------------------------------------------------------------
 
 int sc_device_count(int* count) {
     if (!count) return fail(SC_EINVAL, "sc_handoff: missing output");
     *count = 0;
     SC_HIP(hipGetDeviceCount(count), "device count");
+    return ok();
+}
+int sc_get_device(int* device) {
+    if (!device) return fail(SC_EINVAL, "sc_handoff: missing output");
+    SC_HIP(hipGetDevice(device), "get device");
+    return ok();
+}
+int sc_set_device(int device) {
+    SC_HIP(hipSetDevice(device), "set device");
     return ok();
 }
 int sc_device_alloc(void** ptr, uint64_t bytes) {

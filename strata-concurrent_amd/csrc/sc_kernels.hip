@@ -297,9 +297,43 @@ __global__ void __launch_bounds__(kThreads) decode_probe_kernel(const uint8_t* k
     if (threadIdx.x == 0) sink[blockIdx.x] = s[0] ^ s[1] ^ s[2] ^ s[3];
 }
 
+// Every block of a streamed layer evicted (the reference's reset, src/kernels/cuda/kv_stream.cu:173-182).
+__global__ void stream_reset_kernel(int32_t* table, int64_t n_blocks, int32_t* slot_block, int32_t* slot_stamp,
+                                    int32_t* slot_ref, int64_t n_slots, int32_t* ctl) {
+    const int64_t i0 = int64_t(blockIdx.x) * blockDim.x + threadIdx.x, stride = int64_t(gridDim.x) * blockDim.x;
+    for (int64_t i = i0; i < n_blocks; i += stride) table[i] = -1;
+    for (int64_t i = i0; i < n_slots; i += stride) {
+        slot_block[i] = -1;
+        slot_stamp[i] = -1;
+        slot_ref[i] = 0;
+    }
+    if (i0 < 16) ctl[i0] = 0;
+}
+
+__global__ void ring_table_kernel(int32_t* table, int64_t n_blocks, int64_t n_slots) {
+    for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n_blocks; i += int64_t(gridDim.x) * blockDim.x)
+        table[i] = int32_t(i % n_slots);
+}
+
 }  // namespace
 
 // ---- launchers (host) ------------------------------------------------------------------------------------------
+
+hipError_t launch_stream_reset(int32_t* table, int64_t n_blocks, int32_t* slot_block, int32_t* slot_stamp,
+                               int32_t* slot_ref, int64_t n_slots, int32_t* ctl, hipStream_t stream) {
+    const int64_t n = n_blocks > n_slots ? n_blocks : n_slots;
+    const int64_t blocks = (n + 255) / 256 < 1024 ? ((n + 255) / 256 > 0 ? (n + 255) / 256 : 1) : 1024;
+    hipLaunchKernelGGL(stream_reset_kernel, dim3(unsigned(blocks)), dim3(256), 0, stream, table, n_blocks,
+                       slot_block, slot_stamp, slot_ref, n_slots, ctl);
+    return hipGetLastError();
+}
+
+hipError_t launch_ring_table(int32_t* table, int64_t n_blocks, int64_t n_slots, hipStream_t stream) {
+    if (n_blocks <= 0) return hipSuccess;
+    const int64_t blocks = (n_blocks + 255) / 256 < 1024 ? (n_blocks + 255) / 256 : 1024;
+    hipLaunchKernelGGL(ring_table_kernel, dim3(unsigned(blocks)), dim3(256), 0, stream, table, n_blocks, n_slots);
+    return hipGetLastError();
+}
 
 hipError_t launch_move(const MoveRow* rows, const uint16_t* tile_row, const MoveGeo& geo, uint64_t n_tiles,
                        int64_t grid, hipStream_t stream) {

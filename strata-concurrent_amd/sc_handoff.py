@@ -60,6 +60,10 @@ class DecodeSlot(C.Structure):
         ("page_table", C.POINTER(C.c_void_p)), ("gdn_state", C.c_void_p)]
 
 
+class KvRuns(C.Structure):
+    _fields_ = [("src", C.c_void_p * 4), ("dst", C.c_void_p * 4), ("len", C.c_uint64 * 4), ("n", C.c_int32)]
+
+
 class ImageBlob(C.Structure):
     _fields_ = [("kind", C.c_int32), ("layer", C.c_int32), ("offset", C.c_uint64), ("bytes", C.c_uint64)]
 
@@ -86,7 +90,14 @@ _SIGS = {
     "sc_plan_destroy": (C.c_int, [_P]),
     "sc_park_async": (C.c_int, [_GEO, C.POINTER(DecodeSlot), _I64, _P, _U64, _P, _P]),
     "sc_resume_async": (C.c_int, [_GEO, _P, _U64, _I64, C.POINTER(DecodeSlot), _P, _P]),
+    "sc_kv_ring_restore": (C.c_int, [_P, _I64, _I64, _I64, _P]),
+    "sc_kv_stage_from_host": (C.c_int, [_P, _I64, _P]),
+    "sc_kv_ring_table": (C.c_int, [_P, _I64, _I64, _P]),
+    "sc_kv_stream_reset": (C.c_int, [_P, _I64, _P, _P, _P, _I64, _P, _P]),
+    "sc_kv_block_bytes": (_U64, [_I64, _I64, _I64, C.c_int32]),
     "sc_device_count": (C.c_int, [C.POINTER(C.c_int)]),
+    "sc_get_device": (C.c_int, [C.POINTER(C.c_int)]),
+    "sc_set_device": (C.c_int, [C.c_int]),
     "sc_device_alloc": (C.c_int, [C.POINTER(_P), _U64]),
     "sc_device_free": (C.c_int, [_P]),
     "sc_host_alloc": (C.c_int, [C.POINTER(_P), _U64]),
