@@ -158,6 +158,44 @@ int sc_plan_set_grid(sc_plan* plan, int64_t workgroups);
 /* Frees the device table.  The caller must not destroy a plan whose launch has not completed. */
 int sc_plan_destroy(sc_plan* plan);
 
+/* ---- batched ragged resume + append (many slots, one launch) ---------------------------------------------------- */
+
+/* The multi-slot decode layout: every QSA layer has one shared page arena [arena_pages][H][ps][D] f16, each slot
+ * reads it through its own page table, and each slot has its own GDN rows.  There is no reference counterpart:
+ * the reference keeps one live session (docs/STAGE3-CONCURRENCY.md:182) and designs batching with a shared K/V
+ * arena plus per-sequence page tables (docs/STAGE4-BATCH-DECODE.md:474-518), which is this layout.  Parity rule:
+ * each slot read through its table equals the single-slot handoff of that slot's sequence. */
+typedef struct sc_batch_desc {
+    int32_t n_slots;               /* 1..64 */
+    const int64_t* lens;           /* device [n_slots]: parked tokens L_i, read when the launch runs */
+    int64_t max_tokens;            /* bound on every L_i; a slot outside [0, max_tokens] is skipped and flagged */
+    const void* staging;           /* device: the parked images back to back (sc_batch_staging_layout) */
+    uint64_t staging_bytes;
+    int64_t chunk_tokens;          /* the fresh prefill chunk appended to every slot at cell L_i */
+    const void* const* chunk_k;    /* host array [n_slots * n_qsa] of device [chunk_tokens][H][D] f16, slot-major */
+    const void* const* chunk_v;
+    uint16_t* const* arena_k;      /* host array [n_qsa] of device page arenas */
+    uint16_t* const* arena_v;
+    int64_t arena_pages;
+    const int32_t* const* tables;  /* host array [n_slots] of device page tables, logical page -> arena page */
+    int64_t table_pages;           /* entries per table, >= ceil((max_tokens + chunk_tokens) / page_size) */
+    float* const* gdn;             /* host array [n_slots] of device GDN rows (n_gdn rows each) */
+    int64_t* lens_out;             /* device [n_slots] or NULL: L_i + chunk_tokens, or -1 for a skipped slot */
+} sc_batch_desc;
+
+/* Where slot i's parked image of lens[i] tokens sits in the staging buffer: images back to back, each padded to
+ * 256 bytes (an exclusive prefix sum of the padded image sizes).  The launch recomputes the same offsets on the
+ * device from the device-resident lengths with a wave-level scan; this host twin places the H2D copies. */
+int sc_batch_staging_layout(const sc_geometry* g, const int64_t* lens, int32_t n_slots, uint64_t* offsets,
+                            uint64_t* total_bytes);
+/* One launch for every slot: its parked K/V prefix (whole pages, and the partial last page row by row) and its GDN
+ * rows from the staging buffer into the arena through its table, and its chunk's K/V at cells [L_i, L_i + chunk)
+ * (kv_append's mapping, src/prefill/kernels.cu:567-573, including a start in the middle of a page).  No two
+ * workgroups write the same bytes.  Pass 1 of the tiling - each slot's tile count and staging offset - is a
+ * wave-level exclusive scan over the slots, the device analogue of the reference's block_scan
+ * (src/kernels/cuda/kv_stream.cu:58-80). */
+int sc_plan_resume_append(const sc_geometry* g, const sc_batch_desc* desc, sc_plan** out);
+
 /* ---- park / resume: slot <-> pinned host image ----------------------------------------------------------------- */
 
 /* Park: copy a decode slot (identity page tables) into a pinned host image of sc_image_layout(tokens), with

@@ -30,6 +30,7 @@ hipError_t launch_fill_normal_f32(float* dst, uint64_t n, uint64_t seed, uint64_
 hipError_t launch_fill_bytes(void* dst, uint8_t value, uint64_t n, hipStream_t stream);
 hipError_t launch_decode_probe(const void* kv, uint64_t n_bytes, uint32_t* sink, int64_t workgroups,
                                hipStream_t stream);
+hipError_t launch_batch(const BatchArgs& args, int64_t grid, hipStream_t stream);
 hipError_t launch_stream_reset(int32_t* table, int64_t n_blocks, int32_t* slot_block, int32_t* slot_stamp,
                                int32_t* slot_ref, int64_t n_slots, int32_t* ctl, hipStream_t stream);
 hipError_t launch_ring_table(int32_t* table, int64_t n_blocks, int64_t n_slots, hipStream_t stream);
@@ -44,6 +45,9 @@ uint64_t synth_key(uint64_t seed, uint64_t sid) { return host_mix64(seed ^ host_
 }  // namespace sc
 
 struct sc_plan {
+    bool batch = false;                 // a batched resume + append plan (BatchArgs) instead of a handoff table
+    sc::BatchArgs batch_args{};
+    uint64_t* batch_ptrs_dev = nullptr;
     sc::MoveRow* rows_dev = nullptr;
     uint16_t* tile_row_dev = nullptr;   // row index of every tile
     int n_rows = 0;
@@ -427,8 +431,11 @@ static int page_plan(const sc_geometry* g, const void* image, uint64_t image_byt
     if (!geometry(g, o, why)) return snapshot_fail(why.c_str());
     if (tokens < 0 || tokens > (int64_t(1) << 30)) return snapshot_fail("invalid K/V extent");
     const int64_t cells = cells_of(o, tokens);
-    int rc = check_slot(o, slot, cells, true);
+    // the reference's extent rule (conversation_snapshot.cpp:18-25,80-84): tokens within the capacity, and the
+    // page-rounded extent within the pool's pages
+    int rc = check_slot(o, slot, tokens, true);
     if (rc) return rc;
+    if (slot_identity(slot, o.n_qsa) && cells / o.ps > slot->n_pages) return snapshot_fail("invalid K/V extent");
     uint64_t total = 0;
     const auto blobs = image_blobs(o, tokens, total);
     if (!image || image_bytes < total) return snapshot_fail("invalid K/V payload size");
@@ -476,6 +483,10 @@ int sc_plan_capture(const sc_geometry* g, const sc_decode_slot* src, int64_t tok
 
 int sc_plan_launch(const sc_plan* plan, void* stream) {
     if (!plan) return fail(SC_EINVAL, "sc_handoff: missing plan");
+    if (plan->batch) {
+        const hipError_t e = sc::launch_batch(plan->batch_args, plan->grid, static_cast<hipStream_t>(stream));
+        return e == hipSuccess ? ok() : hip_fail(e, "batch launch");
+    }
     const hipError_t e = sc::launch_move(plan->rows_dev, plan->tile_row_dev, plan->geo, plan->n_tiles, plan->grid,
                                          static_cast<hipStream_t>(stream));
     return e == hipSuccess ? ok() : hip_fail(e, "move launch");
@@ -485,7 +496,7 @@ uint64_t sc_plan_payload_bytes(const sc_plan* plan) { return plan ? plan->payloa
 
 int sc_plan_set_grid(sc_plan* plan, int64_t workgroups) {
     if (!plan || workgroups < 0 || workgroups > (int64_t(1) << 30)) return fail(SC_EINVAL, "sc_handoff: invalid grid");
-    if (workgroups == 0) workgroups = int64_t(std::min<uint64_t>(plan->n_tiles, kMaxGrid));
+    if (workgroups == 0) workgroups = int64_t(std::min<uint64_t>(std::max<uint64_t>(plan->n_tiles, 1), kMaxGrid));
     plan->grid = std::max<int64_t>(workgroups, 1);
     return ok();
 }
@@ -494,7 +505,9 @@ int sc_plan_destroy(sc_plan* plan) {
     if (!plan) return ok();
     hipError_t e = plan->rows_dev ? hipFree(plan->rows_dev) : hipSuccess;
     const hipError_t e2 = plan->tile_row_dev ? hipFree(plan->tile_row_dev) : hipSuccess;
+    const hipError_t e3 = plan->batch_ptrs_dev ? hipFree(plan->batch_ptrs_dev) : hipSuccess;
     if (e == hipSuccess) e = e2;
+    if (e == hipSuccess) e = e3;
     delete plan;
     return e == hipSuccess ? ok() : hip_fail(e, "table free");
 }
@@ -505,6 +518,111 @@ int sc_plan_destroy(sc_plan* plan) {
         if (e_ != hipSuccess) return hip_fail(e_, what);      \
     } while (0)
 
+// ---- batched ragged resume + append ----------------------------------------------------------------------------
+
+static uint64_t image_bytes_of(const Geo& o, int64_t tokens) {
+    uint64_t total = 0;
+    image_blobs(o, tokens, total);
+    return total;
+}
+
+int sc_batch_staging_layout(const sc_geometry* g, const int64_t* lens, int32_t n_slots, uint64_t* offsets,
+                            uint64_t* total_bytes) {
+    return guarded([&] {
+        Geo o;
+        std::string why;
+        if (!geometry(g, o, why)) return snapshot_fail(why.c_str());
+        if (n_slots < 1 || n_slots > sc::kMaxBatchSlots || !lens) return fail(SC_EINVAL, "sc_handoff: invalid slot count");
+        uint64_t at = 0;
+        for (int32_t i = 0; i < n_slots; ++i) {
+            if (lens[i] < 0 || lens[i] > (int64_t(1) << 30)) return snapshot_fail("invalid K/V extent");
+            if (offsets) offsets[i] = at;
+            at += round_up(image_bytes_of(o, lens[i]), 256);
+        }
+        if (total_bytes) *total_bytes = at;
+        return ok();
+    });
+}
+
+int sc_plan_resume_append(const sc_geometry* g, const sc_batch_desc* d, sc_plan** out) {
+    return guarded([&] {
+        if (!out || !d) return fail(SC_EINVAL, "sc_handoff: missing plan output or descriptor");
+        Geo o;
+        std::string why;
+        if (!geometry(g, o, why)) return snapshot_fail(why.c_str());
+        if (d->n_slots < 1 || d->n_slots > sc::kMaxBatchSlots) return fail(SC_ERANGE, "sc_handoff: 1 to 64 slots per batch");
+        if (!d->lens || !d->staging || d->max_tokens < 0 || d->max_tokens > (int64_t(1) << 30) || d->chunk_tokens < 0 ||
+            d->chunk_tokens > (int64_t(1) << 30))
+            return snapshot_fail("invalid K/V extent");
+        if (d->arena_pages < 0 || d->table_pages < (d->max_tokens + d->chunk_tokens + o.ps - 1) / o.ps)
+            return snapshot_fail("invalid K/V extent");
+        if (o.n_gdn > 0 && (!d->gdn || o.gdn_row_bytes % 16)) return snapshot_fail("missing running-state buffer");
+        if (o.n_qsa > 0 && (!d->arena_k || !d->arena_v || !d->tables || (d->chunk_tokens && (!d->chunk_k || !d->chunk_v))))
+            return snapshot_fail("missing target state buffer");
+        if (!aligned16(d->staging)) return fail(SC_EINVAL, "sc_handoff: staging must be 16-byte aligned");
+        // the pointer block: arenas, chunk sources, tables, GDN rows
+        const size_t n_chunk = size_t(d->n_slots) * size_t(o.n_qsa) * 2;
+        std::vector<uint64_t> ptrs;
+        ptrs.reserve(size_t(o.n_qsa) * 2 + n_chunk + size_t(d->n_slots) * 2);
+        for (int64_t j = 0; j < o.n_qsa; ++j) {
+            if (!d->arena_k[j] || !d->arena_v[j] || !aligned16(d->arena_k[j]) || !aligned16(d->arena_v[j]))
+                return snapshot_fail("missing target state buffer");
+            ptrs.push_back(reinterpret_cast<uint64_t>(d->arena_k[j]));
+            ptrs.push_back(reinterpret_cast<uint64_t>(d->arena_v[j]));
+        }
+        for (int32_t i = 0; i < d->n_slots; ++i)
+            for (int64_t j = 0; j < o.n_qsa; ++j) {
+                const void* k = d->chunk_tokens ? d->chunk_k[size_t(i) * size_t(o.n_qsa) + size_t(j)] : nullptr;
+                const void* v = d->chunk_tokens ? d->chunk_v[size_t(i) * size_t(o.n_qsa) + size_t(j)] : nullptr;
+                if (d->chunk_tokens && (!k || !v || !aligned16(k) || !aligned16(v)))
+                    return snapshot_fail("missing prefill K/V");
+                ptrs.push_back(reinterpret_cast<uint64_t>(k));
+                ptrs.push_back(reinterpret_cast<uint64_t>(v));
+            }
+        for (int32_t i = 0; i < d->n_slots; ++i) {
+            if (o.n_qsa > 0 && !d->tables[i]) return snapshot_fail("missing page table");
+            ptrs.push_back(reinterpret_cast<uint64_t>(o.n_qsa > 0 ? d->tables[i] : nullptr));
+        }
+        for (int32_t i = 0; i < d->n_slots; ++i) {
+            float* rows = o.n_gdn > 0 ? d->gdn[i] : nullptr;
+            if (o.n_gdn > 0 && (!rows || !aligned16(rows))) return snapshot_fail("missing running-state buffer");
+            ptrs.push_back(reinterpret_cast<uint64_t>(rows));
+        }
+        sc::BatchArgs a{};
+        a.lens = d->lens;
+        a.lens_out = d->lens_out;
+        a.staging = static_cast<const uint8_t*>(d->staging);
+        a.staging_bytes = d->staging_bytes;
+        a.n_slots = d->n_slots;
+        a.n_qsa = int32_t(o.n_qsa);
+        a.max_tokens = d->max_tokens;
+        a.chunk_tokens = d->chunk_tokens;
+        a.arena_pages = d->arena_pages;
+        a.table_pages = d->table_pages;
+        a.gdn_bytes = uint64_t(o.n_gdn) * o.gdn_row_bytes;
+        a.geo = move_geo(o);
+        // an upper bound on the tiles (every slot at max_tokens) sizes the grid; the kernel walks the real ones
+        const uint64_t full = uint64_t(d->max_tokens / o.ps) * (o.page_bytes / 16);
+        const uint64_t per_blob = (full + sc::kTileChunks - 1) / sc::kTileChunks + 1 +
+                                  (uint64_t(d->chunk_tokens) * uint64_t(o.H) * (o.row_bytes / 16) + sc::kTileChunks - 1) /
+                                      sc::kTileChunks;
+        const uint64_t per_slot = 2 * uint64_t(o.n_qsa) * per_blob + (a.gdn_bytes / 16 + sc::kTileChunks - 1) / sc::kTileChunks;
+        sc_plan* p = new (std::nothrow) sc_plan();
+        if (!p) return fail(SC_ENOMEM, "sc_handoff: plan allocation failed");
+        p->batch = true;
+        p->grid = int64_t(std::min<uint64_t>(std::max<uint64_t>(per_slot * uint64_t(d->n_slots), 1), kMaxGrid));
+        p->payload = 0;   // depends on the device-resident lengths
+        hipError_t e = hipMalloc(reinterpret_cast<void**>(&p->batch_ptrs_dev), ptrs.size() * sizeof(uint64_t));
+        if (e != hipSuccess) { delete p; return fail(SC_ENOMEM, std::string("sc_handoff: descriptor allocation: ") + hipGetErrorString(e)); }
+        e = hipMemcpy(p->batch_ptrs_dev, ptrs.data(), ptrs.size() * sizeof(uint64_t), hipMemcpyHostToDevice);
+        if (e != hipSuccess) { (void) hipFree(p->batch_ptrs_dev); delete p; return hip_fail(e, "descriptor upload"); }
+        a.ptrs = p->batch_ptrs_dev;
+        p->batch_args = a;
+        *out = p;
+        return ok();
+    });
+}
+
 // ---- park / resume --------------------------------------------------------------------------------------------
 
 static int dma_image(const sc_geometry* g, const sc_decode_slot* slot, int64_t tokens, uint8_t* host,
@@ -514,8 +632,9 @@ static int dma_image(const sc_geometry* g, const sc_decode_slot* slot, int64_t t
     if (!geometry(g, o, why)) return snapshot_fail(why.c_str());
     if (tokens < 0 || tokens > (int64_t(1) << 30)) return snapshot_fail("invalid K/V extent");
     const int64_t cells = cells_of(o, tokens);
-    int rc = check_slot(o, slot, cells, true);
+    int rc = check_slot(o, slot, tokens, true);
     if (rc) return rc;
+    if (cells / o.ps > slot->n_pages) return snapshot_fail("invalid K/V extent");
     if (!slot_identity(slot, o.n_qsa))
         return fail(SC_EINVAL, "sc_handoff: park/resume copies identity-layout pools; capture a paged slot first");
     uint64_t total = 0;

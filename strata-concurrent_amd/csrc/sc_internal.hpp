@@ -73,4 +73,20 @@ struct MoveGeo {
     uint32_t pad;
 };
 
+// Arguments of the batched ragged resume + append launch (sc_plan_resume_append).  `ptrs` is one device block
+// of pointers: [2*n_qsa arenas (K, V of layer j at 2j, 2j+1)] [n_slots*n_qsa*2 chunk sources, slot-major]
+// [n_slots page tables] [n_slots GDN row bases].
+constexpr int kMaxBatchSlots = 64;   // one wave64 lane per slot in the offset scan
+struct BatchArgs {
+    const int64_t* lens;
+    int64_t* lens_out;
+    const uint8_t* staging;
+    uint64_t staging_bytes;
+    const uint64_t* ptrs;
+    int32_t n_slots, n_qsa;
+    int64_t max_tokens, chunk_tokens, arena_pages, table_pages;
+    uint64_t gdn_bytes;   // all GDN rows of one slot
+    MoveGeo geo;
+};
+
 }  // namespace sc

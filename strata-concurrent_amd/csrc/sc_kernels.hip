@@ -232,6 +232,161 @@ __global__ void __launch_bounds__(kThreads) sc_move_kernel(const MoveRow* __rest
     }
 }
 
+// ---- batched ragged resume + append ----------------------------------------------------------------------------
+
+__device__ __forceinline__ uint64_t shfl_up64(uint64_t v, int delta) {
+    const uint32_t lo = __shfl_up(uint32_t(v), delta), hi = __shfl_up(uint32_t(v >> 32), delta);
+    return (uint64_t(hi) << 32) | lo;
+}
+__device__ __forceinline__ uint64_t shfl64(uint64_t v, int lane) {
+    const uint32_t lo = __shfl(uint32_t(v), lane), hi = __shfl(uint32_t(v >> 32), lane);
+    return (uint64_t(hi) << 32) | lo;
+}
+// Inclusive prefix sum across the 64 lanes of a wave (Hillis-Steele: six shuffle steps).
+__device__ __forceinline__ uint64_t wave_scan(uint64_t v, int lane) {
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint64_t y = shfl_up64(v, o);
+        if (lane >= o) v += y;
+    }
+    return v;
+}
+
+__device__ __forceinline__ uint64_t align_up(uint64_t x, uint64_t a) { return (x + a - 1) / a * a; }
+
+// The tiles of one slot: its K/V blobs each take full-page tiles, at most one partial-page tile and the chunk's
+// tiles; the GDN rows follow.
+struct SlotTiles {
+    uint64_t full_pages, rem_cells, t_full, t_part, t_chunk, per_blob, t_gdn, total;
+};
+__device__ __forceinline__ SlotTiles slot_tiles(const BatchArgs& a, int64_t L) {
+    SlotTiles t;
+    const uint64_t ps = a.geo.page_size.d, H = a.geo.heads.d, rc = a.geo.row_chunks.d;
+    t.full_pages = uint64_t(L) / ps;
+    t.rem_cells = uint64_t(L) % ps;
+    t.t_full = (t.full_pages * a.geo.page_chunks.d + kTileChunks - 1) / kTileChunks;
+    t.t_part = t.rem_cells ? 1 : 0;   // rem_cells * H rows of rc chunks always fit one tile (checked at plan time)
+    t.t_chunk = (uint64_t(a.chunk_tokens) * H * rc + kTileChunks - 1) / kTileChunks;
+    t.per_blob = t.t_full + t.t_part + t.t_chunk;
+    t.t_gdn = (a.gdn_bytes / 16 + kTileChunks - 1) / kTileChunks;
+    t.total = 2 * uint64_t(a.n_qsa) * t.per_blob + t.t_gdn;
+    return t;
+}
+// Bytes of a slot's parked image (K/V blobs of ceil(L/ps) cells, 64-byte aligned, then the GDN rows).
+__device__ __forceinline__ uint64_t kv_blob_stride(const BatchArgs& a, int64_t L) {
+    const uint64_t ps = a.geo.page_size.d;
+    const uint64_t cells = (uint64_t(L) + ps - 1) / ps * ps;
+    return align_up(cells * a.geo.heads.d * a.geo.row_chunks.d * 16, 64);
+}
+
+__global__ void __launch_bounds__(kThreads) sc_batch_kernel(BatchArgs a) {
+    __shared__ int64_t s_len[kMaxBatchSlots];
+    __shared__ uint64_t s_stage[kMaxBatchSlots];
+    __shared__ uint64_t s_tile0[kMaxBatchSlots + 1];
+    // Pass 1, by wave 0 of every workgroup: each lane one slot; the staging offsets and the tile ranges are two
+    // exclusive scans over the slots' ragged sizes.  The batch is all or nothing, like a restore that validates
+    // before its first write: if any slot's length is out of range or its image would run past the staging
+    // buffer, no slot gets a tile and every lens_out entry is -1.
+    if (threadIdx.x < 64) {
+        const int lane = threadIdx.x;
+        const bool live = lane < a.n_slots;
+        const int64_t L = live ? a.lens[lane] : 0;
+        bool ok = !live || (L >= 0 && L <= a.max_tokens);
+        const uint64_t image = live && ok ? align_up(2 * uint64_t(a.n_qsa) * kv_blob_stride(a, L) + a.gdn_bytes, 64) : 0;
+        const uint64_t padded = align_up(image, 256);
+        const uint64_t stage_end = wave_scan(padded, lane);
+        const uint64_t stage = stage_end - padded;
+        if (stage_end > a.staging_bytes) ok = false;
+        ok = __ballot(!ok) == 0;   // every lane agrees: the whole batch is valid
+        const uint64_t tiles = ok && live ? slot_tiles(a, L).total : 0;
+        const uint64_t tile_end = wave_scan(tiles, lane);
+        if (live) {
+            s_len[lane] = ok ? L : -1;
+            s_stage[lane] = stage;
+            s_tile0[lane] = tile_end - tiles;
+        }
+        const uint64_t total = shfl64(tile_end, 63);
+        if (lane == 0) s_tile0[a.n_slots] = total;
+        if (blockIdx.x == 0 && live && a.lens_out) a.lens_out[lane] = ok ? L + a.chunk_tokens : -1;
+    }
+    __syncthreads();
+    const uint64_t total = s_tile0[a.n_slots];
+    const MoveGeo& g = a.geo;
+    const uint64_t row_bytes = uint64_t(g.row_chunks.d) * 16, page_bytes = uint64_t(g.page_chunks.d) * 16;
+    const uint64_t* arenas = a.ptrs;
+    const uint64_t* chunks = a.ptrs + 2 * a.n_qsa;
+    const uint64_t* tables = chunks + uint64_t(a.n_slots) * a.n_qsa * 2;
+    const uint64_t* gdns = tables + a.n_slots;
+    for (uint64_t tile = blockIdx.x; tile < total; tile += gridDim.x) {
+        int lo = 0, hi = a.n_slots - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (s_tile0[mid] <= tile) lo = mid; else hi = mid - 1;
+        }
+        const int slot = __builtin_amdgcn_readfirstlane(lo);
+        const int64_t L = s_len[slot];
+        const SlotTiles t = slot_tiles(a, L);
+        const uint64_t lt = tile - s_tile0[slot];
+        const uint8_t* image = a.staging + s_stage[slot];
+        const uint64_t stride = kv_blob_stride(a, L);
+        const int32_t* table = reinterpret_cast<const int32_t*>(tables[slot]);
+        if (lt < 2 * uint64_t(a.n_qsa) * t.per_blob) {
+            const uint32_t blob = uint32_t(lt / t.per_blob);
+            const uint64_t w = lt - uint64_t(blob) * t.per_blob;
+            const uint8_t* src_blob = image + uint64_t(blob) * stride;
+            uint8_t* arena = reinterpret_cast<uint8_t*>(arenas[blob]);
+            if (w < t.t_full) {
+                // whole parked pages: image page p -> arena page table[p]
+                u32x4 v[kChunksPerThread];
+                int64_t dst[kChunksPerThread];
+#pragma unroll
+                for (int j = 0; j < kChunksPerThread; ++j) {
+                    dst[j] = -1;
+                    const uint64_t q = w * kTileChunks + uint64_t(j * kThreads) + threadIdx.x;
+                    if (q >= t.full_pages * g.page_chunks.d) continue;
+                    const uint32_t p = fdiv(uint32_t(q), g.page_chunks);
+                    const uint32_t ch = uint32_t(q) - p * g.page_chunks.d;
+                    const int64_t phys = p < uint64_t(a.table_pages) ? int64_t(table[p]) : -1;
+                    if (phys < 0 || phys >= a.arena_pages) continue;
+                    v[j] = ld16(src_blob + uint64_t(p) * page_bytes + ch * 16u);
+                    dst[j] = phys * int64_t(page_bytes) + int64_t(ch) * 16;
+                }
+#pragma unroll
+                for (int j = 0; j < kChunksPerThread; ++j)
+                    if (dst[j] >= 0) st16(arena + dst[j], v[j]);
+            } else if (w < t.t_full + t.t_part) {
+                // the partial last page: only its parked cells, so the chunk's cells of that page are not raced
+                const uint64_t n = t.rem_cells * g.heads.d * g.row_chunks.d;
+                const int64_t phys = t.full_pages < uint64_t(a.table_pages) ? int64_t(table[t.full_pages]) : -1;
+                for (uint64_t q = threadIdx.x; q < n && phys >= 0 && phys < a.arena_pages; q += kThreads) {
+                    const uint32_t r = fdiv(uint32_t(q), g.row_chunks);
+                    const uint32_t ch = uint32_t(q) - r * g.row_chunks.d;
+                    const uint32_t c = fdiv(r, g.heads), h = r - c * g.heads.d;
+                    const uint64_t in_page = (uint64_t(h) * g.page_size.d + c) * row_bytes + ch * 16u;
+                    st16(arena + uint64_t(phys) * page_bytes + in_page,
+                         ld16(src_blob + t.full_pages * page_bytes + in_page));
+                }
+            } else {
+                // the fresh chunk's rows at cells L + t (kv_append's mapping)
+                MoveRow r{};
+                r.src = reinterpret_cast<const uint8_t*>(chunks[(uint64_t(slot) * a.n_qsa + blob / 2) * 2 + (blob & 1)]);
+                r.dst = arena;
+                r.table = table;
+                r.n = uint64_t(a.chunk_tokens) * g.heads.d * g.row_chunks.d;
+                r.pos0 = L;
+                r.ld = a.arena_pages;
+                r.aux = int32_t(a.chunk_tokens);
+                tile_kv16(r, g, w - t.t_full - t.t_part);
+            }
+        } else {
+            MoveRow r{};
+            r.src = image + 2 * uint64_t(a.n_qsa) * stride;
+            r.dst = reinterpret_cast<uint8_t*>(gdns[slot]);
+            r.n = a.gdn_bytes / 16;
+            tile_copy(r, lt - 2 * uint64_t(a.n_qsa) * t.per_blob, false);
+        }
+    }
+}
+
 // ---- synthetic inputs ----------------------------------------------------------------------------------------
 
 __device__ __forceinline__ uint64_t mix64(uint64_t z) {
@@ -318,6 +473,12 @@ __global__ void ring_table_kernel(int32_t* table, int64_t n_blocks, int64_t n_sl
 }  // namespace
 
 // ---- launchers (host) ------------------------------------------------------------------------------------------
+
+hipError_t launch_batch(const BatchArgs& args, int64_t grid, hipStream_t stream) {
+    if (grid <= 0 || args.n_slots < 1 || args.n_slots > kMaxBatchSlots) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(sc_batch_kernel, dim3(unsigned(grid)), dim3(kThreads), 0, stream, args);
+    return hipGetLastError();
+}
 
 hipError_t launch_stream_reset(int32_t* table, int64_t n_blocks, int32_t* slot_block, int32_t* slot_stamp,
                                int32_t* slot_ref, int64_t n_slots, int32_t* ctl, hipStream_t stream) {

@@ -64,6 +64,15 @@ class KvRuns(C.Structure):
     _fields_ = [("src", C.c_void_p * 4), ("dst", C.c_void_p * 4), ("len", C.c_uint64 * 4), ("n", C.c_int32)]
 
 
+class BatchDesc(C.Structure):
+    _fields_ = [("n_slots", C.c_int32), ("lens", C.c_void_p), ("max_tokens", C.c_int64), ("staging", C.c_void_p),
+                ("staging_bytes", C.c_uint64), ("chunk_tokens", C.c_int64),
+                ("chunk_k", C.POINTER(C.c_void_p)), ("chunk_v", C.POINTER(C.c_void_p)),
+                ("arena_k", C.POINTER(C.c_void_p)), ("arena_v", C.POINTER(C.c_void_p)), ("arena_pages", C.c_int64),
+                ("tables", C.POINTER(C.c_void_p)), ("table_pages", C.c_int64), ("gdn", C.POINTER(C.c_void_p)),
+                ("lens_out", C.c_void_p)]
+
+
 class ImageBlob(C.Structure):
     _fields_ = [("kind", C.c_int32), ("layer", C.c_int32), ("offset", C.c_uint64), ("bytes", C.c_uint64)]
 
@@ -85,6 +94,8 @@ _SIGS = {
     "sc_plan_scatter": (C.c_int, [_GEO, _P, _U64, _I64, C.POINTER(DecodeSlot), C.POINTER(_P)]),
     "sc_plan_capture": (C.c_int, [_GEO, C.POINTER(DecodeSlot), _I64, _P, _U64, C.POINTER(_P)]),
     "sc_plan_launch": (C.c_int, [_P, _P]),
+    "sc_batch_staging_layout": (C.c_int, [_GEO, C.POINTER(_I64), C.c_int32, C.POINTER(_U64), C.POINTER(_U64)]),
+    "sc_plan_resume_append": (C.c_int, [_GEO, C.POINTER(BatchDesc), C.POINTER(_P)]),
     "sc_plan_payload_bytes": (_U64, [_P]),
     "sc_plan_set_grid": (C.c_int, [_P, _I64]),
     "sc_plan_destroy": (C.c_int, [_P]),
@@ -552,3 +563,107 @@ def probe_link(nbytes: int = 256 << 20, iters: int = 4) -> tuple[float, float]:
     h2d, d2h = C.c_double(), C.c_double()
     check(lib.sc_probe_link(nbytes, iters, C.byref(h2d), C.byref(d2h)), "sc_probe_link")
     return float(h2d.value), float(d2h.value)
+
+
+# ---- batched ragged resume + append (many slots in one launch) ------------------------------------------------------
+
+def staging_layout(geo: Geometry, lens) -> tuple[list[int], int]:
+    n = len(lens)
+    arr = (C.c_int64 * n)(*lens)
+    offs = (C.c_uint64 * n)()
+    total = C.c_uint64()
+    check(lib.sc_batch_staging_layout(C.byref(geo), arr, n, offs, C.byref(total)), "sc_batch_staging_layout")
+    return list(offs), int(total.value)
+
+
+class BatchCase:
+    """`n` slots with parked prefixes of lens[i] tokens (seeded images in pinned host memory) plus a fresh chunk of
+    `chunk` tokens each, resumed and appended into shared per-layer page arenas through fragmented per-slot page
+    tables.  Holds everything the batched plan reads and writes."""
+
+    def __init__(self, geo: Geometry, lens, chunk: int, seed: int, stream=None):
+        import numpy as np
+        self.geo, self.lens, self.chunk, self.seed = geo, list(lens), chunk, seed
+        n = len(self.lens)
+        ps = geo.page_size
+        # parked images: gather each slot's seeded prefill into a device image, park it in pinned host memory
+        self.images, self.image_bytes = [], []
+        for i, L in enumerate(self.lens):
+            case = SyntheticCase(geo, L, seed * 1000 + i)
+            _, total = image_layout(geo, L)
+            dev = DeviceBuffer(total, "uint8")
+            plan = plan_gather(geo, case.prefill, dev.ptr, total)
+            plan.launch()
+            host = PinnedBuffer(total)
+            check(lib.sc_copy_async(host.ptr, dev.ptr, total, None), "park copy")
+            device_sync()
+            plan.destroy()
+            dev.free()
+            del case
+            self.images.append(host)
+            self.image_bytes.append(total)
+        self.offsets, self.staging_bytes = staging_layout(geo, self.lens)
+        self.staging = DeviceBuffer(max(self.staging_bytes, 16), "uint8")
+        # fresh chunks, K/V only
+        self.chunks = [synthetic_prefill(geo, chunk, seed * 1000 + 500 + i, conv_rows=0) for i in range(n)]
+        # page tables: every slot's pages drawn from one shuffled arena (a fragmented allocator)
+        self.table_pages = (max(self.lens) + chunk + ps - 1) // ps
+        need = [(L + chunk + ps - 1) // ps for L in self.lens]
+        self.arena_pages = sum(need) + 3
+        rng = np.random.default_rng(seed)
+        order = rng.permutation(self.arena_pages).astype(np.int32)
+        self.host_tables, at = [], 0
+        for k in need:
+            t = np.full(self.table_pages, -1, dtype=np.int32)
+            t[:k] = order[at:at + k]
+            at += k
+            self.host_tables.append(t)
+        self.tables = device_tables(self.host_tables)
+        shape = (self.arena_pages, geo.n_head_kv, ps, geo.head_dim)
+        self.arena_k = [DeviceBuffer(shape, "uint16") for _ in range(geo.n_qsa)]
+        self.arena_v = [DeviceBuffer(shape, "uint16") for _ in range(geo.n_qsa)]
+        for b in self.arena_k + self.arena_v:
+            b.fill(0)
+        self.gdn = [DeviceBuffer((geo.n_gdn, geo.gdn_row_floats), "float32") for _ in range(n)] if geo.n_gdn else []
+        self.lens_dev = DeviceBuffer(n, "int64")
+        self.lens_dev.upload(np.array(self.lens, dtype=np.int64))
+        self.lens_out = DeviceBuffer(n, "int64")
+        self.lens_out.fill(0)
+        device_sync()
+
+    @property
+    def parked_bytes(self) -> int:
+        return sum(self.image_bytes)
+
+    def stage(self, stream=None) -> None:
+        """The batched resume: one H2D copy per slot into the staging buffer at its offset."""
+        for host, off, nbytes in zip(self.images, self.offsets, self.image_bytes):
+            check(lib.sc_copy_async(self.staging.ptr + off, host.ptr, nbytes, _stream(stream)), "stage copy")
+
+    def plan(self) -> Plan:
+        geo, n = self.geo, len(self.lens)
+        ck = _ptrs([self.chunks[i].k[j].ptr for i in range(n) for j in range(geo.n_qsa)])
+        cv = _ptrs([self.chunks[i].v[j].ptr for i in range(n) for j in range(geo.n_qsa)])
+        ak = _ptrs([b.ptr for b in self.arena_k])
+        av = _ptrs([b.ptr for b in self.arena_v])
+        ts = _ptrs([t.ptr for t in self.tables])
+        gs = _ptrs([g.ptr for g in self.gdn])
+        P = C.POINTER(C.c_void_p)
+        desc = BatchDesc(n_slots=n, lens=self.lens_dev.ptr, max_tokens=max(self.lens), staging=self.staging.ptr,
+                         staging_bytes=self.staging_bytes, chunk_tokens=self.chunk, chunk_k=C.cast(ck, P),
+                         chunk_v=C.cast(cv, P), arena_k=C.cast(ak, P), arena_v=C.cast(av, P),
+                         arena_pages=self.arena_pages, tables=C.cast(ts, P), table_pages=self.table_pages,
+                         gdn=C.cast(gs, P), lens_out=self.lens_out.ptr)
+        h = C.c_void_p()
+        check(lib.sc_plan_resume_append(C.byref(self.geo), C.byref(desc), C.byref(h)), "sc_plan_resume_append")
+        return Plan(h.value, (ck, cv, ak, av, ts, gs))
+
+    def slot_view(self, i: int) -> Slot:
+        """Slot i as a decode slot: the shared arenas read through its page table."""
+        return Slot(self.geo, self.arena_pages, self.table_pages * self.geo.page_size, self.arena_k, self.arena_v,
+                    self.gdn[i] if self.gdn else None, [self.tables[i]] * self.geo.n_qsa)
+
+    def free(self) -> None:
+        for h in self.images:
+            h.free()
+        self.images = []
