@@ -110,6 +110,131 @@ def cpu_baseline(geo_kw: dict, tokens: int, budget_s: float) -> dict:
     }
 
 
+def config4(sc, geo, seed: int, link_gbps: float) -> dict:
+    """Config 3 slots: contexts 8K / 32K / 96K assigned to roles from `seed`.  One slot keeps decoding (a synthetic
+    decode step reads all of its K/V) on its own stream; the other two park to pinned host memory on a park stream;
+    the first parked one is resumed into a fresh slot on a resume stream as soon as its park lands, overlapping the
+    second park (the link is full duplex).  Checks the round trip bit for bit and reports rates against the link."""
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    lens = [int(x) for x in rng.permutation([8192, 32768, 98304])]
+    decode_len, park_a, park_b = lens
+    cases = {L: sc.SyntheticCase(geo, L, seed + L) for L in lens}
+    slots = {L: cases[L].new_slot(max_cells=L) for L in lens}
+    for L in lens:
+        cases[L].carve_into(slots[L])
+    del cases
+    images = {L: sc.PinnedBuffer(sc.image_layout(geo, L)[1]) for L in (park_a, park_b)}
+    for L in (park_a, park_b):   # touch the pinned pages once
+        sc.park_async(geo, slots[L], L, images[L].ptr, images[L].nbytes)
+    restored = sc.new_slot(geo, park_a, fill=0)
+    sink = sc.DeviceBuffer(4096, "uint32")
+    sc.device_sync()
+    decode, park, resume = sc.Stream(), sc.Stream(), sc.Stream()
+    pools = slots[decode_len].k_pool + slots[decode_len].v_pool
+
+    def decode_step():
+        for b in pools:
+            sc.check(sc.lib.sc_decode_probe(b.ptr, b.nbytes, sink.ptr, 4096, decode.handle), "decode probe")
+
+    # decode alone
+    e0, e1 = sc.Event(), sc.Event()
+    for _ in range(3):
+        decode_step()
+    decode.sync()
+    e0.record(decode)
+    for _ in range(20):
+        decode_step()
+    e1.record(decode)
+    e1.sync()
+    alone_ms = e0.elapsed_ms(e1) / 20
+    # enough decode steps to outlast the two parks at the link rate measured in this run
+    est_ms = (images[park_a].nbytes + images[park_b].nbytes) / (link_gbps * 1e9) * 1e3
+    decode_steps = max(20, int(1.5 * est_ms / alone_ms))
+    # the overlapped window: decode keeps running while two parks and one resume move over the link
+    d0, d1 = sc.Event(), sc.Event()
+    p0, pa, pb, r0, r1 = sc.Event(), sc.Event(), sc.Event(), sc.Event(), sc.Event()
+    d0.record(decode)
+    for _ in range(decode_steps):
+        decode_step()
+    d1.record(decode)
+    p0.record(park)
+    sc.park_async(geo, slots[park_a], park_a, images[park_a].ptr, images[park_a].nbytes, stream=park, done=pa.handle)
+    sc.park_async(geo, slots[park_b], park_b, images[park_b].ptr, images[park_b].nbytes, stream=park, done=pb.handle)
+    resume.wait(pa)
+    r0.record(resume)
+    sc.resume_async(geo, images[park_a].ptr, images[park_a].nbytes, park_a, restored, stream=resume, done=r1.handle)
+    d1.sync()
+    pb.sync()
+    r1.sync()
+    window_ms = p0.elapsed_ms(pb) if p0.elapsed_ms(pb) > p0.elapsed_ms(r1) else p0.elapsed_ms(r1)
+    decode_ms = d0.elapsed_ms(d1) / decode_steps
+    bytes_a, bytes_b = images[park_a].nbytes, images[park_b].nbytes
+    park_ms = p0.elapsed_ms(pb)
+    resume_ms = r0.elapsed_ms(r1)
+    # bit-exact round trip: the restored slot equals the parked one, the images equal the slots
+    ok = True
+    for a, b in zip(slots[park_a].buffers(), restored.buffers()):
+        ok &= bool(np.array_equal(a.numpy().view(np.uint8), b.numpy().view(np.uint8)))
+    for L in (park_a, park_b):
+        _, total = sc.image_layout(geo, L)
+        dev = sc.DeviceBuffer(total, "uint8")
+        cap = sc.plan_capture(geo, slots[L], L, dev.ptr, total)
+        cap.launch()
+        sc.device_sync()
+        ok &= bool(np.array_equal(dev.numpy(total), images[L].numpy()))
+        dev.free()
+    for im in images.values():
+        im.free()
+    return {"lens": {"decode": decode_len, "park": [park_a, park_b], "resume": park_a},
+            "park_bytes": bytes_a + bytes_b, "resume_bytes": bytes_a,
+            "park_ms": round(park_ms, 3), "park_gbps": round((bytes_a + bytes_b) / (park_ms * 1e-3) / 1e9, 2),
+            "resume_ms": round(resume_ms, 3), "resume_gbps": round(bytes_a / (resume_ms * 1e-3) / 1e9, 2),
+            "window_ms": round(window_ms, 3),
+            "decode_steps": decode_steps,
+            "decode_step_alone_ms": round(alone_ms, 4), "decode_step_during_ms": round(decode_ms, 4),
+            "decode_slowdown": round(decode_ms / alone_ms, 3), "round_trip_bit_exact": ok,
+            "streams": "decode, park and resume on three non-blocking streams at the default priority"}
+
+
+def config5(sc, geo, seed: int) -> dict:
+    """Config 5: 8 slots, L_i ~ U[1K, 128K] from `seed`: batched resume of the parked prefixes (one H2D per slot into
+    a staging buffer) plus a fresh 2K-token chunk per slot, all scattered into the shared-arena decode layout by one
+    launch whose ragged offsets come from a device-side scan."""
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    lens = [int(x) for x in rng.integers(1024, 131072 + 1, size=8)]
+    chunk = 2048
+    case = sc.BatchCase(geo, lens, chunk, seed=seed)
+    plan = case.plan()
+    side = sc.Stream()
+    case.stage(side)   # warm-up of the link and of the pinned pages
+    plan.launch(side)
+    side.sync()
+    s0, s1, k1 = sc.Event(), sc.Event(), sc.Event()
+    stage_ms, launch_ms = [], []
+    for _ in range(3):
+        s0.record(side)
+        case.stage(side)
+        s1.record(side)
+        plan.launch(side)
+        k1.record(side)
+        k1.sync()
+        stage_ms.append(s0.elapsed_ms(s1))
+        launch_ms.append(s1.elapsed_ms(k1))
+    parked = case.parked_bytes
+    kv_chunk = len(lens) * chunk * geo.n_head_kv * geo.head_dim * 2 * 2 * geo.n_qsa
+    moved = parked + kv_chunk
+    st, ln = min(stage_ms), min(launch_ms)
+    ok = list(case.lens_out.numpy()) == [L + chunk for L in lens]
+    case.free()
+    return {"lens": lens, "chunk_tokens": chunk, "parked_bytes": parked, "chunk_kv_bytes": kv_chunk,
+            "resume_h2d_ms": round(st, 3), "resume_h2d_gbps": round(parked / (st * 1e-3) / 1e9, 2),
+            "scatter_launch_ms": round(ln, 4), "scatter_hbm_gbps": round(2 * moved / (ln * 1e-3) / 1e9, 1),
+            "scatter_frac": round(2 * moved / (ln * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+            "total_ms": round(st + ln, 3), "lens_out_ok": ok}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -256,6 +381,20 @@ def main() -> int:
                              "p90_ms": round(lat[int(len(lat) * 0.9)], 4), "reps": len(lat),
                              "p50_gbps": round(PL / (p50 * 1e-3) / 1e9, 1)}
     log(f"32K handoff p50 {p50:.4f} ms over {len(lat)} reps")
+
+    log("config 4: three slots, two parks and one resume overlapped with decode")
+    result["config4"] = config4(sc, geo, 0x5EED, d2h)
+    c4 = result["config4"]
+    log(f"config 4: park {c4['park_gbps']} GB/s, resume {c4['resume_gbps']} GB/s, decode slowdown "
+        f"{c4['decode_slowdown']}x, bit-exact {c4['round_trip_bit_exact']}")
+    result["config4"]["park_frac"] = round(c4["park_gbps"] / d2h, 3)
+    result["config4"]["resume_frac"] = round(c4["resume_gbps"] / h2d, 3)
+    log("config 5: eight ragged slots, batched resume + append in one launch")
+    result["config5"] = config5(sc, geo, 0x5EED)
+    c5 = result["config5"]
+    result["config5"]["resume_h2d_frac"] = round(c5["resume_h2d_gbps"] / h2d, 3)
+    log(f"config 5: resume {c5['resume_h2d_gbps']} GB/s, one-launch scatter {c5['scatter_launch_ms']} ms "
+        f"({c5['scatter_hbm_gbps']} GB/s HBM)")
 
     if not args.no_cpu:
         log(f"CPU baseline (~{args.cpu_budget:.0f} s on one core)")
