@@ -26,6 +26,19 @@ sys.path.insert(0, str(ROOT / "strata-concurrent_amd"))
 sys.path.insert(0, str(ROOT))
 
 METRIC = "handoff GB/s (HBM + host park/resume) and p50 handoff latency at 32K ctx"
+PMC_SUMMARY = ROOT / "profiles" / "sc_move_kernel_fused_carve_128k_pmc.md"
+
+
+def measured_traffic() -> int | None:
+    """HBM bytes per launch of the fused 128K carve from the committed FETCH_SIZE / WRITE_SIZE counter runs (each
+    scaled by what the counter reads for a plain copy of known size), or None when no summary is committed."""
+    try:
+        for line in PMC_SUMMARY.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":", 1)[1])
+    except (OSError, ValueError):
+        pass
+    return None
 HBM_PEAK_GBPS = 8000.0
 
 
@@ -247,6 +260,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--grid", type=int, default=0, help="workgroups of the move kernel (0 = library default)")
     ap.add_argument("--kernel-only", action="store_true", help="only the timed handoff (for profiler runs)")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
+                    help="only run 5 device-to-device copies of BYTES (the counter calibration of profiler runs)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -260,6 +275,17 @@ def main() -> int:
         print("bench.py: no HIP device visible", file=sys.stderr)
         return 1
     stream = sc.Stream()   # every timed launch and its events go on this one non-blocking stream
+    if args.copy_calibration:
+        n = args.copy_calibration
+        src, dst = sc.DeviceBuffer(n, "uint8"), sc.DeviceBuffer(n, "uint8")
+        src.fill(1)
+        dst.fill(2)
+        sc.device_sync()
+        for _ in range(5):
+            sc.check(sc.lib.sc_copy_async(dst.ptr, src.ptr, n, stream.handle), "copy")
+        sc.device_sync()
+        print(json.dumps({"copy_calibration_bytes": n, "copies": 5}), flush=True)
+        return 0
     geo_kw = dict(n_layers=48, qsa_interval=4, n_head_kv=2, head_dim=256, page_size=4, ssm_state_size=128,
                   ssm_k_heads=16, ssm_v_heads=32, ssm_d_conv=4, ssm_conv_channels=8192, idx_key_dim=128)
     geo = sc.geometry(**geo_kw)
@@ -291,7 +317,8 @@ def main() -> int:
                                 "decode slot, inputs resident in HBM"),
                    "tokens": T, "layers": 48, "payload_bytes": P},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4),
+                     "traffic": measured_traffic() if T == 131072 else None,
                      "kernel": "sc_move_kernel", "kernel_ms": round(kernel_ms, 4),
                      "algorithmic_bytes_per_launch": 2 * P},
     }
