@@ -210,7 +210,7 @@ def config4(sc, geo, seed: int, link_gbps: float) -> dict:
             "streams": "decode, park and resume on three non-blocking streams at the default priority"}
 
 
-def config5(sc, geo, seed: int) -> dict:
+def config5(sc, geo, seed: int, fragmented: bool = True) -> dict:
     """Config 5: 8 slots, L_i ~ U[1K, 128K] from `seed`: batched resume of the parked prefixes (one H2D per slot into
     a staging buffer) plus a fresh 2K-token chunk per slot, all scattered into the shared-arena decode layout by one
     launch whose ragged offsets come from a device-side scan."""
@@ -218,7 +218,7 @@ def config5(sc, geo, seed: int) -> dict:
     rng = np.random.default_rng(seed)
     lens = [int(x) for x in rng.integers(1024, 131072 + 1, size=8)]
     chunk = 2048
-    case = sc.BatchCase(geo, lens, chunk, seed=seed)
+    case = sc.BatchCase(geo, lens, chunk, seed=seed, fragmented=fragmented)
     plan = case.plan()
     side = sc.Stream()
     case.stage(side)   # warm-up of the link and of the pinned pages

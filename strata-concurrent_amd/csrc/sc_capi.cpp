@@ -556,6 +556,11 @@ int sc_plan_resume_append(const sc_geometry* g, const sc_batch_desc* d, sc_plan*
             return snapshot_fail("invalid K/V extent");
         if (d->arena_pages < 0 || d->table_pages < (d->max_tokens + d->chunk_tokens + o.ps - 1) / o.ps)
             return snapshot_fail("invalid K/V extent");
+        // the launch indexes a slot's chunks with 32-bit integers
+        if (uint64_t(d->max_tokens / o.ps) * (o.page_bytes / 16) >= kMaxRowChunks ||
+            uint64_t(d->chunk_tokens) * uint64_t(o.H) * (o.row_bytes / 16) >= kMaxRowChunks ||
+            uint64_t(o.n_gdn) * o.gdn_row_bytes / 16 >= kMaxRowChunks)
+            return fail(SC_ERANGE, "sc_handoff: a slot beyond 2^31 chunks");
         if (o.n_gdn > 0 && (!d->gdn || o.gdn_row_bytes % 16)) return snapshot_fail("missing running-state buffer");
         if (o.n_qsa > 0 && (!d->arena_k || !d->arena_v || !d->tables || (d->chunk_tokens && (!d->chunk_k || !d->chunk_v))))
             return snapshot_fail("missing target state buffer");

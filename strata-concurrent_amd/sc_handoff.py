@@ -581,7 +581,7 @@ class BatchCase:
     `chunk` tokens each, resumed and appended into shared per-layer page arenas through fragmented per-slot page
     tables.  Holds everything the batched plan reads and writes."""
 
-    def __init__(self, geo: Geometry, lens, chunk: int, seed: int, stream=None):
+    def __init__(self, geo: Geometry, lens, chunk: int, seed: int, stream=None, fragmented: bool = True):
         import numpy as np
         self.geo, self.lens, self.chunk, self.seed = geo, list(lens), chunk, seed
         n = len(self.lens)
@@ -611,7 +611,8 @@ class BatchCase:
         need = [(L + chunk + ps - 1) // ps for L in self.lens]
         self.arena_pages = sum(need) + 3
         rng = np.random.default_rng(seed)
-        order = rng.permutation(self.arena_pages).astype(np.int32)
+        # fragmented: every page drawn from a shuffled arena; otherwise each slot gets one contiguous run
+        order = (rng.permutation(self.arena_pages) if fragmented else np.arange(self.arena_pages)).astype(np.int32)
         self.host_tables, at = [], 0
         for k in need:
             t = np.full(self.table_pages, -1, dtype=np.int32)
