@@ -236,6 +236,24 @@ int sc_kv_stream_reset(int32_t* page_table, int64_t n_blocks, int32_t* slot_bloc
 /* Bytes of one block (page) of K and V together.  Replaces kv_block_bytes (kv_stream.hpp:95-96). */
 uint64_t sc_kv_block_bytes(int64_t n_head_kv, int64_t head_dim, int64_t page_size, int32_t format);
 
+/* ---- FNV-1a 64 of device bytes ------------------------------------------------------------------------------------ */
+
+/* The engine's content hash - for every byte h = (h ^ b) * 1099511628211 mod 2^64 from `seed` - of `bytes` bytes of
+ * device memory, bit-identical to the reference's byte loop fnv1a64 (src/core/pinned.cu:594-601; the payload hash of
+ * conversation_wire_payload_hash, src/core/conversation_wire.cpp:1069-1071, and of HandoffArena::payload_hash_of,
+ * src/core/handoff.cpp:1133-1136), computed in parallel on the device: the low byte of the state is resolved one bit
+ * plane at a time by xor scans, after which the hash is a sum of independent per-segment terms.  The reference seeds
+ * every call with 1469598103934665603 (conversation_wire.hpp:196). */
+/* Device workspace the asynchronous form needs for `bytes` bytes of input (about bytes / 200). */
+uint64_t sc_fnv1a64_workspace_bytes(uint64_t bytes);
+/* Enqueue the hash on `stream`; the result lands as one u64 in device memory at `out`.  `data` may have any
+ * alignment (16-byte aligned input takes the vector path); `workspace` is 16-byte aligned device memory of at least
+ * sc_fnv1a64_workspace_bytes(bytes); nothing is allocated. */
+int sc_fnv1a64_async(const void* data, uint64_t bytes, uint64_t seed, uint64_t* out, void* workspace,
+                     uint64_t workspace_bytes, void* stream);
+/* Synchronous convenience: allocates its workspace, runs on the null stream, waits, and returns the hash in *hash. */
+int sc_fnv1a64_device(const void* data, uint64_t bytes, uint64_t seed, uint64_t* hash);
+
 /* ---- runtime plumbing the C++ host layer calls instead of HIP ---------------------------------------------------- */
 
 /* Number of visible HIP devices (0 and SC_EHIP when the runtime finds none). */

@@ -89,4 +89,13 @@ struct BatchArgs {
     MoveGeo geo;
 };
 
+// The parallel FNV-1a (sc_hash.hip): bytes per lane segment, and where its workspace keeps what.
+constexpr int kFnvLaneBytes = 256;
+struct FnvWorkspace {
+    uint64_t segments = 0, groups = 0;
+    uint64_t off_start = 0, off_word0 = 0, off_word1 = 0, off_parity = 0, off_prefix = 0, off_partial = 0;
+    uint64_t bytes = 0;
+};
+FnvWorkspace fnv_workspace(uint64_t n);
+
 }  // namespace sc

@@ -130,6 +130,9 @@ _SIGS = {
     "sc_fill_uniform_f32": (C.c_int, [_P, _U64, C.c_float, C.c_float, _U64, _U64, _P]),
     "sc_fill_normal_f32": (C.c_int, [_P, _U64, _U64, _U64, _P]),
     "sc_decode_probe": (C.c_int, [_P, _U64, _P, _I64, _P]),
+    "sc_fnv1a64_workspace_bytes": (_U64, [_U64]),
+    "sc_fnv1a64_async": (C.c_int, [_P, _U64, _U64, _P, _P, _U64, _P]),
+    "sc_fnv1a64_device": (C.c_int, [_P, _U64, _U64, C.POINTER(_U64)]),
 }
 for _name, (_res, _args) in _SIGS.items():
     _fn = getattr(lib, _name)
@@ -668,3 +671,37 @@ class BatchCase:
         for h in self.images:
             h.free()
         self.images = []
+
+
+REFERENCE_FNV_SEED = 1469598103934665603   # the seed of every fnv1a64 call in the reference (conversation_wire.hpp:196)
+
+
+def fnv1a64_device(ptr: int, nbytes: int, seed: int = REFERENCE_FNV_SEED) -> int:
+    """FNV-1a 64 of `nbytes` device bytes at `ptr`, computed by the library's parallel hash (synchronous)."""
+    out = _U64(0)
+    check(lib.sc_fnv1a64_device(ptr, nbytes, seed, C.byref(out)), "sc_fnv1a64_device")
+    return int(out.value)
+
+
+class HashPlan:
+    """A reusable device workspace for sc_fnv1a64_async over inputs of up to `max_bytes` bytes, plus a device word
+    for the result."""
+
+    def __init__(self, max_bytes: int):
+        self.max_bytes = max_bytes
+        self.ws_bytes = int(lib.sc_fnv1a64_workspace_bytes(max_bytes))
+        self.ws = DeviceBuffer(self.ws_bytes, "uint8")
+        self.out = DeviceBuffer(1, "uint64")
+
+    def launch(self, ptr: int, nbytes: int, seed: int = REFERENCE_FNV_SEED, stream=None) -> None:
+        if nbytes > self.max_bytes:
+            raise ValueError(f"hash input of {nbytes} bytes exceeds the plan's {self.max_bytes}")
+        check(lib.sc_fnv1a64_async(ptr, nbytes, seed, self.out.ptr, self.ws.ptr, self.ws_bytes, _stream(stream)),
+              "sc_fnv1a64_async")
+
+    def result(self) -> int:
+        return int(self.out.numpy()[0])
+
+    def free(self) -> None:
+        self.ws.free()
+        self.out.free()

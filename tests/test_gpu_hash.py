@@ -1,0 +1,99 @@
+"""The device FNV-1a 64 (sc_fnv1a64_*) against the oracle's byte loop, bit for bit.
+
+The oracle (sco_fnv1a64) restates the reference's fnv1a64 (src/core/pinned.cu:594-601) and is pinned by the published
+FNV-1a 64 test vectors in tests/test_oracle.py.  Here the parallel device hash must equal it on every size class the
+segmenting can get wrong (empty, shorter than a segment, exact multiples of the 256-byte segment, of a workgroup's
+64 KiB and of a scan block, ragged tails), from misaligned starts (the byte path), from any seed, and at the size of a
+full 128K hand-off payload.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+SEEDS = [1469598103934665603, 0xCBF29CE484222325, 0, 0xFFFFFFFFFFFFFFFF, 0x0123456789ABCDEF]
+
+
+def _upload(sc, data: np.ndarray, pad: int = 0):
+    buf = sc.DeviceBuffer(max(data.size + pad, 16), "uint8")
+    if data.size:
+        buf.upload(data, start=pad)
+    return buf
+
+
+@pytest.mark.parametrize("n", [0, 1, 2, 15, 16, 17, 255, 256, 257, 1000, 4095, 4096, 65535, 65536, 65537,
+                               3 * 65536 + 100, 1 << 20, (1 << 20) + 255, 12_345_679])
+def test_device_hash_equals_byte_loop(sc, oracle, cuda, n):
+    rng = np.random.default_rng(n)
+    data = rng.integers(0, 256, size=n, dtype=np.uint8)
+    buf = _upload(sc, data)
+    for seed in SEEDS[: 2 if n > 100000 else len(SEEDS)]:
+        assert sc.fnv1a64_device(buf.ptr, n, seed) == oracle.fnv1a64(data.tobytes(), seed), (n, hex(seed))
+    buf.free()
+
+
+def test_published_vectors_on_device(sc, cuda):
+    basis = 0xCBF29CE484222325   # the textbook offset basis (the published vectors use it)
+    for text, want in [(b"", basis), (b"a", 0xAF63DC4C8601EC8C), (b"foobar", 0x85944171F73967E8)]:
+        arr = np.frombuffer(text, dtype=np.uint8)
+        buf = _upload(sc, arr)
+        assert sc.fnv1a64_device(buf.ptr, arr.size, basis) == want, text
+        buf.free()
+
+
+@pytest.mark.parametrize("offset", [1, 3, 8, 15])
+def test_misaligned_start(sc, oracle, cuda, offset):
+    n = 70_001
+    data = np.random.default_rng(offset).integers(0, 256, size=n, dtype=np.uint8)
+    buf = _upload(sc, data, pad=offset)
+    assert sc.fnv1a64_device(buf.ptr + offset, n) == oracle.fnv1a64(data.tobytes())
+    buf.free()
+
+
+def test_low_entropy_inputs(sc, oracle, cuda):
+    """All-zero, all-0xFF and a repeating ramp: inputs whose low-byte state walks short cycles."""
+    n = 300_000
+    for data in (np.zeros(n, np.uint8), np.full(n, 0xFF, np.uint8), (np.arange(n) % 251).astype(np.uint8)):
+        buf = _upload(sc, data)
+        assert sc.fnv1a64_device(buf.ptr, n) == oracle.fnv1a64(data.tobytes())
+        buf.free()
+
+
+def test_async_plan_on_a_stream_and_reuse(sc, oracle, cuda):
+    """One workspace hashes inputs of different sizes back to back on a non-blocking stream."""
+    plan = sc.HashPlan(1 << 22)
+    stream = sc.Stream()
+    for n in (1 << 22, 123_457, 0, 4096):
+        data = np.random.default_rng(n + 7).integers(0, 256, size=n, dtype=np.uint8)
+        buf = _upload(sc, data)
+        plan.launch(buf.ptr, n, stream=stream)
+        stream.sync()
+        assert plan.result() == oracle.fnv1a64(data.tobytes()), n
+        buf.free()
+    plan.free()
+
+
+def test_workspace_refusals(sc, cuda):
+    buf = sc.DeviceBuffer(1 << 16, "uint8")
+    out = sc.DeviceBuffer(1, "uint64")
+    small = int(sc.lib.sc_fnv1a64_workspace_bytes(1 << 16)) - 256
+    ws = sc.DeviceBuffer(max(small, 16), "uint8")
+    rc = sc.lib.sc_fnv1a64_async(buf.ptr, 1 << 16, 0, out.ptr, ws.ptr, small, None)
+    assert rc == sc.SC_EINVAL and "workspace" in sc.last_error()
+    for b in (buf, out, ws):
+        b.free()
+
+
+def test_full_payload_size(sc, oracle, cuda):
+    """A buffer of the 128K hand-off payload's size (3 300 261 888 bytes), against the byte loop."""
+    n = 3_300_261_888
+    buf = sc.DeviceBuffer(n, "uint8")
+    sc.lib.sc_fill_uniform_f16(buf.ptr, n // 2, -4.0, 4.0, 0x5EED, 77, None)
+    sc.device_sync()
+    host = sc.PinnedBuffer(n)
+    sc.check(sc.lib.sc_copy_async(host.ptr, buf.ptr, n, None), "copy")
+    sc.device_sync()
+    want = oracle.fnv1a64(host.numpy())
+    assert sc.fnv1a64_device(buf.ptr, n) == want
+    host.free()
+    buf.free()
