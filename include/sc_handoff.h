@@ -149,6 +149,27 @@ int sc_plan_scatter(const sc_geometry* g, const void* image, uint64_t image_byte
  * page tables.  The device half of conversation_kv_save (conversation_snapshot.cpp:139-173) for paged pools. */
 int sc_plan_capture(const sc_geometry* g, const sc_decode_slot* src, int64_t tokens, void* image,
                     uint64_t image_bytes, sc_plan** out);
+/* Where the blobs of a capture or scatter sit in a caller-laid-out buffer, e.g. the blob pool of a wire payload
+ * (include/strata/core/conversation_wire.hpp:24-81: the pool of a K/V + running-state image holds each QSA layer's K
+ * then V blob, then the GDN rows, each 64-byte aligned, with other entries - the draft layer, the small checkpoint
+ * buffers - between or after them).  Offsets are bytes from the buffer start, 16-byte aligned; blobs must not overlap. */
+typedef struct sc_blob_map {
+    const uint64_t* k_off;   /* [n_qsa] the K blob of QSA layer j: its first sc_kv_cells(tokens) cells, identity layout */
+    const uint64_t* v_off;   /* [n_qsa] the V blob */
+    uint64_t gdn_off;        /* every GDN row (ignored without GDN layers) */
+    const uint64_t* zero;    /* [2 * n_zero] (offset, bytes) ranges a capture zero-fills: whole 16-byte chunks */
+    int64_t n_zero;
+} sc_blob_map;
+/* A slot's first sc_kv_cells(tokens) cells (through its page tables) and GDN rows into the blobs `map` places in
+ * `dst`, and the zero ranges cleared, in one launch: the device half of writing a payload's pool straight from the
+ * slot (the reference fills the pool from host copies, src/core/conversation_wire.cpp:400-437). */
+int sc_plan_capture_map(const sc_geometry* g, const sc_decode_slot* src, int64_t tokens, void* dst, uint64_t dst_bytes,
+                        const sc_blob_map* map, sc_plan** out);
+/* The inverse: the blobs `map` places in `src` into the slot, in one launch (the device half of mounting a decoded
+ * payload, the reference's Decoder::blobref + conversation_kv_restore, conversation_wire.cpp:694-754 and
+ * src/core/conversation_snapshot.cpp:196-204). */
+int sc_plan_scatter_map(const sc_geometry* g, const void* src, uint64_t src_bytes, const sc_blob_map* map,
+                        int64_t tokens, const sc_decode_slot* dst, sc_plan** out);
 /* Enqueue the plan on `stream` (a hipStream_t; NULL is the null stream).  Asynchronous. */
 int sc_plan_launch(const sc_plan* plan, void* stream);
 /* Algorithmic payload bytes the plan moves (each read once and written once). */

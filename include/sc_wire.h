@@ -1,0 +1,87 @@
+/* sc_wire.h - a C-ABI over the device hand-off payload path of libsc_core.so.
+ *
+ * The C++ engine interface is strata/core/conversation_wire.hpp (the reference's codec API) and
+ * strata/core/conversation_wire_device.hpp (payloads written from and mounted into a decode slot on the device).
+ * These entry points expose the device path to callers that bind C (tests, the bench, a Python or cgo host): plain
+ * pointers and sizes, an int status (SC_OK == 0, the codes of sc_handoff.h) and the message of the last failure in
+ * sc_wire_last_error().  Every refusal happens before anything is written to the slot.
+ *
+ * The payload is the reference's wire format (include/strata/core/conversation_wire.hpp:24-81), byte for byte: a
+ * payload written here decodes with conversation_wire_decode, and a reference payload of a slot's f16 K/V + GDN rows
+ * mounts here.
+ */
+#ifndef SC_WIRE_H
+#define SC_WIRE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "sc_handoff.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* The host side of the conversation a device payload carries: the SavedConversation fields that are not the slot's
+ * K/V and GDN rows (include/strata/core/conversation_cache.hpp:51-162).  Arrays are host memory, read during
+ * sc_wire_encoder_create only. */
+typedef struct sc_wire_live {
+    int64_t geometry[18];          /* SavedConversation::geometry */
+    int64_t layer_lo, layer_hi;
+    int32_t cvec;
+    int32_t draft_record;          /* 1: an empty K/V record follows the slot's layers (the draft layer's place) */
+    int64_t idx_dim;               /* the K/V records' idx_dim */
+    const int32_t* ids;            /* the live checkpoint's token ids; n_ids must equal the slot's token count */
+    int64_t n_ids;
+    const int64_t* img_start;      /* the live checkpoint's image keys */
+    const uint64_t* img_hash;
+    int64_t n_imgs;
+    uint64_t used;
+    const uint8_t* small[4];       /* ple, tails, dead, block_pos (host bytes, may be NULL when empty) */
+    uint64_t small_bytes[4];
+} sc_wire_live;
+
+typedef struct sc_wire_encoder sc_wire_encoder;
+typedef struct sc_wire_decoder sc_wire_decoder;
+
+/* The message of the last failure on this thread. */
+const char* sc_wire_last_error(void);
+
+/* Lays out the payload of `live` carrying the slot's first `tokens` tokens of f16 K/V (through its page tables) and its
+ * GDN rows.  Replaces conversation_wire_plan (src/core/conversation_wire.cpp:988-1004) for slot-resident state. */
+int sc_wire_encoder_create(const sc_geometry* g, const sc_decode_slot* slot, int64_t tokens, const sc_wire_live* live,
+                           uint64_t geom_hash, uint64_t pack_hash, sc_wire_encoder** out);
+/* The payload's total size (WirePlan::total_bytes) and where its blob pool starts. */
+uint64_t sc_wire_encoder_bytes(const sc_wire_encoder* e);
+uint64_t sc_wire_encoder_pool_offset(const sc_wire_encoder* e);
+/* Enqueues the encode on `stream` into 16-byte aligned device memory `payload`: the head copied in, one gather launch
+ * for the pool, one device FNV-1a over the payload.  Replaces conversation_wire_encode's walk and byte-serial hash
+ * (src/core/conversation_wire.cpp:400-480, 1006-1025). */
+int sc_wire_encode_async(sc_wire_encoder* e, void* payload, uint64_t capacity, void* stream);
+/* The payload hash of the last encode (waits for it): WireEncoded::payload_hash. */
+int sc_wire_encoder_hash(sc_wire_encoder* e, uint64_t* hash);
+int sc_wire_encoder_destroy(sc_wire_encoder* e);
+
+/* Reads and checks the head of a device payload against the slot: magic, version, flags, sizes, every record, the
+ * geometry (when `geometry` is not NULL), the identity hashes (when check_identity), and that the first K/V records
+ * are the slot's f16 layers.  Replaces the checks of conversation_wire_decode (src/core/conversation_wire.cpp:
+ * 560-880) for a payload bound for a slot. */
+int sc_wire_decoder_open(const void* payload, uint64_t bytes, const sc_geometry* g, const sc_decode_slot* slot,
+                         const int64_t* geometry, uint64_t geom_hash, uint64_t pack_hash, int32_t check_identity,
+                         uint64_t payload_hash, int32_t check_hash, sc_wire_decoder** out);
+/* Tokens the payload carries (its live token count). */
+int64_t sc_wire_decoder_tokens(const sc_wire_decoder* d);
+/* Verifies the payload hash on the device (when asked), then scatters the K/V and GDN rows into the slot in one launch
+ * and copies the host-side blobs out.  Synchronous; on a refusal the slot is untouched (the reference's "invalid: no
+ * write", include/strata/core/conversation_snapshot.hpp:103-108). */
+int sc_wire_decoder_restore(sc_wire_decoder* d, void* stream);
+/* After a restore: the live checkpoint's ids (n written to *n; needs cap >= tokens) and its small buffers
+ * (which: 0 ple, 1 tails, 2 dead, 3 block_pos). */
+int sc_wire_decoder_live_ids(const sc_wire_decoder* d, int32_t* ids, int64_t cap, int64_t* n);
+int sc_wire_decoder_small(const sc_wire_decoder* d, int32_t which, uint8_t* dst, uint64_t cap, uint64_t* n);
+int sc_wire_decoder_destroy(sc_wire_decoder* d);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SC_WIRE_H */

@@ -473,6 +473,89 @@ static int page_plan(const sc_geometry* g, const void* image, uint64_t image_byt
     return finish_plan(rows, o, kv_payload(o, cells) + uint64_t(o.n_gdn) * o.gdn_row_bytes, out);
 }
 
+// Capture / scatter with caller-placed blobs: the K and V blob of QSA layer j at k_off[j] / v_off[j] and the GDN rows
+// at gdn_off inside one buffer, plus zero-filled ranges (capture only).  Everything is checked before the plan exists.
+static int map_plan(const sc_geometry* g, void* buf, uint64_t buf_bytes, const sc_blob_map* map, int64_t tokens,
+                    const sc_decode_slot* slot, bool scatter, sc_plan** out) {
+    if (!out) return fail(SC_EINVAL, "sc_handoff: missing plan output");
+    Geo o;
+    std::string why;
+    if (!geometry(g, o, why)) return snapshot_fail(why.c_str());
+    if (tokens < 0 || tokens > (int64_t(1) << 30)) return snapshot_fail("invalid K/V extent");
+    int rc = check_slot(o, slot, tokens, true);
+    if (rc) return rc;
+    const int64_t cells = cells_of(o, tokens);
+    if (slot_identity(slot, o.n_qsa) && cells / o.ps > slot->n_pages) return snapshot_fail("invalid K/V extent");
+    if (!map || (o.n_qsa > 0 && (!map->k_off || !map->v_off)) || map->n_zero < 0 || (map->n_zero && !map->zero))
+        return fail(SC_EINVAL, "sc_handoff: missing blob map");
+    if (!buf || !aligned16(buf)) return fail(SC_EINVAL, "sc_handoff: the blob buffer must be 16-byte aligned");
+    const uint64_t kv_bytes = uint64_t(cells) * uint64_t(o.H) * o.row_bytes;
+    const uint64_t gdn_bytes = uint64_t(o.n_gdn) * o.gdn_row_bytes;
+    struct Range { uint64_t at, n; };
+    std::vector<Range> used;
+    auto place = [&](uint64_t at, uint64_t n) {
+        if (at % 16 || at > buf_bytes || n > buf_bytes - at) return false;
+        if (n) used.push_back({at, n});
+        return true;
+    };
+    for (int64_t j = 0; j < o.n_qsa; ++j)
+        if (!place(map->k_off[j], kv_bytes) || !place(map->v_off[j], kv_bytes))
+            return snapshot_fail("a K/V blob lies outside the buffer or off a 16-byte boundary");
+    if (o.n_gdn > 0 && !place(map->gdn_off, gdn_bytes))
+        return snapshot_fail("the running-state blob lies outside the buffer or off a 16-byte boundary");
+    for (int64_t z = 0; z < map->n_zero && !scatter; ++z)
+        if (map->zero[2 * z + 1] % 16 || !place(map->zero[2 * z], map->zero[2 * z + 1]))
+            return fail(SC_EINVAL, "sc_handoff: a zero range must be 16-byte aligned, whole chunks, inside the buffer");
+    std::sort(used.begin(), used.end(), [](const Range& a, const Range& b) { return a.at < b.at; });
+    for (size_t i = 1; i < used.size(); ++i)
+        if (used[i].at < used[i - 1].at + used[i - 1].n) return fail(SC_EINVAL, "sc_handoff: blobs overlap in the buffer");
+    uint8_t* base = static_cast<uint8_t*>(buf);
+    std::vector<sc::MoveRow> rows;
+    const uint64_t pages = uint64_t(cells / o.ps);
+    for (int64_t j = 0; j < o.n_qsa; ++j) {
+        uint16_t* pools[2] = {slot->k_pool[j], slot->v_pool[j]};
+        const uint64_t offs[2] = {map->k_off[j], map->v_off[j]};
+        for (int a = 0; a < 2; ++a) {
+            sc::MoveRow r{};
+            r.kind = scatter ? sc::kPagesScatter : sc::kPagesGather;
+            r.src = scatter ? base + offs[a] : reinterpret_cast<const uint8_t*>(pools[a]);
+            r.dst = scatter ? reinterpret_cast<uint8_t*>(pools[a]) : base + offs[a];
+            r.table = slot->page_table ? slot->page_table[j] : nullptr;
+            r.n = pages * (o.page_bytes / 16);
+            r.ld = slot->n_pages;
+            if (r.n) rows.push_back(r);
+        }
+    }
+    if (o.n_gdn > 0) {
+        sc::MoveRow r{};
+        r.kind = sc::kCopy;
+        r.src = scatter ? base + map->gdn_off : reinterpret_cast<const uint8_t*>(slot->gdn_state);
+        r.dst = scatter ? reinterpret_cast<uint8_t*>(slot->gdn_state) : base + map->gdn_off;
+        r.n = gdn_bytes / 16;
+        rows.push_back(r);
+    }
+    for (int64_t z = 0; z < map->n_zero && !scatter; ++z) {
+        sc::MoveRow r{};
+        r.kind = sc::kZero;
+        r.dst = base + map->zero[2 * z];
+        r.n = map->zero[2 * z + 1] / 16;
+        if (r.n) rows.push_back(r);
+    }
+    return finish_plan(rows, o, 2 * kv_bytes * uint64_t(o.n_qsa) + gdn_bytes, out);
+}
+
+int sc_plan_capture_map(const sc_geometry* g, const sc_decode_slot* src, int64_t tokens, void* dst, uint64_t dst_bytes,
+                        const sc_blob_map* map, sc_plan** out) {
+    return guarded([&] { return map_plan(g, dst, dst_bytes, map, tokens, src, false, out); });
+}
+
+int sc_plan_scatter_map(const sc_geometry* g, const void* src, uint64_t src_bytes, const sc_blob_map* map,
+                        int64_t tokens, const sc_decode_slot* dst, sc_plan** out) {
+    return guarded([&] {
+        return map_plan(g, const_cast<void*>(src), src_bytes, map, tokens, dst, true, out);
+    });
+}
+
 int sc_plan_scatter(const sc_geometry* g, const void* image, uint64_t image_bytes, int64_t tokens,
                     const sc_decode_slot* dst, sc_plan** out) {
     return guarded([&] { return page_plan(g, image, image_bytes, tokens, dst, true, out); });

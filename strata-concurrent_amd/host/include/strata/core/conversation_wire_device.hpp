@@ -1,0 +1,121 @@
+// conversation_wire_device.hpp - hand-off payloads written straight from a decode slot, and mounted straight into
+// one, in device memory.
+//
+// The reference builds a payload on the host: the slot is first saved to host buffers (conversation_snapshot_save,
+// synchronous per-16-MiB cudaMemcpy), then the codec walks those buffers and hashes every byte on one CPU core
+// (src/core/conversation_wire.cpp:400-480), and the receiver hashes the payload again before decoding it
+// (src/core/handoff.cpp:1133-1136).  This library keeps the payload format and moves the heavy parts to the GPU:
+//
+//   encode   the host lays out the head (header, records) with the codec, then on one stream: the head and the few
+//            small host blobs are copied in, ONE launch of the move kernel gathers every K/V page and GDN row of the
+//            slot into its pool offset (and zeroes the pool's gaps), and the parallel device FNV-1a hashes the whole
+//            payload.  The payload is then already what the wire carries: park it with one D2H copy, or hand the
+//            device buffer to another process on the same GPU.
+//   decode   the head is read back and parsed with every check of conversation_wire_decode; the payload hash is
+//            verified on the device; only then does ONE launch scatter the pool into the slot (nothing is written
+//            on a refusal), and the small host blobs are copied out into the returned image.
+//
+// Scope: the slot's QSA layers carry f16 K/V without indexer rows (format 0), the first image K/V records are those
+// layers in order, and the live checkpoint's gdn blob is the slot's GDN rows.  Everything else of the image - the
+// records that follow (a draft layer), the live checkpoint's ids, keys and small buffers, retained checkpoints - is
+// host data carried as is.  A layer-split image (stage parts) is refused on the device path.
+#pragma once
+
+#include "strata/core/conversation_wire.hpp"
+
+#include "sc_handoff.h"
+
+#include <array>
+#include <cstdint>
+#include <string>
+#include <vector>
+
+namespace strata::core {
+
+/// The host side of a conversation whose K/V and GDN rows live in a decode slot.
+struct WireDeviceConversation {
+    std::array<int64_t, 18> geometry{};   // SavedConversation::geometry (the engine's geometry key)
+    int64_t layer_lo = 0, layer_hi = 0;
+    bool cvec = true;
+    int64_t idx_dim = 0;                  // the K/V records' idx_dim (ModelGeometry::idx_key_dim)
+    ConversationCheckpoint live;          // ids, keys, used and the small buffers; its gdn must be empty (it is the slot's)
+    std::vector<ConversationCheckpoint> checkpoints;
+    std::vector<ConversationKv> trailing_kv;   // host K/V records after the slot's layers (the draft layer)
+};
+
+class WireDeviceEncoder {
+public:
+    WireDeviceEncoder() = default;
+    ~WireDeviceEncoder();
+    WireDeviceEncoder(const WireDeviceEncoder&) = delete;
+    WireDeviceEncoder& operator=(const WireDeviceEncoder&) = delete;
+
+    /// Lays out the payload of `conv` carrying the slot's state for `tokens` tokens (== conv.live.ids.size()).
+    bool plan(const sc_geometry& g, const sc_decode_slot& slot, int64_t tokens, const WireDeviceConversation& conv,
+              const WireIdentity& identity, std::string& error);
+    const WirePlan& layout() const { return plan_; }
+    uint64_t bytes() const { return plan_.total_bytes; }
+    /// Enqueues the whole encode on `stream` into `payload` (16-byte aligned device memory of at least bytes()).
+    bool encode(void* payload, uint64_t capacity, void* stream, std::string& error);
+    /// The payload hash of the last encode; waits for it.
+    bool payload_hash(uint64_t& hash, std::string& error);
+
+private:
+    void release();
+
+    sc_geometry g_{};
+    sc_decode_slot slot_{};
+    int64_t tokens_ = 0;
+    WirePlan plan_{};
+    std::vector<uint64_t> k_off_, v_off_, zero_;
+    uint64_t gdn_off_ = 0;
+    struct Upload { uint64_t offset, bytes, staged_at; };
+    std::vector<Upload> uploads_;      // the head and the small host blobs, staged in pinned memory
+    uint8_t* staged_ = nullptr;        // pinned
+    uint64_t staged_bytes_ = 0;
+    void* hash_ws_ = nullptr;          // device
+    uint64_t hash_ws_bytes_ = 0;
+    uint64_t* hash_dev_ = nullptr;     // device
+    uint64_t* hash_host_ = nullptr;    // pinned
+    void* last_stream_ = nullptr;
+    sc_plan* capture_ = nullptr;
+    void* capture_target_ = nullptr;   // the payload the capture plan was built for
+};
+
+class WireDeviceDecoder {
+public:
+    WireDeviceDecoder() = default;
+    ~WireDeviceDecoder();
+    WireDeviceDecoder(const WireDeviceDecoder&) = delete;
+    WireDeviceDecoder& operator=(const WireDeviceDecoder&) = delete;
+
+    /// Reads the head of the payload at `payload` (device memory, `bytes` long), checks it against `expect` and against
+    /// the slot's shape, and plans the scatter.  Nothing is written anywhere.
+    bool open(const void* payload, uint64_t bytes, const sc_geometry& g, const sc_decode_slot& slot,
+              const WireExpect& expect, std::string& error);
+    int64_t tokens() const { return tokens_; }
+    const WireDecoded& info() const { return info_; }
+    /// Verifies the payload hash on the device (when `expect` asked for it), then scatters the K/V and GDN rows into the
+    /// slot and copies every other blob into `image` (whose slot-resident K/V buffers and live gdn stay empty).
+    /// Synchronous.  A refusal writes nothing to the slot.
+    bool restore(void* stream, SavedConversation& image, std::string& error);
+
+private:
+    void release();
+
+    const uint8_t* payload_ = nullptr;
+    uint64_t bytes_ = 0;
+    WireExpect expect_{};
+    WireDecoded info_{};
+    int64_t tokens_ = 0;
+    SavedConversation head_image_;
+    struct Download { void* who; bool buffer; uint64_t offset, bytes; };
+    std::vector<Download> downloads_;   // blobs that go back to the host image (by address inside head_image_)
+    sc_plan* scatter_ = nullptr;
+    void* hash_ws_ = nullptr;
+    uint64_t hash_ws_bytes_ = 0;
+    uint64_t* hash_dev_ = nullptr;
+    uint64_t* hash_host_ = nullptr;
+};
+
+}  // namespace strata::core

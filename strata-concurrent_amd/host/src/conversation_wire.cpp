@@ -9,6 +9,8 @@
 // moves it out only when the whole payload parsed.
 #include "strata/core/conversation_wire.hpp"
 
+#include "wire_internal.hpp"
+
 #include <algorithm>
 #include <cerrno>
 #include <cstdio>
@@ -127,6 +129,14 @@ struct Layout {
     std::vector<PoolEntry> pool;
     uint64_t pool_used = 0;     // end of the last entry, pool-relative
     WirePlan plan;
+    const detail::WireSizes* sizes = nullptr;   // buffers laid out at a given size whatever they hold
+
+    uint64_t size_of(const void* who, uint64_t held) const {
+        if (sizes)
+            for (const auto& s : *sizes)
+                if (s.first == who) return s.second;
+        return held;
+    }
 };
 
 bool lay_out(const SavedConversation& img, int max_depth, Layout& lay, std::string& error) {
@@ -134,7 +144,7 @@ bool lay_out(const SavedConversation& img, int max_depth, Layout& lay, std::stri
         return refuse(error, "a parked image keeps its layer-split state in stage_parts, not in the live checkpoint");
     bool overflow = false;
     each_buffer(img, [&](const ConversationBuffer* b, const std::vector<uint8_t>* v) {
-        const uint64_t n = b ? b->size() : v->size();
+        const uint64_t n = b ? lay.size_of(b, b->size()) : lay.size_of(v, v->size());
         if (!n) return;
         const uint64_t at = up64(lay.pool_used);
         if (at < lay.pool_used || n > kU64Max - at) overflow = true;
@@ -201,6 +211,8 @@ public:
         return true;
     }
     bool record(uint32_t kind, uint64_t body) { return u32(kind) && u32(0) && u64(body); }
+    // The BLOBREF of `who` (a buffer of the image): {bytes, absolute offset} of the next pool entry, or {0, 0}.
+    bool blobref_of(const void* who, uint64_t held) { return blobref(lay_.size_of(who, held)); }
     // The next BLOBREF: {bytes, absolute offset} of the next pool entry, or {0, 0} for an empty buffer.
     bool blobref(uint64_t bytes) {
         if (!bytes) return u64(0) && u64(0);
@@ -257,7 +269,7 @@ bool write_kv(Writer& w, const ConversationKv& k) {
     for (int64_t v : {k.cells, k.heads, k.head_dim, k.page_size, k.pooled_rows, k.idx_dim})
         if (!w.u64(uint64_t(v))) return false;
     for (const ConversationBuffer* b : {&k.k, &k.v, &k.k_scale, &k.v_scale, &k.pooled})
-        if (!w.blobref(b->size())) return false;
+        if (!w.blobref_of(b, b->size())) return false;
     return true;
 }
 
@@ -276,7 +288,7 @@ bool write_checkpoint(Writer& w, const ConversationCheckpoint& c, int depth, int
     for (const ConversationImageKey& key : c.imgs)
         if (!w.u64(uint64_t(key.start)) || !w.u64(key.hash)) return false;
     for (const std::vector<uint8_t>* v : {&c.gdn, &c.ple, &c.tails, &c.dead, &c.block_pos})
-        if (!w.blobref(v->size())) return false;
+        if (!w.blobref_of(v, v->size())) return false;
     if (!w.u64(c.used) || !w.u64(c.stage_parts.size())) return false;
     for (const ConversationCheckpoint& part : c.stage_parts)
         if (!write_checkpoint(w, part, depth + 1, max_depth, error)) return false;
@@ -284,7 +296,7 @@ bool write_checkpoint(Writer& w, const ConversationCheckpoint& c, int depth, int
 }
 
 bool write_payload(const SavedConversation& img, const WireIdentity& id, const Layout& lay, int max_depth, Writer& w,
-                   std::string& error) {
+                   std::string& error, bool head_only = false) {
     const WirePlan& p = lay.plan;
     uint8_t h[kWireHeaderRecordBytes] = {};
     put_le(h + 0, kWireMagic);
@@ -322,6 +334,7 @@ bool write_payload(const SavedConversation& img, const WireIdentity& id, const L
     // zero pad to the pool, then the entries with zero gaps, then the pool's own tail pad
     uint64_t at = kWireHeaderRecordBytes + p.body_bytes;
     if (!w.zeros(p.blob_pool_off - at)) return false;
+    if (head_only) return w.flush();
     uint64_t rel = 0;
     for (const PoolEntry& e : lay.pool) {
         if (!w.zeros(e.rel - rel)) return false;
@@ -410,11 +423,18 @@ WireHeaderRecord parse_header(const uint8_t* p) {
 class Parser {
 public:
     Parser(const WireSource& src, const WireExpect& expect, std::string& error) : src_(src), expect_(expect), error_(error) {}
+    /// Locate mode: blobs are validated and reported here, never read (the buffers stay empty), and the payload hash
+    /// is left to whoever holds the bytes.
+    void locate_into(std::vector<detail::WireBlobAt>* out) { located_ = out; }
 
     bool run(SavedConversation& out, WireDecoded& info) {
         if (!header(info) || !check_hash(info)) return false;
         Cursor c(src_, kWireHeaderRecordBytes, pool_begin_, error_);
-        SavedConversation img;
+        // Normally the image is built aside and moved out only on success.  In locate mode the blob addresses must
+        // be those of the caller's image, so it is built in place (the caller discards it on a refusal).
+        SavedConversation local;
+        SavedConversation& img = located_ ? out : local;
+        img = SavedConversation{};
         for (size_t i = 0; i < 18; ++i) img.geometry[i] = int64_t(h_.geometry[i]);
         img.layer_lo = int64_t(h_.layer_lo);
         img.layer_hi = int64_t(h_.layer_hi);
@@ -438,7 +458,7 @@ public:
         if (h_.live_tokens != int64_t(img.live.ids.size()))
             return refuse(error_, "live_tokens disagrees with the live checkpoint's id count");
         info.blobs = blobs_;
-        out = std::move(img);
+        if (!located_) out = std::move(img);
         return true;
     }
 
@@ -506,7 +526,7 @@ private:
     }
 
     bool check_hash(WireDecoded& info) {
-        if (!expect_.check_payload_hash) return true;
+        if (!expect_.check_payload_hash || located_) return true;
         uint64_t h = kWireHashSeed;
         std::vector<uint8_t> chunk;
         for (uint64_t at = 0; at < h_.payload_bytes; at += kWireChunkBytes) {
@@ -548,6 +568,7 @@ private:
         uint64_t bytes = 0, offset = 0;
         if (!blobref(c, bytes, offset)) return false;
         if (!bytes) return true;
+        if (located_) { located_->push_back({&b, offset, bytes}); return true; }
         b.resize(size_t(bytes));   // bounded: the run lies inside the pool, inside the payload
         bool ok = true;
         b.visit(0, size_t(bytes), [&](uint8_t* p, size_t n, size_t at) { return ok = read_into(p, offset + at, n); });
@@ -557,6 +578,7 @@ private:
         uint64_t bytes = 0, offset = 0;
         if (!blobref(c, bytes, offset)) return false;
         if (!bytes) return true;
+        if (located_) { located_->push_back({&v, offset, bytes}); return true; }
         v.resize(size_t(bytes));
         return read_into(v.data(), offset, bytes);
     }
@@ -641,6 +663,26 @@ private:
     WireHeaderRecord h_{};
     uint64_t pool_begin_ = 0, pool_end_ = 0;
     size_t blobs_ = 0;
+    std::vector<detail::WireBlobAt>* located_ = nullptr;
+};
+
+// The head of a payload (bytes [0, blob_pool_off)) standing in for a whole payload of `total` bytes.
+class HeadSource final : public WireSource {
+public:
+    HeadSource(const uint8_t* head, uint64_t head_bytes, uint64_t total) : p_(head), n_(head_bytes), total_(total) {}
+    uint64_t size() const override { return total_; }
+    bool read(uint8_t* dst, uint64_t offset, size_t bytes) const override {
+        if (offset > n_ || bytes > n_ - offset) return false;
+        if (bytes) std::memcpy(dst, p_ + offset, bytes);
+        return true;
+    }
+    const uint8_t* span(uint64_t offset, size_t bytes) const override {
+        return offset <= n_ && bytes <= n_ - offset ? p_ + offset : nullptr;
+    }
+
+private:
+    const uint8_t* p_;
+    uint64_t n_, total_;
 };
 
 }  // namespace
@@ -771,6 +813,42 @@ bool conversation_wire_peek(const uint8_t* data, uint64_t bytes, WireHeaderRecor
 }
 
 uint64_t conversation_wire_payload_hash(const uint8_t* data, uint64_t bytes) { return fnv1a64(data, bytes, kWireHashSeed); }
+
+namespace detail {
+
+bool wire_head(const SavedConversation& image, const WireIdentity& identity, const WireSizes& sizes,
+               std::vector<uint8_t>& head, std::vector<WireBlobAt>& pool, WirePlan& plan, std::string& error) {
+    Layout lay;
+    lay.sizes = &sizes;
+    if (!lay_out(image, kWireMaxCheckpointDepth, lay, error)) return false;
+    plan = lay.plan;
+    VectorWireSink sink(size_t(plan.blob_pool_off));
+    Writer w(sink, lay, error);
+    if (!write_payload(image, identity, lay, kWireMaxCheckpointDepth, w, error, true)) return false;
+    if (w.written() != plan.blob_pool_off) return refuse(error, "internal: the head is not the bytes before the pool");
+    head = std::move(sink.data());
+    pool.clear();
+    for (const PoolEntry& e : lay.pool)
+        pool.push_back({e.buf ? static_cast<const void*>(e.buf) : static_cast<const void*>(e.vec),
+                        plan.blob_pool_off + e.rel, e.bytes});
+    return true;
+}
+
+bool wire_locate(const uint8_t* head, uint64_t head_bytes, SavedConversation& image, WireDecoded& info,
+                 const WireExpect& expect, std::vector<WireBlobAt>& blobs, std::string& error) {
+    if (!head || head_bytes < kWireHeaderRecordBytes) return refuse(error, "the payload is shorter than the header record");
+    const uint64_t total = get_le<uint64_t>(head + 232);
+    if (get_le<uint64_t>(head + 200) > head_bytes)
+        return refuse(error, "the head given does not reach the blob pool");
+    const HeadSource src(head, head_bytes, std::max(total, head_bytes));
+    info = WireDecoded{};
+    blobs.clear();
+    Parser p(src, expect, error);
+    p.locate_into(&blobs);
+    return p.run(image, info);
+}
+
+}  // namespace detail
 
 std::string conversation_wire_describe(const WireHeaderRecord& h) {
     std::string s = "geometry [";

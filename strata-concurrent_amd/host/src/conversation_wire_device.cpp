@@ -1,0 +1,374 @@
+// conversation_wire_device.cpp - device-resident hand-off payloads (see conversation_wire_device.hpp).
+#include "strata/core/conversation_wire_device.hpp"
+
+#include "wire_internal.hpp"
+
+#include <algorithm>
+#include <cstring>
+
+namespace strata::core {
+namespace {
+
+bool refuse(std::string& error, const std::string& why) {
+    error = "conversation wire: " + why;
+    return false;
+}
+bool abi(int rc, std::string& error, const char* what) {
+    if (rc == SC_OK) return true;
+    error = std::string("conversation wire: ") + what + ": " + sc_last_error();
+    return false;
+}
+uint64_t up64(uint64_t n) { return (n + 63) & ~uint64_t(63); }
+
+// The slot-side shape of the payload: per-layer K/V blob bytes and the GDN blob bytes.
+struct SlotShape {
+    int64_t n_qsa = 0, n_gdn = 0, cells = 0;
+    uint64_t kv_bytes = 0, gdn_bytes = 0;
+};
+
+bool slot_shape(const sc_geometry& g, int64_t tokens, SlotShape& s, std::string& error) {
+    if (tokens < 0) return refuse(error, "a negative token count");
+    s.n_qsa = sc_n_qsa_layers(&g);
+    s.n_gdn = sc_n_gdn_layers(&g);
+    s.cells = sc_kv_cells(&g, tokens);
+    const int64_t row_floats = sc_gdn_row_floats(&g);
+    if (s.cells < 0 || (s.n_gdn > 0 && row_floats <= 0)) return refuse(error, "invalid model geometry");
+    s.kv_bytes = uint64_t(s.cells) * uint64_t(g.n_head_kv) * uint64_t(g.head_dim) * 2;
+    s.gdn_bytes = uint64_t(s.n_gdn) * uint64_t(row_floats) * 4;
+    return true;
+}
+
+// Copies the bytes of the image buffer `who` (a K/V record's ConversationBuffer or a checkpoint's vector) to `dst`.
+bool stage_checkpoint_blob(const ConversationCheckpoint& c, const void* who, uint8_t* dst, uint64_t n) {
+    for (const std::vector<uint8_t>* v : {&c.gdn, &c.ple, &c.tails, &c.dead, &c.block_pos})
+        if (v == who) {
+            std::memcpy(dst, v->data(), size_t(n));
+            return true;
+        }
+    for (const ConversationCheckpoint& part : c.stage_parts)
+        if (stage_checkpoint_blob(part, who, dst, n)) return true;
+    return false;
+}
+bool stage_host_blob(const SavedConversation& img, const void* who, uint8_t* dst, uint64_t n) {
+    for (const ConversationKv& k : img.kv)
+        for (const ConversationBuffer* b : {&k.k, &k.v, &k.k_scale, &k.v_scale, &k.pooled})
+            if (b == who) return b->read(dst, 0, size_t(n));
+    if (stage_checkpoint_blob(img.live, who, dst, n)) return true;
+    for (const ConversationCheckpoint& c : img.checkpoints)
+        if (stage_checkpoint_blob(c, who, dst, n)) return true;
+    return false;
+}
+
+const detail::WireBlobAt* find(const std::vector<detail::WireBlobAt>& pool, const void* who) {
+    for (const auto& e : pool)
+        if (e.who == who) return &e;
+    return nullptr;
+}
+
+}  // namespace
+
+// ---- encoder ---------------------------------------------------------------------------------------------------------
+
+WireDeviceEncoder::~WireDeviceEncoder() { release(); }
+
+void WireDeviceEncoder::release() {
+    if (capture_) sc_plan_destroy(capture_);
+    if (staged_) sc_host_free(staged_);
+    if (hash_host_) sc_host_free(hash_host_);
+    if (hash_ws_) sc_device_free(hash_ws_);
+    if (hash_dev_) sc_device_free(hash_dev_);
+    capture_ = nullptr;
+    staged_ = nullptr;
+    hash_host_ = nullptr;
+    hash_ws_ = nullptr;
+    hash_dev_ = nullptr;
+    capture_target_ = nullptr;
+    uploads_.clear();
+}
+
+bool WireDeviceEncoder::plan(const sc_geometry& g, const sc_decode_slot& slot, int64_t tokens,
+                             const WireDeviceConversation& conv, const WireIdentity& identity, std::string& error) {
+    release();
+    plan_ = WirePlan{};
+    SlotShape s;
+    if (!slot_shape(g, tokens, s, error)) return false;
+    if (int64_t(conv.live.ids.size()) != tokens)
+        return refuse(error, "the live checkpoint's id count is not the slot's token count");
+    if (!conv.live.gdn.empty()) return refuse(error, "the live checkpoint's gdn blob is the slot's GDN rows; leave it empty");
+    // The image as the wire sees it: the slot's layers as f16 K/V records whose buffers are sized, not held.
+    SavedConversation img;
+    img.geometry = conv.geometry;
+    img.layer_lo = conv.layer_lo;
+    img.layer_hi = conv.layer_hi;
+    img.cvec = conv.cvec;
+    // the K/V vector gets its final length before any buffer's address is taken
+    img.kv.resize(size_t(s.n_qsa));
+    img.kv.insert(img.kv.end(), conv.trailing_kv.begin(), conv.trailing_kv.end());
+    detail::WireSizes sizes;
+    for (int64_t j = 0; j < s.n_qsa; ++j) {
+        ConversationKv& k = img.kv[size_t(j)];
+        k.format = 0;
+        k.cells = s.cells;
+        k.heads = g.n_head_kv;
+        k.head_dim = g.head_dim;
+        k.page_size = g.page_size;
+        k.pooled_rows = 0;
+        k.idx_dim = conv.idx_dim;
+        sizes.push_back({&k.k, s.kv_bytes});
+        sizes.push_back({&k.v, s.kv_bytes});
+    }
+    img.live = conv.live;
+    img.checkpoints = conv.checkpoints;
+    if (s.n_gdn > 0) sizes.push_back({&img.live.gdn, s.gdn_bytes});
+    std::vector<uint8_t> head;
+    std::vector<detail::WireBlobAt> pool;
+    if (!detail::wire_head(img, identity, sizes, head, pool, plan_, error)) return false;
+
+    // Device blobs go to the capture plan; a zero range closes each one up to the next 64-byte boundary.  Host blobs
+    // are staged with their own zero padding and copied in.
+    k_off_.assign(size_t(s.n_qsa), 0);
+    v_off_.assign(size_t(s.n_qsa), 0);
+    zero_.clear();
+    gdn_off_ = 0;
+    auto device_blob = [&](const void* who, uint64_t& off) {
+        const detail::WireBlobAt* e = find(pool, who);
+        if (!e) return false;
+        off = e->offset;
+        const uint64_t end = e->offset + e->bytes, padded = up64(end);
+        if (padded > end) { zero_.push_back(end); zero_.push_back(padded - end); }
+        return true;
+    };
+    for (int64_t j = 0; j < s.n_qsa; ++j)
+        if (s.kv_bytes && (!device_blob(&img.kv[size_t(j)].k, k_off_[size_t(j)]) ||
+                           !device_blob(&img.kv[size_t(j)].v, v_off_[size_t(j)])))
+            return refuse(error, "internal: a slot K/V blob is missing from the pool");
+    if (s.n_gdn > 0 && !device_blob(&img.live.gdn, gdn_off_))
+        return refuse(error, "internal: the GDN blob is missing from the pool");
+    std::vector<const detail::WireBlobAt*> host;
+    for (const auto& e : pool) {
+        bool on_device = e.who == &img.live.gdn;
+        for (int64_t j = 0; j < s.n_qsa && !on_device; ++j)
+            on_device = e.who == &img.kv[size_t(j)].k || e.who == &img.kv[size_t(j)].v;
+        if (!on_device) host.push_back(&e);
+    }
+    staged_bytes_ = up64(head.size());
+    for (const auto* e : host) staged_bytes_ += up64(e->bytes);
+    int rc = sc_host_alloc(reinterpret_cast<void**>(&staged_), staged_bytes_ ? staged_bytes_ : 64);
+    if (rc == SC_OK) rc = sc_host_alloc(reinterpret_cast<void**>(&hash_host_), 64);
+    if (!abi(rc, error, "pinned staging")) { release(); return false; }
+    std::memset(staged_, 0, staged_bytes_);
+    std::memcpy(staged_, head.data(), head.size());
+    uploads_.push_back({0, head.size(), 0});
+    uint64_t at = up64(head.size());
+    for (const auto* e : host) {
+        if (!stage_host_blob(img, e->who, staged_ + at, e->bytes)) {
+            release();
+            return refuse(error, "internal: a host blob of the pool was not found");
+        }
+        uploads_.push_back({e->offset, up64(e->bytes), at});
+        at += up64(e->bytes);
+    }
+    hash_ws_bytes_ = sc_fnv1a64_workspace_bytes(plan_.total_bytes);
+    rc = sc_device_alloc(&hash_ws_, hash_ws_bytes_);
+    if (rc == SC_OK) rc = sc_device_alloc(reinterpret_cast<void**>(&hash_dev_), 64);
+    if (!abi(rc, error, "hash workspace")) { release(); return false; }
+    g_ = g;
+    slot_ = slot;
+    tokens_ = tokens;
+    return true;
+}
+
+bool WireDeviceEncoder::encode(void* payload, uint64_t capacity, void* stream, std::string& error) {
+    if (!staged_) return refuse(error, "encode before a successful plan");
+    if (!payload || capacity < plan_.total_bytes)
+        return refuse(error, "the payload buffer holds " + std::to_string(capacity) + " bytes and the payload needs " +
+                                 std::to_string(plan_.total_bytes));
+    if (capture_target_ != payload) {
+        if (capture_) sc_plan_destroy(capture_);
+        capture_ = nullptr;
+        sc_blob_map map{};
+        map.k_off = k_off_.data();
+        map.v_off = v_off_.data();
+        map.gdn_off = gdn_off_;
+        map.zero = zero_.data();
+        map.n_zero = int64_t(zero_.size() / 2);
+        if (!abi(sc_plan_capture_map(&g_, &slot_, tokens_, payload, capacity, &map, &capture_), error, "capture plan"))
+            return false;
+        capture_target_ = payload;
+    }
+    uint8_t* p = static_cast<uint8_t*>(payload);
+    for (const Upload& u : uploads_)
+        if (!abi(sc_copy_async(p + u.offset, staged_ + u.staged_at, u.bytes, stream), error, "head copy")) return false;
+    if (!abi(sc_plan_launch(capture_, stream), error, "pool gather")) return false;
+    if (!abi(sc_fnv1a64_async(payload, plan_.total_bytes, kWireHashSeed, hash_dev_, hash_ws_, hash_ws_bytes_, stream),
+             error, "payload hash"))
+        return false;
+    if (!abi(sc_copy_async(hash_host_, hash_dev_, 8, stream), error, "hash readback")) return false;
+    last_stream_ = stream;
+    return true;
+}
+
+bool WireDeviceEncoder::payload_hash(uint64_t& hash, std::string& error) {
+    if (!hash_host_) return refuse(error, "no encode to read a hash from");
+    if (!abi(sc_stream_sync(last_stream_), error, "encode")) return false;
+    hash = *hash_host_;
+    return true;
+}
+
+// ---- decoder ---------------------------------------------------------------------------------------------------------
+
+WireDeviceDecoder::~WireDeviceDecoder() { release(); }
+
+void WireDeviceDecoder::release() {
+    if (scatter_) sc_plan_destroy(scatter_);
+    if (hash_ws_) sc_device_free(hash_ws_);
+    if (hash_dev_) sc_device_free(hash_dev_);
+    if (hash_host_) sc_host_free(hash_host_);
+    scatter_ = nullptr;
+    hash_ws_ = nullptr;
+    hash_dev_ = nullptr;
+    hash_host_ = nullptr;
+    downloads_.clear();
+}
+
+bool WireDeviceDecoder::open(const void* payload, uint64_t bytes, const sc_geometry& g, const sc_decode_slot& slot,
+                             const WireExpect& expect, std::string& error) {
+    release();
+    if (!payload || bytes < kWireHeaderRecordBytes) return refuse(error, "the payload is shorter than the header record");
+    std::vector<uint8_t> head(kWireHeaderRecordBytes);
+    if (!abi(sc_copy_async(head.data(), payload, head.size(), nullptr), error, "head read") ||
+        !abi(sc_device_sync(), error, "head read"))
+        return false;
+    WireHeaderRecord h{};
+    if (!conversation_wire_peek(head.data(), head.size(), h, error)) return false;
+    if (h.blob_pool_off > bytes) return refuse(error, "the blob pool starts past the end of the buffer");
+    head.resize(size_t(h.blob_pool_off));
+    if (!abi(sc_copy_async(head.data(), payload, head.size(), nullptr), error, "head read") ||
+        !abi(sc_device_sync(), error, "head read"))
+        return false;
+    // every check of the host decoder, against the real buffer size
+    WireExpect bounded = expect;
+    if (!bounded.max_payload_bytes || bounded.max_payload_bytes > bytes) bounded.max_payload_bytes = bytes;
+    std::vector<detail::WireBlobAt> blobs;
+    head_image_ = SavedConversation{};
+    if (!detail::wire_locate(head.data(), head.size(), head_image_, info_, bounded, blobs, error)) return false;
+    if (info_.n_stage_parts) return refuse(error, "a layer-split image cannot be mounted on the device path");
+    SlotShape s;
+    tokens_ = info_.live_tokens;
+    if (!slot_shape(g, tokens_, s, error)) return false;
+    if (int64_t(head_image_.kv.size()) < s.n_qsa)
+        return refuse(error, "the payload carries fewer K/V records than the slot has layers");
+    std::vector<uint64_t> k_off(size_t(s.n_qsa)), v_off(size_t(s.n_qsa));
+    for (int64_t j = 0; j < s.n_qsa; ++j) {
+        const ConversationKv& k = head_image_.kv[size_t(j)];
+        if (k.format != 0 || k.cells != s.cells || k.heads != g.n_head_kv || k.head_dim != g.head_dim ||
+            k.page_size != g.page_size || k.pooled_rows != 0)
+            return refuse(error, "K/V record " + std::to_string(j) + " is not the slot's f16 layer of " +
+                                     std::to_string(tokens_) + " tokens");
+        const detail::WireBlobAt* kb = find(blobs, &k.k);
+        const detail::WireBlobAt* vb = find(blobs, &k.v);
+        if (s.kv_bytes && (!kb || !vb || kb->bytes != s.kv_bytes || vb->bytes != s.kv_bytes))
+            return refuse(error, "K/V record " + std::to_string(j) + " does not carry whole K and V blobs");
+        if (find(blobs, &k.k_scale) || find(blobs, &k.v_scale) || find(blobs, &k.pooled))
+            return refuse(error, "K/V record " + std::to_string(j) + " carries scales or indexer rows");
+        k_off[size_t(j)] = kb ? kb->offset : 0;
+        v_off[size_t(j)] = vb ? vb->offset : 0;
+    }
+    const detail::WireBlobAt* gb = find(blobs, &head_image_.live.gdn);
+    if (s.n_gdn > 0 && (!gb || gb->bytes != s.gdn_bytes))
+        return refuse(error, "the live checkpoint does not carry the slot's GDN rows");
+    for (const auto& b : blobs) {
+        if (b.who == &head_image_.live.gdn) continue;
+        bool slot_blob = false;
+        for (int64_t j = 0; j < s.n_qsa && !slot_blob; ++j)
+            slot_blob = b.who == &head_image_.kv[size_t(j)].k || b.who == &head_image_.kv[size_t(j)].v;
+        if (slot_blob) continue;
+        bool buffer = false;
+        for (const ConversationKv& k : head_image_.kv)
+            for (const ConversationBuffer* x : {&k.k, &k.v, &k.k_scale, &k.v_scale, &k.pooled}) buffer |= x == b.who;
+        downloads_.push_back({const_cast<void*>(b.who), buffer, b.offset, b.bytes});
+    }
+    sc_blob_map map{};
+    map.k_off = k_off.data();
+    map.v_off = v_off.data();
+    map.gdn_off = gb ? gb->offset : 0;
+    if (!abi(sc_plan_scatter_map(&g, payload, bytes, &map, tokens_, &slot, &scatter_), error, "scatter plan")) {
+        release();
+        return false;
+    }
+    if (expect.check_payload_hash) {
+        hash_ws_bytes_ = sc_fnv1a64_workspace_bytes(info_.bytes);
+        int rc = sc_device_alloc(&hash_ws_, hash_ws_bytes_);
+        if (rc == SC_OK) rc = sc_device_alloc(reinterpret_cast<void**>(&hash_dev_), 64);
+        if (rc == SC_OK) rc = sc_host_alloc(reinterpret_cast<void**>(&hash_host_), 64);
+        if (!abi(rc, error, "hash workspace")) { release(); return false; }
+    }
+    payload_ = static_cast<const uint8_t*>(payload);
+    bytes_ = bytes;
+    expect_ = expect;
+    return true;
+}
+
+bool WireDeviceDecoder::restore(void* stream, SavedConversation& image, std::string& error) {
+    if (!scatter_) return refuse(error, "restore before a successful open");
+    if (expect_.check_payload_hash) {
+        if (!abi(sc_fnv1a64_async(payload_, info_.bytes, kWireHashSeed, hash_dev_, hash_ws_, hash_ws_bytes_, stream), error,
+                 "payload hash") ||
+            !abi(sc_copy_async(hash_host_, hash_dev_, 8, stream), error, "hash readback") ||
+            !abi(sc_stream_sync(stream), error, "payload hash"))
+            return false;
+        if (*hash_host_ != expect_.payload_hash)
+            return refuse(error, "payload hash mismatch on the device (the bytes are not the bytes that were written)");
+        info_.payload_hash = *hash_host_;
+    }
+    SavedConversation out = head_image_;
+    // the same blobs inside the copy: re-point the downloads by position
+    auto remap = [&](void* who) -> void* {
+        for (size_t i = 0; i < head_image_.kv.size(); ++i) {
+            ConversationKv& a = head_image_.kv[i];
+            ConversationKv& b = out.kv[i];
+            if (who == &a.k) return &b.k;
+            if (who == &a.v) return &b.v;
+            if (who == &a.k_scale) return &b.k_scale;
+            if (who == &a.v_scale) return &b.v_scale;
+            if (who == &a.pooled) return &b.pooled;
+        }
+        std::vector<std::pair<ConversationCheckpoint*, ConversationCheckpoint*>> cps{{&head_image_.live, &out.live}};
+        for (size_t i = 0; i < head_image_.checkpoints.size(); ++i)
+            cps.push_back({&head_image_.checkpoints[i], &out.checkpoints[i]});
+        for (size_t i = 0; i < cps.size(); ++i)
+            for (size_t k = 0; k < cps[i].first->stage_parts.size(); ++k)
+                cps.push_back({&cps[i].first->stage_parts[k], &cps[i].second->stage_parts[k]});
+        for (auto& [a, b] : cps) {
+            if (who == &a->gdn) return &b->gdn;
+            if (who == &a->ple) return &b->ple;
+            if (who == &a->tails) return &b->tails;
+            if (who == &a->dead) return &b->dead;
+            if (who == &a->block_pos) return &b->block_pos;
+        }
+        return nullptr;
+    };
+    if (!abi(sc_plan_launch(scatter_, stream), error, "pool scatter")) return false;
+    for (const Download& d : downloads_) {
+        void* target = remap(d.who);
+        if (!target) return refuse(error, "internal: a host blob lost its place");
+        if (d.buffer) {
+            auto* b = static_cast<ConversationBuffer*>(target);
+            b->resize(size_t(d.bytes));
+            bool ok = true;
+            b->visit(0, size_t(d.bytes), [&](uint8_t* p, size_t n, size_t at) {
+                return ok = abi(sc_copy_async(p, payload_ + d.offset + at, n, stream), error, "blob read");
+            });
+            if (!ok) return false;
+        } else {
+            auto* v = static_cast<std::vector<uint8_t>*>(target);
+            v->resize(size_t(d.bytes));
+            if (!abi(sc_copy_async(v->data(), payload_ + d.offset, d.bytes, stream), error, "blob read")) return false;
+        }
+    }
+    if (!abi(sc_stream_sync(stream), error, "restore")) return false;
+    image = std::move(out);
+    return true;
+}
+
+}  // namespace strata::core

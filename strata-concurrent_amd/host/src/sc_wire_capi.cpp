@@ -1,0 +1,173 @@
+// sc_wire_capi.cpp - the C-ABI of include/sc_wire.h over the C++ device payload path.
+#include "sc_wire.h"
+
+#include "strata/core/conversation_wire_device.hpp"
+
+#include <exception>
+#include <new>
+#include <string>
+
+using namespace strata::core;
+
+struct sc_wire_encoder {
+    WireDeviceEncoder enc;
+};
+struct sc_wire_decoder {
+    WireDeviceDecoder dec;
+    SavedConversation image;
+    bool restored = false;
+};
+
+namespace {
+
+thread_local std::string g_error;
+
+int done() {
+    g_error.clear();
+    return SC_OK;
+}
+int failed(int code, const std::string& why) {
+    g_error = why;
+    return code;
+}
+
+template <class F> int guarded(F&& f) {
+    try {
+        return f();
+    } catch (const std::bad_alloc&) {
+        return failed(SC_ENOMEM, "conversation wire: host allocation failed");
+    } catch (const std::exception& e) {
+        return failed(SC_EINVAL, std::string("conversation wire: ") + e.what());
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* sc_wire_last_error(void) { return g_error.c_str(); }
+
+int sc_wire_encoder_create(const sc_geometry* g, const sc_decode_slot* slot, int64_t tokens, const sc_wire_live* live,
+                           uint64_t geom_hash, uint64_t pack_hash, sc_wire_encoder** out) {
+    return guarded([&] {
+        if (!g || !slot || !live || !out) return failed(SC_EINVAL, "conversation wire: missing argument");
+        if (live->n_ids < 0 || live->n_imgs < 0 || (live->n_ids && !live->ids) ||
+            (live->n_imgs && (!live->img_start || !live->img_hash)))
+            return failed(SC_EINVAL, "conversation wire: invalid live checkpoint arrays");
+        WireDeviceConversation conv;
+        for (int i = 0; i < 18; ++i) conv.geometry[size_t(i)] = live->geometry[i];
+        conv.layer_lo = live->layer_lo;
+        conv.layer_hi = live->layer_hi;
+        conv.cvec = live->cvec != 0;
+        conv.idx_dim = live->idx_dim;
+        conv.live.ids.assign(live->ids, live->ids + live->n_ids);
+        for (int64_t i = 0; i < live->n_imgs; ++i) conv.live.imgs.push_back({live->img_start[i], live->img_hash[i]});
+        conv.live.used = live->used;
+        std::vector<uint8_t>* small[4] = {&conv.live.ple, &conv.live.tails, &conv.live.dead, &conv.live.block_pos};
+        for (int i = 0; i < 4; ++i) {
+            if (live->small_bytes[i] && !live->small[i]) return failed(SC_EINVAL, "conversation wire: missing small buffer");
+            small[i]->assign(live->small[i], live->small[i] + live->small_bytes[i]);
+        }
+        if (live->draft_record) conv.trailing_kv.emplace_back();
+        auto* e = new sc_wire_encoder();
+        std::string err;
+        if (!e->enc.plan(*g, *slot, tokens, conv, WireIdentity{geom_hash, pack_hash}, err)) {
+            delete e;
+            return failed(SC_EINVAL, err);
+        }
+        *out = e;
+        return done();
+    });
+}
+
+uint64_t sc_wire_encoder_bytes(const sc_wire_encoder* e) { return e ? e->enc.bytes() : 0; }
+uint64_t sc_wire_encoder_pool_offset(const sc_wire_encoder* e) { return e ? e->enc.layout().blob_pool_off : 0; }
+
+int sc_wire_encode_async(sc_wire_encoder* e, void* payload, uint64_t capacity, void* stream) {
+    return guarded([&] {
+        if (!e) return failed(SC_EINVAL, "conversation wire: missing encoder");
+        std::string err;
+        return e->enc.encode(payload, capacity, stream, err) ? done() : failed(SC_EHIP, err);
+    });
+}
+
+int sc_wire_encoder_hash(sc_wire_encoder* e, uint64_t* hash) {
+    return guarded([&] {
+        if (!e || !hash) return failed(SC_EINVAL, "conversation wire: missing argument");
+        std::string err;
+        return e->enc.payload_hash(*hash, err) ? done() : failed(SC_EHIP, err);
+    });
+}
+
+int sc_wire_encoder_destroy(sc_wire_encoder* e) {
+    delete e;
+    return done();
+}
+
+int sc_wire_decoder_open(const void* payload, uint64_t bytes, const sc_geometry* g, const sc_decode_slot* slot,
+                         const int64_t* geometry, uint64_t geom_hash, uint64_t pack_hash, int32_t check_identity,
+                         uint64_t payload_hash, int32_t check_hash, sc_wire_decoder** out) {
+    return guarded([&] {
+        if (!g || !slot || !out) return failed(SC_EINVAL, "conversation wire: missing argument");
+        WireExpect expect;
+        if (geometry) {
+            for (int i = 0; i < 18; ++i) expect.geometry[size_t(i)] = geometry[i];
+            expect.check_geometry = true;
+        }
+        expect.geom_hash = geom_hash;
+        expect.pack_hash = pack_hash;
+        expect.check_hashes = check_identity != 0;
+        expect.payload_hash = payload_hash;
+        expect.check_payload_hash = check_hash != 0;
+        expect.stage_parts = 0;
+        auto* d = new sc_wire_decoder();
+        std::string err;
+        if (!d->dec.open(payload, bytes, *g, *slot, expect, err)) {
+            delete d;
+            return failed(SC_EINVAL, err);
+        }
+        *out = d;
+        return done();
+    });
+}
+
+int64_t sc_wire_decoder_tokens(const sc_wire_decoder* d) { return d ? d->dec.tokens() : -1; }
+
+int sc_wire_decoder_restore(sc_wire_decoder* d, void* stream) {
+    return guarded([&] {
+        if (!d) return failed(SC_EINVAL, "conversation wire: missing decoder");
+        std::string err;
+        if (!d->dec.restore(stream, d->image, err))
+            return failed(err.find("hash mismatch") != std::string::npos || err.find("before a successful") != std::string::npos
+                              ? SC_EINVAL : SC_EHIP, err);
+        d->restored = true;
+        return done();
+    });
+}
+
+int sc_wire_decoder_live_ids(const sc_wire_decoder* d, int32_t* ids, int64_t cap, int64_t* n) {
+    if (!d || !d->restored || !n) return failed(SC_EINVAL, "conversation wire: no restored image");
+    const auto& v = d->image.live.ids;
+    *n = int64_t(v.size());
+    if (cap < int64_t(v.size()) || (!v.empty() && !ids)) return failed(SC_ERANGE, "conversation wire: id buffer too small");
+    for (size_t i = 0; i < v.size(); ++i) ids[i] = v[i];
+    return done();
+}
+
+int sc_wire_decoder_small(const sc_wire_decoder* d, int32_t which, uint8_t* dst, uint64_t cap, uint64_t* n) {
+    if (!d || !d->restored || !n || which < 0 || which > 3) return failed(SC_EINVAL, "conversation wire: no such buffer");
+    const std::vector<uint8_t>* small[4] = {&d->image.live.ple, &d->image.live.tails, &d->image.live.dead,
+                                            &d->image.live.block_pos};
+    const auto& v = *small[which];
+    *n = v.size();
+    if (cap < v.size() || (!v.empty() && !dst)) return failed(SC_ERANGE, "conversation wire: buffer too small");
+    for (size_t i = 0; i < v.size(); ++i) dst[i] = v[i];
+    return done();
+}
+
+int sc_wire_decoder_destroy(sc_wire_decoder* d) {
+    delete d;
+    return done();
+}
+
+}  // extern "C"

@@ -73,6 +73,11 @@ class BatchDesc(C.Structure):
                 ("lens_out", C.c_void_p)]
 
 
+class BlobMap(C.Structure):
+    _fields_ = [("k_off", C.POINTER(C.c_uint64)), ("v_off", C.POINTER(C.c_uint64)), ("gdn_off", C.c_uint64),
+                ("zero", C.POINTER(C.c_uint64)), ("n_zero", C.c_int64)]
+
+
 class ImageBlob(C.Structure):
     _fields_ = [("kind", C.c_int32), ("layer", C.c_int32), ("offset", C.c_uint64), ("bytes", C.c_uint64)]
 
@@ -130,6 +135,8 @@ _SIGS = {
     "sc_fill_uniform_f32": (C.c_int, [_P, _U64, C.c_float, C.c_float, _U64, _U64, _P]),
     "sc_fill_normal_f32": (C.c_int, [_P, _U64, _U64, _U64, _P]),
     "sc_decode_probe": (C.c_int, [_P, _U64, _P, _I64, _P]),
+    "sc_plan_capture_map": (C.c_int, [_GEO, C.POINTER(DecodeSlot), _I64, _P, _U64, C.POINTER(BlobMap), C.POINTER(_P)]),
+    "sc_plan_scatter_map": (C.c_int, [_GEO, _P, _U64, C.POINTER(BlobMap), _I64, C.POINTER(DecodeSlot), C.POINTER(_P)]),
     "sc_fnv1a64_workspace_bytes": (_U64, [_U64]),
     "sc_fnv1a64_async": (C.c_int, [_P, _U64, _U64, _P, _P, _U64, _P]),
     "sc_fnv1a64_device": (C.c_int, [_P, _U64, _U64, C.POINTER(_U64)]),

@@ -107,3 +107,25 @@ def test_image_refusals(sc):
     slot.page_table = C.cast(tab, C.POINTER(C.c_void_p))
     assert sc.lib.sc_park_async(C.byref(geo), C.byref(slot), 60, 1 << 40, total, None, None) == sc.SC_EINVAL
     assert "identity-layout" in sc.last_error()
+
+
+def test_core_library_exports_the_wire_abi():
+    """libsc_core.so exports every entry point include/sc_wire.h declares (the device payload path)."""
+    import sc_wire
+    text = (ROOT / "include" / "sc_wire.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    names = sorted(set(re.findall(r"\b(sc_wire_[a-z0-9_]+)\s*\(", text)))
+    assert len(names) >= 10
+    for name in names:
+        assert hasattr(sc_wire.lib, name), name
+    assert set(names) == set(sc_wire.EXPORTS)
+
+
+def test_wire_refusals_before_any_hip_call(sc):
+    """The device payload path refuses malformed requests on the host (no GPU needed)."""
+    import sc_wire
+    geo = sc.geometry(n_layers=8)
+    h = C.c_void_p()
+    assert sc_wire.lib.sc_wire_encoder_create(None, None, 0, None, 0, 0, C.byref(h)) == sc.SC_EINVAL
+    assert "missing" in sc_wire.lib.sc_wire_last_error().decode()
+    assert sc_wire.lib.sc_wire_decoder_open(None, 0, C.byref(geo), None, None, 0, 0, 0, 0, 0, C.byref(h)) == sc.SC_EINVAL
