@@ -248,6 +248,91 @@ def config5(sc, geo, seed: int, fragmented: bool = True) -> dict:
             "total_ms": round(st + ln, 3), "lens_out_ok": ok}
 
 
+def wire_payload(sc, geo, tokens: int, slot, link_h2d: float, link_d2h: float, reps: int = 5) -> dict:
+    """The codec row: the slot written straight into a wire payload on the device (head copied in, one gather launch,
+    the parallel FNV-1a over the whole payload), mounted back (device hash check, one scatter launch), and the checked
+    park / resume through pinned host memory.  Compared with the reference's host codec, whose byte-serial FNV-1a
+    runs twice per handoff (encode, then the reader's check)."""
+    import numpy as np
+    import sc_wire
+    geokey = [2560, 48, 4, 128, 16, 32, 4, 8192, 4096, 24, 2, 256, 128, 4, 4, 3, 1, 0]
+    ids = (np.arange(tokens, dtype=np.int64) % 151_000).astype(np.int32)
+    live, keep = sc_wire.make_live(geokey, ids, layer_hi=48, idx_dim=128)
+    enc = sc_wire.Encoder(geo, slot, tokens, live, 0x1122334455667788, 0x0AABBCCDDEEFF001)
+    n = enc.bytes
+    payload = sc.DeviceBuffer(n, "uint8")
+    stream = sc.Stream()
+    hp = sc.HashPlan(n)
+    for _ in range(2):
+        enc.encode(payload.ptr, n, stream)
+    h = enc.hash()
+    e0, e1 = sc.Event(), sc.Event()
+    enc_ms, hash_ms = [], []
+    for _ in range(reps):
+        e0.record(stream)
+        enc.encode(payload.ptr, n, stream)
+        e1.record(stream)
+        e1.sync()
+        enc_ms.append(e0.elapsed_ms(e1))
+        e0.record(stream)
+        hp.launch(payload.ptr, n, stream=stream)
+        e1.record(stream)
+        e1.sync()
+        hash_ms.append(e0.elapsed_ms(e1))
+    assert hp.result() == h
+    dst = sc.new_slot(geo, tokens, fill=0)
+    mount_ms = []
+    for _ in range(reps):
+        dec = sc_wire.Decoder(payload.ptr, n, geo, dst, payload_hash=h, check_hash=True)
+        t0 = time.perf_counter()
+        dec.restore(stream)
+        mount_ms.append((time.perf_counter() - t0) * 1e3)
+        dec.destroy()
+    same = all(sc.fnv1a64_device(a.ptr, a.nbytes) == sc.fnv1a64_device(b.ptr, b.nbytes)
+               for a, b in zip(slot.buffers(), dst.buffers()))
+    # checked park: encode on the device, then one D2H of the payload on a second stream that starts as soon as the
+    # payload bytes are in place, overlapping the hash; checked resume: one H2D, then mount
+    host = sc.PinnedBuffer(n)
+    side, copy = sc.Stream(), sc.Stream()
+    gathered, e2 = sc.Event(), sc.Event()
+    park_ms, resume_ms = [], []
+    for _ in range(3):
+        e0.record(side)
+        enc.encode(payload.ptr, n, side, gathered=gathered)
+        copy.wait(gathered)
+        sc.check(sc.lib.sc_copy_async(host.ptr, payload.ptr, n, copy.handle), "park copy")
+        e1.record(copy)
+        e2.record(side)
+        e1.sync()
+        e2.sync()
+        park_ms.append(max(e0.elapsed_ms(e1), e0.elapsed_ms(e2)))
+        assert enc.hash() == h
+        t0 = time.perf_counter()
+        sc.check(sc.lib.sc_copy_async(payload.ptr, host.ptr, n, side.handle), "resume copy")
+        dec = sc_wire.Decoder(payload.ptr, n, geo, dst, payload_hash=h, check_hash=True)
+        dec.restore(side)
+        resume_ms.append((time.perf_counter() - t0) * 1e3)
+        dec.destroy()
+    host.free()
+    payload.free()
+    hp.free()
+    enc_t, hash_t, mount_t = min(enc_ms), min(hash_ms), min(mount_ms)
+    pk, rs = min(park_ms), min(resume_ms)
+    return {"tokens": tokens, "payload_bytes": n, "pool_offset": enc.pool_offset,
+            "encode_ms": round(enc_t, 3), "encode_gbps": round(n / (enc_t * 1e-3) / 1e9, 1),
+            "hash_ms": round(hash_t, 3), "hash_gbps": round(n / (hash_t * 1e-3) / 1e9, 1),
+            "mount_ms": round(mount_t, 3), "mount_gbps": round(n / (mount_t * 1e-3) / 1e9, 1),
+            "checked_park_ms": round(pk, 2), "checked_park_gbps": round(n / (pk * 1e-3) / 1e9, 2),
+            "checked_park_frac_of_link": round(n / (pk * 1e-3) / 1e9 / link_d2h, 3),
+            "checked_resume_ms": round(rs, 2), "checked_resume_gbps": round(n / (rs * 1e-3) / 1e9, 2),
+            "checked_resume_frac_of_link": round(n / (rs * 1e-3) / 1e9 / link_h2d, 3),
+            "round_trip_bit_exact": bool(same),
+            "method": "payload in the reference's wire format; encode = head copy + one gather launch + device FNV-1a; "
+                      "mount = device FNV-1a check + one scatter launch (host-synchronous); park = encode with the "
+                      "pinned D2H of the payload on a second stream overlapping the hash; resume = one pinned H2D, "
+                      "then mount"}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -408,6 +493,12 @@ def main() -> int:
                              "p90_ms": round(lat[int(len(lat) * 0.9)], 4), "reps": len(lat),
                              "p50_gbps": round(PL / (p50 * 1e-3) / 1e9, 1)}
     log(f"32K handoff p50 {p50:.4f} ms over {len(lat)} reps")
+
+    log("wire payload: device encode / hash / mount of the 128K slot, checked park and resume")
+    result["wire_payload"] = wire_payload(sc, geo, T, slot, h2d, d2h)
+    wp = result["wire_payload"]
+    log(f"wire: encode {wp['encode_ms']} ms ({wp['encode_gbps']} GB/s), hash {wp['hash_ms']} ms, mount "
+        f"{wp['mount_ms']} ms; checked park {wp['checked_park_gbps']} GB/s, resume {wp['checked_resume_gbps']} GB/s")
 
     log("config 4: three slots, two parks and one resume overlapped with decode")
     result["config4"] = config4(sc, geo, 0x5EED, d2h)

@@ -55,9 +55,10 @@ int sc_wire_encoder_create(const sc_geometry* g, const sc_decode_slot* slot, int
 uint64_t sc_wire_encoder_bytes(const sc_wire_encoder* e);
 uint64_t sc_wire_encoder_pool_offset(const sc_wire_encoder* e);
 /* Enqueues the encode on `stream` into 16-byte aligned device memory `payload`: the head copied in, one gather launch
- * for the pool, one device FNV-1a over the payload.  Replaces conversation_wire_encode's walk and byte-serial hash
- * (src/core/conversation_wire.cpp:400-480, 1006-1025). */
-int sc_wire_encode_async(sc_wire_encoder* e, void* payload, uint64_t capacity, void* stream);
+ * for the pool, one device FNV-1a over the payload.  `gathered` (a hipEvent_t, may be NULL) is recorded when every
+ * payload byte is in place, before the hash: a park on another stream can wait on it and overlap the hash.  Replaces
+ * conversation_wire_encode's walk and byte-serial hash (src/core/conversation_wire.cpp:400-480, 1006-1025). */
+int sc_wire_encode_async(sc_wire_encoder* e, void* payload, uint64_t capacity, void* stream, void* gathered);
 /* The payload hash of the last encode (waits for it): WireEncoded::payload_hash. */
 int sc_wire_encoder_hash(sc_wire_encoder* e, uint64_t* hash);
 int sc_wire_encoder_destroy(sc_wire_encoder* e);

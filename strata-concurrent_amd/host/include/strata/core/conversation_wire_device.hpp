@@ -55,8 +55,10 @@ public:
               const WireIdentity& identity, std::string& error);
     const WirePlan& layout() const { return plan_; }
     uint64_t bytes() const { return plan_.total_bytes; }
-    /// Enqueues the whole encode on `stream` into `payload` (16-byte aligned device memory of at least bytes()).
-    bool encode(void* payload, uint64_t capacity, void* stream, std::string& error);
+    /// Enqueues the whole encode on `stream` into `payload` (16-byte aligned device memory of at least bytes()).  When
+    /// `gathered` (a hipEvent_t) is given it is recorded once every payload byte is in place and before the hash runs,
+    /// so a copy of the payload on another stream (a park) can start while the hash is computed.
+    bool encode(void* payload, uint64_t capacity, void* stream, std::string& error, void* gathered = nullptr);
     /// The payload hash of the last encode; waits for it.
     bool payload_hash(uint64_t& hash, std::string& error);
 
@@ -89,8 +91,9 @@ public:
     WireDeviceDecoder(const WireDeviceDecoder&) = delete;
     WireDeviceDecoder& operator=(const WireDeviceDecoder&) = delete;
 
-    /// Reads the head of the payload at `payload` (device memory, `bytes` long), checks it against `expect` and against
-    /// the slot's shape, and plans the scatter.  Nothing is written anywhere.
+    /// Waits for the device (so a payload still arriving on any stream is complete), reads the head of the payload at
+    /// `payload` (device memory, `bytes` long), checks it against `expect` and against the slot's shape, and plans the
+    /// scatter.  Nothing is written anywhere.
     bool open(const void* payload, uint64_t bytes, const sc_geometry& g, const sc_decode_slot& slot,
               const WireExpect& expect, std::string& error);
     int64_t tokens() const { return tokens_; }

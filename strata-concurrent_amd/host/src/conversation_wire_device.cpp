@@ -178,7 +178,7 @@ bool WireDeviceEncoder::plan(const sc_geometry& g, const sc_decode_slot& slot, i
     return true;
 }
 
-bool WireDeviceEncoder::encode(void* payload, uint64_t capacity, void* stream, std::string& error) {
+bool WireDeviceEncoder::encode(void* payload, uint64_t capacity, void* stream, std::string& error, void* gathered) {
     if (!staged_) return refuse(error, "encode before a successful plan");
     if (!payload || capacity < plan_.total_bytes)
         return refuse(error, "the payload buffer holds " + std::to_string(capacity) + " bytes and the payload needs " +
@@ -200,6 +200,7 @@ bool WireDeviceEncoder::encode(void* payload, uint64_t capacity, void* stream, s
     for (const Upload& u : uploads_)
         if (!abi(sc_copy_async(p + u.offset, staged_ + u.staged_at, u.bytes, stream), error, "head copy")) return false;
     if (!abi(sc_plan_launch(capture_, stream), error, "pool gather")) return false;
+    if (gathered && !abi(sc_event_record(gathered, stream), error, "gather event")) return false;
     if (!abi(sc_fnv1a64_async(payload, plan_.total_bytes, kWireHashSeed, hash_dev_, hash_ws_, hash_ws_bytes_, stream),
              error, "payload hash"))
         return false;
@@ -235,6 +236,8 @@ bool WireDeviceDecoder::open(const void* payload, uint64_t bytes, const sc_geome
                              const WireExpect& expect, std::string& error) {
     release();
     if (!payload || bytes < kWireHeaderRecordBytes) return refuse(error, "the payload is shorter than the header record");
+    // the payload may still be arriving on another stream: everything enqueued before this call completes first
+    if (!abi(sc_device_sync(), error, "wait for the payload")) return false;
     std::vector<uint8_t> head(kWireHeaderRecordBytes);
     if (!abi(sc_copy_async(head.data(), payload, head.size(), nullptr), error, "head read") ||
         !abi(sc_device_sync(), error, "head read"))

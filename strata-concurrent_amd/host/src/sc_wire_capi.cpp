@@ -83,11 +83,11 @@ int sc_wire_encoder_create(const sc_geometry* g, const sc_decode_slot* slot, int
 uint64_t sc_wire_encoder_bytes(const sc_wire_encoder* e) { return e ? e->enc.bytes() : 0; }
 uint64_t sc_wire_encoder_pool_offset(const sc_wire_encoder* e) { return e ? e->enc.layout().blob_pool_off : 0; }
 
-int sc_wire_encode_async(sc_wire_encoder* e, void* payload, uint64_t capacity, void* stream) {
+int sc_wire_encode_async(sc_wire_encoder* e, void* payload, uint64_t capacity, void* stream, void* gathered) {
     return guarded([&] {
         if (!e) return failed(SC_EINVAL, "conversation wire: missing encoder");
         std::string err;
-        return e->enc.encode(payload, capacity, stream, err) ? done() : failed(SC_EHIP, err);
+        return e->enc.encode(payload, capacity, stream, err, gathered) ? done() : failed(SC_EHIP, err);
     });
 }
 

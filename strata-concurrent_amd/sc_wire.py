@@ -27,7 +27,7 @@ for _name, _res, _args in (
                                          _U64, C.POINTER(_P)]),
     ("sc_wire_encoder_bytes", _U64, [_P]),
     ("sc_wire_encoder_pool_offset", _U64, [_P]),
-    ("sc_wire_encode_async", C.c_int, [_P, _P, _U64, _P]),
+    ("sc_wire_encode_async", C.c_int, [_P, _P, _U64, _P, _P]),
     ("sc_wire_encoder_hash", C.c_int, [_P, C.POINTER(_U64)]),
     ("sc_wire_encoder_destroy", C.c_int, [_P]),
     ("sc_wire_decoder_open", C.c_int, [_P, _U64, C.POINTER(sc.Geometry), C.POINTER(sc.DecodeSlot), C.POINTER(C.c_int64),
@@ -98,8 +98,10 @@ class Encoder:
     def pool_offset(self) -> int:
         return int(lib.sc_wire_encoder_pool_offset(self.handle))
 
-    def encode(self, payload_ptr: int, capacity: int, stream=None) -> None:
-        _check(lib.sc_wire_encode_async(self.handle, payload_ptr, capacity, sc._stream(stream)), "sc_wire_encode_async")
+    def encode(self, payload_ptr: int, capacity: int, stream=None, gathered=None) -> None:
+        """Enqueue the encode; `gathered` (an sc_handoff.Event) is recorded once the payload bytes are in place."""
+        _check(lib.sc_wire_encode_async(self.handle, payload_ptr, capacity, sc._stream(stream),
+                                        gathered.handle if gathered is not None else None), "sc_wire_encode_async")
 
     def hash(self) -> int:
         out = C.c_uint64(0)
