@@ -345,6 +345,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--grid", type=int, default=0, help="workgroups of the move kernel (0 = library default)")
     ap.add_argument("--kernel-only", action="store_true", help="only the timed handoff (for profiler runs)")
+    ap.add_argument("--wire-only", action="store_true",
+                    help="only the wire payload row of the same slot (for profiler runs); prints its JSON")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run 5 device-to-device copies of BYTES (the counter calibration of profiler runs)")
     args = ap.parse_args()
@@ -407,6 +409,10 @@ def main() -> int:
                      "kernel": "sc_move_kernel", "kernel_ms": round(kernel_ms, 4),
                      "algorithmic_bytes_per_launch": 2 * P},
     }
+    if args.wire_only:
+        h2d, d2h = sc.probe_link(256 << 20, 2)
+        print(json.dumps({"wire_payload": wire_payload(sc, geo, T, slot, h2d, d2h)}), flush=True)
+        return 0
     if args.kernel_only:
         print(json.dumps(result), flush=True)
         return 0
