@@ -333,6 +333,25 @@ def wire_payload(sc, geo, tokens: int, slot, link_h2d: float, link_d2h: float, r
                       "then mount"}
 
 
+def quant_carve(sc, geo, tokens: int, stream, reps: int = 10) -> dict:
+    """The quantizing carve of the config-3 geometry: f32 K/V rows into int8 / q4_0 / K8V4 pools plus the GDN state,
+    one launch each.  HBM bytes = the f32 rows read + the codes and scales written + the GDN rows read and written."""
+    case = sc.SyntheticCase(geo, tokens, seed=0x5EED, kv_dtype=sc.SC_DTYPE_F32)
+    out = {"tokens": tokens}
+    for name, fmt in (("int8", sc.SC_KV_INT8), ("q4_0", sc.SC_KV_Q4), ("k8v4", sc.SC_KV_K8V4)):
+        slot = sc.new_quant_slot(geo, fmt, tokens)
+        plan = sc.plan_carve_quant(geo, case.prefill, slot)
+        _, per = time_launches(plan, stream, reps, 2, sc)
+        ms = sum(per) / len(per)
+        moved = plan.payload_bytes
+        out[name] = {"ms": round(ms, 4), "hbm_bytes": moved, "hbm_gbps": round(moved / (ms * 1e-3) / 1e9, 1),
+                     "frac": round(moved / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
+        plan.destroy()
+        for b in slot.buffers():
+            b.free()
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -505,6 +524,11 @@ def main() -> int:
     wp = result["wire_payload"]
     log(f"wire: encode {wp['encode_ms']} ms ({wp['encode_gbps']} GB/s), hash {wp['hash_ms']} ms, mount "
         f"{wp['mount_ms']} ms; checked park {wp['checked_park_gbps']} GB/s, resume {wp['checked_resume_gbps']} GB/s")
+
+    log("quantizing carve: int8 / q4_0 / K8V4 pools from f32 rows, 128K")
+    result["quant_carve"] = quant_carve(sc, geo, T, stream)
+    qc = result["quant_carve"]
+    log("quant carve: " + ", ".join(f"{k} {v['ms']} ms ({v['hbm_gbps']} GB/s)" for k, v in qc.items() if k != "tokens"))
 
     log("config 4: three slots, two parks and one resume overlapped with decode")
     result["config4"] = config4(sc, geo, 0x5EED, d2h)

@@ -135,6 +135,32 @@ int sc_image_layout(const sc_geometry* g, int64_t tokens, sc_image_blob* blobs, 
  * gdn_conv_hist (src/prefill/kernels.cu:219-228) as the writers of the decode layout, plus the GDN row
  * placement of src/prefill/prefill.cpp:1282-1283.  Validates extents against the slot first. */
 int sc_plan_carve(const sc_geometry* g, const sc_prefill_view* src, const sc_decode_slot* dst, sc_plan** out);
+/* Quantized K/V storage of the decode pools (include/strata/kernels/kv_stream.hpp:44-46 KvFormat, plus the K8V4
+ * hybrid of src/core/conversation_snapshot.cpp's format 3): int8 codes with one f16 scale per 64 values (kv_q8.hpp),
+ * q4_0 blocks of 32 values, 18 bytes each (kv_q4.hpp:21-28), or int8 K with q4_0 V. */
+enum { SC_KV_F16 = 0, SC_KV_INT8 = 1, SC_KV_Q4 = 2, SC_KV_K8V4 = 3 };
+
+/* A decode slot whose K/V pools are quantized (QsaState::k_q / v_q / k_scale / v_scale / k_q4 / v_q4,
+ * include/strata/core/layer.hpp:206-215).  Pools are indexed by pool row (page * H + h) * page_size + cell % page_size:
+ * int8 codes 256 bytes per row, int8 scales 4 f16 (8 bytes) per row, q4_0 8 blocks (144 bytes) per row. */
+typedef struct sc_quant_slot {
+    int64_t n_pages;
+    int64_t max_cells;
+    int32_t format;                     /* SC_KV_INT8, SC_KV_Q4 or SC_KV_K8V4 */
+    void* const* k_codes;               /* [n_qsa]: int8 codes (INT8, K8V4) or q4_0 blocks (Q4) */
+    void* const* v_codes;               /* [n_qsa]: int8 codes (INT8) or q4_0 blocks (Q4, K8V4) */
+    uint16_t* const* k_scale;           /* [n_qsa] f16 scales of K (INT8, K8V4), else NULL */
+    uint16_t* const* v_scale;           /* [n_qsa] f16 scales of V (INT8), else NULL */
+    const int32_t* const* page_table;   /* as sc_decode_slot */
+    float* gdn_state;
+} sc_quant_slot;
+
+/* The quantizing carve: f32 prefill K/V rows [T][H][256] (q4_0 rows already rotated, as the reference rotates before
+ * kv_append_q4) into quantized decode pools, plus the GDN state, in one launch.  Replaces the int8 path of kv_append
+ * (src/prefill/kernels.cu:578-600) and kv_append_q4 (src/kernels/cuda/kv_q4.cu:111-129, launched from
+ * src/prefill/prefill.cpp).  src->kv_dtype must be SC_DTYPE_F32 and head_dim 256.  sc_plan_payload_bytes() of the
+ * plan counts the bytes it reads plus the bytes it writes. */
+int sc_plan_carve_quant(const sc_geometry* g, const sc_prefill_view* src, const sc_quant_slot* dst, sc_plan** out);
 /* Pass 1 of the two-pass handoff: carve into a transfer buffer laid out as the image for src->tokens
  * (pos0 must be 0).  The transfer buffer is what a park writes and what crosses to another instance. */
 int sc_plan_gather(const sc_geometry* g, const sc_prefill_view* src, void* image, uint64_t image_bytes,

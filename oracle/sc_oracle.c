@@ -17,6 +17,10 @@
  *   sco_park / sco_resume   A/B/A round trips and byte accounting
  *   sco_fnv1a64             textbook FNV-1a 64 vectors with the standard basis; the reference's seed on empty input
  *   sco_fill_*              the device generators of libsc_handoff.so, bit for bit (GPU tests), and moments
+ *   sco_f32_of_f16          numpy float16 -> float32 on all 65536 bit patterns
+ *   sco_q8_row / sco_q4_row numpy vectorised restatements of the same rules (independent of these loops) on random and
+ *                           edge groups (zero, tied magnitudes, exact .5 quotients, clamping, tiny and huge scales),
+ *                           plus hand-computed blocks
  */
 #include <math.h>
 #include <stdint.h>
@@ -142,6 +146,106 @@ void sco_kv_append(const void* src, int dtype, int64_t T, int64_t pos0, const in
                 }
                 pool[row * D + d] = v;
             }
+        }
+}
+
+/* ---- quantized K/V formats ------------------------------------------------------------------------------------- */
+
+/* binary16 bits -> binary32, exactly (every f16 value is an f32 value). */
+float sco_f32_of_f16(uint16_t h) {
+    const uint32_t sign = (uint32_t) (h & 0x8000u) << 16;
+    const uint32_t e = (h >> 10) & 0x1Fu, m = h & 0x3FFu;
+    uint32_t bits;
+    if (e == 0x1F) bits = sign | 0x7F800000u | (m << 13);
+    else if (e) bits = sign | ((e + 112u) << 23) | (m << 13);
+    else if (!m) bits = sign;
+    else {   /* subnormal: normalise */
+        int shift = 0;
+        uint32_t mm = m;
+        while (!(mm & 0x400u)) { mm <<= 1; ++shift; }
+        bits = sign | ((uint32_t) (113 - shift) << 23) | ((mm & 0x3FFu) << 13);
+    }
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+/* int8 K/V: the reference's int8 kv_append (src/prefill/kernels.cu:578-600) and kv_append_q8
+ * (src/kernels/cuda/kv_q8.cu:29-64), whose host restatement is src/kernels/kv_q8_parity.cpp:78-92.  Per group of 64
+ * values: amax = max |x|; the stored scale is f16(amax / 127) rounded to nearest even; each code is
+ * rint(x / f32(scale)) (ties to even) clamped to [-127, 127], or 0 when the scale is 0.  A NaN value gets code 0
+ * (the reference leaves NaN undefined).  `codes` gets D bytes, `scales` D/64 f16 words. */
+void sco_q8_row(const float* x, int64_t D, int8_t* codes, uint16_t* scales) {
+    for (int64_t g = 0; g < D / 64; ++g) {
+        const float* v = x + g * 64;
+        float amax = 0.0f;
+        for (int t = 0; t < 64; ++t) amax = fmaxf(amax, fabsf(v[t]));
+        const float ratio = amax / 127.0f;
+        uint32_t rb;
+        memcpy(&rb, &ratio, 4);
+        const uint16_t sb = sco_f16_bits(rb);
+        const float sf = sco_f32_of_f16(sb);
+        scales[g] = sb;
+        for (int t = 0; t < 64; ++t) {
+            int q = 0;
+            if (sf > 0.0f && v[t] == v[t]) {
+                const float r = rintf(v[t] / sf);
+                q = r < -127.0f ? -127 : (r > 127.0f ? 127 : (int) r);
+            }
+            codes[g * 64 + t] = (int8_t) q;
+        }
+    }
+}
+
+/* q4_0 K/V: kv_append_q4 (src/kernels/cuda/kv_q4.cu:72-89 q4_group, :111-129), host restatement
+ * src/kernels/kv_q4_parity.cpp:64-87.  Per block of 32 values: the value of largest |x| (ties go to the larger value,
+ * the device kernel's rule); d = that value / -8; id = 1/d (0 when d is 0); each code is trunc(x*id + 8.5) with the
+ * product and the sum rounded separately (the host quantizer's form), clamped to [0, 15]; byte j of the block is
+ * code j | code j+16 << 4; the block is {f16(d) RNE, 16 bytes} = 18 bytes.  Among values equal in magnitude and in
+ * value (only +0 and -0 can be), the first in index order is the maximum, so the sign of a zero d is defined.
+ * `blocks` gets D/32 * 18 bytes. */
+void sco_q4_row(const float* x, int64_t D, uint8_t* blocks) {
+    for (int64_t b = 0; b < D / 32; ++b) {
+        const float* v = x + b * 32;
+        float amax = fabsf(v[0]), mval = v[0];
+        for (int t = 1; t < 32; ++t) {
+            const float a = fabsf(v[t]);
+            if (a > amax || (a == amax && v[t] > mval)) { amax = a; mval = v[t]; }
+        }
+        const float d = mval / -8.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        uint8_t q[32];
+        for (int t = 0; t < 32; ++t) {
+            volatile float prod = v[t] * id;            /* rounded on its own, as the host quantizer does */
+            const float sum = prod + 8.5f;
+            int c = sum == sum ? (int) sum : 0;
+            q[t] = (uint8_t) (c < 0 ? 0 : (c > 15 ? 15 : c));
+        }
+        uint32_t db;
+        memcpy(&db, &d, 4);
+        const uint16_t dh = sco_f16_bits(db);
+        uint8_t* blk = blocks + b * 18;
+        blk[0] = (uint8_t) dh;
+        blk[1] = (uint8_t) (dh >> 8);
+        for (int j = 0; j < 16; ++j) blk[2 + j] = (uint8_t) (q[j] | (q[j + 16] << 4));
+    }
+}
+
+/* The quantizing kv_append: f32 rows [T][H][D] (for q4_0 already rotated, as the reference rotates before
+ * kv_append_q4) into a codes pool [page][H][ps][row_bytes] (row_bytes = D for int8, D/32*18 for q4_0) and, for int8,
+ * a scale pool [page][H][ps][D/64] f16, through the page table like sco_kv_append. fmt: 1 int8, 2 q4_0. */
+void sco_kv_append_quant(const float* src, int fmt, int64_t T, int64_t pos0, const int32_t* table, int64_t n_pages,
+                         int64_t H, int64_t D, int64_t ps, uint8_t* codes, uint16_t* scales) {
+    const int64_t row_bytes = fmt == 1 ? D : D / 32 * 18;
+    for (int64_t t = 0; t < T; ++t)
+        for (int64_t h = 0; h < H; ++h) {
+            const int64_t pos = pos0 + t;
+            const int64_t page = table ? (int64_t) table[pos / ps] : pos / ps;
+            if (page < 0 || page >= n_pages) continue;
+            const int64_t row = (page * H + h) * ps + pos % ps;
+            const float* x = src + (t * H + h) * D;
+            if (fmt == 1) sco_q8_row(x, D, (int8_t*) codes + row * row_bytes, scales + row * (D / 64));
+            else sco_q4_row(x, D, codes + row * row_bytes);
         }
 }
 

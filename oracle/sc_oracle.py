@@ -50,6 +50,10 @@ for _name, _res, _args in (
     ("sco_park", None, [_G, _I64, C.POINTER(_P), C.POINTER(_P), _P, _P]),
     ("sco_resume", None, [_G, _I64, _P, C.POINTER(_P), C.POINTER(_P), _P]),
     ("sco_fnv1a64", _U64, [_P, _U64, _U64]),
+    ("sco_f32_of_f16", C.c_float, [C.c_uint16]),
+    ("sco_q8_row", None, [_P, _I64, _P, _P]),
+    ("sco_q4_row", None, [_P, _I64, _P]),
+    ("sco_kv_append_quant", None, [_P, C.c_int, _I64, _I64, _P, _I64, _I64, _I64, _I64, _P, _P]),
     ("sco_handoff_carve", None, [_G, _I64, _I64, C.c_int, C.POINTER(_P), C.POINTER(_P), C.c_int, C.POINTER(_P),
                                  C.POINTER(_P), _I64, _I64, C.POINTER(_P), C.POINTER(_P), C.POINTER(_P), _I64, _P]),
     ("sco_cpu_handoff", _U64, [_P, _P, _U64, _P]),
@@ -218,3 +222,37 @@ def resume(geo, tokens: int, image: np.ndarray, state: dict) -> None:
 
 def cpu_handoff(src: np.ndarray, dst: np.ndarray, scratch: np.ndarray) -> int:
     return int(lib.sco_cpu_handoff(_ptr(src), _ptr(dst), src.size, _ptr(scratch)))
+
+
+# ---- quantized K/V formats ---------------------------------------------------------------------------------------
+
+def q8_rows(x: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """int8 codes [rows][D] and f16 scale bits [rows][D/64] of f32 rows [rows][D] (sco_q8_row)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    D = x.shape[-1]
+    rows = x.reshape(-1, D)
+    codes = np.zeros(rows.shape, dtype=np.int8)
+    scales = np.zeros((rows.shape[0], D // 64), dtype=np.uint16)
+    for r in range(rows.shape[0]):
+        lib.sco_q8_row(_ptr(rows[r]), D, _ptr(codes[r]), _ptr(scales[r]))
+    return codes, scales
+
+
+def q4_rows(x: np.ndarray) -> np.ndarray:
+    """q4_0 blocks [rows][D/32*18] of f32 rows [rows][D] (sco_q4_row)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    D = x.shape[-1]
+    rows = x.reshape(-1, D)
+    out = np.zeros((rows.shape[0], D // 32 * 18), dtype=np.uint8)
+    for r in range(rows.shape[0]):
+        lib.sco_q4_row(_ptr(rows[r]), D, _ptr(out[r]))
+    return out
+
+
+def kv_append_quant(src: np.ndarray, fmt: int, T: int, pos0: int, table, n_pages: int, H: int, D: int, ps: int,
+                    codes: np.ndarray, scales: np.ndarray | None) -> None:
+    """In place: the quantizing carve of f32 [T][H][D] into a codes pool (and int8 scale pool) (sco_kv_append_quant)."""
+    src = np.ascontiguousarray(src, dtype=np.float32)
+    t = None if table is None else np.ascontiguousarray(table, dtype=np.int32)
+    lib.sco_kv_append_quant(_ptr(src), fmt, T, pos0, _ptr(t) if t is not None else None, n_pages, H, D, ps,
+                            _ptr(codes), _ptr(scales) if scales is not None else None)

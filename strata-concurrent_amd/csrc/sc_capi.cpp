@@ -176,8 +176,10 @@ int finish_plan(std::vector<sc::MoveRow>& rows, const Geo& g, uint64_t payload, 
     for (auto& r : rows) {
         if (r.n >= kMaxRowChunks) return fail(SC_ERANGE, "sc_handoff: a handoff table row beyond 2^31 chunks");
         r.tile0 = tiles;
-        tiles += r.kind == sc::kConv ? (r.n + sc::kConvTileChannels - 1) / sc::kConvTileChannels
-                                     : (r.n + sc::kTileChunks - 1) / sc::kTileChunks;
+        const uint64_t per_tile = r.kind == sc::kConv ? sc::kConvTileChannels
+                                : (r.kind == sc::kKvQ8 || r.kind == sc::kKvQ4) ? sc::kQuantUnitsPerTile
+                                                                              : sc::kTileChunks;
+        tiles += (r.n + per_tile - 1) / per_tile;
     }
     // rows that move nothing still own an (empty) tile range; the kernel never visits them
     sc_plan* p = new (std::nothrow) sc_plan();
@@ -392,6 +394,73 @@ int sc_plan_carve(const sc_geometry* g, const sc_prefill_view* src, const sc_dec
             gdn_rows(o, src, dst->gdn_state, rows);
             payload += uint64_t(o.n_gdn) * o.gdn_row_bytes;
         }
+        return finish_plan(rows, o, payload, out);
+    });
+}
+
+int sc_plan_carve_quant(const sc_geometry* g, const sc_prefill_view* src, const sc_quant_slot* dst, sc_plan** out) {
+    return guarded([&] {
+        if (!out) return fail(SC_EINVAL, "sc_handoff: missing plan output");
+        Geo o;
+        std::string why;
+        if (!geometry(g, o, why)) return snapshot_fail(why.c_str());
+        int rc = check_view(o, src);
+        if (rc) return rc;
+        if (src->kv_dtype != SC_DTYPE_F32) return fail(SC_EINVAL, "sc_handoff: a quantizing carve reads f32 K/V rows");
+        if (o.D != sc::kQuantDim) return fail(SC_EINVAL, "sc_handoff: the quantizing carve supports head_dim 256");
+        if (!dst) return snapshot_fail("missing decode slot");
+        if (dst->format != SC_KV_INT8 && dst->format != SC_KV_Q4 && dst->format != SC_KV_K8V4)
+            return fail(SC_EINVAL, "sc_handoff: unknown quantized K/V format");
+        if (dst->n_pages < 0 || dst->max_cells < 0 || src->pos0 + src->tokens > dst->max_cells)
+            return snapshot_fail("invalid K/V extent");
+        const bool k_int8 = dst->format != SC_KV_Q4, v_int8 = dst->format == SC_KV_INT8;
+        const bool identity = !dst->page_table || std::all_of(dst->page_table, dst->page_table + o.n_qsa,
+                                                              [](const int32_t* t) { return t == nullptr; });
+        if (identity && dst->max_cells > dst->n_pages * o.ps) return snapshot_fail("invalid K/V extent");
+        if (o.n_qsa > 0 && (!dst->k_codes || !dst->v_codes || (k_int8 && !dst->k_scale) || (v_int8 && !dst->v_scale)))
+            return snapshot_fail("missing target state buffer");
+        for (int64_t j = 0; j < o.n_qsa; ++j) {
+            if (!dst->k_codes[j] || !dst->v_codes[j] || (k_int8 && !dst->k_scale[j]) || (v_int8 && !dst->v_scale[j]))
+                return snapshot_fail("missing target state buffer");
+            if ((reinterpret_cast<uintptr_t>(dst->k_codes[j]) | reinterpret_cast<uintptr_t>(dst->v_codes[j])) & 3u ||
+                (k_int8 && (reinterpret_cast<uintptr_t>(dst->k_scale[j]) & 7u)) ||
+                (v_int8 && (reinterpret_cast<uintptr_t>(dst->v_scale[j]) & 7u)))
+                return fail(SC_EINVAL, "sc_handoff: code pools must be 4-byte and scale pools 8-byte aligned");
+        }
+        if (src->with_gdn && o.n_gdn > 0) {
+            if (!dst->gdn_state) return snapshot_fail("missing running-state buffer");
+            if (!aligned16(dst->gdn_state) || o.gdn_row_bytes % 16)
+                return fail(SC_EINVAL, "sc_handoff: GDN rows must be 16-byte aligned multiples of 16 bytes");
+        }
+        std::vector<sc::MoveRow> rows;
+        uint64_t payload = 0;
+        const uint64_t units = uint64_t(src->tokens) * uint64_t(o.H);
+        for (int64_t j = 0; j < o.n_qsa && units; ++j) {
+            const int32_t* table = dst->page_table ? dst->page_table[j] : nullptr;
+            const void* srcs[2] = {src->k[j], src->v[j]};
+            void* codes[2] = {dst->k_codes[j], dst->v_codes[j]};
+            uint16_t* scales[2] = {k_int8 ? dst->k_scale[j] : nullptr, v_int8 ? dst->v_scale[j] : nullptr};
+            const bool int8[2] = {k_int8, v_int8};
+            for (int a = 0; a < 2; ++a) {
+                sc::MoveRow r{};
+                r.kind = int8[a] ? sc::kKvQ8 : sc::kKvQ4;
+                r.src = static_cast<const uint8_t*>(srcs[a]);
+                r.dst = static_cast<uint8_t*>(codes[a]);
+                r.dst2 = reinterpret_cast<uint8_t*>(scales[a]);
+                r.table = table;
+                r.pos0 = src->pos0;
+                r.ld = dst->n_pages;
+                r.aux = int32_t(src->tokens);
+                r.n = units;
+                rows.push_back(r);
+                payload += units * sc::kQuantDim * 4 + units * (int8[a] ? sc::kQuantDim + 8 : sc::kQuantDim / 32 * 18);
+            }
+        }
+        if (src->with_gdn) {
+            gdn_rows(o, src, dst->gdn_state, rows);
+            payload += 2 * uint64_t(o.n_gdn) * o.gdn_row_bytes;
+        }
+        // the payload of a quantizing carve counts bytes read plus bytes written (they differ)
         return finish_plan(rows, o, payload, out);
     });
 }

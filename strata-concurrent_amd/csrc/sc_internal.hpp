@@ -27,7 +27,13 @@ enum MoveKind : int32_t {
     kPagesGather = 6,   // pool pages through the page table -> contiguous pages
     kCopy = 7,          // contiguous 16-byte chunks
     kZero = 8,          // zero-fill 16-byte chunks (padding and stale-cell tails of an image)
+    kKvQ8 = 9,          // f32 rows [T][H][256] -> int8 codes [prow][256] + f16 scales [prow][4] (quantizing kv_append)
+    kKvQ4 = 10,         // f32 rows [T][H][256] (already rotated) -> q4_0 blocks [prow][8 x 18 B]
 };
+
+// Quantizing rows move one (token, head) row of 256 values per wave at a time: a tile is 16 rows (16 KiB of f32).
+constexpr int kQuantUnitsPerTile = 16;
+constexpr int kQuantDim = 256;
 
 // Division by a runtime constant d >= 1 for 32-bit numerators: q = (umulhi(n, m) + n) >> s with
 // s = ceil(log2 d), m = floor(2^32 * (2^s - d) / d) + 1 (the round-up method of Granlund and Montgomery,
@@ -46,7 +52,7 @@ inline FastDiv make_fastdiv(uint32_t d) {
     return f;
 }
 
-// One row of the handoff table (device-resident, 64 bytes).
+// One row of the handoff table (device-resident, 72 bytes).
 struct MoveRow {
     int32_t kind;
     int32_t aux;            // kKv*: source tokens (rows past them are zero-filled); kConv: history rows
@@ -58,8 +64,9 @@ struct MoveRow {
     uint64_t n;             // chunks (kKv*, kRec, kPages*, kCopy, kZero) or channels (kConv)
     int64_t pos0;           // kKv*: first decode cell; kConv: rows available in the source
     int64_t ld;             // kConv: source row stride in floats; kKv*, kPages*: physical pages in the pool
+    uint8_t* dst2;          // kKvQ8: the f16 scale pool
 };
-static_assert(sizeof(MoveRow) == 64, "handoff table rows are 64 bytes");
+static_assert(sizeof(MoveRow) == 72, "handoff table rows are 72 bytes");
 
 // Geometry every row of one plan shares.
 struct MoveGeo {

@@ -221,6 +221,134 @@ __device__ void tile_conv(const MoveRow& r, uint64_t local, float (*lds)[kConvTi
     __syncthreads();
 }
 
+// ---- quantizing rows (int8, q4_0) -------------------------------------------------------------------------------
+// One wave quantizes one (token, head) row of 256 f32 values: lane l holds values 4l..4l+3 (one 16-byte load, the
+// row's 1 KiB read coalesced).  The rules are the reference's int8 kv_append (src/prefill/kernels.cu:578-600,
+// src/kernels/cuda/kv_q8.cu:29-64) and q4_0 kv_append_q4 (src/kernels/cuda/kv_q4.cu:72-129): see the oracle
+// (sco_q8_row, sco_q4_row) for the exact definitions these lanes reproduce.  Divisions are IEEE divisions (the
+// library is built with correctly rounded f32 divide), and the q4 product and sum are rounded separately.
+
+__device__ __forceinline__ float f32_of_f16(uint32_t h) {
+    const uint32_t sign = (h & 0x8000u) << 16, e = (h >> 10) & 0x1Fu, m = h & 0x3FFu;
+    if (e == 0x1Fu) return __uint_as_float(sign | 0x7F800000u | (m << 13));
+    if (e) return __uint_as_float(sign | ((e + 112u) << 23) | (m << 13));
+    // zero or subnormal: m * 2^-24 is exact in f32
+    const float v = float(m) * 0x1p-24f;
+    return sign ? -v : v;
+}
+
+__device__ __forceinline__ uint32_t q8_code(float x, float sf) {
+    if (!(sf > 0.0f) || x != x) return 0u;
+    const float r = __builtin_rintf(x / sf);
+    const int q = r < -127.0f ? -127 : (r > 127.0f ? 127 : int(r));
+    return uint32_t(q) & 0xFFu;
+}
+
+constexpr int kQuantUnitsPerWave = kQuantUnitsPerTile / (kThreads / 64);
+
+// The wave's rows of a tile, all loads issued before any row is quantized (four 1 KiB reads in flight per wave).
+__device__ __forceinline__ int load_units(const MoveRow& r, uint64_t local, int lane, int wave,
+                                          u32x4 (&v)[kQuantUnitsPerWave], uint32_t (&unit)[kQuantUnitsPerWave]) {
+    int n = 0;
+#pragma unroll
+    for (int i = 0; i < kQuantUnitsPerWave; ++i) {
+        unit[i] = uint32_t(local) * kQuantUnitsPerTile + uint32_t(wave * kQuantUnitsPerWave + i);
+        if (unit[i] < r.n) {   // uniform across the wave
+            v[i] = ld16(r.src + uint64_t(unit[i]) * (kQuantDim * 4) + lane * 16);
+            n = i + 1;
+        }
+    }
+    return n;
+}
+
+__device__ void tile_q8(const MoveRow& r, const MoveGeo& g, uint64_t local) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    u32x4 vs[kQuantUnitsPerWave];
+    uint32_t units[kQuantUnitsPerWave];
+    const int n_units = load_units(r, local, lane, wave, vs, units);
+#pragma unroll
+    for (int i = 0; i < kQuantUnitsPerWave; ++i) {
+        if (i >= n_units) break;
+        const uint32_t unit = units[i];
+        const u32x4 v = vs[i];
+        const float x0 = __uint_as_float(v.x), x1 = __uint_as_float(v.y), x2 = __uint_as_float(v.z),
+                    x3 = __uint_as_float(v.w);
+        // max |x| over the 64 values of this lane's group: 16 lanes (fmax is exact, so any order gives the same)
+        float a = fmaxf(fmaxf(fabsf(x0), fabsf(x1)), fmaxf(fabsf(x2), fabsf(x3)));
+        a = fmaxf(a, __shfl_xor(a, 8));
+        a = fmaxf(a, __shfl_xor(a, 4));
+        a = fmaxf(a, __shfl_xor(a, 2));
+        a = fmaxf(a, __shfl_xor(a, 1));
+        const uint32_t sb = f16_bits_rne(__float_as_uint(a / 127.0f));
+        const float sf = f32_of_f16(sb);
+        const uint32_t codes = q8_code(x0, sf) | (q8_code(x1, sf) << 8) | (q8_code(x2, sf) << 16) | (q8_code(x3, sf) << 24);
+        const uint32_t s1 = __shfl(sb, 16), s2 = __shfl(sb, 32), s3 = __shfl(sb, 48);
+        const int64_t prow = pool_row(r, g, unit);
+        if (prow < 0) continue;
+        using g32 = __attribute__((address_space(1))) uint32_t;
+        using g64 = __attribute__((address_space(1))) uint64_t;
+        *(g32*) (r.dst + uint64_t(prow) * kQuantDim + lane * 4) = codes;
+        if (lane == 0) {
+            const uint64_t packed = uint64_t(sb | (s1 << 16)) | (uint64_t(s2 | (s3 << 16)) << 32);
+            *(g64*) (r.dst2 + uint64_t(prow) * 8) = packed;
+        }
+    }
+}
+
+// The q4_0 block maximum: larger |x|, then larger value, then lower index (so the sign of a zero maximum is the
+// first zero's).
+__device__ __forceinline__ void q4_pick(float& amax, float& mval, uint32_t& idx, float a, float v, uint32_t j) {
+    if (a > amax || (a == amax && (v > mval || (v == mval && j < idx)))) { amax = a; mval = v; idx = j; }
+}
+
+__device__ __forceinline__ uint32_t q4_code(float x, float id) {
+#pragma clang fp contract(off)
+    const float prod = x * id;
+    const float sum = prod + 8.5f;
+    const int c = sum == sum ? int(sum) : 0;
+    return uint32_t(c < 0 ? 0 : (c > 15 ? 15 : c));
+}
+
+__device__ void tile_q4(const MoveRow& r, const MoveGeo& g, uint64_t local) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lb = lane & 7;            // lane within its 32-value block
+    const uint32_t blk = uint32_t(lane >> 3);
+    u32x4 vs[kQuantUnitsPerWave];
+    uint32_t units[kQuantUnitsPerWave];
+    const int n_units = load_units(r, local, lane, wave, vs, units);
+#pragma unroll
+    for (int i = 0; i < kQuantUnitsPerWave; ++i) {
+        if (i >= n_units) break;
+        const uint32_t unit = units[i];
+        const u32x4 v = vs[i];
+        const float x[4] = {__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w)};
+        float amax = fabsf(x[0]), mval = x[0];
+        uint32_t idx = uint32_t(lb * 4);
+        for (int k = 1; k < 4; ++k) q4_pick(amax, mval, idx, fabsf(x[k]), x[k], uint32_t(lb * 4 + k));
+        for (int o = 4; o > 0; o >>= 1) {
+            const float a2 = __shfl_xor(amax, o), v2 = __shfl_xor(mval, o);
+            const uint32_t j2 = __shfl_xor(idx, o);
+            q4_pick(amax, mval, idx, a2, v2, j2);
+        }
+        const float d = mval / -8.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        const uint32_t q = q4_code(x[0], id) | (q4_code(x[1], id) << 8) | (q4_code(x[2], id) << 16) |
+                           (q4_code(x[3], id) << 24);
+        const uint32_t hi = __shfl_down(q, 4);   // lane lb + 4 holds the block's values 16 + 4 lb .. 19 + 4 lb
+        const int64_t prow = pool_row(r, g, unit);
+        if (prow < 0) continue;
+        // block `blk` of the row: {f16 d, qs[16]}, 18 bytes at 18 * blk; qs[4 lb .. 4 lb + 3] from lanes lb, lb + 4
+        uint8_t* row = r.dst + uint64_t(prow) * (kQuantDim / 32 * 18) + blk * 18;
+        using g16 = __attribute__((address_space(1))) uint16_t;
+        if (lb == 0) *(g16*) (row) = uint16_t(f16_bits_rne(__float_as_uint(d)));
+        if (lb < 4) {
+            const uint32_t bytes = q | (hi << 4);
+            *(g16*) (row + 2 + 4 * lb) = uint16_t(bytes);
+            *(g16*) (row + 4 + 4 * lb) = uint16_t(bytes >> 16);
+        }
+    }
+}
+
 // One workgroup per tile (the grid strides only when a plan has more tiles than one launch may hold): measured
 // on the 128K handoff, a grid of one tile per workgroup beat every persistent grid from 1024 to 65536 workgroups.
 // `tile_row[t]` names the handoff table row of tile t, so a workgroup finds its row with two scalar loads and no
@@ -244,6 +372,8 @@ __global__ void __launch_bounds__(kThreads) sc_move_kernel(const MoveRow* __rest
             case kPagesGather: tile_pages(r, geo, local, false); break;
             case kCopy: tile_copy(r, local, false); break;
             case kZero: tile_copy(r, local, true); break;
+            case kKvQ8: tile_q8(r, geo, local); break;
+            case kKvQ4: tile_q4(r, geo, local); break;
             default: break;
         }
     }

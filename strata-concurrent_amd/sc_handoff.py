@@ -73,6 +73,16 @@ class BatchDesc(C.Structure):
                 ("lens_out", C.c_void_p)]
 
 
+SC_KV_F16, SC_KV_INT8, SC_KV_Q4, SC_KV_K8V4 = 0, 1, 2, 3
+
+
+class QuantSlot(C.Structure):
+    _fields_ = [("n_pages", C.c_int64), ("max_cells", C.c_int64), ("format", C.c_int32),
+                ("k_codes", C.POINTER(C.c_void_p)), ("v_codes", C.POINTER(C.c_void_p)),
+                ("k_scale", C.POINTER(C.c_void_p)), ("v_scale", C.POINTER(C.c_void_p)),
+                ("page_table", C.POINTER(C.c_void_p)), ("gdn_state", C.c_void_p)]
+
+
 class BlobMap(C.Structure):
     _fields_ = [("k_off", C.POINTER(C.c_uint64)), ("v_off", C.POINTER(C.c_uint64)), ("gdn_off", C.c_uint64),
                 ("zero", C.POINTER(C.c_uint64)), ("n_zero", C.c_int64)]
@@ -135,6 +145,7 @@ _SIGS = {
     "sc_fill_uniform_f32": (C.c_int, [_P, _U64, C.c_float, C.c_float, _U64, _U64, _P]),
     "sc_fill_normal_f32": (C.c_int, [_P, _U64, _U64, _U64, _P]),
     "sc_decode_probe": (C.c_int, [_P, _U64, _P, _I64, _P]),
+    "sc_plan_carve_quant": (C.c_int, [_GEO, C.POINTER(PrefillView), C.POINTER(QuantSlot), C.POINTER(_P)]),
     "sc_plan_capture_map": (C.c_int, [_GEO, C.POINTER(DecodeSlot), _I64, _P, _U64, C.POINTER(BlobMap), C.POINTER(_P)]),
     "sc_plan_scatter_map": (C.c_int, [_GEO, _P, _U64, C.POINTER(BlobMap), _I64, C.POINTER(DecodeSlot), C.POINTER(_P)]),
     "sc_fnv1a64_workspace_bytes": (_U64, [_U64]),
@@ -712,3 +723,61 @@ class HashPlan:
     def free(self) -> None:
         self.ws.free()
         self.out.free()
+
+
+@dataclass
+class QuantPools:
+    """Quantized decode pools of one slot: per QSA layer K and V codes (int8 [n_pages][H][ps][256] or q4_0
+    [n_pages][H][ps][144] bytes) and int8 scales ([n_pages][H][ps][4] f16), plus the GDN rows."""
+    geo: Geometry
+    fmt: int
+    n_pages: int
+    max_cells: int
+    k_codes: list
+    v_codes: list
+    k_scale: list
+    v_scale: list
+    gdn: object
+    tables: list | None = None
+    _keep: tuple = field(default=(), repr=False)
+
+    def c_struct(self) -> QuantSlot:
+        kc = _ptrs([t.ptr for t in self.k_codes])
+        vc = _ptrs([t.ptr for t in self.v_codes])
+        ks = _ptrs([t.ptr for t in self.k_scale]) if self.k_scale else None
+        vs = _ptrs([t.ptr for t in self.v_scale]) if self.v_scale else None
+        ts = _ptrs([t.data_ptr() if t is not None else None for t in self.tables]) if self.tables else None
+        self._keep = (kc, vc, ks, vs, ts)
+        cast = lambda a: C.cast(a, C.POINTER(C.c_void_p)) if a is not None else None  # noqa: E731
+        return QuantSlot(n_pages=self.n_pages, max_cells=self.max_cells, format=self.fmt, k_codes=cast(kc),
+                         v_codes=cast(vc), k_scale=cast(ks), v_scale=cast(vs), page_table=cast(ts),
+                         gdn_state=self.gdn.data_ptr() if self.gdn is not None else None)
+
+    def buffers(self) -> list:
+        return [*self.k_codes, *self.v_codes, *self.k_scale, *self.v_scale, *([self.gdn] if self.gdn is not None else [])]
+
+
+def new_quant_slot(geo: Geometry, fmt: int, max_cells: int, n_pages: int | None = None, tables=None,
+                   fill: int = 0) -> QuantPools:
+    ps, H = geo.page_size, geo.n_head_kv
+    n_pages = n_pages if n_pages is not None else (max_cells + ps - 1) // ps
+    rows = n_pages * H * ps
+    k_int8, v_int8 = fmt != SC_KV_Q4, fmt == SC_KV_INT8
+    k = [DeviceBuffer(rows * (256 if k_int8 else 144), "uint8") for _ in range(geo.n_qsa)]
+    v = [DeviceBuffer(rows * (256 if v_int8 else 144), "uint8") for _ in range(geo.n_qsa)]
+    ks = [DeviceBuffer(rows * 4, "uint16") for _ in range(geo.n_qsa)] if k_int8 else []
+    vs = [DeviceBuffer(rows * 4, "uint16") for _ in range(geo.n_qsa)] if v_int8 else []
+    gdn = DeviceBuffer((geo.n_gdn, geo.gdn_row_floats), "float32") if geo.n_gdn else None
+    slot = QuantPools(geo, fmt, n_pages, max_cells, k, v, ks, vs, gdn, tables)
+    for b in slot.buffers():
+        b.fill(fill)
+    return slot
+
+
+def plan_carve_quant(geo: Geometry, prefill: PrefillBuffers, slot: QuantPools, pos0: int = 0,
+                     with_gdn: bool = True) -> Plan:
+    view, keep = prefill.view(pos0, with_gdn)
+    cs = slot.c_struct()
+    h = C.c_void_p()
+    check(lib.sc_plan_carve_quant(C.byref(geo), C.byref(view), C.byref(cs), C.byref(h)), "sc_plan_carve_quant")
+    return Plan(h.value, (keep, slot._keep))

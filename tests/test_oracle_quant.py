@@ -1,0 +1,144 @@
+"""Pins the oracle's quantized K/V formats (sco_q8_row, sco_q4_row, sco_kv_append_quant) with independent numpy
+restatements of the reference's rules and with hand-computed groups.
+
+int8 (src/prefill/kernels.cu:578-600; kv_q8.cu:29-64; host form kv_q8_parity.cpp:78-92): per 64 values the scale is
+f16(max|x| / 127) rounded to nearest even, codes rint(x / f32(scale)) clamped to +-127 (0 when the scale is 0).
+q4_0 (kv_q4.cu:72-89; host form kv_q4_parity.cpp:64-87): per 32 values d = (value of largest |x|, ties to the larger)
+/ -8, codes trunc(x * (1/d) + 8.5) with separately rounded product and sum, clamped to [0, 15], packed j | j+16 << 4
+after the f16 scale.  numpy float32 arithmetic is IEEE single precision with no contraction, so these vectorised
+forms are the same definitions computed a different way: a wrong group size, a dropped clamp, a rounding mode or a
+nibble order fails them.
+"""
+import numpy as np
+import pytest
+
+F32 = np.float32
+
+
+def q8_numpy(x):
+    g = x.reshape(-1, 64).astype(F32)
+    amax = np.max(np.abs(g), axis=1)
+    scale = (amax / F32(127)).astype(np.float16)
+    sf = scale.astype(F32)[:, None]
+    with np.errstate(divide="ignore", invalid="ignore"):
+        q = np.rint(g / np.where(sf > 0, sf, F32(1)))
+    q = np.where((sf > 0) & ~np.isnan(g), np.clip(q, -127, 127), 0).astype(np.int8)
+    return q.reshape(x.shape), scale.view(np.uint16).reshape(x.shape[:-1] + (x.shape[-1] // 64,))
+
+
+def q4_numpy(x):
+    g = x.reshape(-1, 32).astype(F32)
+    a = np.abs(g)
+    amax = a.max(axis=1, keepdims=True)
+    mval = np.where(a == amax, g, -np.inf).max(axis=1)
+    d = (mval / F32(-8)).astype(F32)
+    with np.errstate(divide="ignore"):
+        idv = np.where(d != 0, F32(1) / np.where(d != 0, d, F32(1)), F32(0)).astype(F32)
+    prod = (g * idv[:, None]).astype(F32)
+    s = (prod + F32(8.5)).astype(F32)
+    q = np.clip(np.trunc(s), 0, 15).astype(np.uint8)
+    packed = (q[:, :16] | (q[:, 16:] << 4)).astype(np.uint8)
+    dh = d.astype(np.float16).view(np.uint16)
+    out = np.zeros((g.shape[0], 18), np.uint8)
+    out[:, 0] = dh & 0xFF
+    out[:, 1] = dh >> 8
+    out[:, 2:] = packed
+    return out.reshape(x.shape[:-1] + (x.shape[-1] // 32 * 18,))
+
+
+def _groups(rng, n, D):
+    x = rng.standard_normal((n, D)).astype(F32) * F32(3)
+    x[0] = 0                                       # an all-zero row: scale 0, codes 0 / d 0, codes 8
+    n64 = min(D, 64)
+    x[1, :n64] = np.linspace(-127, 127, n64, dtype=F32)     # exact integer quotients
+    x[2, :32] = F32(2.0)
+    x[2, 5] = F32(-5.0)
+    x[2, 9] = F32(5.0)                             # tied magnitudes: the positive value is the q4 maximum
+    x[3] = rng.standard_normal(D).astype(F32) * F32(1e-3)   # tiny values: f16 scales near the subnormal range
+    x[4] = rng.standard_normal(D).astype(F32) * F32(2e4)    # large values: scales near the f16 top
+    x[5, :n64] = F32(127) * np.arange(n64, dtype=F32) / F32(64) + F32(0.5)   # quotients near .5
+    return x
+
+
+def test_f32_of_f16_all_patterns(oracle):
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    want = bits.view(np.float16).astype(F32)
+    got = np.array([oracle.lib.sco_f32_of_f16(int(b)) for b in bits], dtype=F32)
+    same = (got.view(np.uint32) == want.view(np.uint32)) | (np.isnan(got) & np.isnan(want))
+    assert same.all()
+
+
+@pytest.mark.parametrize("D", [64, 256, 512])
+def test_q8_matches_numpy(oracle, D):
+    x = _groups(np.random.default_rng(D), 200, D)
+    codes, scales = oracle.q8_rows(x)
+    wc, ws = q8_numpy(x)
+    assert np.array_equal(codes, wc)
+    assert np.array_equal(scales, ws)
+
+
+def test_q8_hand_computed(oracle):
+    x = np.zeros(64, F32)
+    x[0], x[1], x[2], x[3] = F32(127), F32(-63.5), F32(0.49999997), F32(-127)
+    codes, scales = oracle.q8_rows(x[None])
+    assert scales[0, 0] == 0x3C00                  # 127 / 127 = 1.0
+    assert list(codes[0, :4]) == [127, -64, 0, -127]   # -63.5 rounds half to even: -64
+    y = np.zeros(64, F32)
+    y[0] = F32(1e-9)                              # 1e-9 / 127 is below half the smallest f16 subnormal: scale 0
+    codes, scales = oracle.q8_rows(y[None])
+    assert scales[0, 0] == 0 and not codes.any()
+
+
+@pytest.mark.parametrize("D", [32, 256])
+def test_q4_matches_numpy(oracle, D):
+    x = _groups(np.random.default_rng(D + 1), 200, D)
+    assert np.array_equal(oracle.q4_rows(x), q4_numpy(x))
+
+
+def test_q4_hand_computed(oracle):
+    x = np.zeros(32, F32)
+    x[0], x[16], x[3], x[19] = F32(-8), F32(4), F32(1), F32(-8)   # tie at |8|: both -8, so d = -8 / -8 = 1
+    blk = oracle.q4_rows(x[None])[0]
+    assert int(blk[0]) | (int(blk[1]) << 8) == 0x3C00       # d = 1.0
+    # codes: trunc(x / 1 + 8.5): -8 -> 0, 4 -> 12, 1 -> 9, 0 -> 8
+    assert blk[2 + 0] == (0 | (12 << 4))
+    assert blk[2 + 3] == (9 | (0 << 4))
+    assert blk[2 + 1] == (8 | (8 << 4))
+    z = np.zeros(32, F32)
+    zb = oracle.q4_rows(z[None])[0]
+    # all +0: the maximum is +0, d = +0 / -8 = -0 (f16 0x8000), id 0, every code trunc(8.5) = 8
+    assert zb[0] == 0 and zb[1] == 0x80 and all(b == 0x88 for b in zb[2:])
+    t = np.zeros(32, F32)
+    t[0], t[1] = F32(-3), F32(3)                   # tied magnitudes: the larger value (+3) is the maximum
+    tb = oracle.q4_rows(t[None])[0]
+    d = F32(3) / F32(-8)
+    assert int(tb[0]) | (int(tb[1]) << 8) == int(np.array([d], F32).astype(np.float16).view(np.uint16)[0])
+
+
+@pytest.mark.parametrize("fmt", [1, 2])
+def test_quant_placement(oracle, fmt):
+    """The quantizing carve places row (t, h) where kv_append places it, and skips non-resident pages."""
+    T, H, D, ps, n_pages, pos0 = 11, 2, 256, 4, 8, 3
+    rng = np.random.default_rng(fmt)
+    src = rng.standard_normal((T, H, D)).astype(F32)
+    table = np.array([5, -1, 0, 7, 2, 1, 3, 4], np.int32)
+    row_bytes = D if fmt == 1 else D // 32 * 18
+    codes = np.full((n_pages, H, ps, row_bytes), 0xEE, np.uint8)
+    scales = np.full((n_pages, H, ps, D // 64), 0xEEEE, np.uint16)
+    oracle.kv_append_quant(src, fmt, T, pos0, table, n_pages, H, D, ps, codes, scales if fmt == 1 else None)
+    for t in range(T):
+        pos = pos0 + t
+        page = table[pos // ps]
+        for h in range(H):
+            if page < 0:
+                continue
+            got = codes[page, h, pos % ps]
+            if fmt == 1:
+                c, s = q8_numpy(src[t, h])
+                assert np.array_equal(got.view(np.int8), c) and np.array_equal(scales[page, h, pos % ps], s)
+            else:
+                assert np.array_equal(got, q4_numpy(src[t, h]))
+    # the page behind the -1 entry (cells 4..7) is never written
+    untouched = [p for p in range(n_pages) if p not in set(table[table >= 0][: (pos0 + T + ps - 1) // ps].tolist())]
+    for p in untouched:
+        assert (codes[p] == 0xEE).all()
