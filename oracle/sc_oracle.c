@@ -178,7 +178,7 @@ float sco_f32_of_f16(uint16_t h) {
 void sco_q8_row(const float* x, int64_t D, int8_t* codes, uint16_t* scales) {
     for (int64_t g = 0; g < D / 64; ++g) {
         const float* v = x + g * 64;
-        float amax = 0.0f;
+        float amax = 0.0f;                              /* from 0, as kv_q8_parity.cpp:83-84: NaNs never count */
         for (int t = 0; t < 64; ++t) amax = fmaxf(amax, fabsf(v[t]));
         const float ratio = amax / 127.0f;
         uint32_t rb;
@@ -187,10 +187,10 @@ void sco_q8_row(const float* x, int64_t D, int8_t* codes, uint16_t* scales) {
         const float sf = sco_f32_of_f16(sb);
         scales[g] = sb;
         for (int t = 0; t < 64; ++t) {
-            int q = 0;
+            int q = 0;                                  /* a NaN quotient converts to 0 (CUDA's float->int rule) */
             if (sf > 0.0f && v[t] == v[t]) {
                 const float r = rintf(v[t] / sf);
-                q = r < -127.0f ? -127 : (r > 127.0f ? 127 : (int) r);
+                q = r != r ? 0 : (r < -127.0f ? -127 : (r > 127.0f ? 127 : (int) r));
             }
             codes[g * 64 + t] = (int8_t) q;
         }
@@ -207,8 +207,10 @@ void sco_q8_row(const float* x, int64_t D, int8_t* codes, uint16_t* scales) {
 void sco_q4_row(const float* x, int64_t D, uint8_t* blocks) {
     for (int64_t b = 0; b < D / 32; ++b) {
         const float* v = x + b * 32;
-        float amax = fabsf(v[0]), mval = v[0];
-        for (int t = 1; t < 32; ++t) {
+        /* NaN never compares larger, so it is never picked (the host form's rule, kv_q4_parity.cpp:68-73); a block
+         * of NaNs keeps the start value +0.  Among equals the first index stays. */
+        float amax = -1.0f, mval = 0.0f;
+        for (int t = 0; t < 32; ++t) {
             const float a = fabsf(v[t]);
             if (a > amax || (a == amax && v[t] > mval)) { amax = a; mval = v[t]; }
         }

@@ -17,6 +17,7 @@
 
 #include <cstdint>
 
+#include "sc_convert.hpp"
 #include "sc_internal.hpp"
 
 namespace sc {
@@ -36,33 +37,6 @@ using u32x4 = __attribute__((ext_vector_type(4))) uint32_t;
 using gu32x4 = __attribute__((address_space(1))) u32x4;
 __device__ __forceinline__ u32x4 ld16(const uint8_t* p) { return *(const gu32x4*) (p); }
 __device__ __forceinline__ void st16(uint8_t* p, u32x4 v) { __builtin_nontemporal_store(v, (gu32x4*) (p)); }
-
-// IEEE-754 binary32 -> binary16, round to nearest even, as raw bits.  Finite values too large for f16 become
-// infinities, an f32 infinity stays one and a NaN becomes a quiet NaN (sign | 0x7C00 | 0x200), the convention
-// of the reference's f16_from_f32 (include/strata/kernels/f16_bits.hpp:37-70).  Written from the format
-// definition: keep 10 mantissa bits, round on the 13 dropped bits with ties to even, and in the subnormal range
-// shift the restored implicit bit right so the rounding point moves with the exponent.
-__device__ __forceinline__ uint32_t f16_bits_rne(uint32_t x) {
-    const uint32_t sign = (x >> 16) & 0x8000u;
-    const uint32_t e8 = (x >> 23) & 0xFFu;
-    uint32_t man = x & 0x7FFFFFu;
-    if (e8 == 0xFFu) return sign | 0x7C00u | (man ? 0x200u : 0u);
-    const int e = int(e8) - 112;   // rebias 127 -> 15
-    if (e >= 31) return sign | 0x7C00u;
-    if (e <= 0) {
-        if (e < -10) return sign;
-        man |= 0x800000u;
-        const uint32_t sh = uint32_t(14 - e);
-        uint32_t h = man >> sh;
-        const uint32_t rem = man & ((1u << sh) - 1u), half = 1u << (sh - 1);
-        h += (rem > half || (rem == half && (h & 1u))) ? 1u : 0u;
-        return sign | h;
-    }
-    uint32_t h = sign | (uint32_t(e) << 10) | (man >> 13);
-    const uint32_t rem = man & 0x1FFFu;
-    h += (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) ? 1u : 0u;
-    return h;
-}
 
 // Pool byte offset of (cell, head) for a K/V row; -1 when the page is not resident or out of the pool.
 __device__ __forceinline__ int64_t pool_row(const MoveRow& r, const MoveGeo& g, uint32_t src_row) {
@@ -225,26 +199,46 @@ __device__ void tile_conv(const MoveRow& r, uint64_t local, float (*lds)[kConvTi
 // One wave quantizes one (token, head) row of 256 f32 values: lane l holds values 4l..4l+3 (one 16-byte load, the
 // row's 1 KiB read coalesced).  The rules are the reference's int8 kv_append (src/prefill/kernels.cu:578-600,
 // src/kernels/cuda/kv_q8.cu:29-64) and q4_0 kv_append_q4 (src/kernels/cuda/kv_q4.cu:72-129): see the oracle
-// (sco_q8_row, sco_q4_row) for the exact definitions these lanes reproduce.  Divisions are IEEE divisions (the
-// library is built with correctly rounded f32 divide), and the q4 product and sum are rounded separately.
+// (sco_q8_row, sco_q4_row) for the exact definitions these lanes reproduce.  The divisions written with `/` are
+// IEEE divisions (the library is built with correctly rounded f32 divide), the int8 quotients are formed so that
+// they equal them (q8_code), and the q4 product and sum are rounded separately.
 
-__device__ __forceinline__ float f32_of_f16(uint32_t h) {
-    const uint32_t sign = (h & 0x8000u) << 16, e = (h >> 10) & 0x1Fu, m = h & 0x3FFu;
-    if (e == 0x1Fu) return __uint_as_float(sign | 0x7F800000u | (m << 13));
-    if (e) return __uint_as_float(sign | ((e + 112u) << 23) | (m << 13));
-    // zero or subnormal: m * 2^-24 is exact in f32
-    const float v = float(m) * 0x1p-24f;
-    return sign ? -v : v;
-}
-
-__device__ __forceinline__ uint32_t q8_code(float x, float sf) {
-    if (!(sf > 0.0f) || x != x) return 0u;
-    const float r = __builtin_rintf(x / sf);
-    const int q = r < -127.0f ? -127 : (r > 127.0f ? 127 : int(r));
-    return uint32_t(q) & 0xFFu;
+// The int8 code rint(x / sf) clamped to [-127, 127], with x / sf the correctly rounded quotient, formed from y, the
+// correctly rounded 1 / sf computed once per group: q0 = x * y, then one correction q = q0 + (x - q0 * sf) * y with
+// the residual exact in an fma (Markstein's method: P. Markstein, "Computation of elementary functions on the IBM
+// RISC System/6000 processor", IBM J. Res. Dev. 34(1), 1990).  That q equals the IEEE quotient for every f32
+// significand over every f16 significand is checked exhaustively by the test suite; the operations scale exactly
+// with the exponents, and where they would not (a residual below the normal range) |x / sf| < 2^-78 codes 0 both
+// ways.  sf = +inf gives y = 0 and a NaN q, which codes 0 as x / inf does.  A NaN quotient (x NaN, or x infinite
+// over an infinite scale) codes 0, as a NaN converts to integer 0.  Written as selects: every lane forms its
+// quotient and discards it where the code is 0.
+__device__ __forceinline__ uint32_t q8_code(float x, float sf, float y) {
+#pragma clang fp contract(off)
+    const float q0 = x * y;
+    const float q = __builtin_fmaf(__builtin_fmaf(-q0, sf, x), y, q0);
+    const float r = __builtin_rintf(q);
+    const float c = __builtin_fminf(__builtin_fmaxf(r, -127.0f), 127.0f);
+    const bool coded = sf > 0.0f && r == r;
+    return coded ? uint32_t(int(c)) & 0xFFu : 0u;
 }
 
 constexpr int kQuantUnitsPerWave = kQuantUnitsPerTile / (kThreads / 64);
+
+// Cross-lane moves inside a 16-lane DPP row (VALU operations, no LDS round trip).  A row of 16 lanes holds one
+// int8 group of 64 values; half a row holds one q4_0 block of 32.
+constexpr int kDppXor1 = 0xB1;         // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;         // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141;  // lane i <-> 7 - i within each half row (pairs the two quads of a half)
+constexpr int kDppMirror = 0x140;      // lane i <-> 15 - i within the row (pairs the two halves)
+constexpr int kDppRowShl4 = 0x104;     // lane i reads lane i + 4 of its row (lanes 12..15 keep their own value)
+template <int kCtrl>
+__device__ __forceinline__ uint32_t dpp(uint32_t v) {
+    return uint32_t(__builtin_amdgcn_update_dpp(int(v), int(v), kCtrl, 0xF, 0xF, false));
+}
+template <int kCtrl>
+__device__ __forceinline__ float dpp(float v) {
+    return __uint_as_float(dpp<kCtrl>(__float_as_uint(v)));
+}
 
 // The wave's rows of a tile, all loads issued before any row is quantized (four 1 KiB reads in flight per wave).
 __device__ __forceinline__ int load_units(const MoveRow& r, uint64_t local, int lane, int wave,
@@ -273,16 +267,20 @@ __device__ void tile_q8(const MoveRow& r, const MoveGeo& g, uint64_t local) {
         const u32x4 v = vs[i];
         const float x0 = __uint_as_float(v.x), x1 = __uint_as_float(v.y), x2 = __uint_as_float(v.z),
                     x3 = __uint_as_float(v.w);
-        // max |x| over the 64 values of this lane's group: 16 lanes (fmax is exact, so any order gives the same)
-        float a = fmaxf(fmaxf(fabsf(x0), fabsf(x1)), fmaxf(fabsf(x2), fabsf(x3)));
-        a = fmaxf(a, __shfl_xor(a, 8));
-        a = fmaxf(a, __shfl_xor(a, 4));
-        a = fmaxf(a, __shfl_xor(a, 2));
-        a = fmaxf(a, __shfl_xor(a, 1));
+        // max |x| over the 64 values of this lane's group, the 16 lanes of its DPP row (fmax is exact, so any
+        // order gives the same).  It starts from 0, so NaNs never count and a group of NaNs has scale 0.
+        float a = fmaxf(fmaxf(fmaxf(fabsf(x0), fabsf(x1)), fmaxf(fabsf(x2), fabsf(x3))), 0.0f);
+        a = fmaxf(a, dpp<kDppXor1>(a));
+        a = fmaxf(a, dpp<kDppXor2>(a));
+        a = fmaxf(a, dpp<kDppHalfMirror>(a));
+        a = fmaxf(a, dpp<kDppMirror>(a));
         const uint32_t sb = f16_bits_rne(__float_as_uint(a / 127.0f));
         const float sf = f32_of_f16(sb);
-        const uint32_t codes = q8_code(x0, sf) | (q8_code(x1, sf) << 8) | (q8_code(x2, sf) << 16) | (q8_code(x3, sf) << 24);
-        const uint32_t s1 = __shfl(sb, 16), s2 = __shfl(sb, 32), s3 = __shfl(sb, 48);
+        const float y = 1.0f / sf;
+        const uint32_t codes = q8_code(x0, sf, y) | (q8_code(x1, sf, y) << 8) | (q8_code(x2, sf, y) << 16) |
+                               (q8_code(x3, sf, y) << 24);
+        const uint32_t s1 = __builtin_amdgcn_readlane(sb, 16), s2 = __builtin_amdgcn_readlane(sb, 32),
+                       s3 = __builtin_amdgcn_readlane(sb, 48);
         const int64_t prow = pool_row(r, g, unit);
         if (prow < 0) continue;
         using g32 = __attribute__((address_space(1))) uint32_t;
@@ -296,9 +294,13 @@ __device__ void tile_q8(const MoveRow& r, const MoveGeo& g, uint64_t local) {
 }
 
 // The q4_0 block maximum: larger |x|, then larger value, then lower index (so the sign of a zero maximum is the
-// first zero's).
+// first zero's).  A NaN never compares larger, so it is never picked; the start (amax -1, value +0) stands for a
+// block of NaNs.  The pick is the maximum of a total order, so any pairing of candidates gives the same result.
 __device__ __forceinline__ void q4_pick(float& amax, float& mval, uint32_t& idx, float a, float v, uint32_t j) {
-    if (a > amax || (a == amax && (v > mval || (v == mval && j < idx)))) { amax = a; mval = v; idx = j; }
+    const bool take = a > amax || (a == amax && (v > mval || (v == mval && j < idx)));
+    amax = take ? a : amax;
+    mval = take ? v : mval;
+    idx = take ? j : idx;
 }
 
 __device__ __forceinline__ uint32_t q4_code(float x, float id) {
@@ -322,19 +324,20 @@ __device__ void tile_q4(const MoveRow& r, const MoveGeo& g, uint64_t local) {
         const uint32_t unit = units[i];
         const u32x4 v = vs[i];
         const float x[4] = {__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w)};
-        float amax = fabsf(x[0]), mval = x[0];
-        uint32_t idx = uint32_t(lb * 4);
-        for (int k = 1; k < 4; ++k) q4_pick(amax, mval, idx, fabsf(x[k]), x[k], uint32_t(lb * 4 + k));
-        for (int o = 4; o > 0; o >>= 1) {
-            const float a2 = __shfl_xor(amax, o), v2 = __shfl_xor(mval, o);
-            const uint32_t j2 = __shfl_xor(idx, o);
-            q4_pick(amax, mval, idx, a2, v2, j2);
-        }
+        float amax = -1.0f, mval = 0.0f;
+        uint32_t idx = 32u;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) q4_pick(amax, mval, idx, fabsf(x[k]), x[k], uint32_t(lb * 4 + k));
+        // the pick is a maximum under a total order, so pairing within quads, then the two quads of the block,
+        // reaches every lane's candidate
+        q4_pick(amax, mval, idx, dpp<kDppXor1>(amax), dpp<kDppXor1>(mval), dpp<kDppXor1>(idx));
+        q4_pick(amax, mval, idx, dpp<kDppXor2>(amax), dpp<kDppXor2>(mval), dpp<kDppXor2>(idx));
+        q4_pick(amax, mval, idx, dpp<kDppHalfMirror>(amax), dpp<kDppHalfMirror>(mval), dpp<kDppHalfMirror>(idx));
         const float d = mval / -8.0f;
         const float id = d != 0.0f ? 1.0f / d : 0.0f;
         const uint32_t q = q4_code(x[0], id) | (q4_code(x[1], id) << 8) | (q4_code(x[2], id) << 16) |
                            (q4_code(x[3], id) << 24);
-        const uint32_t hi = __shfl_down(q, 4);   // lane lb + 4 holds the block's values 16 + 4 lb .. 19 + 4 lb
+        const uint32_t hi = dpp<kDppRowShl4>(q);   // lane lb + 4 holds the block's values 16 + 4 lb .. 19 + 4 lb
         const int64_t prow = pool_row(r, g, unit);
         if (prow < 0) continue;
         // block `blk` of the row: {f16 d, qs[16]}, 18 bytes at 18 * blk; qs[4 lb .. 4 lb + 3] from lanes lb, lb + 4
@@ -352,7 +355,9 @@ __device__ void tile_q4(const MoveRow& r, const MoveGeo& g, uint64_t local) {
 // One workgroup per tile (the grid strides only when a plan has more tiles than one launch may hold): measured
 // on the 128K handoff, a grid of one tile per workgroup beat every persistent grid from 1024 to 65536 workgroups.
 // `tile_row[t]` names the handoff table row of tile t, so a workgroup finds its row with two scalar loads and no
-// search.
+// search.  Plans with quantizing rows launch the kQuant instance: the quantizers need 80 VGPRs, and compiled into
+// the one instance they would take the plain movers from 7 to 6 waves per SIMD.
+template <bool kQuant>
 __global__ void __launch_bounds__(kThreads) sc_move_kernel(const MoveRow* __restrict__ rows,
                                                             const uint16_t* __restrict__ tile_row, MoveGeo geo,
                                                             uint64_t n_tiles) {
@@ -372,8 +377,8 @@ __global__ void __launch_bounds__(kThreads) sc_move_kernel(const MoveRow* __rest
             case kPagesGather: tile_pages(r, geo, local, false); break;
             case kCopy: tile_copy(r, local, false); break;
             case kZero: tile_copy(r, local, true); break;
-            case kKvQ8: tile_q8(r, geo, local); break;
-            case kKvQ4: tile_q4(r, geo, local); break;
+            case kKvQ8: if constexpr (kQuant) tile_q8(r, geo, local); break;
+            case kKvQ4: if constexpr (kQuant) tile_q4(r, geo, local); break;
             default: break;
         }
     }
@@ -649,11 +654,16 @@ hipError_t launch_ring_table(int32_t* table, int64_t n_blocks, int64_t n_slots, 
 }
 
 hipError_t launch_move(const MoveRow* rows, const uint16_t* tile_row, const MoveGeo& geo, uint64_t n_tiles,
-                       int64_t grid, hipStream_t stream) {
+                       int64_t grid, bool quant, hipStream_t stream) {
     if (n_tiles == 0) return hipSuccess;
     if (!rows || !tile_row || grid <= 0) return hipErrorInvalidValue;
     const uint64_t g = uint64_t(grid) < n_tiles ? uint64_t(grid) : n_tiles;
-    hipLaunchKernelGGL(sc_move_kernel, dim3(unsigned(g)), dim3(kThreads), 0, stream, rows, tile_row, geo, n_tiles);
+    if (quant)
+        hipLaunchKernelGGL(sc_move_kernel<true>, dim3(unsigned(g)), dim3(kThreads), 0, stream, rows, tile_row, geo,
+                           n_tiles);
+    else
+        hipLaunchKernelGGL(sc_move_kernel<false>, dim3(unsigned(g)), dim3(kThreads), 0, stream, rows, tile_row, geo,
+                           n_tiles);
     return hipGetLastError();
 }
 

@@ -3,7 +3,8 @@
 The oracle's rules (sco_q8_row, sco_q4_row) are pinned in tests/test_oracle_quant.py by independent numpy forms of the
 reference's int8 kv_append and kv_append_q4 quantizers.  Here every code byte, every scale and every untouched byte of
 the device pools must equal the oracle's, for every table shape the f16 carve is tested with, a start in the middle of
-a page, and rows built to hit the edge cases (zero groups, tied magnitudes, exact .5 quotients, tiny and huge scales).
+a page, and rows built to hit the edge cases (zero groups, tied magnitudes, exact .5 quotients, tiny and huge scales,
+NaN and infinite values, signed zeros).
 """
 import numpy as np
 import pytest
@@ -29,6 +30,13 @@ def _edge_rows(src: np.ndarray) -> np.ndarray:
         x[2, 1] = x[2, 1] * np.float32(5e3)
     if T > 3:
         x[3, 0, :64] = np.float32(127) * np.arange(64, dtype=np.float32) / np.float32(64) + np.float32(0.5)
+    if T > 6:
+        x[4, 0, :64] = np.nan                       # a group / blocks of NaNs
+        x[4, 1, 0], x[4, 1, 37] = np.nan, np.nan    # NaN first in a group, NaN inside a block
+        x[5, 0, 2], x[5, 0, 9] = np.inf, -np.inf    # infinite scale; inf / inf
+        x[5, 1, :32] = -np.float32(0)
+        x[5, 1, 3] = np.float32(0)                  # -0 first among zeros
+        x[6, 0, 1] = np.float32(1e7)                # max / 127 beyond f16: infinite scale
     return x
 
 

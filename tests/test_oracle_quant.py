@@ -17,28 +17,37 @@ F32 = np.float32
 
 def q8_numpy(x):
     g = x.reshape(-1, 64).astype(F32)
-    amax = np.max(np.abs(g), axis=1)
-    scale = (amax / F32(127)).astype(np.float16)
+    a = np.abs(g)
+    amax = np.max(np.where(np.isnan(a), F32(0), a), axis=1)      # fmaxf from 0: NaNs do not count
+    with np.errstate(over="ignore"):
+        scale = (amax / F32(127)).astype(np.float16)
     sf = scale.astype(F32)[:, None]
     with np.errstate(divide="ignore", invalid="ignore"):
         q = np.rint(g / np.where(sf > 0, sf, F32(1)))
-    q = np.where((sf > 0) & ~np.isnan(g), np.clip(q, -127, 127), 0).astype(np.int8)
+    ok = (sf > 0) & ~np.isnan(g) & ~np.isnan(q)                   # a NaN quotient (inf / inf) codes 0
+    q = np.where(ok, np.clip(np.where(ok, q, 0), -127, 127), 0).astype(np.int8)
     return q.reshape(x.shape), scale.view(np.uint16).reshape(x.shape[:-1] + (x.shape[-1] // 64,))
 
 
 def q4_numpy(x):
     g = x.reshape(-1, 32).astype(F32)
     a = np.abs(g)
+    a = np.where(np.isnan(a), F32(-1), a)                         # a NaN is never the maximum
     amax = a.max(axis=1, keepdims=True)
-    mval = np.where(a == amax, g, -np.inf).max(axis=1)
+    with np.errstate(invalid="ignore"):
+        mval = np.where(a == amax, g, -np.inf).max(axis=1)
+    first = g[np.arange(g.shape[0]), np.argmax(a == amax, axis=1)]
+    mval = np.where(mval == 0, first, mval)                       # +0 and -0 tie: the first in index order
+    mval = np.where(amax[:, 0] < 0, F32(0), mval).astype(F32)     # a block of NaNs: +0
     d = (mval / F32(-8)).astype(F32)
-    with np.errstate(divide="ignore"):
+    with np.errstate(divide="ignore", invalid="ignore", over="ignore"):
         idv = np.where(d != 0, F32(1) / np.where(d != 0, d, F32(1)), F32(0)).astype(F32)
-    prod = (g * idv[:, None]).astype(F32)
-    s = (prod + F32(8.5)).astype(F32)
-    q = np.clip(np.trunc(s), 0, 15).astype(np.uint8)
+        prod = (g * idv[:, None]).astype(F32)
+        s = (prod + F32(8.5)).astype(F32)
+    q = np.where(np.isnan(s), 0, np.clip(np.trunc(np.where(np.isnan(s), 0, s)), 0, 15)).astype(np.uint8)
     packed = (q[:, :16] | (q[:, 16:] << 4)).astype(np.uint8)
-    dh = d.astype(np.float16).view(np.uint16)
+    with np.errstate(over="ignore"):
+        dh = d.astype(np.float16).view(np.uint16)
     out = np.zeros((g.shape[0], 18), np.uint8)
     out[:, 0] = dh & 0xFF
     out[:, 1] = dh >> 8
@@ -57,6 +66,14 @@ def _groups(rng, n, D):
     x[3] = rng.standard_normal(D).astype(F32) * F32(1e-3)   # tiny values: f16 scales near the subnormal range
     x[4] = rng.standard_normal(D).astype(F32) * F32(2e4)    # large values: scales near the f16 top
     x[5, :n64] = F32(127) * np.arange(n64, dtype=F32) / F32(64) + F32(0.5)   # quotients near .5
+    x[6, 0] = np.nan                               # NaN first in its group: never the maximum, codes 0
+    x[7, 5] = np.nan
+    x[7, 9] = F32(50)                              # ... and NaN before the group's maximum
+    x[8, :n64] = np.nan                            # a group of NaNs: scale 0 / d -0, codes 0 / 0
+    x[9, 2], x[9, 7] = F32(np.inf), -F32(np.inf)   # infinities: an infinite scale; inf / inf codes 0
+    x[10, :32] = -F32(0)
+    x[10, 3] = F32(0)                              # -0 first among zeros: d = -0 / -8 = +0
+    x[11, 1] = F32(1e7)                            # max / 127 beyond the f16 range: an infinite scale
     return x
 
 
@@ -113,6 +130,23 @@ def test_q4_hand_computed(oracle):
     tb = oracle.q4_rows(t[None])[0]
     d = F32(3) / F32(-8)
     assert int(tb[0]) | (int(tb[1]) << 8) == int(np.array([d], F32).astype(np.float16).view(np.uint16)[0])
+
+
+def test_nan_and_infinity_hand_computed(oracle):
+    nan8 = np.full(64, np.nan, F32)
+    codes, scales = oracle.q8_rows(nan8[None])
+    assert scales[0, 0] == 0 and not codes.any()                  # NaNs do not count toward the maximum
+    y = np.zeros(64, F32)
+    y[0], y[1], y[2] = F32(np.inf), F32(1), F32(-np.inf)
+    codes, scales = oracle.q8_rows(y[None])
+    assert scales[0, 0] == 0x7C00 and not codes.any()             # scale inf: x / inf is 0, inf / inf codes 0
+    blk = oracle.q4_rows(np.full(32, np.nan, F32)[None])[0]
+    assert blk[0] == 0 and blk[1] == 0x80 and not blk[2:].any()   # d = +0 / -8 = -0; NaN codes 0
+    z = np.zeros(32, F32)
+    z[0], z[1], z[2] = np.nan, F32(-4), F32(2)                    # the NaN is passed over: d = -4 / -8 = 0.5
+    blk = oracle.q4_rows(z[None])[0]
+    assert int(blk[0]) | (int(blk[1]) << 8) == 0x3800
+    assert blk[2] == 0 | (8 << 4) and blk[3] == 0 | (8 << 4) and blk[4] == 12 | (8 << 4)
 
 
 @pytest.mark.parametrize("fmt", [1, 2])
