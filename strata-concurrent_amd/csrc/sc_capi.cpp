@@ -21,7 +21,7 @@
 
 namespace sc {
 hipError_t launch_move(const MoveRow* rows, const uint16_t* tile_row, const MoveGeo& geo, uint64_t n_tiles,
-                       int64_t grid, bool quant, hipStream_t stream);
+                       int64_t grid, int32_t mix, hipStream_t stream);
 hipError_t launch_fill_uniform_f16(uint16_t* dst, uint64_t n, float lo, float hi, uint64_t seed, uint64_t sid,
                                    hipStream_t stream);
 hipError_t launch_fill_uniform_f32(float* dst, uint64_t n, float lo, float hi, uint64_t seed, uint64_t sid,
@@ -57,7 +57,7 @@ struct sc_plan {
     uint64_t n_tiles = 0;
     uint64_t payload = 0;
     int64_t grid = 0;
-    bool quant = false;                 // has quantizing rows (launches the quantizing kernel instance)
+    int32_t mix = sc::kMixPlain;        // the kernel instance that holds every row kind of the plan
 };
 
 namespace {
@@ -174,7 +174,7 @@ constexpr uint64_t kMaxGrid = 65536;
 int finish_plan(std::vector<sc::MoveRow>& rows, const Geo& g, uint64_t payload, sc_plan** out) {
     if (rows.size() > 65535) return fail(SC_ERANGE, "sc_handoff: more than 65535 handoff table rows in one plan");
     uint64_t tiles = 0;
-    bool quant = false;
+    bool quant = false, kv32 = false;
     for (auto& r : rows) {
         if (r.n >= kMaxRowChunks) return fail(SC_ERANGE, "sc_handoff: a handoff table row beyond 2^31 chunks");
         r.tile0 = tiles;
@@ -183,6 +183,7 @@ int finish_plan(std::vector<sc::MoveRow>& rows, const Geo& g, uint64_t payload, 
                                                                               : sc::kTileChunks;
         tiles += (r.n + per_tile - 1) / per_tile;
         quant = quant || r.kind == sc::kKvQ8 || r.kind == sc::kKvQ4;
+        kv32 = kv32 || r.kind == sc::kKv32;
     }
     // rows that move nothing still own an (empty) tile range; the kernel never visits them
     sc_plan* p = new (std::nothrow) sc_plan();
@@ -192,7 +193,7 @@ int finish_plan(std::vector<sc::MoveRow>& rows, const Geo& g, uint64_t payload, 
     p->n_tiles = tiles;
     p->payload = payload;
     p->grid = int64_t(std::min<uint64_t>(tiles, kMaxGrid));
-    p->quant = quant;
+    p->mix = sc::mix_of(kv32, quant);
     if (rows.empty() || tiles == 0) {   // an empty handoff (0 tokens, no running state) is a valid no-op
         *out = p;
         return ok();
@@ -646,7 +647,7 @@ int sc_plan_launch(const sc_plan* plan, void* stream) {
         return e == hipSuccess ? ok() : hip_fail(e, "batch launch");
     }
     const hipError_t e = sc::launch_move(plan->rows_dev, plan->tile_row_dev, plan->geo, plan->n_tiles, plan->grid,
-                                         plan->quant, static_cast<hipStream_t>(stream));
+                                         plan->mix, static_cast<hipStream_t>(stream));
     return e == hipSuccess ? ok() : hip_fail(e, "move launch");
 }
 

@@ -31,6 +31,19 @@ enum MoveKind : int32_t {
     kKvQ4 = 10,         // f32 rows [T][H][256] (already rotated) -> q4_0 blocks [prow][8 x 18 B]
 };
 
+// The kernel instances: each compiles the tiles of a set of row kinds, so a plan of plain moves is not held to the
+// register budget of the f32 rounding or the quantizing tiles.  A plan launches the smallest instance whose set
+// holds every kind it has (mix_of).
+enum MoveMix : int32_t {
+    kMixPlain = 0,   // kKv16, kRec, kConv, kPages*, kCopy, kZero
+    kMixWide = 1,    // plain + kKv32
+    kMixQuant = 2,   // plain + kKvQ8, kKvQ4
+    kMixAll = 3,     // every kind
+};
+constexpr int32_t mix_of(bool has_kv32, bool has_quant) {
+    return has_quant ? (has_kv32 ? kMixAll : kMixQuant) : (has_kv32 ? kMixWide : kMixPlain);
+}
+
 // Quantizing rows move one (token, head) row of 256 values per wave at a time: a tile is 16 rows (16 KiB of f32).
 constexpr int kQuantUnitsPerTile = 16;
 constexpr int kQuantDim = 256;

@@ -38,59 +38,92 @@ using gu32x4 = __attribute__((address_space(1))) u32x4;
 __device__ __forceinline__ u32x4 ld16(const uint8_t* p) { return *(const gu32x4*) (p); }
 __device__ __forceinline__ void st16(uint8_t* p, u32x4 v) { __builtin_nontemporal_store(v, (gu32x4*) (p)); }
 
-// Pool byte offset of (cell, head) for a K/V row; -1 when the page is not resident or out of the pool.
-__device__ __forceinline__ int64_t pool_row(const MoveRow& r, const MoveGeo& g, uint32_t src_row) {
-    const uint32_t t = fdiv(src_row, g.heads);
-    const uint32_t h = src_row - t * g.heads.d;
-    const int64_t cell = r.pos0 + int64_t(t);
-    const uint32_t page = fdiv(uint32_t(cell), g.page_size);
-    const uint32_t in_page = uint32_t(cell) - page * g.page_size.d;
-    int64_t phys = r.table ? int64_t(r.table[page]) : int64_t(page);
-    if (phys < 0 || phys >= r.ld) return -1;
-    return (phys * g.heads.d + h) * g.page_size.d + in_page;
+// Page tables are read through global loads.  Every tile issues all of its loads, table entries included, before
+// its first store: a table load placed after a store (which might alias the table) waits for it, and the
+// per-chunk load -> store chains that result measured 10-14% slower on the 128K handoff through a page table.
+using gi32 = __attribute__((address_space(1))) const int32_t;
+__device__ __forceinline__ int32_t table_entry(const MoveRow& r, uint32_t page) {
+    return r.table ? *(gi32*) (r.table + page) : int32_t(page);
 }
 
+// The (cell, head) address of K/V source row `src_row` (token-major [T][H]): the logical page, and the row's
+// place inside a physical page.
+struct KvCell {
+    uint32_t page, h, in_page;
+};
+__device__ __forceinline__ KvCell kv_cell(const MoveRow& r, const MoveGeo& g, uint32_t src_row) {
+    const uint32_t t = fdiv(src_row, g.heads);
+    const uint32_t cell = uint32_t(r.pos0 + int64_t(t));
+    const uint32_t page = fdiv(cell, g.page_size);
+    return {page, src_row - t * g.heads.d, cell - page * g.page_size.d};
+}
+// Pool row of a K/V row in physical page `phys`; -1 when the page is not resident or out of the pool.
+__device__ __forceinline__ int64_t pool_row(const MoveRow& r, const MoveGeo& g, int32_t phys, const KvCell& c) {
+    if (phys < 0 || int64_t(phys) >= r.ld) return -1;
+    return (int64_t(phys) * g.heads.d + c.h) * g.page_size.d + c.in_page;
+}
+
+// kTable: the row has a page table, whose entries are loaded with the data; without one the physical page is the
+// logical page and nothing but the data is loaded before the stores.
+template <bool kTable>
 __device__ void tile_kv16(const MoveRow& r, const MoveGeo& g, uint64_t local) {
     const uint32_t row_bytes = g.row_chunks.d * 16u;
     u32x4 v[kChunksPerThread];
     uint32_t q[kChunksPerThread];
+    int32_t phys[kChunksPerThread];
 #pragma unroll
     for (int j = 0; j < kChunksPerThread; ++j) {
         q[j] = uint32_t(local * kTileChunks) + uint32_t(j * kThreads) + threadIdx.x;
         if (q[j] >= r.n) continue;
         // rows past the source's tokens (an image's stale-cell tail) are written as zeros
-        const uint32_t t = fdiv(fdiv(q[j], g.row_chunks), g.heads);
+        const uint32_t row = fdiv(q[j], g.row_chunks);
+        const uint32_t t = fdiv(row, g.heads);
         v[j] = t < uint32_t(r.aux) ? ld16(r.src + uint64_t(q[j]) * 16u) : u32x4{0u, 0u, 0u, 0u};
+        if constexpr (kTable) phys[j] = table_entry(r, kv_cell(r, g, row).page);
     }
 #pragma unroll
     for (int j = 0; j < kChunksPerThread; ++j) {
         if (q[j] >= r.n) continue;
         const uint32_t row = fdiv(q[j], g.row_chunks);
         const uint32_t ch = q[j] - row * g.row_chunks.d;
-        const int64_t prow = pool_row(r, g, row);
+        const KvCell c = kv_cell(r, g, row);
+        const int64_t prow = pool_row(r, g, kTable ? phys[j] : int32_t(c.page), c);
         if (prow >= 0) st16(r.dst + uint64_t(prow) * row_bytes + ch * 16u, v[j]);
     }
 }
 
+// The same map from f32 rows, rounded to f16: destination chunk q holds 8 halves = 32 source bytes at q * 32.
+template <bool kTable>
 __device__ void tile_kv32(const MoveRow& r, const MoveGeo& g, uint64_t local) {
     const uint32_t row_bytes = g.row_chunks.d * 16u;
+    u32x4 a[kChunksPerThread], b[kChunksPerThread];
+    uint32_t q[kChunksPerThread];
+    int32_t phys[kChunksPerThread];
 #pragma unroll
     for (int j = 0; j < kChunksPerThread; ++j) {
-        const uint32_t q = uint32_t(local * kTileChunks) + uint32_t(j * kThreads) + threadIdx.x;
-        if (q >= r.n) continue;
-        const uint32_t row = fdiv(q, g.row_chunks);
-        u32x4 o = {0u, 0u, 0u, 0u};
+        q[j] = uint32_t(local * kTileChunks) + uint32_t(j * kThreads) + threadIdx.x;
+        if (q[j] >= r.n) continue;
+        const uint32_t row = fdiv(q[j], g.row_chunks);
         if (fdiv(row, g.heads) < uint32_t(r.aux)) {
-            // destination chunk q holds 8 halves = 32 source bytes at q * 32
-            const u32x4 a = ld16(r.src + uint64_t(q) * 32u);
-            const u32x4 b = ld16(r.src + uint64_t(q) * 32u + 16u);
-            o.x = f16_bits_rne(a.x) | (f16_bits_rne(a.y) << 16);
-            o.y = f16_bits_rne(a.z) | (f16_bits_rne(a.w) << 16);
-            o.z = f16_bits_rne(b.x) | (f16_bits_rne(b.y) << 16);
-            o.w = f16_bits_rne(b.z) | (f16_bits_rne(b.w) << 16);
+            a[j] = ld16(r.src + uint64_t(q[j]) * 32u);
+            b[j] = ld16(r.src + uint64_t(q[j]) * 32u + 16u);
+        } else {
+            a[j] = b[j] = u32x4{0u, 0u, 0u, 0u};
         }
-        const uint32_t ch = q - row * g.row_chunks.d;
-        const int64_t prow = pool_row(r, g, row);
+        if constexpr (kTable) phys[j] = table_entry(r, kv_cell(r, g, row).page);
+    }
+#pragma unroll
+    for (int j = 0; j < kChunksPerThread; ++j) {
+        if (q[j] >= r.n) continue;
+        u32x4 o;
+        o.x = f16_bits_rne(a[j].x) | (f16_bits_rne(a[j].y) << 16);
+        o.y = f16_bits_rne(a[j].z) | (f16_bits_rne(a[j].w) << 16);
+        o.z = f16_bits_rne(b[j].x) | (f16_bits_rne(b[j].y) << 16);
+        o.w = f16_bits_rne(b[j].z) | (f16_bits_rne(b[j].w) << 16);
+        const uint32_t row = fdiv(q[j], g.row_chunks);
+        const uint32_t ch = q[j] - row * g.row_chunks.d;
+        const KvCell c = kv_cell(r, g, row);
+        const int64_t prow = pool_row(r, g, kTable ? phys[j] : int32_t(c.page), c);
         if (prow >= 0) st16(r.dst + uint64_t(prow) * row_bytes + ch * 16u, o);
     }
 }
@@ -124,18 +157,21 @@ __device__ void tile_pages(const MoveRow& r, const MoveGeo& g, uint64_t local, b
     int64_t dst_off[kChunksPerThread];
     if (scatter) {
         uint32_t q[kChunksPerThread];
+        int32_t phys[kChunksPerThread];
 #pragma unroll
         for (int j = 0; j < kChunksPerThread; ++j) {
             q[j] = uint32_t(local * kTileChunks) + uint32_t(j * kThreads) + threadIdx.x;
             if (q[j] < r.n) v[j] = ld16(r.src + uint64_t(q[j]) * 16u);
         }
 #pragma unroll
+        for (int j = 0; j < kChunksPerThread; ++j)
+            if (q[j] < r.n) phys[j] = table_entry(r, fdiv(q[j], g.page_chunks));
+#pragma unroll
         for (int j = 0; j < kChunksPerThread; ++j) {
             if (q[j] >= r.n) continue;
             const uint32_t page = fdiv(q[j], g.page_chunks);
             const uint32_t ch = q[j] - page * g.page_chunks.d;
-            const int64_t phys = r.table ? int64_t(r.table[page]) : int64_t(page);
-            if (phys >= 0 && phys < r.ld) st16(r.dst + uint64_t(phys) * page_bytes + ch * 16u, v[j]);
+            if (phys[j] >= 0 && int64_t(phys[j]) < r.ld) st16(r.dst + uint64_t(phys[j]) * page_bytes + ch * 16u, v[j]);
         }
         return;
     }
@@ -146,7 +182,7 @@ __device__ void tile_pages(const MoveRow& r, const MoveGeo& g, uint64_t local, b
         if (q >= r.n) continue;
         const uint32_t page = fdiv(q, g.page_chunks);
         const uint32_t ch = q - page * g.page_chunks.d;
-        const int64_t phys = r.table ? int64_t(r.table[page]) : int64_t(page);
+        const int64_t phys = table_entry(r, page);
         if (phys < 0 || phys >= r.ld) continue;
         v[j] = ld16(r.src + uint64_t(phys) * page_bytes + ch * 16u);
         dst_off[j] = int64_t(q) * 16;
@@ -240,9 +276,11 @@ __device__ __forceinline__ float dpp(float v) {
     return __uint_as_float(dpp<kCtrl>(__float_as_uint(v)));
 }
 
-// The wave's rows of a tile, all loads issued before any row is quantized (four 1 KiB reads in flight per wave).
-__device__ __forceinline__ int load_units(const MoveRow& r, uint64_t local, int lane, int wave,
-                                          u32x4 (&v)[kQuantUnitsPerWave], uint32_t (&unit)[kQuantUnitsPerWave]) {
+// The wave's rows of a tile, all loads (rows and their pages' table entries) issued before any row is quantized:
+// four 1 KiB reads in flight per wave.
+__device__ __forceinline__ int load_units(const MoveRow& r, const MoveGeo& g, uint64_t local, int lane, int wave,
+                                          u32x4 (&v)[kQuantUnitsPerWave], uint32_t (&unit)[kQuantUnitsPerWave],
+                                          int32_t (&phys)[kQuantUnitsPerWave]) {
     int n = 0;
 #pragma unroll
     for (int i = 0; i < kQuantUnitsPerWave; ++i) {
@@ -252,6 +290,9 @@ __device__ __forceinline__ int load_units(const MoveRow& r, uint64_t local, int 
             n = i + 1;
         }
     }
+#pragma unroll
+    for (int i = 0; i < kQuantUnitsPerWave; ++i)
+        if (i < n) phys[i] = table_entry(r, kv_cell(r, g, unit[i]).page);
     return n;
 }
 
@@ -259,7 +300,8 @@ __device__ void tile_q8(const MoveRow& r, const MoveGeo& g, uint64_t local) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     u32x4 vs[kQuantUnitsPerWave];
     uint32_t units[kQuantUnitsPerWave];
-    const int n_units = load_units(r, local, lane, wave, vs, units);
+    int32_t phys[kQuantUnitsPerWave];
+    const int n_units = load_units(r, g, local, lane, wave, vs, units, phys);
 #pragma unroll
     for (int i = 0; i < kQuantUnitsPerWave; ++i) {
         if (i >= n_units) break;
@@ -281,7 +323,7 @@ __device__ void tile_q8(const MoveRow& r, const MoveGeo& g, uint64_t local) {
                                (q8_code(x3, sf, y) << 24);
         const uint32_t s1 = __builtin_amdgcn_readlane(sb, 16), s2 = __builtin_amdgcn_readlane(sb, 32),
                        s3 = __builtin_amdgcn_readlane(sb, 48);
-        const int64_t prow = pool_row(r, g, unit);
+        const int64_t prow = pool_row(r, g, phys[i], kv_cell(r, g, unit));
         if (prow < 0) continue;
         using g32 = __attribute__((address_space(1))) uint32_t;
         using g64 = __attribute__((address_space(1))) uint64_t;
@@ -317,7 +359,8 @@ __device__ void tile_q4(const MoveRow& r, const MoveGeo& g, uint64_t local) {
     const uint32_t blk = uint32_t(lane >> 3);
     u32x4 vs[kQuantUnitsPerWave];
     uint32_t units[kQuantUnitsPerWave];
-    const int n_units = load_units(r, local, lane, wave, vs, units);
+    int32_t phys[kQuantUnitsPerWave];
+    const int n_units = load_units(r, g, local, lane, wave, vs, units, phys);
 #pragma unroll
     for (int i = 0; i < kQuantUnitsPerWave; ++i) {
         if (i >= n_units) break;
@@ -338,7 +381,7 @@ __device__ void tile_q4(const MoveRow& r, const MoveGeo& g, uint64_t local) {
         const uint32_t q = q4_code(x[0], id) | (q4_code(x[1], id) << 8) | (q4_code(x[2], id) << 16) |
                            (q4_code(x[3], id) << 24);
         const uint32_t hi = dpp<kDppRowShl4>(q);   // lane lb + 4 holds the block's values 16 + 4 lb .. 19 + 4 lb
-        const int64_t prow = pool_row(r, g, unit);
+        const int64_t prow = pool_row(r, g, phys[i], kv_cell(r, g, unit));
         if (prow < 0) continue;
         // block `blk` of the row: {f16 d, qs[16]}, 18 bytes at 18 * blk; qs[4 lb .. 4 lb + 3] from lanes lb, lb + 4
         uint8_t* row = r.dst + uint64_t(prow) * (kQuantDim / 32 * 18) + blk * 18;
@@ -355,9 +398,10 @@ __device__ void tile_q4(const MoveRow& r, const MoveGeo& g, uint64_t local) {
 // One workgroup per tile (the grid strides only when a plan has more tiles than one launch may hold): measured
 // on the 128K handoff, a grid of one tile per workgroup beat every persistent grid from 1024 to 65536 workgroups.
 // `tile_row[t]` names the handoff table row of tile t, so a workgroup finds its row with two scalar loads and no
-// search.  Plans with quantizing rows launch the kQuant instance: the quantizers need 80 VGPRs, and compiled into
-// the one instance they would take the plain movers from 7 to 6 waves per SIMD.
-template <bool kQuant>
+// search.  The instance (kMix) compiles only its set of row kinds: the f32 rounding tile holds twice the loads
+// and the quantizers need 80-90 VGPRs, and compiled into one kernel they took the plain movers from 8 to 6 waves
+// per SIMD.
+template <int kMix>
 __global__ void __launch_bounds__(kThreads) sc_move_kernel(const MoveRow* __restrict__ rows,
                                                             const uint16_t* __restrict__ tile_row, MoveGeo geo,
                                                             uint64_t n_tiles) {
@@ -369,16 +413,24 @@ __global__ void __launch_bounds__(kThreads) sc_move_kernel(const MoveRow* __rest
         if (k != cur) { cur = k; r = rows[k]; }
         const uint64_t local = tile - r.tile0;
         switch (r.kind) {
-            case kKv16: tile_kv16(r, geo, local); break;
-            case kKv32: tile_kv32(r, geo, local); break;
+            case kKv16:
+                if (r.table) tile_kv16<true>(r, geo, local);
+                else tile_kv16<false>(r, geo, local);
+                break;
+            case kKv32:
+                if constexpr (kMix == kMixWide || kMix == kMixAll) {
+                    if (r.table) tile_kv32<true>(r, geo, local);
+                    else tile_kv32<false>(r, geo, local);
+                }
+                break;
             case kRec: tile_rec(r, geo, local); break;
             case kConv: tile_conv(r, local, s_conv); break;
             case kPagesScatter: tile_pages(r, geo, local, true); break;
             case kPagesGather: tile_pages(r, geo, local, false); break;
             case kCopy: tile_copy(r, local, false); break;
             case kZero: tile_copy(r, local, true); break;
-            case kKvQ8: if constexpr (kQuant) tile_q8(r, geo, local); break;
-            case kKvQ4: if constexpr (kQuant) tile_q4(r, geo, local); break;
+            case kKvQ8: if constexpr (kMix == kMixQuant || kMix == kMixAll) tile_q8(r, geo, local); break;
+            case kKvQ4: if constexpr (kMix == kMixQuant || kMix == kMixAll) tile_q4(r, geo, local); break;
             default: break;
         }
     }
@@ -532,7 +584,7 @@ __global__ void __launch_bounds__(kThreads) sc_batch_kernel(BatchArgs a) {
                 r.pos0 = L;
                 r.ld = a.arena_pages;
                 r.aux = int32_t(a.chunk_tokens);
-                tile_kv16(r, g, w - t_full - t_part);
+                tile_kv16<true>(r, g, w - t_full - t_part);
             }
         } else {
             MoveRow r{};
@@ -654,16 +706,24 @@ hipError_t launch_ring_table(int32_t* table, int64_t n_blocks, int64_t n_slots, 
 }
 
 hipError_t launch_move(const MoveRow* rows, const uint16_t* tile_row, const MoveGeo& geo, uint64_t n_tiles,
-                       int64_t grid, bool quant, hipStream_t stream) {
+                       int64_t grid, int32_t mix, hipStream_t stream) {
     if (n_tiles == 0) return hipSuccess;
-    if (!rows || !tile_row || grid <= 0) return hipErrorInvalidValue;
-    const uint64_t g = uint64_t(grid) < n_tiles ? uint64_t(grid) : n_tiles;
-    if (quant)
-        hipLaunchKernelGGL(sc_move_kernel<true>, dim3(unsigned(g)), dim3(kThreads), 0, stream, rows, tile_row, geo,
-                           n_tiles);
-    else
-        hipLaunchKernelGGL(sc_move_kernel<false>, dim3(unsigned(g)), dim3(kThreads), 0, stream, rows, tile_row, geo,
-                           n_tiles);
+    if (!rows || !tile_row || grid <= 0 || mix < kMixPlain || mix > kMixAll) return hipErrorInvalidValue;
+    const dim3 blocks(unsigned(uint64_t(grid) < n_tiles ? uint64_t(grid) : n_tiles)), threads(kThreads);
+    switch (mix) {
+        case kMixPlain:
+            hipLaunchKernelGGL(sc_move_kernel<kMixPlain>, blocks, threads, 0, stream, rows, tile_row, geo, n_tiles);
+            break;
+        case kMixWide:
+            hipLaunchKernelGGL(sc_move_kernel<kMixWide>, blocks, threads, 0, stream, rows, tile_row, geo, n_tiles);
+            break;
+        case kMixQuant:
+            hipLaunchKernelGGL(sc_move_kernel<kMixQuant>, blocks, threads, 0, stream, rows, tile_row, geo, n_tiles);
+            break;
+        default:
+            hipLaunchKernelGGL(sc_move_kernel<kMixAll>, blocks, threads, 0, stream, rows, tile_row, geo, n_tiles);
+            break;
+    }
     return hipGetLastError();
 }
 
