@@ -17,12 +17,17 @@
 //      number), h_N = h_0 p^N + sum_n d_n p^(N-n) mod 2^64: independent per-segment Horner sums, folded with powers
 //      of p in any order.
 //
-// The buffer is split into lane segments of kFnvLaneBytes bytes.  Level j (one launch each) runs every segment's
-// (j+1)-bit machine serially from its known start bits with bit j set to 0 - the end value of bit j is then the
-// segment's xor of t_j - and ballots those bits; a single-workgroup scan turns the per-workgroup parities into
-// exclusive prefixes, and the next level derives bit j of each segment's start from them.  The last launch runs the
-// full machine from the now complete start byte, forms each segment's Horner sum, scales it by p^(bytes after the
-// segment) and reduces; a final workgroup adds h_0 p^N.  Every kernel reads each input byte once; ten launches in all.
+// The buffer is split into lane segments of kFnvLaneBytes bytes, and the low byte is resolved two bits per pass over
+// the data.  Pass j (j = 0, 2, 4, 6) runs every segment's machine from its known start bits 0..j-1 twice, with start
+// bit j = 0 and = 1 (bit j+1 = 0 in both): the two machines share one 24-bit multiply, one in byte 0 and one in byte 2
+// of a register.  Bit j at the end, from the first machine, is the segment's xor term for bit j; bit j+1 at the end
+// of the machine whose start bit j is the true one is its xor term for bit j+1 (the term for a bit depends on the
+// lower start bits, and bit j is resolved before bit j+1 is needed).  Per pass: the data pass ballots the bit-j terms
+// and both candidate bit-(j+1) terms; a single-workgroup scan turns per-workgroup parities into exclusive prefixes;
+// a data-free launch resolves each segment's start bit j, picks its bit-(j+1) term and ballots it; a second scan
+// resolves bit j+1.  The last data pass runs the full machine from the now complete start byte, forms each segment's
+// Horner sum, scales it by p^(bytes after the segment) and reduces; a final workgroup adds h_0 p^N.  Five reads of
+// the input in all.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -61,24 +66,72 @@ __device__ __forceinline__ void load_segment(const uint8_t* p, uint32_t (&w)[kFn
     }
 }
 
-// The low-bit machine over a segment from state `l`.  Only the low 8 bits of the result are meaningful: the 24-bit
-// multiply reads the low 24 bits of its operands and its low 8 result bits depend only on their low 8 bits, so the
-// other bytes of a dword may ride along unmasked.
-__device__ __forceinline__ uint32_t run_low(const uint8_t* p, uint64_t n, bool full, uint32_t l) {
+// Two low-byte machines side by side, in bytes 0 and 2 of `x`: xor the byte into both, drop the products' high
+// bytes, one 24-bit multiply (byte 0's product stays below bit 16).  `bb` holds the byte in bytes 0 and 2.
+__device__ __forceinline__ uint32_t step_pair(uint32_t x, uint32_t bb) {
+    return __umul24((x ^ bb) & 0x00FF00FFu, kPrimeLow);
+}
+// Byte k of w, in bytes 0 and 2 (v_perm_b32: selector 0x0c gives a zero byte).
+template <int k>
+__device__ __forceinline__ uint32_t spread(uint32_t w) {
+    return __builtin_amdgcn_perm(0u, w, uint32_t(k | 0x0c00 | (k << 16) | 0x0c000000));
+}
+
+__device__ __forceinline__ uint32_t run_pair(const uint8_t* p, uint64_t n, bool full, uint32_t x) {
     if (full) {
         uint32_t w[kFnvLaneBytes / 4];
         load_segment(p, w);
 #pragma unroll
         for (int k = 0; k < kFnvLaneBytes / 4; ++k) {
-            l = __umul24(l ^ w[k], kPrimeLow);
-            l = __umul24(l ^ (w[k] >> 8), kPrimeLow);
-            l = __umul24(l ^ (w[k] >> 16), kPrimeLow);
-            l = __umul24(l ^ (w[k] >> 24), kPrimeLow);
+            x = step_pair(x, spread<0>(w[k]));
+            x = step_pair(x, spread<1>(w[k]));
+            x = step_pair(x, spread<2>(w[k]));
+            x = step_pair(x, spread<3>(w[k]));
         }
-        return l;
+        return x;
     }
-    for (uint64_t i = 0; i < n; ++i) l = __umul24(l ^ uint32_t(p[i]), kPrimeLow);
-    return l;
+    for (uint64_t i = 0; i < n; ++i) x = step_pair(x, uint32_t(p[i]) * 0x10001u);
+    return x;
+}
+
+// p^k mod 2^64 for k = 1..16 as four 16-bit limbs, limb[16 - k] for the byte k places before a block's end.
+struct PowLimbs {
+    uint32_t limb[16][4];
+};
+constexpr PowLimbs pow_limbs() {
+    PowLimbs t{};
+    uint64_t pk = 1;
+    for (int k = 1; k <= 16; ++k) {
+        pk *= kFnvPrime;
+        for (int j = 0; j < 4; ++j) t.limb[16 - k][j] = uint32_t((pk >> (16 * j)) & 0xFFFFu);
+    }
+    return t;
+}
+constexpr PowLimbs kPowLimbs = pow_limbs();
+constexpr uint64_t kPrime16 = [] {
+    uint64_t r = 1;
+    for (int k = 0; k < 16; ++k) r *= kFnvPrime;
+    return r;
+}();
+
+// The Horner sum of 16 bytes given the true low byte `l` before them: sum over c of d_c p^(16-c), d_c = (l ^ b) - l.
+// With |d| <= 255 and 16-bit limbs of the powers, each limb's sum of 16 products stays below 2^28, so the four sums
+// are exact in 32-bit integers and every product is a full-rate 24-bit multiply-add.
+__device__ __forceinline__ uint64_t block_sum(const u32x4 v, uint32_t& l) {
+    const uint32_t dw[4] = {v.x, v.y, v.z, v.w};
+    int32_t s0 = 0, s1 = 0, s2 = 0, s3 = 0;
+#pragma unroll
+    for (int c = 0; c < 16; ++c) {
+        const uint32_t x = (l ^ (dw[c >> 2] >> (8 * (c & 3)))) & 0xFFu;
+        const int32_t d = int32_t(x) - int32_t(l);
+        l = __umul24(x, kPrimeLow) & 0xFFu;
+        s0 += d * int32_t(kPowLimbs.limb[c][0]);
+        s1 += d * int32_t(kPowLimbs.limb[c][1]);
+        s2 += d * int32_t(kPowLimbs.limb[c][2]);
+        s3 += d * int32_t(kPowLimbs.limb[c][3]);
+    }
+    return uint64_t(int64_t(s0)) + (uint64_t(int64_t(s1)) << 16) + (uint64_t(int64_t(s2)) << 32) +
+           (uint64_t(int64_t(s3)) << 48);
 }
 
 // One step of the full hash given the true low byte `l` of the state: accumulate d = (l ^ b) - l, then multiply.
@@ -88,67 +141,143 @@ __device__ __forceinline__ void step_full(uint32_t b, uint32_t& l, uint64_t& acc
     l = __umul24(x, kPrimeLow) & 0xFFu;
 }
 
-// Bit `bit` of the start state of this lane's segment, from the previous level's ballots and scan: the seed's bit,
-// xor the parity of every earlier workgroup (scan), of the earlier waves of this workgroup, and of the earlier lanes
-// of this wave.
-__device__ __forceinline__ uint32_t start_bit(uint64_t seed, int bit, const uint64_t* word, const uint8_t* prefix) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    uint32_t v = uint32_t(seed >> bit) & 1u;
-    v ^= prefix[blockIdx.x];
-    for (int w = 0; w < wave; ++w) v ^= uint32_t(__popcll(word[uint64_t(blockIdx.x) * 4 + w])) & 1u;
-    const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
-    v ^= uint32_t(__popcll(word[uint64_t(blockIdx.x) * 4 + wave] & below)) & 1u;
-    return v;
+// Exclusive xor prefix of a 64-bit word: bit i of the result is the xor of bits 0..i-1.
+__device__ __forceinline__ uint64_t xor_prefix_excl(uint64_t x) {
+    x ^= x << 1;
+    x ^= x << 2;
+    x ^= x << 4;
+    x ^= x << 8;
+    x ^= x << 16;
+    x ^= x << 32;
+    return x << 1;
 }
 
-__global__ void __launch_bounds__(kThreads) fnv_level_kernel(const uint8_t* data, uint64_t n, int level, uint64_t seed,
-                                                              bool aligned, uint8_t* start, const uint64_t* word_prev,
-                                                              const uint8_t* prefix, uint64_t* word, uint8_t* parity) {
+// The ballots of one pass: per wave, T (bit-j terms), U0 and U1 (bit-(j+1) terms of the machines started with bit
+// j = 0 and = 1); a wave's V word (the bit-(j+1) terms of the machines that started from the true bit j) follows
+// from them and the true bit j of each lane.
+struct PassWords {
+    uint64_t* t;
+    uint64_t* u0;
+    uint64_t* u1;
+};
+
+// One wave's step of the two-bit resolution: (a, c) are the true bits j, j+1 at the wave's first segment; returns
+// the lanes' bit-j values and advances (a, c) past the wave.
+__device__ __forceinline__ uint64_t wave_step(uint64_t t, uint64_t u0, uint64_t u1, uint32_t& a, uint32_t& c,
+                                              uint64_t& v) {
+    const uint64_t sj = xor_prefix_excl(t) ^ (a ? ~0ull : 0ull);
+    v = (sj & u1) | (~sj & u0);
+    a ^= uint32_t(__popcll(t)) & 1u;
+    c ^= uint32_t(__popcll(v)) & 1u;
+    return sj;
+}
+
+// This lane's true start bits j (bit 0 of the result) and j + 1 (bit 1), from its workgroup's start state `gstate`
+// (bit j, bit j + 1 at the workgroup's first segment) and the ballots of the workgroup's waves.
+__device__ __forceinline__ uint32_t lane_bits(uint32_t gstate, const PassWords& w) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint64_t base = uint64_t(blockIdx.x) * 4;
+    uint32_t a = gstate & 1u, c = (gstate >> 1) & 1u;
+    uint64_t v = 0, sj = 0;
+    for (int k = 0; k <= wave; ++k) {
+        const uint32_t a0 = a, c0 = c;
+        sj = wave_step(w.t[base + k], w.u0[base + k], w.u1[base + k], a, c, v);
+        if (k == wave) { a = a0; c = c0; }
+    }
+    const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
+    return (uint32_t(sj >> lane) & 1u) | ((c ^ (uint32_t(__popcll(v & below)) & 1u)) << 1);
+}
+
+// Data pass for bits j, j + 1.  First completes each segment's start bits j - 2 and j - 1 from the previous pass
+// (bits 0..j-3 are in start[]), then runs the pair of machines, ballots T, U0, U1, and leaves the workgroup's
+// summary: bit 0 = xor of its T terms, bits 1 and 2 = xor of its V terms if bit j enters the workgroup as 0 or 1.
+__global__ void __launch_bounds__(kThreads) fnv_pair_kernel(const uint8_t* data, uint64_t n, int j, bool aligned,
+                                                             uint8_t* start, PassWords prev, const uint8_t* gstate_prev,
+                                                             PassWords out, uint8_t* summary) {
     const uint64_t seg = uint64_t(blockIdx.x) * kThreads + threadIdx.x;
     const uint64_t begin = seg * kFnvLaneBytes;
     const bool live = begin < n;
     uint32_t s = 0;
-    if (level > 0) {
-        const uint32_t bit = start_bit(seed, level - 1, word_prev, prefix);
-        s = (level > 1 && live ? uint32_t(start[seg]) : 0u) | (bit << (level - 1));
+    if (j > 0) {
+        const uint32_t bits = lane_bits(gstate_prev[blockIdx.x], prev);
+        s = (j > 2 && live ? uint32_t(start[seg]) : 0u) | (bits << (j - 2));
         if (live) start[seg] = uint8_t(s);
     }
-    uint32_t t = 0;
+    uint32_t e = 0;
     if (live) {
         const uint64_t len = n - begin < kFnvLaneBytes ? n - begin : kFnvLaneBytes;
-        t = (run_low(data + begin, len, aligned && len == kFnvLaneBytes, s) >> level) & 1u;
+        e = run_pair(data + begin, len, aligned && len == kFnvLaneBytes, s | ((s | (1u << j)) << 16));
     }
-    const uint64_t ballot = __ballot(t);
-    __shared__ uint64_t s_word[kThreads / 64];
+    const uint64_t bt = __ballot((e >> j) & 1u), b0 = __ballot((e >> (j + 1)) & 1u),
+                   b1 = __ballot((e >> (16 + j + 1)) & 1u);
+    __shared__ uint64_t s_w[3][kThreads / 64];
+    const int wave = threadIdx.x >> 6;
     if ((threadIdx.x & 63) == 0) {
-        word[uint64_t(blockIdx.x) * 4 + (threadIdx.x >> 6)] = ballot;
-        s_word[threadIdx.x >> 6] = ballot;
+        const uint64_t at = uint64_t(blockIdx.x) * 4 + wave;
+        out.t[at] = bt;
+        out.u0[at] = b0;
+        out.u1[at] = b1;
+        s_w[0][wave] = bt;
+        s_w[1][wave] = b0;
+        s_w[2][wave] = b1;
     }
     __syncthreads();
-    if (threadIdx.x == 0)
-        parity[blockIdx.x] = uint8_t(__popcll(s_word[0] ^ s_word[1] ^ s_word[2] ^ s_word[3]) & 1);
+    if (threadIdx.x == 0) {
+        uint32_t sum = 0;
+        for (uint32_t in = 0; in < 2; ++in) {
+            uint32_t a = in, c = 0;
+            uint64_t v;
+            for (int k = 0; k < kThreads / 64; ++k) wave_step(s_w[0][k], s_w[1][k], s_w[2][k], a, c, v);
+            if (in == 0) sum |= a ^ in;   // the xor of the T terms
+            sum |= c << (1 + in);
+        }
+        summary[blockIdx.x] = uint8_t(sum);
+    }
 }
 
-// Exclusive xor prefix of the per-workgroup parities, in one workgroup: each thread folds a contiguous run, a ballot
-// scan joins the runs.
-__global__ void __launch_bounds__(kScanThreads) fnv_scan_kernel(const uint8_t* parity, uint64_t groups, uint8_t* prefix) {
+// The workgroups' start states for one pass, in one workgroup.  Workgroup g maps the state (a, c) = (bit j, bit
+// j + 1) at its first segment to (a ^ T_g, c ^ V_g(a)) at the next workgroup's; such maps of a 2-bit state are
+// 4-entry tables (one byte, two bits per entry), composed in a run per thread, scanned across threads in LDS, and
+// applied to the seed's bits.
+__device__ __forceinline__ uint32_t map_of(uint32_t summary) {
+    uint32_t m = 0;
+    for (uint32_t st = 0; st < 4; ++st) {
+        const uint32_t a = st & 1u, c = st >> 1;
+        const uint32_t na = a ^ (summary & 1u), nc = c ^ ((summary >> (1 + a)) & 1u);
+        m |= (na | (nc << 1)) << (2 * st);
+    }
+    return m;
+}
+// g after f
+__device__ __forceinline__ uint32_t compose(uint32_t g, uint32_t f) {
+    uint32_t m = 0;
+    for (uint32_t st = 0; st < 4; ++st) m |= ((g >> (2 * ((f >> (2 * st)) & 3u))) & 3u) << (2 * st);
+    return m;
+}
+constexpr uint32_t kIdentityMap = 0u | (1u << 2) | (2u << 4) | (3u << 6);
+
+__global__ void __launch_bounds__(kScanThreads) fnv_scan_kernel(const uint8_t* summary, uint64_t groups, uint32_t init,
+                                                                 uint8_t* gstate) {
     const uint64_t per = (groups + kScanThreads - 1) / kScanThreads;
     const uint64_t b = uint64_t(threadIdx.x) * per;
     const uint64_t e = b + per < groups ? b + per : groups;
-    uint32_t p = 0;
-    for (uint64_t i = b; i < e; ++i) p ^= parity[i];
-    const uint64_t ballot = __ballot(p & 1u);
-    __shared__ uint64_t s_word[kScanThreads / 64];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    if (lane == 0) s_word[wave] = ballot;
+    uint32_t f = kIdentityMap;
+    for (uint64_t i = b; i < e; ++i) f = compose(map_of(summary[i]), f);
+    // inclusive scan of the run maps (Hillis-Steele), then the exclusive prefix of this thread's run
+    __shared__ uint32_t s_map[kScanThreads];
+    s_map[threadIdx.x] = f;
     __syncthreads();
-    uint32_t pre = 0;
-    for (int w = 0; w < wave; ++w) pre ^= uint32_t(__popcll(s_word[w])) & 1u;
-    const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
-    pre ^= uint32_t(__popcll(ballot & below)) & 1u;
+    for (int o = 1; o < kScanThreads; o <<= 1) {
+        const uint32_t earlier = threadIdx.x >= uint32_t(o) ? s_map[threadIdx.x - o] : kIdentityMap;
+        __syncthreads();
+        s_map[threadIdx.x] = compose(s_map[threadIdx.x], earlier);
+        __syncthreads();
+    }
+    const uint32_t before = threadIdx.x ? s_map[threadIdx.x - 1] : kIdentityMap;
+    uint32_t st = (before >> (2 * init)) & 3u;
     for (uint64_t i = b; i < e; ++i) {
-        prefix[i] = uint8_t(pre);
-        pre ^= parity[i];
+        gstate[i] = uint8_t(st);
+        st = (map_of(summary[i]) >> (2 * st)) & 3u;
     }
 }
 
@@ -157,33 +286,26 @@ __device__ __forceinline__ uint64_t shfl_xor64(uint64_t v, int m) {
     return (uint64_t(hi) << 32) | lo;
 }
 
-__global__ void __launch_bounds__(kThreads) fnv_final_kernel(const uint8_t* data, uint64_t n, uint64_t seed, bool aligned,
-                                                              const uint8_t* start, const uint64_t* word_prev,
-                                                              const uint8_t* prefix, uint64_t* partial) {
+__global__ void __launch_bounds__(kThreads) fnv_final_kernel(const uint8_t* data, uint64_t n, bool aligned,
+                                                              const uint8_t* start, PassWords prev,
+                                                              const uint8_t* gstate_prev, uint64_t* partial) {
     const uint64_t seg = uint64_t(blockIdx.x) * kThreads + threadIdx.x;
     const uint64_t begin = seg * kFnvLaneBytes;
-    const uint32_t bit7 = start_bit(seed, 7, word_prev, prefix);
+    const uint32_t bits67 = lane_bits(gstate_prev[blockIdx.x], prev);
     uint64_t acc = 0;
     if (begin < n) {
-        uint32_t l = uint32_t(start[seg]) | (bit7 << 7);
+        uint32_t l = uint32_t(start[seg]) | (bits67 << 6);
         const uint64_t len = n - begin < kFnvLaneBytes ? n - begin : kFnvLaneBytes;
         const uint8_t* p = data + begin;
         if (aligned && len == kFnvLaneBytes) {
-            // 16 bytes per iteration: the Horner step is ~20 instructions, so a fully unrolled segment would not fit
-            // the instruction cache; the next chunk's load is issued before this chunk's steps.
-            u32x4 next = *(const gu32x4*) p;
-            for (int k = 0; k < kFnvLaneBytes / 16; ++k) {
-                const u32x4 v = next;
-                if (k + 1 < kFnvLaneBytes / 16) next = *(const gu32x4*) (p + 16 * (k + 1));
-                const uint32_t dw[4] = {v.x, v.y, v.z, v.w};
+            // the whole segment is loaded first (lanes are 256 bytes apart, so each 128-byte line is read by eight
+            // of a lane's loads: issued together they are served by one fetch), then 16 bytes per step: a block
+            // sum, then acc * p^16
+            u32x4 v[kFnvLaneBytes / 16];
 #pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    step_full(dw[c] & 0xFFu, l, acc);
-                    step_full((dw[c] >> 8) & 0xFFu, l, acc);
-                    step_full((dw[c] >> 16) & 0xFFu, l, acc);
-                    step_full(dw[c] >> 24, l, acc);
-                }
-            }
+            for (int k = 0; k < kFnvLaneBytes / 16; ++k) v[k] = *(const gu32x4*) (p + 16 * k);
+#pragma unroll
+            for (int k = 0; k < kFnvLaneBytes / 16; ++k) acc = acc * kPrime16 + block_sum(v[k], l);
         } else {
             for (uint64_t i = 0; i < len; ++i) step_full(p[i], l, acc);
         }
@@ -214,7 +336,8 @@ __global__ void __launch_bounds__(kScanThreads) fnv_reduce_kernel(const uint64_t
 
 }  // namespace
 
-// Workspace: [start bytes: one per segment][ballot words, two sets][parities][prefixes][partial sums].
+// Workspace: [start bytes: one per segment][ballot words T, U0, U1: two sets (this pass, the previous)]
+// [summaries][workgroup start states: two sets][partial sums].
 FnvWorkspace fnv_workspace(uint64_t n) {
     FnvWorkspace w{};
     w.segments = (n + kFnvLaneBytes - 1) / kFnvLaneBytes;
@@ -222,10 +345,10 @@ FnvWorkspace fnv_workspace(uint64_t n) {
     auto up = [](uint64_t x) { return (x + 255) / 256 * 256; };
     w.off_start = 0;
     w.off_word0 = up(w.segments);
-    w.off_word1 = w.off_word0 + up(w.groups * 4 * 8);
-    w.off_parity = w.off_word1 + up(w.groups * 4 * 8);
-    w.off_prefix = w.off_parity + up(w.groups);
-    w.off_partial = w.off_prefix + up(w.groups);
+    w.off_word1 = w.off_word0 + 3 * up(w.groups * 4 * 8);
+    w.off_parity = w.off_word1 + 3 * up(w.groups * 4 * 8);   // summaries
+    w.off_prefix = w.off_parity + up(w.groups);               // start states, two sets
+    w.off_partial = w.off_prefix + 2 * up(w.groups);
     w.bytes = w.off_partial + up(w.groups * 8 > 8 ? w.groups * 8 : 8);
     return w;
 }
@@ -236,19 +359,29 @@ hipError_t launch_fnv1a64(const void* data, uint64_t n, uint64_t seed, uint64_t*
     uint8_t* ws = static_cast<uint8_t*>(workspace);
     const uint8_t* src = static_cast<const uint8_t*>(data);
     const bool aligned = (reinterpret_cast<uintptr_t>(data) & 15u) == 0;
+    const uint64_t word_bytes = (w.off_word1 - w.off_word0) / 3;
+    auto words = [&](uint64_t off) {
+        return PassWords{reinterpret_cast<uint64_t*>(ws + off), reinterpret_cast<uint64_t*>(ws + off + word_bytes),
+                         reinterpret_cast<uint64_t*>(ws + off + 2 * word_bytes)};
+    };
+    const PassWords set[2] = {words(w.off_word0), words(w.off_word1)};
     uint8_t* start = ws + w.off_start;
-    uint64_t* words[2] = {reinterpret_cast<uint64_t*>(ws + w.off_word0), reinterpret_cast<uint64_t*>(ws + w.off_word1)};
-    uint8_t* parity = ws + w.off_parity;
-    uint8_t* prefix = ws + w.off_prefix;
+    uint8_t* summary = ws + w.off_parity;
+    const uint64_t half = (w.off_partial - w.off_prefix) / 2;
+    uint8_t* gstate[2] = {ws + w.off_prefix, ws + w.off_prefix + half};
     uint64_t* partial = reinterpret_cast<uint64_t*>(ws + w.off_partial);
     if (w.groups > 0) {
-        for (int level = 0; level < 8; ++level) {
-            hipLaunchKernelGGL(fnv_level_kernel, dim3(unsigned(w.groups)), dim3(kThreads), 0, stream, src, n, level,
-                               seed, aligned, start, words[(level + 1) & 1], prefix, words[level & 1], parity);
-            hipLaunchKernelGGL(fnv_scan_kernel, dim3(1), dim3(kScanThreads), 0, stream, parity, w.groups, prefix);
+        const dim3 grid(unsigned(w.groups)), block(kThreads), one(1), scan(kScanThreads);
+        for (int q = 0; q < 4; ++q) {
+            // pass q resolves bits 2q and 2q + 1; it reads the previous pass's ballots and workgroup states
+            const int j = 2 * q;
+            hipLaunchKernelGGL(fnv_pair_kernel, grid, block, 0, stream, src, n, j, aligned, start, set[(q + 1) & 1],
+                               gstate[(q + 1) & 1], set[q & 1], summary);
+            const uint32_t init = uint32_t((seed >> j) & 3u);
+            hipLaunchKernelGGL(fnv_scan_kernel, one, scan, 0, stream, summary, w.groups, init, gstate[q & 1]);
         }
-        hipLaunchKernelGGL(fnv_final_kernel, dim3(unsigned(w.groups)), dim3(kThreads), 0, stream, src, n, seed, aligned,
-                           start, words[1], prefix, partial);
+        hipLaunchKernelGGL(fnv_final_kernel, grid, block, 0, stream, src, n, aligned, start, set[1], gstate[1],
+                           partial);
     }
     hipLaunchKernelGGL(fnv_reduce_kernel, dim3(1), dim3(kScanThreads), 0, stream, partial, w.groups, seed, n, out);
     return hipGetLastError();
