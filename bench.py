@@ -42,6 +42,30 @@ def measured_traffic() -> int | None:
 HBM_PEAK_GBPS = 8000.0
 
 
+def settle_link(sc, floor_gbps: float, limit_s: float = 3.0) -> float:
+    """Waits until a 64 MiB pinned D2H copy runs at >= 97% of `floor_gbps` again and returns the wait in ms.
+
+    Device memory this process frees is wiped by the driver on the same copy engines that carry the host link: right
+    after a row frees a few GB, parks and resumes run at about half the link rate for up to half a second (measured:
+    30 GB/s right after freeing 3.3 GB of pools, 57 GB/s again after ~0.5 s).  A serving process keeps its pools,
+    so each host-link row starts once the link is back to its rate; the wait is reported beside the row."""
+    n = 64 << 20
+    host, dev = sc.PinnedBuffer(n), sc.DeviceBuffer(n, "uint8")
+    st = sc.Stream()
+    e0, e1 = sc.Event(), sc.Event()
+    t0 = time.perf_counter()
+    while True:
+        e0.record(st)
+        sc.check(sc.lib.sc_copy_async(host.ptr, dev.ptr, n, st.handle), "settle copy")
+        e1.record(st)
+        e1.sync()
+        if n / (e0.elapsed_ms(e1) * 1e-3) / 1e9 >= 0.97 * floor_gbps or time.perf_counter() - t0 > limit_s:
+            break
+    host.free()
+    dev.free()
+    return round((time.perf_counter() - t0) * 1e3, 1)
+
+
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
@@ -123,7 +147,7 @@ def cpu_baseline(geo_kw: dict, tokens: int, budget_s: float) -> dict:
     }
 
 
-def config4(sc, geo, seed: int, link_gbps: float) -> dict:
+def config4(sc, geo, seed: int, link_gbps: float, streams=None) -> dict:
     """Config 3 slots: contexts 8K / 32K / 96K assigned to roles from `seed`.  One slot keeps decoding (a synthetic
     decode step reads all of its K/V) on its own stream; the other two park to pinned host memory on a park stream;
     the first parked one is resumed into a fresh slot on a resume stream as soon as its park lands, overlapping the
@@ -143,7 +167,7 @@ def config4(sc, geo, seed: int, link_gbps: float) -> dict:
     restored = sc.new_slot(geo, park_a, fill=0)
     sink = sc.DeviceBuffer(4096, "uint32")
     sc.device_sync()
-    decode, park, resume = sc.Stream(), sc.Stream(), sc.Stream()
+    decode, park, resume = streams if streams is not None else (sc.Stream(), sc.Stream(), sc.Stream())
     pools = slots[decode_len].k_pool + slots[decode_len].v_pool
 
     def decode_step():
@@ -335,11 +359,17 @@ def wire_payload(sc, geo, tokens: int, slot, link_h2d: float, link_d2h: float, r
 
 def quant_carve(sc, geo, tokens: int, stream, reps: int = 10) -> dict:
     """The quantizing carve of the config-3 geometry: f32 K/V rows into int8 / q4_0 / K8V4 pools plus the GDN state,
-    one launch each.  HBM bytes = the f32 rows read + the codes and scales written + the GDN rows read and written."""
+    one launch each (and int8 once more through a shuffled page table).  HBM bytes = the f32 rows read + the codes and
+    scales written + the GDN rows read and written."""
+    import numpy as np
     case = sc.SyntheticCase(geo, tokens, seed=0x5EED, kv_dtype=sc.SC_DTYPE_F32)
     out = {"tokens": tokens}
-    for name, fmt in (("int8", sc.SC_KV_INT8), ("q4_0", sc.SC_KV_Q4), ("k8v4", sc.SC_KV_K8V4)):
-        slot = sc.new_quant_slot(geo, fmt, tokens)
+    n_pages = (tokens + geo.page_size - 1) // geo.page_size
+    shuffled = sc.device_tables([np.random.default_rng(j).permutation(n_pages).astype(np.int32)
+                                 for j in range(geo.n_qsa)])
+    for name, fmt, tables in (("int8", sc.SC_KV_INT8, None), ("q4_0", sc.SC_KV_Q4, None),
+                              ("k8v4", sc.SC_KV_K8V4, None), ("int8_paged", sc.SC_KV_INT8, shuffled)):
+        slot = sc.new_quant_slot(geo, fmt, tokens, tables=tables)
         plan = sc.plan_carve_quant(geo, case.prefill, slot)
         _, per = time_launches(plan, stream, reps, 2, sc)
         ms = sum(per) / len(per)
@@ -366,6 +396,8 @@ def main() -> int:
     ap.add_argument("--kernel-only", action="store_true", help="only the timed handoff (for profiler runs)")
     ap.add_argument("--wire-only", action="store_true",
                     help="only the wire payload row of the same slot (for profiler runs); prints its JSON")
+    ap.add_argument("--quant-only", action="store_true",
+                    help="only the quantizing carve row of the same geometry (for profiler runs); prints its JSON")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run 5 device-to-device copies of BYTES (the counter calibration of profiler runs)")
     args = ap.parse_args()
@@ -392,12 +424,17 @@ def main() -> int:
         sc.device_sync()
         print(json.dumps({"copy_calibration_bytes": n, "copies": 5}), flush=True)
         return 0
+    # the host link, measured before anything large is allocated (the reference's probe method, both directions)
+    h2d, d2h = sc.probe_link(256 << 20, 4)
     geo_kw = dict(n_layers=48, qsa_interval=4, n_head_kv=2, head_dim=256, page_size=4, ssm_state_size=128,
                   ssm_k_heads=16, ssm_v_heads=32, ssm_d_conv=4, ssm_conv_channels=8192, idx_key_dim=128)
     geo = sc.geometry(**geo_kw)
     T = args.tokens
     P = sc.payload_bytes(geo, T)
 
+    if args.quant_only:
+        print(json.dumps({"quant_carve": quant_carve(sc, geo, T, stream)}), flush=True)
+        return 0
     log(f"config 3: {T} tokens, payload {P} B; generating inputs on the device")
     case = sc.SyntheticCase(geo, tokens=T, seed=0x5EED)
     slot = case.new_slot(max_cells=T)
@@ -429,12 +466,29 @@ def main() -> int:
                      "algorithmic_bytes_per_launch": 2 * P},
     }
     if args.wire_only:
-        h2d, d2h = sc.probe_link(256 << 20, 2)
         print(json.dumps({"wire_payload": wire_payload(sc, geo, T, slot, h2d, d2h)}), flush=True)
         return 0
     if args.kernel_only:
         print(json.dumps(result), flush=True)
         return 0
+
+    # the same carve into a slot whose pages are placed through a shuffled page table (a decode slot's pages are
+    # wherever the pool had them free); the table entries are loaded with the data
+    import numpy as np
+    n_pages = (T + geo.page_size - 1) // geo.page_size
+    tables = sc.device_tables([np.random.default_rng(j).permutation(n_pages).astype(np.int32)
+                               for j in range(geo.n_qsa)])
+    paged_slot = case.new_slot(max_cells=T, tables=tables)
+    paged = sc.plan_carve(geo, case.prefill, paged_slot)
+    _, per_paged = time_launches(paged, stream, 10, 2, sc)
+    paged_ms = sum(per_paged) / len(per_paged)
+    result["paged_carve"] = {"ms": round(paged_ms, 4), "hbm_gbps": round(2 * P / (paged_ms * 1e-3) / 1e9, 1),
+                             "frac": round(2 * P / (paged_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+                             "table": "a random permutation of the pool's pages per QSA layer"}
+    log(f"paged carve (shuffled page table): {paged_ms:.3f} ms")
+    paged.destroy()
+    for b in paged_slot.buffers():
+        b.free()
 
     # two-pass gather -> scatter through a transfer buffer (the cross-instance path)
     _, total = sc.image_layout(geo, T)
@@ -463,8 +517,8 @@ def main() -> int:
                           "scatter_hbm_gbps": round(2 * P / (s_ms * 1e-3) / 1e9, 1)}
     log(f"two-pass: gather {g_ms:.3f} ms, scatter {s_ms:.3f} ms")
 
-    # park / resume of the 128K slot against the measured host link
-    h2d, d2h = sc.probe_link(256 << 20, 4)
+    # park / resume of the 128K slot against the host link measured at the start of the run
+    settle_pr = settle_link(sc, d2h)
     host = sc.PinnedBuffer(total)
     side = sc.Stream()
     t0, t1 = sc.Event(), sc.Event()
@@ -489,7 +543,8 @@ def main() -> int:
         "link_d2h_gbps": round(d2h, 2), "link_h2d_gbps": round(h2d, 2),
         "park_frac": round(total / (pk * 1e-3) / 1e9 / d2h, 3), "resume_frac": round(total / (rs * 1e-3) / 1e9 / h2d, 3),
         "method": "hipMemcpyAsync per blob on a non-blocking side stream, pinned hipHostMalloc image; link probe "
-                  "pinned 256 MiB x 4 per direction"}
+                  "pinned 256 MiB x 4 per direction at the start of the run",
+        "link_settle_ms": settle_pr}
     log(f"park {pk:.1f} ms, resume {rs:.1f} ms; link d2h {d2h:.1f} GB/s, h2d {h2d:.1f} GB/s")
     host.free()
     image.free()
@@ -520,7 +575,9 @@ def main() -> int:
     log(f"32K handoff p50 {p50:.4f} ms over {len(lat)} reps")
 
     log("wire payload: device encode / hash / mount of the 128K slot, checked park and resume")
+    settle_wire = settle_link(sc, d2h)
     result["wire_payload"] = wire_payload(sc, geo, T, slot, h2d, d2h)
+    result["wire_payload"]["link_settle_ms"] = settle_wire
     wp = result["wire_payload"]
     log(f"wire: encode {wp['encode_ms']} ms ({wp['encode_gbps']} GB/s), hash {wp['hash_ms']} ms, mount "
         f"{wp['mount_ms']} ms; checked park {wp['checked_park_gbps']} GB/s, resume {wp['checked_resume_gbps']} GB/s")
@@ -531,14 +588,18 @@ def main() -> int:
     log("quant carve: " + ", ".join(f"{k} {v['ms']} ms ({v['hbm_gbps']} GB/s)" for k, v in qc.items() if k != "tokens"))
 
     log("config 4: three slots, two parks and one resume overlapped with decode")
+    settle_c4 = settle_link(sc, d2h)
     result["config4"] = config4(sc, geo, 0x5EED, d2h)
+    result["config4"]["link_settle_ms"] = settle_c4
     c4 = result["config4"]
     log(f"config 4: park {c4['park_gbps']} GB/s, resume {c4['resume_gbps']} GB/s, decode slowdown "
         f"{c4['decode_slowdown']}x, bit-exact {c4['round_trip_bit_exact']}")
     result["config4"]["park_frac"] = round(c4["park_gbps"] / d2h, 3)
     result["config4"]["resume_frac"] = round(c4["resume_gbps"] / h2d, 3)
     log("config 5: eight ragged slots, batched resume + append in one launch")
+    settle_c5 = settle_link(sc, d2h)
     result["config5"] = config5(sc, geo, 0x5EED)
+    result["config5"]["link_settle_ms"] = settle_c5
     c5 = result["config5"]
     result["config5"]["resume_h2d_frac"] = round(c5["resume_h2d_gbps"] / h2d, 3)
     log(f"config 5: resume {c5['resume_h2d_gbps']} GB/s, one-launch scatter {c5['scatter_launch_ms']} ms "
