@@ -196,6 +196,56 @@ int sc_plan_capture_map(const sc_geometry* g, const sc_decode_slot* src, int64_t
  * src/core/conversation_snapshot.cpp:196-204). */
 int sc_plan_scatter_map(const sc_geometry* g, const void* src, uint64_t src_bytes, const sc_blob_map* map,
                         int64_t tokens, const sc_decode_slot* dst, sc_plan** out);
+/* ---- slot images in every K/V format ------------------------------------------------------------------------------
+ * A slot's per-layer buffers as conversation_kv_save takes them (src/core/conversation_snapshot.cpp:69-78, pools()):
+ * the K and V data, the K and V int8 scales and the indexer's pooled rows, each in the identity layout (kv_mode 0, the
+ * layout a snapshot copies a prefix of), plus the GDN rows. */
+enum { SC_BUF_K = 0, SC_BUF_V = 1, SC_BUF_K_SCALE = 2, SC_BUF_V_SCALE = 3, SC_BUF_POOLED = 4, SC_N_BUF = 5 };
+/* The indexer pools one key per 4 cells (include/strata/kernels/qsa.hpp:103,112: idx_block). */
+enum { SC_IDX_BLOCK = 4 };
+typedef struct sc_slot_layers {
+    int32_t format;               /* SC_KV_F16, SC_KV_INT8, SC_KV_Q4 or SC_KV_K8V4 */
+    int32_t with_index;           /* 1: the indexer's pooled rows belong to the image (include_index) */
+    int64_t max_cells;            /* cells every K/V buffer holds (QsaState::max_cells) */
+    int64_t pooled_capacity;      /* rows every pooled buffer holds (QsaState::idx_pooled_rows) */
+    void* const* buf[SC_N_BUF];   /* host arrays of [n_qsa] device pointers, by SC_BUF_*; NULL where the format or
+                                     with_index has no such buffer */
+    float* gdn_state;             /* the n_gdn GDN rows (NULL without GDN layers) */
+} sc_slot_layers;
+/* Bytes of one QSA layer's five blobs for `tokens` tokens, by conversation_snapshot.cpp:27-66 (layout()): cells =
+ * sc_kv_cells(tokens); K and V data cells*H*(2D f16, D int8, D/32*18 q4_0; K8V4: D for K, D/32*18 for V); int8 scales
+ * cells*H*(D/64)*2 (K8V4: K only); pooled rows (tokens/SC_IDX_BLOCK + 1)*idx_key_dim*4 when with_index and tokens > 0.
+ * Refuses a head_dim the format cannot hold (int8 needs D % 64 == 0, q4_0 D % 32 == 0). */
+int sc_layer_blob_bytes(const sc_geometry* g, int32_t format, int32_t with_index, int64_t tokens, uint64_t* bytes);
+/* The image of a slot in any format: for each QSA layer its nonempty blobs in SC_BUF order, then the GDN rows, each
+ * on a 64-byte boundary (the wire codec's pool order, src/core/conversation_wire.cpp:400-437).  offsets (may be NULL)
+ * gets n_qsa*SC_N_BUF + 1 entries: blob b of layer j at [j*SC_N_BUF + b], the GDN rows last; UINT64_MAX marks an
+ * empty blob.  For SC_KV_F16 without the index it is sc_image_layout. */
+int sc_image_layout_layers(const sc_geometry* g, int32_t format, int32_t with_index, int64_t tokens, uint64_t* offsets,
+                           uint64_t* total_bytes);
+/* Where a capture or scatter of sc_slot_layers puts each blob in a caller-laid-out buffer (a wire payload's pool):
+ * `off` as sc_image_layout_layers writes it (16-byte aligned, UINT64_MAX for an empty blob), and zero ranges as in
+ * sc_blob_map.  A NULL map means the image layout of sc_image_layout_layers with its gaps zeroed. */
+typedef struct sc_layers_map {
+    const uint64_t* off;     /* [n_qsa*SC_N_BUF + 1] */
+    const uint64_t* zero;    /* [2*n_zero] (offset, bytes) ranges a capture zero-fills: whole 16-byte chunks */
+    int64_t n_zero;
+} sc_layers_map;
+/* The slot's blob prefixes and GDN rows into `dst`, in one launch: the device half of conversation_kv_save for every
+ * format (conversation_snapshot.cpp:139-173) and of conversation_checkpoint_save's GDN copy (conversation_state.cpp:235).
+ * Every blob must be whole 16-byte chunks (SC_ERANGE otherwise). */
+int sc_plan_capture_layers(const sc_geometry* g, const sc_slot_layers* src, int64_t tokens, void* dst,
+                           uint64_t dst_bytes, const sc_layers_map* map, sc_plan** out);
+/* The inverse, in one launch: conversation_kv_restore for every format (conversation_snapshot.cpp:196-204) and the GDN
+ * restore (conversation_state.cpp:251).  Bytes of the slot past the image's cells and rows are left as they are. */
+int sc_plan_scatter_layers(const sc_geometry* g, const void* src, uint64_t src_bytes, const sc_layers_map* map,
+                           int64_t tokens, const sc_slot_layers* dst, sc_plan** out);
+/* Park / resume of a slot in any format to / from a pinned host image of sc_image_layout_layers, one hipMemcpyAsync per
+ * blob on `stream`, `done` recorded after the last (as sc_park_async / sc_resume_async for f16 slots). */
+int sc_park_layers_async(const sc_geometry* g, const sc_slot_layers* slot, int64_t tokens, void* host_image,
+                         uint64_t image_bytes, void* stream, void* done);
+int sc_resume_layers_async(const sc_geometry* g, const void* host_image, uint64_t image_bytes, int64_t tokens,
+                           const sc_slot_layers* slot, void* stream, void* done);
 /* Enqueue the plan on `stream` (a hipStream_t; NULL is the null stream).  Asynchronous. */
 int sc_plan_launch(const sc_plan* plan, void* stream);
 /* Algorithmic payload bytes the plan moves (each read once and written once). */

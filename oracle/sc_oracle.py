@@ -137,6 +137,59 @@ def image_layout(geo, tokens: int) -> tuple[list[tuple[int, int, int, int]], int
     return [(b.kind, b.layer, b.offset, b.bytes) for b in blobs[:n]], int(total.value)
 
 
+# ---- slot images in every K/V format ----------------------------------------------------------------------------------
+
+KV_F16, KV_INT8, KV_Q4, KV_K8V4 = 0, 1, 2, 3
+IDX_BLOCK = 4          # the indexer pools one key per 4 cells (include/strata/kernels/qsa.hpp:103,112)
+BUF_NAMES = ("k", "v", "k_scale", "v_scale", "pooled")   # ConversationKv's buffers, in the wire pool order
+
+
+def layer_blob_bytes(geo, fmt: int, with_index: bool, tokens: int) -> list[int]:
+    """One QSA layer's five blob sizes (k, v, k_scale, v_scale, pooled) for `tokens` tokens, restating layout() of
+    src/core/conversation_snapshot.cpp:27-66: cells = ceil(T/page_size)*page_size; per head f16 2D bytes, int8 D, q4_0
+    (D/32)*18 (kv_q4_bytes_per_head, include/strata/kernels/kv_q4.hpp:33); int8 keys carry (D/64)*2 bytes of f16 scales
+    per head; K8V4 (format 3) is int8 K with q4_0 V and no V scales; pooled rows T/4 + 1 of idx_key_dim f32 with the
+    index."""
+    g = geometry_from(geo)
+    H, D, ps = g.n_head_kv, g.head_dim, g.page_size
+    cells = (tokens + ps - 1) // ps * ps
+    q4_head = D // 32 * 18
+    per_head = {KV_F16: 2 * D, KV_INT8: D, KV_Q4: q4_head, KV_K8V4: D}[fmt]
+    k = cells * H * per_head
+    v = cells * H * (q4_head if fmt == KV_K8V4 else per_head)
+    ks = cells * H * (D // 64) * 2 if fmt in (KV_INT8, KV_K8V4) else 0
+    vs = ks if fmt == KV_INT8 else 0
+    pooled = (tokens // IDX_BLOCK + 1) * g.idx_key_dim * 4 if with_index and tokens > 0 else 0
+    return [k, v, ks, vs, pooled]
+
+
+def image_layout_layers(geo, fmt: int, with_index: bool, tokens: int) -> tuple[list[int | None], int]:
+    """The slot image in any format: for each QSA layer its nonempty blobs in BUF_NAMES order, then the GDN rows, each
+    64-byte aligned (the pool order of src/core/conversation_wire.cpp:400-437).  Returns the offsets (layer-major,
+    five per layer, None for an empty blob; the GDN rows last) and the total."""
+    g = geometry_from(geo)
+    n_qsa = g.n_layers // g.qsa_interval
+    n_gdn = g.n_layers - n_qsa
+    sizes = layer_blob_bytes(geo, fmt, with_index, tokens)
+    offs: list[int | None] = []
+    at = 0
+    for _ in range(n_qsa):
+        for n in sizes:
+            if n:
+                at = (at + 63) // 64 * 64
+                offs.append(at)
+                at += n
+            else:
+                offs.append(None)
+    if n_gdn:
+        at = (at + 63) // 64 * 64
+        offs.append(at)
+        at += n_gdn * int(lib.sco_gdn_row_floats(C.byref(g))) * 4
+    else:
+        offs.append(None)
+    return offs, (at + 63) // 64 * 64
+
+
 def fnv1a64(data: bytes | np.ndarray, seed: int = REFERENCE_FNV_SEED) -> int:
     a = np.frombuffer(bytes(data), dtype=np.uint8) if not isinstance(data, np.ndarray) else \
         np.ascontiguousarray(data).view(np.uint8).reshape(-1)

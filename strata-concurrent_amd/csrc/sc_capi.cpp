@@ -109,6 +109,7 @@ bool geometry(const sc_geometry* g, Geo& o, std::string& why) {
     o.page_bytes = uint64_t(o.H) * uint64_t(o.ps) * o.row_bytes;
     o.rec_bytes = uint64_t(o.S) * uint64_t(o.HV) * uint64_t(o.S) * 4;
     o.gdn_row_bytes = o.rec_bytes + uint64_t(o.C) * uint64_t(o.hist) * 4;
+    if (o.gdn_row_bytes % 16) { why = "a GDN row must be whole 16-byte chunks (C*(d_conv-1) a multiple of 4)"; return false; }
     return true;
 }
 
@@ -321,6 +322,71 @@ void gdn_rows(const Geo& g, const sc_prefill_view* v, float* gdn, std::vector<sc
 }
 
 uint64_t kv_payload(const Geo& g, int64_t tokens) { return uint64_t(tokens) * uint64_t(g.H) * g.row_bytes * 2 * uint64_t(g.n_qsa); }
+
+// ---- slot images in every K/V format (sc_slot_layers) ----
+
+constexpr uint64_t kAbsent = ~uint64_t(0);
+
+// The five blob sizes of one QSA layer (conversation_snapshot.cpp:27-66): data, value data, key scales, value scales,
+// pooled indexer rows.  Returns an empty string or the refusal.
+std::string layer_blob_sizes(const Geo& o, const sc_geometry* g, int32_t format, bool index, int64_t tokens,
+                             uint64_t (&b)[SC_N_BUF]) {
+    if (format < SC_KV_F16 || format > SC_KV_K8V4) return "unknown K/V format";
+    if (tokens < 0 || tokens > (int64_t(1) << 30)) return "invalid K/V extent";
+    const bool q4 = format == SC_KV_Q4, int8_keys = format == SC_KV_INT8 || format == SC_KV_K8V4;
+    if (g->idx_key_dim <= 0 || g->idx_key_dim > (1 << 20) || (q4 && o.D % 32) || (int8_keys && o.D % 64) ||
+        (format == SC_KV_K8V4 && o.D % 32))
+        return "invalid K/V geometry";
+    const uint64_t cells = uint64_t(cells_of(o, tokens)), H = uint64_t(o.H), D = uint64_t(o.D);
+    const uint64_t q4_head = D / 32 * 18;
+    const uint64_t per_head = format == SC_KV_F16 ? 2 * D : q4 ? q4_head : D;
+    b[SC_BUF_K] = cells * H * per_head;
+    b[SC_BUF_V] = format == SC_KV_K8V4 ? cells * H * q4_head : b[SC_BUF_K];
+    b[SC_BUF_K_SCALE] = int8_keys ? cells * H * (D / 64) * 2 : 0;
+    b[SC_BUF_V_SCALE] = format == SC_KV_INT8 ? b[SC_BUF_K_SCALE] : 0;
+    const uint64_t pooled_rows = index && tokens > 0 ? uint64_t(tokens) / SC_IDX_BLOCK + 1 : 0;
+    b[SC_BUF_POOLED] = pooled_rows * uint64_t(g->idx_key_dim) * 4;
+    return "";
+}
+
+// Offsets of every blob in the image (kAbsent for an empty one), the GDN rows last; returns the total.
+uint64_t layers_layout(const Geo& o, const uint64_t (&b)[SC_N_BUF], std::vector<uint64_t>& off) {
+    off.assign(size_t(o.n_qsa) * SC_N_BUF + 1, kAbsent);
+    uint64_t at = 0;
+    for (int64_t j = 0; j < o.n_qsa; ++j)
+        for (int k = 0; k < SC_N_BUF; ++k)
+            if (b[k]) {
+                at = round_up(at, kBlobAlign);
+                off[size_t(j) * SC_N_BUF + k] = at;
+                at += b[k];
+            }
+    if (o.n_gdn > 0) {
+        at = round_up(at, kBlobAlign);
+        off.back() = at;
+        at += uint64_t(o.n_gdn) * o.gdn_row_bytes;
+    }
+    return round_up(at, kBlobAlign);
+}
+
+// A validated sc_slot_layers request: the blob sizes, and every buffer present where its blob is nonempty.
+int check_layers(const Geo& o, const sc_geometry* g, const sc_slot_layers* s, int64_t tokens, uint64_t (&b)[SC_N_BUF]) {
+    if (!s) return snapshot_fail("missing decode slot");
+    const std::string why = layer_blob_sizes(o, g, s->format, s->with_index != 0, tokens, b);
+    if (!why.empty()) return snapshot_fail(why.c_str());
+    if (s->max_cells < 0 || cells_of(o, tokens) > s->max_cells) return snapshot_fail("invalid K/V extent");
+    const uint64_t pooled_rows = b[SC_BUF_POOLED] / (uint64_t(g->idx_key_dim) * 4);
+    if (s->pooled_capacity < 0 || pooled_rows > uint64_t(s->pooled_capacity))
+        return snapshot_fail("invalid indexer extent");
+    for (int k = 0; k < SC_N_BUF; ++k) {
+        if (b[k] % 16) return fail(SC_ERANGE, "sc_handoff: a K/V blob is not a whole number of 16-byte chunks");
+        if (!b[k] || o.n_qsa == 0) continue;
+        if (!s->buf[k]) return snapshot_fail("missing K/V buffer for the slot's format");
+        for (int64_t j = 0; j < o.n_qsa; ++j)
+            if (!s->buf[k][j] || !aligned16(s->buf[k][j])) return snapshot_fail("missing or misaligned K/V buffer");
+    }
+    if (o.n_gdn > 0 && (!s->gdn_state || !aligned16(s->gdn_state))) return snapshot_fail("missing running-state buffer");
+    return SC_OK;
+}
 
 template <class F>
 int guarded(F&& f) {
@@ -640,6 +706,139 @@ int sc_plan_capture(const sc_geometry* g, const sc_decode_slot* src, int64_t tok
     return guarded([&] { return page_plan(g, image, image_bytes, tokens, src, false, out); });
 }
 
+int sc_layer_blob_bytes(const sc_geometry* g, int32_t format, int32_t with_index, int64_t tokens, uint64_t* bytes) {
+    return guarded([&] {
+        Geo o;
+        std::string why;
+        if (!geometry(g, o, why)) return snapshot_fail(why.c_str());
+        uint64_t b[SC_N_BUF];
+        why = layer_blob_sizes(o, g, format, with_index != 0, tokens, b);
+        if (!why.empty()) return snapshot_fail(why.c_str());
+        if (bytes) std::copy(b, b + SC_N_BUF, bytes);
+        return ok();
+    });
+}
+
+int sc_image_layout_layers(const sc_geometry* g, int32_t format, int32_t with_index, int64_t tokens, uint64_t* offsets,
+                           uint64_t* total_bytes) {
+    return guarded([&] {
+        Geo o;
+        std::string why;
+        if (!geometry(g, o, why)) return snapshot_fail(why.c_str());
+        uint64_t b[SC_N_BUF];
+        why = layer_blob_sizes(o, g, format, with_index != 0, tokens, b);
+        if (!why.empty()) return snapshot_fail(why.c_str());
+        std::vector<uint64_t> off;
+        const uint64_t total = layers_layout(o, b, off);
+        if (offsets) std::copy(off.begin(), off.end(), offsets);
+        if (total_bytes) *total_bytes = total;
+        return ok();
+    });
+}
+
+// One launch moving every blob of an sc_slot_layers slot between the slot (identity pools: a blob is a prefix of
+// its buffer) and a buffer laid out by `map` (or the standard image when map is NULL).
+static int layers_plan(const sc_geometry* g, void* buf, uint64_t buf_bytes, const sc_layers_map* map, int64_t tokens,
+                       const sc_slot_layers* slot, bool scatter, sc_plan** out) {
+    if (!out) return fail(SC_EINVAL, "sc_handoff: missing plan output");
+    Geo o;
+    std::string why;
+    if (!geometry(g, o, why)) return snapshot_fail(why.c_str());
+    uint64_t b[SC_N_BUF];
+    int rc = check_layers(o, g, slot, tokens, b);
+    if (rc) return rc;
+    if (!buf || !aligned16(buf)) return fail(SC_EINVAL, "sc_handoff: the blob buffer must be 16-byte aligned");
+    std::vector<uint64_t> std_off, zero;
+    const uint64_t* off = nullptr;
+    if (map) {
+        if (!map->off || map->n_zero < 0 || (map->n_zero && !map->zero))
+            return fail(SC_EINVAL, "sc_handoff: missing blob map");
+        off = map->off;
+        if (!scatter) zero.assign(map->zero, map->zero + 2 * map->n_zero);
+    } else {
+        const uint64_t total = layers_layout(o, b, std_off);
+        if (total > buf_bytes) return snapshot_fail("invalid K/V payload size");
+        off = std_off.data();
+        if (!scatter) {   // a capture clears the gaps of the standard image
+            uint64_t at = 0;
+            auto gap = [&](uint64_t end) {
+                if (end > at) { zero.push_back(at); zero.push_back(end - at); }
+            };
+            for (int64_t j = 0; j < o.n_qsa; ++j)
+                for (int k = 0; k < SC_N_BUF; ++k)
+                    if (b[k]) {
+                        gap(off[size_t(j) * SC_N_BUF + k]);
+                        at = off[size_t(j) * SC_N_BUF + k] + b[k];
+                    }
+            if (o.n_gdn > 0) {
+                gap(off[size_t(o.n_qsa) * SC_N_BUF]);
+                at = off[size_t(o.n_qsa) * SC_N_BUF] + uint64_t(o.n_gdn) * o.gdn_row_bytes;
+            }
+            gap(total);
+        }
+    }
+    struct Range { uint64_t at, n; };
+    std::vector<Range> used;
+    auto place = [&](uint64_t at, uint64_t n) {
+        if (at % 16 || at > buf_bytes || n > buf_bytes - at) return false;
+        if (n) used.push_back({at, n});
+        return true;
+    };
+    const uint64_t gdn_bytes = uint64_t(o.n_gdn) * o.gdn_row_bytes;
+    for (int64_t j = 0; j < o.n_qsa; ++j)
+        for (int k = 0; k < SC_N_BUF; ++k) {
+            const uint64_t at = off[size_t(j) * SC_N_BUF + k];
+            if (!b[k]) {
+                if (at != kAbsent) return snapshot_fail("a blob map places a blob the slot's format does not have");
+                continue;
+            }
+            if (!place(at, b[k])) return snapshot_fail("a K/V blob lies outside the buffer or off a 16-byte boundary");
+        }
+    const uint64_t gdn_at = off[size_t(o.n_qsa) * SC_N_BUF];
+    if (o.n_gdn > 0 && !place(gdn_at, gdn_bytes))
+        return snapshot_fail("the running-state blob lies outside the buffer or off a 16-byte boundary");
+    for (size_t z = 0; z < zero.size(); z += 2)
+        if (zero[z + 1] % 16 || !place(zero[z], zero[z + 1]))
+            return fail(SC_EINVAL, "sc_handoff: a zero range must be 16-byte aligned, whole chunks, inside the buffer");
+    std::sort(used.begin(), used.end(), [](const Range& x, const Range& y) { return x.at < y.at; });
+    for (size_t i = 1; i < used.size(); ++i)
+        if (used[i].at < used[i - 1].at + used[i - 1].n) return fail(SC_EINVAL, "sc_handoff: blobs overlap in the buffer");
+    uint8_t* base = static_cast<uint8_t*>(buf);
+    std::vector<sc::MoveRow> rows;
+    uint64_t moved = 0;
+    auto copy = [&](uint8_t* slot_side, uint64_t at, uint64_t n) {
+        sc::MoveRow r{};
+        r.kind = sc::kCopy;
+        r.src = scatter ? base + at : slot_side;
+        r.dst = scatter ? slot_side : base + at;
+        r.n = n / 16;
+        if (r.n) rows.push_back(r);
+        moved += n;
+    };
+    for (int64_t j = 0; j < o.n_qsa; ++j)
+        for (int k = 0; k < SC_N_BUF; ++k)
+            if (b[k]) copy(static_cast<uint8_t*>(slot->buf[k][j]), off[size_t(j) * SC_N_BUF + k], b[k]);
+    if (o.n_gdn > 0) copy(reinterpret_cast<uint8_t*>(slot->gdn_state), gdn_at, gdn_bytes);
+    for (size_t z = 0; z < zero.size(); z += 2) {
+        sc::MoveRow r{};
+        r.kind = sc::kZero;
+        r.dst = base + zero[z];
+        r.n = zero[z + 1] / 16;
+        if (r.n) rows.push_back(r);
+    }
+    return finish_plan(rows, o, moved, out);
+}
+
+int sc_plan_capture_layers(const sc_geometry* g, const sc_slot_layers* src, int64_t tokens, void* dst,
+                           uint64_t dst_bytes, const sc_layers_map* map, sc_plan** out) {
+    return guarded([&] { return layers_plan(g, dst, dst_bytes, map, tokens, src, false, out); });
+}
+
+int sc_plan_scatter_layers(const sc_geometry* g, const void* src, uint64_t src_bytes, const sc_layers_map* map,
+                           int64_t tokens, const sc_slot_layers* dst, sc_plan** out) {
+    return guarded([&] { return layers_plan(g, const_cast<void*>(src), src_bytes, map, tokens, dst, true, out); });
+}
+
 int sc_plan_launch(const sc_plan* plan, void* stream) {
     if (!plan) return fail(SC_EINVAL, "sc_handoff: missing plan");
     if (plan->batch) {
@@ -836,6 +1035,59 @@ static int dma_image(const sc_geometry* g, const sc_decode_slot* slot, int64_t t
         if (e != hipSuccess) return hip_fail(e, "event record");
     }
     return ok();
+}
+
+// Park / resume of an sc_slot_layers slot: one copy per blob between its buffers' prefixes and the pinned image.
+static int dma_layers(const sc_geometry* g, const sc_slot_layers* slot, int64_t tokens, uint8_t* host,
+                      uint64_t image_bytes, bool park, void* stream, void* done) {
+    Geo o;
+    std::string why;
+    if (!geometry(g, o, why)) return snapshot_fail(why.c_str());
+    uint64_t b[SC_N_BUF];
+    int rc = check_layers(o, g, slot, tokens, b);
+    if (rc) return rc;
+    std::vector<uint64_t> off;
+    const uint64_t total = layers_layout(o, b, off);
+    if (!host || image_bytes < total) return snapshot_fail("invalid K/V payload size");
+    struct Item { uint8_t* dev; uint64_t at, n; };
+    std::vector<Item> items;
+    for (int64_t j = 0; j < o.n_qsa; ++j)
+        for (int k = 0; k < SC_N_BUF; ++k)
+            if (b[k]) items.push_back({static_cast<uint8_t*>(slot->buf[k][j]), off[size_t(j) * SC_N_BUF + k], b[k]});
+    if (o.n_gdn > 0)
+        items.push_back({reinterpret_cast<uint8_t*>(slot->gdn_state), off.back(), uint64_t(o.n_gdn) * o.gdn_row_bytes});
+    if (park) {   // the gaps are never copied; clear them so the image is deterministic
+        uint64_t at = 0;
+        for (const Item& it : items) {
+            if (it.at > at) std::memset(host + at, 0, it.at - at);
+            at = it.at + it.n;
+        }
+        if (total > at) std::memset(host + at, 0, total - at);
+    }
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    for (const Item& it : items) {
+        const hipError_t e = park ? hipMemcpyAsync(host + it.at, it.dev, it.n, hipMemcpyDeviceToHost, s)
+                                  : hipMemcpyAsync(it.dev, host + it.at, it.n, hipMemcpyHostToDevice, s);
+        if (e != hipSuccess) return hip_fail(e, park ? "park copy" : "resume copy");
+    }
+    if (done) {
+        const hipError_t e = hipEventRecord(static_cast<hipEvent_t>(done), s);
+        if (e != hipSuccess) return hip_fail(e, "event record");
+    }
+    return ok();
+}
+
+int sc_park_layers_async(const sc_geometry* g, const sc_slot_layers* slot, int64_t tokens, void* host_image,
+                         uint64_t image_bytes, void* stream, void* done) {
+    return guarded([&] { return dma_layers(g, slot, tokens, static_cast<uint8_t*>(host_image), image_bytes, true, stream, done); });
+}
+
+int sc_resume_layers_async(const sc_geometry* g, const void* host_image, uint64_t image_bytes, int64_t tokens,
+                           const sc_slot_layers* slot, void* stream, void* done) {
+    return guarded([&] {
+        return dma_layers(g, slot, tokens, const_cast<uint8_t*>(static_cast<const uint8_t*>(host_image)), image_bytes,
+                          false, stream, done);
+    });
 }
 
 int sc_park_async(const sc_geometry* g, const sc_decode_slot* slot, int64_t tokens, void* host_image,

@@ -36,6 +36,9 @@ using u32x4 = __attribute__((ext_vector_type(4))) uint32_t;
 // the 128K handoff) than write-allocating it.
 using gu32x4 = __attribute__((address_space(1))) u32x4;
 __device__ __forceinline__ u32x4 ld16(const uint8_t* p) { return *(const gu32x4*) (p); }
+// A non-temporal load, for a packed source read exactly once (an image scattered into pages): measured 4-6% faster
+// on the 128K scatter; the carves' row reads gained nothing from it.
+__device__ __forceinline__ u32x4 ld16_stream(const uint8_t* p) { return __builtin_nontemporal_load((const gu32x4*) (p)); }
 __device__ __forceinline__ void st16(uint8_t* p, u32x4 v) { __builtin_nontemporal_store(v, (gu32x4*) (p)); }
 
 // Page tables are read through global loads.  Every tile issues all of its loads, table entries included, before
@@ -161,7 +164,7 @@ __device__ void tile_pages(const MoveRow& r, const MoveGeo& g, uint64_t local, b
 #pragma unroll
         for (int j = 0; j < kChunksPerThread; ++j) {
             q[j] = uint32_t(local * kTileChunks) + uint32_t(j * kThreads) + threadIdx.x;
-            if (q[j] < r.n) v[j] = ld16(r.src + uint64_t(q[j]) * 16u);
+            if (q[j] < r.n) v[j] = ld16_stream(r.src + uint64_t(q[j]) * 16u);
         }
 #pragma unroll
         for (int j = 0; j < kChunksPerThread; ++j)

@@ -88,6 +88,19 @@ class BlobMap(C.Structure):
                 ("zero", C.POINTER(C.c_uint64)), ("n_zero", C.c_int64)]
 
 
+SC_N_BUF = 5                     # K, V, K scales, V scales, indexer pooled rows (SC_BUF_* order)
+ABSENT = 0xFFFFFFFFFFFFFFFF      # the offset of an empty blob in sc_image_layout_layers
+
+
+class SlotLayers(C.Structure):
+    _fields_ = [("format", C.c_int32), ("with_index", C.c_int32), ("max_cells", C.c_int64),
+                ("pooled_capacity", C.c_int64), ("buf", C.POINTER(C.c_void_p) * SC_N_BUF), ("gdn_state", C.c_void_p)]
+
+
+class LayersMap(C.Structure):
+    _fields_ = [("off", C.POINTER(C.c_uint64)), ("zero", C.POINTER(C.c_uint64)), ("n_zero", C.c_int64)]
+
+
 class ImageBlob(C.Structure):
     _fields_ = [("kind", C.c_int32), ("layer", C.c_int32), ("offset", C.c_uint64), ("bytes", C.c_uint64)]
 
@@ -148,6 +161,14 @@ _SIGS = {
     "sc_plan_carve_quant": (C.c_int, [_GEO, C.POINTER(PrefillView), C.POINTER(QuantSlot), C.POINTER(_P)]),
     "sc_plan_capture_map": (C.c_int, [_GEO, C.POINTER(DecodeSlot), _I64, _P, _U64, C.POINTER(BlobMap), C.POINTER(_P)]),
     "sc_plan_scatter_map": (C.c_int, [_GEO, _P, _U64, C.POINTER(BlobMap), _I64, C.POINTER(DecodeSlot), C.POINTER(_P)]),
+    "sc_layer_blob_bytes": (C.c_int, [_GEO, C.c_int32, C.c_int32, _I64, C.POINTER(_U64)]),
+    "sc_image_layout_layers": (C.c_int, [_GEO, C.c_int32, C.c_int32, _I64, C.POINTER(_U64), C.POINTER(_U64)]),
+    "sc_plan_capture_layers": (C.c_int, [_GEO, C.POINTER(SlotLayers), _I64, _P, _U64, C.POINTER(LayersMap),
+                                         C.POINTER(_P)]),
+    "sc_plan_scatter_layers": (C.c_int, [_GEO, _P, _U64, C.POINTER(LayersMap), _I64, C.POINTER(SlotLayers),
+                                         C.POINTER(_P)]),
+    "sc_park_layers_async": (C.c_int, [_GEO, C.POINTER(SlotLayers), _I64, _P, _U64, _P, _P]),
+    "sc_resume_layers_async": (C.c_int, [_GEO, _P, _U64, _I64, C.POINTER(SlotLayers), _P, _P]),
     "sc_fnv1a64_workspace_bytes": (_U64, [_U64]),
     "sc_fnv1a64_async": (C.c_int, [_P, _U64, _U64, _P, _P, _U64, _P]),
     "sc_fnv1a64_device": (C.c_int, [_P, _U64, _U64, C.POINTER(_U64)]),
@@ -781,3 +802,126 @@ def plan_carve_quant(geo: Geometry, prefill: PrefillBuffers, slot: QuantPools, p
     h = C.c_void_p()
     check(lib.sc_plan_carve_quant(C.byref(geo), C.byref(view), C.byref(cs), C.byref(h)), "sc_plan_carve_quant")
     return Plan(h.value, (keep, slot._keep))
+
+
+# ---- slot images in every K/V format --------------------------------------------------------------------------------
+
+def layer_blob_bytes(geo: Geometry, fmt: int, with_index: bool, tokens: int) -> list[int]:
+    out = (_U64 * SC_N_BUF)()
+    check(lib.sc_layer_blob_bytes(C.byref(geo), fmt, int(with_index), tokens, out), "sc_layer_blob_bytes")
+    return [int(x) for x in out]
+
+
+def image_layout_layers(geo: Geometry, fmt: int, with_index: bool, tokens: int) -> tuple[list[int | None], int]:
+    """Offsets (five per QSA layer, then the GDN rows; None for an empty blob) and the total of the slot image."""
+    offs = (_U64 * (geo.n_qsa * SC_N_BUF + 1))()
+    total = _U64(0)
+    check(lib.sc_image_layout_layers(C.byref(geo), fmt, int(with_index), tokens, offs, C.byref(total)),
+          "sc_image_layout_layers")
+    return [None if int(x) == ABSENT else int(x) for x in offs], int(total.value)
+
+
+class LayerPools:
+    """One slot's per-layer buffers in any format (identity layout), sized for `max_cells` cells, plus the GDN rows:
+    the five SC_BUF_* buffers of each QSA layer (absent ones are None) and the indexer's pooled rows when with_index."""
+
+    def __init__(self, geo: Geometry, fmt: int, max_cells: int, with_index: bool, buffers=None, gdn=None):
+        self.geo, self.fmt, self.max_cells, self.with_index = geo, fmt, max_cells, with_index
+        cap = layer_blob_bytes(geo, fmt, True, max_cells)       # a full pool, pooled rows for max_cells tokens
+        self.pooled_capacity = (max_cells // 4 + 1) if with_index and max_cells > 0 else 0
+        self.capacity = [cap[k] if (k != 4 or with_index) else 0 for k in range(SC_N_BUF)]
+        if buffers is None:
+            buffers = [[DeviceBuffer(n, "uint8") for _ in range(geo.n_qsa)] if n else None for n in self.capacity]
+        self.bufs = buffers
+        if gdn is None and geo.n_gdn:
+            gdn = DeviceBuffer((geo.n_gdn, geo.gdn_row_floats), "float32")
+        self.gdn = gdn
+        self._keep = ()
+
+    @classmethod
+    def from_quant(cls, slot: "QuantPools", pooled=None) -> "LayerPools":
+        """The pools of a quantizing carve's slot (identity tables), with optional indexer pooled-row buffers."""
+        fmt = slot.fmt
+        bufs = [list(slot.k_codes), list(slot.v_codes), list(slot.k_scale) or None, list(slot.v_scale) or None,
+                list(pooled) if pooled else None]
+        return cls(slot.geo, fmt, slot.max_cells, bool(pooled), buffers=bufs, gdn=slot.gdn)
+
+    def c_struct(self) -> SlotLayers:
+        arrs = [(_ptrs([b.ptr for b in bl]) if bl else None) for bl in self.bufs]
+        self._keep = tuple(arrs)
+        st = SlotLayers(format=self.fmt, with_index=int(self.with_index), max_cells=self.max_cells,
+                        pooled_capacity=self.pooled_capacity,
+                        gdn_state=self.gdn.ptr if self.gdn is not None else None)
+        for k, a in enumerate(arrs):
+            st.buf[k] = C.cast(a, C.POINTER(C.c_void_p)) if a is not None else None
+        return st
+
+    def buffers(self) -> list:
+        out = [b for bl in self.bufs if bl for b in bl]
+        return out + ([self.gdn] if self.gdn is not None else [])
+
+    def randomize(self, seed: int) -> None:
+        """Seeded pseudo-random contents in every buffer (device generator; each buffer its own stream)."""
+        for i, b in enumerate(self.buffers()):
+            check(lib.sc_fill_uniform_f16(b.ptr, b.nbytes // 2, -4.0, 4.0, seed, 7000 + i, None), "fill")
+
+    def fill(self, value: int) -> None:
+        for b in self.buffers():
+            b.fill(value)
+
+    def host(self) -> dict:
+        import numpy as np
+        out = {}
+        for k, bl in enumerate(self.bufs):
+            if bl:
+                for j, b in enumerate(bl):
+                    out[(k, j)] = b.numpy().view(np.uint8).reshape(-1)
+        if self.gdn is not None:
+            out["gdn"] = self.gdn.numpy().view(np.uint8).reshape(-1)
+        return out
+
+    def free(self) -> None:
+        for b in self.buffers():
+            b.free()
+
+
+def _layers_map(offsets, zero) -> tuple:
+    if offsets is None:
+        return None, ()
+    off = (_U64 * len(offsets))(*[ABSENT if x is None else x for x in offsets])
+    z = (_U64 * max(len(zero or ()), 1))(*(zero or ()))
+    m = LayersMap(off=C.cast(off, C.POINTER(_U64)), zero=C.cast(z, C.POINTER(_U64)), n_zero=len(zero or ()) // 2)
+    return m, (off, z)
+
+
+def plan_capture_layers(geo: Geometry, pools: LayerPools, tokens: int, ptr: int, nbytes: int, offsets=None,
+                        zero=None) -> Plan:
+    cs = pools.c_struct()
+    m, keep = _layers_map(offsets, zero)
+    h = C.c_void_p()
+    check(lib.sc_plan_capture_layers(C.byref(geo), C.byref(cs), tokens, ptr, nbytes,
+                                     C.byref(m) if m is not None else None, C.byref(h)), "sc_plan_capture_layers")
+    return Plan(h.value, (pools._keep, keep))
+
+
+def plan_scatter_layers(geo: Geometry, ptr: int, nbytes: int, tokens: int, pools: LayerPools, offsets=None) -> Plan:
+    cs = pools.c_struct()
+    m, keep = _layers_map(offsets, None)
+    h = C.c_void_p()
+    check(lib.sc_plan_scatter_layers(C.byref(geo), ptr, nbytes, C.byref(m) if m is not None else None, tokens,
+                                     C.byref(cs), C.byref(h)), "sc_plan_scatter_layers")
+    return Plan(h.value, (pools._keep, keep))
+
+
+def park_layers_async(geo: Geometry, pools: LayerPools, tokens: int, host_ptr: int, host_bytes: int, stream=None,
+                      done=None) -> None:
+    cs = pools.c_struct()
+    check(lib.sc_park_layers_async(C.byref(geo), C.byref(cs), tokens, host_ptr, host_bytes, _stream(stream), done),
+          "sc_park_layers_async")
+
+
+def resume_layers_async(geo: Geometry, host_ptr: int, host_bytes: int, tokens: int, pools: LayerPools, stream=None,
+                        done=None) -> None:
+    cs = pools.c_struct()
+    check(lib.sc_resume_layers_async(C.byref(geo), host_ptr, host_bytes, tokens, C.byref(cs), _stream(stream), done),
+          "sc_resume_layers_async")
