@@ -51,6 +51,12 @@ const char* sc_wire_last_error(void);
  * GDN rows.  Replaces conversation_wire_plan (src/core/conversation_wire.cpp:988-1004) for slot-resident state. */
 int sc_wire_encoder_create(const sc_geometry* g, const sc_decode_slot* slot, int64_t tokens, const sc_wire_live* live,
                            uint64_t geom_hash, uint64_t pack_hash, sc_wire_encoder** out);
+/* The same for a slot in any K/V format (sc_slot_layers, include/sc_handoff.h): its layers become K/V records of
+ * slot->format carrying data, int8 scales and, with slot->with_index, the indexer's pooled rows, all gathered from the
+ * slot's identity pools by one launch (conversation_kv_save's five buffers, src/core/conversation_snapshot.cpp:69-78). */
+int sc_wire_encoder_create_layers(const sc_geometry* g, const sc_slot_layers* slot, int64_t tokens,
+                                  const sc_wire_live* live, uint64_t geom_hash, uint64_t pack_hash,
+                                  sc_wire_encoder** out);
 /* The payload's total size (WirePlan::total_bytes) and where its blob pool starts. */
 uint64_t sc_wire_encoder_bytes(const sc_wire_encoder* e);
 uint64_t sc_wire_encoder_pool_offset(const sc_wire_encoder* e);
@@ -70,6 +76,11 @@ int sc_wire_encoder_destroy(sc_wire_encoder* e);
 int sc_wire_decoder_open(const void* payload, uint64_t bytes, const sc_geometry* g, const sc_decode_slot* slot,
                          const int64_t* geometry, uint64_t geom_hash, uint64_t pack_hash, int32_t check_identity,
                          uint64_t payload_hash, int32_t check_hash, sc_wire_decoder** out);
+/* The same for a slot in any K/V format: the first K/V records must be the slot's layers in slot->format, with the
+ * indexer's rows exactly when slot->with_index. */
+int sc_wire_decoder_open_layers(const void* payload, uint64_t bytes, const sc_geometry* g, const sc_slot_layers* slot,
+                                const int64_t* geometry, uint64_t geom_hash, uint64_t pack_hash, int32_t check_identity,
+                                uint64_t payload_hash, int32_t check_hash, sc_wire_decoder** out);
 /* Tokens the payload carries (its live token count). */
 int64_t sc_wire_decoder_tokens(const sc_wire_decoder* d);
 /* Verifies the payload hash on the device (when asked), then scatters the K/V and GDN rows into the slot in one launch

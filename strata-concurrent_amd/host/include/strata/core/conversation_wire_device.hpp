@@ -28,9 +28,14 @@
 #include <array>
 #include <cstdint>
 #include <string>
+#include <utility>
 #include <vector>
 
 namespace strata::core {
+
+namespace detail {
+struct WireBlobAt;   // one pool entry of a payload (the codec's internals)
+}
 
 /// The host side of a conversation whose K/V and GDN rows live in a decode slot.
 struct WireDeviceConversation {
@@ -53,6 +58,11 @@ public:
     /// Lays out the payload of `conv` carrying the slot's state for `tokens` tokens (== conv.live.ids.size()).
     bool plan(const sc_geometry& g, const sc_decode_slot& slot, int64_t tokens, const WireDeviceConversation& conv,
               const WireIdentity& identity, std::string& error);
+    /// The same for a slot in any K/V format (sc_slot_layers: int8, q4_0, K8V4 or f16, with the indexer's pooled rows
+    /// when slot.with_index): its layers become K/V records of slot.format whose data, scale and pooled-row blobs are
+    /// gathered from the slot's identity pools.
+    bool plan(const sc_geometry& g, const sc_slot_layers& slot, int64_t tokens, const WireDeviceConversation& conv,
+              const WireIdentity& identity, std::string& error);
     const WirePlan& layout() const { return plan_; }
     uint64_t bytes() const { return plan_.total_bytes; }
     /// Enqueues the whole encode on `stream` into `payload` (16-byte aligned device memory of at least bytes()).  When
@@ -64,9 +74,16 @@ public:
 
 private:
     void release();
+    bool stage(const SavedConversation& img, const std::vector<std::pair<const void*, uint64_t>>& sizes,
+               const std::vector<const void*>& device, const WireIdentity& identity,
+               std::vector<detail::WireBlobAt>& pool, std::string& error);
 
     sc_geometry g_{};
     sc_decode_slot slot_{};
+    bool layered_ = false;                             // an sc_slot_layers slot (lay_off_) rather than f16 pools
+    sc_slot_layers layers_{};
+    std::array<std::vector<void*>, SC_N_BUF> layer_bufs_;
+    std::vector<uint64_t> lay_off_;                    // sc_layers_map offsets of the slot's blobs in the payload
     int64_t tokens_ = 0;
     WirePlan plan_{};
     std::vector<uint64_t> k_off_, v_off_, zero_;
@@ -96,6 +113,10 @@ public:
     /// scatter.  Nothing is written anywhere.
     bool open(const void* payload, uint64_t bytes, const sc_geometry& g, const sc_decode_slot& slot,
               const WireExpect& expect, std::string& error);
+    /// The same for a slot in any K/V format: the first K/V records must be the slot's layers in its format, with the
+    /// indexer's rows exactly when slot.with_index.
+    bool open(const void* payload, uint64_t bytes, const sc_geometry& g, const sc_slot_layers& slot,
+              const WireExpect& expect, std::string& error);
     int64_t tokens() const { return tokens_; }
     const WireDecoded& info() const { return info_; }
     /// Verifies the payload hash on the device (when `expect` asked for it), then scatters the K/V and GDN rows into the
@@ -105,6 +126,11 @@ public:
 
 private:
     void release();
+    bool read_head(const void* payload, uint64_t bytes, const WireExpect& expect, std::vector<detail::WireBlobAt>& blobs,
+                   std::string& error);
+    bool finish_open(const void* payload, uint64_t bytes, const WireExpect& expect,
+                     const std::vector<detail::WireBlobAt>& blobs, const std::vector<const void*>& device,
+                     std::string& error);
 
     const uint8_t* payload_ = nullptr;
     uint64_t bytes_ = 0;

@@ -86,25 +86,75 @@ void WireDeviceEncoder::release() {
     uploads_.clear();
 }
 
-bool WireDeviceEncoder::plan(const sc_geometry& g, const sc_decode_slot& slot, int64_t tokens,
-                             const WireDeviceConversation& conv, const WireIdentity& identity, std::string& error) {
-    release();
-    plan_ = WirePlan{};
-    SlotShape s;
-    if (!slot_shape(g, tokens, s, error)) return false;
-    if (int64_t(conv.live.ids.size()) != tokens)
-        return refuse(error, "the live checkpoint's id count is not the slot's token count");
-    if (!conv.live.gdn.empty()) return refuse(error, "the live checkpoint's gdn blob is the slot's GDN rows; leave it empty");
-    // The image as the wire sees it: the slot's layers as f16 K/V records whose buffers are sized, not held.
-    SavedConversation img;
+// The image the wire sees for a slot: geometry and flags from `conv`, `n_qsa` K/V records first (sized, not held), the
+// trailing host records after them, then the live checkpoint and the retained checkpoints.
+static void slot_image(const WireDeviceConversation& conv, int64_t n_qsa, SavedConversation& img) {
     img.geometry = conv.geometry;
     img.layer_lo = conv.layer_lo;
     img.layer_hi = conv.layer_hi;
     img.cvec = conv.cvec;
     // the K/V vector gets its final length before any buffer's address is taken
-    img.kv.resize(size_t(s.n_qsa));
+    img.kv.resize(size_t(n_qsa));
     img.kv.insert(img.kv.end(), conv.trailing_kv.begin(), conv.trailing_kv.end());
+    img.live = conv.live;
+    img.checkpoints = conv.checkpoints;
+}
+
+static bool check_conversation(const WireDeviceConversation& conv, int64_t tokens, std::string& error) {
+    if (int64_t(conv.live.ids.size()) != tokens)
+        return refuse(error, "the live checkpoint's id count is not the slot's token count");
+    if (!conv.live.gdn.empty()) return refuse(error, "the live checkpoint's gdn blob is the slot's GDN rows; leave it empty");
+    return true;
+}
+
+bool WireDeviceEncoder::stage(const SavedConversation& img, const std::vector<std::pair<const void*, uint64_t>>& sizes,
+                              const std::vector<const void*>& device, const WireIdentity& identity,
+                              std::vector<detail::WireBlobAt>& pool, std::string& error) {
+    std::vector<uint8_t> head;
+    if (!detail::wire_head(img, identity, sizes, head, pool, plan_, error)) return false;
+    // Device blobs go to the capture plan; a zero range closes each one up to the next 64-byte boundary.  Host blobs
+    // are staged with their own zero padding and copied in.
+    zero_.clear();
+    for (const void* who : device) {
+        const detail::WireBlobAt* e = find(pool, who);
+        if (!e) return refuse(error, "internal: a slot blob is missing from the pool");
+        const uint64_t end = e->offset + e->bytes, padded = up64(end);
+        if (padded > end) { zero_.push_back(end); zero_.push_back(padded - end); }
+    }
+    std::vector<const detail::WireBlobAt*> host;
+    for (const auto& e : pool)
+        if (std::find(device.begin(), device.end(), e.who) == device.end()) host.push_back(&e);
+    staged_bytes_ = up64(head.size());
+    for (const auto* e : host) staged_bytes_ += up64(e->bytes);
+    int rc = sc_host_alloc(reinterpret_cast<void**>(&staged_), staged_bytes_ ? staged_bytes_ : 64);
+    if (rc == SC_OK) rc = sc_host_alloc(reinterpret_cast<void**>(&hash_host_), 64);
+    if (!abi(rc, error, "pinned staging")) return false;
+    std::memset(staged_, 0, staged_bytes_);
+    std::memcpy(staged_, head.data(), head.size());
+    uploads_.push_back({0, head.size(), 0});
+    uint64_t at = up64(head.size());
+    for (const auto* e : host) {
+        if (!stage_host_blob(img, e->who, staged_ + at, e->bytes)) return refuse(error, "internal: a host blob of the pool was not found");
+        uploads_.push_back({e->offset, up64(e->bytes), at});
+        at += up64(e->bytes);
+    }
+    hash_ws_bytes_ = sc_fnv1a64_workspace_bytes(plan_.total_bytes);
+    rc = sc_device_alloc(&hash_ws_, hash_ws_bytes_);
+    if (rc == SC_OK) rc = sc_device_alloc(reinterpret_cast<void**>(&hash_dev_), 64);
+    return abi(rc, error, "hash workspace");
+}
+
+bool WireDeviceEncoder::plan(const sc_geometry& g, const sc_decode_slot& slot, int64_t tokens,
+                             const WireDeviceConversation& conv, const WireIdentity& identity, std::string& error) {
+    release();
+    plan_ = WirePlan{};
+    SlotShape s;
+    if (!slot_shape(g, tokens, s, error) || !check_conversation(conv, tokens, error)) return false;
+    // the slot's layers as f16 K/V records whose buffers are sized, not held
+    SavedConversation img;
+    slot_image(conv, s.n_qsa, img);
     detail::WireSizes sizes;
+    std::vector<const void*> device;
     for (int64_t j = 0; j < s.n_qsa; ++j) {
         ConversationKv& k = img.kv[size_t(j)];
         k.format = 0;
@@ -116,64 +166,78 @@ bool WireDeviceEncoder::plan(const sc_geometry& g, const sc_decode_slot& slot, i
         k.idx_dim = conv.idx_dim;
         sizes.push_back({&k.k, s.kv_bytes});
         sizes.push_back({&k.v, s.kv_bytes});
+        if (s.kv_bytes) { device.push_back(&k.k); device.push_back(&k.v); }
     }
-    img.live = conv.live;
-    img.checkpoints = conv.checkpoints;
-    if (s.n_gdn > 0) sizes.push_back({&img.live.gdn, s.gdn_bytes});
-    std::vector<uint8_t> head;
+    if (s.n_gdn > 0) {
+        sizes.push_back({&img.live.gdn, s.gdn_bytes});
+        device.push_back(&img.live.gdn);
+    }
     std::vector<detail::WireBlobAt> pool;
-    if (!detail::wire_head(img, identity, sizes, head, pool, plan_, error)) return false;
-
-    // Device blobs go to the capture plan; a zero range closes each one up to the next 64-byte boundary.  Host blobs
-    // are staged with their own zero padding and copied in.
+    if (!stage(img, sizes, device, identity, pool, error)) { release(); return false; }
     k_off_.assign(size_t(s.n_qsa), 0);
     v_off_.assign(size_t(s.n_qsa), 0);
-    zero_.clear();
-    gdn_off_ = 0;
-    auto device_blob = [&](const void* who, uint64_t& off) {
-        const detail::WireBlobAt* e = find(pool, who);
-        if (!e) return false;
-        off = e->offset;
-        const uint64_t end = e->offset + e->bytes, padded = up64(end);
-        if (padded > end) { zero_.push_back(end); zero_.push_back(padded - end); }
-        return true;
-    };
-    for (int64_t j = 0; j < s.n_qsa; ++j)
-        if (s.kv_bytes && (!device_blob(&img.kv[size_t(j)].k, k_off_[size_t(j)]) ||
-                           !device_blob(&img.kv[size_t(j)].v, v_off_[size_t(j)])))
-            return refuse(error, "internal: a slot K/V blob is missing from the pool");
-    if (s.n_gdn > 0 && !device_blob(&img.live.gdn, gdn_off_))
-        return refuse(error, "internal: the GDN blob is missing from the pool");
-    std::vector<const detail::WireBlobAt*> host;
-    for (const auto& e : pool) {
-        bool on_device = e.who == &img.live.gdn;
-        for (int64_t j = 0; j < s.n_qsa && !on_device; ++j)
-            on_device = e.who == &img.kv[size_t(j)].k || e.who == &img.kv[size_t(j)].v;
-        if (!on_device) host.push_back(&e);
+    for (int64_t j = 0; j < s.n_qsa && s.kv_bytes; ++j) {
+        k_off_[size_t(j)] = find(pool, &img.kv[size_t(j)].k)->offset;
+        v_off_[size_t(j)] = find(pool, &img.kv[size_t(j)].v)->offset;
     }
-    staged_bytes_ = up64(head.size());
-    for (const auto* e : host) staged_bytes_ += up64(e->bytes);
-    int rc = sc_host_alloc(reinterpret_cast<void**>(&staged_), staged_bytes_ ? staged_bytes_ : 64);
-    if (rc == SC_OK) rc = sc_host_alloc(reinterpret_cast<void**>(&hash_host_), 64);
-    if (!abi(rc, error, "pinned staging")) { release(); return false; }
-    std::memset(staged_, 0, staged_bytes_);
-    std::memcpy(staged_, head.data(), head.size());
-    uploads_.push_back({0, head.size(), 0});
-    uint64_t at = up64(head.size());
-    for (const auto* e : host) {
-        if (!stage_host_blob(img, e->who, staged_ + at, e->bytes)) {
-            release();
-            return refuse(error, "internal: a host blob of the pool was not found");
-        }
-        uploads_.push_back({e->offset, up64(e->bytes), at});
-        at += up64(e->bytes);
-    }
-    hash_ws_bytes_ = sc_fnv1a64_workspace_bytes(plan_.total_bytes);
-    rc = sc_device_alloc(&hash_ws_, hash_ws_bytes_);
-    if (rc == SC_OK) rc = sc_device_alloc(reinterpret_cast<void**>(&hash_dev_), 64);
-    if (!abi(rc, error, "hash workspace")) { release(); return false; }
+    gdn_off_ = s.n_gdn > 0 ? find(pool, &img.live.gdn)->offset : 0;
+    layered_ = false;
     g_ = g;
     slot_ = slot;
+    tokens_ = tokens;
+    return true;
+}
+
+bool WireDeviceEncoder::plan(const sc_geometry& g, const sc_slot_layers& slot, int64_t tokens,
+                             const WireDeviceConversation& conv, const WireIdentity& identity, std::string& error) {
+    release();
+    plan_ = WirePlan{};
+    SlotShape s;
+    if (!slot_shape(g, tokens, s, error) || !check_conversation(conv, tokens, error)) return false;
+    uint64_t b[SC_N_BUF];
+    if (!abi(sc_layer_blob_bytes(&g, slot.format, slot.with_index, tokens, b), error, "K/V layout")) return false;
+    // the slot's layers as K/V records of its format (data, scales, indexer rows) whose buffers are sized, not held
+    SavedConversation img;
+    slot_image(conv, s.n_qsa, img);
+    detail::WireSizes sizes;
+    std::vector<const void*> device;
+    for (int64_t j = 0; j < s.n_qsa; ++j) {
+        ConversationKv& k = img.kv[size_t(j)];
+        k.format = slot.format;
+        k.cells = s.cells;
+        k.heads = g.n_head_kv;
+        k.head_dim = g.head_dim;
+        k.page_size = g.page_size;
+        k.pooled_rows = int64_t(b[SC_BUF_POOLED] / (uint64_t(g.idx_key_dim) * 4));
+        k.idx_dim = conv.idx_dim;
+        const ConversationBuffer* bufs[SC_N_BUF] = {&k.k, &k.v, &k.k_scale, &k.v_scale, &k.pooled};
+        for (int x = 0; x < SC_N_BUF; ++x) {
+            sizes.push_back({bufs[x], b[x]});
+            if (b[x]) device.push_back(bufs[x]);
+        }
+    }
+    if (s.n_gdn > 0) {
+        sizes.push_back({&img.live.gdn, s.gdn_bytes});
+        device.push_back(&img.live.gdn);
+    }
+    std::vector<detail::WireBlobAt> pool;
+    if (!stage(img, sizes, device, identity, pool, error)) { release(); return false; }
+    lay_off_.assign(size_t(s.n_qsa) * SC_N_BUF + 1, ~uint64_t(0));
+    for (int64_t j = 0; j < s.n_qsa; ++j) {
+        const ConversationKv& k = img.kv[size_t(j)];
+        const ConversationBuffer* bufs[SC_N_BUF] = {&k.k, &k.v, &k.k_scale, &k.v_scale, &k.pooled};
+        for (int x = 0; x < SC_N_BUF; ++x)
+            if (b[x]) lay_off_[size_t(j) * SC_N_BUF + size_t(x)] = find(pool, bufs[x])->offset;
+    }
+    if (s.n_gdn > 0) lay_off_.back() = find(pool, &img.live.gdn)->offset;
+    // own copies of the slot's pointer arrays: the caller's may not outlive the encoder
+    layers_ = slot;
+    for (int x = 0; x < SC_N_BUF; ++x) {
+        layer_bufs_[size_t(x)].assign(slot.buf[x] ? slot.buf[x] : nullptr, slot.buf[x] ? slot.buf[x] + s.n_qsa : nullptr);
+        layers_.buf[x] = slot.buf[x] ? layer_bufs_[size_t(x)].data() : nullptr;
+    }
+    layered_ = true;
+    g_ = g;
     tokens_ = tokens;
     return true;
 }
@@ -186,14 +250,20 @@ bool WireDeviceEncoder::encode(void* payload, uint64_t capacity, void* stream, s
     if (capture_target_ != payload) {
         if (capture_) sc_plan_destroy(capture_);
         capture_ = nullptr;
-        sc_blob_map map{};
-        map.k_off = k_off_.data();
-        map.v_off = v_off_.data();
-        map.gdn_off = gdn_off_;
-        map.zero = zero_.data();
-        map.n_zero = int64_t(zero_.size() / 2);
-        if (!abi(sc_plan_capture_map(&g_, &slot_, tokens_, payload, capacity, &map, &capture_), error, "capture plan"))
-            return false;
+        int rc;
+        if (layered_) {
+            sc_layers_map map{lay_off_.data(), zero_.data(), int64_t(zero_.size() / 2)};
+            rc = sc_plan_capture_layers(&g_, &layers_, tokens_, payload, capacity, &map, &capture_);
+        } else {
+            sc_blob_map map{};
+            map.k_off = k_off_.data();
+            map.v_off = v_off_.data();
+            map.gdn_off = gdn_off_;
+            map.zero = zero_.data();
+            map.n_zero = int64_t(zero_.size() / 2);
+            rc = sc_plan_capture_map(&g_, &slot_, tokens_, payload, capacity, &map, &capture_);
+        }
+        if (!abi(rc, error, "capture plan")) return false;
         capture_target_ = payload;
     }
     uint8_t* p = static_cast<uint8_t*>(payload);
@@ -230,10 +300,11 @@ void WireDeviceDecoder::release() {
     hash_dev_ = nullptr;
     hash_host_ = nullptr;
     downloads_.clear();
+    head_image_ = SavedConversation{};
 }
 
-bool WireDeviceDecoder::open(const void* payload, uint64_t bytes, const sc_geometry& g, const sc_decode_slot& slot,
-                             const WireExpect& expect, std::string& error) {
+bool WireDeviceDecoder::read_head(const void* payload, uint64_t bytes, const WireExpect& expect,
+                                  std::vector<detail::WireBlobAt>& blobs, std::string& error) {
     release();
     if (!payload || bytes < kWireHeaderRecordBytes) return refuse(error, "the payload is shorter than the header record");
     // the payload may still be arriving on another stream: everything enqueued before this call completes first
@@ -252,16 +323,46 @@ bool WireDeviceDecoder::open(const void* payload, uint64_t bytes, const sc_geome
     // every check of the host decoder, against the real buffer size
     WireExpect bounded = expect;
     if (!bounded.max_payload_bytes || bounded.max_payload_bytes > bytes) bounded.max_payload_bytes = bytes;
-    std::vector<detail::WireBlobAt> blobs;
     head_image_ = SavedConversation{};
     if (!detail::wire_locate(head.data(), head.size(), head_image_, info_, bounded, blobs, error)) return false;
     if (info_.n_stage_parts) return refuse(error, "a layer-split image cannot be mounted on the device path");
-    SlotShape s;
     tokens_ = info_.live_tokens;
+    return true;
+}
+
+bool WireDeviceDecoder::finish_open(const void* payload, uint64_t bytes, const WireExpect& expect,
+                                    const std::vector<detail::WireBlobAt>& blobs, const std::vector<const void*>& device,
+                                    std::string& error) {
+    for (const auto& b : blobs) {
+        if (std::find(device.begin(), device.end(), b.who) != device.end()) continue;
+        bool buffer = false;
+        for (const ConversationKv& k : head_image_.kv)
+            for (const ConversationBuffer* x : {&k.k, &k.v, &k.k_scale, &k.v_scale, &k.pooled}) buffer |= x == b.who;
+        downloads_.push_back({const_cast<void*>(b.who), buffer, b.offset, b.bytes});
+    }
+    if (expect.check_payload_hash) {
+        hash_ws_bytes_ = sc_fnv1a64_workspace_bytes(info_.bytes);
+        int rc = sc_device_alloc(&hash_ws_, hash_ws_bytes_);
+        if (rc == SC_OK) rc = sc_device_alloc(reinterpret_cast<void**>(&hash_dev_), 64);
+        if (rc == SC_OK) rc = sc_host_alloc(reinterpret_cast<void**>(&hash_host_), 64);
+        if (!abi(rc, error, "hash workspace")) { release(); return false; }
+    }
+    payload_ = static_cast<const uint8_t*>(payload);
+    bytes_ = bytes;
+    expect_ = expect;
+    return true;
+}
+
+bool WireDeviceDecoder::open(const void* payload, uint64_t bytes, const sc_geometry& g, const sc_decode_slot& slot,
+                             const WireExpect& expect, std::string& error) {
+    std::vector<detail::WireBlobAt> blobs;
+    if (!read_head(payload, bytes, expect, blobs, error)) return false;
+    SlotShape s;
     if (!slot_shape(g, tokens_, s, error)) return false;
     if (int64_t(head_image_.kv.size()) < s.n_qsa)
         return refuse(error, "the payload carries fewer K/V records than the slot has layers");
     std::vector<uint64_t> k_off(size_t(s.n_qsa)), v_off(size_t(s.n_qsa));
+    std::vector<const void*> device;
     for (int64_t j = 0; j < s.n_qsa; ++j) {
         const ConversationKv& k = head_image_.kv[size_t(j)];
         if (k.format != 0 || k.cells != s.cells || k.heads != g.n_head_kv || k.head_dim != g.head_dim ||
@@ -276,21 +377,13 @@ bool WireDeviceDecoder::open(const void* payload, uint64_t bytes, const sc_geome
             return refuse(error, "K/V record " + std::to_string(j) + " carries scales or indexer rows");
         k_off[size_t(j)] = kb ? kb->offset : 0;
         v_off[size_t(j)] = vb ? vb->offset : 0;
+        device.push_back(&k.k);
+        device.push_back(&k.v);
     }
     const detail::WireBlobAt* gb = find(blobs, &head_image_.live.gdn);
     if (s.n_gdn > 0 && (!gb || gb->bytes != s.gdn_bytes))
         return refuse(error, "the live checkpoint does not carry the slot's GDN rows");
-    for (const auto& b : blobs) {
-        if (b.who == &head_image_.live.gdn) continue;
-        bool slot_blob = false;
-        for (int64_t j = 0; j < s.n_qsa && !slot_blob; ++j)
-            slot_blob = b.who == &head_image_.kv[size_t(j)].k || b.who == &head_image_.kv[size_t(j)].v;
-        if (slot_blob) continue;
-        bool buffer = false;
-        for (const ConversationKv& k : head_image_.kv)
-            for (const ConversationBuffer* x : {&k.k, &k.v, &k.k_scale, &k.v_scale, &k.pooled}) buffer |= x == b.who;
-        downloads_.push_back({const_cast<void*>(b.who), buffer, b.offset, b.bytes});
-    }
+    device.push_back(&head_image_.live.gdn);
     sc_blob_map map{};
     map.k_off = k_off.data();
     map.v_off = v_off.data();
@@ -299,17 +392,50 @@ bool WireDeviceDecoder::open(const void* payload, uint64_t bytes, const sc_geome
         release();
         return false;
     }
-    if (expect.check_payload_hash) {
-        hash_ws_bytes_ = sc_fnv1a64_workspace_bytes(info_.bytes);
-        int rc = sc_device_alloc(&hash_ws_, hash_ws_bytes_);
-        if (rc == SC_OK) rc = sc_device_alloc(reinterpret_cast<void**>(&hash_dev_), 64);
-        if (rc == SC_OK) rc = sc_host_alloc(reinterpret_cast<void**>(&hash_host_), 64);
-        if (!abi(rc, error, "hash workspace")) { release(); return false; }
+    return finish_open(payload, bytes, expect, blobs, device, error);
+}
+
+bool WireDeviceDecoder::open(const void* payload, uint64_t bytes, const sc_geometry& g, const sc_slot_layers& slot,
+                             const WireExpect& expect, std::string& error) {
+    std::vector<detail::WireBlobAt> blobs;
+    if (!read_head(payload, bytes, expect, blobs, error)) return false;
+    SlotShape s;
+    if (!slot_shape(g, tokens_, s, error)) return false;
+    uint64_t b[SC_N_BUF];
+    if (!abi(sc_layer_blob_bytes(&g, slot.format, slot.with_index, tokens_, b), error, "K/V layout")) return false;
+    if (int64_t(head_image_.kv.size()) < s.n_qsa)
+        return refuse(error, "the payload carries fewer K/V records than the slot has layers");
+    const int64_t pooled_rows = int64_t(b[SC_BUF_POOLED] / (uint64_t(g.idx_key_dim) * 4));
+    std::vector<uint64_t> off(size_t(s.n_qsa) * SC_N_BUF + 1, ~uint64_t(0));
+    std::vector<const void*> device;
+    for (int64_t j = 0; j < s.n_qsa; ++j) {
+        const ConversationKv& k = head_image_.kv[size_t(j)];
+        if (k.format != slot.format || k.cells != s.cells || k.heads != g.n_head_kv || k.head_dim != g.head_dim ||
+            k.page_size != g.page_size || k.pooled_rows != pooled_rows)
+            return refuse(error, "K/V record " + std::to_string(j) + " is not the slot's layer (format " +
+                                     std::to_string(slot.format) + ", " + std::to_string(tokens_) + " tokens)");
+        const ConversationBuffer* bufs[SC_N_BUF] = {&k.k, &k.v, &k.k_scale, &k.v_scale, &k.pooled};
+        for (int x = 0; x < SC_N_BUF; ++x) {
+            const detail::WireBlobAt* e = find(blobs, bufs[x]);
+            if (b[x] ? (!e || e->bytes != b[x]) : e != nullptr)
+                return refuse(error, "K/V record " + std::to_string(j) + " does not carry the slot format's blobs");
+            if (e) {
+                off[size_t(j) * SC_N_BUF + size_t(x)] = e->offset;
+                device.push_back(bufs[x]);
+            }
+        }
     }
-    payload_ = static_cast<const uint8_t*>(payload);
-    bytes_ = bytes;
-    expect_ = expect;
-    return true;
+    const detail::WireBlobAt* gb = find(blobs, &head_image_.live.gdn);
+    if (s.n_gdn > 0 && (!gb || gb->bytes != s.gdn_bytes))
+        return refuse(error, "the live checkpoint does not carry the slot's GDN rows");
+    if (gb) off.back() = gb->offset;
+    device.push_back(&head_image_.live.gdn);
+    sc_layers_map map{off.data(), nullptr, 0};
+    if (!abi(sc_plan_scatter_layers(&g, payload, bytes, &map, tokens_, &slot, &scatter_), error, "scatter plan")) {
+        release();
+        return false;
+    }
+    return finish_open(payload, bytes, expect, blobs, device, error);
 }
 
 bool WireDeviceDecoder::restore(void* stream, SavedConversation& image, std::string& error) {

@@ -47,8 +47,10 @@ extern "C" {
 
 const char* sc_wire_last_error(void) { return g_error.c_str(); }
 
-int sc_wire_encoder_create(const sc_geometry* g, const sc_decode_slot* slot, int64_t tokens, const sc_wire_live* live,
-                           uint64_t geom_hash, uint64_t pack_hash, sc_wire_encoder** out) {
+extern "C++" {
+template <class Slot>
+static int encoder_create(const sc_geometry* g, const Slot* slot, int64_t tokens, const sc_wire_live* live,
+                          uint64_t geom_hash, uint64_t pack_hash, sc_wire_encoder** out) {
     return guarded([&] {
         if (!g || !slot || !live || !out) return failed(SC_EINVAL, "conversation wire: missing argument");
         if (live->n_ids < 0 || live->n_imgs < 0 || (live->n_ids && !live->ids) ||
@@ -79,6 +81,18 @@ int sc_wire_encoder_create(const sc_geometry* g, const sc_decode_slot* slot, int
         return done();
     });
 }
+}  // extern "C++"
+
+int sc_wire_encoder_create(const sc_geometry* g, const sc_decode_slot* slot, int64_t tokens, const sc_wire_live* live,
+                           uint64_t geom_hash, uint64_t pack_hash, sc_wire_encoder** out) {
+    return encoder_create(g, slot, tokens, live, geom_hash, pack_hash, out);
+}
+
+int sc_wire_encoder_create_layers(const sc_geometry* g, const sc_slot_layers* slot, int64_t tokens,
+                                  const sc_wire_live* live, uint64_t geom_hash, uint64_t pack_hash,
+                                  sc_wire_encoder** out) {
+    return encoder_create(g, slot, tokens, live, geom_hash, pack_hash, out);
+}
 
 uint64_t sc_wire_encoder_bytes(const sc_wire_encoder* e) { return e ? e->enc.bytes() : 0; }
 uint64_t sc_wire_encoder_pool_offset(const sc_wire_encoder* e) { return e ? e->enc.layout().blob_pool_off : 0; }
@@ -104,9 +118,11 @@ int sc_wire_encoder_destroy(sc_wire_encoder* e) {
     return done();
 }
 
-int sc_wire_decoder_open(const void* payload, uint64_t bytes, const sc_geometry* g, const sc_decode_slot* slot,
-                         const int64_t* geometry, uint64_t geom_hash, uint64_t pack_hash, int32_t check_identity,
-                         uint64_t payload_hash, int32_t check_hash, sc_wire_decoder** out) {
+extern "C++" {
+template <class Slot>
+static int decoder_open(const void* payload, uint64_t bytes, const sc_geometry* g, const Slot* slot,
+                        const int64_t* geometry, uint64_t geom_hash, uint64_t pack_hash, int32_t check_identity,
+                        uint64_t payload_hash, int32_t check_hash, sc_wire_decoder** out) {
     return guarded([&] {
         if (!g || !slot || !out) return failed(SC_EINVAL, "conversation wire: missing argument");
         WireExpect expect;
@@ -129,6 +145,21 @@ int sc_wire_decoder_open(const void* payload, uint64_t bytes, const sc_geometry*
         *out = d;
         return done();
     });
+}
+}  // extern "C++"
+
+int sc_wire_decoder_open(const void* payload, uint64_t bytes, const sc_geometry* g, const sc_decode_slot* slot,
+                         const int64_t* geometry, uint64_t geom_hash, uint64_t pack_hash, int32_t check_identity,
+                         uint64_t payload_hash, int32_t check_hash, sc_wire_decoder** out) {
+    return decoder_open(payload, bytes, g, slot, geometry, geom_hash, pack_hash, check_identity, payload_hash, check_hash,
+                        out);
+}
+
+int sc_wire_decoder_open_layers(const void* payload, uint64_t bytes, const sc_geometry* g, const sc_slot_layers* slot,
+                                const int64_t* geometry, uint64_t geom_hash, uint64_t pack_hash, int32_t check_identity,
+                                uint64_t payload_hash, int32_t check_hash, sc_wire_decoder** out) {
+    return decoder_open(payload, bytes, g, slot, geometry, geom_hash, pack_hash, check_identity, payload_hash, check_hash,
+                        out);
 }
 
 int64_t sc_wire_decoder_tokens(const sc_wire_decoder* d) { return d ? d->dec.tokens() : -1; }

@@ -25,6 +25,8 @@ for _name, _res, _args in (
     ("sc_wire_last_error", C.c_char_p, []),
     ("sc_wire_encoder_create", C.c_int, [C.POINTER(sc.Geometry), C.POINTER(sc.DecodeSlot), _I64, C.POINTER(Live), _U64,
                                          _U64, C.POINTER(_P)]),
+    ("sc_wire_encoder_create_layers", C.c_int, [C.POINTER(sc.Geometry), C.POINTER(sc.SlotLayers), _I64,
+                                                C.POINTER(Live), _U64, _U64, C.POINTER(_P)]),
     ("sc_wire_encoder_bytes", _U64, [_P]),
     ("sc_wire_encoder_pool_offset", _U64, [_P]),
     ("sc_wire_encode_async", C.c_int, [_P, _P, _U64, _P, _P]),
@@ -32,6 +34,8 @@ for _name, _res, _args in (
     ("sc_wire_encoder_destroy", C.c_int, [_P]),
     ("sc_wire_decoder_open", C.c_int, [_P, _U64, C.POINTER(sc.Geometry), C.POINTER(sc.DecodeSlot), C.POINTER(C.c_int64),
                                        _U64, _U64, _I32, _U64, _I32, C.POINTER(_P)]),
+    ("sc_wire_decoder_open_layers", C.c_int, [_P, _U64, C.POINTER(sc.Geometry), C.POINTER(sc.SlotLayers),
+                                              C.POINTER(C.c_int64), _U64, _U64, _I32, _U64, _I32, C.POINTER(_P)]),
     ("sc_wire_decoder_tokens", _I64, [_P]),
     ("sc_wire_decoder_restore", C.c_int, [_P, _P]),
     ("sc_wire_decoder_live_ids", C.c_int, [_P, C.POINTER(C.c_int32), _I64, C.POINTER(_I64)]),
@@ -41,10 +45,10 @@ for _name, _res, _args in (
     _fn = getattr(lib, _name)
     _fn.restype, _fn.argtypes = _res, _args
 
-EXPORTS = ("sc_wire_last_error", "sc_wire_encoder_create", "sc_wire_encoder_bytes", "sc_wire_encoder_pool_offset",
-           "sc_wire_encode_async", "sc_wire_encoder_hash", "sc_wire_encoder_destroy", "sc_wire_decoder_open",
-           "sc_wire_decoder_tokens", "sc_wire_decoder_restore", "sc_wire_decoder_live_ids", "sc_wire_decoder_small",
-           "sc_wire_decoder_destroy")
+EXPORTS = ("sc_wire_last_error", "sc_wire_encoder_create", "sc_wire_encoder_create_layers", "sc_wire_encoder_bytes",
+           "sc_wire_encoder_pool_offset", "sc_wire_encode_async", "sc_wire_encoder_hash", "sc_wire_encoder_destroy",
+           "sc_wire_decoder_open", "sc_wire_decoder_open_layers", "sc_wire_decoder_tokens", "sc_wire_decoder_restore",
+           "sc_wire_decoder_live_ids", "sc_wire_decoder_small", "sc_wire_decoder_destroy")
 
 
 class WireError(RuntimeError):
@@ -83,11 +87,15 @@ def make_live(geometry, ids, layer_lo=0, layer_hi=0, cvec=True, draft_record=Tru
 
 
 class Encoder:
+    """The device encoder of a slot: an f16 decode slot (sc_handoff.Slot) or a slot in any K/V format
+    (sc_handoff.LayerPools)."""
+
     def __init__(self, geo, slot, tokens: int, live: Live, geom_hash: int = 0, pack_hash: int = 0):
         self._slot = slot.c_struct()
         h = C.c_void_p()
-        _check(lib.sc_wire_encoder_create(C.byref(geo), C.byref(self._slot), tokens, C.byref(live), geom_hash, pack_hash,
-                                          C.byref(h)), "sc_wire_encoder_create")
+        create = lib.sc_wire_encoder_create_layers if isinstance(slot, sc.LayerPools) else lib.sc_wire_encoder_create
+        _check(create(C.byref(geo), C.byref(self._slot), tokens, C.byref(live), geom_hash, pack_hash, C.byref(h)),
+               "sc_wire_encoder_create")
         self.handle = h.value
 
     @property
@@ -126,9 +134,9 @@ class Decoder:
         self._slot = slot.c_struct()
         self._geo18 = (C.c_int64 * 18)(*geometry) if geometry is not None else None
         h = C.c_void_p()
-        _check(lib.sc_wire_decoder_open(payload_ptr, nbytes, C.byref(geo), C.byref(self._slot), self._geo18, geom_hash,
-                                        pack_hash, int(check_identity), payload_hash, int(check_hash), C.byref(h)),
-               "sc_wire_decoder_open")
+        open_ = lib.sc_wire_decoder_open_layers if isinstance(slot, sc.LayerPools) else lib.sc_wire_decoder_open
+        _check(open_(payload_ptr, nbytes, C.byref(geo), C.byref(self._slot), self._geo18, geom_hash, pack_hash,
+                     int(check_identity), payload_hash, int(check_hash), C.byref(h)), "sc_wire_decoder_open")
         self.handle = h.value
 
     @property
