@@ -357,6 +357,147 @@ def wire_payload(sc, geo, tokens: int, slot, link_h2d: float, link_d2h: float, r
                       "then mount"}
 
 
+def arena_dir(need: int) -> str:
+    """/dev/shm when it has room for `need` bytes (the reference's default hand-off directory is a tmpfs), else the
+    temp directory."""
+    import os
+    st = os.statvfs("/dev/shm") if os.path.isdir("/dev/shm") else None
+    if st and st.f_bavail * st.f_frsize > need + (1 << 30):
+        return "/dev/shm"
+    return os.environ.get("TMPDIR", "/tmp")
+
+
+def arena_handoff(sc, geo, tokens: int, slot, link_h2d: float, link_d2h: float, chunk_mib: int = 32, depth: int = 4,
+                  threads: int = 8, reps: int = 3) -> dict:
+    """The cross-process row: the 128K slot's payload written on the device, handed through a hand-off arena slot
+    (the reference's HandoffArena file, same format) and mounted into a fresh slot.  Writer = device encode, then the
+    mover (pinned DMA chunks copied into the slot's mapped window by host threads, device FNV-1a beside it) and publish;
+    reader = the mover (slot -> pinned chunks -> HBM) and the device mount with its hash check.  Both directions are
+    bounded by the host link; the reference moves the same payload with one pwrite and checks it with a byte-serial
+    FNV-1a on the CPU."""
+    import os
+    import shutil
+    import numpy as np
+    import sc_arena
+    import sc_wire
+    geokey = [2560, 48, 4, 128, 16, 32, 4, 8192, 4096, 24, 2, 256, 128, 4, 4, 3, 1, 0]
+    pack, geom = 0x0AABBCCDDEEFF001, 0x1122334455667788
+    ids = (np.arange(tokens, dtype=np.int64) % 151_000).astype(np.int32)
+    live, keep = sc_wire.make_live(geokey, ids, layer_hi=48, idx_dim=128)
+    enc = sc_wire.Encoder(geo, slot, tokens, live, geom, pack)
+    n = enc.bytes
+    payload = sc.DeviceBuffer(n, "uint8")
+    arrived = sc.DeviceBuffer(n, "uint8")
+    stream = sc.Stream()
+    enc.encode(payload.ptr, n, stream)
+    h = enc.hash()
+    base = arena_dir(n + (64 << 20))
+    d = os.path.join(base, f"sc-bench-arena-{os.getpid()}")
+    path = os.path.join(d, "arena")
+    out = {"tokens": tokens, "payload_bytes": n, "arena_dir": base, "chunk_mib": chunk_mib, "depth": depth,
+           "threads": threads}
+    try:
+        mover = sc_arena.Mover(chunk_mib << 20, depth, threads)
+        t0 = time.perf_counter()
+        w = sc_arena.Arena.writer(path, [(tokens, 1)], [n], pack, geom, reserve=False)
+        c = w.claim(0, 7, 1)
+        mover.publish(w, c, payload.ptr, n, tokens, stream.handle)        # first hand-off: the slot's pages are new
+        out["cold_publish_ms"] = round(mover.last()[1], 2)
+        w.release(c.index, c.nonce)
+        t0 = time.perf_counter()
+        w.close()
+        w = sc_arena.Arena.writer(path, [(tokens, 1)], [n], pack, geom, reserve=True)   # re-open: pages committed, mapped
+        out["reserve_ms"] = round((time.perf_counter() - t0) * 1e3, 1)
+        r = sc_arena.Arena.reader(path, pack, geom)
+        dst = sc.new_slot(geo, tokens, fill=0)
+        pub, mpub, rd, rdv, mnt = [], [], [], [], []
+        for rep in range(reps):
+            c = w.claim(0, 7, 2 + rep)
+            t0 = time.perf_counter()
+            enc.encode(payload.ptr, n, stream)
+            mover.publish(w, c, payload.ptr, n, tokens, stream.handle)
+            pub.append((time.perf_counter() - t0) * 1e3)
+            mpub.append(mover.last()[1])
+            t0 = time.perf_counter()
+            s = mover.read(r, c.index, c.nonce, 7, arrived.ptr, n, stream.handle, verify=False)
+            dec = sc_wire.Decoder(arrived.ptr, s.payload_bytes, geo, dst, payload_hash=s.payload_hash, check_hash=True)
+            dec.restore(stream)
+            mnt.append((time.perf_counter() - t0) * 1e3)
+            dec.destroy()
+            mover.read(r, c.index, c.nonce, 7, arrived.ptr, n, stream.handle, verify=False)
+            rd.append(mover.last()[1])
+            mover.read(r, c.index, c.nonce, 7, arrived.ptr, n, stream.handle, verify=True)
+            rdv.append(mover.last()[1])
+            w.release(c.index, c.nonce)
+        same = all(sc.fnv1a64_device(a.ptr, a.nbytes) == sc.fnv1a64_device(b.ptr, b.nbytes)
+                   for a, b in zip(slot.buffers(), dst.buffers()))
+        assert s.payload_hash == h
+        r.close()
+        w.close()
+        mover.destroy()
+        for b in dst.buffers():
+            b.free()
+    finally:
+        shutil.rmtree(d, ignore_errors=True)
+    payload.free()
+    arrived.free()
+    p, q, qv, m = min(pub), min(rd), min(rdv), min(mnt)
+    gb = lambda ms: round(n / (ms * 1e-3) / 1e9, 2)   # noqa: E731
+    out.update({
+        "publish_ms": round(p, 2), "publish_gbps": gb(p), "publish_frac_of_link": round(gb(p) / link_d2h, 3),
+        "mover_publish_ms": round(min(mpub), 2), "mover_publish_gbps": gb(min(mpub)),
+        "mover_publish_frac_of_link": round(gb(min(mpub)) / link_d2h, 3),
+        "read_ms": round(q, 2), "read_gbps": gb(q), "read_frac_of_link": round(gb(q) / link_h2d, 3),
+        "read_verified_ms": round(qv, 2), "read_verified_gbps": gb(qv),
+        "read_and_mount_ms": round(m, 2), "read_and_mount_gbps": gb(m),
+        "round_trip_bit_exact": bool(same),
+        "method": "publish = device encode + mover (D2H in pinned chunks, host threads copy each chunk into the "
+                  "slot's mapped window while later chunks are in flight, device FNV-1a on a side stream) + the "
+                  "arena's publish; read = mover (host threads copy slot chunks into pinned buffers, H2D of each "
+                  "while the next is copied); read_verified adds the device FNV-1a check; read_and_mount = read + "
+                  "device mount with its hash check; host wall clock, best of the reps; arena reserved "
+                  "(posix_fallocate + populated mapping) before the timed reps"})
+    return out
+
+
+def arena_cpu_baseline(sc, budget_bytes: int = 1 << 30) -> dict:
+    """The reference's hand-off path on the host for a bounded sample: write_payload (one pwrite) + the byte-serial
+    FNV-1a of the writer + publish, then read_slot + payload_hash_of + a copy out (src/core/handoff.cpp:821-901,
+    1053-1136), through this library's arena (same file and algorithm)."""
+    import os
+    import shutil
+    import numpy as np
+    import sc_arena
+    from oracle import sc_oracle
+    n = budget_bytes
+    data = np.random.default_rng(1).integers(0, 256, n, dtype=np.uint8)
+    base = arena_dir(n + (64 << 20))
+    d = os.path.join(base, f"sc-bench-arena-cpu-{os.getpid()}")
+    try:
+        w = sc_arena.Arena.writer(os.path.join(d, "arena"), [(131072, 1)], [n], 7, 9)
+        r = sc_arena.Arena.reader(os.path.join(d, "arena"), 7, 9)
+        best_w = best_r = None
+        for rep in range(2):
+            c = w.claim(0, 1, rep)
+            t0 = time.perf_counter()
+            w.write(c, 0, data)
+            hh = sc_oracle.fnv1a64(data)
+            w.publish(c, 1, n, hh)
+            tw = time.perf_counter() - t0
+            t0 = time.perf_counter()
+            got, s = r.read_host(c.index, c.nonce, 1, n, check_hash=True)
+            tr = time.perf_counter() - t0
+            w.release(c.index, c.nonce)
+            best_w = tw if best_w is None else min(best_w, tw)
+            best_r = tr if best_r is None else min(best_r, tr)
+        r.close()
+        w.close()
+    finally:
+        shutil.rmtree(d, ignore_errors=True)
+    return {"sample_bytes": n, "write_gbps": round(n / best_w / 1e9, 2), "read_gbps": round(n / best_r / 1e9, 2),
+            "handoff_gbps": round(n / (best_w + best_r) / 1e9, 2), "cores": 1, "kind": "port"}
+
+
 def quant_carve(sc, geo, tokens: int, stream, reps: int = 10) -> dict:
     """The quantizing carve of the config-3 geometry: f32 K/V rows into int8 / q4_0 / K8V4 pools plus the GDN state,
     one launch each (and int8 once more through a shuffled page table).  HBM bytes = the f32 rows read + the codes and
@@ -398,6 +539,9 @@ def main() -> int:
                     help="only the wire payload row of the same slot (for profiler runs); prints its JSON")
     ap.add_argument("--quant-only", action="store_true",
                     help="only the quantizing carve row of the same geometry (for profiler runs); prints its JSON")
+    ap.add_argument("--arena-only", action="store_true",
+                    help="only the hand-off arena row of the same geometry; prints its JSON")
+    ap.add_argument("--mover", default="64,4,8", help="arena mover chunk MiB, depth, threads")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run 5 device-to-device copies of BYTES (the counter calibration of profiler runs)")
     args = ap.parse_args()
@@ -467,6 +611,17 @@ def main() -> int:
     }
     if args.wire_only:
         print(json.dumps({"wire_payload": wire_payload(sc, geo, T, slot, h2d, d2h)}), flush=True)
+        return 0
+    mv = [int(x) for x in args.mover.split(",")]
+    if args.arena_only:
+        rows = {"link_h2d_gbps": round(h2d, 2), "link_d2h_gbps": round(d2h, 2)}
+        for cfg in ([mv] if len(mv) == 3 else [mv[i:i + 3] for i in range(0, len(mv), 3)]):
+            settle_link(sc, d2h)
+            key = "arena_%d_%d_%d" % tuple(cfg)
+            rows[key] = arena_handoff(sc, geo, T, slot, h2d, d2h, *cfg)
+            log(f"{key}: " + json.dumps(rows[key]))
+        rows["arena_cpu_baseline"] = arena_cpu_baseline(sc)
+        print(json.dumps(rows), flush=True)
         return 0
     if args.kernel_only:
         print(json.dumps(result), flush=True)

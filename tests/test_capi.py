@@ -129,3 +129,15 @@ def test_wire_refusals_before_any_hip_call(sc):
     assert sc_wire.lib.sc_wire_encoder_create(None, None, 0, None, 0, 0, C.byref(h)) == sc.SC_EINVAL
     assert "missing" in sc_wire.lib.sc_wire_last_error().decode()
     assert sc_wire.lib.sc_wire_decoder_open(None, 0, C.byref(geo), None, None, 0, 0, 0, 0, 0, C.byref(h)) == sc.SC_EINVAL
+
+
+def test_core_library_exports_the_arena_abi():
+    """libsc_core.so exports every entry point include/sc_arena.h declares (the hand-off arena and its movers)."""
+    import sc_arena
+    text = (ROOT / "include" / "sc_arena.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    names = sorted(set(re.findall(r"\b(sc_(?:arena|mover)_[a-z0-9_]+)\s*\(", text)))
+    assert len(names) >= 19
+    for name in names:
+        assert hasattr(sc_arena.lib, name), name
+    assert set(names) == set(sc_arena.EXPORTS)
