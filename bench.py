@@ -8,7 +8,9 @@ handoff = one launch of the move kernel.  value = P / step time (GB/s).
 Also reported: the roofline of that kernel (2P algorithmic HBM bytes per launch over its event-timed duration,
 against MI355X's 8 TB/s), the p50 latency of the 32K handoff (config 2, first enqueue to completion event, over
 >= 20 repetitions), the two-pass gather -> scatter rate, park (D2H) and resume (H2D) of the 128K slot against the
-host link measured in the same run, and the CPU baseline: the oracle's single-core carve of a bounded sample of the
+host link measured in the same run, the device payload codec, the hand-off arena (payload published from HBM into a
+tmpfs slot and read back, against the host link), the same-GPU hand-off between processes (exported device segments),
+the quantizing carve, configs 4 and 5, and the CPU baseline: the oracle's single-core carve of a bounded sample of the
 same workload, plus the reference-style host pipeline (16 MiB segment save, FNV-1a encode, decode + re-hash,
 restore).
 """
@@ -417,6 +419,10 @@ def arena_handoff(sc, geo, tokens: int, slot, link_h2d: float, link_d2h: float, 
             enc.encode(payload.ptr, n, stream)
             mover.publish(w, c, payload.ptr, n, tokens, stream.handle)
             pub.append((time.perf_counter() - t0) * 1e3)
+            w.release(c.index, c.nonce)
+            c = w.claim(0, 7, 2 + rep)
+            stream.sync()                                   # the payload is in place: the mover alone
+            mover.publish(w, c, payload.ptr, n, tokens, stream.handle)
             mpub.append(mover.last()[1])
             t0 = time.perf_counter()
             s = mover.read(r, c.index, c.nonce, 7, arrived.ptr, n, stream.handle, verify=False)
@@ -453,7 +459,7 @@ def arena_handoff(sc, geo, tokens: int, slot, link_h2d: float, link_d2h: float, 
         "round_trip_bit_exact": bool(same),
         "method": "publish = device encode + mover (D2H in pinned chunks, host threads copy each chunk into the "
                   "slot's mapped window while later chunks are in flight, device FNV-1a on a side stream) + the "
-                  "arena's publish; read = mover (host threads copy slot chunks into pinned buffers, H2D of each "
+                  "arena's publish; mover_publish = the same with the payload already encoded; read = mover (host threads copy slot chunks into pinned buffers, H2D of each "
                   "while the next is copied); read_verified adds the device FNV-1a check; read_and_mount = read + "
                   "device mount with its hash check; host wall clock, best of the reps; arena reserved "
                   "(posix_fallocate + populated mapping) before the timed reps"})
@@ -496,6 +502,76 @@ def arena_cpu_baseline(sc, budget_bytes: int = 1 << 30) -> dict:
         shutil.rmtree(d, ignore_errors=True)
     return {"sample_bytes": n, "write_gbps": round(n / best_w / 1e9, 2), "read_gbps": round(n / best_r / 1e9, 2),
             "handoff_gbps": round(n / (best_w + best_r) / 1e9, 2), "cores": 1, "kind": "port"}
+
+
+def ipc_export_role(capacity: int) -> int:
+    """The exporting process of the same-GPU row (started by ipc_handoff): a payload-sized device buffer, segments of
+    1 GiB exported, and on every "stage" line one timed staging copy, answered with its time and the device hash."""
+    import sc_handoff as sc
+    stream = sc.Stream()
+    payload = sc.DeviceBuffer(capacity, "uint8")
+    sc.check(sc.lib.sc_fill_uniform_f16(payload.ptr, capacity // 2, -1.0, 1.0, 5, 0, stream.handle), "fill")
+    stream.sync()
+    ex = sc.IpcExport(capacity, sc.IPC_MAX_SEGMENT)
+    print(json.dumps({"segments": [[h.hex(), n] for h, n in ex.segments()],
+                      "hash": sc.fnv1a64_device(payload.ptr, capacity)}), flush=True)
+    e0, e1 = sc.Event(), sc.Event()
+    for line in sys.stdin:
+        if line.strip() != "stage":
+            break
+        e0.record(stream)
+        ex.stage(payload.ptr, capacity, stream)
+        e1.record(stream)
+        e1.sync()
+        print(json.dumps({"stage_ms": e0.elapsed_ms(e1)}), flush=True)
+    ex.destroy()
+    return 0
+
+
+def ipc_handoff(sc, nbytes: int, reps: int = 5) -> dict:
+    """The same-GPU row: a payload of `nbytes` handed from another process on this GPU through exported device
+    segments (one staging copy in the exporter, one fetch copy here), against the HBM roofline of the two copies."""
+    import subprocess
+    proc = subprocess.Popen([sys.executable, "-u", __file__, "--ipc-export", str(nbytes)], stdin=subprocess.PIPE,
+                            stdout=subprocess.PIPE, text=True)
+    imp = None
+    try:
+        first = json.loads(proc.stdout.readline())
+        imp = sc.IpcImport([(bytes.fromhex(h), n) for h, n in first["segments"]])
+        dst = sc.DeviceBuffer(nbytes, "uint8")
+        stream = sc.Stream()
+        e0, e1 = sc.Event(), sc.Event()
+        stage, fetch = [], []
+        for _ in range(reps + 1):
+            proc.stdin.write("stage\n")
+            proc.stdin.flush()
+            stage.append(json.loads(proc.stdout.readline())["stage_ms"])
+            e0.record(stream)
+            imp.fetch(dst.ptr, nbytes, stream)
+            e1.record(stream)
+            e1.sync()
+            fetch.append(e0.elapsed_ms(e1))
+        same = sc.fnv1a64_device(dst.ptr, nbytes) == first["hash"]
+        dst.free()
+    finally:
+        if imp:
+            imp.close()
+        try:
+            proc.stdin.write("done\n")
+            proc.stdin.flush()
+        except BrokenPipeError:
+            pass
+        proc.wait(timeout=60)
+    st, fe = min(stage[1:]), min(fetch[1:])
+    hbm = lambda ms: round(2 * nbytes / (ms * 1e-3) / 1e9, 1)   # noqa: E731
+    return {"payload_bytes": nbytes, "segments": len(first["segments"]), "stage_ms": round(st, 3),
+            "fetch_ms": round(fe, 3), "handoff_ms": round(st + fe, 3),
+            "handoff_gbps": round(nbytes / ((st + fe) * 1e-3) / 1e9, 1), "stage_hbm_gbps": hbm(st),
+            "fetch_hbm_gbps": hbm(fe), "fetch_frac": round(hbm(fe) / HBM_PEAK_GBPS, 4), "bit_exact": bool(same),
+            "method": "exporter process: payload staged into 1 GiB hipMalloc segments exported with hipIpcGetMemHandle "
+                      "(device copy kernel, HIP events); importer (this process): segments opened once with "
+                      "hipIpcOpenMemHandle, payload fetched into its own buffer by the same kernel; best of the reps "
+                      "after one warm-up; HBM bytes = 2 x payload per copy"}
 
 
 def quant_carve(sc, geo, tokens: int, stream, reps: int = 10) -> dict:
@@ -542,9 +618,13 @@ def main() -> int:
     ap.add_argument("--arena-only", action="store_true",
                     help="only the hand-off arena row of the same geometry; prints its JSON")
     ap.add_argument("--mover", default="64,4,8", help="arena mover chunk MiB, depth, threads")
+    ap.add_argument("--ipc-only", action="store_true", help="only the same-GPU inter-process row; prints its JSON")
+    ap.add_argument("--ipc-export", type=int, default=0, metavar="BYTES", help=argparse.SUPPRESS)
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run 5 device-to-device copies of BYTES (the counter calibration of profiler runs)")
     args = ap.parse_args()
+    if args.ipc_export:
+        return ipc_export_role(args.ipc_export)
 
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
@@ -578,6 +658,9 @@ def main() -> int:
 
     if args.quant_only:
         print(json.dumps({"quant_carve": quant_carve(sc, geo, T, stream)}), flush=True)
+        return 0
+    if args.ipc_only:
+        print(json.dumps({"ipc_handoff": ipc_handoff(sc, P)}), flush=True)
         return 0
     log(f"config 3: {T} tokens, payload {P} B; generating inputs on the device")
     case = sc.SyntheticCase(geo, tokens=T, seed=0x5EED)
@@ -736,6 +819,21 @@ def main() -> int:
     wp = result["wire_payload"]
     log(f"wire: encode {wp['encode_ms']} ms ({wp['encode_gbps']} GB/s), hash {wp['hash_ms']} ms, mount "
         f"{wp['mount_ms']} ms; checked park {wp['checked_park_gbps']} GB/s, resume {wp['checked_resume_gbps']} GB/s")
+
+    log("hand-off arena: the 128K slot's payload through a tmpfs arena slot and back into a fresh slot")
+    settle_ar = settle_link(sc, d2h)
+    result["arena_handoff"] = arena_handoff(sc, geo, T, slot, h2d, d2h, *mv[:3])
+    result["arena_handoff"]["link_settle_ms"] = settle_ar
+    ah = result["arena_handoff"]
+    log(f"arena: publish {ah['mover_publish_gbps']} GB/s ({ah['mover_publish_frac_of_link']} of link), read "
+        f"{ah['read_gbps']} GB/s ({ah['read_frac_of_link']}), read+mount {ah['read_and_mount_ms']} ms")
+    if not args.no_cpu:
+        result["arena_handoff"]["cpu_baseline"] = arena_cpu_baseline(sc, 512 << 20)
+    log("same-GPU hand-off between processes: exported device segments")
+    result["ipc_handoff"] = ipc_handoff(sc, P)
+    ih = result["ipc_handoff"]
+    log(f"ipc: stage {ih['stage_ms']} ms + fetch {ih['fetch_ms']} ms = {ih['handoff_gbps']} GB/s, bit-exact "
+        f"{ih['bit_exact']}")
 
     log("quantizing carve: int8 / q4_0 / K8V4 pools from f32 rows, 128K")
     result["quant_carve"] = quant_carve(sc, geo, T, stream)

@@ -384,6 +384,47 @@ int sc_stream_wait_event(void* stream, void* event);
  * probe_pcie_h2d_gbps (src/program/generate.cpp:1133-1161) applied to both directions. */
 int sc_probe_link(uint64_t bytes, int iters, double* h2d_gbps, double* d2h_gbps);
 
+/* A device-to-device copy by a shader kernel (16-byte vectors when both pointers share their alignment modulo 16), for
+ * sources the runtime's own copy might hand to a copy engine (memory of another process mapped by a handle). */
+int sc_copy_device_async(void* dst, const void* src, uint64_t bytes, void* stream);
+
+/* ---- same-GPU hand-off between processes (hipIpcMemHandle) --------------------------------------------------------
+ *
+ * No counterpart in the reference: its prefill and decode instances hand a payload over only through the tmpfs arena
+ * (include/strata/core/handoff.hpp:432-551), through host memory and the host link twice.  When both instances run on
+ * one GPU the payload can stay in HBM: the exporter (prefill) allocates device segments once, exports a memory handle
+ * for each, and stages every payload into them with one device copy; the importer (decode) opens the handles once and
+ * copies the payload out into its own buffer with one device copy, after which the exporter may reuse the segments.
+ * Which payload is in the segments, and when the importer is done with it, travel on the caller's own channel (a
+ * socket line, or an arena slot).  Every segment is its own allocation of at most SC_IPC_MAX_SEGMENT bytes. */
+#define SC_IPC_HANDLE_BYTES 64
+#define SC_IPC_MAX_SEGMENT (1ull << 30)
+#define SC_IPC_MAX_SEGMENTS 64
+typedef struct sc_ipc_segment {
+    uint8_t handle[SC_IPC_HANDLE_BYTES];   /* hipIpcMemHandle_t of the segment's allocation */
+    uint64_t bytes;                        /* the segment's size */
+} sc_ipc_segment;
+typedef struct sc_ipc_export sc_ipc_export;
+typedef struct sc_ipc_import sc_ipc_import;
+
+/* Segments of `segment_bytes` (a multiple of 4 KiB, at most SC_IPC_MAX_SEGMENT; the last one holds the remainder)
+ * covering `capacity` bytes, on the current device, each exported. */
+int sc_ipc_export_create(uint64_t capacity, uint64_t segment_bytes, sc_ipc_export** out);
+int32_t sc_ipc_export_count(const sc_ipc_export* ex);
+/* The segments' handles and sizes, in payload order (`max_segments` entries of room). */
+int sc_ipc_export_segments(const sc_ipc_export* ex, sc_ipc_segment* segments, int32_t max_segments);
+/* Stage `bytes` of device memory into the segments, on `stream` (ordered after the work already on it). */
+int sc_ipc_export_stage(sc_ipc_export* ex, const void* device_payload, uint64_t bytes, void* stream);
+int sc_ipc_export_destroy(sc_ipc_export* ex);
+
+/* Map another process's segments into this one (refused, before any handle is opened, when a segment is larger than
+ * SC_IPC_MAX_SEGMENT or there are more than SC_IPC_MAX_SEGMENTS). */
+int sc_ipc_import_open(const sc_ipc_segment* segments, int32_t n_segments, sc_ipc_import** out);
+/* Copy the first `bytes` of the segments into `device_dst`, on `stream`. */
+int sc_ipc_import_fetch(sc_ipc_import* im, void* device_dst, uint64_t bytes, void* stream);
+/* Unmap the segments (before the exporter frees them). */
+int sc_ipc_import_close(sc_ipc_import* im);
+
 /* ---- synthetic inputs (bench and tests; not on the handoff path) ---------------------------------------------- */
 
 /* Counter-based fills, bit-identical to the host generator of the test oracle:

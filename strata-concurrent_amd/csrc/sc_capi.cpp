@@ -28,6 +28,7 @@ hipError_t launch_fill_uniform_f32(float* dst, uint64_t n, float lo, float hi, u
                                    hipStream_t stream);
 hipError_t launch_fill_normal_f32(float* dst, uint64_t n, uint64_t seed, uint64_t sid, hipStream_t stream);
 hipError_t launch_fill_bytes(void* dst, uint8_t value, uint64_t n, hipStream_t stream);
+hipError_t launch_copy_bytes(void* dst, const void* src, uint64_t n, hipStream_t stream);
 hipError_t launch_decode_probe(const void* kv, uint64_t n_bytes, uint32_t* sink, int64_t workgroups,
                                hipStream_t stream);
 hipError_t launch_batch(const BatchArgs& args, int64_t grid, hipStream_t stream);
@@ -1287,6 +1288,148 @@ int sc_event_elapsed_ms(void* start, void* end, float* ms) {
 int sc_stream_wait_event(void* stream, void* event) {
     SC_HIP(hipStreamWaitEvent(static_cast<hipStream_t>(stream), static_cast<hipEvent_t>(event), 0), "stream wait");
     return ok();
+}
+
+int sc_copy_device_async(void* dst, const void* src, uint64_t bytes, void* stream) {
+    if (!bytes) return ok();
+    if (!dst || !src) return fail(SC_EINVAL, "sc_handoff: missing copy buffer");
+    SC_HIP(sc::launch_copy_bytes(dst, src, bytes, static_cast<hipStream_t>(stream)), "device copy");
+    return ok();
+}
+
+// ---- same-GPU hand-off between processes ------------------------------------------------------------------------
+
+struct sc_ipc_export {
+    std::vector<void*> ptr;
+    std::vector<uint64_t> bytes;
+    std::vector<hipIpcMemHandle_t> handle;
+};
+struct sc_ipc_import {
+    std::vector<void*> ptr;
+    std::vector<uint64_t> bytes;
+};
+
+static void ipc_export_free(sc_ipc_export* ex) {
+    for (void* p : ex->ptr) (void) hipFree(p);
+    delete ex;
+}
+
+int sc_ipc_export_create(uint64_t capacity, uint64_t segment_bytes, sc_ipc_export** out) {
+    if (!out) return fail(SC_EINVAL, "sc_handoff: missing output");
+    *out = nullptr;
+    if (!capacity || segment_bytes < 4096 || segment_bytes % 4096 || segment_bytes > SC_IPC_MAX_SEGMENT)
+        return fail(SC_ERANGE, "sc_handoff: IPC segments are 4 KiB multiples of at most 1 GiB, over a nonzero capacity");
+    const uint64_t n = (capacity + segment_bytes - 1) / segment_bytes;
+    if (n > SC_IPC_MAX_SEGMENTS) return fail(SC_ERANGE, "sc_handoff: more than SC_IPC_MAX_SEGMENTS IPC segments");
+    auto* ex = new (std::nothrow) sc_ipc_export;
+    if (!ex) return fail(SC_ENOMEM, "sc_handoff: out of host memory");
+    for (uint64_t i = 0; i < n; ++i) {
+        const uint64_t left = capacity - i * segment_bytes;
+        const uint64_t b = left < segment_bytes ? (left + 4095) & ~uint64_t(4095) : segment_bytes;
+        void* p = nullptr;
+        hipError_t e = hipMalloc(&p, b);
+        if (e != hipSuccess) {
+            ipc_export_free(ex);
+            return fail(SC_ENOMEM, std::string("sc_handoff: IPC segment allocation: ") + hipGetErrorString(e));
+        }
+        ex->ptr.push_back(p);
+        ex->bytes.push_back(b);
+        hipIpcMemHandle_t h;
+        e = hipIpcGetMemHandle(&h, p);
+        if (e != hipSuccess) {
+            ipc_export_free(ex);
+            return hip_fail(e, "IPC handle");
+        }
+        ex->handle.push_back(h);
+    }
+    *out = ex;
+    return ok();
+}
+
+int32_t sc_ipc_export_count(const sc_ipc_export* ex) { return ex ? int32_t(ex->ptr.size()) : 0; }
+
+int sc_ipc_export_segments(const sc_ipc_export* ex, sc_ipc_segment* segments, int32_t max_segments) {
+    if (!ex || !segments) return fail(SC_EINVAL, "sc_handoff: missing export or output");
+    if (max_segments < int32_t(ex->ptr.size())) return fail(SC_ERANGE, "sc_handoff: room for fewer segments than exported");
+    static_assert(sizeof(hipIpcMemHandle_t) == SC_IPC_HANDLE_BYTES, "hipIpcMemHandle_t is 64 bytes");
+    for (size_t i = 0; i < ex->ptr.size(); ++i) {
+        std::memcpy(segments[i].handle, &ex->handle[i], SC_IPC_HANDLE_BYTES);
+        segments[i].bytes = ex->bytes[i];
+    }
+    return ok();
+}
+
+/// Copy `bytes` between a contiguous buffer and a list of segments (to_segments: buffer -> segments).
+static int segmented_copy(const std::vector<void*>& ptr, const std::vector<uint64_t>& seg_bytes, void* buffer,
+                          uint64_t bytes, bool to_segments, hipStream_t stream) {
+    uint64_t total = 0;
+    for (uint64_t b : seg_bytes) total += b;
+    if (bytes > total) return fail(SC_ERANGE, "sc_handoff: the payload is larger than the IPC segments");
+    if (bytes && !buffer) return fail(SC_EINVAL, "sc_handoff: missing payload buffer");
+    uint64_t off = 0;
+    for (size_t i = 0; i < ptr.size() && off < bytes; ++i) {
+        const uint64_t n = std::min(seg_bytes[i], bytes - off);
+        uint8_t* b = static_cast<uint8_t*>(buffer) + off;
+        const hipError_t e = to_segments ? sc::launch_copy_bytes(ptr[i], b, n, stream)
+                                         : sc::launch_copy_bytes(b, ptr[i], n, stream);
+        if (e != hipSuccess) return hip_fail(e, "IPC segment copy");
+        off += n;
+    }
+    return ok();
+}
+
+int sc_ipc_export_stage(sc_ipc_export* ex, const void* device_payload, uint64_t bytes, void* stream) {
+    if (!ex) return fail(SC_EINVAL, "sc_handoff: missing export");
+    return segmented_copy(ex->ptr, ex->bytes, const_cast<void*>(device_payload), bytes, true,
+                          static_cast<hipStream_t>(stream));
+}
+
+int sc_ipc_export_destroy(sc_ipc_export* ex) {
+    if (ex) ipc_export_free(ex);
+    return ok();
+}
+
+int sc_ipc_import_open(const sc_ipc_segment* segments, int32_t n_segments, sc_ipc_import** out) {
+    if (!out || (n_segments && !segments)) return fail(SC_EINVAL, "sc_handoff: missing segments or output");
+    *out = nullptr;
+    if (n_segments < 1 || n_segments > SC_IPC_MAX_SEGMENTS)
+        return fail(SC_ERANGE, "sc_handoff: 1 to SC_IPC_MAX_SEGMENTS IPC segments");
+    for (int32_t i = 0; i < n_segments; ++i)
+        if (segments[i].bytes == 0 || segments[i].bytes > SC_IPC_MAX_SEGMENT)
+            return fail(SC_ERANGE, "sc_handoff: an IPC segment is empty or larger than SC_IPC_MAX_SEGMENT");
+    auto* im = new (std::nothrow) sc_ipc_import;
+    if (!im) return fail(SC_ENOMEM, "sc_handoff: out of host memory");
+    for (int32_t i = 0; i < n_segments; ++i) {
+        hipIpcMemHandle_t h;
+        std::memcpy(&h, segments[i].handle, SC_IPC_HANDLE_BYTES);
+        void* p = nullptr;
+        const hipError_t e = hipIpcOpenMemHandle(&p, h, hipIpcMemLazyEnablePeerAccess);
+        if (e != hipSuccess) {
+            for (void* q : im->ptr) (void) hipIpcCloseMemHandle(q);
+            delete im;
+            return hip_fail(e, "IPC open");
+        }
+        im->ptr.push_back(p);
+        im->bytes.push_back(segments[i].bytes);
+    }
+    *out = im;
+    return ok();
+}
+
+int sc_ipc_import_fetch(sc_ipc_import* im, void* device_dst, uint64_t bytes, void* stream) {
+    if (!im) return fail(SC_EINVAL, "sc_handoff: missing import");
+    return segmented_copy(im->ptr, im->bytes, device_dst, bytes, false, static_cast<hipStream_t>(stream));
+}
+
+int sc_ipc_import_close(sc_ipc_import* im) {
+    if (!im) return ok();
+    hipError_t first = hipSuccess;
+    for (void* p : im->ptr) {
+        const hipError_t e = hipIpcCloseMemHandle(p);
+        if (first == hipSuccess) first = e;
+    }
+    delete im;
+    return first == hipSuccess ? ok() : hip_fail(first, "IPC close");
 }
 
 int sc_probe_link(uint64_t bytes, int iters, double* h2d_gbps, double* d2h_gbps) {

@@ -650,6 +650,32 @@ __global__ void fill_bytes_kernel(uint8_t* dst, uint8_t value, uint64_t n) {
     for (uint64_t i = tail0 + gid; i < n; i += stride) dst[i] = value;
 }
 
+// A device-to-device byte copy: 16-byte vectors (four in flight per thread) when source and destination share their
+// alignment modulo 16, bytes otherwise.  Used where the source is another process's memory mapped by a memory handle,
+// which the runtime's own copy may route to a copy engine instead of the shader.
+__global__ void __launch_bounds__(256) copy_bytes_kernel(uint8_t* dst, const uint8_t* src, uint64_t n) {
+    const uint64_t gid = uint64_t(blockIdx.x) * 256 + threadIdx.x;
+    const uint64_t stride = uint64_t(gridDim.x) * 256;
+    const bool vec = ((reinterpret_cast<uintptr_t>(dst) ^ reinterpret_cast<uintptr_t>(src)) & 15u) == 0;
+    uint64_t pre = vec ? ((16u - (reinterpret_cast<uintptr_t>(dst) & 15u)) & 15u) : n;
+    if (pre > n) pre = n;
+    for (uint64_t i = gid; i < pre; i += stride) dst[i] = src[i];
+    const uint64_t body = (n - pre) / 16;
+    const uint8_t* s = src + pre;
+    uint8_t* d = dst + pre;
+    uint64_t i = gid;
+    for (; i + 3 * stride < body; i += 4 * stride) {
+        const u32x4 a = ld16(s + i * 16), b = ld16(s + (i + stride) * 16);
+        const u32x4 c = ld16(s + (i + 2 * stride) * 16), e = ld16(s + (i + 3 * stride) * 16);
+        st16(d + i * 16, a);
+        st16(d + (i + stride) * 16, b);
+        st16(d + (i + 2 * stride) * 16, c);
+        st16(d + (i + 3 * stride) * 16, e);
+    }
+    for (; i < body; i += stride) st16(d + i * 16, ld16(s + i * 16));
+    for (uint64_t j = pre + body * 16 + gid; j < n; j += stride) dst[j] = src[j];
+}
+
 // Reads its share of the K/V bytes and folds them into one word per workgroup.
 __global__ void __launch_bounds__(kThreads) decode_probe_kernel(const uint8_t* kv, uint64_t n16, uint32_t* sink) {
     uint32_t acc = 0;
@@ -764,6 +790,15 @@ hipError_t launch_fill_bytes(void* dst, uint8_t value, uint64_t n, hipStream_t s
     if (!n) return hipSuccess;
     hipLaunchKernelGGL(fill_bytes_kernel, dim3(fill_grid(n / 16 + 16)), dim3(256), 0, stream,
                        static_cast<uint8_t*>(dst), value, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_copy_bytes(void* dst, const void* src, uint64_t n, hipStream_t stream) {
+    if (!n) return hipSuccess;
+    // four 16-byte vectors per thread and pass; capped so that every CU holds several workgroups
+    const uint64_t blocks = (n / 16 + 1023) / 1024;
+    hipLaunchKernelGGL(copy_bytes_kernel, dim3(unsigned(blocks < 16384 ? (blocks ? blocks : 1) : 16384)), dim3(256), 0,
+                       stream, static_cast<uint8_t*>(dst), static_cast<const uint8_t*>(src), n);
     return hipGetLastError();
 }
 

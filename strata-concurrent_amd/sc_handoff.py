@@ -108,6 +108,13 @@ class ImageBlob(C.Structure):
 _P = C.c_void_p
 _I64, _U64 = C.c_int64, C.c_uint64
 _GEO = C.POINTER(Geometry)
+class IpcSegment(C.Structure):
+    """sc_ipc_segment: one exported device allocation (a 64-byte memory handle and its size)."""
+    _fields_ = [("handle", C.c_uint8 * 64), ("bytes", C.c_uint64)]
+
+
+IPC_MAX_SEGMENT = 1 << 30
+
 _SIGS = {
     "sc_last_error": (C.c_char_p, []),
     "sc_version": (C.c_char_p, []),
@@ -172,6 +179,15 @@ _SIGS = {
     "sc_fnv1a64_workspace_bytes": (_U64, [_U64]),
     "sc_fnv1a64_async": (C.c_int, [_P, _U64, _U64, _P, _P, _U64, _P]),
     "sc_fnv1a64_device": (C.c_int, [_P, _U64, _U64, C.POINTER(_U64)]),
+    "sc_copy_device_async": (C.c_int, [_P, _P, _U64, _P]),
+    "sc_ipc_export_create": (C.c_int, [_U64, _U64, C.POINTER(_P)]),
+    "sc_ipc_export_count": (C.c_int32, [_P]),
+    "sc_ipc_export_segments": (C.c_int, [_P, C.POINTER(IpcSegment), C.c_int32]),
+    "sc_ipc_export_stage": (C.c_int, [_P, _P, _U64, _P]),
+    "sc_ipc_export_destroy": (C.c_int, [_P]),
+    "sc_ipc_import_open": (C.c_int, [C.POINTER(IpcSegment), C.c_int32, C.POINTER(_P)]),
+    "sc_ipc_import_fetch": (C.c_int, [_P, _P, _U64, _P]),
+    "sc_ipc_import_close": (C.c_int, [_P]),
 }
 for _name, (_res, _args) in _SIGS.items():
     _fn = getattr(lib, _name)
@@ -925,3 +941,47 @@ def resume_layers_async(geo: Geometry, host_ptr: int, host_bytes: int, tokens: i
     cs = pools.c_struct()
     check(lib.sc_resume_layers_async(C.byref(geo), host_ptr, host_bytes, tokens, C.byref(cs), _stream(stream), done),
           "sc_resume_layers_async")
+
+
+class IpcExport:
+    """The exporting side of a same-GPU hand-off: device segments allocated and exported once."""
+
+    def __init__(self, capacity: int, segment_bytes: int = IPC_MAX_SEGMENT):
+        h = C.c_void_p()
+        check(lib.sc_ipc_export_create(capacity, segment_bytes, C.byref(h)), "sc_ipc_export_create")
+        self.handle = h.value
+
+    def segments(self) -> list:
+        n = lib.sc_ipc_export_count(self.handle)
+        arr = (IpcSegment * n)()
+        check(lib.sc_ipc_export_segments(self.handle, arr, n), "sc_ipc_export_segments")
+        return [(bytes(s.handle), int(s.bytes)) for s in arr]
+
+    def stage(self, device_ptr: int, nbytes: int, stream=None) -> None:
+        check(lib.sc_ipc_export_stage(self.handle, device_ptr, nbytes, _stream(stream)), "sc_ipc_export_stage")
+
+    def destroy(self) -> None:
+        if self.handle:
+            check(lib.sc_ipc_export_destroy(self.handle), "sc_ipc_export_destroy")
+            self.handle = None
+
+
+class IpcImport:
+    """The importing side: another process's segments mapped into this one."""
+
+    def __init__(self, segments):
+        arr = (IpcSegment * len(segments))()
+        for i, (handle, nbytes) in enumerate(segments):
+            C.memmove(arr[i].handle, handle, 64)
+            arr[i].bytes = nbytes
+        h = C.c_void_p()
+        check(lib.sc_ipc_import_open(arr, len(segments), C.byref(h)), "sc_ipc_import_open")
+        self.handle = h.value
+
+    def fetch(self, device_ptr: int, nbytes: int, stream=None) -> None:
+        check(lib.sc_ipc_import_fetch(self.handle, device_ptr, nbytes, _stream(stream)), "sc_ipc_import_fetch")
+
+    def close(self) -> None:
+        if self.handle:
+            check(lib.sc_ipc_import_close(self.handle), "sc_ipc_import_close")
+            self.handle = None

@@ -141,3 +141,17 @@ def test_core_library_exports_the_arena_abi():
     for name in names:
         assert hasattr(sc_arena.lib, name), name
     assert set(names) == set(sc_arena.EXPORTS)
+
+
+def test_ipc_refusals_before_any_hip_call(sc):
+    """Same-GPU hand-off segments over 1 GiB, of odd sizes or too many are refused on the host (no handle opened)."""
+    h = C.c_void_p()
+    assert sc.lib.sc_ipc_export_create(1 << 20, (1 << 30) + 4096, C.byref(h)) == sc.SC_ERANGE
+    assert sc.lib.sc_ipc_export_create(1 << 20, 1000, C.byref(h)) == sc.SC_ERANGE
+    assert sc.lib.sc_ipc_export_create(65 << 20, 1 << 20, C.byref(h)) == sc.SC_ERANGE   # 65 segments
+    assert sc.lib.sc_ipc_export_create(0, 1 << 20, C.byref(h)) == sc.SC_ERANGE
+    seg = (sc.IpcSegment * 2)()
+    seg[0].bytes, seg[1].bytes = 1 << 20, (1 << 30) + 1
+    assert sc.lib.sc_ipc_import_open(seg, 2, C.byref(h)) == sc.SC_ERANGE
+    assert "SC_IPC_MAX_SEGMENT" in sc.last_error()
+    assert sc.lib.sc_ipc_import_open(seg, 65, C.byref(h)) == sc.SC_ERANGE
