@@ -96,8 +96,9 @@ int sc_mover_publish(sc_mover* mover, sc_arena* arena, const sc_arena_claim* cla
  * the copy. */
 int sc_mover_read(sc_mover* mover, sc_arena* arena, int32_t index, uint64_t nonce, uint64_t client_id, void* device_dst,
                   uint64_t capacity, void* stream, int32_t verify, sc_arena_slot* out);
-/* The last transfer's host wall-clock time and, for a verified read, the part spent on the hash. */
-int sc_mover_last(const sc_mover* mover, uint64_t* bytes, double* ms, double* hash_ms);
+/* The last transfer's host wall-clock time, the part spent on the hash (a verified read), in host copies between
+ * staging and the slot, and waiting for DMA.  Any output may be NULL. */
+int sc_mover_last(const sc_mover* mover, uint64_t* bytes, double* ms, double* hash_ms, double* copy_ms, double* wait_ms);
 
 #ifdef __cplusplus
 }

@@ -650,30 +650,35 @@ __global__ void fill_bytes_kernel(uint8_t* dst, uint8_t value, uint64_t n) {
     for (uint64_t i = tail0 + gid; i < n; i += stride) dst[i] = value;
 }
 
-// A device-to-device byte copy: 16-byte vectors (four in flight per thread) when source and destination share their
-// alignment modulo 16, bytes otherwise.  Used where the source is another process's memory mapped by a memory handle,
-// which the runtime's own copy may route to a copy engine instead of the shader.
-__global__ void __launch_bounds__(256) copy_bytes_kernel(uint8_t* dst, const uint8_t* src, uint64_t n) {
-    const uint64_t gid = uint64_t(blockIdx.x) * 256 + threadIdx.x;
-    const uint64_t stride = uint64_t(gridDim.x) * 256;
-    const bool vec = ((reinterpret_cast<uintptr_t>(dst) ^ reinterpret_cast<uintptr_t>(src)) & 15u) == 0;
-    uint64_t pre = vec ? ((16u - (reinterpret_cast<uintptr_t>(dst) & 15u)) & 15u) : n;
-    if (pre > n) pre = n;
-    for (uint64_t i = gid; i < pre; i += stride) dst[i] = src[i];
-    const uint64_t body = (n - pre) / 16;
-    const uint8_t* s = src + pre;
-    uint8_t* d = dst + pre;
-    uint64_t i = gid;
-    for (; i + 3 * stride < body; i += 4 * stride) {
-        const u32x4 a = ld16(s + i * 16), b = ld16(s + (i + stride) * 16);
-        const u32x4 c = ld16(s + (i + 2 * stride) * 16), e = ld16(s + (i + 3 * stride) * 16);
-        st16(d + i * 16, a);
-        st16(d + (i + stride) * 16, b);
-        st16(d + (i + 2 * stride) * 16, c);
-        st16(d + (i + 3 * stride) * 16, e);
+// Device-to-device copies, used where the source is another process's memory mapped by a memory handle (which the
+// runtime's own copy may hand to a copy engine).  When source and destination share their alignment modulo 16 the
+// copy is cut into 16 KiB tiles, one per workgroup, each thread issuing its four 16-byte loads before its four
+// non-temporal stores (the shape that measures fastest for a plain copy on this part); one extra workgroup copies the
+// unaligned head and the tail.  Other pairs take a grid-stride byte loop.
+constexpr uint64_t kCopyTile = 256 * 4 * 16;
+
+__global__ void __launch_bounds__(256) copy_tiles_kernel(uint8_t* dst, const uint8_t* src, uint64_t n, uint64_t pre,
+                                                        uint64_t tiles) {
+    const uint32_t tid = threadIdx.x;
+    if (blockIdx.x < tiles) {
+        const uint64_t base = pre + uint64_t(blockIdx.x) * kCopyTile;
+        u32x4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = ld16(src + base + (u * 256 + tid) * 16);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) st16(dst + base + (u * 256 + tid) * 16, v[u]);
+        return;
     }
-    for (; i < body; i += stride) st16(d + i * 16, ld16(s + i * 16));
-    for (uint64_t j = pre + body * 16 + gid; j < n; j += stride) dst[j] = src[j];
+    for (uint64_t i = tid; i < pre; i += 256) dst[i] = src[i];
+    const uint64_t tail0 = pre + tiles * kCopyTile;
+    const uint64_t vecs = (n - tail0) / 16;
+    for (uint64_t i = tid; i < vecs; i += 256) st16(dst + tail0 + i * 16, ld16(src + tail0 + i * 16));
+    for (uint64_t i = tail0 + vecs * 16 + tid; i < n; i += 256) dst[i] = src[i];
+}
+
+__global__ void __launch_bounds__(256) copy_bytes_kernel(uint8_t* dst, const uint8_t* src, uint64_t n) {
+    const uint64_t stride = uint64_t(gridDim.x) * 256;
+    for (uint64_t i = uint64_t(blockIdx.x) * 256 + threadIdx.x; i < n; i += stride) dst[i] = src[i];
 }
 
 // Reads its share of the K/V bytes and folds them into one word per workgroup.
@@ -795,10 +800,20 @@ hipError_t launch_fill_bytes(void* dst, uint8_t value, uint64_t n, hipStream_t s
 
 hipError_t launch_copy_bytes(void* dst, const void* src, uint64_t n, hipStream_t stream) {
     if (!n) return hipSuccess;
-    // four 16-byte vectors per thread and pass; capped so that every CU holds several workgroups
-    const uint64_t blocks = (n / 16 + 1023) / 1024;
-    hipLaunchKernelGGL(copy_bytes_kernel, dim3(unsigned(blocks < 16384 ? (blocks ? blocks : 1) : 16384)), dim3(256), 0,
-                       stream, static_cast<uint8_t*>(dst), static_cast<const uint8_t*>(src), n);
+    auto* d = static_cast<uint8_t*>(dst);
+    auto* s = static_cast<const uint8_t*>(src);
+    const uintptr_t da = reinterpret_cast<uintptr_t>(d), sa = reinterpret_cast<uintptr_t>(s);
+    if (((da ^ sa) & 15u) != 0) {
+        const uint64_t blocks = (n + 255) / 256;
+        hipLaunchKernelGGL(copy_bytes_kernel, dim3(unsigned(blocks < 16384 ? blocks : 16384)), dim3(256), 0, stream, d, s,
+                           n);
+        return hipGetLastError();
+    }
+    const uint64_t head = (16u - (da & 15u)) & 15u;
+    const uint64_t pre = head < n ? head : n;
+    const uint64_t tiles = (n - pre) / kCopyTile;
+    if (tiles + 1 > 0x7FFFFFFFull) return hipErrorInvalidValue;   // 32 TiB: beyond any allocation here
+    hipLaunchKernelGGL(copy_tiles_kernel, dim3(unsigned(tiles + 1)), dim3(256), 0, stream, d, s, n, pre, tiles);
     return hipGetLastError();
 }
 

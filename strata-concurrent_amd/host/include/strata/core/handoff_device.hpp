@@ -37,6 +37,8 @@ struct HandoffMoveStats {
     uint64_t bytes = 0;
     double ms = 0.0;
     double hash_ms = 0.0;   ///< the part of `ms` spent waiting for the device hash after the copies (reader)
+    double copy_ms = 0.0;   ///< host threads copying between staging and the slot
+    double wait_ms = 0.0;   ///< waiting for DMA (a staging buffer's event, the stream at the end)
     bool wrote_device = false;   ///< a failed read that had already written device memory
     bool device_error = false;   ///< the failure was a device call's
 };

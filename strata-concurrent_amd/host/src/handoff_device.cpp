@@ -211,9 +211,13 @@ bool HandoffMover::write_from_device(HandoffArena& arena, const HandoffClaim& cl
     uint64_t issued = 0;
     for (; issued < std::min(R, n_chunks) && ok; ++issued) ok = enqueue(issued);
     for (uint64_t k = 0; k < n_chunks && ok; ++k) {
+        const auto tw = std::chrono::steady_clock::now();
         ok = sc_event_sync(done_[k % R]) == SC_OK;
         if (!ok) break;
+        const auto tc = std::chrono::steady_clock::now();
         crew_->copy(window + k * C, stage_[k % R], std::min(C, bytes - k * C));
+        last_.wait_ms += std::chrono::duration<double, std::milli>(tc - tw).count();
+        last_.copy_ms += ms_since(tc);
         if (issued < n_chunks) ok = enqueue(issued++);
     }
     if (!ok) {
@@ -266,14 +270,20 @@ bool HandoffMover::read_to_device(HandoffArena& arena, int index, uint64_t nonce
     last_.wrote_device = bytes != 0;
     bool ok = true;
     for (uint64_t k = 0; k < n_chunks && ok; ++k) {
+        const auto tw = std::chrono::steady_clock::now();
         if (k >= R) ok = sc_event_sync(done_[k % R]) == SC_OK;   // the DMA that last read this staging buffer is done
         if (!ok) break;
+        const auto tc = std::chrono::steady_clock::now();
         const uint64_t len = std::min(C, bytes - k * C);
         crew_->copy(stage_[k % R], p.data + k * C, len);
+        last_.wait_ms += std::chrono::duration<double, std::milli>(tc - tw).count();
+        last_.copy_ms += ms_since(tc);
         ok = sc_copy_async(dst + k * C, stage_[k % R], len, stream) == SC_OK &&
              sc_event_record(done_[k % R], stream) == SC_OK;
     }
+    const auto tf = std::chrono::steady_clock::now();
     if (ok) ok = sc_stream_sync(stream) == SC_OK;
+    last_.wait_ms += ms_since(tf);
     if (!ok) {
         err = abi_error("handoff mover slot-to-device copy");
         last_.device_error = true;

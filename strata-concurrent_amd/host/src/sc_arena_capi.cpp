@@ -322,12 +322,14 @@ int sc_mover_read(sc_mover* mover, sc_arena* arena, int32_t index, uint64_t nonc
     });
 }
 
-int sc_mover_last(const sc_mover* mover, uint64_t* bytes, double* ms, double* hash_ms) {
+int sc_mover_last(const sc_mover* mover, uint64_t* bytes, double* ms, double* hash_ms, double* copy_ms, double* wait_ms) {
     if (!mover) return fail(SC_EINVAL, "sc_arena: missing mover");
     const auto& st = mover->mover.last();
     if (bytes) *bytes = st.bytes;
     if (ms) *ms = st.ms;
     if (hash_ms) *hash_ms = st.hash_ms;
+    if (copy_ms) *copy_ms = st.copy_ms;
+    if (wait_ms) *wait_ms = st.wait_ms;
     return SC_OK;
 }
 

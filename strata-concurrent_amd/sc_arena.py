@@ -52,7 +52,7 @@ _SIGS = {
     "sc_mover_write": (C.c_int, [_P, _P, C.POINTER(Claim), _P, _U64, _P, _PU64]),
     "sc_mover_publish": (C.c_int, [_P, _P, C.POINTER(Claim), _P, _U64, _U64, _P]),
     "sc_mover_read": (C.c_int, [_P, _P, _I32, _U64, _U64, _P, _U64, _P, _I32, C.POINTER(Slot)]),
-    "sc_mover_last": (C.c_int, [_P, _PU64, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
+    "sc_mover_last": (C.c_int, [_P, _PU64] + [C.POINTER(C.c_double)] * 4),
 }
 for _name, (_res, _args) in _SIGS.items():
     _fn = getattr(lib, _name)
@@ -189,6 +189,8 @@ class Mover:
         return s
 
     def last(self):
-        b, ms, hms = C.c_uint64(), C.c_double(), C.c_double()
-        _check(lib.sc_mover_last(self.handle, C.byref(b), C.byref(ms), C.byref(hms)), "sc_mover_last")
-        return b.value, ms.value, hms.value
+        """(bytes, ms, hash_ms, copy_ms, wait_ms) of the last transfer."""
+        b, ms, hms, cms, wms = C.c_uint64(), C.c_double(), C.c_double(), C.c_double(), C.c_double()
+        _check(lib.sc_mover_last(self.handle, C.byref(b), C.byref(ms), C.byref(hms), C.byref(cms), C.byref(wms)),
+               "sc_mover_last")
+        return b.value, ms.value, hms.value, cms.value, wms.value
