@@ -414,6 +414,9 @@ def arena_handoff(sc, geo, tokens: int, slot, link_h2d: float, link_d2h: float, 
         w = sc_arena.Arena.writer(path, [(tokens, 1)], [n], pack, geom, reserve=True)   # re-open: pages committed, mapped
         out["reserve_ms"] = round((time.perf_counter() - t0) * 1e3, 1)
         r = sc_arena.Arena.reader(path, pack, geom)
+        t0 = time.perf_counter()
+        r.reserve()                                       # the reader's one mapping of the arena, populated
+        out["reader_reserve_ms"] = round((time.perf_counter() - t0) * 1e3, 1)
         dst = sc.new_slot(geo, tokens, fill=0)
         pub, mpub, rd, rdv, mnt, opn, rim, rim_mover = [], [], [], [], [], [], [], []
         for rep in range(reps):
@@ -425,8 +428,9 @@ def arena_handoff(sc, geo, tokens: int, slot, link_h2d: float, link_d2h: float, 
             w.release(c.index, c.nonce)
             c = w.claim(0, 7, 2 + rep)
             stream.sync()                                   # the payload is in place: the mover alone
+            t0 = time.perf_counter()
             mover.publish(w, c, payload.ptr, n, tokens, stream.handle)
-            mpub.append(mover.last()[1])
+            mpub.append((time.perf_counter() - t0) * 1e3)
             t0 = time.perf_counter()
             s = mover.read(r, c.index, c.nonce, 7, arrived.ptr, n, stream.handle, verify=False)
             t1 = time.perf_counter()
@@ -438,10 +442,12 @@ def arena_handoff(sc, geo, tokens: int, slot, link_h2d: float, link_d2h: float, 
             opn.append((t2 - t1) * 1e3)
             rim.append((t1 - t0) * 1e3)
             dec.destroy()
+            t0 = time.perf_counter()
             mover.read(r, c.index, c.nonce, 7, arrived.ptr, n, stream.handle, verify=False)
-            rd.append(mover.last()[1])
+            rd.append((time.perf_counter() - t0) * 1e3)
+            t0 = time.perf_counter()
             mover.read(r, c.index, c.nonce, 7, arrived.ptr, n, stream.handle, verify=True)
-            rdv.append(mover.last()[1])
+            rdv.append((time.perf_counter() - t0) * 1e3)
             w.release(c.index, c.nonce)
         same = all(sc.fnv1a64_device(a.ptr, a.nbytes) == sc.fnv1a64_device(b.ptr, b.nbytes)
                    for a, b in zip(slot.buffers(), dst.buffers()))
@@ -471,8 +477,9 @@ def arena_handoff(sc, geo, tokens: int, slot, link_h2d: float, link_d2h: float, 
                   "slot's mapped window while later chunks are in flight, device FNV-1a on a side stream) + the "
                   "arena's publish; mover_publish = the same with the payload already encoded; read = mover (host threads copy slot chunks into pinned buffers, H2D of each "
                   "while the next is copied); read_verified adds the device FNV-1a check; read_and_mount = read + "
-                  "device mount with its hash check; host wall clock, best of the reps; arena reserved "
-                  "(posix_fallocate + populated mapping) before the timed reps"})
+                  "device mount with its hash check; host wall clock around each call, best of the reps; the writer's "
+                  "arena reserved (posix_fallocate + populated mapping) and the reader's mapping populated before the "
+                  "timed reps"})
     return out
 
 

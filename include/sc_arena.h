@@ -60,6 +60,9 @@ int sc_arena_open_writer(const char* path, int32_t n_tiers, const uint64_t* tier
 /* HandoffArena::open_reader (src/core/handoff.cpp:978-1018). */
 int sc_arena_open_reader(const char* path, uint64_t pack_hash, uint64_t geom_hash, sc_arena** out);
 int sc_arena_close(sc_arena* arena);
+/* HandoffArena::reserve: a writer commits every page of the file and maps it populated; a reader maps it read-only
+ * populated (this library's addition, for the device movers; a start-up cost paid once per arena). */
+int sc_arena_reserve(sc_arena* arena);
 
 /* HandoffArena::claim / write_payload / publish / release / abort_claim / cancel (src/core/handoff.cpp:729-976).
  * sc_arena_claim_slot answers SC_EBUSY (not an error: queue the job) when no slot of the tier or above is free. */

@@ -19,8 +19,8 @@
 // a shared flock; payload bytes are never written or read under the lock.
 //
 // The payload movers between HBM and a slot (pinned staging, parallel host copies, the device hash) are in
-// handoff_device.hpp; this file is host-only and makes no device call.  Its two additions to the reference's API
-// (claim_window, reserve) serve those movers.
+// handoff_device.hpp; this file is host-only and makes no device call.  Its three additions to the reference's API
+// (claim_window, read_window, reserve) serve those movers.
 #pragma once
 
 #include <array>
@@ -338,10 +338,15 @@ class HandoffArena {
     /// tmpfs file is serialized) and page tables are set up once, not per hand-off.  Null + err when the claim does
     /// not match this arena's slot table.
     uint8_t* claim_window(const HandoffClaim& c, std::string& err);
-    /// Commit every page of the arena file now (posix_fallocate: a full filesystem is an error here instead of a
-    /// SIGBUS in the middle of a payload copy) and populate the writer's mapping, so the first hand-off through each
-    /// slot does not pay page allocation and faults.  Writer only.
+    /// Writer: commit every page of the arena file now (posix_fallocate: a full filesystem is an error here instead
+    /// of a SIGBUS in the middle of a payload copy) and populate its mapping, so the first hand-off through each slot
+    /// does not pay page allocation and faults.  Reader: map the file read-only with its page tables populated.
     bool reserve(std::string& err);
+    /// Reader: every check of read_slot, then the slot's first payload byte inside one read-only mapping of the whole
+    /// arena that the reader keeps until it closes the arena (no mapping is made or torn down per read; tearing down
+    /// a 3 GB mapping costs ~17 ms).  `info` is the slot header as checked.  Null + err on refusal.
+    const uint8_t* read_window(int index, uint64_t expect_nonce, uint64_t client_id, HandoffSlotInfo& info,
+                               std::string& err);
 
     // -- the reader (a decode instance) --
 
@@ -392,10 +397,12 @@ class HandoffArena {
     uint64_t count_free_() const;                           // needs the lock
 
     bool map_all_(bool populate, std::string& err);
+    bool ready_slot_(int index, uint64_t expect_nonce, uint64_t client_id, HandoffSlotHeader& s, Place& p,
+                     std::string& err) const;
 
     int fd_ = -1;
     bool writer_ = false;
-    uint8_t* map_ = nullptr;      ///< the writer's mapping of the whole file, or null
+    uint8_t* map_ = nullptr;      ///< the whole file, mapped once for the device movers (writable for the writer)
     uint64_t map_bytes_ = 0;
     std::string path_;
     HandoffArenaHeader hdr_{};

@@ -896,7 +896,8 @@ bool HandoffArena::cancel(int index, uint64_t nonce, std::string& err) {
 
 bool HandoffArena::map_all_(bool populate, std::string& err) {
     if (map_) return true;
-    void* m = ::mmap(nullptr, (size_t) hdr_.arena_bytes, PROT_READ | PROT_WRITE,
+    // the writer's mapping is writable; a reader's is read-only (its descriptor is too)
+    void* m = ::mmap(nullptr, (size_t) hdr_.arena_bytes, writer_ ? PROT_READ | PROT_WRITE : PROT_READ,
                      MAP_SHARED | (populate ? MAP_POPULATE : 0), fd_, 0);
     if (m == MAP_FAILED) {
         err = "cannot map the handoff arena " + path_ + ": " + std::strerror(errno);
@@ -924,7 +925,14 @@ uint8_t* HandoffArena::claim_window(const HandoffClaim& c, std::string& err) {
 bool HandoffArena::reserve(std::string& err) {
     std::lock_guard<std::mutex> guard(mu_);
     if (fd_ < 0) { err = "the handoff arena is not open"; return false; }
-    if (!writer_) { err = "only the writer reserves the handoff arena"; return false; }
+    if (!writer_) {
+        // a reader commits nothing: it maps the file read-only with its page tables populated
+        if (map_) {
+            ::munmap(map_, (size_t) map_bytes_);
+            map_ = nullptr;
+        }
+        return map_all_(true, err);
+    }
     const int rc = ::posix_fallocate(fd_, 0, (off_t) hdr_.arena_bytes);
     if (rc != 0) {
         err = "cannot commit the " + num(hdr_.arena_bytes) + " B of handoff arena " + path_ + ": " + std::strerror(rc);
@@ -1012,16 +1020,12 @@ bool HandoffArena::slot_info(int index, HandoffSlotInfo& out) const {
     return true;
 }
 
-bool HandoffArena::read_slot(int index, uint64_t expect_nonce, uint64_t client_id, HandoffPayload& out,
-                             std::string& err) {
-    // src/core/handoff.cpp:1053-1131: the header under a shared lock, every check, then a PROT_READ mapping of the
-    // payload region only (from the page holding its first byte)
-    std::lock_guard<std::mutex> guard(mu_);
-    out = HandoffPayload{};
+/// The slot header under a shared lock and every check a reader makes before it copies a byte
+/// (src/core/handoff.cpp:1053-1111).  The caller holds mu_.
+bool HandoffArena::ready_slot_(int index, uint64_t expect_nonce, uint64_t client_id, HandoffSlotHeader& s, Place& p,
+                               std::string& err) const {
     if (fd_ < 0) { err = "the handoff arena is not open"; return false; }
     if (writer_) { err = "open the arena as a reader to read a handoff slot"; return false; }
-    HandoffSlotHeader s{};
-    Place p;
     {
         FileLock lock(fd_, false);
         if (!lock.held()) { err = lock.error(); return false; }
@@ -1062,6 +1066,18 @@ bool HandoffArena::read_slot(int index, uint64_t expect_nonce, uint64_t client_i
         err = slot + " has seq " + num(s.seq) + "; this protocol version reads seq 1 only";
         return false;
     }
+    return true;
+}
+
+bool HandoffArena::read_slot(int index, uint64_t expect_nonce, uint64_t client_id, HandoffPayload& out,
+                             std::string& err) {
+    // src/core/handoff.cpp:1053-1131: every check, then a PROT_READ mapping of the payload region only (from the
+    // page holding its first byte)
+    std::lock_guard<std::mutex> guard(mu_);
+    out = HandoffPayload{};
+    HandoffSlotHeader s{};
+    Place p;
+    if (!ready_slot_(index, expect_nonce, client_id, s, p, err)) return false;
     const uint64_t first = p.base + kHandoffHeaderBytes;
     const long ps = ::sysconf(_SC_PAGESIZE);
     const uint64_t page = ps > 0 ? (uint64_t) ps : 4096;
@@ -1069,7 +1085,7 @@ bool HandoffArena::read_slot(int index, uint64_t expect_nonce, uint64_t client_i
     const uint64_t span = lead + std::max<uint64_t>(s.payload_bytes, 1);
     void* m = ::mmap(nullptr, (size_t) span, PROT_READ, MAP_SHARED, fd_, (off_t) (first - lead));
     if (m == MAP_FAILED) {
-        err = "cannot map " + slot + ": " + std::strerror(errno);
+        err = "cannot map handoff slot " + num(index) + ": " + std::strerror(errno);
         return false;
     }
     out.bind_mapping(m, span, static_cast<const uint8_t*>(m) + lead, s.payload_bytes);
@@ -1083,6 +1099,36 @@ bool HandoffArena::read_slot(int index, uint64_t expect_nonce, uint64_t client_i
     out.payload_hash = s.payload_hash;
     out.seq = s.seq;
     return true;
+}
+
+const uint8_t* HandoffArena::read_window(int index, uint64_t expect_nonce, uint64_t client_id, HandoffSlotInfo& info,
+                                         std::string& err) {
+    std::lock_guard<std::mutex> guard(mu_);
+    info = HandoffSlotInfo{};
+    HandoffSlotHeader s{};
+    Place p;
+    if (!ready_slot_(index, expect_nonce, client_id, s, p, err)) return nullptr;
+    if (!map_all_(false, err)) return nullptr;
+    info.index = index;
+    info.base = p.base;
+    info.capacity = p.capacity;
+    info.state = s.state;
+    info.flags = s.flags;
+    info.tier = s.tier;
+    info.owner_pid = s.owner_pid;
+    info.owner_start = s.owner_start;
+    info.nonce = s.nonce;
+    info.client_id = s.client_id;
+    info.request_id = s.request_id;
+    info.pack_hash = s.pack_hash;
+    info.geom_hash = s.geom_hash;
+    info.tokens = s.tokens;
+    info.payload_bytes = s.payload_bytes;
+    info.payload_hash = s.payload_hash;
+    info.claimed_ms = s.claimed_ms;
+    info.published_ms = s.published_ms;
+    info.seq = s.seq;
+    return map_ + p.base + kHandoffHeaderBytes;
 }
 
 uint64_t HandoffArena::payload_hash_of(const HandoffPayload& p) {

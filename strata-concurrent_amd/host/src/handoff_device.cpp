@@ -250,13 +250,9 @@ bool HandoffMover::read_to_device(HandoffArena& arena, int index, uint64_t nonce
     last_ = HandoffMoveStats{};
     info = HandoffSlotInfo{};
     if (!ready()) { err = "handoff mover: not initialised"; return false; }
-    HandoffPayload p;
-    if (!arena.read_slot(index, nonce, client_id, p, err)) return false;
-    if (!arena.slot_info(index, info) || info.nonce != nonce) {
-        err = "handoff slot " + std::to_string(index) + " changed while it was opened";
-        return false;
-    }
-    const uint64_t bytes = p.payload_bytes;
+    const uint8_t* data = arena.read_window(index, nonce, client_id, info, err);
+    if (!data) return false;
+    const uint64_t bytes = info.payload_bytes;
     if (bytes > dst_capacity) {
         err = "handoff slot " + std::to_string(index) + " holds a " + std::to_string(bytes) +
               " B payload and the device buffer has room for " + std::to_string(dst_capacity) + " B";
@@ -275,7 +271,7 @@ bool HandoffMover::read_to_device(HandoffArena& arena, int index, uint64_t nonce
         if (!ok) break;
         const auto tc = std::chrono::steady_clock::now();
         const uint64_t len = std::min(C, bytes - k * C);
-        crew_->copy(stage_[k % R], p.data + k * C, len);
+        crew_->copy(stage_[k % R], data + k * C, len);
         last_.wait_ms += std::chrono::duration<double, std::milli>(tc - tw).count();
         last_.copy_ms += ms_since(tc);
         ok = sc_copy_async(dst + k * C, stage_[k % R], len, stream) == SC_OK &&
@@ -293,7 +289,7 @@ bool HandoffMover::read_to_device(HandoffArena& arena, int index, uint64_t nonce
     // is refused rather than mounted
     HandoffSlotInfo after;
     if (!arena.slot_info(index, after) || after.state != kHandoffReady || after.nonce != nonce ||
-        after.payload_bytes != bytes || after.payload_hash != p.payload_hash || after.published_ms != info.published_ms) {
+        after.payload_bytes != bytes || after.payload_hash != info.payload_hash || after.published_ms != info.published_ms) {
         err = "handoff slot " + std::to_string(index) + " was released or reclaimed while it was read";
         return false;
     }
@@ -302,10 +298,10 @@ bool HandoffMover::read_to_device(HandoffArena& arena, int index, uint64_t nonce
         uint64_t h = kEngineSeed;
         if (bytes && (!hash_on_device_(device_dst, bytes, stream, err) || !fetch_hash_(&h, err))) return false;
         last_.hash_ms = ms_since(th);
-        if (h != p.payload_hash) {
+        if (h != info.payload_hash) {
             char buf[160];
             std::snprintf(buf, sizeof buf, "handoff slot %d: the payload hash is %016llx but the slot records %016llx",
-                          index, (unsigned long long) h, (unsigned long long) p.payload_hash);
+                          index, (unsigned long long) h, (unsigned long long) info.payload_hash);
             err = buf;
             return false;
         }

@@ -173,6 +173,14 @@ int sc_arena_close(sc_arena* arena) {
     return SC_OK;
 }
 
+int sc_arena_reserve(sc_arena* arena) {
+    return guarded([&] {
+        if (!arena) return fail(SC_EINVAL, "sc_arena: missing arena");
+        std::string err;
+        return arena->arena.reserve(err) ? (int) SC_OK : fail(SC_EINVAL, err);
+    });
+}
+
 int sc_arena_claim_slot(sc_arena* arena, uint32_t tier, uint64_t client_id, uint64_t request_id, sc_arena_claim* out) {
     return guarded([&] {
         if (!arena || !out) return fail(SC_EINVAL, "sc_arena: missing arena or output");

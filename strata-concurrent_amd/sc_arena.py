@@ -39,6 +39,7 @@ _SIGS = {
                                        C.POINTER(_P)]),
     "sc_arena_open_reader": (C.c_int, [C.c_char_p, _U64, _U64, C.POINTER(_P)]),
     "sc_arena_close": (C.c_int, [_P]),
+    "sc_arena_reserve": (C.c_int, [_P]),
     "sc_arena_claim_slot": (C.c_int, [_P, _U32, _U64, _U64, C.POINTER(Claim)]),
     "sc_arena_write": (C.c_int, [_P, C.POINTER(Claim), _U64, _P, _U64]),
     "sc_arena_publish": (C.c_int, [_P, C.POINTER(Claim), _U64, _U64, _U64]),
@@ -113,6 +114,10 @@ class Arena:
         if self.handle:
             lib.sc_arena_close(self.handle)
             self.handle = None
+
+    def reserve(self):
+        """Writer: commit the file's pages and map them; reader: map the file read-only, populated."""
+        _check(lib.sc_arena_reserve(self.handle), "sc_arena_reserve")
 
     def __enter__(self):
         return self

@@ -460,8 +460,8 @@ int main() {
         HandoffClaim rc;
         expect(!r.claim(0, 1, 1, rc, err) && has(err, "reader never claims"), "a reader does not claim", err);
         expect(!r.write_payload(d, 0, blob.data(), 16, err) && !r.publish(d, 1, 16, 1, err) && !r.release(0, 1, err) &&
-                   !r.abort_claim(0, 1, err) && !r.cancel(0, 1, err) && !r.claim_window(d, err) && !r.reserve(err),
-               "nor write, publish, release, abort, cancel, map or reserve");
+                   !r.abort_claim(0, 1, err) && !r.cancel(0, 1, err) && !r.claim_window(d, err),
+               "nor write, publish, release, abort, cancel or map a claim");
         HandoffPayload p;
         expect(!a.read_slot(0, 1, 1, p, err) && has(err, "as a reader"), "a writer does not read slots", err);
     }
@@ -804,6 +804,20 @@ int main() {
         HandoffClaim fake = c;
         fake.payload_off += 64;
         expect(a.claim_window(fake, err) == nullptr && has(err, "slot table"), "a window only for a real claim", err);
+        // the reader's window: the same checks as read_slot, the same bytes, one mapping for every read
+        HandoffSlotInfo wi;
+        expect(r.reserve(err), "a reader maps the arena read-only, populated", err);
+        const uint8_t* rw = r.read_window(c.index, c.nonce, 5, wi, err);
+        expect(rw != nullptr && wi.payload_bytes == n && wi.payload_hash == h && wi.tokens == 65536 && wi.nonce == c.nonce &&
+                   fnv1a64(rw, n) == h,
+               "read_window gives the published bytes and the checked header", err);
+        expect(r.read_window(c.index, c.nonce, 5, wi, err) == rw, "and the same mapping on the next read");
+        expect(r.read_window(c.index, c.nonce ^ 1, 5, wi, err) == nullptr && has(err, "nonce"), "another nonce", err);
+        expect(r.read_window(c.index, c.nonce, 6, wi, err) == nullptr && has(err, "addressed to client"), "another client",
+               err);
+        expect(r.read_window(0, c.nonce, 5, wi, err) == nullptr && has(err, "not READY"), "a FREE slot", err);
+        expect(a.read_window(c.index, c.nonce, 5, wi, err) == nullptr && has(err, "as a reader"), "a writer has no read window",
+               err);
         HandoffArena moved = std::move(a);
         expect(moved.valid() && !a.valid() && moved.claim_window(c, err) == win, "the window moves with the arena");
         expect(moved.release(c.index, c.nonce, err), "release", err);
