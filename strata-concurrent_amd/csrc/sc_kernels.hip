@@ -279,8 +279,33 @@ __device__ __forceinline__ float dpp(float v) {
     return __uint_as_float(dpp<kCtrl>(__float_as_uint(v)));
 }
 
+// The maximum over a 16-lane DPP row of non-negative, non-NaN floats, as unsigned integers: for such values the bit
+// patterns order as the numbers do, so the comparison needs no NaN handling and each step folds into one DPP max.
+__device__ __forceinline__ float row16_max_nonneg(float a) {
+    uint32_t u = __float_as_uint(a);
+    u = max(u, uint32_t(__builtin_amdgcn_update_dpp(0, int(u), kDppXor1, 0xF, 0xF, true)));
+    u = max(u, uint32_t(__builtin_amdgcn_update_dpp(0, int(u), kDppXor2, 0xF, 0xF, true)));
+    u = max(u, uint32_t(__builtin_amdgcn_update_dpp(0, int(u), kDppHalfMirror, 0xF, 0xF, true)));
+    u = max(u, uint32_t(__builtin_amdgcn_update_dpp(0, int(u), kDppMirror, 0xF, 0xF, true)));
+    return __uint_as_float(u);
+}
+
+// a / 127 for a >= 0 (not NaN), the correctly rounded quotient, by the same single correction as q8_code from the
+// correctly rounded 1/127 (127 = 1.984375 x 2^6 is one of the divisors the exhaustive quotient check covers, so the
+// result is the IEEE quotient wherever nothing leaves the normal range; below it, a < 2^-100, both are far below
+// the smallest binary16 and round to the same +0).  +inf stays +inf (the correction would make it NaN).
+__device__ __forceinline__ float div127(float a) {
+#pragma clang fp contract(off)
+    constexpr float kInv127 = 1.0f / 127.0f;
+    const float q0 = a * kInv127;
+    const float q = __builtin_fmaf(__builtin_fmaf(-q0, 127.0f, a), kInv127, q0);
+    return a == __builtin_inff() ? a : q;
+}
+
 // The wave's rows of a tile, all loads (rows and their pages' table entries) issued before any row is quantized:
 // four 1 KiB reads in flight per wave.
+// `wave` is wave-uniform (the caller reads it with readfirstlane), so every row index, page-table entry and pool
+// row below is scalar work: the vector units only carry the rows' values.
 __device__ __forceinline__ int load_units(const MoveRow& r, const MoveGeo& g, uint64_t local, int lane, int wave,
                                           u32x4 (&v)[kQuantUnitsPerWave], uint32_t (&unit)[kQuantUnitsPerWave],
                                           int32_t (&phys)[kQuantUnitsPerWave]) {
@@ -295,12 +320,12 @@ __device__ __forceinline__ int load_units(const MoveRow& r, const MoveGeo& g, ui
     }
 #pragma unroll
     for (int i = 0; i < kQuantUnitsPerWave; ++i)
-        if (i < n) phys[i] = table_entry(r, kv_cell(r, g, unit[i]).page);
+        if (i < n) phys[i] = __builtin_amdgcn_readfirstlane(table_entry(r, kv_cell(r, g, unit[i]).page));
     return n;
 }
 
 __device__ void tile_q8(const MoveRow& r, const MoveGeo& g, uint64_t local) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     u32x4 vs[kQuantUnitsPerWave];
     uint32_t units[kQuantUnitsPerWave];
     int32_t phys[kQuantUnitsPerWave];
@@ -314,12 +339,8 @@ __device__ void tile_q8(const MoveRow& r, const MoveGeo& g, uint64_t local) {
                     x3 = __uint_as_float(v.w);
         // max |x| over the 64 values of this lane's group, the 16 lanes of its DPP row (fmax is exact, so any
         // order gives the same).  It starts from 0, so NaNs never count and a group of NaNs has scale 0.
-        float a = fmaxf(fmaxf(fmaxf(fabsf(x0), fabsf(x1)), fmaxf(fabsf(x2), fabsf(x3))), 0.0f);
-        a = fmaxf(a, dpp<kDppXor1>(a));
-        a = fmaxf(a, dpp<kDppXor2>(a));
-        a = fmaxf(a, dpp<kDppHalfMirror>(a));
-        a = fmaxf(a, dpp<kDppMirror>(a));
-        const uint32_t sb = f16_bits_rne(__float_as_uint(a / 127.0f));
+        const float a = row16_max_nonneg(fmaxf(fmaxf(fmaxf(fabsf(x0), fabsf(x1)), fmaxf(fabsf(x2), fabsf(x3))), 0.0f));
+        const uint32_t sb = f16_bits_rne_not_nan(div127(a));   // a is never NaN, nor is a / 127
         const float sf = f32_of_f16(sb);
         const float y = 1.0f / sf;
         const uint32_t codes = q8_code(x0, sf, y) | (q8_code(x1, sf, y) << 8) | (q8_code(x2, sf, y) << 16) |
@@ -338,14 +359,39 @@ __device__ void tile_q8(const MoveRow& r, const MoveGeo& g, uint64_t local) {
     }
 }
 
-// The q4_0 block maximum: larger |x|, then larger value, then lower index (so the sign of a zero maximum is the
-// first zero's).  A NaN never compares larger, so it is never picked; the start (amax -1, value +0) stands for a
-// block of NaNs.  The pick is the maximum of a total order, so any pairing of candidates gives the same result.
-__device__ __forceinline__ void q4_pick(float& amax, float& mval, uint32_t& idx, float a, float v, uint32_t j) {
-    const bool take = a > amax || (a == amax && (v > mval || (v == mval && j < idx)));
-    amax = take ? a : amax;
-    mval = take ? v : mval;
-    idx = take ? j : idx;
+// The q4_0 block's chosen value: the candidate of largest |x|, then of larger value, then of lower index; a NaN is
+// never chosen and a block of NaNs chooses +0.  Only three facts decide it, each the maximum of an unsigned key
+// over the block's 32 values (four per lane, then a DPP max over the block's 8 lanes):
+//   m  = max over non-NaN x of bits(|x|) + 1 (0: no candidate)  -> |chosen| = the value of bits m - 1;
+//   p  = max over x > 0 of bits(x) + 1                          -> the chosen value is +|max| iff p == m (a positive
+//        candidate reaches the maximum; any positive beats the negative of the same magnitude);
+//   z  = max over x == 0 of ((31 - j) << 1 | sign(x)) + 1       -> when the maximum is 0 every candidate is a zero,
+//        all equal as values, so the lowest index j wins and its sign is the low bit.
+// Keys of non-negative floats order as the numbers, so every step is one DPP max without NaN handling.
+__device__ __forceinline__ uint32_t half16_max(uint32_t u) {
+    u = max(u, uint32_t(__builtin_amdgcn_update_dpp(0, int(u), kDppXor1, 0xF, 0xF, true)));
+    u = max(u, uint32_t(__builtin_amdgcn_update_dpp(0, int(u), kDppXor2, 0xF, 0xF, true)));
+    u = max(u, uint32_t(__builtin_amdgcn_update_dpp(0, int(u), kDppHalfMirror, 0xF, 0xF, true)));
+    return u;
+}
+
+__device__ __forceinline__ float q4_chosen(const float (&x)[4], uint32_t lb) {
+    uint32_t m = 0, p = 0, z = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const uint32_t bits = __float_as_uint(x[k]);
+        const uint32_t mag = bits & 0x7FFFFFFFu;
+        const bool real = x[k] == x[k];
+        m = max(m, real ? mag + 1u : 0u);
+        p = max(p, x[k] > 0.0f ? bits + 1u : 0u);
+        z = max(z, real && mag == 0u ? (((31u - (lb * 4u + uint32_t(k))) << 1) | (bits >> 31)) + 1u : 0u);
+    }
+    m = half16_max(m);
+    p = half16_max(p);
+    z = half16_max(z);
+    const float amax = __uint_as_float(m - 1u);
+    const float zero = __uint_as_float(((z - 1u) & 1u) << 31);
+    return m == 0u ? 0.0f : amax > 0.0f ? (p == m ? amax : -amax) : zero;
 }
 
 __device__ __forceinline__ uint32_t q4_code(float x, float id) {
@@ -357,7 +403,7 @@ __device__ __forceinline__ uint32_t q4_code(float x, float id) {
 }
 
 __device__ void tile_q4(const MoveRow& r, const MoveGeo& g, uint64_t local) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lb = lane & 7;            // lane within its 32-value block
     const uint32_t blk = uint32_t(lane >> 3);
     u32x4 vs[kQuantUnitsPerWave];
@@ -370,15 +416,7 @@ __device__ void tile_q4(const MoveRow& r, const MoveGeo& g, uint64_t local) {
         const uint32_t unit = units[i];
         const u32x4 v = vs[i];
         const float x[4] = {__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w)};
-        float amax = -1.0f, mval = 0.0f;
-        uint32_t idx = 32u;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) q4_pick(amax, mval, idx, fabsf(x[k]), x[k], uint32_t(lb * 4 + k));
-        // the pick is a maximum under a total order, so pairing within quads, then the two quads of the block,
-        // reaches every lane's candidate
-        q4_pick(amax, mval, idx, dpp<kDppXor1>(amax), dpp<kDppXor1>(mval), dpp<kDppXor1>(idx));
-        q4_pick(amax, mval, idx, dpp<kDppXor2>(amax), dpp<kDppXor2>(mval), dpp<kDppXor2>(idx));
-        q4_pick(amax, mval, idx, dpp<kDppHalfMirror>(amax), dpp<kDppHalfMirror>(mval), dpp<kDppHalfMirror>(idx));
+        const float mval = q4_chosen(x, uint32_t(lb));
         const float d = mval / -8.0f;
         const float id = d != 0.0f ? 1.0f / d : 0.0f;
         const uint32_t q = q4_code(x[0], id) | (q4_code(x[1], id) << 8) | (q4_code(x[2], id) << 16) |
@@ -389,7 +427,7 @@ __device__ void tile_q4(const MoveRow& r, const MoveGeo& g, uint64_t local) {
         // block `blk` of the row: {f16 d, qs[16]}, 18 bytes at 18 * blk; qs[4 lb .. 4 lb + 3] from lanes lb, lb + 4
         uint8_t* row = r.dst + uint64_t(prow) * (kQuantDim / 32 * 18) + blk * 18;
         using g16 = __attribute__((address_space(1))) uint16_t;
-        if (lb == 0) *(g16*) (row) = uint16_t(f16_bits_rne(__float_as_uint(d)));
+        if (lb == 0) *(g16*) (row) = uint16_t(f16_bits_rne_not_nan(d));   // the chosen value is never NaN
         if (lb < 4) {
             const uint32_t bytes = q | (hi << 4);
             *(g16*) (row + 2 + 4 * lb) = uint16_t(bytes);
