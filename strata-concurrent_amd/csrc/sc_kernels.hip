@@ -17,6 +17,7 @@
 
 #include <cstdint>
 
+#include "sc_arith.hpp"
 #include "sc_convert.hpp"
 #include "sc_internal.hpp"
 
@@ -290,18 +291,6 @@ __device__ __forceinline__ float row16_max_nonneg(float a) {
     return __uint_as_float(u);
 }
 
-// a / 127 for a >= 0 (not NaN), the correctly rounded quotient, by the same single correction as q8_code from the
-// correctly rounded 1/127 (127 = 1.984375 x 2^6 is one of the divisors the exhaustive quotient check covers, so the
-// result is the IEEE quotient wherever nothing leaves the normal range; below it, a < 2^-100, both are far below
-// the smallest binary16 and round to the same +0).  +inf stays +inf (the correction would make it NaN).
-__device__ __forceinline__ float div127(float a) {
-#pragma clang fp contract(off)
-    constexpr float kInv127 = 1.0f / 127.0f;
-    const float q0 = a * kInv127;
-    const float q = __builtin_fmaf(__builtin_fmaf(-q0, 127.0f, a), kInv127, q0);
-    return a == __builtin_inff() ? a : q;
-}
-
 // The wave's rows of a tile, all loads (rows and their pages' table entries) issued before any row is quantized:
 // four 1 KiB reads in flight per wave.
 // `wave` is wave-uniform (the caller reads it with readfirstlane), so every row index, page-table entry and pool
@@ -342,7 +331,7 @@ __device__ void tile_q8(const MoveRow& r, const MoveGeo& g, uint64_t local) {
         const float a = row16_max_nonneg(fmaxf(fmaxf(fmaxf(fabsf(x0), fabsf(x1)), fmaxf(fabsf(x2), fabsf(x3))), 0.0f));
         const uint32_t sb = f16_bits_rne_not_nan(div127(a));   // a is never NaN, nor is a / 127
         const float sf = f32_of_f16(sb);
-        const float y = 1.0f / sf;
+        const float y = recip_normal(sf);   // sf is a binary16 value: 2^-24 <= sf <= 65504 wherever it codes
         const uint32_t codes = q8_code(x0, sf, y) | (q8_code(x1, sf, y) << 8) | (q8_code(x2, sf, y) << 16) |
                                (q8_code(x3, sf, y) << 24);
         const uint32_t s1 = __builtin_amdgcn_readlane(sb, 16), s2 = __builtin_amdgcn_readlane(sb, 32),
@@ -418,7 +407,11 @@ __device__ void tile_q4(const MoveRow& r, const MoveGeo& g, uint64_t local) {
         const float x[4] = {__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w)};
         const float mval = q4_chosen(x, uint32_t(lb));
         const float d = mval / -8.0f;
-        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        // 1 / d: the fast reciprocal where it is exact, the division for the rare blocks of subnormal or infinite d
+        float id = recip_normal(d);
+        const bool fast = recip_normal_ok(d);
+        if (__any(!fast)) id = fast ? id : 1.0f / d;
+        id = d != 0.0f ? id : 0.0f;
         const uint32_t q = q4_code(x[0], id) | (q4_code(x[1], id) << 8) | (q4_code(x[2], id) << 16) |
                            (q4_code(x[3], id) << 24);
         const uint32_t hi = dpp<kDppRowShl4>(q);   // lane lb + 4 holds the block's values 16 + 4 lb .. 19 + 4 lb

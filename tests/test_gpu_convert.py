@@ -49,3 +49,48 @@ def test_f32_of_every_f16(probe):
     nan = np.isnan(want)
     assert np.array_equal(np.isnan(g), nan)
     assert np.array_equal(got[~nan], want.view(np.uint32)[~nan])
+
+
+@pytest.fixture(scope="module")
+def arith(probe):
+    probe.probe_arith_mismatches.argtypes = [C.c_uint32, C.c_uint64, C.c_int, C.POINTER(C.c_ulonglong),
+                                             C.POINTER(C.c_uint32)]
+    probe.probe_arith_mismatches.restype = C.c_int
+    probe.probe_recip.argtypes = [C.c_uint32, C.c_uint64, C.c_void_p]
+    probe.probe_recip.restype = C.c_int
+    return probe
+
+
+def _mismatches(arith, mode, lo, n):
+    total, first = 0, []
+    step = 1 << 30
+    for s in range(lo, lo + n, step):
+        cnt, f = C.c_ulonglong(), (C.c_uint32 * 8)()
+        assert arith.probe_arith_mismatches(s, min(step, lo + n - s), mode, C.byref(cnt), f) == 0
+        total += cnt.value
+        first += [f[i] for i in range(min(8, cnt.value))]
+    return total, first
+
+
+def test_recip_normal_is_the_ieee_reciprocal_over_its_range(arith):
+    """sc_arith.hpp's recip_normal (v_rcp_f32 + one fused Newton step), used by the quantizers for 1/scale, equals
+    the IEEE division 1.0f / d for every binary32 d with 2^-126 <= |d| < 2^126 (counted on the device), and agrees
+    with numpy's division on a random sample (checked here on the CPU)."""
+    total, first = _mismatches(arith, 0, 0, 1 << 32)
+    assert total == 0, [hex(x) for x in first]
+    rng = np.random.default_rng(11)
+    lo = int(rng.integers(0x00800000, 0x7E000000))   # a window of consecutive normal patterns
+    n = 1 << 24
+    got = np.empty(n, np.uint32)
+    assert arith.probe_recip(lo, n, got.ctypes.data) == 0
+    d = np.arange(lo, lo + n, dtype=np.uint64).astype(np.uint32).view(np.float32)
+    want = (np.float32(1.0) / d).view(np.uint32)
+    ok = (np.abs(d) >= np.float32(2.0 ** -126)) & (np.abs(d) < np.float32(2.0 ** 126))
+    assert np.array_equal(got[ok], want[ok])
+
+
+def test_div127_is_the_ieee_quotient_for_every_non_negative_input(arith):
+    """div127 (one product with RN(1/127) and one fused correction), the int8 scale's division, equals a / 127.0f for
+    every non-negative binary32 a including +0, subnormals and +inf (counted on the device)."""
+    total, first = _mismatches(arith, 1, 0, 1 << 31)
+    assert total == 0, [hex(x) for x in first]
