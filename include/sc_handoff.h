@@ -348,6 +348,15 @@ uint64_t sc_fnv1a64_workspace_bytes(uint64_t bytes);
  * sc_fnv1a64_workspace_bytes(bytes); nothing is allocated. */
 int sc_fnv1a64_async(const void* data, uint64_t bytes, uint64_t seed, uint64_t* out, void* workspace,
                      uint64_t workspace_bytes, void* stream);
+/* The same hash continued over one more piece: the running hash is the u64 at `state` in device memory (the seed
+ * before the first piece), read when the piece's kernels run on `stream` and replaced by the hash of everything so
+ * far.  Hashing a buffer piece by piece in order, each call after the one before it on the same stream, gives the
+ * one-shot hash of the whole buffer: fnv1a64 is a left fold, and the reference chains it the same way through its
+ * seed argument (src/core/conversation_wire.cpp:135,679-683).  This lets a copy into device memory be verified piece
+ * by piece while later pieces are still in flight.  `state` is 8-byte aligned; the workspace rules are those of
+ * sc_fnv1a64_async for `bytes`.  Nothing is allocated. */
+int sc_fnv1a64_chain_async(const void* data, uint64_t bytes, uint64_t* state, void* workspace, uint64_t workspace_bytes,
+                           void* stream);
 /* Synchronous convenience: allocates its workspace, runs on the null stream, waits, and returns the hash in *hash. */
 int sc_fnv1a64_device(const void* data, uint64_t bytes, uint64_t seed, uint64_t* hash);
 

@@ -35,8 +35,8 @@ hipError_t launch_batch(const BatchArgs& args, int64_t grid, hipStream_t stream)
 hipError_t launch_stream_reset(int32_t* table, int64_t n_blocks, int32_t* slot_block, int32_t* slot_stamp,
                                int32_t* slot_ref, int64_t n_slots, int32_t* ctl, hipStream_t stream);
 hipError_t launch_ring_table(int32_t* table, int64_t n_blocks, int64_t n_slots, hipStream_t stream);
-hipError_t launch_fnv1a64(const void* data, uint64_t n, uint64_t seed, uint64_t* out, void* workspace,
-                          hipStream_t stream);
+hipError_t launch_fnv1a64(const void* data, uint64_t n, uint64_t seed, const uint64_t* seed_dev, uint64_t* out,
+                          void* workspace, hipStream_t stream);
 
 static uint64_t host_mix64(uint64_t z) {
     z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
@@ -1175,7 +1175,21 @@ int sc_fnv1a64_async(const void* data, uint64_t bytes, uint64_t seed, uint64_t* 
         return fail(SC_EINVAL, "sc_handoff: hash workspace smaller than sc_fnv1a64_workspace_bytes()");
     if (reinterpret_cast<uintptr_t>(workspace) & 15u) return fail(SC_EINVAL, "sc_handoff: hash workspace must be 16-byte aligned");
     if (bytes > (uint64_t(1) << 46)) return fail(SC_ERANGE, "sc_handoff: hash input beyond 2^46 bytes");
-    SC_HIP(sc::launch_fnv1a64(data, bytes, seed, out, workspace, static_cast<hipStream_t>(stream)), "hash launch");
+    SC_HIP(sc::launch_fnv1a64(data, bytes, seed, nullptr, out, workspace, static_cast<hipStream_t>(stream)),
+           "hash launch");
+    return ok();
+}
+
+int sc_fnv1a64_chain_async(const void* data, uint64_t bytes, uint64_t* state, void* workspace, uint64_t workspace_bytes,
+                           void* stream) {
+    if (!state || (bytes && !data)) return fail(SC_EINVAL, "sc_handoff: missing hash input or state");
+    if (reinterpret_cast<uintptr_t>(state) & 7u) return fail(SC_EINVAL, "sc_handoff: hash state must be 8-byte aligned");
+    if (!workspace || workspace_bytes < sc::fnv_workspace(bytes).bytes)
+        return fail(SC_EINVAL, "sc_handoff: hash workspace smaller than sc_fnv1a64_workspace_bytes()");
+    if (reinterpret_cast<uintptr_t>(workspace) & 15u) return fail(SC_EINVAL, "sc_handoff: hash workspace must be 16-byte aligned");
+    if (bytes > (uint64_t(1) << 46)) return fail(SC_ERANGE, "sc_handoff: hash input beyond 2^46 bytes");
+    SC_HIP(sc::launch_fnv1a64(data, bytes, 0, state, state, workspace, static_cast<hipStream_t>(stream)),
+           "hash launch");
     return ok();
 }
 
@@ -1187,7 +1201,7 @@ int sc_fnv1a64_device(const void* data, uint64_t bytes, uint64_t seed, uint64_t*
     hipError_t e = hipMalloc(&ws, ws_bytes + 256);
     if (e != hipSuccess) return fail(SC_ENOMEM, std::string("sc_handoff: hash workspace: ") + hipGetErrorString(e));
     uint64_t* out = reinterpret_cast<uint64_t*>(static_cast<uint8_t*>(ws) + ws_bytes);
-    e = sc::launch_fnv1a64(data, bytes, seed, out, ws, nullptr);
+    e = sc::launch_fnv1a64(data, bytes, seed, nullptr, out, ws, nullptr);
     if (e == hipSuccess) e = hipMemcpy(hash, out, sizeof(uint64_t), hipMemcpyDeviceToHost);
     const hipError_t f = hipFree(ws);
     if (e != hipSuccess) return hip_fail(e, "hash");

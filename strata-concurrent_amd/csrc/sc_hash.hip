@@ -256,8 +256,16 @@ __device__ __forceinline__ uint32_t compose(uint32_t g, uint32_t f) {
 }
 constexpr uint32_t kIdentityMap = 0u | (1u << 2) | (2u << 4) | (3u << 6);
 
-__global__ void __launch_bounds__(kScanThreads) fnv_scan_kernel(const uint8_t* summary, uint64_t groups, uint32_t init,
+// The state the hash starts from: the launch's seed, or the running hash at `seed_dev` when the input continues an
+// earlier one (read by every kernel that needs it, so one stream can chain pieces without a host round trip).
+__device__ __forceinline__ uint64_t start_state(uint64_t seed, const uint64_t* seed_dev) {
+    return seed_dev ? *seed_dev : seed;
+}
+
+__global__ void __launch_bounds__(kScanThreads) fnv_scan_kernel(const uint8_t* summary, uint64_t groups, int j,
+                                                                 uint64_t seed, const uint64_t* seed_dev,
                                                                  uint8_t* gstate) {
+    const uint32_t init = uint32_t((start_state(seed, seed_dev) >> j) & 3u);
     const uint64_t per = (groups + kScanThreads - 1) / kScanThreads;
     const uint64_t b = uint64_t(threadIdx.x) * per;
     const uint64_t e = b + per < groups ? b + per : groups;
@@ -320,7 +328,7 @@ __global__ void __launch_bounds__(kThreads) fnv_final_kernel(const uint8_t* data
 
 // h = seed * p^n + sum of the partial sums (mod 2^64; the order of the additions does not matter).
 __global__ void __launch_bounds__(kScanThreads) fnv_reduce_kernel(const uint64_t* partial, uint64_t groups, uint64_t seed,
-                                                                   uint64_t n, uint64_t* out) {
+                                                                   const uint64_t* seed_dev, uint64_t n, uint64_t* out) {
     uint64_t acc = 0;
     for (uint64_t i = threadIdx.x; i < groups; i += kScanThreads) acc += partial[i];
     for (int m = 32; m > 0; m >>= 1) acc += shfl_xor64(acc, m);
@@ -328,7 +336,7 @@ __global__ void __launch_bounds__(kScanThreads) fnv_reduce_kernel(const uint64_t
     if ((threadIdx.x & 63) == 0) s_sum[threadIdx.x >> 6] = acc;
     __syncthreads();
     if (threadIdx.x == 0) {
-        uint64_t h = seed * pow_prime(n);
+        uint64_t h = start_state(seed, seed_dev) * pow_prime(n);
         for (int w = 0; w < kScanThreads / 64; ++w) h += s_sum[w];
         out[0] = h;
     }
@@ -353,8 +361,8 @@ FnvWorkspace fnv_workspace(uint64_t n) {
     return w;
 }
 
-hipError_t launch_fnv1a64(const void* data, uint64_t n, uint64_t seed, uint64_t* out, void* workspace,
-                          hipStream_t stream) {
+hipError_t launch_fnv1a64(const void* data, uint64_t n, uint64_t seed, const uint64_t* seed_dev, uint64_t* out,
+                          void* workspace, hipStream_t stream) {
     const FnvWorkspace w = fnv_workspace(n);
     uint8_t* ws = static_cast<uint8_t*>(workspace);
     const uint8_t* src = static_cast<const uint8_t*>(data);
@@ -377,13 +385,15 @@ hipError_t launch_fnv1a64(const void* data, uint64_t n, uint64_t seed, uint64_t*
             const int j = 2 * q;
             hipLaunchKernelGGL(fnv_pair_kernel, grid, block, 0, stream, src, n, j, aligned, start, set[(q + 1) & 1],
                                gstate[(q + 1) & 1], set[q & 1], summary);
-            const uint32_t init = uint32_t((seed >> j) & 3u);
-            hipLaunchKernelGGL(fnv_scan_kernel, one, scan, 0, stream, summary, w.groups, init, gstate[q & 1]);
+            hipLaunchKernelGGL(fnv_scan_kernel, one, scan, 0, stream, summary, w.groups, j, seed, seed_dev,
+                               gstate[q & 1]);
         }
         hipLaunchKernelGGL(fnv_final_kernel, grid, block, 0, stream, src, n, aligned, start, set[1], gstate[1],
                            partial);
     }
-    hipLaunchKernelGGL(fnv_reduce_kernel, dim3(1), dim3(kScanThreads), 0, stream, partial, w.groups, seed, n, out);
+    // the reduce reads the start state before it writes `out`, so `out` may be `seed_dev` itself
+    hipLaunchKernelGGL(fnv_reduce_kernel, dim3(1), dim3(kScanThreads), 0, stream, partial, w.groups, seed, seed_dev, n,
+                       out);
     return hipGetLastError();
 }
 

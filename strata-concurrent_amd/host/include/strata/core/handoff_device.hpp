@@ -10,7 +10,8 @@
 //
 // Tmpfs pages are filled by several threads through a mapping (one file's write path is serialized), DMA and host
 // copies of neighbouring chunks overlap, and the payload's FNV-1a (the arena's payload_hash) is computed on the
-// device, beside the copies on the writer and after them on the reader.  The slot protocol is untouched: the writer
+// device beside the copies: over the whole payload while the writer's chunks drain, and on the reader chunk by chunk
+// as each lands in HBM, the running hash chained on the device.  The slot protocol is untouched: the writer
 // still publishes through HandoffArena::publish, the reader still checks the slot with HandoffArena::read_slot, and a
 // slot written here reads back through the reference's own reader.
 #pragma once
@@ -100,6 +101,7 @@ class HandoffMover {
     const HandoffMoveStats& last() const { return last_; }
 
   private:
+    uint64_t* hash_space_(uint64_t bytes, std::string& err);
     bool hash_on_device_(const void* data, uint64_t bytes, void* stream, std::string& err);
     bool fetch_hash_(uint64_t* out, std::string& err);
     void release_();
@@ -109,7 +111,7 @@ class HandoffMover {
     std::vector<void*> done_;     ///< one event per staging buffer: its last DMA finished
     void* entry_ = nullptr;       ///< event: the caller's stream at entry (the hash stream waits on it)
     void* hash_stream_ = nullptr;
-    void* hash_ws_ = nullptr;     ///< device hash workspace (grown on demand) + the u64 result at its end
+    void* hash_ws_ = nullptr;     ///< device hash workspace (grown on demand) + the u64 result / running hash at its end
     uint64_t hash_ws_bytes_ = 0;
     uint64_t* hash_host_ = nullptr;   ///< pinned landing place of the device hash
     HandoffCopyCrew* crew_ = nullptr;

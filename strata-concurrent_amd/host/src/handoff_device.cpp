@@ -144,9 +144,9 @@ bool HandoffMover::init(const HandoffMoverConfig& cfg, std::string& err) {
     return true;
 }
 
-/// Enqueue the device FNV-1a of `bytes` at `data` on the hash stream, after the work on `stream` so far; the result
-/// lands in pinned memory (fetch_hash_ waits for it).
-bool HandoffMover::hash_on_device_(const void* data, uint64_t bytes, void* stream, std::string& err) {
+/// The hash workspace, grown to serve inputs of `bytes` bytes, and the device word after it (the result, or the
+/// running hash of a chained hash).  Only called while nothing is queued on the hash stream.
+uint64_t* HandoffMover::hash_space_(uint64_t bytes, std::string& err) {
     const uint64_t need = (sc_fnv1a64_workspace_bytes(bytes) + 255) & ~255ull;
     if (need + 256 > hash_ws_bytes_) {
         if (hash_ws_) sc_device_free(hash_ws_);
@@ -156,11 +156,18 @@ bool HandoffMover::hash_on_device_(const void* data, uint64_t bytes, void* strea
         if (sc_device_alloc(&hash_ws_, grow) != SC_OK) {
             err = abi_error("handoff mover hash workspace");
             last_.device_error = true;
-            return false;
+            return nullptr;
         }
         hash_ws_bytes_ = grow;
     }
-    auto* dev_out = reinterpret_cast<uint64_t*>(static_cast<uint8_t*>(hash_ws_) + hash_ws_bytes_ - 256);
+    return reinterpret_cast<uint64_t*>(static_cast<uint8_t*>(hash_ws_) + hash_ws_bytes_ - 256);
+}
+
+/// Enqueue the device FNV-1a of `bytes` at `data` on the hash stream, after the work on `stream` so far; the result
+/// lands in pinned memory (fetch_hash_ waits for it).
+bool HandoffMover::hash_on_device_(const void* data, uint64_t bytes, void* stream, std::string& err) {
+    uint64_t* dev_out = hash_space_(bytes, err);
+    if (!dev_out) return false;
     if (sc_event_record(entry_, stream) != SC_OK || sc_stream_wait_event(hash_stream_, entry_) != SC_OK ||
         sc_fnv1a64_async(data, bytes, kEngineSeed, dev_out, hash_ws_, hash_ws_bytes_ - 256, hash_stream_) != SC_OK ||
         sc_copy_async(hash_host_, dev_out, sizeof(uint64_t), hash_stream_) != SC_OK) {
@@ -263,6 +270,20 @@ bool HandoffMover::read_to_device(HandoffArena& arena, int index, uint64_t nonce
     const uint64_t n_chunks = (bytes + C - 1) / C;
     const uint64_t R = (uint64_t) cfg_.depth;
     auto* dst = static_cast<uint8_t*>(device_dst);
+    // with `verify`, each chunk is hashed on the hash stream as soon as its DMA is done, continuing the running hash
+    // in device memory (seeded from pinned memory first), so the check ends a chunk's hash after the last copy
+    uint64_t* state = nullptr;
+    const bool chain = verify && bytes != 0;
+    if (chain) {
+        state = hash_space_(std::min(C, bytes), err);
+        if (!state) return false;
+        *hash_host_ = kEngineSeed;
+        if (sc_copy_async(state, hash_host_, sizeof(uint64_t), hash_stream_) != SC_OK) {
+            err = abi_error("handoff mover hash seed");
+            last_.device_error = true;
+            return false;
+        }
+    }
     last_.wrote_device = bytes != 0;
     bool ok = true;
     for (uint64_t k = 0; k < n_chunks && ok; ++k) {
@@ -276,6 +297,9 @@ bool HandoffMover::read_to_device(HandoffArena& arena, int index, uint64_t nonce
         last_.copy_ms += ms_since(tc);
         ok = sc_copy_async(dst + k * C, stage_[k % R], len, stream) == SC_OK &&
              sc_event_record(done_[k % R], stream) == SC_OK;
+        if (ok && chain)
+            ok = sc_stream_wait_event(hash_stream_, done_[k % R]) == SC_OK &&
+                 sc_fnv1a64_chain_async(dst + k * C, len, state, hash_ws_, hash_ws_bytes_ - 256, hash_stream_) == SC_OK;
     }
     const auto tf = std::chrono::steady_clock::now();
     if (ok) ok = sc_stream_sync(stream) == SC_OK;
@@ -283,6 +307,8 @@ bool HandoffMover::read_to_device(HandoffArena& arena, int index, uint64_t nonce
     if (!ok) {
         err = abi_error("handoff mover slot-to-device copy");
         last_.device_error = true;
+        sc_stream_sync(stream);
+        if (chain) sc_stream_sync(hash_stream_);   // nothing may still read the caller's buffer after we return
         return false;
     }
     // the writer may only reuse the slot after our ACK, or after its lease: a publication that moved while we copied
@@ -291,12 +317,21 @@ bool HandoffMover::read_to_device(HandoffArena& arena, int index, uint64_t nonce
     if (!arena.slot_info(index, after) || after.state != kHandoffReady || after.nonce != nonce ||
         after.payload_bytes != bytes || after.payload_hash != info.payload_hash || after.published_ms != info.published_ms) {
         err = "handoff slot " + std::to_string(index) + " was released or reclaimed while it was read";
+        if (chain) sc_stream_sync(hash_stream_);
         return false;
     }
     if (verify) {
         const auto th = std::chrono::steady_clock::now();
         uint64_t h = kEngineSeed;
-        if (bytes && (!hash_on_device_(device_dst, bytes, stream, err) || !fetch_hash_(&h, err))) return false;
+        if (chain) {
+            if (sc_copy_async(hash_host_, state, sizeof(uint64_t), hash_stream_) != SC_OK) {
+                err = abi_error("handoff mover hash");
+                last_.device_error = true;
+                sc_stream_sync(hash_stream_);
+                return false;
+            }
+            if (!fetch_hash_(&h, err)) return false;
+        }
         last_.hash_ms = ms_since(th);
         if (h != info.payload_hash) {
             char buf[160];

@@ -178,6 +178,7 @@ _SIGS = {
     "sc_resume_layers_async": (C.c_int, [_GEO, _P, _U64, _I64, C.POINTER(SlotLayers), _P, _P]),
     "sc_fnv1a64_workspace_bytes": (_U64, [_U64]),
     "sc_fnv1a64_async": (C.c_int, [_P, _U64, _U64, _P, _P, _U64, _P]),
+    "sc_fnv1a64_chain_async": (C.c_int, [_P, _U64, _P, _P, _U64, _P]),
     "sc_fnv1a64_device": (C.c_int, [_P, _U64, _U64, C.POINTER(_U64)]),
     "sc_copy_device_async": (C.c_int, [_P, _P, _U64, _P]),
     "sc_ipc_export_create": (C.c_int, [_U64, _U64, C.POINTER(_P)]),
@@ -753,6 +754,17 @@ class HashPlan:
             raise ValueError(f"hash input of {nbytes} bytes exceeds the plan's {self.max_bytes}")
         check(lib.sc_fnv1a64_async(ptr, nbytes, seed, self.out.ptr, self.ws.ptr, self.ws_bytes, _stream(stream)),
               "sc_fnv1a64_async")
+
+    def start(self, seed: int = REFERENCE_FNV_SEED) -> None:
+        """Set the running hash of chain() to `seed` (a synchronous upload)."""
+        self.out.upload([seed])
+
+    def chain(self, ptr: int, nbytes: int, stream=None) -> None:
+        """Continue the running hash over `nbytes` more device bytes at `ptr` (sc_fnv1a64_chain_async)."""
+        if nbytes > self.max_bytes:
+            raise ValueError(f"hash input of {nbytes} bytes exceeds the plan's {self.max_bytes}")
+        check(lib.sc_fnv1a64_chain_async(ptr, nbytes, self.out.ptr, self.ws.ptr, self.ws_bytes, _stream(stream)),
+              "sc_fnv1a64_chain_async")
 
     def result(self) -> int:
         return int(self.out.numpy()[0])

@@ -179,6 +179,37 @@ def test_refusals_leave_device_memory_alone(sc, ar, mover, shm):
     assert got[777] == data[777] ^ 1 and np.array_equal(np.delete(got, 777), np.delete(data, 777))
 
 
+def test_verified_read_refuses_a_change_in_a_later_chunk(sc, oracle, ar, mover, shm):
+    """The device reader hashes each 8 MiB chunk as it lands (the running hash chained on the device): a byte changed
+    in the slot's third chunk or in its last byte is caught, and the unchanged payload passes."""
+    nbytes = (20 << 20) + 3
+    data = np.random.default_rng(21).integers(0, 256, nbytes, dtype=np.uint8)
+    src = device_bytes(sc, data)
+    path = shm / "g" / "arena"
+    w = ar.Arena.writer(path, TIERS, PRICED, PACK, GEOM)
+    r = ar.Arena.reader(path, PACK, GEOM)
+    c = w.claim(1, 8, 1)
+    mover.publish(w, c, src.ptr, nbytes, 5)
+    dst = sc.DeviceBuffer(nbytes, "uint8")
+    s = mover.read(r, c.index, c.nonce, 8, dst.ptr, nbytes, verify=True)
+    assert s.payload_hash == oracle.fnv1a64(data.tobytes(), SEED)
+    assert dst.numpy().tobytes() == data.tobytes()
+    for at in ((16 << 20) + 12345, nbytes - 1):
+        print(f"case tampered byte {at}", flush=True)
+        with open(path, "r+b") as f:
+            f.seek(c.payload_off + at)
+            f.write(bytes([data[at] ^ 0x80]))
+        with pytest.raises(ar.ArenaError) as e:
+            mover.read(r, c.index, c.nonce, 8, dst.ptr, nbytes, verify=True)
+        assert e.value.code == ar.SC_ESTALE and "payload hash" in str(e.value)
+        with open(path, "r+b") as f:
+            f.seek(c.payload_off + at)
+            f.write(bytes([data[at]]))
+    mover.read(r, c.index, c.nonce, 8, dst.ptr, nbytes, verify=True)   # restored: accepted again
+    w.close()
+    r.close()
+
+
 SMALL = dict(n_layers=8, qsa_interval=4, n_head_kv=2, head_dim=256, page_size=4, ssm_state_size=32,
              ssm_k_heads=4, ssm_v_heads=8, ssm_d_conv=4, ssm_conv_channels=520, idx_key_dim=128)
 GEOKEY = [2560, 8, 4, 32, 4, 8, 4, 520, 256, 24, 2, 256, 128, 4, 4, 3, 1, 0]

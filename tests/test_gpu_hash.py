@@ -73,6 +73,34 @@ def test_async_plan_on_a_stream_and_reuse(sc, oracle, cuda):
     plan.free()
 
 
+@pytest.mark.parametrize("seed", [1469598103934665603, 0xFFFFFFFFFFFFFFFF])
+def test_chained_pieces_equal_the_one_shot_hash(sc, oracle, cuda, seed):
+    """sc_fnv1a64_chain_async over consecutive pieces (empty ones, ragged and misaligned boundaries, pieces shorter
+    than a segment and spanning several workgroups) ends at the one-shot hash of the whole buffer, and the running
+    hash after each piece is the byte loop's hash of the prefix so far."""
+    rng = np.random.default_rng(seed & 0xFFFF)
+    n = 5_000_011
+    data = rng.integers(0, 256, size=n, dtype=np.uint8)
+    buf = _upload(sc, data)
+    cuts = [0, 0, 1, 17, 256, 4096 + 3, 65_536 * 3 + 5, 65_536 * 3 + 5, 1_000_000, 3_333_333, n - 1, n]
+    plan = sc.HashPlan(n)
+    stream = sc.Stream()
+    plan.start(seed)
+    for a, b in zip(cuts, cuts[1:]):
+        plan.chain(buf.ptr + a, b - a, stream=stream)
+        stream.sync()
+        assert plan.result() == oracle.fnv1a64(data[:b].tobytes(), seed), (a, b)
+    assert plan.result() == sc.fnv1a64_device(buf.ptr, n, seed)
+    # queued back to back without waiting in between, the result is the same
+    plan.start(seed)
+    for a, b in zip(cuts, cuts[1:]):
+        plan.chain(buf.ptr + a, b - a, stream=stream)
+    stream.sync()
+    assert plan.result() == oracle.fnv1a64(data.tobytes(), seed)
+    plan.free()
+    buf.free()
+
+
 def test_workspace_refusals(sc, cuda):
     buf = sc.DeviceBuffer(1 << 16, "uint8")
     out = sc.DeviceBuffer(1, "uint64")
@@ -80,6 +108,10 @@ def test_workspace_refusals(sc, cuda):
     ws = sc.DeviceBuffer(max(small, 16), "uint8")
     rc = sc.lib.sc_fnv1a64_async(buf.ptr, 1 << 16, 0, out.ptr, ws.ptr, small, None)
     assert rc == sc.SC_EINVAL and "workspace" in sc.last_error()
+    rc = sc.lib.sc_fnv1a64_chain_async(buf.ptr, 1 << 16, out.ptr, ws.ptr, small, None)
+    assert rc == sc.SC_EINVAL and "workspace" in sc.last_error()
+    rc = sc.lib.sc_fnv1a64_chain_async(buf.ptr, 16, out.ptr + 4, ws.ptr, small, None)
+    assert rc == sc.SC_EINVAL and "aligned" in sc.last_error()
     for b in (buf, out, ws):
         b.free()
 
