@@ -10,6 +10,7 @@
 
 #include "strata/core/conversation_cache.hpp"
 #include "strata/core/engine_types.hpp"
+#include "strata/kernels/kv_stream.hpp"   // the block movers (the reference reaches them through layer.hpp)
 
 #include <cstdint>
 #include <string>

@@ -6,6 +6,7 @@
 #pragma once
 
 #include "strata/core/engine_types.hpp"
+#include "strata/kernels/qsa.hpp"
 
 #include <cstdint>
 
@@ -22,13 +23,6 @@ struct QsaAttnPools {
     const uint8_t* k_q4 = nullptr;
     const uint8_t* v_q4 = nullptr;
     const int32_t* page_table = nullptr;
-};
-
-/// The shape the movers need (the n_head_kv / head_dim / page_size of include/strata/kernels/qsa.hpp:96-107).
-struct QsaShapes {
-    int64_t n_head_kv = 2;
-    int64_t head_dim = 256;
-    int64_t page_size = 4;
 };
 
 void kv_stream_reset(const KvStreamMap& m, void* stream);

@@ -191,7 +191,7 @@ bool kv_restore_enqueue(const ConversationKv& image, const QsaState& st, const M
     // refills from the restored host copy before any attention reads.  A ring refills its window from the host.
     if (st.kv_mode == 1) strata::kernels::kv_stream_reset(st.map, stream);
     if (st.kv_mode == 2 && upto > 0) {
-        strata::kernels::QsaShapes s;
+        strata::kernels::QsaShapes s = strata::kernels::qsa_real_shapes();
         s.n_head_kv = g.n_head_kv;
         s.head_dim = g.head_dim;
         s.page_size = image.page_size;

@@ -210,7 +210,9 @@ public:
         }
         return true;
     }
-    bool record(uint32_t kind, uint64_t body) { return u32(kind) && u32(0) && u64(body); }
+    // Each record starts a new sink write (the staged bytes before it go out first), so a sink sees the head as one
+    // write per record, as the reference's encoder writes it (src/core/conversation_wire.cpp:293-396).
+    bool record(uint32_t kind, uint64_t body) { return flush() && u32(kind) && u32(0) && u64(body); }
     // The BLOBREF of `who` (a buffer of the image): {bytes, absolute offset} of the next pool entry, or {0, 0}.
     bool blobref_of(const void* who, uint64_t held) { return blobref(lay_.size_of(who, held)); }
     // The next BLOBREF: {bytes, absolute offset} of the next pool entry, or {0, 0} for an empty buffer.
@@ -220,7 +222,7 @@ public:
             return refuse(error_, "internal: the pool order changed between the layout and the write");
         return u64(bytes) && u64(lay_.plan.blob_pool_off + lay_.pool[next_++].rel);
     }
-    // Large runs bypass the staging buffer (after flushing it) in pieces of at most kWireChunkBytes.
+    // Large contiguous runs bypass the staging buffer (after flushing it) in pieces of at most kWireChunkBytes.
     bool bulk(const uint8_t* p, uint64_t n) {
         if (n < kStagingBytes) return put(p, n);
         if (!flush()) return false;
@@ -231,6 +233,13 @@ public:
             n -= k;
         }
         return true;
+    }
+    // A ConversationBuffer's segment run goes to the sink as one write (after flushing the staging buffer), as the
+    // reference hands each visited segment to its sink (src/core/conversation_wire.cpp:421-427): a 20 MiB buffer is
+    // written as a 16 MiB and a 4 MiB write, straight from the segments' own memory.
+    bool segment(const uint8_t* p, uint64_t n) {
+        if (n < kStagingBytes) return put(p, n);
+        return flush() && emit(p, n);
     }
     bool flush() {
         if (staging_.empty()) return true;
@@ -342,7 +351,7 @@ bool write_payload(const SavedConversation& img, const WireIdentity& id, const L
             if (!w.bulk(e.vec->data(), e.bytes)) return false;
         } else {
             bool ok = true;
-            e.buf->visit(0, size_t(e.bytes), [&](const uint8_t* q, size_t n, size_t) { return ok = w.bulk(q, n); });
+            e.buf->visit(0, size_t(e.bytes), [&](const uint8_t* q, size_t n, size_t) { return ok = w.segment(q, n); });
             if (!ok) return false;
         }
         rel = e.rel + e.bytes;
@@ -588,7 +597,8 @@ private:
         uint64_t body = 0;
         if (!c.record_header(kind, flags, body)) return false;
         if (kind != kWireRecordKv || flags || body != kKvBodyBytes)
-            return refuse(error_, std::string("the ") + where + " does not hold plain KV records (kind " + hex64(kind) + ")");
+            return refuse(error_, std::string("the ") + where + " does not hold plain KV records (kind " + hex64(kind) +
+                                      ", flags " + num(flags) + ", " + num(body) + " body bytes)");
         uint32_t fmt = 0;
         if (!c.u32(fmt) || !c.zeros(4)) return false;
         k.format = int(int32_t(fmt));
@@ -702,7 +712,8 @@ SlotWireSink::SlotWireSink(uint8_t* mapping, uint64_t capacity) : map_(mapping),
 bool SlotWireSink::write(const uint8_t* data, size_t bytes) {
     if (!bytes) return true;
     if (pos_ > capacity_ || bytes > capacity_ - pos_) {
-        error_ = "conversation wire: the payload needs " + num(pos_ + bytes) + " bytes and the slot holds " + num(capacity_);
+        error_ = "conversation wire: the payload needs " + num(pos_ + bytes) + " bytes and the slot holds " +
+                 num(capacity_) + " (claim a larger tier)";
         return false;
     }
     if (map_) {

@@ -392,7 +392,7 @@ void layer_cases(int fmt, int mode) {
                   "a restore evicts every VRAM page of a streamed layer" + utag);
         }
         if (mode == 2 && upto > 0) {
-            QsaShapes s;
+            const QsaShapes s = qsa_real_shapes();
             const int64_t b1 = (upto + s.page_size - 1) / s.page_size, b0 = std::max<int64_t>(0, b1 - f.st.n_slots);
             const size_t block = size_t(kv_block_bytes(s, fmt)) / 2;
             const size_t code_block = fmt == kKvInt8 ? size_t(s.page_size * s.n_head_kv * s.head_dim) : block;

@@ -205,8 +205,9 @@ void test_segments() {
     WireEncoded enc;
     std::string err;
     check_ok(conversation_wire_encode(s, sink, {1, 2}, enc, err), err, "big encode");
-    check(sink.max_write <= kWireChunkBytes, "no single write exceeds the codec's chunk");
-    check(sink.writes > 20, "the big buffer went out in many pieces, never staged whole");
+    check(sink.max_write == ConversationBuffer::segment_bytes,
+          "each segment goes out as one write, straight from the segment (none larger)");
+    check(sink.writes > 8, "the payload went out record by record and segment by segment, never staged whole");
     ChunkySource src(sink.bytes, 4096);
     SavedConversation out;
     WireDecoded info;

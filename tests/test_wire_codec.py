@@ -3,7 +3,9 @@
 tests/cpp/bin/wire_driver is oracle/ref_wire_driver.cpp - the program that produced the golden vectors from the
 reference's codec - compiled against this library's codec instead.  Every spec must encode to the same bytes and hash
 the reference produced, and every corrupted payload must be accepted or refused exactly as the reference decided.
-conversation_wire_test restates the reference's own codec test scenarios in C++ (host only).
+conversation_wire_test restates the reference's own codec test scenarios in C++ (host only), and where the
+reference's sources are at hand, oracle/_ref/ref_wire_test_on_ours is the reference's own codec test
+(src/core/saved_conv_wire_test.cpp) compiled unmodified against this library's codec header and library.
 """
 import json
 import subprocess
@@ -15,6 +17,27 @@ ROOT = Path(__file__).resolve().parent.parent
 GOLDEN = ROOT / "tests" / "golden"
 BIN = ROOT / "tests" / "cpp" / "bin"
 MANIFEST = json.loads((GOLDEN / "wire_manifest.json").read_text())
+
+
+REF_TEST = ROOT / "oracle" / "_ref" / "ref_wire_test"
+REF_TEST_ON_OURS = ROOT / "oracle" / "_ref" / "ref_wire_test_on_ours"
+
+
+def _run_ref_test(exe: Path) -> str:
+    proc = subprocess.run([str(exe)], capture_output=True, text=True, timeout=300)
+    out = proc.stdout + proc.stderr
+    assert proc.returncode == 0 and "FAIL" not in out, "\n".join(l for l in out.splitlines() if "FAIL" in l) or out
+    return out
+
+
+@pytest.mark.skipif(not REF_TEST_ON_OURS.exists(), reason="the reference codec test build (oracle/_ref) is not here")
+def test_reference_codec_test_against_this_library():
+    """src/core/saved_conv_wire_test.cpp, unmodified, on this library's codec: every one of its checks passes, and it
+    counts as many checks as it does on the reference's own codec."""
+    out = _run_ref_test(REF_TEST_ON_OURS)
+    assert "checks passed" in out
+    if REF_TEST.exists():
+        assert out.split()[-3:] == _run_ref_test(REF_TEST).split()[-3:]
 
 
 def _driver(*args) -> str:
