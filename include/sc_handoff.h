@@ -161,6 +161,40 @@ typedef struct sc_quant_slot {
  * src/prefill/prefill.cpp).  src->kv_dtype must be SC_DTYPE_F32 and head_dim 256.  sc_plan_payload_bytes() of the
  * plan counts the bytes it reads plus the bytes it writes. */
 int sc_plan_carve_quant(const sc_geometry* g, const sc_prefill_view* src, const sc_quant_slot* dst, sc_plan** out);
+/* ---- kv_append: the per-layer prefill writers, with the reference's arguments ---------------------------------
+ * One launch per call, nothing allocated, like the reference's own (the plans above build a whole slot in one launch
+ * instead).  Every entry point returns before its launch when T <= 0, and refuses (SC_EINVAL, nothing launched)
+ * missing or misaligned buffers and impossible extents; pools are not bounded, the caller sized them, as there. */
+
+/* strata::kernels::KvHostPools (include/strata/kernels/kv_stream.hpp:30-39), member for member: one layer's host
+ * copy (device-mapped pinned memory) or staging pool, identity layout [block][kv_head][page_size][row]. */
+typedef struct sc_kv_pools {
+    uint16_t* k_pool;   /* f16 rows */
+    uint16_t* v_pool;
+    int8_t* k_q;        /* int8 codes */
+    int8_t* v_q;
+    uint16_t* k_scale;  /* int8: one f16 scale per 64 values */
+    uint16_t* v_scale;
+    uint8_t* k_q4;      /* q4_0 blocks, 144 bytes per cell and head */
+    uint8_t* v_q4;
+} sc_kv_pools;
+
+/* kv_append (include/strata/prefill/kernels.hpp:78-83, src/prefill/kernels.cu:558-625): K and V, f32 [T][2][256]
+ * (positions pos0 .. pos0 + T - 1), into the paged pool - f16 rows (RNE) when k_pool is given, else int8 codes with an
+ * f16 scale per 64 values - through page_table (NULL: identity), skipping cells whose page entry is negative; also
+ * into the host copy and the staging pool (identity layout, every cell) when `host` / `stage` name pools of the same
+ * format.  K8V4's K-only call (K == V, k_q == v_q) is allowed.  Pool alignment: f16 16 bytes, int8 codes 4, scales 8. */
+int sc_kv_append_async(const float* K, const float* V, int64_t T, int64_t pos0, const int32_t* page_table,
+                       int64_t page_size, uint16_t* k_pool, uint16_t* v_pool, int8_t* k_q, int8_t* v_q,
+                       uint16_t* k_scale, uint16_t* v_scale, void* stream, const sc_kv_pools* host,
+                       const sc_kv_pools* stage);
+/* kv_append_q4 (include/strata/kernels/kv_q4.hpp:50-54, src/kernels/cuda/kv_q4.cu:110-135,205-215): already rotated
+ * K and V, f32 [T][n_head_kv][256], into q4_0 pools through page_table, and into host->k_q4 / stage->k_q4 (identity)
+ * when given.  head_dim must be 256. */
+int sc_kv_append_q4_async(uint8_t* k_q4, uint8_t* v_q4, const int32_t* page_table, int64_t pos0, int64_t T,
+                          const float* K, const float* V, int64_t n_head_kv, int64_t head_dim, int64_t page_size,
+                          void* stream, const sc_kv_pools* host, const sc_kv_pools* stage);
+
 /* Pass 1 of the two-pass handoff: carve into a transfer buffer laid out as the image for src->tokens
  * (pos0 must be 0).  The transfer buffer is what a park writes and what crosses to another instance. */
 int sc_plan_gather(const sc_geometry* g, const sc_prefill_view* src, void* image, uint64_t image_bytes,

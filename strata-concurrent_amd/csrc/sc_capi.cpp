@@ -20,6 +20,8 @@
 #include "sc_internal.hpp"
 
 namespace sc {
+hipError_t launch_append(const AppendRows& rows, int n_rows, uint64_t tiles_per_row, const MoveGeo& geo, int32_t kind,
+                         hipStream_t stream);
 hipError_t launch_move(const MoveRow* rows, const uint16_t* tile_row, const MoveGeo& geo, uint64_t n_tiles,
                        int64_t grid, int32_t mix, hipStream_t stream);
 hipError_t launch_fill_uniform_f16(uint16_t* dst, uint64_t n, float lo, float hi, uint64_t seed, uint64_t sid,
@@ -876,6 +878,109 @@ int sc_plan_destroy(sc_plan* plan) {
         const hipError_t e_ = (call);                         \
         if (e_ != hipSuccess) return hip_fail(e_, what);      \
     } while (0)
+
+// ---- kv_append: the per-layer prefill writers ---------------------------------------------------------------------
+
+namespace {
+
+bool misaligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) != 0; }
+
+// One destination set of a kv_append call: K and V codes (f16 rows, int8 codes or q4_0 blocks), the int8 scales,
+// and the page table (NULL: identity, the layout of the host copy and of the staging pool).
+struct AppendDest {
+    void* k;
+    void* v;
+    uint16_t* ks;
+    uint16_t* vs;
+    const int32_t* table;
+};
+
+// Checks and lays out the rows of one call.  `kind` is sc::kKv32, kKvQ8 or kKvQ4; `dests` holds the pool first.
+int append_launch(int32_t kind, const float* K, const float* V, int64_t T, int64_t pos0, int64_t H, int64_t D,
+                  int64_t page_size, const AppendDest* dests, int n_dests, void* stream) {
+    if (pos0 < 0 || T > (int64_t(1) << 30) || pos0 > (int64_t(1) << 30) || page_size < 1 || page_size > (1 << 20))
+        return fail(SC_EINVAL, "sc_handoff: kv_append: invalid extent (pos0, T or page_size)");
+    if (!K || !V) return fail(SC_EINVAL, "sc_handoff: kv_append: missing K or V");
+    if (misaligned(K, 16) || misaligned(V, 16))
+        return fail(SC_EINVAL, "sc_handoff: kv_append: K and V must be 16-byte aligned");
+    const uintptr_t code_align = kind == sc::kKv32 ? 16 : kind == sc::kKvQ8 ? 4 : 2;
+    sc::AppendRows rows{};
+    int n = 0;
+    for (int d = 0; d < n_dests; ++d) {
+        const AppendDest& a = dests[d];
+        if (!a.k || !a.v || (kind == sc::kKvQ8 && (!a.ks || !a.vs)))
+            return fail(SC_EINVAL, kind == sc::kKvQ8 ? "sc_handoff: kv_append: int8 destinations need K and V codes "
+                                                       "and both scale arrays"
+                                                     : "sc_handoff: kv_append: a destination needs both K and V");
+        if (misaligned(a.k, code_align) || misaligned(a.v, code_align) ||
+            (kind == sc::kKvQ8 && (misaligned(a.ks, 8) || misaligned(a.vs, 8))))
+            return fail(SC_EINVAL, "sc_handoff: kv_append: f16 pools must be 16-byte, int8 codes 4-byte, int8 scales "
+                                   "8-byte and q4_0 pools 2-byte aligned");
+        const float* srcs[2] = {K, V};
+        void* codes[2] = {a.k, a.v};
+        uint16_t* scales[2] = {a.ks, a.vs};
+        for (int kv = 0; kv < 2; ++kv) {
+            sc::MoveRow& r = rows.row[n++];
+            r.kind = kind;
+            r.src = reinterpret_cast<const uint8_t*>(srcs[kv]);
+            r.dst = static_cast<uint8_t*>(codes[kv]);
+            r.dst2 = reinterpret_cast<uint8_t*>(scales[kv]);
+            r.table = a.table;
+            r.pos0 = pos0;
+            r.ld = std::numeric_limits<int64_t>::max();   // the reference bounds no page: the caller sized the pools
+            r.aux = int32_t(T);
+            r.n = kind == sc::kKv32 ? uint64_t(T * H) * uint64_t(D * 2 / 16) : uint64_t(T * H);
+        }
+    }
+    const uint64_t per_tile = kind == sc::kKv32 ? sc::kTileChunks : sc::kQuantUnitsPerTile;
+    const uint64_t tiles = (rows.row[0].n + per_tile - 1) / per_tile;
+    sc::MoveGeo geo{};
+    geo.row_chunks = sc::make_fastdiv(uint32_t(D * 2 / 16));
+    geo.heads = sc::make_fastdiv(uint32_t(H));
+    geo.page_size = sc::make_fastdiv(uint32_t(page_size));
+    SC_HIP(sc::launch_append(rows, n, tiles, geo, kind, static_cast<hipStream_t>(stream)), "kv_append launch");
+    return ok();
+}
+
+}  // namespace
+
+int sc_kv_append_async(const float* K, const float* V, int64_t T, int64_t pos0, const int32_t* page_table,
+                       int64_t page_size, uint16_t* k_pool, uint16_t* v_pool, int8_t* k_q, int8_t* v_q,
+                       uint16_t* k_scale, uint16_t* v_scale, void* stream, const sc_kv_pools* host,
+                       const sc_kv_pools* stage) {
+    return guarded([&] {
+        if (T <= 0) return ok();   // the reference launches nothing (src/prefill/kernels.cu:617)
+        // f16 when the f16 pools are given, else int8 codes + scales (kernels.cu:576-582)
+        const bool f16 = k_pool != nullptr;
+        AppendDest dests[3];
+        int n = 0;
+        dests[n++] = f16 ? AppendDest{k_pool, v_pool, nullptr, nullptr, page_table}
+                         : AppendDest{k_q, v_q, k_scale, v_scale, page_table};
+        for (const sc_kv_pools* p : {host, stage}) {
+            if (!p || !(f16 ? static_cast<const void*>(p->k_pool) : static_cast<const void*>(p->k_q))) continue;
+            dests[n++] = f16 ? AppendDest{p->k_pool, p->v_pool, nullptr, nullptr, nullptr}
+                             : AppendDest{p->k_q, p->v_q, p->k_scale, p->v_scale, nullptr};
+        }
+        return append_launch(f16 ? sc::kKv32 : sc::kKvQ8, K, V, T, pos0, 2, 256, page_size, dests, n, stream);
+    });
+}
+
+int sc_kv_append_q4_async(uint8_t* k_q4, uint8_t* v_q4, const int32_t* page_table, int64_t pos0, int64_t T,
+                          const float* K, const float* V, int64_t n_head_kv, int64_t head_dim, int64_t page_size,
+                          void* stream, const sc_kv_pools* host, const sc_kv_pools* stage) {
+    return guarded([&] {
+        if (T <= 0) return ok();   // src/kernels/cuda/kv_q4.cu:207
+        if (head_dim != sc::kQuantDim)
+            return fail(SC_EINVAL, "sc_handoff: kv_append_q4: head_dim must be 256 (the Hadamard transform's size)");
+        if (n_head_kv < 1 || n_head_kv > 4096) return fail(SC_EINVAL, "sc_handoff: kv_append_q4: invalid n_head_kv");
+        AppendDest dests[3];
+        int n = 0;
+        dests[n++] = AppendDest{k_q4, v_q4, nullptr, nullptr, page_table};
+        for (const sc_kv_pools* p : {host, stage})
+            if (p && p->k_q4) dests[n++] = AppendDest{p->k_q4, p->v_q4, nullptr, nullptr, nullptr};
+        return append_launch(sc::kKvQ4, K, V, T, pos0, n_head_kv, head_dim, page_size, dests, n, stream);
+    });
+}
 
 // ---- batched ragged resume + append ----------------------------------------------------------------------------
 

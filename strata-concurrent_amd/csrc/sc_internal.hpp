@@ -109,6 +109,14 @@ struct BatchArgs {
     MoveGeo geo;
 };
 
+// The rows of one kv_append call (sc_kv_append_async, sc_kv_append_q4_async), carried in the kernel arguments
+// rather than a device table: K and V into the paged pool, into the host copy and into the staging pool.  Every row
+// is of one kind (kKv32, kKvQ8 or kKvQ4) and spans the same number of tiles.
+constexpr int kAppendMaxRows = 6;
+struct AppendRows {
+    MoveRow row[kAppendMaxRows];
+};
+
 // The parallel FNV-1a (sc_hash.hip): bytes per lane segment, and where its workspace keeps what.
 constexpr int kFnvLaneBytes = 256;
 struct FnvWorkspace {

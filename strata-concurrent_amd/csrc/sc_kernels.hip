@@ -792,6 +792,61 @@ hipError_t launch_move(const MoveRow* rows, const uint16_t* tile_row, const Move
     return hipGetLastError();
 }
 
+// ---- kv_append: one call's rows in the kernel arguments -----------------------------------------------------------
+// The reference's per-layer prefill writers (kv_append, src/prefill/kernels.cu:558-625; kv_append_q4,
+// src/kernels/cuda/kv_q4.cu:111-135,205-215) take their destinations as arguments and allocate nothing, so this launch
+// takes its up to six rows the same way.  Row k owns tiles [k * tiles_per_row, (k + 1) * tiles_per_row); the switch
+// reads the selected row with scalar loads from the argument segment (an indexed read of the argument array would
+// copy it to scratch first).
+namespace {
+template <int kKind>
+__global__ void __launch_bounds__(kThreads) sc_append_kernel(AppendRows rows, int32_t n_rows, uint64_t tiles_per_row,
+                                                              MoveGeo geo) {
+    const uint64_t n_tiles = uint64_t(n_rows) * tiles_per_row;
+    for (uint64_t tile = blockIdx.x; tile < n_tiles; tile += gridDim.x) {
+        const int k = __builtin_amdgcn_readfirstlane(int(tile / tiles_per_row));
+        MoveRow r;
+        switch (k) {
+            case 0: r = rows.row[0]; break;
+            case 1: r = rows.row[1]; break;
+            case 2: r = rows.row[2]; break;
+            case 3: r = rows.row[3]; break;
+            case 4: r = rows.row[4]; break;
+            default: r = rows.row[5]; break;
+        }
+        const uint64_t local = tile - uint64_t(k) * tiles_per_row;
+        if constexpr (kKind == kKv32) {
+            if (r.table) tile_kv32<true>(r, geo, local);
+            else tile_kv32<false>(r, geo, local);
+        } else if constexpr (kKind == kKvQ8) {
+            tile_q8(r, geo, local);
+        } else {
+            tile_q4(r, geo, local);
+        }
+    }
+}
+}  // namespace
+
+hipError_t launch_append(const AppendRows& rows, int n_rows, uint64_t tiles_per_row, const MoveGeo& geo, int32_t kind,
+                         hipStream_t stream) {
+    if (n_rows <= 0 || tiles_per_row == 0) return hipSuccess;
+    if (n_rows > kAppendMaxRows || (kind != kKv32 && kind != kKvQ8 && kind != kKvQ4)) return hipErrorInvalidValue;
+    const uint64_t n_tiles = uint64_t(n_rows) * tiles_per_row;
+    const dim3 blocks(unsigned(n_tiles < 65536 ? n_tiles : 65536)), threads(kThreads);
+    switch (kind) {
+        case kKv32:
+            hipLaunchKernelGGL(sc_append_kernel<kKv32>, blocks, threads, 0, stream, rows, n_rows, tiles_per_row, geo);
+            break;
+        case kKvQ8:
+            hipLaunchKernelGGL(sc_append_kernel<kKvQ8>, blocks, threads, 0, stream, rows, n_rows, tiles_per_row, geo);
+            break;
+        default:
+            hipLaunchKernelGGL(sc_append_kernel<kKvQ4>, blocks, threads, 0, stream, rows, n_rows, tiles_per_row, geo);
+            break;
+    }
+    return hipGetLastError();
+}
+
 static unsigned fill_grid(uint64_t n) {
     const uint64_t b = (n + 255) / 256;
     return unsigned(b < 8192 ? (b ? b : 1) : 8192);

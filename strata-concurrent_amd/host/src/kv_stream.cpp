@@ -1,7 +1,12 @@
-// kv_stream.cpp - the block movers over libsc_handoff.so (see strata/kernels/kv_stream.hpp).
+// kv_stream.cpp - the block movers and the prefill K/V appends over libsc_handoff.so (see strata/kernels/kv_stream.hpp,
+// strata/kernels/kv_q4.hpp and strata/prefill/kernels.hpp).
 #include "strata/kernels/kv_stream.hpp"
 
 #include "sc_handoff.h"
+#include "strata/kernels/kv_q4.hpp"
+#include "strata/prefill/kernels.hpp"
+
+#include <type_traits>
 
 #include <cstdio>
 #include <cstdlib>
@@ -44,7 +49,25 @@ sc_kv_runs runs_of(const QsaAttnPools& slots, const KvHostPools& host, int fmt, 
     return r;
 }
 
+// KvHostPools as the C-ABI's sc_kv_pools (the same eight pointers; null stays null).
+static_assert(std::is_standard_layout_v<KvHostPools> && sizeof(KvHostPools) == sizeof(sc_kv_pools),
+              "KvHostPools and sc_kv_pools hold the same eight pointers");
+const sc_kv_pools* c_pools(const KvHostPools* p, sc_kv_pools& out) {
+    if (!p) return nullptr;
+    out = sc_kv_pools{p->k_pool, p->v_pool, p->k_q, p->v_q, p->k_scale, p->v_scale, p->k_q4, p->v_q4};
+    return &out;
+}
+
 }  // namespace
+
+void kv_append_q4(uint8_t* k_q4, uint8_t* v_q4, const int32_t* page_table, int64_t pos0, int64_t T, const float* K,
+                  const float* V, const QsaShapes& s, void* stream, const KvHostPools* host,
+                  const KvHostPools* stage) {
+    sc_kv_pools h{}, st{};
+    check(sc_kv_append_q4_async(k_q4, v_q4, page_table, pos0, T, K, V, s.n_head_kv, s.head_dim, s.page_size, stream,
+                                c_pools(host, h), c_pools(stage, st)),
+          "kv_append_q4");
+}
 
 void kv_stream_reset(const KvStreamMap& m, void* stream) {
     check(sc_kv_stream_reset(m.page_table, m.n_blocks, m.slot_block, m.slot_stamp, m.slot_ref, m.n_slots, m.ctl, stream),
@@ -86,3 +109,19 @@ strata::kernels::QsaAttnPools qsa_attn_pools(const QsaState& st) {
     return p;
 }
 }  // namespace strata::core
+
+namespace strata::prefill {
+
+void kv_append(const float* K, const float* V, int64_t T, int64_t pos0, const int32_t* page_table, int64_t page_size,
+               uint16_t* k_pool, uint16_t* v_pool, int8_t* k_q, int8_t* v_q, uint16_t* k_scale, uint16_t* v_scale,
+               void* stream, const strata::kernels::KvHostPools* host, const strata::kernels::KvHostPools* stage) {
+    sc_kv_pools h{}, st{};
+    const int rc = sc_kv_append_async(K, V, T, pos0, page_table, page_size, k_pool, v_pool, k_q, v_q, k_scale, v_scale,
+                                      stream, strata::kernels::c_pools(host, h), strata::kernels::c_pools(stage, st));
+    if (rc != SC_OK) {
+        std::fprintf(stderr, "kv_append: %s\n", sc_last_error());
+        std::exit(1);
+    }
+}
+
+}  // namespace strata::prefill

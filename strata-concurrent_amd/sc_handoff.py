@@ -60,6 +60,12 @@ class DecodeSlot(C.Structure):
         ("page_table", C.POINTER(C.c_void_p)), ("gdn_state", C.c_void_p)]
 
 
+class KvPools(C.Structure):
+    """sc_kv_pools (strata::kernels::KvHostPools): a layer's host copy or staging pool; unused members NULL."""
+    _fields_ = [("k_pool", C.c_void_p), ("v_pool", C.c_void_p), ("k_q", C.c_void_p), ("v_q", C.c_void_p),
+                ("k_scale", C.c_void_p), ("v_scale", C.c_void_p), ("k_q4", C.c_void_p), ("v_q4", C.c_void_p)]
+
+
 class KvRuns(C.Structure):
     _fields_ = [("src", C.c_void_p * 4), ("dst", C.c_void_p * 4), ("len", C.c_uint64 * 4), ("n", C.c_int32)]
 
@@ -139,6 +145,10 @@ _SIGS = {
     "sc_kv_ring_restore": (C.c_int, [_P, _I64, _I64, _I64, _P]),
     "sc_kv_stage_from_host": (C.c_int, [_P, _I64, _P]),
     "sc_kv_ring_table": (C.c_int, [_P, _I64, _I64, _P]),
+    "sc_kv_append_async": (C.c_int, [_P, _P, _I64, _I64, _P, _I64, _P, _P, _P, _P, _P, _P, _P, C.POINTER(KvPools),
+                                     C.POINTER(KvPools)]),
+    "sc_kv_append_q4_async": (C.c_int, [_P, _P, _P, _I64, _I64, _P, _P, _I64, _I64, _I64, _P, C.POINTER(KvPools),
+                                        C.POINTER(KvPools)]),
     "sc_kv_stream_reset": (C.c_int, [_P, _I64, _P, _P, _P, _I64, _P, _P]),
     "sc_kv_block_bytes": (_U64, [_I64, _I64, _I64, C.c_int32]),
     "sc_device_count": (C.c_int, [C.POINTER(C.c_int)]),

@@ -40,6 +40,15 @@ int sc_host_free(void*) { return SC_OK; }
 int sc_kv_ring_restore(const sc_kv_runs*, int64_t, int64_t, int64_t, void*) { ++fake::movers; return SC_OK; }
 int sc_kv_stage_from_host(const sc_kv_runs*, int64_t, void*) { ++fake::movers; return SC_OK; }
 int sc_kv_ring_table(int32_t*, int64_t, int64_t, void*) { return SC_OK; }
+// the prefill appends are device kernels with no host stand-in: a host-only program that reaches one is refused
+int sc_kv_append_async(const float*, const float*, int64_t, int64_t, const int32_t*, int64_t, uint16_t*, uint16_t*,
+                       int8_t*, int8_t*, uint16_t*, uint16_t*, void*, const sc_kv_pools*, const sc_kv_pools*) {
+    return failed("kv_append runs on the device only");
+}
+int sc_kv_append_q4_async(uint8_t*, uint8_t*, const int32_t*, int64_t, int64_t, const float*, const float*, int64_t,
+                          int64_t, int64_t, void*, const sc_kv_pools*, const sc_kv_pools*) {
+    return failed("kv_append_q4 runs on the device only");
+}
 int sc_kv_stream_reset(int32_t*, int64_t, int32_t*, int32_t*, int32_t*, int64_t, int32_t*, void*) { ++fake::movers; return SC_OK; }
 uint64_t sc_kv_block_bytes(int64_t h, int64_t d, int64_t ps, int32_t) { return uint64_t(h * d * ps * 4); }
 }
