@@ -431,12 +431,18 @@ def arena_handoff(sc, geo, tokens: int, slot, link_h2d: float, link_d2h: float, 
         r.reserve()                                       # the reader's one mapping of the arena, populated
         out["reader_reserve_ms"] = round((time.perf_counter() - t0) * 1e3, 1)
         dst = sc.new_slot(geo, tokens, fill=0)
+        side, gathered = sc.Stream(), sc.Event()
         pub, mpub, rd, rdv, mnt, opn, rim, rim_mover = [], [], [], [], [], [], [], []
         for rep in range(reps):
             c = w.claim(0, 7, 2 + rep)
             t0 = time.perf_counter()
-            enc.encode(payload.ptr, n, stream)
-            mover.publish(w, c, payload.ptr, n, tokens, stream.handle)
+            # the mover's D2H starts once the gather has placed every payload byte; the encoder's FNV-1a (which is
+            # the arena's payload hash: the same function and seed over the same bytes) runs beside it, so the
+            # mover does not hash again and the arena publishes the encoder's hash
+            enc.encode(payload.ptr, n, stream, gathered=gathered)
+            side.wait(gathered)
+            mover.write(w, c, payload.ptr, n, side.handle, want_hash=False)
+            w.publish(c, tokens, n, enc.hash())
             pub.append((time.perf_counter() - t0) * 1e3)
             w.release(c.index, c.nonce)
             c = w.claim(0, 7, 2 + rep)
@@ -487,9 +493,11 @@ def arena_handoff(sc, geo, tokens: int, slot, link_h2d: float, link_d2h: float, 
         "read_before_mount_ms": round(min(rim), 2),
         "read_before_mount_mover": [[round(x, 2) for x in t] for t in rim_mover],
         "round_trip_bit_exact": bool(same),
-        "method": "publish = device encode + mover (D2H in pinned chunks, host threads copy each chunk into the "
-                  "slot's mapped window while later chunks are in flight, device FNV-1a on a side stream) + the "
-                  "arena's publish; mover_publish = the same with the payload already encoded; read = mover (host threads copy slot chunks into pinned buffers, H2D of each "
+        "method": "publish = device encode, with the mover's D2H (pinned chunks, host threads copying each chunk "
+                  "into the slot's mapped window while later chunks are in flight) starting once the gather has "
+                  "placed the payload and the encoder's FNV-1a beside it, then the arena's publish with that hash; "
+                  "mover_publish = the mover alone on an encoded payload (its own device FNV-1a on a side stream) + "
+                  "the publish; read = mover (host threads copy slot chunks into pinned buffers, H2D of each "
                   "while the next is copied); read_verified adds the device FNV-1a check, each chunk hashed as it "
                   "lands with the running hash chained on the device; read_and_mount = verified read + decoder open + "
                   "one scatter launch; host wall clock around each call, best of the reps; the writer's "

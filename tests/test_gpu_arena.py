@@ -255,3 +255,38 @@ def test_slot_to_arena_to_slot(sc, ar, mover, shm, fmt):
             assert np.array_equal(a[key][:n], b[key][:n]) and (b[key][n:] == 0x5A).all(), key
     assert np.array_equal(dec.live_ids(), ids) and dec.small(0) == b"ple!" and dec.small(3) == bytes(range(16))
     w.release(c.index, c.nonce)
+
+
+def test_publish_overlapping_the_encoder_hash(sc, oracle, ar, mover, shm):
+    """The writer's fast order: the mover's D2H on a second stream waits only for the encoder's gather (its
+    `gathered` event), the encoder's FNV-1a runs beside the copy, the mover does not hash, and the arena publishes the
+    encoder's hash.  The slot must hold exactly the payload and pass the device reader's chunk-by-chunk check."""
+    import sc_wire as wire
+    geo = sc.geometry(**SMALL)
+    tokens = 1501
+    pools = sc.LayerPools(geo, 1, 1520, True)
+    pools.randomize(0xBEE)
+    ids = (np.arange(tokens, dtype=np.int64) * 31 % 151_000).astype(np.int32)
+    live, keep = wire.make_live(GEOKEY, ids, layer_lo=0, layer_hi=8, idx_dim=128, used=tokens)
+    enc = wire.Encoder(geo, pools, tokens, live, GEOM, PACK)
+    payload = sc.DeviceBuffer(enc.bytes, "uint8")
+    payload.fill(0x77)
+    path = shm / "h" / "arena"
+    w = ar.Arena.writer(path, TIERS, [enc.bytes, 160 << 20], PACK, GEOM)
+    r = ar.Arena.reader(path, PACK, GEOM)
+    stream, side, gathered = sc.Stream(), sc.Stream(), sc.Event()
+    c = w.claim(0, 5, 1)
+    enc.encode(payload.ptr, enc.bytes, stream, gathered=gathered)
+    side.wait(gathered)
+    assert mover.write(w, c, payload.ptr, enc.bytes, side.handle, want_hash=False) is None
+    h = enc.hash()
+    w.publish(c, tokens, enc.bytes, h)
+    got, s = r.read_host(c.index, c.nonce, 5, enc.bytes, check_hash=True)
+    stream.sync()
+    assert got.tobytes() == payload.numpy().tobytes() and s.payload_hash == h == oracle.fnv1a64(got.tobytes())
+    arrived = sc.DeviceBuffer(enc.bytes, "uint8")
+    mover.read(r, c.index, c.nonce, 5, arrived.ptr, enc.bytes, verify=True)
+    assert arrived.numpy().tobytes() == got.tobytes()
+    w.release(c.index, c.nonce)
+    w.close()
+    r.close()
