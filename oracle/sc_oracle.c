@@ -23,6 +23,7 @@
  *                           plus hand-computed blocks
  */
 #include <math.h>
+#include <pthread.h>
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
@@ -415,4 +416,42 @@ uint64_t sco_cpu_handoff(const uint8_t* slot_src, uint8_t* slot_dst, uint64_t by
     for (uint64_t at = 0; at < bytes; at += seg) memcpy(decoded + at, wire + at, bytes - at < seg ? bytes - at : seg);
     for (uint64_t at = 0; at < bytes; at += seg) memcpy(slot_dst + at, decoded + at, bytes - at < seg ? bytes - at : seg);
     return h_enc;
+}
+
+/* Not the reference's path: the host's plain copy ceiling for the CPU baseline's labelled N-core variant.  `threads`
+ * threads each memcpy one contiguous 1/threads share of `bytes` (at 4 KiB granules) from src to dst. */
+typedef struct {
+    uint8_t* dst;
+    const uint8_t* src;
+    uint64_t n;
+} sco_copy_share;
+
+static void* sco_copy_worker(void* arg) {
+    const sco_copy_share* s = (const sco_copy_share*) arg;
+    memcpy(s->dst, s->src, s->n);
+    return NULL;
+}
+
+int sco_memcpy_threads(uint8_t* dst, const uint8_t* src, uint64_t bytes, int threads) {
+    enum { kMaxThreads = 64 };
+    if (threads < 1 || threads > kMaxThreads) return -1;
+    pthread_t tid[kMaxThreads];
+    sco_copy_share share[kMaxThreads];
+    const uint64_t per = ((bytes / (uint64_t) threads) + 4095) & ~4095ull;
+    int started = 0;
+    for (int i = 0; i < threads; ++i) {
+        const uint64_t at = per * (uint64_t) i;
+        share[i].dst = dst + at;
+        share[i].src = src + at;
+        share[i].n = at >= bytes ? 0 : (bytes - at < per ? bytes - at : per);
+        if (i == 0) continue;   /* the calling thread takes share 0 */
+        if (pthread_create(&tid[i], NULL, sco_copy_worker, &share[i]) != 0) break;
+        started = i;
+    }
+    sco_copy_worker(&share[0]);
+    for (int i = 1; i <= started; ++i) pthread_join(tid[i], NULL);
+    if (started != threads - 1) {   /* a thread could not start: copy its shares here */
+        for (int i = started + 1; i < threads; ++i) sco_copy_worker(&share[i]);
+    }
+    return 0;
 }

@@ -57,6 +57,7 @@ for _name, _res, _args in (
     ("sco_handoff_carve", None, [_G, _I64, _I64, C.c_int, C.POINTER(_P), C.POINTER(_P), C.c_int, C.POINTER(_P),
                                  C.POINTER(_P), _I64, _I64, C.POINTER(_P), C.POINTER(_P), C.POINTER(_P), _I64, _P]),
     ("sco_cpu_handoff", _U64, [_P, _P, _U64, _P]),
+    ("sco_memcpy_threads", C.c_int, [_P, _P, _U64, C.c_int]),
 ):
     _fn = getattr(lib, _name)
     _fn.restype = _res
@@ -275,6 +276,11 @@ def resume(geo, tokens: int, image: np.ndarray, state: dict) -> None:
 
 def cpu_handoff(src: np.ndarray, dst: np.ndarray, scratch: np.ndarray) -> int:
     return int(lib.sco_cpu_handoff(_ptr(src), _ptr(dst), src.size, _ptr(scratch)))
+
+
+def memcpy_threads(src: np.ndarray, dst: np.ndarray, threads: int) -> None:
+    """Not the reference's path: `threads` threads memcpy one share each (the host's plain copy ceiling)."""
+    assert src.nbytes == dst.nbytes and lib.sco_memcpy_threads(_ptr(dst), _ptr(src), src.nbytes, threads) == 0
 
 
 # ---- quantized K/V formats ---------------------------------------------------------------------------------------

@@ -258,3 +258,13 @@ def test_cpu_handoff_pipeline_round_trip(oracle):
     scratch = np.empty(3 * src.size, dtype=np.uint8)
     h = oracle.cpu_handoff(src, dst, scratch)
     assert h == oracle.fnv1a64(src) and np.array_equal(src, dst)
+
+
+def test_memcpy_threads_copies_every_byte(oracle):
+    """The CPU baseline's labelled N-core copy ceiling copies the buffer exactly, for share boundaries that fall
+    inside the buffer, past its end, and for one thread."""
+    data = np.random.default_rng(5).integers(0, 256, 1_000_003, dtype=np.uint8)
+    for threads in (1, 3, 8, 64):
+        out = np.zeros_like(data)
+        oracle.memcpy_threads(data, out, threads)
+        assert np.array_equal(out, data), threads
