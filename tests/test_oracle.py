@@ -177,7 +177,7 @@ def _geo(oracle, **kw):
 
 
 @pytest.mark.parametrize("layers,tokens,payload", [
-    (16, 4096, 59_899_904),        # config 1
+    (16, 4096, 59_899_904),        # config 1: the toy handoff of 16 layers at 4096 tokens
     (48, 32768, 884_342_784),      # config 2
     (48, 131072, 3_300_261_888),   # config 3
     (48, 8192, 280_363_008),       # config 4, 8K slot
