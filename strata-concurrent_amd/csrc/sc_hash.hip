@@ -94,20 +94,32 @@ __device__ __forceinline__ uint32_t run_pair(const uint8_t* p, uint64_t n, bool 
     return x;
 }
 
-// p^k mod 2^64 for k = 1..16 as four 16-bit limbs, limb[16 - k] for the byte k places before a block's end.
-struct PowLimbs {
-    uint32_t limb[16][4];
+// p^k mod 2^64 for k = 1..16 as four signed 16-bit digits, digit[16 - k] for the byte k places before a block's end:
+// p^k = sum_j digit[j] 2^(16 j) mod 2^64 with every digit in [-2^15, 2^15) (balanced base 2^16; the carry out of the
+// top digit is a multiple of 2^64 and drops).  The digits of bytes c and c + 1 of a block pair up as one 32-bit word,
+// the operand layout of the packed 16-bit dot product.
+struct PowDigits {
+    uint32_t pair[8][4];   // [c / 2][j]: digit of byte c in the low half, of byte c + 1 in the high half
 };
-constexpr PowLimbs pow_limbs() {
-    PowLimbs t{};
+constexpr PowDigits pow_digits() {
+    int32_t digit[16][4] = {};
     uint64_t pk = 1;
     for (int k = 1; k <= 16; ++k) {
         pk *= kFnvPrime;
-        for (int j = 0; j < 4; ++j) t.limb[16 - k][j] = uint32_t((pk >> (16 * j)) & 0xFFFFu);
+        uint64_t v = pk;
+        for (int j = 0; j < 4; ++j) {
+            const int32_t d = int32_t(int16_t(uint16_t(v & 0xFFFFu)));
+            digit[16 - k][j] = d;
+            v = (v - uint64_t(int64_t(d))) >> 16;
+        }
     }
+    PowDigits t{};
+    for (int c = 0; c < 16; c += 2)
+        for (int j = 0; j < 4; ++j)
+            t.pair[c / 2][j] = (uint32_t(digit[c][j]) & 0xFFFFu) | (uint32_t(digit[c + 1][j]) << 16);
     return t;
 }
-constexpr PowLimbs kPowLimbs = pow_limbs();
+constexpr PowDigits kPowDigits = pow_digits();
 constexpr uint64_t kPrime16 = [] {
     uint64_t r = 1;
     for (int k = 0; k < 16; ++k) r *= kFnvPrime;
@@ -115,21 +127,33 @@ constexpr uint64_t kPrime16 = [] {
 }();
 
 // The Horner sum of 16 bytes given the true low byte `l` before them: sum over c of d_c p^(16-c), d_c = (l ^ b) - l.
-// With |d| <= 255 and 16-bit limbs of the powers, each limb's sum of 16 products stays below 2^28, so the four sums
-// are exact in 32-bit integers and every product is a full-rate 24-bit multiply-add.
+// Per digit j, S_j = sum_c d_c digit[c][j]: |d| <= 255 and |digit| <= 2^15, so |S_j| < 16 * 255 * 2^15 < 2^28 and the
+// sums are exact in 32-bit integers.  Two bytes' d values share one word as signed 16-bit halves, so each S_j takes
+// one packed dot product (v_dot2_i32_i16) per byte pair: 2 operations per byte for the four digits.
+typedef short v2i16 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ int32_t dot2(uint32_t a, uint32_t b, int32_t acc) {
+    return __builtin_amdgcn_sdot2(__builtin_bit_cast(v2i16, a), __builtin_bit_cast(v2i16, b), acc, false);
+}
 __device__ __forceinline__ uint64_t block_sum(const u32x4 v, uint32_t& l) {
     const uint32_t dw[4] = {v.x, v.y, v.z, v.w};
     int32_t s0 = 0, s1 = 0, s2 = 0, s3 = 0;
+    // `m` carries the low byte's product unmasked: only its low 8 bits are ever read
+    uint32_t m = l;
 #pragma unroll
-    for (int c = 0; c < 16; ++c) {
-        const uint32_t x = (l ^ (dw[c >> 2] >> (8 * (c & 3)))) & 0xFFu;
-        const int32_t d = int32_t(x) - int32_t(l);
-        l = __umul24(x, kPrimeLow) & 0xFFu;
-        s0 += d * int32_t(kPowLimbs.limb[c][0]);
-        s1 += d * int32_t(kPowLimbs.limb[c][1]);
-        s2 += d * int32_t(kPowLimbs.limb[c][2]);
-        s3 += d * int32_t(kPowLimbs.limb[c][3]);
+    for (int c = 0; c < 16; c += 2) {
+        const uint32_t x0 = (m ^ (dw[c >> 2] >> (8 * (c & 3)))) & 0xFFu;
+        const uint32_t d0 = x0 - (m & 0xFFu);
+        m = __umul24(x0, kPrimeLow);
+        const uint32_t x1 = (m ^ (dw[(c + 1) >> 2] >> (8 * ((c + 1) & 3)))) & 0xFFu;
+        const uint32_t d1 = x1 - (m & 0xFFu);
+        m = __umul24(x1, kPrimeLow);
+        const uint32_t dp = __builtin_amdgcn_perm(d1, d0, 0x05040100u);   // low halves: d0 | d1 << 16
+        s0 = dot2(dp, kPowDigits.pair[c / 2][0], s0);
+        s1 = dot2(dp, kPowDigits.pair[c / 2][1], s1);
+        s2 = dot2(dp, kPowDigits.pair[c / 2][2], s2);
+        s3 = dot2(dp, kPowDigits.pair[c / 2][3], s3);
     }
+    l = m & 0xFFu;
     return uint64_t(int64_t(s0)) + (uint64_t(int64_t(s1)) << 16) + (uint64_t(int64_t(s2)) << 32) +
            (uint64_t(int64_t(s3)) << 48);
 }
@@ -236,56 +260,70 @@ __global__ void __launch_bounds__(kThreads) fnv_pair_kernel(const uint8_t* data,
 }
 
 // The workgroups' start states for one pass, in one workgroup.  Workgroup g maps the state (a, c) = (bit j, bit
-// j + 1) at its first segment to (a ^ T_g, c ^ V_g(a)) at the next workgroup's; such maps of a 2-bit state are
-// 4-entry tables (one byte, two bits per entry), composed in a run per thread, scanned across threads in LDS, and
-// applied to the seed's bits.
-__device__ __forceinline__ uint32_t map_of(uint32_t summary) {
-    uint32_t m = 0;
-    for (uint32_t st = 0; st < 4; ++st) {
-        const uint32_t a = st & 1u, c = st >> 1;
-        const uint32_t na = a ^ (summary & 1u), nc = c ^ ((summary >> (1 + a)) & 1u);
-        m |= (na | (nc << 1)) << (2 * st);
-    }
-    return m;
-}
-// g after f
-__device__ __forceinline__ uint32_t compose(uint32_t g, uint32_t f) {
-    uint32_t m = 0;
-    for (uint32_t st = 0; st < 4; ++st) m |= ((g >> (2 * ((f >> (2 * st)) & 3u))) & 3u) << (2 * st);
-    return m;
-}
-constexpr uint32_t kIdentityMap = 0u | (1u << 2) | (2u << 4) | (3u << 6);
-
+// j + 1) at its first segment to (a ^ t, c ^ v_a) at the next workgroup's, and its summary byte is that map: t in bit
+// 0, v_0 in bit 1, v_1 in bit 2 (0 is the identity).  Such maps compose in a few bit operations (g after f):
+//   t = t_f ^ t_g,  v_a = v_a(f) ^ v_(a ^ t_f)(g)   (g's two v bits trade places when t_f is set).
+// Each thread composes its run of summaries (read 16 bytes at a time), the runs are scanned across threads in LDS,
+// and each thread then walks its run again from its start state, writing the states 16 at a time.
 // The state the hash starts from: the launch's seed, or the running hash at `seed_dev` when the input continues an
 // earlier one (read by every kernel that needs it, so one stream can chain pieces without a host round trip).
 __device__ __forceinline__ uint64_t start_state(uint64_t seed, const uint64_t* seed_dev) {
     return seed_dev ? *seed_dev : seed;
 }
 
+__device__ __forceinline__ uint32_t compose(uint32_t g, uint32_t f) {
+    const uint32_t gv = (f & 1u) ? (((g >> 1) & 2u) | ((g << 1) & 4u)) : (g & 6u);
+    return f ^ (g & 1u) ^ gv;
+}
+__device__ __forceinline__ uint32_t apply(uint32_t m, uint32_t st) {
+    const uint32_t a = st & 1u;
+    return (st ^ (m & 1u)) ^ (((m >> (1u + a)) & 1u) << 1);
+}
+
+constexpr uint64_t kScanVec = 16;   // summary bytes per vector load / state bytes per vector store
+
 __global__ void __launch_bounds__(kScanThreads) fnv_scan_kernel(const uint8_t* summary, uint64_t groups, int j,
                                                                  uint64_t seed, const uint64_t* seed_dev,
                                                                  uint8_t* gstate) {
     const uint32_t init = uint32_t((start_state(seed, seed_dev) >> j) & 3u);
-    const uint64_t per = (groups + kScanThreads - 1) / kScanThreads;
+    // runs of whole 16-byte vectors: the summaries and states live in 256-byte aligned buffers padded to 256 bytes,
+    // so a vector that starts before `groups` stays inside its buffer
+    const uint64_t per = ((groups + kScanThreads - 1) / kScanThreads + kScanVec - 1) / kScanVec * kScanVec;
     const uint64_t b = uint64_t(threadIdx.x) * per;
     const uint64_t e = b + per < groups ? b + per : groups;
-    uint32_t f = kIdentityMap;
-    for (uint64_t i = b; i < e; ++i) f = compose(map_of(summary[i]), f);
+    uint32_t f = 0;
+    for (uint64_t c = b; c < e; c += kScanVec) {
+        const u32x4 w = *(const gu32x4*) (summary + c);
+        const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int k = 0; k < int(kScanVec); ++k)
+            if (c + uint64_t(k) < e) f = compose((words[k >> 2] >> (8 * (k & 3))) & 7u, f);
+    }
     // inclusive scan of the run maps (Hillis-Steele), then the exclusive prefix of this thread's run
     __shared__ uint32_t s_map[kScanThreads];
     s_map[threadIdx.x] = f;
     __syncthreads();
     for (int o = 1; o < kScanThreads; o <<= 1) {
-        const uint32_t earlier = threadIdx.x >= uint32_t(o) ? s_map[threadIdx.x - o] : kIdentityMap;
+        const uint32_t earlier = threadIdx.x >= uint32_t(o) ? s_map[threadIdx.x - o] : 0u;
         __syncthreads();
         s_map[threadIdx.x] = compose(s_map[threadIdx.x], earlier);
         __syncthreads();
     }
-    const uint32_t before = threadIdx.x ? s_map[threadIdx.x - 1] : kIdentityMap;
-    uint32_t st = (before >> (2 * init)) & 3u;
-    for (uint64_t i = b; i < e; ++i) {
-        gstate[i] = uint8_t(st);
-        st = (map_of(summary[i]) >> (2 * st)) & 3u;
+    uint32_t st = apply(threadIdx.x ? s_map[threadIdx.x - 1] : 0u, init);
+    for (uint64_t c = b; c < e; c += kScanVec) {
+        const u32x4 w = *(const gu32x4*) (summary + c);
+        const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+        uint32_t out[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int k = 0; k < int(kScanVec); ++k) {
+            out[k >> 2] |= st << (8 * (k & 3));
+            st = apply((words[k >> 2] >> (8 * (k & 3))) & 7u, st);
+        }
+        if (c + kScanVec <= e) {
+            *(gu32x4*) (gstate + c) = u32x4{out[0], out[1], out[2], out[3]};
+        } else {
+            for (uint64_t k = 0; c + k < e; ++k) gstate[c + k] = uint8_t(out[k >> 2] >> (8 * (k & 3)));
+        }
     }
 }
 
@@ -307,8 +345,9 @@ __global__ void __launch_bounds__(kThreads) fnv_final_kernel(const uint8_t* data
         const uint8_t* p = data + begin;
         if (aligned && len == kFnvLaneBytes) {
             // the whole segment is loaded first (lanes are 256 bytes apart, so each 128-byte line is read by eight
-            // of a lane's loads: issued together they are served by one fetch), then 16 bytes per step: a block
-            // sum, then acc * p^16
+            // of a lane's loads, issued together), then 16 bytes per step: a block sum, then acc * p^16.  Loading
+            // the wave's 16 KiB with coalesced loads and handing segments to lanes through LDS measured slower
+            // (the 68 KiB of LDS per workgroup halves the waves per SIMD)
             u32x4 v[kFnvLaneBytes / 16];
 #pragma unroll
             for (int k = 0; k < kFnvLaneBytes / 16; ++k) v[k] = *(const gu32x4*) (p + 16 * k);
