@@ -17,17 +17,17 @@
 //      number), h_N = h_0 p^N + sum_n d_n p^(N-n) mod 2^64: independent per-segment Horner sums, folded with powers
 //      of p in any order.
 //
-// The buffer is split into lane segments of kFnvLaneBytes bytes, and the low byte is resolved two bits per pass over
-// the data.  Pass j (j = 0, 2, 4, 6) runs every segment's machine from its known start bits 0..j-1 twice, with start
-// bit j = 0 and = 1 (bit j+1 = 0 in both): the two machines share one 24-bit multiply, one in byte 0 and one in byte 2
-// of a register.  Bit j at the end, from the first machine, is the segment's xor term for bit j; bit j+1 at the end
-// of the machine whose start bit j is the true one is its xor term for bit j+1 (the term for a bit depends on the
-// lower start bits, and bit j is resolved before bit j+1 is needed).  Per pass: the data pass ballots the bit-j terms
-// and both candidate bit-(j+1) terms; a single-workgroup scan turns per-workgroup parities into exclusive prefixes;
-// a data-free launch resolves each segment's start bit j, picks its bit-(j+1) term and ballots it; a second scan
-// resolves bit j+1.  The last data pass runs the full machine from the now complete start byte, forms each segment's
-// Horner sum, scales it by p^(bytes after the segment) and reduces; a final workgroup adds h_0 p^N.  Five reads of
-// the input in all.
+// The buffer is split into lane segments of kFnvLaneBytes bytes, and the low byte is resolved in three passes over
+// the data: bits 0-2, 3-5 and 6-7.  A pass for bits j .. j + k - 1 runs every segment's machine from its known start
+// bits 0..j-1 once per combination of the unknown start bits j .. j + k - 2, with the pass's top bit started at 0:
+// the end value of a bit in a machine started from the true lower bits is the segment's xor term for that bit (the
+// term of a bit depends only on the lower start bits).  Two machines share one 24-bit multiply (bytes 0 and 2 of a
+// register); the first pass needs only bits 0..2, which follow l' = (l ^ b) * 3 mod 8, so its four machines share
+// one register a byte each.  Per pass: the data pass ballots the terms, each workgroup leaves its map of the k-bit
+// state (a byte), one workgroup scans the maps, and the next pass derives each lane's start bits from its
+// workgroup's state and the ballots by xor-prefix arithmetic.  The last data pass runs the full machine from the now
+// complete start byte, forms each segment's Horner sum, scales it by p^(bytes after the segment) and reduces; a final
+// workgroup adds h_0 p^N.  Four reads of the input in all.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -176,116 +176,247 @@ __device__ __forceinline__ uint64_t xor_prefix_excl(uint64_t x) {
     return x << 1;
 }
 
-// The ballots of one pass: per wave, T (bit-j terms), U0 and U1 (bit-(j+1) terms of the machines started with bit
-// j = 0 and = 1); a wave's V word (the bit-(j+1) terms of the machines that started from the true bit j) follows
-// from them and the true bit j of each lane.
+// The ballots of one pass, per wave: the terms of the lowest unresolved bit j (T), of bit j + 1 for either start
+// value a of bit j (U_a), and, in a three-bit pass, of bit j + 2 for each start pair (a, c) of bits j, j + 1 (W_ac).
+// A bit's term over a run is the xor of per-byte contributions that depend only on the lower bits of the state, so
+// each is the end value of that bit in a machine started from the right lower bits with the bit itself 0.
+constexpr int kMaxPassWords = 7;   // T, U0, U1, W00, W01, W10, W11
 struct PassWords {
-    uint64_t* t;
-    uint64_t* u0;
-    uint64_t* u1;
+    uint64_t* w[kMaxPassWords];
 };
+template <int kBits>
+constexpr int pass_words() { return kBits == 3 ? 7 : 3; }
 
-// One wave's step of the two-bit resolution: (a, c) are the true bits j, j+1 at the wave's first segment; returns
-// the lanes' bit-j values and advances (a, c) past the wave.
-__device__ __forceinline__ uint64_t wave_step(uint64_t t, uint64_t u0, uint64_t u1, uint32_t& a, uint32_t& c,
-                                              uint64_t& v) {
-    const uint64_t sj = xor_prefix_excl(t) ^ (a ? ~0ull : 0ull);
-    v = (sj & u1) | (~sj & u0);
-    a ^= uint32_t(__popcll(t)) & 1u;
-    c ^= uint32_t(__popcll(v)) & 1u;
-    return sj;
+// The lanes' true start bits of one wave, as masks, from `st` (bit j in bit 0, j + 1 in bit 1, j + 2 in bit 2) at
+// the wave's first segment; `st` advances past the wave.  Each lane's term for a bit is chosen by its own true lower
+// bits, and the bit at a lane is the wave's incoming bit xor the terms of the lanes before it.
+template <int kBits>
+__device__ __forceinline__ void wave_masks(const uint64_t (&wd)[kMaxPassWords], uint32_t& st, uint64_t (&m)[3]) {
+    const uint32_t a = st & 1u, c = (st >> 1) & 1u;
+    const uint64_t sj = xor_prefix_excl(wd[0]) ^ (a ? ~0ull : 0ull);
+    const uint64_t v = (sj & wd[2]) | (~sj & wd[1]);
+    const uint64_t sc = xor_prefix_excl(v) ^ (c ? ~0ull : 0ull);
+    m[0] = sj;
+    m[1] = sc;
+    uint32_t next = (a ^ (uint32_t(__popcll(wd[0])) & 1u)) | ((c ^ (uint32_t(__popcll(v)) & 1u)) << 1);
+    if constexpr (kBits == 3) {
+        const uint32_t e = (st >> 2) & 1u;
+        const uint64_t x = (~sj & ~sc & wd[3]) | (~sj & sc & wd[4]) | (sj & ~sc & wd[5]) | (sj & sc & wd[6]);
+        m[2] = xor_prefix_excl(x) ^ (e ? ~0ull : 0ull);
+        next |= (e ^ (uint32_t(__popcll(x)) & 1u)) << 2;
+    }
+    st = next;
 }
 
-// This lane's true start bits j (bit 0 of the result) and j + 1 (bit 1), from its workgroup's start state `gstate`
-// (bit j, bit j + 1 at the workgroup's first segment) and the ballots of the workgroup's waves.
+// This lane's true start bits j .. j + kBits - 1 (bit 0 of the result upward), from its workgroup's start state and
+// the ballots of the workgroup's waves.
+template <int kBits>
 __device__ __forceinline__ uint32_t lane_bits(uint32_t gstate, const PassWords& w) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint64_t base = uint64_t(blockIdx.x) * 4;
-    uint32_t a = gstate & 1u, c = (gstate >> 1) & 1u;
-    uint64_t v = 0, sj = 0;
-    for (int k = 0; k <= wave; ++k) {
-        const uint32_t a0 = a, c0 = c;
-        sj = wave_step(w.t[base + k], w.u0[base + k], w.u1[base + k], a, c, v);
-        if (k == wave) { a = a0; c = c0; }
-    }
-    const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
-    return (uint32_t(sj >> lane) & 1u) | ((c ^ (uint32_t(__popcll(v & below)) & 1u)) << 1);
+    uint32_t st = gstate;
+    uint64_t m[3] = {0, 0, 0};
+    // every word this lane may need is loaded before the first step, so the loads overlap
+    uint64_t wd[kThreads / 64][kMaxPassWords] = {};
+#pragma unroll
+    for (int k = 0; k < kThreads / 64; ++k)
+#pragma unroll
+        for (int i = 0; i < pass_words<kBits>(); ++i)
+            if (k <= wave) wd[k][i] = w.w[i][base + k];
+#pragma unroll
+    for (int k = 0; k < kThreads / 64; ++k)
+        if (k <= wave) wave_masks<kBits>(wd[k], st, m);
+    uint32_t bits = 0;
+#pragma unroll
+    for (int i = 0; i < kBits; ++i) bits |= (uint32_t(m[i] >> lane) & 1u) << i;
+    return bits;
 }
 
-// Data pass for bits j, j + 1.  First completes each segment's start bits j - 2 and j - 1 from the previous pass
-// (bits 0..j-3 are in start[]), then runs the pair of machines, ballots T, U0, U1, and leaves the workgroup's
-// summary: bit 0 = xor of its T terms, bits 1 and 2 = xor of its V terms if bit j enters the workgroup as 0 or 1.
-__global__ void __launch_bounds__(kThreads) fnv_pair_kernel(const uint8_t* data, uint64_t n, int j, bool aligned,
+// The first pass only needs bits 0..2 of the state, which follow l' = ((l ^ b) * 3) mod 8 (179 = 3 mod 8): four
+// such machines share one register, one per byte (a 3-bit state times 3 stays below 2^8, so nothing carries across
+// bytes; the product's bits above 2 are masked by the next step).  Machine (a, c) - start bits 0, 1 = a, c - sits in
+// byte a + 2c.
+template <int k>
+__device__ __forceinline__ uint32_t spread4(uint32_t w) {
+    return __builtin_amdgcn_perm(0u, w, uint32_t(k | (k << 8) | (k << 16) | (k << 24)));
+}
+__device__ __forceinline__ uint32_t step_low3(uint32_t x, uint32_t b4) {
+    const uint32_t y = (x ^ b4) & 0x07070707u;
+    return y + (y << 1);
+}
+__device__ __forceinline__ uint32_t run_low3(const uint8_t* p, uint64_t n, bool full) {
+    uint32_t x = 0x03020100u;
+    if (full) {
+        uint32_t w[kFnvLaneBytes / 4];
+        load_segment(p, w);
+#pragma unroll
+        for (int k = 0; k < kFnvLaneBytes / 4; ++k) {
+            x = step_low3(x, spread4<0>(w[k]));
+            x = step_low3(x, spread4<1>(w[k]));
+            x = step_low3(x, spread4<2>(w[k]));
+            x = step_low3(x, spread4<3>(w[k]));
+        }
+    } else {
+        for (uint64_t i = 0; i < n; ++i) x = step_low3(x, uint32_t(p[i]) * 0x01010101u);
+    }
+    return x & 0x07070707u;
+}
+
+// Four low-byte machines in two registers (bytes 0 and 2 of each), one spread byte for both.
+__device__ __forceinline__ void run_quad(const uint8_t* p, uint64_t n, bool full, uint32_t& xa, uint32_t& xb) {
+    if (full) {
+        uint32_t w[kFnvLaneBytes / 4];
+        load_segment(p, w);
+#pragma unroll
+        for (int k = 0; k < kFnvLaneBytes / 4; ++k) {
+            uint32_t bb = spread<0>(w[k]);
+            xa = step_pair(xa, bb);
+            xb = step_pair(xb, bb);
+            bb = spread<1>(w[k]);
+            xa = step_pair(xa, bb);
+            xb = step_pair(xb, bb);
+            bb = spread<2>(w[k]);
+            xa = step_pair(xa, bb);
+            xb = step_pair(xb, bb);
+            bb = spread<3>(w[k]);
+            xa = step_pair(xa, bb);
+            xb = step_pair(xb, bb);
+        }
+        return;
+    }
+    for (uint64_t i = 0; i < n; ++i) {
+        const uint32_t bb = uint32_t(p[i]) * 0x10001u;
+        xa = step_pair(xa, bb);
+        xb = step_pair(xb, bb);
+    }
+}
+
+// Data pass for bits j .. j + kBits - 1.  First completes each segment's start bits from the previous pass (which
+// resolved kPrevBits bits; the bits below it are in start[]), then runs the machines - two (start bit j = 0, 1) for
+// a two-bit pass, four (start bits j, j + 1 = 00, 10, 01, 11) for a three-bit one - ballots the terms, and leaves
+// the workgroup's summary: its map of the state at its first segment (bit 0 t, bits 1-2 v_a, bits 3-6 w_ac).
+template <int kBits, int kPrevBits>
+__global__ void __launch_bounds__(kThreads) fnv_pass_kernel(const uint8_t* data, uint64_t n, int j, bool aligned,
                                                              uint8_t* start, PassWords prev, const uint8_t* gstate_prev,
                                                              PassWords out, uint8_t* summary) {
     const uint64_t seg = uint64_t(blockIdx.x) * kThreads + threadIdx.x;
     const uint64_t begin = seg * kFnvLaneBytes;
     const bool live = begin < n;
     uint32_t s = 0;
-    if (j > 0) {
-        const uint32_t bits = lane_bits(gstate_prev[blockIdx.x], prev);
-        s = (j > 2 && live ? uint32_t(start[seg]) : 0u) | (bits << (j - 2));
+    if constexpr (kPrevBits > 0) {
+        const uint32_t bits = lane_bits<kPrevBits>(gstate_prev[blockIdx.x], prev);
+        const int lo = j - kPrevBits;
+        s = (lo > 0 && live ? uint32_t(start[seg]) : 0u) | (bits << lo);
         if (live) start[seg] = uint8_t(s);
     }
-    uint32_t e = 0;
-    if (live) {
+    uint32_t ea = 0, eb = 0;
+    if constexpr (kBits == 3 && kPrevBits == 0) {
+        // bits 0..2 (j = 0): the four machines of run_low3 end in bytes a + 2c; regroup them into the layout the
+        // ballots below read (ea: machines (0, 0) in byte 0 and (1, 0) in byte 2; eb: (0, 1) and (1, 1))
+        if (live) {
+            const uint64_t len = n - begin < kFnvLaneBytes ? n - begin : kFnvLaneBytes;
+            const uint32_t x = run_low3(data + begin, len, aligned && len == kFnvLaneBytes);
+            ea = (x & 0xFFu) | (((x >> 8) & 0xFFu) << 16);
+            eb = ((x >> 16) & 0xFFu) | ((x >> 24) << 16);
+        }
+    } else if (live) {
         const uint64_t len = n - begin < kFnvLaneBytes ? n - begin : kFnvLaneBytes;
-        e = run_pair(data + begin, len, aligned && len == kFnvLaneBytes, s | ((s | (1u << j)) << 16));
+        const bool full = aligned && len == kFnvLaneBytes;
+        ea = s | ((s | (1u << j)) << 16);
+        if constexpr (kBits == 2) {
+            ea = run_pair(data + begin, len, full, ea);
+        } else {
+            const uint32_t sc = s | (1u << (j + 1));
+            eb = sc | ((sc | (1u << j)) << 16);
+            run_quad(data + begin, len, full, ea, eb);
+        }
     }
-    const uint64_t bt = __ballot((e >> j) & 1u), b0 = __ballot((e >> (j + 1)) & 1u),
-                   b1 = __ballot((e >> (16 + j + 1)) & 1u);
-    __shared__ uint64_t s_w[3][kThreads / 64];
+    uint64_t bw[kMaxPassWords] = {};
+    bw[0] = __ballot((ea >> j) & 1u);
+    bw[1] = __ballot((ea >> (j + 1)) & 1u);
+    bw[2] = __ballot((ea >> (16 + j + 1)) & 1u);
+    if constexpr (kBits == 3) {
+        bw[3] = __ballot((ea >> (j + 2)) & 1u);        // start (a, c) = (0, 0)
+        bw[4] = __ballot((eb >> (j + 2)) & 1u);        // (0, 1)
+        bw[5] = __ballot((ea >> (16 + j + 2)) & 1u);   // (1, 0)
+        bw[6] = __ballot((eb >> (16 + j + 2)) & 1u);   // (1, 1)
+    }
+    __shared__ uint64_t s_w[kMaxPassWords][kThreads / 64];
     const int wave = threadIdx.x >> 6;
     if ((threadIdx.x & 63) == 0) {
         const uint64_t at = uint64_t(blockIdx.x) * 4 + wave;
-        out.t[at] = bt;
-        out.u0[at] = b0;
-        out.u1[at] = b1;
-        s_w[0][wave] = bt;
-        s_w[1][wave] = b0;
-        s_w[2][wave] = b1;
+#pragma unroll
+        for (int i = 0; i < pass_words<kBits>(); ++i) {
+            out.w[i][at] = bw[i];
+            s_w[i][wave] = bw[i];
+        }
     }
     __syncthreads();
     if (threadIdx.x == 0) {
         uint32_t sum = 0;
-        for (uint32_t in = 0; in < 2; ++in) {
-            uint32_t a = in, c = 0;
-            uint64_t v;
-            for (int k = 0; k < kThreads / 64; ++k) wave_step(s_w[0][k], s_w[1][k], s_w[2][k], a, c, v);
-            if (in == 0) sum |= a ^ in;   // the xor of the T terms
-            sum |= c << (1 + in);
+        for (uint32_t in = 0; in < (1u << (kBits - 1)); ++in) {   // start (a, c) = (in & 1, in >> 1), e = 0
+            const uint32_t a = in & 1u, c = (in >> 1) & 1u;
+            uint32_t st = in;
+            uint64_t m[3];
+            for (int k = 0; k < kThreads / 64; ++k) {
+                uint64_t wd[kMaxPassWords] = {};
+#pragma unroll
+                for (int i = 0; i < pass_words<kBits>(); ++i) wd[i] = s_w[i][k];
+                wave_masks<kBits>(wd, st, m);
+            }
+            if (in == 0) sum |= st & 1u;                                  // t
+            if (c == 0) sum |= ((st >> 1) & 1u) << (1 + a);               // v_a: the end bit j + 1 from c = 0
+            if constexpr (kBits == 3) sum |= ((st >> 2) & 1u) << (3 + 2 * a + c);   // w_ac: end bit j + 2 from e = 0
         }
         summary[blockIdx.x] = uint8_t(sum);
     }
 }
 
-// The workgroups' start states for one pass, in one workgroup.  Workgroup g maps the state (a, c) = (bit j, bit
-// j + 1) at its first segment to (a ^ t, c ^ v_a) at the next workgroup's, and its summary byte is that map: t in bit
-// 0, v_0 in bit 1, v_1 in bit 2 (0 is the identity).  Such maps compose in a few bit operations (g after f):
-//   t = t_f ^ t_g,  v_a = v_a(f) ^ v_(a ^ t_f)(g)   (g's two v bits trade places when t_f is set).
-// Each thread composes its run of summaries (read 16 bytes at a time), the runs are scanned across threads in LDS,
-// and each thread then walks its run again from its start state, writing the states 16 at a time.
 // The state the hash starts from: the launch's seed, or the running hash at `seed_dev` when the input continues an
 // earlier one (read by every kernel that needs it, so one stream can chain pieces without a host round trip).
 __device__ __forceinline__ uint64_t start_state(uint64_t seed, const uint64_t* seed_dev) {
     return seed_dev ? *seed_dev : seed;
 }
 
+// The workgroups' start states for one pass, in one workgroup.  Workgroup g maps the state (a, c, e) = (bit j,
+// j + 1, j + 2) at its first segment to (a ^ t, c ^ v_a, e ^ w_ac) at the next workgroup's, and its summary byte is
+// that map (bit 0 t, bits 1-2 v_0 v_1, bits 3-6 w_00 w_01 w_10 w_11; a two-bit pass has no e and no w).  Maps compose
+// as (g after f): t = t_f ^ t_g, v_a = v_a(f) ^ v_(a ^ t_f)(g), w_ac = w_ac(f) ^ w_(a ^ t_f, c ^ v_a(f))(g).
+// Each thread composes its run of summaries (read 16 bytes at a time), the runs are scanned across threads in LDS,
+// and each thread then walks its run again from its start state, writing the states 16 at a time.
+__device__ __forceinline__ uint32_t map_v(uint32_t m, uint32_t a) { return (m >> (1u + a)) & 1u; }
+__device__ __forceinline__ uint32_t map_w(uint32_t m, uint32_t a, uint32_t c) { return (m >> (3u + 2u * a + c)) & 1u; }
+template <int kBits>
 __device__ __forceinline__ uint32_t compose(uint32_t g, uint32_t f) {
-    const uint32_t gv = (f & 1u) ? (((g >> 1) & 2u) | ((g << 1) & 4u)) : (g & 6u);
-    return f ^ (g & 1u) ^ gv;
+    const uint32_t tf = f & 1u;
+    uint32_t r = tf ^ (g & 1u);
+#pragma unroll
+    for (uint32_t a = 0; a < 2; ++a) r |= (map_v(f, a) ^ map_v(g, a ^ tf)) << (1u + a);
+    if constexpr (kBits == 3) {
+#pragma unroll
+        for (uint32_t a = 0; a < 2; ++a)
+#pragma unroll
+            for (uint32_t c = 0; c < 2; ++c)
+                r |= (map_w(f, a, c) ^ map_w(g, a ^ tf, c ^ map_v(f, a))) << (3u + 2u * a + c);
+    }
+    return r;
 }
+template <int kBits>
 __device__ __forceinline__ uint32_t apply(uint32_t m, uint32_t st) {
-    const uint32_t a = st & 1u;
-    return (st ^ (m & 1u)) ^ (((m >> (1u + a)) & 1u) << 1);
+    const uint32_t a = st & 1u, c = (st >> 1) & 1u;
+    uint32_t r = (a ^ (m & 1u)) | ((c ^ map_v(m, a)) << 1);
+    if constexpr (kBits == 3) r |= (((st >> 2) & 1u) ^ map_w(m, a, c)) << 2;
+    return r;
 }
 
 constexpr uint64_t kScanVec = 16;   // summary bytes per vector load / state bytes per vector store
 
+template <int kBits>
 __global__ void __launch_bounds__(kScanThreads) fnv_scan_kernel(const uint8_t* summary, uint64_t groups, int j,
                                                                  uint64_t seed, const uint64_t* seed_dev,
                                                                  uint8_t* gstate) {
-    const uint32_t init = uint32_t((start_state(seed, seed_dev) >> j) & 3u);
+    constexpr uint32_t kMask = kBits == 3 ? 0x7Fu : 0x7u;
+    const uint32_t init = uint32_t(start_state(seed, seed_dev) >> j) & ((1u << kBits) - 1u);
     // runs of whole 16-byte vectors: the summaries and states live in 256-byte aligned buffers padded to 256 bytes,
     // so a vector that starts before `groups` stays inside its buffer
     const uint64_t per = ((groups + kScanThreads - 1) / kScanThreads + kScanVec - 1) / kScanVec * kScanVec;
@@ -297,7 +428,7 @@ __global__ void __launch_bounds__(kScanThreads) fnv_scan_kernel(const uint8_t* s
         const uint32_t words[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
         for (int k = 0; k < int(kScanVec); ++k)
-            if (c + uint64_t(k) < e) f = compose((words[k >> 2] >> (8 * (k & 3))) & 7u, f);
+            if (c + uint64_t(k) < e) f = compose<kBits>((words[k >> 2] >> (8 * (k & 3))) & kMask, f);
     }
     // inclusive scan of the run maps (Hillis-Steele), then the exclusive prefix of this thread's run
     __shared__ uint32_t s_map[kScanThreads];
@@ -306,10 +437,10 @@ __global__ void __launch_bounds__(kScanThreads) fnv_scan_kernel(const uint8_t* s
     for (int o = 1; o < kScanThreads; o <<= 1) {
         const uint32_t earlier = threadIdx.x >= uint32_t(o) ? s_map[threadIdx.x - o] : 0u;
         __syncthreads();
-        s_map[threadIdx.x] = compose(s_map[threadIdx.x], earlier);
+        s_map[threadIdx.x] = compose<kBits>(s_map[threadIdx.x], earlier);
         __syncthreads();
     }
-    uint32_t st = apply(threadIdx.x ? s_map[threadIdx.x - 1] : 0u, init);
+    uint32_t st = apply<kBits>(threadIdx.x ? s_map[threadIdx.x - 1] : 0u, init);
     for (uint64_t c = b; c < e; c += kScanVec) {
         const u32x4 w = *(const gu32x4*) (summary + c);
         const uint32_t words[4] = {w.x, w.y, w.z, w.w};
@@ -317,7 +448,7 @@ __global__ void __launch_bounds__(kScanThreads) fnv_scan_kernel(const uint8_t* s
 #pragma unroll
         for (int k = 0; k < int(kScanVec); ++k) {
             out[k >> 2] |= st << (8 * (k & 3));
-            st = apply((words[k >> 2] >> (8 * (k & 3))) & 7u, st);
+            st = apply<kBits>((words[k >> 2] >> (8 * (k & 3))) & kMask, st);
         }
         if (c + kScanVec <= e) {
             *(gu32x4*) (gstate + c) = u32x4{out[0], out[1], out[2], out[3]};
@@ -337,7 +468,7 @@ __global__ void __launch_bounds__(kThreads) fnv_final_kernel(const uint8_t* data
                                                               const uint8_t* gstate_prev, uint64_t* partial) {
     const uint64_t seg = uint64_t(blockIdx.x) * kThreads + threadIdx.x;
     const uint64_t begin = seg * kFnvLaneBytes;
-    const uint32_t bits67 = lane_bits(gstate_prev[blockIdx.x], prev);
+    const uint32_t bits67 = lane_bits<2>(gstate_prev[blockIdx.x], prev);
     uint64_t acc = 0;
     if (begin < n) {
         uint32_t l = uint32_t(start[seg]) | (bits67 << 6);
@@ -383,7 +514,7 @@ __global__ void __launch_bounds__(kScanThreads) fnv_reduce_kernel(const uint64_t
 
 }  // namespace
 
-// Workspace: [start bytes: one per segment][ballot words T, U0, U1: two sets (this pass, the previous)]
+// Workspace: [start bytes: one per segment][ballot words T, U0, U1, W00..W11: two sets (this pass, the previous)]
 // [summaries][workgroup start states: two sets][partial sums].
 FnvWorkspace fnv_workspace(uint64_t n) {
     FnvWorkspace w{};
@@ -392,8 +523,8 @@ FnvWorkspace fnv_workspace(uint64_t n) {
     auto up = [](uint64_t x) { return (x + 255) / 256 * 256; };
     w.off_start = 0;
     w.off_word0 = up(w.segments);
-    w.off_word1 = w.off_word0 + 3 * up(w.groups * 4 * 8);
-    w.off_parity = w.off_word1 + 3 * up(w.groups * 4 * 8);   // summaries
+    w.off_word1 = w.off_word0 + kMaxPassWords * up(w.groups * 4 * 8);
+    w.off_parity = w.off_word1 + kMaxPassWords * up(w.groups * 4 * 8);   // summaries
     w.off_prefix = w.off_parity + up(w.groups);               // start states, two sets
     w.off_partial = w.off_prefix + 2 * up(w.groups);
     w.bytes = w.off_partial + up(w.groups * 8 > 8 ? w.groups * 8 : 8);
@@ -406,10 +537,11 @@ hipError_t launch_fnv1a64(const void* data, uint64_t n, uint64_t seed, const uin
     uint8_t* ws = static_cast<uint8_t*>(workspace);
     const uint8_t* src = static_cast<const uint8_t*>(data);
     const bool aligned = (reinterpret_cast<uintptr_t>(data) & 15u) == 0;
-    const uint64_t word_bytes = (w.off_word1 - w.off_word0) / 3;
+    const uint64_t word_bytes = (w.off_word1 - w.off_word0) / kMaxPassWords;
     auto words = [&](uint64_t off) {
-        return PassWords{reinterpret_cast<uint64_t*>(ws + off), reinterpret_cast<uint64_t*>(ws + off + word_bytes),
-                         reinterpret_cast<uint64_t*>(ws + off + 2 * word_bytes)};
+        PassWords p{};
+        for (int k = 0; k < kMaxPassWords; ++k) p.w[k] = reinterpret_cast<uint64_t*>(ws + off + k * word_bytes);
+        return p;
     };
     const PassWords set[2] = {words(w.off_word0), words(w.off_word1)};
     uint8_t* start = ws + w.off_start;
@@ -418,16 +550,19 @@ hipError_t launch_fnv1a64(const void* data, uint64_t n, uint64_t seed, const uin
     uint8_t* gstate[2] = {ws + w.off_prefix, ws + w.off_prefix + half};
     uint64_t* partial = reinterpret_cast<uint64_t*>(ws + w.off_partial);
     if (w.groups > 0) {
+        // bits 0-2, then 3-5 (four machines per lane), then 6-7 (two): three reads of the data before the final one;
+        // each pass reads the previous pass's ballots and workgroup states
         const dim3 grid(unsigned(w.groups)), block(kThreads), one(1), scan(kScanThreads);
-        for (int q = 0; q < 4; ++q) {
-            // pass q resolves bits 2q and 2q + 1; it reads the previous pass's ballots and workgroup states
-            const int j = 2 * q;
-            hipLaunchKernelGGL(fnv_pair_kernel, grid, block, 0, stream, src, n, j, aligned, start, set[(q + 1) & 1],
-                               gstate[(q + 1) & 1], set[q & 1], summary);
-            hipLaunchKernelGGL(fnv_scan_kernel, one, scan, 0, stream, summary, w.groups, j, seed, seed_dev,
-                               gstate[q & 1]);
-        }
-        hipLaunchKernelGGL(fnv_final_kernel, grid, block, 0, stream, src, n, aligned, start, set[1], gstate[1],
+        hipLaunchKernelGGL((fnv_pass_kernel<3, 0>), grid, block, 0, stream, src, n, 0, aligned, start, set[1],
+                           gstate[1], set[0], summary);
+        hipLaunchKernelGGL(fnv_scan_kernel<3>, one, scan, 0, stream, summary, w.groups, 0, seed, seed_dev, gstate[0]);
+        hipLaunchKernelGGL((fnv_pass_kernel<3, 3>), grid, block, 0, stream, src, n, 3, aligned, start, set[0],
+                           gstate[0], set[1], summary);
+        hipLaunchKernelGGL(fnv_scan_kernel<3>, one, scan, 0, stream, summary, w.groups, 3, seed, seed_dev, gstate[1]);
+        hipLaunchKernelGGL((fnv_pass_kernel<2, 3>), grid, block, 0, stream, src, n, 6, aligned, start, set[1],
+                           gstate[1], set[0], summary);
+        hipLaunchKernelGGL(fnv_scan_kernel<2>, one, scan, 0, stream, summary, w.groups, 6, seed, seed_dev, gstate[0]);
+        hipLaunchKernelGGL(fnv_final_kernel, grid, block, 0, stream, src, n, aligned, start, set[0], gstate[0],
                            partial);
     }
     // the reduce reads the start state before it writes `out`, so `out` may be `seed_dev` itself
