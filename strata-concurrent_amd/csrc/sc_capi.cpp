@@ -903,6 +903,10 @@ int append_launch(int32_t kind, const float* K, const float* V, int64_t T, int64
     if (!K || !V) return fail(SC_EINVAL, "sc_handoff: kv_append: missing K or V");
     if (misaligned(K, 16) || misaligned(V, 16))
         return fail(SC_EINVAL, "sc_handoff: kv_append: K and V must be 16-byte aligned");
+    // the tiles index a row's chunks (f16 rows) or (token, head) rows (quantized) with 32-bit integers
+    const uint64_t units = uint64_t(T) * uint64_t(H) * (kind == sc::kKv32 ? uint64_t(D * 2 / 16) : 1u);
+    if (units >= kMaxRowChunks)
+        return fail(SC_ERANGE, "sc_handoff: kv_append: one call's K or V beyond 2^31 chunks (split the chunk)");
     const uintptr_t code_align = kind == sc::kKv32 ? 16 : kind == sc::kKvQ8 ? 4 : 2;
     sc::AppendRows rows{};
     int n = 0;
@@ -929,7 +933,7 @@ int append_launch(int32_t kind, const float* K, const float* V, int64_t T, int64
             r.pos0 = pos0;
             r.ld = std::numeric_limits<int64_t>::max();   // the reference bounds no page: the caller sized the pools
             r.aux = int32_t(T);
-            r.n = kind == sc::kKv32 ? uint64_t(T * H) * uint64_t(D * 2 / 16) : uint64_t(T * H);
+            r.n = units;
         }
     }
     const uint64_t per_tile = kind == sc::kKv32 ? sc::kTileChunks : sc::kQuantUnitsPerTile;
