@@ -163,6 +163,28 @@ def test_k8v4_aliased_calls(sc, oracle, cuda):
     assert (_read(sc, kq["v"]) == SENTINEL).all() and (_read(sc, vq4["k"]) == SENTINEL).all()
 
 
+def test_q4_pool_aligned_to_two_bytes(sc, oracle, cuda):
+    """q4_0 pools need only 2-byte alignment (the reference's block is 18 bytes): a pool that starts 2 bytes past a
+    16-byte boundary takes the 2-byte store path and must hold the same bytes as the oracle's."""
+    T, pos0 = 19, 1
+    n_pages = (pos0 + T + PS - 1) // PS + 1
+    x_k, x_v = _source(T, 31), _source(T, 32)
+    K, V = sc.DeviceBuffer(x_k.size, "float32"), sc.DeviceBuffer(x_v.size, "float32")
+    K.upload(x_k)
+    V.upload(x_v)
+    rows = n_pages * H * PS
+    kb, vb = sc.DeviceBuffer(rows * ROW["q4"] + 16, "uint8"), sc.DeviceBuffer(rows * ROW["q4"] + 16, "uint8")
+    kb.fill(SENTINEL)
+    vb.fill(SENTINEL)
+    assert sc.lib.sc_kv_append_q4_async(kb.ptr + 2, vb.ptr + 2, None, pos0, T, K.ptr, V.ptr, H, D, PS, None, None,
+                                        None) == 0, sc.last_error()
+    for buf, x in ((kb, x_k), (vb, x_v)):
+        want, _ = _expected(oracle, "q4", x, T, pos0, None, n_pages)
+        got = _read(sc, buf)
+        assert np.array_equal(got[2:2 + want.size], want)
+        assert (got[:2] == SENTINEL).all() and (got[2 + want.size:] == SENTINEL).all()
+
+
 def test_refusals_write_nothing(sc, cuda):
     T = 8
     K = sc.DeviceBuffer(T * H * D + 16, "float32")
