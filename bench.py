@@ -674,6 +674,43 @@ def quant_carve(sc, geo, tokens: int, stream, reps: int = 10) -> dict:
         plan.destroy()
         for b in slot.buffers():
             b.free()
+    # the per-layer writers with the reference's arguments (sc_kv_append_async: one launch per QSA layer, nothing
+    # allocated), K and V of every QSA layer in turn, f16 and int8 pools; HBM bytes = the f32 rows read + what is written
+    T, H, D = tokens, geo.n_head_kv, geo.head_dim
+    ev0, ev1 = sc.Event(), sc.Event()
+    per_layer = {}
+    for name, f16 in (("f16", True), ("int8", False)):
+        slot = sc.new_slot(geo, max_cells=tokens) if f16 else sc.new_quant_slot(geo, sc.SC_KV_INT8, tokens)
+
+        def appends():
+            for j in range(geo.n_qsa):
+                K, V = case.prefill.k[j].data_ptr(), case.prefill.v[j].data_ptr()
+                if f16:
+                    rc = sc.lib.sc_kv_append_async(K, V, T, 0, None, geo.page_size, slot.k_pool[j].data_ptr(),
+                                                   slot.v_pool[j].data_ptr(), None, None, None, None, stream.handle,
+                                                   None, None)
+                else:
+                    rc = sc.lib.sc_kv_append_async(K, V, T, 0, None, geo.page_size, None, None, slot.k_codes[j].ptr,
+                                                   slot.v_codes[j].ptr, slot.k_scale[j].ptr, slot.v_scale[j].ptr,
+                                                   stream.handle, None, None)
+                sc.check(rc, "sc_kv_append_async")
+        for _ in range(2):
+            appends()
+        times = []
+        for _ in range(reps):
+            ev0.record(stream)
+            appends()
+            ev1.record(stream)
+            ev1.sync()
+            times.append(ev0.elapsed_ms(ev1))
+        ms = sum(times) / len(times)
+        moved = geo.n_qsa * 2 * T * H * (D * 4 + (D * 2 if f16 else D + 8))
+        per_layer[name] = {"ms_all_layers": round(ms, 4), "launches": geo.n_qsa, "hbm_bytes": moved,
+                           "hbm_gbps": round(moved / (ms * 1e-3) / 1e9, 1),
+                           "frac": round(moved / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
+        for b in slot.buffers():
+            b.free()
+    out["kv_append_per_layer"] = per_layer
     return out
 
 
