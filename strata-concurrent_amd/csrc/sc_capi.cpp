@@ -173,6 +173,10 @@ constexpr uint64_t kMaxRowChunks = uint64_t(1) << 31;
 // Workgroups per launch; larger plans stride.  Measured on the 128K handoff (48 layers, 201K tiles): 65536
 // workgroups 5.83 TB/s, one per tile 5.67, 16384 5.62, 4096 5.29, 2048 4.52.
 constexpr uint64_t kMaxGrid = 65536;
+// Plans with quantizing rows: their tiles read 16 KiB but write a quarter of that after per-row work, and more
+// workgroups in flight measured faster (the 128K int8 carve: 65536 workgroups 1.56 ms, 131072 1.50, 262144 1.43,
+// one per tile 1.46; q4_0: 1.53, 1.51, 1.52, 1.53).
+constexpr uint64_t kMaxGridQuant = 262144;
 
 // Assigns tile ranges, uploads the table and fills the plan.  The only HIP calls a plan builder makes.
 int finish_plan(std::vector<sc::MoveRow>& rows, const Geo& g, uint64_t payload, sc_plan** out) {
@@ -196,7 +200,7 @@ int finish_plan(std::vector<sc::MoveRow>& rows, const Geo& g, uint64_t payload, 
     p->geo = move_geo(g);
     p->n_tiles = tiles;
     p->payload = payload;
-    p->grid = int64_t(std::min<uint64_t>(tiles, kMaxGrid));
+    p->grid = int64_t(std::min<uint64_t>(tiles, quant ? kMaxGridQuant : kMaxGrid));
     p->mix = sc::mix_of(kv32, quant);
     if (rows.empty() || tiles == 0) {   // an empty handoff (0 tokens, no running state) is a valid no-op
         *out = p;

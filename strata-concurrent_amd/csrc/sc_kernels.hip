@@ -832,7 +832,8 @@ hipError_t launch_append(const AppendRows& rows, int n_rows, uint64_t tiles_per_
     if (n_rows <= 0 || tiles_per_row == 0) return hipSuccess;
     if (n_rows > kAppendMaxRows || (kind != kKv32 && kind != kKvQ8 && kind != kKvQ4)) return hipErrorInvalidValue;
     const uint64_t n_tiles = uint64_t(n_rows) * tiles_per_row;
-    const dim3 blocks(unsigned(n_tiles < 65536 ? n_tiles : 65536)), threads(kThreads);
+    const uint64_t cap = kind == kKv32 ? 65536 : 262144;   // quantizing tiles gain from more workgroups in flight
+    const dim3 blocks(unsigned(n_tiles < cap ? n_tiles : cap)), threads(kThreads);
     switch (kind) {
         case kKv32:
             hipLaunchKernelGGL(sc_append_kernel<kKv32>, blocks, threads, 0, stream, rows, n_rows, tiles_per_row, geo);
