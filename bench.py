@@ -956,7 +956,10 @@ def main() -> int:
     log("quantizing carve: int8 / q4_0 / K8V4 pools from f32 rows, 128K")
     result["quant_carve"] = quant_carve(sc, geo, T, stream)
     qc = result["quant_carve"]
-    log("quant carve: " + ", ".join(f"{k} {v['ms']} ms ({v['hbm_gbps']} GB/s)" for k, v in qc.items() if k != "tokens"))
+    log("quant carve: " + ", ".join(f"{k} {v['ms']} ms ({v['hbm_gbps']} GB/s)" for k, v in qc.items()
+                                    if isinstance(v, dict) and "ms" in v))
+    log("kv_append per layer: " + ", ".join(f"{k} {v['ms_all_layers']} ms for {v['launches']} launches "
+                                            f"({v['hbm_gbps']} GB/s)" for k, v in qc["kv_append_per_layer"].items()))
 
     log("config 4: three slots, two parks and one resume overlapped with decode")
     settle_c4 = settle_link(sc, d2h)
