@@ -182,6 +182,10 @@ def config4(sc, geo, seed: int, link_gbps: float, streams=None) -> dict:
     restored = sc.new_slot(geo, park_a, fill=0)
     sink = sc.DeviceBuffer(4096, "uint32")
     sc.device_sync()
+    # the warm-up left correct bytes in the images: poison them, so a resume that read an image before the timed
+    # park had landed would restore the poison and fail the round-trip check below
+    for im in images.values():
+        im.numpy()[:] = 0xEE
     decode, park, resume = streams if streams is not None else (sc.Stream(), sc.Stream(), sc.Stream())
     pools = slots[decode_len].k_pool + slots[decode_len].v_pool
 

@@ -485,6 +485,9 @@ int sc_fill_normal_f32(float* dst, uint64_t n, uint64_t seed, uint64_t stream_id
  * at `kv` and folds them into one u32 per workgroup in `sink` (so the reads cannot be elided).  It stands in
  * for the attention reading the slot that keeps decoding while others park or resume. */
 int sc_decode_probe(const void* kv, uint64_t n_bytes, uint32_t* sink, int64_t workgroups, void* stream);
+/* Long work that always ends: one wave holds `stream` for `microseconds` (at most 2 s) of the device's constant-rate
+ * wall clock.  Queued ahead of a transfer, it shows that event-gated work on another stream waits for that transfer. */
+int sc_delay_async(uint32_t microseconds, void* stream);
 
 #ifdef __cplusplus
 }

@@ -17,6 +17,8 @@
  *   sco_park / sco_resume   A/B/A round trips and byte accounting
  *   sco_fnv1a64             textbook FNV-1a 64 vectors with the standard basis; the reference's seed on empty input
  *   sco_fill_*              the device generators of libsc_handoff.so, bit for bit (GPU tests), and moments
+ *   sco_synth_*_hash        sco_fnv1a64 over the outputs of sco_fill_* -> sco_kv_append / sco_rec_carve /
+ *                           sco_conv_hist -> sco_park on small sequences (one and two sources per blob)
  *   sco_f32_of_f16          numpy float16 -> float32 on all 65536 bit patterns
  *   sco_q8_row / sco_q4_row numpy vectorised restatements of the same rules (independent of these loops) on random and
  *                           edge groups (zero, tied magnitudes, exact .5 quotients, clamping, tiny and huge scales),
@@ -360,6 +362,93 @@ uint64_t sco_fnv1a64(const uint8_t* p, uint64_t n, uint64_t seed) {
     for (uint64_t i = 0; i < n; ++i) {
         h ^= p[i];
         h *= 1099511628211ull;
+    }
+    return h;
+}
+
+/* ---- whole-blob hashes of synthetic sequences -------------------------------------------------------------------
+ * The FNV-1a of one blob of the image a synthetic sequence carves to, generated value by value from the counter-based
+ * generators (sco_fill_*) and folded into the hash as it goes, so the full-size configs (up to 3.3 GB of payload) are
+ * compared with the device byte for byte without materialising the expected bytes.  The layouts are the ones
+ * sco_kv_append, sco_rec_carve, sco_conv_hist and sco_image_layout restate: a K/V blob is the identity pool's first
+ * `cells` cells ([page][H][ps][D] f16, conversation_snapshot.cpp:40-49), the GDN blob is every GDN row
+ * ((S, HV, S) recurrence then the [C][d_conv-1] history, conversation_state.cpp:186-189).  Pinned by the tests against
+ * sco_fnv1a64 over those functions' outputs (fill -> carve -> park) on small sequences, single and two-source. */
+
+/* One source of a K/V blob: cells [t0, t0 + n) hold tokens 0 .. n-1 of a synthetic sequence whose K (or V) rows are
+ * element (t * H + h) * D + d of stream `sid` under `seed`, U[lo, hi] rounded to f16 (sco_fill_uniform_f16; an f32
+ * source rounded by the carve gives the same bits, sco_fill_uniform_f32 then sco_f16_bits). */
+typedef struct sco_kv_source {
+    uint64_t seed, sid;
+    int64_t t0, n;
+    float lo, hi;
+} sco_kv_source;
+
+static uint64_t fnv_byte(uint64_t h, uint8_t b) { return (h ^ b) * 1099511628211ull; }
+
+uint64_t sco_synth_kv_blob_hash(int64_t H, int64_t D, int64_t ps, int64_t cells, const sco_kv_source* src,
+                                int32_t n_src, uint8_t tail, uint64_t fnv_seed) {
+    uint64_t h = fnv_seed;
+    uint64_t keys[8];
+    for (int32_t s = 0; s < n_src && s < 8; ++s) keys[s] = sco_synth_key(src[s].seed, src[s].sid);
+    for (int64_t page = 0; page * ps < cells; ++page)
+        for (int64_t kh = 0; kh < H; ++kh)
+            for (int64_t c = 0; c < ps; ++c) {
+                const int64_t cell = page * ps + c;
+                int32_t s = 0;
+                while (s < n_src && !(cell >= src[s].t0 && cell < src[s].t0 + src[s].n)) ++s;
+                if (s == n_src || s >= 8) {
+                    for (int64_t d = 0; d < D; ++d) h = fnv_byte(fnv_byte(h, tail), tail);
+                    continue;
+                }
+                const uint64_t base = (uint64_t) (((cell - src[s].t0) * H + kh) * D);
+                const float span = src[s].hi - src[s].lo;
+                for (int64_t d = 0; d < D; ++d) {
+                    const float u = (float) (uint32_t) (draw(keys[s], base + (uint64_t) d) >> 40) * 0x1p-24f;
+                    const float x = fmaf(span, u, src[s].lo);
+                    uint32_t b;
+                    memcpy(&b, &x, 4);
+                    const uint16_t v = sco_f16_bits(b);
+                    h = fnv_byte(fnv_byte(h, (uint8_t) v), (uint8_t) (v >> 8));
+                }
+            }
+    return h;
+}
+
+static float normal_at(uint64_t key, uint64_t i) {
+    int64_t sum = 0;
+    for (int k = 0; k < 6; ++k) {
+        const uint64_t x = draw(key, i * 6 + (uint64_t) k);
+        sum += (int64_t) (x >> 40) + (int64_t) ((x >> 16) & 0xFFFFFFull);
+    }
+    return (float) (int32_t) (sum - ((int64_t) 6 << 24)) * 0x1p-24f;
+}
+
+static uint64_t fnv_f32(uint64_t h, float x) {
+    uint32_t b;
+    memcpy(&b, &x, 4);
+    for (int k = 0; k < 4; ++k) h = fnv_byte(h, (uint8_t) (b >> (8 * k)));
+    return h;
+}
+
+/* The GDN blob of a sequence carved fresh (pos0 = 0): GDN layer i's recurrence is stream sid_rec0 + i, head-major
+ * [HV][S][S] N(0,1) (sco_fill_normal_f32), carved to (S, HV, S); its history is the last d_conv-1 of `conv_rows`
+ * rows of stream sid_conv0 + i ([rows][C], row stride C), rows before the first reading as zero. */
+uint64_t sco_synth_gdn_hash(const sco_geometry* g, uint64_t seed, uint64_t sid_rec0, uint64_t sid_conv0,
+                            int64_t conv_rows, uint64_t fnv_seed) {
+    const int64_t S = g->ssm_state_size, HV = g->ssm_v_heads, Cc = g->ssm_conv_channels, nh = g->ssm_d_conv - 1;
+    uint64_t h = fnv_seed;
+    for (int64_t i = 0; i < n_gdn(g); ++i) {
+        const uint64_t kr = sco_synth_key(seed, sid_rec0 + (uint64_t) i);
+        const uint64_t kc = sco_synth_key(seed, sid_conv0 + (uint64_t) i);
+        for (int64_t a = 0; a < S; ++a)
+            for (int64_t hv = 0; hv < HV; ++hv)
+                for (int64_t b = 0; b < S; ++b) h = fnv_f32(h, normal_at(kr, (uint64_t) ((hv * S + a) * S + b)));
+        for (int64_t c = 0; c < Cc; ++c)
+            for (int64_t k = 0; k < nh; ++k) {
+                const int64_t t = conv_rows - nh + k;
+                h = fnv_f32(h, t >= 0 ? normal_at(kc, (uint64_t) (t * Cc + c)) : 0.0f);
+            }
     }
     return h;
 }

@@ -58,6 +58,8 @@ for _name, _res, _args in (
                                  C.POINTER(_P), _I64, _I64, C.POINTER(_P), C.POINTER(_P), C.POINTER(_P), _I64, _P]),
     ("sco_cpu_handoff", _U64, [_P, _P, _U64, _P]),
     ("sco_memcpy_threads", C.c_int, [_P, _P, _U64, C.c_int]),
+    ("sco_synth_kv_blob_hash", _U64, [_I64, _I64, _I64, _I64, _P, C.c_int32, C.c_uint8, _U64]),
+    ("sco_synth_gdn_hash", _U64, [_G, _U64, _U64, _U64, _I64, _U64]),
 ):
     _fn = getattr(lib, _name)
     _fn.restype = _res
@@ -195,6 +197,63 @@ def fnv1a64(data: bytes | np.ndarray, seed: int = REFERENCE_FNV_SEED) -> int:
     a = np.frombuffer(bytes(data), dtype=np.uint8) if not isinstance(data, np.ndarray) else \
         np.ascontiguousarray(data).view(np.uint8).reshape(-1)
     return int(lib.sco_fnv1a64(_ptr(a) if a.size else None, a.size, seed))
+
+
+# ---- whole-blob hashes of synthetic sequences ------------------------------------------------------------------------
+
+class KvSource(C.Structure):
+    """Cells [t0, t0 + n) of a K/V blob hold tokens 0..n-1 of stream `sid` under `seed` (U[lo, hi] -> f16)."""
+    _fields_ = [("seed", _U64), ("sid", _U64), ("t0", _I64), ("n", _I64), ("lo", C.c_float), ("hi", C.c_float)]
+
+
+# Stream ids of the synthetic sequences the product binding generates (sc_handoff.synthetic_prefill): K of QSA layer j
+# is stream 1000 + 2j, V 1001 + 2j, the recurrence of GDN layer i 5000 + i and its conv rows 9000 + i.
+SID_K0, SID_V0, SID_REC0, SID_CONV0 = 1000, 1001, 5000, 9000
+
+
+def kv_blob_hash(geo, cells: int, sources, tail: int = 0, seed: int = REFERENCE_FNV_SEED) -> int:
+    """FNV-1a of an identity-layout K or V blob of `cells` cells; `sources` are (seed, sid, t0, n) tuples (U[-4, 4]),
+    cells no source covers hold `tail` bytes (sco_synth_kv_blob_hash)."""
+    arr = (KvSource * max(len(sources), 1))(*[KvSource(s, sid, t0, n, -4.0, 4.0) for s, sid, t0, n in sources])
+    return int(lib.sco_synth_kv_blob_hash(geo.n_head_kv, geo.head_dim, geo.page_size, cells, C.addressof(arr),
+                                          len(sources), tail, seed))
+
+
+def gdn_blob_hash(geo, seed: int, conv_rows: int, fnv_seed: int = REFERENCE_FNV_SEED) -> int:
+    """FNV-1a of the GDN blob of a sequence carved fresh (sco_synth_gdn_hash)."""
+    g = geometry_from(geo)
+    return int(lib.sco_synth_gdn_hash(C.byref(g), seed, SID_REC0, SID_CONV0, conv_rows, fnv_seed))
+
+
+def synthetic_image_hashes(geo, tokens: int, seed: int, conv_rows: int | None = None, tail: int = 0,
+                           chunk: tuple[int, int] | None = None, threads: int = 16) -> list[int]:
+    """The FNV-1a of every blob of the image (sco_image_layout order: K, V per QSA layer, then the GDN rows) of a
+    synthetic sequence of `tokens` tokens under `seed`, carved fresh into a slot whose untouched bytes are `tail`.
+    `chunk` = (chunk_seed, chunk_tokens) appends a K/V-only chunk at cell `tokens` (the batched resume + append), so
+    the blobs cover tokens + chunk_tokens tokens.  Blobs are hashed on `threads` threads."""
+    from concurrent.futures import ThreadPoolExecutor
+    g = geometry_from(geo)
+    n_qsa = g.n_layers // g.qsa_interval
+    n_gdn = g.n_layers - n_qsa
+    total = tokens + (chunk[1] if chunk else 0)
+    cells = int(lib.sco_cells(C.byref(g), total))
+    conv_rows = min(tokens, g.ssm_d_conv - 1) if conv_rows is None else conv_rows
+    jobs = []
+    for j in range(n_qsa):
+        for sid in (SID_K0 + 2 * j, SID_V0 + 2 * j):
+            src = [(seed, sid, 0, tokens)]
+            if chunk:
+                src.append((chunk[0], sid, tokens, chunk[1]))
+            jobs.append(("kv", src))
+    if n_gdn:
+        jobs.append(("gdn", None))
+
+    def run(job):
+        kind, src = job
+        return kv_blob_hash(g, cells, src, tail) if kind == "kv" else gdn_blob_hash(g, seed, conv_rows)
+
+    with ThreadPoolExecutor(max_workers=threads) as pool:
+        return list(pool.map(run, jobs))
 
 
 # ---- whole handoff -------------------------------------------------------------------------------------------------

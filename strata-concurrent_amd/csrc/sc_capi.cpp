@@ -34,6 +34,7 @@ hipError_t launch_copy_bytes(void* dst, const void* src, uint64_t n, hipStream_t
 hipError_t launch_decode_probe(const void* kv, uint64_t n_bytes, uint32_t* sink, int64_t workgroups,
                                hipStream_t stream);
 hipError_t launch_batch(const BatchArgs& args, int64_t grid, hipStream_t stream);
+hipError_t launch_delay(uint64_t ticks, uint32_t max_iters, hipStream_t stream);
 hipError_t launch_stream_reset(int32_t* table, int64_t n_blocks, int32_t* slot_block, int32_t* slot_stamp,
                                int32_t* slot_ref, int64_t n_slots, int32_t* ctl, hipStream_t stream);
 hipError_t launch_ring_table(int32_t* table, int64_t n_blocks, int64_t n_slots, hipStream_t stream);
@@ -1620,6 +1621,18 @@ int sc_decode_probe(const void* kv, uint64_t n_bytes, uint32_t* sink, int64_t wo
     if (!kv || !sink || workgroups <= 0 || workgroups > (int64_t(1) << 20) || (n_bytes % 16))
         return fail(SC_EINVAL, "sc_handoff: invalid decode probe request");
     SC_HIP(sc::launch_decode_probe(kv, n_bytes, sink, workgroups, static_cast<hipStream_t>(stream)), "decode probe");
+    return ok();
+}
+
+int sc_delay_async(uint32_t microseconds, void* stream) {
+    if (microseconds > 2000000u) return fail(SC_EINVAL, "sc_handoff: a delay is at most 2 s");
+    int dev = 0, khz = 0;
+    SC_HIP(hipGetDevice(&dev), "hipGetDevice");
+    SC_HIP(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev), "wall clock rate");
+    if (khz <= 0) return fail(SC_EHIP, "sc_handoff: the device reports no wall clock rate");
+    const uint64_t ticks = uint64_t(microseconds) * uint64_t(khz) / 1000u;
+    // one sleep of 100 * 64 clocks lasts well over a microsecond, so `microseconds` sleeps outlast the request
+    SC_HIP(sc::launch_delay(ticks, microseconds + 16u, static_cast<hipStream_t>(stream)), "delay");
     return ok();
 }
 

@@ -726,6 +726,17 @@ __global__ void __launch_bounds__(kThreads) decode_probe_kernel(const uint8_t* k
     if (threadIdx.x == 0) sink[blockIdx.x] = s[0] ^ s[1] ^ s[2] ^ s[3];
 }
 
+// Holds its stream for `ticks` ticks of the constant-rate wall clock, then exits: a stand-in for long work queued
+// ahead of a transfer, so tests can show that an event-gated transfer does not start early.  Every exit path is
+// bounded: the loop ends after `max_iters` sleeps even if the clock were not to advance.
+__global__ void delay_kernel(uint64_t ticks, uint32_t max_iters) {
+    const uint64_t t0 = wall_clock64();
+    for (uint32_t i = 0; i < max_iters; ++i) {
+        if (wall_clock64() - t0 >= ticks) break;
+        __builtin_amdgcn_s_sleep(100);
+    }
+}
+
 // Every block of a streamed layer evicted (the reference's reset, src/kernels/cuda/kv_stream.cu:173-182).
 __global__ void stream_reset_kernel(int32_t* table, int64_t n_blocks, int32_t* slot_block, int32_t* slot_stamp,
                                     int32_t* slot_ref, int64_t n_slots, int32_t* ctl) {
@@ -901,6 +912,11 @@ hipError_t launch_copy_bytes(void* dst, const void* src, uint64_t n, hipStream_t
     const uint64_t tiles = (n - pre) / kCopyTile;
     if (tiles + 1 > 0x7FFFFFFFull) return hipErrorInvalidValue;   // 32 TiB: beyond any allocation here
     hipLaunchKernelGGL(copy_tiles_kernel, dim3(unsigned(tiles + 1)), dim3(256), 0, stream, d, s, n, pre, tiles);
+    return hipGetLastError();
+}
+
+hipError_t launch_delay(uint64_t ticks, uint32_t max_iters, hipStream_t stream) {
+    hipLaunchKernelGGL(delay_kernel, dim3(1), dim3(64), 0, stream, ticks, max_iters);
     return hipGetLastError();
 }
 

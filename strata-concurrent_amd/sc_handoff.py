@@ -175,6 +175,7 @@ _SIGS = {
     "sc_fill_uniform_f32": (C.c_int, [_P, _U64, C.c_float, C.c_float, _U64, _U64, _P]),
     "sc_fill_normal_f32": (C.c_int, [_P, _U64, _U64, _U64, _P]),
     "sc_decode_probe": (C.c_int, [_P, _U64, _P, _I64, _P]),
+    "sc_delay_async": (C.c_int, [C.c_uint32, _P]),
     "sc_plan_carve_quant": (C.c_int, [_GEO, C.POINTER(PrefillView), C.POINTER(QuantSlot), C.POINTER(_P)]),
     "sc_plan_capture_map": (C.c_int, [_GEO, C.POINTER(DecodeSlot), _I64, _P, _U64, C.POINTER(BlobMap), C.POINTER(_P)]),
     "sc_plan_scatter_map": (C.c_int, [_GEO, _P, _U64, C.POINTER(BlobMap), _I64, C.POINTER(DecodeSlot), C.POINTER(_P)]),
@@ -626,6 +627,11 @@ class Stream:
             lib.sc_stream_destroy(self.handle)
         except Exception:
             pass
+
+
+def delay_async(microseconds: int, stream=None) -> None:
+    """Hold `stream` for `microseconds` with one sleeping wave (sc_delay_async): long work that always ends."""
+    check(lib.sc_delay_async(microseconds, _stream(stream)), "sc_delay_async")
 
 
 def probe_link(nbytes: int = 256 << 20, iters: int = 4) -> tuple[float, float]:

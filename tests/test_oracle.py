@@ -268,3 +268,68 @@ def test_memcpy_threads_copies_every_byte(oracle):
         out = np.zeros_like(data)
         oracle.memcpy_threads(data, out, threads)
         assert np.array_equal(out, data), threads
+
+
+# ---- whole-blob hashes of synthetic sequences (the full-size parity checker) -----------------------------------------
+
+def _synthetic_inputs(oracle, g, tokens, seed, conv_rows, dtype=0):
+    """What the product's synthetic_prefill generates, from the oracle's generators (host arrays)."""
+    H, D, S, HV, Cc = g.n_head_kv, g.head_dim, g.ssm_state_size, g.ssm_v_heads, g.ssm_conv_channels
+    n_qsa = g.n_layers // g.qsa_interval
+    n_gdn = g.n_layers - n_qsa
+    fill = oracle.fill_uniform_f16 if dtype == 0 else oracle.fill_uniform_f32
+    k = [fill(tokens * H * D, -4.0, 4.0, seed, oracle.SID_K0 + 2 * j).reshape(tokens, H, D) for j in range(n_qsa)]
+    v = [fill(tokens * H * D, -4.0, 4.0, seed, oracle.SID_V0 + 2 * j).reshape(tokens, H, D) for j in range(n_qsa)]
+    rec = [oracle.fill_normal_f32(HV * S * S, seed, oracle.SID_REC0 + i).reshape(HV, S, S) for i in range(n_gdn)]
+    conv = [oracle.fill_normal_f32(max(conv_rows, 1) * Cc, seed, oracle.SID_CONV0 + i).reshape(-1, Cc)
+            for i in range(n_gdn)]
+    return {"k": k, "v": v, "rec": rec, "conv": conv, "tokens": tokens, "conv_rows": conv_rows}
+
+
+def _blob_hashes(oracle, geo, tokens, image):
+    blobs, _ = oracle.image_layout(geo, tokens)
+    return [oracle.fnv1a64(image[off:off + n]) for _, _, off, n in blobs]
+
+
+SMALL_GEO = dict(n_layers=8, qsa_interval=4, n_head_kv=2, head_dim=64, page_size=4, ssm_state_size=16,
+                 ssm_k_heads=2, ssm_v_heads=4, ssm_d_conv=4, ssm_conv_channels=96, idx_key_dim=32)
+
+
+@pytest.mark.parametrize("tokens,conv_rows,dtype,tail", [(37, 3, 0, 0), (40, 3, 1, 0), (2, 2, 0, 0x5A),
+                                                         (13, 0, 0, 0x11)])
+def test_synthetic_image_hashes_equal_fill_carve_park(oracle, tokens, conv_rows, dtype, tail):
+    """sco_synth_*_hash == FNV-1a of each blob of sco_park(sco_handoff_carve(sco_fill_*)): the streaming checker of
+    the full-size configs computes exactly the bytes the pinned oracle chain produces (f16 and f32 sources, a page
+    tail of untouched bytes, short conv histories)."""
+    g = oracle.Geometry(*SMALL_GEO.values())
+    inputs = _synthetic_inputs(oracle, g, tokens, seed=77, conv_rows=conv_rows, dtype=dtype)
+    n_pages = (tokens + g.page_size - 1) // g.page_size
+    initial = oracle.new_state(g, n_pages)
+    for key in initial:
+        initial[key].view(np.uint8)[:] = tail
+    state = oracle.expected_slot(g, inputs, slot_cells=n_pages * g.page_size, initial=initial)
+    want = _blob_hashes(oracle, g, tokens, oracle.park(g, tokens, state))
+    got = oracle.synthetic_image_hashes(g, tokens, 77, conv_rows=conv_rows, tail=tail, threads=3)
+    assert got == want
+
+
+def test_synthetic_image_hashes_with_appended_chunk(oracle):
+    """Two sources per K/V blob (a parked prefix of L tokens, then a chunk appended at cell L mid-page): the form the
+    batched resume + append is checked with."""
+    g = oracle.Geometry(*SMALL_GEO.values())
+    L, chunk = 21, 10
+    first = _synthetic_inputs(oracle, g, L, seed=5, conv_rows=3)
+    second = _synthetic_inputs(oracle, g, chunk, seed=905, conv_rows=0)
+    n_pages = (L + chunk + g.page_size - 1) // g.page_size
+    state = oracle.expected_slot(g, first, slot_cells=n_pages * g.page_size)
+    oracle.carve_into(g, second, state, n_pages, pos0=L, with_gdn=False)
+    want = _blob_hashes(oracle, g, L + chunk, oracle.park(g, L + chunk, state))
+    got = oracle.synthetic_image_hashes(g, L, 5, chunk=(905, chunk), threads=2)
+    assert got == want
+    # a plausible mistake fails: the chunk placed one cell early, or the recurrence left head-major
+    assert oracle.synthetic_image_hashes(g, L - 1, 5, chunk=(905, chunk), threads=2)[0] != want[0]
+    bad = dict(state)
+    rec_len = g.ssm_state_size * g.ssm_v_heads * g.ssm_state_size
+    bad["gdn"] = state["gdn"].copy()
+    bad["gdn"][0, :rec_len] = first["rec"][0].reshape(-1)
+    assert _blob_hashes(oracle, g, L + chunk, oracle.park(g, L + chunk, bad))[-1] != want[-1]
