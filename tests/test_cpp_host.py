@@ -28,15 +28,6 @@ def test_validation_refuses_before_any_write():
     assert "checks passed" in out
 
 
-@pytest.mark.gpu
-def test_snapshot_aba_on_device(cuda):
-    """Device pools in f16/int8/q4/K8V4 x resident/streamed/ring: A/B/A exactness, refusals, incremental capture,
-    checkpoint spare-row rebuild, layer split."""
-    out = _run("conversation_snapshot_test", 240)
-    assert "checks passed" in out
-    print(out.strip().splitlines()[-1])
-
-
 @pytest.mark.skipif(not (REF / "ref_validation_test_on_ours").exists(),
                     reason="the reference test builds (oracle/_ref) are not here")
 def test_reference_validation_test_against_this_library():
