@@ -393,6 +393,14 @@ int sc_fnv1a64_chain_async(const void* data, uint64_t bytes, uint64_t* state, vo
                            void* stream);
 /* Synchronous convenience: allocates its workspace, runs on the null stream, waits, and returns the hash in *hash. */
 int sc_fnv1a64_device(const void* data, uint64_t bytes, uint64_t seed, uint64_t* hash);
+/* sc_fnv1a64_async without a workspace argument and without any allocation.  No counterpart in the reference: it is
+ * for callers that cannot allocate (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  The workspace is a static device array the library holds on each GPU until the process ends, sized for
+ * inputs of at most SC_FNV_NOALLOC_MAX_BYTES (larger inputs are refused with SC_ERANGE before anything is enqueued).
+ * It keeps the last call's contents and needs no clearing.  Calls ordered on one stream are safe; calls that overlap
+ * on one GPU (on different streams) race on the shared array and must not be issued. */
+#define SC_FNV_NOALLOC_MAX_BYTES (4ull << 30)
+int sc_fnv1a64_noalloc_async(const void* data, uint64_t bytes, uint64_t seed, uint64_t* out, void* stream);
 
 /* ---- runtime plumbing the C++ host layer calls instead of HIP ---------------------------------------------------- */
 

@@ -77,6 +77,12 @@ int fail(int code, const std::string& message) {
     return code;
 }
 int snapshot_fail(const char* message) { return fail(SC_EINVAL, std::string("conversation snapshot: ") + message); }
+}  // namespace
+
+int sc::record_ok() { return ok(); }
+int sc::record_error(int code, const std::string& message) { return fail(code, message); }
+
+namespace {
 int hip_fail(hipError_t e, const char* what) {
     return fail(SC_EHIP, std::string("sc_handoff ") + what + ": " + hipGetErrorString(e));
 }

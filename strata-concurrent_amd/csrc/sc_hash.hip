@@ -31,7 +31,9 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <mutex>
 
+#include "sc_handoff.h"
 #include "sc_internal.hpp"
 
 namespace sc {
@@ -572,3 +574,53 @@ hipError_t launch_fnv1a64(const void* data, uint64_t n, uint64_t seed, const uin
 }
 
 }  // namespace sc
+
+// ---- the hash that allocates nothing ----------------------------------------------------------------------------------
+// For callers that cannot allocate (code under HIP graph capture, tight serving loops): the workspace is `scratch`, one
+// array per GPU that the library holds until the process ends, sized for inputs of up to SC_FNV_NOALLOC_MAX_BYTES
+// (fnv_workspace(4 GiB) is 44.7 MiB).  Its kernels write every workspace word they later read, so nothing in it is
+// cleared between calls; a call after another on the same stream is ordered after it, and calls that overlap on one
+// GPU (on different streams) race on the one array.
+namespace {
+
+constexpr uint64_t kScratchBytes = 48ull << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};   // the device address of `scratch` on each GPU, looked up once per GPU
+
+// The current device's copy of `scratch`.  In host code the array's name is only a stand-in for the device symbol, so
+// kernels get the address the runtime reports for it, looked up with the device current.
+hipError_t scratch_of_current_device(void** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        if (!p) return hipErrorInvalidSymbol;
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return hipSuccess;
+}
+
+}  // namespace
+
+extern "C" int sc_fnv1a64_noalloc_async(const void* data, uint64_t bytes, uint64_t seed, uint64_t* out, void* stream) {
+    if (!out || (bytes && !data)) return sc::record_error(SC_EINVAL, "sc_handoff: missing hash input or output");
+    if (bytes > SC_FNV_NOALLOC_MAX_BYTES || sc::fnv_workspace(bytes).bytes > kScratchBytes)
+        return sc::record_error(SC_ERANGE, "sc_handoff: the hash without allocation takes at most 4 GiB "
+                                           "(SC_FNV_NOALLOC_MAX_BYTES); use sc_fnv1a64_async with a workspace");
+    void* ws = nullptr;
+    hipError_t e = scratch_of_current_device(&ws);
+    if (e != hipSuccess)
+        return sc::record_error(SC_EHIP, std::string("sc_handoff hash scratch: ") + hipGetErrorString(e));
+    e = sc::launch_fnv1a64(data, bytes, seed, nullptr, out, ws, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return sc::record_error(SC_EHIP, std::string("sc_handoff hash launch: ") + hipGetErrorString(e));
+    return sc::record_ok();
+}

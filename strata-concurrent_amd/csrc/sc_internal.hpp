@@ -8,8 +8,13 @@
 #pragma once
 
 #include <cstdint>
+#include <string>
 
 namespace sc {
+
+// The C-ABI's per-thread error record (sc_last_error), for entry points defined outside sc_capi.cpp.
+int record_ok();
+int record_error(int code, const std::string& message);
 
 constexpr int kThreads = 256;            // one workgroup = 4 wave64
 constexpr int kChunksPerThread = 4;      // 16-byte chunks in flight per thread per tile

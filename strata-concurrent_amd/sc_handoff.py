@@ -191,6 +191,7 @@ _SIGS = {
     "sc_fnv1a64_async": (C.c_int, [_P, _U64, _U64, _P, _P, _U64, _P]),
     "sc_fnv1a64_chain_async": (C.c_int, [_P, _U64, _P, _P, _U64, _P]),
     "sc_fnv1a64_device": (C.c_int, [_P, _U64, _U64, C.POINTER(_U64)]),
+    "sc_fnv1a64_noalloc_async": (C.c_int, [_P, _U64, _U64, _P, _P]),
     "sc_copy_device_async": (C.c_int, [_P, _P, _U64, _P]),
     "sc_ipc_export_create": (C.c_int, [_U64, _U64, C.POINTER(_P)]),
     "sc_ipc_export_count": (C.c_int32, [_P]),

@@ -109,6 +109,15 @@ def test_image_refusals(sc):
     assert "identity-layout" in sc.last_error()
 
 
+def test_noalloc_hash_refusals_before_any_hip_call(sc):
+    """The hash without allocation refuses inputs past its static workspace, and missing pointers, on the host."""
+    out = 1 << 40   # never dereferenced: the refusals come first
+    assert sc.lib.sc_fnv1a64_noalloc_async(1 << 40, (4 << 30) + 1, 0, out, None) == sc.SC_ERANGE
+    assert "at most 4 GiB" in sc.last_error()
+    assert sc.lib.sc_fnv1a64_noalloc_async(None, 16, 0, out, None) == sc.SC_EINVAL
+    assert sc.lib.sc_fnv1a64_noalloc_async(1 << 40, 16, 0, None, None) == sc.SC_EINVAL
+
+
 def test_core_library_exports_the_wire_abi():
     """libsc_core.so exports every entry point include/sc_wire.h declares (the device payload path)."""
     import sc_wire
