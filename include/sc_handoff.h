@@ -284,7 +284,7 @@ int sc_resume_layers_async(const sc_geometry* g, const void* host_image, uint64_
 int sc_plan_launch(const sc_plan* plan, void* stream);
 /* Algorithmic payload bytes the plan moves (each read once and written once). */
 uint64_t sc_plan_payload_bytes(const sc_plan* plan);
-/* Workgroups the launch uses (0 = the library's default); for launch-shape sweeps. */
+/* Workgroups the launch uses, for launch-shape sweeps; 0 restores the grid the plan was built with. */
 int sc_plan_set_grid(sc_plan* plan, int64_t workgroups);
 /* Frees the device table.  The caller must not destroy a plan whose launch has not completed. */
 int sc_plan_destroy(sc_plan* plan);

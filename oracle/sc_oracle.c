@@ -175,18 +175,24 @@ float sco_f32_of_f16(uint16_t h) {
 
 /* int8 K/V: the reference's int8 kv_append (src/prefill/kernels.cu:578-600) and kv_append_q8
  * (src/kernels/cuda/kv_q8.cu:29-64), whose host restatement is src/kernels/kv_q8_parity.cpp:78-92.  Per group of 64
- * values: amax = max |x|; the stored scale is f16(amax / 127) rounded to nearest even; each code is
- * rint(x / f32(scale)) (ties to even) clamped to [-127, 127], or 0 when the scale is 0.  A NaN value gets code 0
- * (the reference leaves NaN undefined).  `codes` gets D bytes, `scales` D/64 f16 words. */
+ * values: amax = max |x| over the values that are not NaN (the device writers' fmaxf reduction passes a NaN over);
+ * the stored scale is f16(amax / 127) rounded to nearest even; each code is rint(x / f32(scale)) (ties to even)
+ * clamped to [-127, 127], or 0 when the scale is 0.  A NaN value gets code 0 (the reference leaves NaN undefined).  A
+ * group of NaNs only reduces to NaN there, so its scale is f16 NaN, 0x7E00 under the reference's converter
+ * (f16_bits.hpp:37-70, |NaN| being positive), and every code 0.  `codes` gets D bytes, `scales` D/64 f16 words. */
 void sco_q8_row(const float* x, int64_t D, int8_t* codes, uint16_t* scales) {
     for (int64_t g = 0; g < D / 64; ++g) {
         const float* v = x + g * 64;
-        float amax = 0.0f;                              /* from 0, as kv_q8_parity.cpp:83-84: NaNs never count */
-        for (int t = 0; t < 64; ++t) amax = fmaxf(amax, fabsf(v[t]));
+        float amax = 0.0f;                              /* NaNs never count toward the maximum */
+        int real = 0;
+        for (int t = 0; t < 64; ++t) {
+            amax = fmaxf(amax, fabsf(v[t]));
+            real |= v[t] == v[t];
+        }
         const float ratio = amax / 127.0f;
         uint32_t rb;
         memcpy(&rb, &ratio, 4);
-        const uint16_t sb = sco_f16_bits(rb);
+        const uint16_t sb = real ? sco_f16_bits(rb) : (uint16_t) 0x7E00u;
         const float sf = sco_f32_of_f16(sb);
         scales[g] = sb;
         for (int t = 0; t < 64; ++t) {
@@ -202,8 +208,9 @@ void sco_q8_row(const float* x, int64_t D, int8_t* codes, uint16_t* scales) {
 
 /* q4_0 K/V: kv_append_q4 (src/kernels/cuda/kv_q4.cu:72-89 q4_group, :111-129), host restatement
  * src/kernels/kv_q4_parity.cpp:64-87.  Per block of 32 values: the value of largest |x| (ties go to the larger value,
- * the device kernel's rule); d = that value / -8; id = 1/d (0 when d is 0); each code is trunc(x*id + 8.5) with the
- * product and the sum rounded separately (the host quantizer's form), clamped to [0, 15]; byte j of the block is
+ * the device kernel's rule); d = that value / -8; id = 1/d (0 when d is 0); each code is trunc(x*id + 8.5) with one
+ * rounding, a fused multiply-add (the device writer's form: kv_q4.cu:84 is contracted to an FMA by nvcc's default
+ * --fmad=true and by clang's HIP default; the host checker rounds the product first), clamped to [0, 15]; byte j is
  * code j | code j+16 << 4; the block is {f16(d) RNE, 16 bytes} = 18 bytes.  Among values equal in magnitude and in
  * value (only +0 and -0 can be), the first in index order is the maximum, so the sign of a zero d is defined.
  * `blocks` gets D/32 * 18 bytes. */
@@ -221,8 +228,7 @@ void sco_q4_row(const float* x, int64_t D, uint8_t* blocks) {
         const float id = d != 0.0f ? 1.0f / d : 0.0f;
         uint8_t q[32];
         for (int t = 0; t < 32; ++t) {
-            volatile float prod = v[t] * id;            /* rounded on its own, as the host quantizer does */
-            const float sum = prod + 8.5f;
+            const float sum = fmaf(v[t], id, 8.5f);      /* one rounding, as the device writer's FMA */
             int c = sum == sum ? (int) sum : 0;
             q[t] = (uint8_t) (c < 0 ? 0 : (c > 15 ? 15 : c));
         }

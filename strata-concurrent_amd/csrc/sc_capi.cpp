@@ -61,6 +61,7 @@ struct sc_plan {
     uint64_t n_tiles = 0;
     uint64_t payload = 0;
     int64_t grid = 0;
+    int64_t default_grid = 0;           // what the builder chose; sc_plan_set_grid(plan, 0) returns to it
     int32_t mix = sc::kMixPlain;        // the kernel instance that holds every row kind of the plan
 };
 
@@ -207,7 +208,7 @@ int finish_plan(std::vector<sc::MoveRow>& rows, const Geo& g, uint64_t payload, 
     p->geo = move_geo(g);
     p->n_tiles = tiles;
     p->payload = payload;
-    p->grid = int64_t(std::min<uint64_t>(tiles, quant ? kMaxGridQuant : kMaxGrid));
+    p->grid = p->default_grid = int64_t(std::min<uint64_t>(tiles, quant ? kMaxGridQuant : kMaxGrid));
     p->mix = sc::mix_of(kv32, quant);
     if (rows.empty() || tiles == 0) {   // an empty handoff (0 tokens, no running state) is a valid no-op
         *out = p;
@@ -868,8 +869,7 @@ uint64_t sc_plan_payload_bytes(const sc_plan* plan) { return plan ? plan->payloa
 
 int sc_plan_set_grid(sc_plan* plan, int64_t workgroups) {
     if (!plan || workgroups < 0 || workgroups > (int64_t(1) << 30)) return fail(SC_EINVAL, "sc_handoff: invalid grid");
-    if (workgroups == 0) workgroups = int64_t(std::min<uint64_t>(std::max<uint64_t>(plan->n_tiles, 1), kMaxGrid));
-    plan->grid = std::max<int64_t>(workgroups, 1);
+    plan->grid = workgroups == 0 ? plan->default_grid : workgroups;
     return ok();
 }
 
@@ -1094,7 +1094,8 @@ int sc_plan_resume_append(const sc_geometry* g, const sc_batch_desc* d, sc_plan*
         sc_plan* p = new (std::nothrow) sc_plan();
         if (!p) return fail(SC_ENOMEM, "sc_handoff: plan allocation failed");
         p->batch = true;
-        p->grid = int64_t(std::min<uint64_t>(std::max<uint64_t>(per_slot * uint64_t(d->n_slots), 1), kMaxGrid));
+        p->grid = p->default_grid =
+            int64_t(std::min<uint64_t>(std::max<uint64_t>(per_slot * uint64_t(d->n_slots), 1), kMaxGrid));
         p->payload = 0;   // depends on the device-resident lengths
         hipError_t e = hipMalloc(reinterpret_cast<void**>(&p->batch_ptrs_dev), ptrs.size() * sizeof(uint64_t));
         if (e != hipSuccess) { delete p; return fail(SC_ENOMEM, std::string("sc_handoff: descriptor allocation: ") + hipGetErrorString(e)); }

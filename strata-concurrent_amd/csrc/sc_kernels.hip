@@ -241,7 +241,8 @@ __device__ void tile_conv(const MoveRow& r, uint64_t local, float (*lds)[kConvTi
 // src/kernels/cuda/kv_q8.cu:29-64) and q4_0 kv_append_q4 (src/kernels/cuda/kv_q4.cu:72-129): see the oracle
 // (sco_q8_row, sco_q4_row) for the exact definitions these lanes reproduce.  The divisions written with `/` are
 // IEEE divisions (the library is built with correctly rounded f32 divide), the int8 quotients are formed so that
-// they equal them (q8_code), and the q4 product and sum are rounded separately.
+// they equal them (q8_code), and the q4 code x * id + 8.5 is one fused multiply-add, as the reference's device writer
+// computes it (kv_q4.cu:84, contracted by its compilers' defaults).
 
 // The int8 code rint(x / sf) clamped to [-127, 127], with x / sf the correctly rounded quotient, formed from y, the
 // correctly rounded 1 / sf computed once per group: q0 = x * y, then one correction q = q0 + (x - q0 * sf) * y with
@@ -327,9 +328,12 @@ __device__ void tile_q8(const MoveRow& r, const MoveGeo& g, uint64_t local) {
         const float x0 = __uint_as_float(v.x), x1 = __uint_as_float(v.y), x2 = __uint_as_float(v.z),
                     x3 = __uint_as_float(v.w);
         // max |x| over the 64 values of this lane's group, the 16 lanes of its DPP row (fmax is exact, so any
-        // order gives the same).  It starts from 0, so NaNs never count and a group of NaNs has scale 0.
+        // order gives the same).  It starts from 0, so NaNs never count; a group of NaNs only (which the reference's
+        // fmaxf reduction leaves NaN) gets the f16 NaN 0x7E00 as its scale, and codes 0.
         const float a = row16_max_nonneg(fmaxf(fmaxf(fmaxf(fabsf(x0), fabsf(x1)), fmaxf(fabsf(x2), fabsf(x3))), 0.0f));
-        const uint32_t sb = f16_bits_rne_not_nan(div127(a));   // a is never NaN, nor is a / 127
+        const uint32_t real = uint32_t((x0 == x0) | (x1 == x1) | (x2 == x2) | (x3 == x3));
+        const bool any_real = __float_as_uint(row16_max_nonneg(__uint_as_float(real))) != 0u;
+        const uint32_t sb = any_real ? f16_bits_rne_not_nan(div127(a)) : 0x7E00u;   // a is never NaN, nor a / 127
         const float sf = f32_of_f16(sb);
         const float y = recip_normal(sf);   // sf is a binary16 value: 2^-24 <= sf <= 65504 wherever it codes
         const uint32_t codes = q8_code(x0, sf, y) | (q8_code(x1, sf, y) << 8) | (q8_code(x2, sf, y) << 16) |
@@ -384,9 +388,7 @@ __device__ __forceinline__ float q4_chosen(const float (&x)[4], uint32_t lb) {
 }
 
 __device__ __forceinline__ uint32_t q4_code(float x, float id) {
-#pragma clang fp contract(off)
-    const float prod = x * id;
-    const float sum = prod + 8.5f;
+    const float sum = __builtin_fmaf(x, id, 8.5f);
     const int c = sum == sum ? int(sum) : 0;
     return uint32_t(c < 0 ? 0 : (c > 15 ? 15 : c));
 }

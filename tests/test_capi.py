@@ -109,6 +109,18 @@ def test_image_refusals(sc):
     assert "identity-layout" in sc.last_error()
 
 
+def test_kv_append_range_refusals_before_any_hip_call(sc):
+    """A per-layer append whose rows the tiles could not index (2^31 chunks or more) is refused on the host, before
+    any launch: the pointers here are aligned stand-ins that are never dereferenced."""
+    K, pools = 1 << 40, 1 << 41
+    assert sc.lib.sc_kv_append_q4_async(pools, pools, None, 0, 1 << 30, K, K, 4, 256, 4, None, None,
+                                        None) == sc.SC_ERANGE
+    assert "2^31 chunks" in sc.last_error()
+    assert sc.lib.sc_kv_append_async(K, K, 1 << 26, 0, None, 4, pools, pools, None, None, None, None, None, None,
+                                     None) == sc.SC_ERANGE
+    assert "2^31 chunks" in sc.last_error()
+
+
 def test_noalloc_hash_refusals_before_any_hip_call(sc):
     """The hash without allocation refuses inputs past its static workspace, and missing pointers, on the host."""
     out = 1 << 40   # never dereferenced: the refusals come first

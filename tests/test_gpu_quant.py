@@ -37,6 +37,10 @@ def _edge_rows(src: np.ndarray) -> np.ndarray:
         x[5, 1, :32] = -np.float32(0)
         x[5, 1, 3] = np.float32(0)                  # -0 first among zeros
         x[6, 0, 1] = np.float32(1e7)                # max / 127 beyond f16: infinite scale
+    if T > 7:
+        # q4_0 blocks with values where a fused and a separately rounded x * id + 8.5 give different codes
+        from quant_cases import boundary_blocks
+        x[7] = boundary_blocks(2 * 8).reshape(2, 256)
     return x
 
 

@@ -4,10 +4,11 @@ restatements of the reference's rules and with hand-computed groups.
 int8 (src/prefill/kernels.cu:578-600; kv_q8.cu:29-64; host form kv_q8_parity.cpp:78-92): per 64 values the scale is
 f16(max|x| / 127) rounded to nearest even, codes rint(x / f32(scale)) clamped to +-127 (0 when the scale is 0).
 q4_0 (kv_q4.cu:72-89; host form kv_q4_parity.cpp:64-87): per 32 values d = (value of largest |x|, ties to the larger)
-/ -8, codes trunc(x * (1/d) + 8.5) with separately rounded product and sum, clamped to [0, 15], packed j | j+16 << 4
-after the f16 scale.  numpy float32 arithmetic is IEEE single precision with no contraction, so these vectorised
-forms are the same definitions computed a different way: a wrong group size, a dropped clamp, a rounding mode or a
-nibble order fails them.
+/ -8, codes trunc(x * (1/d) + 8.5) rounded once (the device writer's fused multiply-add), clamped to [0, 15], packed
+j | j+16 << 4 after the f16 scale.  numpy float32 arithmetic is IEEE single precision with no contraction; the fused
+q4 sum is formed exactly in float64 (the product of two binary32 values is exact there) with an error-free TwoSum
+deciding the rare ties.  So these vectorised forms are the same definitions computed a different way: a wrong group
+size, a dropped clamp, a rounding mode, a separately rounded product or a nibble order fails them.
 """
 import numpy as np
 import pytest
@@ -18,15 +19,35 @@ F32 = np.float32
 def q8_numpy(x):
     g = x.reshape(-1, 64).astype(F32)
     a = np.abs(g)
-    amax = np.max(np.where(np.isnan(a), F32(0), a), axis=1)      # fmaxf from 0: NaNs do not count
+    amax = np.max(np.where(np.isnan(a), F32(0), a), axis=1)      # NaNs do not count toward the maximum
     with np.errstate(over="ignore"):
         scale = (amax / F32(127)).astype(np.float16)
+    scale = np.where(np.isnan(g).all(axis=1), np.uint16(0x7E00).view(np.float16), scale)   # only NaNs: an f16 NaN
     sf = scale.astype(F32)[:, None]
     with np.errstate(divide="ignore", invalid="ignore"):
         q = np.rint(g / np.where(sf > 0, sf, F32(1)))
     ok = (sf > 0) & ~np.isnan(g) & ~np.isnan(q)                   # a NaN quotient (inf / inf) codes 0
     q = np.where(ok, np.clip(np.where(ok, q, 0), -127, 127), 0).astype(np.int8)
     return q.reshape(x.shape), scale.view(np.uint16).reshape(x.shape[:-1] + (x.shape[-1] // 64,))
+
+
+def fma_f32(a, b, c):
+    """RN_binary32(a * b + c) for binary32 arrays, rounded once: a * b is exact in float64, the float64 sum's error is
+    recovered exactly (Knuth's TwoSum), and where the float64 sum sits exactly halfway between two binary32 values the
+    error decides the side (elsewhere the float64 sum rounds to the same binary32 value as the exact one)."""
+    with np.errstate(invalid="ignore", over="ignore"):
+        p = a.astype(np.float64) * b.astype(np.float64)
+        c64 = np.float64(c)
+        s = p + c64
+        bb = s - p
+        err = (p - (s - bb)) + (c64 - bb)
+        f = s.astype(F32)
+        back = f.astype(np.float64)
+        other = np.where(back < s, np.nextafter(f, F32(np.inf)), np.nextafter(f, F32(-np.inf))).astype(np.float64)
+        tie = np.isfinite(s) & (back != s) & (s - back == other - s)
+        up, down = np.maximum(back, other), np.minimum(back, other)
+        fixed = np.where(err > 0, up, down).astype(F32)
+        return np.where(tie & (err != 0), fixed, f).astype(F32)
 
 
 def q4_numpy(x):
@@ -42,8 +63,7 @@ def q4_numpy(x):
     d = (mval / F32(-8)).astype(F32)
     with np.errstate(divide="ignore", invalid="ignore", over="ignore"):
         idv = np.where(d != 0, F32(1) / np.where(d != 0, d, F32(1)), F32(0)).astype(F32)
-        prod = (g * idv[:, None]).astype(F32)
-        s = (prod + F32(8.5)).astype(F32)
+        s = fma_f32(g, idv[:, None], F32(8.5))
     q = np.where(np.isnan(s), 0, np.clip(np.trunc(np.where(np.isnan(s), 0, s)), 0, 15)).astype(np.uint8)
     packed = (q[:, :16] | (q[:, 16:] << 4)).astype(np.uint8)
     with np.errstate(over="ignore"):
@@ -69,7 +89,7 @@ def _groups(rng, n, D):
     x[6, 0] = np.nan                               # NaN first in its group: never the maximum, codes 0
     x[7, 5] = np.nan
     x[7, 9] = F32(50)                              # ... and NaN before the group's maximum
-    x[8, :n64] = np.nan                            # a group of NaNs: scale 0 / d -0, codes 0 / 0
+    x[8, :n64] = np.nan                            # a group of NaNs: scale NaN / d -0, codes 0 / 0
     x[9, 2], x[9, 7] = F32(np.inf), -F32(np.inf)   # infinities: an infinite scale; inf / inf codes 0
     x[10, :32] = -F32(0)
     x[10, 3] = F32(0)                              # -0 first among zeros: d = -0 / -8 = +0
@@ -132,10 +152,28 @@ def test_q4_hand_computed(oracle):
     assert int(tb[0]) | (int(tb[1]) << 8) == int(np.array([d], F32).astype(np.float16).view(np.uint16)[0])
 
 
+def test_q4_codes_round_once_like_the_device_writer(oracle):
+    """Blocks with values on code boundaries, where trunc(RN(x * id + 8.5)) and trunc(RN(RN(x * id) + 8.5)) differ
+    (found with exact rational arithmetic): the oracle follows the fused form, code for code, and the numpy form agrees
+    with it; the separately rounded form would fail."""
+    from quant_cases import boundary_blocks, fused_code, separate_code
+    blocks = boundary_blocks(8)
+    got = oracle.q4_rows(blocks)
+    assert np.array_equal(got, q4_numpy(blocks))
+    differing = 0
+    for row, blk in zip(blocks, got):
+        d = F32(row[0] / F32(-8))
+        idv = F32(F32(1) / d)
+        codes = [(blk[2 + (t % 16)] >> (4 * (t // 16))) & 15 for t in range(32)]
+        assert codes == [fused_code(x, idv) for x in row]
+        differing += sum(fused_code(x, idv) != separate_code(x, idv) for x in row)
+    assert differing >= 8
+
+
 def test_nan_and_infinity_hand_computed(oracle):
     nan8 = np.full(64, np.nan, F32)
     codes, scales = oracle.q8_rows(nan8[None])
-    assert scales[0, 0] == 0 and not codes.any()                  # NaNs do not count toward the maximum
+    assert scales[0, 0] == 0x7E00 and not codes.any()             # only NaNs: the device writers' NaN maximum
     y = np.zeros(64, F32)
     y[0], y[1], y[2] = F32(np.inf), F32(1), F32(-np.inf)
     codes, scales = oracle.q8_rows(y[None])
