@@ -185,9 +185,10 @@ void sco_q8_row(const float* x, int64_t D, int8_t* codes, uint16_t* scales) {
         const float* v = x + g * 64;
         float amax = 0.0f;                              /* NaNs never count toward the maximum */
         int real = 0;
-        for (int t = 0; t < 64; ++t) {
-            amax = fmaxf(amax, fabsf(v[t]));
-            real |= v[t] == v[t];
+        for (int t = 0; t < 64; ++t) {   /* any NaN, quiet or signalling, is passed over (CUDA's fmaxf rule) */
+            const int is_real = v[t] == v[t];
+            if (is_real && fabsf(v[t]) > amax) amax = fabsf(v[t]);
+            real |= is_real;
         }
         const float ratio = amax / 127.0f;
         uint32_t rb;
@@ -229,8 +230,10 @@ void sco_q4_row(const float* x, int64_t D, uint8_t* blocks) {
         uint8_t q[32];
         for (int t = 0; t < 32; ++t) {
             const float sum = fmaf(v[t], id, 8.5f);      /* one rounding, as the device writer's FMA */
-            int c = sum == sum ? (int) sum : 0;
-            q[t] = (uint8_t) (c < 0 ? 0 : (c > 15 ? 15 : c));
+            /* truncation toward zero saturating, as __float2int_rz does: an infinite sum (id overflows for a block
+             * whose d is subnormal) clamps to 0 or 15, a NaN one (inf * 0) codes 0 */
+            const float c = sum != sum ? 0.0f : (sum < 0.0f ? 0.0f : (sum > 15.0f ? 15.0f : sum));
+            q[t] = (uint8_t) (int) c;
         }
         uint32_t db;
         memcpy(&db, &d, 4);

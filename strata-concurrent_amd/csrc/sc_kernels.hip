@@ -353,14 +353,15 @@ __device__ void tile_q8(const MoveRow& r, const MoveGeo& g, uint64_t local) {
 }
 
 // The q4_0 block's chosen value: the candidate of largest |x|, then of larger value, then of lower index; a NaN is
-// never chosen and a block of NaNs chooses +0.  Only three facts decide it, each the maximum of an unsigned key
-// over the block's 32 values (four per lane, then a DPP max over the block's 8 lanes):
-//   m  = max over non-NaN x of bits(|x|) + 1 (0: no candidate)  -> |chosen| = the value of bits m - 1;
-//   p  = max over x > 0 of bits(x) + 1                          -> the chosen value is +|max| iff p == m (a positive
-//        candidate reaches the maximum; any positive beats the negative of the same magnitude);
-//   z  = max over x == 0 of ((31 - j) << 1 | sign(x)) + 1       -> when the maximum is 0 every candidate is a zero,
-//        all equal as values, so the lowest index j wins and its sign is the low bit.
-// Keys of non-negative floats order as the numbers, so every step is one DPP max without NaN handling.
+// never chosen and a block of NaNs chooses +0.  One maximum decides the common case.  With f = rotl(bits(x), 1) =
+// 2 * bits(|x|) + sign, the key (f ^ 1) + kQ4KeyBase orders the values by magnitude and, at equal magnitude, puts the
+// positive value first; every NaN (f >= 0xFF000002) wraps below every number (f <= 0xFF000001), so none is chosen.
+// The maximum key over the block's 32 values (four per lane, then a DPP max over its 8 lanes) gives the chosen value
+// back.  When the largest magnitude is 0 (the block holds only zeros and NaNs) every candidate is a zero and all are
+// equal as values, so the lowest index wins: that rare case (a wave vote) takes a second maximum over the zeros,
+// z = ((31 - j) << 1 | sign) + 1.  Keys order as unsigned integers, so every step is one DPP max.
+constexpr uint32_t kQ4KeyBase = 0x00FFFFFEu;   // -0 keys to this, +0 to one more, NaNs below it
+
 __device__ __forceinline__ uint32_t half16_max(uint32_t u) {
     u = max(u, uint32_t(__builtin_amdgcn_update_dpp(0, int(u), kDppXor1, 0xF, 0xF, true)));
     u = max(u, uint32_t(__builtin_amdgcn_update_dpp(0, int(u), kDppXor2, 0xF, 0xF, true)));
@@ -368,29 +369,36 @@ __device__ __forceinline__ uint32_t half16_max(uint32_t u) {
     return u;
 }
 
-__device__ __forceinline__ float q4_chosen(const float (&x)[4], uint32_t lb) {
-    uint32_t m = 0, p = 0, z = 0;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const uint32_t bits = __float_as_uint(x[k]);
-        const uint32_t mag = bits & 0x7FFFFFFFu;
-        const bool real = x[k] == x[k];
-        m = max(m, real ? mag + 1u : 0u);
-        p = max(p, x[k] > 0.0f ? bits + 1u : 0u);
-        z = max(z, real && mag == 0u ? (((31u - (lb * 4u + uint32_t(k))) << 1) | (bits >> 31)) + 1u : 0u);
-    }
-    m = half16_max(m);
-    p = half16_max(p);
-    z = half16_max(z);
-    const float amax = __uint_as_float(m - 1u);
-    const float zero = __uint_as_float(((z - 1u) & 1u) << 31);
-    return m == 0u ? 0.0f : amax > 0.0f ? (p == m ? amax : -amax) : zero;
+__device__ __forceinline__ uint32_t q4_key(float x) {
+    return (__builtin_rotateleft32(__float_as_uint(x), 1) ^ 1u) + kQ4KeyBase;
 }
 
+__device__ __forceinline__ float q4_chosen(const float (&x)[4], uint32_t lb) {
+    uint32_t m = max(max(q4_key(x[0]), q4_key(x[1])), max(q4_key(x[2]), q4_key(x[3])));
+    m = half16_max(m);
+    const uint32_t f = (m - kQ4KeyBase) ^ 1u;
+    float chosen = __uint_as_float(__builtin_rotateright32(f, 1));
+    if (__any(m <= kQ4KeyBase + 1u)) {
+        uint32_t z = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t bits = __float_as_uint(x[k]);
+            const bool zero = (bits & 0x7FFFFFFFu) == 0u;
+            z = max(z, zero ? (((31u - (lb * 4u + uint32_t(k))) << 1) | (bits >> 31)) + 1u : 0u);
+        }
+        z = half16_max(z);
+        const float first_zero = __uint_as_float(((z - 1u) & 1u) << 31);
+        chosen = m < kQ4KeyBase ? 0.0f : m <= kQ4KeyBase + 1u ? first_zero : chosen;
+    }
+    return chosen;
+}
+
+// trunc(x * id + 8.5) clamped to [0, 15], the sum rounded once.  The clamp comes first, in float (one v_med3): a NaN sum
+// (inf * 0) clamps to 0 under the maximum's NaN rule and an infinite one to 0 or 15, as a saturating conversion would
+// give, so the conversion always sees a value in [0, 15].
 __device__ __forceinline__ uint32_t q4_code(float x, float id) {
     const float sum = __builtin_fmaf(x, id, 8.5f);
-    const int c = sum == sum ? int(sum) : 0;
-    return uint32_t(c < 0 ? 0 : (c > 15 ? 15 : c));
+    return uint32_t(__builtin_fminf(__builtin_fmaxf(sum, 0.0f), 15.0f));
 }
 
 __device__ void tile_q4(const MoveRow& r, const MoveGeo& g, uint64_t local) {
@@ -419,7 +427,9 @@ __device__ void tile_q4(const MoveRow& r, const MoveGeo& g, uint64_t local) {
         const uint32_t hi = dpp<kDppRowShl4>(q);   // lane lb + 4 holds the block's values 16 + 4 lb .. 19 + 4 lb
         const int64_t prow = pool_row(r, g, phys[i], kv_cell(r, g, unit));
         if (prow < 0) continue;
-        // block `blk` of the row: {f16 d, qs[16]}, 18 bytes at 18 * blk; qs[4 lb .. 4 lb + 3] from lanes lb, lb + 4
+        // block `blk` of the row: {f16 d, qs[16]}, 18 bytes at 18 * blk; qs[4 lb .. 4 lb + 3] from lanes lb, lb + 4.
+        // (Assembling each row into 36 aligned dwords with two more DPP moves, one store per row, measured slower:
+        // 1.397 against 1.375 ms for the 128K carve.)
         uint8_t* row = r.dst + uint64_t(prow) * (kQuantDim / 32 * 18) + blk * 18;
         using g16 = __attribute__((address_space(1))) uint16_t;
         if (lb == 0) *(g16*) (row) = uint16_t(f16_bits_rne_not_nan(d));   // the chosen value is never NaN
@@ -436,11 +446,11 @@ __device__ void tile_q4(const MoveRow& r, const MoveGeo& g, uint64_t local) {
 // `tile_row[t]` names the handoff table row of tile t, so a workgroup finds its row with two scalar loads and no
 // search.  The instance (kMix) compiles only its set of row kinds: the f32 rounding tile holds twice the loads
 // and the quantizers need 80-90 VGPRs, and compiled into one kernel they took the plain movers from 8 to 6 waves
-// per SIMD.
+// per SIMD.  The quantizing instance is held to 80 VGPRs (6 waves per SIMD): at 84 it fell to 5 waves and every
+// quantizing row slowed by 3-6%; the instance of every kind keeps 5 waves (at 80 VGPRs it would spill).
 template <int kMix>
-__global__ void __launch_bounds__(kThreads) sc_move_kernel(const MoveRow* __restrict__ rows,
-                                                            const uint16_t* __restrict__ tile_row, MoveGeo geo,
-                                                            uint64_t n_tiles) {
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kMix == kMixAll ? 5 : 6)))
+sc_move_kernel(const MoveRow* __restrict__ rows, const uint16_t* __restrict__ tile_row, MoveGeo geo, uint64_t n_tiles) {
     __shared__ float s_conv[kMaxHist][kConvTileChannels];
     int cur = -1;
     MoveRow r{};

@@ -33,6 +33,8 @@ def _edge_rows(src: np.ndarray) -> np.ndarray:
     if T > 6:
         x[4, 0, :64] = np.nan                       # a group / blocks of NaNs
         x[4, 1, 0], x[4, 1, 37] = np.nan, np.nan    # NaN first in a group, NaN inside a block
+        # a negative quiet NaN, a signalling NaN and the largest-payload negative NaN: never a block's maximum
+        x[4, 1, 40:43] = np.array([0xFFC00001, 0x7F800001, 0xFFFFFFFF], np.uint32).view(np.float32)
         x[5, 0, 2], x[5, 0, 9] = np.inf, -np.inf    # infinite scale; inf / inf
         x[5, 1, :32] = -np.float32(0)
         x[5, 1, 3] = np.float32(0)                  # -0 first among zeros

@@ -89,11 +89,14 @@ def _groups(rng, n, D):
     x[6, 0] = np.nan                               # NaN first in its group: never the maximum, codes 0
     x[7, 5] = np.nan
     x[7, 9] = F32(50)                              # ... and NaN before the group's maximum
+    x[7, n64 - 3:n64] = np.array([0xFFC00001, 0x7F800001, 0xFFFFFFFF], np.uint32).view(F32)   # negative, signalling
     x[8, :n64] = np.nan                            # a group of NaNs: scale NaN / d -0, codes 0 / 0
     x[9, 2], x[9, 7] = F32(np.inf), -F32(np.inf)   # infinities: an infinite scale; inf / inf codes 0
     x[10, :32] = -F32(0)
     x[10, 3] = F32(0)                              # -0 first among zeros: d = -0 / -8 = +0
     x[11, 1] = F32(1e7)                            # max / 127 beyond the f16 range: an infinite scale
+    x[12, :32] = 0                                 # a q4_0 block with a subnormal d: 1/d overflows to -inf, so
+    x[12, 0], x[12, 1] = F32(2.0 ** -146), -F32(2.0 ** -147)   # x * id + 8.5 is -inf (code 0) and +inf (code 15)
     return x
 
 
@@ -168,6 +171,16 @@ def test_q4_codes_round_once_like_the_device_writer(oracle):
         assert codes == [fused_code(x, idv) for x in row]
         differing += sum(fused_code(x, idv) != separate_code(x, idv) for x in row)
     assert differing >= 8
+
+
+def test_q4_overflowing_reciprocal_hand_computed(oracle):
+    """d = 2^-146 / -8 = -2^-149 is the smallest subnormal, 1/d overflows to -inf: a positive value codes 0, a negative
+    one 15 (a saturating conversion of +inf), a zero 0 (0 * inf is NaN)."""
+    x = np.zeros(32, F32)
+    x[0], x[1] = F32(2.0 ** -146), -F32(2.0 ** -147)
+    blk = oracle.q4_rows(x[None])[0]
+    assert int(blk[0]) | (int(blk[1]) << 8) == 0x8000               # d = -2^-149 rounds to -0 in f16
+    assert blk[2] == 0 and blk[3] == 15 and not blk[4:].any()
 
 
 def test_nan_and_infinity_hand_computed(oracle):
