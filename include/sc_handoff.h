@@ -79,6 +79,19 @@ typedef struct sc_prefill_view {
     int64_t conv_ld;              /* row stride of the conv source in floats (>= C) */
 } sc_prefill_view;
 
+/* strata::kernels::KvHostPools (include/strata/kernels/kv_stream.hpp:30-39), member for member: one layer's host
+ * copy (device-mapped pinned memory) or staging pool, identity layout [block][kv_head][page_size][row]. */
+typedef struct sc_kv_pools {
+    uint16_t* k_pool;   /* f16 rows */
+    uint16_t* v_pool;
+    int8_t* k_q;        /* int8 codes */
+    int8_t* v_q;
+    uint16_t* k_scale;  /* int8: one f16 scale per 64 values */
+    uint16_t* v_scale;
+    uint8_t* k_q4;      /* q4_0 blocks, 144 bytes per cell and head */
+    uint8_t* v_q4;
+} sc_kv_pools;
+
 /* The decode slot: the device pointers of a strata::core::SessionState's state for one sequence
  * (include/strata/core/session.hpp:30-60 and QsaState, include/strata/core/layer.hpp:203-225). */
 typedef struct sc_decode_slot {
@@ -89,6 +102,14 @@ typedef struct sc_decode_slot {
     const int32_t* const* page_table;   /* NULL, or [n_qsa] device tables logical page -> physical page;
                                            a NULL entry is the identity table (kv_mode 0) */
     float* gdn_state;                   /* n_gdn rows of sc_gdn_row_floats() floats (session.hpp:34) */
+    /* A streamed layer's authoritative host copy and the prompt path's staging pool: NULL, or host arrays [n_qsa] of
+     * sc_kv_pools in the identity layout [logical page][n_head_kv][page_size][row] holding max_cells cells (the host
+     * copy is device-mapped pinned memory, the staging pool device memory).  An entry whose pools of the slot's
+     * format are NULL is skipped.  A carve writes every cell it carves into each given pool as well, resident in the
+     * paged pool or not, in the same launch (kv_append, src/prefill/kernels.cu:574-577,587-600;
+     * kv_append_q4, src/kernels/cuda/kv_q4.cu:124-128). */
+    const sc_kv_pools* host;
+    const sc_kv_pools* stage;
 } sc_decode_slot;
 
 /* One row of an image layout. */
@@ -153,6 +174,8 @@ typedef struct sc_quant_slot {
     uint16_t* const* v_scale;           /* [n_qsa] f16 scales of V (INT8), else NULL */
     const int32_t* const* page_table;   /* as sc_decode_slot */
     float* gdn_state;
+    const sc_kv_pools* host;            /* as sc_decode_slot: int8 codes + scales, or q4_0 blocks (not for K8V4, which */
+    const sc_kv_pools* stage;           /* is resident only, conversation_snapshot.cpp's hybrid rule) */
 } sc_quant_slot;
 
 /* The quantizing carve: f32 prefill K/V rows [T][H][256] (q4_0 rows already rotated, as the reference rotates before
@@ -166,18 +189,6 @@ int sc_plan_carve_quant(const sc_geometry* g, const sc_prefill_view* src, const 
  * instead).  Every entry point returns before its launch when T <= 0, and refuses (SC_EINVAL, nothing launched)
  * missing or misaligned buffers and impossible extents; pools are not bounded, the caller sized them, as there. */
 
-/* strata::kernels::KvHostPools (include/strata/kernels/kv_stream.hpp:30-39), member for member: one layer's host
- * copy (device-mapped pinned memory) or staging pool, identity layout [block][kv_head][page_size][row]. */
-typedef struct sc_kv_pools {
-    uint16_t* k_pool;   /* f16 rows */
-    uint16_t* v_pool;
-    int8_t* k_q;        /* int8 codes */
-    int8_t* v_q;
-    uint16_t* k_scale;  /* int8: one f16 scale per 64 values */
-    uint16_t* v_scale;
-    uint8_t* k_q4;      /* q4_0 blocks, 144 bytes per cell and head */
-    uint8_t* v_q4;
-} sc_kv_pools;
 
 /* kv_append (include/strata/prefill/kernels.hpp:78-83, src/prefill/kernels.cu:558-625): K and V, f32 [T][2][256]
  * (positions pos0 .. pos0 + T - 1), into the paged pool - f16 rows (RNE) when k_pool is given, else int8 codes with an

@@ -336,6 +336,48 @@ void gdn_rows(const Geo& g, const sc_prefill_view* v, float* gdn, std::vector<sc
     }
 }
 
+// The identity-layout pools a carve writes beside the paged pool (a streamed layer's host copy, the prompt path's
+// staging pool): `pools` is NULL or [n_qsa].  Returns, per layer, the K, V (and int8 scale) destinations of `format`,
+// or nulls for a layer that has none; refuses half-given or misaligned pools.
+struct ExtraKv {
+    uint8_t* k = nullptr;
+    uint8_t* v = nullptr;
+    uint16_t* ks = nullptr;
+    uint16_t* vs = nullptr;
+};
+int extra_kv(const Geo& g, const sc_kv_pools* pools, int32_t format, const char* what, std::vector<ExtraKv>& out) {
+    out.assign(size_t(g.n_qsa), ExtraKv{});
+    if (!pools) return SC_OK;
+    for (int64_t j = 0; j < g.n_qsa; ++j) {
+        const sc_kv_pools& p = pools[j];
+        ExtraKv& e = out[size_t(j)];
+        switch (format) {
+            case SC_KV_F16:
+                e.k = reinterpret_cast<uint8_t*>(p.k_pool), e.v = reinterpret_cast<uint8_t*>(p.v_pool);
+                break;
+            case SC_KV_INT8:
+                e.k = reinterpret_cast<uint8_t*>(p.k_q), e.v = reinterpret_cast<uint8_t*>(p.v_q);
+                e.ks = p.k_scale, e.vs = p.v_scale;
+                break;
+            case SC_KV_Q4:
+                e.k = p.k_q4, e.v = p.v_q4;
+                break;
+            default:   // K8V4 is resident only: it has no host copy or staging pool
+                if (p.k_pool || p.v_pool || p.k_q || p.v_q || p.k_scale || p.v_scale || p.k_q4 || p.v_q4)
+                    return snapshot_fail("hybrid K8V4 requires an identity layout and distinct format flags");
+                continue;
+        }
+        const bool any = e.k || e.v || e.ks || e.vs;
+        const bool all = e.k && e.v && (format != SC_KV_INT8 || (e.ks && e.vs));
+        if (any && !all) return fail(SC_EINVAL, std::string("sc_handoff: ") + what + " needs every pool of its format");
+        const uintptr_t a = format == SC_KV_F16 ? 16 : 4;
+        if (any && ((reinterpret_cast<uintptr_t>(e.k) | reinterpret_cast<uintptr_t>(e.v)) & (a - 1) ||
+                    (format == SC_KV_INT8 && ((reinterpret_cast<uintptr_t>(e.ks) | reinterpret_cast<uintptr_t>(e.vs)) & 7u))))
+            return fail(SC_EINVAL, std::string("sc_handoff: ") + what + " pools must be aligned as the slot's pools are");
+    }
+    return SC_OK;
+}
+
 uint64_t kv_payload(const Geo& g, int64_t tokens) { return uint64_t(tokens) * uint64_t(g.H) * g.row_bytes * 2 * uint64_t(g.n_qsa); }
 
 // ---- slot images in every K/V format (sc_slot_layers) ----
@@ -470,12 +512,24 @@ int sc_plan_carve(const sc_geometry* g, const sc_prefill_view* src, const sc_dec
         if (rc) return rc;
         rc = check_slot(o, dst, src->pos0 + src->tokens, src->with_gdn != 0);
         if (rc) return rc;
+        std::vector<ExtraKv> host, stage;
+        if ((rc = extra_kv(o, dst->host, SC_KV_F16, "a host copy", host)) ||
+            (rc = extra_kv(o, dst->stage, SC_KV_F16, "a staging pool", stage)))
+            return rc;
+        const int64_t logical_pages = (dst->max_cells + o.ps - 1) / o.ps;
         std::vector<sc::MoveRow> rows;
+        uint64_t payload = kv_payload(o, src->tokens);
         for (int64_t j = 0; j < o.n_qsa; ++j) {
             const int32_t* table = dst->page_table ? dst->page_table[j] : nullptr;
             kv_rows(o, src, j, dst->k_pool[j], dst->v_pool[j], table, dst->n_pages, 0, rows);
+            // the identity-layout copies get every carved cell, resident in the paged pool or not
+            for (const ExtraKv* e : {&host[size_t(j)], &stage[size_t(j)]}) {
+                if (!e->k) continue;
+                kv_rows(o, src, j, reinterpret_cast<uint16_t*>(e->k), reinterpret_cast<uint16_t*>(e->v), nullptr,
+                        logical_pages, 0, rows);
+                payload += uint64_t(src->tokens) * uint64_t(o.H) * o.row_bytes * 2;
+            }
         }
-        uint64_t payload = kv_payload(o, src->tokens);
         if (src->with_gdn) {
             gdn_rows(o, src, dst->gdn_state, rows);
             payload += uint64_t(o.n_gdn) * o.gdn_row_bytes;
@@ -518,28 +572,40 @@ int sc_plan_carve_quant(const sc_geometry* g, const sc_prefill_view* src, const 
             if (!aligned16(dst->gdn_state) || o.gdn_row_bytes % 16)
                 return fail(SC_EINVAL, "sc_handoff: GDN rows must be 16-byte aligned multiples of 16 bytes");
         }
+        std::vector<ExtraKv> host, stage;
+        if ((rc = extra_kv(o, dst->host, dst->format, "a host copy", host)) ||
+            (rc = extra_kv(o, dst->stage, dst->format, "a staging pool", stage)))
+            return rc;
+        const int64_t logical_pages = (dst->max_cells + o.ps - 1) / o.ps;
         std::vector<sc::MoveRow> rows;
         uint64_t payload = 0;
         const uint64_t units = uint64_t(src->tokens) * uint64_t(o.H);
         for (int64_t j = 0; j < o.n_qsa && units; ++j) {
-            const int32_t* table = dst->page_table ? dst->page_table[j] : nullptr;
             const void* srcs[2] = {src->k[j], src->v[j]};
-            void* codes[2] = {dst->k_codes[j], dst->v_codes[j]};
-            uint16_t* scales[2] = {k_int8 ? dst->k_scale[j] : nullptr, v_int8 ? dst->v_scale[j] : nullptr};
             const bool int8[2] = {k_int8, v_int8};
-            for (int a = 0; a < 2; ++a) {
-                sc::MoveRow r{};
-                r.kind = int8[a] ? sc::kKvQ8 : sc::kKvQ4;
-                r.src = static_cast<const uint8_t*>(srcs[a]);
-                r.dst = static_cast<uint8_t*>(codes[a]);
-                r.dst2 = reinterpret_cast<uint8_t*>(scales[a]);
-                r.table = table;
-                r.pos0 = src->pos0;
-                r.ld = dst->n_pages;
-                r.aux = int32_t(src->tokens);
-                r.n = units;
-                rows.push_back(r);
-                payload += units * sc::kQuantDim * 4 + units * (int8[a] ? sc::kQuantDim + 8 : sc::kQuantDim / 32 * 18);
+            // the paged pool through the page table, then the identity-layout copies (every carved cell)
+            const ExtraKv pool{static_cast<uint8_t*>(dst->k_codes[j]), static_cast<uint8_t*>(dst->v_codes[j]),
+                               k_int8 ? dst->k_scale[j] : nullptr, v_int8 ? dst->v_scale[j] : nullptr};
+            const ExtraKv* dests[3] = {&pool, &host[size_t(j)], &stage[size_t(j)]};
+            for (int d = 0; d < 3; ++d) {
+                if (!dests[d]->k) continue;
+                uint8_t* codes[2] = {dests[d]->k, dests[d]->v};
+                uint16_t* scales[2] = {dests[d]->ks, dests[d]->vs};
+                for (int a = 0; a < 2; ++a) {
+                    sc::MoveRow r{};
+                    r.kind = int8[a] ? sc::kKvQ8 : sc::kKvQ4;
+                    r.src = static_cast<const uint8_t*>(srcs[a]);
+                    r.dst = codes[a];
+                    r.dst2 = reinterpret_cast<uint8_t*>(scales[a]);
+                    r.table = d == 0 && dst->page_table ? dst->page_table[j] : nullptr;
+                    r.pos0 = src->pos0;
+                    r.ld = d == 0 ? dst->n_pages : logical_pages;
+                    r.aux = int32_t(src->tokens);
+                    r.n = units;
+                    rows.push_back(r);
+                    payload +=
+                        units * sc::kQuantDim * 4 + units * (int8[a] ? sc::kQuantDim + 8 : sc::kQuantDim / 32 * 18);
+                }
             }
         }
         if (src->with_gdn) {

@@ -53,17 +53,18 @@ class PrefillView(C.Structure):
         ("conv_rows", C.c_int64), ("conv_ld", C.c_int64)]
 
 
-class DecodeSlot(C.Structure):
-    _fields_ = [
-        ("n_pages", C.c_int64), ("max_cells", C.c_int64),
-        ("k_pool", C.POINTER(C.c_void_p)), ("v_pool", C.POINTER(C.c_void_p)),
-        ("page_table", C.POINTER(C.c_void_p)), ("gdn_state", C.c_void_p)]
-
-
 class KvPools(C.Structure):
     """sc_kv_pools (strata::kernels::KvHostPools): a layer's host copy or staging pool; unused members NULL."""
     _fields_ = [("k_pool", C.c_void_p), ("v_pool", C.c_void_p), ("k_q", C.c_void_p), ("v_q", C.c_void_p),
                 ("k_scale", C.c_void_p), ("v_scale", C.c_void_p), ("k_q4", C.c_void_p), ("v_q4", C.c_void_p)]
+
+
+class DecodeSlot(C.Structure):
+    _fields_ = [
+        ("n_pages", C.c_int64), ("max_cells", C.c_int64),
+        ("k_pool", C.POINTER(C.c_void_p)), ("v_pool", C.POINTER(C.c_void_p)),
+        ("page_table", C.POINTER(C.c_void_p)), ("gdn_state", C.c_void_p),
+        ("host", C.POINTER(KvPools)), ("stage", C.POINTER(KvPools))]
 
 
 class KvRuns(C.Structure):
@@ -86,7 +87,8 @@ class QuantSlot(C.Structure):
     _fields_ = [("n_pages", C.c_int64), ("max_cells", C.c_int64), ("format", C.c_int32),
                 ("k_codes", C.POINTER(C.c_void_p)), ("v_codes", C.POINTER(C.c_void_p)),
                 ("k_scale", C.POINTER(C.c_void_p)), ("v_scale", C.POINTER(C.c_void_p)),
-                ("page_table", C.POINTER(C.c_void_p)), ("gdn_state", C.c_void_p)]
+                ("page_table", C.POINTER(C.c_void_p)), ("gdn_state", C.c_void_p),
+                ("host", C.POINTER(KvPools)), ("stage", C.POINTER(KvPools))]
 
 
 class BlobMap(C.Structure):
@@ -400,16 +402,21 @@ class Slot:
     gdn: object
     tables: list | None = None
     _keep: tuple = field(default=(), repr=False)
+    host: list | None = None    # per QSA layer a KvPools (a streamed layer's host copy), or None
+    stage: list | None = None   # per QSA layer a KvPools (the staging pool), or None
 
     def c_struct(self) -> DecodeSlot:
         ks = _ptrs([t.data_ptr() for t in self.k_pool])
         vs = _ptrs([t.data_ptr() for t in self.v_pool])
         ts = _ptrs([t.data_ptr() if t is not None else None for t in self.tables]) if self.tables else None
-        self._keep = (ks, vs, ts)
+        hs, ss = _pools_array(self.host), _pools_array(self.stage)
+        self._keep = (ks, vs, ts, hs, ss)
         return DecodeSlot(n_pages=self.n_pages, max_cells=self.max_cells,
                           k_pool=C.cast(ks, C.POINTER(C.c_void_p)), v_pool=C.cast(vs, C.POINTER(C.c_void_p)),
                           page_table=C.cast(ts, C.POINTER(C.c_void_p)) if ts is not None else None,
-                          gdn_state=self.gdn.data_ptr() if self.gdn is not None else None)
+                          gdn_state=self.gdn.data_ptr() if self.gdn is not None else None,
+                          host=C.cast(hs, C.POINTER(KvPools)) if hs is not None else None,
+                          stage=C.cast(ss, C.POINTER(KvPools)) if ss is not None else None)
 
     def buffers(self) -> list:
         return [*self.k_pool, *self.v_pool, *([self.gdn] if self.gdn is not None else [])]
@@ -424,6 +431,13 @@ class Slot:
         if self.gdn is not None:
             out["gdn"] = self.gdn.numpy()
         return out
+
+
+def _pools_array(pools):
+    """A ctypes array of KvPools (None entries are all-NULL pools), or None."""
+    if not pools:
+        return None
+    return (KvPools * len(pools))(*[p if p is not None else KvPools() for p in pools])
 
 
 def new_slot(geo: Geometry, max_cells: int, n_pages: int | None = None, tables=None, fill: int = 0) -> Slot:
@@ -806,6 +820,8 @@ class QuantPools:
     gdn: object
     tables: list | None = None
     _keep: tuple = field(default=(), repr=False)
+    host: list | None = None    # per QSA layer a KvPools (a streamed layer's host copy), or None
+    stage: list | None = None   # per QSA layer a KvPools (the staging pool), or None
 
     def c_struct(self) -> QuantSlot:
         kc = _ptrs([t.ptr for t in self.k_codes])
@@ -813,11 +829,14 @@ class QuantPools:
         ks = _ptrs([t.ptr for t in self.k_scale]) if self.k_scale else None
         vs = _ptrs([t.ptr for t in self.v_scale]) if self.v_scale else None
         ts = _ptrs([t.data_ptr() if t is not None else None for t in self.tables]) if self.tables else None
-        self._keep = (kc, vc, ks, vs, ts)
+        hs, ss = _pools_array(self.host), _pools_array(self.stage)
+        self._keep = (kc, vc, ks, vs, ts, hs, ss)
         cast = lambda a: C.cast(a, C.POINTER(C.c_void_p)) if a is not None else None  # noqa: E731
         return QuantSlot(n_pages=self.n_pages, max_cells=self.max_cells, format=self.fmt, k_codes=cast(kc),
                          v_codes=cast(vc), k_scale=cast(ks), v_scale=cast(vs), page_table=cast(ts),
-                         gdn_state=self.gdn.data_ptr() if self.gdn is not None else None)
+                         gdn_state=self.gdn.data_ptr() if self.gdn is not None else None,
+                         host=C.cast(hs, C.POINTER(KvPools)) if hs is not None else None,
+                         stage=C.cast(ss, C.POINTER(KvPools)) if ss is not None else None)
 
     def buffers(self) -> list:
         return [*self.k_codes, *self.v_codes, *self.k_scale, *self.v_scale, *([self.gdn] if self.gdn is not None else [])]
