@@ -293,6 +293,12 @@ int sc_resume_layers_async(const sc_geometry* g, const void* host_image, uint64_
                            const sc_slot_layers* slot, void* stream, void* done);
 /* Enqueue the plan on `stream` (a hipStream_t; NULL is the null stream).  Asynchronous. */
 int sc_plan_launch(const sc_plan* plan, void* stream);
+/* sc_plan_launch that moves nothing unless the 32-bit word at `gate` (device memory, written by earlier work on the
+ * same stream, e.g. the verdict of sc_fnv1a64_check_async) is nonzero when the launch runs.  Every workgroup reads the
+ * same word, so the launch writes all of the plan's bytes or none: a mount that checks its payload hash on the device
+ * and scatters without a host round trip (the reference compares the hash on the host before it mounts,
+ * src/core/conversation_wire.cpp:1069-1071).  Not for batched plans (SC_EINVAL). */
+int sc_plan_launch_gated(const sc_plan* plan, const uint32_t* gate, void* stream);
 /* Algorithmic payload bytes the plan moves (each read once and written once). */
 uint64_t sc_plan_payload_bytes(const sc_plan* plan);
 /* Workgroups the launch uses, for launch-shape sweeps; 0 restores the grid the plan was built with. */
@@ -393,6 +399,10 @@ uint64_t sc_fnv1a64_workspace_bytes(uint64_t bytes);
  * sc_fnv1a64_workspace_bytes(bytes); nothing is allocated. */
 int sc_fnv1a64_async(const void* data, uint64_t bytes, uint64_t seed, uint64_t* out, void* workspace,
                      uint64_t workspace_bytes, void* stream);
+/* sc_fnv1a64_async that also writes, at `verdict` (4-byte aligned device memory), 1 when the hash equals `expected` and
+ * 0 otherwise: the gate of sc_plan_launch_gated. */
+int sc_fnv1a64_check_async(const void* data, uint64_t bytes, uint64_t seed, uint64_t expected, uint64_t* out,
+                           uint32_t* verdict, void* workspace, uint64_t workspace_bytes, void* stream);
 /* The same hash continued over one more piece: the running hash is the u64 at `state` in device memory (the seed
  * before the first piece), read when the piece's kernels run on `stream` and replaced by the hash of everything so
  * far.  Hashing a buffer piece by piece in order, each call after the one before it on the same stream, gives the

@@ -23,7 +23,7 @@ namespace sc {
 hipError_t launch_append(const AppendRows& rows, int n_rows, uint64_t tiles_per_row, const MoveGeo& geo, int32_t kind,
                          hipStream_t stream);
 hipError_t launch_move(const MoveRow* rows, const uint16_t* tile_row, const MoveGeo& geo, uint64_t n_tiles,
-                       int64_t grid, int32_t mix, hipStream_t stream);
+                       int64_t grid, int32_t mix, hipStream_t stream, const uint32_t* gate = nullptr);
 hipError_t launch_fill_uniform_f16(uint16_t* dst, uint64_t n, float lo, float hi, uint64_t seed, uint64_t sid,
                                    hipStream_t stream);
 hipError_t launch_fill_uniform_f32(float* dst, uint64_t n, float lo, float hi, uint64_t seed, uint64_t sid,
@@ -39,7 +39,7 @@ hipError_t launch_stream_reset(int32_t* table, int64_t n_blocks, int32_t* slot_b
                                int32_t* slot_ref, int64_t n_slots, int32_t* ctl, hipStream_t stream);
 hipError_t launch_ring_table(int32_t* table, int64_t n_blocks, int64_t n_slots, hipStream_t stream);
 hipError_t launch_fnv1a64(const void* data, uint64_t n, uint64_t seed, const uint64_t* seed_dev, uint64_t* out,
-                          void* workspace, hipStream_t stream);
+                          void* workspace, hipStream_t stream, uint64_t expected = 0, uint32_t* verdict = nullptr);
 
 static uint64_t host_mix64(uint64_t z) {
     z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
@@ -931,6 +931,15 @@ int sc_plan_launch(const sc_plan* plan, void* stream) {
     return e == hipSuccess ? ok() : hip_fail(e, "move launch");
 }
 
+int sc_plan_launch_gated(const sc_plan* plan, const uint32_t* gate, void* stream) {
+    if (!plan || !gate || (reinterpret_cast<uintptr_t>(gate) & 3u))
+        return fail(SC_EINVAL, "sc_handoff: a gated launch needs a plan and a 4-byte aligned gate word");
+    if (plan->batch) return fail(SC_EINVAL, "sc_handoff: a batched plan is all or nothing on its own lengths");
+    const hipError_t e = sc::launch_move(plan->rows_dev, plan->tile_row_dev, plan->geo, plan->n_tiles, plan->grid,
+                                         plan->mix, static_cast<hipStream_t>(stream), gate);
+    return e == hipSuccess ? ok() : hip_fail(e, "move launch");
+}
+
 uint64_t sc_plan_payload_bytes(const sc_plan* plan) { return plan ? plan->payload : 0; }
 
 int sc_plan_set_grid(sc_plan* plan, int64_t workgroups) {
@@ -1363,6 +1372,20 @@ int sc_fnv1a64_async(const void* data, uint64_t bytes, uint64_t seed, uint64_t* 
     if (reinterpret_cast<uintptr_t>(workspace) & 15u) return fail(SC_EINVAL, "sc_handoff: hash workspace must be 16-byte aligned");
     if (bytes > (uint64_t(1) << 46)) return fail(SC_ERANGE, "sc_handoff: hash input beyond 2^46 bytes");
     SC_HIP(sc::launch_fnv1a64(data, bytes, seed, nullptr, out, workspace, static_cast<hipStream_t>(stream)),
+           "hash launch");
+    return ok();
+}
+
+int sc_fnv1a64_check_async(const void* data, uint64_t bytes, uint64_t seed, uint64_t expected, uint64_t* out,
+                           uint32_t* verdict, void* workspace, uint64_t workspace_bytes, void* stream) {
+    if (!out || !verdict || (bytes && !data)) return fail(SC_EINVAL, "sc_handoff: missing hash input, output or verdict");
+    if (reinterpret_cast<uintptr_t>(verdict) & 3u) return fail(SC_EINVAL, "sc_handoff: the verdict must be 4-byte aligned");
+    if (!workspace || workspace_bytes < sc::fnv_workspace(bytes).bytes)
+        return fail(SC_EINVAL, "sc_handoff: hash workspace smaller than sc_fnv1a64_workspace_bytes()");
+    if (reinterpret_cast<uintptr_t>(workspace) & 15u) return fail(SC_EINVAL, "sc_handoff: hash workspace must be 16-byte aligned");
+    if (bytes > (uint64_t(1) << 46)) return fail(SC_ERANGE, "sc_handoff: hash input beyond 2^46 bytes");
+    SC_HIP(sc::launch_fnv1a64(data, bytes, seed, nullptr, out, workspace, static_cast<hipStream_t>(stream), expected,
+                              verdict),
            "hash launch");
     return ok();
 }

@@ -498,9 +498,12 @@ __global__ void __launch_bounds__(kThreads) fnv_final_kernel(const uint8_t* data
     if (threadIdx.x == 0) partial[blockIdx.x] = s_sum[0] + s_sum[1] + s_sum[2] + s_sum[3];
 }
 
-// h = seed * p^n + sum of the partial sums (mod 2^64; the order of the additions does not matter).
+// h = seed * p^n + sum of the partial sums (mod 2^64; the order of the additions does not matter).  With `verdict`,
+// also 1 there when h equals `expected`, else 0: a later kernel on the stream can act on the check without a host
+// round trip.
 __global__ void __launch_bounds__(kScanThreads) fnv_reduce_kernel(const uint64_t* partial, uint64_t groups, uint64_t seed,
-                                                                   const uint64_t* seed_dev, uint64_t n, uint64_t* out) {
+                                                                   const uint64_t* seed_dev, uint64_t n, uint64_t* out,
+                                                                   uint64_t expected, uint32_t* verdict) {
     uint64_t acc = 0;
     for (uint64_t i = threadIdx.x; i < groups; i += kScanThreads) acc += partial[i];
     for (int m = 32; m > 0; m >>= 1) acc += shfl_xor64(acc, m);
@@ -511,6 +514,7 @@ __global__ void __launch_bounds__(kScanThreads) fnv_reduce_kernel(const uint64_t
         uint64_t h = start_state(seed, seed_dev) * pow_prime(n);
         for (int w = 0; w < kScanThreads / 64; ++w) h += s_sum[w];
         out[0] = h;
+        if (verdict) verdict[0] = h == expected ? 1u : 0u;
     }
 }
 
@@ -534,7 +538,7 @@ FnvWorkspace fnv_workspace(uint64_t n) {
 }
 
 hipError_t launch_fnv1a64(const void* data, uint64_t n, uint64_t seed, const uint64_t* seed_dev, uint64_t* out,
-                          void* workspace, hipStream_t stream) {
+                          void* workspace, hipStream_t stream, uint64_t expected, uint32_t* verdict) {
     const FnvWorkspace w = fnv_workspace(n);
     uint8_t* ws = static_cast<uint8_t*>(workspace);
     const uint8_t* src = static_cast<const uint8_t*>(data);
@@ -569,7 +573,7 @@ hipError_t launch_fnv1a64(const void* data, uint64_t n, uint64_t seed, const uin
     }
     // the reduce reads the start state before it writes `out`, so `out` may be `seed_dev` itself
     hipLaunchKernelGGL(fnv_reduce_kernel, dim3(1), dim3(kScanThreads), 0, stream, partial, w.groups, seed, seed_dev, n,
-                       out);
+                       out, expected, verdict);
     return hipGetLastError();
 }
 
@@ -620,7 +624,7 @@ extern "C" int sc_fnv1a64_noalloc_async(const void* data, uint64_t bytes, uint64
     hipError_t e = scratch_of_current_device(&ws);
     if (e != hipSuccess)
         return sc::record_error(SC_EHIP, std::string("sc_handoff hash scratch: ") + hipGetErrorString(e));
-    e = sc::launch_fnv1a64(data, bytes, seed, nullptr, out, ws, static_cast<hipStream_t>(stream));
+    e = sc::launch_fnv1a64(data, bytes, seed, nullptr, out, ws, static_cast<hipStream_t>(stream), 0, nullptr);
     if (e != hipSuccess) return sc::record_error(SC_EHIP, std::string("sc_handoff hash launch: ") + hipGetErrorString(e));
     return sc::record_ok();
 }

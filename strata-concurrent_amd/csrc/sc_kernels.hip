@@ -450,7 +450,11 @@ __device__ void tile_q4(const MoveRow& r, const MoveGeo& g, uint64_t local) {
 // quantizing row slowed by 3-6%; the instance of every kind keeps 5 waves (at 80 VGPRs it would spill).
 template <int kMix>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kMix == kMixAll ? 5 : 6)))
-sc_move_kernel(const MoveRow* __restrict__ rows, const uint16_t* __restrict__ tile_row, MoveGeo geo, uint64_t n_tiles) {
+sc_move_kernel(const MoveRow* __restrict__ rows, const uint16_t* __restrict__ tile_row, MoveGeo geo, uint64_t n_tiles,
+               const uint32_t* __restrict__ gate) {
+    // A gated launch moves nothing unless the word a kernel before it on the stream left at `gate` is nonzero (a
+    // payload hash that matched): every workgroup reads the same word, so the launch writes all or nothing.
+    if (gate && __builtin_amdgcn_readfirstlane(*gate) == 0u) return;
     __shared__ float s_conv[kMaxHist][kConvTileChannels];
     int cur = -1;
     MoveRow r{};
@@ -794,22 +798,22 @@ hipError_t launch_ring_table(int32_t* table, int64_t n_blocks, int64_t n_slots, 
 }
 
 hipError_t launch_move(const MoveRow* rows, const uint16_t* tile_row, const MoveGeo& geo, uint64_t n_tiles,
-                       int64_t grid, int32_t mix, hipStream_t stream) {
+                       int64_t grid, int32_t mix, hipStream_t stream, const uint32_t* gate) {
     if (n_tiles == 0) return hipSuccess;
     if (!rows || !tile_row || grid <= 0 || mix < kMixPlain || mix > kMixAll) return hipErrorInvalidValue;
     const dim3 blocks(unsigned(uint64_t(grid) < n_tiles ? uint64_t(grid) : n_tiles)), threads(kThreads);
     switch (mix) {
         case kMixPlain:
-            hipLaunchKernelGGL(sc_move_kernel<kMixPlain>, blocks, threads, 0, stream, rows, tile_row, geo, n_tiles);
+            hipLaunchKernelGGL(sc_move_kernel<kMixPlain>, blocks, threads, 0, stream, rows, tile_row, geo, n_tiles, gate);
             break;
         case kMixWide:
-            hipLaunchKernelGGL(sc_move_kernel<kMixWide>, blocks, threads, 0, stream, rows, tile_row, geo, n_tiles);
+            hipLaunchKernelGGL(sc_move_kernel<kMixWide>, blocks, threads, 0, stream, rows, tile_row, geo, n_tiles, gate);
             break;
         case kMixQuant:
-            hipLaunchKernelGGL(sc_move_kernel<kMixQuant>, blocks, threads, 0, stream, rows, tile_row, geo, n_tiles);
+            hipLaunchKernelGGL(sc_move_kernel<kMixQuant>, blocks, threads, 0, stream, rows, tile_row, geo, n_tiles, gate);
             break;
         default:
-            hipLaunchKernelGGL(sc_move_kernel<kMixAll>, blocks, threads, 0, stream, rows, tile_row, geo, n_tiles);
+            hipLaunchKernelGGL(sc_move_kernel<kMixAll>, blocks, threads, 0, stream, rows, tile_row, geo, n_tiles, gate);
             break;
     }
     return hipGetLastError();

@@ -440,16 +440,15 @@ bool WireDeviceDecoder::open(const void* payload, uint64_t bytes, const sc_geome
 
 bool WireDeviceDecoder::restore(void* stream, SavedConversation& image, std::string& error) {
     if (!scatter_) return refuse(error, "restore before a successful open");
-    if (expect_.check_payload_hash) {
-        if (!abi(sc_fnv1a64_async(payload_, info_.bytes, kWireHashSeed, hash_dev_, hash_ws_, hash_ws_bytes_, stream), error,
-                 "payload hash") ||
-            !abi(sc_copy_async(hash_host_, hash_dev_, 8, stream), error, "hash readback") ||
-            !abi(sc_stream_sync(stream), error, "payload hash"))
-            return false;
-        if (*hash_host_ != expect_.payload_hash)
-            return refuse(error, "payload hash mismatch on the device (the bytes are not the bytes that were written)");
-        info_.payload_hash = *hash_host_;
-    }
+    // The payload hash is checked on the device: the hash's last kernel compares it with the expected one and leaves a
+    // verdict word that gates the scatter, so a mismatch writes nothing and there is no host round trip before the
+    // scatter; the host reads the hash back with the other small blobs, once, at the end.
+    uint32_t* verdict = reinterpret_cast<uint32_t*>(hash_dev_ + 1);
+    if (expect_.check_payload_hash &&
+        !abi(sc_fnv1a64_check_async(payload_, info_.bytes, kWireHashSeed, expect_.payload_hash, hash_dev_, verdict,
+                                    hash_ws_, hash_ws_bytes_, stream),
+             error, "payload hash"))
+        return false;
     SavedConversation out = head_image_;
     // the same blobs inside the copy: re-point the downloads by position
     auto remap = [&](void* who) -> void* {
@@ -477,7 +476,11 @@ bool WireDeviceDecoder::restore(void* stream, SavedConversation& image, std::str
         }
         return nullptr;
     };
-    if (!abi(sc_plan_launch(scatter_, stream), error, "pool scatter")) return false;
+    if (expect_.check_payload_hash ? !abi(sc_plan_launch_gated(scatter_, verdict, stream), error, "pool scatter")
+                                   : !abi(sc_plan_launch(scatter_, stream), error, "pool scatter"))
+        return false;
+    if (expect_.check_payload_hash && !abi(sc_copy_async(hash_host_, hash_dev_, 8, stream), error, "hash readback"))
+        return false;
     for (const Download& d : downloads_) {
         void* target = remap(d.who);
         if (!target) return refuse(error, "internal: a host blob lost its place");
@@ -496,6 +499,11 @@ bool WireDeviceDecoder::restore(void* stream, SavedConversation& image, std::str
         }
     }
     if (!abi(sc_stream_sync(stream), error, "restore")) return false;
+    if (expect_.check_payload_hash) {
+        if (*hash_host_ != expect_.payload_hash)   // the gated scatter wrote nothing
+            return refuse(error, "payload hash mismatch on the device (the bytes are not the bytes that were written)");
+        info_.payload_hash = *hash_host_;
+    }
     image = std::move(out);
     return true;
 }

@@ -137,6 +137,7 @@ _SIGS = {
     "sc_plan_scatter": (C.c_int, [_GEO, _P, _U64, _I64, C.POINTER(DecodeSlot), C.POINTER(_P)]),
     "sc_plan_capture": (C.c_int, [_GEO, C.POINTER(DecodeSlot), _I64, _P, _U64, C.POINTER(_P)]),
     "sc_plan_launch": (C.c_int, [_P, _P]),
+    "sc_plan_launch_gated": (C.c_int, [_P, _P, _P]),
     "sc_batch_staging_layout": (C.c_int, [_GEO, C.POINTER(_I64), C.c_int32, C.POINTER(_U64), C.POINTER(_U64)]),
     "sc_plan_resume_append": (C.c_int, [_GEO, C.POINTER(BatchDesc), C.POINTER(_P)]),
     "sc_plan_payload_bytes": (_U64, [_P]),
@@ -192,6 +193,7 @@ _SIGS = {
     "sc_fnv1a64_workspace_bytes": (_U64, [_U64]),
     "sc_fnv1a64_async": (C.c_int, [_P, _U64, _U64, _P, _P, _U64, _P]),
     "sc_fnv1a64_chain_async": (C.c_int, [_P, _U64, _P, _P, _U64, _P]),
+    "sc_fnv1a64_check_async": (C.c_int, [_P, _U64, _U64, _U64, _P, _P, _P, _U64, _P]),
     "sc_fnv1a64_device": (C.c_int, [_P, _U64, _U64, C.POINTER(_U64)]),
     "sc_fnv1a64_noalloc_async": (C.c_int, [_P, _U64, _U64, _P, _P]),
     "sc_copy_device_async": (C.c_int, [_P, _P, _U64, _P]),

@@ -129,3 +129,37 @@ def test_full_payload_size(sc, oracle, cuda):
     assert sc.fnv1a64_device(buf.ptr, n) == want
     host.free()
     buf.free()
+
+
+def test_gated_scatter_writes_all_or_nothing(sc, oracle, cuda):
+    """sc_fnv1a64_check_async leaves a verdict on the device and sc_plan_launch_gated scatters only when it is 1: a
+    wrong expected hash leaves the slot untouched, the right one mounts it, with no host round trip in between."""
+    geo = sc.geometry(n_layers=8, qsa_interval=4, n_head_kv=2, head_dim=256, page_size=4, ssm_state_size=32,
+                      ssm_k_heads=4, ssm_v_heads=8, ssm_d_conv=4, ssm_conv_channels=520)
+    tokens = 53
+    case = sc.SyntheticCase(geo, tokens=tokens, seed=99)
+    _, total = sc.image_layout(geo, tokens)
+    image = sc.DeviceBuffer(total, "uint8")
+    gather = sc.plan_gather(geo, case.prefill, image.ptr, total)
+    gather.launch()
+    sc.device_sync()
+    want = oracle.fnv1a64(image.numpy(total))
+    slot = case.new_slot(max_cells=64, fill=0x5C)
+    scatter = sc.plan_scatter(geo, image.ptr, total, tokens, slot)
+    hp = sc.HashPlan(total)
+    verdict = sc.DeviceBuffer(1, "uint32")
+    for expected, mounted in ((want ^ 1, False), (want, True)):
+        verdict.fill(0xAB)
+        sc.device_sync()
+        sc.check(sc.lib.sc_fnv1a64_check_async(image.ptr, total, sc.REFERENCE_FNV_SEED, expected, hp.out.ptr,
+                                               verdict.ptr, hp.ws.ptr, hp.ws_bytes, None), "check")
+        sc.check(sc.lib.sc_plan_launch_gated(scatter.handle, verdict.ptr, None), "gated launch")
+        sc.device_sync()
+        assert hp.result() == want
+        assert int(verdict.numpy()[0]) == int(mounted)
+        state = slot.host_state()
+        if mounted:
+            assert np.array_equal(oracle.park(geo, tokens, state), image.numpy(total))
+        else:
+            assert all(np.all(v.view(np.uint8) == 0x5C) for v in state.values())
+    hp.free()
