@@ -41,6 +41,17 @@ typedef struct sc_wire_live {
     uint64_t small_bytes[4];
 } sc_wire_live;
 
+/* One later stage of a layer split (ConversationStageSnapshot, include/strata/core/conversation_cache.hpp): its own f16
+ * decode slot, laid out by its own geometry (the QSA layers and GDN rows the stage owns; identity page tables), its
+ * layer range, and - when encoding - its running state's small host buffers (the part's ids are the live ids). */
+typedef struct sc_wire_stage {
+    sc_geometry geometry;
+    sc_decode_slot slot;
+    int64_t layer_lo, layer_hi;
+    const uint8_t* small[4];       /* ple, tails, dead, block_pos (host bytes, may be NULL when empty; encode only) */
+    uint64_t small_bytes[4];
+} sc_wire_stage;
+
 typedef struct sc_wire_encoder sc_wire_encoder;
 typedef struct sc_wire_decoder sc_wire_decoder;
 
@@ -51,6 +62,12 @@ const char* sc_wire_last_error(void);
  * GDN rows.  Replaces conversation_wire_plan (src/core/conversation_wire.cpp:988-1004) for slot-resident state. */
 int sc_wire_encoder_create(const sc_geometry* g, const sc_decode_slot* slot, int64_t tokens, const sc_wire_live* live,
                            uint64_t geom_hash, uint64_t pack_hash, sc_wire_encoder** out);
+/* The same with a layer split (the reference's conversation_snapshot_save, src/core/conversation_state.cpp:397-413):
+ * `slot` holds the main session's layers, each of `stages` a later stage's, and the payload carries one stage part
+ * per stage, in order, its K/V records and GDN rows gathered from the stage's slot by a launch of its own. */
+int sc_wire_encoder_create_split(const sc_geometry* g, const sc_decode_slot* slot, int64_t tokens,
+                                 const sc_wire_live* live, const sc_wire_stage* stages, int32_t n_stages,
+                                 uint64_t geom_hash, uint64_t pack_hash, sc_wire_encoder** out);
 /* The same for a slot in any K/V format (sc_slot_layers, include/sc_handoff.h): its layers become K/V records of
  * slot->format carrying data, int8 scales and, with slot->with_index, the indexer's pooled rows, all gathered from the
  * slot's identity pools by one launch (conversation_kv_save's five buffers, src/core/conversation_snapshot.cpp:69-78). */
@@ -76,6 +93,14 @@ int sc_wire_encoder_destroy(sc_wire_encoder* e);
 int sc_wire_decoder_open(const void* payload, uint64_t bytes, const sc_geometry* g, const sc_decode_slot* slot,
                          const int64_t* geometry, uint64_t geom_hash, uint64_t pack_hash, int32_t check_identity,
                          uint64_t payload_hash, int32_t check_hash, sc_wire_decoder** out);
+/* The same for a layer-split payload (the reference's conversation_snapshot_restore of stage parts,
+ * src/core/conversation_state.cpp:497-509): exactly n_stages stage parts, each with its stage's layer range and the
+ * shape of its slot; the restore scatters every part into its stage's slot, gated by the same device hash check as the
+ * main slot (all or nothing). */
+int sc_wire_decoder_open_split(const void* payload, uint64_t bytes, const sc_geometry* g, const sc_decode_slot* slot,
+                               const sc_wire_stage* stages, int32_t n_stages, const int64_t* geometry,
+                               uint64_t geom_hash, uint64_t pack_hash, int32_t check_identity, uint64_t payload_hash,
+                               int32_t check_hash, sc_wire_decoder** out);
 /* The same for a slot in any K/V format: the first K/V records must be the slot's layers in slot->format, with the
  * indexer's rows exactly when slot->with_index. */
 int sc_wire_decoder_open_layers(const void* payload, uint64_t bytes, const sc_geometry* g, const sc_slot_layers* slot,
@@ -91,6 +116,9 @@ int sc_wire_decoder_restore(sc_wire_decoder* d, void* stream);
  * (which: 0 ple, 1 tails, 2 dead, 3 block_pos). */
 int sc_wire_decoder_live_ids(const sc_wire_decoder* d, int32_t* ids, int64_t cap, int64_t* n);
 int sc_wire_decoder_small(const sc_wire_decoder* d, int32_t which, uint8_t* dst, uint64_t cap, uint64_t* n);
+/* After a restore of a layer-split payload: stage part `stage`'s small buffers (which as above). */
+int sc_wire_decoder_stage_small(const sc_wire_decoder* d, int32_t stage, int32_t which, uint8_t* dst, uint64_t cap,
+                                uint64_t* n);
 int sc_wire_decoder_destroy(sc_wire_decoder* d);
 
 #ifdef __cplusplus

@@ -18,7 +18,10 @@
 // Scope: the slot's QSA layers carry f16 K/V without indexer rows (format 0), the first image K/V records are those
 // layers in order, and the live checkpoint's gdn blob is the slot's GDN rows.  Everything else of the image - the
 // records that follow (a draft layer), the live checkpoint's ids, keys and small buffers, retained checkpoints - is
-// host data carried as is.  A layer-split image (stage parts) is refused on the device path.
+// host data carried as is.  A layer-split image carries one stage part per later stage (the reference's
+// conversation_snapshot_save, src/core/conversation_state.cpp:397-413): given the stages' own slots, their K/V records
+// and GDN rows are gathered from and scattered into those slots by launches of their own, the rest of each part's
+// running state travels as host data (f16 slots).  Without stages, a layer-split payload is refused.
 #pragma once
 
 #include "strata/core/conversation_wire.hpp"
@@ -48,6 +51,17 @@ struct WireDeviceConversation {
     std::vector<ConversationKv> trailing_kv;   // host K/V records after the slot's layers (the draft layer)
 };
 
+/// One later stage of a layer split (ConversationStageSnapshot, include/strata/core/conversation_cache.hpp): its own
+/// decode slot, laid out by its own geometry (the QSA layers and GDN rows the stage owns), its layer range, and the host
+/// half of its running state: `state.ids` are the live ids, ple / tails / dead / block_pos host bytes, gdn empty (the
+/// slot's rows).  A decoder fills `state` of the stages it mounts into.
+struct WireDeviceStage {
+    sc_geometry geometry{};
+    sc_decode_slot slot{};
+    int64_t layer_lo = 0, layer_hi = 0;
+    ConversationCheckpoint state;
+};
+
 class WireDeviceEncoder {
 public:
     WireDeviceEncoder() = default;
@@ -58,6 +72,10 @@ public:
     /// Lays out the payload of `conv` carrying the slot's state for `tokens` tokens (== conv.live.ids.size()).
     bool plan(const sc_geometry& g, const sc_decode_slot& slot, int64_t tokens, const WireDeviceConversation& conv,
               const WireIdentity& identity, std::string& error);
+    /// The same with a layer split: `slot` holds the main session's layers and each of `stages` a later stage's; the
+    /// payload carries one stage part per stage, in order.
+    bool plan(const sc_geometry& g, const sc_decode_slot& slot, int64_t tokens, const WireDeviceConversation& conv,
+              const std::vector<WireDeviceStage>& stages, const WireIdentity& identity, std::string& error);
     /// The same for a slot in any K/V format (sc_slot_layers: int8, q4_0, K8V4 or f16, with the indexer's pooled rows
     /// when slot.with_index): its layers become K/V records of slot.format whose data, scale and pooled-row blobs are
     /// gathered from the slot's identity pools.
@@ -80,6 +98,16 @@ private:
 
     sc_geometry g_{};
     sc_decode_slot slot_{};
+    // a later stage's slot (own copies of its pointer arrays) and where its blobs sit in the payload
+    struct StagePlan {
+        sc_geometry g{};
+        sc_decode_slot slot{};
+        std::vector<uint16_t*> k, v;
+        std::vector<uint64_t> k_off, v_off;
+        uint64_t gdn_off = 0;
+        sc_plan* plan = nullptr;
+    };
+    std::vector<StagePlan> stage_plans_;
     bool layered_ = false;                             // an sc_slot_layers slot (lay_off_) rather than f16 pools
     sc_slot_layers layers_{};
     std::array<std::vector<void*>, SC_N_BUF> layer_bufs_;
@@ -113,6 +141,11 @@ public:
     /// scatter.  Nothing is written anywhere.
     bool open(const void* payload, uint64_t bytes, const sc_geometry& g, const sc_decode_slot& slot,
               const WireExpect& expect, std::string& error);
+    /// The same for a layer-split payload: `slot` takes the main session's layers and each stage's slot its stage
+    /// part (layer ranges and shapes must match, in order).  After restore, the parts' host halves are in the returned
+    /// image's stage_parts.
+    bool open(const void* payload, uint64_t bytes, const sc_geometry& g, const sc_decode_slot& slot,
+              const std::vector<WireDeviceStage>& stages, const WireExpect& expect, std::string& error);
     /// The same for a slot in any K/V format: the first K/V records must be the slot's layers in its format, with the
     /// indexer's rows exactly when slot.with_index.
     bool open(const void* payload, uint64_t bytes, const sc_geometry& g, const sc_slot_layers& slot,
@@ -141,6 +174,8 @@ private:
     struct Download { void* who; bool buffer; uint64_t offset, bytes; };
     std::vector<Download> downloads_;   // blobs that go back to the host image (by address inside head_image_)
     sc_plan* scatter_ = nullptr;
+    std::vector<sc_plan*> stage_scatters_;   // one per stage part, gated by the same hash verdict
+    bool split_ok_ = false;                  // open() was given the stages a split payload needs
     void* hash_ws_ = nullptr;
     uint64_t hash_ws_bytes_ = 0;
     uint64_t* hash_dev_ = nullptr;

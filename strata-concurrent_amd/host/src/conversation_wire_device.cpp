@@ -56,7 +56,57 @@ bool stage_host_blob(const SavedConversation& img, const void* who, uint8_t* dst
     if (stage_checkpoint_blob(img.live, who, dst, n)) return true;
     for (const ConversationCheckpoint& c : img.checkpoints)
         if (stage_checkpoint_blob(c, who, dst, n)) return true;
+    for (const ConversationStageSnapshot& part : img.stage_parts)
+        if (stage_checkpoint_blob(part.state, who, dst, n)) return true;
     return false;
+}
+
+const detail::WireBlobAt* find(const std::vector<detail::WireBlobAt>& pool, const void* who);
+
+// The K/V records of a slot's f16 layers for `tokens` tokens, sized (not held), appended to `sizes` and `device`.
+void size_f16_records(std::vector<ConversationKv>& kv, const sc_geometry& g, const SlotShape& s, int64_t idx_dim,
+                      detail::WireSizes& sizes, std::vector<const void*>& device) {
+    for (int64_t j = 0; j < s.n_qsa; ++j) {
+        ConversationKv& k = kv[size_t(j)];
+        k.format = 0;
+        k.cells = s.cells;
+        k.heads = g.n_head_kv;
+        k.head_dim = g.head_dim;
+        k.page_size = g.page_size;
+        k.pooled_rows = 0;
+        k.idx_dim = idx_dim;
+        sizes.push_back({&k.k, s.kv_bytes});
+        sizes.push_back({&k.v, s.kv_bytes});
+        if (s.kv_bytes) { device.push_back(&k.k); device.push_back(&k.v); }
+    }
+}
+
+// Checks that the first s.n_qsa records of `kv` are a slot's f16 layers for `tokens` tokens, carried as whole K and V
+// blobs, and notes where those blobs sit.
+bool f16_records(const std::vector<ConversationKv>& kv, const sc_geometry& g, const SlotShape& s, int64_t tokens,
+                 const std::vector<detail::WireBlobAt>& blobs, const std::string& whose, std::vector<uint64_t>& k_off,
+                 std::vector<uint64_t>& v_off, std::vector<const void*>& device, std::string& error) {
+    if (int64_t(kv.size()) < s.n_qsa) return refuse(error, whose + " carries fewer K/V records than its slot has layers");
+    k_off.assign(size_t(s.n_qsa), 0);
+    v_off.assign(size_t(s.n_qsa), 0);
+    for (int64_t j = 0; j < s.n_qsa; ++j) {
+        const ConversationKv& k = kv[size_t(j)];
+        const std::string rec = whose + " K/V record " + std::to_string(j);
+        if (k.format != 0 || k.cells != s.cells || k.heads != g.n_head_kv || k.head_dim != g.head_dim ||
+            k.page_size != g.page_size || k.pooled_rows != 0)
+            return refuse(error, rec + " is not the slot's f16 layer of " + std::to_string(tokens) + " tokens");
+        const detail::WireBlobAt* kb = find(blobs, &k.k);
+        const detail::WireBlobAt* vb = find(blobs, &k.v);
+        if (s.kv_bytes && (!kb || !vb || kb->bytes != s.kv_bytes || vb->bytes != s.kv_bytes))
+            return refuse(error, rec + " does not carry whole K and V blobs");
+        if (find(blobs, &k.k_scale) || find(blobs, &k.v_scale) || find(blobs, &k.pooled))
+            return refuse(error, rec + " carries scales or indexer rows");
+        k_off[size_t(j)] = kb ? kb->offset : 0;
+        v_off[size_t(j)] = vb ? vb->offset : 0;
+        device.push_back(&k.k);
+        device.push_back(&k.v);
+    }
+    return true;
 }
 
 const detail::WireBlobAt* find(const std::vector<detail::WireBlobAt>& pool, const void* who) {
@@ -72,6 +122,9 @@ const detail::WireBlobAt* find(const std::vector<detail::WireBlobAt>& pool, cons
 WireDeviceEncoder::~WireDeviceEncoder() { release(); }
 
 void WireDeviceEncoder::release() {
+    for (StagePlan& sp : stage_plans_)
+        if (sp.plan) sc_plan_destroy(sp.plan);
+    stage_plans_.clear();
     if (capture_) sc_plan_destroy(capture_);
     if (staged_) sc_host_free(staged_);
     if (hash_host_) sc_host_free(hash_host_);
@@ -146,6 +199,12 @@ bool WireDeviceEncoder::stage(const SavedConversation& img, const std::vector<st
 
 bool WireDeviceEncoder::plan(const sc_geometry& g, const sc_decode_slot& slot, int64_t tokens,
                              const WireDeviceConversation& conv, const WireIdentity& identity, std::string& error) {
+    return plan(g, slot, tokens, conv, {}, identity, error);
+}
+
+bool WireDeviceEncoder::plan(const sc_geometry& g, const sc_decode_slot& slot, int64_t tokens,
+                             const WireDeviceConversation& conv, const std::vector<WireDeviceStage>& stages,
+                             const WireIdentity& identity, std::string& error) {
     release();
     plan_ = WirePlan{};
     SlotShape s;
@@ -155,22 +214,31 @@ bool WireDeviceEncoder::plan(const sc_geometry& g, const sc_decode_slot& slot, i
     slot_image(conv, s.n_qsa, img);
     detail::WireSizes sizes;
     std::vector<const void*> device;
-    for (int64_t j = 0; j < s.n_qsa; ++j) {
-        ConversationKv& k = img.kv[size_t(j)];
-        k.format = 0;
-        k.cells = s.cells;
-        k.heads = g.n_head_kv;
-        k.head_dim = g.head_dim;
-        k.page_size = g.page_size;
-        k.pooled_rows = 0;
-        k.idx_dim = conv.idx_dim;
-        sizes.push_back({&k.k, s.kv_bytes});
-        sizes.push_back({&k.v, s.kv_bytes});
-        if (s.kv_bytes) { device.push_back(&k.k); device.push_back(&k.v); }
-    }
+    size_f16_records(img.kv, g, s, conv.idx_dim, sizes, device);
     if (s.n_gdn > 0) {
         sizes.push_back({&img.live.gdn, s.gdn_bytes});
         device.push_back(&img.live.gdn);
+    }
+    // each later stage: a part whose K/V records and GDN rows are its own slot's, the rest its host running state
+    std::vector<SlotShape> stage_shapes(stages.size());
+    img.stage_parts.resize(stages.size());
+    for (size_t i = 0; i < stages.size(); ++i) {
+        const WireDeviceStage& st = stages[i];
+        SlotShape& ss = stage_shapes[i];
+        if (!slot_shape(st.geometry, tokens, ss, error)) return false;
+        if (st.state.ids != conv.live.ids) return refuse(error, "a stage part's ids are not the live ids");
+        if (!st.state.gdn.empty() || !st.state.imgs.empty() || !st.state.stage_parts.empty())
+            return refuse(error, "a stage part's state carries only its small host buffers (its GDN rows are the slot's)");
+        ConversationStageSnapshot& part = img.stage_parts[i];
+        part.layer_lo = st.layer_lo;
+        part.layer_hi = st.layer_hi;
+        part.state = st.state;
+        part.kv.resize(size_t(ss.n_qsa));
+        size_f16_records(part.kv, st.geometry, ss, conv.idx_dim, sizes, device);
+        if (ss.n_gdn > 0) {
+            sizes.push_back({&part.state.gdn, ss.gdn_bytes});
+            device.push_back(&part.state.gdn);
+        }
     }
     std::vector<detail::WireBlobAt> pool;
     if (!stage(img, sizes, device, identity, pool, error)) { release(); return false; }
@@ -181,6 +249,32 @@ bool WireDeviceEncoder::plan(const sc_geometry& g, const sc_decode_slot& slot, i
         v_off_[size_t(j)] = find(pool, &img.kv[size_t(j)].v)->offset;
     }
     gdn_off_ = s.n_gdn > 0 ? find(pool, &img.live.gdn)->offset : 0;
+    stage_plans_.resize(stages.size());
+    for (size_t i = 0; i < stages.size(); ++i) {
+        const WireDeviceStage& st = stages[i];
+        const SlotShape& ss = stage_shapes[i];
+        const ConversationStageSnapshot& part = img.stage_parts[i];
+        StagePlan& sp = stage_plans_[i];
+        sp.g = st.geometry;
+        sp.slot = st.slot;
+        // own copies of the stage slot's pointer arrays: the caller's may not outlive the encoder
+        sp.k.assign(st.slot.k_pool ? st.slot.k_pool : nullptr, st.slot.k_pool ? st.slot.k_pool + ss.n_qsa : nullptr);
+        sp.v.assign(st.slot.v_pool ? st.slot.v_pool : nullptr, st.slot.v_pool ? st.slot.v_pool + ss.n_qsa : nullptr);
+        sp.slot.k_pool = st.slot.k_pool ? sp.k.data() : nullptr;
+        sp.slot.v_pool = st.slot.v_pool ? sp.v.data() : nullptr;
+        sp.slot.page_table = nullptr;
+        if (st.slot.page_table)
+            for (int64_t j = 0; j < ss.n_qsa; ++j)
+                if (st.slot.page_table[j]) return refuse(error, "a stage slot must use identity page tables");
+        sp.slot.host = sp.slot.stage = nullptr;
+        sp.k_off.assign(size_t(ss.n_qsa), 0);
+        sp.v_off.assign(size_t(ss.n_qsa), 0);
+        for (int64_t j = 0; j < ss.n_qsa && ss.kv_bytes; ++j) {
+            sp.k_off[size_t(j)] = find(pool, &part.kv[size_t(j)].k)->offset;
+            sp.v_off[size_t(j)] = find(pool, &part.kv[size_t(j)].v)->offset;
+        }
+        sp.gdn_off = ss.n_gdn > 0 ? find(pool, &part.state.gdn)->offset : 0;
+    }
     layered_ = false;
     g_ = g;
     slot_ = slot;
@@ -264,12 +358,25 @@ bool WireDeviceEncoder::encode(void* payload, uint64_t capacity, void* stream, s
             rc = sc_plan_capture_map(&g_, &slot_, tokens_, payload, capacity, &map, &capture_);
         }
         if (!abi(rc, error, "capture plan")) return false;
+        for (StagePlan& sp : stage_plans_) {   // every gap of the pool is cleared by the main plan's zero ranges
+            if (sp.plan) sc_plan_destroy(sp.plan);
+            sp.plan = nullptr;
+            sc_blob_map map{};
+            map.k_off = sp.k_off.data();
+            map.v_off = sp.v_off.data();
+            map.gdn_off = sp.gdn_off;
+            if (!abi(sc_plan_capture_map(&sp.g, &sp.slot, tokens_, payload, capacity, &map, &sp.plan), error,
+                     "stage capture plan"))
+                return false;
+        }
         capture_target_ = payload;
     }
     uint8_t* p = static_cast<uint8_t*>(payload);
     for (const Upload& u : uploads_)
         if (!abi(sc_copy_async(p + u.offset, staged_ + u.staged_at, u.bytes, stream), error, "head copy")) return false;
     if (!abi(sc_plan_launch(capture_, stream), error, "pool gather")) return false;
+    for (const StagePlan& sp : stage_plans_)
+        if (!abi(sc_plan_launch(sp.plan, stream), error, "stage gather")) return false;
     if (gathered && !abi(sc_event_record(gathered, stream), error, "gather event")) return false;
     if (!abi(sc_fnv1a64_async(payload, plan_.total_bytes, kWireHashSeed, hash_dev_, hash_ws_, hash_ws_bytes_, stream),
              error, "payload hash"))
@@ -291,6 +398,9 @@ bool WireDeviceEncoder::payload_hash(uint64_t& hash, std::string& error) {
 WireDeviceDecoder::~WireDeviceDecoder() { release(); }
 
 void WireDeviceDecoder::release() {
+    for (sc_plan* p : stage_scatters_)
+        if (p) sc_plan_destroy(p);
+    stage_scatters_.clear();
     if (scatter_) sc_plan_destroy(scatter_);
     if (hash_ws_) sc_device_free(hash_ws_);
     if (hash_dev_) sc_device_free(hash_dev_);
@@ -325,7 +435,6 @@ bool WireDeviceDecoder::read_head(const void* payload, uint64_t bytes, const Wir
     if (!bounded.max_payload_bytes || bounded.max_payload_bytes > bytes) bounded.max_payload_bytes = bytes;
     head_image_ = SavedConversation{};
     if (!detail::wire_locate(head.data(), head.size(), head_image_, info_, bounded, blobs, error)) return false;
-    if (info_.n_stage_parts) return refuse(error, "a layer-split image cannot be mounted on the device path");
     tokens_ = info_.live_tokens;
     return true;
 }
@@ -355,35 +464,50 @@ bool WireDeviceDecoder::finish_open(const void* payload, uint64_t bytes, const W
 
 bool WireDeviceDecoder::open(const void* payload, uint64_t bytes, const sc_geometry& g, const sc_decode_slot& slot,
                              const WireExpect& expect, std::string& error) {
+    return open(payload, bytes, g, slot, {}, expect, error);
+}
+
+bool WireDeviceDecoder::open(const void* payload, uint64_t bytes, const sc_geometry& g, const sc_decode_slot& slot,
+                             const std::vector<WireDeviceStage>& stages, const WireExpect& expect, std::string& error) {
     std::vector<detail::WireBlobAt> blobs;
     if (!read_head(payload, bytes, expect, blobs, error)) return false;
+    if (info_.n_stage_parts != int64_t(stages.size()))
+        return refuse(error, stages.empty() ? "a layer-split image cannot be mounted on the device path without its "
+                                              "stages' slots"
+                                            : "the payload carries " + std::to_string(info_.n_stage_parts) +
+                                                  " stage parts and " + std::to_string(stages.size()) +
+                                                  " stage slots were given");
     SlotShape s;
     if (!slot_shape(g, tokens_, s, error)) return false;
-    if (int64_t(head_image_.kv.size()) < s.n_qsa)
-        return refuse(error, "the payload carries fewer K/V records than the slot has layers");
-    std::vector<uint64_t> k_off(size_t(s.n_qsa)), v_off(size_t(s.n_qsa));
+    std::vector<uint64_t> k_off, v_off;
     std::vector<const void*> device;
-    for (int64_t j = 0; j < s.n_qsa; ++j) {
-        const ConversationKv& k = head_image_.kv[size_t(j)];
-        if (k.format != 0 || k.cells != s.cells || k.heads != g.n_head_kv || k.head_dim != g.head_dim ||
-            k.page_size != g.page_size || k.pooled_rows != 0)
-            return refuse(error, "K/V record " + std::to_string(j) + " is not the slot's f16 layer of " +
-                                     std::to_string(tokens_) + " tokens");
-        const detail::WireBlobAt* kb = find(blobs, &k.k);
-        const detail::WireBlobAt* vb = find(blobs, &k.v);
-        if (s.kv_bytes && (!kb || !vb || kb->bytes != s.kv_bytes || vb->bytes != s.kv_bytes))
-            return refuse(error, "K/V record " + std::to_string(j) + " does not carry whole K and V blobs");
-        if (find(blobs, &k.k_scale) || find(blobs, &k.v_scale) || find(blobs, &k.pooled))
-            return refuse(error, "K/V record " + std::to_string(j) + " carries scales or indexer rows");
-        k_off[size_t(j)] = kb ? kb->offset : 0;
-        v_off[size_t(j)] = vb ? vb->offset : 0;
-        device.push_back(&k.k);
-        device.push_back(&k.v);
-    }
+    if (!f16_records(head_image_.kv, g, s, tokens_, blobs, "the payload", k_off, v_off, device, error)) return false;
     const detail::WireBlobAt* gb = find(blobs, &head_image_.live.gdn);
     if (s.n_gdn > 0 && (!gb || gb->bytes != s.gdn_bytes))
         return refuse(error, "the live checkpoint does not carry the slot's GDN rows");
     device.push_back(&head_image_.live.gdn);
+    // every stage part against its slot, checked before any plan is built
+    struct Part { SlotShape shape; std::vector<uint64_t> k_off, v_off; uint64_t gdn_off; };
+    std::vector<Part> parts(stages.size());
+    for (size_t i = 0; i < stages.size(); ++i) {
+        const WireDeviceStage& st = stages[i];
+        const ConversationStageSnapshot& part = head_image_.stage_parts[i];
+        const std::string whose = "stage part " + std::to_string(i);
+        if (part.layer_lo != st.layer_lo || part.layer_hi != st.layer_hi)
+            return refuse(error, whose + " covers layers [" + std::to_string(part.layer_lo) + ", " +
+                                     std::to_string(part.layer_hi) + "), not its slot's");
+        if (!slot_shape(st.geometry, tokens_, parts[i].shape, error)) return false;
+        if (int64_t(part.kv.size()) != parts[i].shape.n_qsa)
+            return refuse(error, whose + " does not carry one K/V record per layer of its slot");
+        if (!f16_records(part.kv, st.geometry, parts[i].shape, tokens_, blobs, whose, parts[i].k_off, parts[i].v_off,
+                         device, error))
+            return false;
+        const detail::WireBlobAt* sg = find(blobs, &part.state.gdn);
+        if (parts[i].shape.n_gdn > 0 && (!sg || sg->bytes != parts[i].shape.gdn_bytes))
+            return refuse(error, whose + " does not carry its slot's GDN rows");
+        parts[i].gdn_off = sg ? sg->offset : 0;
+        device.push_back(&part.state.gdn);
+    }
     sc_blob_map map{};
     map.k_off = k_off.data();
     map.v_off = v_off.data();
@@ -392,6 +516,19 @@ bool WireDeviceDecoder::open(const void* payload, uint64_t bytes, const sc_geome
         release();
         return false;
     }
+    stage_scatters_.assign(stages.size(), nullptr);
+    for (size_t i = 0; i < stages.size(); ++i) {
+        sc_blob_map pm{};
+        pm.k_off = parts[i].k_off.data();
+        pm.v_off = parts[i].v_off.data();
+        pm.gdn_off = parts[i].gdn_off;
+        if (!abi(sc_plan_scatter_map(&stages[i].geometry, payload, bytes, &pm, tokens_, &stages[i].slot,
+                                     &stage_scatters_[i]),
+                 error, "stage scatter plan")) {
+            release();
+            return false;
+        }
+    }
     return finish_open(payload, bytes, expect, blobs, device, error);
 }
 
@@ -399,6 +536,7 @@ bool WireDeviceDecoder::open(const void* payload, uint64_t bytes, const sc_geome
                              const WireExpect& expect, std::string& error) {
     std::vector<detail::WireBlobAt> blobs;
     if (!read_head(payload, bytes, expect, blobs, error)) return false;
+    if (info_.n_stage_parts) return refuse(error, "a layer-split image cannot be mounted into a single layered slot");
     SlotShape s;
     if (!slot_shape(g, tokens_, s, error)) return false;
     uint64_t b[SC_N_BUF];
@@ -464,6 +602,8 @@ bool WireDeviceDecoder::restore(void* stream, SavedConversation& image, std::str
         std::vector<std::pair<ConversationCheckpoint*, ConversationCheckpoint*>> cps{{&head_image_.live, &out.live}};
         for (size_t i = 0; i < head_image_.checkpoints.size(); ++i)
             cps.push_back({&head_image_.checkpoints[i], &out.checkpoints[i]});
+        for (size_t i = 0; i < head_image_.stage_parts.size(); ++i)
+            cps.push_back({&head_image_.stage_parts[i].state, &out.stage_parts[i].state});
         for (size_t i = 0; i < cps.size(); ++i)
             for (size_t k = 0; k < cps[i].first->stage_parts.size(); ++k)
                 cps.push_back({&cps[i].first->stage_parts[k], &cps[i].second->stage_parts[k]});
@@ -476,6 +616,11 @@ bool WireDeviceDecoder::restore(void* stream, SavedConversation& image, std::str
         }
         return nullptr;
     };
+    for (sc_plan* p : stage_scatters_) {   // the stages' parts share the main scatter's verdict: all or nothing
+        if (expect_.check_payload_hash ? !abi(sc_plan_launch_gated(p, verdict, stream), error, "stage scatter")
+                                       : !abi(sc_plan_launch(p, stream), error, "stage scatter"))
+            return false;
+    }
     if (expect_.check_payload_hash ? !abi(sc_plan_launch_gated(scatter_, verdict, stream), error, "pool scatter")
                                    : !abi(sc_plan_launch(scatter_, stream), error, "pool scatter"))
         return false;

@@ -6,6 +6,7 @@
 #include <exception>
 #include <new>
 #include <string>
+#include <type_traits>
 
 using namespace strata::core;
 
@@ -48,32 +49,73 @@ extern "C" {
 const char* sc_wire_last_error(void) { return g_error.c_str(); }
 
 extern "C++" {
+// The host side of a conversation from its C description; SC_OK or the refusal.
+static int conversation_of(const sc_wire_live* live, WireDeviceConversation& conv) {
+    if (live->n_ids < 0 || live->n_imgs < 0 || (live->n_ids && !live->ids) ||
+        (live->n_imgs && (!live->img_start || !live->img_hash)))
+        return failed(SC_EINVAL, "conversation wire: invalid live checkpoint arrays");
+    for (int i = 0; i < 18; ++i) conv.geometry[size_t(i)] = live->geometry[i];
+    conv.layer_lo = live->layer_lo;
+    conv.layer_hi = live->layer_hi;
+    conv.cvec = live->cvec != 0;
+    conv.idx_dim = live->idx_dim;
+    conv.live.ids.assign(live->ids, live->ids + live->n_ids);
+    for (int64_t i = 0; i < live->n_imgs; ++i) conv.live.imgs.push_back({live->img_start[i], live->img_hash[i]});
+    conv.live.used = live->used;
+    std::vector<uint8_t>* small[4] = {&conv.live.ple, &conv.live.tails, &conv.live.dead, &conv.live.block_pos};
+    for (int i = 0; i < 4; ++i) {
+        if (live->small_bytes[i] && !live->small[i]) return failed(SC_EINVAL, "conversation wire: missing small buffer");
+        small[i]->assign(live->small[i], live->small[i] + live->small_bytes[i]);
+    }
+    if (live->draft_record) conv.trailing_kv.emplace_back();
+    return SC_OK;
+}
+
+// The stages of a layer split from their C description (the small buffers only when `with_state`).
+static int stages_of(const sc_wire_stage* stages, int32_t n, const std::vector<int32_t>& ids, bool with_state,
+                     std::vector<WireDeviceStage>& out) {
+    if (n < 0 || (n && !stages)) return failed(SC_EINVAL, "conversation wire: invalid stage array");
+    out.resize(size_t(n));
+    for (int32_t i = 0; i < n; ++i) {
+        const sc_wire_stage& in = stages[i];
+        WireDeviceStage& st = out[size_t(i)];
+        st.geometry = in.geometry;
+        st.slot = in.slot;
+        st.layer_lo = in.layer_lo;
+        st.layer_hi = in.layer_hi;
+        if (!with_state) continue;
+        st.state.ids = ids;
+        std::vector<uint8_t>* small[4] = {&st.state.ple, &st.state.tails, &st.state.dead, &st.state.block_pos};
+        for (int k = 0; k < 4; ++k) {
+            if (in.small_bytes[k] && !in.small[k]) return failed(SC_EINVAL, "conversation wire: missing stage buffer");
+            small[k]->assign(in.small[k], in.small[k] + in.small_bytes[k]);
+        }
+    }
+    return SC_OK;
+}
+
 template <class Slot>
 static int encoder_create(const sc_geometry* g, const Slot* slot, int64_t tokens, const sc_wire_live* live,
-                          uint64_t geom_hash, uint64_t pack_hash, sc_wire_encoder** out) {
+                          const sc_wire_stage* stages, int32_t n_stages, uint64_t geom_hash, uint64_t pack_hash,
+                          sc_wire_encoder** out) {
     return guarded([&] {
         if (!g || !slot || !live || !out) return failed(SC_EINVAL, "conversation wire: missing argument");
-        if (live->n_ids < 0 || live->n_imgs < 0 || (live->n_ids && !live->ids) ||
-            (live->n_imgs && (!live->img_start || !live->img_hash)))
-            return failed(SC_EINVAL, "conversation wire: invalid live checkpoint arrays");
         WireDeviceConversation conv;
-        for (int i = 0; i < 18; ++i) conv.geometry[size_t(i)] = live->geometry[i];
-        conv.layer_lo = live->layer_lo;
-        conv.layer_hi = live->layer_hi;
-        conv.cvec = live->cvec != 0;
-        conv.idx_dim = live->idx_dim;
-        conv.live.ids.assign(live->ids, live->ids + live->n_ids);
-        for (int64_t i = 0; i < live->n_imgs; ++i) conv.live.imgs.push_back({live->img_start[i], live->img_hash[i]});
-        conv.live.used = live->used;
-        std::vector<uint8_t>* small[4] = {&conv.live.ple, &conv.live.tails, &conv.live.dead, &conv.live.block_pos};
-        for (int i = 0; i < 4; ++i) {
-            if (live->small_bytes[i] && !live->small[i]) return failed(SC_EINVAL, "conversation wire: missing small buffer");
-            small[i]->assign(live->small[i], live->small[i] + live->small_bytes[i]);
-        }
-        if (live->draft_record) conv.trailing_kv.emplace_back();
+        if (const int rc = conversation_of(live, conv)) return rc;
         auto* e = new sc_wire_encoder();
         std::string err;
-        if (!e->enc.plan(*g, *slot, tokens, conv, WireIdentity{geom_hash, pack_hash}, err)) {
+        bool planned;
+        if constexpr (std::is_same_v<Slot, sc_decode_slot>) {
+            std::vector<WireDeviceStage> parts;
+            if (const int rc = stages_of(stages, n_stages, conv.live.ids, true, parts)) {
+                delete e;
+                return rc;
+            }
+            planned = e->enc.plan(*g, *slot, tokens, conv, parts, WireIdentity{geom_hash, pack_hash}, err);
+        } else {
+            planned = e->enc.plan(*g, *slot, tokens, conv, WireIdentity{geom_hash, pack_hash}, err);
+        }
+        if (!planned) {
             delete e;
             return failed(SC_EINVAL, err);
         }
@@ -85,13 +127,19 @@ static int encoder_create(const sc_geometry* g, const Slot* slot, int64_t tokens
 
 int sc_wire_encoder_create(const sc_geometry* g, const sc_decode_slot* slot, int64_t tokens, const sc_wire_live* live,
                            uint64_t geom_hash, uint64_t pack_hash, sc_wire_encoder** out) {
-    return encoder_create(g, slot, tokens, live, geom_hash, pack_hash, out);
+    return encoder_create(g, slot, tokens, live, nullptr, 0, geom_hash, pack_hash, out);
+}
+
+int sc_wire_encoder_create_split(const sc_geometry* g, const sc_decode_slot* slot, int64_t tokens,
+                                 const sc_wire_live* live, const sc_wire_stage* stages, int32_t n_stages,
+                                 uint64_t geom_hash, uint64_t pack_hash, sc_wire_encoder** out) {
+    return encoder_create(g, slot, tokens, live, stages, n_stages, geom_hash, pack_hash, out);
 }
 
 int sc_wire_encoder_create_layers(const sc_geometry* g, const sc_slot_layers* slot, int64_t tokens,
                                   const sc_wire_live* live, uint64_t geom_hash, uint64_t pack_hash,
                                   sc_wire_encoder** out) {
-    return encoder_create(g, slot, tokens, live, geom_hash, pack_hash, out);
+    return encoder_create(g, slot, tokens, live, nullptr, 0, geom_hash, pack_hash, out);
 }
 
 uint64_t sc_wire_encoder_bytes(const sc_wire_encoder* e) { return e ? e->enc.bytes() : 0; }
@@ -121,8 +169,9 @@ int sc_wire_encoder_destroy(sc_wire_encoder* e) {
 extern "C++" {
 template <class Slot>
 static int decoder_open(const void* payload, uint64_t bytes, const sc_geometry* g, const Slot* slot,
-                        const int64_t* geometry, uint64_t geom_hash, uint64_t pack_hash, int32_t check_identity,
-                        uint64_t payload_hash, int32_t check_hash, sc_wire_decoder** out) {
+                        const sc_wire_stage* stages, int32_t n_stages, const int64_t* geometry, uint64_t geom_hash,
+                        uint64_t pack_hash, int32_t check_identity, uint64_t payload_hash, int32_t check_hash,
+                        sc_wire_decoder** out) {
     return guarded([&] {
         if (!g || !slot || !out) return failed(SC_EINVAL, "conversation wire: missing argument");
         WireExpect expect;
@@ -135,10 +184,21 @@ static int decoder_open(const void* payload, uint64_t bytes, const sc_geometry* 
         expect.check_hashes = check_identity != 0;
         expect.payload_hash = payload_hash;
         expect.check_payload_hash = check_hash != 0;
-        expect.stage_parts = 0;
+        expect.stage_parts = n_stages;
         auto* d = new sc_wire_decoder();
         std::string err;
-        if (!d->dec.open(payload, bytes, *g, *slot, expect, err)) {
+        bool opened;
+        if constexpr (std::is_same_v<Slot, sc_decode_slot>) {
+            std::vector<WireDeviceStage> parts;
+            if (const int rc = stages_of(stages, n_stages, {}, false, parts)) {
+                delete d;
+                return rc;
+            }
+            opened = d->dec.open(payload, bytes, *g, *slot, parts, expect, err);
+        } else {
+            opened = d->dec.open(payload, bytes, *g, *slot, expect, err);
+        }
+        if (!opened) {
             delete d;
             return failed(SC_EINVAL, err);
         }
@@ -151,15 +211,23 @@ static int decoder_open(const void* payload, uint64_t bytes, const sc_geometry* 
 int sc_wire_decoder_open(const void* payload, uint64_t bytes, const sc_geometry* g, const sc_decode_slot* slot,
                          const int64_t* geometry, uint64_t geom_hash, uint64_t pack_hash, int32_t check_identity,
                          uint64_t payload_hash, int32_t check_hash, sc_wire_decoder** out) {
-    return decoder_open(payload, bytes, g, slot, geometry, geom_hash, pack_hash, check_identity, payload_hash, check_hash,
-                        out);
+    return decoder_open(payload, bytes, g, slot, nullptr, 0, geometry, geom_hash, pack_hash, check_identity, payload_hash,
+                        check_hash, out);
+}
+
+int sc_wire_decoder_open_split(const void* payload, uint64_t bytes, const sc_geometry* g, const sc_decode_slot* slot,
+                               const sc_wire_stage* stages, int32_t n_stages, const int64_t* geometry,
+                               uint64_t geom_hash, uint64_t pack_hash, int32_t check_identity, uint64_t payload_hash,
+                               int32_t check_hash, sc_wire_decoder** out) {
+    return decoder_open(payload, bytes, g, slot, stages, n_stages, geometry, geom_hash, pack_hash, check_identity,
+                        payload_hash, check_hash, out);
 }
 
 int sc_wire_decoder_open_layers(const void* payload, uint64_t bytes, const sc_geometry* g, const sc_slot_layers* slot,
                                 const int64_t* geometry, uint64_t geom_hash, uint64_t pack_hash, int32_t check_identity,
                                 uint64_t payload_hash, int32_t check_hash, sc_wire_decoder** out) {
-    return decoder_open(payload, bytes, g, slot, geometry, geom_hash, pack_hash, check_identity, payload_hash, check_hash,
-                        out);
+    return decoder_open(payload, bytes, g, slot, nullptr, 0, geometry, geom_hash, pack_hash, check_identity, payload_hash,
+                        check_hash, out);
 }
 
 int64_t sc_wire_decoder_tokens(const sc_wire_decoder* d) { return d ? d->dec.tokens() : -1; }
@@ -189,6 +257,20 @@ int sc_wire_decoder_small(const sc_wire_decoder* d, int32_t which, uint8_t* dst,
     if (!d || !d->restored || !n || which < 0 || which > 3) return failed(SC_EINVAL, "conversation wire: no such buffer");
     const std::vector<uint8_t>* small[4] = {&d->image.live.ple, &d->image.live.tails, &d->image.live.dead,
                                             &d->image.live.block_pos};
+    const auto& v = *small[which];
+    *n = v.size();
+    if (cap < v.size() || (!v.empty() && !dst)) return failed(SC_ERANGE, "conversation wire: buffer too small");
+    for (size_t i = 0; i < v.size(); ++i) dst[i] = v[i];
+    return done();
+}
+
+int sc_wire_decoder_stage_small(const sc_wire_decoder* d, int32_t stage, int32_t which, uint8_t* dst, uint64_t cap,
+                                uint64_t* n) {
+    if (!d || !d->restored || !n || which < 0 || which > 3 || stage < 0 ||
+        size_t(stage) >= d->image.stage_parts.size())
+        return failed(SC_EINVAL, "conversation wire: no such stage buffer");
+    const ConversationCheckpoint& st = d->image.stage_parts[size_t(stage)].state;
+    const std::vector<uint8_t>* small[4] = {&st.ple, &st.tails, &st.dead, &st.block_pos};
     const auto& v = *small[which];
     *n = v.size();
     if (cap < v.size() || (!v.empty() && !dst)) return failed(SC_ERANGE, "conversation wire: buffer too small");

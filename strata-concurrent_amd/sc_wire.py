@@ -20,11 +20,19 @@ class Live(C.Structure):
                 ("used", C.c_uint64), ("small", C.c_void_p * 4), ("small_bytes", C.c_uint64 * 4)]
 
 
+class Stage(C.Structure):
+    """One later stage of a layer split: its f16 slot, geometry, layer range and (encode) small host buffers."""
+    _fields_ = [("geometry", sc.Geometry), ("slot", sc.DecodeSlot), ("layer_lo", C.c_int64), ("layer_hi", C.c_int64),
+                ("small", C.c_void_p * 4), ("small_bytes", C.c_uint64 * 4)]
+
+
 _P, _I64, _U64, _I32 = C.c_void_p, C.c_int64, C.c_uint64, C.c_int32
 for _name, _res, _args in (
     ("sc_wire_last_error", C.c_char_p, []),
     ("sc_wire_encoder_create", C.c_int, [C.POINTER(sc.Geometry), C.POINTER(sc.DecodeSlot), _I64, C.POINTER(Live), _U64,
                                          _U64, C.POINTER(_P)]),
+    ("sc_wire_encoder_create_split", C.c_int, [C.POINTER(sc.Geometry), C.POINTER(sc.DecodeSlot), _I64,
+                                               C.POINTER(Live), C.POINTER(Stage), _I32, _U64, _U64, C.POINTER(_P)]),
     ("sc_wire_encoder_create_layers", C.c_int, [C.POINTER(sc.Geometry), C.POINTER(sc.SlotLayers), _I64,
                                                 C.POINTER(Live), _U64, _U64, C.POINTER(_P)]),
     ("sc_wire_encoder_bytes", _U64, [_P]),
@@ -34,21 +42,27 @@ for _name, _res, _args in (
     ("sc_wire_encoder_destroy", C.c_int, [_P]),
     ("sc_wire_decoder_open", C.c_int, [_P, _U64, C.POINTER(sc.Geometry), C.POINTER(sc.DecodeSlot), C.POINTER(C.c_int64),
                                        _U64, _U64, _I32, _U64, _I32, C.POINTER(_P)]),
+    ("sc_wire_decoder_open_split", C.c_int, [_P, _U64, C.POINTER(sc.Geometry), C.POINTER(sc.DecodeSlot),
+                                             C.POINTER(Stage), _I32, C.POINTER(C.c_int64), _U64, _U64, _I32, _U64, _I32,
+                                             C.POINTER(_P)]),
     ("sc_wire_decoder_open_layers", C.c_int, [_P, _U64, C.POINTER(sc.Geometry), C.POINTER(sc.SlotLayers),
                                               C.POINTER(C.c_int64), _U64, _U64, _I32, _U64, _I32, C.POINTER(_P)]),
     ("sc_wire_decoder_tokens", _I64, [_P]),
     ("sc_wire_decoder_restore", C.c_int, [_P, _P]),
     ("sc_wire_decoder_live_ids", C.c_int, [_P, C.POINTER(C.c_int32), _I64, C.POINTER(_I64)]),
     ("sc_wire_decoder_small", C.c_int, [_P, _I32, C.POINTER(C.c_uint8), _U64, C.POINTER(_U64)]),
+    ("sc_wire_decoder_stage_small", C.c_int, [_P, _I32, _I32, C.POINTER(C.c_uint8), _U64, C.POINTER(_U64)]),
     ("sc_wire_decoder_destroy", C.c_int, [_P]),
 ):
     _fn = getattr(lib, _name)
     _fn.restype, _fn.argtypes = _res, _args
 
-EXPORTS = ("sc_wire_last_error", "sc_wire_encoder_create", "sc_wire_encoder_create_layers", "sc_wire_encoder_bytes",
-           "sc_wire_encoder_pool_offset", "sc_wire_encode_async", "sc_wire_encoder_hash", "sc_wire_encoder_destroy",
-           "sc_wire_decoder_open", "sc_wire_decoder_open_layers", "sc_wire_decoder_tokens", "sc_wire_decoder_restore",
-           "sc_wire_decoder_live_ids", "sc_wire_decoder_small", "sc_wire_decoder_destroy")
+EXPORTS = ("sc_wire_last_error", "sc_wire_encoder_create", "sc_wire_encoder_create_split",
+           "sc_wire_encoder_create_layers", "sc_wire_encoder_bytes", "sc_wire_encoder_pool_offset",
+           "sc_wire_encode_async", "sc_wire_encoder_hash", "sc_wire_encoder_destroy", "sc_wire_decoder_open",
+           "sc_wire_decoder_open_split", "sc_wire_decoder_open_layers", "sc_wire_decoder_tokens",
+           "sc_wire_decoder_restore", "sc_wire_decoder_live_ids", "sc_wire_decoder_small", "sc_wire_decoder_stage_small",
+           "sc_wire_decoder_destroy")
 
 
 class WireError(RuntimeError):
@@ -86,16 +100,43 @@ def make_live(geometry, ids, layer_lo=0, layer_hi=0, cvec=True, draft_record=Tru
     return lv, (ids, starts, hashes, smalls)
 
 
+def make_stages(stages) -> tuple:
+    """A Stage array from (geometry, slot, layer_lo, layer_hi, small) tuples (`small` the four byte strings, or None
+    when decoding), plus the host arrays it points into (keep both alive while the encoder or decoder is created)."""
+    import numpy as np
+    arr = (Stage * max(len(stages), 1))()
+    keep = []
+    for i, (geo, slot, lo, hi, small) in enumerate(stages):
+        st = arr[i]
+        st.geometry = geo
+        cs = slot.c_struct()
+        keep.append(cs)
+        st.slot = cs
+        st.layer_lo, st.layer_hi = lo, hi
+        for k, b in enumerate(small or (b"",) * 4):
+            buf = np.frombuffer(bytes(b), dtype=np.uint8) if len(b) else np.zeros(1, np.uint8)
+            keep.append(buf)
+            st.small[k] = buf.ctypes.data
+            st.small_bytes[k] = len(b)
+    return arr, keep
+
+
 class Encoder:
     """The device encoder of a slot: an f16 decode slot (sc_handoff.Slot) or a slot in any K/V format
-    (sc_handoff.LayerPools)."""
+    (sc_handoff.LayerPools); with `stages` (from make_stages) a layer-split payload of an f16 slot."""
 
-    def __init__(self, geo, slot, tokens: int, live: Live, geom_hash: int = 0, pack_hash: int = 0):
+    def __init__(self, geo, slot, tokens: int, live: Live, geom_hash: int = 0, pack_hash: int = 0, stages=None,
+                 n_stages: int = 0):
         self._slot = slot.c_struct()
         h = C.c_void_p()
-        create = lib.sc_wire_encoder_create_layers if isinstance(slot, sc.LayerPools) else lib.sc_wire_encoder_create
-        _check(create(C.byref(geo), C.byref(self._slot), tokens, C.byref(live), geom_hash, pack_hash, C.byref(h)),
-               "sc_wire_encoder_create")
+        if stages is not None:
+            _check(lib.sc_wire_encoder_create_split(C.byref(geo), C.byref(self._slot), tokens, C.byref(live), stages,
+                                                    n_stages, geom_hash, pack_hash, C.byref(h)),
+                   "sc_wire_encoder_create_split")
+        else:
+            create = lib.sc_wire_encoder_create_layers if isinstance(slot, sc.LayerPools) else lib.sc_wire_encoder_create
+            _check(create(C.byref(geo), C.byref(self._slot), tokens, C.byref(live), geom_hash, pack_hash, C.byref(h)),
+                   "sc_wire_encoder_create")
         self.handle = h.value
 
     @property
@@ -130,13 +171,19 @@ class Encoder:
 
 class Decoder:
     def __init__(self, payload_ptr: int, nbytes: int, geo, slot, geometry=None, geom_hash=0, pack_hash=0,
-                 check_identity=False, payload_hash=0, check_hash=False):
+                 check_identity=False, payload_hash=0, check_hash=False, stages=None, n_stages: int = 0):
         self._slot = slot.c_struct()
         self._geo18 = (C.c_int64 * 18)(*geometry) if geometry is not None else None
         h = C.c_void_p()
-        open_ = lib.sc_wire_decoder_open_layers if isinstance(slot, sc.LayerPools) else lib.sc_wire_decoder_open
-        _check(open_(payload_ptr, nbytes, C.byref(geo), C.byref(self._slot), self._geo18, geom_hash, pack_hash,
-                     int(check_identity), payload_hash, int(check_hash), C.byref(h)), "sc_wire_decoder_open")
+        if stages is not None:
+            _check(lib.sc_wire_decoder_open_split(payload_ptr, nbytes, C.byref(geo), C.byref(self._slot), stages,
+                                                  n_stages, self._geo18, geom_hash, pack_hash, int(check_identity),
+                                                  payload_hash, int(check_hash), C.byref(h)),
+                   "sc_wire_decoder_open_split")
+        else:
+            open_ = lib.sc_wire_decoder_open_layers if isinstance(slot, sc.LayerPools) else lib.sc_wire_decoder_open
+            _check(open_(payload_ptr, nbytes, C.byref(geo), C.byref(self._slot), self._geo18, geom_hash, pack_hash,
+                         int(check_identity), payload_hash, int(check_hash), C.byref(h)), "sc_wire_decoder_open")
         self.handle = h.value
 
     @property
@@ -161,6 +208,15 @@ class Decoder:
         out = np.zeros(max(n.value, 1), dtype=np.uint8)
         _check(lib.sc_wire_decoder_small(self.handle, which, out.ctypes.data_as(C.POINTER(C.c_uint8)), out.size,
                                          C.byref(n)), "sc_wire_decoder_small")
+        return out[: n.value].tobytes()
+
+    def stage_small(self, stage: int, which: int) -> bytes:
+        import numpy as np
+        n = C.c_uint64(0)
+        lib.sc_wire_decoder_stage_small(self.handle, stage, which, None, 0, C.byref(n))
+        out = np.zeros(max(n.value, 1), dtype=np.uint8)
+        _check(lib.sc_wire_decoder_stage_small(self.handle, stage, which, out.ctypes.data_as(C.POINTER(C.c_uint8)),
+                                               out.size, C.byref(n)), "sc_wire_decoder_stage_small")
         return out[: n.value].tobytes()
 
     def destroy(self) -> None:
