@@ -7,12 +7,13 @@ handoff = one launch of the move kernel.  value = P / step time (GB/s).
 
 Also reported: the roofline of that kernel (2P algorithmic HBM bytes per launch over its event-timed duration,
 against MI355X's 8 TB/s), the p50 latency of the 32K handoff (config 2, first enqueue to completion event, over
->= 20 repetitions), the two-pass gather -> scatter rate, park (D2H) and resume (H2D) of the 128K slot against the
-host link measured in the same run, the device payload codec, the hand-off arena (payload published from HBM into a
+>= 20 repetitions) and of the 32K park + resume through pinned host memory (host wall clock and device events), the
+two-pass gather -> scatter rate, park (D2H) and resume (H2D) of the 128K slot (p50 of 20) against a probe of the host
+link at the same transfer size, the device payload codec, the hand-off arena (payload published from HBM into a
 tmpfs slot and read back, against the host link), the same-GPU hand-off between processes (exported device segments),
-the quantizing carve, configs 4 and 5, and the CPU baseline: the oracle's single-core carve of a bounded sample of the
-same workload, plus the reference-style host pipeline (16 MiB segment save, FNV-1a encode, decode + re-hash,
-restore).
+the quantizing carve, configs 4 and 5, and the CPU baselines: the oracle's single-core carve of a bounded sample of
+the same workload, plus the reference-style host pipeline (16 MiB segment save, FNV-1a encode, decode + re-hash,
+restore); for the codec and arena rows the reference's own codec and arena, compiled from its sources.
 """
 from __future__ import annotations
 
@@ -42,6 +43,42 @@ def measured_traffic() -> int | None:
         pass
     return None
 HBM_PEAK_GBPS = 8000.0
+# PCIe Gen5 x16, one direction: 32 GT/s x 16 lanes x 128/130 line coding / 8 bits (before packet overheads)
+PCIE5_X16_GBPS = 32.0 * 16 * 128 / 130 / 8
+REF_BIN = ROOT / "oracle" / "_ref"
+
+
+def spread(ms: list[float]) -> dict:
+    """p50 / p90 / min of a list of timings in ms, with the repetition count."""
+    xs = sorted(ms)
+    return {"p50_ms": round(xs[len(xs) // 2], 4), "p90_ms": round(xs[min(len(xs) - 1, int(len(xs) * 0.9))], 4),
+            "min_ms": round(xs[0], 4), "reps": len(xs)}
+
+
+def link_at(sc, dev_ptr: int, host_ptr: int, n: int, reps: int = 3) -> tuple[float, float]:
+    """The host link at one transfer size: p50 GB/s of `reps` plain pinned copies of n bytes each way (one
+    hipMemcpyAsync each, event-timed on a side stream), so a row's fraction of the link compares transfers of the
+    same size."""
+    st = sc.Stream()
+    e0, e1 = sc.Event(), sc.Event()
+    out = []
+    for dst, src in ((dev_ptr, host_ptr), (host_ptr, dev_ptr)):
+        sc.check(sc.lib.sc_copy_async(dst, src, n, st.handle), "link probe")   # warm-up
+        ms = []
+        for _ in range(reps):
+            e0.record(st)
+            sc.check(sc.lib.sc_copy_async(dst, src, n, st.handle), "link probe")
+            e1.record(st)
+            e1.sync()
+            ms.append(e0.elapsed_ms(e1))
+        out.append(n / (sorted(ms)[len(ms) // 2] * 1e-3) / 1e9)
+    return out[0], out[1]
+
+
+def link_fracs(gbps: float, probe: float, small_probe: float) -> dict:
+    """A host-link rate against the same-size probe, the 256 MiB probe and the PCIe Gen5 x16 line rate."""
+    return {"frac_of_probe": round(gbps / probe, 3), "frac_of_small_probe": round(gbps / small_probe, 3),
+            "frac_of_pcie5_x16": round(gbps / PCIE5_X16_GBPS, 3)}
 
 
 def settle_link(sc, floor_gbps: float, limit_s: float = 3.0) -> float:
@@ -311,7 +348,7 @@ def wire_payload(sc, geo, tokens: int, slot, link_h2d: float, link_d2h: float, r
     h = enc.hash()
     e0, e1 = sc.Event(), sc.Event()
     enc_ms, hash_ms = [], []
-    for _ in range(reps):
+    for _ in range(2 * reps):
         e0.record(stream)
         enc.encode(payload.ptr, n, stream)
         e1.record(stream)
@@ -325,7 +362,7 @@ def wire_payload(sc, geo, tokens: int, slot, link_h2d: float, link_d2h: float, r
     assert hp.result() == h
     dst = sc.new_slot(geo, tokens, fill=0)
     mount_ms, mount_dev_ms, open_ms, scatter_ms = [], [], [], []
-    for _ in range(reps):
+    for _ in range(2 * reps):
         t0 = time.perf_counter()
         dec = sc_wire.Decoder(payload.ptr, n, geo, dst, payload_hash=h, check_hash=True)
         t1 = time.perf_counter()
@@ -337,7 +374,10 @@ def wire_payload(sc, geo, tokens: int, slot, link_h2d: float, link_d2h: float, r
         mount_dev_ms.append(e0.elapsed_ms(e1))
         open_ms.append((t1 - t0) * 1e3)
         dec.destroy()
+    same = all(sc.fnv1a64_device(a.ptr, a.nbytes) == sc.fnv1a64_device(b.ptr, b.nbytes)
+               for a, b in zip(slot.buffers(), dst.buffers()))
     # the bare scatter of the same blobs (no hash): the device mount is this plus the hash, with no round trip between
+    # (from an unset transfer image into the mount's slot, which the checked resume below mounts again)
     _, total = sc.image_layout(geo, tokens)
     image = sc.DeviceBuffer(total, "uint8")
     plain = sc.plan_scatter(geo, image.ptr, total, tokens, dst)
@@ -349,18 +389,19 @@ def wire_payload(sc, geo, tokens: int, slot, link_h2d: float, link_d2h: float, r
         scatter_ms.append(e0.elapsed_ms(e1))
     plain.destroy()
     image.free()
-    same = all(sc.fnv1a64_device(a.ptr, a.nbytes) == sc.fnv1a64_device(b.ptr, b.nbytes)
-               for a, b in zip(slot.buffers(), dst.buffers()))
     # checked park: encode on the device, then one D2H of the payload on a second stream that starts as soon as the
     # payload bytes are in place, overlapping the hash; checked resume: the H2D in 64 MiB pieces, each piece hashed on
     # a second stream as soon as it lands (the running hash chained on the device), the hash compared, then the mount
     # (decoder open + one scatter launch, no second hash)
     host = sc.PinnedBuffer(n)
+    sc.check(sc.lib.sc_copy_async(host.ptr, payload.ptr, n, stream.handle), "touch")   # touch the pinned pages once
+    stream.sync()
+    probe_h2d, probe_d2h = link_at(sc, payload.ptr, host.ptr, n)
     side, copy = sc.Stream(), sc.Stream()
     gathered, e2, landed = sc.Event(), sc.Event(), sc.Event()
     piece = 64 << 20
     park_ms, resume_ms = [], []
-    for _ in range(3):
+    for _ in range(reps):
         e0.record(side)
         enc.encode(payload.ptr, n, side, gathered=gathered)
         copy.wait(gathered)
@@ -386,22 +427,30 @@ def wire_payload(sc, geo, tokens: int, slot, link_h2d: float, link_d2h: float, r
         dec.restore(side)
         resume_ms.append((time.perf_counter() - t0) * 1e3)
         dec.destroy()
+    same = same and all(sc.fnv1a64_device(a.ptr, a.nbytes) == sc.fnv1a64_device(b.ptr, b.nbytes)
+                        for a, b in zip(slot.buffers(), dst.buffers()))
     host.free()
     payload.free()
     hp.free()
-    enc_t, hash_t, mount_t = min(enc_ms), min(hash_ms), min(mount_ms)
-    pk, rs = min(park_ms), min(resume_ms)
+    def p50(xs):
+        return sorted(xs)[len(xs) // 2]
+    enc_t, hash_t, mount_t = p50(enc_ms), p50(hash_ms), p50(mount_ms)
+    pk, rs = p50(park_ms), p50(resume_ms)
+    pk_gbps, rs_gbps = n / (pk * 1e-3) / 1e9, n / (rs * 1e-3) / 1e9
     return {"tokens": tokens, "payload_bytes": n, "pool_offset": enc.pool_offset,
             "encode_ms": round(enc_t, 3), "encode_gbps": round(n / (enc_t * 1e-3) / 1e9, 1),
             "hash_ms": round(hash_t, 3), "hash_gbps": round(n / (hash_t * 1e-3) / 1e9, 1),
             "mount_ms": round(mount_t, 3), "mount_gbps": round(n / (mount_t * 1e-3) / 1e9, 1),
-            "open_ms": round(min(open_ms), 3),
-            "checked_park_ms": round(pk, 2), "checked_park_gbps": round(n / (pk * 1e-3) / 1e9, 2),
-            "checked_park_frac_of_link": round(n / (pk * 1e-3) / 1e9 / link_d2h, 3),
-            "checked_resume_ms": round(rs, 2), "checked_resume_gbps": round(n / (rs * 1e-3) / 1e9, 2),
-            "checked_resume_frac_of_link": round(n / (rs * 1e-3) / 1e9 / link_h2d, 3),
+            "open_ms": round(p50(open_ms), 3),
+            "checked_park_ms": round(pk, 2), "checked_park_gbps": round(pk_gbps, 2),
+            "checked_park_vs_link": link_fracs(pk_gbps, probe_d2h, link_d2h),
+            "checked_resume_ms": round(rs, 2), "checked_resume_gbps": round(rs_gbps, 2),
+            "checked_resume_vs_link": link_fracs(rs_gbps, probe_h2d, link_h2d),
+            "link_probe_d2h_gbps": round(probe_d2h, 2), "link_probe_h2d_gbps": round(probe_h2d, 2),
             "round_trip_bit_exact": bool(same),
-            "mount_device_ms": round(min(mount_dev_ms), 3), "scatter_ms": round(min(scatter_ms[1:]), 3),
+            "mount_device_ms": round(p50(mount_dev_ms), 3), "scatter_ms": round(p50(scatter_ms[1:]), 3),
+            "timing": (f"p50 of {2 * reps} encodes, hashes and mounts and of {reps} checked parks and resumes; the "
+                       "link probe is one plain pinned copy of the payload's size each way between the same buffers"),
             "method": "payload in the reference's wire format; encode = head copy + one gather launch + device FNV-1a; "
                       "mount = device FNV-1a whose last kernel compares with the expected hash and leaves a verdict "
                       "word, then one scatter launch gated by it (all or nothing, no host round trip); mount_ms is the "
@@ -422,7 +471,7 @@ def arena_dir(need: int) -> str:
 
 
 def arena_handoff(sc, geo, tokens: int, slot, link_h2d: float, link_d2h: float, chunk_mib: int = 32, depth: int = 4,
-                  threads: int = 8, reps: int = 3) -> dict:
+                  threads: int = 8, reps: int = 5) -> dict:
     """The cross-process row: the 128K slot's payload written on the device, handed through a hand-off arena slot
     (the reference's HandoffArena file, same format) and mounted into a fresh slot.  Writer = device encode, then the
     mover (pinned DMA chunks copied into the slot's mapped window by host threads, device FNV-1a beside it) and publish;
@@ -445,6 +494,12 @@ def arena_handoff(sc, geo, tokens: int, slot, link_h2d: float, link_d2h: float, 
     stream = sc.Stream()
     enc.encode(payload.ptr, n, stream)
     h = enc.hash()
+    # the link at the payload's size: plain pinned copies of n bytes each way
+    probe_host = sc.PinnedBuffer(n)
+    sc.check(sc.lib.sc_copy_async(probe_host.ptr, payload.ptr, n, stream.handle), "touch")
+    stream.sync()
+    probe_h2d, probe_d2h = link_at(sc, arrived.ptr, probe_host.ptr, n)
+    probe_host.free()
     base = arena_dir(n + (64 << 20))
     d = os.path.join(base, f"sc-bench-arena-{os.getpid()}")
     path = os.path.join(d, "arena")
@@ -517,16 +572,20 @@ def arena_handoff(sc, geo, tokens: int, slot, link_h2d: float, link_d2h: float, 
         shutil.rmtree(d, ignore_errors=True)
     payload.free()
     arrived.free()
-    p, q, qv, m = min(pub), min(rd), min(rdv), min(mnt)
+    def p50(xs):
+        return sorted(xs)[len(xs) // 2]
+    p, q, qv, m, mp = p50(pub), p50(rd), p50(rdv), p50(mnt), p50(mpub)
     gb = lambda ms: round(n / (ms * 1e-3) / 1e9, 2)   # noqa: E731
     out.update({
-        "publish_ms": round(p, 2), "publish_gbps": gb(p), "publish_frac_of_link": round(gb(p) / link_d2h, 3),
-        "mover_publish_ms": round(min(mpub), 2), "mover_publish_gbps": gb(min(mpub)),
-        "mover_publish_frac_of_link": round(gb(min(mpub)) / link_d2h, 3),
-        "read_ms": round(q, 2), "read_gbps": gb(q), "read_frac_of_link": round(gb(q) / link_h2d, 3),
+        "publish_ms": round(p, 2), "publish_gbps": gb(p), "publish_vs_link": link_fracs(gb(p), probe_d2h, link_d2h),
+        "mover_publish_ms": round(mp, 2), "mover_publish_gbps": gb(mp),
+        "mover_publish_vs_link": link_fracs(gb(mp), probe_d2h, link_d2h),
+        "read_ms": round(q, 2), "read_gbps": gb(q), "read_vs_link": link_fracs(gb(q), probe_h2d, link_h2d),
         "read_verified_ms": round(qv, 2), "read_verified_gbps": gb(qv),
-        "read_and_mount_ms": round(m, 2), "read_and_mount_gbps": gb(m), "decoder_open_ms": round(min(opn), 2),
-        "read_before_mount_ms": round(min(rim), 2),
+        "read_verified_vs_link": link_fracs(gb(qv), probe_h2d, link_h2d),
+        "read_and_mount_ms": round(m, 2), "read_and_mount_gbps": gb(m), "decoder_open_ms": round(p50(opn), 2),
+        "read_before_mount_ms": round(p50(rim), 2),
+        "link_probe_d2h_gbps": round(probe_d2h, 2), "link_probe_h2d_gbps": round(probe_h2d, 2),
         "read_before_mount_mover": [[round(x, 2) for x in t] for t in rim_mover],
         "round_trip_bit_exact": bool(same),
         "method": "publish = device encode, with the mover's D2H (pinned chunks, host threads copying each chunk "
@@ -536,17 +595,85 @@ def arena_handoff(sc, geo, tokens: int, slot, link_h2d: float, link_d2h: float, 
                   "the publish; read = mover (host threads copy slot chunks into pinned buffers, H2D of each "
                   "while the next is copied); read_verified adds the device FNV-1a check, each chunk hashed as it "
                   "lands with the running hash chained on the device; read_and_mount = verified read + decoder open + "
-                  "one scatter launch; host wall clock around each call, best of the reps; the writer's "
+                  "one scatter launch; host wall clock around each call, p50 of the reps; the writer's "
                   "arena reserved (posix_fallocate + populated mapping) and the reader's mapping populated before the "
                   "timed reps"})
     return out
 
 
+def wire_spec(geo, tokens: int) -> str:
+    """The wire spec (the grammar of oracle/ref_wire_driver.cpp) of a slot's image at `tokens`: one f16 K/V record per
+    QSA layer, the empty draft record, and the live checkpoint with the ids and the slot's GDN rows."""
+    import sc_handoff as sc
+    cells = geo.cells(tokens)
+    kvb = cells * geo.n_head_kv * geo.head_dim * 2
+    gdn = sc.payload_bytes(geo, tokens) - 2 * kvb * geo.n_qsa
+    geokey = [2560, geo.n_layers, 4, 128, 16, 32, 4, 8192, 4096, 24, 2, 256, 128, 4, 4, 3, 1, 0]
+    words = [0x1122334455667788, 0x0AABBCCDDEEFF001, *geokey, 0, geo.n_layers, 1, geo.n_qsa + 1]
+    for _ in range(geo.n_qsa):
+        words += [0, cells, geo.n_head_kv, geo.head_dim, geo.page_size, 0, 128, kvb, kvb, 0, 0, 0]
+    words += [0] * 12
+    words += [tokens, 0, gdn, 0, 0, 0, 0, tokens * 3, 0]   # live checkpoint
+    words += [0, 0]                                          # no retained checkpoints, no stage parts
+    return " ".join(str(w) for w in words)
+
+
+def wire_cpu_baseline(geo_kw: dict, tokens: int, reps: int = 3) -> dict:
+    """The reference's own codec on one core (src/core/conversation_wire.cpp, compiled from its sources into
+    oracle/_ref/ref_wire): encode into memory with the payload's FNV-1a, then decode with the hash checked, over a
+    bounded sample - the 48-layer slot's image at `tokens` tokens."""
+    import subprocess
+    import tempfile
+    import sc_handoff as sc
+    exe = REF_BIN / "ref_wire"
+    if not exe.exists():
+        return {"kind": "reference", "skipped": f"{exe} is not built"}
+    geo = sc.geometry(**geo_kw)
+    with tempfile.NamedTemporaryFile("w", suffix=".spec", delete=False) as f:
+        f.write(wire_spec(geo, tokens))
+        spec = f.name
+    try:
+        out = subprocess.run([str(exe), "time", spec, str(reps)], capture_output=True, text=True, timeout=600,
+                             check=True).stdout.split()
+    finally:
+        os.unlink(spec)
+    kv = dict(w.split("=", 1) for w in out)
+    n, te, td = int(kv["bytes"]), float(kv["encode_s"]), float(kv["decode_s"])
+    return {"value": round(n / (te + td) / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "reference",
+            "encode_gbps": round(n / te / 1e9, 3), "decode_checked_gbps": round(n / td / 1e9, 3),
+            "sample": (f"the reference codec (oracle/_ref/ref_wire, built from src/core/conversation_wire.cpp) on the "
+                       f"48-layer slot's image at {tokens} tokens ({n} payload bytes): encode into memory with the "
+                       f"payload hash, then decode with the hash checked; best of {reps}, 1 thread"),
+            "cpu": cpu_model()}
+
+
 def arena_cpu_baseline(sc, budget_bytes: int = 1 << 30) -> dict:
     """The reference's hand-off path on the host for a bounded sample: write_payload (one pwrite) + the byte-serial
-    FNV-1a of the writer + publish, then read_slot + payload_hash_of + a copy out (src/core/handoff.cpp:821-901,
-    1053-1136), through this library's arena (same file and algorithm)."""
-    import os
+    FNV-1a of the writer + publish, then read_slot + payload_hash_of (src/core/handoff.cpp:821-901, 1053-1136), timed
+    on the reference's own arena (oracle/_ref/ref_arena, built from its sources) when it is built, else on this
+    library's arena (same file format and algorithm) with the oracle's FNV-1a."""
+    import subprocess
+    exe = REF_BIN / "ref_arena"
+    if exe.exists():
+        n = budget_bytes
+        base = arena_dir(n + (64 << 20))
+        d = os.path.join(base, f"sc-bench-arena-ref-{os.getpid()}")
+        os.makedirs(d, exist_ok=True)
+        try:
+            out = subprocess.run([str(exe), "time", os.path.join(d, "arena"), "0aabbccddeeff001", "1122334455667788",
+                                  "131072:1", str(n), str(n), "3"], capture_output=True, text=True, timeout=600,
+                                 check=True).stdout.split()
+        finally:
+            import shutil
+            shutil.rmtree(d, ignore_errors=True)
+        kv = dict(w.split("=", 1) for w in out if "=" in w)
+        if kv.get("ok") == "1":
+            tw, tr = float(kv["write_s"]), float(kv["read_s"])
+            return {"sample_bytes": n, "write_gbps": round(n / tw / 1e9, 2), "read_gbps": round(n / tr / 1e9, 2),
+                    "handoff_gbps": round(n / (tw + tr) / 1e9, 2), "cores": 1, "kind": "reference",
+                    "sample": (f"the reference arena (oracle/_ref/ref_arena, built from src/core/handoff.cpp): "
+                               f"{n} payload bytes, claim + write_payload + fnv1a64 + publish, then read_slot + "
+                               "payload_hash_of; best of 3, 1 thread")}
     import shutil
     import numpy as np
     import sc_arena
@@ -903,8 +1030,10 @@ def main() -> int:
     t0, t1 = sc.Event(), sc.Event()
     sc.park_async(geo, slot, T, host.ptr, total, stream=side)   # warm-up: touch the pinned pages once
     side.sync()
+    # the link at the payload's own size: plain copies of `total` bytes between the same two buffers
+    big_h2d, big_d2h = link_at(sc, image.ptr, host.ptr, total)
     park_ms, resume_ms = [], []
-    for _ in range(3):
+    for _ in range(20):
         t0.record(side)
         sc.park_async(geo, slot, T, host.ptr, total, stream=side)
         t1.record(side)
@@ -915,16 +1044,22 @@ def main() -> int:
         t1.record(side)
         t1.sync()
         resume_ms.append(t0.elapsed_ms(t1))
-    pk, rs = min(park_ms), min(resume_ms)
+    pk, rs = spread(park_ms), spread(resume_ms)
+    pk_gbps = total / (pk["p50_ms"] * 1e-3) / 1e9
+    rs_gbps = total / (rs["p50_ms"] * 1e-3) / 1e9
     result["park_resume"] = {
-        "bytes": total, "park_ms": round(pk, 3), "resume_ms": round(rs, 3),
-        "park_gbps": round(total / (pk * 1e-3) / 1e9, 2), "resume_gbps": round(total / (rs * 1e-3) / 1e9, 2),
-        "link_d2h_gbps": round(d2h, 2), "link_h2d_gbps": round(h2d, 2),
-        "park_frac": round(total / (pk * 1e-3) / 1e9 / d2h, 3), "resume_frac": round(total / (rs * 1e-3) / 1e9 / h2d, 3),
-        "method": "hipMemcpyAsync per blob on a non-blocking side stream, pinned hipHostMalloc image; link probe "
-                  "pinned 256 MiB x 4 per direction at the start of the run",
+        "bytes": total, "park": pk, "resume": rs,
+        "park_gbps": round(pk_gbps, 2), "resume_gbps": round(rs_gbps, 2),
+        "link_probe_d2h_gbps": round(big_d2h, 2), "link_probe_h2d_gbps": round(big_h2d, 2),
+        "link_small_probe_d2h_gbps": round(d2h, 2), "link_small_probe_h2d_gbps": round(h2d, 2),
+        "pcie5_x16_gbps": round(PCIE5_X16_GBPS, 2),
+        "park_vs_link": link_fracs(pk_gbps, big_d2h, d2h), "resume_vs_link": link_fracs(rs_gbps, big_h2d, h2d),
+        "method": "p50 of 20 reps, device events around the enqueue; hipMemcpyAsync per blob on a non-blocking side "
+                  "stream, pinned hipHostMalloc image; the probe is one plain pinned copy of the same byte count "
+                  "between the same buffers (p50 of 3), the small probe 256 MiB x 4 at the start of the run",
         "link_settle_ms": settle_pr}
-    log(f"park {pk:.1f} ms, resume {rs:.1f} ms; link d2h {d2h:.1f} GB/s, h2d {h2d:.1f} GB/s")
+    log(f"park p50 {pk['p50_ms']:.1f} ms, resume p50 {rs['p50_ms']:.1f} ms; same-size link d2h {big_d2h:.1f} GB/s, "
+        f"h2d {big_h2d:.1f} GB/s")
     host.free()
     image.free()
 
@@ -952,6 +1087,48 @@ def main() -> int:
                              "p90_ms": round(lat[int(len(lat) * 0.9)], 4), "reps": len(lat),
                              "p50_gbps": round(PL / (p50 * 1e-3) / 1e9, 1)}
     log(f"32K handoff p50 {p50:.4f} ms over {len(lat)} reps")
+    # the 32K hand-off through host memory: park to a pinned image, resume into a second slot; wall clock from the
+    # first enqueue to the host seeing completion, beside the device events around the same work
+    settle_32 = settle_link(sc, d2h)
+    _, total_l = sc.image_layout(geo, TL)
+    host_l = sc.PinnedBuffer(total_l)
+    dev_l = sc.DeviceBuffer(total_l, "uint8")
+    back_l = sc.new_slot(geo, TL, fill=0)
+    side = sc.Stream()
+    sc.park_async(geo, slot_l, TL, host_l.ptr, total_l, stream=side)   # warm-up: touch the pinned pages once
+    sc.resume_async(geo, host_l.ptr, total_l, TL, back_l, stream=side)
+    side.sync()
+    l_h2d, l_d2h = link_at(sc, dev_l.ptr, host_l.ptr, total_l)
+    dev_l.free()
+    wall, dev = [], []
+    for _ in range(max(20, args.latency_reps)):
+        t0 = time.perf_counter()
+        a.record(side)
+        sc.park_async(geo, slot_l, TL, host_l.ptr, total_l, stream=side)
+        sc.resume_async(geo, host_l.ptr, total_l, TL, back_l, stream=side)
+        b.record(side)
+        b.sync()
+        wall.append((time.perf_counter() - t0) * 1e3)
+        dev.append(a.elapsed_ms(b))
+    same = all(sc.fnv1a64_device(x.ptr, x.nbytes) == sc.fnv1a64_device(y.ptr, y.nbytes)
+               for x, y in zip(slot_l.buffers(), back_l.buffers()))
+    w, d = spread(wall), spread(dev)
+    both = total_l / (d["p50_ms"] * 1e-3) / 1e9
+    ideal_ms = total_l / (l_d2h * 1e9) * 1e3 + total_l / (l_h2d * 1e9) * 1e3
+    result["park_resume_32k"] = {
+        "tokens": TL, "bytes": total_l, "wall": w, "device": d, "round_trip_bit_exact": bool(same),
+        "link_probe_d2h_gbps": round(l_d2h, 2), "link_probe_h2d_gbps": round(l_h2d, 2),
+        "probe_round_trip_ms": round(ideal_ms, 3), "device_p50_vs_probe": round(ideal_ms / d["p50_ms"], 3),
+        "bytes_each_way_gbps_p50": round(both, 2),
+        "method": "park (D2H of every blob) then resume (H2D) of the 32K slot on one non-blocking stream, pinned "
+                  "image; wall = host clock from before the first enqueue to the completion event's sync; device = "
+                  "events around the same work; probe = one plain pinned copy of the image's size each way",
+        "link_settle_ms": settle_32}
+    log(f"32K park+resume p50: wall {w['p50_ms']:.3f} ms, device {d['p50_ms']:.3f} ms (probe round trip "
+        f"{ideal_ms:.3f} ms)")
+    host_l.free()
+    for x in back_l.buffers():
+        x.free()
 
     log("wire payload: device encode / hash / mount of the 128K slot, checked park and resume")
     settle_wire = settle_link(sc, d2h)
@@ -966,10 +1143,12 @@ def main() -> int:
     result["arena_handoff"] = arena_handoff(sc, geo, T, slot, h2d, d2h, *mv[:3])
     result["arena_handoff"]["link_settle_ms"] = settle_ar
     ah = result["arena_handoff"]
-    log(f"arena: publish {ah['mover_publish_gbps']} GB/s ({ah['mover_publish_frac_of_link']} of link), read "
-        f"{ah['read_gbps']} GB/s ({ah['read_frac_of_link']}), read+mount {ah['read_and_mount_ms']} ms")
+    log(f"arena: publish {ah['mover_publish_gbps']} GB/s ({ah['mover_publish_vs_link']['frac_of_probe']} of the "
+        f"probe), read {ah['read_gbps']} GB/s ({ah['read_vs_link']['frac_of_probe']}), read+mount "
+        f"{ah['read_and_mount_ms']} ms")
     if not args.no_cpu:
         result["arena_handoff"]["cpu_baseline"] = arena_cpu_baseline(sc, 512 << 20)
+        result["wire_payload"]["cpu_baseline"] = wire_cpu_baseline(geo_kw, 8192)
     log("same-GPU hand-off between processes: exported device segments")
     result["ipc_handoff"] = ipc_handoff(sc, P)
     ih = result["ipc_handoff"]
@@ -991,14 +1170,15 @@ def main() -> int:
     c4 = result["config4"]
     log(f"config 4: park {c4['park_gbps']} GB/s, resume {c4['resume_gbps']} GB/s, decode slowdown "
         f"{c4['decode_slowdown']}x, bit-exact {c4['round_trip_bit_exact']}")
-    result["config4"]["park_frac"] = round(c4["park_gbps"] / d2h, 3)
-    result["config4"]["resume_frac"] = round(c4["resume_gbps"] / h2d, 3)
+    # against the 128K payload-size probe (config 4 moves 0.2-2.4 GB per transfer) and the small probe
+    result["config4"]["park_vs_link"] = link_fracs(c4["park_gbps"], big_d2h, d2h)
+    result["config4"]["resume_vs_link"] = link_fracs(c4["resume_gbps"], big_h2d, h2d)
     log("config 5: eight ragged slots, batched resume + append in one launch")
     settle_c5 = settle_link(sc, d2h)
     result["config5"] = config5(sc, geo, 0x5EED)
     result["config5"]["link_settle_ms"] = settle_c5
     c5 = result["config5"]
-    result["config5"]["resume_h2d_frac"] = round(c5["resume_h2d_gbps"] / h2d, 3)
+    result["config5"]["resume_h2d_vs_link"] = link_fracs(c5["resume_h2d_gbps"], big_h2d, h2d)
     log(f"config 5: resume {c5['resume_h2d_gbps']} GB/s, one-launch scatter {c5['scatter_launch_ms']} ms "
         f"({c5['scatter_hbm_gbps']} GB/s HBM)")
 

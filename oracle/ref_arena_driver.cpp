@@ -19,8 +19,14 @@
 //   read PATH PACK16 GEOM16 SLOT NONCE16 CLIENT SEED
 //                                               open_reader, read_slot, check every byte and the hash
 //   info PATH PACK16 GEOM16 SLOT                 slot_info of one slot, every field
+//   time PATH PACK16 GEOM16 TIERS PRICED BYTES REPS
+//                                               the CPU baseline of the hand-off: REPS times claim, write_payload
+//                                               (one call), fnv1a64, publish (the writer's leg), then read_slot and
+//                                               payload_hash_of (the reader's leg), release; print the best of each
 #include "strata/core/handoff.hpp"
 
+#include <algorithm>
+#include <chrono>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -153,6 +159,38 @@ int main(int argc, char** argv) {
                     (unsigned long long) p.payload_bytes, (unsigned long long) p.tokens,
                     (unsigned long long) p.request_id, p.tier, (unsigned long long) h,
                     (unsigned long long) p.payload_hash, (int) same);
+        return 0;
+    }
+    if (cmd == "time" && argc == 9) {
+        HandoffSizing s;
+        if (!sizing(argv[5], argv[6], s, err)) return fail("SIZE", err);
+        HandoffArena a, r;
+        a.set_lease_ms(600000);
+        if (!a.open_writer(argv[2], s, hexarg(argv[3]), hexarg(argv[4]), err)) return fail("OPEN", err);
+        if (!r.open_reader(argv[2], hexarg(argv[3]), hexarg(argv[4]), err)) return fail("OPEN", err);
+        const uint64_t bytes = decarg(argv[7]);
+        const int reps = std::atoi(argv[8]) > 0 ? std::atoi(argv[8]) : 1;
+        std::vector<uint8_t> payload(bytes);
+        for (uint64_t i = 0; i < bytes; ++i) payload[i] = pattern(i, 3);
+        double best_w = 1e30, best_r = 1e30;
+        for (int rep = 0; rep < reps; ++rep) {
+            HandoffClaim c;
+            if (!a.claim(0, 1, uint64_t(rep), c, err)) return fail("CLAIM", err);
+            const auto t0 = std::chrono::steady_clock::now();
+            if (!a.write_payload(c, 0, payload.data(), bytes, err)) return fail("WRITE", err);
+            const uint64_t h = fnv1a64(payload.data(), bytes);
+            if (!a.publish(c, 1, bytes, h, err)) return fail("PUBLISH", err);
+            const auto t1 = std::chrono::steady_clock::now();
+            HandoffPayload p;
+            if (!r.read_slot(c.index, c.nonce, 1, p, err)) return fail("READ", err);
+            const uint64_t got = HandoffArena::payload_hash_of(p);
+            const auto t2 = std::chrono::steady_clock::now();
+            if (got != h) return fail("READ", "hash mismatch");
+            if (!a.release(c.index, c.nonce, err)) return fail("RELEASE", err);
+            best_w = std::min(best_w, std::chrono::duration<double>(t1 - t0).count());
+            best_r = std::min(best_r, std::chrono::duration<double>(t2 - t1).count());
+        }
+        std::printf("TIME ok=1 bytes=%llu write_s=%.6f read_s=%.6f\n", (unsigned long long) bytes, best_w, best_r);
         return 0;
     }
     if (cmd == "info" && argc == 6) {

@@ -21,12 +21,17 @@
 //   imgs[i]   = {start = 4*i + salt, hash = splitmix64 finaliser of (salt*1000003 + i)}
 //
 // Usage:
+//   ref_wire time SPEC REPS        the CPU baseline of the codec: build the image (untimed), then REPS times encode it
+//                                  into memory (payload hash included) and decode it back with the payload hash
+//                                  checked; print "bytes=<n> encode_s=<best> decode_s=<best>"
 //   ref_wire encode SPEC OUT       write the payload; print "<bytes> <payload_hash hex>"
 //   ref_wire decode PAYLOAD GEOM_HASH PACK_HASH PAYLOAD_HASH|- [STAGE_PARTS [MAX_PAYLOAD_BYTES]]
 //                                  decode with those expectations (a '-' hash is not checked); print
 //                                  "ok <re-encode equal 0|1>" or "refused <message>"
 #include "strata/core/conversation_wire.hpp"
 
+#include <algorithm>
+#include <chrono>
 #include <cinttypes>
 #include <cstdio>
 #include <cstdlib>
@@ -155,6 +160,42 @@ std::vector<uint8_t> slurp(const std::string& path) {
 }  // namespace
 
 int main(int argc, char** argv) {
+    if (argc >= 4 && std::string(argv[1]) == "time") {
+        WireIdentity id;
+        const SavedConversation img = read_spec(argv[2], id);
+        const int reps = std::atoi(argv[3]) > 0 ? std::atoi(argv[3]) : 1;
+        double best_enc = 1e30, best_dec = 1e30;
+        uint64_t bytes = 0;
+        std::string err;
+        for (int r = 0; r < reps; ++r) {
+            VectorWireSink sink;
+            WireEncoded enc;
+            auto t0 = std::chrono::steady_clock::now();
+            if (!conversation_wire_encode(img, sink, id, enc, err)) {
+                std::printf("refused %s\n", err.c_str());
+                return 1;
+            }
+            auto t1 = std::chrono::steady_clock::now();
+            WireExpect expect;
+            expect.geom_hash = id.geom_hash;
+            expect.pack_hash = id.pack_hash;
+            expect.check_hashes = true;
+            expect.check_payload_hash = true;
+            expect.payload_hash = enc.payload_hash;
+            SavedConversation back;
+            WireDecoded info;
+            if (!conversation_wire_decode(sink.data().data(), sink.data().size(), back, info, expect, err)) {
+                std::printf("refused %s\n", err.c_str());
+                return 1;
+            }
+            auto t2 = std::chrono::steady_clock::now();
+            bytes = sink.data().size();
+            best_enc = std::min(best_enc, std::chrono::duration<double>(t1 - t0).count());
+            best_dec = std::min(best_dec, std::chrono::duration<double>(t2 - t1).count());
+        }
+        std::printf("bytes=%" PRIu64 " encode_s=%.6f decode_s=%.6f\n", bytes, best_enc, best_dec);
+        return 0;
+    }
     if (argc >= 4 && std::string(argv[1]) == "encode") {
         WireIdentity id;
         SavedConversation img = read_spec(argv[2], id);

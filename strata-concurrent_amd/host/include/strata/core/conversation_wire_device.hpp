@@ -122,8 +122,7 @@ private:
     uint64_t staged_bytes_ = 0;
     void* hash_ws_ = nullptr;          // device
     uint64_t hash_ws_bytes_ = 0;
-    uint64_t* hash_dev_ = nullptr;     // device
-    uint64_t* hash_host_ = nullptr;    // pinned
+    uint64_t* hash_host_ = nullptr;    // pinned; the hash's last kernel stores the payload hash here
     void* last_stream_ = nullptr;
     sc_plan* capture_ = nullptr;
     void* capture_target_ = nullptr;   // the payload the capture plan was built for
@@ -171,15 +170,18 @@ private:
     WireDecoded info_{};
     int64_t tokens_ = 0;
     SavedConversation head_image_;
-    struct Download { void* who; bool buffer; uint64_t offset, bytes; };
+    struct Download { void* who; bool buffer; uint64_t offset, bytes, staged_at; };
     std::vector<Download> downloads_;   // blobs that go back to the host image (by address inside head_image_)
+    uint8_t* staged_ = nullptr;         // pinned host staging of the downloads (64-byte aligned pieces)
+    void* side_ = nullptr;              // the downloads' stream, beside the hash
+    void* ev_start_ = nullptr;
+    void* ev_done_ = nullptr;
     sc_plan* scatter_ = nullptr;
     std::vector<sc_plan*> stage_scatters_;   // one per stage part, gated by the same hash verdict
-    bool split_ok_ = false;                  // open() was given the stages a split payload needs
     void* hash_ws_ = nullptr;
     uint64_t hash_ws_bytes_ = 0;
-    uint64_t* hash_dev_ = nullptr;
-    uint64_t* hash_host_ = nullptr;
+    uint64_t* hash_dev_ = nullptr;    // device: the hash check's verdict word
+    uint64_t* hash_host_ = nullptr;   // pinned; the hash's last kernel stores the payload hash here
 };
 
 }  // namespace strata::core

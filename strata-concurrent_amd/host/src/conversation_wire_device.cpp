@@ -129,12 +129,10 @@ void WireDeviceEncoder::release() {
     if (staged_) sc_host_free(staged_);
     if (hash_host_) sc_host_free(hash_host_);
     if (hash_ws_) sc_device_free(hash_ws_);
-    if (hash_dev_) sc_device_free(hash_dev_);
     capture_ = nullptr;
     staged_ = nullptr;
     hash_host_ = nullptr;
     hash_ws_ = nullptr;
-    hash_dev_ = nullptr;
     capture_target_ = nullptr;
     uploads_.clear();
 }
@@ -193,7 +191,6 @@ bool WireDeviceEncoder::stage(const SavedConversation& img, const std::vector<st
     }
     hash_ws_bytes_ = sc_fnv1a64_workspace_bytes(plan_.total_bytes);
     rc = sc_device_alloc(&hash_ws_, hash_ws_bytes_);
-    if (rc == SC_OK) rc = sc_device_alloc(reinterpret_cast<void**>(&hash_dev_), 64);
     return abi(rc, error, "hash workspace");
 }
 
@@ -378,10 +375,10 @@ bool WireDeviceEncoder::encode(void* payload, uint64_t capacity, void* stream, s
     for (const StagePlan& sp : stage_plans_)
         if (!abi(sc_plan_launch(sp.plan, stream), error, "stage gather")) return false;
     if (gathered && !abi(sc_event_record(gathered, stream), error, "gather event")) return false;
-    if (!abi(sc_fnv1a64_async(payload, plan_.total_bytes, kWireHashSeed, hash_dev_, hash_ws_, hash_ws_bytes_, stream),
+    // the hash goes straight to pinned host memory (the last kernel's store): no readback copy
+    if (!abi(sc_fnv1a64_async(payload, plan_.total_bytes, kWireHashSeed, hash_host_, hash_ws_, hash_ws_bytes_, stream),
              error, "payload hash"))
         return false;
-    if (!abi(sc_copy_async(hash_host_, hash_dev_, 8, stream), error, "hash readback")) return false;
     last_stream_ = stream;
     return true;
 }
@@ -405,10 +402,16 @@ void WireDeviceDecoder::release() {
     if (hash_ws_) sc_device_free(hash_ws_);
     if (hash_dev_) sc_device_free(hash_dev_);
     if (hash_host_) sc_host_free(hash_host_);
+    if (staged_) sc_host_free(staged_);
+    if (ev_start_) sc_event_destroy(ev_start_);
+    if (ev_done_) sc_event_destroy(ev_done_);
+    if (side_) sc_stream_destroy(side_);
     scatter_ = nullptr;
     hash_ws_ = nullptr;
     hash_dev_ = nullptr;
     hash_host_ = nullptr;
+    staged_ = nullptr;
+    ev_start_ = ev_done_ = side_ = nullptr;
     downloads_.clear();
     head_image_ = SavedConversation{};
 }
@@ -442,16 +445,26 @@ bool WireDeviceDecoder::read_head(const void* payload, uint64_t bytes, const Wir
 bool WireDeviceDecoder::finish_open(const void* payload, uint64_t bytes, const WireExpect& expect,
                                     const std::vector<detail::WireBlobAt>& blobs, const std::vector<const void*>& device,
                                     std::string& error) {
+    uint64_t staged = 0;
     for (const auto& b : blobs) {
         if (std::find(device.begin(), device.end(), b.who) != device.end()) continue;
         bool buffer = false;
         for (const ConversationKv& k : head_image_.kv)
             for (const ConversationBuffer* x : {&k.k, &k.v, &k.k_scale, &k.v_scale, &k.pooled}) buffer |= x == b.who;
-        downloads_.push_back({const_cast<void*>(b.who), buffer, b.offset, b.bytes});
+        downloads_.push_back({const_cast<void*>(b.who), buffer, b.offset, b.bytes, staged});
+        staged += up64(b.bytes);
     }
+    // The host blobs are read into pinned staging on a stream of their own, beside the hash and the scatter (pinned
+    // reads are plain DMA; reads into pageable memory would each wait for a bounce copy), and handed out after the
+    // verdict is read.
+    int rc = sc_host_alloc(reinterpret_cast<void**>(&staged_), staged ? staged : 64);
+    if (rc == SC_OK) rc = sc_stream_create(&side_);
+    if (rc == SC_OK) rc = sc_event_create(&ev_start_);
+    if (rc == SC_OK) rc = sc_event_create(&ev_done_);
+    if (!abi(rc, error, "host blob staging")) { release(); return false; }
     if (expect.check_payload_hash) {
         hash_ws_bytes_ = sc_fnv1a64_workspace_bytes(info_.bytes);
-        int rc = sc_device_alloc(&hash_ws_, hash_ws_bytes_);
+        rc = sc_device_alloc(&hash_ws_, hash_ws_bytes_);
         if (rc == SC_OK) rc = sc_device_alloc(reinterpret_cast<void**>(&hash_dev_), 64);
         if (rc == SC_OK) rc = sc_host_alloc(reinterpret_cast<void**>(&hash_host_), 64);
         if (!abi(rc, error, "hash workspace")) { release(); return false; }
@@ -582,8 +595,17 @@ bool WireDeviceDecoder::restore(void* stream, SavedConversation& image, std::str
     // verdict word that gates the scatter, so a mismatch writes nothing and there is no host round trip before the
     // scatter; the host reads the hash back with the other small blobs, once, at the end.
     uint32_t* verdict = reinterpret_cast<uint32_t*>(hash_dev_ + 1);
+    // host blobs: read on the side stream once everything before this call on `stream` (the payload's arrival) is done
+    if (!abi(sc_event_record(ev_start_, stream), error, "restore start") ||
+        !abi(sc_stream_wait_event(side_, ev_start_), error, "restore start"))
+        return false;
+    for (const Download& d : downloads_)
+        if (d.bytes && !abi(sc_copy_async(staged_ + d.staged_at, payload_ + d.offset, d.bytes, side_), error, "blob read"))
+            return false;
+    if (!abi(sc_event_record(ev_done_, side_), error, "blob read")) return false;
+    // the hash itself goes straight to pinned host memory (the last kernel's store), the verdict stays on the device
     if (expect_.check_payload_hash &&
-        !abi(sc_fnv1a64_check_async(payload_, info_.bytes, kWireHashSeed, expect_.payload_hash, hash_dev_, verdict,
+        !abi(sc_fnv1a64_check_async(payload_, info_.bytes, kWireHashSeed, expect_.payload_hash, hash_host_, verdict,
                                     hash_ws_, hash_ws_bytes_, stream),
              error, "payload hash"))
         return false;
@@ -624,30 +646,31 @@ bool WireDeviceDecoder::restore(void* stream, SavedConversation& image, std::str
     if (expect_.check_payload_hash ? !abi(sc_plan_launch_gated(scatter_, verdict, stream), error, "pool scatter")
                                    : !abi(sc_plan_launch(scatter_, stream), error, "pool scatter"))
         return false;
-    if (expect_.check_payload_hash && !abi(sc_copy_async(hash_host_, hash_dev_, 8, stream), error, "hash readback"))
+    // the caller's stream covers the whole restore, the side stream's reads included
+    if (!abi(sc_stream_wait_event(stream, ev_done_), error, "restore") ||
+        !abi(sc_stream_sync(stream), error, "restore"))
         return false;
-    for (const Download& d : downloads_) {
-        void* target = remap(d.who);
-        if (!target) return refuse(error, "internal: a host blob lost its place");
-        if (d.buffer) {
-            auto* b = static_cast<ConversationBuffer*>(target);
-            b->resize(size_t(d.bytes));
-            bool ok = true;
-            b->visit(0, size_t(d.bytes), [&](uint8_t* p, size_t n, size_t at) {
-                return ok = abi(sc_copy_async(p, payload_ + d.offset + at, n, stream), error, "blob read");
-            });
-            if (!ok) return false;
-        } else {
-            auto* v = static_cast<std::vector<uint8_t>*>(target);
-            v->resize(size_t(d.bytes));
-            if (!abi(sc_copy_async(v->data(), payload_ + d.offset, d.bytes, stream), error, "blob read")) return false;
-        }
-    }
-    if (!abi(sc_stream_sync(stream), error, "restore")) return false;
     if (expect_.check_payload_hash) {
         if (*hash_host_ != expect_.payload_hash)   // the gated scatter wrote nothing
             return refuse(error, "payload hash mismatch on the device (the bytes are not the bytes that were written)");
         info_.payload_hash = *hash_host_;
+    }
+    for (const Download& d : downloads_) {
+        void* target = remap(d.who);
+        if (!target) return refuse(error, "internal: a host blob lost its place");
+        const uint8_t* src = staged_ + d.staged_at;
+        if (d.buffer) {
+            auto* b = static_cast<ConversationBuffer*>(target);
+            b->resize(size_t(d.bytes));
+            b->visit(0, size_t(d.bytes), [&](uint8_t* p, size_t n, size_t at) {
+                std::memcpy(p, src + at, n);
+                return true;
+            });
+        } else {
+            auto* v = static_cast<std::vector<uint8_t>*>(target);
+            v->resize(size_t(d.bytes));
+            if (d.bytes) std::memcpy(v->data(), src, size_t(d.bytes));
+        }
     }
     image = std::move(out);
     return true;
