@@ -303,6 +303,16 @@ int sc_plan_launch_gated(const sc_plan* plan, const uint32_t* gate, void* stream
 uint64_t sc_plan_payload_bytes(const sc_plan* plan);
 /* Workgroups the launch uses, for launch-shape sweeps; 0 restores the grid the plan was built with. */
 int sc_plan_set_grid(sc_plan* plan, int64_t workgroups);
+/* Destination order (no reference counterpart: a launch-shape choice of this build).  Rows that write through a page
+ * table (K/V carves into a paged slot, image pages scattered into one) visit their pages in the order of the
+ * physical pages, so the writes of a launch form one ascending run of the pool; the order is rebuilt on the device by
+ * three small kernels before every launch of the plan (the table may change between launches), in the plan's own
+ * workspace - so launches of one such plan on different streams must not overlap.  A table gets the order when it
+ * covers at least `pages` logical pages in a pool of at most 8 times as many physical pages.  Library-wide, for plans
+ * built afterwards; pages <= 0 turns it off.  Returns the previous value (default 2048). */
+int64_t sc_set_order_min_pages(int64_t pages);
+/* How many page tables of the plan are visited in destination order (0: every row follows its source). */
+int sc_plan_order_groups(const sc_plan* plan);
 /* Frees the device table.  The caller must not destroy a plan whose launch has not completed. */
 int sc_plan_destroy(sc_plan* plan);
 

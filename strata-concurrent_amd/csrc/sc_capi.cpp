@@ -8,6 +8,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstdint>
 #include <cstring>
 #include <exception>
@@ -24,6 +25,8 @@ hipError_t launch_append(const AppendRows& rows, int n_rows, uint64_t tiles_per_
                          hipStream_t stream);
 hipError_t launch_move(const MoveRow* rows, const uint16_t* tile_row, const MoveGeo& geo, uint64_t n_tiles,
                        int64_t grid, int32_t mix, hipStream_t stream, const uint32_t* gate = nullptr);
+hipError_t launch_page_order(const OrderGroup* groups, int32_t n_groups, int64_t max_pages, uint32_t max_blocks,
+                             hipStream_t stream);
 hipError_t launch_fill_uniform_f16(uint16_t* dst, uint64_t n, float lo, float hi, uint64_t seed, uint64_t sid,
                                    hipStream_t stream);
 hipError_t launch_fill_uniform_f32(float* dst, uint64_t n, float lo, float hi, uint64_t seed, uint64_t sid,
@@ -63,6 +66,12 @@ struct sc_plan {
     int64_t grid = 0;
     int64_t default_grid = 0;           // what the builder chose; sc_plan_set_grid(plan, 0) returns to it
     int32_t mix = sc::kMixPlain;        // the kernel instance that holds every row kind of the plan
+    // destination order of the rows that write through page tables (OrderGroup, sc_internal.hpp)
+    void* order_ws = nullptr;           // one device block: the groups, then inv / order / counts per group
+    const sc::OrderGroup* order_groups = nullptr;
+    int32_t n_order_groups = 0;
+    int64_t order_max_pages = 0;
+    uint32_t order_max_blocks = 0;
 };
 
 namespace {
@@ -186,18 +195,134 @@ constexpr uint64_t kMaxGrid = 65536;
 // one per tile 1.46; q4_0: 1.53, 1.51, 1.52, 1.53).
 constexpr uint64_t kMaxGridQuant = 262144;
 
+// Rows that write through a page table visit their pages in destination order when the table covers at least this
+// many logical pages (fewer pages gain nothing from the pre-pass) and the pool is at most kOrderMaxSparsity times
+// larger (the pre-pass reads every physical page of the pool).  sc_set_order_min_pages changes it; <= 0 turns it off.
+std::atomic<int64_t> g_order_min_pages{2048};
+constexpr int64_t kOrderMaxSparsity = 8;
+
+// The logical pages a row writes through its table: K/V rows the cells [pos0, pos0 + rows), page rows their pages.
+void table_pages_of(const sc::MoveRow& r, const Geo& g, int64_t& lo, int64_t& hi) {
+    if (r.kind == sc::kPagesScatter) {
+        lo = 0;
+        hi = int64_t((r.n + g.page_bytes / 16 - 1) / (g.page_bytes / 16));
+        return;
+    }
+    const int64_t tokens = int64_t(r.n / (uint64_t(g.H) * (g.row_bytes / 16)));
+    lo = r.pos0 / g.ps;
+    hi = (r.pos0 + tokens + g.ps - 1) / g.ps;
+}
+
+struct OrderPlan {
+    std::vector<sc::OrderGroup> groups;   // device pointers filled once the workspace exists
+    std::vector<int> row_group;           // per row: its group, or -1
+};
+
+OrderPlan order_plan(const std::vector<sc::MoveRow>& rows, const Geo& g) {
+    OrderPlan o;
+    o.row_group.assign(rows.size(), -1);
+    const int64_t min_pages = g_order_min_pages.load();
+    if (min_pages <= 0) return o;
+    for (size_t k = 0; k < rows.size(); ++k) {
+        const sc::MoveRow& r = rows[k];
+        if (!r.table || !r.n || (r.kind != sc::kKv16 && r.kind != sc::kKv32 && r.kind != sc::kPagesScatter)) continue;
+        int64_t lo, hi;
+        table_pages_of(r, g, lo, hi);
+        int gi = -1;
+        for (size_t i = 0; i < o.groups.size(); ++i)
+            if (o.groups[i].table == r.table && o.groups[i].ld == r.ld) gi = int(i);
+        if (gi < 0) {
+            sc::OrderGroup G{};
+            G.table = r.table;
+            G.ld = r.ld;
+            G.lp_lo = lo;
+            G.lp_hi = hi;
+            o.groups.push_back(G);
+            gi = int(o.groups.size()) - 1;
+        }
+        o.groups[size_t(gi)].lp_lo = std::min(o.groups[size_t(gi)].lp_lo, lo);
+        o.groups[size_t(gi)].lp_hi = std::max(o.groups[size_t(gi)].lp_hi, hi);
+        o.row_group[k] = gi;
+    }
+    // groups too small or too sparse keep the source order
+    std::vector<int> keep(o.groups.size(), -1);
+    std::vector<sc::OrderGroup> kept;
+    const uint64_t page_chunks = g.page_bytes / 16;
+    for (size_t i = 0; i < o.groups.size(); ++i) {
+        const sc::OrderGroup& G = o.groups[i];
+        const int64_t m = G.lp_hi - G.lp_lo;
+        if (m < min_pages || G.ld > kOrderMaxSparsity * m || G.ld <= 0 ||
+            uint64_t(m) * page_chunks >= kMaxRowChunks || G.ld >= (int64_t(1) << 31))
+            continue;
+        keep[i] = int(kept.size());
+        kept.push_back(G);
+    }
+    for (int& gi : o.row_group) gi = gi >= 0 ? keep[size_t(gi)] : -1;
+    o.groups = std::move(kept);
+    for (sc::OrderGroup& G : o.groups) {
+        G.n_blocks = uint32_t((G.ld + sc::kOrderBlockPages - 1) / sc::kOrderBlockPages);
+        const uint64_t tiles = (uint64_t(G.lp_hi - G.lp_lo) * page_chunks + sc::kTileChunks - 1) / sc::kTileChunks;
+        G.order_len = (tiles * sc::kTileChunks + page_chunks - 1) / page_chunks;
+    }
+    return o;
+}
+
+// One device block for the order pre-pass: the groups, then each group's inv (set to -1), order and counts.  Fills
+// the rows' order pointers.
+int order_workspace(OrderPlan& o, std::vector<sc::MoveRow>& rows, sc_plan* p) {
+    if (o.groups.empty()) return ok();
+    auto up = [](uint64_t x) { return (x + 255) / 256 * 256; };
+    uint64_t at = up(o.groups.size() * sizeof(sc::OrderGroup));
+    std::vector<uint64_t> inv_at, order_at, counts_at;
+    for (const sc::OrderGroup& G : o.groups) {
+        inv_at.push_back(at);
+        at += up(uint64_t(G.ld) * 4);
+        order_at.push_back(at);
+        at += up(G.order_len * 4);
+        counts_at.push_back(at);
+        at += up(uint64_t(G.n_blocks) * 4);
+    }
+    hipError_t e = hipMalloc(&p->order_ws, at);
+    if (e != hipSuccess) return fail(SC_ENOMEM, std::string("sc_handoff: order workspace: ") + hipGetErrorString(e));
+    uint8_t* base = static_cast<uint8_t*>(p->order_ws);
+    for (size_t i = 0; i < o.groups.size(); ++i) {
+        sc::OrderGroup& G = o.groups[i];
+        G.inv = reinterpret_cast<int32_t*>(base + inv_at[i]);
+        G.order = reinterpret_cast<int32_t*>(base + order_at[i]);
+        G.counts = reinterpret_cast<uint32_t*>(base + counts_at[i]);
+        p->order_max_pages = std::max(p->order_max_pages, G.lp_hi - G.lp_lo);
+        p->order_max_blocks = std::max(p->order_max_blocks, G.n_blocks);
+        e = hipMemset(G.inv, 0xFF, uint64_t(G.ld) * 4);   // every entry -1; each launch leaves it so
+        if (e != hipSuccess) return hip_fail(e, "order workspace");
+    }
+    p->order_groups = reinterpret_cast<const sc::OrderGroup*>(base);
+    p->n_order_groups = int32_t(o.groups.size());
+    e = hipMemcpy(base, o.groups.data(), o.groups.size() * sizeof(sc::OrderGroup), hipMemcpyHostToDevice);
+    if (e != hipSuccess) return hip_fail(e, "order workspace");
+    for (size_t k = 0; k < rows.size(); ++k)
+        if (o.row_group[k] >= 0) rows[k].order = o.groups[size_t(o.row_group[k])].order;
+    return ok();
+}
+
 // Assigns tile ranges, uploads the table and fills the plan.  The only HIP calls a plan builder makes.
 int finish_plan(std::vector<sc::MoveRow>& rows, const Geo& g, uint64_t payload, sc_plan** out) {
     if (rows.size() > 65535) return fail(SC_ERANGE, "sc_handoff: more than 65535 handoff table rows in one plan");
+    OrderPlan order = order_plan(rows, g);
     uint64_t tiles = 0;
     bool quant = false, kv32 = false;
-    for (auto& r : rows) {
+    for (size_t k = 0; k < rows.size(); ++k) {
+        sc::MoveRow& r = rows[k];
         if (r.n >= kMaxRowChunks) return fail(SC_ERANGE, "sc_handoff: a handoff table row beyond 2^31 chunks");
         r.tile0 = tiles;
         const uint64_t per_tile = r.kind == sc::kConv ? sc::kConvTileChannels
                                 : (r.kind == sc::kKvQ8 || r.kind == sc::kKvQ4) ? sc::kQuantUnitsPerTile
                                                                               : sc::kTileChunks;
-        tiles += (r.n + per_tile - 1) / per_tile;
+        // an ordered row spans the chunks of its group's pages (whole pages, in destination order)
+        const int gi = order.row_group[k];
+        const uint64_t chunks = gi >= 0 ? uint64_t(order.groups[size_t(gi)].lp_hi - order.groups[size_t(gi)].lp_lo) *
+                                              (g.page_bytes / 16)
+                                        : r.n;
+        tiles += (chunks + per_tile - 1) / per_tile;
         quant = quant || r.kind == sc::kKvQ8 || r.kind == sc::kKvQ4;
         kv32 = kv32 || r.kind == sc::kKv32;
     }
@@ -219,10 +344,16 @@ int finish_plan(std::vector<sc::MoveRow>& rows, const Geo& g, uint64_t payload, 
         const uint64_t end = k + 1 < rows.size() ? rows[k + 1].tile0 : tiles;
         std::fill(tile_row.begin() + int64_t(rows[k].tile0), tile_row.begin() + int64_t(end), uint16_t(k));
     }
+    if (const int rc = order_workspace(order, rows, p)) {
+        if (p->order_ws) (void) hipFree(p->order_ws);
+        delete p;
+        return rc;
+    }
     hipError_t e = hipMalloc(reinterpret_cast<void**>(&p->rows_dev), rows.size() * sizeof(sc::MoveRow));
     if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&p->tile_row_dev), tiles * sizeof(uint16_t));
     if (e != hipSuccess) {
         if (p->rows_dev) (void) hipFree(p->rows_dev);
+        if (p->order_ws) (void) hipFree(p->order_ws);
         delete p;
         return fail(SC_ENOMEM, std::string("sc_handoff: table allocation: ") + hipGetErrorString(e));
     }
@@ -231,6 +362,7 @@ int finish_plan(std::vector<sc::MoveRow>& rows, const Geo& g, uint64_t payload, 
     if (e != hipSuccess) {
         (void) hipFree(p->rows_dev);
         (void) hipFree(p->tile_row_dev);
+        if (p->order_ws) (void) hipFree(p->order_ws);
         delete p;
         return hip_fail(e, "table upload");
     }
@@ -920,14 +1052,30 @@ int sc_plan_scatter_layers(const sc_geometry* g, const void* src, uint64_t src_b
     return guarded([&] { return layers_plan(g, const_cast<void*>(src), src_bytes, map, tokens, dst, true, out); });
 }
 
+namespace {
+// The order pre-pass of a plan with destination-ordered rows; it writes only the plan's own workspace, so launches
+// of one plan on different streams must not overlap.
+hipError_t launch_order(const sc_plan* plan, hipStream_t stream) {
+    if (!plan->n_order_groups || !plan->n_tiles) return hipSuccess;
+    return sc::launch_page_order(plan->order_groups, plan->n_order_groups, plan->order_max_pages, plan->order_max_blocks,
+                                 stream);
+}
+}  // namespace
+
+int64_t sc_set_order_min_pages(int64_t pages) { return g_order_min_pages.exchange(pages); }
+
+int sc_plan_order_groups(const sc_plan* plan) { return plan ? plan->n_order_groups : 0; }
+
 int sc_plan_launch(const sc_plan* plan, void* stream) {
     if (!plan) return fail(SC_EINVAL, "sc_handoff: missing plan");
     if (plan->batch) {
         const hipError_t e = sc::launch_batch(plan->batch_args, plan->grid, static_cast<hipStream_t>(stream));
         return e == hipSuccess ? ok() : hip_fail(e, "batch launch");
     }
-    const hipError_t e = sc::launch_move(plan->rows_dev, plan->tile_row_dev, plan->geo, plan->n_tiles, plan->grid,
-                                         plan->mix, static_cast<hipStream_t>(stream));
+    hipError_t e = launch_order(plan, static_cast<hipStream_t>(stream));
+    if (e == hipSuccess)
+        e = sc::launch_move(plan->rows_dev, plan->tile_row_dev, plan->geo, plan->n_tiles, plan->grid, plan->mix,
+                            static_cast<hipStream_t>(stream));
     return e == hipSuccess ? ok() : hip_fail(e, "move launch");
 }
 
@@ -935,8 +1083,10 @@ int sc_plan_launch_gated(const sc_plan* plan, const uint32_t* gate, void* stream
     if (!plan || !gate || (reinterpret_cast<uintptr_t>(gate) & 3u))
         return fail(SC_EINVAL, "sc_handoff: a gated launch needs a plan and a 4-byte aligned gate word");
     if (plan->batch) return fail(SC_EINVAL, "sc_handoff: a batched plan is all or nothing on its own lengths");
-    const hipError_t e = sc::launch_move(plan->rows_dev, plan->tile_row_dev, plan->geo, plan->n_tiles, plan->grid,
-                                         plan->mix, static_cast<hipStream_t>(stream), gate);
+    hipError_t e = launch_order(plan, static_cast<hipStream_t>(stream));
+    if (e == hipSuccess)
+        e = sc::launch_move(plan->rows_dev, plan->tile_row_dev, plan->geo, plan->n_tiles, plan->grid, plan->mix,
+                            static_cast<hipStream_t>(stream), gate);
     return e == hipSuccess ? ok() : hip_fail(e, "move launch");
 }
 
@@ -953,8 +1103,10 @@ int sc_plan_destroy(sc_plan* plan) {
     hipError_t e = plan->rows_dev ? hipFree(plan->rows_dev) : hipSuccess;
     const hipError_t e2 = plan->tile_row_dev ? hipFree(plan->tile_row_dev) : hipSuccess;
     const hipError_t e3 = plan->batch_ptrs_dev ? hipFree(plan->batch_ptrs_dev) : hipSuccess;
+    const hipError_t e4 = plan->order_ws ? hipFree(plan->order_ws) : hipSuccess;
     if (e == hipSuccess) e = e2;
     if (e == hipSuccess) e = e3;
+    if (e == hipSuccess) e = e4;
     delete plan;
     return e == hipSuccess ? ok() : hip_fail(e, "table free");
 }

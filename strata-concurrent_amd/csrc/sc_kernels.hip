@@ -67,9 +67,25 @@ __device__ __forceinline__ int64_t pool_row(const MoveRow& r, const MoveGeo& g, 
     return (int64_t(phys) * g.heads.d + c.h) * g.page_size.d + c.in_page;
 }
 
+// Destination order (MoveRow::order): virtual chunk vq of a row is in-page chunk vq % page_chunks of the order's
+// entry vq / page_chunks, a logical page (-1 past the pages the table places).  Its source rows are that page's cells
+// in token-major order, so the page's chunks are one contiguous run of the row's source: the source chunk is
+// (lp * ps - pos0) * H * row_chunks plus the in-page index.  Returns ~0u (>= every row's chunk count) for a -1 entry
+// and for cells outside the row.
+__device__ __forceinline__ uint32_t ordered_chunk(const MoveRow& r, const MoveGeo& g, uint32_t vq, bool kv) {
+    const uint32_t vp = fdiv(vq, g.page_chunks);
+    const uint32_t ip = vq - vp * g.page_chunks.d;
+    const int64_t lp = *(gi32*) (r.order + vp);
+    if (lp < 0) return ~0u;
+    const int64_t q = kv ? (lp * int64_t(g.page_size.d) - r.pos0) * int64_t(g.heads.d * g.row_chunks.d) + ip
+                         : lp * int64_t(g.page_chunks.d) + ip;
+    return q >= 0 && q < int64_t(r.n) ? uint32_t(q) : ~0u;
+}
+
 // kTable: the row has a page table, whose entries are loaded with the data; without one the physical page is the
-// logical page and nothing but the data is loaded before the stores.
-template <bool kTable>
+// logical page and nothing but the data is loaded before the stores.  kOrder: the tiles visit the row's pages in
+// destination order (the order's load comes before the data's).
+template <bool kTable, bool kOrder = false>
 __device__ void tile_kv16(const MoveRow& r, const MoveGeo& g, uint64_t local) {
     const uint32_t row_bytes = g.row_chunks.d * 16u;
     u32x4 v[kChunksPerThread];
@@ -78,6 +94,7 @@ __device__ void tile_kv16(const MoveRow& r, const MoveGeo& g, uint64_t local) {
 #pragma unroll
     for (int j = 0; j < kChunksPerThread; ++j) {
         q[j] = uint32_t(local * kTileChunks) + uint32_t(j * kThreads) + threadIdx.x;
+        if constexpr (kOrder) q[j] = ordered_chunk(r, g, q[j], true);
         if (q[j] >= r.n) continue;
         // rows past the source's tokens (an image's stale-cell tail) are written as zeros
         const uint32_t row = fdiv(q[j], g.row_chunks);
@@ -97,7 +114,7 @@ __device__ void tile_kv16(const MoveRow& r, const MoveGeo& g, uint64_t local) {
 }
 
 // The same map from f32 rows, rounded to f16: destination chunk q holds 8 halves = 32 source bytes at q * 32.
-template <bool kTable>
+template <bool kTable, bool kOrder = false>
 __device__ void tile_kv32(const MoveRow& r, const MoveGeo& g, uint64_t local) {
     const uint32_t row_bytes = g.row_chunks.d * 16u;
     u32x4 a[kChunksPerThread], b[kChunksPerThread];
@@ -106,6 +123,7 @@ __device__ void tile_kv32(const MoveRow& r, const MoveGeo& g, uint64_t local) {
 #pragma unroll
     for (int j = 0; j < kChunksPerThread; ++j) {
         q[j] = uint32_t(local * kTileChunks) + uint32_t(j * kThreads) + threadIdx.x;
+        if constexpr (kOrder) q[j] = ordered_chunk(r, g, q[j], true);
         if (q[j] >= r.n) continue;
         const uint32_t row = fdiv(q[j], g.row_chunks);
         if (fdiv(row, g.heads) < uint32_t(r.aux)) {
@@ -155,6 +173,7 @@ __device__ void tile_rec(const MoveRow& r, const MoveGeo& g, uint64_t local) {
 // Whole pages between a contiguous run and a paged pool.  Scattering, the packed source does not depend on the
 // table, so its loads are issued before the table is read and the table's latency hides behind them (a
 // table-first order measured about 20% slower); gathering, the table must come first.
+template <bool kOrder = false>
 __device__ void tile_pages(const MoveRow& r, const MoveGeo& g, uint64_t local, bool scatter) {
     const uint64_t page_bytes = uint64_t(g.page_chunks.d) * 16u;
     u32x4 v[kChunksPerThread];
@@ -162,9 +181,10 @@ __device__ void tile_pages(const MoveRow& r, const MoveGeo& g, uint64_t local, b
     if (scatter) {
         uint32_t q[kChunksPerThread];
         int32_t phys[kChunksPerThread];
-#pragma unroll
+    #pragma unroll
         for (int j = 0; j < kChunksPerThread; ++j) {
             q[j] = uint32_t(local * kTileChunks) + uint32_t(j * kThreads) + threadIdx.x;
+            if constexpr (kOrder) q[j] = ordered_chunk(r, g, q[j], false);
             if (q[j] < r.n) v[j] = ld16_stream(r.src + uint64_t(q[j]) * 16u);
         }
 #pragma unroll
@@ -464,18 +484,23 @@ sc_move_kernel(const MoveRow* __restrict__ rows, const uint16_t* __restrict__ ti
         const uint64_t local = tile - r.tile0;
         switch (r.kind) {
             case kKv16:
-                if (r.table) tile_kv16<true>(r, geo, local);
+                if (r.order) tile_kv16<true, true>(r, geo, local);
+                else if (r.table) tile_kv16<true>(r, geo, local);
                 else tile_kv16<false>(r, geo, local);
                 break;
             case kKv32:
                 if constexpr (kMix == kMixWide || kMix == kMixAll) {
-                    if (r.table) tile_kv32<true>(r, geo, local);
+                    if (r.order) tile_kv32<true, true>(r, geo, local);
+                    else if (r.table) tile_kv32<true>(r, geo, local);
                     else tile_kv32<false>(r, geo, local);
                 }
                 break;
             case kRec: tile_rec(r, geo, local); break;
             case kConv: tile_conv(r, local, s_conv); break;
-            case kPagesScatter: tile_pages(r, geo, local, true); break;
+            case kPagesScatter:
+                if (r.order) tile_pages<true>(r, geo, local, true);
+                else tile_pages(r, geo, local, true);
+                break;
             case kPagesGather: tile_pages(r, geo, local, false); break;
             case kCopy: tile_copy(r, local, false); break;
             case kZero: tile_copy(r, local, true); break;
@@ -771,9 +796,99 @@ __global__ void ring_table_kernel(int32_t* table, int64_t n_blocks, int64_t n_sl
         table[i] = int32_t(i % n_slots);
 }
 
+// ---- destination order: the pre-pass of a plan whose rows write through page tables ------------------------------
+// (OrderGroup, sc_internal.hpp.)  Three launches, one group (page table) per blockIdx.y.
+
+// The inverse table: inv[table[lp]] = lp for the group's logical pages whose physical page is in the pool.
+__global__ void __launch_bounds__(kThreads) order_scatter_kernel(const OrderGroup* __restrict__ groups) {
+    const OrderGroup& G = groups[blockIdx.y];
+    const int64_t lp = G.lp_lo + int64_t(blockIdx.x) * kThreads + threadIdx.x;
+    if (lp >= G.lp_hi) return;
+    const int32_t p = *(gi32*) (G.table + lp);
+    if (p >= 0 && int64_t(p) < G.ld) G.inv[p] = int32_t(lp);
+}
+
+// Exclusive prefix of one value per thread across the workgroup; `total` gets the sum.
+__device__ __forceinline__ uint32_t block_scan(uint32_t v, uint32_t& total) {
+    __shared__ uint32_t s_wave[kThreads / 64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    uint32_t x = v;
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t y = __shfl_up(x, o);
+        if (lane >= o) x += y;
+    }
+    if (lane == 63) s_wave[wave] = x;
+    __syncthreads();
+    uint32_t before = 0;
+    total = 0;
+    for (int w = 0; w < kThreads / 64; ++w) {
+        if (w < wave) before += s_wave[w];
+        total += s_wave[w];
+    }
+    __syncthreads();   // s_wave is reused by the next call
+    return before + x - v;
+}
+
+// Entries per block of kOrderBlockPages physical pages.
+__global__ void __launch_bounds__(kThreads) order_count_kernel(const OrderGroup* __restrict__ groups) {
+    const OrderGroup& G = groups[blockIdx.y];
+    const uint32_t b = blockIdx.x;
+    if (b >= G.n_blocks) return;
+    const int64_t base = int64_t(b) * kOrderBlockPages;
+    uint32_t c = 0;
+    for (int k = threadIdx.x; k < kOrderBlockPages; k += kThreads)
+        if (base + k < G.ld && G.inv[base + k] >= 0) ++c;
+    uint32_t total;
+    (void) block_scan(c, total);
+    if (threadIdx.x == 0) G.counts[b] = total;
+}
+
+// Each block sums the counts before it, writes its entries, ascending by physical page, at that prefix and clears them
+// from inv; the last block fills the list past the last entry with -1.
+__global__ void __launch_bounds__(kThreads) order_write_kernel(const OrderGroup* __restrict__ groups) {
+    constexpr int kPer = kOrderBlockPages / kThreads;
+    const OrderGroup& G = groups[blockIdx.y];
+    const uint32_t b = blockIdx.x;
+    if (b >= G.n_blocks) return;
+    uint32_t before = 0;
+    for (uint32_t i = threadIdx.x; i < b; i += kThreads) before += G.counts[i];
+    uint32_t prefix;
+    (void) block_scan(before, prefix);
+    const int64_t base = int64_t(b) * kOrderBlockPages + int64_t(threadIdx.x) * kPer;
+    int32_t e[kPer];
+    uint32_t c = 0;
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+        e[k] = base + k < G.ld ? G.inv[base + k] : -1;
+        c += e[k] >= 0 ? 1u : 0u;
+    }
+    uint32_t total;
+    uint32_t at = prefix + block_scan(c, total);
+#pragma unroll
+    for (int k = 0; k < kPer; ++k)
+        if (e[k] >= 0) {
+            G.order[at++] = e[k];
+            G.inv[base + k] = -1;
+        }
+    if (b + 1 == G.n_blocks)
+        for (uint64_t i = uint64_t(prefix) + total + threadIdx.x; i < G.order_len; i += kThreads) G.order[i] = -1;
+}
+
 }  // namespace
 
 // ---- launchers (host) ------------------------------------------------------------------------------------------
+
+hipError_t launch_page_order(const OrderGroup* groups, int32_t n_groups, int64_t max_pages, uint32_t max_blocks,
+                             hipStream_t stream) {
+    if (n_groups <= 0) return hipSuccess;
+    if (!groups || n_groups > 65535 || max_pages <= 0 || max_blocks == 0) return hipErrorInvalidValue;
+    const dim3 threads(kThreads);
+    hipLaunchKernelGGL(order_scatter_kernel, dim3(unsigned((max_pages + kThreads - 1) / kThreads), unsigned(n_groups)),
+                       threads, 0, stream, groups);
+    hipLaunchKernelGGL(order_count_kernel, dim3(max_blocks, unsigned(n_groups)), threads, 0, stream, groups);
+    hipLaunchKernelGGL(order_write_kernel, dim3(max_blocks, unsigned(n_groups)), threads, 0, stream, groups);
+    return hipGetLastError();
+}
 
 hipError_t launch_batch(const BatchArgs& args, int64_t grid, hipStream_t stream) {
     if (grid <= 0 || args.n_slots < 1 || args.n_slots > kMaxBatchSlots) return hipErrorInvalidValue;

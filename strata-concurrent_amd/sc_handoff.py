@@ -142,6 +142,8 @@ _SIGS = {
     "sc_plan_resume_append": (C.c_int, [_GEO, C.POINTER(BatchDesc), C.POINTER(_P)]),
     "sc_plan_payload_bytes": (_U64, [_P]),
     "sc_plan_set_grid": (C.c_int, [_P, _I64]),
+    "sc_set_order_min_pages": (_I64, [_I64]),
+    "sc_plan_order_groups": (C.c_int, [_P]),
     "sc_plan_destroy": (C.c_int, [_P]),
     "sc_park_async": (C.c_int, [_GEO, C.POINTER(DecodeSlot), _I64, _P, _U64, _P, _P]),
     "sc_resume_async": (C.c_int, [_GEO, _P, _U64, _I64, C.POINTER(DecodeSlot), _P, _P]),
@@ -329,6 +331,12 @@ class DeviceBuffer:
             pass
 
 
+def set_order_min_pages(pages: int) -> int:
+    """Library-wide: tables of at least `pages` logical pages are visited in destination order by plans built from now
+    on (<= 0: never).  Returns the previous value."""
+    return int(lib.sc_set_order_min_pages(pages))
+
+
 class Plan:
     """An owned sc_plan (a device-resident handoff table)."""
 
@@ -345,6 +353,11 @@ class Plan:
 
     def set_grid(self, workgroups: int) -> None:
         check(lib.sc_plan_set_grid(self.handle, workgroups), "sc_plan_set_grid")
+
+    @property
+    def order_groups(self) -> int:
+        """Page tables of the plan visited in destination order."""
+        return int(lib.sc_plan_order_groups(self.handle))
 
     def destroy(self) -> None:
         if self.handle:
