@@ -150,3 +150,41 @@ def test_default_threshold_orders_large_tables_only(sc, oracle, cuda):
         for name, w in want.items():
             assert np.array_equal(got[name].reshape(-1), w), f"T={T}: {name} differs"
         plan.destroy()
+
+
+@pytest.mark.parametrize("fmt", ["int8", "q4"])
+@pytest.mark.parametrize("kind", ["permuted", "holes"])
+@pytest.mark.parametrize("T,pos0,spare", [(77, 0, 0), (61, 6, 9)])
+def test_quantizing_carve_keeps_source_order(sc, oracle, cuda, ordered, fmt, kind, T, pos0, spare):
+    """Quantizing rows keep the source order even where every table would be ordered; their pools still equal the
+    oracle's."""
+    print(f"case quant carve {fmt} {kind} T={T} pos0={pos0} spare={spare}", flush=True)
+    geo = sc.geometry(**GEO)
+    H, D, ps = geo.n_head_kv, geo.head_dim, geo.page_size
+    logical = (pos0 + T + ps - 1) // ps + 1
+    n_pages = logical + spare
+    rng = np.random.default_rng(T * 3 + spare)
+    tables = [_table(rng, logical, n_pages, kind) for _ in range(geo.n_qsa)]
+    case = sc.SyntheticCase(geo, tokens=T, seed=600 + T, kv_dtype=sc.SC_DTYPE_F32)
+    code = sc.SC_KV_INT8 if fmt == "int8" else sc.SC_KV_Q4
+    slot = sc.new_quant_slot(geo, code, logical * ps, n_pages=n_pages, tables=sc.device_tables(tables),
+                             fill=SENTINEL)
+    sc.device_sync()
+    plan = sc.plan_carve_quant(geo, case.prefill, slot, pos0=pos0, with_gdn=False)
+    assert plan.order_groups == 0   # quantizing rows keep the source order
+    plan.launch()
+    sc.device_sync()
+    inputs = case.host_inputs()
+    row = 256 if fmt == "int8" else 144
+    for j in range(geo.n_qsa):
+        for kv in ("k", "v"):
+            codes = np.full(n_pages * H * ps * row, SENTINEL, dtype=np.uint8)
+            scales = np.full(n_pages * H * ps * 4, SENTINEL | SENTINEL << 8, dtype=np.uint16) if fmt == "int8" else None
+            oracle.kv_append_quant(inputs[kv][j], 1 if fmt == "int8" else 2, T, pos0, tables[j], n_pages, H, D, ps,
+                                   codes, scales)
+            got = (slot.k_codes if kv == "k" else slot.v_codes)[j].numpy().view(np.uint8).reshape(-1)
+            assert np.array_equal(got, codes), f"{kv}{j} codes differ"
+            if scales is not None:
+                got_s = (slot.k_scale if kv == "k" else slot.v_scale)[j].numpy().view(np.uint8).reshape(-1)
+                assert np.array_equal(got_s, scales.view(np.uint8)), f"{kv}{j} scales differ"
+    plan.destroy()
