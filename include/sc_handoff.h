@@ -326,7 +326,7 @@ int sc_plan_destroy(sc_plan* plan);
 typedef struct sc_batch_desc {
     int32_t n_slots;               /* 1..64 */
     const int64_t* lens;           /* device [n_slots]: parked tokens L_i, read when the launch runs */
-    int64_t max_tokens;            /* bound on every L_i; a slot outside [0, max_tokens] is skipped and flagged */
+    int64_t max_tokens;            /* bound on every L_i; a slot outside [0, max_tokens] refuses the whole batch */
     const void* staging;           /* device: the parked images back to back (sc_batch_staging_layout) */
     uint64_t staging_bytes;
     int64_t chunk_tokens;          /* the fresh prefill chunk appended to every slot at cell L_i */
@@ -346,12 +346,15 @@ typedef struct sc_batch_desc {
  * device from the device-resident lengths with a wave-level scan; this host twin places the H2D copies. */
 int sc_batch_staging_layout(const sc_geometry* g, const int64_t* lens, int32_t n_slots, uint64_t* offsets,
                             uint64_t* total_bytes);
-/* One launch for every slot: its parked K/V prefix (whole pages, and the partial last page row by row) and its GDN
- * rows from the staging buffer into the arena through its table, and its chunk's K/V at cells [L_i, L_i + chunk)
- * (kv_append's mapping, src/prefill/kernels.cu:567-573, including a start in the middle of a page).  No two
- * workgroups write the same bytes.  Pass 1 of the tiling - each slot's tile count and staging offset - is a
- * wave-level exclusive scan over the slots, the device analogue of the reference's block_scan
- * (src/kernels/cuda/kv_stream.cu:58-80). */
+/* One launch for every slot: its parked K/V prefix and its GDN rows from the staging buffer into the arena through
+ * its table, and its chunk's K/V at cells [L_i, L_i + chunk) (kv_append's mapping, src/prefill/kernels.cu:567-573,
+ * including a start in the middle of a page).  A small pre-pass reads the lengths: the staging offsets are a
+ * wave-level exclusive scan over the slots (the device analogue of the reference's block_scan,
+ * src/kernels/cuda/kv_stream.cu:58-80), and the arena pages the slots' tables name are put in ascending arena order;
+ * the move then assembles each arena page once, in that order (parked cells from the image, chunk cells from the
+ * chunk), so no two workgroups write the same bytes and the arena is written as one ascending run.  If any length is
+ * outside [0, max_tokens] or any image would run past the staging buffer, nothing is written and every lens_out
+ * entry is -1.  The pre-pass uses the plan's workspace: launches of one plan on different streams must not overlap. */
 int sc_plan_resume_append(const sc_geometry* g, const sc_batch_desc* desc, sc_plan** out);
 
 /* ---- park / resume: slot <-> pinned host image ----------------------------------------------------------------- */

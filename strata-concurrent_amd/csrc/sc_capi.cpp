@@ -36,7 +36,8 @@ hipError_t launch_fill_bytes(void* dst, uint8_t value, uint64_t n, hipStream_t s
 hipError_t launch_copy_bytes(void* dst, const void* src, uint64_t n, hipStream_t stream);
 hipError_t launch_decode_probe(const void* kv, uint64_t n_bytes, uint32_t* sink, int64_t workgroups,
                                hipStream_t stream);
-hipError_t launch_batch(const BatchArgs& args, int64_t grid, hipStream_t stream);
+hipError_t launch_batch(const BatchArgs& args, const OrderGroup* arena, uint32_t arena_blocks, int64_t grid,
+                        hipStream_t stream);
 hipError_t launch_delay(uint64_t ticks, uint32_t max_iters, hipStream_t stream);
 hipError_t launch_stream_reset(int32_t* table, int64_t n_blocks, int32_t* slot_block, int32_t* slot_stamp,
                                int32_t* slot_ref, int64_t n_slots, int32_t* ctl, hipStream_t stream);
@@ -1083,7 +1084,8 @@ int sc_plan_order_groups(const sc_plan* plan) { return plan ? plan->n_order_grou
 int sc_plan_launch(const sc_plan* plan, void* stream) {
     if (!plan) return fail(SC_EINVAL, "sc_handoff: missing plan");
     if (plan->batch) {
-        const hipError_t e = sc::launch_batch(plan->batch_args, plan->grid, static_cast<hipStream_t>(stream));
+        const hipError_t e = sc::launch_batch(plan->batch_args, plan->order_groups, plan->order_max_blocks, plan->grid,
+                                              static_cast<hipStream_t>(stream));
         return e == hipSuccess ? ok() : hip_fail(e, "batch launch");
     }
     hipError_t e = launch_order(plan, static_cast<hipStream_t>(stream));
@@ -1276,6 +1278,9 @@ int sc_plan_resume_append(const sc_geometry* g, const sc_batch_desc* d, sc_plan*
             return snapshot_fail("invalid K/V extent");
         if (d->arena_pages < 0 || d->table_pages < (d->max_tokens + d->chunk_tokens + o.ps - 1) / o.ps)
             return snapshot_fail("invalid K/V extent");
+        // arena entries carry the logical page in 25 bits and the arena page in 31
+        if (d->table_pages >= (int64_t(1) << sc::kBatchSlotShift) || d->arena_pages >= (int64_t(1) << 31))
+            return fail(SC_ERANGE, "sc_handoff: page tables beyond 2^25 pages or an arena beyond 2^31 pages");
         // the launch indexes a slot's chunks with 32-bit integers
         if (uint64_t(d->max_tokens / o.ps) * (o.page_bytes / 16) >= kMaxRowChunks ||
             uint64_t(d->chunk_tokens) * uint64_t(o.H) * (o.row_bytes / 16) >= kMaxRowChunks ||
@@ -1326,22 +1331,67 @@ int sc_plan_resume_append(const sc_geometry* g, const sc_batch_desc* d, sc_plan*
         a.table_pages = d->table_pages;
         a.gdn_bytes = uint64_t(o.n_gdn) * o.gdn_row_bytes;
         a.geo = move_geo(o);
-        // an upper bound on the tiles (every slot at max_tokens) sizes the grid; the kernel walks the real ones
-        const uint64_t full = uint64_t(d->max_tokens / o.ps) * (o.page_bytes / 16);
-        const uint64_t per_blob = (full + sc::kTileChunks - 1) / sc::kTileChunks + 1 +
-                                  (uint64_t(d->chunk_tokens) * uint64_t(o.H) * (o.row_bytes / 16) + sc::kTileChunks - 1) /
-                                      sc::kTileChunks;
-        const uint64_t per_slot = 2 * uint64_t(o.n_qsa) * per_blob + (a.gdn_bytes / 16 + sc::kTileChunks - 1) / sc::kTileChunks;
+        // The arena pages a launch can write: at most every arena page, at most every slot at max_tokens.  The K/V
+        // tiles of a blob cover that many pages in ascending arena order; pages past the ones the lengths reach are
+        // -1 entries and move nothing.
+        const uint64_t page_chunks = o.page_bytes / 16;
+        const uint64_t slot_pages = uint64_t((d->max_tokens + d->chunk_tokens + o.ps - 1) / o.ps);
+        const uint64_t pages = o.n_qsa > 0 ? std::min<uint64_t>(uint64_t(d->arena_pages), slot_pages * uint64_t(d->n_slots))
+                                           : 0;
+        const uint64_t kv_tiles = (pages * page_chunks + sc::kTileChunks - 1) / sc::kTileChunks;
+        if (kv_tiles * sc::kTileChunks >= kMaxRowChunks) return fail(SC_ERANGE, "sc_handoff: an arena beyond 2^31 chunks");
+        const uint64_t order_len = (kv_tiles * sc::kTileChunks + page_chunks - 1) / page_chunks;
+        a.kv_tiles = uint32_t(kv_tiles);
+        a.kv_tiles_div = sc::make_fastdiv(uint32_t(std::max<uint64_t>(kv_tiles, 1)));
+        a.gdn_tiles = uint32_t((a.gdn_bytes / 16 + sc::kTileChunks - 1) / sc::kTileChunks);
+        a.gdn_tiles_div = sc::make_fastdiv(std::max<uint32_t>(a.gdn_tiles, 1));
+        const uint64_t tiles = 2 * uint64_t(o.n_qsa) * kv_tiles + uint64_t(d->n_slots) * a.gdn_tiles;
         sc_plan* p = new (std::nothrow) sc_plan();
         if (!p) return fail(SC_ENOMEM, "sc_handoff: plan allocation failed");
         p->batch = true;
-        p->grid = p->default_grid =
-            int64_t(std::min<uint64_t>(std::max<uint64_t>(per_slot * uint64_t(d->n_slots), 1), kMaxGrid));
+        p->grid = p->default_grid = int64_t(std::min<uint64_t>(std::max<uint64_t>(tiles, 1), kMaxGrid));
         p->payload = 0;   // depends on the device-resident lengths
+        // workspace: [slots][ok][arena order group][inv][order pairs][counts]
+        auto up = [](uint64_t x) { return (x + 255) / 256 * 256; };
+        const uint32_t n_blocks = uint32_t((uint64_t(d->arena_pages) + sc::kOrderBlockPages - 1) / sc::kOrderBlockPages);
+        const uint64_t at_ok = up(sizeof(sc::BatchSlot) * sc::kMaxBatchSlots), at_group = at_ok + 256,
+                       at_inv = at_group + up(sizeof(sc::OrderGroup)), at_order = at_inv + up(uint64_t(d->arena_pages) * 4),
+                       at_counts = at_order + up(2 * order_len * 4), ws_bytes = at_counts + up(uint64_t(n_blocks) * 4);
+        auto release = [&] {
+            if (p->batch_ptrs_dev) (void) hipFree(p->batch_ptrs_dev);
+            if (p->order_ws) (void) hipFree(p->order_ws);
+            delete p;
+        };
         hipError_t e = hipMalloc(reinterpret_cast<void**>(&p->batch_ptrs_dev), ptrs.size() * sizeof(uint64_t));
-        if (e != hipSuccess) { delete p; return fail(SC_ENOMEM, std::string("sc_handoff: descriptor allocation: ") + hipGetErrorString(e)); }
+        if (e == hipSuccess) e = hipMalloc(&p->order_ws, ws_bytes);
+        if (e != hipSuccess) {
+            release();
+            return fail(SC_ENOMEM, std::string("sc_handoff: batch allocation: ") + hipGetErrorString(e));
+        }
+        uint8_t* ws = static_cast<uint8_t*>(p->order_ws);
+        a.slots = reinterpret_cast<sc::BatchSlot*>(ws);
+        a.ok = reinterpret_cast<uint32_t*>(ws + at_ok);
+        a.inv = reinterpret_cast<int32_t*>(ws + at_inv);
+        a.order = reinterpret_cast<const int32_t*>(ws + at_order);
+        sc::OrderGroup arena{};
+        arena.inv = a.inv;
+        arena.order = reinterpret_cast<int32_t*>(ws + at_order);
+        arena.counts = reinterpret_cast<uint32_t*>(ws + at_counts);
+        arena.lp_hi = int64_t(pages);
+        arena.ld = d->arena_pages;
+        arena.order_len = order_len;
+        arena.n_blocks = n_blocks;
+        arena.pairs = 1;
+        p->order_groups = reinterpret_cast<const sc::OrderGroup*>(ws + at_group);
+        p->order_max_blocks = n_blocks;
         e = hipMemcpy(p->batch_ptrs_dev, ptrs.data(), ptrs.size() * sizeof(uint64_t), hipMemcpyHostToDevice);
-        if (e != hipSuccess) { (void) hipFree(p->batch_ptrs_dev); delete p; return hip_fail(e, "descriptor upload"); }
+        if (e == hipSuccess) e = hipMemcpy(ws + at_group, &arena, sizeof arena, hipMemcpyHostToDevice);
+        if (e == hipSuccess) e = hipMemset(ws, 0, at_group);   // slots and ok: nothing valid before the first launch
+        if (e == hipSuccess && d->arena_pages) e = hipMemset(a.inv, 0xFF, uint64_t(d->arena_pages) * 4);
+        if (e != hipSuccess) {
+            release();
+            return hip_fail(e, "batch workspace");
+        }
         a.ptrs = p->batch_ptrs_dev;
         p->batch_args = a;
         *out = p;

@@ -106,7 +106,8 @@ struct OrderGroup {
     int64_t lp_lo, lp_hi;   // the logical pages the plan's rows of this table touch
     int64_t ld;             // physical pages in the pool
     uint64_t order_len;     // >= the pages of the rows' tiles: ceil(tiles * kTileChunks / page chunks)
-    uint32_t n_blocks, pad;
+    uint32_t n_blocks;
+    uint32_t pairs;         // 1: order holds (entry, physical page) pairs, as the batched launch reads it
 };
 
 // Geometry every row of one plan shares.
@@ -124,7 +125,21 @@ struct MoveGeo {
 // Arguments of the batched ragged resume + append launch (sc_plan_resume_append).  `ptrs` is one device block
 // of pointers: [2*n_qsa arenas (K, V of layer j at 2j, 2j+1)] [n_slots*n_qsa*2 chunk sources, slot-major]
 // [n_slots page tables] [n_slots GDN row bases].
+//
+// A launch is a pre-pass and the move.  The pre-pass (one workgroup) checks every slot's length and places its image
+// in the staging buffer (a wave-level scan over the slots), then the arena's destination order is built as for a
+// page table: every slot's logical pages [0, need) scattered into the inverse arena table as (slot << 25 | page),
+// counted and compacted into (entry, arena page) pairs in ascending arena order.  The move then assembles each arena
+// page in that order - its parked cells from the slot's staged image, its chunk cells from the slot's chunk - so the
+// launch writes the arena as one ascending run, and copies every slot's GDN rows.
 constexpr int kMaxBatchSlots = 64;   // one wave64 lane per slot in the offset scan
+constexpr int kBatchSlotShift = 25;  // an arena entry is slot << 25 | logical page (pages < 2^25)
+struct BatchSlot {
+    int64_t len;       // L, or -1 when the batch is refused
+    uint64_t stage;    // staging offset of the slot's image
+    uint64_t stride;   // bytes between the image's K/V blobs
+    int64_t need;      // logical pages the slot writes: ceil((L + chunk) / ps)
+};
 struct BatchArgs {
     const int64_t* lens;
     int64_t* lens_out;
@@ -133,8 +148,17 @@ struct BatchArgs {
     const uint64_t* ptrs;
     int32_t n_slots, n_qsa;
     int64_t max_tokens, chunk_tokens, arena_pages, table_pages;
-    uint64_t gdn_bytes;   // all GDN rows of one slot
+    uint64_t gdn_bytes;      // all GDN rows of one slot
     MoveGeo geo;
+    // the plan's workspace
+    BatchSlot* slots;        // [n_slots]
+    uint32_t* ok;            // 1 when every slot's length is in range and every image fits the staging buffer
+    int32_t* inv;            // [arena_pages] arena page -> slot << 25 | logical page; -1 between launches
+    const int32_t* order;    // [2 * order_len]: (entry, arena page) pairs in ascending arena order, then -1
+    uint32_t kv_tiles;       // tiles per K/V blob: ceil(order_len pages * page chunks / kTileChunks)
+    FastDiv kv_tiles_div;    // kv_tiles, for the blob of a tile
+    uint32_t gdn_tiles;      // tiles per slot's GDN rows
+    FastDiv gdn_tiles_div;
 };
 
 // The rows of one kv_append call (sc_kv_append_async, sc_kv_append_q4_async), carried in the kernel arguments

@@ -532,24 +532,6 @@ __device__ __forceinline__ uint64_t wave_scan(uint64_t v, int lane) {
 
 __device__ __forceinline__ uint64_t align_up(uint64_t x, uint64_t a) { return (x + a - 1) / a * a; }
 
-// The tiles of one slot: its K/V blobs each take full-page tiles, at most one partial-page tile and the chunk's
-// tiles; the GDN rows follow.
-struct SlotTiles {
-    uint64_t full_pages, rem_cells, t_full, t_part, t_chunk, per_blob, t_gdn, total;
-};
-__device__ __forceinline__ SlotTiles slot_tiles(const BatchArgs& a, int64_t L) {
-    SlotTiles t;
-    const uint64_t ps = a.geo.page_size.d, H = a.geo.heads.d, rc = a.geo.row_chunks.d;
-    t.full_pages = uint64_t(L) / ps;
-    t.rem_cells = uint64_t(L) % ps;
-    t.t_full = (t.full_pages * a.geo.page_chunks.d + kTileChunks - 1) / kTileChunks;
-    t.t_part = t.rem_cells ? 1 : 0;   // rem_cells * H rows of rc chunks always fit one tile (checked at plan time)
-    t.t_chunk = (uint64_t(a.chunk_tokens) * H * rc + kTileChunks - 1) / kTileChunks;
-    t.per_blob = t.t_full + t.t_part + t.t_chunk;
-    t.t_gdn = (a.gdn_bytes / 16 + kTileChunks - 1) / kTileChunks;
-    t.total = 2 * uint64_t(a.n_qsa) * t.per_blob + t.t_gdn;
-    return t;
-}
 // Bytes of a slot's parked image (K/V blobs of ceil(L/ps) cells, 64-byte aligned, then the GDN rows).
 __device__ __forceinline__ uint64_t kv_blob_stride(const BatchArgs& a, int64_t L) {
     const uint64_t ps = a.geo.page_size.d;
@@ -557,116 +539,120 @@ __device__ __forceinline__ uint64_t kv_blob_stride(const BatchArgs& a, int64_t L
     return align_up(cells * a.geo.heads.d * a.geo.row_chunks.d * 16, 64);
 }
 
-__global__ void __launch_bounds__(kThreads) sc_batch_kernel(BatchArgs a) {
-    // Per-slot constants, computed once per workgroup by wave 0 so the tile loop does no 64-bit division.
-    __shared__ uint64_t s_stage[kMaxBatchSlots];       // staging offset of the slot's image
-    __shared__ uint64_t s_stride[kMaxBatchSlots];      // bytes between the slot image's K/V blobs
-    __shared__ uint64_t s_tile0[kMaxBatchSlots + 1];   // first tile of the slot; [n_slots] = total
-    __shared__ int64_t s_len[kMaxBatchSlots];
-    __shared__ uint32_t s_full[kMaxBatchSlots], s_rem[kMaxBatchSlots];
-    __shared__ uint32_t s_tfull[kMaxBatchSlots], s_tpart[kMaxBatchSlots], s_perblob[kMaxBatchSlots];
-    // Pass 1, by wave 0 of every workgroup: each lane one slot; the staging offsets and the tile ranges are two
-    // exclusive scans over the slots' ragged sizes.  The batch is all or nothing, like a restore that validates
-    // before its first write: if any slot's length is out of range or its image would run past the staging
-    // buffer, no slot gets a tile and every lens_out entry is -1.
-    if (threadIdx.x < 64) {
-        const int lane = threadIdx.x;
-        const bool live = lane < a.n_slots;
-        const int64_t L = live ? a.lens[lane] : 0;
-        bool ok = !live || (L >= 0 && L <= a.max_tokens);
-        const uint64_t stride = live && ok ? kv_blob_stride(a, L) : 0;
-        const uint64_t image = live && ok ? align_up(2 * uint64_t(a.n_qsa) * stride + a.gdn_bytes, 64) : 0;
-        const uint64_t padded = align_up(image, 256);
-        const uint64_t stage_end = wave_scan(padded, lane);
-        if (stage_end > a.staging_bytes) ok = false;
-        ok = __ballot(!ok) == 0;   // every lane agrees: the whole batch is valid
-        SlotTiles t{};
-        if (ok && live) t = slot_tiles(a, L);
-        const uint64_t tiles = ok && live ? t.total : 0;
-        const uint64_t tile_end = wave_scan(tiles, lane);
-        if (live) {
-            s_len[lane] = ok ? L : -1;
-            s_stage[lane] = stage_end - padded;
-            s_stride[lane] = stride;
-            s_tile0[lane] = tile_end - tiles;
-            s_full[lane] = uint32_t(t.full_pages);
-            s_rem[lane] = uint32_t(t.rem_cells);
-            s_tfull[lane] = uint32_t(t.t_full);
-            s_tpart[lane] = uint32_t(t.t_part);
-            s_perblob[lane] = uint32_t(t.per_blob);
+// The batch's pre-pass, one wave: each lane one slot.  The staging offsets are an exclusive scan over the slots'
+// padded image sizes.  The batch is all or nothing, like a restore that validates before its first write: if any
+// slot's length is out of range or its image would run past the staging buffer, `ok` is 0, nothing is written and
+// every lens_out entry is -1.
+__global__ void __launch_bounds__(64) batch_prep_kernel(BatchArgs a) {
+    const int lane = threadIdx.x;
+    const bool live = lane < a.n_slots;
+    const int64_t L = live ? a.lens[lane] : 0;
+    bool ok = !live || (L >= 0 && L <= a.max_tokens);
+    const uint64_t stride = live && ok ? kv_blob_stride(a, L) : 0;
+    const uint64_t image = live && ok ? align_up(2 * uint64_t(a.n_qsa) * stride + a.gdn_bytes, 64) : 0;
+    const uint64_t padded = align_up(image, 256);
+    const uint64_t stage_end = wave_scan(padded, lane);
+    if (stage_end > a.staging_bytes) ok = false;
+    ok = __ballot(!ok) == 0;   // every lane agrees: the whole batch is valid
+    if (live) {
+        const uint64_t ps = a.geo.page_size.d;
+        BatchSlot& S = a.slots[lane];
+        S.len = ok ? L : -1;
+        S.stage = stage_end - padded;
+        S.stride = stride;
+        S.need = ok ? int64_t((uint64_t(L) + uint64_t(a.chunk_tokens) + ps - 1) / ps) : 0;
+        if (a.lens_out) a.lens_out[lane] = ok ? L + a.chunk_tokens : -1;
+    }
+    if (lane == 0) *a.ok = ok ? 1u : 0u;
+}
+
+// Every slot's logical pages into the inverse arena table (blockIdx.y = slot).
+__global__ void __launch_bounds__(kThreads) batch_inverse_kernel(BatchArgs a) {
+    const int slot = blockIdx.y;
+    const int64_t lp = int64_t(blockIdx.x) * kThreads + threadIdx.x;
+    if (lp >= a.slots[slot].need) return;   // 0 for every slot of a refused batch
+    const int32_t* table = reinterpret_cast<const int32_t*>(a.ptrs[2 * a.n_qsa + uint64_t(a.n_slots) * a.n_qsa * 2 + slot]);
+    const int32_t p = *(gi32*) (table + lp);
+    if (p >= 0 && int64_t(p) < a.arena_pages) a.inv[p] = int32_t((uint32_t(slot) << kBatchSlotShift) | uint32_t(lp));
+}
+
+// One 16 KiB tile of arena pages of K/V blob `blob` (K, V of layer blob / 2), in ascending arena order.  A page's
+// chunk ip is row (h * ps + c) of the page, chunk ch: cell c of logical page lp is token lp * ps + c of its slot, from
+// the staged image (whose pages have the arena's layout) below L and from the slot's chunk ([chunk][H][D], kv_append's
+// mapping) in [L, L + chunk); cells past L + chunk are left alone.
+// The slots' placement, staged in LDS by every workgroup of the move: a page's source address then costs the
+// order's load and an LDS read, not a second global load.
+struct BatchSlotsLds {
+    int64_t len[kMaxBatchSlots];
+    uint64_t stage[kMaxBatchSlots], stride[kMaxBatchSlots];
+};
+
+__device__ void batch_page_tile(const BatchArgs& a, const BatchSlotsLds& S, uint32_t blob, uint32_t w) {
+    const MoveGeo& g = a.geo;
+    const uint64_t page_bytes = uint64_t(g.page_chunks.d) * 16u, row_bytes = uint64_t(g.row_chunks.d) * 16u;
+    const uint64_t* chunks = a.ptrs + 2 * a.n_qsa;
+    uint8_t* arena = reinterpret_cast<uint8_t*>(a.ptrs[blob]);
+    u32x4 v[kChunksPerThread];
+    int64_t dst[kChunksPerThread];
+    using gi64 = __attribute__((address_space(1))) const int64_t;
+#pragma unroll
+    for (int j = 0; j < kChunksPerThread; ++j) {
+        dst[j] = -1;
+        const uint32_t vq = w * kTileChunks + uint32_t(j * kThreads) + threadIdx.x;
+        const uint32_t vp = fdiv(vq, g.page_chunks);
+        const uint32_t ip = vq - vp * g.page_chunks.d;
+        const int64_t pair = *(gi64*) (a.order + 2 * uint64_t(vp));   // (entry, arena page), little-endian
+        const int32_t e = int32_t(uint32_t(pair)), phys = int32_t(uint32_t(uint64_t(pair) >> 32));
+        if (e < 0) continue;
+        const uint32_t slot = uint32_t(e) >> kBatchSlotShift, lp = uint32_t(e) & ((1u << kBatchSlotShift) - 1u);
+        const int64_t L = S.len[slot];
+        const uint32_t row = fdiv(ip, g.row_chunks), ch = ip - row * g.row_chunks.d;
+        const uint32_t h = fdiv(row, g.page_size), c = row - h * g.page_size.d;
+        const int64_t token = int64_t(lp) * g.page_size.d + c;
+        if (token < L) {
+            v[j] = ld16_stream(a.staging + S.stage[slot] + uint64_t(blob) * S.stride[slot] + uint64_t(lp) * page_bytes +
+                               ip * 16u);
+        } else if (token < L + a.chunk_tokens) {
+            const uint8_t* src = reinterpret_cast<const uint8_t*>(chunks[(uint64_t(slot) * a.n_qsa + blob / 2) * 2 + (blob & 1)]);
+            v[j] = ld16(src + (uint64_t(token - L) * g.heads.d + h) * row_bytes + ch * 16u);
+        } else {
+            continue;
         }
-        const uint64_t total = shfl64(tile_end, 63);
-        if (lane == 0) s_tile0[a.n_slots] = total;
-        if (blockIdx.x == 0 && live && a.lens_out) a.lens_out[lane] = ok ? L + a.chunk_tokens : -1;
+        dst[j] = int64_t(phys) * int64_t(page_bytes) + int64_t(ip) * 16;
+    }
+#pragma unroll
+    for (int j = 0; j < kChunksPerThread; ++j)
+        if (dst[j] >= 0) st16(arena + dst[j], v[j]);
+}
+
+// A refused batch writes nothing: its order holds no page (every slot's `need` is 0) and its slots' lengths are -1,
+// which the GDN tiles check.
+__global__ void __launch_bounds__(kThreads) sc_batch_kernel(BatchArgs a) {
+    __shared__ BatchSlotsLds S;
+    if (threadIdx.x < uint32_t(a.n_slots)) {
+        const BatchSlot& x = a.slots[threadIdx.x];
+        S.len[threadIdx.x] = x.len;
+        S.stage[threadIdx.x] = x.stage;
+        S.stride[threadIdx.x] = x.stride;
     }
     __syncthreads();
-    const uint64_t total = s_tile0[a.n_slots];
-    const MoveGeo& g = a.geo;
-    const uint64_t row_bytes = uint64_t(g.row_chunks.d) * 16, page_bytes = uint64_t(g.page_chunks.d) * 16;
-    const uint64_t* arenas = a.ptrs;
-    const uint64_t* chunks = a.ptrs + 2 * a.n_qsa;
-    const uint64_t* tables = chunks + uint64_t(a.n_slots) * a.n_qsa * 2;
-    const uint64_t* gdns = tables + a.n_slots;
-    const uint32_t kv_tiles_factor = 2u * uint32_t(a.n_qsa);
+    const uint64_t kv_tiles = 2 * uint64_t(a.n_qsa) * a.kv_tiles;
+    const uint64_t total = kv_tiles + uint64_t(a.n_slots) * a.gdn_tiles;
+    const uint64_t* gdns = a.ptrs + 2 * a.n_qsa + uint64_t(a.n_slots) * a.n_qsa * 2 + a.n_slots;
     for (uint64_t tile = blockIdx.x; tile < total; tile += gridDim.x) {
-        int lo = 0, hi = a.n_slots - 1;
-        while (lo < hi) {
-            const int mid = (lo + hi + 1) >> 1;
-            if (s_tile0[mid] <= tile) lo = mid; else hi = mid - 1;
-        }
-        const int slot = __builtin_amdgcn_readfirstlane(lo);
-        const int64_t L = s_len[slot];
-        const uint32_t per_blob = s_perblob[slot], t_full = s_tfull[slot], t_part = s_tpart[slot];
-        const uint32_t full_pages = s_full[slot];
-        const uint32_t lt = uint32_t(tile - s_tile0[slot]);
-        const uint8_t* image = a.staging + s_stage[slot];
-        const uint64_t stride = s_stride[slot];
-        const int32_t* table = reinterpret_cast<const int32_t*>(tables[slot]);
-        if (lt < kv_tiles_factor * per_blob) {
-            const uint32_t blob = lt / per_blob;
-            const uint32_t w = lt - blob * per_blob;
-            const uint8_t* src_blob = image + uint64_t(blob) * stride;
-            uint8_t* arena = reinterpret_cast<uint8_t*>(arenas[blob]);
-            if (w < t_full) {
-                // whole parked pages: image page p -> arena page table[p]; the packed loads go out before the
-                // table is read
-                MoveRow r{};
-                r.src = src_blob;
-                r.dst = arena;
-                r.table = table;
-                r.n = uint64_t(full_pages) * g.page_chunks.d;
-                r.ld = a.arena_pages;
-                tile_pages(r, g, w, true);
-            } else if (w < t_full + t_part) {
-                // the partial last page: only its parked cells, so the chunk's cells of that page are not raced
-                const uint32_t n = s_rem[slot] * g.heads.d * g.row_chunks.d;
-                const int64_t phys = full_pages < uint64_t(a.table_pages) ? int64_t(table[full_pages]) : -1;
-                for (uint32_t q = threadIdx.x; q < n && phys >= 0 && phys < a.arena_pages; q += kThreads) {
-                    const uint32_t r = fdiv(q, g.row_chunks);
-                    const uint32_t ch = q - r * g.row_chunks.d;
-                    const uint32_t c = fdiv(r, g.heads), h = r - c * g.heads.d;
-                    const uint64_t in_page = (uint64_t(h) * g.page_size.d + c) * row_bytes + ch * 16u;
-                    st16(arena + uint64_t(phys) * page_bytes + in_page,
-                         ld16(src_blob + uint64_t(full_pages) * page_bytes + in_page));
-                }
-            } else {
-                // the fresh chunk's rows at cells L + t (kv_append's mapping)
-                MoveRow r{};
-                r.src = reinterpret_cast<const uint8_t*>(chunks[(uint64_t(slot) * a.n_qsa + blob / 2) * 2 + (blob & 1)]);
-                r.dst = arena;
-                r.table = table;
-                r.n = uint64_t(a.chunk_tokens) * g.heads.d * g.row_chunks.d;
-                r.pos0 = L;
-                r.ld = a.arena_pages;
-                r.aux = int32_t(a.chunk_tokens);
-                tile_kv16<true>(r, g, w - t_full - t_part);
-            }
+        if (tile < kv_tiles) {
+            const uint32_t t = uint32_t(tile);
+            const uint32_t blob = __builtin_amdgcn_readfirstlane(fdiv(t, a.kv_tiles_div));
+            batch_page_tile(a, S, blob, t - blob * a.kv_tiles);
         } else {
+            const uint32_t t = uint32_t(tile - kv_tiles);
+            const uint32_t slot = __builtin_amdgcn_readfirstlane(fdiv(t, a.gdn_tiles_div));
+            if (S.len[slot] < 0) continue;
             MoveRow r{};
-            r.src = image + uint64_t(kv_tiles_factor) * stride;
+            r.src = a.staging + S.stage[slot] + 2 * uint64_t(a.n_qsa) * S.stride[slot];
             r.dst = reinterpret_cast<uint8_t*>(gdns[slot]);
             r.n = a.gdn_bytes / 16;
-            tile_copy(r, lt - kv_tiles_factor * per_blob, false);
+            tile_copy(r, t - slot * a.gdn_tiles, false);
         }
     }
 }
@@ -864,14 +850,18 @@ __global__ void __launch_bounds__(kThreads) order_write_kernel(const OrderGroup*
     }
     uint32_t total;
     uint32_t at = prefix + block_scan(c, total);
+    const uint32_t width = G.pairs ? 2u : 1u;
 #pragma unroll
     for (int k = 0; k < kPer; ++k)
         if (e[k] >= 0) {
-            G.order[at++] = e[k];
+            G.order[uint64_t(at) * width] = e[k];
+            if (G.pairs) G.order[uint64_t(at) * width + 1] = int32_t(base + k);
+            ++at;
             G.inv[base + k] = -1;
         }
     if (b + 1 == G.n_blocks)
-        for (uint64_t i = uint64_t(prefix) + total + threadIdx.x; i < G.order_len; i += kThreads) G.order[i] = -1;
+        for (uint64_t i = (uint64_t(prefix) + total) * width + threadIdx.x; i < G.order_len * width; i += kThreads)
+            G.order[i] = -1;
 }
 
 }  // namespace
@@ -890,8 +880,19 @@ hipError_t launch_page_order(const OrderGroup* groups, int32_t n_groups, int64_t
     return hipGetLastError();
 }
 
-hipError_t launch_batch(const BatchArgs& args, int64_t grid, hipStream_t stream) {
-    if (grid <= 0 || args.n_slots < 1 || args.n_slots > kMaxBatchSlots) return hipErrorInvalidValue;
+hipError_t launch_batch(const BatchArgs& args, const OrderGroup* arena, uint32_t arena_blocks, int64_t grid,
+                        hipStream_t stream) {
+    if (grid <= 0 || args.n_slots < 1 || args.n_slots > kMaxBatchSlots || !args.slots || !args.ok)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(batch_prep_kernel, dim3(1), dim3(64), 0, stream, args);
+    if (args.n_qsa > 0 && args.kv_tiles > 0) {
+        if (!arena || !arena_blocks || args.table_pages <= 0) return hipErrorInvalidValue;
+        hipLaunchKernelGGL(batch_inverse_kernel, dim3(unsigned((args.table_pages + kThreads - 1) / kThreads),
+                                                      unsigned(args.n_slots)),
+                           dim3(kThreads), 0, stream, args);
+        hipLaunchKernelGGL(order_count_kernel, dim3(arena_blocks, 1), dim3(kThreads), 0, stream, arena);
+        hipLaunchKernelGGL(order_write_kernel, dim3(arena_blocks, 1), dim3(kThreads), 0, stream, arena);
+    }
     hipLaunchKernelGGL(sc_batch_kernel, dim3(unsigned(grid)), dim3(kThreads), 0, stream, args);
     return hipGetLastError();
 }
