@@ -75,10 +75,13 @@ def link_at(sc, dev_ptr: int, host_ptr: int, n: int, reps: int = 3) -> tuple[flo
     return out[0], out[1]
 
 
-def link_fracs(gbps: float, probe: float, small_probe: float) -> dict:
-    """A host-link rate against the same-size probe, the 256 MiB probe and the PCIe Gen5 x16 line rate."""
-    return {"frac_of_probe": round(gbps / probe, 3), "frac_of_small_probe": round(gbps / small_probe, 3),
-            "frac_of_pcie5_x16": round(gbps / PCIE5_X16_GBPS, 3)}
+def link_fracs(gbps: float, probe: float, small_probe: float | None = None) -> dict:
+    """A host-link rate against the same-size probe, the 256 MiB probe (when given) and the PCIe Gen5 x16 line rate."""
+    out = {"frac_of_probe": round(gbps / probe, 3)}
+    if small_probe:
+        out["frac_of_small_probe"] = round(gbps / small_probe, 3)
+    out["frac_of_pcie5_x16"] = round(gbps / PCIE5_X16_GBPS, 3)
+    return out
 
 
 def settle_link(sc, floor_gbps: float, limit_s: float = 3.0) -> float:
@@ -358,6 +361,38 @@ def paged_carve(sc, geo, case, tokens: int, stream) -> dict:
                      "small kernels) before the move kernel"}
     source_order.destroy()
     paged.destroy()
+    # park and resume of the paged slot itself: its pages go through the tables straight to and from pinned memory
+    _, total = sc.image_layout(geo, tokens)
+    host = sc.PinnedBuffer(total)
+    dev = sc.DeviceBuffer(total, "uint8")
+    side = sc.Stream()
+    sc.park_async(geo, paged_slot, tokens, host.ptr, total, stream=side)   # warm-up: touch the pinned pages
+    side.sync()
+    probe_h2d, probe_d2h = link_at(sc, dev.ptr, host.ptr, total)
+    dev.free()
+    e0, e1 = sc.Event(), sc.Event()
+    pk, rs = [], []
+    for _ in range(5):
+        e0.record(side)
+        sc.park_async(geo, paged_slot, tokens, host.ptr, total, stream=side)
+        e1.record(side)
+        e1.sync()
+        pk.append(e0.elapsed_ms(e1))
+        e0.record(side)
+        sc.resume_async(geo, host.ptr, total, tokens, paged_slot, stream=side)
+        e1.record(side)
+        e1.sync()
+        rs.append(e0.elapsed_ms(e1))
+    host.free()
+    pk_ms, rs_ms = sorted(pk)[2], sorted(rs)[2]
+    out["park_resume"] = {
+        "bytes": total, "park_ms": round(pk_ms, 3), "resume_ms": round(rs_ms, 3),
+        "park_gbps": round(total / (pk_ms * 1e-3) / 1e9, 2), "resume_gbps": round(total / (rs_ms * 1e-3) / 1e9, 2),
+        "park_vs_link": link_fracs(total / (pk_ms * 1e-3) / 1e9, probe_d2h),
+        "resume_vs_link": link_fracs(total / (rs_ms * 1e-3) / 1e9, probe_h2d),
+        "method": "p50 of 5; sc_park_async / sc_resume_async of the paged slot: one kernel per 32 layers moves every "
+                  "K/V page through its table straight between the pool and the pinned image, then one copy of the "
+                  "GDN rows; the probe is a plain pinned copy of the same byte count"}
     for b in paged_slot.buffers():
         b.free()
     for t in tables:

@@ -359,13 +359,16 @@ int sc_plan_resume_append(const sc_geometry* g, const sc_batch_desc* desc, sc_pl
 
 /* ---- park / resume: slot <-> pinned host image ----------------------------------------------------------------- */
 
-/* Park: copy a decode slot (identity page tables) into a pinned host image of sc_image_layout(tokens), with
- * hipMemcpyAsync on `stream`, one copy per blob; records `done` (a hipEvent_t, may be NULL) after the last.
- * Replaces conversation_kv_save's synchronous per-16-MiB cudaMemcpy loop (conversation_snapshot.cpp:105-113,
- * 160-171) and conversation_checkpoint_save's GDN copy (conversation_state.cpp:235). */
+/* Park: copy a decode slot into a pinned host image of sc_image_layout(tokens) on `stream`; records `done` (a
+ * hipEvent_t, may be NULL) after the last copy.  An identity-layout slot takes one hipMemcpyAsync per blob; a paged
+ * slot (any non-null page table) has its K/V pages gathered through the tables straight into the pinned image by a
+ * kernel that writes the host memory itself (no staging copy in HBM, nothing allocated; 32 layers per launch), then
+ * its GDN rows by one copy.  Replaces conversation_kv_save's synchronous per-16-MiB cudaMemcpy loop
+ * (conversation_snapshot.cpp:105-113, 160-171) and conversation_checkpoint_save's GDN copy (conversation_state.cpp:235). */
 int sc_park_async(const sc_geometry* g, const sc_decode_slot* slot, int64_t tokens, void* host_image,
                   uint64_t image_bytes, void* stream, void* done);
-/* Resume: the inverse, H2D.  Replaces conversation_kv_restore (conversation_snapshot.cpp:196-204) and
+/* Resume: the inverse, H2D (a paged slot's pages scattered through its tables by a kernel that reads the pinned
+ * image itself).  Replaces conversation_kv_restore (conversation_snapshot.cpp:196-204) and
  * conversation_checkpoint_restore's GDN copy (conversation_state.cpp:251). */
 int sc_resume_async(const sc_geometry* g, const void* host_image, uint64_t image_bytes, int64_t tokens,
                     const sc_decode_slot* slot, void* stream, void* done);

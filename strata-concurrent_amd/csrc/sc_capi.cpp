@@ -27,6 +27,7 @@ hipError_t launch_move(const MoveRow* rows, const uint16_t* tile_row, const Move
                        int64_t grid, int32_t mix, hipStream_t stream, const uint32_t* gate = nullptr);
 hipError_t launch_page_order(const OrderGroup* groups, int32_t n_groups, int64_t max_pages, uint32_t max_blocks,
                              hipStream_t stream);
+hipError_t launch_paged_image(const PagedImage& a, const MoveGeo& geo, hipStream_t stream);
 hipError_t launch_fill_uniform_f16(uint16_t* dst, uint64_t n, float lo, float hi, uint64_t seed, uint64_t sid,
                                    hipStream_t stream);
 hipError_t launch_fill_uniform_f32(float* dst, uint64_t n, float lo, float hi, uint64_t seed, uint64_t sid,
@@ -1410,9 +1411,8 @@ static int dma_image(const sc_geometry* g, const sc_decode_slot* slot, int64_t t
     const int64_t cells = cells_of(o, tokens);
     int rc = check_slot(o, slot, tokens, true);
     if (rc) return rc;
-    if (cells / o.ps > slot->n_pages) return snapshot_fail("invalid K/V extent");
-    if (!slot_identity(slot, o.n_qsa))
-        return fail(SC_EINVAL, "sc_handoff: park/resume copies identity-layout pools; capture a paged slot first");
+    const bool identity = slot_identity(slot, o.n_qsa);
+    if (identity && cells / o.ps > slot->n_pages) return snapshot_fail("invalid K/V extent");
     uint64_t total = 0;
     const auto blobs = image_blobs(o, tokens, total);
     if (!host || image_bytes < total) return snapshot_fail("invalid K/V payload size");
@@ -1427,7 +1427,37 @@ static int dma_image(const sc_geometry* g, const sc_decode_slot* slot, int64_t t
     }
     const hipStream_t s = static_cast<hipStream_t>(stream);
     size_t b = 0;
-    for (int64_t j = 0; j < o.n_qsa; ++j, b += 2) {
+    // A paged slot: its pages go through the tables between the pools and the pinned image, moved by a kernel that
+    // reads or writes the host memory itself (measured at 95-99% of a plain DMA of the same bytes), kPagedLayers
+    // layers per launch.  The K/V blobs of an image are equal and 64-byte aligned, so blob b sits at b * stride.
+    if (!identity && o.n_qsa > 0) {
+        const uint64_t stride = blobs.size() > 1 ? blobs[1].offset : round_up(blobs[0].bytes, kBlobAlign);
+        const uint64_t chunks = blobs[0].bytes / 16;
+        const uint64_t tiles = (chunks + sc::kTileChunks - 1) / sc::kTileChunks;
+        if (chunks >= kMaxRowChunks || tiles * 2 * sc::kPagedLayers >= (uint64_t(1) << 32))
+            return fail(SC_ERANGE, "sc_handoff: a K/V blob beyond 2^31 chunks");
+        for (int64_t j0 = 0; j0 < o.n_qsa; j0 += sc::kPagedLayers) {
+            const int64_t n = std::min<int64_t>(sc::kPagedLayers, o.n_qsa - j0);
+            sc::PagedImage a{};
+            for (int64_t j = 0; j < n; ++j) {
+                a.pool[2 * j] = reinterpret_cast<uint8_t*>(slot->k_pool[j0 + j]);
+                a.pool[2 * j + 1] = reinterpret_cast<uint8_t*>(slot->v_pool[j0 + j]);
+                a.table[j] = slot->page_table ? slot->page_table[j0 + j] : nullptr;
+            }
+            a.image = host + uint64_t(2 * j0) * stride;
+            a.blob_stride = stride;
+            a.blob_chunks = chunks;
+            a.pool_pages = slot->n_pages;
+            a.n_blobs = uint32_t(2 * n);
+            a.park = park ? 1u : 0u;
+            a.tiles_per_blob = uint32_t(tiles);
+            a.tiles_div = sc::make_fastdiv(uint32_t(std::max<uint64_t>(tiles, 1)));
+            const hipError_t e = sc::launch_paged_image(a, move_geo(o), s);
+            if (e != hipSuccess) return hip_fail(e, park ? "paged park" : "paged resume");
+        }
+        b = 2 * size_t(o.n_qsa);
+    }
+    for (int64_t j = identity ? 0 : o.n_qsa; j < o.n_qsa; ++j, b += 2) {
         uint16_t* pools[2] = {slot->k_pool[j], slot->v_pool[j]};
         for (int a = 0; a < 2; ++a) {
             const Blob& blob = blobs[b + a];

@@ -169,6 +169,23 @@ struct AppendRows {
     MoveRow row[kAppendMaxRows];
 };
 
+// A paged slot parked into, or resumed from, a pinned host image by one kernel that writes or reads the mapped host
+// memory itself: every K/V page goes through its layer's table between the pool and the image's packed blob, with no
+// staging copy in HBM and nothing allocated.  Up to kPagedLayers QSA layers per launch, their pointers in the kernel
+// arguments (read through the argument segment with scalar loads).
+constexpr int kPagedLayers = 32;
+struct PagedImage {
+    uint8_t* pool[2 * kPagedLayers];     // K, V of each layer (device)
+    const int32_t* table[kPagedLayers];  // the layer's page table (null: identity)
+    uint8_t* image;                      // the image's first K/V blob of this launch (pinned host memory)
+    uint64_t blob_stride;                // bytes between the image's K/V blobs
+    uint64_t blob_chunks;                // 16-byte chunks per blob: cells * H * row_chunks
+    int64_t pool_pages;                  // physical pages per pool
+    uint32_t n_blobs, park;              // 2 * layers of this launch; 1: pool -> image, 0: image -> pool
+    uint32_t tiles_per_blob;
+    FastDiv tiles_div;
+};
+
 // The parallel FNV-1a (sc_hash.hip): bytes per lane segment, and where its workspace keeps what.
 constexpr int kFnvLaneBytes = 256;
 struct FnvWorkspace {

@@ -864,9 +864,44 @@ __global__ void __launch_bounds__(kThreads) order_write_kernel(const OrderGroup*
             G.order[i] = -1;
 }
 
+// ---- paged park / resume straight through pinned host memory ---------------------------------------------------
+// (PagedImage, sc_internal.hpp.)  The blob of a tile is wave-uniform, so its pool and table pointers are read from the
+// argument segment with scalar loads (indexing the argument array directly would copy it to scratch first).
+__global__ void __launch_bounds__(kThreads) paged_image_kernel(PagedImage a, MoveGeo geo) {
+    using karg = __attribute__((address_space(4))) const PagedImage*;
+    const karg args = (karg) __builtin_amdgcn_kernarg_segment_ptr();
+    const uint64_t total = uint64_t(a.n_blobs) * a.tiles_per_blob;
+    for (uint64_t tile = blockIdx.x; tile < total; tile += gridDim.x) {
+        const uint32_t t = uint32_t(tile);
+        const uint32_t blob = __builtin_amdgcn_readfirstlane(fdiv(t, a.tiles_div));
+        MoveRow r{};
+        uint8_t* image = a.image + uint64_t(blob) * a.blob_stride;
+        r.table = args->table[blob / 2];
+        r.n = a.blob_chunks;
+        r.ld = a.pool_pages;
+        if (a.park) {
+            r.src = args->pool[blob];
+            r.dst = image;
+        } else {
+            r.src = image;
+            r.dst = args->pool[blob];
+        }
+        tile_pages(r, geo, t - blob * a.tiles_per_blob, !a.park);
+    }
+}
+
 }  // namespace
 
 // ---- launchers (host) ------------------------------------------------------------------------------------------
+
+hipError_t launch_paged_image(const PagedImage& a, const MoveGeo& geo, hipStream_t stream) {
+    const uint64_t tiles = uint64_t(a.n_blobs) * a.tiles_per_blob;
+    if (tiles == 0) return hipSuccess;
+    if (!a.image || a.n_blobs > 2u * kPagedLayers || tiles >= (uint64_t(1) << 32)) return hipErrorInvalidValue;
+    const uint64_t grid = tiles < 65536 ? tiles : 65536;
+    hipLaunchKernelGGL(paged_image_kernel, dim3(unsigned(grid)), dim3(kThreads), 0, stream, a, geo);
+    return hipGetLastError();
+}
 
 hipError_t launch_page_order(const OrderGroup* groups, int32_t n_groups, int64_t max_pages, uint32_t max_blocks,
                              hipStream_t stream) {

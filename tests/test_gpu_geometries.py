@@ -86,8 +86,8 @@ def test_gather_scatter_and_park_resume(sc, oracle, cuda, name):
     sc.device_sync()
     want = oracle.expected_slot(geo, case.host_inputs(), slot_cells=max_cells, tables=host_tabs, n_pages=n_pages)
     _compare(want, slot.host_state())
-    # park an identity slot carved from the same inputs to pinned memory (a park copies identity-layout pools; a
-    # paged slot is captured instead) and resume it into a fresh identity slot
+    # park an identity slot carved from the same inputs to pinned memory (one copy per blob) and resume it into a
+    # fresh identity slot
     parked = case.new_slot(max_cells=max_cells)
     case.carve_into(parked)
     sc.device_sync()
@@ -110,4 +110,52 @@ def test_gather_scatter_and_park_resume(sc, oracle, cuda, name):
         else:
             assert np.array_equal(got[key][:extent], ident[key][:extent]), key
             assert np.all(got[key][extent:].view(np.uint8) == 0x5A), key
+    # park the paged slot itself (its pages gathered through the tables straight into pinned memory) and resume the
+    # image into a fresh paged slot (scattered through the tables straight from pinned memory)
+    host.numpy()[:] = 0x33
+    sc.park_async(geo, slot, tokens, host.ptr, total, stream=side, done=done.handle)
+    done.sync()
+    assert np.array_equal(host.numpy()[:total], image.numpy(total)), "paged park"
+    fresh_paged = case.new_slot(max_cells=max_cells, tables=dev_tabs, fill=0)
+    sc.device_sync()
+    sc.resume_async(geo, host.ptr, total, tokens, fresh_paged, stream=side, done=done.handle)
+    done.sync()
+    _compare(want, fresh_paged.host_state())
+    host.free()
+
+
+def test_paged_park_resume_beyond_one_launch(sc, cuda):
+    """40 QSA layers: the paged park and resume take two launches of 32 and 8 layers; the parked image equals the
+    capture of the slot and the resumed slot reads back as the same image."""
+    geo = sc.geometry(n_layers=40, qsa_interval=1, n_head_kv=1, head_dim=64, page_size=8, ssm_state_size=16,
+                      ssm_k_heads=2, ssm_v_heads=2, ssm_d_conv=4, ssm_conv_channels=64, idx_key_dim=64)
+    assert geo.n_qsa == 40
+    tokens, max_cells = 75, 96
+    n_pages = max_cells // geo.page_size + 4
+    rng = np.random.default_rng(40)
+    tabs = sc.device_tables([rng.permutation(n_pages)[: max_cells // geo.page_size].astype(np.int32)
+                             for _ in range(geo.n_qsa)])
+    case = sc.SyntheticCase(geo, tokens, seed=404)
+    slot = case.new_slot(max_cells=max_cells, n_pages=n_pages, tables=tabs)
+    case.carve_into(slot)
+    _, total = sc.image_layout(geo, tokens)
+    image = sc.DeviceBuffer(total, "uint8")
+    image.fill(0)
+    sc.plan_capture(geo, slot, tokens, image.ptr, total).launch()
+    sc.device_sync()
+    host = sc.PinnedBuffer(total)
+    host.numpy()[:] = 0
+    side, done = sc.Stream(), sc.Event()
+    sc.park_async(geo, slot, tokens, host.ptr, total, stream=side, done=done.handle)
+    done.sync()
+    assert np.array_equal(host.numpy()[:total], image.numpy(total)), "paged park"
+    back = case.new_slot(max_cells=max_cells, n_pages=n_pages, tables=tabs, fill=0)
+    sc.device_sync()
+    sc.resume_async(geo, host.ptr, total, tokens, back, stream=side, done=done.handle)
+    done.sync()
+    again = sc.DeviceBuffer(total, "uint8")
+    again.fill(0xAA)
+    sc.plan_capture(geo, back, tokens, again.ptr, total).launch()
+    sc.device_sync()
+    assert np.array_equal(again.numpy(total), image.numpy(total)), "paged resume"
     host.free()
