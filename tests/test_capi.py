@@ -102,11 +102,14 @@ def test_image_refusals(sc):
     # more tokens than the slot holds
     assert sc.lib.sc_plan_scatter(C.byref(geo), 1 << 40, 1 << 40, 65, C.byref(slot), C.byref(h)) == sc.SC_EINVAL
     assert sc.last_error() == "conversation snapshot: invalid K/V extent"
-    # park of a paged slot needs a capture first
+    # a paged slot's park is checked the same way before anything is enqueued: an image smaller than the layout, and
+    # more tokens than the slot holds, are refused
     tab = (C.c_void_p * 2)(1 << 42, None)
     slot.page_table = C.cast(tab, C.POINTER(C.c_void_p))
-    assert sc.lib.sc_park_async(C.byref(geo), C.byref(slot), 60, 1 << 40, total, None, None) == sc.SC_EINVAL
-    assert "identity-layout" in sc.last_error()
+    assert sc.lib.sc_park_async(C.byref(geo), C.byref(slot), 60, 1 << 40, total - 64, None, None) == sc.SC_EINVAL
+    assert "invalid K/V payload size" in sc.last_error()
+    assert sc.lib.sc_resume_async(C.byref(geo), 1 << 40, 1 << 40, 65, C.byref(slot), None, None) == sc.SC_EINVAL
+    assert sc.last_error() == "conversation snapshot: invalid K/V extent"
 
 
 def test_kv_append_range_refusals_before_any_hip_call(sc):
