@@ -43,6 +43,12 @@ def measured_traffic() -> int | None:
         pass
     return None
 HBM_PEAK_GBPS = 8000.0
+
+
+def synth():
+    """The seeded synthetic workloads (imported once the device library is known to load)."""
+    import sc_synthetic
+    return sc_synthetic
 # PCIe Gen5 x16, one direction: 32 GT/s x 16 lanes x 128/130 line coding / 8 bits (before packet overheads)
 PCIE5_X16_GBPS = 32.0 * 16 * 128 / 130 / 8
 REF_BIN = ROOT / "oracle" / "_ref"
@@ -211,7 +217,7 @@ def config4(sc, geo, seed: int, link_gbps: float, streams=None) -> dict:
     rng = np.random.default_rng(seed)
     lens = [int(x) for x in rng.permutation([8192, 32768, 98304])]
     decode_len, park_a, park_b = lens
-    cases = {L: sc.SyntheticCase(geo, L, seed + L) for L in lens}
+    cases = {L: synth().SyntheticCase(geo, L, seed + L) for L in lens}
     slots = {L: cases[L].new_slot(max_cells=L) for L in lens}
     for L in lens:
         cases[L].carve_into(slots[L])
@@ -301,7 +307,7 @@ def config5(sc, geo, seed: int, fragmented: bool = True) -> dict:
     rng = np.random.default_rng(seed)
     lens = [int(x) for x in rng.integers(1024, 131072 + 1, size=8)]
     chunk = 2048
-    case = sc.BatchCase(geo, lens, chunk, seed=seed, fragmented=fragmented)
+    case = synth().BatchCase(geo, lens, chunk, seed=seed, fragmented=fragmented)
     plan = case.plan()
     side = sc.Stream()
     case.stage(side)   # warm-up of the link and of the pinned pages
@@ -879,7 +885,7 @@ def quant_carve(sc, geo, tokens: int, stream, reps: int = 10) -> dict:
     one launch each (and int8 once more through a shuffled page table).  HBM bytes = the f32 rows read + the codes and
     scales written + the GDN rows read and written."""
     import numpy as np
-    case = sc.SyntheticCase(geo, tokens, seed=0x5EED, kv_dtype=sc.SC_DTYPE_F32)
+    case = synth().SyntheticCase(geo, tokens, seed=0x5EED, kv_dtype=sc.SC_DTYPE_F32)
     out = {"tokens": tokens}
     n_pages = (tokens + geo.page_size - 1) // geo.page_size
     shuffled = sc.device_tables([np.random.default_rng(j).permutation(n_pages).astype(np.int32)
@@ -1009,7 +1015,7 @@ def main() -> int:
         print(json.dumps({"config5": config5(sc, geo, 0x5EED)}), flush=True)
         return 0
     log(f"config 3: {T} tokens, payload {P} B; generating inputs on the device")
-    case = sc.SyntheticCase(geo, tokens=T, seed=0x5EED)
+    case = synth().SyntheticCase(geo, tokens=T, seed=0x5EED)
     slot = case.new_slot(max_cells=T)
     sc.device_sync()
     plan = sc.plan_carve(geo, case.prefill, slot)
@@ -1136,7 +1142,7 @@ def main() -> int:
     # p50 latency of the 32K handoff (config 2): first enqueue to completion event
     TL = args.latency_tokens
     PL = sc.payload_bytes(geo, TL)
-    case_l = sc.SyntheticCase(geo, tokens=TL, seed=0x5EED + 1)
+    case_l = synth().SyntheticCase(geo, tokens=TL, seed=0x5EED + 1)
     slot_l = case_l.new_slot(max_cells=TL)
     plan_l = sc.plan_carve(geo, case_l.prefill, slot_l)
     sc.device_sync()

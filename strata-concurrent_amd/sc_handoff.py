@@ -486,62 +486,6 @@ def fill_bytes(ptr: int, value: int, nbytes: int, stream=None) -> None:
     check(lib.sc_fill_bytes_async(ptr, value, nbytes, _stream(stream)), "sc_fill_bytes_async")
 
 
-# Stream ids of the synthetic inputs (one counter stream per buffer).
-def sid_k(j: int) -> int: return 1000 + 2 * j
-def sid_v(j: int) -> int: return 1001 + 2 * j
-def sid_rec(i: int) -> int: return 5000 + i
-def sid_conv(i: int) -> int: return 9000 + i
-
-
-def synthetic_prefill(geo: Geometry, tokens: int, seed: int, kv_dtype: int = SC_DTYPE_F16,
-                      conv_rows: int | None = None, stream=None) -> PrefillBuffers:
-    """K/V ~ U[-4, 4] (f16, or f32 when kv_dtype is F32), recurrence and conv rows ~ N(0, 1) (Irwin-Hall 12),
-    generated on the device by the library's counter-based generators."""
-    H, D = geo.n_head_kv, geo.head_dim
-    S, HV, Cc = geo.ssm_state_size, geo.ssm_v_heads, geo.ssm_conv_channels
-    conv_rows = min(tokens, geo.ssm_d_conv - 1) if conv_rows is None else conv_rows
-    s = _stream(stream)
-    ks, vs, recs, convs = [], [], [], []
-    for j in range(geo.n_qsa):
-        for lst, sid in ((ks, sid_k(j)), (vs, sid_v(j))):
-            n = tokens * H * D
-            if kv_dtype == SC_DTYPE_F16:
-                t = DeviceBuffer((max(tokens, 1), H, D), "uint16")
-                check(lib.sc_fill_uniform_f16(t.ptr, n, -4.0, 4.0, seed, sid, s), "fill")
-            else:
-                t = DeviceBuffer((max(tokens, 1), H, D), "float32")
-                check(lib.sc_fill_uniform_f32(t.ptr, n, -4.0, 4.0, seed, sid, s), "fill")
-            lst.append(t)
-    for i in range(geo.n_gdn):
-        r = DeviceBuffer((HV, S, S), "float32")
-        check(lib.sc_fill_normal_f32(r.ptr, r.numel(), seed, sid_rec(i), s), "fill")
-        recs.append(r)
-        c = DeviceBuffer((max(conv_rows, 1), Cc), "float32")
-        check(lib.sc_fill_normal_f32(c.ptr, conv_rows * Cc, seed, sid_conv(i), s), "fill")
-        convs.append(c)
-    return PrefillBuffers(geo, tokens, ks, vs, recs, convs, conv_rows, kv_dtype)
-
-
-class SyntheticCase:
-    """A seeded prefill sequence on the device plus the helpers smoke() and the tests use."""
-
-    def __init__(self, geo: Geometry, tokens: int, seed: int, kv_dtype: int = SC_DTYPE_F16):
-        self.geo, self.tokens, self.seed = geo, tokens, seed
-        self.prefill = synthetic_prefill(geo, tokens, seed, kv_dtype)
-
-    def new_slot(self, max_cells: int, **kw) -> Slot:
-        return new_slot(self.geo, max_cells, **kw)
-
-    def carve_into(self, slot: Slot, pos0: int = 0, stream=None) -> None:
-        plan = plan_carve(self.geo, self.prefill, slot, pos0)
-        plan.launch(stream)
-        device_sync()
-        plan.destroy()
-
-    def host_inputs(self) -> dict:
-        return self.prefill.host()
-
-
 def plan_carve(geo: Geometry, prefill: PrefillBuffers, slot: Slot, pos0: int = 0, with_gdn: bool = True) -> Plan:
     view, keep = prefill.view(pos0, with_gdn)
     cs = slot.c_struct()
@@ -679,100 +623,6 @@ def staging_layout(geo: Geometry, lens) -> tuple[list[int], int]:
     total = C.c_uint64()
     check(lib.sc_batch_staging_layout(C.byref(geo), arr, n, offs, C.byref(total)), "sc_batch_staging_layout")
     return list(offs), int(total.value)
-
-
-class BatchCase:
-    """`n` slots with parked prefixes of lens[i] tokens (seeded images in pinned host memory) plus a fresh chunk of
-    `chunk` tokens each, resumed and appended into shared per-layer page arenas through fragmented per-slot page
-    tables.  Holds everything the batched plan reads and writes."""
-
-    def __init__(self, geo: Geometry, lens, chunk: int, seed: int, stream=None, fragmented: bool = True):
-        import numpy as np
-        self.geo, self.lens, self.chunk, self.seed = geo, list(lens), chunk, seed
-        n = len(self.lens)
-        ps = geo.page_size
-        # parked images: gather each slot's seeded prefill into a device image, park it in pinned host memory
-        self.images, self.image_bytes = [], []
-        for i, L in enumerate(self.lens):
-            case = SyntheticCase(geo, L, seed * 1000 + i)
-            _, total = image_layout(geo, L)
-            dev = DeviceBuffer(total, "uint8")
-            plan = plan_gather(geo, case.prefill, dev.ptr, total)
-            plan.launch()
-            host = PinnedBuffer(total)
-            check(lib.sc_copy_async(host.ptr, dev.ptr, total, None), "park copy")
-            device_sync()
-            plan.destroy()
-            dev.free()
-            del case
-            self.images.append(host)
-            self.image_bytes.append(total)
-        self.offsets, self.staging_bytes = staging_layout(geo, self.lens)
-        self.staging = DeviceBuffer(max(self.staging_bytes, 16), "uint8")
-        # fresh chunks, K/V only
-        self.chunks = [synthetic_prefill(geo, chunk, seed * 1000 + 500 + i, conv_rows=0) for i in range(n)]
-        # page tables: every slot's pages drawn from one shuffled arena (a fragmented allocator)
-        self.table_pages = (max(self.lens) + chunk + ps - 1) // ps
-        need = [(L + chunk + ps - 1) // ps for L in self.lens]
-        self.arena_pages = sum(need) + 3
-        rng = np.random.default_rng(seed)
-        # fragmented: every page drawn from a shuffled arena; otherwise each slot gets one contiguous run
-        order = (rng.permutation(self.arena_pages) if fragmented else np.arange(self.arena_pages)).astype(np.int32)
-        self.host_tables, at = [], 0
-        for k in need:
-            t = np.full(self.table_pages, -1, dtype=np.int32)
-            t[:k] = order[at:at + k]
-            at += k
-            self.host_tables.append(t)
-        self.tables = device_tables(self.host_tables)
-        shape = (self.arena_pages, geo.n_head_kv, ps, geo.head_dim)
-        self.arena_k = [DeviceBuffer(shape, "uint16") for _ in range(geo.n_qsa)]
-        self.arena_v = [DeviceBuffer(shape, "uint16") for _ in range(geo.n_qsa)]
-        for b in self.arena_k + self.arena_v:
-            b.fill(0)
-        self.gdn = [DeviceBuffer((geo.n_gdn, geo.gdn_row_floats), "float32") for _ in range(n)] if geo.n_gdn else []
-        self.lens_dev = DeviceBuffer(n, "int64")
-        self.lens_dev.upload(np.array(self.lens, dtype=np.int64))
-        self.lens_out = DeviceBuffer(n, "int64")
-        self.lens_out.fill(0)
-        device_sync()
-
-    @property
-    def parked_bytes(self) -> int:
-        return sum(self.image_bytes)
-
-    def stage(self, stream=None) -> None:
-        """The batched resume: one H2D copy per slot into the staging buffer at its offset."""
-        for host, off, nbytes in zip(self.images, self.offsets, self.image_bytes):
-            check(lib.sc_copy_async(self.staging.ptr + off, host.ptr, nbytes, _stream(stream)), "stage copy")
-
-    def plan(self) -> Plan:
-        geo, n = self.geo, len(self.lens)
-        ck = _ptrs([self.chunks[i].k[j].ptr for i in range(n) for j in range(geo.n_qsa)])
-        cv = _ptrs([self.chunks[i].v[j].ptr for i in range(n) for j in range(geo.n_qsa)])
-        ak = _ptrs([b.ptr for b in self.arena_k])
-        av = _ptrs([b.ptr for b in self.arena_v])
-        ts = _ptrs([t.ptr for t in self.tables])
-        gs = _ptrs([g.ptr for g in self.gdn])
-        P = C.POINTER(C.c_void_p)
-        desc = BatchDesc(n_slots=n, lens=self.lens_dev.ptr, max_tokens=max(self.lens), staging=self.staging.ptr,
-                         staging_bytes=self.staging_bytes, chunk_tokens=self.chunk, chunk_k=C.cast(ck, P),
-                         chunk_v=C.cast(cv, P), arena_k=C.cast(ak, P), arena_v=C.cast(av, P),
-                         arena_pages=self.arena_pages, tables=C.cast(ts, P), table_pages=self.table_pages,
-                         gdn=C.cast(gs, P), lens_out=self.lens_out.ptr)
-        h = C.c_void_p()
-        check(lib.sc_plan_resume_append(C.byref(self.geo), C.byref(desc), C.byref(h)), "sc_plan_resume_append")
-        return Plan(h.value, (ck, cv, ak, av, ts, gs))
-
-    def slot_view(self, i: int) -> Slot:
-        """Slot i as a decode slot: the shared arenas read through its page table."""
-        return Slot(self.geo, self.arena_pages, self.table_pages * self.geo.page_size, self.arena_k, self.arena_v,
-                    self.gdn[i] if self.gdn else None, [self.tables[i]] * self.geo.n_qsa)
-
-    def free(self) -> None:
-        for h in self.images:
-            h.free()
-        self.images = []
 
 
 REFERENCE_FNV_SEED = 1469598103934665603   # the seed of every fnv1a64 call in the reference (conversation_wire.hpp:196)

@@ -8,6 +8,8 @@ single-slot HIP path (resume into an identity slot, then the fused carve of the 
 import numpy as np
 import pytest
 
+import sc_synthetic as synth
+
 pytestmark = pytest.mark.gpu
 
 SMALL = dict(n_layers=8, qsa_interval=4, n_head_kv=2, head_dim=256, page_size=4, ssm_state_size=32,
@@ -42,7 +44,7 @@ def test_staging_layout_is_the_padded_prefix_sum(sc):
                                         ([4096, 1001, 2], 2048)])
 def test_batch_matches_oracle(sc, oracle, cuda, lens, chunk):
     geo = sc.geometry(**SMALL)
-    case = sc.BatchCase(geo, lens, chunk, seed=len(lens) * 7 + chunk)
+    case = synth.BatchCase(geo, lens, chunk, seed=len(lens) * 7 + chunk)
     case.stage()
     plan = case.plan()
     plan.launch()
@@ -66,7 +68,7 @@ def test_batch_is_all_or_nothing(sc, cuda):
     """One length beyond max_tokens refuses the whole batch on the device: nothing is written, lens_out is -1."""
     geo = sc.geometry(**SMALL)
     lens = [12, 40, 7]
-    case = sc.BatchCase(geo, lens, 5, seed=3)
+    case = synth.BatchCase(geo, lens, 5, seed=3)
     case.stage()
     plan = case.plan()
     case.lens_dev.upload(np.array([12, max(lens) + 1, 7], dtype=np.int64))
@@ -93,7 +95,7 @@ def test_config5_full_size_equals_single_slot_path(sc, cuda):
     rng = np.random.default_rng(0x5EED)
     lens = [int(x) for x in rng.integers(1024, 131072 + 1, size=8)]
     chunk = 2048
-    case = sc.BatchCase(geo, lens, chunk, seed=5)
+    case = synth.BatchCase(geo, lens, chunk, seed=5)
     case.stage()
     plan = case.plan()
     plan.launch()

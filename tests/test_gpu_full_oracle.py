@@ -10,6 +10,8 @@ past a layer index or past 2^31 bytes fails here.
 import numpy as np
 import pytest
 
+import sc_synthetic as synth
+
 pytestmark = pytest.mark.gpu
 
 MAX_BLOB = 131072 * 2 * 256 * 2   # the largest blob at the configs: one 128K-token K or V pool prefix
@@ -55,7 +57,7 @@ def test_full_depth_oracle_hash(sc, oracle, cuda, tokens):
     want_slot = oracle.synthetic_image_hashes(geo, tokens, seed, tail=0x5A)
     want_image = oracle.synthetic_image_hashes(geo, tokens, seed, tail=0) if tokens % geo.page_size else want_slot
     hp = sc.HashPlan(MAX_BLOB)
-    case = sc.SyntheticCase(geo, tokens=tokens, seed=seed)
+    case = synth.SyntheticCase(geo, tokens=tokens, seed=seed)
     slot = case.new_slot(max_cells=geo.cells(tokens), fill=0x5A)
     case.carve_into(slot)
     got = _hashes(hp, _slot_spans(geo, slot, tokens))
@@ -90,7 +92,7 @@ def test_full_depth_oracle_hash_f32_rows(sc, oracle, cuda):
     geo = sc.geometry()
     tokens = 32768
     want = oracle.synthetic_image_hashes(geo, tokens, 0xF32)
-    case = sc.SyntheticCase(geo, tokens=tokens, seed=0xF32, kv_dtype=sc.SC_DTYPE_F32)
+    case = synth.SyntheticCase(geo, tokens=tokens, seed=0xF32, kv_dtype=sc.SC_DTYPE_F32)
     slot = case.new_slot(max_cells=tokens)
     case.carve_into(slot)
     hp = sc.HashPlan(MAX_BLOB)
@@ -107,7 +109,7 @@ def test_config5_every_slot_matches_oracle_hash(sc, oracle, cuda):
     rng = np.random.default_rng(0x5EED)
     lens = [int(x) for x in rng.integers(1024, 131072 + 1, size=8)]
     chunk, seed = 2048, 5
-    case = sc.BatchCase(geo, lens, chunk, seed=seed)
+    case = synth.BatchCase(geo, lens, chunk, seed=seed)
     case.stage()
     plan = case.plan()
     plan.launch()

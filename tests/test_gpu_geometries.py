@@ -9,6 +9,8 @@ park -> resume round trip, and every byte of the slot must equal the oracle's.
 import numpy as np
 import pytest
 
+import sc_synthetic as synth
+
 pytestmark = pytest.mark.gpu
 
 BASE = dict(n_layers=8, qsa_interval=4, n_head_kv=2, head_dim=256, page_size=4, ssm_state_size=32,
@@ -51,7 +53,7 @@ def test_fused_carve(sc, oracle, cuda, name, table, pos0):
     ps = GEOMETRIES[name]["page_size"]
     max_cells = (pos0 + tokens + ps - 1) // ps * ps + 2 * ps
     n_pages = max_cells // ps
-    case = sc.SyntheticCase(geo, tokens=tokens, seed=len(name) * 101 + pos0)
+    case = synth.SyntheticCase(geo, tokens=tokens, seed=len(name) * 101 + pos0)
     dev_tabs, host_tabs = _tables(sc, table, geo.n_qsa, n_pages)
     slot = case.new_slot(max_cells=max_cells, tables=dev_tabs, fill=0xA5)
     sc.device_sync()
@@ -67,7 +69,7 @@ def test_gather_scatter_and_park_resume(sc, oracle, cuda, name):
     print(f"case geometry {name} two-pass + park/resume", flush=True)
     geo = sc.geometry(**GEOMETRIES[name])
     tokens = 45
-    case = sc.SyntheticCase(geo, tokens=tokens, seed=len(name))
+    case = synth.SyntheticCase(geo, tokens=tokens, seed=len(name))
     _, total = sc.image_layout(geo, tokens)
     image = sc.DeviceBuffer(max(total, 16), "uint8")
     image.fill(0xEE)
@@ -135,7 +137,7 @@ def test_paged_park_resume_beyond_one_launch(sc, cuda):
     rng = np.random.default_rng(40)
     tabs = sc.device_tables([rng.permutation(n_pages)[: max_cells // geo.page_size].astype(np.int32)
                              for _ in range(geo.n_qsa)])
-    case = sc.SyntheticCase(geo, tokens, seed=404)
+    case = synth.SyntheticCase(geo, tokens, seed=404)
     slot = case.new_slot(max_cells=max_cells, n_pages=n_pages, tables=tabs)
     case.carve_into(slot)
     _, total = sc.image_layout(geo, tokens)

@@ -9,6 +9,8 @@ full 128K hand-off payload.
 import numpy as np
 import pytest
 
+import sc_synthetic as synth
+
 pytestmark = pytest.mark.gpu
 
 SEEDS = [1469598103934665603, 0xCBF29CE484222325, 0, 0xFFFFFFFFFFFFFFFF, 0x0123456789ABCDEF]
@@ -137,7 +139,7 @@ def test_gated_scatter_writes_all_or_nothing(sc, oracle, cuda):
     geo = sc.geometry(n_layers=8, qsa_interval=4, n_head_kv=2, head_dim=256, page_size=4, ssm_state_size=32,
                       ssm_k_heads=4, ssm_v_heads=8, ssm_d_conv=4, ssm_conv_channels=520)
     tokens = 53
-    case = sc.SyntheticCase(geo, tokens=tokens, seed=99)
+    case = synth.SyntheticCase(geo, tokens=tokens, seed=99)
     _, total = sc.image_layout(geo, tokens)
     image = sc.DeviceBuffer(total, "uint8")
     gather = sc.plan_gather(geo, case.prefill, image.ptr, total)

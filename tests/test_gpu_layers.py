@@ -7,6 +7,8 @@ resumes must restore exactly the blob prefixes and leave every byte past them as
 import numpy as np
 import pytest
 
+import sc_synthetic as synth
+
 pytestmark = pytest.mark.gpu
 
 SMALL = dict(n_layers=8, qsa_interval=4, n_head_kv=2, head_dim=256, page_size=4, ssm_state_size=32,
@@ -105,7 +107,7 @@ def test_quantized_carve_parks_and_resumes(sc, oracle, cuda):
     codes, scales, rows and the GDN state come back bit for bit, and the image equals the host-built one."""
     geo = sc.geometry(**SMALL)
     T = 501
-    case = sc.SyntheticCase(geo, T, seed=0x5EED, kv_dtype=sc.SC_DTYPE_F32)
+    case = synth.SyntheticCase(geo, T, seed=0x5EED, kv_dtype=sc.SC_DTYPE_F32)
     cap = (T + 3) // 4 * 4 + 16
     slot = sc.new_quant_slot(geo, sc.SC_KV_INT8, cap)
     sc.plan_carve_quant(geo, case.prefill, slot).launch()

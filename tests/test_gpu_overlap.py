@@ -18,6 +18,8 @@ from concurrent.futures import ThreadPoolExecutor
 import numpy as np
 import pytest
 
+import sc_synthetic as synth
+
 pytestmark = pytest.mark.gpu
 
 MAX_BLOB = 98304 * 2 * 256 * 2
@@ -57,11 +59,11 @@ def test_config4_park_resume_overlap_event_ordering(sc, oracle, cuda):
 
     slots = {}
     for L in (decode_len, park_a, park_b):
-        case = sc.SyntheticCase(geo, L, seeds[L])
+        case = synth.SyntheticCase(geo, L, seeds[L])
         slots[L] = case.new_slot(max_cells=cap)
         case.carve_into(slots[L])
         del case
-    newcomer = sc.SyntheticCase(geo, new_tokens, new_seed)
+    newcomer = synth.SyntheticCase(geo, new_tokens, new_seed)
     carve_new = sc.plan_carve(geo, newcomer.prefill, slots[park_a])
     images = {L: sc.PinnedBuffer(sc.image_layout(geo, L)[1]) for L in (park_a, park_b)}
     for im in images.values():

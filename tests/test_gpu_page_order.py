@@ -9,6 +9,8 @@ two launches of one plan, and the scatter of a parked image into a paged slot.
 import numpy as np
 import pytest
 
+import sc_synthetic as synth
+
 pytestmark = pytest.mark.gpu
 
 GEO = dict(n_layers=8, qsa_interval=4, n_head_kv=2, head_dim=256, page_size=4, ssm_state_size=32, ssm_k_heads=4,
@@ -60,7 +62,7 @@ def test_ordered_carve_equals_oracle(sc, oracle, cuda, ordered, dtype, kind, T, 
     n_pages = logical + spare   # spare: physical pages the table never names
     rng = np.random.default_rng(T * 7 + spare)
     tables = [_table(rng, logical, n_pages, kind) for _ in range(geo.n_qsa)]
-    case = sc.SyntheticCase(geo, tokens=T, seed=900 + T,
+    case = synth.SyntheticCase(geo, tokens=T, seed=900 + T,
                             kv_dtype=sc.SC_DTYPE_F16 if dtype == "f16" else sc.SC_DTYPE_F32)
     slot = sc.new_slot(geo, logical * ps, n_pages=n_pages, tables=sc.device_tables(tables), fill=SENTINEL)
     sc.device_sync()
@@ -82,7 +84,7 @@ def test_table_changed_between_launches(sc, oracle, cuda, ordered):
     logical = (T + ps - 1) // ps
     n_pages = logical + 7
     rng = np.random.default_rng(11)
-    case = sc.SyntheticCase(geo, tokens=T, seed=77)
+    case = synth.SyntheticCase(geo, tokens=T, seed=77)
     first = [_table(rng, logical, n_pages, "permuted") for _ in range(geo.n_qsa)]
     second = [_table(rng, logical, n_pages, "holes") for _ in range(geo.n_qsa)]
     dev = sc.device_tables(first)
@@ -108,7 +110,7 @@ def test_ordered_scatter_of_an_image(sc, cuda, ordered):
     """A parked image scattered into a paged slot in destination order reads back as the same image."""
     geo = sc.geometry(**GEO)
     T, ps = 101, geo.page_size
-    case = sc.SyntheticCase(geo, tokens=T, seed=5)
+    case = synth.SyntheticCase(geo, tokens=T, seed=5)
     flat = case.new_slot(max_cells=128)
     case.carve_into(flat)
     _, total = sc.image_layout(geo, T)
@@ -138,7 +140,7 @@ def test_default_threshold_orders_large_tables_only(sc, oracle, cuda):
         logical = T // ps
         rng = np.random.default_rng(T)
         tables = [rng.permutation(logical).astype(np.int32) for _ in range(geo.n_qsa)]
-        case = sc.SyntheticCase(geo, tokens=T, seed=31 + T)
+        case = synth.SyntheticCase(geo, tokens=T, seed=31 + T)
         slot = sc.new_slot(geo, T, n_pages=logical, tables=sc.device_tables(tables), fill=SENTINEL)
         sc.device_sync()
         plan = sc.plan_carve(geo, case.prefill, slot, with_gdn=False)
@@ -165,7 +167,7 @@ def test_quantizing_carve_keeps_source_order(sc, oracle, cuda, ordered, fmt, kin
     n_pages = logical + spare
     rng = np.random.default_rng(T * 3 + spare)
     tables = [_table(rng, logical, n_pages, kind) for _ in range(geo.n_qsa)]
-    case = sc.SyntheticCase(geo, tokens=T, seed=600 + T, kv_dtype=sc.SC_DTYPE_F32)
+    case = synth.SyntheticCase(geo, tokens=T, seed=600 + T, kv_dtype=sc.SC_DTYPE_F32)
     code = sc.SC_KV_INT8 if fmt == "int8" else sc.SC_KV_Q4
     slot = sc.new_quant_slot(geo, code, logical * ps, n_pages=n_pages, tables=sc.device_tables(tables),
                              fill=SENTINEL)

@@ -11,6 +11,8 @@ import ctypes as C
 import numpy as np
 import pytest
 
+import sc_synthetic as synth
+
 pytestmark = pytest.mark.gpu
 
 SMALL = dict(n_layers=8, qsa_interval=4, n_head_kv=2, head_dim=256, page_size=4, ssm_state_size=32,
@@ -74,7 +76,7 @@ def test_device_generators_match_oracle(sc, oracle, cuda, n):
 def test_toy_config_fused_carve_bit_exact(sc, oracle, cuda):
     """Config 1: 16 layers (4 QSA, 12 GDN), 4096 tokens, K/V U[-4,4] f16, state N(0,1), one decode slot."""
     geo = sc.geometry(**TOY)
-    case = sc.SyntheticCase(geo, tokens=4096, seed=0x5EED)
+    case = synth.SyntheticCase(geo, tokens=4096, seed=0x5EED)
     slot = case.new_slot(max_cells=4096)
     case.carve_into(slot)
     want = oracle.expected_slot(geo, case.host_inputs(), slot_cells=4096)
@@ -96,7 +98,7 @@ def test_toy_config_fused_carve_bit_exact(sc, oracle, cuda):
 def test_fused_carve_cases(sc, oracle, cuda, tokens, pos0, max_cells, table, dtype):
     geo = sc.geometry(**SMALL)
     kv_dtype = sc.SC_DTYPE_F16 if dtype == "f16" else sc.SC_DTYPE_F32
-    case = sc.SyntheticCase(geo, tokens=tokens, seed=tokens * 31 + pos0, kv_dtype=kv_dtype)
+    case = synth.SyntheticCase(geo, tokens=tokens, seed=tokens * 31 + pos0, kv_dtype=kv_dtype)
     n_pages = max_cells // geo.page_size
     dev_tabs, host_tabs = _tables(table, geo.n_qsa, n_pages)
     slot = case.new_slot(max_cells=max_cells, tables=dev_tabs, fill=0xA5)
@@ -110,7 +112,7 @@ def test_fused_carve_cases(sc, oracle, cuda, tokens, pos0, max_cells, table, dty
 
 def test_kv_only_chunk_leaves_running_state(sc, oracle, cuda):
     geo = sc.geometry(**SMALL)
-    case = sc.SyntheticCase(geo, tokens=40, seed=5)
+    case = synth.SyntheticCase(geo, tokens=40, seed=5)
     slot = case.new_slot(max_cells=64, fill=0x3C)
     _sync()
     initial = slot.host_state()
@@ -128,7 +130,7 @@ def test_kv_only_chunk_leaves_running_state(sc, oracle, cuda):
 @pytest.mark.parametrize("tokens,table", [(77, "identity"), (96, "reversed"), (4096, "identity")])
 def test_gather_then_scatter(sc, oracle, cuda, tokens, table):
     geo = sc.geometry(**(SMALL if tokens < 1000 else TOY))
-    case = sc.SyntheticCase(geo, tokens=tokens, seed=tokens)
+    case = synth.SyntheticCase(geo, tokens=tokens, seed=tokens)
     _, total = sc.image_layout(geo, tokens)
     image = _device_u8(total)
     image.fill(0xEE)
@@ -160,7 +162,7 @@ def test_gather_then_scatter(sc, oracle, cuda, tokens, table):
 def test_capture_reads_through_the_page_table(sc, oracle, cuda, table):
     geo = sc.geometry(**SMALL)
     tokens, max_cells = 90, 96
-    case = sc.SyntheticCase(geo, tokens=tokens, seed=77)
+    case = synth.SyntheticCase(geo, tokens=tokens, seed=77)
     n_pages = max_cells // geo.page_size
     dev_tabs, host_tabs = _tables(table, geo.n_qsa, n_pages)
     slot = case.new_slot(max_cells=max_cells, tables=dev_tabs)
@@ -189,7 +191,7 @@ def test_capture_reads_through_the_page_table(sc, oracle, cuda, table):
 def test_park_resume_round_trip(sc, oracle, cuda):
     geo = sc.geometry(**TOY)
     tokens = 4093
-    case = sc.SyntheticCase(geo, tokens=tokens, seed=4093)
+    case = synth.SyntheticCase(geo, tokens=tokens, seed=4093)
     slot = case.new_slot(max_cells=4096)
     case.carve_into(slot)
     _, total = sc.image_layout(geo, tokens)
@@ -219,7 +221,7 @@ def test_park_resume_round_trip(sc, oracle, cuda):
 def test_refusal_writes_nothing(sc, cuda):
     """Invalid requests are refused before the first write (conversation_snapshot.hpp:104-105)."""
     geo = sc.geometry(**SMALL)
-    case = sc.SyntheticCase(geo, tokens=60, seed=1)
+    case = synth.SyntheticCase(geo, tokens=60, seed=1)
     slot = case.new_slot(max_cells=64, fill=0xA5)
     _sync()
     before = slot.host_state()
@@ -276,7 +278,7 @@ def _equal_buffers(a_list, b_list):
 def test_full_depth_properties(sc, oracle, cuda, tokens):
     """Configs 2 and 3: 48 layers (12 QSA, 36 GDN) at 32K and 128K tokens."""
     geo = sc.geometry()
-    case = sc.SyntheticCase(geo, tokens=tokens, seed=0x5EED + tokens)
+    case = synth.SyntheticCase(geo, tokens=tokens, seed=0x5EED + tokens)
     fused = case.new_slot(max_cells=tokens)
     case.carve_into(fused)
     _sampled_rows_check(sc, oracle, geo, case, fused, seed=tokens)

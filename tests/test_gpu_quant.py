@@ -9,6 +9,8 @@ NaN and infinite values, signed zeros).
 import numpy as np
 import pytest
 
+import sc_synthetic as synth
+
 pytestmark = pytest.mark.gpu
 
 SMALL = dict(n_layers=8, qsa_interval=4, n_head_kv=2, head_dim=256, page_size=4, ssm_state_size=32,
@@ -65,7 +67,7 @@ def _tables(sc, kind, n_qsa, n_pages):
 def test_quant_carve_matches_oracle(sc, oracle, cuda, fmt, tokens, pos0, table):
     geo = sc.geometry(**SMALL)
     code = {"int8": sc.SC_KV_INT8, "q4": sc.SC_KV_Q4, "k8v4": sc.SC_KV_K8V4}[fmt]
-    case = sc.SyntheticCase(geo, tokens, seed=0x5EED + tokens, kv_dtype=sc.SC_DTYPE_F32)
+    case = synth.SyntheticCase(geo, tokens, seed=0x5EED + tokens, kv_dtype=sc.SC_DTYPE_F32)
     # plant the edge rows in every layer's K and V
     for buf in case.prefill.k + case.prefill.v:
         host = buf.numpy()
@@ -105,17 +107,17 @@ def test_quant_carve_matches_oracle(sc, oracle, cuda, fmt, tokens, pos0, table):
 
 def test_quant_carve_refusals(sc, cuda):
     geo = sc.geometry(**SMALL)
-    case16 = sc.SyntheticCase(geo, 8, seed=1)                       # f16 rows: refused, the carve reads f32
+    case16 = synth.SyntheticCase(geo, 8, seed=1)                       # f16 rows: refused, the carve reads f32
     slot = sc.new_quant_slot(geo, sc.SC_KV_INT8, 16)
     with pytest.raises(sc.ScError):
         sc.plan_carve_quant(geo, case16.prefill, slot)
-    case = sc.SyntheticCase(geo, 8, seed=1, kv_dtype=sc.SC_DTYPE_F32)
+    case = synth.SyntheticCase(geo, 8, seed=1, kv_dtype=sc.SC_DTYPE_F32)
     small = sc.new_quant_slot(geo, sc.SC_KV_INT8, 4)                 # 8 tokens do not fit 4 cells
     with pytest.raises(sc.ScError):
         sc.plan_carve_quant(geo, case.prefill, small)
     other = sc.geometry(**dict(SMALL, head_dim=128))                 # head_dim 256 only
     with pytest.raises(sc.ScError):
-        sc.plan_carve_quant(other, sc.SyntheticCase(other, 8, seed=1, kv_dtype=sc.SC_DTYPE_F32).prefill,
+        sc.plan_carve_quant(other, synth.SyntheticCase(other, 8, seed=1, kv_dtype=sc.SC_DTYPE_F32).prefill,
                             sc.new_quant_slot(other, sc.SC_KV_INT8, 16))
 
 
@@ -124,7 +126,7 @@ def test_quant_carve_full_depth_int8(sc, oracle, cuda):
     scales' decoded magnitudes bound every code's reconstruction error by half a step."""
     geo = sc.geometry()
     T = 32768
-    case = sc.SyntheticCase(geo, T, seed=0x5EED, kv_dtype=sc.SC_DTYPE_F32)
+    case = synth.SyntheticCase(geo, T, seed=0x5EED, kv_dtype=sc.SC_DTYPE_F32)
     slot = sc.new_quant_slot(geo, sc.SC_KV_INT8, T)
     plan = sc.plan_carve_quant(geo, case.prefill, slot)
     plan.launch()

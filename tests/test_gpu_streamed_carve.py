@@ -10,6 +10,8 @@ staging pool device memory, and every byte of all three (written or not) must eq
 import numpy as np
 import pytest
 
+import sc_synthetic as synth
+
 pytestmark = pytest.mark.gpu
 
 GEO = dict(n_layers=8, qsa_interval=4, n_head_kv=2, head_dim=256, page_size=4, ssm_state_size=32, ssm_k_heads=4,
@@ -81,7 +83,7 @@ def test_carve_writes_pool_host_copy_and_staging(sc, oracle, cuda, fmt, dtype, t
         table = np.random.default_rng(T).permutation(n_pages)[:logical].astype(np.int32)
         table[1::3] = -1
     kv_dtype = sc.SC_DTYPE_F16 if dtype == "f16" else sc.SC_DTYPE_F32
-    case = sc.SyntheticCase(geo, tokens=T, seed=700 + T, kv_dtype=kv_dtype)
+    case = synth.SyntheticCase(geo, tokens=T, seed=700 + T, kv_dtype=kv_dtype)
     tabs = None if table is None else sc.device_tables([table] * geo.n_qsa)
     host_bufs, host_pools = _extra(sc, geo, fmt, logical, host=True)
     stage_bufs, stage_pools = _extra(sc, geo, fmt, logical, host=False)
@@ -120,7 +122,7 @@ def test_carve_writes_pool_host_copy_and_staging(sc, oracle, cuda, fmt, dtype, t
 def test_k8v4_slot_refuses_host_copies(sc, cuda):
     """K8V4 is resident only (the reference's hybrid rule): a host copy is refused before anything is written."""
     geo = sc.geometry(**GEO)
-    case = sc.SyntheticCase(geo, tokens=8, seed=3, kv_dtype=sc.SC_DTYPE_F32)
+    case = synth.SyntheticCase(geo, tokens=8, seed=3, kv_dtype=sc.SC_DTYPE_F32)
     slot = sc.new_quant_slot(geo, sc.SC_KV_K8V4, 16, fill=SENTINEL)
     _, pools = _extra(sc, geo, "int8", 4, host=False)
     slot.host = pools

@@ -9,6 +9,8 @@ reproduce the slot and the host fields; and every refusal must leave the target 
 import numpy as np
 import pytest
 
+import sc_synthetic as synth
+
 pytestmark = pytest.mark.gpu
 
 SMALL = dict(n_layers=8, qsa_interval=4, n_head_kv=2, head_dim=256, page_size=4, ssm_state_size=32,
@@ -69,7 +71,7 @@ def _encode(sc, wire, geo, slot, tokens, live):
 @pytest.mark.parametrize("tokens", [77, 80, 1, 0])
 def test_device_payload_equals_oracle_encode(sc, oracle, wire, codec, cuda, tokens):
     geo = sc.geometry(**SMALL)
-    case = sc.SyntheticCase(geo, tokens, seed=0x5EED + tokens)
+    case = synth.SyntheticCase(geo, tokens, seed=0x5EED + tokens)
     slot = case.new_slot(max_cells=128)
     case.carve_into(slot)
     live, keep, ids = _live(wire, tokens)
@@ -91,7 +93,7 @@ def test_paged_slot_payload_equals_identity(sc, wire, cuda, table):
     """The capture reads through the page tables: a paged slot holding the same cells writes the same payload."""
     geo = sc.geometry(**SMALL)
     tokens = 77
-    case = sc.SyntheticCase(geo, tokens, seed=99)
+    case = synth.SyntheticCase(geo, tokens, seed=99)
     flat = case.new_slot(max_cells=128)
     case.carve_into(flat)
     n_pages = 32
@@ -110,7 +112,7 @@ def test_paged_slot_payload_equals_identity(sc, wire, cuda, table):
 def test_mount_round_trip_and_host_fields(sc, oracle, wire, cuda):
     geo = sc.geometry(**SMALL)
     tokens = 77
-    case = sc.SyntheticCase(geo, tokens, seed=7)
+    case = synth.SyntheticCase(geo, tokens, seed=7)
     src = case.new_slot(max_cells=128)
     case.carve_into(src)
     live, keep, ids = _live(wire, tokens)
@@ -137,7 +139,7 @@ def test_mount_round_trip_and_host_fields(sc, oracle, wire, cuda):
 def test_mount_into_paged_slot(sc, wire, cuda):
     geo = sc.geometry(**SMALL)
     tokens = 61
-    case = sc.SyntheticCase(geo, tokens, seed=8)
+    case = synth.SyntheticCase(geo, tokens, seed=8)
     src = case.new_slot(max_cells=64)
     case.carve_into(src)
     live, keep, ids = _live(wire, tokens)
@@ -155,7 +157,7 @@ def test_mount_into_paged_slot(sc, wire, cuda):
 def test_refusals_leave_the_slot_untouched(sc, wire, cuda):
     geo = sc.geometry(**SMALL)
     tokens = 40
-    case = sc.SyntheticCase(geo, tokens, seed=21)
+    case = synth.SyntheticCase(geo, tokens, seed=21)
     src = case.new_slot(max_cells=64)
     case.carve_into(src)
     live, keep, ids = _live(wire, tokens)
@@ -219,7 +221,7 @@ def test_full_depth_payload(sc, oracle, wire, cuda, tokens):
     """Configs 2 and 3: the device hash equals the byte loop over the payload read back, the pool equals the park image
     of the slot, and a mount into a fresh slot reproduces every pool byte (compared by device hash)."""
     geo = sc.geometry()
-    case = sc.SyntheticCase(geo, tokens, seed=0x5EED)
+    case = synth.SyntheticCase(geo, tokens, seed=0x5EED)
     src = case.new_slot(max_cells=tokens)
     case.carve_into(src)
     del case

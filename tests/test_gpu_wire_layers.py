@@ -9,6 +9,8 @@ whose records are not the slot's format is refused with the slot untouched.
 import numpy as np
 import pytest
 
+import sc_synthetic as synth
+
 pytestmark = pytest.mark.gpu
 
 SMALL = dict(n_layers=8, qsa_interval=4, n_head_kv=2, head_dim=256, page_size=4, ssm_state_size=32,
@@ -130,7 +132,7 @@ def test_quantized_carve_to_payload_and_back(sc, wire, cuda):
     """The quantizing carve's K8V4 pools with indexer rows, encoded on the device and mounted into fresh pools."""
     geo = sc.geometry(**SMALL)
     T = 257
-    case = sc.SyntheticCase(geo, T, seed=0xAB, kv_dtype=sc.SC_DTYPE_F32)
+    case = synth.SyntheticCase(geo, T, seed=0xAB, kv_dtype=sc.SC_DTYPE_F32)
     cap = 272
     slot = sc.new_quant_slot(geo, sc.SC_KV_K8V4, cap)
     sc.plan_carve_quant(geo, case.prefill, slot).launch()

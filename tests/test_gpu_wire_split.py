@@ -11,6 +11,8 @@ pinned to the reference codec's payloads in tests/test_wire_oracle.py) of the im
 import numpy as np
 import pytest
 
+import sc_synthetic as synth
+
 pytestmark = pytest.mark.gpu
 
 BASE = dict(qsa_interval=4, n_head_kv=2, head_dim=256, page_size=4, ssm_state_size=32, ssm_k_heads=4, ssm_v_heads=8,
@@ -52,13 +54,13 @@ class Split:
     def __init__(self, sc, tokens, seed):
         self.tokens = tokens
         self.geo = sc.geometry(n_layers=4, **BASE)
-        self.case = sc.SyntheticCase(self.geo, tokens, seed=seed)
+        self.case = synth.SyntheticCase(self.geo, tokens, seed=seed)
         self.slot = self.case.new_slot(max_cells=CELLS)
         self.case.carve_into(self.slot)
         self.stages = []
         for i, (layers, rng, small) in enumerate(STAGES):
             geo = sc.geometry(n_layers=layers, **BASE)
-            case = sc.SyntheticCase(geo, tokens, seed=seed + 101 * (i + 1))
+            case = synth.SyntheticCase(geo, tokens, seed=seed + 101 * (i + 1))
             slot = case.new_slot(max_cells=CELLS)
             case.carve_into(slot)
             self.stages.append((geo, case, slot, rng, small))
