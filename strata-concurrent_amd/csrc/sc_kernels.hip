@@ -469,7 +469,8 @@ __device__ void tile_q4(const MoveRow& r, const MoveGeo& g, uint64_t local) {
 // per SIMD.  The quantizing instance is held to 80 VGPRs (6 waves per SIMD): at 84 it fell to 5 waves and every
 // quantizing row slowed by 3-6%; the instance of every kind keeps 5 waves (at 80 VGPRs it would spill).
 template <int kMix>
-__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kMix == kMixAll ? 5 : 6)))
+__global__ void __launch_bounds__(kThreads)
+__attribute__((amdgpu_waves_per_eu(kMix == kMixAll ? 5 : 6)))
 sc_move_kernel(const MoveRow* __restrict__ rows, const uint16_t* __restrict__ tile_row, MoveGeo geo, uint64_t n_tiles,
                const uint32_t* __restrict__ gate) {
     // A gated launch moves nothing unless the word a kernel before it on the stream left at `gate` is nonzero (a
@@ -515,10 +516,6 @@ sc_move_kernel(const MoveRow* __restrict__ rows, const uint16_t* __restrict__ ti
 
 __device__ __forceinline__ uint64_t shfl_up64(uint64_t v, int delta) {
     const uint32_t lo = __shfl_up(uint32_t(v), delta), hi = __shfl_up(uint32_t(v >> 32), delta);
-    return (uint64_t(hi) << 32) | lo;
-}
-__device__ __forceinline__ uint64_t shfl64(uint64_t v, int lane) {
-    const uint32_t lo = __shfl(uint32_t(v), lane), hi = __shfl(uint32_t(v >> 32), lane);
     return (uint64_t(hi) << 32) | lo;
 }
 // Inclusive prefix sum across the 64 lanes of a wave (Hillis-Steele: six shuffle steps).
