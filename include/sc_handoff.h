@@ -363,7 +363,8 @@ int sc_plan_resume_append(const sc_geometry* g, const sc_batch_desc* desc, sc_pl
  * hipEvent_t, may be NULL) after the last copy.  An identity-layout slot takes one hipMemcpyAsync per blob; a paged
  * slot (any non-null page table) has its K/V pages gathered through the tables straight into the pinned image by a
  * kernel that writes the host memory itself (no staging copy in HBM, nothing allocated; 32 layers per launch), then
- * its GDN rows by one copy.  Replaces conversation_kv_save's synchronous per-16-MiB cudaMemcpy loop
+ * its GDN rows by one copy; a page whose entry is negative or past the pool (not resident) is skipped, and its bytes
+ * of the image are left as they were.  Replaces conversation_kv_save's synchronous per-16-MiB cudaMemcpy loop
  * (conversation_snapshot.cpp:105-113, 160-171) and conversation_checkpoint_save's GDN copy (conversation_state.cpp:235). */
 int sc_park_async(const sc_geometry* g, const sc_decode_slot* slot, int64_t tokens, void* host_image,
                   uint64_t image_bytes, void* stream, void* done);
