@@ -205,7 +205,8 @@ constexpr int64_t kOrderMaxSparsity = 8;
 
 bool quant_kind(int32_t kind) { return kind == sc::kKvQ8 || kind == sc::kKvQ4; }
 // The quantizing rows keep the source order: measured on the 128K int8 carve through a shuffled table, destination
-// order took it from 1.64 to 2.12 ms (each wave's four rows then wait on the order's entries before their loads).
+// order took it from 1.64 to 2.12 ms (1.85 ms with the order entries read by scalar loads): a quantizing row reads 4-7x
+// the bytes it writes, and destination order gives up the sequential reads.
 bool orderable_kind(int32_t kind) { return kind == sc::kKv16 || kind == sc::kKv32 || kind == sc::kPagesScatter; }
 // A row's work items per page and per tile: 16-byte chunks, or (cell, head) rows for the quantizing kinds.
 uint64_t items_per_page(int32_t kind, const Geo& g) {
