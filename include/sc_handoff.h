@@ -309,7 +309,9 @@ int sc_plan_set_grid(sc_plan* plan, int64_t workgroups);
  * three small kernels before every launch of the plan (the table may change between launches), in the plan's own
  * workspace - so launches of one such plan on different streams must not overlap.  A table gets the order when it
  * covers at least `pages` logical pages in a pool of at most 8 times as many physical pages.  Library-wide, for plans
- * built afterwards; pages <= 0 turns it off.  Returns the previous value (default 2048). */
+ * built afterwards; pages <= 0 turns it off.  Returns the previous value (default 2048).  A table must name each
+ * physical page at most once: in source order two logical pages on one physical page race (as the reference's
+ * kv_append does), and in destination order that page receives one of them whole. */
 int64_t sc_set_order_min_pages(int64_t pages);
 /* How many page tables of the plan are visited in destination order (0: every row follows its source). */
 int sc_plan_order_groups(const sc_plan* plan);
@@ -354,7 +356,9 @@ int sc_batch_staging_layout(const sc_geometry* g, const int64_t* lens, int32_t n
  * the move then assembles each arena page once, in that order (parked cells from the image, chunk cells from the
  * chunk), so no two workgroups write the same bytes and the arena is written as one ascending run.  If any length is
  * outside [0, max_tokens] or any image would run past the staging buffer, nothing is written and every lens_out
- * entry is -1.  The pre-pass uses the plan's workspace: launches of one plan on different streams must not overlap. */
+ * entry is -1.  The slots' tables must name disjoint arena pages (an arena page named twice receives one of its
+ * logical pages).  The pre-pass uses the plan's workspace: launches of one plan on different streams must not
+ * overlap. */
 int sc_plan_resume_append(const sc_geometry* g, const sc_batch_desc* desc, sc_plan** out);
 
 /* ---- park / resume: slot <-> pinned host image ----------------------------------------------------------------- */
