@@ -69,9 +69,15 @@ __device__ __forceinline__ void load_segment(const uint8_t* p, uint32_t (&w)[kFn
 }
 
 // Two low-byte machines side by side, in bytes 0 and 2 of `x`: xor the byte into both, drop the products' high
-// bytes, one 24-bit multiply (byte 0's product stays below bit 16).  `bb` holds the byte in bytes 0 and 2.
+// bytes, one 24-bit multiply (byte 0's product stays below bit 16).  `bb` holds the byte in bytes 0 and 2.  (A packed
+// 16-bit multiply, v_pk_mul_lo_u16, needs no mask but measured slower here: 843 against 777 us for bits 3-5 of 3.3 GB.)
 __device__ __forceinline__ uint32_t step_pair(uint32_t x, uint32_t bb) {
     return __umul24((x ^ bb) & 0x00FF00FFu, kPrimeLow);
+}
+// Packed 16-bit subtraction of the two halves of a word (v_pk_sub_i16).
+typedef short v2i16 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pk_sub(uint32_t a, uint32_t b) {
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(v2i16, a) - __builtin_bit_cast(v2i16, b));
 }
 // Byte k of w, in bytes 0 and 2 (v_perm_b32: selector 0x0c gives a zero byte).
 template <int k>
@@ -96,45 +102,53 @@ __device__ __forceinline__ uint32_t run_pair(const uint8_t* p, uint64_t n, bool 
     return x;
 }
 
-// p^k mod 2^64 for k = 1..16 as four signed 16-bit digits, digit[16 - k] for the byte k places before a block's end:
+// p^k mod 2^64 for k = 1..K as four signed 16-bit digits, digit[K - k] for the byte k places before a block's end:
 // p^k = sum_j digit[j] 2^(16 j) mod 2^64 with every digit in [-2^15, 2^15) (balanced base 2^16; the carry out of the
 // top digit is a multiple of 2^64 and drops).  The digits of bytes c and c + 1 of a block pair up as one 32-bit word,
 // the operand layout of the packed 16-bit dot product.
+template <int K>
 struct PowDigits {
-    uint32_t pair[8][4];   // [c / 2][j]: digit of byte c in the low half, of byte c + 1 in the high half
+    uint32_t pair[K / 2][4];   // [c / 2][j]: digit of byte c in the low half, of byte c + 1 in the high half
 };
-constexpr PowDigits pow_digits() {
-    int32_t digit[16][4] = {};
+template <int K>
+constexpr PowDigits<K> pow_digits() {
+    int32_t digit[K][4] = {};
     uint64_t pk = 1;
-    for (int k = 1; k <= 16; ++k) {
+    for (int k = 1; k <= K; ++k) {
         pk *= kFnvPrime;
         uint64_t v = pk;
         for (int j = 0; j < 4; ++j) {
             const int32_t d = int32_t(int16_t(uint16_t(v & 0xFFFFu)));
-            digit[16 - k][j] = d;
+            digit[K - k][j] = d;
             v = (v - uint64_t(int64_t(d))) >> 16;
         }
     }
-    PowDigits t{};
-    for (int c = 0; c < 16; c += 2)
+    PowDigits<K> t{};
+    for (int c = 0; c < K; c += 2)
         for (int j = 0; j < 4; ++j)
             t.pair[c / 2][j] = (uint32_t(digit[c][j]) & 0xFFFFu) | (uint32_t(digit[c + 1][j]) << 16);
     return t;
 }
-constexpr PowDigits kPowDigits = pow_digits();
-constexpr uint64_t kPrime16 = [] {
+template <int K>
+constexpr uint64_t prime_pow() {
     uint64_t r = 1;
-    for (int k = 0; k < 16; ++k) r *= kFnvPrime;
+    for (int k = 0; k < K; ++k) r *= kFnvPrime;
     return r;
-}();
+}
+constexpr PowDigits<16> kPowDigits = pow_digits<16>();
+constexpr uint64_t kPrime16 = prime_pow<16>();
 
 // The Horner sum of 16 bytes given the true low byte `l` before them: sum over c of d_c p^(16-c), d_c = (l ^ b) - l.
 // Per digit j, S_j = sum_c d_c digit[c][j]: |d| <= 255 and |digit| <= 2^15, so |S_j| < 16 * 255 * 2^15 < 2^28 and the
 // sums are exact in 32-bit integers.  Two bytes' d values share one word as signed 16-bit halves, so each S_j takes
 // one packed dot product (v_dot2_i32_i16) per byte pair: 2 operations per byte for the four digits.
-typedef short v2i16 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ int32_t dot2(uint32_t a, uint32_t b, int32_t acc) {
     return __builtin_amdgcn_sdot2(__builtin_bit_cast(v2i16, a), __builtin_bit_cast(v2i16, b), acc, false);
+}
+// sum_j S_j 2^(16 j) mod 2^64.
+__device__ __forceinline__ uint64_t digit_sum(int32_t s0, int32_t s1, int32_t s2, int32_t s3) {
+    return uint64_t(int64_t(s0)) + (uint64_t(int64_t(s1)) << 16) + (uint64_t(int64_t(s2)) << 32) +
+           (uint64_t(int64_t(s3)) << 48);
 }
 __device__ __forceinline__ uint64_t block_sum(const u32x4 v, uint32_t& l) {
     const uint32_t dw[4] = {v.x, v.y, v.z, v.w};
@@ -156,8 +170,49 @@ __device__ __forceinline__ uint64_t block_sum(const u32x4 v, uint32_t& l) {
         s3 = dot2(dp, kPowDigits.pair[c / 2][3], s3);
     }
     l = m & 0xFFu;
-    return uint64_t(int64_t(s0)) + (uint64_t(int64_t(s1)) << 16) + (uint64_t(int64_t(s2)) << 32) +
-           (uint64_t(int64_t(s3)) << 48);
+    return digit_sum(s0, s1, s2, s3);
+}
+
+// Byte k of `a` in byte 0 and byte k of `b` in byte 2, zeros elsewhere (v_perm_b32: selector 0x0c gives a zero byte).
+__device__ __forceinline__ uint32_t pair_byte(uint32_t a, uint32_t b, int k) {
+    return __builtin_amdgcn_perm(b, a, uint32_t(k) | 0x0c00u | (uint32_t(4 + k) << 16) | 0x0c000000u);
+}
+
+// The Horner sums of 128 bytes of two segments at once: the true low bytes of their states sit in the low bytes of
+// the halves of `m` (segment A low, B high, each half's high byte 0).  Per step one permute lines up a byte of each,
+// one xor, one packed subtract gives both d values, one 24-bit multiply and a mask the next low bytes (the masked
+// byte A's product stays below bit 16, as in step_pair); every two steps two permutes regroup the d values per segment
+// for the dot products.  The digits are those of p^1 .. p^128, so the
+// 64-bit sums are formed once per 128 bytes (|S_j| < 128 * 255 * 2^15 < 2^31 stays exact): about 5 VALU operations
+// per byte, against 7.5 for one segment at a time (3.3 GB: 0.78-0.79 ms, from 1.01).
+constexpr int kPairBytes = 128;
+constexpr PowDigits<kPairBytes> kPowDigitsPair = pow_digits<kPairBytes>();
+constexpr uint64_t kPrimePair = prime_pow<kPairBytes>();
+__device__ __forceinline__ void run_sum2(const u32x4 (&va)[kPairBytes / 16], const u32x4 (&vb)[kPairBytes / 16],
+                                         uint32_t& m, uint64_t& sa, uint64_t& sb) {
+    int32_t a0 = 0, a1 = 0, a2 = 0, a3 = 0, b0 = 0, b1 = 0, b2 = 0, b3 = 0;
+#pragma unroll
+    for (int c = 0; c < kPairBytes; c += 2) {
+        const int w0 = c >> 2, w1 = (c + 1) >> 2;   // the dwords of bytes c and c + 1
+        const uint32_t x0 = m ^ pair_byte(va[w0 >> 2][w0 & 3], vb[w0 >> 2][w0 & 3], c & 3);
+        const uint32_t d0 = pk_sub(x0, m);
+        m = __umul24(x0, kPrimeLow) & 0x00FF00FFu;
+        const uint32_t x1 = m ^ pair_byte(va[w1 >> 2][w1 & 3], vb[w1 >> 2][w1 & 3], (c + 1) & 3);
+        const uint32_t d1 = pk_sub(x1, m);
+        m = __umul24(x1, kPrimeLow) & 0x00FF00FFu;
+        const uint32_t da = __builtin_amdgcn_perm(d1, d0, 0x05040100u);   // A: d_c | d_(c+1) << 16
+        const uint32_t db = __builtin_amdgcn_perm(d1, d0, 0x07060302u);   // B
+        a0 = dot2(da, kPowDigitsPair.pair[c / 2][0], a0);
+        a1 = dot2(da, kPowDigitsPair.pair[c / 2][1], a1);
+        a2 = dot2(da, kPowDigitsPair.pair[c / 2][2], a2);
+        a3 = dot2(da, kPowDigitsPair.pair[c / 2][3], a3);
+        b0 = dot2(db, kPowDigitsPair.pair[c / 2][0], b0);
+        b1 = dot2(db, kPowDigitsPair.pair[c / 2][1], b1);
+        b2 = dot2(db, kPowDigitsPair.pair[c / 2][2], b2);
+        b3 = dot2(db, kPowDigitsPair.pair[c / 2][3], b3);
+    }
+    sa = digit_sum(a0, a1, a2, a3);
+    sb = digit_sum(b0, b1, b2, b3);
 }
 
 // One step of the full hash given the true low byte `l` of the state: accumulate d = (l ^ b) - l, then multiply.
@@ -210,12 +265,12 @@ __device__ __forceinline__ void wave_masks(const uint64_t (&wd)[kMaxPassWords], 
     st = next;
 }
 
-// This lane's true start bits j .. j + kBits - 1 (bit 0 of the result upward), from its workgroup's start state and
-// the ballots of the workgroup's waves.
+// This lane's true start bits j .. j + kBits - 1 (bit 0 of the result upward) in the pass's workgroup `group`, from
+// that workgroup's start state and the ballots of its waves.
 template <int kBits>
-__device__ __forceinline__ uint32_t lane_bits(uint32_t gstate, const PassWords& w) {
+__device__ __forceinline__ uint32_t lane_bits(uint64_t group, uint32_t gstate, const PassWords& w) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint64_t base = uint64_t(blockIdx.x) * 4;
+    const uint64_t base = group * 4;
     uint32_t st = gstate;
     uint64_t m[3] = {0, 0, 0};
     // every word this lane may need is loaded before the first step, so the loads overlap
@@ -306,7 +361,7 @@ __global__ void __launch_bounds__(kThreads) fnv_pass_kernel(const uint8_t* data,
     const bool live = begin < n;
     uint32_t s = 0;
     if constexpr (kPrevBits > 0) {
-        const uint32_t bits = lane_bits<kPrevBits>(gstate_prev[blockIdx.x], prev);
+        const uint32_t bits = lane_bits<kPrevBits>(blockIdx.x, gstate_prev[blockIdx.x], prev);
         const int lo = j - kPrevBits;
         s = (lo > 0 && live ? uint32_t(start[seg]) : 0u) | (bits << lo);
         if (live) start[seg] = uint8_t(s);
@@ -465,31 +520,57 @@ __device__ __forceinline__ uint64_t shfl_xor64(uint64_t v, int m) {
     return (uint64_t(hi) << 32) | lo;
 }
 
-__global__ void __launch_bounds__(kThreads) fnv_final_kernel(const uint8_t* data, uint64_t n, bool aligned,
-                                                              const uint8_t* start, PassWords prev,
-                                                              const uint8_t* gstate_prev, uint64_t* partial) {
-    const uint64_t seg = uint64_t(blockIdx.x) * kThreads + threadIdx.x;
-    const uint64_t begin = seg * kFnvLaneBytes;
-    const uint32_t bits67 = lane_bits<2>(gstate_prev[blockIdx.x], prev);
+// One segment's Horner sum, scaled by p^(bytes after it), from the true low byte `l` at its start.
+__device__ __forceinline__ uint64_t segment_sum(const uint8_t* data, uint64_t n, uint64_t begin, bool aligned,
+                                                uint32_t l) {
+    const uint64_t len = n - begin < kFnvLaneBytes ? n - begin : kFnvLaneBytes;
+    const uint8_t* p = data + begin;
     uint64_t acc = 0;
-    if (begin < n) {
-        uint32_t l = uint32_t(start[seg]) | (bits67 << 6);
-        const uint64_t len = n - begin < kFnvLaneBytes ? n - begin : kFnvLaneBytes;
-        const uint8_t* p = data + begin;
-        if (aligned && len == kFnvLaneBytes) {
-            // the whole segment is loaded first (lanes are 256 bytes apart, so each 128-byte line is read by eight
-            // of a lane's loads, issued together), then 16 bytes per step: a block sum, then acc * p^16.  Loading
-            // the wave's 16 KiB with coalesced loads and handing segments to lanes through LDS measured slower
-            // (the 68 KiB of LDS per workgroup halves the waves per SIMD)
-            u32x4 v[kFnvLaneBytes / 16];
+    if (aligned && len == kFnvLaneBytes) {
+        u32x4 v[kFnvLaneBytes / 16];
 #pragma unroll
-            for (int k = 0; k < kFnvLaneBytes / 16; ++k) v[k] = *(const gu32x4*) (p + 16 * k);
+        for (int k = 0; k < kFnvLaneBytes / 16; ++k) v[k] = *(const gu32x4*) (p + 16 * k);
 #pragma unroll
-            for (int k = 0; k < kFnvLaneBytes / 16; ++k) acc = acc * kPrime16 + block_sum(v[k], l);
-        } else {
-            for (uint64_t i = 0; i < len; ++i) step_full(p[i], l, acc);
+        for (int k = 0; k < kFnvLaneBytes / 16; ++k) acc = acc * kPrime16 + block_sum(v[k], l);
+    } else {
+        for (uint64_t i = 0; i < len; ++i) step_full(p[i], l, acc);
+    }
+    return acc * pow_prime(n - begin - len);
+}
+
+// Each lane takes two segments, its own in the pass's workgroups 2g and 2g + 1, and runs their machines side by side
+// (run_sum2).  A lane's segment is read in two halves of 128 bytes, each half of both segments loaded before it is
+// summed (lanes are 256 bytes apart, so each half is one 128-byte line per segment, read by eight loads issued
+// together).  The last, partial segments and unaligned data take the one-segment path.
+__global__ void __launch_bounds__(kThreads) fnv_final_kernel(const uint8_t* data, uint64_t n, uint64_t groups,
+                                                              bool aligned, const uint8_t* start, PassWords prev,
+                                                              const uint8_t* gstate_prev, uint64_t* partial) {
+    const uint64_t ga = uint64_t(blockIdx.x) * 2, gb = ga + 1;
+    const uint64_t sa = ga * kThreads + threadIdx.x, sb = gb * kThreads + threadIdx.x;
+    const uint64_t ba = sa * kFnvLaneBytes, bb = sb * kFnvLaneBytes;
+    const uint32_t bits_a = lane_bits<2>(ga, gstate_prev[ga], prev);
+    const uint32_t bits_b = gb < groups ? lane_bits<2>(gb, gstate_prev[gb], prev) : 0u;
+    uint64_t acc = 0;
+    if (aligned && bb + kFnvLaneBytes <= n) {   // both segments whole
+        uint32_t m = (uint32_t(start[sa]) | (bits_a << 6)) | ((uint32_t(start[sb]) | (bits_b << 6)) << 16);
+        uint64_t acc_a = 0, acc_b = 0;
+#pragma unroll 1
+        for (int h = 0; h < kFnvLaneBytes; h += kPairBytes) {
+            u32x4 va[kPairBytes / 16], vb[kPairBytes / 16];
+#pragma unroll
+            for (int k = 0; k < kPairBytes / 16; ++k) {
+                va[k] = *(const gu32x4*) (data + ba + h + 16 * k);
+                vb[k] = *(const gu32x4*) (data + bb + h + 16 * k);
+            }
+            uint64_t s_a, s_b;
+            run_sum2(va, vb, m, s_a, s_b);
+            acc_a = acc_a * kPrimePair + s_a;
+            acc_b = acc_b * kPrimePair + s_b;
         }
-        acc *= pow_prime(n - begin - len);
+        acc = acc_a * pow_prime(n - ba - kFnvLaneBytes) + acc_b * pow_prime(n - bb - kFnvLaneBytes);
+    } else {
+        if (ba < n) acc += segment_sum(data, n, ba, aligned, uint32_t(start[sa]) | (bits_a << 6));
+        if (bb < n) acc += segment_sum(data, n, bb, aligned, uint32_t(start[sb]) | (bits_b << 6));
     }
     for (int m = 32; m > 0; m >>= 1) acc += shfl_xor64(acc, m);
     __shared__ uint64_t s_sum[kThreads / 64];
@@ -555,6 +636,7 @@ hipError_t launch_fnv1a64(const void* data, uint64_t n, uint64_t seed, const uin
     const uint64_t half = (w.off_partial - w.off_prefix) / 2;
     uint8_t* gstate[2] = {ws + w.off_prefix, ws + w.off_prefix + half};
     uint64_t* partial = reinterpret_cast<uint64_t*>(ws + w.off_partial);
+    const uint64_t final_groups = (w.groups + 1) / 2;   // the final pass takes two of the passes' workgroups each
     if (w.groups > 0) {
         // bits 0-2, then 3-5 (four machines per lane), then 6-7 (two): three reads of the data before the final one;
         // each pass reads the previous pass's ballots and workgroup states
@@ -568,12 +650,12 @@ hipError_t launch_fnv1a64(const void* data, uint64_t n, uint64_t seed, const uin
         hipLaunchKernelGGL((fnv_pass_kernel<2, 3>), grid, block, 0, stream, src, n, 6, aligned, start, set[1],
                            gstate[1], set[0], summary);
         hipLaunchKernelGGL(fnv_scan_kernel<2>, one, scan, 0, stream, summary, w.groups, 6, seed, seed_dev, gstate[0]);
-        hipLaunchKernelGGL(fnv_final_kernel, grid, block, 0, stream, src, n, aligned, start, set[0], gstate[0],
-                           partial);
+        hipLaunchKernelGGL(fnv_final_kernel, dim3(unsigned(final_groups)), block, 0, stream, src, n, w.groups, aligned,
+                           start, set[0], gstate[0], partial);
     }
     // the reduce reads the start state before it writes `out`, so `out` may be `seed_dev` itself
-    hipLaunchKernelGGL(fnv_reduce_kernel, dim3(1), dim3(kScanThreads), 0, stream, partial, w.groups, seed, seed_dev, n,
-                       out, expected, verdict);
+    hipLaunchKernelGGL(fnv_reduce_kernel, dim3(1), dim3(kScanThreads), 0, stream, partial, final_groups, seed, seed_dev,
+                       n, out, expected, verdict);
     return hipGetLastError();
 }
 
