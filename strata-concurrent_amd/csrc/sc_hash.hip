@@ -178,41 +178,55 @@ __device__ __forceinline__ uint32_t pair_byte(uint32_t a, uint32_t b, int k) {
     return __builtin_amdgcn_perm(b, a, uint32_t(k) | 0x0c00u | (uint32_t(4 + k) << 16) | 0x0c000000u);
 }
 
-// The Horner sums of 128 bytes of two segments at once: the true low bytes of their states sit in the low bytes of
-// the halves of `m` (segment A low, B high, each half's high byte 0).  Per step one permute lines up a byte of each,
-// one xor, one packed subtract gives both d values, one 24-bit multiply and a mask the next low bytes (the masked
-// byte A's product stays below bit 16, as in step_pair); every two steps two permutes regroup the d values per segment
-// for the dot products.  The digits are those of p^1 .. p^128, so the
-// 64-bit sums are formed once per 128 bytes (|S_j| < 128 * 255 * 2^15 < 2^31 stays exact): about 5 VALU operations
-// per byte, against 7.5 for one segment at a time (3.3 GB: 0.78-0.79 ms, from 1.01).
+// The Horner sums of 128 bytes of two segments at once, as one sum: the true low bytes of their states sit in the
+// low bytes of the halves of `m` (segment A low, B high, each half's high byte 0), and B starts kPairGap bytes after
+// A.  Per step one permute lines up a byte of each, one xor, one packed subtract gives both d values (A's in the low
+// half), one 24-bit multiply and a mask the next low bytes (the masked byte A's product stays below bit 16, as in
+// step_pair).  Byte c of B is weighted by p^(128 - c) and byte c of A by p^(kPairGap + 128 - c), so each digit sum
+// takes one packed dot product per step against a word holding both digits, and the block sum is A's and B's scaled
+// to B's block end; the 64-bit sums are formed once per 128 bytes (|S_j| < 128 * 2 * 255 * 2^15 < 2^31 stays exact).
+// About 4 VALU operations per byte of each segment, against 7.5 for one segment at a time.
 constexpr int kPairBytes = 128;
-constexpr PowDigits<kPairBytes> kPowDigitsPair = pow_digits<kPairBytes>();
-constexpr uint64_t kPrimePair = prime_pow<kPairBytes>();
-__device__ __forceinline__ void run_sum2(const u32x4 (&va)[kPairBytes / 16], const u32x4 (&vb)[kPairBytes / 16],
-                                         uint32_t& m, uint64_t& sa, uint64_t& sb) {
-    int32_t a0 = 0, a1 = 0, a2 = 0, a3 = 0, b0 = 0, b1 = 0, b2 = 0, b3 = 0;
-#pragma unroll
-    for (int c = 0; c < kPairBytes; c += 2) {
-        const int w0 = c >> 2, w1 = (c + 1) >> 2;   // the dwords of bytes c and c + 1
-        const uint32_t x0 = m ^ pair_byte(va[w0 >> 2][w0 & 3], vb[w0 >> 2][w0 & 3], c & 3);
-        const uint32_t d0 = pk_sub(x0, m);
-        m = __umul24(x0, kPrimeLow) & 0x00FF00FFu;
-        const uint32_t x1 = m ^ pair_byte(va[w1 >> 2][w1 & 3], vb[w1 >> 2][w1 & 3], (c + 1) & 3);
-        const uint32_t d1 = pk_sub(x1, m);
-        m = __umul24(x1, kPrimeLow) & 0x00FF00FFu;
-        const uint32_t da = __builtin_amdgcn_perm(d1, d0, 0x05040100u);   // A: d_c | d_(c+1) << 16
-        const uint32_t db = __builtin_amdgcn_perm(d1, d0, 0x07060302u);   // B
-        a0 = dot2(da, kPowDigitsPair.pair[c / 2][0], a0);
-        a1 = dot2(da, kPowDigitsPair.pair[c / 2][1], a1);
-        a2 = dot2(da, kPowDigitsPair.pair[c / 2][2], a2);
-        a3 = dot2(da, kPowDigitsPair.pair[c / 2][3], a3);
-        b0 = dot2(db, kPowDigitsPair.pair[c / 2][0], b0);
-        b1 = dot2(db, kPowDigitsPair.pair[c / 2][1], b1);
-        b2 = dot2(db, kPowDigitsPair.pair[c / 2][2], b2);
-        b3 = dot2(db, kPowDigitsPair.pair[c / 2][3], b3);
+constexpr uint64_t kPairGap = uint64_t(kThreads) * kFnvLaneBytes;   // a lane's two segments, a workgroup apart
+constexpr uint64_t prime_pow_of(uint64_t e) {
+    uint64_t r = 1, b = kFnvPrime;
+    for (; e; e >>= 1, b *= b)
+        if (e & 1) r *= b;
+    return r;
+}
+struct PairDigits {
+    uint32_t w[kPairBytes][4];   // [c][j]: digit j of p^(kPairGap + 128 - c) in the low half, of p^(128 - c) above
+};
+constexpr PairDigits pair_digits() {
+    PairDigits t{};
+    for (int c = 0; c < kPairBytes; ++c) {
+        uint64_t va = prime_pow_of(kPairGap + kPairBytes - c), vb = prime_pow_of(kPairBytes - c);
+        for (int j = 0; j < 4; ++j) {
+            const int32_t da = int32_t(int16_t(uint16_t(va & 0xFFFFu))), db = int32_t(int16_t(uint16_t(vb & 0xFFFFu)));
+            t.w[c][j] = (uint32_t(da) & 0xFFFFu) | (uint32_t(db) << 16);
+            va = (va - uint64_t(int64_t(da))) >> 16;
+            vb = (vb - uint64_t(int64_t(db))) >> 16;
+        }
     }
-    sa = digit_sum(a0, a1, a2, a3);
-    sb = digit_sum(b0, b1, b2, b3);
+    return t;
+}
+constexpr PairDigits kPairDigits = pair_digits();
+constexpr uint64_t kPrimePair = prime_pow<kPairBytes>();
+__device__ __forceinline__ uint64_t run_sum2(const u32x4 (&va)[kPairBytes / 16], const u32x4 (&vb)[kPairBytes / 16],
+                                             uint32_t& m) {
+    int32_t s0 = 0, s1 = 0, s2 = 0, s3 = 0;
+#pragma unroll
+    for (int c = 0; c < kPairBytes; ++c) {
+        const int w = c >> 2;   // the dword of byte c
+        const uint32_t x = m ^ pair_byte(va[w >> 2][w & 3], vb[w >> 2][w & 3], c & 3);
+        const uint32_t d = pk_sub(x, m);
+        m = __umul24(x, kPrimeLow) & 0x00FF00FFu;
+        s0 = dot2(d, kPairDigits.w[c][0], s0);
+        s1 = dot2(d, kPairDigits.w[c][1], s1);
+        s2 = dot2(d, kPairDigits.w[c][2], s2);
+        s3 = dot2(d, kPairDigits.w[c][3], s3);
+    }
+    return digit_sum(s0, s1, s2, s3);
 }
 
 // One step of the full hash given the true low byte `l` of the state: accumulate d = (l ^ b) - l, then multiply.
@@ -553,7 +567,7 @@ __global__ void __launch_bounds__(kThreads) fnv_final_kernel(const uint8_t* data
     uint64_t acc = 0;
     if (aligned && bb + kFnvLaneBytes <= n) {   // both segments whole
         uint32_t m = (uint32_t(start[sa]) | (bits_a << 6)) | ((uint32_t(start[sb]) | (bits_b << 6)) << 16);
-        uint64_t acc_a = 0, acc_b = 0;
+        uint64_t acc2 = 0;
 #pragma unroll 1
         for (int h = 0; h < kFnvLaneBytes; h += kPairBytes) {
             u32x4 va[kPairBytes / 16], vb[kPairBytes / 16];
@@ -562,12 +576,9 @@ __global__ void __launch_bounds__(kThreads) fnv_final_kernel(const uint8_t* data
                 va[k] = *(const gu32x4*) (data + ba + h + 16 * k);
                 vb[k] = *(const gu32x4*) (data + bb + h + 16 * k);
             }
-            uint64_t s_a, s_b;
-            run_sum2(va, vb, m, s_a, s_b);
-            acc_a = acc_a * kPrimePair + s_a;
-            acc_b = acc_b * kPrimePair + s_b;
+            acc2 = acc2 * kPrimePair + run_sum2(va, vb, m);
         }
-        acc = acc_a * pow_prime(n - ba - kFnvLaneBytes) + acc_b * pow_prime(n - bb - kFnvLaneBytes);
+        acc = acc2 * pow_prime(n - bb - kFnvLaneBytes);   // both segments, scaled to B's end
     } else {
         if (ba < n) acc += segment_sum(data, n, ba, aligned, uint32_t(start[sa]) | (bits_a << 6));
         if (bb < n) acc += segment_sum(data, n, bb, aligned, uint32_t(start[sb]) | (bits_b << 6));
