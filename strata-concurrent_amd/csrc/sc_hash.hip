@@ -212,6 +212,17 @@ constexpr PairDigits pair_digits() {
 }
 constexpr PairDigits kPairDigits = pair_digits();
 constexpr uint64_t kPrimePair = prime_pow<kPairBytes>();
+// p^(256 (63 - l)) for lane l: a lane's sum, relative to the end of its segment B, times this is relative to the end of
+// the wave's last segment B.
+struct LanePow {
+    uint64_t v[64];
+};
+constexpr LanePow lane_pow() {
+    LanePow t{};
+    for (int l = 0; l < 64; ++l) t.v[l] = prime_pow_of(uint64_t(kFnvLaneBytes) * uint64_t(63 - l));
+    return t;
+}
+__constant__ LanePow kLanePow = lane_pow();
 __device__ __forceinline__ uint64_t run_sum2(const u32x4 (&va)[kPairBytes / 16], const u32x4 (&vb)[kPairBytes / 16],
                                              uint32_t& m) {
     int32_t s0 = 0, s1 = 0, s2 = 0, s3 = 0;
@@ -283,7 +294,8 @@ __device__ __forceinline__ void wave_masks(const uint64_t (&wd)[kMaxPassWords], 
 // that workgroup's start state and the ballots of its waves.
 template <int kBits>
 __device__ __forceinline__ uint32_t lane_bits(uint64_t group, uint32_t gstate, const PassWords& w) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    // the wave index is read as wave-uniform, so the masks below are scalar work
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint64_t base = group * 4;
     uint32_t st = gstate;
     uint64_t m[3] = {0, 0, 0};
@@ -362,6 +374,31 @@ __device__ __forceinline__ void run_quad(const uint8_t* p, uint64_t n, bool full
     }
 }
 
+__device__ __forceinline__ uint32_t map_v(uint32_t m, uint32_t a) { return (m >> (1u + a)) & 1u; }
+__device__ __forceinline__ uint32_t map_w(uint32_t m, uint32_t a, uint32_t c) { return (m >> (3u + 2u * a + c)) & 1u; }
+template <int kBits>
+__device__ __forceinline__ uint32_t compose(uint32_t g, uint32_t f) {
+    const uint32_t tf = f & 1u;
+    uint32_t r = tf ^ (g & 1u);
+#pragma unroll
+    for (uint32_t a = 0; a < 2; ++a) r |= (map_v(f, a) ^ map_v(g, a ^ tf)) << (1u + a);
+    if constexpr (kBits == 3) {
+#pragma unroll
+        for (uint32_t a = 0; a < 2; ++a)
+#pragma unroll
+            for (uint32_t c = 0; c < 2; ++c)
+                r |= (map_w(f, a, c) ^ map_w(g, a ^ tf, c ^ map_v(f, a))) << (3u + 2u * a + c);
+    }
+    return r;
+}
+template <int kBits>
+__device__ __forceinline__ uint32_t apply(uint32_t m, uint32_t st) {
+    const uint32_t a = st & 1u, c = (st >> 1) & 1u;
+    uint32_t r = (a ^ (m & 1u)) | ((c ^ map_v(m, a)) << 1);
+    if constexpr (kBits == 3) r |= (((st >> 2) & 1u) ^ map_w(m, a, c)) << 2;
+    return r;
+}
+
 // Data pass for bits j .. j + kBits - 1.  First completes each segment's start bits from the previous pass (which
 // resolved kPrevBits bits; the bits below it are in start[]), then runs the machines - two (start bit j = 0, 1) for
 // a two-bit pass, four (start bits j, j + 1 = 00, 10, 01, 11) for a three-bit one - ballots the terms, and leaves
@@ -412,33 +449,31 @@ __global__ void __launch_bounds__(kThreads) fnv_pass_kernel(const uint8_t* data,
         bw[5] = __ballot((ea >> (16 + j + 2)) & 1u);   // (1, 0)
         bw[6] = __ballot((eb >> (16 + j + 2)) & 1u);   // (1, 1)
     }
-    __shared__ uint64_t s_w[kMaxPassWords][kThreads / 64];
-    const int wave = threadIdx.x >> 6;
+    // this wave's map of the state at its first segment, from its ballots (wave-uniform, so scalar work); the
+    // workgroup's map is the four waves' maps composed in order
+    uint32_t wmap = 0;
+#pragma unroll
+    for (uint32_t in = 0; in < (1u << (kBits - 1)); ++in) {   // start (a, c) = (in & 1, in >> 1), e = 0
+        const uint32_t a = in & 1u, c = (in >> 1) & 1u;
+        uint32_t st = in;
+        uint64_t m[3];
+        wave_masks<kBits>(bw, st, m);
+        if (in == 0) wmap |= st & 1u;                                  // t
+        if (c == 0) wmap |= ((st >> 1) & 1u) << (1 + a);               // v_a: the end bit j + 1 from c = 0
+        if constexpr (kBits == 3) wmap |= ((st >> 2) & 1u) << (3 + 2 * a + c);   // w_ac: end bit j + 2 from e = 0
+    }
+    __shared__ uint32_t s_map[kThreads / 64];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if ((threadIdx.x & 63) == 0) {
         const uint64_t at = uint64_t(blockIdx.x) * 4 + wave;
 #pragma unroll
-        for (int i = 0; i < pass_words<kBits>(); ++i) {
-            out.w[i][at] = bw[i];
-            s_w[i][wave] = bw[i];
-        }
+        for (int i = 0; i < pass_words<kBits>(); ++i) out.w[i][at] = bw[i];
+        s_map[wave] = wmap;
     }
     __syncthreads();
     if (threadIdx.x == 0) {
-        uint32_t sum = 0;
-        for (uint32_t in = 0; in < (1u << (kBits - 1)); ++in) {   // start (a, c) = (in & 1, in >> 1), e = 0
-            const uint32_t a = in & 1u, c = (in >> 1) & 1u;
-            uint32_t st = in;
-            uint64_t m[3];
-            for (int k = 0; k < kThreads / 64; ++k) {
-                uint64_t wd[kMaxPassWords] = {};
-#pragma unroll
-                for (int i = 0; i < pass_words<kBits>(); ++i) wd[i] = s_w[i][k];
-                wave_masks<kBits>(wd, st, m);
-            }
-            if (in == 0) sum |= st & 1u;                                  // t
-            if (c == 0) sum |= ((st >> 1) & 1u) << (1 + a);               // v_a: the end bit j + 1 from c = 0
-            if constexpr (kBits == 3) sum |= ((st >> 2) & 1u) << (3 + 2 * a + c);   // w_ac: end bit j + 2 from e = 0
-        }
+        uint32_t sum = s_map[0];
+        for (int k = 1; k < kThreads / 64; ++k) sum = compose<kBits>(s_map[k], sum);
         summary[blockIdx.x] = uint8_t(sum);
     }
 }
@@ -455,31 +490,6 @@ __device__ __forceinline__ uint64_t start_state(uint64_t seed, const uint64_t* s
 // as (g after f): t = t_f ^ t_g, v_a = v_a(f) ^ v_(a ^ t_f)(g), w_ac = w_ac(f) ^ w_(a ^ t_f, c ^ v_a(f))(g).
 // Each thread composes its run of summaries (read 16 bytes at a time), the runs are scanned across threads in LDS,
 // and each thread then walks its run again from its start state, writing the states 16 at a time.
-__device__ __forceinline__ uint32_t map_v(uint32_t m, uint32_t a) { return (m >> (1u + a)) & 1u; }
-__device__ __forceinline__ uint32_t map_w(uint32_t m, uint32_t a, uint32_t c) { return (m >> (3u + 2u * a + c)) & 1u; }
-template <int kBits>
-__device__ __forceinline__ uint32_t compose(uint32_t g, uint32_t f) {
-    const uint32_t tf = f & 1u;
-    uint32_t r = tf ^ (g & 1u);
-#pragma unroll
-    for (uint32_t a = 0; a < 2; ++a) r |= (map_v(f, a) ^ map_v(g, a ^ tf)) << (1u + a);
-    if constexpr (kBits == 3) {
-#pragma unroll
-        for (uint32_t a = 0; a < 2; ++a)
-#pragma unroll
-            for (uint32_t c = 0; c < 2; ++c)
-                r |= (map_w(f, a, c) ^ map_w(g, a ^ tf, c ^ map_v(f, a))) << (3u + 2u * a + c);
-    }
-    return r;
-}
-template <int kBits>
-__device__ __forceinline__ uint32_t apply(uint32_t m, uint32_t st) {
-    const uint32_t a = st & 1u, c = (st >> 1) & 1u;
-    uint32_t r = (a ^ (m & 1u)) | ((c ^ map_v(m, a)) << 1);
-    if constexpr (kBits == 3) r |= (((st >> 2) & 1u) ^ map_w(m, a, c)) << 2;
-    return r;
-}
-
 constexpr uint64_t kScanVec = 16;   // summary bytes per vector load / state bytes per vector store
 
 template <int kBits>
@@ -564,6 +574,11 @@ __global__ void __launch_bounds__(kThreads) fnv_final_kernel(const uint8_t* data
     const uint64_t ba = sa * kFnvLaneBytes, bb = sb * kFnvLaneBytes;
     const uint32_t bits_a = lane_bits<2>(ga, gstate_prev[ga], prev);
     const uint32_t bits_b = gb < groups ? lane_bits<2>(gb, gstate_prev[gb], prev) : 0u;
+    // p^(n - r), r the end of the wave's last segment B: wave-uniform, one power per wave rather than one per lane.  p
+    // has order dividing 2^62 modulo 2^64, so the exponent is taken modulo 2^62 (r passes n in the buffer's last wave)
+    const uint64_t wave_end =
+        (gb * kThreads + uint64_t(__builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) * 64 + 64) * kFnvLaneBytes;
+    const uint64_t wave_pow = pow_prime((n - wave_end) & ((uint64_t(1) << 62) - 1));
     uint64_t acc = 0;
     if (aligned && bb + kFnvLaneBytes <= n) {   // both segments whole
         uint32_t m = (uint32_t(start[sa]) | (bits_a << 6)) | ((uint32_t(start[sb]) | (bits_b << 6)) << 16);
@@ -578,7 +593,7 @@ __global__ void __launch_bounds__(kThreads) fnv_final_kernel(const uint8_t* data
             }
             acc2 = acc2 * kPrimePair + run_sum2(va, vb, m);
         }
-        acc = acc2 * pow_prime(n - bb - kFnvLaneBytes);   // both segments, scaled to B's end
+        acc = acc2 * kLanePow.v[threadIdx.x & 63] * wave_pow;   // both segments, scaled to the input's end
     } else {
         if (ba < n) acc += segment_sum(data, n, ba, aligned, uint32_t(start[sa]) | (bits_a << 6));
         if (bb < n) acc += segment_sum(data, n, bb, aligned, uint32_t(start[sb]) | (bits_b << 6));
