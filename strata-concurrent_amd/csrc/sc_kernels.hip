@@ -49,6 +49,13 @@ using gi32 = __attribute__((address_space(1))) const int32_t;
 __device__ __forceinline__ int32_t table_entry(const MoveRow& r, uint32_t page) {
     return r.table ? *(gi32*) (r.table + page) : int32_t(page);
 }
+// The same entry for a wave-uniform page, read with a scalar load (through the constant address space: no kernel
+// writes a table).  A vector load would share the wave's in-order load counter, so taking its value into a scalar
+// register would first wait for every row load issued before it.
+using ci32 = __attribute__((address_space(4))) const int32_t;
+__device__ __forceinline__ int32_t table_entry_uniform(const MoveRow& r, uint32_t page) {
+    return r.table ? *((ci32*) r.table + page) : int32_t(page);
+}
 
 // The (cell, head) address of K/V source row `src_row` (token-major [T][H]): the logical page, and the row's
 // place inside a physical page.
@@ -330,7 +337,7 @@ __device__ __forceinline__ int load_units(const MoveRow& r, const MoveGeo& g, ui
     }
 #pragma unroll
     for (int i = 0; i < kQuantUnitsPerWave; ++i)
-        if (i < n) phys[i] = __builtin_amdgcn_readfirstlane(table_entry(r, kv_cell(r, g, unit[i]).page));
+        if (i < n) phys[i] = table_entry_uniform(r, kv_cell(r, g, unit[i]).page);
     return n;
 }
 
