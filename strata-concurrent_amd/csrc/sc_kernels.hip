@@ -82,7 +82,10 @@ __device__ __forceinline__ int64_t pool_row(const MoveRow& r, const MoveGeo& g, 
 __device__ __forceinline__ uint32_t ordered_chunk(const MoveRow& r, const MoveGeo& g, uint32_t vq, bool kv) {
     const uint32_t vp = fdiv(vq, g.page_chunks);
     const uint32_t ip = vq - vp * g.page_chunks.d;
-    const int64_t lp = *(gi32*) (r.order + vp);
+    // a page of a multiple of 64 chunks holds the wave's 64 consecutive chunks, and its entry is then read with a
+    // scalar load
+    const int64_t lp = g.page_chunks.d % 64u == 0u ? *((ci32*) r.order + __builtin_amdgcn_readfirstlane(vp))
+                                                   : *(gi32*) (r.order + vp);
     if (lp < 0) return ~0u;
     const int64_t q = kv ? (lp * int64_t(g.page_size.d) - r.pos0) * int64_t(g.heads.d * g.row_chunks.d) + ip
                          : lp * int64_t(g.page_chunks.d) + ip;
