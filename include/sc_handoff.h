@@ -368,7 +368,10 @@ int sc_plan_resume_append(const sc_geometry* g, const sc_batch_desc* desc, sc_pl
  * slot (any non-null page table) has its K/V pages gathered through the tables straight into the pinned image by a
  * kernel that writes the host memory itself (no staging copy in HBM, nothing allocated; 32 layers per launch), then
  * its GDN rows by one copy; a page whose entry is negative or past the pool (not resident) is skipped, and its bytes
- * of the image are left as they were.  Replaces conversation_kv_save's synchronous per-16-MiB cudaMemcpy loop
+ * of the image are left as they were.  A paged slot's image must be pinned memory mapped for the device (sc_host_alloc,
+ * hipHostMalloc), which is checked before anything is enqueued (SC_EINVAL otherwise, see sc_host_range_mapped); an
+ * identity slot's image may be any host memory hipMemcpyAsync accepts.  Replaces conversation_kv_save's synchronous
+ * per-16-MiB cudaMemcpy loop
  * (conversation_snapshot.cpp:105-113, 160-171) and conversation_checkpoint_save's GDN copy (conversation_state.cpp:235). */
 int sc_park_async(const sc_geometry* g, const sc_decode_slot* slot, int64_t tokens, void* host_image,
                   uint64_t image_bytes, void* stream, void* done);
@@ -457,6 +460,9 @@ int sc_device_free(void* ptr);
 /* Pinned host memory (hipHostMalloc): the park pool. */
 int sc_host_alloc(void** ptr, uint64_t bytes);
 int sc_host_free(void* ptr);
+/* *mapped = 1 when [host, host + bytes) is pinned host memory mapped for the device (its first and last byte in one
+ * mapping), else 0: what a paged slot's park or resume checks before its kernel touches the image. */
+int sc_host_range_mapped(const void* host, uint64_t bytes, int32_t* mapped);
 /* hipMemcpyAsync(hipMemcpyDefault) on `stream`. */
 int sc_copy_async(void* dst, const void* src, uint64_t bytes, void* stream);
 /* A device-side fill of `bytes` bytes with `value` by a small kernel (never a memset node). */

@@ -1403,6 +1403,25 @@ int sc_plan_resume_append(const sc_geometry* g, const sc_batch_desc* d, sc_plan*
 
 // ---- park / resume --------------------------------------------------------------------------------------------
 
+// The device address of a pinned host range the device can reach, or nullptr: its first and last byte must both be
+// pinned host memory mapped for the device, at device addresses `bytes - 1` apart (one mapping).  A kernel that reads
+// or writes a host image itself needs this; a pageable image would fault the GPU rather than fail a copy.
+uint8_t* mapped_host_range(const void* host, uint64_t bytes) {
+    if (!host || bytes == 0) return nullptr;
+    hipPointerAttribute_t first{}, last{};
+    hipError_t e = hipPointerGetAttributes(&first, host);
+    if (e == hipSuccess) e = hipPointerGetAttributes(&last, static_cast<const uint8_t*>(host) + (bytes - 1));
+    if (e != hipSuccess) {
+        (void) hipGetLastError();   // an unknown pointer is an answer here, not an error for the next call
+        return nullptr;
+    }
+    if (first.type != hipMemoryTypeHost || last.type != hipMemoryTypeHost || !first.devicePointer ||
+        !last.devicePointer ||
+        static_cast<uint8_t*>(last.devicePointer) - static_cast<uint8_t*>(first.devicePointer) != ptrdiff_t(bytes - 1))
+        return nullptr;
+    return static_cast<uint8_t*>(first.devicePointer);
+}
+
 static int dma_image(const sc_geometry* g, const sc_decode_slot* slot, int64_t tokens, uint8_t* host,
                      uint64_t image_bytes, bool park, void* stream, void* done) {
     Geo o;
@@ -1417,6 +1436,12 @@ static int dma_image(const sc_geometry* g, const sc_decode_slot* slot, int64_t t
     uint64_t total = 0;
     const auto blobs = image_blobs(o, tokens, total);
     if (!host || image_bytes < total) return snapshot_fail("invalid K/V payload size");
+    // a paged slot's pages are moved by a kernel that reads or writes the image itself
+    uint8_t* host_dev = nullptr;
+    if (!identity && o.n_qsa > 0 && total > 0) {
+        host_dev = mapped_host_range(host, total);
+        if (!host_dev) return snapshot_fail("a paged slot's host image must be pinned memory mapped for the device");
+    }
     if (park) {
         // the gaps between blobs are never copied; clear them so the image is deterministic
         uint64_t at = 0;
@@ -1445,7 +1470,7 @@ static int dma_image(const sc_geometry* g, const sc_decode_slot* slot, int64_t t
                 a.pool[2 * j + 1] = reinterpret_cast<uint8_t*>(slot->v_pool[j0 + j]);
                 a.table[j] = slot->page_table ? slot->page_table[j0 + j] : nullptr;
             }
-            a.image = host + uint64_t(2 * j0) * stride;
+            a.image = host_dev + uint64_t(2 * j0) * stride;
             a.blob_stride = stride;
             a.blob_chunks = chunks;
             a.pool_pages = slot->n_pages;
@@ -1697,6 +1722,12 @@ int sc_host_alloc(void** ptr, uint64_t bytes) {
     const hipError_t e = hipHostMalloc(ptr, bytes ? bytes : 16, hipHostMallocDefault);
     return e == hipSuccess ? ok() : fail(SC_ENOMEM, std::string("sc_handoff: pinned allocation: ") + hipGetErrorString(e));
 }
+int sc_host_range_mapped(const void* host, uint64_t bytes, int32_t* mapped) {
+    if (!mapped) return fail(SC_EINVAL, "sc_handoff: missing output");
+    *mapped = mapped_host_range(host, bytes) ? 1 : 0;
+    return ok();
+}
+
 int sc_host_free(void* ptr) {
     SC_HIP(hipHostFree(ptr), "pinned free");
     return ok();

@@ -163,6 +163,7 @@ _SIGS = {
     "sc_device_free": (C.c_int, [_P]),
     "sc_host_alloc": (C.c_int, [C.POINTER(_P), _U64]),
     "sc_host_free": (C.c_int, [_P]),
+    "sc_host_range_mapped": (C.c_int, [_P, _U64, C.POINTER(C.c_int32)]),
     "sc_copy_async": (C.c_int, [_P, _P, _U64, _P]),
     "sc_fill_bytes_async": (C.c_int, [_P, C.c_uint8, _U64, _P]),
     "sc_stream_create": (C.c_int, [C.POINTER(_P)]),

@@ -161,3 +161,41 @@ def test_paged_park_resume_beyond_one_launch(sc, cuda):
     sc.device_sync()
     assert np.array_equal(again.numpy(total), image.numpy(total)), "paged resume"
     host.free()
+
+
+def test_paged_park_refuses_an_image_the_device_cannot_reach(sc, cuda):
+    """A paged slot's pages are moved by a kernel that reads or writes the host image itself, so the image must be
+    pinned memory mapped for the device: a pageable buffer is refused before anything is enqueued.  The park and the
+    resume are only attempted after sc_host_range_mapped has reported the buffer unmapped, the same check they make."""
+    import ctypes as C
+    geo = sc.geometry(n_layers=8, qsa_interval=4, n_head_kv=2, head_dim=256, page_size=4, ssm_state_size=32,
+                      ssm_k_heads=4, ssm_v_heads=8, ssm_d_conv=4, ssm_conv_channels=512)
+    tokens, max_cells = 61, 96
+    n_pages = max_cells // geo.page_size + 3
+    rng = np.random.default_rng(61)
+    tabs = sc.device_tables([rng.permutation(n_pages)[: max_cells // geo.page_size].astype(np.int32)
+                             for _ in range(geo.n_qsa)])
+    case = synth.SyntheticCase(geo, tokens, seed=611)
+    slot = case.new_slot(max_cells=max_cells, n_pages=n_pages, tables=tabs, fill=0x5A)
+    sc.device_sync()
+    _, total = sc.image_layout(geo, tokens)
+    pageable = np.full(total, 0x33, dtype=np.uint8)
+    mapped = C.c_int32(-1)
+    assert sc.lib.sc_host_range_mapped(pageable.ctypes.data, total, C.byref(mapped)) == sc.SC_OK
+    if mapped.value != 0:
+        pytest.fail("a pageable buffer reads as mapped for the device; the refusal below cannot be tested safely")
+    cs = slot.c_struct()
+    assert sc.lib.sc_park_async(C.byref(geo), C.byref(cs), tokens, pageable.ctypes.data, total, None, None) == \
+        sc.SC_EINVAL
+    assert "pinned memory mapped for the device" in sc.last_error()
+    assert sc.lib.sc_resume_async(C.byref(geo), pageable.ctypes.data, total, tokens, C.byref(cs), None, None) == \
+        sc.SC_EINVAL
+    sc.device_sync()
+    assert np.all(pageable == 0x33)
+    for name, pool in slot.host_state().items():
+        if name != "gdn":
+            assert np.all(pool.view(np.uint8) == 0x5A), name   # nothing was written
+    pinned = sc.PinnedBuffer(total)
+    assert sc.lib.sc_host_range_mapped(pinned.ptr, total, C.byref(mapped)) == sc.SC_OK
+    assert mapped.value == 1
+    pinned.free()
