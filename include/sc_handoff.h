@@ -105,7 +105,8 @@ typedef struct sc_decode_slot {
     /* A streamed layer's authoritative host copy and the prompt path's staging pool: NULL, or host arrays [n_qsa] of
      * sc_kv_pools in the identity layout [logical page][n_head_kv][page_size][row] holding max_cells cells (the host
      * copy is device-mapped pinned memory, the staging pool device memory).  An entry whose pools of the slot's
-     * format are NULL is skipped.  A carve writes every cell it carves into each given pool as well, resident in the
+     * format are NULL is skipped.  The kernels write a host copy straight into host memory, so one that is not
+     * pinned memory mapped for the device is refused when the plan is built (sc_host_range_mapped).  A carve writes every cell it carves into each given pool as well, resident in the
      * paged pool or not, in the same launch (kv_append, src/prefill/kernels.cu:574-577,587-600;
      * kv_append_q4, src/kernels/cuda/kv_q4.cu:124-128). */
     const sc_kv_pools* host;
@@ -187,7 +188,9 @@ int sc_plan_carve_quant(const sc_geometry* g, const sc_prefill_view* src, const 
 /* ---- kv_append: the per-layer prefill writers, with the reference's arguments ---------------------------------
  * One launch per call, nothing allocated, like the reference's own (the plans above build a whole slot in one launch
  * instead).  Every entry point returns before its launch when T <= 0, and refuses (SC_EINVAL, nothing launched)
- * missing or misaligned buffers and impossible extents; pools are not bounded, the caller sized them, as there. */
+ * missing or misaligned buffers and impossible extents; pools are not bounded, the caller sized them, as there.  A
+ * host copy is written by the kernel straight into host memory: the pages a call writes must be pinned memory mapped
+ * for the device, which is checked before the launch (SC_EINVAL otherwise). */
 
 
 /* kv_append (include/strata/prefill/kernels.hpp:78-83, src/prefill/kernels.cu:558-625): K and V, f32 [T][2][256]

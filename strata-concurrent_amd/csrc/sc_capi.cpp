@@ -488,13 +488,53 @@ void gdn_rows(const Geo& g, const sc_prefill_view* v, float* gdn, std::vector<sc
 // The identity-layout pools a carve writes beside the paged pool (a streamed layer's host copy, the prompt path's
 // staging pool): `pools` is NULL or [n_qsa].  Returns, per layer, the K, V (and int8 scale) destinations of `format`,
 // or nulls for a layer that has none; refuses half-given or misaligned pools.
+// The device address of a pinned host range the device can reach, or nullptr: its first and last byte must both be
+// pinned host memory mapped for the device, at device addresses `bytes - 1` apart (one mapping).  A kernel that reads
+// or writes a host image itself needs this; a pageable image would fault the GPU rather than fail a copy.
+uint8_t* mapped_host_range(const void* host, uint64_t bytes) {
+    if (!host || bytes == 0) return nullptr;
+    hipPointerAttribute_t first{}, last{};
+    hipError_t e = hipPointerGetAttributes(&first, host);
+    if (e == hipSuccess) e = hipPointerGetAttributes(&last, static_cast<const uint8_t*>(host) + (bytes - 1));
+    if (e != hipSuccess) {
+        (void) hipGetLastError();   // an unknown pointer is an answer here, not an error for the next call
+        return nullptr;
+    }
+    if (first.type != hipMemoryTypeHost || last.type != hipMemoryTypeHost || !first.devicePointer ||
+        !last.devicePointer ||
+        static_cast<uint8_t*>(last.devicePointer) - static_cast<uint8_t*>(first.devicePointer) != ptrdiff_t(bytes - 1))
+        return nullptr;
+    return static_cast<uint8_t*>(first.devicePointer);
+}
+
 struct ExtraKv {
     uint8_t* k = nullptr;
     uint8_t* v = nullptr;
     uint16_t* ks = nullptr;
     uint16_t* vs = nullptr;
 };
-int extra_kv(const Geo& g, const sc_kv_pools* pools, int32_t format, const char* what, std::vector<ExtraKv>& out) {
+// Bytes per (cell, head) row of a pool of `format`: codes (or f16 values), and int8 scales.
+uint64_t code_row_bytes(const Geo& g, int32_t format, bool value) {
+    if (format == SC_KV_F16) return uint64_t(g.D) * 2;
+    if (format == SC_KV_Q4 || (format == SC_KV_K8V4 && value)) return uint64_t(g.D) / 32 * 18;
+    return uint64_t(g.D);
+}
+uint64_t scale_row_bytes(const Geo& g) { return uint64_t(g.D) / 64 * 2; }
+
+// A host copy is written by the kernels themselves, so each of its pools must be pinned host memory mapped for the
+// device over the rows a launch may write, rows [row0, row0 + rows) of `H` heads; checked before anything is enqueued.
+int check_host_copy(const Geo& g, const ExtraKv& e, int32_t format, uint64_t row0, uint64_t rows) {
+    const uint64_t cr = code_row_bytes(g, format, false), vr = code_row_bytes(g, format, true), sr = scale_row_bytes(g);
+    const struct { const void* p; uint64_t row; } pools[4] = {{e.k, cr}, {e.v, vr}, {e.ks, sr}, {e.vs, sr}};
+    for (const auto& q : pools)
+        if (q.p && rows && !mapped_host_range(static_cast<const uint8_t*>(q.p) + row0 * q.row, rows * q.row))
+            return snapshot_fail("a host copy must be pinned memory mapped for the device");
+    return SC_OK;
+}
+
+// `map_cells` > 0: the pools are a host copy of that many cells (checked with check_host_copy).
+int extra_kv(const Geo& g, const sc_kv_pools* pools, int32_t format, const char* what, std::vector<ExtraKv>& out,
+             int64_t map_cells = 0) {
     out.assign(size_t(g.n_qsa), ExtraKv{});
     if (!pools) return SC_OK;
     for (int64_t j = 0; j < g.n_qsa; ++j) {
@@ -523,6 +563,10 @@ int extra_kv(const Geo& g, const sc_kv_pools* pools, int32_t format, const char*
         if (any && ((reinterpret_cast<uintptr_t>(e.k) | reinterpret_cast<uintptr_t>(e.v)) & (a - 1) ||
                     (format == SC_KV_INT8 && ((reinterpret_cast<uintptr_t>(e.ks) | reinterpret_cast<uintptr_t>(e.vs)) & 7u))))
             return fail(SC_EINVAL, std::string("sc_handoff: ") + what + " pools must be aligned as the slot's pools are");
+        if (any && map_cells > 0) {
+            const int rc = check_host_copy(g, e, format, 0, uint64_t(map_cells) * uint64_t(g.H));
+            if (rc) return rc;
+        }
     }
     return SC_OK;
 }
@@ -662,7 +706,8 @@ int sc_plan_carve(const sc_geometry* g, const sc_prefill_view* src, const sc_dec
         rc = check_slot(o, dst, src->pos0 + src->tokens, src->with_gdn != 0);
         if (rc) return rc;
         std::vector<ExtraKv> host, stage;
-        if ((rc = extra_kv(o, dst->host, SC_KV_F16, "a host copy", host)) ||
+        const int64_t host_cells = (dst->max_cells + o.ps - 1) / o.ps * o.ps;
+        if ((rc = extra_kv(o, dst->host, SC_KV_F16, "a host copy", host, host_cells)) ||
             (rc = extra_kv(o, dst->stage, SC_KV_F16, "a staging pool", stage)))
             return rc;
         const int64_t logical_pages = (dst->max_cells + o.ps - 1) / o.ps;
@@ -722,7 +767,8 @@ int sc_plan_carve_quant(const sc_geometry* g, const sc_prefill_view* src, const 
                 return fail(SC_EINVAL, "sc_handoff: GDN rows must be 16-byte aligned multiples of 16 bytes");
         }
         std::vector<ExtraKv> host, stage;
-        if ((rc = extra_kv(o, dst->host, dst->format, "a host copy", host)) ||
+        const int64_t host_cells = (dst->max_cells + o.ps - 1) / o.ps * o.ps;
+        if ((rc = extra_kv(o, dst->host, dst->format, "a host copy", host, host_cells)) ||
             (rc = extra_kv(o, dst->stage, dst->format, "a staging pool", stage)))
             return rc;
         const int64_t logical_pages = (dst->max_cells + o.ps - 1) / o.ps;
@@ -1149,6 +1195,7 @@ struct AppendDest {
     uint16_t* ks;
     uint16_t* vs;
     const int32_t* table;
+    bool host_copy = false;   // written by the kernel straight into host memory
 };
 
 // Checks and lays out the rows of one call.  `kind` is sc::kKv32, kKvQ8 or kKvQ4; `dests` holds the pool first.
@@ -1176,6 +1223,18 @@ int append_launch(int32_t kind, const float* K, const float* V, int64_t T, int64
             (kind == sc::kKvQ8 && (misaligned(a.ks, 8) || misaligned(a.vs, 8))))
             return fail(SC_EINVAL, "sc_handoff: kv_append: f16 pools must be 16-byte, int8 codes 4-byte, int8 scales "
                                    "8-byte and q4_0 pools 2-byte aligned");
+        if (a.host_copy) {
+            // the pages of cells [pos0, pos0 + T) of the identity layout, which the kernel writes in host memory
+            const uint64_t first = uint64_t(pos0 / page_size), end = uint64_t((pos0 + T + page_size - 1) / page_size);
+            const uint64_t row0 = first * uint64_t(page_size) * uint64_t(H), rows_n = (end - first) * uint64_t(page_size) * uint64_t(H);
+            const uint64_t code_row = kind == sc::kKv32 ? uint64_t(D) * 2 : kind == sc::kKvQ8 ? uint64_t(D) : uint64_t(D) / 32 * 18;
+            const struct { const void* p; uint64_t row; } pools[4] = {
+                {a.k, code_row}, {a.v, code_row}, {a.ks, uint64_t(D) / 64 * 2}, {a.vs, uint64_t(D) / 64 * 2}};
+            for (const auto& q : pools)
+                if (q.p && !mapped_host_range(static_cast<const uint8_t*>(q.p) + row0 * q.row, rows_n * q.row))
+                    return fail(SC_EINVAL, "sc_handoff: kv_append: a host copy must be pinned memory mapped for the "
+                                           "device");
+        }
         const float* srcs[2] = {K, V};
         void* codes[2] = {a.k, a.v};
         uint16_t* scales[2] = {a.ks, a.vs};
@@ -1218,8 +1277,8 @@ int sc_kv_append_async(const float* K, const float* V, int64_t T, int64_t pos0, 
                          : AppendDest{k_q, v_q, k_scale, v_scale, page_table};
         for (const sc_kv_pools* p : {host, stage}) {
             if (!p || !(f16 ? static_cast<const void*>(p->k_pool) : static_cast<const void*>(p->k_q))) continue;
-            dests[n++] = f16 ? AppendDest{p->k_pool, p->v_pool, nullptr, nullptr, nullptr}
-                             : AppendDest{p->k_q, p->v_q, p->k_scale, p->v_scale, nullptr};
+            dests[n++] = f16 ? AppendDest{p->k_pool, p->v_pool, nullptr, nullptr, nullptr, p == host}
+                             : AppendDest{p->k_q, p->v_q, p->k_scale, p->v_scale, nullptr, p == host};
         }
         return append_launch(f16 ? sc::kKv32 : sc::kKvQ8, K, V, T, pos0, 2, 256, page_size, dests, n, stream);
     });
@@ -1237,7 +1296,7 @@ int sc_kv_append_q4_async(uint8_t* k_q4, uint8_t* v_q4, const int32_t* page_tabl
         int n = 0;
         dests[n++] = AppendDest{k_q4, v_q4, nullptr, nullptr, page_table};
         for (const sc_kv_pools* p : {host, stage})
-            if (p && p->k_q4) dests[n++] = AppendDest{p->k_q4, p->v_q4, nullptr, nullptr, nullptr};
+            if (p && p->k_q4) dests[n++] = AppendDest{p->k_q4, p->v_q4, nullptr, nullptr, nullptr, p == host};
         return append_launch(sc::kKvQ4, K, V, T, pos0, n_head_kv, head_dim, page_size, dests, n, stream);
     });
 }
@@ -1402,25 +1461,6 @@ int sc_plan_resume_append(const sc_geometry* g, const sc_batch_desc* d, sc_plan*
 }
 
 // ---- park / resume --------------------------------------------------------------------------------------------
-
-// The device address of a pinned host range the device can reach, or nullptr: its first and last byte must both be
-// pinned host memory mapped for the device, at device addresses `bytes - 1` apart (one mapping).  A kernel that reads
-// or writes a host image itself needs this; a pageable image would fault the GPU rather than fail a copy.
-uint8_t* mapped_host_range(const void* host, uint64_t bytes) {
-    if (!host || bytes == 0) return nullptr;
-    hipPointerAttribute_t first{}, last{};
-    hipError_t e = hipPointerGetAttributes(&first, host);
-    if (e == hipSuccess) e = hipPointerGetAttributes(&last, static_cast<const uint8_t*>(host) + (bytes - 1));
-    if (e != hipSuccess) {
-        (void) hipGetLastError();   // an unknown pointer is an answer here, not an error for the next call
-        return nullptr;
-    }
-    if (first.type != hipMemoryTypeHost || last.type != hipMemoryTypeHost || !first.devicePointer ||
-        !last.devicePointer ||
-        static_cast<uint8_t*>(last.devicePointer) - static_cast<uint8_t*>(first.devicePointer) != ptrdiff_t(bytes - 1))
-        return nullptr;
-    return static_cast<uint8_t*>(first.devicePointer);
-}
 
 static int dma_image(const sc_geometry* g, const sc_decode_slot* slot, int64_t tokens, uint8_t* host,
                      uint64_t image_bytes, bool park, void* stream, void* done) {

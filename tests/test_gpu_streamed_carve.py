@@ -129,3 +129,42 @@ def test_k8v4_slot_refuses_host_copies(sc, cuda):
     with pytest.raises(sc.ScError) as err:
         sc.plan_carve_quant(geo, case.prefill, slot, with_gdn=False)
     assert err.value.code == sc.SC_EINVAL and "hybrid K8V4" in str(err.value)
+
+
+def test_host_copy_must_be_mapped_pinned_memory(sc, cuda):
+    """The kernels write a host copy straight into host memory, so its pools must be pinned memory mapped for the
+    device: pageable buffers (and device memory) are refused when the plan is built, and by the per-layer append before
+    its launch (attempted only after sc_host_range_mapped has reported the buffer unmapped, the same check it makes)."""
+    import ctypes as C
+    geo = sc.geometry(**GEO)
+    T, logical = 12, 5
+    case = synth.SyntheticCase(geo, tokens=T, seed=5, kv_dtype=sc.SC_DTYPE_F32)
+    rows = logical * geo.n_head_kv * geo.page_size
+    pageable = [np.zeros(rows * ROW["f16"], np.uint8) for _ in range(2 * geo.n_qsa)]
+    pools = []
+    for j in range(geo.n_qsa):
+        kp = sc.KvPools()
+        kp.k_pool, kp.v_pool = pageable[2 * j].ctypes.data, pageable[2 * j + 1].ctypes.data
+        pools.append(kp)
+    mapped = C.c_int32(-1)
+    assert sc.lib.sc_host_range_mapped(pageable[0].ctypes.data, pageable[0].nbytes, C.byref(mapped)) == sc.SC_OK
+    assert mapped.value == 0
+    slot = sc.new_slot(geo, logical * geo.page_size, fill=SENTINEL)
+    slot.host = pools
+    with pytest.raises(sc.ScError) as err:
+        sc.plan_carve(geo, case.prefill, slot, with_gdn=False)
+    assert err.value.code == sc.SC_EINVAL and "pinned memory mapped for the device" in str(err.value)
+    # device memory is not a host copy either
+    dev_bufs, dev_pools = _extra(sc, geo, "f16", logical, host=False)
+    slot.host = dev_pools
+    with pytest.raises(sc.ScError):
+        sc.plan_carve(geo, case.prefill, slot, with_gdn=False)
+    # the per-layer append, f16 pools with a pageable host copy
+    kp = pools[0]
+    rc = sc.lib.sc_kv_append_async(case.prefill.k[0].data_ptr(), case.prefill.v[0].data_ptr(), T, 0, None,
+                                   geo.page_size, slot.k_pool[0].data_ptr(), slot.v_pool[0].data_ptr(), None, None,
+                                   None, None, None, C.byref(kp), None)
+    assert rc == sc.SC_EINVAL and "pinned memory mapped for the device" in sc.last_error()
+    sc.device_sync()
+    assert all(np.all(b == 0) for b in pageable)
+    assert np.all(slot.host_state()["k0"].view(np.uint8) == SENTINEL)   # nothing was launched
