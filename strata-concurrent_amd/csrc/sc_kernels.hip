@@ -471,8 +471,8 @@ __device__ void tile_q4(const MoveRow& r, const MoveGeo& g, uint64_t local) {
     }
 }
 
-// One workgroup per tile (the grid strides only when a plan has more tiles than one launch may hold): measured
-// on the 128K handoff, a grid of one tile per workgroup beat every persistent grid from 1024 to 65536 workgroups.
+// A workgroup takes tiles blockIdx.x, + gridDim.x, ...; the plan picks the grid (65536 workgroups for the plain
+// movers, which measured faster on the 128K handoff than one workgroup per tile or smaller grids).
 // `tile_row[t]` names the handoff table row of tile t, so a workgroup finds its row with two scalar loads and no
 // search.  The instance (kMix) compiles only its set of row kinds: the f32 rounding tile holds twice the loads
 // and the quantizers need 80-90 VGPRs, and compiled into one kernel they took the plain movers from 8 to 6 waves
@@ -717,9 +717,10 @@ __global__ void fill_bytes_kernel(uint8_t* dst, uint8_t value, uint64_t n) {
 
 // Device-to-device copies, used where the source is another process's memory mapped by a memory handle (which the
 // runtime's own copy may hand to a copy engine).  When source and destination share their alignment modulo 16 the
-// copy is cut into 16 KiB tiles, one per workgroup, each thread issuing its four 16-byte loads before its four
-// non-temporal stores (the shape that measures fastest for a plain copy on this part); one extra workgroup copies the
-// unaligned head and the tail.  Other pairs take a grid-stride byte loop.
+// copy is cut into 16 KiB tiles, one per workgroup, each thread issuing its four 16-byte non-temporal loads before its
+// four non-temporal stores (the shape that measures fastest for a plain copy on this part: 3.3 GB in 1.10 ms against
+// 1.15 ms with regular loads, three alternating pairs); one extra workgroup copies the unaligned head and the tail.
+// Other pairs take a grid-stride byte loop.
 constexpr uint64_t kCopyTile = 256 * 4 * 16;
 
 __global__ void __launch_bounds__(256) copy_tiles_kernel(uint8_t* dst, const uint8_t* src, uint64_t n, uint64_t pre,
@@ -729,7 +730,7 @@ __global__ void __launch_bounds__(256) copy_tiles_kernel(uint8_t* dst, const uin
         const uint64_t base = pre + uint64_t(blockIdx.x) * kCopyTile;
         u32x4 v[4];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) v[u] = ld16(src + base + (u * 256 + tid) * 16);
+        for (int u = 0; u < 4; ++u) v[u] = ld16_stream(src + base + (u * 256 + tid) * 16);
 #pragma unroll
         for (int u = 0; u < 4; ++u) st16(dst + base + (u * 256 + tid) * 16, v[u]);
         return;
