@@ -390,14 +390,19 @@ int main() {
                 }
             });
             std::this_thread::sleep_for(std::chrono::microseconds(100));
+            const int before = seen.load();
             if (a.publish(c, round + 5, body.size(), h, err)) ++published;
-            std::this_thread::sleep_for(std::chrono::microseconds(400));
+            // let the reader see the READY slot at least once (a loaded machine may not schedule it for a while)
+            const auto t_pub = std::chrono::steady_clock::now();
+            while (seen.load() == before && std::chrono::steady_clock::now() - t_pub < std::chrono::seconds(2))
+                std::this_thread::sleep_for(std::chrono::microseconds(50));
+            std::this_thread::sleep_for(std::chrono::microseconds(200));
             stop = true;
             reader.join();
             a.release(c.index, c.nonce, err);
         }
         expect(published == 120, "every round published");
-        expect(seen.load() > 120, "the racing reader saw READY slots", std::to_string(seen.load()) + " reads");
+        expect(seen.load() >= 120, "the racing reader saw every round's READY slot", std::to_string(seen.load()) + " reads");
         expect(bad.load() == 0, "no read saw READY with a stale record or body");
         drop(path);
     }
@@ -513,19 +518,20 @@ int main() {
         HandoffArena a;
         std::string err;
         a.open_writer(main_path, three_by_two(), kPack, geom, err);
-        a.set_lease_ms(150);
+        // a lease long enough that claim -> publish -> reclaim fits in it on a loaded machine
+        a.set_lease_ms(400);
         std::vector<uint8_t> body(1000, 3);
         const uint64_t h = fnv1a64(body.data(), body.size());
         HandoffClaim c;
         expect(a.claim(1, 0xA, 1, c, err) && a.write_payload(c, 0, body.data(), body.size(), err) &&
                    a.publish(c, 1, body.size(), h, err) && a.reclaim(&err).empty(),
                "a fresh READY slot survives a reclaim");
-        std::this_thread::sleep_for(std::chrono::milliseconds(220));
+        std::this_thread::sleep_for(std::chrono::milliseconds(480));
         auto took = a.reclaim(&err);
-        expect(took.size() == 1 && took[0].was_state == kHandoffReady && has(took[0].why, "lease") && took[0].age_ms >= 150,
+        expect(took.size() == 1 && took[0].was_state == kHandoffReady && has(took[0].why, "lease") && took[0].age_ms >= 400,
                "an unread READY slot is reclaimed at the lease", took.empty() ? "" : took[0].why);
         expect(a.claim(1, 0xA, 2, c, err), "claim again");
-        std::this_thread::sleep_for(std::chrono::milliseconds(220));
+        std::this_thread::sleep_for(std::chrono::milliseconds(480));
         took = a.reclaim(&err);
         expect(took.size() == 1 && took[0].was_state == kHandoffClaimed && has(took[0].why, "lease"), "so is a stuck claim");
         a.set_lease_ms(1000000);
