@@ -189,9 +189,12 @@ sc::MoveGeo move_geo(const Geo& g) {
 }
 
 constexpr uint64_t kMaxRowChunks = uint64_t(1) << 31;
-// Workgroups per launch; larger plans stride.  Measured on the 128K handoff (48 layers, 201K tiles): 65536
-// workgroups 5.83 TB/s, one per tile 5.67, 16384 5.62, 4096 5.29, 2048 4.52.
-constexpr uint64_t kMaxGrid = 65536;
+// Workgroups per launch; larger plans stride.  Measured on the 128K handoff (48 layers, 201K tiles), four alternating
+// rounds: one workgroup per tile 1.155 ms, 65536 workgroups 1.166 ms (with the rows' loads non-temporal: 1.148 and
+// 1.159 ms); an earlier version of the kernel, whose loads waited on the table lookups, had measured the opposite.
+constexpr uint64_t kMaxGrid = uint64_t(1) << 20;
+// The batched launch: 65536, 131072 and 262144 workgroups measured alike (5.59-5.61 ms for config 5).
+constexpr uint64_t kMaxGridBatch = 65536;
 // Plans with quantizing rows: their tiles read 16 KiB but write a quarter of that after per-row work, and more
 // workgroups in flight measured faster (the 128K int8 carve: 65536 workgroups 1.56 ms, 131072 1.50, 262144 1.43,
 // one per tile 1.46; q4_0: 1.53, 1.51, 1.52, 1.53).
@@ -1410,7 +1413,7 @@ int sc_plan_resume_append(const sc_geometry* g, const sc_batch_desc* d, sc_plan*
         sc_plan* p = new (std::nothrow) sc_plan();
         if (!p) return fail(SC_ENOMEM, "sc_handoff: plan allocation failed");
         p->batch = true;
-        p->grid = p->default_grid = int64_t(std::min<uint64_t>(std::max<uint64_t>(tiles, 1), kMaxGrid));
+        p->grid = p->default_grid = int64_t(std::min<uint64_t>(std::max<uint64_t>(tiles, 1), kMaxGridBatch));
         p->payload = 0;   // depends on the device-resident lengths
         // workspace: [slots][ok][arena order group][inv][order pairs][counts]
         auto up = [](uint64_t x) { return (x + 255) / 256 * 256; };

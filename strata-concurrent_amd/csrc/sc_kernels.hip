@@ -32,14 +32,16 @@ __device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv& f) {
 using u32x4 = __attribute__((ext_vector_type(4))) uint32_t;
 
 // Every buffer the handoff touches is global memory: say so, so the 16-byte accesses are global_load/store_dwordx4
-// rather than flat ones that also arbitrate for LDS.  Stores are non-temporal: a handoff writes each destination
-// byte once and nothing reads it back soon, so streaming it past the caches measured faster (5.83 vs 5.57 TB/s on
-// the 128K handoff) than write-allocating it.
+// rather than flat ones that also arbitrate for LDS.  Loads and stores are non-temporal: a handoff reads each source
+// byte once and writes each destination byte once, and nothing reads them back soon.  Streaming the stores past the
+// caches measured faster (5.83 vs 5.57 TB/s on the 128K handoff) than write-allocating them; streaming the loads as
+// well, 1% faster on the 128K carve (four alternating rounds), 4-6% on an image scattered into pages and 4% on a
+// plain tile copy.
 using gu32x4 = __attribute__((address_space(1))) u32x4;
-__device__ __forceinline__ u32x4 ld16(const uint8_t* p) { return *(const gu32x4*) (p); }
-// A non-temporal load, for a packed source read exactly once (an image scattered into pages): measured 4-6% faster
-// on the 128K scatter; the carves' row reads gained nothing from it.
-__device__ __forceinline__ u32x4 ld16_stream(const uint8_t* p) { return __builtin_nontemporal_load((const gu32x4*) (p)); }
+__device__ __forceinline__ u32x4 ld16(const uint8_t* p) { return __builtin_nontemporal_load((const gu32x4*) (p)); }
+// A regular load, for the quantizing rows: with non-temporal loads the int8 carve through a shuffled table took
+// 1.628 ms against 1.548 and the per-layer int8 appends 1.509 against 1.396 ms (the f16 rows gained).
+__device__ __forceinline__ u32x4 ld16_cached(const uint8_t* p) { return *(const gu32x4*) (p); }
 __device__ __forceinline__ void st16(uint8_t* p, u32x4 v) { __builtin_nontemporal_store(v, (gu32x4*) (p)); }
 
 // Page tables are read through global loads.  Every tile issues all of its loads, table entries included, before
@@ -195,7 +197,7 @@ __device__ void tile_pages(const MoveRow& r, const MoveGeo& g, uint64_t local, b
         for (int j = 0; j < kChunksPerThread; ++j) {
             q[j] = uint32_t(local * kTileChunks) + uint32_t(j * kThreads) + threadIdx.x;
             if constexpr (kOrder) q[j] = ordered_chunk(r, g, q[j], false);
-            if (q[j] < r.n) v[j] = ld16_stream(r.src + uint64_t(q[j]) * 16u);
+            if (q[j] < r.n) v[j] = ld16(r.src + uint64_t(q[j]) * 16u);
         }
 #pragma unroll
         for (int j = 0; j < kChunksPerThread; ++j)
@@ -334,7 +336,7 @@ __device__ __forceinline__ int load_units(const MoveRow& r, const MoveGeo& g, ui
     for (int i = 0; i < kQuantUnitsPerWave; ++i) {
         unit[i] = uint32_t(local) * kQuantUnitsPerTile + uint32_t(wave * kQuantUnitsPerWave + i);
         if (unit[i] < r.n) {   // uniform across the wave
-            v[i] = ld16(r.src + uint64_t(unit[i]) * (kQuantDim * 4) + lane * 16);
+            v[i] = ld16_cached(r.src + uint64_t(unit[i]) * (kQuantDim * 4) + lane * 16);
             n = i + 1;
         }
     }
@@ -617,7 +619,7 @@ __device__ void batch_page_tile(const BatchArgs& a, const BatchSlotsLds& S, uint
         const uint32_t h = fdiv(row, g.page_size), c = row - h * g.page_size.d;
         const int64_t token = int64_t(lp) * g.page_size.d + c;
         if (token < L) {
-            v[j] = ld16_stream(a.staging + S.stage[slot] + uint64_t(blob) * S.stride[slot] + uint64_t(lp) * page_bytes +
+            v[j] = ld16(a.staging + S.stage[slot] + uint64_t(blob) * S.stride[slot] + uint64_t(lp) * page_bytes +
                                ip * 16u);
         } else if (token < L + a.chunk_tokens) {
             const uint8_t* src = reinterpret_cast<const uint8_t*>(chunks[(uint64_t(slot) * a.n_qsa + blob / 2) * 2 + (blob & 1)]);
@@ -730,7 +732,7 @@ __global__ void __launch_bounds__(256) copy_tiles_kernel(uint8_t* dst, const uin
         const uint64_t base = pre + uint64_t(blockIdx.x) * kCopyTile;
         u32x4 v[4];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) v[u] = ld16_stream(src + base + (u * 256 + tid) * 16);
+        for (int u = 0; u < 4; ++u) v[u] = ld16(src + base + (u * 256 + tid) * 16);
 #pragma unroll
         for (int u = 0; u < 4; ++u) st16(dst + base + (u * 256 + tid) * 16, v[u]);
         return;
