@@ -193,8 +193,10 @@ constexpr uint64_t kMaxRowChunks = uint64_t(1) << 31;
 // rounds: one workgroup per tile 1.155 ms, 65536 workgroups 1.166 ms (with the rows' loads non-temporal: 1.148 and
 // 1.159 ms); an earlier version of the kernel, whose loads waited on the table lookups, had measured the opposite.
 constexpr uint64_t kMaxGrid = uint64_t(1) << 20;
-// The batched launch: 65536, 131072 and 262144 workgroups measured alike (5.59-5.61 ms for config 5).
-constexpr uint64_t kMaxGridBatch = 65536;
+// The batched launch takes one workgroup per tile as well: config 5's scatter (870K tiles) at a median of 7 launches,
+// 65536 workgroups 5.42 ms, 262144 5.11-5.19, one per tile 5.05-5.07 (with regular loads, 65536 to 262144 had
+// measured alike).
+constexpr uint64_t kMaxGridBatch = kMaxGrid;
 // Plans with quantizing rows: their tiles read 16 KiB but write a quarter of that after per-row work, and more
 // workgroups in flight measured faster (the 128K int8 carve: 65536 workgroups 1.56 ms, 131072 1.50, 262144 1.43,
 // one per tile 1.46; q4_0: 1.53, 1.51, 1.52, 1.53).
@@ -359,7 +361,8 @@ int finish_plan(std::vector<sc::MoveRow>& rows, const Geo& g, uint64_t payload, 
         *out = p;
         return ok();
     }
-    std::vector<uint16_t> tile_row(tiles);
+    // padded to an even count: the kernel reads the entries a 4-byte word (two entries) at a time
+    std::vector<uint16_t> tile_row(tiles + (tiles & 1), uint16_t(rows.size() - 1));
     for (size_t k = 0; k < rows.size(); ++k) {
         const uint64_t end = k + 1 < rows.size() ? rows[k + 1].tile0 : tiles;
         std::fill(tile_row.begin() + int64_t(rows[k].tile0), tile_row.begin() + int64_t(end), uint16_t(k));
@@ -370,7 +373,8 @@ int finish_plan(std::vector<sc::MoveRow>& rows, const Geo& g, uint64_t payload, 
         return rc;
     }
     hipError_t e = hipMalloc(reinterpret_cast<void**>(&p->rows_dev), rows.size() * sizeof(sc::MoveRow));
-    if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&p->tile_row_dev), tiles * sizeof(uint16_t));
+    if (e == hipSuccess)
+        e = hipMalloc(reinterpret_cast<void**>(&p->tile_row_dev), tile_row.size() * sizeof(uint16_t));
     if (e != hipSuccess) {
         if (p->rows_dev) (void) hipFree(p->rows_dev);
         if (p->order_ws) (void) hipFree(p->order_ws);
@@ -378,7 +382,8 @@ int finish_plan(std::vector<sc::MoveRow>& rows, const Geo& g, uint64_t payload, 
         return fail(SC_ENOMEM, std::string("sc_handoff: table allocation: ") + hipGetErrorString(e));
     }
     e = hipMemcpy(p->rows_dev, rows.data(), rows.size() * sizeof(sc::MoveRow), hipMemcpyHostToDevice);
-    if (e == hipSuccess) e = hipMemcpy(p->tile_row_dev, tile_row.data(), tiles * sizeof(uint16_t), hipMemcpyHostToDevice);
+    if (e == hipSuccess)
+        e = hipMemcpy(p->tile_row_dev, tile_row.data(), tile_row.size() * sizeof(uint16_t), hipMemcpyHostToDevice);
     if (e != hipSuccess) {
         (void) hipFree(p->rows_dev);
         (void) hipFree(p->tile_row_dev);

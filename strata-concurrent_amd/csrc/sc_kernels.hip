@@ -44,12 +44,24 @@ __device__ __forceinline__ u32x4 ld16(const uint8_t* p) { return __builtin_nonte
 __device__ __forceinline__ u32x4 ld16_cached(const uint8_t* p) { return *(const gu32x4*) (p); }
 __device__ __forceinline__ void st16(uint8_t* p, u32x4 v) { __builtin_nontemporal_store(v, (gu32x4*) (p)); }
 
+// Thirty-two zero bytes in global memory, which no kernel writes.  A lane with nothing to read (past its row, in a
+// row's zero-filled tail, on a page the table does not place) loads from here instead of skipping its load, so every
+// lane of a tile issues the same loads in the same order.  The compiler can then count them, and each store waits for
+// its own load only.  With loads skipped on some lanes it waited for every earlier memory operation before each
+// store, and this part counts stores and loads in one counter: every store waited for the previous store's
+// acknowledgement.
+__device__ u32x4 g_zero_chunks[2];
+__device__ __forceinline__ const uint8_t* zero_chunks() { return reinterpret_cast<const uint8_t*>(g_zero_chunks); }
+
 // Page tables are read through global loads.  Every tile issues all of its loads, table entries included, before
 // its first store: a table load placed after a store (which might alias the table) waits for it, and the
 // per-chunk load -> store chains that result measured 10-14% slower on the 128K handoff through a page table.
+// Whether the row has a table is a template argument, so the entry's load is never skipped (see g_zero_chunks).
 using gi32 = __attribute__((address_space(1))) const int32_t;
+template <bool kTable>
 __device__ __forceinline__ int32_t table_entry(const MoveRow& r, uint32_t page) {
-    return r.table ? *(gi32*) (r.table + page) : int32_t(page);
+    if constexpr (kTable) return *(gi32*) (r.table + page);
+    return int32_t(page);
 }
 // The same entry for a wave-uniform page, read with a scalar load (through the constant address space: no kernel
 // writes a table).  A vector load would share the wave's in-order load counter, so taking its value into a scalar
@@ -81,13 +93,17 @@ __device__ __forceinline__ int64_t pool_row(const MoveRow& r, const MoveGeo& g, 
 // in token-major order, so the page's chunks are one contiguous run of the row's source: the source chunk is
 // (lp * ps - pos0) * H * row_chunks plus the in-page index.  Returns ~0u (>= every row's chunk count) for a -1 entry
 // and for cells outside the row.
+// kOrder: kDestOrderWave when a page holds a multiple of 64 chunks, so that the wave's 64 consecutive chunks share
+// one page and its entry is read with a scalar load; kDestOrder reads it per lane.  The choice is a template argument
+// so that no tile has a branch around one of its loads.
+enum TileOrder { kSourceOrder = 0, kDestOrder = 1, kDestOrderWave = 2 };
+template <int kOrder>
 __device__ __forceinline__ uint32_t ordered_chunk(const MoveRow& r, const MoveGeo& g, uint32_t vq, bool kv) {
     const uint32_t vp = fdiv(vq, g.page_chunks);
     const uint32_t ip = vq - vp * g.page_chunks.d;
-    // a page of a multiple of 64 chunks holds the wave's 64 consecutive chunks, and its entry is then read with a
-    // scalar load
-    const int64_t lp = g.page_chunks.d % 64u == 0u ? *((ci32*) r.order + __builtin_amdgcn_readfirstlane(vp))
-                                                   : *(gi32*) (r.order + vp);
+    int64_t lp;
+    if constexpr (kOrder == kDestOrderWave) lp = *((ci32*) r.order + __builtin_amdgcn_readfirstlane(vp));
+    else lp = *(gi32*) (r.order + vp);
     if (lp < 0) return ~0u;
     const int64_t q = kv ? (lp * int64_t(g.page_size.d) - r.pos0) * int64_t(g.heads.d * g.row_chunks.d) + ip
                          : lp * int64_t(g.page_chunks.d) + ip;
@@ -97,22 +113,26 @@ __device__ __forceinline__ uint32_t ordered_chunk(const MoveRow& r, const MoveGe
 // kTable: the row has a page table, whose entries are loaded with the data; without one the physical page is the
 // logical page and nothing but the data is loaded before the stores.  kOrder: the tiles visit the row's pages in
 // destination order (the order's load comes before the data's).
-template <bool kTable, bool kOrder = false>
+template <bool kTable, int kOrder = kSourceOrder>
 __device__ void tile_kv16(const MoveRow& r, const MoveGeo& g, uint64_t local) {
     const uint32_t row_bytes = g.row_chunks.d * 16u;
+    const uint32_t last = uint32_t(r.n) - 1u;
     u32x4 v[kChunksPerThread];
     uint32_t q[kChunksPerThread];
     int32_t phys[kChunksPerThread];
+    // every order entry is read before the first data load, so no data load waits behind the next entry's
 #pragma unroll
     for (int j = 0; j < kChunksPerThread; ++j) {
         q[j] = uint32_t(local * kTileChunks) + uint32_t(j * kThreads) + threadIdx.x;
-        if constexpr (kOrder) q[j] = ordered_chunk(r, g, q[j], true);
-        if (q[j] >= r.n) continue;
+        if constexpr (kOrder != kSourceOrder) q[j] = ordered_chunk<kOrder>(r, g, q[j], true);
+    }
+#pragma unroll
+    for (int j = 0; j < kChunksPerThread; ++j) {
         // rows past the source's tokens (an image's stale-cell tail) are written as zeros
-        const uint32_t row = fdiv(q[j], g.row_chunks);
-        const uint32_t t = fdiv(row, g.heads);
-        v[j] = t < uint32_t(r.aux) ? ld16(r.src + uint64_t(q[j]) * 16u) : u32x4{0u, 0u, 0u, 0u};
-        if constexpr (kTable) phys[j] = table_entry(r, kv_cell(r, g, row).page);
+        const uint32_t row = fdiv(min(q[j], last), g.row_chunks);
+        const bool live = q[j] <= last && fdiv(row, g.heads) < uint32_t(r.aux);
+        v[j] = ld16(live ? r.src + uint64_t(q[j]) * 16u : zero_chunks());
+        if constexpr (kTable) phys[j] = table_entry<true>(r, kv_cell(r, g, row).page);
     }
 #pragma unroll
     for (int j = 0; j < kChunksPerThread; ++j) {
@@ -126,25 +146,27 @@ __device__ void tile_kv16(const MoveRow& r, const MoveGeo& g, uint64_t local) {
 }
 
 // The same map from f32 rows, rounded to f16: destination chunk q holds 8 halves = 32 source bytes at q * 32.
-template <bool kTable, bool kOrder = false>
+template <bool kTable, int kOrder = kSourceOrder>
 __device__ void tile_kv32(const MoveRow& r, const MoveGeo& g, uint64_t local) {
     const uint32_t row_bytes = g.row_chunks.d * 16u;
+    const uint32_t last = uint32_t(r.n) - 1u;
     u32x4 a[kChunksPerThread], b[kChunksPerThread];
     uint32_t q[kChunksPerThread];
     int32_t phys[kChunksPerThread];
+    // every order entry is read before the first data load, so no data load waits behind the next entry's
 #pragma unroll
     for (int j = 0; j < kChunksPerThread; ++j) {
         q[j] = uint32_t(local * kTileChunks) + uint32_t(j * kThreads) + threadIdx.x;
-        if constexpr (kOrder) q[j] = ordered_chunk(r, g, q[j], true);
-        if (q[j] >= r.n) continue;
-        const uint32_t row = fdiv(q[j], g.row_chunks);
-        if (fdiv(row, g.heads) < uint32_t(r.aux)) {
-            a[j] = ld16(r.src + uint64_t(q[j]) * 32u);
-            b[j] = ld16(r.src + uint64_t(q[j]) * 32u + 16u);
-        } else {
-            a[j] = b[j] = u32x4{0u, 0u, 0u, 0u};
-        }
-        if constexpr (kTable) phys[j] = table_entry(r, kv_cell(r, g, row).page);
+        if constexpr (kOrder != kSourceOrder) q[j] = ordered_chunk<kOrder>(r, g, q[j], true);
+    }
+#pragma unroll
+    for (int j = 0; j < kChunksPerThread; ++j) {
+        const uint32_t row = fdiv(min(q[j], last), g.row_chunks);
+        const bool live = q[j] <= last && fdiv(row, g.heads) < uint32_t(r.aux);
+        const uint8_t* p = live ? r.src + uint64_t(q[j]) * 32u : zero_chunks();
+        a[j] = ld16(p);
+        b[j] = ld16(p + 16u);
+        if constexpr (kTable) phys[j] = table_entry<true>(r, kv_cell(r, g, row).page);
     }
 #pragma unroll
     for (int j = 0; j < kChunksPerThread; ++j) {
@@ -170,12 +192,11 @@ __device__ void tile_rec(const MoveRow& r, const MoveGeo& g, uint64_t local) {
 #pragma unroll
     for (int j = 0; j < kChunksPerThread; ++j) {
         q[j] = uint32_t(local * kTileChunks) + uint32_t(j * kThreads) + threadIdx.x;
-        if (q[j] >= r.n) continue;
         const uint32_t row = fdiv(q[j], g.rec_chunks);
         const uint32_t ch = q[j] - row * g.rec_chunks.d;
         const uint32_t i = fdiv(row, g.v_heads);
         const uint32_t h = row - i * g.v_heads.d;
-        v[j] = ld16(r.src + (uint64_t(h) * g.state + i) * row_bytes + ch * 16u);
+        v[j] = ld16(q[j] < r.n ? r.src + (uint64_t(h) * g.state + i) * row_bytes + ch * 16u : zero_chunks());
     }
 #pragma unroll
     for (int j = 0; j < kChunksPerThread; ++j)
@@ -185,23 +206,24 @@ __device__ void tile_rec(const MoveRow& r, const MoveGeo& g, uint64_t local) {
 // Whole pages between a contiguous run and a paged pool.  Scattering, the packed source does not depend on the
 // table, so its loads are issued before the table is read and the table's latency hides behind them (a
 // table-first order measured about 20% slower); gathering, the table must come first.
-template <bool kOrder = false>
+template <bool kTable, int kOrder = kSourceOrder>
 __device__ void tile_pages(const MoveRow& r, const MoveGeo& g, uint64_t local, bool scatter) {
     const uint64_t page_bytes = uint64_t(g.page_chunks.d) * 16u;
     u32x4 v[kChunksPerThread];
     int64_t dst_off[kChunksPerThread];
     if (scatter) {
+        const uint32_t last = uint32_t(r.n) - 1u;
         uint32_t q[kChunksPerThread];
         int32_t phys[kChunksPerThread];
-    #pragma unroll
+#pragma unroll
         for (int j = 0; j < kChunksPerThread; ++j) {
             q[j] = uint32_t(local * kTileChunks) + uint32_t(j * kThreads) + threadIdx.x;
-            if constexpr (kOrder) q[j] = ordered_chunk(r, g, q[j], false);
-            if (q[j] < r.n) v[j] = ld16(r.src + uint64_t(q[j]) * 16u);
+            if constexpr (kOrder != kSourceOrder) q[j] = ordered_chunk<kOrder>(r, g, q[j], false);
         }
 #pragma unroll
-        for (int j = 0; j < kChunksPerThread; ++j)
-            if (q[j] < r.n) phys[j] = table_entry(r, fdiv(q[j], g.page_chunks));
+        for (int j = 0; j < kChunksPerThread; ++j) v[j] = ld16(q[j] <= last ? r.src + uint64_t(q[j]) * 16u : zero_chunks());
+#pragma unroll
+        for (int j = 0; j < kChunksPerThread; ++j) phys[j] = table_entry<kTable>(r, fdiv(min(q[j], last), g.page_chunks));
 #pragma unroll
         for (int j = 0; j < kChunksPerThread; ++j) {
             if (q[j] >= r.n) continue;
@@ -211,17 +233,16 @@ __device__ void tile_pages(const MoveRow& r, const MoveGeo& g, uint64_t local, b
         }
         return;
     }
+    const uint32_t last = uint32_t(r.n) - 1u;
 #pragma unroll
     for (int j = 0; j < kChunksPerThread; ++j) {
-        dst_off[j] = -1;
         const uint32_t q = uint32_t(local * kTileChunks) + uint32_t(j * kThreads) + threadIdx.x;
-        if (q >= r.n) continue;
-        const uint32_t page = fdiv(q, g.page_chunks);
+        const uint32_t page = fdiv(min(q, last), g.page_chunks);
         const uint32_t ch = q - page * g.page_chunks.d;
-        const int64_t phys = table_entry(r, page);
-        if (phys < 0 || phys >= r.ld) continue;
-        v[j] = ld16(r.src + uint64_t(phys) * page_bytes + ch * 16u);
-        dst_off[j] = int64_t(q) * 16;
+        const int64_t phys = table_entry<kTable>(r, page);
+        const bool placed = q <= last && phys >= 0 && phys < r.ld;
+        v[j] = ld16(placed ? r.src + uint64_t(phys) * page_bytes + ch * 16u : zero_chunks());
+        dst_off[j] = placed ? int64_t(q) * 16 : -1;
     }
 #pragma unroll
     for (int j = 0; j < kChunksPerThread; ++j)
@@ -232,10 +253,15 @@ __device__ void tile_copy(const MoveRow& r, uint64_t local, bool zero) {
     u32x4 v[kChunksPerThread];
     uint64_t q[kChunksPerThread];
 #pragma unroll
-    for (int j = 0; j < kChunksPerThread; ++j) {
-        q[j] = local * kTileChunks + uint64_t(j * kThreads) + threadIdx.x;
-        if (q[j] < r.n) v[j] = zero ? u32x4{0u, 0u, 0u, 0u} : ld16(r.src + q[j] * 16u);
+    for (int j = 0; j < kChunksPerThread; ++j) q[j] = local * kTileChunks + uint64_t(j * kThreads) + threadIdx.x;
+    if (zero) {
+#pragma unroll
+        for (int j = 0; j < kChunksPerThread; ++j)
+            if (q[j] < r.n) st16(r.dst + q[j] * 16u, u32x4{0u, 0u, 0u, 0u});
+        return;
     }
+#pragma unroll
+    for (int j = 0; j < kChunksPerThread; ++j) v[j] = ld16(q[j] < r.n ? r.src + q[j] * 16u : zero_chunks());
 #pragma unroll
     for (int j = 0; j < kChunksPerThread; ++j)
         if (q[j] < r.n) st16(r.dst + q[j] * 16u, v[j]);
@@ -473,10 +499,10 @@ __device__ void tile_q4(const MoveRow& r, const MoveGeo& g, uint64_t local) {
     }
 }
 
-// A workgroup takes tiles blockIdx.x, + gridDim.x, ...; the plan picks the grid (65536 workgroups for the plain
-// movers, which measured faster on the 128K handoff than one workgroup per tile or smaller grids).
-// `tile_row[t]` names the handoff table row of tile t, so a workgroup finds its row with two scalar loads and no
-// search.  The instance (kMix) compiles only its set of row kinds: the f32 rounding tile holds twice the loads
+// A workgroup takes tiles blockIdx.x, + gridDim.x, ...; the plan picks the grid (one workgroup per tile up to 2^20
+// workgroups, then grid-stride).  `tile_row[t]` names the handoff table row of tile t (the host pads the array to an
+// even count), so a workgroup finds its row with two scalar loads and no search: a vector load of the entry would
+// make the wave wait, before its next tile and before it ends, for every store it issued.  The instance (kMix) compiles only its set of row kinds: the f32 rounding tile holds twice the loads
 // and the quantizers need 80-90 VGPRs, and compiled into one kernel they took the plain movers from 8 to 6 waves
 // per SIMD.  The quantizing instance is held to 80 VGPRs (6 waves per SIMD): at 84 it fell to 5 waves and every
 // quantizing row slowed by 3-6%; the instance of every kind keeps 5 waves (at 80 VGPRs it would spill).
@@ -489,21 +515,26 @@ sc_move_kernel(const MoveRow* __restrict__ rows, const uint16_t* __restrict__ ti
     // payload hash that matched): every workgroup reads the same word, so the launch writes all or nothing.
     if (gate && __builtin_amdgcn_readfirstlane(*gate) == 0u) return;
     __shared__ float s_conv[kMaxHist][kConvTileChannels];
+    const bool wave_pages = geo.page_chunks.d % 64u == 0u;
     int cur = -1;
     MoveRow r{};
     for (uint64_t tile = blockIdx.x; tile < n_tiles; tile += gridDim.x) {
-        const int k = __builtin_amdgcn_readfirstlane(int(tile_row[tile]));
+        using cu32 = __attribute__((address_space(4))) const uint32_t;
+        const uint32_t pair = *((cu32*) tile_row + (tile >> 1));
+        const int k = int((tile & 1) ? pair >> 16 : pair & 0xFFFFu);
         if (k != cur) { cur = k; r = rows[k]; }
         const uint64_t local = tile - r.tile0;
         switch (r.kind) {
             case kKv16:
-                if (r.order) tile_kv16<true, true>(r, geo, local);
+                if (r.order && wave_pages) tile_kv16<true, kDestOrderWave>(r, geo, local);
+                else if (r.order) tile_kv16<true, kDestOrder>(r, geo, local);
                 else if (r.table) tile_kv16<true>(r, geo, local);
                 else tile_kv16<false>(r, geo, local);
                 break;
             case kKv32:
                 if constexpr (kMix == kMixWide || kMix == kMixAll) {
-                    if (r.order) tile_kv32<true, true>(r, geo, local);
+                    if (r.order && wave_pages) tile_kv32<true, kDestOrderWave>(r, geo, local);
+                    else if (r.order) tile_kv32<true, kDestOrder>(r, geo, local);
                     else if (r.table) tile_kv32<true>(r, geo, local);
                     else tile_kv32<false>(r, geo, local);
                 }
@@ -511,10 +542,15 @@ sc_move_kernel(const MoveRow* __restrict__ rows, const uint16_t* __restrict__ ti
             case kRec: tile_rec(r, geo, local); break;
             case kConv: tile_conv(r, local, s_conv); break;
             case kPagesScatter:
-                if (r.order) tile_pages<true>(r, geo, local, true);
-                else tile_pages(r, geo, local, true);
+                if (r.order && wave_pages) tile_pages<true, kDestOrderWave>(r, geo, local, true);
+                else if (r.order) tile_pages<true, kDestOrder>(r, geo, local, true);
+                else if (r.table) tile_pages<true>(r, geo, local, true);
+                else tile_pages<false>(r, geo, local, true);
                 break;
-            case kPagesGather: tile_pages(r, geo, local, false); break;
+            case kPagesGather:
+                if (r.table) tile_pages<true>(r, geo, local, false);
+                else tile_pages<false>(r, geo, local, false);
+                break;
             case kCopy: tile_copy(r, local, false); break;
             case kZero: tile_copy(r, local, true); break;
             case kKvQ8: if constexpr (kMix == kMixQuant || kMix == kMixAll) tile_q8(r, geo, local); break;
@@ -896,7 +932,8 @@ __global__ void __launch_bounds__(kThreads) paged_image_kernel(PagedImage a, Mov
             r.src = image;
             r.dst = args->pool[blob];
         }
-        tile_pages(r, geo, t - blob * a.tiles_per_blob, !a.park);
+        if (r.table) tile_pages<true>(r, geo, t - blob * a.tiles_per_blob, !a.park);
+        else tile_pages<false>(r, geo, t - blob * a.tiles_per_blob, !a.park);
     }
 }
 
