@@ -197,10 +197,9 @@ constexpr uint64_t kMaxGrid = uint64_t(1) << 20;
 // 65536 workgroups 5.42 ms, 262144 5.11-5.19, one per tile 5.05-5.07 (with regular loads, 65536 to 262144 had
 // measured alike).
 constexpr uint64_t kMaxGridBatch = kMaxGrid;
-// Plans with quantizing rows: their tiles read 16 KiB but write a quarter of that after per-row work, and more
-// workgroups in flight measured faster (the 128K int8 carve: 65536 workgroups 1.56 ms, 131072 1.50, 262144 1.43,
-// one per tile 1.46; q4_0: 1.53, 1.51, 1.52, 1.53).
-constexpr uint64_t kMaxGridQuant = 262144;
+// Plans with quantizing rows take one workgroup per tile too: against 262144 workgroups, the 128K int8 carve 1.35
+// against 1.38 ms, q4_0 1.24 against 1.33, K8V4 1.30 against 1.35, int8 through a shuffled table 1.49 against 1.55
+// (two alternating rounds).  Before the tile's table entry was read with scalar loads, 262144 had measured fastest.
 
 // Rows that write through a page table visit their pages in destination order when the table covers at least this
 // many logical pages (fewer pages gain nothing from the pre-pass) and the pool is at most kOrderMaxSparsity times
@@ -355,7 +354,7 @@ int finish_plan(std::vector<sc::MoveRow>& rows, const Geo& g, uint64_t payload, 
     p->geo = move_geo(g);
     p->n_tiles = tiles;
     p->payload = payload;
-    p->grid = p->default_grid = int64_t(std::min<uint64_t>(tiles, quant ? kMaxGridQuant : kMaxGrid));
+    p->grid = p->default_grid = int64_t(std::min<uint64_t>(tiles, kMaxGrid));
     p->mix = sc::mix_of(kv32, quant);
     if (rows.empty() || tiles == 0) {   // an empty handoff (0 tokens, no running state) is a valid no-op
         *out = p;
