@@ -97,13 +97,16 @@ __device__ __forceinline__ int64_t pool_row(const MoveRow& r, const MoveGeo& g, 
 // one page and its entry is read with a scalar load; kDestOrder reads it per lane.  The choice is a template argument
 // so that no tile has a branch around one of its loads.
 enum TileOrder { kSourceOrder = 0, kDestOrder = 1, kDestOrderWave = 2 };
+// `page` receives the entry (wave-uniform under kDestOrderWave, so its table entry can be read with a scalar load).
 template <int kOrder>
-__device__ __forceinline__ uint32_t ordered_chunk(const MoveRow& r, const MoveGeo& g, uint32_t vq, bool kv) {
+__device__ __forceinline__ uint32_t ordered_chunk(const MoveRow& r, const MoveGeo& g, uint32_t vq, bool kv,
+                                                  int32_t& page) {
     const uint32_t vp = fdiv(vq, g.page_chunks);
     const uint32_t ip = vq - vp * g.page_chunks.d;
     int64_t lp;
     if constexpr (kOrder == kDestOrderWave) lp = *((ci32*) r.order + __builtin_amdgcn_readfirstlane(vp));
     else lp = *(gi32*) (r.order + vp);
+    page = int32_t(lp);
     if (lp < 0) return ~0u;
     const int64_t q = kv ? (lp * int64_t(g.page_size.d) - r.pos0) * int64_t(g.heads.d * g.row_chunks.d) + ip
                          : lp * int64_t(g.page_chunks.d) + ip;
@@ -119,12 +122,12 @@ __device__ void tile_kv16(const MoveRow& r, const MoveGeo& g, uint64_t local) {
     const uint32_t last = uint32_t(r.n) - 1u;
     u32x4 v[kChunksPerThread];
     uint32_t q[kChunksPerThread];
-    int32_t phys[kChunksPerThread];
+    int32_t phys[kChunksPerThread], lpage[kChunksPerThread];
     // every order entry is read before the first data load, so no data load waits behind the next entry's
 #pragma unroll
     for (int j = 0; j < kChunksPerThread; ++j) {
         q[j] = uint32_t(local * kTileChunks) + uint32_t(j * kThreads) + threadIdx.x;
-        if constexpr (kOrder != kSourceOrder) q[j] = ordered_chunk<kOrder>(r, g, q[j], true);
+        if constexpr (kOrder != kSourceOrder) q[j] = ordered_chunk<kOrder>(r, g, q[j], true, lpage[j]);
     }
 #pragma unroll
     for (int j = 0; j < kChunksPerThread; ++j) {
@@ -132,7 +135,12 @@ __device__ void tile_kv16(const MoveRow& r, const MoveGeo& g, uint64_t local) {
         const uint32_t row = fdiv(min(q[j], last), g.row_chunks);
         const bool live = q[j] <= last && fdiv(row, g.heads) < uint32_t(r.aux);
         v[j] = ld16(live ? r.src + uint64_t(q[j]) * 16u : zero_chunks());
-        if constexpr (kTable) phys[j] = table_entry<true>(r, kv_cell(r, g, row).page);
+        // in wave-uniform destination order the wave's chunks share the order's logical page (a lane outside the
+        // row stores nothing), whose table entry is read with a scalar load
+        if constexpr (kTable && kOrder == kDestOrderWave)
+            phys[j] = lpage[j] >= 0 ? table_entry_uniform(r, uint32_t(lpage[j])) : -1;
+        else if constexpr (kTable)
+            phys[j] = table_entry<true>(r, kv_cell(r, g, row).page);
     }
 #pragma unroll
     for (int j = 0; j < kChunksPerThread; ++j) {
@@ -152,12 +160,12 @@ __device__ void tile_kv32(const MoveRow& r, const MoveGeo& g, uint64_t local) {
     const uint32_t last = uint32_t(r.n) - 1u;
     u32x4 a[kChunksPerThread], b[kChunksPerThread];
     uint32_t q[kChunksPerThread];
-    int32_t phys[kChunksPerThread];
+    int32_t phys[kChunksPerThread], lpage[kChunksPerThread];
     // every order entry is read before the first data load, so no data load waits behind the next entry's
 #pragma unroll
     for (int j = 0; j < kChunksPerThread; ++j) {
         q[j] = uint32_t(local * kTileChunks) + uint32_t(j * kThreads) + threadIdx.x;
-        if constexpr (kOrder != kSourceOrder) q[j] = ordered_chunk<kOrder>(r, g, q[j], true);
+        if constexpr (kOrder != kSourceOrder) q[j] = ordered_chunk<kOrder>(r, g, q[j], true, lpage[j]);
     }
 #pragma unroll
     for (int j = 0; j < kChunksPerThread; ++j) {
@@ -166,7 +174,12 @@ __device__ void tile_kv32(const MoveRow& r, const MoveGeo& g, uint64_t local) {
         const uint8_t* p = live ? r.src + uint64_t(q[j]) * 32u : zero_chunks();
         a[j] = ld16(p);
         b[j] = ld16(p + 16u);
-        if constexpr (kTable) phys[j] = table_entry<true>(r, kv_cell(r, g, row).page);
+        // in wave-uniform destination order the wave's chunks share the order's logical page (a lane outside the
+        // row stores nothing), whose table entry is read with a scalar load
+        if constexpr (kTable && kOrder == kDestOrderWave)
+            phys[j] = lpage[j] >= 0 ? table_entry_uniform(r, uint32_t(lpage[j])) : -1;
+        else if constexpr (kTable)
+            phys[j] = table_entry<true>(r, kv_cell(r, g, row).page);
     }
 #pragma unroll
     for (int j = 0; j < kChunksPerThread; ++j) {
@@ -214,16 +227,21 @@ __device__ void tile_pages(const MoveRow& r, const MoveGeo& g, uint64_t local, b
     if (scatter) {
         const uint32_t last = uint32_t(r.n) - 1u;
         uint32_t q[kChunksPerThread];
-        int32_t phys[kChunksPerThread];
+        int32_t phys[kChunksPerThread], lpage[kChunksPerThread];
 #pragma unroll
         for (int j = 0; j < kChunksPerThread; ++j) {
             q[j] = uint32_t(local * kTileChunks) + uint32_t(j * kThreads) + threadIdx.x;
-            if constexpr (kOrder != kSourceOrder) q[j] = ordered_chunk<kOrder>(r, g, q[j], false);
+            if constexpr (kOrder != kSourceOrder) q[j] = ordered_chunk<kOrder>(r, g, q[j], false, lpage[j]);
         }
 #pragma unroll
         for (int j = 0; j < kChunksPerThread; ++j) v[j] = ld16(q[j] <= last ? r.src + uint64_t(q[j]) * 16u : zero_chunks());
 #pragma unroll
-        for (int j = 0; j < kChunksPerThread; ++j) phys[j] = table_entry<kTable>(r, fdiv(min(q[j], last), g.page_chunks));
+        for (int j = 0; j < kChunksPerThread; ++j) {
+            if constexpr (kTable && kOrder == kDestOrderWave)
+                phys[j] = lpage[j] >= 0 ? table_entry_uniform(r, uint32_t(lpage[j])) : -1;
+            else
+                phys[j] = table_entry<kTable>(r, fdiv(min(q[j], last), g.page_chunks));
+        }
 #pragma unroll
         for (int j = 0; j < kChunksPerThread; ++j) {
             if (q[j] >= r.n) continue;
