@@ -416,10 +416,11 @@ uint64_t sc_kv_block_bytes(int64_t n_head_kv, int64_t head_dim, int64_t page_siz
 /* The engine's content hash - for every byte h = (h ^ b) * 1099511628211 mod 2^64 from `seed` - of `bytes` bytes of
  * device memory, bit-identical to the reference's byte loop fnv1a64 (src/core/pinned.cu:594-601; the payload hash of
  * conversation_wire_payload_hash, src/core/conversation_wire.cpp:1069-1071, and of HandoffArena::payload_hash_of,
- * src/core/handoff.cpp:1133-1136), computed in parallel on the device: the low byte of the state is resolved one bit
- * plane at a time by xor scans, after which the hash is a sum of independent per-segment terms.  The reference seeds
- * every call with 1469598103934665603 (conversation_wire.hpp:196). */
-/* Device workspace the asynchronous form needs for `bytes` bytes of input (about bytes / 200). */
+ * src/core/handoff.cpp:1133-1136), computed in parallel on the device in one read of the input: the low byte of the
+ * state is resolved a few bit planes at a time by xor prefixes and a look-back across workgroups, after which the hash
+ * is a sum of independent per-segment terms.  The reference seeds every call with 1469598103934665603
+ * (conversation_wire.hpp:196). */
+/* Device workspace the asynchronous form needs for `bytes` bytes of input (about bytes / 3000, at least 512 bytes). */
 uint64_t sc_fnv1a64_workspace_bytes(uint64_t bytes);
 /* Enqueue the hash on `stream`; the result lands as one u64 in device memory at `out`.  `data` may have any
  * alignment (16-byte aligned input takes the vector path); `workspace` is 16-byte aligned device memory of at least

@@ -17,17 +17,18 @@
 //      number), h_N = h_0 p^N + sum_n d_n p^(N-n) mod 2^64: independent per-segment Horner sums, folded with powers
 //      of p in any order.
 //
-// The buffer is split into lane segments of kFnvLaneBytes bytes, and the low byte is resolved in three passes over
-// the data: bits 0-2, 3-5 and 6-7.  A pass for bits j .. j + k - 1 runs every segment's machine from its known start
-// bits 0..j-1 once per combination of the unknown start bits j .. j + k - 2, with the pass's top bit started at 0:
-// the end value of a bit in a machine started from the true lower bits is the segment's xor term for that bit (the
-// term of a bit depends only on the lower start bits).  Two machines share one 24-bit multiply (bytes 0 and 2 of a
-// register); the first pass needs only bits 0..2, which follow l' = (l ^ b) * 3 mod 8, so its four machines share
-// one register a byte each.  Per pass: the data pass ballots the terms, each workgroup leaves its map of the k-bit
-// state (a byte), one workgroup scans the maps, and the next pass derives each lane's start bits from its
-// workgroup's state and the ballots by xor-prefix arithmetic.  The last data pass runs the full machine from the now
-// complete start byte, forms each segment's Horner sum, scales it by p^(bytes after the segment) and reduces; a final
-// workgroup adds h_0 p^N.  Four reads of the input in all.
+// The buffer is split into lane segments of kFnvLaneBytes bytes, a workgroup's 256 lanes covering 64 KiB, and the
+// low byte is resolved in three levels: bits 0-2, 3-5 and 6-7.  A level for bits j .. j + k - 1 runs every segment's
+// machine from its known start bits 0..j-1 once per combination of the unknown start bits j .. j + k - 2, with the
+// level's top bit started at 0: the end value of a bit in a machine started from the true lower bits is the segment's
+// xor term for that bit (the term of a bit depends only on the lower start bits).  Two machines share one 24-bit
+// multiply (bytes 0 and 2 of a register); the first level needs only bits 0..2, which follow l' = (l ^ b) * 3 mod 8,
+// so its four machines share one register a byte each.  Per level: the lanes ballot the terms, each workgroup forms
+// its map of the k-bit state from them, finds its start state by a look-back over the workgroups before it, and each
+// lane derives its start bits from the workgroup's state and the ballots by xor-prefix arithmetic.  After the third
+// level every lane runs the full machine from its now complete start byte and forms its segment's Horner sum, scaled
+// by p^(bytes after the segment); the workgroups' sums are added, and a last kernel adds h_0 p^N.  All of it is one
+// kernel that reads the input once (the one-pass hash, below).
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -85,63 +86,17 @@ __device__ __forceinline__ uint32_t spread(uint32_t w) {
     return __builtin_amdgcn_perm(0u, w, uint32_t(k | 0x0c00 | (k << 16) | 0x0c000000));
 }
 
-__device__ __forceinline__ uint32_t run_pair(const uint8_t* p, uint64_t n, bool full, uint32_t x) {
-    if (full) {
-        uint32_t w[kFnvLaneBytes / 4];
-        load_segment(p, w);
-#pragma unroll
-        for (int k = 0; k < kFnvLaneBytes / 4; ++k) {
-            x = step_pair(x, spread<0>(w[k]));
-            x = step_pair(x, spread<1>(w[k]));
-            x = step_pair(x, spread<2>(w[k]));
-            x = step_pair(x, spread<3>(w[k]));
-        }
-        return x;
-    }
+// The byte loops of the machines, for partial and unaligned segments (whole segments run from registers, below).
+__device__ __forceinline__ uint32_t pair_bytes(const uint8_t* p, uint64_t n, uint32_t x) {
     for (uint64_t i = 0; i < n; ++i) x = step_pair(x, uint32_t(p[i]) * 0x10001u);
     return x;
 }
 
-// p^k mod 2^64 for k = 1..K as four signed 16-bit digits, digit[K - k] for the byte k places before a block's end:
-// p^k = sum_j digit[j] 2^(16 j) mod 2^64 with every digit in [-2^15, 2^15) (balanced base 2^16; the carry out of the
-// top digit is a multiple of 2^64 and drops).  The digits of bytes c and c + 1 of a block pair up as one 32-bit word,
-// the operand layout of the packed 16-bit dot product.
-template <int K>
-struct PowDigits {
-    uint32_t pair[K / 2][4];   // [c / 2][j]: digit of byte c in the low half, of byte c + 1 in the high half
-};
-template <int K>
-constexpr PowDigits<K> pow_digits() {
-    int32_t digit[K][4] = {};
-    uint64_t pk = 1;
-    for (int k = 1; k <= K; ++k) {
-        pk *= kFnvPrime;
-        uint64_t v = pk;
-        for (int j = 0; j < 4; ++j) {
-            const int32_t d = int32_t(int16_t(uint16_t(v & 0xFFFFu)));
-            digit[K - k][j] = d;
-            v = (v - uint64_t(int64_t(d))) >> 16;
-        }
-    }
-    PowDigits<K> t{};
-    for (int c = 0; c < K; c += 2)
-        for (int j = 0; j < 4; ++j)
-            t.pair[c / 2][j] = (uint32_t(digit[c][j]) & 0xFFFFu) | (uint32_t(digit[c + 1][j]) << 16);
-    return t;
-}
-template <int K>
-constexpr uint64_t prime_pow() {
-    uint64_t r = 1;
-    for (int k = 0; k < K; ++k) r *= kFnvPrime;
-    return r;
-}
-constexpr PowDigits<16> kPowDigits = pow_digits<16>();
-constexpr uint64_t kPrime16 = prime_pow<16>();
-
-// The Horner sum of 16 bytes given the true low byte `l` before them: sum over c of d_c p^(16-c), d_c = (l ^ b) - l.
-// Per digit j, S_j = sum_c d_c digit[c][j]: |d| <= 255 and |digit| <= 2^15, so |S_j| < 16 * 255 * 2^15 < 2^28 and the
-// sums are exact in 32-bit integers.  Two bytes' d values share one word as signed 16-bit halves, so each S_j takes
-// one packed dot product (v_dot2_i32_i16) per byte pair: 2 operations per byte for the four digits.
+// The Horner sum of a run of bytes is sum over c of d_c p^(len - c), d_c = (l ^ b) - l.  Each power of p is written
+// as four signed 16-bit digits (balanced base 2^16: p^k = sum_j digit_j 2^(16 j) mod 2^64, every digit in
+// [-2^15, 2^15); the carry out of the top digit is a multiple of 2^64 and drops), so per digit j the sum
+// S_j = sum_c d_c digit_j is exact in 32 bits (|d| <= 255), and two d values packed as signed 16-bit halves take one
+// packed dot product (v_dot2_i32_i16) per digit.
 __device__ __forceinline__ int32_t dot2(uint32_t a, uint32_t b, int32_t acc) {
     return __builtin_amdgcn_sdot2(__builtin_bit_cast(v2i16, a), __builtin_bit_cast(v2i16, b), acc, false);
 }
@@ -150,68 +105,27 @@ __device__ __forceinline__ uint64_t digit_sum(int32_t s0, int32_t s1, int32_t s2
     return uint64_t(int64_t(s0)) + (uint64_t(int64_t(s1)) << 16) + (uint64_t(int64_t(s2)) << 32) +
            (uint64_t(int64_t(s3)) << 48);
 }
-__device__ __forceinline__ uint64_t block_sum(const u32x4 v, uint32_t& l) {
-    const uint32_t dw[4] = {v.x, v.y, v.z, v.w};
-    int32_t s0 = 0, s1 = 0, s2 = 0, s3 = 0;
-    // `m` carries the low byte's product unmasked: only its low 8 bits are ever read
-    uint32_t m = l;
-#pragma unroll
-    for (int c = 0; c < 16; c += 2) {
-        const uint32_t x0 = (m ^ (dw[c >> 2] >> (8 * (c & 3)))) & 0xFFu;
-        const uint32_t d0 = x0 - (m & 0xFFu);
-        m = __umul24(x0, kPrimeLow);
-        const uint32_t x1 = (m ^ (dw[(c + 1) >> 2] >> (8 * ((c + 1) & 3)))) & 0xFFu;
-        const uint32_t d1 = x1 - (m & 0xFFu);
-        m = __umul24(x1, kPrimeLow);
-        const uint32_t dp = __builtin_amdgcn_perm(d1, d0, 0x05040100u);   // low halves: d0 | d1 << 16
-        s0 = dot2(dp, kPowDigits.pair[c / 2][0], s0);
-        s1 = dot2(dp, kPowDigits.pair[c / 2][1], s1);
-        s2 = dot2(dp, kPowDigits.pair[c / 2][2], s2);
-        s3 = dot2(dp, kPowDigits.pair[c / 2][3], s3);
-    }
-    l = m & 0xFFu;
-    return digit_sum(s0, s1, s2, s3);
-}
 
 // Byte k of `a` in byte 0 and byte k of `b` in byte 2, zeros elsewhere (v_perm_b32: selector 0x0c gives a zero byte).
 __device__ __forceinline__ uint32_t pair_byte(uint32_t a, uint32_t b, int k) {
     return __builtin_amdgcn_perm(b, a, uint32_t(k) | 0x0c00u | (uint32_t(4 + k) << 16) | 0x0c000000u);
 }
 
-// The Horner sums of 128 bytes of two segments at once, as one sum: the true low bytes of their states sit in the
-// low bytes of the halves of `m` (segment A low, B high, each half's high byte 0), and B starts kPairGap bytes after
-// A.  Per step one permute lines up a byte of each, one xor, one packed subtract gives both d values (A's in the low
+// A lane's segment is summed as two halves of 128 bytes, their machines side by side in one register: the true low
+// bytes of their states sit in the low bytes of the halves of `m` (half A low, half B high, each half's high byte 0).
+// Per step one permute lines up a byte of each, one xor, one packed subtract gives both d values (A's in the low
 // half), one 24-bit multiply and a mask the next low bytes (the masked byte A's product stays below bit 16, as in
-// step_pair).  Byte c of B is weighted by p^(128 - c) and byte c of A by p^(kPairGap + 128 - c), so each digit sum
-// takes one packed dot product per step against a word holding both digits, and the block sum is A's and B's scaled
-// to B's block end; the 64-bit sums are formed once per 128 bytes (|S_j| < 128 * 2 * 255 * 2^15 < 2^31 stays exact).
-// About 4 VALU operations per byte of each segment, against 7.5 for one segment at a time.
+// step_pair).  Byte c of B is weighted by p^(128 - c) and byte c of A by p^(256 - c), so each digit sum takes one
+// packed dot product per step against a word holding both digits, and the one sum is the segment's Horner sum
+// relative to its end (|S_j| < 128 * 2 * 255 * 2^15 < 2^31 stays exact).  About 4 VALU operations per byte, against
+// 7.5 for one byte at a time.
 constexpr int kPairBytes = 128;
-constexpr uint64_t kPairGap = uint64_t(kThreads) * kFnvLaneBytes;   // a lane's two segments, a workgroup apart
 constexpr uint64_t prime_pow_of(uint64_t e) {
     uint64_t r = 1, b = kFnvPrime;
     for (; e; e >>= 1, b *= b)
         if (e & 1) r *= b;
     return r;
 }
-struct PairDigits {
-    uint32_t w[kPairBytes][4];   // [c][j]: digit j of p^(kPairGap + 128 - c) in the low half, of p^(128 - c) above
-};
-constexpr PairDigits pair_digits() {
-    PairDigits t{};
-    for (int c = 0; c < kPairBytes; ++c) {
-        uint64_t va = prime_pow_of(kPairGap + kPairBytes - c), vb = prime_pow_of(kPairBytes - c);
-        for (int j = 0; j < 4; ++j) {
-            const int32_t da = int32_t(int16_t(uint16_t(va & 0xFFFFu))), db = int32_t(int16_t(uint16_t(vb & 0xFFFFu)));
-            t.w[c][j] = (uint32_t(da) & 0xFFFFu) | (uint32_t(db) << 16);
-            va = (va - uint64_t(int64_t(da))) >> 16;
-            vb = (vb - uint64_t(int64_t(db))) >> 16;
-        }
-    }
-    return t;
-}
-constexpr PairDigits kPairDigits = pair_digits();
-constexpr uint64_t kPrimePair = prime_pow<kPairBytes>();
 // p^(256 (63 - l)) for lane l: a lane's sum, relative to the end of its segment B, times this is relative to the end of
 // the wave's last segment B.
 struct LanePow {
@@ -223,19 +137,36 @@ constexpr LanePow lane_pow() {
     return t;
 }
 __constant__ LanePow kLanePow = lane_pow();
-__device__ __forceinline__ uint64_t run_sum2(const u32x4 (&va)[kPairBytes / 16], const u32x4 (&vb)[kPairBytes / 16],
-                                             uint32_t& m) {
+struct HalfDigits {
+    uint32_t w[kPairBytes][4];   // [c][j]: digit j of p^(256 - c) in the low half, of p^(128 - c) above
+};
+constexpr HalfDigits half_digits() {
+    HalfDigits t{};
+    for (int c = 0; c < kPairBytes; ++c) {
+        uint64_t va = prime_pow_of(2 * kPairBytes - c), vb = prime_pow_of(kPairBytes - c);
+        for (int j = 0; j < 4; ++j) {
+            const int32_t da = int32_t(int16_t(uint16_t(va & 0xFFFFu))), db = int32_t(int16_t(uint16_t(vb & 0xFFFFu)));
+            t.w[c][j] = (uint32_t(da) & 0xFFFFu) | (uint32_t(db) << 16);
+            va = (va - uint64_t(int64_t(da))) >> 16;
+            vb = (vb - uint64_t(int64_t(db))) >> 16;
+        }
+    }
+    return t;
+}
+constexpr HalfDigits kHalfDigits = half_digits();
+// `m`: the true low byte at the segment's start in the low half, at its midpoint in the high half.
+__device__ __forceinline__ uint64_t halves_sum(const uint32_t (&w)[kFnvLaneBytes / 4], uint32_t m) {
+    constexpr int kHalfWords = kPairBytes / 4;
     int32_t s0 = 0, s1 = 0, s2 = 0, s3 = 0;
 #pragma unroll
     for (int c = 0; c < kPairBytes; ++c) {
-        const int w = c >> 2;   // the dword of byte c
-        const uint32_t x = m ^ pair_byte(va[w >> 2][w & 3], vb[w >> 2][w & 3], c & 3);
+        const uint32_t x = m ^ pair_byte(w[c >> 2], w[kHalfWords + (c >> 2)], c & 3);
         const uint32_t d = pk_sub(x, m);
         m = __umul24(x, kPrimeLow) & 0x00FF00FFu;
-        s0 = dot2(d, kPairDigits.w[c][0], s0);
-        s1 = dot2(d, kPairDigits.w[c][1], s1);
-        s2 = dot2(d, kPairDigits.w[c][2], s2);
-        s3 = dot2(d, kPairDigits.w[c][3], s3);
+        s0 = dot2(d, kHalfDigits.w[c][0], s0);
+        s1 = dot2(d, kHalfDigits.w[c][1], s1);
+        s2 = dot2(d, kHalfDigits.w[c][2], s2);
+        s3 = dot2(d, kHalfDigits.w[c][3], s3);
     }
     return digit_sum(s0, s1, s2, s3);
 }
@@ -258,22 +189,19 @@ __device__ __forceinline__ uint64_t xor_prefix_excl(uint64_t x) {
     return x << 1;
 }
 
-// The ballots of one pass, per wave: the terms of the lowest unresolved bit j (T), of bit j + 1 for either start
-// value a of bit j (U_a), and, in a three-bit pass, of bit j + 2 for each start pair (a, c) of bits j, j + 1 (W_ac).
+// The ballots of one level, per wave: the terms of the lowest unresolved bit j (T), of bit j + 1 for either start
+// value a of bit j (U_a), and, in a three-bit level, of bit j + 2 for each start pair (a, c) of bits j, j + 1 (W_ac).
 // A bit's term over a run is the xor of per-byte contributions that depend only on the lower bits of the state, so
 // each is the end value of that bit in a machine started from the right lower bits with the bit itself 0.
-constexpr int kMaxPassWords = 7;   // T, U0, U1, W00, W01, W10, W11
-struct PassWords {
-    uint64_t* w[kMaxPassWords];
-};
+constexpr int kMaxLevelWords = 7;   // T, U0, U1, W00, W01, W10, W11
 template <int kBits>
-constexpr int pass_words() { return kBits == 3 ? 7 : 3; }
+constexpr int level_words() { return kBits == 3 ? 7 : 3; }
 
 // The lanes' true start bits of one wave, as masks, from `st` (bit j in bit 0, j + 1 in bit 1, j + 2 in bit 2) at
 // the wave's first segment; `st` advances past the wave.  Each lane's term for a bit is chosen by its own true lower
 // bits, and the bit at a lane is the wave's incoming bit xor the terms of the lanes before it.
 template <int kBits>
-__device__ __forceinline__ void wave_masks(const uint64_t (&wd)[kMaxPassWords], uint32_t& st, uint64_t (&m)[3]) {
+__device__ __forceinline__ void wave_masks(const uint64_t (&wd)[kMaxLevelWords], uint32_t& st, uint64_t (&m)[3]) {
     const uint32_t a = st & 1u, c = (st >> 1) & 1u;
     const uint64_t sj = xor_prefix_excl(wd[0]) ^ (a ? ~0ull : 0ull);
     const uint64_t v = (sj & wd[2]) | (~sj & wd[1]);
@@ -290,32 +218,7 @@ __device__ __forceinline__ void wave_masks(const uint64_t (&wd)[kMaxPassWords], 
     st = next;
 }
 
-// This lane's true start bits j .. j + kBits - 1 (bit 0 of the result upward) in the pass's workgroup `group`, from
-// that workgroup's start state and the ballots of its waves.
-template <int kBits>
-__device__ __forceinline__ uint32_t lane_bits(uint64_t group, uint32_t gstate, const PassWords& w) {
-    // the wave index is read as wave-uniform, so the masks below are scalar work
-    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint64_t base = group * 4;
-    uint32_t st = gstate;
-    uint64_t m[3] = {0, 0, 0};
-    // every word this lane may need is loaded before the first step, so the loads overlap
-    uint64_t wd[kThreads / 64][kMaxPassWords] = {};
-#pragma unroll
-    for (int k = 0; k < kThreads / 64; ++k)
-#pragma unroll
-        for (int i = 0; i < pass_words<kBits>(); ++i)
-            if (k <= wave) wd[k][i] = w.w[i][base + k];
-#pragma unroll
-    for (int k = 0; k < kThreads / 64; ++k)
-        if (k <= wave) wave_masks<kBits>(wd[k], st, m);
-    uint32_t bits = 0;
-#pragma unroll
-    for (int i = 0; i < kBits; ++i) bits |= (uint32_t(m[i] >> lane) & 1u) << i;
-    return bits;
-}
-
-// The first pass only needs bits 0..2 of the state, which follow l' = ((l ^ b) * 3) mod 8 (179 = 3 mod 8): four
+// The first level only needs bits 0..2 of the state, which follow l' = ((l ^ b) * 3) mod 8 (179 = 3 mod 8): four
 // such machines share one register, one per byte (a 3-bit state times 3 stays below 2^8, so nothing carries across
 // bytes; the product's bits above 2 are masked by the next step).  Machine (a, c) - start bits 0, 1 = a, c - sits in
 // byte a + 2c.
@@ -327,46 +230,12 @@ __device__ __forceinline__ uint32_t step_low3(uint32_t x, uint32_t b4) {
     const uint32_t y = (x ^ b4) & 0x07070707u;
     return y + (y << 1);
 }
-__device__ __forceinline__ uint32_t run_low3(const uint8_t* p, uint64_t n, bool full) {
+__device__ __forceinline__ uint32_t low3_bytes(const uint8_t* p, uint64_t n) {
     uint32_t x = 0x03020100u;
-    if (full) {
-        uint32_t w[kFnvLaneBytes / 4];
-        load_segment(p, w);
-#pragma unroll
-        for (int k = 0; k < kFnvLaneBytes / 4; ++k) {
-            x = step_low3(x, spread4<0>(w[k]));
-            x = step_low3(x, spread4<1>(w[k]));
-            x = step_low3(x, spread4<2>(w[k]));
-            x = step_low3(x, spread4<3>(w[k]));
-        }
-    } else {
-        for (uint64_t i = 0; i < n; ++i) x = step_low3(x, uint32_t(p[i]) * 0x01010101u);
-    }
+    for (uint64_t i = 0; i < n; ++i) x = step_low3(x, uint32_t(p[i]) * 0x01010101u);
     return x & 0x07070707u;
 }
-
-// Four low-byte machines in two registers (bytes 0 and 2 of each), one spread byte for both.
-__device__ __forceinline__ void run_quad(const uint8_t* p, uint64_t n, bool full, uint32_t& xa, uint32_t& xb) {
-    if (full) {
-        uint32_t w[kFnvLaneBytes / 4];
-        load_segment(p, w);
-#pragma unroll
-        for (int k = 0; k < kFnvLaneBytes / 4; ++k) {
-            uint32_t bb = spread<0>(w[k]);
-            xa = step_pair(xa, bb);
-            xb = step_pair(xb, bb);
-            bb = spread<1>(w[k]);
-            xa = step_pair(xa, bb);
-            xb = step_pair(xb, bb);
-            bb = spread<2>(w[k]);
-            xa = step_pair(xa, bb);
-            xb = step_pair(xb, bb);
-            bb = spread<3>(w[k]);
-            xa = step_pair(xa, bb);
-            xb = step_pair(xb, bb);
-        }
-        return;
-    }
+__device__ __forceinline__ void quad_bytes(const uint8_t* p, uint64_t n, uint32_t& xa, uint32_t& xb) {
     for (uint64_t i = 0; i < n; ++i) {
         const uint32_t bb = uint32_t(p[i]) * 0x10001u;
         xa = step_pair(xa, bb);
@@ -374,6 +243,10 @@ __device__ __forceinline__ void run_quad(const uint8_t* p, uint64_t n, bool full
     }
 }
 
+// A workgroup's map of a level's state: (a, c, e) = (bit j, j + 1, j + 2) at its first segment goes to
+// (a ^ t, c ^ v_a, e ^ w_ac) at the next workgroup's first segment; the map is a byte (bit 0 t, bits 1-2 v_0 v_1,
+// bits 3-6 w_00 w_01 w_10 w_11; a two-bit level has no e and no w), 0 being the identity.  Maps compose as
+// (g after f): t = t_f ^ t_g, v_a = v_a(f) ^ v_(a ^ t_f)(g), w_ac = w_ac(f) ^ w_(a ^ t_f, c ^ v_a(f))(g).
 __device__ __forceinline__ uint32_t map_v(uint32_t m, uint32_t a) { return (m >> (1u + a)) & 1u; }
 __device__ __forceinline__ uint32_t map_w(uint32_t m, uint32_t a, uint32_t c) { return (m >> (3u + 2u * a + c)) & 1u; }
 template <int kBits>
@@ -399,144 +272,10 @@ __device__ __forceinline__ uint32_t apply(uint32_t m, uint32_t st) {
     return r;
 }
 
-// Data pass for bits j .. j + kBits - 1.  First completes each segment's start bits from the previous pass (which
-// resolved kPrevBits bits; the bits below it are in start[]), then runs the machines - two (start bit j = 0, 1) for
-// a two-bit pass, four (start bits j, j + 1 = 00, 10, 01, 11) for a three-bit one - ballots the terms, and leaves
-// the workgroup's summary: its map of the state at its first segment (bit 0 t, bits 1-2 v_a, bits 3-6 w_ac).
-template <int kBits, int kPrevBits>
-__global__ void __launch_bounds__(kThreads) fnv_pass_kernel(const uint8_t* data, uint64_t n, int j, bool aligned,
-                                                             uint8_t* start, PassWords prev, const uint8_t* gstate_prev,
-                                                             PassWords out, uint8_t* summary) {
-    const uint64_t seg = uint64_t(blockIdx.x) * kThreads + threadIdx.x;
-    const uint64_t begin = seg * kFnvLaneBytes;
-    const bool live = begin < n;
-    uint32_t s = 0;
-    if constexpr (kPrevBits > 0) {
-        const uint32_t bits = lane_bits<kPrevBits>(blockIdx.x, gstate_prev[blockIdx.x], prev);
-        const int lo = j - kPrevBits;
-        s = (lo > 0 && live ? uint32_t(start[seg]) : 0u) | (bits << lo);
-        if (live) start[seg] = uint8_t(s);
-    }
-    uint32_t ea = 0, eb = 0;
-    if constexpr (kBits == 3 && kPrevBits == 0) {
-        // bits 0..2 (j = 0): the four machines of run_low3 end in bytes a + 2c; regroup them into the layout the
-        // ballots below read (ea: machines (0, 0) in byte 0 and (1, 0) in byte 2; eb: (0, 1) and (1, 1))
-        if (live) {
-            const uint64_t len = n - begin < kFnvLaneBytes ? n - begin : kFnvLaneBytes;
-            const uint32_t x = run_low3(data + begin, len, aligned && len == kFnvLaneBytes);
-            ea = (x & 0xFFu) | (((x >> 8) & 0xFFu) << 16);
-            eb = ((x >> 16) & 0xFFu) | ((x >> 24) << 16);
-        }
-    } else if (live) {
-        const uint64_t len = n - begin < kFnvLaneBytes ? n - begin : kFnvLaneBytes;
-        const bool full = aligned && len == kFnvLaneBytes;
-        ea = s | ((s | (1u << j)) << 16);
-        if constexpr (kBits == 2) {
-            ea = run_pair(data + begin, len, full, ea);
-        } else {
-            const uint32_t sc = s | (1u << (j + 1));
-            eb = sc | ((sc | (1u << j)) << 16);
-            run_quad(data + begin, len, full, ea, eb);
-        }
-    }
-    uint64_t bw[kMaxPassWords] = {};
-    bw[0] = __ballot((ea >> j) & 1u);
-    bw[1] = __ballot((ea >> (j + 1)) & 1u);
-    bw[2] = __ballot((ea >> (16 + j + 1)) & 1u);
-    if constexpr (kBits == 3) {
-        bw[3] = __ballot((ea >> (j + 2)) & 1u);        // start (a, c) = (0, 0)
-        bw[4] = __ballot((eb >> (j + 2)) & 1u);        // (0, 1)
-        bw[5] = __ballot((ea >> (16 + j + 2)) & 1u);   // (1, 0)
-        bw[6] = __ballot((eb >> (16 + j + 2)) & 1u);   // (1, 1)
-    }
-    // this wave's map of the state at its first segment, from its ballots (wave-uniform, so scalar work); the
-    // workgroup's map is the four waves' maps composed in order
-    uint32_t wmap = 0;
-#pragma unroll
-    for (uint32_t in = 0; in < (1u << (kBits - 1)); ++in) {   // start (a, c) = (in & 1, in >> 1), e = 0
-        const uint32_t a = in & 1u, c = (in >> 1) & 1u;
-        uint32_t st = in;
-        uint64_t m[3];
-        wave_masks<kBits>(bw, st, m);
-        if (in == 0) wmap |= st & 1u;                                  // t
-        if (c == 0) wmap |= ((st >> 1) & 1u) << (1 + a);               // v_a: the end bit j + 1 from c = 0
-        if constexpr (kBits == 3) wmap |= ((st >> 2) & 1u) << (3 + 2 * a + c);   // w_ac: end bit j + 2 from e = 0
-    }
-    __shared__ uint32_t s_map[kThreads / 64];
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    if ((threadIdx.x & 63) == 0) {
-        const uint64_t at = uint64_t(blockIdx.x) * 4 + wave;
-#pragma unroll
-        for (int i = 0; i < pass_words<kBits>(); ++i) out.w[i][at] = bw[i];
-        s_map[wave] = wmap;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        uint32_t sum = s_map[0];
-        for (int k = 1; k < kThreads / 64; ++k) sum = compose<kBits>(s_map[k], sum);
-        summary[blockIdx.x] = uint8_t(sum);
-    }
-}
-
 // The state the hash starts from: the launch's seed, or the running hash at `seed_dev` when the input continues an
 // earlier one (read by every kernel that needs it, so one stream can chain pieces without a host round trip).
 __device__ __forceinline__ uint64_t start_state(uint64_t seed, const uint64_t* seed_dev) {
     return seed_dev ? *seed_dev : seed;
-}
-
-// The workgroups' start states for one pass, in one workgroup.  Workgroup g maps the state (a, c, e) = (bit j,
-// j + 1, j + 2) at its first segment to (a ^ t, c ^ v_a, e ^ w_ac) at the next workgroup's, and its summary byte is
-// that map (bit 0 t, bits 1-2 v_0 v_1, bits 3-6 w_00 w_01 w_10 w_11; a two-bit pass has no e and no w).  Maps compose
-// as (g after f): t = t_f ^ t_g, v_a = v_a(f) ^ v_(a ^ t_f)(g), w_ac = w_ac(f) ^ w_(a ^ t_f, c ^ v_a(f))(g).
-// Each thread composes its run of summaries (read 16 bytes at a time), the runs are scanned across threads in LDS,
-// and each thread then walks its run again from its start state, writing the states 16 at a time.
-constexpr uint64_t kScanVec = 16;   // summary bytes per vector load / state bytes per vector store
-
-template <int kBits>
-__global__ void __launch_bounds__(kScanThreads) fnv_scan_kernel(const uint8_t* summary, uint64_t groups, int j,
-                                                                 uint64_t seed, const uint64_t* seed_dev,
-                                                                 uint8_t* gstate) {
-    constexpr uint32_t kMask = kBits == 3 ? 0x7Fu : 0x7u;
-    const uint32_t init = uint32_t(start_state(seed, seed_dev) >> j) & ((1u << kBits) - 1u);
-    // runs of whole 16-byte vectors: the summaries and states live in 256-byte aligned buffers padded to 256 bytes,
-    // so a vector that starts before `groups` stays inside its buffer
-    const uint64_t per = ((groups + kScanThreads - 1) / kScanThreads + kScanVec - 1) / kScanVec * kScanVec;
-    const uint64_t b = uint64_t(threadIdx.x) * per;
-    const uint64_t e = b + per < groups ? b + per : groups;
-    uint32_t f = 0;
-    for (uint64_t c = b; c < e; c += kScanVec) {
-        const u32x4 w = *(const gu32x4*) (summary + c);
-        const uint32_t words[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-        for (int k = 0; k < int(kScanVec); ++k)
-            if (c + uint64_t(k) < e) f = compose<kBits>((words[k >> 2] >> (8 * (k & 3))) & kMask, f);
-    }
-    // inclusive scan of the run maps (Hillis-Steele), then the exclusive prefix of this thread's run
-    __shared__ uint32_t s_map[kScanThreads];
-    s_map[threadIdx.x] = f;
-    __syncthreads();
-    for (int o = 1; o < kScanThreads; o <<= 1) {
-        const uint32_t earlier = threadIdx.x >= uint32_t(o) ? s_map[threadIdx.x - o] : 0u;
-        __syncthreads();
-        s_map[threadIdx.x] = compose<kBits>(s_map[threadIdx.x], earlier);
-        __syncthreads();
-    }
-    uint32_t st = apply<kBits>(threadIdx.x ? s_map[threadIdx.x - 1] : 0u, init);
-    for (uint64_t c = b; c < e; c += kScanVec) {
-        const u32x4 w = *(const gu32x4*) (summary + c);
-        const uint32_t words[4] = {w.x, w.y, w.z, w.w};
-        uint32_t out[4] = {0u, 0u, 0u, 0u};
-#pragma unroll
-        for (int k = 0; k < int(kScanVec); ++k) {
-            out[k >> 2] |= st << (8 * (k & 3));
-            st = apply<kBits>((words[k >> 2] >> (8 * (k & 3))) & kMask, st);
-        }
-        if (c + kScanVec <= e) {
-            *(gu32x4*) (gstate + c) = u32x4{out[0], out[1], out[2], out[3]};
-        } else {
-            for (uint64_t k = 0; c + k < e; ++k) gstate[c + k] = uint8_t(out[k >> 2] >> (8 * (k & 3)));
-        }
-    }
 }
 
 __device__ __forceinline__ uint64_t shfl_xor64(uint64_t v, int m) {
@@ -544,65 +283,14 @@ __device__ __forceinline__ uint64_t shfl_xor64(uint64_t v, int m) {
     return (uint64_t(hi) << 32) | lo;
 }
 
-// One segment's Horner sum, scaled by p^(bytes after it), from the true low byte `l` at its start.
-__device__ __forceinline__ uint64_t segment_sum(const uint8_t* data, uint64_t n, uint64_t begin, bool aligned,
-                                                uint32_t l) {
+// One partial or unaligned segment's Horner sum, scaled by p^(bytes after it), from the true low byte `l` at its
+// start, a byte at a time.
+__device__ __forceinline__ uint64_t segment_sum(const uint8_t* data, uint64_t n, uint64_t begin, uint32_t l) {
     const uint64_t len = n - begin < kFnvLaneBytes ? n - begin : kFnvLaneBytes;
     const uint8_t* p = data + begin;
     uint64_t acc = 0;
-    if (aligned && len == kFnvLaneBytes) {
-        u32x4 v[kFnvLaneBytes / 16];
-#pragma unroll
-        for (int k = 0; k < kFnvLaneBytes / 16; ++k) v[k] = *(const gu32x4*) (p + 16 * k);
-#pragma unroll
-        for (int k = 0; k < kFnvLaneBytes / 16; ++k) acc = acc * kPrime16 + block_sum(v[k], l);
-    } else {
-        for (uint64_t i = 0; i < len; ++i) step_full(p[i], l, acc);
-    }
+    for (uint64_t i = 0; i < len; ++i) step_full(p[i], l, acc);
     return acc * pow_prime(n - begin - len);
-}
-
-// Each lane takes two segments, its own in the pass's workgroups 2g and 2g + 1, and runs their machines side by side
-// (run_sum2).  A lane's segment is read in two halves of 128 bytes, each half of both segments loaded before it is
-// summed (lanes are 256 bytes apart, so each half is one 128-byte line per segment, read by eight loads issued
-// together).  The last, partial segments and unaligned data take the one-segment path.
-__global__ void __launch_bounds__(kThreads) fnv_final_kernel(const uint8_t* data, uint64_t n, uint64_t groups,
-                                                              bool aligned, const uint8_t* start, PassWords prev,
-                                                              const uint8_t* gstate_prev, uint64_t* partial) {
-    const uint64_t ga = uint64_t(blockIdx.x) * 2, gb = ga + 1;
-    const uint64_t sa = ga * kThreads + threadIdx.x, sb = gb * kThreads + threadIdx.x;
-    const uint64_t ba = sa * kFnvLaneBytes, bb = sb * kFnvLaneBytes;
-    const uint32_t bits_a = lane_bits<2>(ga, gstate_prev[ga], prev);
-    const uint32_t bits_b = gb < groups ? lane_bits<2>(gb, gstate_prev[gb], prev) : 0u;
-    // p^(n - r), r the end of the wave's last segment B: wave-uniform, one power per wave rather than one per lane.  p
-    // has order dividing 2^62 modulo 2^64, so the exponent is taken modulo 2^62 (r passes n in the buffer's last wave)
-    const uint64_t wave_end =
-        (gb * kThreads + uint64_t(__builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) * 64 + 64) * kFnvLaneBytes;
-    const uint64_t wave_pow = pow_prime((n - wave_end) & ((uint64_t(1) << 62) - 1));
-    uint64_t acc = 0;
-    if (aligned && bb + kFnvLaneBytes <= n) {   // both segments whole
-        uint32_t m = (uint32_t(start[sa]) | (bits_a << 6)) | ((uint32_t(start[sb]) | (bits_b << 6)) << 16);
-        uint64_t acc2 = 0;
-#pragma unroll 1
-        for (int h = 0; h < kFnvLaneBytes; h += kPairBytes) {
-            u32x4 va[kPairBytes / 16], vb[kPairBytes / 16];
-#pragma unroll
-            for (int k = 0; k < kPairBytes / 16; ++k) {
-                va[k] = *(const gu32x4*) (data + ba + h + 16 * k);
-                vb[k] = *(const gu32x4*) (data + bb + h + 16 * k);
-            }
-            acc2 = acc2 * kPrimePair + run_sum2(va, vb, m);
-        }
-        acc = acc2 * kLanePow.v[threadIdx.x & 63] * wave_pow;   // both segments, scaled to the input's end
-    } else {
-        if (ba < n) acc += segment_sum(data, n, ba, aligned, uint32_t(start[sa]) | (bits_a << 6));
-        if (bb < n) acc += segment_sum(data, n, bb, aligned, uint32_t(start[sb]) | (bits_b << 6));
-    }
-    for (int m = 32; m > 0; m >>= 1) acc += shfl_xor64(acc, m);
-    __shared__ uint64_t s_sum[kThreads / 64];
-    if ((threadIdx.x & 63) == 0) s_sum[threadIdx.x >> 6] = acc;
-    __syncthreads();
-    if (threadIdx.x == 0) partial[blockIdx.x] = s_sum[0] + s_sum[1] + s_sum[2] + s_sum[3];
 }
 
 // h = seed * p^n + sum of the partial sums (mod 2^64; the order of the additions does not matter).  With `verdict`,
@@ -610,7 +298,8 @@ __global__ void __launch_bounds__(kThreads) fnv_final_kernel(const uint8_t* data
 // round trip.
 __global__ void __launch_bounds__(kScanThreads) fnv_reduce_kernel(const uint64_t* partial, uint64_t groups, uint64_t seed,
                                                                    const uint64_t* seed_dev, uint64_t n, uint64_t* out,
-                                                                   uint64_t expected, uint32_t* verdict) {
+                                                                   uint64_t expected, uint32_t* verdict,
+                                                                   const uint32_t* fault) {
     uint64_t acc = 0;
     for (uint64_t i = threadIdx.x; i < groups; i += kScanThreads) acc += partial[i];
     for (int m = 32; m > 0; m >>= 1) acc += shfl_xor64(acc, m);
@@ -621,25 +310,282 @@ __global__ void __launch_bounds__(kScanThreads) fnv_reduce_kernel(const uint64_t
         uint64_t h = start_state(seed, seed_dev) * pow_prime(n);
         for (int w = 0; w < kScanThreads / 64; ++w) h += s_sum[w];
         out[0] = h;
-        if (verdict) verdict[0] = h == expected ? 1u : 0u;
+        if (verdict) verdict[0] = h == expected && !(fault && fault[0]) ? 1u : 0u;
     }
 }
 
+
+// ---- the one-pass hash ---------------------------------------------------------------------------------------------
+// One kernel reads the input once: each lane keeps its 256-byte segment in registers through the three levels of the
+// low byte and the Horner sums.  A level's workgroup start state comes from a decoupled look-back rather than a scan
+// kernel: workgroups take their index from a ticket counter in the order they start, publish their map of the level's
+// state as soon as they have it and their end state once they know their start, and a workgroup finds its start by
+// reading the words of the 64 workgroups before it at once and composing maps back to the nearest end state.  A
+// workgroup waits only on lower tickets, held by workgroups that are running or done, so every wait ends; each wait is
+// also bounded (kSpinLimit reads), after which the launch records a fault that fails the verdict and the workgroup
+// publishes an end state anyway, so no other workgroup waits on it.
+constexpr uint32_t kHasMap = 1u << 8, kHasState = 1u << 9;   // a status word: 0, kHasMap | map, kHasState | state
+constexpr uint32_t kSpinLimit = 1u << 16;   // reads of one window, about 0.1 s
+
+__device__ __forceinline__ void publish(uint32_t* word, uint32_t v) {
+    __hip_atomic_store(word, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t peek(uint32_t* word) {
+    return __hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Workgroup g's start state at one level, run by one whole wave (the result is wave-uniform); publishes g's map
+// before the look-back and its end state after.  `init` is the state before workgroup 0.  Lane l reads the word of
+// workgroup top - l.  The maps of lanes 0..l compose in one inclusive scan across the wave (six shuffle steps), so
+// resolving a window costs the same wherever its nearest end state lies.
+template <int kBits>
+__device__ __forceinline__ uint32_t look_back(uint32_t* status, uint64_t g, uint32_t map, uint32_t init, uint32_t* fault) {
+    const int lane = threadIdx.x & 63;
+    if (g == 0) {
+        if (lane == 0) publish(status, kHasState | apply<kBits>(map, init));
+        return init;
+    }
+    if (lane == 0) publish(status + g, kHasMap | map);
+    uint32_t acc = 0;                  // the maps of the workgroups from above the window up to g, composed
+    int64_t top = int64_t(g) - 1;      // the window is workgroups top, top - 1, ...; before workgroup 0 stands `init`
+    uint32_t spins = 0;
+    for (;;) {
+        const int64_t h = top - lane;
+        const uint32_t word = h >= 0 ? peek(status + h) : (kHasState | init);
+        const uint64_t have_state = __ballot((word & kHasState) != 0u);
+        const uint64_t ready = __ballot((word & (kHasMap | kHasState)) != 0u);
+        const int first = have_state ? __builtin_ctzll(have_state) : 64;   // the lane of the nearest end state
+        const uint64_t need = first == 64 ? ~0ull : (1ull << first) - 1ull;
+        if ((ready & need) != need) {   // a workgroup between g and that end state has not published its map yet
+            if (++spins > kSpinLimit) {   // never in a correct launch; successors still get an end state
+                if (lane == 0) {
+                    publish(fault, 1u);
+                    publish(status + g, kHasState | apply<kBits>(map, 0u));
+                }
+                return 0u;
+            }
+            __builtin_amdgcn_s_sleep(1);
+            continue;
+        }
+        // x_l = map_0 o map_1 o ... o map_l (map_l applied first); the lanes from `first` on are not used
+        uint32_t x = word & 0xFFu;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const uint32_t lower = uint32_t(__shfl_up(int(x), d));
+            if (lane >= d) x = compose<kBits>(lower, x);
+        }
+        if (first < 64) {
+            uint32_t st = uint32_t(__builtin_amdgcn_readlane(int(word), first)) & 0xFFu;
+            if (first > 0) st = apply<kBits>(uint32_t(__builtin_amdgcn_readlane(int(x), first - 1)), st);
+            st = apply<kBits>(acc, st);
+            if (lane == 0) publish(status + g, kHasState | apply<kBits>(map, st));
+            return st;
+        }
+        acc = compose<kBits>(acc, uint32_t(__builtin_amdgcn_readlane(int(x), 63)));   // all maps: read the window before
+        top -= 64;
+        spins = 0;
+    }
+}
+
+struct LevelLds {
+    uint64_t bw[kThreads / 64][kMaxLevelWords];
+    uint32_t map[kThreads / 64];
+    uint32_t state;
+};
+
+__device__ __forceinline__ uint64_t uniform64(uint64_t v) {
+    return uint64_t(uint32_t(__builtin_amdgcn_readfirstlane(int(uint32_t(v))))) |
+           (uint64_t(uint32_t(__builtin_amdgcn_readfirstlane(int(uint32_t(v >> 32))))) << 32);
+}
+
+// One level (bits j .. j + kBits - 1) once the machines have run: ballots the terms, forms the workgroup's map, looks
+// back for the workgroup's start state, and returns this lane's start bits of the level (bit 0 upward).
+template <int kBits>
+__device__ __forceinline__ uint32_t resolve_level(uint32_t ea, uint32_t eb, int j, uint64_t g, uint32_t* status, uint32_t init,
+                                  uint32_t* fault, LevelLds& L) {
+    uint64_t bw[kMaxLevelWords] = {};
+    bw[0] = __ballot((ea >> j) & 1u);
+    bw[1] = __ballot((ea >> (j + 1)) & 1u);
+    bw[2] = __ballot((ea >> (16 + j + 1)) & 1u);
+    if constexpr (kBits == 3) {
+        bw[3] = __ballot((ea >> (j + 2)) & 1u);        // start (a, c) = (0, 0)
+        bw[4] = __ballot((eb >> (j + 2)) & 1u);        // (0, 1)
+        bw[5] = __ballot((ea >> (16 + j + 2)) & 1u);   // (1, 0)
+        bw[6] = __ballot((eb >> (16 + j + 2)) & 1u);   // (1, 1)
+    }
+    uint32_t wmap = 0;
+#pragma unroll
+    for (uint32_t in = 0; in < (1u << (kBits - 1)); ++in) {
+        const uint32_t a = in & 1u, c = (in >> 1) & 1u;
+        uint32_t st = in;
+        uint64_t m[3];
+        wave_masks<kBits>(bw, st, m);
+        if (in == 0) wmap |= st & 1u;
+        if (c == 0) wmap |= ((st >> 1) & 1u) << (1 + a);
+        if constexpr (kBits == 3) wmap |= ((st >> 2) & 1u) << (3 + 2 * a + c);
+    }
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (lane == 0) {
+#pragma unroll
+        for (int i = 0; i < level_words<kBits>(); ++i) L.bw[wave][i] = bw[i];
+        L.map[wave] = wmap;
+    }
+    __syncthreads();
+    if (wave == 0) {
+        uint32_t sum = L.map[0];
+        for (int k = 1; k < kThreads / 64; ++k) sum = compose<kBits>(L.map[k], sum);
+        const uint32_t st = look_back<kBits>(status, g, __builtin_amdgcn_readfirstlane(sum), init, fault);
+        if (lane == 0) L.state = st;
+    }
+    __syncthreads();
+    uint32_t st = __builtin_amdgcn_readfirstlane(L.state);
+    uint64_t m[3] = {0, 0, 0};
+#pragma unroll
+    for (int k = 0; k < kThreads / 64; ++k) {
+        if (k > wave) break;
+        uint64_t wd[kMaxLevelWords] = {};
+#pragma unroll
+        for (int i = 0; i < level_words<kBits>(); ++i) wd[i] = uniform64(L.bw[k][i]);
+        wave_masks<kBits>(wd, st, m);
+    }
+    uint32_t bits = 0;
+#pragma unroll
+    for (int i = 0; i < kBits; ++i) bits |= (uint32_t(m[i] >> lane) & 1u) << i;
+    __syncthreads();   // the next level rewrites L
+    return bits;
+}
+
+// The machines of each level over a segment held in registers.
+__device__ __forceinline__ uint32_t low3_regs(const uint32_t (&w)[kFnvLaneBytes / 4]) {
+    uint32_t x = 0x03020100u;
+#pragma unroll
+    for (int k = 0; k < kFnvLaneBytes / 4; ++k) {
+        x = step_low3(x, spread4<0>(w[k]));
+        x = step_low3(x, spread4<1>(w[k]));
+        x = step_low3(x, spread4<2>(w[k]));
+        x = step_low3(x, spread4<3>(w[k]));
+    }
+    return x & 0x07070707u;
+}
+__device__ __forceinline__ void quad_regs(const uint32_t (&w)[kFnvLaneBytes / 4], uint32_t& xa, uint32_t& xb) {
+#pragma unroll
+    for (int k = 0; k < kFnvLaneBytes / 4; ++k) {
+        uint32_t bb = spread<0>(w[k]);
+        xa = step_pair(xa, bb);
+        xb = step_pair(xb, bb);
+        bb = spread<1>(w[k]);
+        xa = step_pair(xa, bb);
+        xb = step_pair(xb, bb);
+        bb = spread<2>(w[k]);
+        xa = step_pair(xa, bb);
+        xb = step_pair(xb, bb);
+        bb = spread<3>(w[k]);
+        xa = step_pair(xa, bb);
+        xb = step_pair(xb, bb);
+    }
+}
+// Also leaves the two machines' states at the segment's midpoint in `mid`.
+__device__ __forceinline__ uint32_t pair_regs(const uint32_t (&w)[kFnvLaneBytes / 4], uint32_t x, uint32_t& mid) {
+#pragma unroll
+    for (int k = 0; k < kFnvLaneBytes / 4; ++k) {
+        if (k == kPairBytes / 4) mid = x;
+        x = step_pair(x, spread<0>(w[k]));
+        x = step_pair(x, spread<1>(w[k]));
+        x = step_pair(x, spread<2>(w[k]));
+        x = step_pair(x, spread<3>(w[k]));
+    }
+    return x;
+}
+
+// status: three arrays of `stride` words (one per level); ctl: [0] the ticket counter, [1] the fault word.
+__global__ void __launch_bounds__(kThreads) fnv_onepass_kernel(const uint8_t* data, uint64_t n, bool aligned,
+                                                                uint64_t seed, const uint64_t* seed_dev,
+                                                                uint32_t* status, uint64_t stride, uint32_t* ctl,
+                                                                uint64_t* partial) {
+    __shared__ LevelLds L;
+    __shared__ uint32_t s_ticket;
+    __shared__ uint64_t s_sum[kThreads / 64];
+    if (threadIdx.x == 0) s_ticket = atomicAdd(ctl, 1u);
+    __syncthreads();
+    const uint64_t g = uint32_t(__builtin_amdgcn_readfirstlane(int(s_ticket)));
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint64_t begin = (g * kThreads + threadIdx.x) * kFnvLaneBytes;
+    const bool live = begin < n;
+    const uint64_t len = !live ? 0 : n - begin < kFnvLaneBytes ? n - begin : kFnvLaneBytes;
+    const bool full = aligned && len == kFnvLaneBytes;
+    const uint8_t* p = data + begin;
+    uint32_t* fault = ctl + 1;
+    uint32_t w[kFnvLaneBytes / 4] = {};
+    if (full) load_segment(p, w);
+    const uint64_t h0 = start_state(seed, seed_dev);
+
+    // bits 0-2: the four machines of run_low3 end in bytes a + 2c; regrouped into the layout the ballots read
+    uint32_t ea = 0, eb = 0;
+    if (live) {
+        const uint32_t x = full ? low3_regs(w) : low3_bytes(p, len);
+        ea = (x & 0xFFu) | (((x >> 8) & 0xFFu) << 16);
+        eb = ((x >> 16) & 0xFFu) | ((x >> 24) << 16);
+    }
+    uint32_t s = resolve_level<3>(ea, eb, 0, g, status, uint32_t(h0) & 7u, fault, L);
+
+    // bits 3-5: four full machines (start bits 3, 4 = 00, 10, 01, 11), bit 5 started at 0
+    ea = eb = 0;
+    if (live) {
+        ea = s | ((s | (1u << 3)) << 16);
+        const uint32_t sc = s | (1u << 4);
+        eb = sc | ((sc | (1u << 3)) << 16);
+        if (full) quad_regs(w, ea, eb);
+        else quad_bytes(p, len, ea, eb);
+    }
+    s |= resolve_level<3>(ea, eb, 3, g, status + stride, uint32_t(h0 >> 3) & 7u, fault, L) << 3;
+
+    // bits 6-7: two machines (start bit 6 = 0, 1), bit 7 started at 0
+    uint32_t mid = 0;
+    ea = 0;
+    if (live) {
+        ea = s | ((s | (1u << 6)) << 16);
+        ea = full ? pair_regs(w, ea, mid) : pair_bytes(p, len, ea);
+    }
+    s |= resolve_level<2>(ea, 0u, 6, g, status + 2 * stride, uint32_t(h0 >> 6) & 3u, fault, L) << 6;
+
+    // the Horner sums.  The low byte at the midpoint is the bits 6-7 machine started from the true bit 6, with bit 7
+    // flipped when the true start bit 7 is 1 (bit 7 of the state is its start value xor terms of the lower bits).
+    uint64_t acc = 0;
+    if (full) {
+        const uint32_t lm = ((((s >> 6) & 1u) ? mid >> 16 : mid) & 0xFFu) ^ (s & 0x80u);
+        // p^(n - r), r the end of the wave's last segment: wave-uniform.  p has order dividing 2^62 modulo 2^64, so
+        // the exponent is taken modulo 2^62 (r passes n in the buffer's last wave)
+        const uint64_t wave_end = ((g * kThreads) + uint64_t(wave) * 64 + 64) * kFnvLaneBytes;
+        const uint64_t wave_pow = pow_prime((n - wave_end) & ((uint64_t(1) << 62) - 1));
+        acc = halves_sum(w, s | (lm << 16)) * kLanePow.v[lane] * wave_pow;
+    } else if (live) {
+        acc = segment_sum(data, n, begin, s);
+    }
+    for (int m = 32; m > 0; m >>= 1) acc += shfl_xor64(acc, m);
+    if (lane == 0) s_sum[wave] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) partial[g] = s_sum[0] + s_sum[1] + s_sum[2] + s_sum[3];
+}
+
+// Clears the status words and the ticket and fault words before a launch (a kernel rather than a memset, so a graph
+// may hold it).
+__global__ void __launch_bounds__(kThreads) fnv_onepass_init_kernel(uint32_t* status, uint64_t words, uint32_t* ctl) {
+    const uint64_t stride = uint64_t(gridDim.x) * kThreads;
+    for (uint64_t i = uint64_t(blockIdx.x) * kThreads + threadIdx.x; i < words; i += stride) status[i] = 0u;
+    if (blockIdx.x == 0 && threadIdx.x < 2) ctl[threadIdx.x] = 0u;
+}
 }  // namespace
 
-// Workspace: [start bytes: one per segment][ballot words T, U0, U1, W00..W11: two sets (this pass, the previous)]
-// [summaries][workgroup start states: two sets][partial sums].
+// Workspace: [ticket and fault words][status words: three levels of `stride` words][partial sums].
 FnvWorkspace fnv_workspace(uint64_t n) {
     FnvWorkspace w{};
     w.segments = (n + kFnvLaneBytes - 1) / kFnvLaneBytes;
     w.groups = (w.segments + kThreads - 1) / kThreads;
     auto up = [](uint64_t x) { return (x + 255) / 256 * 256; };
-    w.off_start = 0;
-    w.off_word0 = up(w.segments);
-    w.off_word1 = w.off_word0 + kMaxPassWords * up(w.groups * 4 * 8);
-    w.off_parity = w.off_word1 + kMaxPassWords * up(w.groups * 4 * 8);   // summaries
-    w.off_prefix = w.off_parity + up(w.groups);               // start states, two sets
-    w.off_partial = w.off_prefix + 2 * up(w.groups);
+    w.off_ctl = 0;
+    w.off_status = 256;
+    w.stride = up(w.groups * 4) / 4;
+    w.off_partial = w.off_status + 3 * w.stride * 4;
     w.bytes = w.off_partial + up(w.groups * 8 > 8 ? w.groups * 8 : 8);
     return w;
 }
@@ -650,38 +596,20 @@ hipError_t launch_fnv1a64(const void* data, uint64_t n, uint64_t seed, const uin
     uint8_t* ws = static_cast<uint8_t*>(workspace);
     const uint8_t* src = static_cast<const uint8_t*>(data);
     const bool aligned = (reinterpret_cast<uintptr_t>(data) & 15u) == 0;
-    const uint64_t word_bytes = (w.off_word1 - w.off_word0) / kMaxPassWords;
-    auto words = [&](uint64_t off) {
-        PassWords p{};
-        for (int k = 0; k < kMaxPassWords; ++k) p.w[k] = reinterpret_cast<uint64_t*>(ws + off + k * word_bytes);
-        return p;
-    };
-    const PassWords set[2] = {words(w.off_word0), words(w.off_word1)};
-    uint8_t* start = ws + w.off_start;
-    uint8_t* summary = ws + w.off_parity;
-    const uint64_t half = (w.off_partial - w.off_prefix) / 2;
-    uint8_t* gstate[2] = {ws + w.off_prefix, ws + w.off_prefix + half};
+    uint32_t* ctl = reinterpret_cast<uint32_t*>(ws + w.off_ctl);
+    uint32_t* status = reinterpret_cast<uint32_t*>(ws + w.off_status);
     uint64_t* partial = reinterpret_cast<uint64_t*>(ws + w.off_partial);
-    const uint64_t final_groups = (w.groups + 1) / 2;   // the final pass takes two of the passes' workgroups each
     if (w.groups > 0) {
-        // bits 0-2, then 3-5 (four machines per lane), then 6-7 (two): three reads of the data before the final one;
-        // each pass reads the previous pass's ballots and workgroup states
-        const dim3 grid(unsigned(w.groups)), block(kThreads), one(1), scan(kScanThreads);
-        hipLaunchKernelGGL((fnv_pass_kernel<3, 0>), grid, block, 0, stream, src, n, 0, aligned, start, set[1],
-                           gstate[1], set[0], summary);
-        hipLaunchKernelGGL(fnv_scan_kernel<3>, one, scan, 0, stream, summary, w.groups, 0, seed, seed_dev, gstate[0]);
-        hipLaunchKernelGGL((fnv_pass_kernel<3, 3>), grid, block, 0, stream, src, n, 3, aligned, start, set[0],
-                           gstate[0], set[1], summary);
-        hipLaunchKernelGGL(fnv_scan_kernel<3>, one, scan, 0, stream, summary, w.groups, 3, seed, seed_dev, gstate[1]);
-        hipLaunchKernelGGL((fnv_pass_kernel<2, 3>), grid, block, 0, stream, src, n, 6, aligned, start, set[1],
-                           gstate[1], set[0], summary);
-        hipLaunchKernelGGL(fnv_scan_kernel<2>, one, scan, 0, stream, summary, w.groups, 6, seed, seed_dev, gstate[0]);
-        hipLaunchKernelGGL(fnv_final_kernel, dim3(unsigned(final_groups)), block, 0, stream, src, n, w.groups, aligned,
-                           start, set[0], gstate[0], partial);
+        const uint64_t words = 3 * w.stride;
+        const uint64_t init_blocks = (words + kThreads - 1) / kThreads < 1024 ? (words + kThreads - 1) / kThreads : 1024;
+        hipLaunchKernelGGL(fnv_onepass_init_kernel, dim3(unsigned(init_blocks)), dim3(kThreads), 0, stream, status, words,
+                           ctl);
+        hipLaunchKernelGGL(fnv_onepass_kernel, dim3(unsigned(w.groups)), dim3(kThreads), 0, stream, src, n, aligned, seed,
+                           seed_dev, status, w.stride, ctl, partial);
     }
     // the reduce reads the start state before it writes `out`, so `out` may be `seed_dev` itself
-    hipLaunchKernelGGL(fnv_reduce_kernel, dim3(1), dim3(kScanThreads), 0, stream, partial, final_groups, seed, seed_dev,
-                       n, out, expected, verdict);
+    hipLaunchKernelGGL(fnv_reduce_kernel, dim3(1), dim3(kScanThreads), 0, stream, partial, w.groups, seed, seed_dev, n,
+                       out, expected, verdict, w.groups > 0 ? ctl + 1 : nullptr);
     return hipGetLastError();
 }
 
@@ -690,12 +618,13 @@ hipError_t launch_fnv1a64(const void* data, uint64_t n, uint64_t seed, const uin
 // ---- the hash that allocates nothing ----------------------------------------------------------------------------------
 // For callers that cannot allocate (code under HIP graph capture, tight serving loops): the workspace is `scratch`, one
 // array per GPU that the library holds until the process ends, sized for inputs of up to SC_FNV_NOALLOC_MAX_BYTES
-// (fnv_workspace(4 GiB) is 44.7 MiB).  Its kernels write every workspace word they later read, so nothing in it is
-// cleared between calls; a call after another on the same stream is ordered after it, and calls that overlap on one
-// GPU (on different streams) race on the one array.
+// (fnv_workspace(4 GiB) is 1.25 MiB).  Every call clears the words that must start at zero (the ticket, the fault word
+// and the look-back's status words) with a kernel of its own before the hash kernel, and writes the partial sums
+// before it reads them; a call after another on the same stream is ordered after it, and calls that overlap on one GPU
+// (on different streams) race on the one array.
 namespace {
 
-constexpr uint64_t kScratchBytes = 48ull << 20;
+constexpr uint64_t kScratchBytes = 2ull << 20;
 static __device__ __align__(256) uint8_t scratch[kScratchBytes];
 
 constexpr int kMaxDevices = 64;
