@@ -42,7 +42,6 @@ namespace {
 
 constexpr uint64_t kFnvPrime = 1099511628211ull;
 constexpr uint32_t kPrimeLow = 179u;   // kFnvPrime mod 256
-constexpr int kScanThreads = 1024;
 
 using u32x4 = __attribute__((ext_vector_type(4))) uint32_t;
 using gu32x4 = __attribute__((address_space(1))) u32x4;
@@ -293,27 +292,15 @@ __device__ __forceinline__ uint64_t segment_sum(const uint8_t* data, uint64_t n,
     return acc * pow_prime(n - begin - len);
 }
 
-// h = seed * p^n + sum of the partial sums (mod 2^64; the order of the additions does not matter).  With `verdict`,
-// also 1 there when h equals `expected`, else 0: a later kernel on the stream can act on the check without a host
-// round trip.
-__global__ void __launch_bounds__(kScanThreads) fnv_reduce_kernel(const uint64_t* partial, uint64_t groups, uint64_t seed,
-                                                                   const uint64_t* seed_dev, uint64_t n, uint64_t* out,
-                                                                   uint64_t expected, uint32_t* verdict,
-                                                                   const uint32_t* fault) {
-    uint64_t acc = 0;
-    for (uint64_t i = threadIdx.x; i < groups; i += kScanThreads) acc += partial[i];
-    for (int m = 32; m > 0; m >>= 1) acc += shfl_xor64(acc, m);
-    __shared__ uint64_t s_sum[kScanThreads / 64];
-    if ((threadIdx.x & 63) == 0) s_sum[threadIdx.x >> 6] = acc;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        uint64_t h = start_state(seed, seed_dev) * pow_prime(n);
-        for (int w = 0; w < kScanThreads / 64; ++w) h += s_sum[w];
-        out[0] = h;
-        if (verdict) verdict[0] = h == expected && !(fault && fault[0]) ? 1u : 0u;
-    }
+// h = seed * p^n + the sum of the workgroups' sums (mod 2^64; the order of the additions does not matter), `acc` being
+// that sum, or null for an empty input.  With `verdict`, also 1 there when h equals `expected` and no wait of the
+// launch ran out, else 0: a later kernel on the stream can act on the check without a host round trip.
+__global__ void fnv_finish_kernel(const uint64_t* acc, uint64_t seed, const uint64_t* seed_dev, uint64_t n, uint64_t* out,
+                                  uint64_t expected, uint32_t* verdict, const uint32_t* fault) {
+    const uint64_t h = start_state(seed, seed_dev) * pow_prime(n) + (acc ? acc[0] : 0u);
+    out[0] = h;
+    if (verdict) verdict[0] = h == expected && !(fault && fault[0]) ? 1u : 0u;
 }
-
 
 // ---- the one-pass hash ---------------------------------------------------------------------------------------------
 // One kernel reads the input once: each lane keeps its 256-byte segment in registers through the three levels of the
@@ -497,11 +484,11 @@ __device__ __forceinline__ uint32_t pair_regs(const uint32_t (&w)[kFnvLaneBytes 
     return x;
 }
 
-// status: three arrays of `stride` words (one per level); ctl: [0] the ticket counter, [1] the fault word.
+// status: three arrays of `stride` words (one per level); ctl: [0] the ticket counter, [1] the fault word, [2..3] the
+// sum of the workgroups' sums (each workgroup adds its own with one 64-bit atomic).
 __global__ void __launch_bounds__(kThreads) fnv_onepass_kernel(const uint8_t* data, uint64_t n, bool aligned,
                                                                 uint64_t seed, const uint64_t* seed_dev,
-                                                                uint32_t* status, uint64_t stride, uint32_t* ctl,
-                                                                uint64_t* partial) {
+                                                                uint32_t* status, uint64_t stride, uint32_t* ctl) {
     __shared__ LevelLds L;
     __shared__ uint32_t s_ticket;
     __shared__ uint64_t s_sum[kThreads / 64];
@@ -564,19 +551,21 @@ __global__ void __launch_bounds__(kThreads) fnv_onepass_kernel(const uint8_t* da
     for (int m = 32; m > 0; m >>= 1) acc += shfl_xor64(acc, m);
     if (lane == 0) s_sum[wave] = acc;
     __syncthreads();
-    if (threadIdx.x == 0) partial[g] = s_sum[0] + s_sum[1] + s_sum[2] + s_sum[3];
+    if (threadIdx.x == 0)
+        atomicAdd(reinterpret_cast<unsigned long long*>(ctl + 2),
+                  (unsigned long long) (s_sum[0] + s_sum[1] + s_sum[2] + s_sum[3]));
 }
 
-// Clears the status words and the ticket and fault words before a launch (a kernel rather than a memset, so a graph
-// may hold it).
+// Clears the status words, the ticket and fault words and the sum before a launch (a kernel rather than a memset, so a
+// graph may hold it).
 __global__ void __launch_bounds__(kThreads) fnv_onepass_init_kernel(uint32_t* status, uint64_t words, uint32_t* ctl) {
     const uint64_t stride = uint64_t(gridDim.x) * kThreads;
     for (uint64_t i = uint64_t(blockIdx.x) * kThreads + threadIdx.x; i < words; i += stride) status[i] = 0u;
-    if (blockIdx.x == 0 && threadIdx.x < 2) ctl[threadIdx.x] = 0u;
+    if (blockIdx.x == 0 && threadIdx.x < 4) ctl[threadIdx.x] = 0u;
 }
 }  // namespace
 
-// Workspace: [ticket and fault words][status words: three levels of `stride` words][partial sums].
+// Workspace: [ticket, fault and sum words][status words: three levels of `stride` words].
 FnvWorkspace fnv_workspace(uint64_t n) {
     FnvWorkspace w{};
     w.segments = (n + kFnvLaneBytes - 1) / kFnvLaneBytes;
@@ -585,8 +574,7 @@ FnvWorkspace fnv_workspace(uint64_t n) {
     w.off_ctl = 0;
     w.off_status = 256;
     w.stride = up(w.groups * 4) / 4;
-    w.off_partial = w.off_status + 3 * w.stride * 4;
-    w.bytes = w.off_partial + up(w.groups * 8 > 8 ? w.groups * 8 : 8);
+    w.bytes = w.off_status + 3 * w.stride * 4;
     return w;
 }
 
@@ -598,18 +586,18 @@ hipError_t launch_fnv1a64(const void* data, uint64_t n, uint64_t seed, const uin
     const bool aligned = (reinterpret_cast<uintptr_t>(data) & 15u) == 0;
     uint32_t* ctl = reinterpret_cast<uint32_t*>(ws + w.off_ctl);
     uint32_t* status = reinterpret_cast<uint32_t*>(ws + w.off_status);
-    uint64_t* partial = reinterpret_cast<uint64_t*>(ws + w.off_partial);
     if (w.groups > 0) {
         const uint64_t words = 3 * w.stride;
         const uint64_t init_blocks = (words + kThreads - 1) / kThreads < 1024 ? (words + kThreads - 1) / kThreads : 1024;
         hipLaunchKernelGGL(fnv_onepass_init_kernel, dim3(unsigned(init_blocks)), dim3(kThreads), 0, stream, status, words,
                            ctl);
         hipLaunchKernelGGL(fnv_onepass_kernel, dim3(unsigned(w.groups)), dim3(kThreads), 0, stream, src, n, aligned, seed,
-                           seed_dev, status, w.stride, ctl, partial);
+                           seed_dev, status, w.stride, ctl);
     }
-    // the reduce reads the start state before it writes `out`, so `out` may be `seed_dev` itself
-    hipLaunchKernelGGL(fnv_reduce_kernel, dim3(1), dim3(kScanThreads), 0, stream, partial, w.groups, seed, seed_dev, n,
-                       out, expected, verdict, w.groups > 0 ? ctl + 1 : nullptr);
+    // the finish reads the start state before it writes `out`, so `out` may be `seed_dev` itself
+    const bool any = w.groups > 0;
+    hipLaunchKernelGGL(fnv_finish_kernel, dim3(1), dim3(1), 0, stream, any ? reinterpret_cast<const uint64_t*>(ctl + 2) : nullptr,
+                       seed, seed_dev, n, out, expected, verdict, any ? ctl + 1 : nullptr);
     return hipGetLastError();
 }
 
@@ -618,10 +606,9 @@ hipError_t launch_fnv1a64(const void* data, uint64_t n, uint64_t seed, const uin
 // ---- the hash that allocates nothing ----------------------------------------------------------------------------------
 // For callers that cannot allocate (code under HIP graph capture, tight serving loops): the workspace is `scratch`, one
 // array per GPU that the library holds until the process ends, sized for inputs of up to SC_FNV_NOALLOC_MAX_BYTES
-// (fnv_workspace(4 GiB) is 1.25 MiB).  Every call clears the words that must start at zero (the ticket, the fault word
-// and the look-back's status words) with a kernel of its own before the hash kernel, and writes the partial sums
-// before it reads them; a call after another on the same stream is ordered after it, and calls that overlap on one GPU
-// (on different streams) race on the one array.
+// (fnv_workspace(4 GiB) is 0.75 MiB).  Every call clears all of it that it uses (the ticket, the fault word, the sum
+// and the look-back's status words) with a kernel of its own before the hash kernel; a call after another on the same
+// stream is ordered after it, and calls that overlap on one GPU (on different streams) race on the one array.
 namespace {
 
 constexpr uint64_t kScratchBytes = 2ull << 20;

@@ -190,7 +190,7 @@ struct PagedImage {
 constexpr int kFnvLaneBytes = 256;
 struct FnvWorkspace {
     uint64_t segments = 0, groups = 0;
-    uint64_t off_ctl = 0, off_status = 0, stride = 0, off_partial = 0;   // stride: status words per level
+    uint64_t off_ctl = 0, off_status = 0, stride = 0;   // stride: status words per level
     uint64_t bytes = 0;
 };
 FnvWorkspace fnv_workspace(uint64_t n);
