@@ -446,10 +446,16 @@ int sc_fnv1a64_device(const void* data, uint64_t bytes, uint64_t seed, uint64_t*
  * for callers that cannot allocate (code under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc).  The workspace is a static device array the library holds on each GPU until the process ends, sized for
  * inputs of at most SC_FNV_NOALLOC_MAX_BYTES (larger inputs are refused with SC_ERANGE before anything is enqueued).
- * It keeps the last call's contents and needs no clearing.  Calls ordered on one stream are safe; calls that overlap
- * on one GPU (on different streams) race on the shared array and must not be issued. */
+ * Each call clears what it uses of the array with a kernel of its own first.  Calls ordered on one stream are safe;
+ * calls that overlap on one GPU (on different streams) race on the shared array and must not be issued. */
 #define SC_FNV_NOALLOC_MAX_BYTES (4ull << 30)
 int sc_fnv1a64_noalloc_async(const void* data, uint64_t bytes, uint64_t seed, uint64_t* out, void* stream);
+/* The bound on each of the hash kernel's look-back waits, in reads of its window (0 restores the default, 65536, about
+ * 0.1 s).  No counterpart in the reference: a workgroup only waits on workgroups that are running or done, so a
+ * correct launch never reaches the bound; tests lower it to force a wait to run out, which must fail the verdict of
+ * sc_fnv1a64_check_async (the launch still ends, and the hash is not to be used).  Applies to launches enqueued
+ * after the call, in this process. */
+int sc_fnv1a64_set_spin_limit(uint32_t reads);
 
 /* ---- runtime plumbing the C++ host layer calls instead of HIP ---------------------------------------------------- */
 

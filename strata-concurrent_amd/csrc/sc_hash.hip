@@ -31,6 +31,7 @@
 // kernel that reads the input once (the one-pass hash, below).
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cstdint>
 #include <mutex>
 
@@ -312,7 +313,7 @@ __global__ void fnv_finish_kernel(const uint64_t* acc, uint64_t seed, const uint
 // also bounded (kSpinLimit reads), after which the launch records a fault that fails the verdict and the workgroup
 // publishes an end state anyway, so no other workgroup waits on it.
 constexpr uint32_t kHasMap = 1u << 8, kHasState = 1u << 9;   // a status word: 0, kHasMap | map, kHasState | state
-constexpr uint32_t kSpinLimit = 1u << 16;   // reads of one window, about 0.1 s
+constexpr uint32_t kSpinLimit = 1u << 16;   // reads of one window, about 0.1 s (sc_fnv1a64_set_spin_limit)
 
 __device__ __forceinline__ void publish(uint32_t* word, uint32_t v) {
     __hip_atomic_store(word, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -326,7 +327,8 @@ __device__ __forceinline__ uint32_t peek(uint32_t* word) {
 // workgroup top - l.  The maps of lanes 0..l compose in one inclusive scan across the wave (six shuffle steps), so
 // resolving a window costs the same wherever its nearest end state lies.
 template <int kBits>
-__device__ __forceinline__ uint32_t look_back(uint32_t* status, uint64_t g, uint32_t map, uint32_t init, uint32_t* fault) {
+__device__ __forceinline__ uint32_t look_back(uint32_t* status, uint64_t g, uint32_t map, uint32_t init, uint32_t* fault,
+                                              uint32_t spin_limit) {
     const int lane = threadIdx.x & 63;
     if (g == 0) {
         if (lane == 0) publish(status, kHasState | apply<kBits>(map, init));
@@ -344,7 +346,7 @@ __device__ __forceinline__ uint32_t look_back(uint32_t* status, uint64_t g, uint
         const int first = have_state ? __builtin_ctzll(have_state) : 64;   // the lane of the nearest end state
         const uint64_t need = first == 64 ? ~0ull : (1ull << first) - 1ull;
         if ((ready & need) != need) {   // a workgroup between g and that end state has not published its map yet
-            if (++spins > kSpinLimit) {   // never in a correct launch; successors still get an end state
+            if (++spins > spin_limit) {   // never in a correct launch; successors still get an end state
                 if (lane == 0) {
                     publish(fault, 1u);
                     publish(status + g, kHasState | apply<kBits>(map, 0u));
@@ -389,7 +391,7 @@ __device__ __forceinline__ uint64_t uniform64(uint64_t v) {
 // back for the workgroup's start state, and returns this lane's start bits of the level (bit 0 upward).
 template <int kBits>
 __device__ __forceinline__ uint32_t resolve_level(uint32_t ea, uint32_t eb, int j, uint64_t g, uint32_t* status, uint32_t init,
-                                  uint32_t* fault, LevelLds& L) {
+                                                  uint32_t* fault, uint32_t spin_limit, LevelLds& L) {
     uint64_t bw[kMaxLevelWords] = {};
     bw[0] = __ballot((ea >> j) & 1u);
     bw[1] = __ballot((ea >> (j + 1)) & 1u);
@@ -421,7 +423,7 @@ __device__ __forceinline__ uint32_t resolve_level(uint32_t ea, uint32_t eb, int 
     if (wave == 0) {
         uint32_t sum = L.map[0];
         for (int k = 1; k < kThreads / 64; ++k) sum = compose<kBits>(L.map[k], sum);
-        const uint32_t st = look_back<kBits>(status, g, __builtin_amdgcn_readfirstlane(sum), init, fault);
+        const uint32_t st = look_back<kBits>(status, g, __builtin_amdgcn_readfirstlane(sum), init, fault, spin_limit);
         if (lane == 0) L.state = st;
     }
     __syncthreads();
@@ -488,7 +490,8 @@ __device__ __forceinline__ uint32_t pair_regs(const uint32_t (&w)[kFnvLaneBytes 
 // sum of the workgroups' sums (each workgroup adds its own with one 64-bit atomic).
 __global__ void __launch_bounds__(kThreads) fnv_onepass_kernel(const uint8_t* data, uint64_t n, bool aligned,
                                                                 uint64_t seed, const uint64_t* seed_dev,
-                                                                uint32_t* status, uint64_t stride, uint32_t* ctl) {
+                                                                uint32_t* status, uint64_t stride, uint32_t* ctl,
+                                                                uint32_t spin_limit) {
     __shared__ LevelLds L;
     __shared__ uint32_t s_ticket;
     __shared__ uint64_t s_sum[kThreads / 64];
@@ -513,7 +516,7 @@ __global__ void __launch_bounds__(kThreads) fnv_onepass_kernel(const uint8_t* da
         ea = (x & 0xFFu) | (((x >> 8) & 0xFFu) << 16);
         eb = ((x >> 16) & 0xFFu) | ((x >> 24) << 16);
     }
-    uint32_t s = resolve_level<3>(ea, eb, 0, g, status, uint32_t(h0) & 7u, fault, L);
+    uint32_t s = resolve_level<3>(ea, eb, 0, g, status, uint32_t(h0) & 7u, fault, spin_limit, L);
 
     // bits 3-5: four full machines (start bits 3, 4 = 00, 10, 01, 11), bit 5 started at 0
     ea = eb = 0;
@@ -524,7 +527,7 @@ __global__ void __launch_bounds__(kThreads) fnv_onepass_kernel(const uint8_t* da
         if (full) quad_regs(w, ea, eb);
         else quad_bytes(p, len, ea, eb);
     }
-    s |= resolve_level<3>(ea, eb, 3, g, status + stride, uint32_t(h0 >> 3) & 7u, fault, L) << 3;
+    s |= resolve_level<3>(ea, eb, 3, g, status + stride, uint32_t(h0 >> 3) & 7u, fault, spin_limit, L) << 3;
 
     // bits 6-7: two machines (start bit 6 = 0, 1), bit 7 started at 0
     uint32_t mid = 0;
@@ -533,7 +536,7 @@ __global__ void __launch_bounds__(kThreads) fnv_onepass_kernel(const uint8_t* da
         ea = s | ((s | (1u << 6)) << 16);
         ea = full ? pair_regs(w, ea, mid) : pair_bytes(p, len, ea);
     }
-    s |= resolve_level<2>(ea, 0u, 6, g, status + 2 * stride, uint32_t(h0 >> 6) & 3u, fault, L) << 6;
+    s |= resolve_level<2>(ea, 0u, 6, g, status + 2 * stride, uint32_t(h0 >> 6) & 3u, fault, spin_limit, L) << 6;
 
     // the Horner sums.  The low byte at the midpoint is the bits 6-7 machine started from the true bit 6, with bit 7
     // flipped when the true start bit 7 is 1 (bit 7 of the state is its start value xor terms of the lower bits).
@@ -565,6 +568,9 @@ __global__ void __launch_bounds__(kThreads) fnv_onepass_init_kernel(uint32_t* st
 }
 }  // namespace
 
+// The bound on each look-back wait, in window reads; tests lower it to force a wait to run out.
+std::atomic<uint32_t> g_spin_limit{kSpinLimit};
+
 // Workspace: [ticket, fault and sum words][status words: three levels of `stride` words].
 FnvWorkspace fnv_workspace(uint64_t n) {
     FnvWorkspace w{};
@@ -592,7 +598,7 @@ hipError_t launch_fnv1a64(const void* data, uint64_t n, uint64_t seed, const uin
         hipLaunchKernelGGL(fnv_onepass_init_kernel, dim3(unsigned(init_blocks)), dim3(kThreads), 0, stream, status, words,
                            ctl);
         hipLaunchKernelGGL(fnv_onepass_kernel, dim3(unsigned(w.groups)), dim3(kThreads), 0, stream, src, n, aligned, seed,
-                           seed_dev, status, w.stride, ctl);
+                           seed_dev, status, w.stride, ctl, g_spin_limit.load());
     }
     // the finish reads the start state before it writes `out`, so `out` may be `seed_dev` itself
     const bool any = w.groups > 0;
@@ -650,5 +656,10 @@ extern "C" int sc_fnv1a64_noalloc_async(const void* data, uint64_t bytes, uint64
         return sc::record_error(SC_EHIP, std::string("sc_handoff hash scratch: ") + hipGetErrorString(e));
     e = sc::launch_fnv1a64(data, bytes, seed, nullptr, out, ws, static_cast<hipStream_t>(stream), 0, nullptr);
     if (e != hipSuccess) return sc::record_error(SC_EHIP, std::string("sc_handoff hash launch: ") + hipGetErrorString(e));
+    return sc::record_ok();
+}
+
+extern "C" int sc_fnv1a64_set_spin_limit(uint32_t reads) {
+    sc::g_spin_limit.store(reads ? reads : sc::kSpinLimit);
     return sc::record_ok();
 }

@@ -199,6 +199,7 @@ _SIGS = {
     "sc_fnv1a64_check_async": (C.c_int, [_P, _U64, _U64, _U64, _P, _P, _P, _U64, _P]),
     "sc_fnv1a64_device": (C.c_int, [_P, _U64, _U64, C.POINTER(_U64)]),
     "sc_fnv1a64_noalloc_async": (C.c_int, [_P, _U64, _U64, _P, _P]),
+    "sc_fnv1a64_set_spin_limit": (C.c_int, [C.c_uint32]),
     "sc_copy_device_async": (C.c_int, [_P, _P, _U64, _P]),
     "sc_ipc_export_create": (C.c_int, [_U64, _U64, C.POINTER(_P)]),
     "sc_ipc_export_count": (C.c_int32, [_P]),

@@ -133,6 +133,39 @@ def test_full_payload_size(sc, oracle, cuda):
     buf.free()
 
 
+def test_a_look_back_wait_that_runs_out_fails_the_verdict(sc, oracle, cuda):
+    """The hash kernel's waits on earlier workgroups are bounded.  With the bound forced down to one read, waits run
+    out (thousands of workgroups start together, and most cannot find their start state on their first reads): the
+    launch still ends, and the verdict is 0 even though the expected hash is the true one.  With the default bound
+    the same check passes."""
+    n = 256 << 20
+    buf = sc.DeviceBuffer(n, "uint8")
+    sc.lib.sc_fill_uniform_f16(buf.ptr, n // 2, -4.0, 4.0, 0x5EED, 91, None)
+    sc.device_sync()
+    host = sc.PinnedBuffer(n)
+    sc.check(sc.lib.sc_copy_async(host.ptr, buf.ptr, n, None), "copy")
+    sc.device_sync()
+    want = oracle.fnv1a64(host.numpy(), sc.REFERENCE_FNV_SEED)
+    hp = sc.HashPlan(n)
+    verdict = sc.DeviceBuffer(1, "uint32")
+    try:
+        for limit, passes in ((1, False), (0, True)):
+            sc.check(sc.lib.sc_fnv1a64_set_spin_limit(limit), "spin limit")
+            verdict.fill(0xAB)
+            sc.check(sc.lib.sc_fnv1a64_check_async(buf.ptr, n, sc.REFERENCE_FNV_SEED, want, hp.out.ptr, verdict.ptr,
+                                                   hp.ws.ptr, hp.ws_bytes, None), "check")
+            sc.device_sync()
+            print(f"case spin limit {limit}: verdict {int(verdict.numpy()[0])}", flush=True)
+            assert int(verdict.numpy()[0]) == (1 if passes else 0)
+            if passes:
+                assert hp.result() == want
+    finally:
+        sc.check(sc.lib.sc_fnv1a64_set_spin_limit(0), "spin limit")
+        for b in (buf, host, verdict):
+            b.free()
+        hp.free()
+
+
 def test_gated_scatter_writes_all_or_nothing(sc, oracle, cuda):
     """sc_fnv1a64_check_async leaves a verdict on the device and sc_plan_launch_gated scatters only when it is 1: a
     wrong expected hash leaves the slot untouched, the right one mounts it, with no host round trip in between."""
