@@ -53,6 +53,16 @@ __device__ __forceinline__ void st16(uint8_t* p, u32x4 v) { __builtin_nontempora
 __device__ u32x4 g_zero_chunks[2];
 __device__ __forceinline__ const uint8_t* zero_chunks() { return reinterpret_cast<const uint8_t*>(g_zero_chunks); }
 
+// The tile a workgroup starts on.  Workgroups are dispatched to the part's eight XCDs in turn (workgroup b to XCD
+// b mod 8), each XCD with its own L2; numbering the tiles so that each XCD takes one contiguous eighth of them, in
+// order, measured faster than tile b on workgroup b for the identity carve: 128K 1.066-1.075 against 1.088-1.118 ms.
+// The host chooses it per plan (sc_plan::xcd).  Any numbering is correct (this one is a permutation of 0 .. n - 1);
+// only the speed depends on the dispatch order.
+__device__ __forceinline__ uint64_t xcd_tile(uint32_t b, uint32_t n) {
+    const uint32_t q = n / 8, r = n % 8, x = b % 8;
+    return uint64_t(x) * q + (x < r ? x : r) + b / 8;
+}
+
 // Page tables are read through global loads.  Every tile issues all of its loads, table entries included, before
 // its first store: a table load placed after a store (which might alias the table) waits for it, and the
 // per-chunk load -> store chains that result measured 10-14% slower on the 128K handoff through a page table.
@@ -528,7 +538,7 @@ template <int kMix>
 __global__ void __launch_bounds__(kThreads)
 __attribute__((amdgpu_waves_per_eu(kMix == kMixAll ? 5 : 6)))
 sc_move_kernel(const MoveRow* __restrict__ rows, const uint16_t* __restrict__ tile_row, MoveGeo geo, uint64_t n_tiles,
-               const uint32_t* __restrict__ gate) {
+               const uint32_t* __restrict__ gate, bool xcd) {
     // A gated launch moves nothing unless the word a kernel before it on the stream left at `gate` is nonzero (a
     // payload hash that matched): every workgroup reads the same word, so the launch writes all or nothing.
     if (gate && __builtin_amdgcn_readfirstlane(*gate) == 0u) return;
@@ -536,7 +546,9 @@ sc_move_kernel(const MoveRow* __restrict__ rows, const uint16_t* __restrict__ ti
     const bool wave_pages = geo.page_chunks.d % 64u == 0u;
     int cur = -1;
     MoveRow r{};
-    for (uint64_t tile = blockIdx.x; tile < n_tiles; tile += gridDim.x) {
+    // `xcd`: the plan numbers its tiles by XCD (plain plans without page tables; the host decides)
+    const uint64_t first = xcd ? xcd_tile(blockIdx.x, gridDim.x) : uint64_t(blockIdx.x);
+    for (uint64_t tile = first; tile < n_tiles; tile += gridDim.x) {
         using cu32 = __attribute__((address_space(4))) const uint32_t;
         const uint32_t pair = *((cu32*) tile_row + (tile >> 1));
         const int k = int((tile & 1) ? pair >> 16 : pair & 0xFFFFu);
@@ -1014,22 +1026,22 @@ hipError_t launch_ring_table(int32_t* table, int64_t n_blocks, int64_t n_slots, 
 }
 
 hipError_t launch_move(const MoveRow* rows, const uint16_t* tile_row, const MoveGeo& geo, uint64_t n_tiles,
-                       int64_t grid, int32_t mix, hipStream_t stream, const uint32_t* gate) {
+                       int64_t grid, int32_t mix, bool xcd, hipStream_t stream, const uint32_t* gate) {
     if (n_tiles == 0) return hipSuccess;
     if (!rows || !tile_row || grid <= 0 || mix < kMixPlain || mix > kMixAll) return hipErrorInvalidValue;
     const dim3 blocks(unsigned(uint64_t(grid) < n_tiles ? uint64_t(grid) : n_tiles)), threads(kThreads);
     switch (mix) {
         case kMixPlain:
-            hipLaunchKernelGGL(sc_move_kernel<kMixPlain>, blocks, threads, 0, stream, rows, tile_row, geo, n_tiles, gate);
+            hipLaunchKernelGGL(sc_move_kernel<kMixPlain>, blocks, threads, 0, stream, rows, tile_row, geo, n_tiles, gate, xcd);
             break;
         case kMixWide:
-            hipLaunchKernelGGL(sc_move_kernel<kMixWide>, blocks, threads, 0, stream, rows, tile_row, geo, n_tiles, gate);
+            hipLaunchKernelGGL(sc_move_kernel<kMixWide>, blocks, threads, 0, stream, rows, tile_row, geo, n_tiles, gate, xcd);
             break;
         case kMixQuant:
-            hipLaunchKernelGGL(sc_move_kernel<kMixQuant>, blocks, threads, 0, stream, rows, tile_row, geo, n_tiles, gate);
+            hipLaunchKernelGGL(sc_move_kernel<kMixQuant>, blocks, threads, 0, stream, rows, tile_row, geo, n_tiles, gate, xcd);
             break;
         default:
-            hipLaunchKernelGGL(sc_move_kernel<kMixAll>, blocks, threads, 0, stream, rows, tile_row, geo, n_tiles, gate);
+            hipLaunchKernelGGL(sc_move_kernel<kMixAll>, blocks, threads, 0, stream, rows, tile_row, geo, n_tiles, gate, xcd);
             break;
     }
     return hipGetLastError();

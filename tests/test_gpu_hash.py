@@ -23,8 +23,11 @@ def _upload(sc, data: np.ndarray, pad: int = 0):
     return buf
 
 
+# sizes include one workgroup's 64 KiB and the look-back's window of 64 workgroups (4 MiB) with neighbours, so a
+# workgroup's window reaches before the input's start, holds only maps, or starts exactly on a workgroup boundary
 @pytest.mark.parametrize("n", [0, 1, 2, 15, 16, 17, 255, 256, 257, 1000, 4095, 4096, 65535, 65536, 65537,
-                               3 * 65536 + 100, 1 << 20, (1 << 20) + 255, 12_345_679])
+                               3 * 65536 + 100, 1 << 20, (1 << 20) + 255, 64 << 16, (64 << 16) + 1, (65 << 16) + 300,
+                               (129 << 16) - 7, 12_345_679, (257 << 16) + 3])
 def test_device_hash_equals_byte_loop(sc, oracle, cuda, n):
     rng = np.random.default_rng(n)
     data = rng.integers(0, 256, size=n, dtype=np.uint8)
