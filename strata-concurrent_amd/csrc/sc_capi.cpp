@@ -1414,9 +1414,10 @@ int sc_plan_resume_append(const sc_geometry* g, const sc_batch_desc* d, sc_plan*
         const uint64_t slot_pages = uint64_t((d->max_tokens + d->chunk_tokens + o.ps - 1) / o.ps);
         const uint64_t pages = o.n_qsa > 0 ? std::min<uint64_t>(uint64_t(d->arena_pages), slot_pages * uint64_t(d->n_slots))
                                            : 0;
-        const uint64_t kv_tiles = (pages * page_chunks + sc::kTileChunks - 1) / sc::kTileChunks;
-        if (kv_tiles * sc::kTileChunks >= kMaxRowChunks) return fail(SC_ERANGE, "sc_handoff: an arena beyond 2^31 chunks");
-        const uint64_t order_len = (kv_tiles * sc::kTileChunks + page_chunks - 1) / page_chunks;
+        const uint64_t kv_tiles = (pages * page_chunks + sc::kBatchTileChunks - 1) / sc::kBatchTileChunks;
+        if (kv_tiles * sc::kBatchTileChunks >= kMaxRowChunks)
+            return fail(SC_ERANGE, "sc_handoff: an arena beyond 2^31 chunks");
+        const uint64_t order_len = (kv_tiles * sc::kBatchTileChunks + page_chunks - 1) / page_chunks;
         a.kv_tiles = uint32_t(kv_tiles);
         a.kv_tiles_div = sc::make_fastdiv(uint32_t(std::max<uint64_t>(kv_tiles, 1)));
         a.gdn_tiles = uint32_t((a.gdn_bytes / 16 + sc::kTileChunks - 1) / sc::kTileChunks);

@@ -17,8 +17,16 @@ int record_ok();
 int record_error(int code, const std::string& message);
 
 constexpr int kThreads = 256;            // one workgroup = 4 wave64
-constexpr int kChunksPerThread = 4;      // 16-byte chunks in flight per thread per tile
-constexpr int kTileChunks = kThreads * kChunksPerThread;   // 1024 chunks = 16 KiB per tile
+// 16-byte chunks in flight per thread per tile: 8 KiB tiles measured faster than 16 KiB ones for the 128K carve
+// (1.045-1.053 against 1.064-1.074 ms), the paged carve in source order (1.20 against 1.24 ms) and the per-layer f32
+// appends (1.57 against 1.64 ms), alike for the destination-ordered paged carve; 4 KiB (1.26 ms) and 32 KiB (1.11 ms)
+// tiles measured slower.
+constexpr int kChunksPerThread = 2;
+constexpr int kTileChunks = kThreads * kChunksPerThread;   // 512 chunks = 8 KiB per tile
+// The batched resume's page tiles keep 16 KiB (4 pages of 4 KiB): config 5 measured 4.98-5.02 ms with them against
+// 5.08-5.10 ms with 8 KiB tiles.
+constexpr int kBatchChunksPerThread = 4;
+constexpr int kBatchTileChunks = kThreads * kBatchChunksPerThread;
 constexpr int kConvTileChannels = 512;   // channels per conv-history tile (LDS-staged transpose)
 constexpr int kMaxHist = 4;              // d_conv - 1 rows of history the conv tile supports
 
@@ -155,7 +163,7 @@ struct BatchArgs {
     uint32_t* ok;            // 1 when every slot's length is in range and every image fits the staging buffer
     int32_t* inv;            // [arena_pages] arena page -> slot << 25 | logical page; -1 between launches
     const int32_t* order;    // [2 * order_len]: (entry, arena page) pairs in ascending arena order, then -1
-    uint32_t kv_tiles;       // tiles per K/V blob: ceil(order_len pages * page chunks / kTileChunks)
+    uint32_t kv_tiles;       // tiles per K/V blob: ceil(order_len pages * page chunks / kBatchTileChunks)
     FastDiv kv_tiles_div;    // kv_tiles, for the blob of a tile
     uint32_t gdn_tiles;      // tiles per slot's GDN rows
     FastDiv gdn_tiles_div;

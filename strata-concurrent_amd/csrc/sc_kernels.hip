@@ -1,7 +1,7 @@
 // sc_kernels.hip - the CDNA4 (gfx950) kernels of the prefill->decode cache handoff.
 //
 // All of it is data movement, so every kernel here is bounded by HBM bandwidth, not by the matrix cores:
-//   * sc_move_kernel  - walks a handoff table (sc_internal.hpp) in 16 KiB tiles.  Every K/V, recurrence, page
+//   * sc_move_kernel  - walks a handoff table (sc_internal.hpp) in 8 KiB tiles.  Every K/V, recurrence, page
 //                       and copy row moves whole 16-byte chunks: 64 lanes x 16 B = 1 KiB per wave instruction,
 //                       and a 512-byte pool row is one contiguous run on both sides, so both the loads and the
 //                       stores are fully coalesced without LDS.  The conv history is the one real transpose
@@ -667,13 +667,13 @@ __device__ void batch_page_tile(const BatchArgs& a, const BatchSlotsLds& S, uint
     const uint64_t page_bytes = uint64_t(g.page_chunks.d) * 16u, row_bytes = uint64_t(g.row_chunks.d) * 16u;
     const uint64_t* chunks = a.ptrs + 2 * a.n_qsa;
     uint8_t* arena = reinterpret_cast<uint8_t*>(a.ptrs[blob]);
-    u32x4 v[kChunksPerThread];
-    int64_t dst[kChunksPerThread];
+    u32x4 v[kBatchChunksPerThread];
+    int64_t dst[kBatchChunksPerThread];
     using gi64 = __attribute__((address_space(1))) const int64_t;
 #pragma unroll
-    for (int j = 0; j < kChunksPerThread; ++j) {
+    for (int j = 0; j < kBatchChunksPerThread; ++j) {
         dst[j] = -1;
-        const uint32_t vq = w * kTileChunks + uint32_t(j * kThreads) + threadIdx.x;
+        const uint32_t vq = w * kBatchTileChunks + uint32_t(j * kThreads) + threadIdx.x;
         const uint32_t vp = fdiv(vq, g.page_chunks);
         const uint32_t ip = vq - vp * g.page_chunks.d;
         const int64_t pair = *(gi64*) (a.order + 2 * uint64_t(vp));   // (entry, arena page), little-endian
@@ -696,7 +696,7 @@ __device__ void batch_page_tile(const BatchArgs& a, const BatchSlotsLds& S, uint
         dst[j] = int64_t(phys) * int64_t(page_bytes) + int64_t(ip) * 16;
     }
 #pragma unroll
-    for (int j = 0; j < kChunksPerThread; ++j)
+    for (int j = 0; j < kBatchChunksPerThread; ++j)
         if (dst[j] >= 0) st16(arena + dst[j], v[j]);
 }
 
