@@ -451,7 +451,7 @@ int sc_fnv1a64_device(const void* data, uint64_t bytes, uint64_t seed, uint64_t*
 #define SC_FNV_NOALLOC_MAX_BYTES (4ull << 30)
 int sc_fnv1a64_noalloc_async(const void* data, uint64_t bytes, uint64_t seed, uint64_t* out, void* stream);
 /* The bound on each of the hash kernel's look-back waits, in reads of its window (0 restores the default, 65536, about
- * 0.1 s).  No counterpart in the reference: a workgroup only waits on workgroups that are running or done, so a
+ * 0.2 s).  No counterpart in the reference: a workgroup only waits on workgroups that are running or done, so a
  * correct launch never reaches the bound; tests lower it to force a wait to run out, which must fail the verdict of
  * sc_fnv1a64_check_async (the launch still ends, and the hash is not to be used).  Applies to launches enqueued
  * after the call, in this process. */
