@@ -88,7 +88,8 @@ int sc_arena_read_host(sc_arena* arena, int32_t index, uint64_t nonce, uint64_t 
 int sc_mover_create(uint64_t chunk_bytes, int32_t depth, int32_t threads, sc_mover** out);
 int sc_mover_destroy(sc_mover* mover);
 /* `bytes` of device memory into the claimed slot (after the work on `stream`); with `hash` != NULL also the payload's
- * FNV-1a, computed on the device. */
+ * FNV-1a, computed on the device.  SC_ETIMEOUT when that hash did not complete (a bounded wait of its kernel ran out,
+ * sc_fnv1a64_async): the slot holds the bytes, no hash is returned, and nothing is published. */
 int sc_mover_write(sc_mover* mover, sc_arena* arena, const sc_arena_claim* claim, const void* device_src,
                    uint64_t bytes, void* stream, uint64_t* hash);
 /* sc_mover_write with the device hash, then sc_arena_publish. */
@@ -96,7 +97,8 @@ int sc_mover_publish(sc_mover* mover, sc_arena* arena, const sc_arena_claim* cla
                      uint64_t bytes, uint64_t tokens, void* stream);
 /* A READY slot (every check of read_slot) into device memory, re-checked after the copy, and with `verify` its
  * FNV-1a on the device against the slot's record.  Nothing is written to `device_dst` when the slot is refused before
- * the copy. */
+ * the copy.  SC_ETIMEOUT when the device hash did not complete: the destination holds the bytes, unverified, and is
+ * not to be mounted. */
 int sc_mover_read(sc_mover* mover, sc_arena* arena, int32_t index, uint64_t nonce, uint64_t client_id, void* device_dst,
                   uint64_t capacity, void* stream, int32_t verify, sc_arena_slot* out);
 /* The last transfer's host wall-clock time, the part spent on the hash (a verified read), in host copies between

@@ -39,7 +39,9 @@ enum {
     SC_EINVAL = 1,   /* refused before any write */
     SC_EHIP = 2,     /* HIP failure after work may have been enqueued (transfer_failed) */
     SC_ENOMEM = 3,   /* an allocation the call needed failed; nothing was written */
-    SC_ERANGE = 4    /* a size is beyond what the entry point supports; nothing was written */
+    SC_ERANGE = 4,   /* a size is beyond what the entry point supports; nothing was written */
+    /* 5 and 6 are sc_arena.h's SC_EBUSY and SC_ESTALE */
+    SC_ETIMEOUT = 7  /* a bounded wait on the device ran out: the launch ended, its result is not to be used */
 };
 
 enum { SC_DTYPE_F16 = 0, SC_DTYPE_F32 = 1 };
@@ -422,39 +424,51 @@ uint64_t sc_kv_block_bytes(int64_t n_head_kv, int64_t head_dim, int64_t page_siz
  * (conversation_wire.hpp:196). */
 /* Device workspace the asynchronous form needs for `bytes` bytes of input (about bytes / 3000, at least 512 bytes). */
 uint64_t sc_fnv1a64_workspace_bytes(uint64_t bytes);
-/* Enqueue the hash on `stream`; the result lands as one u64 in device memory at `out`.  `data` may have any
- * alignment (16-byte aligned input takes the vector path); `workspace` is 16-byte aligned device memory of at least
- * sc_fnv1a64_workspace_bytes(bytes); nothing is allocated. */
-int sc_fnv1a64_async(const void* data, uint64_t bytes, uint64_t seed, uint64_t* out, void* workspace,
+/* Enqueue the hash on `stream`; the result lands as one u64 at `out`, and the launch's status as one u32 at `fault`:
+ * 0, or 1 when one of the kernel's bounded look-back waits ran out (never in a correct launch on a GPU that runs its
+ * waves; sc_fnv1a64_set_spin_limit forces it), in which case the u64 at `out` is not the hash and must not be used.
+ * `out` and `fault` (required, 4-byte aligned) may be device memory or pinned host memory mapped for the device.
+ * `data` may have any alignment (16-byte aligned input takes the vector path); `workspace` is 16-byte aligned device
+ * memory of at least sc_fnv1a64_workspace_bytes(bytes); nothing is allocated. */
+int sc_fnv1a64_async(const void* data, uint64_t bytes, uint64_t seed, uint64_t* out, uint32_t* fault, void* workspace,
                      uint64_t workspace_bytes, void* stream);
 /* sc_fnv1a64_async that also writes, at `verdict` (4-byte aligned device memory), 1 when the hash equals `expected` and
- * 0 otherwise: the gate of sc_plan_launch_gated. */
+ * no wait ran out, and 0 otherwise: the gate of sc_plan_launch_gated.  `fault` is optional here (NULL: the verdict
+ * alone carries the fault), with the meaning it has in sc_fnv1a64_async. */
 int sc_fnv1a64_check_async(const void* data, uint64_t bytes, uint64_t seed, uint64_t expected, uint64_t* out,
-                           uint32_t* verdict, void* workspace, uint64_t workspace_bytes, void* stream);
+                           uint32_t* verdict, uint32_t* fault, void* workspace, uint64_t workspace_bytes, void* stream);
 /* The same hash continued over one more piece: the running hash is the u64 at `state` in device memory (the seed
  * before the first piece), read when the piece's kernels run on `stream` and replaced by the hash of everything so
  * far.  Hashing a buffer piece by piece in order, each call after the one before it on the same stream, gives the
  * one-shot hash of the whole buffer: fnv1a64 is a left fold, and the reference chains it the same way through its
  * seed argument (src/core/conversation_wire.cpp:135,679-683).  This lets a copy into device memory be verified piece
  * by piece while later pieces are still in flight.  `state` is 8-byte aligned; the workspace rules are those of
- * sc_fnv1a64_async for `bytes`.  Nothing is allocated. */
-int sc_fnv1a64_chain_async(const void* data, uint64_t bytes, uint64_t* state, void* workspace, uint64_t workspace_bytes,
-                           void* stream);
-/* Synchronous convenience: allocates its workspace, runs on the null stream, waits, and returns the hash in *hash. */
+ * sc_fnv1a64_async for `bytes`.  `fault` (required, 4-byte aligned) is sticky across a chain: a piece whose wait ran
+ * out sets it to 1 and a piece without a fault leaves it as it is, so the caller clears it (0) with the seed before
+ * the first piece and reads it with the final state; 1 means the state is not the hash.  Nothing is allocated. */
+int sc_fnv1a64_chain_async(const void* data, uint64_t bytes, uint64_t* state, uint32_t* fault, void* workspace,
+                           uint64_t workspace_bytes, void* stream);
+/* Synchronous convenience: allocates its workspace, runs on the null stream, waits, and returns the hash in *hash
+ * (SC_ETIMEOUT, and *hash untouched, when a wait of the kernel ran out). */
 int sc_fnv1a64_device(const void* data, uint64_t bytes, uint64_t seed, uint64_t* hash);
 /* sc_fnv1a64_async without a workspace argument and without any allocation.  No counterpart in the reference: it is
  * for callers that cannot allocate (code under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc).  The workspace is a static device array the library holds on each GPU until the process ends, sized for
  * inputs of at most SC_FNV_NOALLOC_MAX_BYTES (larger inputs are refused with SC_ERANGE before anything is enqueued).
- * Each call clears what it uses of the array with a kernel of its own first.  Calls ordered on one stream are safe;
- * calls that overlap on one GPU (on different streams) race on the shared array and must not be issued. */
+ * Each call clears what it uses of the array with a kernel of its own first.  `out` and `fault` are as in
+ * sc_fnv1a64_async.  Calls ordered on one stream are safe; calls that overlap on one GPU (on different streams) race
+ * on the shared array and must not be issued. */
 #define SC_FNV_NOALLOC_MAX_BYTES (4ull << 30)
-int sc_fnv1a64_noalloc_async(const void* data, uint64_t bytes, uint64_t seed, uint64_t* out, void* stream);
+int sc_fnv1a64_noalloc_async(const void* data, uint64_t bytes, uint64_t seed, uint64_t* out, uint32_t* fault,
+                             void* stream);
 /* The bound on each of the hash kernel's look-back waits, in reads of its window (0 restores the default, 65536, about
  * 0.2 s).  No counterpart in the reference: a workgroup only waits on workgroups that are running or done, so a
- * correct launch never reaches the bound; tests lower it to force a wait to run out, which must fail the verdict of
- * sc_fnv1a64_check_async (the launch still ends, and the hash is not to be used).  Applies to launches enqueued
- * after the call, in this process. */
+ * correct launch never reaches the bound; tests lower it to force a wait to run out, which must set the fault word of
+ * every form and fail the verdict of sc_fnv1a64_check_async (the launch still ends, and the hash is not to be used).
+ * SC_FNV_FORCE_FAULT makes every wait run out at once (any input past the first workgroup's 64 KiB then faults, which
+ * makes the failure paths of the callers testable deterministically).  Applies to launches enqueued after the call,
+ * in this process. */
+#define SC_FNV_FORCE_FAULT 0xFFFFFFFFu
 int sc_fnv1a64_set_spin_limit(uint32_t reads);
 
 /* ---- runtime plumbing the C++ host layer calls instead of HIP ---------------------------------------------------- */

@@ -82,7 +82,8 @@ uint64_t sc_wire_encoder_pool_offset(const sc_wire_encoder* e);
  * payload byte is in place, before the hash: a park on another stream can wait on it and overlap the hash.  Replaces
  * conversation_wire_encode's walk and byte-serial hash (src/core/conversation_wire.cpp:400-480, 1006-1025). */
 int sc_wire_encode_async(sc_wire_encoder* e, void* payload, uint64_t capacity, void* stream, void* gathered);
-/* The payload hash of the last encode (waits for it): WireEncoded::payload_hash. */
+/* The payload hash of the last encode (waits for it): WireEncoded::payload_hash.  SC_ETIMEOUT, and no hash, when the
+ * device hash did not complete (a bounded wait of its kernel ran out, sc_fnv1a64_async): encode again. */
 int sc_wire_encoder_hash(sc_wire_encoder* e, uint64_t* hash);
 int sc_wire_encoder_destroy(sc_wire_encoder* e);
 
@@ -110,7 +111,8 @@ int sc_wire_decoder_open_layers(const void* payload, uint64_t bytes, const sc_ge
 int64_t sc_wire_decoder_tokens(const sc_wire_decoder* d);
 /* Verifies the payload hash on the device (when asked), then scatters the K/V and GDN rows into the slot in one launch
  * and copies the host-side blobs out.  Synchronous; on a refusal the slot is untouched (the reference's "invalid: no
- * write", include/strata/core/conversation_snapshot.hpp:103-108). */
+ * write", include/strata/core/conversation_snapshot.hpp:103-108): SC_EINVAL for a hash that differs, SC_ETIMEOUT for a
+ * device hash that did not complete (its verdict gated every scatter off, as for a mismatch). */
 int sc_wire_decoder_restore(sc_wire_decoder* d, void* stream);
 /* After a restore: the live checkpoint's ids (n written to *n; needs cap >= tokens) and its small buffers
  * (which: 0 ple, 1 tails, 2 dead, 3 block_pos). */

@@ -44,7 +44,8 @@ hipError_t launch_stream_reset(int32_t* table, int64_t n_blocks, int32_t* slot_b
                                int32_t* slot_ref, int64_t n_slots, int32_t* ctl, hipStream_t stream);
 hipError_t launch_ring_table(int32_t* table, int64_t n_blocks, int64_t n_slots, hipStream_t stream);
 hipError_t launch_fnv1a64(const void* data, uint64_t n, uint64_t seed, const uint64_t* seed_dev, uint64_t* out,
-                          void* workspace, hipStream_t stream, uint64_t expected = 0, uint32_t* verdict = nullptr);
+                          uint32_t* fault_out, void* workspace, hipStream_t stream, uint64_t expected = 0,
+                          uint32_t* verdict = nullptr);
 
 static uint64_t host_mix64(uint64_t z) {
     z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
@@ -1692,41 +1693,43 @@ uint64_t sc_kv_block_bytes(int64_t n_head_kv, int64_t head_dim, int64_t page_siz
 
 uint64_t sc_fnv1a64_workspace_bytes(uint64_t bytes) { return sc::fnv_workspace(bytes).bytes; }
 
-int sc_fnv1a64_async(const void* data, uint64_t bytes, uint64_t seed, uint64_t* out, void* workspace,
-                     uint64_t workspace_bytes, void* stream) {
+// The checks every asynchronous form makes before it enqueues anything.
+static int check_fnv_args(const void* data, uint64_t bytes, const void* out, const uint32_t* fault, bool fault_required,
+                          const void* workspace, uint64_t workspace_bytes) {
     if (!out || (bytes && !data)) return fail(SC_EINVAL, "sc_handoff: missing hash input or output");
+    if (fault_required && !fault) return fail(SC_EINVAL, "sc_handoff: missing hash fault word");
+    if (reinterpret_cast<uintptr_t>(fault) & 3u) return fail(SC_EINVAL, "sc_handoff: the hash fault word must be 4-byte aligned");
     if (!workspace || workspace_bytes < sc::fnv_workspace(bytes).bytes)
         return fail(SC_EINVAL, "sc_handoff: hash workspace smaller than sc_fnv1a64_workspace_bytes()");
     if (reinterpret_cast<uintptr_t>(workspace) & 15u) return fail(SC_EINVAL, "sc_handoff: hash workspace must be 16-byte aligned");
     if (bytes > (uint64_t(1) << 46)) return fail(SC_ERANGE, "sc_handoff: hash input beyond 2^46 bytes");
-    SC_HIP(sc::launch_fnv1a64(data, bytes, seed, nullptr, out, workspace, static_cast<hipStream_t>(stream)),
+    return SC_OK;
+}
+
+int sc_fnv1a64_async(const void* data, uint64_t bytes, uint64_t seed, uint64_t* out, uint32_t* fault, void* workspace,
+                     uint64_t workspace_bytes, void* stream) {
+    if (const int rc = check_fnv_args(data, bytes, out, fault, true, workspace, workspace_bytes)) return rc;
+    SC_HIP(sc::launch_fnv1a64(data, bytes, seed, nullptr, out, fault, workspace, static_cast<hipStream_t>(stream)),
            "hash launch");
     return ok();
 }
 
 int sc_fnv1a64_check_async(const void* data, uint64_t bytes, uint64_t seed, uint64_t expected, uint64_t* out,
-                           uint32_t* verdict, void* workspace, uint64_t workspace_bytes, void* stream) {
-    if (!out || !verdict || (bytes && !data)) return fail(SC_EINVAL, "sc_handoff: missing hash input, output or verdict");
+                           uint32_t* verdict, uint32_t* fault, void* workspace, uint64_t workspace_bytes, void* stream) {
+    if (!verdict) return fail(SC_EINVAL, "sc_handoff: missing hash verdict");
     if (reinterpret_cast<uintptr_t>(verdict) & 3u) return fail(SC_EINVAL, "sc_handoff: the verdict must be 4-byte aligned");
-    if (!workspace || workspace_bytes < sc::fnv_workspace(bytes).bytes)
-        return fail(SC_EINVAL, "sc_handoff: hash workspace smaller than sc_fnv1a64_workspace_bytes()");
-    if (reinterpret_cast<uintptr_t>(workspace) & 15u) return fail(SC_EINVAL, "sc_handoff: hash workspace must be 16-byte aligned");
-    if (bytes > (uint64_t(1) << 46)) return fail(SC_ERANGE, "sc_handoff: hash input beyond 2^46 bytes");
-    SC_HIP(sc::launch_fnv1a64(data, bytes, seed, nullptr, out, workspace, static_cast<hipStream_t>(stream), expected,
-                              verdict),
+    if (const int rc = check_fnv_args(data, bytes, out, fault, false, workspace, workspace_bytes)) return rc;
+    SC_HIP(sc::launch_fnv1a64(data, bytes, seed, nullptr, out, fault, workspace, static_cast<hipStream_t>(stream),
+                              expected, verdict),
            "hash launch");
     return ok();
 }
 
-int sc_fnv1a64_chain_async(const void* data, uint64_t bytes, uint64_t* state, void* workspace, uint64_t workspace_bytes,
-                           void* stream) {
-    if (!state || (bytes && !data)) return fail(SC_EINVAL, "sc_handoff: missing hash input or state");
+int sc_fnv1a64_chain_async(const void* data, uint64_t bytes, uint64_t* state, uint32_t* fault, void* workspace,
+                           uint64_t workspace_bytes, void* stream) {
     if (reinterpret_cast<uintptr_t>(state) & 7u) return fail(SC_EINVAL, "sc_handoff: hash state must be 8-byte aligned");
-    if (!workspace || workspace_bytes < sc::fnv_workspace(bytes).bytes)
-        return fail(SC_EINVAL, "sc_handoff: hash workspace smaller than sc_fnv1a64_workspace_bytes()");
-    if (reinterpret_cast<uintptr_t>(workspace) & 15u) return fail(SC_EINVAL, "sc_handoff: hash workspace must be 16-byte aligned");
-    if (bytes > (uint64_t(1) << 46)) return fail(SC_ERANGE, "sc_handoff: hash input beyond 2^46 bytes");
-    SC_HIP(sc::launch_fnv1a64(data, bytes, 0, state, state, workspace, static_cast<hipStream_t>(stream)),
+    if (const int rc = check_fnv_args(data, bytes, state, fault, true, workspace, workspace_bytes)) return rc;
+    SC_HIP(sc::launch_fnv1a64(data, bytes, 0, state, state, fault, workspace, static_cast<hipStream_t>(stream)),
            "hash launch");
     return ok();
 }
@@ -1734,16 +1737,22 @@ int sc_fnv1a64_chain_async(const void* data, uint64_t bytes, uint64_t* state, vo
 int sc_fnv1a64_device(const void* data, uint64_t bytes, uint64_t seed, uint64_t* hash) {
     if (!hash || (bytes && !data)) return fail(SC_EINVAL, "sc_handoff: missing hash input or output");
     if (bytes > (uint64_t(1) << 46)) return fail(SC_ERANGE, "sc_handoff: hash input beyond 2^46 bytes");
-    const uint64_t ws_bytes = sc::fnv_workspace(bytes).bytes;
+    const uint64_t ws_bytes = (sc::fnv_workspace(bytes).bytes + 255) / 256 * 256;
     void* ws = nullptr;
     hipError_t e = hipMalloc(&ws, ws_bytes + 256);
     if (e != hipSuccess) return fail(SC_ENOMEM, std::string("sc_handoff: hash workspace: ") + hipGetErrorString(e));
+    // the result and the fault word after the workspace, read back together
     uint64_t* out = reinterpret_cast<uint64_t*>(static_cast<uint8_t*>(ws) + ws_bytes);
-    e = sc::launch_fnv1a64(data, bytes, seed, nullptr, out, ws, nullptr);
-    if (e == hipSuccess) e = hipMemcpy(hash, out, sizeof(uint64_t), hipMemcpyDeviceToHost);
+    uint32_t* fault = reinterpret_cast<uint32_t*>(out + 1);
+    uint64_t back[2] = {0, 0};
+    e = sc::launch_fnv1a64(data, bytes, seed, nullptr, out, fault, ws, nullptr);
+    if (e == hipSuccess) e = hipMemcpy(back, out, sizeof back, hipMemcpyDeviceToHost);
     const hipError_t f = hipFree(ws);
     if (e != hipSuccess) return hip_fail(e, "hash");
     if (f != hipSuccess) return hip_fail(f, "hash workspace free");
+    if (uint32_t(back[1]))
+        return fail(SC_ETIMEOUT, "sc_handoff: a look-back wait of the hash kernel ran out; the hash is not valid");
+    *hash = back[0];
     return ok();
 }
 

@@ -294,13 +294,19 @@ __device__ __forceinline__ uint64_t segment_sum(const uint8_t* data, uint64_t n,
 }
 
 // h = seed * p^n + the sum of the workgroups' sums (mod 2^64; the order of the additions does not matter), `acc` being
-// that sum, or null for an empty input.  With `verdict`, also 1 there when h equals `expected` and no wait of the
-// launch ran out, else 0: a later kernel on the stream can act on the check without a host round trip.
+// that sum, or null for an empty input.  `fault` is the launch's fault word (null for an empty input, which has no
+// waits): a wait that ran out makes h unusable, and the launch says so at `fault_out` - 1 or 0, or, for a chained piece
+// (`sticky`), 1 or'ed into what the earlier pieces left there, so a chain reports a fault of any of its pieces.  With
+// `verdict`, also 1 there when h equals `expected` and no wait of the launch ran out, else 0: a later kernel on the
+// stream can act on the check without a host round trip.
 __global__ void fnv_finish_kernel(const uint64_t* acc, uint64_t seed, const uint64_t* seed_dev, uint64_t n, uint64_t* out,
-                                  uint64_t expected, uint32_t* verdict, const uint32_t* fault) {
+                                  uint32_t* fault_out, bool sticky, uint64_t expected, uint32_t* verdict,
+                                  const uint32_t* fault) {
     const uint64_t h = start_state(seed, seed_dev) * pow_prime(n) + (acc ? acc[0] : 0u);
+    const uint32_t bad = fault && fault[0] ? 1u : 0u;
     out[0] = h;
-    if (verdict) verdict[0] = h == expected && !(fault && fault[0]) ? 1u : 0u;
+    if (fault_out) fault_out[0] = sticky ? (fault_out[0] | bad) : bad;
+    if (verdict) verdict[0] = h == expected && !bad ? 1u : 0u;
 }
 
 // ---- the one-pass hash ---------------------------------------------------------------------------------------------
@@ -314,6 +320,9 @@ __global__ void fnv_finish_kernel(const uint64_t* acc, uint64_t seed, const uint
 // publishes an end state anyway, so no other workgroup waits on it.
 constexpr uint32_t kHasMap = 1u << 8, kHasState = 1u << 9;   // a status word: 0, kHasMap | map, kHasState | state
 constexpr uint32_t kSpinLimit = 1u << 16;   // reads of one window, about 0.2 s (sc_fnv1a64_set_spin_limit)
+// A bound the host sets only to test failure handling: every look-back of a workgroup after the first runs out at
+// once, so any input of more than one workgroup (64 KiB) ends with the fault set, deterministically.
+constexpr uint32_t kForceFault = 0xFFFFFFFFu;
 
 __device__ __forceinline__ void publish(uint32_t* word, uint32_t v) {
     __hip_atomic_store(word, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -333,6 +342,13 @@ __device__ __forceinline__ uint32_t look_back(uint32_t* status, uint64_t g, uint
     if (g == 0) {
         if (lane == 0) publish(status, kHasState | apply<kBits>(map, init));
         return init;
+    }
+    if (spin_limit == kForceFault) {   // the failure-handling tests' forced fault (never set otherwise)
+        if (lane == 0) {
+            publish(fault, 1u);
+            publish(status + g, kHasState | apply<kBits>(map, 0u));
+        }
+        return 0u;
     }
     if (lane == 0) publish(status + g, kHasMap | map);
     uint32_t acc = 0;                  // the maps of the workgroups from above the window up to g, composed
@@ -588,7 +604,7 @@ FnvWorkspace fnv_workspace(uint64_t n) {
 }
 
 hipError_t launch_fnv1a64(const void* data, uint64_t n, uint64_t seed, const uint64_t* seed_dev, uint64_t* out,
-                          void* workspace, hipStream_t stream, uint64_t expected, uint32_t* verdict) {
+                          uint32_t* fault_out, void* workspace, hipStream_t stream, uint64_t expected, uint32_t* verdict) {
     const FnvWorkspace w = fnv_workspace(n);
     uint8_t* ws = static_cast<uint8_t*>(workspace);
     const uint8_t* src = static_cast<const uint8_t*>(data);
@@ -606,7 +622,7 @@ hipError_t launch_fnv1a64(const void* data, uint64_t n, uint64_t seed, const uin
     // the finish reads the start state before it writes `out`, so `out` may be `seed_dev` itself
     const bool any = w.groups > 0;
     hipLaunchKernelGGL(fnv_finish_kernel, dim3(1), dim3(1), 0, stream, any ? reinterpret_cast<const uint64_t*>(ctl + 2) : nullptr,
-                       seed, seed_dev, n, out, expected, verdict, any ? ctl + 1 : nullptr);
+                       seed, seed_dev, n, out, fault_out, seed_dev != nullptr, expected, verdict, any ? ctl + 1 : nullptr);
     return hipGetLastError();
 }
 
@@ -648,8 +664,12 @@ hipError_t scratch_of_current_device(void** out) {
 
 }  // namespace
 
-extern "C" int sc_fnv1a64_noalloc_async(const void* data, uint64_t bytes, uint64_t seed, uint64_t* out, void* stream) {
-    if (!out || (bytes && !data)) return sc::record_error(SC_EINVAL, "sc_handoff: missing hash input or output");
+extern "C" int sc_fnv1a64_noalloc_async(const void* data, uint64_t bytes, uint64_t seed, uint64_t* out, uint32_t* fault,
+                                        void* stream) {
+    if (!out || !fault || (bytes && !data))
+        return sc::record_error(SC_EINVAL, "sc_handoff: missing hash input, output or fault word");
+    if (reinterpret_cast<uintptr_t>(fault) & 3u)
+        return sc::record_error(SC_EINVAL, "sc_handoff: the hash fault word must be 4-byte aligned");
     if (bytes > SC_FNV_NOALLOC_MAX_BYTES || sc::fnv_workspace(bytes).bytes > kScratchBytes)
         return sc::record_error(SC_ERANGE, "sc_handoff: the hash without allocation takes at most 4 GiB "
                                            "(SC_FNV_NOALLOC_MAX_BYTES); use sc_fnv1a64_async with a workspace");
@@ -657,12 +677,13 @@ extern "C" int sc_fnv1a64_noalloc_async(const void* data, uint64_t bytes, uint64
     hipError_t e = scratch_of_current_device(&ws);
     if (e != hipSuccess)
         return sc::record_error(SC_EHIP, std::string("sc_handoff hash scratch: ") + hipGetErrorString(e));
-    e = sc::launch_fnv1a64(data, bytes, seed, nullptr, out, ws, static_cast<hipStream_t>(stream), 0, nullptr);
+    e = sc::launch_fnv1a64(data, bytes, seed, nullptr, out, fault, ws, static_cast<hipStream_t>(stream), 0, nullptr);
     if (e != hipSuccess) return sc::record_error(SC_EHIP, std::string("sc_handoff hash launch: ") + hipGetErrorString(e));
     return sc::record_ok();
 }
 
 extern "C" int sc_fnv1a64_set_spin_limit(uint32_t reads) {
+    static_assert(sc::kForceFault == SC_FNV_FORCE_FAULT, "the forced-fault bound is the header's");
     sc::g_spin_limit.store(reads ? reads : sc::kSpinLimit);
     return sc::record_ok();
 }

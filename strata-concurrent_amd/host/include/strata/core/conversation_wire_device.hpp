@@ -122,7 +122,9 @@ private:
     uint64_t staged_bytes_ = 0;
     void* hash_ws_ = nullptr;          // device
     uint64_t hash_ws_bytes_ = 0;
-    uint64_t* hash_host_ = nullptr;    // pinned; the hash's last kernel stores the payload hash here
+    uint64_t* hash_host_ = nullptr;    // pinned (64 B); the hash's last kernel stores the payload hash here
+    // and the launch's fault word right after it (1: a wait ran out and the hash is not valid)
+    uint32_t* hash_fault_host() { return reinterpret_cast<uint32_t*>(hash_host_ + 1); }
     void* last_stream_ = nullptr;
     sc_plan* capture_ = nullptr;
     void* capture_target_ = nullptr;   // the payload the capture plan was built for
@@ -181,7 +183,9 @@ private:
     void* hash_ws_ = nullptr;
     uint64_t hash_ws_bytes_ = 0;
     uint64_t* hash_dev_ = nullptr;    // device: the hash check's verdict word
-    uint64_t* hash_host_ = nullptr;   // pinned; the hash's last kernel stores the payload hash here
+    uint64_t* hash_host_ = nullptr;   // pinned (64 B); the hash's last kernel stores the payload hash here
+    // and the launch's fault word right after it, so the host sees both words the device verdict is made of
+    uint32_t* hash_fault_host() { return reinterpret_cast<uint32_t*>(hash_host_ + 1); }
 };
 
 }  // namespace strata::core

@@ -42,6 +42,7 @@ struct HandoffMoveStats {
     double wait_ms = 0.0;   ///< waiting for DMA (a staging buffer's event, the stream at the end)
     bool wrote_device = false;   ///< a failed read that had already written device memory
     bool device_error = false;   ///< the failure was a device call's
+    bool hash_fault = false;     ///< the device hash did not complete (a bounded wait of its kernel ran out)
 };
 
 /// A fixed set of host threads that split one copy between them (the calling thread takes part).
@@ -111,9 +112,13 @@ class HandoffMover {
     std::vector<void*> done_;     ///< one event per staging buffer: its last DMA finished
     void* entry_ = nullptr;       ///< event: the caller's stream at entry (the hash stream waits on it)
     void* hash_stream_ = nullptr;
-    void* hash_ws_ = nullptr;     ///< device hash workspace (grown on demand) + the u64 result / running hash at its end
+    void* hash_ws_ = nullptr;     ///< device hash workspace (grown on demand) + the u64 result / running hash at its end,
+                                  ///< then the u32 fault word of the hash launches (sc_fnv1a64_async)
     uint64_t hash_ws_bytes_ = 0;
-    uint64_t* hash_host_ = nullptr;   ///< pinned landing place of the device hash
+    uint64_t* hash_host_ = nullptr;   ///< pinned landing place of the device hash and its fault word
+    /// The two words moved between the device and hash_host_: the hash, then the fault word (in the low half).
+    static constexpr int kHashWords = 2;
+    static uint32_t* fault_word(uint64_t* hash) { return reinterpret_cast<uint32_t*>(hash + 1); }
     HandoffCopyCrew* crew_ = nullptr;
     HandoffMoveStats last_{};
 };

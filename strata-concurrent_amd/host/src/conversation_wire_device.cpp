@@ -375,8 +375,9 @@ bool WireDeviceEncoder::encode(void* payload, uint64_t capacity, void* stream, s
     for (const StagePlan& sp : stage_plans_)
         if (!abi(sc_plan_launch(sp.plan, stream), error, "stage gather")) return false;
     if (gathered && !abi(sc_event_record(gathered, stream), error, "gather event")) return false;
-    // the hash goes straight to pinned host memory (the last kernel's store): no readback copy
-    if (!abi(sc_fnv1a64_async(payload, plan_.total_bytes, kWireHashSeed, hash_host_, hash_ws_, hash_ws_bytes_, stream),
+    // the hash and its fault word go straight to pinned host memory (the last kernel's stores): no readback copy
+    if (!abi(sc_fnv1a64_async(payload, plan_.total_bytes, kWireHashSeed, hash_host_, hash_fault_host(), hash_ws_,
+                              hash_ws_bytes_, stream),
              error, "payload hash"))
         return false;
     last_stream_ = stream;
@@ -386,6 +387,8 @@ bool WireDeviceEncoder::encode(void* payload, uint64_t capacity, void* stream, s
 bool WireDeviceEncoder::payload_hash(uint64_t& hash, std::string& error) {
     if (!hash_host_) return refuse(error, "no encode to read a hash from");
     if (!abi(sc_stream_sync(last_stream_), error, "encode")) return false;
+    if (*hash_fault_host())   // a wait of the hash kernel ran out: the word at hash_host_ is not the payload's hash
+        return refuse(error, "the payload hash did not complete on the device (a look-back wait ran out); encode again");
     hash = *hash_host_;
     return true;
 }
@@ -606,7 +609,7 @@ bool WireDeviceDecoder::restore(void* stream, SavedConversation& image, std::str
     // the hash itself goes straight to pinned host memory (the last kernel's store), the verdict stays on the device
     if (expect_.check_payload_hash &&
         !abi(sc_fnv1a64_check_async(payload_, info_.bytes, kWireHashSeed, expect_.payload_hash, hash_host_, verdict,
-                                    hash_ws_, hash_ws_bytes_, stream),
+                                    hash_fault_host(), hash_ws_, hash_ws_bytes_, stream),
              error, "payload hash"))
         return false;
     SavedConversation out = head_image_;
@@ -651,7 +654,12 @@ bool WireDeviceDecoder::restore(void* stream, SavedConversation& image, std::str
         !abi(sc_stream_sync(stream), error, "restore"))
         return false;
     if (expect_.check_payload_hash) {
-        if (*hash_host_ != expect_.payload_hash)   // the gated scatter wrote nothing
+        // the device verdict that gated the scatters is exactly (hash == expected && no fault); the same two words are
+        // in pinned memory, so the host decides as the scatters did, and a 0 verdict means they wrote nothing
+        if (*hash_fault_host())
+            return refuse(error, "the payload hash did not complete on the device (a look-back wait ran out); nothing "
+                                 "was mounted");
+        if (*hash_host_ != expect_.payload_hash)
             return refuse(error, "payload hash mismatch on the device (the bytes are not the bytes that were written)");
         info_.payload_hash = *hash_host_;
     }

@@ -134,7 +134,7 @@ bool HandoffMover::init(const HandoffMoverConfig& cfg, std::string& err) {
     }
     void* h = nullptr;
     if (sc_event_create(&entry_) != SC_OK || sc_stream_create(&hash_stream_) != SC_OK ||
-        sc_host_alloc(&h, sizeof(uint64_t)) != SC_OK) {
+        sc_host_alloc(&h, kHashWords * sizeof(uint64_t)) != SC_OK) {
         err = abi_error("handoff mover set-up");
         release_();
         return false;
@@ -144,8 +144,9 @@ bool HandoffMover::init(const HandoffMoverConfig& cfg, std::string& err) {
     return true;
 }
 
-/// The hash workspace, grown to serve inputs of `bytes` bytes, and the device word after it (the result, or the
-/// running hash of a chained hash).  Only called while nothing is queued on the hash stream.
+/// The hash workspace, grown to serve inputs of `bytes` bytes, and the device words after it: the result (or the
+/// running hash of a chained hash), then the launch's fault word.  Only called while nothing is queued on the hash
+/// stream.
 uint64_t* HandoffMover::hash_space_(uint64_t bytes, std::string& err) {
     const uint64_t need = (sc_fnv1a64_workspace_bytes(bytes) + 255) & ~255ull;
     if (need + 256 > hash_ws_bytes_) {
@@ -169,8 +170,9 @@ bool HandoffMover::hash_on_device_(const void* data, uint64_t bytes, void* strea
     uint64_t* dev_out = hash_space_(bytes, err);
     if (!dev_out) return false;
     if (sc_event_record(entry_, stream) != SC_OK || sc_stream_wait_event(hash_stream_, entry_) != SC_OK ||
-        sc_fnv1a64_async(data, bytes, kEngineSeed, dev_out, hash_ws_, hash_ws_bytes_ - 256, hash_stream_) != SC_OK ||
-        sc_copy_async(hash_host_, dev_out, sizeof(uint64_t), hash_stream_) != SC_OK) {
+        sc_fnv1a64_async(data, bytes, kEngineSeed, dev_out, fault_word(dev_out), hash_ws_, hash_ws_bytes_ - 256,
+                         hash_stream_) != SC_OK ||
+        sc_copy_async(hash_host_, dev_out, kHashWords * sizeof(uint64_t), hash_stream_) != SC_OK) {
         err = abi_error("handoff mover hash");
         last_.device_error = true;
         return false;
@@ -182,6 +184,11 @@ bool HandoffMover::fetch_hash_(uint64_t* out, std::string& err) {
     if (sc_stream_sync(hash_stream_) != SC_OK) {
         err = abi_error("handoff mover hash wait");
         last_.device_error = true;
+        return false;
+    }
+    if (*fault_word(hash_host_)) {   // a wait of the hash kernel ran out: the word beside it is not the hash
+        err = "handoff mover: the payload hash did not complete on the device (a look-back wait ran out)";
+        last_.hash_fault = true;
         return false;
     }
     *out = *hash_host_;
@@ -277,8 +284,9 @@ bool HandoffMover::read_to_device(HandoffArena& arena, int index, uint64_t nonce
     if (chain) {
         state = hash_space_(std::min(C, bytes), err);
         if (!state) return false;
-        *hash_host_ = kEngineSeed;
-        if (sc_copy_async(state, hash_host_, sizeof(uint64_t), hash_stream_) != SC_OK) {
+        hash_host_[0] = kEngineSeed;   // the running hash, and a clear fault word for the chain to or into
+        hash_host_[1] = 0;
+        if (sc_copy_async(state, hash_host_, kHashWords * sizeof(uint64_t), hash_stream_) != SC_OK) {
             err = abi_error("handoff mover hash seed");
             last_.device_error = true;
             return false;
@@ -299,7 +307,8 @@ bool HandoffMover::read_to_device(HandoffArena& arena, int index, uint64_t nonce
              sc_event_record(done_[k % R], stream) == SC_OK;
         if (ok && chain)
             ok = sc_stream_wait_event(hash_stream_, done_[k % R]) == SC_OK &&
-                 sc_fnv1a64_chain_async(dst + k * C, len, state, hash_ws_, hash_ws_bytes_ - 256, hash_stream_) == SC_OK;
+                 sc_fnv1a64_chain_async(dst + k * C, len, state, fault_word(state), hash_ws_, hash_ws_bytes_ - 256,
+                                        hash_stream_) == SC_OK;
     }
     const auto tf = std::chrono::steady_clock::now();
     if (ok) ok = sc_stream_sync(stream) == SC_OK;
@@ -324,7 +333,7 @@ bool HandoffMover::read_to_device(HandoffArena& arena, int index, uint64_t nonce
         const auto th = std::chrono::steady_clock::now();
         uint64_t h = kEngineSeed;
         if (chain) {
-            if (sc_copy_async(hash_host_, state, sizeof(uint64_t), hash_stream_) != SC_OK) {
+            if (sc_copy_async(hash_host_, state, kHashWords * sizeof(uint64_t), hash_stream_) != SC_OK) {
                 err = abi_error("handoff mover hash");
                 last_.device_error = true;
                 sc_stream_sync(hash_stream_);

@@ -13,6 +13,7 @@
 
 using strata::core::HandoffArena;
 using strata::core::HandoffClaim;
+using strata::core::HandoffMoveStats;
 using strata::core::HandoffMover;
 using strata::core::HandoffMoverConfig;
 using strata::core::HandoffPayload;
@@ -293,6 +294,11 @@ int sc_mover_destroy(sc_mover* mover) {
     return SC_OK;
 }
 
+// The status of a failed transfer: a device hash that did not complete, a device call's failure, or a refusal.
+static int mover_code(const HandoffMoveStats& st) {
+    return st.hash_fault ? (int) SC_ETIMEOUT : st.device_error ? (int) SC_EHIP : (int) SC_EINVAL;
+}
+
 int sc_mover_write(sc_mover* mover, sc_arena* arena, const sc_arena_claim* claim, const void* device_src,
                    uint64_t bytes, void* stream, uint64_t* hash) {
     return guarded([&] {
@@ -300,7 +306,7 @@ int sc_mover_write(sc_mover* mover, sc_arena* arena, const sc_arena_claim* claim
         std::string err;
         if (mover->mover.write_from_device(arena->arena, claim_of(*claim), device_src, bytes, stream, hash, err))
             return (int) SC_OK;
-        return fail(mover->mover.last().device_error ? SC_EHIP : SC_EINVAL, err);
+        return fail(mover_code(mover->mover.last()), err);
     });
 }
 
@@ -311,7 +317,7 @@ int sc_mover_publish(sc_mover* mover, sc_arena* arena, const sc_arena_claim* cla
         std::string err;
         if (mover->mover.publish_from_device(arena->arena, claim_of(*claim), device_src, bytes, tokens, stream, err))
             return (int) SC_OK;
-        return fail(mover->mover.last().device_error ? SC_EHIP : SC_EINVAL, err);
+        return fail(mover_code(mover->mover.last()), err);
     });
 }
 
@@ -326,7 +332,8 @@ int sc_mover_read(sc_mover* mover, sc_arena* arena, int32_t index, uint64_t nonc
         slot_out(i, out);
         if (ok) return (int) SC_OK;
         const auto& st = mover->mover.last();
-        return fail(st.device_error ? (int) SC_EHIP : st.wrote_device ? (int) SC_ESTALE : (int) SC_EINVAL, err);
+        return fail(st.hash_fault || st.device_error ? mover_code(st) : st.wrote_device ? (int) SC_ESTALE : (int) SC_EINVAL,
+                    err);
     });
 }
 

@@ -153,11 +153,15 @@ int sc_wire_encode_async(sc_wire_encoder* e, void* payload, uint64_t capacity, v
     });
 }
 
+// The encoder's and decoder's refusal of a device hash whose kernel's bounded wait ran out.
+static bool hash_incomplete(const std::string& err) { return err.find("did not complete") != std::string::npos; }
+
 int sc_wire_encoder_hash(sc_wire_encoder* e, uint64_t* hash) {
     return guarded([&] {
         if (!e || !hash) return failed(SC_EINVAL, "conversation wire: missing argument");
         std::string err;
-        return e->enc.payload_hash(*hash, err) ? done() : failed(SC_EHIP, err);
+        if (e->enc.payload_hash(*hash, err)) return done();
+        return failed(hash_incomplete(err) ? SC_ETIMEOUT : SC_EHIP, err);
     });
 }
 
@@ -236,8 +240,9 @@ int sc_wire_decoder_restore(sc_wire_decoder* d, void* stream) {
     return guarded([&] {
         if (!d) return failed(SC_EINVAL, "conversation wire: missing decoder");
         std::string err;
-        if (!d->dec.restore(stream, d->image, err))
-            return failed(err.find("hash mismatch") != std::string::npos || err.find("before a successful") != std::string::npos
+        if (!d->dec.restore(stream, d->image, err))   // a timed-out or mismatching hash gated every scatter off
+            return failed(hash_incomplete(err) ? SC_ETIMEOUT
+                          : err.find("hash mismatch") != std::string::npos || err.find("before a successful") != std::string::npos
                               ? SC_EINVAL : SC_EHIP, err);
         d->restored = true;
         return done();

@@ -18,6 +18,8 @@ if not LIB_PATH.exists():
 lib = C.CDLL(str(LIB_PATH))
 
 SC_OK, SC_EINVAL, SC_EHIP, SC_ENOMEM, SC_ERANGE = 0, 1, 2, 3, 4
+SC_ETIMEOUT = 7   # 5 and 6 are sc_arena.h's SC_EBUSY and SC_ESTALE
+SC_FNV_FORCE_FAULT = 0xFFFFFFFF   # sc_fnv1a64_set_spin_limit: every look-back wait runs out (failure tests)
 SC_DTYPE_F16, SC_DTYPE_F32 = 0, 1
 SC_BLOB_K, SC_BLOB_V, SC_BLOB_GDN = 1, 2, 3
 
@@ -194,11 +196,11 @@ _SIGS = {
     "sc_park_layers_async": (C.c_int, [_GEO, C.POINTER(SlotLayers), _I64, _P, _U64, _P, _P]),
     "sc_resume_layers_async": (C.c_int, [_GEO, _P, _U64, _I64, C.POINTER(SlotLayers), _P, _P]),
     "sc_fnv1a64_workspace_bytes": (_U64, [_U64]),
-    "sc_fnv1a64_async": (C.c_int, [_P, _U64, _U64, _P, _P, _U64, _P]),
-    "sc_fnv1a64_chain_async": (C.c_int, [_P, _U64, _P, _P, _U64, _P]),
-    "sc_fnv1a64_check_async": (C.c_int, [_P, _U64, _U64, _U64, _P, _P, _P, _U64, _P]),
+    "sc_fnv1a64_async": (C.c_int, [_P, _U64, _U64, _P, _P, _P, _U64, _P]),
+    "sc_fnv1a64_chain_async": (C.c_int, [_P, _U64, _P, _P, _P, _U64, _P]),
+    "sc_fnv1a64_check_async": (C.c_int, [_P, _U64, _U64, _U64, _P, _P, _P, _P, _U64, _P]),
     "sc_fnv1a64_device": (C.c_int, [_P, _U64, _U64, C.POINTER(_U64)]),
-    "sc_fnv1a64_noalloc_async": (C.c_int, [_P, _U64, _U64, _P, _P]),
+    "sc_fnv1a64_noalloc_async": (C.c_int, [_P, _U64, _U64, _P, _P, _P]),
     "sc_fnv1a64_set_spin_limit": (C.c_int, [C.c_uint32]),
     "sc_copy_device_async": (C.c_int, [_P, _P, _U64, _P]),
     "sc_ipc_export_create": (C.c_int, [_U64, _U64, C.POINTER(_P)]),
@@ -637,39 +639,54 @@ def fnv1a64_device(ptr: int, nbytes: int, seed: int = REFERENCE_FNV_SEED) -> int
     return int(out.value)
 
 
+class HashFault(RuntimeError):
+    """A look-back wait of the device hash ran out (the launch's fault word is 1): the hash is not valid."""
+
+
 class HashPlan:
-    """A reusable device workspace for sc_fnv1a64_async over inputs of up to `max_bytes` bytes, plus a device word
-    for the result."""
+    """A reusable device workspace for sc_fnv1a64_async over inputs of up to `max_bytes` bytes, plus device words for
+    the result and the launch's fault word."""
 
     def __init__(self, max_bytes: int):
         self.max_bytes = max_bytes
         self.ws_bytes = int(lib.sc_fnv1a64_workspace_bytes(max_bytes))
         self.ws = DeviceBuffer(self.ws_bytes, "uint8")
         self.out = DeviceBuffer(1, "uint64")
+        self.fault = DeviceBuffer(1, "uint32")
 
     def launch(self, ptr: int, nbytes: int, seed: int = REFERENCE_FNV_SEED, stream=None) -> None:
         if nbytes > self.max_bytes:
             raise ValueError(f"hash input of {nbytes} bytes exceeds the plan's {self.max_bytes}")
-        check(lib.sc_fnv1a64_async(ptr, nbytes, seed, self.out.ptr, self.ws.ptr, self.ws_bytes, _stream(stream)),
+        check(lib.sc_fnv1a64_async(ptr, nbytes, seed, self.out.ptr, self.fault.ptr, self.ws.ptr, self.ws_bytes,
+                                   _stream(stream)),
               "sc_fnv1a64_async")
 
     def start(self, seed: int = REFERENCE_FNV_SEED) -> None:
-        """Set the running hash of chain() to `seed` (a synchronous upload)."""
+        """Set the running hash of chain() to `seed` and clear the chain's fault word (synchronous uploads)."""
         self.out.upload([seed])
+        self.fault.upload([0])
 
     def chain(self, ptr: int, nbytes: int, stream=None) -> None:
         """Continue the running hash over `nbytes` more device bytes at `ptr` (sc_fnv1a64_chain_async)."""
         if nbytes > self.max_bytes:
             raise ValueError(f"hash input of {nbytes} bytes exceeds the plan's {self.max_bytes}")
-        check(lib.sc_fnv1a64_chain_async(ptr, nbytes, self.out.ptr, self.ws.ptr, self.ws_bytes, _stream(stream)),
+        check(lib.sc_fnv1a64_chain_async(ptr, nbytes, self.out.ptr, self.fault.ptr, self.ws.ptr, self.ws_bytes,
+                                         _stream(stream)),
               "sc_fnv1a64_chain_async")
 
+    def faulted(self) -> bool:
+        return bool(self.fault.numpy()[0])
+
     def result(self) -> int:
+        """The hash of the last launch (or chain); HashFault when a wait of it ran out."""
+        if self.faulted():
+            raise HashFault("a look-back wait of the device hash ran out; the hash is not valid")
         return int(self.out.numpy()[0])
 
     def free(self) -> None:
         self.ws.free()
         self.out.free()
+        self.fault.free()
 
 
 @dataclass

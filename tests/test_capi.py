@@ -127,10 +127,15 @@ def test_kv_append_range_refusals_before_any_hip_call(sc):
 def test_noalloc_hash_refusals_before_any_hip_call(sc):
     """The hash without allocation refuses inputs past its static workspace, and missing pointers, on the host."""
     out = 1 << 40   # never dereferenced: the refusals come first
-    assert sc.lib.sc_fnv1a64_noalloc_async(1 << 40, (4 << 30) + 1, 0, out, None) == sc.SC_ERANGE
+    fault = out + 8
+    assert sc.lib.sc_fnv1a64_noalloc_async(1 << 40, (4 << 30) + 1, 0, out, fault, None) == sc.SC_ERANGE
     assert "at most 4 GiB" in sc.last_error()
-    assert sc.lib.sc_fnv1a64_noalloc_async(None, 16, 0, out, None) == sc.SC_EINVAL
-    assert sc.lib.sc_fnv1a64_noalloc_async(1 << 40, 16, 0, None, None) == sc.SC_EINVAL
+    assert sc.lib.sc_fnv1a64_noalloc_async(None, 16, 0, out, fault, None) == sc.SC_EINVAL
+    assert sc.lib.sc_fnv1a64_noalloc_async(1 << 40, 16, 0, None, fault, None) == sc.SC_EINVAL
+    assert sc.lib.sc_fnv1a64_noalloc_async(1 << 40, 16, 0, out, None, None) == sc.SC_EINVAL
+    assert "fault word" in sc.last_error()
+    assert sc.lib.sc_fnv1a64_noalloc_async(1 << 40, 16, 0, out, fault + 1, None) == sc.SC_EINVAL
+    assert "4-byte aligned" in sc.last_error()
 
 
 def test_core_library_exports_the_wire_abi():
@@ -179,3 +184,19 @@ def test_ipc_refusals_before_any_hip_call(sc):
     assert sc.lib.sc_ipc_import_open(seg, 2, C.byref(h)) == sc.SC_ERANGE
     assert "SC_IPC_MAX_SEGMENT" in sc.last_error()
     assert sc.lib.sc_ipc_import_open(seg, 65, C.byref(h)) == sc.SC_ERANGE
+
+
+def test_kv_block_bytes_per_format(sc):
+    """sc_kv_block_bytes (kv_block_bytes, src/kernels/cuda/kv_stream.cu:192-197): one block (page) of K and V.  At the
+    real model's shapes (2 KV heads of 256, 4 cells per page, include/strata/kernels/qsa.hpp:96-117) the reference's own
+    per-cell figures fix it: f16 2 048 B, int8 1 056 B (the --kv help text, src/program/generate.cpp:532-537), and
+    K8V4's 816 B (same text) is half an int8 cell plus half a q4_0 cell, which fixes q4_0 at 576 B.  Other shapes follow
+    the per-format row sizes: f16 2 * head_dim, int8 head_dim + one f16 scale per 64, q4_0 18 B per 32 values."""
+    f16, int8, q4 = (int(sc.lib.sc_kv_block_bytes(2, 256, 4, fmt)) for fmt in (0, 1, 2))
+    assert (f16, int8) == (4 * 2048, 4 * 1056)
+    assert (int8 + q4) // 2 == 4 * 816 and q4 == 4 * 576
+    for heads, dim, ps in ((1, 64, 1), (4, 128, 8), (2, 512, 16), (3, 256, 2)):
+        rows = heads * ps
+        assert sc.lib.sc_kv_block_bytes(heads, dim, ps, 0) == rows * dim * 2 * 2
+        assert sc.lib.sc_kv_block_bytes(heads, dim, ps, 1) == rows * (dim + dim // 64 * 2) * 2
+        assert sc.lib.sc_kv_block_bytes(heads, dim, ps, 2) == rows * (dim // 32 * 18) * 2

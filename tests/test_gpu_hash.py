@@ -111,12 +111,17 @@ def test_workspace_refusals(sc, cuda):
     out = sc.DeviceBuffer(1, "uint64")
     small = int(sc.lib.sc_fnv1a64_workspace_bytes(1 << 16)) - 256
     ws = sc.DeviceBuffer(max(small, 16), "uint8")
-    rc = sc.lib.sc_fnv1a64_async(buf.ptr, 1 << 16, 0, out.ptr, ws.ptr, small, None)
+    fault = out.ptr + 16   # inside the workspace buffer's allocation is not needed: refusals come first
+    rc = sc.lib.sc_fnv1a64_async(buf.ptr, 1 << 16, 0, out.ptr, fault, ws.ptr, small, None)
     assert rc == sc.SC_EINVAL and "workspace" in sc.last_error()
-    rc = sc.lib.sc_fnv1a64_chain_async(buf.ptr, 1 << 16, out.ptr, ws.ptr, small, None)
+    rc = sc.lib.sc_fnv1a64_chain_async(buf.ptr, 1 << 16, out.ptr, fault, ws.ptr, small, None)
     assert rc == sc.SC_EINVAL and "workspace" in sc.last_error()
-    rc = sc.lib.sc_fnv1a64_chain_async(buf.ptr, 16, out.ptr + 4, ws.ptr, small, None)
+    rc = sc.lib.sc_fnv1a64_chain_async(buf.ptr, 16, out.ptr + 4, fault, ws.ptr, small, None)
     assert rc == sc.SC_EINVAL and "aligned" in sc.last_error()
+    rc = sc.lib.sc_fnv1a64_async(buf.ptr, 16, 0, out.ptr, None, ws.ptr, small, None)
+    assert rc == sc.SC_EINVAL and "fault word" in sc.last_error()
+    rc = sc.lib.sc_fnv1a64_chain_async(buf.ptr, 16, out.ptr, fault + 2, ws.ptr, small, None)
+    assert rc == sc.SC_EINVAL and "fault word" in sc.last_error()
     for b in (buf, out, ws):
         b.free()
 
@@ -156,10 +161,11 @@ def test_a_look_back_wait_that_runs_out_fails_the_verdict(sc, oracle, cuda):
             sc.check(sc.lib.sc_fnv1a64_set_spin_limit(limit), "spin limit")
             verdict.fill(0xAB)
             sc.check(sc.lib.sc_fnv1a64_check_async(buf.ptr, n, sc.REFERENCE_FNV_SEED, want, hp.out.ptr, verdict.ptr,
-                                                   hp.ws.ptr, hp.ws_bytes, None), "check")
+                                                   hp.fault.ptr, hp.ws.ptr, hp.ws_bytes, None), "check")
             sc.device_sync()
             print(f"case spin limit {limit}: verdict {int(verdict.numpy()[0])}", flush=True)
             assert int(verdict.numpy()[0]) == (1 if passes else 0)
+            assert hp.faulted() == (not passes)
             if passes:
                 assert hp.result() == want
     finally:
@@ -190,7 +196,7 @@ def test_gated_scatter_writes_all_or_nothing(sc, oracle, cuda):
         verdict.fill(0xAB)
         sc.device_sync()
         sc.check(sc.lib.sc_fnv1a64_check_async(image.ptr, total, sc.REFERENCE_FNV_SEED, expected, hp.out.ptr,
-                                               verdict.ptr, hp.ws.ptr, hp.ws_bytes, None), "check")
+                                               verdict.ptr, None, hp.ws.ptr, hp.ws_bytes, None), "check")
         sc.check(sc.lib.sc_plan_launch_gated(scatter.handle, verdict.ptr, None), "gated launch")
         sc.device_sync()
         assert hp.result() == want
@@ -201,3 +207,62 @@ def test_gated_scatter_writes_all_or_nothing(sc, oracle, cuda):
         else:
             assert all(np.all(v.view(np.uint8) == 0x5C) for v in state.values())
     hp.free()
+
+
+def test_every_hash_form_reports_a_wait_that_ran_out(sc, oracle, cuda):
+    """With every look-back wait forced to run out (SC_FNV_FORCE_FAULT; the launches still end), the one-shot form
+    sets its fault word to 1, a chain's fault word stays 1 through a later piece that finishes cleanly, the form without
+    allocation sets its fault word, and the synchronous form returns SC_ETIMEOUT instead of a hash.  With the default
+    bound every fault word is 0 and every hash equals the byte loop's."""
+    n = 16 << 20
+    buf = sc.DeviceBuffer(n, "uint8")
+    sc.check(sc.lib.sc_fill_uniform_f16(buf.ptr, n // 2, -4.0, 4.0, 0x5EED, 93, None), "fill")
+    sc.device_sync()
+    want = oracle.fnv1a64(buf.numpy(), sc.REFERENCE_FNV_SEED)
+    hp = sc.HashPlan(n)
+    words = sc.DeviceBuffer(4, "uint64")   # the form without allocation: [hash, fault]
+    try:
+        for limit in (sc.SC_FNV_FORCE_FAULT, 0):
+            forced = limit != 0
+            print(f"case spin limit {limit:#x}", flush=True)
+            sc.check(sc.lib.sc_fnv1a64_set_spin_limit(limit), "spin limit")
+            hp.fault.fill(0xAB)
+            hp.launch(buf.ptr, n)
+            sc.device_sync()
+            assert int(hp.fault.numpy()[0]) == int(forced)
+            if forced:
+                with pytest.raises(sc.HashFault):
+                    hp.result()
+            else:
+                assert hp.result() == want
+            # a chain: the faulting piece first, then a small clean one (a single workgroup never waits)
+            hp.start()
+            hp.chain(buf.ptr, n - 1000)
+            hp.chain(buf.ptr + n - 1000, 1000)
+            sc.device_sync()
+            assert int(hp.fault.numpy()[0]) == int(forced)
+            if not forced:
+                assert hp.result() == want
+            words.fill(0xCD)
+            sc.check(sc.lib.sc_fnv1a64_noalloc_async(buf.ptr, n, sc.REFERENCE_FNV_SEED, words.ptr, words.ptr + 8,
+                                                     None), "noalloc")
+            sc.device_sync()
+            got = words.numpy()
+            assert int(got[1]) & 0xFFFFFFFF == int(forced)
+            if not forced:
+                assert int(got[0]) == want
+            # one workgroup's worth of input never waits, so it never faults
+            hp.launch(buf.ptr, 65536)
+            sc.device_sync()
+            assert hp.result() == oracle.fnv1a64(buf.numpy(65536), sc.REFERENCE_FNV_SEED)
+            out = sc._U64(0)
+            rc = sc.lib.sc_fnv1a64_device(buf.ptr, n, sc.REFERENCE_FNV_SEED, sc.C.byref(out))
+            if forced:
+                assert rc == sc.SC_ETIMEOUT and "ran out" in sc.last_error()
+            else:
+                assert rc == sc.SC_OK and int(out.value) == want
+    finally:
+        sc.check(sc.lib.sc_fnv1a64_set_spin_limit(0), "spin limit")
+        for b in (buf, words):
+            b.free()
+        hp.free()
