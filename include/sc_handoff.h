@@ -159,6 +159,18 @@ int sc_image_layout(const sc_geometry* g, int64_t tokens, sc_image_blob* blobs, 
  * gdn_conv_hist (src/prefill/kernels.cu:219-228) as the writers of the decode layout, plus the GDN row
  * placement of src/prefill/prefill.cpp:1282-1283.  Validates extents against the slot first. */
 int sc_plan_carve(const sc_geometry* g, const sc_prefill_view* src, const sc_decode_slot* dst, sc_plan** out);
+/* Re-points a carve plan at another prefill view of the same slot - new K/V, recurrence and conv pointers, token count,
+ * pos0, dtype, with or without the GDN rows - without allocating and without waiting on the device: the new table rows
+ * go through pinned staging the plan owns, and a small kernel on `stream` copies them into the plan's device table and
+ * rebuilds its tile map before the next launch on that stream.  So a serving engine builds one plan per decode slot and
+ * pays a few microseconds per hand-off instead of a table build (device allocations and blocking uploads); the
+ * reference's per-layer writer likewise takes every pointer as an argument per call (src/prefill/kernels.cu:618-625,
+ * src/prefill/prefill.cpp:1327-1340).  The view must fit what the plan was built with: its rows and tiles at most the
+ * build's (build the plan with the largest view it will carve, e.g. the slot's capacity), the GDN rows only if the build
+ * carved them; otherwise SC_ERANGE and the plan is unchanged, as it is after any refusal (SC_EINVAL).  Retargets and
+ * launches of one plan must be issued on one stream (or ordered by events); the host-side fields change at once, so a
+ * launch enqueued after the call carves the new view.  Only plans from sc_plan_carve can be retargeted. */
+int sc_plan_retarget(sc_plan* plan, const sc_prefill_view* src, void* stream);
 /* Quantized K/V storage of the decode pools (include/strata/kernels/kv_stream.hpp:44-46 KvFormat, plus the K8V4
  * hybrid of src/core/conversation_snapshot.cpp's format 3): int8 codes with one f16 scale per 64 values (kv_q8.hpp),
  * q4_0 blocks of 32 values, 18 bytes each (kv_q4.hpp:21-28), or int8 K with q4_0 V. */

@@ -27,6 +27,9 @@ hipError_t launch_move(const MoveRow* rows, const uint16_t* tile_row, const Move
                        int64_t grid, int32_t mix, bool xcd, hipStream_t stream, const uint32_t* gate = nullptr);
 hipError_t launch_page_order(const OrderGroup* groups, int32_t n_groups, int64_t max_pages, uint32_t max_blocks,
                              hipStream_t stream);
+hipError_t launch_retarget(const MoveRow* staged_rows, int32_t n_rows, const OrderGroup* staged_groups,
+                           int32_t n_groups, MoveRow* rows, uint16_t* tile_row, uint64_t n_tiles, OrderGroup* groups,
+                           hipStream_t stream);
 hipError_t launch_paged_image(const PagedImage& a, const MoveGeo& geo, hipStream_t stream);
 hipError_t launch_fill_uniform_f16(uint16_t* dst, uint64_t n, float lo, float hi, uint64_t seed, uint64_t sid,
                                    hipStream_t stream);
@@ -56,6 +59,8 @@ static uint64_t host_mix64(uint64_t z) {
 uint64_t synth_key(uint64_t seed, uint64_t sid) { return host_mix64(seed ^ host_mix64(sid + 0x9E3779B97F4A7C15ull)); }
 }  // namespace sc
 
+struct CarveRetarget;   // what a carve plan keeps to be re-pointed at another prefill view (sc_plan_retarget)
+
 struct sc_plan {
     bool batch = false;                 // a batched resume + append plan (BatchArgs) instead of a handoff table
     sc::BatchArgs batch_args{};
@@ -76,6 +81,7 @@ struct sc_plan {
     int32_t n_order_groups = 0;
     int64_t order_max_pages = 0;
     uint32_t order_max_blocks = 0;
+    CarveRetarget* rt = nullptr;        // carve plans only
 };
 
 namespace {
@@ -329,18 +335,17 @@ int order_workspace(OrderPlan& o, std::vector<sc::MoveRow>& rows, sc_plan* p) {
     return ok();
 }
 
-// Assigns tile ranges, uploads the table and fills the plan.  The only HIP calls a plan builder makes.
-int finish_plan(std::vector<sc::MoveRow>& rows, const Geo& g, uint64_t payload, sc_plan** out) {
-    if (rows.size() > 65535) return fail(SC_ERANGE, "sc_handoff: more than 65535 handoff table rows in one plan");
-    OrderPlan order = order_plan(rows, g);
-    uint64_t tiles = 0;
-    bool quant = false, kv32 = false;
+// Gives every row its tile range, in row order; an ordered row spans the items of its group's pages (whole pages, in
+// destination order).  Also reports which kernel instance the rows need.
+int assign_tiles(std::vector<sc::MoveRow>& rows, const OrderPlan& order, const Geo& g, uint64_t& tiles, bool& quant,
+                 bool& kv32) {
+    tiles = 0;
+    quant = kv32 = false;
     for (size_t k = 0; k < rows.size(); ++k) {
         sc::MoveRow& r = rows[k];
         if (r.n >= kMaxRowChunks) return fail(SC_ERANGE, "sc_handoff: a handoff table row beyond 2^31 chunks");
         r.tile0 = tiles;
         const uint64_t per_tile = items_per_tile(r.kind);
-        // an ordered row spans the items of its group's pages (whole pages, in destination order)
         const int gi = order.row_group[k];
         const uint64_t items = gi >= 0 ? uint64_t(order.groups[size_t(gi)].lp_hi - order.groups[size_t(gi)].lp_lo) *
                                              items_per_page(r.kind, g)
@@ -349,6 +354,18 @@ int finish_plan(std::vector<sc::MoveRow>& rows, const Geo& g, uint64_t payload, 
         quant = quant || r.kind == sc::kKvQ8 || r.kind == sc::kKvQ4;
         kv32 = kv32 || r.kind == sc::kKv32;
     }
+    return SC_OK;
+}
+
+// Assigns tile ranges, uploads the table and fills the plan.  The only HIP calls a plan builder makes.  `order_out`
+// (may be null) receives the order groups with their workspace pointers.
+int finish_plan(std::vector<sc::MoveRow>& rows, const Geo& g, uint64_t payload, sc_plan** out,
+                OrderPlan* order_out = nullptr) {
+    if (rows.size() > 65535) return fail(SC_ERANGE, "sc_handoff: more than 65535 handoff table rows in one plan");
+    OrderPlan order = order_plan(rows, g);
+    uint64_t tiles = 0;
+    bool quant = false, kv32 = false;
+    if (const int rc = assign_tiles(rows, order, g, tiles, quant, kv32)) return rc;
     // rows that move nothing still own an (empty) tile range; the kernel never visits them
     sc_plan* p = new (std::nothrow) sc_plan();
     if (!p) return fail(SC_ENOMEM, "sc_handoff: plan allocation failed");
@@ -399,6 +416,7 @@ int finish_plan(std::vector<sc::MoveRow>& rows, const Geo& g, uint64_t payload, 
         delete p;
         return hip_fail(e, "table upload");
     }
+    if (order_out) *order_out = std::move(order);
     *out = p;
     return ok();
 }
@@ -654,6 +672,37 @@ int check_layers(const Geo& o, const sc_geometry* g, const sc_slot_layers* s, in
     return SC_OK;
 }
 
+// The slot side of a carve as sc_plan_carve checked it: its pools, tables and identity-layout copies.  A carve plan
+// keeps it so that a retarget re-points only the prefill side.
+struct CarveTarget {
+    std::vector<uint16_t*> k, v;
+    std::vector<const int32_t*> table;
+    int64_t n_pages = 0, max_cells = 0;
+    float* gdn = nullptr;
+    std::vector<ExtraKv> host, stage;
+};
+
+// The rows of a carve of `src` into `t`, and its algorithmic payload.
+void carve_rows(const Geo& o, const sc_prefill_view* src, const CarveTarget& t, std::vector<sc::MoveRow>& rows,
+                uint64_t& payload) {
+    const int64_t logical_pages = (t.max_cells + o.ps - 1) / o.ps;
+    payload = kv_payload(o, src->tokens);
+    for (int64_t j = 0; j < o.n_qsa; ++j) {
+        kv_rows(o, src, j, t.k[size_t(j)], t.v[size_t(j)], t.table[size_t(j)], t.n_pages, 0, rows);
+        // the identity-layout copies get every carved cell, resident in the paged pool or not
+        for (const ExtraKv* e : {&t.host[size_t(j)], &t.stage[size_t(j)]}) {
+            if (!e->k) continue;
+            kv_rows(o, src, j, reinterpret_cast<uint16_t*>(e->k), reinterpret_cast<uint16_t*>(e->v), nullptr,
+                    logical_pages, 0, rows);
+            payload += uint64_t(src->tokens) * uint64_t(o.H) * o.row_bytes * 2;
+        }
+    }
+    if (src->with_gdn) {
+        gdn_rows(o, src, t.gdn, rows);
+        payload += uint64_t(o.n_gdn) * o.gdn_row_bytes;
+    }
+}
+
 template <class F>
 int guarded(F&& f) {
     try {
@@ -667,6 +716,53 @@ int guarded(F&& f) {
     }
 }
 
+}  // namespace
+
+// A carve plan's retarget state: the slot side, the capacity of the device table, tile map and order workspace as
+// built, and two slots of pinned staging for new rows, each free again once the retarget that last used it has run.
+struct CarveRetarget {
+    Geo o;
+    CarveTarget t;
+    size_t rows_cap = 0;
+    uint64_t tile_entries = 0;                // entries of the device tile map
+    std::vector<sc::OrderGroup> built;        // the order groups as built: their workspace and its capacity
+    uint8_t* staging = nullptr;               // pinned: two slots of [rows_cap rows][built.size() groups]
+    uint8_t* staging_dev = nullptr;           // its device address
+    uint64_t slot_bytes = 0;
+    hipEvent_t done[2] = {nullptr, nullptr};  // the last retarget that read each slot
+    int next = 0;
+    bool grid_set = false;                    // sc_plan_set_grid chose the grid
+
+    ~CarveRetarget() {
+        for (hipEvent_t& e : done)
+            if (e) (void) hipEventDestroy(e);
+        if (staging) (void) hipHostFree(staging);
+    }
+};
+
+namespace {
+// Prepares a freshly built carve plan for retargets (sc_plan_retarget): its pinned staging and events, nothing on the
+// device.  Called once per plan, when it is built.
+int attach_retarget(sc_plan* p, const Geo& o, CarveTarget&& t, size_t n_rows, OrderPlan&& order) {
+    auto* rt = new (std::nothrow) CarveRetarget();
+    if (!rt) return fail(SC_ENOMEM, "sc_handoff: plan allocation failed");
+    rt->o = o;
+    rt->t = std::move(t);
+    rt->rows_cap = n_rows;
+    rt->tile_entries = p->n_tiles + (p->n_tiles & 1);
+    rt->built = std::move(order.groups);
+    rt->slot_bytes = round_up(n_rows * sizeof(sc::MoveRow) + rt->built.size() * sizeof(sc::OrderGroup) + 16, 256);
+    hipError_t e = hipHostMalloc(reinterpret_cast<void**>(&rt->staging), 2 * rt->slot_bytes);
+    if (e == hipSuccess) e = hipHostGetDevicePointer(reinterpret_cast<void**>(&rt->staging_dev), rt->staging, 0);
+    for (hipEvent_t& ev : rt->done)
+        if (e == hipSuccess) e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+    if (e != hipSuccess) {
+        delete rt;
+        return fail(SC_ENOMEM, std::string("sc_handoff: retarget staging: ") + hipGetErrorString(e));
+    }
+    p->rt = rt;
+    return SC_OK;
+}
 }  // namespace
 
 extern "C" {
@@ -721,30 +817,109 @@ int sc_plan_carve(const sc_geometry* g, const sc_prefill_view* src, const sc_dec
         if (rc) return rc;
         rc = check_slot(o, dst, src->pos0 + src->tokens, src->with_gdn != 0);
         if (rc) return rc;
-        std::vector<ExtraKv> host, stage;
+        CarveTarget t;
         const int64_t host_cells = (dst->max_cells + o.ps - 1) / o.ps * o.ps;
-        if ((rc = extra_kv(o, dst->host, SC_KV_F16, "a host copy", host, host_cells)) ||
-            (rc = extra_kv(o, dst->stage, SC_KV_F16, "a staging pool", stage)))
+        if ((rc = extra_kv(o, dst->host, SC_KV_F16, "a host copy", t.host, host_cells)) ||
+            (rc = extra_kv(o, dst->stage, SC_KV_F16, "a staging pool", t.stage)))
             return rc;
-        const int64_t logical_pages = (dst->max_cells + o.ps - 1) / o.ps;
-        std::vector<sc::MoveRow> rows;
-        uint64_t payload = kv_payload(o, src->tokens);
         for (int64_t j = 0; j < o.n_qsa; ++j) {
-            const int32_t* table = dst->page_table ? dst->page_table[j] : nullptr;
-            kv_rows(o, src, j, dst->k_pool[j], dst->v_pool[j], table, dst->n_pages, 0, rows);
-            // the identity-layout copies get every carved cell, resident in the paged pool or not
-            for (const ExtraKv* e : {&host[size_t(j)], &stage[size_t(j)]}) {
-                if (!e->k) continue;
-                kv_rows(o, src, j, reinterpret_cast<uint16_t*>(e->k), reinterpret_cast<uint16_t*>(e->v), nullptr,
-                        logical_pages, 0, rows);
-                payload += uint64_t(src->tokens) * uint64_t(o.H) * o.row_bytes * 2;
-            }
+            t.k.push_back(dst->k_pool[j]);
+            t.v.push_back(dst->v_pool[j]);
+            t.table.push_back(dst->page_table ? dst->page_table[j] : nullptr);
         }
-        if (src->with_gdn) {
-            gdn_rows(o, src, dst->gdn_state, rows);
-            payload += uint64_t(o.n_gdn) * o.gdn_row_bytes;
+        t.n_pages = dst->n_pages;
+        t.max_cells = dst->max_cells;
+        t.gdn = src->with_gdn ? dst->gdn_state : nullptr;
+        std::vector<sc::MoveRow> rows;
+        uint64_t payload = 0;
+        carve_rows(o, src, t, rows, payload);
+        OrderPlan order;
+        sc_plan* p = nullptr;
+        if ((rc = finish_plan(rows, o, payload, &p, &order))) return rc;
+        if ((rc = attach_retarget(p, o, std::move(t), rows.size(), std::move(order)))) {
+            sc_plan_destroy(p);
+            return rc;
         }
-        return finish_plan(rows, o, payload, out);
+        *out = p;
+        return ok();
+    });
+}
+
+int sc_plan_retarget(sc_plan* plan, const sc_prefill_view* src, void* stream) {
+    return guarded([&] {
+        if (!plan) return fail(SC_EINVAL, "sc_handoff: missing plan");
+        CarveRetarget* rt = plan->rt;
+        if (!rt) return fail(SC_EINVAL, "sc_handoff: only a carve plan (sc_plan_carve) can be retargeted");
+        const Geo& o = rt->o;
+        int rc = check_view(o, src);
+        if (rc) return rc;
+        if (src->pos0 + src->tokens > rt->t.max_cells) return snapshot_fail("invalid K/V extent");
+        if (src->with_gdn && o.n_gdn > 0 && !rt->t.gdn)
+            return fail(SC_ERANGE, "sc_handoff: the plan was built without the GDN rows; build a plan that carves them");
+        std::vector<sc::MoveRow> rows;
+        uint64_t payload = 0;
+        carve_rows(o, src, rt->t, rows, payload);
+        OrderPlan order = order_plan(rows, o);
+        // each ordered group takes the workspace its table got when the plan was built; a group the build did not
+        // order (or whose pages outgrow it) keeps the source order
+        std::vector<int> remap(order.groups.size(), -1);
+        std::vector<sc::OrderGroup> groups;
+        for (size_t i = 0; i < order.groups.size(); ++i) {
+            const sc::OrderGroup& G = order.groups[i];
+            for (const sc::OrderGroup& B : rt->built)
+                if (B.table == G.table && B.ld == G.ld && G.order_len <= B.order_len && G.n_blocks == B.n_blocks) {
+                    sc::OrderGroup X = G;
+                    X.inv = B.inv;
+                    X.order = B.order;
+                    X.counts = B.counts;
+                    remap[i] = int(groups.size());
+                    groups.push_back(X);
+                    break;
+                }
+        }
+        for (int& gi : order.row_group) gi = gi >= 0 ? remap[size_t(gi)] : -1;
+        order.groups = groups;
+        uint64_t tiles = 0;
+        bool quant = false, kv32 = false;
+        if ((rc = assign_tiles(rows, order, o, tiles, quant, kv32))) return rc;
+        if (rows.size() > rt->rows_cap || tiles + (tiles & 1) > rt->tile_entries)
+            return fail(SC_ERANGE, "sc_handoff: the view needs a larger handoff table than the plan was built with; "
+                                   "build the plan for the largest view it will carve");
+        for (size_t k = 0; k < rows.size(); ++k) {
+            rows[k].order = order.row_group[k] >= 0 ? groups[size_t(order.row_group[k])].order : nullptr;
+        }
+        // the staging slot is free once the retarget that used it two calls ago has run (normally long since)
+        const int slot = rt->next;
+        hipError_t e = hipEventSynchronize(rt->done[slot]);
+        if (e != hipSuccess) return hip_fail(e, "retarget staging wait");
+        uint8_t* host = rt->staging + uint64_t(slot) * rt->slot_bytes;
+        uint8_t* dev = rt->staging_dev + uint64_t(slot) * rt->slot_bytes;
+        const uint64_t groups_at = round_up(rt->rows_cap * sizeof(sc::MoveRow), 16);
+        if (!rows.empty()) std::memcpy(host, rows.data(), rows.size() * sizeof(sc::MoveRow));
+        if (!groups.empty()) std::memcpy(host + groups_at, groups.data(), groups.size() * sizeof(sc::OrderGroup));
+        e = sc::launch_retarget(reinterpret_cast<const sc::MoveRow*>(dev), int32_t(rows.size()),
+                                reinterpret_cast<const sc::OrderGroup*>(dev + groups_at), int32_t(groups.size()),
+                                plan->rows_dev, plan->tile_row_dev, tiles,
+                                const_cast<sc::OrderGroup*>(plan->order_groups), static_cast<hipStream_t>(stream));
+        if (e == hipSuccess) e = hipEventRecord(rt->done[slot], static_cast<hipStream_t>(stream));
+        if (e != hipSuccess) return hip_fail(e, "retarget");
+        rt->next = slot ^ 1;
+        plan->n_rows = int(rows.size());
+        plan->n_tiles = tiles;
+        plan->payload = payload;
+        plan->mix = sc::mix_of(kv32, quant);
+        plan->default_grid = int64_t(std::min<uint64_t>(tiles, kMaxGrid));
+        if (!rt->grid_set) plan->grid = plan->default_grid;
+        plan->xcd = plan->mix == sc::kMixPlain &&
+                    std::none_of(rows.begin(), rows.end(), [](const sc::MoveRow& r) { return r.table != nullptr; });
+        plan->n_order_groups = int32_t(groups.size());
+        plan->order_max_pages = 0;
+        plan->order_max_blocks = 0;
+        for (const sc::OrderGroup& G : groups) {
+            plan->order_max_pages = std::max(plan->order_max_pages, G.lp_hi - G.lp_lo);
+            plan->order_max_blocks = std::max(plan->order_max_blocks, G.n_blocks);
+        }
+        return ok();
     });
 }
 
@@ -1175,6 +1350,7 @@ uint64_t sc_plan_payload_bytes(const sc_plan* plan) { return plan ? plan->payloa
 int sc_plan_set_grid(sc_plan* plan, int64_t workgroups) {
     if (!plan || workgroups < 0 || workgroups > (int64_t(1) << 30)) return fail(SC_EINVAL, "sc_handoff: invalid grid");
     plan->grid = workgroups == 0 ? plan->default_grid : workgroups;
+    if (plan->rt) plan->rt->grid_set = workgroups != 0;
     return ok();
 }
 
@@ -1187,6 +1363,7 @@ int sc_plan_destroy(sc_plan* plan) {
     if (e == hipSuccess) e = e2;
     if (e == hipSuccess) e = e3;
     if (e == hipSuccess) e = e4;
+    delete plan->rt;
     delete plan;
     return e == hipSuccess ? ok() : hip_fail(e, "table free");
 }

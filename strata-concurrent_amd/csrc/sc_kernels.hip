@@ -980,6 +980,50 @@ hipError_t launch_paged_image(const PagedImage& a, const MoveGeo& geo, hipStream
     return hipGetLastError();
 }
 
+// ---- re-pointing a plan without allocating -----------------------------------------------------------------------
+// A retargeted carve plan (sc_plan_retarget) keeps its device table, tile map and order workspace and takes new rows:
+// the host writes them, and the order groups, into pinned staging, and this kernel copies them into the plan's device
+// table and rebuilds the tile -> row map, on the stream the launches use, so nothing is allocated and the host does
+// not wait.  Workgroup b < n_rows copies row b and writes the map entries of its tiles (the last row also takes the
+// pad entry of an odd tile count); workgroup n_rows copies the order groups.
+namespace {
+__global__ void __launch_bounds__(kThreads) retarget_kernel(const MoveRow* staged_rows, int32_t n_rows,
+                                                            const OrderGroup* staged_groups, int32_t n_groups,
+                                                            MoveRow* rows, uint16_t* tile_row, uint64_t n_tiles,
+                                                            OrderGroup* groups) {
+    const int32_t b = int32_t(blockIdx.x);
+    if (b == n_rows) {
+        const uint32_t* s = reinterpret_cast<const uint32_t*>(staged_groups);
+        uint32_t* d = reinterpret_cast<uint32_t*>(groups);
+        const uint32_t words = uint32_t(n_groups) * uint32_t(sizeof(OrderGroup) / 4);
+        for (uint32_t i = threadIdx.x; i < words; i += kThreads) d[i] = s[i];
+        return;
+    }
+    __shared__ uint64_t s_span[2];
+    if (threadIdx.x == 0) {
+        s_span[0] = staged_rows[b].tile0;
+        s_span[1] = b + 1 < n_rows ? staged_rows[b + 1].tile0 : n_tiles + (n_tiles & 1u);
+    }
+    if (threadIdx.x < sizeof(MoveRow) / 4)
+        reinterpret_cast<uint32_t*>(rows + b)[threadIdx.x] = reinterpret_cast<const uint32_t*>(staged_rows + b)[threadIdx.x];
+    __syncthreads();
+    const uint64_t t1 = s_span[1];
+    for (uint64_t t = s_span[0] + threadIdx.x; t < t1; t += kThreads) tile_row[t] = uint16_t(b);
+}
+}  // namespace
+
+hipError_t launch_retarget(const MoveRow* staged_rows, int32_t n_rows, const OrderGroup* staged_groups,
+                           int32_t n_groups, MoveRow* rows, uint16_t* tile_row, uint64_t n_tiles, OrderGroup* groups,
+                           hipStream_t stream) {
+    if (n_rows < 0 || n_groups < 0 || (n_rows && (!staged_rows || !rows || !tile_row)) ||
+        (n_groups && (!staged_groups || !groups)))
+        return hipErrorInvalidValue;
+    if (n_rows == 0 && n_groups == 0) return hipSuccess;
+    hipLaunchKernelGGL(retarget_kernel, dim3(unsigned(n_rows) + 1), dim3(kThreads), 0, stream, staged_rows, n_rows,
+                       staged_groups, n_groups, rows, tile_row, n_tiles, groups);
+    return hipGetLastError();
+}
+
 hipError_t launch_page_order(const OrderGroup* groups, int32_t n_groups, int64_t max_pages, uint32_t max_blocks,
                              hipStream_t stream) {
     if (n_groups <= 0) return hipSuccess;

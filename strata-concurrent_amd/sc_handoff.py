@@ -135,6 +135,7 @@ _SIGS = {
     "sc_payload_bytes": (_U64, [_GEO, _I64]),
     "sc_image_layout": (C.c_int, [_GEO, _I64, C.POINTER(ImageBlob), C.POINTER(_I64), C.POINTER(_U64)]),
     "sc_plan_carve": (C.c_int, [_GEO, C.POINTER(PrefillView), C.POINTER(DecodeSlot), C.POINTER(_P)]),
+    "sc_plan_retarget": (C.c_int, [_P, C.POINTER(PrefillView), _P]),
     "sc_plan_gather": (C.c_int, [_GEO, C.POINTER(PrefillView), _P, _U64, C.POINTER(_P)]),
     "sc_plan_scatter": (C.c_int, [_GEO, _P, _U64, _I64, C.POINTER(DecodeSlot), C.POINTER(_P)]),
     "sc_plan_capture": (C.c_int, [_GEO, C.POINTER(DecodeSlot), _I64, _P, _U64, C.POINTER(_P)]),
@@ -350,6 +351,12 @@ class Plan:
 
     def launch(self, stream=None) -> None:
         check(lib.sc_plan_launch(self.handle, _stream(stream)), "sc_plan_launch")
+
+    def retarget(self, prefill: "PrefillBuffers", pos0: int = 0, with_gdn: bool = True, stream=None) -> None:
+        """Re-point a carve plan at another prefill sequence of the same slot (sc_plan_retarget)."""
+        view, keep = prefill.view(pos0, with_gdn)
+        check(lib.sc_plan_retarget(self.handle, C.byref(view), _stream(stream)), "sc_plan_retarget")
+        self._target = prefill   # the device buffers the next launches read
 
     @property
     def payload_bytes(self) -> int:
