@@ -424,6 +424,47 @@ uint64_t sco_synth_kv_blob_hash(int64_t H, int64_t D, int64_t ps, int64_t cells,
     return h;
 }
 
+/* One blob of a quantized slot a synthetic f32 sequence carves to (the quantizing kv_append of every token, identity
+ * pool): `fmt` 1 int8 or 2 q4_0, `part` 0 the codes pool ([page][H][ps][row] bytes: D int8 codes or D/32 q4_0 blocks of
+ * 18 bytes) or 1 the int8 scales ([page][H][ps][D/64] f16), over the first `cells` cells; row (t, h) quantizes element
+ * (t * H + h) * D + d of stream `sid` under `seed`, U[lo, hi] in f32 (sco_fill_uniform_f32) with sco_q8_row or
+ * sco_q4_row, and the rows of cells at or past `tokens` hold `tail` bytes. */
+uint64_t sco_synth_quant_blob_hash(int64_t H, int64_t D, int64_t ps, int64_t cells, uint64_t seed, uint64_t sid,
+                                   int64_t tokens, float lo, float hi, int32_t fmt, int32_t part, uint8_t tail,
+                                   uint64_t fnv_seed) {
+    if (D > 1024 || D % 64) return 0;
+    const uint64_t key = sco_synth_key(seed, sid);
+    const float span = hi - lo;
+    const int64_t row_bytes = part == 1 ? D / 64 * 2 : fmt == 1 ? D : D / 32 * 18;
+    float x[1024];
+    uint8_t out[1024];
+    uint16_t scales[16];
+    uint64_t h = fnv_seed;
+    for (int64_t page = 0; page * ps < cells; ++page)
+        for (int64_t kh = 0; kh < H; ++kh)
+            for (int64_t c = 0; c < ps; ++c) {
+                const int64_t t = page * ps + c;
+                if (t >= tokens) {
+                    for (int64_t b = 0; b < row_bytes; ++b) h = fnv_byte(h, tail);
+                    continue;
+                }
+                const uint64_t base = (uint64_t) ((t * H + kh) * D);
+                for (int64_t d = 0; d < D; ++d) {
+                    const float u = (float) (uint32_t) (draw(key, base + (uint64_t) d) >> 40) * 0x1p-24f;
+                    x[d] = fmaf(span, u, lo);
+                }
+                const uint8_t* bytes = out;
+                if (fmt == 1) {
+                    sco_q8_row(x, D, (int8_t*) out, scales);
+                    if (part == 1) bytes = (const uint8_t*) scales;
+                } else {
+                    sco_q4_row(x, D, out);
+                }
+                for (int64_t b = 0; b < row_bytes; ++b) h = fnv_byte(h, bytes[b]);
+            }
+    return h;
+}
+
 static float normal_at(uint64_t key, uint64_t i) {
     int64_t sum = 0;
     for (int k = 0; k < 6; ++k) {

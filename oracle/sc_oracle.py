@@ -59,6 +59,8 @@ for _name, _res, _args in (
     ("sco_cpu_handoff", _U64, [_P, _P, _U64, _P]),
     ("sco_memcpy_threads", C.c_int, [_P, _P, _U64, C.c_int]),
     ("sco_synth_kv_blob_hash", _U64, [_I64, _I64, _I64, _I64, _P, C.c_int32, C.c_uint8, _U64]),
+    ("sco_synth_quant_blob_hash", _U64, [_I64, _I64, _I64, _I64, _U64, _U64, _I64, C.c_float, C.c_float, C.c_int32,
+                                         C.c_int32, C.c_uint8, _U64]),
     ("sco_synth_gdn_hash", _U64, [_G, _U64, _U64, _U64, _I64, _U64]),
 ):
     _fn = getattr(lib, _name)
@@ -251,6 +253,52 @@ def synthetic_image_hashes(geo, tokens: int, seed: int, conv_rows: int | None = 
     def run(job):
         kind, src = job
         return kv_blob_hash(g, cells, src, tail) if kind == "kv" else gdn_blob_hash(g, seed, conv_rows)
+
+    with ThreadPoolExecutor(max_workers=threads) as pool:
+        return list(pool.map(run, jobs))
+
+
+def quant_blob_hash(geo, cells: int, seed: int, sid: int, tokens: int, fmt: int, part: int, tail: int = 0,
+                    fnv_seed: int = REFERENCE_FNV_SEED) -> int:
+    """The FNV-1a of one quantized pool blob (codes or int8 scales) of a synthetic f32 sequence, streamed from the
+    generator through sco_q8_row / sco_q4_row (sco_synth_quant_blob_hash)."""
+    return int(lib.sco_synth_quant_blob_hash(geo.n_head_kv, geo.head_dim, geo.page_size, cells, seed, sid, tokens,
+                                             -4.0, 4.0, fmt, part, tail, fnv_seed))
+
+
+QUANT_INT8, QUANT_Q4, QUANT_K8V4 = 1, 2, 3   # the slot formats (sc_handoff.h SC_KV_*)
+
+
+def synthetic_quant_hashes(geo, tokens: int, seed: int, fmt: int, conv_rows: int | None = None, tail: int = 0,
+                           threads: int = 16) -> list[int]:
+    """The FNV-1a of every blob of a quantized slot a synthetic f32 sequence of `tokens` tokens under `seed` carves to
+    (sc_plan_carve_quant): per QSA layer the K codes, the V codes, then the K and V scales where the format has them
+    (int8: both; K8V4: int8 K with its scales, q4_0 V; q4_0: none), then the GDN rows; the first cells(tokens) cells of
+    each identity pool, untouched cells holding `tail`.  Blobs are hashed on `threads` threads."""
+    from concurrent.futures import ThreadPoolExecutor
+    g = geometry_from(geo)
+    n_qsa = g.n_layers // g.qsa_interval
+    n_gdn = g.n_layers - n_qsa
+    cells = int(lib.sco_cells(C.byref(g), tokens))
+    conv_rows = min(tokens, g.ssm_d_conv - 1) if conv_rows is None else conv_rows
+    k_fmt = QUANT_Q4 if fmt == QUANT_Q4 else QUANT_INT8
+    v_fmt = QUANT_INT8 if fmt == QUANT_INT8 else QUANT_Q4
+    jobs = []
+    for j in range(n_qsa):
+        jobs.append((SID_K0 + 2 * j, k_fmt, 0))
+        jobs.append((SID_V0 + 2 * j, v_fmt, 0))
+        if k_fmt == QUANT_INT8:
+            jobs.append((SID_K0 + 2 * j, k_fmt, 1))
+        if v_fmt == QUANT_INT8:
+            jobs.append((SID_V0 + 2 * j, v_fmt, 1))
+    if n_gdn:
+        jobs.append(None)
+
+    def run(job):
+        if job is None:
+            return gdn_blob_hash(g, seed, conv_rows)
+        sid, f, part = job
+        return quant_blob_hash(g, cells, seed, sid, tokens, f, part, tail)
 
     with ThreadPoolExecutor(max_workers=threads) as pool:
         return list(pool.map(run, jobs))

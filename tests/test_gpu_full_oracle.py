@@ -129,3 +129,36 @@ def test_config5_every_slot_matches_oracle_hash(sc, oracle, cuda):
         capture.destroy()
     hp.free()
     case.free()
+
+
+@pytest.mark.parametrize("fmt", ["int8", "q4_0", "k8v4"])
+def test_quant_carve_128k_every_blob(sc, oracle, cuda, fmt):
+    """Config 3's quantizing carves (the bench's quant_carve rows): f32 K/V rows of 131072 tokens into int8, q4_0 and
+    K8V4 pools plus the GDN rows, in one launch; every pool blob (codes, and scales where the format has them) and the
+    GDN rows equal the oracle's streamed hashes (sco_synth_quant_blob_hash over sco_q8_row / sco_q4_row, pinned on the
+    CPU against the materialised quantizers), so every byte of the 128K carve is compared."""
+    geo = sc.geometry()
+    tokens = 131072
+    code = {"int8": sc.SC_KV_INT8, "q4_0": sc.SC_KV_Q4, "k8v4": sc.SC_KV_K8V4}[fmt]
+    seed = 0x5EED + 0x8
+    print(f"oracle hashes for the {fmt} carve of {tokens} tokens", flush=True)
+    want = oracle.synthetic_quant_hashes(geo, tokens, seed, code, tail=0x5A)
+    case = synth.SyntheticCase(geo, tokens=tokens, seed=seed, kv_dtype=sc.SC_DTYPE_F32)
+    slot = sc.new_quant_slot(geo, code, tokens, fill=0x5A)
+    plan = sc.plan_carve_quant(geo, case.prefill, slot)
+    plan.launch()
+    sc.device_sync()
+    plan.destroy()
+    del case
+    spans = []
+    for j in range(geo.n_qsa):
+        spans += [(slot.k_codes[j].ptr, slot.k_codes[j].nbytes), (slot.v_codes[j].ptr, slot.v_codes[j].nbytes)]
+        if slot.k_scale:
+            spans.append((slot.k_scale[j].ptr, slot.k_scale[j].nbytes))
+        if slot.v_scale:
+            spans.append((slot.v_scale[j].ptr, slot.v_scale[j].nbytes))
+    spans.append((slot.gdn.ptr, slot.gdn.nbytes))
+    hp = sc.HashPlan(MAX_BLOB)
+    got = _hashes(hp, spans)
+    assert got == want, f"{fmt}: " + _mismatch(got, want)
+    hp.free()

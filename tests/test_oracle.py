@@ -333,3 +333,39 @@ def test_synthetic_image_hashes_with_appended_chunk(oracle):
     bad["gdn"] = state["gdn"].copy()
     bad["gdn"][0, :rec_len] = first["rec"][0].reshape(-1)
     assert _blob_hashes(oracle, g, L + chunk, oracle.park(g, L + chunk, bad))[-1] != want[-1]
+
+
+@pytest.mark.parametrize("fmt", [1, 2, 3])
+@pytest.mark.parametrize("tokens,tail", [(37, 0x5A), (40, 0)])
+def test_synthetic_quant_hashes_equal_fill_quantize(oracle, fmt, tokens, tail):
+    """sco_synth_quant_blob_hash == FNV-1a of each pool blob of sco_kv_append_quant(sco_fill_uniform_f32): the
+    streaming checker of the full-size quantizing carves computes exactly the bytes of the pinned quantizers (int8
+    codes and scales, q4_0 blocks, K8V4's int8 K with q4_0 V), over pools whose untouched tail cells hold `tail`."""
+    g = oracle.Geometry(*SMALL_GEO.values())
+    H, D, ps = g.n_head_kv, g.head_dim, g.page_size
+    n_qsa = g.n_layers // g.qsa_interval
+    inputs = _synthetic_inputs(oracle, g, tokens, seed=31, conv_rows=3, dtype=1)
+    n_pages = (tokens + ps - 1) // ps
+    rows = n_pages * H * ps
+    want = []
+    for j in range(n_qsa):
+        k_fmt = 2 if fmt == 2 else 1
+        v_fmt = 1 if fmt == 1 else 2
+        scale_blobs = []
+        for x, f in ((inputs["k"][j], k_fmt), (inputs["v"][j], v_fmt)):
+            row_bytes = D if f == 1 else D // 32 * 18
+            codes = np.full(rows * row_bytes, tail, dtype=np.uint8)
+            scales = np.full(rows * (D // 64), tail | tail << 8, dtype=np.uint16) if f == 1 else None
+            oracle.kv_append_quant(x, f, tokens, 0, None, n_pages, H, D, ps, codes, scales)
+            want.append(oracle.fnv1a64(codes))
+            if scales is not None:
+                scale_blobs.append(oracle.fnv1a64(scales.view(np.uint8)))
+        want += scale_blobs
+    state = oracle.expected_slot(g, inputs, slot_cells=n_pages * ps)
+    want.append(oracle.fnv1a64(state["gdn"].view(np.uint8)))
+    got = oracle.synthetic_quant_hashes(g, tokens, 31, fmt, tail=tail, threads=3)
+    assert got == want
+    # a plausible mistake fails: the V rows quantized from the K stream
+    if fmt == 1:
+        bad = oracle.quant_blob_hash(g, n_pages * ps, 31, oracle.SID_K0, tokens, 1, 0, tail)
+        assert bad != want[1]
