@@ -124,6 +124,7 @@ typedef struct sc_image_blob {
 } sc_image_blob;
 
 typedef struct sc_plan sc_plan;   /* a device-resident handoff table plus its launch shape */
+typedef struct sc_hash_map sc_hash_map;   /* capture plans' rows as the sources of a payload, for the fused hash */
 
 /* ---- errors ---------------------------------------------------------------------------------------------- */
 
@@ -473,6 +474,20 @@ int sc_fnv1a64_device(const void* data, uint64_t bytes, uint64_t seed, uint64_t*
 #define SC_FNV_NOALLOC_MAX_BYTES (4ull << 30)
 int sc_fnv1a64_noalloc_async(const void* data, uint64_t bytes, uint64_t seed, uint64_t* out, uint32_t* fault,
                              void* stream);
+/* The capture fused with its hash.  A capture plan (sc_plan_capture*, sc_plan_gather: page gathers, copies and zero
+ * fills into the payload) writes the payload from the slot, and the payload hash then reads it all again; the encode of
+ * a hand-off payload (conversation_wire_encode's walk and hash, src/core/conversation_wire.cpp:400-480, 1069-1071) is
+ * both.  sc_hash_map_create reads the rows of `n_plans` capture plans writing into `payload` (16-byte aligned, `bytes`
+ * a multiple of 16, every row inside it and no two rows on the same bytes; the bytes no row writes are taken as the
+ * payload holds them when the launch runs, e.g. a head copied in before it) and uploads them as a map of the payload
+ * once (this allocates); sc_hash_map_launch then gathers every row's bytes into the payload and hashes the whole payload
+ * in one kernel that reads each source byte once, with the result and fault word of sc_fnv1a64_async.  The payload
+ * afterwards holds exactly what launching the plans would write.  Nothing is allocated per launch; the plans may be
+ * destroyed after the map is made, their sources and the payload must stay where they were. */
+int sc_hash_map_create(const sc_plan* const* plans, int32_t n_plans, void* payload, uint64_t bytes, sc_hash_map** out);
+int sc_hash_map_launch(const sc_hash_map* map, uint64_t seed, uint64_t* out, uint32_t* fault, void* workspace,
+                       uint64_t workspace_bytes, void* stream);
+int sc_hash_map_destroy(sc_hash_map* map);
 /* The bound on each of the hash kernel's look-back waits, in reads of its window (0 restores the default, 65536, about
  * 0.2 s).  No counterpart in the reference: a workgroup only waits on workgroups that are running or done, so a
  * correct launch never reaches the bound; tests lower it to force a wait to run out, which must set the fault word of

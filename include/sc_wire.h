@@ -77,10 +77,12 @@ int sc_wire_encoder_create_layers(const sc_geometry* g, const sc_slot_layers* sl
 /* The payload's total size (WirePlan::total_bytes) and where its blob pool starts. */
 uint64_t sc_wire_encoder_bytes(const sc_wire_encoder* e);
 uint64_t sc_wire_encoder_pool_offset(const sc_wire_encoder* e);
-/* Enqueues the encode on `stream` into 16-byte aligned device memory `payload`: the head copied in, one gather launch
- * for the pool, one device FNV-1a over the payload.  `gathered` (a hipEvent_t, may be NULL) is recorded when every
- * payload byte is in place, before the hash: a park on another stream can wait on it and overlap the hash.  Replaces
- * conversation_wire_encode's walk and byte-serial hash (src/core/conversation_wire.cpp:400-480, 1006-1025). */
+/* Enqueues the encode on `stream` into 16-byte aligned device memory `payload`: the head copied in, then one kernel
+ * that gathers the pool's blobs from the slot and hashes the whole payload as it writes it (sc_hash_map_launch: the
+ * slot is read once and the payload never re-read).  With `gathered` (a hipEvent_t) the gather runs first on its own,
+ * the event is recorded when every payload byte is in place, then the hash: a park on another stream can wait on the
+ * event and overlap the hash.  Replaces conversation_wire_encode's walk and byte-serial hash
+ * (src/core/conversation_wire.cpp:400-480, 1006-1025). */
 int sc_wire_encode_async(sc_wire_encoder* e, void* payload, uint64_t capacity, void* stream, void* gathered);
 /* The payload hash of the last encode (waits for it): WireEncoded::payload_hash.  SC_ETIMEOUT, and no hash, when the
  * device hash did not complete (a bounded wait of its kernel ran out, sc_fnv1a64_async): encode again. */

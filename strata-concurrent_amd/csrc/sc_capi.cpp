@@ -49,6 +49,8 @@ hipError_t launch_ring_table(int32_t* table, int64_t n_blocks, int64_t n_slots, 
 hipError_t launch_fnv1a64(const void* data, uint64_t n, uint64_t seed, const uint64_t* seed_dev, uint64_t* out,
                           uint32_t* fault_out, void* workspace, hipStream_t stream, uint64_t expected = 0,
                           uint32_t* verdict = nullptr);
+hipError_t launch_fnv1a64_mapped(const HashMapArgs& map, uint64_t seed, uint64_t* out, uint32_t* fault_out,
+                                 void* workspace, hipStream_t stream);
 
 static uint64_t host_mix64(uint64_t z) {
     z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
@@ -82,6 +84,14 @@ struct sc_plan {
     int64_t order_max_pages = 0;
     uint32_t order_max_blocks = 0;
     CarveRetarget* rt = nullptr;        // carve plans only
+    std::vector<sc::MoveRow> host_rows; // the table as uploaded (what sc_hash_map_create reads)
+};
+
+struct sc_hash_map {
+    sc::HashExtent* ext_dev = nullptr;   // one device block: the extents, then each workgroup's first extent
+    uint32_t* first_dev = nullptr;
+    uint8_t* payload = nullptr;
+    uint64_t bytes = 0;
 };
 
 namespace {
@@ -417,6 +427,7 @@ int finish_plan(std::vector<sc::MoveRow>& rows, const Geo& g, uint64_t payload, 
         return hip_fail(e, "table upload");
     }
     if (order_out) *order_out = std::move(order);
+    p->host_rows = rows;
     *out = p;
     return ok();
 }
@@ -1366,6 +1377,104 @@ int sc_plan_destroy(sc_plan* plan) {
     delete plan->rt;
     delete plan;
     return e == hipSuccess ? ok() : hip_fail(e, "table free");
+}
+
+// ---- capture plans fused with the payload hash -------------------------------------------------------------------
+
+int sc_hash_map_create(const sc_plan* const* plans, int32_t n_plans, void* payload, uint64_t bytes, sc_hash_map** out) {
+    return guarded([&] {
+        if (!out || (n_plans && !plans) || n_plans < 0) return fail(SC_EINVAL, "sc_handoff: missing hash map argument");
+        if ((bytes && !payload) || !aligned16(payload) || bytes % 16)
+            return fail(SC_EINVAL, "sc_handoff: a hashed payload is 16-byte aligned and whole 16-byte chunks");
+        if (bytes > (uint64_t(1) << 46)) return fail(SC_ERANGE, "sc_handoff: hash input beyond 2^46 bytes");
+        uint8_t* base = static_cast<uint8_t*>(payload);
+        std::vector<sc::HashExtent> rows;
+        for (int32_t i = 0; i < n_plans; ++i) {
+            const sc_plan* p = plans[i];
+            if (!p || p->batch) return fail(SC_EINVAL, "sc_handoff: a hash map reads the rows of capture plans");
+            for (const sc::MoveRow& r : p->host_rows) {
+                sc::HashExtent x{};
+                switch (r.kind) {
+                    case sc::kCopy: x.kind = sc::kExtCopy; x.src = r.src; break;
+                    case sc::kZero: x.kind = sc::kExtZero; break;
+                    case sc::kPagesGather:
+                        x.kind = sc::kExtPages;
+                        x.src = r.src;
+                        x.table = r.table;
+                        x.ld = r.ld;
+                        x.page_chunks = p->geo.page_chunks.d;
+                        break;
+                    default:
+                        return fail(SC_EINVAL, "sc_handoff: only capture plans (page gathers, copies and zero fills into "
+                                               "the payload) can be fused with its hash");
+                }
+                if (r.dst < base || uint64_t(r.dst - base) > bytes || r.n * 16 > bytes - uint64_t(r.dst - base))
+                    return fail(SC_EINVAL, "sc_handoff: a row of the plan writes outside the hashed payload");
+                x.off = uint64_t(r.dst - base);
+                x.end = x.off + r.n * 16;
+                if (x.end > x.off) rows.push_back(x);
+            }
+        }
+        std::sort(rows.begin(), rows.end(), [](const sc::HashExtent& a, const sc::HashExtent& b) { return a.off < b.off; });
+        std::vector<sc::HashExtent> ext;
+        uint64_t at = 0;
+        for (const sc::HashExtent& x : rows) {
+            if (x.off < at) return fail(SC_EINVAL, "sc_handoff: two rows of the plans write the same payload bytes");
+            if (x.off > at) ext.push_back(sc::HashExtent{at, x.off, nullptr, nullptr, 0, sc::kExtSelf, 0});
+            ext.push_back(x);
+            at = x.end;
+        }
+        if (at < bytes || ext.empty()) ext.push_back(sc::HashExtent{at, bytes, nullptr, nullptr, 0, sc::kExtSelf, 0});
+        // every workgroup's first extent (workgroup g hashes payload bytes [g, g + 1) * 64 KiB)
+        const sc::FnvWorkspace w = sc::fnv_workspace(bytes);
+        std::vector<uint32_t> first(std::max<uint64_t>(w.groups, 1), 0);
+        size_t e = 0;
+        for (uint64_t g = 0; g < w.groups; ++g) {
+            const uint64_t o = g * uint64_t(sc::kFnvGroupBytes);
+            while (e + 1 < ext.size() && ext[e].end <= o) ++e;
+            first[g] = uint32_t(e);
+        }
+        auto* m = new (std::nothrow) sc_hash_map();
+        if (!m) return fail(SC_ENOMEM, "sc_handoff: hash map allocation failed");
+        const uint64_t ext_bytes = round_up(ext.size() * sizeof(sc::HashExtent), 256);
+        hipError_t err = hipMalloc(reinterpret_cast<void**>(&m->ext_dev), ext_bytes + first.size() * 4);
+        if (err != hipSuccess) {
+            delete m;
+            return fail(SC_ENOMEM, std::string("sc_handoff: hash map: ") + hipGetErrorString(err));
+        }
+        m->first_dev = reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(m->ext_dev) + ext_bytes);
+        err = hipMemcpy(m->ext_dev, ext.data(), ext.size() * sizeof(sc::HashExtent), hipMemcpyHostToDevice);
+        if (err == hipSuccess) err = hipMemcpy(m->first_dev, first.data(), first.size() * 4, hipMemcpyHostToDevice);
+        if (err != hipSuccess) {
+            (void) hipFree(m->ext_dev);
+            delete m;
+            return hip_fail(err, "hash map upload");
+        }
+        m->payload = base;
+        m->bytes = bytes;
+        *out = m;
+        return ok();
+    });
+}
+
+int sc_hash_map_launch(const sc_hash_map* map, uint64_t seed, uint64_t* out, uint32_t* fault, void* workspace,
+                       uint64_t workspace_bytes, void* stream) {
+    if (!map) return fail(SC_EINVAL, "sc_handoff: missing hash map");
+    if (!out || !fault) return fail(SC_EINVAL, "sc_handoff: missing hash output or fault word");
+    if (reinterpret_cast<uintptr_t>(fault) & 3u) return fail(SC_EINVAL, "sc_handoff: the hash fault word must be 4-byte aligned");
+    if (!workspace || workspace_bytes < sc::fnv_workspace(map->bytes).bytes)
+        return fail(SC_EINVAL, "sc_handoff: hash workspace smaller than sc_fnv1a64_workspace_bytes()");
+    if (reinterpret_cast<uintptr_t>(workspace) & 15u) return fail(SC_EINVAL, "sc_handoff: hash workspace must be 16-byte aligned");
+    sc::HashMapArgs a{map->ext_dev, map->first_dev, map->payload, map->bytes};
+    const hipError_t e = sc::launch_fnv1a64_mapped(a, seed, out, fault, workspace, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? ok() : hip_fail(e, "mapped hash launch");
+}
+
+int sc_hash_map_destroy(sc_hash_map* map) {
+    if (!map) return ok();
+    const hipError_t e = map->ext_dev ? hipFree(map->ext_dev) : hipSuccess;
+    delete map;
+    return e == hipSuccess ? ok() : hip_fail(e, "hash map free");
 }
 
 #define SC_HIP(call, what)                                    \

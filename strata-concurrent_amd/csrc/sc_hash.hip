@@ -301,8 +301,10 @@ __device__ __forceinline__ uint64_t segment_sum(const uint8_t* data, uint64_t n,
 // stream can act on the check without a host round trip.
 __global__ void fnv_finish_kernel(const uint64_t* acc, uint64_t seed, const uint64_t* seed_dev, uint64_t n, uint64_t* out,
                                   uint32_t* fault_out, bool sticky, uint64_t expected, uint32_t* verdict,
-                                  const uint32_t* fault) {
-    const uint64_t h = start_state(seed, seed_dev) * pow_prime(n) + (acc ? acc[0] : 0u);
+                                  const uint32_t* fault, const uint8_t* tail, uint32_t tail_len) {
+    uint64_t h = start_state(seed, seed_dev) * pow_prime(n) + (acc ? acc[0] : 0u);
+    // the mapped hash leaves the payload's last partial lane segment (under 256 bytes) to this loop
+    for (uint32_t i = 0; i < tail_len; ++i) h = (h ^ tail[i]) * kFnvPrime;
     const uint32_t bad = fault && fault[0] ? 1u : 0u;
     out[0] = h;
     if (fault_out) fault_out[0] = sticky ? (fault_out[0] | bad) : bad;
@@ -505,15 +507,143 @@ __device__ __forceinline__ uint32_t pair_regs(const uint32_t (&w)[kFnvLaneBytes 
     return x;
 }
 
+// ---- the gather fused with the hash -------------------------------------------------------------------------------
+// A lane of the mapped hash gathers its segment of the payload from the extents' sources into its registers, stores it
+// into the payload and hashes it from the registers, so a capture's payload is written and hashed in one read of the
+// slot.  Most segments lie inside one extent and one contiguous source (a 256-byte segment of a 4 KiB page); the
+// others, at extent and page boundaries, take their chunks one at a time.
+__device__ __forceinline__ void put16(uint8_t* p, u32x4 v) { *(gu32x4*) p = v; }
+
+// A run of the payload from payload offset `o`: bytes [o, end) come from one contiguous source `src` (a copy extent, a
+// page of a pages extent, the payload itself for a self extent or an unplaced page) or are zeros (src null); `store`
+// says whether the gather writes them (self bytes stay as the payload holds them).
+struct Run {
+    const uint8_t* src;
+    uint64_t end;
+    bool store;
+};
+__device__ __forceinline__ Run run_at(const HashExtent& x, uint64_t o, uint8_t* dst_o) {
+    Run r{dst_o, x.end, false};
+    if (x.kind == kExtCopy) {
+        r.src = x.src + (o - x.off);
+        r.store = true;
+    } else if (x.kind == kExtZero) {
+        r.src = nullptr;
+        r.store = true;
+    } else if (x.kind == kExtPages) {
+        const uint32_t q = uint32_t((o - x.off) >> 4), page = q / x.page_chunks, ch = q - page * x.page_chunks;
+        const uint64_t page_end = x.off + (uint64_t(page) + 1u) * x.page_chunks * 16u;
+        r.end = page_end < x.end ? page_end : x.end;
+        const int64_t phys = x.table ? int64_t(x.table[page]) : int64_t(page);
+        if (phys >= 0 && phys < x.ld) {
+            r.src = x.src + (uint64_t(phys) * x.page_chunks + ch) * 16u;
+            r.store = true;
+        }
+    }
+    return r;
+}
+
+__device__ u32x4 g_hash_zero_chunk;   // read for zero runs, so every chunk takes the same load
+
+// The lane's segment [begin, begin + len) gathered into w.  A segment in one run or two (the usual cases: inside a
+// blob, or across one page or blob boundary) issues its 16 loads at once from one or two bases; a segment over three
+// runs or more, and the payload's last partial segment, goes chunk by chunk into the payload, which the lane then reads
+// back (its own stores, after a fence).  The payload is written by store_wave below (the last partial segment only
+// here).
+__device__ __forceinline__ void gather_segment(const HashMapArgs& m, uint32_t e, uint64_t begin, uint64_t len,
+                                               uint32_t (&w)[kFnvLaneBytes / 4]) {
+    while (m.ext[e].end <= begin) ++e;
+    HashExtent x = m.ext[e];
+    uint8_t* dst = m.dst + begin;
+    const uint64_t seg_end = begin + len;
+    const Run a = run_at(x, begin, dst);
+    if (len == kFnvLaneBytes) {
+        Run b = a;
+        uint32_t ka = kFnvLaneBytes / 16;   // chunks from run a
+        bool two = a.end >= seg_end;
+        if (!two) {
+            ka = uint32_t((a.end - begin) >> 4);
+            if (a.end >= x.end) x = m.ext[++e];
+            b = run_at(x, a.end, dst + 16u * ka);
+            two = b.end >= seg_end;
+        }
+        if (two) {
+            const uint8_t* za = a.src ? a.src : reinterpret_cast<const uint8_t*>(&g_hash_zero_chunk);
+            const uint8_t* zb = b.src ? b.src : reinterpret_cast<const uint8_t*>(&g_hash_zero_chunk);
+            const uint64_t sa = a.src ? 16u : 0u, sb = b.src ? 16u : 0u;
+#pragma unroll
+            for (int k = 0; k < kFnvLaneBytes / 16; ++k) {
+                const bool in_a = uint32_t(k) < ka;
+                const uint8_t* q = in_a ? za + sa * uint64_t(k) : zb + sb * uint64_t(k - int(ka));
+                const u32x4 v = *(const gu32x4*) q;
+                w[4 * k] = v.x;
+                w[4 * k + 1] = v.y;
+                w[4 * k + 2] = v.z;
+                w[4 * k + 3] = v.w;
+            }
+            return;
+        }
+        x = m.ext[e];
+    }
+#pragma unroll 1
+    for (uint64_t o = begin; o < seg_end;) {
+        while (x.end <= o) x = m.ext[++e];
+        const Run r = run_at(x, o, m.dst + o);
+        const uint64_t o0 = o, end = r.end < seg_end ? r.end : seg_end;
+        for (; o < end; o += 16)
+            if (r.store) put16(m.dst + o, r.src ? *(const gu32x4*) (r.src + (o - o0)) : u32x4{0u, 0u, 0u, 0u});
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");   // the lane's stores complete before its reads
+    if (len == kFnvLaneBytes) load_segment(dst, w);
+}
+
+// The wave's 16 KiB of gathered payload into the payload with coalesced stores: each lane holds 256 contiguous bytes,
+// so stores straight from the registers would put 64 lines under every store instruction (measured: the fused kernel
+// 3.3-3.7 ms with them against 2.3 ms without any store, and 8.2 ms with non-temporal ones).  Four passes of 4 KiB: a
+// quarter of the lanes write their segments into the wave's LDS rows (17 chunks apart, so the 16 writers of a
+// 16-byte column fall in different banks), then every lane reads back 16 bytes per 1 KiB and stores it, 1 KiB
+// contiguous per instruction.  Bytes at or past `limit` (the part hashed in the kernel) are not written here.
+constexpr int kXposeRow = kFnvLaneBytes / 16 + 1;   // chunks per LDS row: a lane's 16 and one of padding
+__device__ __forceinline__ void store_wave(u32x4 (&lds)[16 * kXposeRow], const uint32_t (&w)[kFnvLaneBytes / 4],
+                                           uint8_t* dst, uint64_t wave_begin, uint64_t limit, int lane) {
+#pragma unroll
+    for (int pass = 0; pass < 4; ++pass) {
+        if ((lane >> 4) == pass) {
+            const int row = (lane & 15) * kXposeRow;
+#pragma unroll
+            for (int k = 0; k < kFnvLaneBytes / 16; ++k)
+                lds[row + k] = u32x4{w[4 * k], w[4 * k + 1], w[4 * k + 2], w[4 * k + 3]};
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int c = r * 64 + lane;   // chunk of this pass's 4 KiB: lane c / 16's chunk c % 16
+            const u32x4 v = lds[(c >> 4) * kXposeRow + (c & 15)];
+            const uint64_t o = wave_begin + uint64_t(pass) * 4096u + uint64_t(c) * 16u;
+            if (o < limit) put16(dst + o, v);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+}
+
 // status: three arrays of `stride` words (one per level); ctl: [0] the ticket counter, [1] the fault word, [2..3] the
-// sum of the workgroups' sums (each workgroup adds its own with one 64-bit atomic).
-__global__ void __launch_bounds__(kThreads) fnv_onepass_kernel(const uint8_t* data, uint64_t n, bool aligned,
+// sum of the workgroups' sums (each workgroup adds its own with one 64-bit atomic).  kMapped: the payload is gathered
+// through `map` (stored, and hashed up to `n`, its whole lane segments) instead of read from `data`.
+// Five waves per SIMD (the mapped instance would take 110 VGPRs and four; held to 96 it spills a few words and ran
+// the fused 128K capture in 2.73 against 2.82 ms).
+template <bool kMapped>
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5, 8))) fnv_onepass_kernel(const uint8_t* data, uint64_t n, bool aligned,
                                                                 uint64_t seed, const uint64_t* seed_dev,
                                                                 uint32_t* status, uint64_t stride, uint32_t* ctl,
-                                                                uint32_t spin_limit) {
+                                                                uint32_t spin_limit, HashMapArgs map) {
     __shared__ LevelLds L;
     __shared__ uint32_t s_ticket;
     __shared__ uint64_t s_sum[kThreads / 64];
+    __shared__ u32x4 s_xpose[kMapped ? kThreads / 64 : 1][16 * kXposeRow];
     if (threadIdx.x == 0) s_ticket = atomicAdd(ctl, 1u);
     __syncthreads();
     const uint64_t g = uint32_t(__builtin_amdgcn_readfirstlane(int(s_ticket)));
@@ -525,7 +655,15 @@ __global__ void __launch_bounds__(kThreads) fnv_onepass_kernel(const uint8_t* da
     const uint8_t* p = data + begin;
     uint32_t* fault = ctl + 1;
     uint32_t w[kFnvLaneBytes / 4] = {};
-    if (full) load_segment(p, w);
+    if constexpr (kMapped) {
+        if (begin < map.n_total) {
+            const uint64_t left = map.n_total - begin;
+            gather_segment(map, map.first[g], begin, left < kFnvLaneBytes ? left : kFnvLaneBytes, w);
+        }
+        store_wave(s_xpose[wave], w, map.dst, (g * kThreads + uint64_t(wave) * 64) * kFnvLaneBytes, n, lane);
+    } else if (full) {
+        load_segment(p, w);
+    }
     const uint64_t h0 = start_state(seed, seed_dev);
 
     // bits 0-2: the four machines of run_low3 end in bytes a + 2c; regrouped into the layout the ballots read
@@ -616,13 +754,39 @@ hipError_t launch_fnv1a64(const void* data, uint64_t n, uint64_t seed, const uin
         const uint64_t init_blocks = (words + kThreads - 1) / kThreads < 1024 ? (words + kThreads - 1) / kThreads : 1024;
         hipLaunchKernelGGL(fnv_onepass_init_kernel, dim3(unsigned(init_blocks)), dim3(kThreads), 0, stream, status, words,
                            ctl);
-        hipLaunchKernelGGL(fnv_onepass_kernel, dim3(unsigned(w.groups)), dim3(kThreads), 0, stream, src, n, aligned, seed,
-                           seed_dev, status, w.stride, ctl, g_spin_limit.load());
+        hipLaunchKernelGGL(fnv_onepass_kernel<false>, dim3(unsigned(w.groups)), dim3(kThreads), 0, stream, src, n, aligned,
+                           seed, seed_dev, status, w.stride, ctl, g_spin_limit.load(), HashMapArgs{});
     }
     // the finish reads the start state before it writes `out`, so `out` may be `seed_dev` itself
     const bool any = w.groups > 0;
     hipLaunchKernelGGL(fnv_finish_kernel, dim3(1), dim3(1), 0, stream, any ? reinterpret_cast<const uint64_t*>(ctl + 2) : nullptr,
-                       seed, seed_dev, n, out, fault_out, seed_dev != nullptr, expected, verdict, any ? ctl + 1 : nullptr);
+                       seed, seed_dev, n, out, fault_out, seed_dev != nullptr, expected, verdict, any ? ctl + 1 : nullptr,
+                       nullptr, 0u);
+    return hipGetLastError();
+}
+
+// The gather fused with the hash: the payload's `map.n_total` bytes gathered into map.dst and hashed, the whole lane
+// segments in the one-pass kernel and the last partial one (under 256 bytes) by the closing kernel, which runs after
+// every byte is in place.
+hipError_t launch_fnv1a64_mapped(const HashMapArgs& map, uint64_t seed, uint64_t* out, uint32_t* fault_out,
+                                 void* workspace, hipStream_t stream) {
+    const uint64_t n_total = map.n_total, n_full = n_total & ~uint64_t(kFnvLaneBytes - 1);
+    const FnvWorkspace w = fnv_workspace(n_total);
+    uint8_t* ws = static_cast<uint8_t*>(workspace);
+    uint32_t* ctl = reinterpret_cast<uint32_t*>(ws + w.off_ctl);
+    uint32_t* status = reinterpret_cast<uint32_t*>(ws + w.off_status);
+    if (w.groups > 0) {
+        const uint64_t words = 3 * w.stride;
+        const uint64_t init_blocks = (words + kThreads - 1) / kThreads < 1024 ? (words + kThreads - 1) / kThreads : 1024;
+        hipLaunchKernelGGL(fnv_onepass_init_kernel, dim3(unsigned(init_blocks)), dim3(kThreads), 0, stream, status, words,
+                           ctl);
+        hipLaunchKernelGGL(fnv_onepass_kernel<true>, dim3(unsigned(w.groups)), dim3(kThreads), 0, stream, map.dst, n_full,
+                           true, seed, nullptr, status, w.stride, ctl, g_spin_limit.load(), map);
+    }
+    const bool any = w.groups > 0;
+    hipLaunchKernelGGL(fnv_finish_kernel, dim3(1), dim3(1), 0, stream, any ? reinterpret_cast<const uint64_t*>(ctl + 2) : nullptr,
+                       seed, nullptr, n_full, out, fault_out, false, 0ull, nullptr, any ? ctl + 1 : nullptr,
+                       map.dst + n_full, uint32_t(n_total - n_full));
     return hipGetLastError();
 }
 

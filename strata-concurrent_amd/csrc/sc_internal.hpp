@@ -203,4 +203,26 @@ struct FnvWorkspace {
 };
 FnvWorkspace fnv_workspace(uint64_t n);
 
+// The gather fused with the hash (sc_hash_map_*): the payload [0, n) as extents sorted by offset, every byte in exactly
+// one.  A self extent's bytes are already in the payload (written earlier on the stream, or left as they are); a copy
+// extent's come from a contiguous source, a pages extent's from pool pages through a page table (a page whose entry is
+// negative or past the pool is left as the payload holds it, as the page gather leaves it), a zero extent's are zeros.
+enum HashExtentKind : uint32_t { kExtSelf = 0, kExtCopy = 1, kExtPages = 2, kExtZero = 3 };
+struct HashExtent {
+    uint64_t off, end;       // payload bytes [off, end), 16-byte aligned
+    const uint8_t* src;      // copy: the source of byte `off`; pages: the pool
+    const int32_t* table;    // pages: logical -> physical page (null: identity)
+    int64_t ld;              // pages: physical pages of the pool
+    uint32_t kind;
+    uint32_t page_chunks;    // pages: 16-byte chunks per page
+};
+static_assert(sizeof(HashExtent) == 48, "hash extents are 48 bytes");
+constexpr int kFnvGroupBytes = 256 * kFnvLaneBytes;   // the payload bytes of one hash workgroup
+struct HashMapArgs {
+    const HashExtent* ext;   // null: the plain hash of `data`
+    const uint32_t* first;   // per workgroup: the extent holding its first byte
+    uint8_t* dst;            // the payload
+    uint64_t n_total;        // payload bytes gathered (n rounded down to whole lane segments is hashed in the kernel)
+};
+
 }  // namespace sc

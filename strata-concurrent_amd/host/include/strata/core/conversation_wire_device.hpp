@@ -83,9 +83,11 @@ public:
               const WireIdentity& identity, std::string& error);
     const WirePlan& layout() const { return plan_; }
     uint64_t bytes() const { return plan_.total_bytes; }
-    /// Enqueues the whole encode on `stream` into `payload` (16-byte aligned device memory of at least bytes()).  When
-    /// `gathered` (a hipEvent_t) is given it is recorded once every payload byte is in place and before the hash runs,
-    /// so a copy of the payload on another stream (a park) can start while the hash is computed.
+    /// Enqueues the whole encode on `stream` into `payload` (16-byte aligned device memory of at least bytes()): the
+    /// head copied in, then the gather fused with the payload hash (one read of the slot).  When `gathered` (a
+    /// hipEvent_t) is given the gather runs on its own first and the event is recorded once every payload byte is in
+    /// place and before the hash runs, so a copy of the payload on another stream (a park) can start while the hash
+    /// is computed.
     bool encode(void* payload, uint64_t capacity, void* stream, std::string& error, void* gathered = nullptr);
     /// The payload hash of the last encode; waits for it.
     bool payload_hash(uint64_t& hash, std::string& error);
@@ -127,6 +129,7 @@ private:
     uint32_t* hash_fault_host() { return reinterpret_cast<uint32_t*>(hash_host_ + 1); }
     void* last_stream_ = nullptr;
     sc_plan* capture_ = nullptr;
+    sc_hash_map* hash_map_ = nullptr;  // the capture plans' rows fused with the payload hash (one read of the slot)
     void* capture_target_ = nullptr;   // the payload the capture plan was built for
 };
 

@@ -126,6 +126,8 @@ void WireDeviceEncoder::release() {
         if (sp.plan) sc_plan_destroy(sp.plan);
     stage_plans_.clear();
     if (capture_) sc_plan_destroy(capture_);
+    if (hash_map_) sc_hash_map_destroy(hash_map_);
+    hash_map_ = nullptr;
     if (staged_) sc_host_free(staged_);
     if (hash_host_) sc_host_free(hash_host_);
     if (hash_ws_) sc_device_free(hash_ws_);
@@ -341,6 +343,8 @@ bool WireDeviceEncoder::encode(void* payload, uint64_t capacity, void* stream, s
     if (capture_target_ != payload) {
         if (capture_) sc_plan_destroy(capture_);
         capture_ = nullptr;
+        if (hash_map_) sc_hash_map_destroy(hash_map_);
+        hash_map_ = nullptr;
         int rc;
         if (layered_) {
             sc_layers_map map{lay_off_.data(), zero_.data(), int64_t(zero_.size() / 2)};
@@ -366,20 +370,37 @@ bool WireDeviceEncoder::encode(void* payload, uint64_t capacity, void* stream, s
                      "stage capture plan"))
                 return false;
         }
+        // the same rows as the sources of the fused gather + hash (the head and the small host blobs are copied in
+        // first and hashed as the payload holds them)
+        std::vector<const sc_plan*> plans{capture_};
+        for (const StagePlan& sp : stage_plans_) plans.push_back(sp.plan);
+        if (!abi(sc_hash_map_create(plans.data(), int32_t(plans.size()), payload, plan_.total_bytes, &hash_map_), error,
+                 "payload hash map"))
+            return false;
         capture_target_ = payload;
     }
     uint8_t* p = static_cast<uint8_t*>(payload);
     for (const Upload& u : uploads_)
         if (!abi(sc_copy_async(p + u.offset, staged_ + u.staged_at, u.bytes, stream), error, "head copy")) return false;
-    if (!abi(sc_plan_launch(capture_, stream), error, "pool gather")) return false;
-    for (const StagePlan& sp : stage_plans_)
-        if (!abi(sc_plan_launch(sp.plan, stream), error, "stage gather")) return false;
-    if (gathered && !abi(sc_event_record(gathered, stream), error, "gather event")) return false;
     // the hash and its fault word go straight to pinned host memory (the last kernel's stores): no readback copy
-    if (!abi(sc_fnv1a64_async(payload, plan_.total_bytes, kWireHashSeed, hash_host_, hash_fault_host(), hash_ws_,
-                              hash_ws_bytes_, stream),
-             error, "payload hash"))
-        return false;
+    if (!gathered) {
+        // one kernel gathers the slot's blobs into the payload and hashes the payload from its registers
+        if (!abi(sc_hash_map_launch(hash_map_, kWireHashSeed, hash_host_, hash_fault_host(), hash_ws_, hash_ws_bytes_,
+                                    stream),
+                 error, "payload gather and hash"))
+            return false;
+    } else {
+        // a caller that copies the payload out as soon as its bytes are in place (a checked park) gets the gather
+        // first, the event, then the hash, so the copy overlaps the hash
+        if (!abi(sc_plan_launch(capture_, stream), error, "pool gather")) return false;
+        for (const StagePlan& sp : stage_plans_)
+            if (!abi(sc_plan_launch(sp.plan, stream), error, "stage gather")) return false;
+        if (!abi(sc_event_record(gathered, stream), error, "gather event")) return false;
+        if (!abi(sc_fnv1a64_async(payload, plan_.total_bytes, kWireHashSeed, hash_host_, hash_fault_host(), hash_ws_,
+                                  hash_ws_bytes_, stream),
+                 error, "payload hash"))
+            return false;
+    }
     last_stream_ = stream;
     return true;
 }

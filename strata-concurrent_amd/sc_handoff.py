@@ -203,6 +203,9 @@ _SIGS = {
     "sc_fnv1a64_device": (C.c_int, [_P, _U64, _U64, C.POINTER(_U64)]),
     "sc_fnv1a64_noalloc_async": (C.c_int, [_P, _U64, _U64, _P, _P, _P]),
     "sc_fnv1a64_set_spin_limit": (C.c_int, [C.c_uint32]),
+    "sc_hash_map_create": (C.c_int, [C.POINTER(_P), C.c_int32, _P, _U64, C.POINTER(_P)]),
+    "sc_hash_map_launch": (C.c_int, [_P, _U64, _P, _P, _P, _U64, _P]),
+    "sc_hash_map_destroy": (C.c_int, [_P]),
     "sc_copy_device_async": (C.c_int, [_P, _P, _U64, _P]),
     "sc_ipc_export_create": (C.c_int, [_U64, _U64, C.POINTER(_P)]),
     "sc_ipc_export_count": (C.c_int32, [_P]),
@@ -694,6 +697,33 @@ class HashPlan:
         self.ws.free()
         self.out.free()
         self.fault.free()
+
+
+class HashMap:
+    """Capture plans fused with the hash of the payload they write (sc_hash_map_*): launch() gathers and hashes in one
+    read of the sources; the result and fault word land in `plan`'s words (a HashPlan sized for the payload)."""
+
+    def __init__(self, plans, payload_ptr: int, nbytes: int):
+        arr = (C.c_void_p * max(len(plans), 1))(*[p.handle for p in plans])
+        h = C.c_void_p()
+        check(lib.sc_hash_map_create(arr, len(plans), payload_ptr, nbytes, C.byref(h)), "sc_hash_map_create")
+        self.handle, self.nbytes = h.value, nbytes
+
+    def launch(self, hp: "HashPlan", seed: int = REFERENCE_FNV_SEED, stream=None) -> None:
+        check(lib.sc_hash_map_launch(self.handle, seed, hp.out.ptr, hp.fault.ptr, hp.ws.ptr, hp.ws_bytes,
+                                     _stream(stream)), "sc_hash_map_launch")
+
+    def destroy(self) -> None:
+        if self.handle:
+            check(lib.sc_hash_map_destroy(self.handle), "sc_hash_map_destroy")
+            self.handle = None
+
+    def __del__(self):
+        try:
+            if self.handle:
+                lib.sc_hash_map_destroy(self.handle)
+        except Exception:
+            pass
 
 
 @dataclass

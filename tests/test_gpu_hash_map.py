@@ -1,0 +1,148 @@
+"""The capture fused with the payload hash (sc_hash_map_*) against the capture plans launched on their own followed by
+the plain device hash, and against the oracle's byte loop.
+
+A hash map gathers the rows of capture plans (page gathers through page tables, copies, zero fills) into the payload
+and hashes the whole payload in one kernel; the bytes no row writes (a head copied in first, a page the table does not
+place) are hashed as the payload holds them.  Each case fills the payload with a pattern, runs the plans and the plain
+hash, fills it again, runs the map, and requires the same payload bytes and the same hash, which must also be the byte
+loop's (sco_fnv1a64, pinned to the published FNV-1a vectors).  Sizes cover a payload under one lane segment, tails
+that are not whole lane segments, several blobs inside one lane segment, pages that cross lane segments, and a table
+with holes.
+"""
+import numpy as np
+import pytest
+
+import sc_synthetic as synth
+
+pytestmark = pytest.mark.gpu
+
+SMALL = dict(n_layers=8, qsa_interval=4, n_head_kv=2, head_dim=256, page_size=4, ssm_state_size=32,
+             ssm_k_heads=4, ssm_v_heads=8, ssm_d_conv=4, ssm_conv_channels=520, idx_key_dim=128)
+TINY = dict(SMALL, n_layers=4, head_dim=8, page_size=1, ssm_state_size=4, ssm_v_heads=1, ssm_conv_channels=4)
+
+
+def _compare(sc, oracle, plans, payload, nbytes, pattern, head=None):
+    def reset():
+        payload.fill(pattern)
+        if head is not None:
+            payload.upload(head)
+        sc.device_sync()
+
+    hp = sc.HashPlan(nbytes)
+    reset()
+    for p in plans:
+        p.launch()
+    hp.launch(payload.ptr, nbytes)
+    sc.device_sync()
+    want_bytes, want = payload.numpy(nbytes).copy(), hp.result()
+    assert want == oracle.fnv1a64(want_bytes)
+    hmap = sc.HashMap(plans, payload.ptr, nbytes)
+    reset()
+    hp.fault.fill(0xAB)
+    hmap.launch(hp)
+    sc.device_sync()
+    got_bytes = payload.numpy(nbytes)
+    assert np.array_equal(got_bytes, want_bytes), np.flatnonzero(got_bytes != want_bytes)[:8]
+    assert hp.result() == want
+    hmap.destroy()
+    hp.free()
+
+
+@pytest.mark.parametrize("geo_kw,tokens", [(SMALL, 77), (SMALL, 1), (SMALL, 0), (TINY, 5), (TINY, 0)])
+@pytest.mark.parametrize("table", ["identity", "shuffled", "holes"])
+def test_fused_capture_equals_capture_then_hash(sc, oracle, cuda, geo_kw, tokens, table):
+    geo = sc.geometry(**geo_kw)
+    print(f"case hash map {geo.n_layers}x{geo.head_dim} {tokens} tokens {table}", flush=True)
+    case = synth.SyntheticCase(geo, tokens, seed=0x4A5 + tokens)
+    max_cells = 128
+    n_pages = max_cells // geo.page_size + 3
+    tables = None
+    if table != "identity":
+        tabs = []
+        for j in range(geo.n_qsa):
+            t = np.random.default_rng(j + tokens).permutation(n_pages)[:max_cells // geo.page_size].astype(np.int32)
+            if table == "holes":
+                t[1::3] = -1
+            tabs.append(t)
+        tables = sc.device_tables(tabs)
+    slot = case.new_slot(max_cells=max_cells, n_pages=n_pages if tables else None, tables=tables, fill=0x33)
+    case.carve_into(slot)
+    _, total = sc.image_layout(geo, tokens)
+    if total == 0:
+        pytest.skip("an empty geometry has no payload")
+    payload = sc.DeviceBuffer(total + 16, "uint8")
+    plan = sc.plan_capture(geo, slot, tokens, payload.ptr, total)
+    _compare(sc, oracle, [plan], payload, total, 0x5A)
+    plan.destroy()
+
+
+def test_fused_map_with_head_and_offsets(sc, oracle, cuda):
+    """Blobs placed at caller offsets after a head of host bytes (the wire payload's shape): two capture plans into one
+    payload (a main slot and a second slot, as a layer split's stage part), the head copied in before the launch, every
+    gap zero-filled by the rows; a total that is not a whole lane segment."""
+    geo = sc.geometry(**SMALL)
+    tokens = 53
+    a = synth.SyntheticCase(geo, tokens, seed=11)
+    b = synth.SyntheticCase(geo, tokens, seed=12)
+    sa, sb = a.new_slot(max_cells=64), b.new_slot(max_cells=64)
+    a.carve_into(sa)
+    b.carve_into(sb)
+    blobs, image = sc.image_layout(geo, tokens)
+    head = 4096 + 48
+    total = head + 2 * image + 80
+    payload = sc.DeviceBuffer(total, "uint8")
+    plans = []
+    for k, slot in enumerate((sa, sb)):
+        base = head + k * image
+        plans.append(sc.plan_capture(geo, slot, tokens, payload.ptr + base, image))
+    head_bytes = np.random.default_rng(5).integers(0, 256, size=head, dtype=np.uint8)
+    _compare(sc, oracle, plans, payload, total, 0x11, head=head_bytes)
+    for p in plans:
+        p.destroy()
+
+
+def test_fused_map_at_full_size(sc, oracle, cuda):
+    """Config 2's slot (48 layers, 32K tokens) captured into its image: the fused hash equals the plain hash of the
+    captured image, and the image equals the capture's."""
+    geo = sc.geometry()
+    tokens = 32768
+    case = synth.SyntheticCase(geo, tokens, seed=0x32)
+    slot = case.new_slot(max_cells=tokens)
+    case.carve_into(slot)
+    _, total = sc.image_layout(geo, tokens)
+    payload = sc.DeviceBuffer(total, "uint8")
+    plan = sc.plan_capture(geo, slot, tokens, payload.ptr, total)
+    hp = sc.HashPlan(total)
+    payload.fill(0x77)
+    plan.launch()
+    hp.launch(payload.ptr, total)
+    sc.device_sync()
+    want = hp.result()
+    want_bytes = sc.fnv1a64_device(payload.ptr, total)
+    hmap = sc.HashMap([plan], payload.ptr, total)
+    payload.fill(0x77)
+    hmap.launch(hp)
+    sc.device_sync()
+    assert hp.result() == want == want_bytes
+    assert sc.fnv1a64_device(payload.ptr, total) == want
+    hmap.destroy()
+    hp.free()
+
+
+def test_hash_map_refusals(sc, cuda):
+    geo = sc.geometry(**SMALL)
+    case = synth.SyntheticCase(geo, 9, seed=3)
+    slot = case.new_slot(max_cells=16)
+    _, total = sc.image_layout(geo, 9)
+    payload = sc.DeviceBuffer(total + 64, "uint8")
+    carve = sc.plan_carve(geo, case.prefill, slot)
+    with pytest.raises(sc.ScError) as e:
+        sc.HashMap([carve], payload.ptr, total)
+    assert e.value.code == sc.SC_EINVAL and "capture plans" in sc.last_error()
+    capture = sc.plan_capture(geo, slot, 9, payload.ptr, total)
+    with pytest.raises(sc.ScError):
+        sc.HashMap([capture], payload.ptr, total - 64)        # a row past the payload
+    with pytest.raises(sc.ScError):
+        sc.HashMap([capture], payload.ptr + 8, total)         # misaligned
+    with pytest.raises(sc.ScError):
+        sc.HashMap([capture, capture], payload.ptr, total)    # two rows on the same bytes
