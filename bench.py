@@ -43,6 +43,10 @@ def measured_traffic() -> int | None:
         pass
     return None
 HBM_PEAK_GBPS = 8000.0
+# BASELINE.json's model geometry (the headline's slot) and the 18 geometry fields its wire payloads carry
+HEADLINE_GEO = dict(n_layers=48, qsa_interval=4, n_head_kv=2, head_dim=256, page_size=4, ssm_state_size=128,
+                    ssm_k_heads=16, ssm_v_heads=32, ssm_d_conv=4, ssm_conv_channels=8192, idx_key_dim=128)
+WIRE_GEOKEY = [2560, 48, 4, 128, 16, 32, 4, 8192, 4096, 24, 2, 256, 128, 4, 4, 3, 1, 0]
 
 
 def synth():
@@ -475,9 +479,8 @@ def wire_payload(sc, geo, tokens: int, slot, link_h2d: float, link_d2h: float, r
     runs twice per handoff (encode, then the reader's check)."""
     import numpy as np
     import sc_wire
-    geokey = [2560, 48, 4, 128, 16, 32, 4, 8192, 4096, 24, 2, 256, 128, 4, 4, 3, 1, 0]
     ids = (np.arange(tokens, dtype=np.int64) % 151_000).astype(np.int32)
-    live, keep = sc_wire.make_live(geokey, ids, layer_hi=48, idx_dim=128)
+    live, keep = sc_wire.make_live(WIRE_GEOKEY, ids, layer_hi=48, idx_dim=128)
     enc = sc_wire.Encoder(geo, slot, tokens, live, 0x1122334455667788, 0x0AABBCCDDEEFF001)
     n = enc.bytes
     payload = sc.DeviceBuffer(n, "uint8")
@@ -847,55 +850,80 @@ def arena_cpu_baseline(sc, budget_bytes: int = 1 << 30) -> dict:
             "handoff_gbps": round(n / (best_w + best_r) / 1e9, 2), "cores": 1, "kind": "port"}
 
 
-def ipc_export_role(capacity: int) -> int:
-    """The exporting process of the same-GPU row (started by ipc_handoff): a payload-sized device buffer, segments of
-    1 GiB exported, and on every "stage" line one timed staging copy, answered with its time and the device hash."""
+def ipc_export_role(tokens: int) -> int:
+    """The exporting process of the same-GPU row (started by ipc_handoff): a decode slot of the headline geometry
+    holding `tokens` tokens (seeded values), segments of 1 GiB exported, and on every "encode" line the slot's wire
+    payload encoded straight into the exported segments (no payload buffer, no staging copy), answered with the
+    encode's device time and the payload hash."""
+    import numpy as np
     import sc_handoff as sc
+    import sc_wire
+    geo = sc.geometry(**HEADLINE_GEO)
     stream = sc.Stream()
-    payload = sc.DeviceBuffer(capacity, "uint8")
-    sc.check(sc.lib.sc_fill_uniform_f16(payload.ptr, capacity // 2, -1.0, 1.0, 5, 0, stream.handle), "fill")
+    slot = sc.new_slot(geo, tokens, fill=0)
+    for i, b in enumerate(slot.buffers()):
+        sc.check(sc.lib.sc_fill_uniform_f16(b.ptr, b.nbytes // 2, -1.0, 1.0, 5, i, stream.handle), "fill")
     stream.sync()
-    ex = sc.IpcExport(capacity, sc.IPC_MAX_SEGMENT)
-    print(json.dumps({"segments": [[h.hex(), n] for h, n in ex.segments()],
-                      "hash": sc.fnv1a64_device(payload.ptr, capacity)}), flush=True)
+    ids = (np.arange(tokens, dtype=np.int64) % 151_000).astype(np.int32)
+    live, keep = sc_wire.make_live(WIRE_GEOKEY, ids, layer_hi=48, idx_dim=128)
+    enc = sc_wire.Encoder(geo, slot, tokens, live, 0x1122334455667788, 0x0AABBCCDDEEFF001)
+    n = enc.bytes
+    ex = sc.IpcExport(n, sc.IPC_MAX_SEGMENT)
+    ptrs, seg = ex.layout()
+    print(json.dumps({"segments": [[h.hex(), k] for h, k in ex.segments()], "bytes": n,
+                      "buffers": [sc.fnv1a64_device(b.ptr, b.nbytes) for b in slot.buffers()]}), flush=True)
     e0, e1 = sc.Event(), sc.Event()
     for line in sys.stdin:
-        if line.strip() != "stage":
+        if line.strip() != "encode":
             break
         e0.record(stream)
-        ex.stage(payload.ptr, capacity, stream)
+        enc.encode_segments(ptrs, seg, stream)
         e1.record(stream)
         e1.sync()
-        print(json.dumps({"stage_ms": e0.elapsed_ms(e1)}), flush=True)
+        print(json.dumps({"encode_ms": e0.elapsed_ms(e1), "hash": enc.hash()}), flush=True)
+    enc.destroy()
     ex.destroy()
     return 0
 
 
-def ipc_handoff(sc, nbytes: int, reps: int = 5) -> dict:
-    """The same-GPU row: a payload of `nbytes` handed from another process on this GPU through exported device
-    segments (one staging copy in the exporter, one fetch copy here), against the HBM roofline of the two copies."""
+def ipc_handoff(sc, geo, tokens: int, reps: int = 5) -> dict:
+    """The same-GPU row, zero-copy: another process on this GPU encodes its slot's wire payload straight into device
+    segments it exports, and this process mounts the payload where it lies in the imported segments (the hash checked
+    over the segments on the device, then one gated scatter launch straight from them).  No payload buffer, staging copy
+    or fetch copy exists on either side; the hand-off is the encode plus the mount."""
     import subprocess
-    proc = subprocess.Popen([sys.executable, "-u", __file__, "--ipc-export", str(nbytes)], stdin=subprocess.PIPE,
+    import sc_wire
+    proc = subprocess.Popen([sys.executable, "-u", __file__, "--ipc-export", str(tokens)], stdin=subprocess.PIPE,
                             stdout=subprocess.PIPE, text=True)
     imp = None
     try:
         first = json.loads(proc.stdout.readline())
-        imp = sc.IpcImport([(bytes.fromhex(h), n) for h, n in first["segments"]])
-        dst = sc.DeviceBuffer(nbytes, "uint8")
+        n = first["bytes"]
+        imp = sc.IpcImport([(bytes.fromhex(h), k) for h, k in first["segments"]])
+        ptrs, seg = imp.layout()
+        dst = sc.new_slot(geo, tokens, fill=0)
         stream = sc.Stream()
         e0, e1 = sc.Event(), sc.Event()
-        stage, fetch = [], []
+        enc_ms, open_ms, mount_ms, mount_dev_ms = [], [], [], []
         for _ in range(reps + 1):
-            proc.stdin.write("stage\n")
+            proc.stdin.write("encode\n")
             proc.stdin.flush()
-            stage.append(json.loads(proc.stdout.readline())["stage_ms"])
+            r = json.loads(proc.stdout.readline())
+            enc_ms.append(r["encode_ms"])
+            t0 = time.perf_counter()
+            dec = sc_wire.Decoder(0, n, geo, dst, payload_hash=r["hash"], check_hash=True, segments=(ptrs, seg))
+            t1 = time.perf_counter()
             e0.record(stream)
-            imp.fetch(dst.ptr, nbytes, stream)
+            dec.restore(stream)
             e1.record(stream)
+            mount_ms.append((time.perf_counter() - t1) * 1e3)
             e1.sync()
-            fetch.append(e0.elapsed_ms(e1))
-        same = sc.fnv1a64_device(dst.ptr, nbytes) == first["hash"]
-        dst.free()
+            mount_dev_ms.append(e0.elapsed_ms(e1))
+            open_ms.append((t1 - t0) * 1e3)
+            dec.destroy()
+        same = [sc.fnv1a64_device(b.ptr, b.nbytes) for b in dst.buffers()] == first["buffers"]
+        for b in dst.buffers():
+            b.free()
     finally:
         if imp:
             imp.close()
@@ -904,17 +932,22 @@ def ipc_handoff(sc, nbytes: int, reps: int = 5) -> dict:
             proc.stdin.flush()
         except BrokenPipeError:
             pass
-        proc.wait(timeout=60)
-    st, fe = min(stage[1:]), min(fetch[1:])
-    hbm = lambda ms: round(2 * nbytes / (ms * 1e-3) / 1e9, 1)   # noqa: E731
-    return {"payload_bytes": nbytes, "segments": len(first["segments"]), "stage_ms": round(st, 3),
-            "fetch_ms": round(fe, 3), "handoff_ms": round(st + fe, 3),
-            "handoff_gbps": round(nbytes / ((st + fe) * 1e-3) / 1e9, 1), "stage_hbm_gbps": hbm(st),
-            "fetch_hbm_gbps": hbm(fe), "fetch_frac": round(hbm(fe) / HBM_PEAK_GBPS, 4), "bit_exact": bool(same),
-            "method": "exporter process: payload staged into 1 GiB hipMalloc segments exported with hipIpcGetMemHandle "
-                      "(device copy kernel, HIP events); importer (this process): segments opened once with "
-                      "hipIpcOpenMemHandle, payload fetched into its own buffer by the same kernel; best of the reps "
-                      "after one warm-up; HBM bytes = 2 x payload per copy"}
+        proc.wait(timeout=120)
+
+    def p50(xs):
+        return sorted(xs[1:])[len(xs[1:]) // 2]
+    en, mo = p50(enc_ms), p50(mount_ms)
+    return {"tokens": tokens, "payload_bytes": n, "segments": len(ptrs), "segment_bytes": seg,
+            "encode_ms": round(en, 3), "mount_ms": round(mo, 3), "mount_device_ms": round(p50(mount_dev_ms), 3),
+            "open_ms": round(p50(open_ms), 3), "handoff_ms": round(en + mo, 3),
+            "handoff_gbps": round(n / ((en + mo) * 1e-3) / 1e9, 1), "copies": 0, "bit_exact": bool(same),
+            "timing": f"p50 of {reps} hand-offs after one warm-up",
+            "method": "exporter process: the slot's payload encoded into 1 GiB hipMalloc segments exported with "
+                      "hipIpcGetMemHandle (head copies + the fused gather and FNV-1a, cut at segment ends; HIP events); "
+                      "importer (this process): segments opened once with hipIpcOpenMemHandle, the payload mounted "
+                      "from them (device FNV-1a over the segments leaving a verdict, one scatter launch gated by it, "
+                      "reading the segments; host wall time of the synchronous restore); handoff_ms = encode + mount; "
+                      "bit_exact = every destination slot buffer's device hash equals the exporter's source buffer's"}
 
 
 def copy_ceiling(sc, nbytes: int, stream, reps: int = 5) -> dict:
@@ -1030,7 +1063,7 @@ def main() -> int:
                     help="only the hand-off arena row of the same geometry; prints its JSON")
     ap.add_argument("--mover", default="64,4,8", help="arena mover chunk MiB, depth, threads")
     ap.add_argument("--ipc-only", action="store_true", help="only the same-GPU inter-process row; prints its JSON")
-    ap.add_argument("--ipc-export", type=int, default=0, metavar="BYTES", help=argparse.SUPPRESS)
+    ap.add_argument("--ipc-export", type=int, default=0, metavar="TOKENS", help=argparse.SUPPRESS)
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run 5 device-to-device copies of BYTES (the counter calibration of profiler runs)")
     args = ap.parse_args()
@@ -1061,8 +1094,7 @@ def main() -> int:
         return 0
     # the host link, measured before anything large is allocated (the reference's probe method, both directions)
     h2d, d2h = sc.probe_link(256 << 20, 4)
-    geo_kw = dict(n_layers=48, qsa_interval=4, n_head_kv=2, head_dim=256, page_size=4, ssm_state_size=128,
-                  ssm_k_heads=16, ssm_v_heads=32, ssm_d_conv=4, ssm_conv_channels=8192, idx_key_dim=128)
+    geo_kw = HEADLINE_GEO
     geo = sc.geometry(**geo_kw)
     T = args.tokens
     P = sc.payload_bytes(geo, T)
@@ -1071,7 +1103,7 @@ def main() -> int:
         print(json.dumps({"quant_carve": quant_carve(sc, geo, T, stream)}), flush=True)
         return 0
     if args.ipc_only:
-        print(json.dumps({"ipc_handoff": ipc_handoff(sc, P)}), flush=True)
+        print(json.dumps({"ipc_handoff": ipc_handoff(sc, geo, T)}), flush=True)
         return 0
     if args.config5_only:
         print(json.dumps({"config5": config5(sc, geo, 0x5EED)}), flush=True)
@@ -1299,10 +1331,10 @@ def main() -> int:
         result["arena_handoff"]["cpu_baseline"] = arena_cpu_baseline(sc, 512 << 20)
         result["wire_payload"]["cpu_baseline"] = wire_cpu_baseline(geo_kw, 8192)
     log("same-GPU hand-off between processes: exported device segments")
-    result["ipc_handoff"] = ipc_handoff(sc, P)
+    result["ipc_handoff"] = ipc_handoff(sc, geo, T)
     ih = result["ipc_handoff"]
-    log(f"ipc: stage {ih['stage_ms']} ms + fetch {ih['fetch_ms']} ms = {ih['handoff_gbps']} GB/s, bit-exact "
-        f"{ih['bit_exact']}")
+    log(f"ipc: encode {ih['encode_ms']} ms + mount {ih['mount_ms']} ms = {ih['handoff_ms']} ms "
+        f"({ih['handoff_gbps']} GB/s), no copies, bit-exact {ih['bit_exact']}")
 
     log("quantizing carve: int8 / q4_0 / K8V4 pools from f32 rows, 128K")
     result["quant_carve"] = quant_carve(sc, geo, T, stream)

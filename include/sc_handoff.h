@@ -125,6 +125,14 @@ typedef struct sc_image_blob {
 
 typedef struct sc_plan sc_plan;   /* a device-resident handoff table plus its launch shape */
 typedef struct sc_hash_map sc_hash_map;   /* capture plans' rows as the sources of a payload, for the fused hash */
+/* A payload held in segments rather than one allocation (the same-GPU hand-off's exported segments, each its own
+ * allocation of at most SC_IPC_MAX_SEGMENT bytes): payload byte o lives at ptr[o / segment_bytes] + o % segment_bytes,
+ * every segment but the last holding segment_bytes (a multiple of 64 KiB), the last the rest. */
+typedef struct sc_segments {
+    int32_t n;                /* segments, 1 .. SC_IPC_MAX_SEGMENTS */
+    uint64_t segment_bytes;   /* bytes of each segment but the last */
+    void* const* ptr;         /* [n] 16-byte aligned device pointers, host array */
+} sc_segments;
 
 /* ---- errors ---------------------------------------------------------------------------------------------- */
 
@@ -303,6 +311,14 @@ int sc_plan_capture_layers(const sc_geometry* g, const sc_slot_layers* src, int6
  * restore (conversation_state.cpp:251).  Bytes of the slot past the image's cells and rows are left as they are. */
 int sc_plan_scatter_layers(const sc_geometry* g, const void* src, uint64_t src_bytes, const sc_layers_map* map,
                            int64_t tokens, const sc_slot_layers* dst, sc_plan** out);
+/* The scatters of sc_plan_scatter_map / sc_plan_scatter_layers from a segmented payload (a payload mounted straight
+ * from another process's exported segments): the blob map's offsets are payload offsets, and a blob a segment boundary
+ * cuts is read from both segments (the page-scatter rows of its pieces keep their place in its pages). */
+int sc_plan_scatter_map_segments(const sc_geometry* g, const sc_segments* src, uint64_t src_bytes,
+                                 const sc_blob_map* map, int64_t tokens, const sc_decode_slot* dst, sc_plan** out);
+int sc_plan_scatter_layers_segments(const sc_geometry* g, const sc_segments* src, uint64_t src_bytes,
+                                    const sc_layers_map* map, int64_t tokens, const sc_slot_layers* dst,
+                                    sc_plan** out);
 /* Park / resume of a slot in any format to / from a pinned host image of sc_image_layout_layers, one hipMemcpyAsync per
  * blob on `stream`, `done` recorded after the last (as sc_park_async / sc_resume_async for f16 slots). */
 int sc_park_layers_async(const sc_geometry* g, const sc_slot_layers* slot, int64_t tokens, void* host_image,
@@ -487,6 +503,18 @@ int sc_fnv1a64_noalloc_async(const void* data, uint64_t bytes, uint64_t seed, ui
 int sc_hash_map_create(const sc_plan* const* plans, int32_t n_plans, void* payload, uint64_t bytes, sc_hash_map** out);
 int sc_hash_map_launch(const sc_hash_map* map, uint64_t seed, uint64_t* out, uint32_t* fault, void* workspace,
                        uint64_t workspace_bytes, void* stream);
+/* sc_hash_map_create for a segmented payload: the plans were built for a contiguous payload at `frame` (any 16-byte
+ * aligned address: they are never launched, and may be destroyed once the map exists), and the map writes their rows'
+ * bytes into the segments of `into` instead, at the same payload offsets. */
+int sc_hash_map_create_segments(const sc_plan* const* plans, int32_t n_plans, const void* frame, uint64_t bytes,
+                                const sc_segments* into, sc_hash_map** out);
+/* A map that only hashes a segmented payload where it lies (nothing is written): the hash of a payload spread over
+ * imported segments, in one launch. */
+int sc_hash_map_create_read(const sc_segments* from, uint64_t bytes, sc_hash_map** out);
+/* sc_hash_map_launch that also leaves the verdict of sc_fnv1a64_check_async at `verdict` (the gate of
+ * sc_plan_launch_gated); `fault` is optional here. */
+int sc_hash_map_check_async(const sc_hash_map* map, uint64_t seed, uint64_t expected, uint64_t* out, uint32_t* verdict,
+                            uint32_t* fault, void* workspace, uint64_t workspace_bytes, void* stream);
 int sc_hash_map_destroy(sc_hash_map* map);
 /* The bound on each of the hash kernel's look-back waits, in reads of its window (0 restores the default, 65536, about
  * 0.2 s).  No counterpart in the reference: a workgroup only waits on workgroups that are running or done, so a
@@ -572,6 +600,14 @@ int sc_ipc_export_destroy(sc_ipc_export* ex);
 int sc_ipc_import_open(const sc_ipc_segment* segments, int32_t n_segments, sc_ipc_import** out);
 /* Copy the first `bytes` of the segments into `device_dst`, on `stream`. */
 int sc_ipc_import_fetch(sc_ipc_import* im, void* device_dst, uint64_t bytes, void* stream);
+/* The zero-copy form of the hand-off: the segments' device addresses in payload order (`ptr`, room for `max_segments`)
+ * and the size of every segment but the last, which is an sc_segments over them, for sc_wire_encode_segments_async
+ * on the exporter's side and sc_wire_decoder_open_segments on the importer's.  The encode then writes the payload
+ * straight into the exported segments and the mount hashes and scatters it straight out of the imported ones: neither
+ * sc_ipc_export_stage nor sc_ipc_import_fetch runs.  (The hash needs segment_bytes to be a multiple of 64 KiB, as
+ * SC_IPC_MAX_SEGMENT is.) */
+int sc_ipc_export_layout(const sc_ipc_export* ex, void** ptr, int32_t max_segments, int32_t* n, uint64_t* segment_bytes);
+int sc_ipc_import_layout(const sc_ipc_import* im, void** ptr, int32_t max_segments, int32_t* n, uint64_t* segment_bytes);
 /* Unmap the segments (before the exporter frees them). */
 int sc_ipc_import_close(sc_ipc_import* im);
 

@@ -84,6 +84,11 @@ uint64_t sc_wire_encoder_pool_offset(const sc_wire_encoder* e);
  * event and overlap the hash.  Replaces conversation_wire_encode's walk and byte-serial hash
  * (src/core/conversation_wire.cpp:400-480, 1006-1025). */
 int sc_wire_encode_async(sc_wire_encoder* e, void* payload, uint64_t capacity, void* stream, void* gathered);
+/* The encode into a payload held in segments (`into`, sc_handoff.h: the same-GPU hand-off's exported segments, each at
+ * most SC_IPC_MAX_SEGMENT bytes, segment_bytes a multiple of 64 KiB): the head and small blobs copied into their
+ * segments and the blobs gathered into them by the fused gather + hash, cut wherever a segment ends.  The bytes are
+ * exactly sc_wire_encode_async's, and no contiguous copy of the payload exists at any point. */
+int sc_wire_encode_segments_async(sc_wire_encoder* e, const sc_segments* into, void* stream);
 /* The payload hash of the last encode (waits for it): WireEncoded::payload_hash.  SC_ETIMEOUT, and no hash, when the
  * device hash did not complete (a bounded wait of its kernel ran out, sc_fnv1a64_async): encode again. */
 int sc_wire_encoder_hash(sc_wire_encoder* e, uint64_t* hash);
@@ -109,6 +114,17 @@ int sc_wire_decoder_open_split(const void* payload, uint64_t bytes, const sc_geo
 int sc_wire_decoder_open_layers(const void* payload, uint64_t bytes, const sc_geometry* g, const sc_slot_layers* slot,
                                 const int64_t* geometry, uint64_t geom_hash, uint64_t pack_hash, int32_t check_identity,
                                 uint64_t payload_hash, int32_t check_hash, sc_wire_decoder** out);
+/* sc_wire_decoder_open / _open_layers for a payload held in segments (another process's exported segments, imported
+ * with sc_ipc_import_open): the head is read from them, the restore hashes the payload where it lies (one launch) and
+ * scatters every blob straight from them, so nothing is fetched into a contiguous buffer first. */
+int sc_wire_decoder_open_segments(const sc_segments* from, uint64_t bytes, const sc_geometry* g,
+                                  const sc_decode_slot* slot, const int64_t* geometry, uint64_t geom_hash,
+                                  uint64_t pack_hash, int32_t check_identity, uint64_t payload_hash, int32_t check_hash,
+                                  sc_wire_decoder** out);
+int sc_wire_decoder_open_layers_segments(const sc_segments* from, uint64_t bytes, const sc_geometry* g,
+                                         const sc_slot_layers* slot, const int64_t* geometry, uint64_t geom_hash,
+                                         uint64_t pack_hash, int32_t check_identity, uint64_t payload_hash,
+                                         int32_t check_hash, sc_wire_decoder** out);
 /* Tokens the payload carries (its live token count). */
 int64_t sc_wire_decoder_tokens(const sc_wire_decoder* d);
 /* Verifies the payload hash on the device (when asked), then scatters the K/V and GDN rows into the slot in one launch

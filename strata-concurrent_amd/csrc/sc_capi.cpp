@@ -49,8 +49,9 @@ hipError_t launch_ring_table(int32_t* table, int64_t n_blocks, int64_t n_slots, 
 hipError_t launch_fnv1a64(const void* data, uint64_t n, uint64_t seed, const uint64_t* seed_dev, uint64_t* out,
                           uint32_t* fault_out, void* workspace, hipStream_t stream, uint64_t expected = 0,
                           uint32_t* verdict = nullptr);
-hipError_t launch_fnv1a64_mapped(const HashMapArgs& map, uint64_t seed, uint64_t* out, uint32_t* fault_out,
-                                 void* workspace, hipStream_t stream);
+hipError_t launch_fnv1a64_mapped(const HashMapArgs& map, const uint8_t* tail, uint64_t seed, uint64_t* out,
+                                 uint32_t* fault_out, void* workspace, hipStream_t stream, uint64_t expected = 0,
+                                 uint32_t* verdict = nullptr);
 
 static uint64_t host_mix64(uint64_t z) {
     z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
@@ -88,10 +89,13 @@ struct sc_plan {
 };
 
 struct sc_hash_map {
-    sc::HashExtent* ext_dev = nullptr;   // one device block: the extents, then each workgroup's first extent
+    sc::HashExtent* ext_dev = nullptr;   // one device block: the extents, each workgroup's first extent, the segments
     uint32_t* first_dev = nullptr;
-    uint8_t* payload = nullptr;
+    uint8_t** seg_dev = nullptr;
+    uint64_t seg_bytes = 0;
+    const uint8_t* tail = nullptr;       // device address of the payload's last partial lane segment
     uint64_t bytes = 0;
+    bool store = true;
 };
 
 namespace {
@@ -263,6 +267,7 @@ OrderPlan order_plan(const std::vector<sc::MoveRow>& rows, const Geo& g) {
     for (size_t k = 0; k < rows.size(); ++k) {
         const sc::MoveRow& r = rows[k];
         if (!r.table || !r.n || !orderable_kind(r.kind)) continue;
+        if (r.kind == sc::kPagesScatter && r.pos0 != 0) continue;   // a piece of a split blob keeps the source order
         int64_t lo, hi;
         table_pages_of(r, g, lo, hi);
         int gi = -1;
@@ -1091,10 +1096,36 @@ static int page_plan(const sc_geometry* g, const void* image, uint64_t image_byt
     return finish_plan(rows, o, kv_payload(o, cells) + uint64_t(o.n_gdn) * o.gdn_row_bytes, out);
 }
 
+// A scatter from a segmented payload: each row reading payload bytes [off, off + 16 n) of `frame` is cut where a
+// segment ends, every piece reading its own segment.  A page-scatter piece keeps its place in the blob's pages (pos0:
+// the chunks of the blob before it); a copy piece moves its destination with it.
+struct SegSpec {
+    const uint8_t* frame;
+    std::vector<uint8_t*> ptr;
+    uint64_t bytes;   // of every segment but the last
+};
+void split_rows_at_segments(std::vector<sc::MoveRow>& rows, const SegSpec& seg) {
+    std::vector<sc::MoveRow> out;
+    for (const sc::MoveRow& r : rows) {
+        const uint64_t off = uint64_t(r.src - seg.frame), end = off + r.n * 16;
+        for (uint64_t o = off; o < end;) {
+            const uint64_t k = o / seg.bytes, stop = std::min(end, (k + 1) * seg.bytes);
+            sc::MoveRow piece = r;
+            piece.src = seg.ptr[size_t(k)] + (o - k * seg.bytes);
+            piece.n = (stop - o) / 16;
+            if (r.kind == sc::kPagesScatter) piece.pos0 = r.pos0 + int64_t((o - off) / 16);
+            else piece.dst = r.dst + (o - off);
+            out.push_back(piece);
+            o = stop;
+        }
+    }
+    rows = std::move(out);
+}
+
 // Capture / scatter with caller-placed blobs: the K and V blob of QSA layer j at k_off[j] / v_off[j] and the GDN rows
 // at gdn_off inside one buffer, plus zero-filled ranges (capture only).  Everything is checked before the plan exists.
 static int map_plan(const sc_geometry* g, void* buf, uint64_t buf_bytes, const sc_blob_map* map, int64_t tokens,
-                    const sc_decode_slot* slot, bool scatter, sc_plan** out) {
+                    const sc_decode_slot* slot, bool scatter, sc_plan** out, const SegSpec* seg = nullptr) {
     if (!out) return fail(SC_EINVAL, "sc_handoff: missing plan output");
     Geo o;
     std::string why;
@@ -1159,6 +1190,7 @@ static int map_plan(const sc_geometry* g, void* buf, uint64_t buf_bytes, const s
         r.n = map->zero[2 * z + 1] / 16;
         if (r.n) rows.push_back(r);
     }
+    if (seg) split_rows_at_segments(rows, *seg);
     return finish_plan(rows, o, 2 * kv_bytes * uint64_t(o.n_qsa) + gdn_bytes, out);
 }
 
@@ -1217,7 +1249,7 @@ int sc_image_layout_layers(const sc_geometry* g, int32_t format, int32_t with_in
 // One launch moving every blob of an sc_slot_layers slot between the slot (identity pools: a blob is a prefix of
 // its buffer) and a buffer laid out by `map` (or the standard image when map is NULL).
 static int layers_plan(const sc_geometry* g, void* buf, uint64_t buf_bytes, const sc_layers_map* map, int64_t tokens,
-                       const sc_slot_layers* slot, bool scatter, sc_plan** out) {
+                       const sc_slot_layers* slot, bool scatter, sc_plan** out, const SegSpec* seg = nullptr) {
     if (!out) return fail(SC_EINVAL, "sc_handoff: missing plan output");
     Geo o;
     std::string why;
@@ -1304,6 +1336,7 @@ static int layers_plan(const sc_geometry* g, void* buf, uint64_t buf_bytes, cons
         r.n = zero[z + 1] / 16;
         if (r.n) rows.push_back(r);
     }
+    if (seg) split_rows_at_segments(rows, *seg);
     return finish_plan(rows, o, moved, out);
 }
 
@@ -1315,6 +1348,40 @@ int sc_plan_capture_layers(const sc_geometry* g, const sc_slot_layers* src, int6
 int sc_plan_scatter_layers(const sc_geometry* g, const void* src, uint64_t src_bytes, const sc_layers_map* map,
                            int64_t tokens, const sc_slot_layers* dst, sc_plan** out) {
     return guarded([&] { return layers_plan(g, const_cast<void*>(src), src_bytes, map, tokens, dst, true, out); });
+}
+
+// The segments of a segmented payload of `bytes`, as a SegSpec whose frame is the first segment.
+static int seg_spec(const sc_segments* s, uint64_t bytes, SegSpec& spec) {
+    if (!s || s->n < 1 || s->n > SC_IPC_MAX_SEGMENTS || !s->ptr || s->segment_bytes == 0 || s->segment_bytes % 16)
+        return fail(SC_EINVAL, "sc_handoff: a segmented payload needs 1 to SC_IPC_MAX_SEGMENTS segments of whole chunks");
+    if (uint64_t(s->n) < (bytes + s->segment_bytes - 1) / s->segment_bytes)
+        return fail(SC_ERANGE, "sc_handoff: the segments are smaller than the payload");
+    spec.ptr.clear();
+    for (int32_t k = 0; k < s->n; ++k) spec.ptr.push_back(static_cast<uint8_t*>(s->ptr[k]));
+    for (uint8_t* q : spec.ptr)
+        if (!q || !aligned16(q)) return fail(SC_EINVAL, "sc_handoff: every segment is 16-byte aligned device memory");
+    spec.frame = spec.ptr[0];
+    spec.bytes = s->segment_bytes;
+    return SC_OK;
+}
+
+int sc_plan_scatter_map_segments(const sc_geometry* g, const sc_segments* src, uint64_t src_bytes,
+                                 const sc_blob_map* map, int64_t tokens, const sc_decode_slot* dst, sc_plan** out) {
+    return guarded([&] {
+        SegSpec spec;
+        if (const int rc = seg_spec(src, src_bytes, spec)) return rc;
+        return map_plan(g, const_cast<uint8_t*>(spec.frame), src_bytes, map, tokens, dst, true, out, &spec);
+    });
+}
+
+int sc_plan_scatter_layers_segments(const sc_geometry* g, const sc_segments* src, uint64_t src_bytes,
+                                    const sc_layers_map* map, int64_t tokens, const sc_slot_layers* dst,
+                                    sc_plan** out) {
+    return guarded([&] {
+        SegSpec spec;
+        if (const int rc = seg_spec(src, src_bytes, spec)) return rc;
+        return layers_plan(g, const_cast<uint8_t*>(spec.frame), src_bytes, map, tokens, dst, true, out, &spec);
+    });
 }
 
 namespace {
@@ -1381,92 +1448,183 @@ int sc_plan_destroy(sc_plan* plan) {
 
 // ---- capture plans fused with the payload hash -------------------------------------------------------------------
 
+}  // extern "C"
+
+namespace {
+// The extents of the payload [0, bytes) that `n_plans` capture plans write, their rows' destinations taken relative to
+// `frame` (the payload they were built for); the bytes no row writes become self extents.
+int capture_extents(const sc_plan* const* plans, int32_t n_plans, const uint8_t* frame, uint64_t bytes,
+                    std::vector<sc::HashExtent>& ext) {
+    std::vector<sc::HashExtent> rows;
+    for (int32_t i = 0; i < n_plans; ++i) {
+        const sc_plan* p = plans[i];
+        if (!p || p->batch) return fail(SC_EINVAL, "sc_handoff: a hash map reads the rows of capture plans");
+        for (const sc::MoveRow& r : p->host_rows) {
+            sc::HashExtent x{};
+            switch (r.kind) {
+                case sc::kCopy: x.kind = sc::kExtCopy; x.src = r.src; break;
+                case sc::kZero: x.kind = sc::kExtZero; break;
+                case sc::kPagesGather:
+                    x.kind = sc::kExtPages;
+                    x.src = r.src;
+                    x.table = r.table;
+                    x.ld = r.ld;
+                    x.page_chunks = p->geo.page_chunks.d;
+                    break;
+                default:
+                    return fail(SC_EINVAL, "sc_handoff: only capture plans (page gathers, copies and zero fills into "
+                                           "the payload) can be fused with its hash");
+            }
+            if (r.dst < frame || uint64_t(r.dst - frame) > bytes || r.n * 16 > bytes - uint64_t(r.dst - frame))
+                return fail(SC_EINVAL, "sc_handoff: a row of the plan writes outside the hashed payload");
+            x.off = uint64_t(r.dst - frame);
+            x.end = x.off + r.n * 16;
+            if (x.end > x.off) rows.push_back(x);
+        }
+    }
+    std::sort(rows.begin(), rows.end(), [](const sc::HashExtent& a, const sc::HashExtent& b) { return a.off < b.off; });
+    ext.clear();
+    uint64_t at = 0;
+    for (const sc::HashExtent& x : rows) {
+        if (x.off < at) return fail(SC_EINVAL, "sc_handoff: two rows of the plans write the same payload bytes");
+        if (x.off > at) ext.push_back(sc::HashExtent{at, x.off, nullptr, nullptr, 0, sc::kExtSelf, 0});
+        ext.push_back(x);
+        at = x.end;
+    }
+    if (at < bytes || ext.empty()) ext.push_back(sc::HashExtent{at, bytes, nullptr, nullptr, 0, sc::kExtSelf, 0});
+    return SC_OK;
+}
+
+// Checks a segmented payload of `bytes` and lists its segments.
+int segment_list(const sc_segments* s, uint64_t bytes, std::vector<uint8_t*>& segs) {
+    if (!s || s->n < 1 || s->n > SC_IPC_MAX_SEGMENTS || !s->ptr)
+        return fail(SC_EINVAL, "sc_handoff: a segmented payload needs 1 to SC_IPC_MAX_SEGMENTS segments");
+    if (s->segment_bytes == 0 || s->segment_bytes % uint64_t(sc::kFnvGroupBytes))
+        return fail(SC_EINVAL, "sc_handoff: segments of a hashed payload are whole multiples of 64 KiB");
+    if (uint64_t(s->n) < (bytes + s->segment_bytes - 1) / s->segment_bytes)
+        return fail(SC_ERANGE, "sc_handoff: the segments are smaller than the payload");
+    segs.clear();
+    for (int32_t k = 0; k < s->n; ++k) segs.push_back(static_cast<uint8_t*>(s->ptr[k]));
+    for (uint8_t* q : segs)
+        if (!q || !aligned16(q)) return fail(SC_EINVAL, "sc_handoff: every segment is 16-byte aligned device memory");
+    return SC_OK;
+}
+
+// Uploads a map: the extents, each workgroup's first extent and the segment table, in one device block.
+int make_hash_map(const std::vector<sc::HashExtent>& ext, uint64_t bytes, const std::vector<uint8_t*>& segs,
+                  uint64_t seg_bytes, bool store, sc_hash_map** out) {
+    const sc::FnvWorkspace w = sc::fnv_workspace(bytes);
+    std::vector<uint32_t> first(std::max<uint64_t>(w.groups, 1), 0);
+    size_t e = 0;
+    for (uint64_t g = 0; g < w.groups; ++g) {
+        const uint64_t o = g * uint64_t(sc::kFnvGroupBytes);
+        while (e + 1 < ext.size() && ext[e].end <= o) ++e;
+        first[g] = uint32_t(e);
+    }
+    auto* m = new (std::nothrow) sc_hash_map();
+    if (!m) return fail(SC_ENOMEM, "sc_handoff: hash map allocation failed");
+    const uint64_t ext_bytes = round_up(ext.size() * sizeof(sc::HashExtent), 256);
+    const uint64_t first_bytes = round_up(first.size() * 4, 256);
+    hipError_t err = hipMalloc(reinterpret_cast<void**>(&m->ext_dev), ext_bytes + first_bytes + segs.size() * 8);
+    if (err != hipSuccess) {
+        delete m;
+        return fail(SC_ENOMEM, std::string("sc_handoff: hash map: ") + hipGetErrorString(err));
+    }
+    uint8_t* block = reinterpret_cast<uint8_t*>(m->ext_dev);
+    m->first_dev = reinterpret_cast<uint32_t*>(block + ext_bytes);
+    m->seg_dev = reinterpret_cast<uint8_t**>(block + ext_bytes + first_bytes);
+    err = hipMemcpy(m->ext_dev, ext.data(), ext.size() * sizeof(sc::HashExtent), hipMemcpyHostToDevice);
+    if (err == hipSuccess) err = hipMemcpy(m->first_dev, first.data(), first.size() * 4, hipMemcpyHostToDevice);
+    if (err == hipSuccess) err = hipMemcpy(m->seg_dev, segs.data(), segs.size() * 8, hipMemcpyHostToDevice);
+    if (err != hipSuccess) {
+        (void) hipFree(m->ext_dev);
+        delete m;
+        return hip_fail(err, "hash map upload");
+    }
+    const uint64_t n_full = bytes & ~uint64_t(sc::kFnvLaneBytes - 1);
+    m->seg_bytes = seg_bytes;
+    m->tail = segs[size_t(std::min<uint64_t>(n_full / seg_bytes, segs.size() - 1))] + n_full % seg_bytes;
+    m->bytes = bytes;
+    m->store = store;
+    *out = m;
+    return ok();
+}
+
+int hash_map_args(const sc_hash_map* map, const uint32_t* fault, const void* workspace, uint64_t workspace_bytes) {
+    if (!map) return fail(SC_EINVAL, "sc_handoff: missing hash map");
+    if (reinterpret_cast<uintptr_t>(fault) & 3u) return fail(SC_EINVAL, "sc_handoff: the hash fault word must be 4-byte aligned");
+    if (!workspace || workspace_bytes < sc::fnv_workspace(map->bytes).bytes)
+        return fail(SC_EINVAL, "sc_handoff: hash workspace smaller than sc_fnv1a64_workspace_bytes()");
+    if (reinterpret_cast<uintptr_t>(workspace) & 15u) return fail(SC_EINVAL, "sc_handoff: hash workspace must be 16-byte aligned");
+    return SC_OK;
+}
+}  // namespace
+
+extern "C" {
+
 int sc_hash_map_create(const sc_plan* const* plans, int32_t n_plans, void* payload, uint64_t bytes, sc_hash_map** out) {
     return guarded([&] {
         if (!out || (n_plans && !plans) || n_plans < 0) return fail(SC_EINVAL, "sc_handoff: missing hash map argument");
         if ((bytes && !payload) || !aligned16(payload) || bytes % 16)
             return fail(SC_EINVAL, "sc_handoff: a hashed payload is 16-byte aligned and whole 16-byte chunks");
         if (bytes > (uint64_t(1) << 46)) return fail(SC_ERANGE, "sc_handoff: hash input beyond 2^46 bytes");
-        uint8_t* base = static_cast<uint8_t*>(payload);
-        std::vector<sc::HashExtent> rows;
-        for (int32_t i = 0; i < n_plans; ++i) {
-            const sc_plan* p = plans[i];
-            if (!p || p->batch) return fail(SC_EINVAL, "sc_handoff: a hash map reads the rows of capture plans");
-            for (const sc::MoveRow& r : p->host_rows) {
-                sc::HashExtent x{};
-                switch (r.kind) {
-                    case sc::kCopy: x.kind = sc::kExtCopy; x.src = r.src; break;
-                    case sc::kZero: x.kind = sc::kExtZero; break;
-                    case sc::kPagesGather:
-                        x.kind = sc::kExtPages;
-                        x.src = r.src;
-                        x.table = r.table;
-                        x.ld = r.ld;
-                        x.page_chunks = p->geo.page_chunks.d;
-                        break;
-                    default:
-                        return fail(SC_EINVAL, "sc_handoff: only capture plans (page gathers, copies and zero fills into "
-                                               "the payload) can be fused with its hash");
-                }
-                if (r.dst < base || uint64_t(r.dst - base) > bytes || r.n * 16 > bytes - uint64_t(r.dst - base))
-                    return fail(SC_EINVAL, "sc_handoff: a row of the plan writes outside the hashed payload");
-                x.off = uint64_t(r.dst - base);
-                x.end = x.off + r.n * 16;
-                if (x.end > x.off) rows.push_back(x);
-            }
-        }
-        std::sort(rows.begin(), rows.end(), [](const sc::HashExtent& a, const sc::HashExtent& b) { return a.off < b.off; });
         std::vector<sc::HashExtent> ext;
-        uint64_t at = 0;
-        for (const sc::HashExtent& x : rows) {
-            if (x.off < at) return fail(SC_EINVAL, "sc_handoff: two rows of the plans write the same payload bytes");
-            if (x.off > at) ext.push_back(sc::HashExtent{at, x.off, nullptr, nullptr, 0, sc::kExtSelf, 0});
-            ext.push_back(x);
-            at = x.end;
+        if (const int rc = capture_extents(plans, n_plans, static_cast<uint8_t*>(payload), bytes, ext)) return rc;
+        return make_hash_map(ext, bytes, {static_cast<uint8_t*>(payload)}, uint64_t(1) << 62, true, out);
+    });
+}
+
+int sc_hash_map_create_segments(const sc_plan* const* plans, int32_t n_plans, const void* frame, uint64_t bytes,
+                                const sc_segments* into, sc_hash_map** out) {
+    return guarded([&] {
+        if (!out || (n_plans && !plans) || n_plans < 0 || !frame)
+            return fail(SC_EINVAL, "sc_handoff: missing hash map argument");
+        if (!aligned16(frame) || bytes % 16)
+            return fail(SC_EINVAL, "sc_handoff: a hashed payload is 16-byte aligned and whole 16-byte chunks");
+        if (bytes > (uint64_t(1) << 46)) return fail(SC_ERANGE, "sc_handoff: hash input beyond 2^46 bytes");
+        std::vector<uint8_t*> segs;
+        if (const int rc = segment_list(into, bytes, segs)) return rc;
+        std::vector<sc::HashExtent> ext;
+        if (const int rc = capture_extents(plans, n_plans, static_cast<const uint8_t*>(frame), bytes, ext)) return rc;
+        return make_hash_map(ext, bytes, segs, into->segment_bytes, true, out);
+    });
+}
+
+int sc_hash_map_create_read(const sc_segments* from, uint64_t bytes, sc_hash_map** out) {
+    return guarded([&] {
+        if (!out) return fail(SC_EINVAL, "sc_handoff: missing hash map argument");
+        if (bytes % 16) return fail(SC_EINVAL, "sc_handoff: a hashed payload is whole 16-byte chunks");
+        std::vector<uint8_t*> segs;
+        if (const int rc = segment_list(from, bytes, segs)) return rc;
+        std::vector<sc::HashExtent> ext;
+        for (uint64_t k = 0, at = 0; at < bytes || ext.empty(); ++k) {
+            const uint64_t end = std::min(bytes, at + from->segment_bytes);
+            ext.push_back(sc::HashExtent{at, end, segs[size_t(k)], nullptr, 0, sc::kExtCopy, 0});
+            at = end;
+            if (bytes == 0) break;
         }
-        if (at < bytes || ext.empty()) ext.push_back(sc::HashExtent{at, bytes, nullptr, nullptr, 0, sc::kExtSelf, 0});
-        // every workgroup's first extent (workgroup g hashes payload bytes [g, g + 1) * 64 KiB)
-        const sc::FnvWorkspace w = sc::fnv_workspace(bytes);
-        std::vector<uint32_t> first(std::max<uint64_t>(w.groups, 1), 0);
-        size_t e = 0;
-        for (uint64_t g = 0; g < w.groups; ++g) {
-            const uint64_t o = g * uint64_t(sc::kFnvGroupBytes);
-            while (e + 1 < ext.size() && ext[e].end <= o) ++e;
-            first[g] = uint32_t(e);
-        }
-        auto* m = new (std::nothrow) sc_hash_map();
-        if (!m) return fail(SC_ENOMEM, "sc_handoff: hash map allocation failed");
-        const uint64_t ext_bytes = round_up(ext.size() * sizeof(sc::HashExtent), 256);
-        hipError_t err = hipMalloc(reinterpret_cast<void**>(&m->ext_dev), ext_bytes + first.size() * 4);
-        if (err != hipSuccess) {
-            delete m;
-            return fail(SC_ENOMEM, std::string("sc_handoff: hash map: ") + hipGetErrorString(err));
-        }
-        m->first_dev = reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(m->ext_dev) + ext_bytes);
-        err = hipMemcpy(m->ext_dev, ext.data(), ext.size() * sizeof(sc::HashExtent), hipMemcpyHostToDevice);
-        if (err == hipSuccess) err = hipMemcpy(m->first_dev, first.data(), first.size() * 4, hipMemcpyHostToDevice);
-        if (err != hipSuccess) {
-            (void) hipFree(m->ext_dev);
-            delete m;
-            return hip_fail(err, "hash map upload");
-        }
-        m->payload = base;
-        m->bytes = bytes;
-        *out = m;
-        return ok();
+        return make_hash_map(ext, bytes, segs, from->segment_bytes, false, out);
     });
 }
 
 int sc_hash_map_launch(const sc_hash_map* map, uint64_t seed, uint64_t* out, uint32_t* fault, void* workspace,
                        uint64_t workspace_bytes, void* stream) {
-    if (!map) return fail(SC_EINVAL, "sc_handoff: missing hash map");
+    if (const int rc = hash_map_args(map, fault, workspace, workspace_bytes)) return rc;
     if (!out || !fault) return fail(SC_EINVAL, "sc_handoff: missing hash output or fault word");
-    if (reinterpret_cast<uintptr_t>(fault) & 3u) return fail(SC_EINVAL, "sc_handoff: the hash fault word must be 4-byte aligned");
-    if (!workspace || workspace_bytes < sc::fnv_workspace(map->bytes).bytes)
-        return fail(SC_EINVAL, "sc_handoff: hash workspace smaller than sc_fnv1a64_workspace_bytes()");
-    if (reinterpret_cast<uintptr_t>(workspace) & 15u) return fail(SC_EINVAL, "sc_handoff: hash workspace must be 16-byte aligned");
-    sc::HashMapArgs a{map->ext_dev, map->first_dev, map->payload, map->bytes};
-    const hipError_t e = sc::launch_fnv1a64_mapped(a, seed, out, fault, workspace, static_cast<hipStream_t>(stream));
+    const sc::HashMapArgs a{map->ext_dev, map->first_dev, map->seg_dev, map->seg_bytes, map->bytes, map->store ? 1u : 0u};
+    const hipError_t e =
+        sc::launch_fnv1a64_mapped(a, map->tail, seed, out, fault, workspace, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? ok() : hip_fail(e, "mapped hash launch");
+}
+
+int sc_hash_map_check_async(const sc_hash_map* map, uint64_t seed, uint64_t expected, uint64_t* out, uint32_t* verdict,
+                            uint32_t* fault, void* workspace, uint64_t workspace_bytes, void* stream) {
+    if (const int rc = hash_map_args(map, fault, workspace, workspace_bytes)) return rc;
+    if (!out || !verdict || (reinterpret_cast<uintptr_t>(verdict) & 3u))
+        return fail(SC_EINVAL, "sc_handoff: missing hash output, or a verdict word that is not 4-byte aligned");
+    const sc::HashMapArgs a{map->ext_dev, map->first_dev, map->seg_dev, map->seg_bytes, map->bytes, map->store ? 1u : 0u};
+    const hipError_t e = sc::launch_fnv1a64_mapped(a, map->tail, seed, out, fault, workspace,
+                                                   static_cast<hipStream_t>(stream), expected, verdict);
     return e == hipSuccess ? ok() : hip_fail(e, "mapped hash launch");
 }
 
@@ -2267,6 +2425,30 @@ int sc_ipc_import_open(const sc_ipc_segment* segments, int32_t n_segments, sc_ip
     }
     *out = im;
     return ok();
+}
+
+// The segments' device addresses in payload order and the size every one but the last has (refused when the sizes
+// are not uniform, so the list is an sc_segments).
+static int segments_layout(const std::vector<void*>& ptr, const std::vector<uint64_t>& bytes, void** out, int32_t max,
+                           int32_t* n, uint64_t* segment_bytes) {
+    if (!n || !segment_bytes || (max && !out)) return fail(SC_EINVAL, "sc_handoff: missing layout output");
+    if (max < int32_t(ptr.size())) return fail(SC_ERANGE, "sc_handoff: room for fewer segments than there are");
+    for (size_t i = 0; i + 1 < bytes.size(); ++i)
+        if (bytes[i] != bytes[0]) return fail(SC_EINVAL, "sc_handoff: the segments are not of one size");
+    for (size_t i = 0; i < ptr.size(); ++i) out[i] = ptr[i];
+    *n = int32_t(ptr.size());
+    *segment_bytes = bytes.empty() ? 0 : bytes[0];
+    return ok();
+}
+
+int sc_ipc_export_layout(const sc_ipc_export* ex, void** ptr, int32_t max_segments, int32_t* n, uint64_t* segment_bytes) {
+    if (!ex) return fail(SC_EINVAL, "sc_handoff: missing export");
+    return segments_layout(ex->ptr, ex->bytes, ptr, max_segments, n, segment_bytes);
+}
+
+int sc_ipc_import_layout(const sc_ipc_import* im, void** ptr, int32_t max_segments, int32_t* n, uint64_t* segment_bytes) {
+    if (!im) return fail(SC_EINVAL, "sc_handoff: missing import");
+    return segments_layout(im->ptr, im->bytes, ptr, max_segments, n, segment_bytes);
 }
 
 int sc_ipc_import_fetch(sc_ipc_import* im, void* device_dst, uint64_t bytes, void* stream) {

@@ -550,11 +550,12 @@ __device__ u32x4 g_hash_zero_chunk;   // read for zero runs, so every chunk take
 // runs or more, and the payload's last partial segment, goes chunk by chunk into the payload, which the lane then reads
 // back (its own stores, after a fence).  The payload is written by store_wave below (the last partial segment only
 // here).
-__device__ __forceinline__ void gather_segment(const HashMapArgs& m, uint32_t e, uint64_t begin, uint64_t len,
-                                               uint32_t (&w)[kFnvLaneBytes / 4]) {
+__device__ __forceinline__ void gather_segment(const HashMapArgs& m, uint8_t* base, uint32_t e, uint64_t begin,
+                                               uint64_t len, uint32_t (&w)[kFnvLaneBytes / 4]) {
     while (m.ext[e].end <= begin) ++e;
+    const uint32_t e_begin = e;   // the extent holding `begin`: where the chunk-by-chunk walk below starts
     HashExtent x = m.ext[e];
-    uint8_t* dst = m.dst + begin;
+    uint8_t* dst = base + begin;   // `base` + o addresses payload byte o of this workgroup's segment
     const uint64_t seg_end = begin + len;
     const Run a = run_at(x, begin, dst);
     if (len == kFnvLaneBytes) {
@@ -583,15 +584,17 @@ __device__ __forceinline__ void gather_segment(const HashMapArgs& m, uint32_t e,
             }
             return;
         }
+        // three runs or more: walk from the first again (the look-ahead above may have moved past its extent)
+        e = e_begin;
         x = m.ext[e];
     }
 #pragma unroll 1
     for (uint64_t o = begin; o < seg_end;) {
         while (x.end <= o) x = m.ext[++e];
-        const Run r = run_at(x, o, m.dst + o);
+        const Run r = run_at(x, o, base + o);
         const uint64_t o0 = o, end = r.end < seg_end ? r.end : seg_end;
         for (; o < end; o += 16)
-            if (r.store) put16(m.dst + o, r.src ? *(const gu32x4*) (r.src + (o - o0)) : u32x4{0u, 0u, 0u, 0u});
+            if (r.store && m.store) put16(base + o, r.src ? *(const gu32x4*) (r.src + (o - o0)) : u32x4{0u, 0u, 0u, 0u});
     }
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "workgroup");   // the lane's stores complete before its reads
     if (len == kFnvLaneBytes) load_segment(dst, w);
@@ -656,11 +659,14 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5
     uint32_t* fault = ctl + 1;
     uint32_t w[kFnvLaneBytes / 4] = {};
     if constexpr (kMapped) {
+        // this workgroup's payload bytes lie in one segment; `base` + o addresses byte o there
+        const uint64_t k = g * uint64_t(kFnvGroupBytes) / map.seg_bytes;
+        uint8_t* const base = reinterpret_cast<uint8_t*>(reinterpret_cast<uintptr_t>(map.seg[k]) - k * map.seg_bytes);
         if (begin < map.n_total) {
             const uint64_t left = map.n_total - begin;
-            gather_segment(map, map.first[g], begin, left < kFnvLaneBytes ? left : kFnvLaneBytes, w);
+            gather_segment(map, base, map.first[g], begin, left < kFnvLaneBytes ? left : kFnvLaneBytes, w);
         }
-        store_wave(s_xpose[wave], w, map.dst, (g * kThreads + uint64_t(wave) * 64) * kFnvLaneBytes, n, lane);
+        if (map.store) store_wave(s_xpose[wave], w, base, (g * kThreads + uint64_t(wave) * 64) * kFnvLaneBytes, n, lane);
     } else if (full) {
         load_segment(p, w);
     }
@@ -765,11 +771,13 @@ hipError_t launch_fnv1a64(const void* data, uint64_t n, uint64_t seed, const uin
     return hipGetLastError();
 }
 
-// The gather fused with the hash: the payload's `map.n_total` bytes gathered into map.dst and hashed, the whole lane
-// segments in the one-pass kernel and the last partial one (under 256 bytes) by the closing kernel, which runs after
-// every byte is in place.
-hipError_t launch_fnv1a64_mapped(const HashMapArgs& map, uint64_t seed, uint64_t* out, uint32_t* fault_out,
-                                 void* workspace, hipStream_t stream) {
+// The gather fused with the hash: the payload's `map.n_total` bytes gathered into its segments and hashed, the whole
+// lane segments in the one-pass kernel and the last partial one (under 256 bytes, at `tail`) by the closing kernel,
+// which runs after every byte is in place.  With `verdict`, the closing kernel also leaves the check of the hash
+// against `expected` there, as sc_fnv1a64_check_async does.
+hipError_t launch_fnv1a64_mapped(const HashMapArgs& map, const uint8_t* tail, uint64_t seed, uint64_t* out,
+                                 uint32_t* fault_out, void* workspace, hipStream_t stream, uint64_t expected,
+                                 uint32_t* verdict) {
     const uint64_t n_total = map.n_total, n_full = n_total & ~uint64_t(kFnvLaneBytes - 1);
     const FnvWorkspace w = fnv_workspace(n_total);
     uint8_t* ws = static_cast<uint8_t*>(workspace);
@@ -780,13 +788,13 @@ hipError_t launch_fnv1a64_mapped(const HashMapArgs& map, uint64_t seed, uint64_t
         const uint64_t init_blocks = (words + kThreads - 1) / kThreads < 1024 ? (words + kThreads - 1) / kThreads : 1024;
         hipLaunchKernelGGL(fnv_onepass_init_kernel, dim3(unsigned(init_blocks)), dim3(kThreads), 0, stream, status, words,
                            ctl);
-        hipLaunchKernelGGL(fnv_onepass_kernel<true>, dim3(unsigned(w.groups)), dim3(kThreads), 0, stream, map.dst, n_full,
+        hipLaunchKernelGGL(fnv_onepass_kernel<true>, dim3(unsigned(w.groups)), dim3(kThreads), 0, stream, nullptr, n_full,
                            true, seed, nullptr, status, w.stride, ctl, g_spin_limit.load(), map);
     }
     const bool any = w.groups > 0;
     hipLaunchKernelGGL(fnv_finish_kernel, dim3(1), dim3(1), 0, stream, any ? reinterpret_cast<const uint64_t*>(ctl + 2) : nullptr,
-                       seed, nullptr, n_full, out, fault_out, false, 0ull, nullptr, any ? ctl + 1 : nullptr,
-                       map.dst + n_full, uint32_t(n_total - n_full));
+                       seed, nullptr, n_full, out, fault_out, false, expected, verdict, any ? ctl + 1 : nullptr,
+                       tail, uint32_t(n_total - n_full));
     return hipGetLastError();
 }
 

@@ -221,8 +221,10 @@ constexpr int kFnvGroupBytes = 256 * kFnvLaneBytes;   // the payload bytes of on
 struct HashMapArgs {
     const HashExtent* ext;   // null: the plain hash of `data`
     const uint32_t* first;   // per workgroup: the extent holding its first byte
-    uint8_t* dst;            // the payload
+    uint8_t* const* seg;     // the payload's segments: byte o is at seg[o / seg_bytes] + o % seg_bytes
+    uint64_t seg_bytes;      // a multiple of kFnvGroupBytes, so no workgroup's bytes straddle two segments
     uint64_t n_total;        // payload bytes gathered (n rounded down to whole lane segments is hashed in the kernel)
+    uint32_t store;          // 0: the sources are only read and hashed (a payload hashed where it lies)
 };
 
 }  // namespace sc

@@ -235,7 +235,9 @@ __device__ void tile_pages(const MoveRow& r, const MoveGeo& g, uint64_t local, b
     u32x4 v[kChunksPerThread];
     int64_t dst_off[kChunksPerThread];
     if (scatter) {
-        const uint32_t last = uint32_t(r.n) - 1u;
+        // a source-order row may start `c0` chunks into its pages (pos0: a blob split where a payload's segment
+        // ends); the chunk numbers below are relative to the row's source, the page arithmetic adds c0
+        const uint32_t last = uint32_t(r.n) - 1u, c0 = kOrder == kSourceOrder ? uint32_t(r.pos0) : 0u;
         uint32_t q[kChunksPerThread];
         int32_t phys[kChunksPerThread], lpage[kChunksPerThread];
 #pragma unroll
@@ -250,13 +252,13 @@ __device__ void tile_pages(const MoveRow& r, const MoveGeo& g, uint64_t local, b
             if constexpr (kTable && kOrder == kDestOrderWave)
                 phys[j] = lpage[j] >= 0 ? table_entry_uniform(r, uint32_t(lpage[j])) : -1;
             else
-                phys[j] = table_entry<kTable>(r, fdiv(min(q[j], last), g.page_chunks));
+                phys[j] = table_entry<kTable>(r, fdiv(min(q[j], last) + c0, g.page_chunks));
         }
 #pragma unroll
         for (int j = 0; j < kChunksPerThread; ++j) {
             if (q[j] >= r.n) continue;
-            const uint32_t page = fdiv(q[j], g.page_chunks);
-            const uint32_t ch = q[j] - page * g.page_chunks.d;
+            const uint32_t page = fdiv(q[j] + c0, g.page_chunks);
+            const uint32_t ch = q[j] + c0 - page * g.page_chunks.d;
             if (phys[j] >= 0 && int64_t(phys[j]) < r.ld) st16(r.dst + uint64_t(phys[j]) * page_bytes + ch * 16u, v[j]);
         }
         return;

@@ -89,6 +89,11 @@ public:
     /// place and before the hash runs, so a copy of the payload on another stream (a park) can start while the hash
     /// is computed.
     bool encode(void* payload, uint64_t capacity, void* stream, std::string& error, void* gathered = nullptr);
+    /// Enqueues the encode into a segmented payload (`into`: the same-GPU hand-off's exported segments, byte o at
+    /// into.ptr[o / segment_bytes] + o % segment_bytes, segment_bytes a multiple of 64 KiB): the head and small blobs
+    /// copied into their segments, then the gather fused with the hash writing every blob into its segments, cut
+    /// wherever a segment ends.  The payload bytes are exactly encode()'s; nothing is staged in between.
+    bool encode_segments(const sc_segments& into, void* stream, std::string& error);
     /// The payload hash of the last encode; waits for it.
     bool payload_hash(uint64_t& hash, std::string& error);
 
@@ -97,6 +102,8 @@ private:
     bool stage(const SavedConversation& img, const std::vector<std::pair<const void*, uint64_t>>& sizes,
                const std::vector<const void*>& device, const WireIdentity& identity,
                std::vector<detail::WireBlobAt>& pool, std::string& error);
+    /// The capture plans of the slot (and of each stage part) writing the pool of a payload at `base`.
+    bool capture_plans(void* base, uint64_t capacity, std::vector<sc_plan*>& plans, std::string& error);
 
     sc_geometry g_{};
     sc_decode_slot slot_{};
@@ -131,6 +138,9 @@ private:
     sc_plan* capture_ = nullptr;
     sc_hash_map* hash_map_ = nullptr;  // the capture plans' rows fused with the payload hash (one read of the slot)
     void* capture_target_ = nullptr;   // the payload the capture plan was built for
+    sc_hash_map* seg_map_ = nullptr;   // the same into the segments of seg_target_
+    std::vector<void*> seg_target_;
+    uint64_t seg_bytes_ = 0;
 };
 
 class WireDeviceDecoder {
@@ -154,6 +164,13 @@ public:
     /// indexer's rows exactly when slot.with_index.
     bool open(const void* payload, uint64_t bytes, const sc_geometry& g, const sc_slot_layers& slot,
               const WireExpect& expect, std::string& error);
+    /// The same three for a payload held in segments (another process's exported segments, imported: byte o at
+    /// from.ptr[o / segment_bytes] + o % segment_bytes): the head is read from them, the hash checked over them where
+    /// they lie, and every blob scattered straight from them, cut where a segment ends.  Nothing is copied first.
+    bool open(const sc_segments& from, uint64_t bytes, const sc_geometry& g, const sc_decode_slot& slot,
+              const std::vector<WireDeviceStage>& stages, const WireExpect& expect, std::string& error);
+    bool open(const sc_segments& from, uint64_t bytes, const sc_geometry& g, const sc_slot_layers& slot,
+              const WireExpect& expect, std::string& error);
     int64_t tokens() const { return tokens_; }
     const WireDecoded& info() const { return info_; }
     /// Verifies the payload hash on the device (when `expect` asked for it), then scatters the K/V and GDN rows into the
@@ -163,8 +180,16 @@ public:
 
 private:
     void release();
-    bool read_head(const void* payload, uint64_t bytes, const WireExpect& expect, std::vector<detail::WireBlobAt>& blobs,
-                   std::string& error);
+    bool open_f16(const void* payload, const sc_segments* segs, uint64_t bytes, const sc_geometry& g,
+                  const sc_decode_slot& slot, const std::vector<WireDeviceStage>& stages, const WireExpect& expect,
+                  std::string& error);
+    bool open_layers(const void* payload, const sc_segments* segs, uint64_t bytes, const sc_geometry& g,
+                     const sc_slot_layers& slot, const WireExpect& expect, std::string& error);
+    bool read_head(const void* payload, const sc_segments* segs, uint64_t bytes, const WireExpect& expect,
+                   std::vector<detail::WireBlobAt>& blobs, std::string& error);
+    /// Copies payload bytes [off, off + n) to `dst` on `stream`, a piece per segment they lie in.
+    bool copy_payload(void* dst, uint64_t off, uint64_t n, void* stream, std::string& error);
+    sc_segments segments() const { return sc_segments{int32_t(seg_.size()), seg_bytes_, seg_.data()}; }
     bool finish_open(const void* payload, uint64_t bytes, const WireExpect& expect,
                      const std::vector<detail::WireBlobAt>& blobs, const std::vector<const void*>& device,
                      std::string& error);
@@ -185,6 +210,9 @@ private:
     std::vector<sc_plan*> stage_scatters_;   // one per stage part, gated by the same hash verdict
     void* hash_ws_ = nullptr;
     uint64_t hash_ws_bytes_ = 0;
+    std::vector<void*> seg_;          // a segmented payload's segments (empty: the payload is at payload_)
+    uint64_t seg_bytes_ = 0;
+    sc_hash_map* read_map_ = nullptr; // the hash of a segmented payload where it lies
     uint64_t* hash_dev_ = nullptr;    // device: the hash check's verdict word
     uint64_t* hash_host_ = nullptr;   // pinned (64 B); the hash's last kernel stores the payload hash here
     // and the launch's fault word right after it, so the host sees both words the device verdict is made of

@@ -128,6 +128,10 @@ void WireDeviceEncoder::release() {
     if (capture_) sc_plan_destroy(capture_);
     if (hash_map_) sc_hash_map_destroy(hash_map_);
     hash_map_ = nullptr;
+    if (seg_map_) sc_hash_map_destroy(seg_map_);
+    seg_map_ = nullptr;
+    seg_target_.clear();
+    seg_bytes_ = 0;
     if (staged_) sc_host_free(staged_);
     if (hash_host_) sc_host_free(hash_host_);
     if (hash_ws_) sc_device_free(hash_ws_);
@@ -343,37 +347,19 @@ bool WireDeviceEncoder::encode(void* payload, uint64_t capacity, void* stream, s
     if (capture_target_ != payload) {
         if (capture_) sc_plan_destroy(capture_);
         capture_ = nullptr;
-        if (hash_map_) sc_hash_map_destroy(hash_map_);
-        hash_map_ = nullptr;
-        int rc;
-        if (layered_) {
-            sc_layers_map map{lay_off_.data(), zero_.data(), int64_t(zero_.size() / 2)};
-            rc = sc_plan_capture_layers(&g_, &layers_, tokens_, payload, capacity, &map, &capture_);
-        } else {
-            sc_blob_map map{};
-            map.k_off = k_off_.data();
-            map.v_off = v_off_.data();
-            map.gdn_off = gdn_off_;
-            map.zero = zero_.data();
-            map.n_zero = int64_t(zero_.size() / 2);
-            rc = sc_plan_capture_map(&g_, &slot_, tokens_, payload, capacity, &map, &capture_);
-        }
-        if (!abi(rc, error, "capture plan")) return false;
-        for (StagePlan& sp : stage_plans_) {   // every gap of the pool is cleared by the main plan's zero ranges
+        for (StagePlan& sp : stage_plans_) {
             if (sp.plan) sc_plan_destroy(sp.plan);
             sp.plan = nullptr;
-            sc_blob_map map{};
-            map.k_off = sp.k_off.data();
-            map.v_off = sp.v_off.data();
-            map.gdn_off = sp.gdn_off;
-            if (!abi(sc_plan_capture_map(&sp.g, &sp.slot, tokens_, payload, capacity, &map, &sp.plan), error,
-                     "stage capture plan"))
-                return false;
         }
+        if (hash_map_) sc_hash_map_destroy(hash_map_);
+        hash_map_ = nullptr;
+        capture_target_ = nullptr;
+        std::vector<sc_plan*> plans;
+        if (!capture_plans(payload, capacity, plans, error)) return false;
+        capture_ = plans[0];
+        for (size_t i = 0; i < stage_plans_.size(); ++i) stage_plans_[i].plan = plans[i + 1];
         // the same rows as the sources of the fused gather + hash (the head and the small host blobs are copied in
         // first and hashed as the payload holds them)
-        std::vector<const sc_plan*> plans{capture_};
-        for (const StagePlan& sp : stage_plans_) plans.push_back(sp.plan);
         if (!abi(sc_hash_map_create(plans.data(), int32_t(plans.size()), payload, plan_.total_bytes, &hash_map_), error,
                  "payload hash map"))
             return false;
@@ -405,6 +391,79 @@ bool WireDeviceEncoder::encode(void* payload, uint64_t capacity, void* stream, s
     return true;
 }
 
+bool WireDeviceEncoder::capture_plans(void* base, uint64_t capacity, std::vector<sc_plan*>& plans, std::string& error) {
+    plans.clear();
+    auto undo = [&] {
+        for (sc_plan* q : plans) sc_plan_destroy(q);
+        plans.clear();
+        return false;
+    };
+    sc_plan* main = nullptr;
+    int rc;
+    if (layered_) {
+        sc_layers_map map{lay_off_.data(), zero_.data(), int64_t(zero_.size() / 2)};
+        rc = sc_plan_capture_layers(&g_, &layers_, tokens_, base, capacity, &map, &main);
+    } else {
+        sc_blob_map map{};
+        map.k_off = k_off_.data();
+        map.v_off = v_off_.data();
+        map.gdn_off = gdn_off_;
+        map.zero = zero_.data();
+        map.n_zero = int64_t(zero_.size() / 2);
+        rc = sc_plan_capture_map(&g_, &slot_, tokens_, base, capacity, &map, &main);
+    }
+    if (!abi(rc, error, "capture plan")) return false;
+    plans.push_back(main);
+    for (const StagePlan& sp : stage_plans_) {   // every gap of the pool is cleared by the main plan's zero ranges
+        sc_blob_map map{};
+        map.k_off = sp.k_off.data();
+        map.v_off = sp.v_off.data();
+        map.gdn_off = sp.gdn_off;
+        sc_plan* q = nullptr;
+        if (!abi(sc_plan_capture_map(&sp.g, &sp.slot, tokens_, base, capacity, &map, &q), error, "stage capture plan"))
+            return undo();
+        plans.push_back(q);
+    }
+    return true;
+}
+
+bool WireDeviceEncoder::encode_segments(const sc_segments& into, void* stream, std::string& error) {
+    if (!staged_) return refuse(error, "encode before a successful plan");
+    if (into.n < 1 || !into.ptr || !into.segment_bytes) return refuse(error, "a segmented payload needs its segments");
+    std::vector<void*> ptrs(into.ptr, into.ptr + into.n);
+    if (!seg_map_ || ptrs != seg_target_ || into.segment_bytes != seg_bytes_) {
+        if (seg_map_) sc_hash_map_destroy(seg_map_);
+        seg_map_ = nullptr;
+        seg_target_.clear();
+        // the plans are built for a contiguous payload framed at the first segment, never launched: the map takes
+        // their rows as payload offsets and writes them into the segments
+        std::vector<sc_plan*> plans;
+        if (!capture_plans(ptrs[0], plan_.total_bytes, plans, error)) return false;
+        const int rc = sc_hash_map_create_segments(plans.data(), int32_t(plans.size()), ptrs[0], plan_.total_bytes, &into,
+                                                   &seg_map_);
+        for (sc_plan* q : plans) sc_plan_destroy(q);
+        if (!abi(rc, error, "segmented payload hash map")) return false;
+        seg_target_ = ptrs;
+        seg_bytes_ = into.segment_bytes;
+    }
+    // the head and the small host blobs, a piece per segment they touch
+    for (const Upload& u : uploads_)
+        for (uint64_t o = u.offset, end = u.offset + u.bytes; o < end;) {
+            const uint64_t k = o / seg_bytes_, stop = std::min(end, (k + 1) * seg_bytes_);
+            if (k >= ptrs.size()) return refuse(error, "the segments are smaller than the payload");
+            if (!abi(sc_copy_async(static_cast<uint8_t*>(ptrs[size_t(k)]) + (o - k * seg_bytes_),
+                                   staged_ + u.staged_at + (o - u.offset), stop - o, stream),
+                     error, "head copy"))
+                return false;
+            o = stop;
+        }
+    if (!abi(sc_hash_map_launch(seg_map_, kWireHashSeed, hash_host_, hash_fault_host(), hash_ws_, hash_ws_bytes_, stream),
+             error, "payload gather and hash"))
+        return false;
+    last_stream_ = stream;
+    return true;
+}
+
 bool WireDeviceEncoder::payload_hash(uint64_t& hash, std::string& error) {
     if (!hash_host_) return refuse(error, "no encode to read a hash from");
     if (!abi(sc_stream_sync(last_stream_), error, "encode")) return false;
@@ -423,6 +482,10 @@ void WireDeviceDecoder::release() {
         if (p) sc_plan_destroy(p);
     stage_scatters_.clear();
     if (scatter_) sc_plan_destroy(scatter_);
+    if (read_map_) sc_hash_map_destroy(read_map_);
+    read_map_ = nullptr;
+    seg_.clear();
+    seg_bytes_ = 0;
     if (hash_ws_) sc_device_free(hash_ws_);
     if (hash_dev_) sc_device_free(hash_dev_);
     if (hash_host_) sc_host_free(hash_host_);
@@ -440,22 +503,44 @@ void WireDeviceDecoder::release() {
     head_image_ = SavedConversation{};
 }
 
-bool WireDeviceDecoder::read_head(const void* payload, uint64_t bytes, const WireExpect& expect,
-                                  std::vector<detail::WireBlobAt>& blobs, std::string& error) {
+bool WireDeviceDecoder::copy_payload(void* dst, uint64_t off, uint64_t n, void* stream, std::string& error) {
+    if (seg_.empty())
+        return abi(sc_copy_async(dst, payload_ + off, n, stream), error, "payload read");
+    for (uint64_t o = off, end = off + n; o < end;) {
+        const uint64_t k = o / seg_bytes_, stop = std::min(end, (k + 1) * seg_bytes_);
+        if (k >= seg_.size()) return refuse(error, "the payload runs past its segments");
+        if (!abi(sc_copy_async(static_cast<uint8_t*>(dst) + (o - off),
+                               static_cast<const uint8_t*>(seg_[size_t(k)]) + (o - k * seg_bytes_), stop - o, stream),
+                 error, "payload read"))
+            return false;
+        o = stop;
+    }
+    return true;
+}
+
+bool WireDeviceDecoder::read_head(const void* payload, const sc_segments* segs, uint64_t bytes,
+                                  const WireExpect& expect, std::vector<detail::WireBlobAt>& blobs, std::string& error) {
     release();
+    if (segs) {
+        if (segs->n < 1 || !segs->ptr || !segs->segment_bytes || !segs->ptr[0])
+            return refuse(error, "a segmented payload needs its segments");
+        if (uint64_t(segs->n) * segs->segment_bytes < bytes) return refuse(error, "the segments are smaller than the payload");
+        seg_.assign(segs->ptr, segs->ptr + segs->n);
+        seg_bytes_ = segs->segment_bytes;
+        payload = seg_[0];
+    }
+    payload_ = static_cast<const uint8_t*>(payload);
     if (!payload || bytes < kWireHeaderRecordBytes) return refuse(error, "the payload is shorter than the header record");
     // the payload may still be arriving on another stream: everything enqueued before this call completes first
     if (!abi(sc_device_sync(), error, "wait for the payload")) return false;
     std::vector<uint8_t> head(kWireHeaderRecordBytes);
-    if (!abi(sc_copy_async(head.data(), payload, head.size(), nullptr), error, "head read") ||
-        !abi(sc_device_sync(), error, "head read"))
+    if (!copy_payload(head.data(), 0, head.size(), nullptr, error) || !abi(sc_device_sync(), error, "head read"))
         return false;
     WireHeaderRecord h{};
     if (!conversation_wire_peek(head.data(), head.size(), h, error)) return false;
     if (h.blob_pool_off > bytes) return refuse(error, "the blob pool starts past the end of the buffer");
     head.resize(size_t(h.blob_pool_off));
-    if (!abi(sc_copy_async(head.data(), payload, head.size(), nullptr), error, "head read") ||
-        !abi(sc_device_sync(), error, "head read"))
+    if (!copy_payload(head.data(), 0, head.size(), nullptr, error) || !abi(sc_device_sync(), error, "head read"))
         return false;
     // every check of the host decoder, against the real buffer size
     WireExpect bounded = expect;
@@ -491,9 +576,13 @@ bool WireDeviceDecoder::finish_open(const void* payload, uint64_t bytes, const W
         rc = sc_device_alloc(&hash_ws_, hash_ws_bytes_);
         if (rc == SC_OK) rc = sc_device_alloc(reinterpret_cast<void**>(&hash_dev_), 64);
         if (rc == SC_OK) rc = sc_host_alloc(reinterpret_cast<void**>(&hash_host_), 64);
+        if (rc == SC_OK && !seg_.empty()) {   // a segmented payload is hashed where it lies, in one launch
+            const sc_segments segs = segments();
+            rc = sc_hash_map_create_read(&segs, info_.bytes, &read_map_);
+        }
         if (!abi(rc, error, "hash workspace")) { release(); return false; }
     }
-    payload_ = static_cast<const uint8_t*>(payload);
+    (void) payload;
     bytes_ = bytes;
     expect_ = expect;
     return true;
@@ -501,13 +590,35 @@ bool WireDeviceDecoder::finish_open(const void* payload, uint64_t bytes, const W
 
 bool WireDeviceDecoder::open(const void* payload, uint64_t bytes, const sc_geometry& g, const sc_decode_slot& slot,
                              const WireExpect& expect, std::string& error) {
-    return open(payload, bytes, g, slot, {}, expect, error);
+    return open_f16(payload, nullptr, bytes, g, slot, {}, expect, error);
 }
 
 bool WireDeviceDecoder::open(const void* payload, uint64_t bytes, const sc_geometry& g, const sc_decode_slot& slot,
                              const std::vector<WireDeviceStage>& stages, const WireExpect& expect, std::string& error) {
+    return open_f16(payload, nullptr, bytes, g, slot, stages, expect, error);
+}
+
+bool WireDeviceDecoder::open(const sc_segments& from, uint64_t bytes, const sc_geometry& g, const sc_decode_slot& slot,
+                             const std::vector<WireDeviceStage>& stages, const WireExpect& expect, std::string& error) {
+    return open_f16(nullptr, &from, bytes, g, slot, stages, expect, error);
+}
+
+bool WireDeviceDecoder::open(const void* payload, uint64_t bytes, const sc_geometry& g, const sc_slot_layers& slot,
+                             const WireExpect& expect, std::string& error) {
+    return open_layers(payload, nullptr, bytes, g, slot, expect, error);
+}
+
+bool WireDeviceDecoder::open(const sc_segments& from, uint64_t bytes, const sc_geometry& g, const sc_slot_layers& slot,
+                             const WireExpect& expect, std::string& error) {
+    return open_layers(nullptr, &from, bytes, g, slot, expect, error);
+}
+
+bool WireDeviceDecoder::open_f16(const void* payload, const sc_segments* segs, uint64_t bytes, const sc_geometry& g,
+                                 const sc_decode_slot& slot, const std::vector<WireDeviceStage>& stages,
+                                 const WireExpect& expect, std::string& error) {
     std::vector<detail::WireBlobAt> blobs;
-    if (!read_head(payload, bytes, expect, blobs, error)) return false;
+    if (!read_head(payload, segs, bytes, expect, blobs, error)) return false;
+    payload = payload_;
     if (info_.n_stage_parts != int64_t(stages.size()))
         return refuse(error, stages.empty() ? "a layer-split image cannot be mounted on the device path without its "
                                               "stages' slots"
@@ -549,7 +660,12 @@ bool WireDeviceDecoder::open(const void* payload, uint64_t bytes, const sc_geome
     map.k_off = k_off.data();
     map.v_off = v_off.data();
     map.gdn_off = gb ? gb->offset : 0;
-    if (!abi(sc_plan_scatter_map(&g, payload, bytes, &map, tokens_, &slot, &scatter_), error, "scatter plan")) {
+    const sc_segments from = segments();
+    auto scatter_plan = [&](const sc_geometry& sg, const sc_blob_map& m, const sc_decode_slot& s, sc_plan** out) {
+        return seg_.empty() ? sc_plan_scatter_map(&sg, payload, bytes, &m, tokens_, &s, out)
+                            : sc_plan_scatter_map_segments(&sg, &from, bytes, &m, tokens_, &s, out);
+    };
+    if (!abi(scatter_plan(g, map, slot, &scatter_), error, "scatter plan")) {
         release();
         return false;
     }
@@ -559,9 +675,7 @@ bool WireDeviceDecoder::open(const void* payload, uint64_t bytes, const sc_geome
         pm.k_off = parts[i].k_off.data();
         pm.v_off = parts[i].v_off.data();
         pm.gdn_off = parts[i].gdn_off;
-        if (!abi(sc_plan_scatter_map(&stages[i].geometry, payload, bytes, &pm, tokens_, &stages[i].slot,
-                                     &stage_scatters_[i]),
-                 error, "stage scatter plan")) {
+        if (!abi(scatter_plan(stages[i].geometry, pm, stages[i].slot, &stage_scatters_[i]), error, "stage scatter plan")) {
             release();
             return false;
         }
@@ -569,10 +683,11 @@ bool WireDeviceDecoder::open(const void* payload, uint64_t bytes, const sc_geome
     return finish_open(payload, bytes, expect, blobs, device, error);
 }
 
-bool WireDeviceDecoder::open(const void* payload, uint64_t bytes, const sc_geometry& g, const sc_slot_layers& slot,
-                             const WireExpect& expect, std::string& error) {
+bool WireDeviceDecoder::open_layers(const void* payload, const sc_segments* segs, uint64_t bytes, const sc_geometry& g,
+                                    const sc_slot_layers& slot, const WireExpect& expect, std::string& error) {
     std::vector<detail::WireBlobAt> blobs;
-    if (!read_head(payload, bytes, expect, blobs, error)) return false;
+    if (!read_head(payload, segs, bytes, expect, blobs, error)) return false;
+    payload = payload_;
     if (info_.n_stage_parts) return refuse(error, "a layer-split image cannot be mounted into a single layered slot");
     SlotShape s;
     if (!slot_shape(g, tokens_, s, error)) return false;
@@ -606,7 +721,10 @@ bool WireDeviceDecoder::open(const void* payload, uint64_t bytes, const sc_geome
     if (gb) off.back() = gb->offset;
     device.push_back(&head_image_.live.gdn);
     sc_layers_map map{off.data(), nullptr, 0};
-    if (!abi(sc_plan_scatter_layers(&g, payload, bytes, &map, tokens_, &slot, &scatter_), error, "scatter plan")) {
+    const sc_segments from = segments();
+    const int rc = seg_.empty() ? sc_plan_scatter_layers(&g, payload, bytes, &map, tokens_, &slot, &scatter_)
+                                : sc_plan_scatter_layers_segments(&g, &from, bytes, &map, tokens_, &slot, &scatter_);
+    if (!abi(rc, error, "scatter plan")) {
         release();
         return false;
     }
@@ -624,13 +742,14 @@ bool WireDeviceDecoder::restore(void* stream, SavedConversation& image, std::str
         !abi(sc_stream_wait_event(side_, ev_start_), error, "restore start"))
         return false;
     for (const Download& d : downloads_)
-        if (d.bytes && !abi(sc_copy_async(staged_ + d.staged_at, payload_ + d.offset, d.bytes, side_), error, "blob read"))
-            return false;
+        if (d.bytes && !copy_payload(staged_ + d.staged_at, d.offset, d.bytes, side_, error)) return false;
     if (!abi(sc_event_record(ev_done_, side_), error, "blob read")) return false;
     // the hash itself goes straight to pinned host memory (the last kernel's store), the verdict stays on the device
     if (expect_.check_payload_hash &&
-        !abi(sc_fnv1a64_check_async(payload_, info_.bytes, kWireHashSeed, expect_.payload_hash, hash_host_, verdict,
-                                    hash_fault_host(), hash_ws_, hash_ws_bytes_, stream),
+        !abi(read_map_ ? sc_hash_map_check_async(read_map_, kWireHashSeed, expect_.payload_hash, hash_host_, verdict,
+                                                 hash_fault_host(), hash_ws_, hash_ws_bytes_, stream)
+                       : sc_fnv1a64_check_async(payload_, info_.bytes, kWireHashSeed, expect_.payload_hash, hash_host_,
+                                                verdict, hash_fault_host(), hash_ws_, hash_ws_bytes_, stream),
              error, "payload hash"))
         return false;
     SavedConversation out = head_image_;

@@ -153,6 +153,16 @@ int sc_wire_encode_async(sc_wire_encoder* e, void* payload, uint64_t capacity, v
     });
 }
 
+int sc_wire_encode_segments_async(sc_wire_encoder* e, const sc_segments* into, void* stream) {
+    return guarded([&] {
+        if (!e || !into) return failed(SC_EINVAL, "conversation wire: missing encoder or segments");
+        std::string err;
+        if (e->enc.encode_segments(*into, stream, err)) return done();
+        return failed(err.find("conversation wire") != std::string::npos && err.find("sc_handoff") == std::string::npos
+                          ? SC_EINVAL : SC_EHIP, err);
+    });
+}
+
 // The encoder's and decoder's refusal of a device hash whose kernel's bounded wait ran out.
 static bool hash_incomplete(const std::string& err) { return err.find("did not complete") != std::string::npos; }
 
@@ -175,7 +185,7 @@ template <class Slot>
 static int decoder_open(const void* payload, uint64_t bytes, const sc_geometry* g, const Slot* slot,
                         const sc_wire_stage* stages, int32_t n_stages, const int64_t* geometry, uint64_t geom_hash,
                         uint64_t pack_hash, int32_t check_identity, uint64_t payload_hash, int32_t check_hash,
-                        sc_wire_decoder** out) {
+                        sc_wire_decoder** out, const sc_segments* segs = nullptr) {
     return guarded([&] {
         if (!g || !slot || !out) return failed(SC_EINVAL, "conversation wire: missing argument");
         WireExpect expect;
@@ -198,9 +208,11 @@ static int decoder_open(const void* payload, uint64_t bytes, const sc_geometry* 
                 delete d;
                 return rc;
             }
-            opened = d->dec.open(payload, bytes, *g, *slot, parts, expect, err);
+            opened = segs ? d->dec.open(*segs, bytes, *g, *slot, parts, expect, err)
+                          : d->dec.open(payload, bytes, *g, *slot, parts, expect, err);
         } else {
-            opened = d->dec.open(payload, bytes, *g, *slot, expect, err);
+            opened = segs ? d->dec.open(*segs, bytes, *g, *slot, expect, err)
+                          : d->dec.open(payload, bytes, *g, *slot, expect, err);
         }
         if (!opened) {
             delete d;
@@ -232,6 +244,24 @@ int sc_wire_decoder_open_layers(const void* payload, uint64_t bytes, const sc_ge
                                 uint64_t payload_hash, int32_t check_hash, sc_wire_decoder** out) {
     return decoder_open(payload, bytes, g, slot, nullptr, 0, geometry, geom_hash, pack_hash, check_identity, payload_hash,
                         check_hash, out);
+}
+
+int sc_wire_decoder_open_segments(const sc_segments* from, uint64_t bytes, const sc_geometry* g,
+                                  const sc_decode_slot* slot, const int64_t* geometry, uint64_t geom_hash,
+                                  uint64_t pack_hash, int32_t check_identity, uint64_t payload_hash, int32_t check_hash,
+                                  sc_wire_decoder** out) {
+    if (!from) return failed(SC_EINVAL, "conversation wire: missing segments");
+    return decoder_open(nullptr, bytes, g, slot, nullptr, 0, geometry, geom_hash, pack_hash, check_identity,
+                        payload_hash, check_hash, out, from);
+}
+
+int sc_wire_decoder_open_layers_segments(const sc_segments* from, uint64_t bytes, const sc_geometry* g,
+                                         const sc_slot_layers* slot, const int64_t* geometry, uint64_t geom_hash,
+                                         uint64_t pack_hash, int32_t check_identity, uint64_t payload_hash,
+                                         int32_t check_hash, sc_wire_decoder** out) {
+    if (!from) return failed(SC_EINVAL, "conversation wire: missing segments");
+    return decoder_open(nullptr, bytes, g, slot, nullptr, 0, geometry, geom_hash, pack_hash, check_identity,
+                        payload_hash, check_hash, out, from);
 }
 
 int64_t sc_wire_decoder_tokens(const sc_wire_decoder* d) { return d ? d->dec.tokens() : -1; }

@@ -118,12 +118,24 @@ class ImageBlob(C.Structure):
 _P = C.c_void_p
 _I64, _U64 = C.c_int64, C.c_uint64
 _GEO = C.POINTER(Geometry)
+class Segments(C.Structure):
+    """sc_segments: a payload held in segments (byte o at ptr[o // segment_bytes] + o % segment_bytes)."""
+    _fields_ = [("n", C.c_int32), ("segment_bytes", C.c_uint64), ("ptr", C.POINTER(C.c_void_p))]
+
+
+def segments_struct(ptrs, segment_bytes: int) -> tuple[Segments, object]:
+    """A Segments struct over device pointers, plus the host array it points into (keep both alive)."""
+    arr = (C.c_void_p * max(len(ptrs), 1))(*ptrs)
+    return Segments(n=len(ptrs), segment_bytes=segment_bytes, ptr=C.cast(arr, C.POINTER(C.c_void_p))), arr
+
+
 class IpcSegment(C.Structure):
     """sc_ipc_segment: one exported device allocation (a 64-byte memory handle and its size)."""
     _fields_ = [("handle", C.c_uint8 * 64), ("bytes", C.c_uint64)]
 
 
 IPC_MAX_SEGMENT = 1 << 30
+IPC_MAX_SEGMENTS = 64
 
 _SIGS = {
     "sc_last_error": (C.c_char_p, []),
@@ -215,6 +227,15 @@ _SIGS = {
     "sc_ipc_import_open": (C.c_int, [C.POINTER(IpcSegment), C.c_int32, C.POINTER(_P)]),
     "sc_ipc_import_fetch": (C.c_int, [_P, _P, _U64, _P]),
     "sc_ipc_import_close": (C.c_int, [_P]),
+    "sc_ipc_export_layout": (C.c_int, [_P, C.POINTER(_P), C.c_int32, C.POINTER(C.c_int32), C.POINTER(_U64)]),
+    "sc_ipc_import_layout": (C.c_int, [_P, C.POINTER(_P), C.c_int32, C.POINTER(C.c_int32), C.POINTER(_U64)]),
+    "sc_hash_map_create_segments": (C.c_int, [C.POINTER(_P), C.c_int32, _P, _U64, C.POINTER(Segments), C.POINTER(_P)]),
+    "sc_hash_map_create_read": (C.c_int, [C.POINTER(Segments), _U64, C.POINTER(_P)]),
+    "sc_hash_map_check_async": (C.c_int, [_P, _U64, _U64, _P, _P, _P, _P, _U64, _P]),
+    "sc_plan_scatter_map_segments": (C.c_int, [_GEO, C.POINTER(Segments), _U64, C.POINTER(BlobMap), _I64,
+                                               C.POINTER(DecodeSlot), C.POINTER(_P)]),
+    "sc_plan_scatter_layers_segments": (C.c_int, [_GEO, C.POINTER(Segments), _U64, C.POINTER(LayersMap), _I64,
+                                                  C.POINTER(SlotLayers), C.POINTER(_P)]),
 }
 for _name, (_res, _args) in _SIGS.items():
     _fn = getattr(lib, _name)
@@ -663,6 +684,7 @@ class HashPlan:
         self.ws = DeviceBuffer(self.ws_bytes, "uint8")
         self.out = DeviceBuffer(1, "uint64")
         self.fault = DeviceBuffer(1, "uint32")
+        self.verdict = DeviceBuffer(1, "uint32")
 
     def launch(self, ptr: int, nbytes: int, seed: int = REFERENCE_FNV_SEED, stream=None) -> None:
         if nbytes > self.max_bytes:
@@ -697,6 +719,7 @@ class HashPlan:
         self.ws.free()
         self.out.free()
         self.fault.free()
+        self.verdict.free()
 
 
 class HashMap:
@@ -712,6 +735,34 @@ class HashMap:
     def launch(self, hp: "HashPlan", seed: int = REFERENCE_FNV_SEED, stream=None) -> None:
         check(lib.sc_hash_map_launch(self.handle, seed, hp.out.ptr, hp.fault.ptr, hp.ws.ptr, hp.ws_bytes,
                                      _stream(stream)), "sc_hash_map_launch")
+
+    @classmethod
+    def segments(cls, plans, frame: int, nbytes: int, seg_ptrs, segment_bytes: int) -> "HashMap":
+        """The map of `plans` (built for a contiguous payload at `frame`) writing into segments instead
+        (sc_hash_map_create_segments)."""
+        arr = (C.c_void_p * max(len(plans), 1))(*[p.handle for p in plans])
+        segs, keep = segments_struct(seg_ptrs, segment_bytes)
+        h = C.c_void_p()
+        check(lib.sc_hash_map_create_segments(arr, len(plans), frame, nbytes, C.byref(segs), C.byref(h)),
+              "sc_hash_map_create_segments")
+        m = cls.__new__(cls)
+        m.handle, m.nbytes = h.value, nbytes
+        return m
+
+    @classmethod
+    def read(cls, seg_ptrs, segment_bytes: int, nbytes: int) -> "HashMap":
+        """A map that only hashes a segmented payload where it lies (sc_hash_map_create_read)."""
+        segs, keep = segments_struct(seg_ptrs, segment_bytes)
+        h = C.c_void_p()
+        check(lib.sc_hash_map_create_read(C.byref(segs), nbytes, C.byref(h)), "sc_hash_map_create_read")
+        m = cls.__new__(cls)
+        m.handle, m.nbytes = h.value, nbytes
+        return m
+
+    def check(self, hp: "HashPlan", expected: int, seed: int = REFERENCE_FNV_SEED, stream=None) -> None:
+        """launch() that also leaves the verdict (1: equal and complete) in hp.verdict (sc_hash_map_check_async)."""
+        check(lib.sc_hash_map_check_async(self.handle, seed, expected, hp.out.ptr, hp.verdict.ptr, hp.fault.ptr,
+                                          hp.ws.ptr, hp.ws_bytes, _stream(stream)), "sc_hash_map_check_async")
 
     def destroy(self) -> None:
         if self.handle:
@@ -912,6 +963,13 @@ def resume_layers_async(geo: Geometry, host_ptr: int, host_bytes: int, tokens: i
           "sc_resume_layers_async")
 
 
+def _layout(fn, handle) -> tuple[list[int], int]:
+    arr = (C.c_void_p * IPC_MAX_SEGMENTS)()
+    n, sb = C.c_int32(0), _U64(0)
+    check(fn(handle, arr, IPC_MAX_SEGMENTS, C.byref(n), C.byref(sb)), "segment layout")
+    return [int(arr[i]) for i in range(n.value)], int(sb.value)
+
+
 class IpcExport:
     """The exporting side of a same-GPU hand-off: device segments allocated and exported once."""
 
@@ -928,6 +986,10 @@ class IpcExport:
 
     def stage(self, device_ptr: int, nbytes: int, stream=None) -> None:
         check(lib.sc_ipc_export_stage(self.handle, device_ptr, nbytes, _stream(stream)), "sc_ipc_export_stage")
+
+    def layout(self) -> tuple[list[int], int]:
+        """The segments' device addresses and the size of every one but the last (sc_ipc_export_layout)."""
+        return _layout(lib.sc_ipc_export_layout, self.handle)
 
     def destroy(self) -> None:
         if self.handle:
@@ -949,6 +1011,10 @@ class IpcImport:
 
     def fetch(self, device_ptr: int, nbytes: int, stream=None) -> None:
         check(lib.sc_ipc_import_fetch(self.handle, device_ptr, nbytes, _stream(stream)), "sc_ipc_import_fetch")
+
+    def layout(self) -> tuple[list[int], int]:
+        """The imported segments' device addresses in this process and the segment size (sc_ipc_import_layout)."""
+        return _layout(lib.sc_ipc_import_layout, self.handle)
 
     def close(self) -> None:
         if self.handle:

@@ -38,6 +38,7 @@ for _name, _res, _args in (
     ("sc_wire_encoder_bytes", _U64, [_P]),
     ("sc_wire_encoder_pool_offset", _U64, [_P]),
     ("sc_wire_encode_async", C.c_int, [_P, _P, _U64, _P, _P]),
+    ("sc_wire_encode_segments_async", C.c_int, [_P, C.POINTER(sc.Segments), _P]),
     ("sc_wire_encoder_hash", C.c_int, [_P, C.POINTER(_U64)]),
     ("sc_wire_encoder_destroy", C.c_int, [_P]),
     ("sc_wire_decoder_open", C.c_int, [_P, _U64, C.POINTER(sc.Geometry), C.POINTER(sc.DecodeSlot), C.POINTER(C.c_int64),
@@ -47,6 +48,12 @@ for _name, _res, _args in (
                                              C.POINTER(_P)]),
     ("sc_wire_decoder_open_layers", C.c_int, [_P, _U64, C.POINTER(sc.Geometry), C.POINTER(sc.SlotLayers),
                                               C.POINTER(C.c_int64), _U64, _U64, _I32, _U64, _I32, C.POINTER(_P)]),
+    ("sc_wire_decoder_open_segments", C.c_int, [C.POINTER(sc.Segments), _U64, C.POINTER(sc.Geometry),
+                                                C.POINTER(sc.DecodeSlot), C.POINTER(C.c_int64), _U64, _U64, _I32, _U64,
+                                                _I32, C.POINTER(_P)]),
+    ("sc_wire_decoder_open_layers_segments", C.c_int, [C.POINTER(sc.Segments), _U64, C.POINTER(sc.Geometry),
+                                                       C.POINTER(sc.SlotLayers), C.POINTER(C.c_int64), _U64, _U64, _I32,
+                                                       _U64, _I32, C.POINTER(_P)]),
     ("sc_wire_decoder_tokens", _I64, [_P]),
     ("sc_wire_decoder_restore", C.c_int, [_P, _P]),
     ("sc_wire_decoder_live_ids", C.c_int, [_P, C.POINTER(C.c_int32), _I64, C.POINTER(_I64)]),
@@ -59,8 +66,9 @@ for _name, _res, _args in (
 
 EXPORTS = ("sc_wire_last_error", "sc_wire_encoder_create", "sc_wire_encoder_create_split",
            "sc_wire_encoder_create_layers", "sc_wire_encoder_bytes", "sc_wire_encoder_pool_offset",
-           "sc_wire_encode_async", "sc_wire_encoder_hash", "sc_wire_encoder_destroy", "sc_wire_decoder_open",
-           "sc_wire_decoder_open_split", "sc_wire_decoder_open_layers", "sc_wire_decoder_tokens",
+           "sc_wire_encode_async", "sc_wire_encode_segments_async", "sc_wire_encoder_hash", "sc_wire_encoder_destroy",
+           "sc_wire_decoder_open", "sc_wire_decoder_open_split", "sc_wire_decoder_open_layers",
+           "sc_wire_decoder_open_segments", "sc_wire_decoder_open_layers_segments", "sc_wire_decoder_tokens",
            "sc_wire_decoder_restore", "sc_wire_decoder_live_ids", "sc_wire_decoder_small", "sc_wire_decoder_stage_small",
            "sc_wire_decoder_destroy")
 
@@ -152,6 +160,12 @@ class Encoder:
         _check(lib.sc_wire_encode_async(self.handle, payload_ptr, capacity, sc._stream(stream),
                                         gathered.handle if gathered is not None else None), "sc_wire_encode_async")
 
+    def encode_segments(self, seg_ptrs, segment_bytes: int, stream=None) -> None:
+        """Enqueue the encode straight into a payload held in segments (sc_wire_encode_segments_async)."""
+        segs, keep = sc.segments_struct(seg_ptrs, segment_bytes)
+        _check(lib.sc_wire_encode_segments_async(self.handle, C.byref(segs), sc._stream(stream)),
+               "sc_wire_encode_segments_async")
+
     def hash(self) -> int:
         out = C.c_uint64(0)
         _check(lib.sc_wire_encoder_hash(self.handle, C.byref(out)), "sc_wire_encoder_hash")
@@ -170,12 +184,24 @@ class Encoder:
 
 
 class Decoder:
+    """A payload opened for a slot.  `payload_ptr` is a contiguous device payload, or `segments` = (device pointers,
+    segment_bytes) a payload held in segments (another process's imported ones), mounted where it lies."""
+
     def __init__(self, payload_ptr: int, nbytes: int, geo, slot, geometry=None, geom_hash=0, pack_hash=0,
-                 check_identity=False, payload_hash=0, check_hash=False, stages=None, n_stages: int = 0):
+                 check_identity=False, payload_hash=0, check_hash=False, stages=None, n_stages: int = 0,
+                 segments=None):
         self._slot = slot.c_struct()
         self._geo18 = (C.c_int64 * 18)(*geometry) if geometry is not None else None
         h = C.c_void_p()
-        if stages is not None:
+        if segments is not None:
+            if stages is not None:
+                raise ValueError("a layer-split payload is not mounted from segments")
+            segs, keep = sc.segments_struct(*segments)
+            open_ = (lib.sc_wire_decoder_open_layers_segments if isinstance(slot, sc.LayerPools)
+                     else lib.sc_wire_decoder_open_segments)
+            _check(open_(C.byref(segs), nbytes, C.byref(geo), C.byref(self._slot), self._geo18, geom_hash, pack_hash,
+                         int(check_identity), payload_hash, int(check_hash), C.byref(h)), "sc_wire_decoder_open_segments")
+        elif stages is not None:
             _check(lib.sc_wire_decoder_open_split(payload_ptr, nbytes, C.byref(geo), C.byref(self._slot), stages,
                                                   n_stages, self._geo18, geom_hash, pack_hash, int(check_identity),
                                                   payload_hash, int(check_hash), C.byref(h)),

@@ -8,6 +8,8 @@
     python tests/ipc_peer.py slot FORMAT TOKENS SEED
         a slot of LayerPools randomized with SEED, its payload encoded and staged ->
         {"segments": ..., "bytes": ..., "hash": ...}; then waits for "done"
+    python tests/ipc_peer.py zerocopy FORMAT TOKENS SEED
+        the same slot's payload encoded straight into the exported segments (no payload buffer, no stage copy)
 """
 import json
 import sys
@@ -51,7 +53,7 @@ def raw(capacity, segment_bytes):
     ex.destroy()
 
 
-def slot(fmt, tokens, seed):
+def slot(fmt, tokens, seed, zero_copy=False):
     import sc_wire
     geo = sc.geometry(**SMALL)
     pools = sc.LayerPools(geo, fmt, (tokens + 3) // 4 * 4 + 16, True)
@@ -60,10 +62,13 @@ def slot(fmt, tokens, seed):
     live, keep = sc_wire.make_live(GEOKEY, ids, layer_lo=0, layer_hi=8, idx_dim=128, imgs=[(5, 77)], used=tokens,
                                    small=(b"ple", b"tails", b"", b"bp"))
     enc = sc_wire.Encoder(geo, pools, tokens, live, 0x1111, 0x2222)
-    payload = sc.DeviceBuffer(enc.bytes, "uint8")
-    enc.encode(payload.ptr, enc.bytes)
     ex = sc.IpcExport(enc.bytes, 1 << 20)      # 1 MiB segments: the payload spans several
-    ex.stage(payload.ptr, enc.bytes)
+    if zero_copy:
+        enc.encode_segments(*ex.layout())
+    else:
+        payload = sc.DeviceBuffer(enc.bytes, "uint8")
+        enc.encode(payload.ptr, enc.bytes)
+        ex.stage(payload.ptr, enc.bytes)
     sc.device_sync()
     say({"segments": segments_json(ex), "bytes": enc.bytes, "hash": enc.hash()})
     sys.stdin.readline()
@@ -74,4 +79,4 @@ if __name__ == "__main__":
     if sys.argv[1] == "raw":
         raw(int(sys.argv[2]), int(sys.argv[3]))
     else:
-        slot(int(sys.argv[2]), int(sys.argv[3]), int(sys.argv[4]))
+        slot(int(sys.argv[2]), int(sys.argv[3]), int(sys.argv[4]), zero_copy=sys.argv[1] == "zerocopy")

@@ -6,8 +6,8 @@ and hashes the whole payload in one kernel; the bytes no row writes (a head copi
 place) are hashed as the payload holds them.  Each case fills the payload with a pattern, runs the plans and the plain
 hash, fills it again, runs the map, and requires the same payload bytes and the same hash, which must also be the byte
 loop's (sco_fnv1a64, pinned to the published FNV-1a vectors).  Sizes cover a payload under one lane segment, tails
-that are not whole lane segments, several blobs inside one lane segment, pages that cross lane segments, and a table
-with holes.
+that are not whole lane segments, several blobs inside one lane segment (the small scale and indexer blobs of
+quantized slots), pages that cross lane segments, and a table with holes.
 """
 import numpy as np
 import pytest
@@ -99,6 +99,32 @@ def test_fused_map_with_head_and_offsets(sc, oracle, cuda):
     _compare(sc, oracle, plans, payload, total, 0x11, head=head_bytes)
     for p in plans:
         p.destroy()
+
+
+@pytest.mark.parametrize("fmt", [1, 2, 3])
+@pytest.mark.parametrize("index", [False, True])
+@pytest.mark.parametrize("tokens", [1, 77])
+def test_fused_map_small_blobs_of_every_format(sc, oracle, cuda, fmt, index, tokens):
+    """Blobs of a quantized slot packed as a wire payload's pool (64-byte aligned, in record order, after a head):
+    with one token the scales and indexer rows are 32-512 bytes, so one lane segment holds the end of a code blob and
+    two or three whole small blobs (a segment over three runs and more, the first ending at its extent's end)."""
+    geo = sc.geometry(**SMALL)
+    print(f"case hash map format {fmt} index {index} tokens {tokens}", flush=True)
+    pools = sc.LayerPools(geo, fmt, 96, index)
+    pools.randomize(0x3B + fmt)
+    sizes = sc.layer_blob_bytes(geo, fmt, index, tokens)
+    at, offsets = 896, []
+    for _ in range(geo.n_qsa):
+        for b in range(5):
+            offsets.append(at if sizes[b] else None)
+            at += (sizes[b] + 63) // 64 * 64
+    offsets.append(at)
+    total = at + geo.n_gdn * geo.gdn_row_floats * 4 + 48
+    payload = sc.DeviceBuffer(total, "uint8")
+    plan = sc.plan_capture_layers(geo, pools, tokens, payload.ptr, total, offsets=offsets)
+    head = np.random.default_rng(fmt).integers(0, 256, size=896, dtype=np.uint8)
+    _compare(sc, oracle, [plan], payload, total, 0xC4, head=head)
+    plan.destroy()
 
 
 def test_fused_map_at_full_size(sc, oracle, cuda):

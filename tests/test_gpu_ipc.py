@@ -3,8 +3,13 @@
 A second process (tests/ipc_peer.py) exports device segments and stages payloads into them; this process opens the
 segments and fetches each payload into its own device memory.  Every fetched payload must equal, byte for byte, what
 the exporter staged (regenerated here from the same seed) and carry the exporter's device FNV-1a; a slot's payload
-fetched this way must mount into fresh pools equal to the exporter's (rebuilt here from the same seed).  Two
-processes use the GPU; each shared allocation stays at or under 1 GiB.
+fetched this way must mount into fresh pools equal to the exporter's (rebuilt here from the same seed).
+
+The zero-copy hand-off: the exporter encodes the slot straight into its exported segments (no payload buffer, no
+stage), and this process mounts the payload where it lies in the imported segments (no fetch), the hash checked on the
+device over the segments before any byte reaches the slot.  The mounted pools must equal the exporter's, in f16, int8
+and q4_0 with the indexer's rows; a wrong expected hash must leave the pools untouched.  Two processes use the GPU;
+each shared allocation stays at or under 1 GiB.
 """
 import json
 import subprocess
@@ -76,6 +81,28 @@ def test_raw_payloads_cross_the_process_boundary(sc, cuda):
         peer.finish()
 
 
+def _pools(sc, fmt, tokens, seed):
+    geo = sc.geometry(n_layers=8, qsa_interval=4, n_head_kv=2, head_dim=256, page_size=4, ssm_state_size=32,
+                      ssm_k_heads=4, ssm_v_heads=8, ssm_d_conv=4, ssm_conv_channels=520, idx_key_dim=128)
+    cap = (tokens + 3) // 4 * 4 + 16
+    src = sc.LayerPools(geo, fmt, cap, True)
+    src.randomize(seed)                             # the exporter's pools, rebuilt from the same seed
+    dst = sc.LayerPools(geo, fmt, cap, True)
+    dst.fill(0x99)
+    return geo, src, dst
+
+
+def _assert_mounted(sc, geo, fmt, tokens, src, dst):
+    a, b = src.host(), dst.host()
+    sizes = sc.layer_blob_bytes(geo, fmt, True, tokens)
+    for key in a:
+        if key == "gdn":
+            assert np.array_equal(a[key], b[key])
+        else:
+            k = sizes[key[0]]
+            assert np.array_equal(a[key][:k], b[key][:k]) and (b[key][k:] == 0x99).all(), key
+
+
 @pytest.mark.parametrize("fmt", [0, 1, 3])
 def test_slot_payload_mounts_from_another_process(sc, cuda, fmt):
     import sc_wire
@@ -88,25 +115,49 @@ def test_slot_payload_mounts_from_another_process(sc, cuda, fmt):
         payload = sc.DeviceBuffer(n, "uint8")
         imp.fetch(payload.ptr, n)
         sc.device_sync()
-        geo = sc.geometry(n_layers=8, qsa_interval=4, n_head_kv=2, head_dim=256, page_size=4, ssm_state_size=32,
-                          ssm_k_heads=4, ssm_v_heads=8, ssm_d_conv=4, ssm_conv_channels=520, idx_key_dim=128)
-        cap = (tokens + 3) // 4 * 4 + 16
-        src = sc.LayerPools(geo, fmt, cap, True)
-        src.randomize(seed)                             # the exporter's pools, rebuilt from the same seed
-        dst = sc.LayerPools(geo, fmt, cap, True)
-        dst.fill(0x99)
+        geo, src, dst = _pools(sc, fmt, tokens, seed)
         dec = sc_wire.Decoder(payload.ptr, n, geo, dst, geom_hash=0x1111, pack_hash=0x2222, check_identity=True,
                               payload_hash=h, check_hash=True)
         assert dec.tokens == tokens
         dec.restore()
-        a, b = src.host(), dst.host()
-        sizes = sc.layer_blob_bytes(geo, fmt, True, tokens)
-        for key in a:
-            if key == "gdn":
-                assert np.array_equal(a[key], b[key])
-            else:
-                k = sizes[key[0]]
-                assert np.array_equal(a[key][:k], b[key][:k]) and (b[key][k:] == 0x99).all(), key
+        _assert_mounted(sc, geo, fmt, tokens, src, dst)
+    finally:
+        if imp:
+            imp.close()
+        peer.finish()
+
+
+@pytest.mark.parametrize("fmt", [0, 1, 3])
+def test_zero_copy_hand_off(sc, cuda, fmt):
+    """Encode into the exported segments, mount from the imported ones: no stage, no fetch."""
+    import sc_wire
+    tokens, seed = 1203, 0xBEEF + fmt           # a payload over several 1 MiB segments
+    peer = Peer("zerocopy", fmt, tokens, seed)
+    imp = None
+    try:
+        n, h = peer.first["bytes"], peer.first["hash"]
+        imp = sc.IpcImport(peer.segments())
+        ptrs, seg_bytes = imp.layout()
+        assert seg_bytes == 1 << 20 and len(ptrs) == (n + seg_bytes - 1) // seg_bytes >= 2
+        # the exporter's hash is the hash of the bytes the segments hold, hashed here where they lie
+        hp = sc.HashPlan(n)
+        hmap = sc.HashMap.read(ptrs, seg_bytes, n)
+        hmap.launch(hp)
+        sc.device_sync()
+        assert hp.result() == h
+        hmap.destroy()
+        hp.free()
+        geo, src, dst = _pools(sc, fmt, tokens, seed)
+        with pytest.raises(sc_wire.WireError):
+            sc_wire.Decoder(0, n, geo, dst, geom_hash=0x1111, pack_hash=0x2222, check_identity=True,
+                            payload_hash=h ^ 1, check_hash=True, segments=(ptrs, seg_bytes)).restore()
+        assert all((v == 0x99).all() for v in dst.host().values())
+        dec = sc_wire.Decoder(0, n, geo, dst, geom_hash=0x1111, pack_hash=0x2222, check_identity=True,
+                              payload_hash=h, check_hash=True, segments=(ptrs, seg_bytes))
+        assert dec.tokens == tokens
+        dec.restore()
+        assert dec.small(0) == b"ple" and dec.small(1) == b"tails" and dec.small(3) == b"bp"
+        _assert_mounted(sc, geo, fmt, tokens, src, dst)
     finally:
         if imp:
             imp.close()
