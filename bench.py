@@ -151,6 +151,29 @@ def time_launches(plan, stream, steps: int, warmup: int, sc) -> tuple[float, lis
     return wall_ms, per
 
 
+def trace_summary(path: str, kernel: str, warmup: int, steps: int, payload_bytes: int) -> dict:
+    """The headline launches in a rocprofv3 kernel trace (its *_kernel_trace.csv) of `bench.py --kernel-only`: the
+    first warmup + steps dispatches of `kernel` in start order are the bench's warm-up and timed launches; each part's
+    mean / p50 / min / max duration and the roofline fraction 2P / mean of the timed ones, the statistic the line's
+    roofline reports from HIP events."""
+    import csv
+    with open(path) as f:
+        rows = sorted(csv.DictReader(f), key=lambda r: int(r["Start_Timestamp"]))
+    ds = [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-6 for r in rows if kernel in r["Kernel_Name"]]
+    if len(ds) < warmup + steps:
+        raise SystemExit(f"{path}: {len(ds)} dispatches of {kernel}, fewer than {warmup} + {steps}")
+
+    def stats(xs):
+        ys = sorted(xs)
+        mean = sum(xs) / len(xs)
+        return {"n": len(xs), "mean_ms": round(mean, 4), "p50_ms": round(ys[len(ys) // 2], 4),
+                "min_ms": round(ys[0], 4), "max_ms": round(ys[-1], 4)}
+    timed = stats(ds[warmup:warmup + steps])
+    return {"kernel": kernel, "dispatches": len(ds), "warmup": stats(ds[:warmup]) if warmup else None, "timed": timed,
+            "all": stats(ds),
+            "frac_timed_mean": round(2 * payload_bytes / (timed["mean_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
+
+
 def retarget_latency(sc, geo, tokens: int, case, slot, plan, stream, reps: int) -> dict:
     """A serving engine's hand-off at 32K with one plan per decode slot: the plan re-pointed at the next prefill
     sequence (sc_plan_retarget) and launched, host wall clock from before the retarget to the completion event's sync,
@@ -1064,11 +1087,18 @@ def main() -> int:
     ap.add_argument("--mover", default="64,4,8", help="arena mover chunk MiB, depth, threads")
     ap.add_argument("--ipc-only", action="store_true", help="only the same-GPU inter-process row; prints its JSON")
     ap.add_argument("--ipc-export", type=int, default=0, metavar="TOKENS", help=argparse.SUPPRESS)
+    ap.add_argument("--trace-summary", metavar="CSV",
+                    help="summarize the headline launches of a kernel trace of --kernel-only (same --steps/--warmup)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run 5 device-to-device copies of BYTES (the counter calibration of profiler runs)")
     args = ap.parse_args()
     if args.ipc_export:
         return ipc_export_role(args.ipc_export)
+    if args.trace_summary:
+        import sc_handoff as sc
+        P = sc.payload_bytes(sc.geometry(**HEADLINE_GEO), args.tokens)
+        print(json.dumps(trace_summary(args.trace_summary, "sc_move_kernel", args.warmup, args.steps, P)), flush=True)
+        return 0
 
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "

@@ -550,10 +550,10 @@ __device__ u32x4 g_hash_zero_chunk;   // read for zero runs, so every chunk take
 // runs or more, and the payload's last partial segment, goes chunk by chunk into the payload, which the lane then reads
 // back (its own stores, after a fence).  The payload is written by store_wave below (the last partial segment only
 // here).
-__device__ __forceinline__ void gather_segment(const HashMapArgs& m, uint8_t* base, uint32_t e, uint64_t begin,
+__device__ __forceinline__ void gather_segment(const HashMapArgs& m, uint8_t* base, uint32_t e_group, uint64_t begin,
                                                uint64_t len, uint32_t (&w)[kFnvLaneBytes / 4]) {
+    uint32_t e = e_group;
     while (m.ext[e].end <= begin) ++e;
-    const uint32_t e_begin = e;   // the extent holding `begin`: where the chunk-by-chunk walk below starts
     HashExtent x = m.ext[e];
     uint8_t* dst = base + begin;   // `base` + o addresses payload byte o of this workgroup's segment
     const uint64_t seg_end = begin + len;
@@ -584,8 +584,10 @@ __device__ __forceinline__ void gather_segment(const HashMapArgs& m, uint8_t* ba
             }
             return;
         }
-        // three runs or more: walk from the first again (the look-ahead above may have moved past its extent)
-        e = e_begin;
+        // three runs or more: walk from the workgroup's first extent again (the look-ahead above may have moved past
+        // the extent holding `begin`)
+        e = e_group;
+        while (m.ext[e].end <= begin) ++e;
         x = m.ext[e];
     }
 #pragma unroll 1
@@ -636,8 +638,9 @@ __device__ __forceinline__ void store_wave(u32x4 (&lds)[16 * kXposeRow], const u
 // status: three arrays of `stride` words (one per level); ctl: [0] the ticket counter, [1] the fault word, [2..3] the
 // sum of the workgroups' sums (each workgroup adds its own with one 64-bit atomic).  kMapped: the payload is gathered
 // through `map` (stored, and hashed up to `n`, its whole lane segments) instead of read from `data`.
-// Five waves per SIMD (the mapped instance would take 110 VGPRs and four; held to 96 it spills a few words and ran
-// the fused 128K capture in 2.73 against 2.82 ms).
+// Five waves per SIMD (the mapped instance would take 110 VGPRs and four; held to 96 it spills 5 words and runs the
+// fused 128K capture in 2.78-2.85 ms against 2.82 at four waves).  Every value the gather keeps live past its look-ahead
+// costs spills here: an extra extent index held across it spilled 35 words and took the capture to 3.03 ms.
 template <bool kMapped>
 __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5, 8))) fnv_onepass_kernel(const uint8_t* data, uint64_t n, bool aligned,
                                                                 uint64_t seed, const uint64_t* seed_dev,
