@@ -285,9 +285,8 @@ __device__ __forceinline__ uint64_t shfl_xor64(uint64_t v, int m) {
 
 // One partial or unaligned segment's Horner sum, scaled by p^(bytes after it), from the true low byte `l` at its
 // start, a byte at a time.
-__device__ __forceinline__ uint64_t segment_sum(const uint8_t* data, uint64_t n, uint64_t begin, uint32_t l) {
+__device__ __forceinline__ uint64_t segment_sum(const uint8_t* p, uint64_t n, uint64_t begin, uint32_t l) {
     const uint64_t len = n - begin < kFnvLaneBytes ? n - begin : kFnvLaneBytes;
-    const uint8_t* p = data + begin;
     uint64_t acc = 0;
     for (uint64_t i = 0; i < len; ++i) step_full(p[i], l, acc);
     return acc * pow_prime(n - begin - len);
@@ -637,7 +636,8 @@ __device__ __forceinline__ void store_wave(u32x4 (&lds)[16 * kXposeRow], const u
 
 // status: three arrays of `stride` words (one per level); ctl: [0] the ticket counter, [1] the fault word, [2..3] the
 // sum of the workgroups' sums (each workgroup adds its own with one 64-bit atomic).  kMapped: the payload is gathered
-// through `map` (stored, and hashed up to `n`, its whole lane segments) instead of read from `data`.
+// through `map` (stored, and hashed up to `n`, its whole lane segments) instead of read from `data`.  Not kMapped,
+// with `map.seg` set: the payload is read where its segments hold it (`data` unused).
 // Five waves per SIMD (the mapped instance would take 110 VGPRs and four; held to 96 it spills 5 words and runs the
 // fused 128K capture in 2.78-2.85 ms against 2.82 at four waves).  Every value the gather keeps live past its look-ahead
 // costs spills here: an extra extent index held across it spilled 35 words and took the capture to 3.03 ms.
@@ -659,6 +659,11 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5
     const uint64_t len = !live ? 0 : n - begin < kFnvLaneBytes ? n - begin : kFnvLaneBytes;
     const bool full = aligned && len == kFnvLaneBytes;
     const uint8_t* p = data + begin;
+    if (!kMapped && map.seg) {
+        // a payload read where its segments hold it: this workgroup's 64 KiB lie in segment k
+        const uint64_t k = g * uint64_t(kFnvGroupBytes) / map.seg_bytes;
+        p = map.seg[k] + (begin - k * map.seg_bytes);
+    }
     uint32_t* fault = ctl + 1;
     uint32_t w[kFnvLaneBytes / 4] = {};
     if constexpr (kMapped) {
@@ -715,7 +720,7 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5
         const uint64_t wave_pow = pow_prime((n - wave_end) & ((uint64_t(1) << 62) - 1));
         acc = halves_sum(w, s | (lm << 16)) * kLanePow.v[lane] * wave_pow;
     } else if (live) {
-        acc = segment_sum(data, n, begin, s);
+        acc = segment_sum(p, n, begin, s);
     }
     for (int m = 32; m > 0; m >>= 1) acc += shfl_xor64(acc, m);
     if (lane == 0) s_sum[wave] = acc;
@@ -786,6 +791,23 @@ hipError_t launch_fnv1a64_mapped(const HashMapArgs& map, const uint8_t* tail, ui
     uint8_t* ws = static_cast<uint8_t*>(workspace);
     uint32_t* ctl = reinterpret_cast<uint32_t*>(ws + w.off_ctl);
     uint32_t* status = reinterpret_cast<uint32_t*>(ws + w.off_status);
+    if (!map.store) {
+        // a map that only reads: the plain kernel hashes the payload where its segments hold it, the last partial
+        // lane segment included (no gather, so nothing waits for bytes to be placed)
+        if (w.groups > 0) {
+            const uint64_t words = 3 * w.stride;
+            const uint64_t init_blocks = (words + kThreads - 1) / kThreads < 1024 ? (words + kThreads - 1) / kThreads : 1024;
+            hipLaunchKernelGGL(fnv_onepass_init_kernel, dim3(unsigned(init_blocks)), dim3(kThreads), 0, stream, status,
+                               words, ctl);
+            hipLaunchKernelGGL(fnv_onepass_kernel<false>, dim3(unsigned(w.groups)), dim3(kThreads), 0, stream, nullptr,
+                               n_total, true, seed, nullptr, status, w.stride, ctl, g_spin_limit.load(), map);
+        }
+        const bool any = w.groups > 0;
+        hipLaunchKernelGGL(fnv_finish_kernel, dim3(1), dim3(1), 0, stream,
+                           any ? reinterpret_cast<const uint64_t*>(ctl + 2) : nullptr, seed, nullptr, n_total, out,
+                           fault_out, false, expected, verdict, any ? ctl + 1 : nullptr, nullptr, 0u);
+        return hipGetLastError();
+    }
     if (w.groups > 0) {
         const uint64_t words = 3 * w.stride;
         const uint64_t init_blocks = (words + kThreads - 1) / kThreads < 1024 ? (words + kThreads - 1) / kThreads : 1024;

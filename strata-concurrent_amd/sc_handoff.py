@@ -685,6 +685,9 @@ class HashPlan:
         self.out = DeviceBuffer(1, "uint64")
         self.fault = DeviceBuffer(1, "uint32")
         self.verdict = DeviceBuffer(1, "uint32")
+        self.fault.fill(0)     # a launch that is given no fault word leaves this one clear
+        self.verdict.fill(0)
+        device_sync()          # before any launch on another stream writes them
 
     def launch(self, ptr: int, nbytes: int, seed: int = REFERENCE_FNV_SEED, stream=None) -> None:
         if nbytes > self.max_bytes:
