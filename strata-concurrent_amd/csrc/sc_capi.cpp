@@ -238,6 +238,10 @@ bool orderable_kind(int32_t kind) { return kind == sc::kKv16 || kind == sc::kKv3
 uint64_t items_per_page(int32_t kind, const Geo& g) {
     return quant_kind(kind) ? uint64_t(g.ps) * uint64_t(g.H) : g.page_bytes / 16;
 }
+// Whether any quantizing row writes through a page table (such plans launch the instance that stages those rows).
+bool quant_tables(const std::vector<sc::MoveRow>& rows) {
+    return std::any_of(rows.begin(), rows.end(), [](const sc::MoveRow& r) { return quant_kind(r.kind) && r.table; });
+}
 uint64_t items_per_tile(int32_t kind) {
     return kind == sc::kConv ? sc::kConvTileChannels : quant_kind(kind) ? sc::kQuantUnitsPerTile : sc::kTileChunks;
 }
@@ -389,7 +393,7 @@ int finish_plan(std::vector<sc::MoveRow>& rows, const Geo& g, uint64_t payload, 
     p->n_tiles = tiles;
     p->payload = payload;
     p->grid = p->default_grid = int64_t(std::min<uint64_t>(tiles, kMaxGrid));
-    p->mix = sc::mix_of(kv32, quant);
+    p->mix = sc::mix_of(kv32, quant, quant_tables(rows));
     // The XCD-contiguous numbering of the tiles (xcd_tile, sc_kernels.hip) measured faster for the identity carve
     // (1.072-1.075 against 1.088-1.118 ms at 128K) and slower for a carve through shuffled tables in destination order
     // (1.164 against 1.142-1.153 ms) and for the f32 and quantizing rows, which read 2-7 times what they write
@@ -923,7 +927,7 @@ int sc_plan_retarget(sc_plan* plan, const sc_prefill_view* src, void* stream) {
         plan->n_rows = int(rows.size());
         plan->n_tiles = tiles;
         plan->payload = payload;
-        plan->mix = sc::mix_of(kv32, quant);
+        plan->mix = sc::mix_of(kv32, quant, quant_tables(rows));
         plan->default_grid = int64_t(std::min<uint64_t>(tiles, kMaxGrid));
         if (!rt->grid_set) plan->grid = plan->default_grid;
         plan->xcd = plan->mix == sc::kMixPlain &&

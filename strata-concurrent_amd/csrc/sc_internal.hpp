@@ -48,13 +48,16 @@ enum MoveKind : int32_t {
 // register budget of the f32 rounding or the quantizing tiles.  A plan launches the smallest instance whose set
 // holds every kind it has (mix_of).
 enum MoveMix : int32_t {
-    kMixPlain = 0,   // kKv16, kRec, kConv, kPages*, kCopy, kZero
-    kMixWide = 1,    // plain + kKv32
-    kMixQuant = 2,   // plain + kKvQ8, kKvQ4
-    kMixAll = 3,     // every kind
+    kMixPlain = 0,        // kKv16, kRec, kConv, kPages*, kCopy, kZero
+    kMixWide = 1,         // plain + kKv32
+    kMixQuant = 2,        // plain + kKvQ8, kKvQ4
+    kMixAll = 3,          // every kind
+    kMixQuantPaged = 4,   // kMixQuant with the int8 rows through a page table staged in LDS (a separate instance, so
+                          // that the identity carve keeps the code of the instance without the staging)
 };
-constexpr int32_t mix_of(bool has_kv32, bool has_quant) {
-    return has_quant ? (has_kv32 ? kMixAll : kMixQuant) : (has_kv32 ? kMixWide : kMixPlain);
+constexpr int32_t mix_of(bool has_kv32, bool has_quant, bool quant_tables = false) {
+    return has_quant ? (has_kv32 ? kMixAll : quant_tables ? kMixQuantPaged : kMixQuant)
+                     : (has_kv32 ? kMixWide : kMixPlain);
 }
 
 // Quantizing rows move one (token, head) row of 256 values per wave at a time: a tile is 16 rows (16 KiB of f32).

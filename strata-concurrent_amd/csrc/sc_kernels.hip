@@ -466,10 +466,23 @@ __device__ void tile_q8(const MoveRow& r, const MoveGeo& g, uint64_t local) {
                                   s_q8_codes[u][4 * c + 3]};
             *(gu32x4*) (r.dst + uint64_t(prow) * kQuantDim + c * 16) = v;
         }
-        if (t < kQuantUnitsPerTile) {
-            const int64_t sp = s_q8_prow[t];
+        if (t < kQuantUnitsPerTile / 2) {
+            // units u and u + H are (cell, h) and (cell + 1, h): one 16-byte store when their scale rows are
+            // consecutive (one page) and the pair starts on 16 bytes, else one 8-byte store each
+            const uint32_t H = g.heads.d, th = fdiv(uint32_t(t), g.heads);
+            const bool pairs = kQuantUnitsPerTile % (2 * H) == 0;
+            const int u0 = pairs ? int(th * 2 * H + (uint32_t(t) - th * H)) : 2 * t;
+            const int u1 = pairs ? u0 + int(H) : 2 * t + 1;
+            const int64_t p0 = s_q8_prow[u0], p1 = s_q8_prow[u1];
             using g64 = __attribute__((address_space(1))) uint64_t;
-            if (sp >= 0) *(g64*) (r.dst2 + uint64_t(sp) * 8) = s_q8_scale[t];
+            if (p0 >= 0 && p1 == p0 + 1 && (p0 & 1) == 0) {
+                const uint64_t a = s_q8_scale[u0], b = s_q8_scale[u1];
+                *(gu32x4*) (r.dst2 + uint64_t(p0) * 8) =
+                    u32x4{uint32_t(a), uint32_t(a >> 32), uint32_t(b), uint32_t(b >> 32)};
+            } else {
+                if (p0 >= 0) *(g64*) (r.dst2 + uint64_t(p0) * 8) = s_q8_scale[u0];
+                if (p1 >= 0) *(g64*) (r.dst2 + uint64_t(p1) * 8) = s_q8_scale[u1];
+            }
         }
     }
     __syncthreads();
@@ -621,12 +634,16 @@ sc_move_kernel(const MoveRow* __restrict__ rows, const uint16_t* __restrict__ ti
             case kCopy: tile_copy(r, local, false); break;
             case kZero: tile_copy(r, local, true); break;
             case kKvQ8:
-                if constexpr (kMix == kMixQuant || kMix == kMixAll) {
+                if constexpr (kMix == kMixQuant) {
+                    tile_q8<false>(r, geo, local);
+                } else if constexpr (kMix == kMixQuantPaged || kMix == kMixAll) {
                     if (r.table) tile_q8<true>(r, geo, local);
                     else tile_q8<false>(r, geo, local);
                 }
                 break;
-            case kKvQ4: if constexpr (kMix == kMixQuant || kMix == kMixAll) tile_q4(r, geo, local); break;
+            case kKvQ4:
+                if constexpr (kMix == kMixQuant || kMix == kMixQuantPaged || kMix == kMixAll) tile_q4(r, geo, local);
+                break;
             default: break;
         }
     }
@@ -1114,7 +1131,7 @@ hipError_t launch_ring_table(int32_t* table, int64_t n_blocks, int64_t n_slots, 
 hipError_t launch_move(const MoveRow* rows, const uint16_t* tile_row, const MoveGeo& geo, uint64_t n_tiles,
                        int64_t grid, int32_t mix, bool xcd, hipStream_t stream, const uint32_t* gate) {
     if (n_tiles == 0) return hipSuccess;
-    if (!rows || !tile_row || grid <= 0 || mix < kMixPlain || mix > kMixAll) return hipErrorInvalidValue;
+    if (!rows || !tile_row || grid <= 0 || mix < kMixPlain || mix > kMixQuantPaged) return hipErrorInvalidValue;
     const dim3 blocks(unsigned(uint64_t(grid) < n_tiles ? uint64_t(grid) : n_tiles)), threads(kThreads);
     switch (mix) {
         case kMixPlain:
@@ -1125,6 +1142,10 @@ hipError_t launch_move(const MoveRow* rows, const uint16_t* tile_row, const Move
             break;
         case kMixQuant:
             hipLaunchKernelGGL(sc_move_kernel<kMixQuant>, blocks, threads, 0, stream, rows, tile_row, geo, n_tiles, gate, xcd);
+            break;
+        case kMixQuantPaged:
+            hipLaunchKernelGGL(sc_move_kernel<kMixQuantPaged>, blocks, threads, 0, stream, rows, tile_row, geo, n_tiles, gate,
+                               xcd);
             break;
         default:
             hipLaunchKernelGGL(sc_move_kernel<kMixAll>, blocks, threads, 0, stream, rows, tile_row, geo, n_tiles, gate, xcd);
