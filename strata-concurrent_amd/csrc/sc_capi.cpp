@@ -1514,13 +1514,14 @@ int segment_list(const sc_segments* s, uint64_t bytes, std::vector<uint8_t*>& se
     return SC_OK;
 }
 
-// Uploads a map: the extents, each workgroup's first extent and the segment table, in one device block.
+// Uploads a map: the extents, each workgroup's first extent and the segment table, in one device block.  A map that
+// only reads (no extents) is hashed by the plain kernel from the segment table alone, so it uploads nothing else.
 int make_hash_map(const std::vector<sc::HashExtent>& ext, uint64_t bytes, const std::vector<uint8_t*>& segs,
                   uint64_t seg_bytes, bool store, sc_hash_map** out) {
     const sc::FnvWorkspace w = sc::fnv_workspace(bytes);
-    std::vector<uint32_t> first(std::max<uint64_t>(w.groups, 1), 0);
+    std::vector<uint32_t> first(store ? std::max<uint64_t>(w.groups, 1) : 1, 0);
     size_t e = 0;
-    for (uint64_t g = 0; g < w.groups; ++g) {
+    for (uint64_t g = 0; store && g < w.groups; ++g) {
         const uint64_t o = g * uint64_t(sc::kFnvGroupBytes);
         while (e + 1 < ext.size() && ext[e].end <= o) ++e;
         first[g] = uint32_t(e);
@@ -1537,7 +1538,7 @@ int make_hash_map(const std::vector<sc::HashExtent>& ext, uint64_t bytes, const 
     uint8_t* block = reinterpret_cast<uint8_t*>(m->ext_dev);
     m->first_dev = reinterpret_cast<uint32_t*>(block + ext_bytes);
     m->seg_dev = reinterpret_cast<uint8_t**>(block + ext_bytes + first_bytes);
-    err = hipMemcpy(m->ext_dev, ext.data(), ext.size() * sizeof(sc::HashExtent), hipMemcpyHostToDevice);
+    if (!ext.empty()) err = hipMemcpy(m->ext_dev, ext.data(), ext.size() * sizeof(sc::HashExtent), hipMemcpyHostToDevice);
     if (err == hipSuccess) err = hipMemcpy(m->first_dev, first.data(), first.size() * 4, hipMemcpyHostToDevice);
     if (err == hipSuccess) err = hipMemcpy(m->seg_dev, segs.data(), segs.size() * 8, hipMemcpyHostToDevice);
     if (err != hipSuccess) {
@@ -1600,14 +1601,7 @@ int sc_hash_map_create_read(const sc_segments* from, uint64_t bytes, sc_hash_map
         if (bytes % 16) return fail(SC_EINVAL, "sc_handoff: a hashed payload is whole 16-byte chunks");
         std::vector<uint8_t*> segs;
         if (const int rc = segment_list(from, bytes, segs)) return rc;
-        std::vector<sc::HashExtent> ext;
-        for (uint64_t k = 0, at = 0; at < bytes || ext.empty(); ++k) {
-            const uint64_t end = std::min(bytes, at + from->segment_bytes);
-            ext.push_back(sc::HashExtent{at, end, segs[size_t(k)], nullptr, 0, sc::kExtCopy, 0});
-            at = end;
-            if (bytes == 0) break;
-        }
-        return make_hash_map(ext, bytes, segs, from->segment_bytes, false, out);
+        return make_hash_map({}, bytes, segs, from->segment_bytes, false, out);
     });
 }
 
