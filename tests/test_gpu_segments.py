@@ -9,7 +9,9 @@ segment boundaries at many offsets):
   - the segments' bytes, joined, equal the contiguous encode's, and the two hashes are equal (and the byte loop's);
   - the mount from the segments, hash checked on the device over the segments, leaves the slot byte for byte as the
     mount of the contiguous payload does;
-  - a wrong expected hash refuses and leaves the slot untouched.
+  - a wrong expected hash refuses and leaves the slot untouched;
+  - with every page table in destination order, the first piece of each blob cut at a segment end is ordered and the
+    later pieces keep the source order at their chunk offset, and the mount still equals the contiguous one.
 The contiguous path is itself held to the oracle by tests/test_gpu_wire.py and tests/test_gpu_wire_layers.py.
 """
 import numpy as np
@@ -59,13 +61,24 @@ def _tables(sc, geo, n_pages, per, seed):
     return sc.device_tables(tabs)
 
 
+@pytest.fixture
+def order_all(sc, request):
+    """With request.param, every page table gets the destination order, however few pages it covers: the first piece
+    of a blob cut at a segment end is then ordered and the later pieces keep the source order."""
+    prev = sc.set_order_min_pages(1) if request.param else None
+    yield request.param
+    if prev is not None:
+        sc.set_order_min_pages(prev)
+
+
+@pytest.mark.parametrize("order_all", [False, True], indirect=True, ids=["default_order", "ordered"])
 @pytest.mark.parametrize("seg", SEGS)
 @pytest.mark.parametrize("table", ["identity", "shuffled"])
-def test_f16_slot_through_segments(sc, oracle, cuda, seg, table):
+def test_f16_slot_through_segments(sc, oracle, cuda, seg, table, order_all):
     import sc_wire as wire
     geo = sc.geometry(**SMALL)
     tokens, max_cells = 301, 320
-    print(f"case segments f16 {table} seg {seg}", flush=True)
+    print(f"case segments f16 {table} seg {seg} ordered {order_all}", flush=True)
     case = synth.SyntheticCase(geo, tokens, seed=0x5E6 + seg // 65536)
     n_pages = max_cells // geo.page_size + 5
     per = max_cells // geo.page_size
