@@ -5,7 +5,7 @@ sc_wire_encode_segments_async writes the payload straight into segments (the sam
 sc_wire_decoder_open_segments / _open_layers_segments mount it from them (the imported ones); no contiguous copy of the
 payload exists on either side.  For an f16 slot through identity and shuffled page tables and for slots in f16, int8
 and q4_0 with the indexer's rows, with 64 KiB and 192 KiB segments (so that the head, blobs and single pages straddle
-segment boundaries at many offsets):
+segment boundaries at many offsets) and with one segment larger than the payload:
   - the segments' bytes, joined, equal the contiguous encode's, and the two hashes are equal (and the byte loop's);
   - the mount from the segments, hash checked on the device over the segments, leaves the slot byte for byte as the
     mount of the contiguous payload does;
@@ -26,7 +26,7 @@ SMALL = dict(n_layers=8, qsa_interval=4, n_head_kv=2, head_dim=256, page_size=4,
 GEOKEY = [2560, 8, 4, 32, 4, 8, 4, 520, 256, 24, 2, 256, 128, 4, 4, 3, 1, 0]
 PACK, GEOM = 0x0123456789ABCDEF, 0x1F2E3D4C5B6A7988
 SEED = 1469598103934665603
-SEGS = [65536, 3 * 65536]
+SEGS = [65536, 3 * 65536, 64 << 20]   # the last: one segment larger than the payload
 
 
 def _segments(sc, n, seg, fill):
@@ -48,7 +48,7 @@ def _encode_both(sc, oracle, wire, enc, seg):
     want = buf.numpy(n).copy()
     assert h == oracle.fnv1a64(want, SEED)
     segs = _segments(sc, n, seg, 0xCD)
-    assert len(segs) >= 4
+    assert len(segs) >= 4 or seg > n
     enc.encode_segments([b.ptr for b in segs], seg)
     assert enc.hash() == h
     got = _joined(segs)
