@@ -11,7 +11,9 @@ segment boundaries at many offsets) and with one segment larger than the payload
     mount of the contiguous payload does;
   - a wrong expected hash refuses and leaves the slot untouched;
   - with every page table in destination order, the first piece of each blob cut at a segment end is ordered and the
-    later pieces keep the source order at their chunk offset, and the mount still equals the contiguous one.
+    later pieces keep the source order at their chunk offset, and the mount still equals the contiguous one;
+  - at config 2's full depth (884 MB in 64 MiB segments) the segments equal the contiguous payload and the mount from
+    them reproduces the source slot.
 The contiguous path is itself held to the oracle by tests/test_gpu_wire.py and tests/test_gpu_wire_layers.py.
 """
 import numpy as np
@@ -175,4 +177,43 @@ def test_segment_refusals(sc, cuda):
         wire.Decoder(0, n, geo, dst, payload_hash=h, check_hash=True, segments=(ptrs[:-1], seg))
     with pytest.raises(wire.WireError):
         wire.Decoder(0, n, geo, dst, payload_hash=h, check_hash=True, segments=(ptrs, seg + 4096))
+    enc.destroy()
+
+
+def test_full_depth_through_segments(sc, oracle, cuda):
+    """Config 2 (48 layers, 32K tokens): the 884 MB payload encoded into 64 MiB segments equals the contiguous encode
+    byte for byte with the same hash, and its mount from the segments reproduces every buffer of the source slot."""
+    import sc_wire as wire
+    geo = sc.geometry()
+    tokens = 32768
+    print(f"case full-depth segments {tokens} tokens", flush=True)
+    case = synth.SyntheticCase(geo, tokens, seed=0x5E9)
+    src = case.new_slot(max_cells=tokens)
+    case.carve_into(src)
+    del case
+    ids = (np.arange(tokens, dtype=np.int64) % 151_000).astype(np.int32)
+    geokey = [2560, 48, 4, 128, 16, 32, 4, 8192, 4096, 24, 2, 256, 128, 4, 4, 3, 1, 0]
+    live, keep = wire.make_live(geokey, ids, layer_hi=48, idx_dim=128)
+    enc = wire.Encoder(geo, src, tokens, live, GEOM, PACK)
+    n, seg = enc.bytes, 64 << 20
+    buf = sc.DeviceBuffer(n, "uint8")
+    enc.encode(buf.ptr, n)
+    h = enc.hash()
+    segs = _segments(sc, n, seg, 0xCD)
+    assert len(segs) >= 13
+    enc.encode_segments([b.ptr for b in segs], seg)
+    assert enc.hash() == h
+    assert sc.fnv1a64_device(buf.ptr, n) == h
+    want = buf.numpy(n)
+    at = 0
+    for b in segs:
+        got = b.numpy()
+        assert np.array_equal(got, want[at:at + b.nbytes]), at
+        at += b.nbytes
+    del want
+    buf.free()
+    dst = sc.new_slot(geo, tokens, fill=0)
+    wire.Decoder(0, n, geo, dst, payload_hash=h, check_hash=True, segments=([b.ptr for b in segs], seg)).restore()
+    for a, b in zip(src.buffers(), dst.buffers()):
+        assert sc.fnv1a64_device(a.ptr, a.nbytes) == sc.fnv1a64_device(b.ptr, b.nbytes)
     enc.destroy()
