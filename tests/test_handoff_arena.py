@@ -33,7 +33,8 @@ PRICED = "1048576,2097152,4194309"
 
 
 def run(binary, *args, stdin=None):
-    proc = subprocess.run([str(binary), *map(str, args)], capture_output=True, text=True, timeout=120, input=stdin)
+    # the window and big-slot cases commit several GiB of arena pages: a minute alone, longer beside other tests
+    proc = subprocess.run([str(binary), *map(str, args)], capture_output=True, text=True, timeout=600, input=stdin)
     assert proc.returncode == 0, proc.stderr + proc.stdout
     return proc.stdout
 
