@@ -18,17 +18,25 @@
 //      of p in any order.
 //
 // The buffer is split into lane segments of kFnvLaneBytes bytes, a workgroup's 256 lanes covering 64 KiB, and the
-// low byte is resolved in three levels: bits 0-2, 3-5 and 6-7.  A level for bits j .. j + k - 1 runs every segment's
-// machine from its known start bits 0..j-1 once per combination of the unknown start bits j .. j + k - 2, with the
-// level's top bit started at 0: the end value of a bit in a machine started from the true lower bits is the segment's
-// xor term for that bit (the term of a bit depends only on the lower start bits).  Two machines share one 24-bit
-// multiply (bytes 0 and 2 of a register); the first level needs only bits 0..2, which follow l' = (l ^ b) * 3 mod 8,
-// so its four machines share one register a byte each.  Per level: the lanes ballot the terms, each workgroup forms
-// its map of the k-bit state from them, finds its start state by a look-back over the workgroups before it, and each
-// lane derives its start bits from the workgroup's state and the ballots by xor-prefix arithmetic.  After the third
-// level every lane runs the full machine from its now complete start byte and forms its segment's Horner sum, scaled
-// by p^(bytes after the segment); the workgroups' sums are added, and a last kernel adds h_0 p^N.  All of it is one
-// kernel that reads the input once (the one-pass hash, below).
+// low byte is resolved in three levels: bits 0-2, 3-5 and 6-7.  A level's map of a run of bytes takes the level's bits
+// at the run's start to their values at its end, given the true lower bits.  The term of a bit depends only on the
+// lower start bits, so the end value of a bit in a machine started from the true lower bits, with the bit itself 0,
+// is the run's term for that bit.  The top two bits of a level need no machines of their own: flipping start bit i
+// (the bits below it fixed) flips bit i at every position, which changes the term of bit i + 1 by the xor over the run
+// of 1 ^ y_i, y_i being bit i of ((l ^ b) mod 2^i) * 179; and y_i = l_i ^ l'_i ^ b_i, so that xor is
+//     (length mod 2) ^ (term of bit i) ^ (parity of bit i over the run's bytes).
+// A level for bits j .. j + k - 1 therefore runs 2^(k-2) machines (one per value of the unknown start bits
+// j .. j + k - 3): two for a three-bit level (start bit j = 0, 1) and one for a two-bit level.  Each lane runs its
+// segment as two halves of 128 bytes side by side: both halves' machines share the multiplies (two 8-bit machines per
+// 24-bit multiply, bytes 0 and 2; the first level needs only bits 0..2, which follow l' = (l ^ b) * 3 mod 8, so four
+// machines share one register a byte each), each half's map comes from its machines and its byte parities, and the
+// lane's map is the second half's after the first's.  Per level: the lanes ballot their maps, each workgroup forms
+// its map of the k-bit state from them, finds its start state by a look-back over the workgroups before it, each
+// lane derives its start bits from the workgroup's state and the ballots by xor-prefix arithmetic, and its first
+// half's map gives the bits at its midpoint.  After the third level every lane runs the full machine of both halves
+// from their now complete start bytes and forms its segment's Horner sum, scaled by p^(bytes after the segment); the
+// workgroups' sums are added, and a last kernel adds h_0 p^N.  All of it is one kernel that reads the input once (the
+// one-pass hash, below).
 #include <hip/hip_runtime.h>
 
 #include <atomic>
@@ -80,17 +88,6 @@ typedef short v2i16 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pk_sub(uint32_t a, uint32_t b) {
     return __builtin_bit_cast(uint32_t, __builtin_bit_cast(v2i16, a) - __builtin_bit_cast(v2i16, b));
 }
-// Byte k of w, in bytes 0 and 2 (v_perm_b32: selector 0x0c gives a zero byte).
-template <int k>
-__device__ __forceinline__ uint32_t spread(uint32_t w) {
-    return __builtin_amdgcn_perm(0u, w, uint32_t(k | 0x0c00 | (k << 16) | 0x0c000000));
-}
-
-// The byte loops of the machines, for partial and unaligned segments (whole segments run from registers, below).
-__device__ __forceinline__ uint32_t pair_bytes(const uint8_t* p, uint64_t n, uint32_t x) {
-    for (uint64_t i = 0; i < n; ++i) x = step_pair(x, uint32_t(p[i]) * 0x10001u);
-    return x;
-}
 
 // The Horner sum of a run of bytes is sum over c of d_c p^(len - c), d_c = (l ^ b) - l.  Each power of p is written
 // as four signed 16-bit digits (balanced base 2^16: p^k = sum_j digit_j 2^(16 j) mod 2^64, every digit in
@@ -119,7 +116,7 @@ __device__ __forceinline__ uint32_t pair_byte(uint32_t a, uint32_t b, int k) {
 // packed dot product per step against a word holding both digits, and the one sum is the segment's Horner sum
 // relative to its end (|S_j| < 128 * 2 * 255 * 2^15 < 2^31 stays exact).  About 4 VALU operations per byte, against
 // 7.5 for one byte at a time.
-constexpr int kPairBytes = 128;
+constexpr int kPairBytes = 128, kHalfWords = kPairBytes / 4;
 constexpr uint64_t prime_pow_of(uint64_t e) {
     uint64_t r = 1, b = kFnvPrime;
     for (; e; e >>= 1, b *= b)
@@ -156,7 +153,6 @@ constexpr HalfDigits half_digits() {
 constexpr HalfDigits kHalfDigits = half_digits();
 // `m`: the true low byte at the segment's start in the low half, at its midpoint in the high half.
 __device__ __forceinline__ uint64_t halves_sum(const uint32_t (&w)[kFnvLaneBytes / 4], uint32_t m) {
-    constexpr int kHalfWords = kPairBytes / 4;
     int32_t s0 = 0, s1 = 0, s2 = 0, s3 = 0;
 #pragma unroll
     for (int c = 0; c < kPairBytes; ++c) {
@@ -189,10 +185,9 @@ __device__ __forceinline__ uint64_t xor_prefix_excl(uint64_t x) {
     return x << 1;
 }
 
-// The ballots of one level, per wave: the terms of the lowest unresolved bit j (T), of bit j + 1 for either start
-// value a of bit j (U_a), and, in a three-bit level, of bit j + 2 for each start pair (a, c) of bits j, j + 1 (W_ac).
-// A bit's term over a run is the xor of per-byte contributions that depend only on the lower bits of the state, so
-// each is the end value of that bit in a machine started from the right lower bits with the bit itself 0.
+// The ballots of one level, per wave: the bits of the lanes' maps of the level (below) - the term of the lowest
+// unresolved bit j (T), of bit j + 1 for either start value a of bit j (U_a), and, in a three-bit level, of bit j + 2
+// for each start pair (a, c) of bits j, j + 1 (W_ac).
 constexpr int kMaxLevelWords = 7;   // T, U0, U1, W00, W01, W10, W11
 template <int kBits>
 constexpr int level_words() { return kBits == 3 ? 7 : 3; }
@@ -220,27 +215,49 @@ __device__ __forceinline__ void wave_masks(const uint64_t (&wd)[kMaxLevelWords],
 
 // The first level only needs bits 0..2 of the state, which follow l' = ((l ^ b) * 3) mod 8 (179 = 3 mod 8): four
 // such machines share one register, one per byte (a 3-bit state times 3 stays below 2^8, so nothing carries across
-// bytes; the product's bits above 2 are masked by the next step).  Machine (a, c) - start bits 0, 1 = a, c - sits in
-// byte a + 2c.
-template <int k>
-__device__ __forceinline__ uint32_t spread4(uint32_t w) {
-    return __builtin_amdgcn_perm(0u, w, uint32_t(k | (k << 8) | (k << 16) | (k << 24)));
-}
+// bytes; the product's bits above 2 are masked by the next step).
 __device__ __forceinline__ uint32_t step_low3(uint32_t x, uint32_t b4) {
     const uint32_t y = (x ^ b4) & 0x07070707u;
     return y + (y << 1);
 }
-__device__ __forceinline__ uint32_t low3_bytes(const uint8_t* p, uint64_t n) {
-    uint32_t x = 0x03020100u;
-    for (uint64_t i = 0; i < n; ++i) x = step_low3(x, uint32_t(p[i]) * 0x01010101u);
-    return x & 0x07070707u;
+
+// A run's map of a level from its machines' end states.  Three-bit level for bits j..j+2: e0 and e1 ended the machines
+// started from the true lower bits with bit j = 0 and 1 (bits j + 1, j + 2 = 0); two-bit level for bits j, j + 1: e
+// ended the one machine started with both 0.  The bits the machines do not give follow from the term of the bit below,
+// the parity of that bit over the run's bytes (bit i of `par`, the xor of the bytes) and the run's length (`odd`).
+template <int j>
+__device__ __forceinline__ uint32_t map3_of(uint32_t e0, uint32_t e1, uint32_t par, uint32_t odd) {
+    const uint32_t t = (e0 >> j) & 1u, v0 = (e0 >> (j + 1)) & 1u, v1 = (e1 >> (j + 1)) & 1u;
+    const uint32_t w00 = (e0 >> (j + 2)) & 1u, w10 = (e1 >> (j + 2)) & 1u, q = ((par >> (j + 1)) & 1u) ^ odd;
+    return t | (v0 << 1) | (v1 << 2) | (w00 << 3) | ((w00 ^ v0 ^ q) << 4) | (w10 << 5) | ((w10 ^ v1 ^ q) << 6);
 }
-__device__ __forceinline__ void quad_bytes(const uint8_t* p, uint64_t n, uint32_t& xa, uint32_t& xb) {
+template <int j>
+__device__ __forceinline__ uint32_t map2_of(uint32_t e, uint32_t par, uint32_t odd) {
+    const uint32_t t = (e >> j) & 1u, v0 = (e >> (j + 1)) & 1u;
+    return t | (v0 << 1) | ((v0 ^ t ^ ((par >> j) & 1u) ^ odd) << 2);
+}
+
+// The same maps of a partial or unaligned segment (whole segments run from registers, below), a byte at a time from
+// memory; `low` holds the true bits below j at the segment's start.
+template <int j>
+__device__ __forceinline__ uint32_t map3_bytes(const uint8_t* p, uint64_t n, uint32_t low) {
+    uint32_t x = low | ((low | (1u << j)) << 16), par = 0;
     for (uint64_t i = 0; i < n; ++i) {
-        const uint32_t bb = uint32_t(p[i]) * 0x10001u;
-        xa = step_pair(xa, bb);
-        xb = step_pair(xb, bb);
+        const uint32_t b = p[i];
+        par ^= b;
+        x = step_pair(x, b * 0x10001u);
     }
+    return map3_of<j>(x & 0xFFFFu, x >> 16, par, uint32_t(n & 1u));
+}
+template <int j>
+__device__ __forceinline__ uint32_t map2_bytes(const uint8_t* p, uint64_t n, uint32_t low) {
+    uint32_t x = low, par = 0;
+    for (uint64_t i = 0; i < n; ++i) {
+        const uint32_t b = p[i];
+        par ^= b;
+        x = step_pair(x, b * 0x10001u);
+    }
+    return map2_of<j>(x, par, uint32_t(n & 1u));
 }
 
 // A workgroup's map of a level's state: (a, c, e) = (bit j, j + 1, j + 2) at its first segment goes to
@@ -320,6 +337,9 @@ __global__ void fnv_finish_kernel(const uint64_t* acc, uint64_t seed, const uint
 // also bounded (kSpinLimit reads), after which the launch records a fault that fails the verdict and the workgroup
 // publishes an end state anyway, so no other workgroup waits on it.
 constexpr uint32_t kHasMap = 1u << 8, kHasState = 1u << 9;   // a status word: 0, kHasMap | map, kHasState | state
+// Sleeps of 64 x 64 cycles before a look-back's first read of its window (the mapped kernel's first level writes its
+// gathered payload instead): 3.3 GB hashed in 1.77 ms with two, 1.79 ms with none
+constexpr int kFirstSleeps = 2, kFirstSleepsMapped = 0;
 constexpr uint32_t kSpinLimit = 1u << 16;   // reads of one window, about 0.2 s (sc_fnv1a64_set_spin_limit)
 // A bound the host sets only to test failure handling: every look-back of a workgroup after the first runs out at
 // once, so any input of more than one workgroup (64 KiB) ends with the fault set, deterministically.
@@ -338,7 +358,7 @@ __device__ __forceinline__ uint32_t peek(uint32_t* word) {
 // resolving a window costs the same wherever its nearest end state lies.
 template <int kBits>
 __device__ __forceinline__ uint32_t look_back(uint32_t* status, uint64_t g, uint32_t map, uint32_t init, uint32_t* fault,
-                                              uint32_t spin_limit) {
+                                              uint32_t spin_limit, int first_sleeps) {
     const int lane = threadIdx.x & 63;
     if (g == 0) {
         if (lane == 0) publish(status, kHasState | apply<kBits>(map, init));
@@ -351,7 +371,10 @@ __device__ __forceinline__ uint32_t look_back(uint32_t* status, uint64_t g, uint
         }
         return 0u;
     }
-    if (lane == 0) publish(status + g, kHasMap | map);
+    // the caller has published g's map.  The workgroups just before g publish theirs a few microseconds after g on
+    // average (their work varies with what shares their SIMDs), so a read right away would mostly find the window
+    // incomplete and cost a round trip and a sleep anyway
+    for (int i = 0; i < first_sleeps; ++i) __builtin_amdgcn_s_sleep(64);
     uint32_t acc = 0;                  // the maps of the workgroups from above the window up to g, composed
     int64_t top = int64_t(g) - 1;      // the window is workgroups top, top - 1, ...; before workgroup 0 stands `init`
     uint32_t spins = 0;
@@ -397,8 +420,8 @@ __device__ __forceinline__ uint32_t look_back(uint32_t* status, uint64_t g, uint
 }
 
 struct LevelLds {
-    uint64_t bw[kThreads / 64][kMaxLevelWords];
-    uint32_t map[kThreads / 64];
+    uint64_t bw[kFnvThreads / 64][kMaxLevelWords];
+    uint32_t map[kFnvThreads / 64];
     uint32_t state;
 };
 
@@ -407,21 +430,17 @@ __device__ __forceinline__ uint64_t uniform64(uint64_t v) {
            (uint64_t(uint32_t(__builtin_amdgcn_readfirstlane(int(uint32_t(v >> 32))))) << 32);
 }
 
-// One level (bits j .. j + kBits - 1) once the machines have run: ballots the terms, forms the workgroup's map, looks
-// back for the workgroup's start state, and returns this lane's start bits of the level (bit 0 upward).
-template <int kBits>
-__device__ __forceinline__ uint32_t resolve_level(uint32_t ea, uint32_t eb, int j, uint64_t g, uint32_t* status, uint32_t init,
-                                                  uint32_t* fault, uint32_t spin_limit, LevelLds& L) {
+// One level (bits j .. j + kBits - 1) once every lane has its map of the level (`lane_map`, the identity 0 for a lane
+// past the input): ballots the maps, forms and publishes the workgroup's map, runs `during` in every wave (work that
+// does not need the level's result, done while the look-back waits), looks back for the workgroup's start state after
+// `first_sleeps` sleeps of 64 x 64 cycles, and returns this lane's start bits of the level (bit 0 upward).
+template <int kBits, typename During>
+__device__ __forceinline__ uint32_t resolve_level(uint32_t lane_map, uint64_t g, uint32_t* status, uint32_t init,
+                                                  uint32_t* fault, uint32_t spin_limit, LevelLds& L, int first_sleeps,
+                                                  During during) {
     uint64_t bw[kMaxLevelWords] = {};
-    bw[0] = __ballot((ea >> j) & 1u);
-    bw[1] = __ballot((ea >> (j + 1)) & 1u);
-    bw[2] = __ballot((ea >> (16 + j + 1)) & 1u);
-    if constexpr (kBits == 3) {
-        bw[3] = __ballot((ea >> (j + 2)) & 1u);        // start (a, c) = (0, 0)
-        bw[4] = __ballot((eb >> (j + 2)) & 1u);        // (0, 1)
-        bw[5] = __ballot((ea >> (16 + j + 2)) & 1u);   // (1, 0)
-        bw[6] = __ballot((eb >> (16 + j + 2)) & 1u);   // (1, 1)
-    }
+#pragma unroll
+    for (int i = 0; i < level_words<kBits>(); ++i) bw[i] = __ballot((lane_map >> i) & 1u);
     uint32_t wmap = 0;
 #pragma unroll
     for (uint32_t in = 0; in < (1u << (kBits - 1)); ++in) {
@@ -440,17 +459,22 @@ __device__ __forceinline__ uint32_t resolve_level(uint32_t ea, uint32_t eb, int 
         L.map[wave] = wmap;
     }
     __syncthreads();
+    uint32_t sum = L.map[0];
     if (wave == 0) {
-        uint32_t sum = L.map[0];
-        for (int k = 1; k < kThreads / 64; ++k) sum = compose<kBits>(L.map[k], sum);
-        const uint32_t st = look_back<kBits>(status, g, __builtin_amdgcn_readfirstlane(sum), init, fault, spin_limit);
+        for (int k = 1; k < kFnvThreads / 64; ++k) sum = compose<kBits>(L.map[k], sum);
+        sum = __builtin_amdgcn_readfirstlane(sum);
+        if (lane == 0 && g > 0) publish(status + g, kHasMap | sum);
+    }
+    during();
+    if (wave == 0) {
+        const uint32_t st = look_back<kBits>(status, g, sum, init, fault, spin_limit, first_sleeps);
         if (lane == 0) L.state = st;
     }
     __syncthreads();
     uint32_t st = __builtin_amdgcn_readfirstlane(L.state);
     uint64_t m[3] = {0, 0, 0};
 #pragma unroll
-    for (int k = 0; k < kThreads / 64; ++k) {
+    for (int k = 0; k < kFnvThreads / 64; ++k) {
         if (k > wave) break;
         uint64_t wd[kMaxLevelWords] = {};
 #pragma unroll
@@ -464,46 +488,59 @@ __device__ __forceinline__ uint32_t resolve_level(uint32_t ea, uint32_t eb, int 
     return bits;
 }
 
-// The machines of each level over a segment held in registers.
-__device__ __forceinline__ uint32_t low3_regs(const uint32_t (&w)[kFnvLaneBytes / 4]) {
-    uint32_t x = 0x03020100u;
+// The levels of a whole segment held in registers, run as its two halves of kPairBytes bytes side by side (half A the
+// first, half B the second): each returns half A's map of the level in its low 16 bits and half B's above.  `par` holds
+// the xor of half A's bytes in byte 0 and of half B's in byte 2, `low` the true bits below the level at half A's start
+// in byte 0 and at half B's in byte 2.
+__device__ __forceinline__ uint32_t half_parities(const uint32_t (&w)[kFnvLaneBytes / 4]) {
+    uint32_t a = 0, b = 0;
 #pragma unroll
-    for (int k = 0; k < kFnvLaneBytes / 4; ++k) {
-        x = step_low3(x, spread4<0>(w[k]));
-        x = step_low3(x, spread4<1>(w[k]));
-        x = step_low3(x, spread4<2>(w[k]));
-        x = step_low3(x, spread4<3>(w[k]));
+    for (int k = 0; k < kHalfWords; ++k) {
+        a ^= w[k];
+        b ^= w[kHalfWords + k];
     }
-    return x & 0x07070707u;
+    a ^= a >> 16;
+    a ^= a >> 8;
+    b ^= b >> 16;
+    b ^= b >> 8;
+    return (a & 0xFFu) | ((b & 0xFFu) << 16);
 }
-__device__ __forceinline__ void quad_regs(const uint32_t (&w)[kFnvLaneBytes / 4], uint32_t& xa, uint32_t& xb) {
-#pragma unroll
-    for (int k = 0; k < kFnvLaneBytes / 4; ++k) {
-        uint32_t bb = spread<0>(w[k]);
-        xa = step_pair(xa, bb);
-        xb = step_pair(xb, bb);
-        bb = spread<1>(w[k]);
-        xa = step_pair(xa, bb);
-        xb = step_pair(xb, bb);
-        bb = spread<2>(w[k]);
-        xa = step_pair(xa, bb);
-        xb = step_pair(xb, bb);
-        bb = spread<3>(w[k]);
-        xa = step_pair(xa, bb);
-        xb = step_pair(xb, bb);
-    }
+// Byte k of `a` in bytes 0 and 1, byte k of `b` in bytes 2 and 3.
+__device__ __forceinline__ uint32_t pair_byte2(uint32_t a, uint32_t b, int k) {
+    return __builtin_amdgcn_perm(b, a, uint32_t(k) | (uint32_t(k) << 8) | (uint32_t(4 + k) << 16) | (uint32_t(4 + k) << 24));
 }
-// Also leaves the two machines' states at the segment's midpoint in `mid`.
-__device__ __forceinline__ uint32_t pair_regs(const uint32_t (&w)[kFnvLaneBytes / 4], uint32_t x, uint32_t& mid) {
+// Bits 0-2: four 3-bit machines, half A's started from bit 0 = 0 and 1 in bytes 0 and 1, half B's in bytes 2 and 3.
+__device__ __forceinline__ uint32_t level1_maps(const uint32_t (&w)[kFnvLaneBytes / 4], uint32_t par) {
+    uint32_t x = 0x01000100u;
 #pragma unroll
-    for (int k = 0; k < kFnvLaneBytes / 4; ++k) {
-        if (k == kPairBytes / 4) mid = x;
-        x = step_pair(x, spread<0>(w[k]));
-        x = step_pair(x, spread<1>(w[k]));
-        x = step_pair(x, spread<2>(w[k]));
-        x = step_pair(x, spread<3>(w[k]));
-    }
-    return x;
+    for (int k = 0; k < kHalfWords; ++k)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x = step_low3(x, pair_byte2(w[k], w[kHalfWords + k], i));
+    return map3_of<0>(x & 0xFFu, (x >> 8) & 0xFFu, par, 0u) |
+           (map3_of<0>((x >> 16) & 0xFFu, x >> 24, par >> 16, 0u) << 16);
+}
+// Bits 3-5: half A's machines in byte 0 of r0 (start bit 3 = 0) and r1 (= 1), half B's in their byte 2.
+__device__ __forceinline__ uint32_t level2_maps(const uint32_t (&w)[kFnvLaneBytes / 4], uint32_t low, uint32_t par) {
+    uint32_t r0 = low, r1 = low | 0x00080008u;
+#pragma unroll
+    for (int k = 0; k < kHalfWords; ++k)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t bb = pair_byte(w[k], w[kHalfWords + k], i);
+            r0 = step_pair(r0, bb);
+            r1 = step_pair(r1, bb);
+        }
+    return map3_of<3>(r0 & 0xFFu, r1 & 0xFFu, par, 0u) |
+           (map3_of<3>((r0 >> 16) & 0xFFu, (r1 >> 16) & 0xFFu, par >> 16, 0u) << 16);
+}
+// Bits 6-7: one machine per half, half A's in byte 0, half B's in byte 2.
+__device__ __forceinline__ uint32_t level3_maps(const uint32_t (&w)[kFnvLaneBytes / 4], uint32_t low, uint32_t par) {
+    uint32_t r = low;
+#pragma unroll
+    for (int k = 0; k < kHalfWords; ++k)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) r = step_pair(r, pair_byte(w[k], w[kHalfWords + k], i));
+    return map2_of<6>(r & 0xFFu, par, 0u) | (map2_of<6>((r >> 16) & 0xFFu, par >> 16, 0u) << 16);
 }
 
 // ---- the gather fused with the hash -------------------------------------------------------------------------------
@@ -644,19 +681,19 @@ __device__ __forceinline__ void store_wave(u32x4 (&lds)[16 * kXposeRow], const u
 // fused 128K capture in 2.78-2.85 ms against 2.82 at four waves).  Every value the gather keeps live past its look-ahead
 // costs spills here: an extra extent index held across it spilled 35 words and took the capture to 3.03 ms.
 template <bool kMapped>
-__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5, 8))) fnv_onepass_kernel(const uint8_t* data, uint64_t n, bool aligned,
+__global__ void __launch_bounds__(kFnvThreads) __attribute__((amdgpu_waves_per_eu(5, 8))) fnv_onepass_kernel(const uint8_t* data, uint64_t n, bool aligned,
                                                                 uint64_t seed, const uint64_t* seed_dev,
                                                                 uint32_t* status, uint64_t stride, uint32_t* ctl,
                                                                 uint32_t spin_limit, HashMapArgs map) {
     __shared__ LevelLds L;
     __shared__ uint32_t s_ticket;
-    __shared__ uint64_t s_sum[kThreads / 64];
-    __shared__ u32x4 s_xpose[kMapped ? kThreads / 64 : 1][16 * kXposeRow];
+    __shared__ uint64_t s_sum[kFnvThreads / 64];
+    __shared__ u32x4 s_xpose[kMapped ? kFnvThreads / 64 : 1][16 * kXposeRow];
     if (threadIdx.x == 0) s_ticket = atomicAdd(ctl, 1u);
     __syncthreads();
     const uint64_t g = uint32_t(__builtin_amdgcn_readfirstlane(int(s_ticket)));
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint64_t begin = (g * kThreads + threadIdx.x) * kFnvLaneBytes;
+    const uint64_t begin = (g * kFnvThreads + threadIdx.x) * kFnvLaneBytes;
     const bool live = begin < n;
     const uint64_t len = !live ? 0 : n - begin < kFnvLaneBytes ? n - begin : kFnvLaneBytes;
     const bool full = aligned && len == kFnvLaneBytes;
@@ -668,68 +705,85 @@ __global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5
     }
     uint32_t* fault = ctl + 1;
     uint32_t w[kFnvLaneBytes / 4] = {};
+    uint8_t* base = nullptr;   // mapped: `base` + o addresses payload byte o in the segment holding this workgroup's bytes
     if constexpr (kMapped) {
-        // this workgroup's payload bytes lie in one segment; `base` + o addresses byte o there
         const uint64_t k = g * uint64_t(kFnvGroupBytes) / map.seg_bytes;
-        uint8_t* const base = reinterpret_cast<uint8_t*>(reinterpret_cast<uintptr_t>(map.seg[k]) - k * map.seg_bytes);
+        base = reinterpret_cast<uint8_t*>(reinterpret_cast<uintptr_t>(map.seg[k]) - k * map.seg_bytes);
         if (begin < map.n_total) {
             const uint64_t left = map.n_total - begin;
             gather_segment(map, base, map.first[g], begin, left < kFnvLaneBytes ? left : kFnvLaneBytes, w);
         }
-        if (map.store) store_wave(s_xpose[wave], w, base, (g * kThreads + uint64_t(wave) * 64) * kFnvLaneBytes, n, lane);
     } else if (full) {
         load_segment(p, w);
     }
     const uint64_t h0 = start_state(seed, seed_dev);
 
-    // bits 0-2: the four machines of run_low3 end in bytes a + 2c; regrouped into the layout the ballots read
-    uint32_t ea = 0, eb = 0;
-    if (live) {
-        const uint32_t x = full ? low3_regs(w) : low3_bytes(p, len);
-        ea = (x & 0xFFu) | (((x >> 8) & 0xFFu) << 16);
-        eb = ((x >> 16) & 0xFFu) | ((x >> 24) << 16);
+    // the three levels: every lane's map of the level (a whole segment from its two halves in registers, a partial or
+    // unaligned one a byte at a time), then the workgroup's look-back.  `s` gathers the true start bits at the lane's
+    // segment, `sb` at its midpoint (its first half's map applied to the level's start bits)
+    const uint32_t par = full ? half_parities(w) : 0u;
+    uint32_t halves = 0, lane_map = 0;
+    if (full) {
+        halves = level1_maps(w, par);
+        lane_map = compose<3>(halves >> 16, halves & 0xFFFFu);
+    } else if (live) {
+        lane_map = map3_bytes<0>(p, len, 0u);
     }
-    uint32_t s = resolve_level<3>(ea, eb, 0, g, status, uint32_t(h0) & 7u, fault, spin_limit, L);
+    // the gathered payload is written while the first look-back waits (its waits are the longest: they follow the
+    // predecessors' gathers)
+    const auto store_gathered = [&] {
+        if constexpr (kMapped)
+            if (map.store)
+                store_wave(s_xpose[wave], w, base, (g * kFnvThreads + uint64_t(wave) * 64) * kFnvLaneBytes, n, lane);
+    };
+    uint32_t s = resolve_level<3>(lane_map, g, status, uint32_t(h0) & 7u, fault, spin_limit, L,
+                                  kMapped ? kFirstSleepsMapped : kFirstSleeps, store_gathered);
+    uint32_t sb = apply<3>(halves & 0xFFFFu, s);
 
-    // bits 3-5: four full machines (start bits 3, 4 = 00, 10, 01, 11), bit 5 started at 0
-    ea = eb = 0;
-    if (live) {
-        ea = s | ((s | (1u << 3)) << 16);
-        const uint32_t sc = s | (1u << 4);
-        eb = sc | ((sc | (1u << 3)) << 16);
-        if (full) quad_regs(w, ea, eb);
-        else quad_bytes(p, len, ea, eb);
+    lane_map = 0;
+    if (full) {
+        halves = level2_maps(w, s | (sb << 16), par);
+        lane_map = compose<3>(halves >> 16, halves & 0xFFFFu);
+    } else if (live) {
+        lane_map = map3_bytes<3>(p, len, s);
     }
-    s |= resolve_level<3>(ea, eb, 3, g, status + stride, uint32_t(h0 >> 3) & 7u, fault, spin_limit, L) << 3;
+    uint32_t st = resolve_level<3>(lane_map, g, status + stride, uint32_t(h0 >> 3) & 7u, fault, spin_limit, L,
+                                   kFirstSleeps, [] {});
+    s |= st << 3;
+    sb |= apply<3>(halves & 0xFFFFu, st) << 3;
 
-    // bits 6-7: two machines (start bit 6 = 0, 1), bit 7 started at 0
-    uint32_t mid = 0;
-    ea = 0;
-    if (live) {
-        ea = s | ((s | (1u << 6)) << 16);
-        ea = full ? pair_regs(w, ea, mid) : pair_bytes(p, len, ea);
+    lane_map = 0;
+    if (full) {
+        halves = level3_maps(w, s | (sb << 16), par);
+        lane_map = compose<2>(halves >> 16, halves & 0xFFFFu);
+    } else if (live) {
+        lane_map = map2_bytes<6>(p, len, s);
     }
-    s |= resolve_level<2>(ea, 0u, 6, g, status + 2 * stride, uint32_t(h0 >> 6) & 3u, fault, spin_limit, L) << 6;
+    st = resolve_level<2>(lane_map, g, status + 2 * stride, uint32_t(h0 >> 6) & 3u, fault, spin_limit, L, kFirstSleeps,
+                          [] {});
+    s |= st << 6;
+    sb |= apply<2>(halves & 0xFFFFu, st) << 6;
 
-    // the Horner sums.  The low byte at the midpoint is the bits 6-7 machine started from the true bit 6, with bit 7
-    // flipped when the true start bit 7 is 1 (bit 7 of the state is its start value xor terms of the lower bits).
+    // the Horner sums, from the true low bytes at the segment's start and midpoint
     uint64_t acc = 0;
     if (full) {
-        const uint32_t lm = ((((s >> 6) & 1u) ? mid >> 16 : mid) & 0xFFu) ^ (s & 0x80u);
         // p^(n - r), r the end of the wave's last segment: wave-uniform.  p has order dividing 2^62 modulo 2^64, so
         // the exponent is taken modulo 2^62 (r passes n in the buffer's last wave)
-        const uint64_t wave_end = ((g * kThreads) + uint64_t(wave) * 64 + 64) * kFnvLaneBytes;
+        const uint64_t wave_end = ((g * kFnvThreads) + uint64_t(wave) * 64 + 64) * kFnvLaneBytes;
         const uint64_t wave_pow = pow_prime((n - wave_end) & ((uint64_t(1) << 62) - 1));
-        acc = halves_sum(w, s | (lm << 16)) * kLanePow.v[lane] * wave_pow;
+        acc = halves_sum(w, s | (sb << 16)) * kLanePow.v[lane] * wave_pow;
     } else if (live) {
         acc = segment_sum(p, n, begin, s);
     }
     for (int m = 32; m > 0; m >>= 1) acc += shfl_xor64(acc, m);
     if (lane == 0) s_sum[wave] = acc;
     __syncthreads();
-    if (threadIdx.x == 0)
-        atomicAdd(reinterpret_cast<unsigned long long*>(ctl + 2),
-                  (unsigned long long) (s_sum[0] + s_sum[1] + s_sum[2] + s_sum[3]));
+    if (threadIdx.x == 0) {
+        uint64_t sum = 0;
+#pragma unroll
+        for (int k = 0; k < kFnvThreads / 64; ++k) sum += s_sum[k];
+        atomicAdd(reinterpret_cast<unsigned long long*>(ctl + 2), (unsigned long long) sum);
+    }
 }
 
 // Clears the status words, the ticket and fault words and the sum before a launch (a kernel rather than a memset, so a
@@ -748,7 +802,7 @@ std::atomic<uint32_t> g_spin_limit{kSpinLimit};
 FnvWorkspace fnv_workspace(uint64_t n) {
     FnvWorkspace w{};
     w.segments = (n + kFnvLaneBytes - 1) / kFnvLaneBytes;
-    w.groups = (w.segments + kThreads - 1) / kThreads;
+    w.groups = (w.segments + kFnvThreads - 1) / kFnvThreads;
     auto up = [](uint64_t x) { return (x + 255) / 256 * 256; };
     w.off_ctl = 0;
     w.off_status = 256;
@@ -770,7 +824,7 @@ hipError_t launch_fnv1a64(const void* data, uint64_t n, uint64_t seed, const uin
         const uint64_t init_blocks = (words + kThreads - 1) / kThreads < 1024 ? (words + kThreads - 1) / kThreads : 1024;
         hipLaunchKernelGGL(fnv_onepass_init_kernel, dim3(unsigned(init_blocks)), dim3(kThreads), 0, stream, status, words,
                            ctl);
-        hipLaunchKernelGGL(fnv_onepass_kernel<false>, dim3(unsigned(w.groups)), dim3(kThreads), 0, stream, src, n, aligned,
+        hipLaunchKernelGGL(fnv_onepass_kernel<false>, dim3(unsigned(w.groups)), dim3(kFnvThreads), 0, stream, src, n, aligned,
                            seed, seed_dev, status, w.stride, ctl, g_spin_limit.load(), HashMapArgs{});
     }
     // the finish reads the start state before it writes `out`, so `out` may be `seed_dev` itself
@@ -801,7 +855,7 @@ hipError_t launch_fnv1a64_mapped(const HashMapArgs& map, const uint8_t* tail, ui
             const uint64_t init_blocks = (words + kThreads - 1) / kThreads < 1024 ? (words + kThreads - 1) / kThreads : 1024;
             hipLaunchKernelGGL(fnv_onepass_init_kernel, dim3(unsigned(init_blocks)), dim3(kThreads), 0, stream, status,
                                words, ctl);
-            hipLaunchKernelGGL(fnv_onepass_kernel<false>, dim3(unsigned(w.groups)), dim3(kThreads), 0, stream, nullptr,
+            hipLaunchKernelGGL(fnv_onepass_kernel<false>, dim3(unsigned(w.groups)), dim3(kFnvThreads), 0, stream, nullptr,
                                n_total, true, seed, nullptr, status, w.stride, ctl, g_spin_limit.load(), map);
         }
         const bool any = w.groups > 0;
@@ -815,7 +869,7 @@ hipError_t launch_fnv1a64_mapped(const HashMapArgs& map, const uint8_t* tail, ui
         const uint64_t init_blocks = (words + kThreads - 1) / kThreads < 1024 ? (words + kThreads - 1) / kThreads : 1024;
         hipLaunchKernelGGL(fnv_onepass_init_kernel, dim3(unsigned(init_blocks)), dim3(kThreads), 0, stream, status, words,
                            ctl);
-        hipLaunchKernelGGL(fnv_onepass_kernel<true>, dim3(unsigned(w.groups)), dim3(kThreads), 0, stream, nullptr, n_full,
+        hipLaunchKernelGGL(fnv_onepass_kernel<true>, dim3(unsigned(w.groups)), dim3(kFnvThreads), 0, stream, nullptr, n_full,
                            true, seed, nullptr, status, w.stride, ctl, g_spin_limit.load(), map);
     }
     const bool any = w.groups > 0;

@@ -220,7 +220,8 @@ struct HashExtent {
     uint32_t page_chunks;    // pages: 16-byte chunks per page
 };
 static_assert(sizeof(HashExtent) == 48, "hash extents are 48 bytes");
-constexpr int kFnvGroupBytes = 256 * kFnvLaneBytes;   // the payload bytes of one hash workgroup
+constexpr int kFnvThreads = 256;                         // lanes of one hash workgroup
+constexpr int kFnvGroupBytes = kFnvThreads * kFnvLaneBytes;   // the payload bytes of one hash workgroup
 struct HashMapArgs {
     const HashExtent* ext;   // null: the plain hash of `data`
     const uint32_t* first;   // per workgroup: the extent holding its first byte
