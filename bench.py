@@ -617,7 +617,7 @@ def wire_payload(sc, geo, tokens: int, slot, link_h2d: float, link_d2h: float, r
             "mount_device_ms": round(p50(mount_dev_ms), 3), "scatter_ms": round(p50(scatter_ms[1:]), 3),
             "timing": (f"p50 of {2 * reps} encodes, hashes and mounts and of {reps} checked parks and resumes; the "
                        "link probe is one plain pinned copy of the payload's size each way between the same buffers"),
-            "method": "payload in the reference's wire format; encode = head copy + one gather launch + device FNV-1a; "
+            "method": "payload in the reference's wire format; encode = head copy + one launch that gathers the slot into the payload and hashes it from the same registers (FNV-1a); "
                       "mount = device FNV-1a whose last kernel compares with the expected hash and leaves a verdict "
                       "word, then one scatter launch gated by it (all or nothing, no host round trip); mount_ms is the "
                       "host's wall time of the call, mount_device_ms the events around it; park = encode with the "
