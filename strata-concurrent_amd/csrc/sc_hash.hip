@@ -393,9 +393,9 @@ __device__ __forceinline__ uint32_t look_back(uint32_t* status, uint64_t g, uint
                 }
                 return 0u;
             }
-            // a long sleep (64 x 64 cycles, about 1.7 us, the status words' round trip under load) leaves the SIMD's
-            // issue slots to the other waves' level work: 3.3 GB hashed in 1.93 ms, against 1.95 ms at 16 and 1.98 ms
-            // at 1 (a sleep of 100 measured the same as 64)
+            // a long sleep (64 x 64 cycles, about 1.7 us) leaves the SIMD's issue slots to the other waves' level work:
+            // sleeps of 16 or 32 between reads measured slower (1.77-1.78 against 1.76 ms for 3.3 GB; the fused
+            // capture 2.42-2.47 against 2.37 ms), and so did 1 in the earlier form of the levels
             __builtin_amdgcn_s_sleep(64);
             continue;
         }

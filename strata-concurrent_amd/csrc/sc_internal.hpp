@@ -220,7 +220,9 @@ struct HashExtent {
     uint32_t page_chunks;    // pages: 16-byte chunks per page
 };
 static_assert(sizeof(HashExtent) == 48, "hash extents are 48 bytes");
-constexpr int kFnvThreads = 256;                         // lanes of one hash workgroup
+// Lanes of one hash workgroup: 256 (64 KiB) hashed 3.3 GB in 1.77 ms, against 4.84, 2.53 and 2.22 ms with 64, 128
+// and 512 (more workgroups mean more look-backs per byte, larger ones fewer resident workgroups per CU).
+constexpr int kFnvThreads = 256;
 constexpr int kFnvGroupBytes = kFnvThreads * kFnvLaneBytes;   // the payload bytes of one hash workgroup
 struct HashMapArgs {
     const HashExtent* ext;   // null: the plain hash of `data`
