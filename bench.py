@@ -542,6 +542,27 @@ def wire_payload(sc, geo, tokens: int, slot, link_h2d: float, link_d2h: float, r
         dec.destroy()
     same = all(sc.fnv1a64_device(a.ptr, a.nbytes) == sc.fnv1a64_device(b.ptr, b.nbytes)
                for a, b in zip(slot.buffers(), dst.buffers()))
+    # the same mount given the payload's carries (written by the encode beside the payload): the hash check starts
+    # every 64 KiB from its carry instead of looking back across the payload
+    carry = sc.DeviceBuffer(max(sc.carry_bytes(n), 1), "uint8")
+    enc.set_carry(carry.ptr)
+    enc.encode(payload.ptr, n, stream)
+    assert enc.hash() == h
+    enc.set_carry(None)
+    mount_c_ms, mount_c_dev_ms = [], []
+    for _ in range(2 * reps):
+        dec = sc_wire.Decoder(payload.ptr, n, geo, dst, payload_hash=h, check_hash=True, carry=carry.ptr)
+        t1 = time.perf_counter()
+        e0.record(stream)
+        dec.restore(stream)
+        e1.record(stream)
+        mount_c_ms.append((time.perf_counter() - t1) * 1e3)
+        e1.sync()
+        mount_c_dev_ms.append(e0.elapsed_ms(e1))
+        dec.destroy()
+    same = same and all(sc.fnv1a64_device(a.ptr, a.nbytes) == sc.fnv1a64_device(b.ptr, b.nbytes)
+                        for a, b in zip(slot.buffers(), dst.buffers()))
+    carry.free()
     # the bare scatter of the same blobs (no hash): the device mount is this plus the hash, with no round trip between
     # (from an unset transfer image into the mount's slot, which the checked resume below mounts again)
     _, total = sc.image_layout(geo, tokens)
@@ -608,6 +629,8 @@ def wire_payload(sc, geo, tokens: int, slot, link_h2d: float, link_d2h: float, r
             "hash_ms": round(hash_t, 3), "hash_gbps": round(n / (hash_t * 1e-3) / 1e9, 1),
             "mount_ms": round(mount_t, 3), "mount_gbps": round(n / (mount_t * 1e-3) / 1e9, 1),
             "open_ms": round(p50(open_ms), 3),
+            "mount_carried_ms": round(p50(mount_c_ms), 3), "mount_carried_device_ms": round(p50(mount_c_dev_ms), 3),
+            "mount_carried_gbps": round(n / (p50(mount_c_ms) * 1e-3) / 1e9, 1),
             "checked_park_ms": round(pk, 2), "checked_park_gbps": round(pk_gbps, 2),
             "checked_park_vs_link": link_fracs(pk_gbps, probe_d2h, link_d2h),
             "checked_resume_ms": round(rs, 2), "checked_resume_gbps": round(rs_gbps, 2),
@@ -623,7 +646,9 @@ def wire_payload(sc, geo, tokens: int, slot, link_h2d: float, link_d2h: float, r
                       "host's wall time of the call, mount_device_ms the events around it; park = encode with the "
                       "pinned D2H of the payload on a second stream overlapping the hash; resume = pinned H2D in 64 MiB "
                       "pieces, each hashed on a second stream as it lands (chained device FNV-1a), then the mount "
-                      "without a second hash"}
+                      "without a second hash; mount_carried = the mount given the payload's carries (the low byte of "
+                      "the running hash after every 64 KiB, written by the encode beside the payload): the same "
+                      "verdict, every 64 KiB of the hash starting from its carry instead of looking back"}
 
 
 def arena_dir(need: int) -> str:
@@ -891,9 +916,15 @@ def ipc_export_role(tokens: int) -> int:
     live, keep = sc_wire.make_live(WIRE_GEOKEY, ids, layer_hi=48, idx_dim=128)
     enc = sc_wire.Encoder(geo, slot, tokens, live, 0x1122334455667788, 0x0AABBCCDDEEFF001)
     n = enc.bytes
-    ex = sc.IpcExport(n, sc.IPC_MAX_SEGMENT)
+    nc = max(sc.carry_bytes(n), 1)
+    # the payload's carries ride in the exported segments after the payload, inside one segment
+    at = (n + 255) // 256 * 256
+    if at % sc.IPC_MAX_SEGMENT + nc > sc.IPC_MAX_SEGMENT:
+        at = (at + sc.IPC_MAX_SEGMENT - 1) // sc.IPC_MAX_SEGMENT * sc.IPC_MAX_SEGMENT
+    ex = sc.IpcExport(at + nc, sc.IPC_MAX_SEGMENT)
     ptrs, seg = ex.layout()
-    print(json.dumps({"segments": [[h.hex(), k] for h, k in ex.segments()], "bytes": n,
+    enc.set_carry(ptrs[at // seg] + at % seg)
+    print(json.dumps({"segments": [[h.hex(), k] for h, k in ex.segments()], "bytes": n, "carry_at": at,
                       "buffers": [sc.fnv1a64_device(b.ptr, b.nbytes) for b in slot.buffers()]}), flush=True)
     e0, e1 = sc.Event(), sc.Event()
     for line in sys.stdin:
@@ -924,6 +955,8 @@ def ipc_handoff(sc, geo, tokens: int, reps: int = 5) -> dict:
         n = first["bytes"]
         imp = sc.IpcImport([(bytes.fromhex(h), k) for h, k in first["segments"]])
         ptrs, seg = imp.layout()
+        at = first["carry_at"]
+        carry = ptrs[at // seg] + at % seg   # the exporter's carries of each payload, in its exported segments
         dst = sc.new_slot(geo, tokens, fill=0)
         stream = sc.Stream()
         e0, e1 = sc.Event(), sc.Event()
@@ -934,7 +967,8 @@ def ipc_handoff(sc, geo, tokens: int, reps: int = 5) -> dict:
             r = json.loads(proc.stdout.readline())
             enc_ms.append(r["encode_ms"])
             t0 = time.perf_counter()
-            dec = sc_wire.Decoder(0, n, geo, dst, payload_hash=r["hash"], check_hash=True, segments=(ptrs, seg))
+            dec = sc_wire.Decoder(0, n, geo, dst, payload_hash=r["hash"], check_hash=True, segments=(ptrs, seg),
+                                  carry=carry)
             t1 = time.perf_counter()
             e0.record(stream)
             dec.restore(stream)
@@ -969,7 +1003,9 @@ def ipc_handoff(sc, geo, tokens: int, reps: int = 5) -> dict:
                       "hipIpcGetMemHandle (head copies + the fused gather and FNV-1a, cut at segment ends; HIP events); "
                       "importer (this process): segments opened once with hipIpcOpenMemHandle, the payload mounted "
                       "from them (device FNV-1a over the segments leaving a verdict, one scatter launch gated by it, "
-                      "reading the segments; host wall time of the synchronous restore); handoff_ms = encode + mount; "
+                      "reading the segments; host wall time of the synchronous restore), the hash check given the "
+                      "payload's carries (the low byte of the running hash after every 64 KiB, written by the "
+                      "exporter's encode after the payload in its segments); handoff_ms = encode + mount; "
                       "bit_exact = every destination slot buffer's device hash equals the exporter's source buffer's"}
 
 
@@ -1347,7 +1383,8 @@ def main() -> int:
     result["wire_payload"]["link_settle_ms"] = settle_wire
     wp = result["wire_payload"]
     log(f"wire: encode {wp['encode_ms']} ms ({wp['encode_gbps']} GB/s), hash {wp['hash_ms']} ms, mount "
-        f"{wp['mount_ms']} ms; checked park {wp['checked_park_gbps']} GB/s, resume {wp['checked_resume_gbps']} GB/s")
+        f"{wp['mount_ms']} ms (given the carries {wp['mount_carried_ms']} ms); checked park "
+        f"{wp['checked_park_gbps']} GB/s, resume {wp['checked_resume_gbps']} GB/s")
 
     log("hand-off arena: the 128K slot's payload through a tmpfs arena slot and back into a fresh slot")
     settle_ar = settle_link(sc, d2h)

@@ -515,6 +515,33 @@ int sc_hash_map_create_read(const sc_segments* from, uint64_t bytes, sc_hash_map
  * sc_plan_launch_gated); `fault` is optional here. */
 int sc_hash_map_check_async(const sc_hash_map* map, uint64_t seed, uint64_t expected, uint64_t* out, uint32_t* verdict,
                             uint32_t* fault, void* workspace, uint64_t workspace_bytes, void* stream);
+/* The carries of a hashed input: the low byte of the running hash after each whole 64 KiB of the input whose end lies
+ * strictly inside it - sc_fnv1a64_carry_bytes(bytes) bytes, one per boundary, in order.  No counterpart in the
+ * reference: they are what lets a consumer check a payload's hash without the kernel's serial look-back across
+ * workgroups.  The hash kernel resolves the low byte of the state at every 64 KiB boundary anyway; a producer writes
+ * those bytes out beside the hash (sc_fnv1a64_carry_async, sc_hash_map_launch_carry: the same launch, one byte store per
+ * 64 KiB), ships them with the payload, and a consumer's check given them (sc_fnv1a64_check_carried_async,
+ * sc_hash_map_check_carried_async) starts every 64 KiB workgroup from the carry before it instead of waiting for its
+ * predecessors, and checks that it ends with the carry after it.  The check stays exact: if every workgroup ends with
+ * the carry after it, every carry is the true state (by induction from the seed), so the hash computed is the
+ * payload's FNV-1a; if any does not, the payload or its carries are not what was hashed, the fault word gets
+ * SC_FNV_FAULT_CARRY and the verdict is 0 (nothing gated by it runs).  A mismatch is refused, never repaired: hash
+ * again without carries to tell a corrupted payload from corrupted carries.  `carry_out` / `carry` are device memory
+ * (or pinned host memory mapped for the device); the other arguments are those of the forms without carries. */
+#define SC_FNV_FAULT_WAIT 1u    /* a look-back wait ran out (the launch still ended) */
+#define SC_FNV_FAULT_CARRY 2u   /* a check given carries: a workgroup did not end with the carry after it */
+uint64_t sc_fnv1a64_carry_bytes(uint64_t bytes);
+int sc_fnv1a64_carry_async(const void* data, uint64_t bytes, uint64_t seed, uint64_t* out, uint32_t* fault,
+                           uint8_t* carry_out, void* workspace, uint64_t workspace_bytes, void* stream);
+int sc_fnv1a64_check_carried_async(const void* data, uint64_t bytes, uint64_t seed, uint64_t expected,
+                                   const uint8_t* carry, uint64_t* out, uint32_t* verdict, uint32_t* fault,
+                                   void* workspace, uint64_t workspace_bytes, void* stream);
+int sc_hash_map_launch_carry(const sc_hash_map* map, uint64_t seed, uint64_t* out, uint32_t* fault, uint8_t* carry_out,
+                             void* workspace, uint64_t workspace_bytes, void* stream);
+/* A read map only (sc_hash_map_create_read: a payload hashed where its segments hold it). */
+int sc_hash_map_check_carried_async(const sc_hash_map* map, uint64_t seed, uint64_t expected, const uint8_t* carry,
+                                    uint64_t* out, uint32_t* verdict, uint32_t* fault, void* workspace,
+                                    uint64_t workspace_bytes, void* stream);
 int sc_hash_map_destroy(sc_hash_map* map);
 /* The bound on each of the hash kernel's look-back waits, in reads of its window (0 restores the default, 65536, about
  * 0.2 s).  No counterpart in the reference: a workgroup only waits on workgroups that are running or done, so a

@@ -92,6 +92,12 @@ int sc_wire_encode_segments_async(sc_wire_encoder* e, const sc_segments* into, v
 /* The payload hash of the last encode (waits for it): WireEncoded::payload_hash.  SC_ETIMEOUT, and no hash, when the
  * device hash did not complete (a bounded wait of its kernel ran out, sc_fnv1a64_async): encode again. */
 int sc_wire_encoder_hash(sc_wire_encoder* e, uint64_t* hash);
+/* Later encodes also write the payload's carries at `carry` (device memory of sc_fnv1a64_carry_bytes(
+ * sc_wire_encoder_bytes(e)) bytes, sc_handoff.h): the low byte of the running payload hash after every 64 KiB, from the
+ * same launch.  A consumer that receives them with the payload checks its hash without the look-back across the
+ * payload (sc_wire_decoder_set_carry).  NULL stops writing them.  No counterpart in the reference (its hash is the
+ * byte-serial loop). */
+int sc_wire_encoder_set_carry(sc_wire_encoder* e, void* carry);
 int sc_wire_encoder_destroy(sc_wire_encoder* e);
 
 /* Reads and checks the head of a device payload against the slot: magic, version, flags, sizes, every record, the
@@ -132,6 +138,11 @@ int64_t sc_wire_decoder_tokens(const sc_wire_decoder* d);
  * write", include/strata/core/conversation_snapshot.hpp:103-108): SC_EINVAL for a hash that differs, SC_ETIMEOUT for a
  * device hash that did not complete (its verdict gated every scatter off, as for a mismatch). */
 int sc_wire_decoder_restore(sc_wire_decoder* d, void* stream);
+/* The payload's carries as its encoder wrote them (device memory; sc_wire_encoder_set_carry), for the next restore of
+ * this opened decoder: the payload hash is then checked starting every 64 KiB from its carry, with the same verdict -
+ * a payload or carries that are not what was hashed are refused with SC_EINVAL and nothing is mounted.  NULL checks
+ * without them.  No counterpart in the reference. */
+int sc_wire_decoder_set_carry(sc_wire_decoder* d, const void* carry);
 /* After a restore: the live checkpoint's ids (n written to *n; needs cap >= tokens) and its small buffers
  * (which: 0 ple, 1 tails, 2 dead, 3 block_pos). */
 int sc_wire_decoder_live_ids(const sc_wire_decoder* d, int32_t* ids, int64_t cap, int64_t* n);

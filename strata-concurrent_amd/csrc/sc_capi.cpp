@@ -48,10 +48,10 @@ hipError_t launch_stream_reset(int32_t* table, int64_t n_blocks, int32_t* slot_b
 hipError_t launch_ring_table(int32_t* table, int64_t n_blocks, int64_t n_slots, hipStream_t stream);
 hipError_t launch_fnv1a64(const void* data, uint64_t n, uint64_t seed, const uint64_t* seed_dev, uint64_t* out,
                           uint32_t* fault_out, void* workspace, hipStream_t stream, uint64_t expected = 0,
-                          uint32_t* verdict = nullptr);
+                          uint32_t* verdict = nullptr, const FnvCarries& carries = {});
 hipError_t launch_fnv1a64_mapped(const HashMapArgs& map, const uint8_t* tail, uint64_t seed, uint64_t* out,
                                  uint32_t* fault_out, void* workspace, hipStream_t stream, uint64_t expected = 0,
-                                 uint32_t* verdict = nullptr);
+                                 uint32_t* verdict = nullptr, const FnvCarries& carries = {});
 
 static uint64_t host_mix64(uint64_t z) {
     z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
@@ -1626,6 +1626,36 @@ int sc_hash_map_check_async(const sc_hash_map* map, uint64_t seed, uint64_t expe
     return e == hipSuccess ? ok() : hip_fail(e, "mapped hash launch");
 }
 
+int sc_hash_map_launch_carry(const sc_hash_map* map, uint64_t seed, uint64_t* out, uint32_t* fault, uint8_t* carry_out,
+                             void* workspace, uint64_t workspace_bytes, void* stream) {
+    if (const int rc = hash_map_args(map, fault, workspace, workspace_bytes)) return rc;
+    if (!out || !fault) return fail(SC_EINVAL, "sc_handoff: missing hash output or fault word");
+    if (!carry_out && sc::fnv_carry_count(map->bytes)) return fail(SC_EINVAL, "sc_handoff: missing carry output");
+    const sc::HashMapArgs a{map->ext_dev, map->first_dev, map->seg_dev, map->seg_bytes, map->bytes, map->store ? 1u : 0u};
+    sc::FnvCarries c;
+    c.out = carry_out;
+    const hipError_t e = sc::launch_fnv1a64_mapped(a, map->tail, seed, out, fault, workspace,
+                                                   static_cast<hipStream_t>(stream), 0, nullptr, c);
+    return e == hipSuccess ? ok() : hip_fail(e, "mapped hash launch");
+}
+
+int sc_hash_map_check_carried_async(const sc_hash_map* map, uint64_t seed, uint64_t expected, const uint8_t* carry,
+                                    uint64_t* out, uint32_t* verdict, uint32_t* fault, void* workspace,
+                                    uint64_t workspace_bytes, void* stream) {
+    if (const int rc = hash_map_args(map, fault, workspace, workspace_bytes)) return rc;
+    if (!out || !verdict || (reinterpret_cast<uintptr_t>(verdict) & 3u))
+        return fail(SC_EINVAL, "sc_handoff: missing hash output, or a verdict word that is not 4-byte aligned");
+    if (!carry && sc::fnv_carry_count(map->bytes)) return fail(SC_EINVAL, "sc_handoff: missing carries");
+    if (map->store)
+        return fail(SC_EINVAL, "sc_handoff: a check with carries reads the payload where it lies (sc_hash_map_create_read)");
+    const sc::HashMapArgs a{map->ext_dev, map->first_dev, map->seg_dev, map->seg_bytes, map->bytes, 0u};
+    sc::FnvCarries c;
+    c.in = carry;
+    const hipError_t e = sc::launch_fnv1a64_mapped(a, map->tail, seed, out, fault, workspace,
+                                                   static_cast<hipStream_t>(stream), expected, verdict, c);
+    return e == hipSuccess ? ok() : hip_fail(e, "mapped hash launch");
+}
+
 int sc_hash_map_destroy(sc_hash_map* map) {
     if (!map) return ok();
     const hipError_t e = map->ext_dev ? hipFree(map->ext_dev) : hipSuccess;
@@ -2163,6 +2193,35 @@ int sc_fnv1a64_check_async(const void* data, uint64_t bytes, uint64_t seed, uint
     if (const int rc = check_fnv_args(data, bytes, out, fault, false, workspace, workspace_bytes)) return rc;
     SC_HIP(sc::launch_fnv1a64(data, bytes, seed, nullptr, out, fault, workspace, static_cast<hipStream_t>(stream),
                               expected, verdict),
+           "hash launch");
+    return ok();
+}
+
+uint64_t sc_fnv1a64_carry_bytes(uint64_t bytes) { return sc::fnv_carry_count(bytes); }
+
+int sc_fnv1a64_carry_async(const void* data, uint64_t bytes, uint64_t seed, uint64_t* out, uint32_t* fault,
+                           uint8_t* carry_out, void* workspace, uint64_t workspace_bytes, void* stream) {
+    if (const int rc = check_fnv_args(data, bytes, out, fault, true, workspace, workspace_bytes)) return rc;
+    if (!carry_out && sc::fnv_carry_count(bytes)) return fail(SC_EINVAL, "sc_handoff: missing carry output");
+    sc::FnvCarries c;
+    c.out = carry_out;
+    SC_HIP(sc::launch_fnv1a64(data, bytes, seed, nullptr, out, fault, workspace, static_cast<hipStream_t>(stream), 0,
+                              nullptr, c),
+           "hash launch");
+    return ok();
+}
+
+int sc_fnv1a64_check_carried_async(const void* data, uint64_t bytes, uint64_t seed, uint64_t expected,
+                                   const uint8_t* carry, uint64_t* out, uint32_t* verdict, uint32_t* fault,
+                                   void* workspace, uint64_t workspace_bytes, void* stream) {
+    if (!verdict) return fail(SC_EINVAL, "sc_handoff: missing hash verdict");
+    if (reinterpret_cast<uintptr_t>(verdict) & 3u) return fail(SC_EINVAL, "sc_handoff: the verdict must be 4-byte aligned");
+    if (const int rc = check_fnv_args(data, bytes, out, fault, false, workspace, workspace_bytes)) return rc;
+    if (!carry && sc::fnv_carry_count(bytes)) return fail(SC_EINVAL, "sc_handoff: missing carries");
+    sc::FnvCarries c;
+    c.in = carry;
+    SC_HIP(sc::launch_fnv1a64(data, bytes, seed, nullptr, out, fault, workspace, static_cast<hipStream_t>(stream),
+                              expected, verdict, c),
            "hash launch");
     return ok();
 }

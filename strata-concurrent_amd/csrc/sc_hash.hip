@@ -311,17 +311,18 @@ __device__ __forceinline__ uint64_t segment_sum(const uint8_t* p, uint64_t n, ui
 
 // h = seed * p^n + the sum of the workgroups' sums (mod 2^64; the order of the additions does not matter), `acc` being
 // that sum, or null for an empty input.  `fault` is the launch's fault word (null for an empty input, which has no
-// waits): a wait that ran out makes h unusable, and the launch says so at `fault_out` - 1 or 0, or, for a chained piece
-// (`sticky`), 1 or'ed into what the earlier pieces left there, so a chain reports a fault of any of its pieces.  With
-// `verdict`, also 1 there when h equals `expected` and no wait of the launch ran out, else 0: a later kernel on the
-// stream can act on the check without a host round trip.
+// waits): a wait that ran out (kFaultWait) or carries that do not match the input (kFaultCarry) make h unusable, and the
+// launch says so at `fault_out` - the fault word, 0 for none, or, for a chained piece (`sticky`), or'ed into what the
+// earlier pieces left there, so a chain reports a fault of any of its pieces.  With `verdict`, also 1 there when h
+// equals `expected` and the launch has no fault, else 0: a later kernel on the stream can act on the check without a
+// host round trip.
 __global__ void fnv_finish_kernel(const uint64_t* acc, uint64_t seed, const uint64_t* seed_dev, uint64_t n, uint64_t* out,
                                   uint32_t* fault_out, bool sticky, uint64_t expected, uint32_t* verdict,
                                   const uint32_t* fault, const uint8_t* tail, uint32_t tail_len) {
     uint64_t h = start_state(seed, seed_dev) * pow_prime(n) + (acc ? acc[0] : 0u);
     // the mapped hash leaves the payload's last partial lane segment (under 256 bytes) to this loop
     for (uint32_t i = 0; i < tail_len; ++i) h = (h ^ tail[i]) * kFnvPrime;
-    const uint32_t bad = fault && fault[0] ? 1u : 0u;
+    const uint32_t bad = fault ? fault[0] : 0u;   // kFaultWait and / or kFaultCarry
     out[0] = h;
     if (fault_out) fault_out[0] = sticky ? (fault_out[0] | bad) : bad;
     if (verdict) verdict[0] = h == expected && !bad ? 1u : 0u;
@@ -345,6 +346,12 @@ constexpr uint32_t kSpinLimit = 1u << 16;   // reads of one window, about 0.2 s 
 // once, so any input of more than one workgroup (64 KiB) ends with the fault set, deterministically.
 constexpr uint32_t kForceFault = 0xFFFFFFFFu;
 
+// The launch's fault word: 0, or the or of kFaultWait (a look-back wait ran out) and kFaultCarry (a workgroup of a check
+// given carries did not end with the carry after it: the input or its carries are not what was hashed).
+constexpr uint32_t kFaultWait = SC_FNV_FAULT_WAIT, kFaultCarry = SC_FNV_FAULT_CARRY;
+__device__ __forceinline__ void flag_fault(uint32_t* fault, uint32_t v) {
+    __hip_atomic_fetch_or(fault, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 __device__ __forceinline__ void publish(uint32_t* word, uint32_t v) {
     __hip_atomic_store(word, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -366,7 +373,7 @@ __device__ __forceinline__ uint32_t look_back(uint32_t* status, uint64_t g, uint
     }
     if (spin_limit == kForceFault) {   // the failure-handling tests' forced fault (never set otherwise)
         if (lane == 0) {
-            publish(fault, 1u);
+            flag_fault(fault, kFaultWait);
             publish(status + g, kHasState | apply<kBits>(map, 0u));
         }
         return 0u;
@@ -388,7 +395,7 @@ __device__ __forceinline__ uint32_t look_back(uint32_t* status, uint64_t g, uint
         if ((ready & need) != need) {   // a workgroup between g and that end state has not published its map yet
             if (++spins > spin_limit) {   // never in a correct launch; successors still get an end state
                 if (lane == 0) {
-                    publish(fault, 1u);
+                    flag_fault(fault, kFaultWait);
                     publish(status + g, kHasState | apply<kBits>(map, 0u));
                 }
                 return 0u;
@@ -437,7 +444,8 @@ __device__ __forceinline__ uint64_t uniform64(uint64_t v) {
 template <int kBits, typename During>
 __device__ __forceinline__ uint32_t resolve_level(uint32_t lane_map, uint64_t g, uint32_t* status, uint32_t init,
                                                   uint32_t* fault, uint32_t spin_limit, LevelLds& L, int first_sleeps,
-                                                  During during) {
+                                                  During during, int j, const uint8_t* carry_in, uint64_t carry_count,
+                                                  uint32_t& end_bits) {
     uint64_t bw[kMaxLevelWords] = {};
 #pragma unroll
     for (int i = 0; i < level_words<kBits>(); ++i) bw[i] = __ballot((lane_map >> i) & 1u);
@@ -463,12 +471,21 @@ __device__ __forceinline__ uint32_t resolve_level(uint32_t lane_map, uint64_t g,
     if (wave == 0) {
         for (int k = 1; k < kFnvThreads / 64; ++k) sum = compose<kBits>(L.map[k], sum);
         sum = __builtin_amdgcn_readfirstlane(sum);
-        if (lane == 0 && g > 0) publish(status + g, kHasMap | sum);
+        if (lane == 0 && g > 0 && !carry_in) publish(status + g, kHasMap | sum);
     }
     during();
     if (wave == 0) {
-        const uint32_t st = look_back<kBits>(status, g, sum, init, fault, spin_limit, first_sleeps);
+        constexpr uint32_t kMask = (1u << kBits) - 1u;
+        uint32_t st;
+        if (carry_in) {   // the start is the carry before the workgroup, checked by the one after it
+            st = g == 0 ? init : (uint32_t(carry_in[g - 1]) >> j) & kMask;
+            if (g < carry_count && apply<kBits>(sum, st) != ((uint32_t(carry_in[g]) >> j) & kMask) && lane == 0)
+                flag_fault(fault, kFaultCarry);
+        } else {
+            st = look_back<kBits>(status, g, sum, init, fault, spin_limit, first_sleeps);
+        }
         if (lane == 0) L.state = st;
+        end_bits |= apply<kBits>(sum, st) << j;
     }
     __syncthreads();
     uint32_t st = __builtin_amdgcn_readfirstlane(L.state);
@@ -684,7 +701,8 @@ template <bool kMapped>
 __global__ void __launch_bounds__(kFnvThreads) __attribute__((amdgpu_waves_per_eu(5, 8))) fnv_onepass_kernel(const uint8_t* data, uint64_t n, bool aligned,
                                                                 uint64_t seed, const uint64_t* seed_dev,
                                                                 uint32_t* status, uint64_t stride, uint32_t* ctl,
-                                                                uint32_t spin_limit, HashMapArgs map) {
+                                                                uint32_t spin_limit, HashMapArgs map,
+                                                                FnvCarries carries, uint64_t carry_count) {
     __shared__ LevelLds L;
     __shared__ uint32_t s_ticket;
     __shared__ uint64_t s_sum[kFnvThreads / 64];
@@ -736,8 +754,10 @@ __global__ void __launch_bounds__(kFnvThreads) __attribute__((amdgpu_waves_per_e
             if (map.store)
                 store_wave(s_xpose[wave], w, base, (g * kFnvThreads + uint64_t(wave) * 64) * kFnvLaneBytes, n, lane);
     };
+    uint32_t end_bits = 0;   // wave 0: the workgroup's end state, level by level (its carry)
     uint32_t s = resolve_level<3>(lane_map, g, status, uint32_t(h0) & 7u, fault, spin_limit, L,
-                                  kMapped ? kFirstSleepsMapped : kFirstSleeps, store_gathered);
+                                  kMapped ? kFirstSleepsMapped : kFirstSleeps, store_gathered, 0, carries.in,
+                                  carry_count, end_bits);
     uint32_t sb = apply<3>(halves & 0xFFFFu, s);
 
     lane_map = 0;
@@ -748,7 +768,7 @@ __global__ void __launch_bounds__(kFnvThreads) __attribute__((amdgpu_waves_per_e
         lane_map = map3_bytes<3>(p, len, s);
     }
     uint32_t st = resolve_level<3>(lane_map, g, status + stride, uint32_t(h0 >> 3) & 7u, fault, spin_limit, L,
-                                   kFirstSleeps, [] {});
+                                   kFirstSleeps, [] {}, 3, carries.in, carry_count, end_bits);
     s |= st << 3;
     sb |= apply<3>(halves & 0xFFFFu, st) << 3;
 
@@ -760,7 +780,8 @@ __global__ void __launch_bounds__(kFnvThreads) __attribute__((amdgpu_waves_per_e
         lane_map = map2_bytes<6>(p, len, s);
     }
     st = resolve_level<2>(lane_map, g, status + 2 * stride, uint32_t(h0 >> 6) & 3u, fault, spin_limit, L, kFirstSleeps,
-                          [] {});
+                          [] {}, 6, carries.in, carry_count, end_bits);
+    if (carries.out && threadIdx.x == 0 && g < carry_count) carries.out[g] = uint8_t(end_bits);
     s |= st << 6;
     sb |= apply<2>(halves & 0xFFFFu, st) << 6;
 
@@ -812,7 +833,8 @@ FnvWorkspace fnv_workspace(uint64_t n) {
 }
 
 hipError_t launch_fnv1a64(const void* data, uint64_t n, uint64_t seed, const uint64_t* seed_dev, uint64_t* out,
-                          uint32_t* fault_out, void* workspace, hipStream_t stream, uint64_t expected, uint32_t* verdict) {
+                          uint32_t* fault_out, void* workspace, hipStream_t stream, uint64_t expected, uint32_t* verdict,
+                          const FnvCarries& carries) {
     const FnvWorkspace w = fnv_workspace(n);
     uint8_t* ws = static_cast<uint8_t*>(workspace);
     const uint8_t* src = static_cast<const uint8_t*>(data);
@@ -825,7 +847,8 @@ hipError_t launch_fnv1a64(const void* data, uint64_t n, uint64_t seed, const uin
         hipLaunchKernelGGL(fnv_onepass_init_kernel, dim3(unsigned(init_blocks)), dim3(kThreads), 0, stream, status, words,
                            ctl);
         hipLaunchKernelGGL(fnv_onepass_kernel<false>, dim3(unsigned(w.groups)), dim3(kFnvThreads), 0, stream, src, n, aligned,
-                           seed, seed_dev, status, w.stride, ctl, g_spin_limit.load(), HashMapArgs{});
+                           seed, seed_dev, status, w.stride, ctl, g_spin_limit.load(), HashMapArgs{}, carries,
+                           fnv_carry_count(n));
     }
     // the finish reads the start state before it writes `out`, so `out` may be `seed_dev` itself
     const bool any = w.groups > 0;
@@ -838,10 +861,11 @@ hipError_t launch_fnv1a64(const void* data, uint64_t n, uint64_t seed, const uin
 // The gather fused with the hash: the payload's `map.n_total` bytes gathered into its segments and hashed, the whole
 // lane segments in the one-pass kernel and the last partial one (under 256 bytes, at `tail`) by the closing kernel,
 // which runs after every byte is in place.  With `verdict`, the closing kernel also leaves the check of the hash
-// against `expected` there, as sc_fnv1a64_check_async does.
+// against `expected` there, as sc_fnv1a64_check_async does.  The carries are those of the whole payload (`n_total`
+// bytes): a carry at a boundary inside the last partial lane segment cannot occur (boundaries are 64 KiB apart).
 hipError_t launch_fnv1a64_mapped(const HashMapArgs& map, const uint8_t* tail, uint64_t seed, uint64_t* out,
                                  uint32_t* fault_out, void* workspace, hipStream_t stream, uint64_t expected,
-                                 uint32_t* verdict) {
+                                 uint32_t* verdict, const FnvCarries& carries) {
     const uint64_t n_total = map.n_total, n_full = n_total & ~uint64_t(kFnvLaneBytes - 1);
     const FnvWorkspace w = fnv_workspace(n_total);
     uint8_t* ws = static_cast<uint8_t*>(workspace);
@@ -856,7 +880,8 @@ hipError_t launch_fnv1a64_mapped(const HashMapArgs& map, const uint8_t* tail, ui
             hipLaunchKernelGGL(fnv_onepass_init_kernel, dim3(unsigned(init_blocks)), dim3(kThreads), 0, stream, status,
                                words, ctl);
             hipLaunchKernelGGL(fnv_onepass_kernel<false>, dim3(unsigned(w.groups)), dim3(kFnvThreads), 0, stream, nullptr,
-                               n_total, true, seed, nullptr, status, w.stride, ctl, g_spin_limit.load(), map);
+                               n_total, true, seed, nullptr, status, w.stride, ctl, g_spin_limit.load(), map, carries,
+                               fnv_carry_count(n_total));
         }
         const bool any = w.groups > 0;
         hipLaunchKernelGGL(fnv_finish_kernel, dim3(1), dim3(1), 0, stream,
@@ -870,7 +895,8 @@ hipError_t launch_fnv1a64_mapped(const HashMapArgs& map, const uint8_t* tail, ui
         hipLaunchKernelGGL(fnv_onepass_init_kernel, dim3(unsigned(init_blocks)), dim3(kThreads), 0, stream, status, words,
                            ctl);
         hipLaunchKernelGGL(fnv_onepass_kernel<true>, dim3(unsigned(w.groups)), dim3(kFnvThreads), 0, stream, nullptr, n_full,
-                           true, seed, nullptr, status, w.stride, ctl, g_spin_limit.load(), map);
+                           true, seed, nullptr, status, w.stride, ctl, g_spin_limit.load(), map, carries,
+                           fnv_carry_count(n_total));
     }
     const bool any = w.groups > 0;
     hipLaunchKernelGGL(fnv_finish_kernel, dim3(1), dim3(1), 0, stream, any ? reinterpret_cast<const uint64_t*>(ctl + 2) : nullptr,
@@ -930,7 +956,8 @@ extern "C" int sc_fnv1a64_noalloc_async(const void* data, uint64_t bytes, uint64
     hipError_t e = scratch_of_current_device(&ws);
     if (e != hipSuccess)
         return sc::record_error(SC_EHIP, std::string("sc_handoff hash scratch: ") + hipGetErrorString(e));
-    e = sc::launch_fnv1a64(data, bytes, seed, nullptr, out, fault, ws, static_cast<hipStream_t>(stream), 0, nullptr);
+    e = sc::launch_fnv1a64(data, bytes, seed, nullptr, out, fault, ws, static_cast<hipStream_t>(stream), 0, nullptr,
+                           sc::FnvCarries{});
     if (e != hipSuccess) return sc::record_error(SC_EHIP, std::string("sc_handoff hash launch: ") + hipGetErrorString(e));
     return sc::record_ok();
 }

@@ -224,6 +224,15 @@ static_assert(sizeof(HashExtent) == 48, "hash extents are 48 bytes");
 // and 512 (more workgroups mean more look-backs per byte, larger ones fewer resident workgroups per CU).
 constexpr int kFnvThreads = 256;
 constexpr int kFnvGroupBytes = kFnvThreads * kFnvLaneBytes;   // the payload bytes of one hash workgroup
+// The carries of a hashed input: the low byte of the running hash after each whole 64 KiB workgroup whose end lies
+// strictly inside the input, one byte per boundary (fnv_carry_count).  A launch may write them (`out`); a check given
+// them (`in`) starts every workgroup from the carry before it instead of looking back across workgroups, and checks
+// that the low byte it ends with is the carry after it.
+struct FnvCarries {
+    const uint8_t* in = nullptr;
+    uint8_t* out = nullptr;
+};
+constexpr uint64_t fnv_carry_count(uint64_t bytes) { return bytes ? (bytes - 1) / uint64_t(kFnvGroupBytes) : 0; }
 struct HashMapArgs {
     const HashExtent* ext;   // null: the plain hash of `data`
     const uint32_t* first;   // per workgroup: the extent holding its first byte

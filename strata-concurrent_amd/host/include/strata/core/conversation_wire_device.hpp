@@ -96,6 +96,10 @@ public:
     bool encode_segments(const sc_segments& into, void* stream, std::string& error);
     /// The payload hash of the last encode; waits for it.
     bool payload_hash(uint64_t& hash, std::string& error);
+    /// Later encodes also write the payload's carries (sc_fnv1a64_carry_bytes(bytes()) bytes of device memory at
+    /// `carry`, e.g. beside an exported payload): the low byte of the running hash after every 64 KiB, which lets a
+    /// decoder given them check the hash without the kernel's look-back (WireDeviceDecoder::set_carry).  Null stops it.
+    void set_carry(uint8_t* carry) { carry_ = carry; }
 
 private:
     void release();
@@ -141,6 +145,7 @@ private:
     sc_hash_map* seg_map_ = nullptr;   // the same into the segments of seg_target_
     std::vector<void*> seg_target_;
     uint64_t seg_bytes_ = 0;
+    uint8_t* carry_ = nullptr;         // device: where encodes write the payload's carries (null: not written)
 };
 
 class WireDeviceDecoder {
@@ -177,6 +182,11 @@ public:
     /// slot and copies every other blob into `image` (whose slot-resident K/V buffers and live gdn stay empty).
     /// Synchronous.  A refusal writes nothing to the slot.
     bool restore(void* stream, SavedConversation& image, std::string& error);
+    /// The payload's carries, as the encoder wrote them (device memory, sc_fnv1a64_carry_bytes(bytes) bytes): restore
+    /// then checks the hash starting every 64 KiB from its carry instead of looking back across the payload, with the
+    /// same verdict - a payload or carries that are not what was hashed is refused and nothing is mounted.  Null (the
+    /// default) checks without them.  Kept until the next open().
+    void set_carry(const uint8_t* carry) { carry_ = carry; }
 
 private:
     void release();
@@ -213,6 +223,7 @@ private:
     std::vector<void*> seg_;          // a segmented payload's segments (empty: the payload is at payload_)
     uint64_t seg_bytes_ = 0;
     sc_hash_map* read_map_ = nullptr; // the hash of a segmented payload where it lies
+    const uint8_t* carry_ = nullptr;  // device: the payload's carries (null: the check looks back)
     uint64_t* hash_dev_ = nullptr;    // device: the hash check's verdict word
     uint64_t* hash_host_ = nullptr;   // pinned (64 B); the hash's last kernel stores the payload hash here
     // and the launch's fault word right after it, so the host sees both words the device verdict is made of

@@ -371,8 +371,10 @@ bool WireDeviceEncoder::encode(void* payload, uint64_t capacity, void* stream, s
     // the hash and its fault word go straight to pinned host memory (the last kernel's stores): no readback copy
     if (!gathered) {
         // one kernel gathers the slot's blobs into the payload and hashes the payload from its registers
-        if (!abi(sc_hash_map_launch(hash_map_, kWireHashSeed, hash_host_, hash_fault_host(), hash_ws_, hash_ws_bytes_,
-                                    stream),
+        if (!abi(carry_ ? sc_hash_map_launch_carry(hash_map_, kWireHashSeed, hash_host_, hash_fault_host(), carry_,
+                                                   hash_ws_, hash_ws_bytes_, stream)
+                        : sc_hash_map_launch(hash_map_, kWireHashSeed, hash_host_, hash_fault_host(), hash_ws_,
+                                             hash_ws_bytes_, stream),
                  error, "payload gather and hash"))
             return false;
     } else {
@@ -382,8 +384,10 @@ bool WireDeviceEncoder::encode(void* payload, uint64_t capacity, void* stream, s
         for (const StagePlan& sp : stage_plans_)
             if (!abi(sc_plan_launch(sp.plan, stream), error, "stage gather")) return false;
         if (!abi(sc_event_record(gathered, stream), error, "gather event")) return false;
-        if (!abi(sc_fnv1a64_async(payload, plan_.total_bytes, kWireHashSeed, hash_host_, hash_fault_host(), hash_ws_,
-                                  hash_ws_bytes_, stream),
+        if (!abi(carry_ ? sc_fnv1a64_carry_async(payload, plan_.total_bytes, kWireHashSeed, hash_host_,
+                                                 hash_fault_host(), carry_, hash_ws_, hash_ws_bytes_, stream)
+                        : sc_fnv1a64_async(payload, plan_.total_bytes, kWireHashSeed, hash_host_, hash_fault_host(),
+                                           hash_ws_, hash_ws_bytes_, stream),
                  error, "payload hash"))
             return false;
     }
@@ -457,7 +461,10 @@ bool WireDeviceEncoder::encode_segments(const sc_segments& into, void* stream, s
                 return false;
             o = stop;
         }
-    if (!abi(sc_hash_map_launch(seg_map_, kWireHashSeed, hash_host_, hash_fault_host(), hash_ws_, hash_ws_bytes_, stream),
+    if (!abi(carry_ ? sc_hash_map_launch_carry(seg_map_, kWireHashSeed, hash_host_, hash_fault_host(), carry_, hash_ws_,
+                                               hash_ws_bytes_, stream)
+                    : sc_hash_map_launch(seg_map_, kWireHashSeed, hash_host_, hash_fault_host(), hash_ws_,
+                                         hash_ws_bytes_, stream),
              error, "payload gather and hash"))
         return false;
     last_stream_ = stream;
@@ -501,6 +508,7 @@ void WireDeviceDecoder::release() {
     ev_start_ = ev_done_ = side_ = nullptr;
     downloads_.clear();
     head_image_ = SavedConversation{};
+    carry_ = nullptr;
 }
 
 bool WireDeviceDecoder::copy_payload(void* dst, uint64_t off, uint64_t n, void* stream, std::string& error) {
@@ -745,13 +753,21 @@ bool WireDeviceDecoder::restore(void* stream, SavedConversation& image, std::str
         if (d.bytes && !copy_payload(staged_ + d.staged_at, d.offset, d.bytes, side_, error)) return false;
     if (!abi(sc_event_record(ev_done_, side_), error, "blob read")) return false;
     // the hash itself goes straight to pinned host memory (the last kernel's store), the verdict stays on the device
-    if (expect_.check_payload_hash &&
-        !abi(read_map_ ? sc_hash_map_check_async(read_map_, kWireHashSeed, expect_.payload_hash, hash_host_, verdict,
-                                                 hash_fault_host(), hash_ws_, hash_ws_bytes_, stream)
-                       : sc_fnv1a64_check_async(payload_, info_.bytes, kWireHashSeed, expect_.payload_hash, hash_host_,
-                                                verdict, hash_fault_host(), hash_ws_, hash_ws_bytes_, stream),
-             error, "payload hash"))
-        return false;
+    int hrc = SC_OK;
+    if (expect_.check_payload_hash) {
+        const uint64_t want = expect_.payload_hash;
+        if (read_map_)
+            hrc = carry_ ? sc_hash_map_check_carried_async(read_map_, kWireHashSeed, want, carry_, hash_host_, verdict,
+                                                           hash_fault_host(), hash_ws_, hash_ws_bytes_, stream)
+                         : sc_hash_map_check_async(read_map_, kWireHashSeed, want, hash_host_, verdict,
+                                                   hash_fault_host(), hash_ws_, hash_ws_bytes_, stream);
+        else
+            hrc = carry_ ? sc_fnv1a64_check_carried_async(payload_, info_.bytes, kWireHashSeed, want, carry_, hash_host_,
+                                                          verdict, hash_fault_host(), hash_ws_, hash_ws_bytes_, stream)
+                         : sc_fnv1a64_check_async(payload_, info_.bytes, kWireHashSeed, want, hash_host_, verdict,
+                                                  hash_fault_host(), hash_ws_, hash_ws_bytes_, stream);
+    }
+    if (!abi(hrc, error, "payload hash")) return false;
     SavedConversation out = head_image_;
     // the same blobs inside the copy: re-point the downloads by position
     auto remap = [&](void* who) -> void* {
@@ -796,6 +812,9 @@ bool WireDeviceDecoder::restore(void* stream, SavedConversation& image, std::str
     if (expect_.check_payload_hash) {
         // the device verdict that gated the scatters is exactly (hash == expected && no fault); the same two words are
         // in pinned memory, so the host decides as the scatters did, and a 0 verdict means they wrote nothing
+        if (*hash_fault_host() & SC_FNV_FAULT_CARRY)
+            return refuse(error, "the payload or its carries are not what was hashed (a 64 KiB piece of the payload "
+                                 "does not end with its carry); nothing was mounted");
         if (*hash_fault_host())
             return refuse(error, "the payload hash did not complete on the device (a look-back wait ran out); nothing "
                                  "was mounted");

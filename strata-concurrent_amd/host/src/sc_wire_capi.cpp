@@ -175,6 +175,12 @@ int sc_wire_encoder_hash(sc_wire_encoder* e, uint64_t* hash) {
     });
 }
 
+int sc_wire_encoder_set_carry(sc_wire_encoder* e, void* carry) {
+    if (!e) return failed(SC_EINVAL, "conversation wire: missing encoder");
+    e->enc.set_carry(static_cast<uint8_t*>(carry));
+    return done();
+}
+
 int sc_wire_encoder_destroy(sc_wire_encoder* e) {
     delete e;
     return done();
@@ -266,13 +272,20 @@ int sc_wire_decoder_open_layers_segments(const sc_segments* from, uint64_t bytes
 
 int64_t sc_wire_decoder_tokens(const sc_wire_decoder* d) { return d ? d->dec.tokens() : -1; }
 
+int sc_wire_decoder_set_carry(sc_wire_decoder* d, const void* carry) {
+    if (!d) return failed(SC_EINVAL, "conversation wire: missing decoder");
+    d->dec.set_carry(static_cast<const uint8_t*>(carry));
+    return done();
+}
+
 int sc_wire_decoder_restore(sc_wire_decoder* d, void* stream) {
     return guarded([&] {
         if (!d) return failed(SC_EINVAL, "conversation wire: missing decoder");
         std::string err;
         if (!d->dec.restore(stream, d->image, err))   // a timed-out or mismatching hash gated every scatter off
             return failed(hash_incomplete(err) ? SC_ETIMEOUT
-                          : err.find("hash mismatch") != std::string::npos || err.find("before a successful") != std::string::npos
+                          : err.find("hash mismatch") != std::string::npos || err.find("before a successful") != std::string::npos ||
+                                    err.find("its carries") != std::string::npos
                               ? SC_EINVAL : SC_EHIP, err);
         d->restored = true;
         return done();

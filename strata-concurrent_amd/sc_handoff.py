@@ -232,6 +232,11 @@ _SIGS = {
     "sc_hash_map_create_segments": (C.c_int, [C.POINTER(_P), C.c_int32, _P, _U64, C.POINTER(Segments), C.POINTER(_P)]),
     "sc_hash_map_create_read": (C.c_int, [C.POINTER(Segments), _U64, C.POINTER(_P)]),
     "sc_hash_map_check_async": (C.c_int, [_P, _U64, _U64, _P, _P, _P, _P, _U64, _P]),
+    "sc_fnv1a64_carry_bytes": (_U64, [_U64]),
+    "sc_fnv1a64_carry_async": (C.c_int, [_P, _U64, _U64, _P, _P, _P, _P, _U64, _P]),
+    "sc_fnv1a64_check_carried_async": (C.c_int, [_P, _U64, _U64, _U64, _P, _P, _P, _P, _P, _U64, _P]),
+    "sc_hash_map_launch_carry": (C.c_int, [_P, _U64, _P, _P, _P, _P, _U64, _P]),
+    "sc_hash_map_check_carried_async": (C.c_int, [_P, _U64, _U64, _P, _P, _P, _P, _P, _U64, _P]),
     "sc_plan_scatter_map_segments": (C.c_int, [_GEO, C.POINTER(Segments), _U64, C.POINTER(BlobMap), _I64,
                                                C.POINTER(DecodeSlot), C.POINTER(_P)]),
     "sc_plan_scatter_layers_segments": (C.c_int, [_GEO, C.POINTER(Segments), _U64, C.POINTER(LayersMap), _I64,
@@ -674,6 +679,14 @@ class HashFault(RuntimeError):
     """A look-back wait of the device hash ran out (the launch's fault word is 1): the hash is not valid."""
 
 
+FNV_FAULT_WAIT, FNV_FAULT_CARRY = 1, 2
+
+
+def carry_bytes(nbytes: int) -> int:
+    """Bytes of the carries of an `nbytes`-byte input (sc_fnv1a64_carry_bytes): one per 64 KiB boundary inside it."""
+    return int(lib.sc_fnv1a64_carry_bytes(nbytes))
+
+
 class HashPlan:
     """A reusable device workspace for sc_fnv1a64_async over inputs of up to `max_bytes` bytes, plus device words for
     the result and the launch's fault word."""
@@ -708,6 +721,29 @@ class HashPlan:
         check(lib.sc_fnv1a64_chain_async(ptr, nbytes, self.out.ptr, self.fault.ptr, self.ws.ptr, self.ws_bytes,
                                          _stream(stream)),
               "sc_fnv1a64_chain_async")
+
+    def launch_carry(self, ptr: int, nbytes: int, carry_ptr: int, seed: int = REFERENCE_FNV_SEED, stream=None) -> None:
+        """launch() that also writes the input's carries at `carry_ptr` (sc_fnv1a64_carry_async)."""
+        if nbytes > self.max_bytes:
+            raise ValueError(f"hash input of {nbytes} bytes exceeds the plan's {self.max_bytes}")
+        check(lib.sc_fnv1a64_carry_async(ptr, nbytes, seed, self.out.ptr, self.fault.ptr, carry_ptr, self.ws.ptr,
+                                         self.ws_bytes, _stream(stream)),
+              "sc_fnv1a64_carry_async")
+
+    def check_carried(self, ptr: int, nbytes: int, expected: int, carry_ptr: int, seed: int = REFERENCE_FNV_SEED,
+                      stream=None) -> None:
+        """The check of `expected` given the input's carries (sc_fnv1a64_check_carried_async): the hash in `out`, the
+        verdict in `verdict`, the fault word (FNV_FAULT_CARRY when the input or the carries are not what was hashed)
+        in `fault`."""
+        if nbytes > self.max_bytes:
+            raise ValueError(f"hash input of {nbytes} bytes exceeds the plan's {self.max_bytes}")
+        check(lib.sc_fnv1a64_check_carried_async(ptr, nbytes, seed, expected, carry_ptr, self.out.ptr,
+                                                 self.verdict.ptr, self.fault.ptr, self.ws.ptr, self.ws_bytes,
+                                                 _stream(stream)),
+              "sc_fnv1a64_check_carried_async")
+
+    def fault_word(self) -> int:
+        return int(self.fault.numpy()[0])
 
     def faulted(self) -> bool:
         return bool(self.fault.numpy()[0])
@@ -766,6 +802,18 @@ class HashMap:
         """launch() that also leaves the verdict (1: equal and complete) in hp.verdict (sc_hash_map_check_async)."""
         check(lib.sc_hash_map_check_async(self.handle, seed, expected, hp.out.ptr, hp.verdict.ptr, hp.fault.ptr,
                                           hp.ws.ptr, hp.ws_bytes, _stream(stream)), "sc_hash_map_check_async")
+
+    def launch_carry(self, hp: "HashPlan", carry_ptr: int, seed: int = REFERENCE_FNV_SEED, stream=None) -> None:
+        """launch() that also writes the payload's carries at `carry_ptr` (sc_hash_map_launch_carry)."""
+        check(lib.sc_hash_map_launch_carry(self.handle, seed, hp.out.ptr, hp.fault.ptr, carry_ptr, hp.ws.ptr,
+                                           hp.ws_bytes, _stream(stream)), "sc_hash_map_launch_carry")
+
+    def check_carried(self, hp: "HashPlan", expected: int, carry_ptr: int, seed: int = REFERENCE_FNV_SEED,
+                      stream=None) -> None:
+        """check() of a read map given the payload's carries (sc_hash_map_check_carried_async)."""
+        check(lib.sc_hash_map_check_carried_async(self.handle, seed, expected, carry_ptr, hp.out.ptr, hp.verdict.ptr,
+                                                  hp.fault.ptr, hp.ws.ptr, hp.ws_bytes, _stream(stream)),
+              "sc_hash_map_check_carried_async")
 
     def destroy(self) -> None:
         if self.handle:

@@ -40,6 +40,7 @@ for _name, _res, _args in (
     ("sc_wire_encode_async", C.c_int, [_P, _P, _U64, _P, _P]),
     ("sc_wire_encode_segments_async", C.c_int, [_P, C.POINTER(sc.Segments), _P]),
     ("sc_wire_encoder_hash", C.c_int, [_P, C.POINTER(_U64)]),
+    ("sc_wire_encoder_set_carry", C.c_int, [_P, _P]),
     ("sc_wire_encoder_destroy", C.c_int, [_P]),
     ("sc_wire_decoder_open", C.c_int, [_P, _U64, C.POINTER(sc.Geometry), C.POINTER(sc.DecodeSlot), C.POINTER(C.c_int64),
                                        _U64, _U64, _I32, _U64, _I32, C.POINTER(_P)]),
@@ -56,6 +57,7 @@ for _name, _res, _args in (
                                                        _U64, _I32, C.POINTER(_P)]),
     ("sc_wire_decoder_tokens", _I64, [_P]),
     ("sc_wire_decoder_restore", C.c_int, [_P, _P]),
+    ("sc_wire_decoder_set_carry", C.c_int, [_P, _P]),
     ("sc_wire_decoder_live_ids", C.c_int, [_P, C.POINTER(C.c_int32), _I64, C.POINTER(_I64)]),
     ("sc_wire_decoder_small", C.c_int, [_P, _I32, C.POINTER(C.c_uint8), _U64, C.POINTER(_U64)]),
     ("sc_wire_decoder_stage_small", C.c_int, [_P, _I32, _I32, C.POINTER(C.c_uint8), _U64, C.POINTER(_U64)]),
@@ -66,10 +68,11 @@ for _name, _res, _args in (
 
 EXPORTS = ("sc_wire_last_error", "sc_wire_encoder_create", "sc_wire_encoder_create_split",
            "sc_wire_encoder_create_layers", "sc_wire_encoder_bytes", "sc_wire_encoder_pool_offset",
-           "sc_wire_encode_async", "sc_wire_encode_segments_async", "sc_wire_encoder_hash", "sc_wire_encoder_destroy",
+           "sc_wire_encode_async", "sc_wire_encode_segments_async", "sc_wire_encoder_hash", "sc_wire_encoder_set_carry",
+           "sc_wire_encoder_destroy",
            "sc_wire_decoder_open", "sc_wire_decoder_open_split", "sc_wire_decoder_open_layers",
            "sc_wire_decoder_open_segments", "sc_wire_decoder_open_layers_segments", "sc_wire_decoder_tokens",
-           "sc_wire_decoder_restore", "sc_wire_decoder_live_ids", "sc_wire_decoder_small", "sc_wire_decoder_stage_small",
+           "sc_wire_decoder_restore", "sc_wire_decoder_set_carry", "sc_wire_decoder_live_ids", "sc_wire_decoder_small", "sc_wire_decoder_stage_small",
            "sc_wire_decoder_destroy")
 
 
@@ -166,6 +169,10 @@ class Encoder:
         _check(lib.sc_wire_encode_segments_async(self.handle, C.byref(segs), sc._stream(stream)),
                "sc_wire_encode_segments_async")
 
+    def set_carry(self, carry_ptr) -> None:
+        """Later encodes also write the payload's carries at `carry_ptr` (None stops it; sc_wire_encoder_set_carry)."""
+        _check(lib.sc_wire_encoder_set_carry(self.handle, carry_ptr), "sc_wire_encoder_set_carry")
+
     def hash(self) -> int:
         out = C.c_uint64(0)
         _check(lib.sc_wire_encoder_hash(self.handle, C.byref(out)), "sc_wire_encoder_hash")
@@ -189,7 +196,7 @@ class Decoder:
 
     def __init__(self, payload_ptr: int, nbytes: int, geo, slot, geometry=None, geom_hash=0, pack_hash=0,
                  check_identity=False, payload_hash=0, check_hash=False, stages=None, n_stages: int = 0,
-                 segments=None):
+                 segments=None, carry=None):
         self._slot = slot.c_struct()
         self._geo18 = (C.c_int64 * 18)(*geometry) if geometry is not None else None
         h = C.c_void_p()
@@ -211,6 +218,8 @@ class Decoder:
             _check(open_(payload_ptr, nbytes, C.byref(geo), C.byref(self._slot), self._geo18, geom_hash, pack_hash,
                          int(check_identity), payload_hash, int(check_hash), C.byref(h)), "sc_wire_decoder_open")
         self.handle = h.value
+        if carry is not None:   # the payload's carries as its encoder wrote them (sc_wire_decoder_set_carry)
+            _check(lib.sc_wire_decoder_set_carry(self.handle, carry), "sc_wire_decoder_set_carry")
 
     @property
     def tokens(self) -> int:
