@@ -138,6 +138,15 @@ int64_t sc_wire_decoder_tokens(const sc_wire_decoder* d);
  * write", include/strata/core/conversation_snapshot.hpp:103-108): SC_EINVAL for a hash that differs, SC_ETIMEOUT for a
  * device hash that did not complete (its verdict gated every scatter off, as for a mismatch). */
 int sc_wire_decoder_restore(sc_wire_decoder* d, void* stream);
+/* Opens `d` again for the next payload, with the geometry, slot, identity checks and kind of payload place it was
+ * opened with (not for a decoder of a layer-split payload): `payload` is the next payload's device memory, or NULL for
+ * a decoder opened on segments (the next payload lies in the same segments), `bytes` its size and `payload_hash` its
+ * expected hash.  The decoder keeps its staging, streams, events and hash words, and keeps its scatter plan when the
+ * payload's place, the slot and the blob offsets are unchanged (the next hand-off of a same-shaped conversation), so
+ * an engine that holds one decoder per slot opens each hand-off without allocating.  Carries set for the previous
+ * payload are dropped.  A refusal leaves the decoder to be opened again or destroyed.  No counterpart in the reference
+ * (its decoder is a function over a host buffer). */
+int sc_wire_decoder_reopen(sc_wire_decoder* d, const void* payload, uint64_t bytes, uint64_t payload_hash);
 /* The payload's carries as its encoder wrote them (device memory; sc_wire_encoder_set_carry), for the next restore of
  * this opened decoder: the payload hash is then checked starting every 64 KiB from its carry, with the same verdict -
  * a payload or carries that are not what was hashed are refused with SC_EINVAL and nothing is mounted.  NULL checks

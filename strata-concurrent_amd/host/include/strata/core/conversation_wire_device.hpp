@@ -157,7 +157,10 @@ public:
 
     /// Waits for the device (so a payload still arriving on any stream is complete), reads the head of the payload at
     /// `payload` (device memory, `bytes` long), checks it against `expect` and against the slot's shape, and plans the
-    /// scatter.  Nothing is written anywhere.
+    /// scatter.  Nothing is written anywhere.  A decoder may be opened again for the next payload: it keeps its staging,
+    /// streams, events and hash words, and keeps its scatter plan when the payload's place, the slot and the blob
+    /// offsets are the ones it was built for (the same-shaped payload of the next hand-off), so an engine that holds
+    /// one decoder per slot pays the allocations once.
     bool open(const void* payload, uint64_t bytes, const sc_geometry& g, const sc_decode_slot& slot,
               const WireExpect& expect, std::string& error);
     /// The same for a layer-split payload: `slot` takes the main session's layers and each stage's slot its stage
@@ -190,6 +193,7 @@ public:
 
 private:
     void release();
+    void drop_open();   // what one open holds; the buffers and the cached plans stay
     bool open_f16(const void* payload, const sc_segments* segs, uint64_t bytes, const sc_geometry& g,
                   const sc_decode_slot& slot, const std::vector<WireDeviceStage>& stages, const WireExpect& expect,
                   std::string& error);
@@ -224,6 +228,9 @@ private:
     uint64_t seg_bytes_ = 0;
     sc_hash_map* read_map_ = nullptr; // the hash of a segmented payload where it lies
     const uint8_t* carry_ = nullptr;  // device: the payload's carries (null: the check looks back)
+    std::vector<uint8_t> plan_key_;   // what scatter_ was built for (empty: nothing, or a plan not kept across opens)
+    std::vector<uint8_t> map_key_;    // what read_map_ was built for
+    uint64_t staged_cap_ = 0;         // bytes at staged_
     uint64_t* hash_dev_ = nullptr;    // device: the hash check's verdict word
     uint64_t* hash_host_ = nullptr;   // pinned (64 B); the hash's last kernel stores the payload hash here
     // and the launch's fault word right after it, so the host sees both words the device verdict is made of

@@ -21,6 +21,13 @@ bool abi(int rc, std::string& error, const char* what) {
 uint64_t up64(uint64_t n) { return (n + 63) & ~uint64_t(63); }
 
 // The slot-side shape of the payload: per-layer K/V blob bytes and the GDN blob bytes.
+// The bytes of a value, appended to the key of a plan (what it was built for).
+template <class T>
+void put_key(std::vector<uint8_t>& key, const T& v) {
+    const auto* p = reinterpret_cast<const uint8_t*>(&v);
+    key.insert(key.end(), p, p + sizeof(T));
+}
+
 struct SlotShape {
     int64_t n_qsa = 0, n_gdn = 0, cells = 0;
     uint64_t kv_bytes = 0, gdn_bytes = 0;
@@ -484,15 +491,24 @@ bool WireDeviceEncoder::payload_hash(uint64_t& hash, std::string& error) {
 
 WireDeviceDecoder::~WireDeviceDecoder() { release(); }
 
-void WireDeviceDecoder::release() {
+void WireDeviceDecoder::drop_open() {
     for (sc_plan* p : stage_scatters_)
         if (p) sc_plan_destroy(p);
     stage_scatters_.clear();
+    seg_.clear();
+    seg_bytes_ = 0;
+    downloads_.clear();
+    head_image_ = SavedConversation{};
+    carry_ = nullptr;
+}
+
+void WireDeviceDecoder::release() {
+    drop_open();
     if (scatter_) sc_plan_destroy(scatter_);
     if (read_map_) sc_hash_map_destroy(read_map_);
     read_map_ = nullptr;
-    seg_.clear();
-    seg_bytes_ = 0;
+    plan_key_.clear();
+    map_key_.clear();
     if (hash_ws_) sc_device_free(hash_ws_);
     if (hash_dev_) sc_device_free(hash_dev_);
     if (hash_host_) sc_host_free(hash_host_);
@@ -502,13 +518,12 @@ void WireDeviceDecoder::release() {
     if (side_) sc_stream_destroy(side_);
     scatter_ = nullptr;
     hash_ws_ = nullptr;
+    hash_ws_bytes_ = 0;
     hash_dev_ = nullptr;
     hash_host_ = nullptr;
     staged_ = nullptr;
+    staged_cap_ = 0;
     ev_start_ = ev_done_ = side_ = nullptr;
-    downloads_.clear();
-    head_image_ = SavedConversation{};
-    carry_ = nullptr;
 }
 
 bool WireDeviceDecoder::copy_payload(void* dst, uint64_t off, uint64_t n, void* stream, std::string& error) {
@@ -528,7 +543,7 @@ bool WireDeviceDecoder::copy_payload(void* dst, uint64_t off, uint64_t n, void* 
 
 bool WireDeviceDecoder::read_head(const void* payload, const sc_segments* segs, uint64_t bytes,
                                   const WireExpect& expect, std::vector<detail::WireBlobAt>& blobs, std::string& error) {
-    release();
+    drop_open();
     if (segs) {
         if (segs->n < 1 || !segs->ptr || !segs->segment_bytes || !segs->ptr[0])
             return refuse(error, "a segmented payload needs its segments");
@@ -574,19 +589,44 @@ bool WireDeviceDecoder::finish_open(const void* payload, uint64_t bytes, const W
     // The host blobs are read into pinned staging on a stream of their own, beside the hash and the scatter (pinned
     // reads are plain DMA; reads into pageable memory would each wait for a bounce copy), and handed out after the
     // verdict is read.
-    int rc = sc_host_alloc(reinterpret_cast<void**>(&staged_), staged ? staged : 64);
-    if (rc == SC_OK) rc = sc_stream_create(&side_);
-    if (rc == SC_OK) rc = sc_event_create(&ev_start_);
-    if (rc == SC_OK) rc = sc_event_create(&ev_done_);
+    // the buffers of an earlier open are kept when they are large enough
+    int rc = SC_OK;
+    const uint64_t need = staged ? staged : 64;
+    if (staged_cap_ < need) {
+        if (staged_) sc_host_free(staged_);
+        staged_ = nullptr;
+        staged_cap_ = 0;
+        rc = sc_host_alloc(reinterpret_cast<void**>(&staged_), need);
+        if (rc == SC_OK) staged_cap_ = need;
+    }
+    if (rc == SC_OK && !side_) rc = sc_stream_create(&side_);
+    if (rc == SC_OK && !ev_start_) rc = sc_event_create(&ev_start_);
+    if (rc == SC_OK && !ev_done_) rc = sc_event_create(&ev_done_);
     if (!abi(rc, error, "host blob staging")) { release(); return false; }
     if (expect.check_payload_hash) {
-        hash_ws_bytes_ = sc_fnv1a64_workspace_bytes(info_.bytes);
-        rc = sc_device_alloc(&hash_ws_, hash_ws_bytes_);
-        if (rc == SC_OK) rc = sc_device_alloc(reinterpret_cast<void**>(&hash_dev_), 64);
-        if (rc == SC_OK) rc = sc_host_alloc(reinterpret_cast<void**>(&hash_host_), 64);
+        const uint64_t ws = sc_fnv1a64_workspace_bytes(info_.bytes);
+        if (hash_ws_bytes_ < ws) {
+            if (hash_ws_) sc_device_free(hash_ws_);
+            hash_ws_ = nullptr;
+            hash_ws_bytes_ = 0;
+            rc = sc_device_alloc(&hash_ws_, ws);
+            if (rc == SC_OK) hash_ws_bytes_ = ws;
+        }
+        if (rc == SC_OK && !hash_dev_) rc = sc_device_alloc(reinterpret_cast<void**>(&hash_dev_), 64);
+        if (rc == SC_OK && !hash_host_) rc = sc_host_alloc(reinterpret_cast<void**>(&hash_host_), 64);
         if (rc == SC_OK && !seg_.empty()) {   // a segmented payload is hashed where it lies, in one launch
-            const sc_segments segs = segments();
-            rc = sc_hash_map_create_read(&segs, info_.bytes, &read_map_);
+            std::vector<uint8_t> key;
+            put_key(key, seg_bytes_);
+            put_key(key, info_.bytes);
+            for (void* q : seg_) put_key(key, q);
+            if (!read_map_ || key != map_key_) {
+                if (read_map_) sc_hash_map_destroy(read_map_);
+                read_map_ = nullptr;
+                map_key_.clear();
+                const sc_segments segs = segments();
+                rc = sc_hash_map_create_read(&segs, info_.bytes, &read_map_);
+                if (rc == SC_OK) map_key_ = key;
+            }
         }
         if (!abi(rc, error, "hash workspace")) { release(); return false; }
     }
@@ -673,9 +713,51 @@ bool WireDeviceDecoder::open_f16(const void* payload, const sc_segments* segs, u
         return seg_.empty() ? sc_plan_scatter_map(&sg, payload, bytes, &m, tokens_, &s, out)
                             : sc_plan_scatter_map_segments(&sg, &from, bytes, &m, tokens_, &s, out);
     };
-    if (!abi(scatter_plan(g, map, slot, &scatter_), error, "scatter plan")) {
-        release();
-        return false;
+    // the plan is kept for the next open of the same payload place, slot and blob offsets (no stages)
+    std::vector<uint8_t> key;
+    if (stages.empty()) {
+        put_key(key, int32_t(1));
+        put_key(key, g.n_layers);
+        put_key(key, g.qsa_interval);
+        put_key(key, g.n_head_kv);
+        put_key(key, g.head_dim);
+        put_key(key, g.page_size);
+        put_key(key, g.ssm_state_size);
+        put_key(key, g.ssm_k_heads);
+        put_key(key, g.ssm_v_heads);
+        put_key(key, g.ssm_d_conv);
+        put_key(key, g.ssm_conv_channels);
+        put_key(key, g.idx_key_dim);
+        put_key(key, slot.n_pages);
+        put_key(key, slot.max_cells);
+        put_key(key, slot.gdn_state);
+        for (int64_t j = 0; j < s.n_qsa; ++j) {
+            put_key(key, slot.k_pool[j]);
+            put_key(key, slot.v_pool[j]);
+            put_key(key, slot.page_table ? slot.page_table[j] : nullptr);
+            if (slot.host) put_key(key, slot.host[j]);
+            if (slot.stage) put_key(key, slot.stage[j]);
+        }
+        put_key(key, slot.host != nullptr);
+        put_key(key, slot.stage != nullptr);
+        put_key(key, payload);
+        put_key(key, bytes);
+        put_key(key, seg_bytes_);
+        for (void* q : seg_) put_key(key, q);
+        put_key(key, tokens_);
+        put_key(key, map.gdn_off);
+        for (uint64_t o : k_off) put_key(key, o);
+        for (uint64_t o : v_off) put_key(key, o);
+    }
+    if (key.empty() || !scatter_ || key != plan_key_) {
+        if (scatter_) sc_plan_destroy(scatter_);
+        scatter_ = nullptr;
+        plan_key_.clear();
+        if (!abi(scatter_plan(g, map, slot, &scatter_), error, "scatter plan")) {
+            release();
+            return false;
+        }
+        plan_key_ = key;
     }
     stage_scatters_.assign(stages.size(), nullptr);
     for (size_t i = 0; i < stages.size(); ++i) {
@@ -730,11 +812,44 @@ bool WireDeviceDecoder::open_layers(const void* payload, const sc_segments* segs
     device.push_back(&head_image_.live.gdn);
     sc_layers_map map{off.data(), nullptr, 0};
     const sc_segments from = segments();
-    const int rc = seg_.empty() ? sc_plan_scatter_layers(&g, payload, bytes, &map, tokens_, &slot, &scatter_)
-                                : sc_plan_scatter_layers_segments(&g, &from, bytes, &map, tokens_, &slot, &scatter_);
-    if (!abi(rc, error, "scatter plan")) {
-        release();
-        return false;
+    // the plan is kept for the next open of the same payload place, slot and blob offsets
+    std::vector<uint8_t> key;
+    put_key(key, int32_t(2));
+    put_key(key, g.n_layers);
+    put_key(key, g.qsa_interval);
+    put_key(key, g.n_head_kv);
+    put_key(key, g.head_dim);
+    put_key(key, g.page_size);
+    put_key(key, g.ssm_state_size);
+    put_key(key, g.ssm_k_heads);
+    put_key(key, g.ssm_v_heads);
+    put_key(key, g.ssm_d_conv);
+    put_key(key, g.ssm_conv_channels);
+    put_key(key, g.idx_key_dim);
+    put_key(key, slot.format);
+    put_key(key, slot.with_index);
+    put_key(key, slot.max_cells);
+    put_key(key, slot.pooled_capacity);
+    put_key(key, slot.gdn_state);
+    for (int x = 0; x < SC_N_BUF; ++x)
+        for (int64_t j = 0; j < s.n_qsa; ++j) put_key(key, slot.buf[x] ? slot.buf[x][j] : nullptr);
+    put_key(key, payload);
+    put_key(key, bytes);
+    put_key(key, seg_bytes_);
+    for (void* q : seg_) put_key(key, q);
+    put_key(key, tokens_);
+    for (uint64_t o : off) put_key(key, o);
+    if (!scatter_ || key != plan_key_) {
+        if (scatter_) sc_plan_destroy(scatter_);
+        scatter_ = nullptr;
+        plan_key_.clear();
+        const int rc = seg_.empty() ? sc_plan_scatter_layers(&g, payload, bytes, &map, tokens_, &slot, &scatter_)
+                                    : sc_plan_scatter_layers_segments(&g, &from, bytes, &map, tokens_, &slot, &scatter_);
+        if (!abi(rc, error, "scatter plan")) {
+            release();
+            return false;
+        }
+        plan_key_ = key;
     }
     return finish_open(payload, bytes, expect, blobs, device, error);
 }

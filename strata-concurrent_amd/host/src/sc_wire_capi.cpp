@@ -3,6 +3,8 @@
 
 #include "strata/core/conversation_wire_device.hpp"
 
+#include <algorithm>
+#include <array>
 #include <exception>
 #include <new>
 #include <string>
@@ -17,6 +19,55 @@ struct sc_wire_decoder {
     WireDeviceDecoder dec;
     SavedConversation image;
     bool restored = false;
+    // what it was opened with, for sc_wire_decoder_reopen: own copies of the slot's pointer arrays and segments
+    bool reopenable = false, layered = false, segmented = false;
+    sc_geometry g{};
+    WireExpect expect{};
+    sc_decode_slot slot{};
+    sc_slot_layers layers{};
+    std::vector<uint16_t*> k_pool, v_pool;
+    std::vector<const int32_t*> tables;
+    std::vector<sc_kv_pools> host, stage;
+    std::array<std::vector<void*>, SC_N_BUF> bufs;
+    std::vector<void*> seg_ptr;
+    uint64_t seg_bytes = 0;
+
+    void remember(const sc_geometry& geo, const sc_decode_slot& s, const sc_segments* segs, const WireExpect& e) {
+        const size_t n = size_t(std::max<int64_t>(sc_n_qsa_layers(&geo), 0));
+        g = geo;
+        expect = e;
+        slot = s;
+        layered = false;
+        k_pool.assign(s.k_pool, s.k_pool + (s.k_pool ? n : 0));
+        v_pool.assign(s.v_pool, s.v_pool + (s.v_pool ? n : 0));
+        tables.assign(s.page_table, s.page_table + (s.page_table ? n : 0));
+        host.assign(s.host, s.host + (s.host ? n : 0));
+        stage.assign(s.stage, s.stage + (s.stage ? n : 0));
+        slot.k_pool = s.k_pool ? k_pool.data() : nullptr;
+        slot.v_pool = s.v_pool ? v_pool.data() : nullptr;
+        slot.page_table = s.page_table ? tables.data() : nullptr;
+        slot.host = s.host ? host.data() : nullptr;
+        slot.stage = s.stage ? stage.data() : nullptr;
+        remember_segments(segs);
+    }
+    void remember(const sc_geometry& geo, const sc_slot_layers& s, const sc_segments* segs, const WireExpect& e) {
+        const size_t n = size_t(std::max<int64_t>(sc_n_qsa_layers(&geo), 0));
+        g = geo;
+        expect = e;
+        layers = s;
+        layered = true;
+        for (int x = 0; x < SC_N_BUF; ++x) {
+            bufs[size_t(x)].assign(s.buf[x], s.buf[x] + (s.buf[x] ? n : 0));
+            layers.buf[x] = s.buf[x] ? bufs[size_t(x)].data() : nullptr;
+        }
+        remember_segments(segs);
+    }
+    void remember_segments(const sc_segments* segs) {
+        segmented = segs != nullptr;
+        seg_ptr.assign(segs ? segs->ptr : nullptr, segs ? segs->ptr + segs->n : nullptr);
+        seg_bytes = segs ? segs->segment_bytes : 0;
+        reopenable = true;
+    }
 };
 
 namespace {
@@ -224,6 +275,7 @@ static int decoder_open(const void* payload, uint64_t bytes, const sc_geometry* 
             delete d;
             return failed(SC_EINVAL, err);
         }
+        if (n_stages == 0) d->remember(*g, *slot, segs, expect);
         *out = d;
         return done();
     });
@@ -271,6 +323,34 @@ int sc_wire_decoder_open_layers_segments(const sc_segments* from, uint64_t bytes
 }
 
 int64_t sc_wire_decoder_tokens(const sc_wire_decoder* d) { return d ? d->dec.tokens() : -1; }
+
+int sc_wire_decoder_reopen(sc_wire_decoder* d, const void* payload, uint64_t bytes, uint64_t payload_hash) {
+    return guarded([&] {
+        if (!d) return failed(SC_EINVAL, "conversation wire: missing decoder");
+        if (!d->reopenable)
+            return failed(SC_EINVAL, "conversation wire: a decoder of a layer-split payload is not opened again; open a new one");
+        if (d->segmented != (payload == nullptr))
+            return failed(SC_EINVAL, d->segmented ? "conversation wire: this decoder reads its payload from its segments "
+                                                    "(payload must be NULL)"
+                                                  : "conversation wire: missing payload");
+        WireExpect expect = d->expect;
+        expect.payload_hash = payload_hash;
+        d->restored = false;
+        d->image = SavedConversation{};
+        const sc_segments segs{int32_t(d->seg_ptr.size()), d->seg_bytes, d->seg_ptr.data()};
+        std::string err;
+        bool opened;
+        if (d->layered)
+            opened = d->segmented ? d->dec.open(segs, bytes, d->g, d->layers, expect, err)
+                                  : d->dec.open(payload, bytes, d->g, d->layers, expect, err);
+        else
+            opened = d->segmented ? d->dec.open(segs, bytes, d->g, d->slot, {}, expect, err)
+                                  : d->dec.open(payload, bytes, d->g, d->slot, expect, err);
+        if (!opened) return failed(SC_EINVAL, err);
+        d->expect = expect;
+        return done();
+    });
+}
 
 int sc_wire_decoder_set_carry(sc_wire_decoder* d, const void* carry) {
     if (!d) return failed(SC_EINVAL, "conversation wire: missing decoder");

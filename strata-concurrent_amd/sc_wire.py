@@ -58,6 +58,7 @@ for _name, _res, _args in (
     ("sc_wire_decoder_tokens", _I64, [_P]),
     ("sc_wire_decoder_restore", C.c_int, [_P, _P]),
     ("sc_wire_decoder_set_carry", C.c_int, [_P, _P]),
+    ("sc_wire_decoder_reopen", C.c_int, [_P, _P, _U64, _U64]),
     ("sc_wire_decoder_live_ids", C.c_int, [_P, C.POINTER(C.c_int32), _I64, C.POINTER(_I64)]),
     ("sc_wire_decoder_small", C.c_int, [_P, _I32, C.POINTER(C.c_uint8), _U64, C.POINTER(_U64)]),
     ("sc_wire_decoder_stage_small", C.c_int, [_P, _I32, _I32, C.POINTER(C.c_uint8), _U64, C.POINTER(_U64)]),
@@ -72,7 +73,7 @@ EXPORTS = ("sc_wire_last_error", "sc_wire_encoder_create", "sc_wire_encoder_crea
            "sc_wire_encoder_destroy",
            "sc_wire_decoder_open", "sc_wire_decoder_open_split", "sc_wire_decoder_open_layers",
            "sc_wire_decoder_open_segments", "sc_wire_decoder_open_layers_segments", "sc_wire_decoder_tokens",
-           "sc_wire_decoder_restore", "sc_wire_decoder_set_carry", "sc_wire_decoder_live_ids", "sc_wire_decoder_small", "sc_wire_decoder_stage_small",
+           "sc_wire_decoder_restore", "sc_wire_decoder_set_carry", "sc_wire_decoder_reopen", "sc_wire_decoder_live_ids", "sc_wire_decoder_small", "sc_wire_decoder_stage_small",
            "sc_wire_decoder_destroy")
 
 
@@ -227,6 +228,13 @@ class Decoder:
 
     def restore(self, stream=None) -> None:
         _check(lib.sc_wire_decoder_restore(self.handle, sc._stream(stream)), "sc_wire_decoder_restore")
+
+    def reopen(self, payload_ptr, nbytes: int, payload_hash: int = 0, carry=None) -> None:
+        """Open this decoder again for the next payload (None: the same segments), keeping its buffers and, when the
+        place, slot and blob offsets are unchanged, its scatter plan (sc_wire_decoder_reopen)."""
+        _check(lib.sc_wire_decoder_reopen(self.handle, payload_ptr, nbytes, payload_hash), "sc_wire_decoder_reopen")
+        if carry is not None:
+            _check(lib.sc_wire_decoder_set_carry(self.handle, carry), "sc_wire_decoder_set_carry")
 
     def live_ids(self):
         import numpy as np
