@@ -143,7 +143,7 @@ int sc_wire_decoder_restore(sc_wire_decoder* d, void* stream);
  * a decoder opened on segments (the next payload lies in the same segments), `bytes` its size and `payload_hash` its
  * expected hash.  The decoder keeps its staging, streams, events and hash words, and keeps its scatter plan when the
  * payload's place, the slot and the blob offsets are unchanged (the next hand-off of a same-shaped conversation), so
- * an engine that holds one decoder per slot opens each hand-off without allocating.  Carries set for the previous
+ * an engine that holds one decoder per slot opens each such hand-off without allocating device memory.  Carries set for the previous
  * payload are dropped.  A refusal leaves the decoder to be opened again or destroyed.  No counterpart in the reference
  * (its decoder is a function over a host buffer). */
 int sc_wire_decoder_reopen(sc_wire_decoder* d, const void* payload, uint64_t bytes, uint64_t payload_hash);
