@@ -89,8 +89,8 @@ struct sc_plan {
 };
 
 struct sc_hash_map {
-    sc::HashExtent* ext_dev = nullptr;   // one device block: the extents, each workgroup's first extent, the segments
-    uint32_t* first_dev = nullptr;
+    sc::HashExtent* ext_dev = nullptr;   // one device block: the extents, the workgroups' parts, the segments
+    sc::HashGroup* grp_dev = nullptr;
     uint8_t** seg_dev = nullptr;
     uint64_t seg_bytes = 0;
     const uint8_t* tail = nullptr;       // device address of the payload's last partial lane segment
@@ -1483,6 +1483,11 @@ int capture_extents(const sc_plan* const* plans, int32_t n_plans, const uint8_t*
                 return fail(SC_EINVAL, "sc_handoff: a row of the plan writes outside the hashed payload");
             x.off = uint64_t(r.dst - frame);
             x.end = x.off + r.n * 16;
+            // pages through the identity table, every one inside the pool, are one contiguous source: page k of
+            // the row is pool page k, so payload byte o comes from src + (o - off)
+            if (x.kind == sc::kExtPages && !x.table && x.page_chunks &&
+                (r.n + x.page_chunks - 1) / x.page_chunks <= uint64_t(std::max<int64_t>(x.ld, 0)))
+                x = sc::HashExtent{x.off, x.end, x.src, nullptr, 0, sc::kExtCopy, 0};
             if (x.end > x.off) rows.push_back(x);
         }
     }
@@ -1514,32 +1519,39 @@ int segment_list(const sc_segments* s, uint64_t bytes, std::vector<uint8_t*>& se
     return SC_OK;
 }
 
-// Uploads a map: the extents, each workgroup's first extent and the segment table, in one device block.  A map that
-// only reads (no extents) is hashed by the plain kernel from the segment table alone, so it uploads nothing else.
+// Uploads a map: the extents, each workgroup's part (sc::HashGroup) and the segment table, in one device block.  A map
+// that only reads (no extents) is hashed by the plain kernel from the segment table alone, so it uploads nothing else.
 int make_hash_map(const std::vector<sc::HashExtent>& ext, uint64_t bytes, const std::vector<uint8_t*>& segs,
                   uint64_t seg_bytes, bool store, sc_hash_map** out) {
     const sc::FnvWorkspace w = sc::fnv_workspace(bytes);
-    std::vector<uint32_t> first(store ? std::max<uint64_t>(w.groups, 1) : 1, 0);
+    std::vector<sc::HashGroup> grp(store ? std::max<uint64_t>(w.groups, 1) : 1, sc::HashGroup{});
     size_t e = 0;
     for (uint64_t g = 0; store && g < w.groups; ++g) {
-        const uint64_t o = g * uint64_t(sc::kFnvGroupBytes);
+        const uint64_t o = g * uint64_t(sc::kFnvGroupBytes), o_end = std::min(o + uint64_t(sc::kFnvGroupBytes), bytes);
         while (e + 1 < ext.size() && ext[e].end <= o) ++e;
-        first[g] = uint32_t(e);
+        sc::HashGroup& h = grp[g];
+        const uint64_t k = o / seg_bytes;
+        h.base = reinterpret_cast<uint8_t*>(
+            reinterpret_cast<uintptr_t>(segs[size_t(std::min<uint64_t>(k, segs.size() - 1))]) - k * seg_bytes);
+        h.first = uint32_t(e);
+        h.x[0] = ext[e];
+        if (e + 1 < ext.size()) h.x[1] = ext[e + 1];
+        h.two = ext[e].end >= o_end || (e + 1 < ext.size() && ext[e + 1].end >= o_end) ? 1u : 0u;
     }
     auto* m = new (std::nothrow) sc_hash_map();
     if (!m) return fail(SC_ENOMEM, "sc_handoff: hash map allocation failed");
     const uint64_t ext_bytes = round_up(ext.size() * sizeof(sc::HashExtent), 256);
-    const uint64_t first_bytes = round_up(first.size() * 4, 256);
-    hipError_t err = hipMalloc(reinterpret_cast<void**>(&m->ext_dev), ext_bytes + first_bytes + segs.size() * 8);
+    const uint64_t grp_bytes = round_up(grp.size() * sizeof(sc::HashGroup), 256);
+    hipError_t err = hipMalloc(reinterpret_cast<void**>(&m->ext_dev), ext_bytes + grp_bytes + segs.size() * 8);
     if (err != hipSuccess) {
         delete m;
         return fail(SC_ENOMEM, std::string("sc_handoff: hash map: ") + hipGetErrorString(err));
     }
     uint8_t* block = reinterpret_cast<uint8_t*>(m->ext_dev);
-    m->first_dev = reinterpret_cast<uint32_t*>(block + ext_bytes);
-    m->seg_dev = reinterpret_cast<uint8_t**>(block + ext_bytes + first_bytes);
+    m->grp_dev = reinterpret_cast<sc::HashGroup*>(block + ext_bytes);
+    m->seg_dev = reinterpret_cast<uint8_t**>(block + ext_bytes + grp_bytes);
     if (!ext.empty()) err = hipMemcpy(m->ext_dev, ext.data(), ext.size() * sizeof(sc::HashExtent), hipMemcpyHostToDevice);
-    if (err == hipSuccess) err = hipMemcpy(m->first_dev, first.data(), first.size() * 4, hipMemcpyHostToDevice);
+    if (err == hipSuccess) err = hipMemcpy(m->grp_dev, grp.data(), grp.size() * sizeof(sc::HashGroup), hipMemcpyHostToDevice);
     if (err == hipSuccess) err = hipMemcpy(m->seg_dev, segs.data(), segs.size() * 8, hipMemcpyHostToDevice);
     if (err != hipSuccess) {
         (void) hipFree(m->ext_dev);
@@ -1609,7 +1621,7 @@ int sc_hash_map_launch(const sc_hash_map* map, uint64_t seed, uint64_t* out, uin
                        uint64_t workspace_bytes, void* stream) {
     if (const int rc = hash_map_args(map, fault, workspace, workspace_bytes)) return rc;
     if (!out || !fault) return fail(SC_EINVAL, "sc_handoff: missing hash output or fault word");
-    const sc::HashMapArgs a{map->ext_dev, map->first_dev, map->seg_dev, map->seg_bytes, map->bytes, map->store ? 1u : 0u};
+    const sc::HashMapArgs a{map->ext_dev, map->grp_dev, map->seg_dev, map->seg_bytes, map->bytes, map->store ? 1u : 0u};
     const hipError_t e =
         sc::launch_fnv1a64_mapped(a, map->tail, seed, out, fault, workspace, static_cast<hipStream_t>(stream));
     return e == hipSuccess ? ok() : hip_fail(e, "mapped hash launch");
@@ -1620,7 +1632,7 @@ int sc_hash_map_check_async(const sc_hash_map* map, uint64_t seed, uint64_t expe
     if (const int rc = hash_map_args(map, fault, workspace, workspace_bytes)) return rc;
     if (!out || !verdict || (reinterpret_cast<uintptr_t>(verdict) & 3u))
         return fail(SC_EINVAL, "sc_handoff: missing hash output, or a verdict word that is not 4-byte aligned");
-    const sc::HashMapArgs a{map->ext_dev, map->first_dev, map->seg_dev, map->seg_bytes, map->bytes, map->store ? 1u : 0u};
+    const sc::HashMapArgs a{map->ext_dev, map->grp_dev, map->seg_dev, map->seg_bytes, map->bytes, map->store ? 1u : 0u};
     const hipError_t e = sc::launch_fnv1a64_mapped(a, map->tail, seed, out, fault, workspace,
                                                    static_cast<hipStream_t>(stream), expected, verdict);
     return e == hipSuccess ? ok() : hip_fail(e, "mapped hash launch");
@@ -1631,7 +1643,7 @@ int sc_hash_map_launch_carry(const sc_hash_map* map, uint64_t seed, uint64_t* ou
     if (const int rc = hash_map_args(map, fault, workspace, workspace_bytes)) return rc;
     if (!out || !fault) return fail(SC_EINVAL, "sc_handoff: missing hash output or fault word");
     if (!carry_out && sc::fnv_carry_count(map->bytes)) return fail(SC_EINVAL, "sc_handoff: missing carry output");
-    const sc::HashMapArgs a{map->ext_dev, map->first_dev, map->seg_dev, map->seg_bytes, map->bytes, map->store ? 1u : 0u};
+    const sc::HashMapArgs a{map->ext_dev, map->grp_dev, map->seg_dev, map->seg_bytes, map->bytes, map->store ? 1u : 0u};
     sc::FnvCarries c;
     c.out = carry_out;
     const hipError_t e = sc::launch_fnv1a64_mapped(a, map->tail, seed, out, fault, workspace,
@@ -1648,7 +1660,7 @@ int sc_hash_map_check_carried_async(const sc_hash_map* map, uint64_t seed, uint6
     if (!carry && sc::fnv_carry_count(map->bytes)) return fail(SC_EINVAL, "sc_handoff: missing carries");
     if (map->store)
         return fail(SC_EINVAL, "sc_handoff: a check with carries reads the payload where it lies (sc_hash_map_create_read)");
-    const sc::HashMapArgs a{map->ext_dev, map->first_dev, map->seg_dev, map->seg_bytes, map->bytes, 0u};
+    const sc::HashMapArgs a{map->ext_dev, map->grp_dev, map->seg_dev, map->seg_bytes, map->bytes, 0u};
     sc::FnvCarries c;
     c.in = carry;
     const hipError_t e = sc::launch_fnv1a64_mapped(a, map->tail, seed, out, fault, workspace,

@@ -337,8 +337,11 @@ __global__ void fnv_finish_kernel(const uint64_t* acc, uint64_t seed, const uint
 // workgroup waits only on lower tickets, held by workgroups that are running or done, so every wait ends; each wait is
 // also bounded (kSpinLimit reads), after which the launch records a fault that fails the verdict and the workgroup
 // publishes an end state anyway, so no other workgroup waits on it.
+// The lane within its wave, from the exec-independent lane count (two VALU operations): used where keeping threadIdx.x
+// live across the kernel would spill it and reload it from scratch, a memory round trip each time.
+__device__ __forceinline__ int lane_id() { return int(__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u))); }
 constexpr uint32_t kHasMap = 1u << 8, kHasState = 1u << 9;   // a status word: 0, kHasMap | map, kHasState | state
-// Sleeps of 64 x 64 cycles before a look-back's first read of its window (the mapped kernel's first level writes its
+// Sleeps of 64 x 64 cycles before a look-back's first read of its window (the mapped kernel's last level writes its
 // gathered payload instead): 3.3 GB hashed in 1.77 ms with two, 1.79 ms with none
 constexpr int kFirstSleeps = 2, kFirstSleepsMapped = 0;
 constexpr uint32_t kSpinLimit = 1u << 16;   // reads of one window, about 0.2 s (sc_fnv1a64_set_spin_limit)
@@ -366,7 +369,7 @@ __device__ __forceinline__ uint32_t peek(uint32_t* word) {
 template <int kBits>
 __device__ __forceinline__ uint32_t look_back(uint32_t* status, uint64_t g, uint32_t map, uint32_t init, uint32_t* fault,
                                               uint32_t spin_limit, int first_sleeps) {
-    const int lane = threadIdx.x & 63;
+    const int lane = lane_id();
     if (g == 0) {
         if (lane == 0) publish(status, kHasState | apply<kBits>(map, init));
         return init;
@@ -442,7 +445,7 @@ __device__ __forceinline__ uint64_t uniform64(uint64_t v) {
 // does not need the level's result, done while the look-back waits), looks back for the workgroup's start state after
 // `first_sleeps` sleeps of 64 x 64 cycles, and returns this lane's start bits of the level (bit 0 upward).
 template <int kBits, typename During>
-__device__ __forceinline__ uint32_t resolve_level(uint32_t lane_map, uint64_t g, uint32_t* status, uint32_t init,
+__device__ __forceinline__ uint32_t resolve_level(int wave, uint32_t lane_map, uint64_t g, uint32_t* status, uint32_t init,
                                                   uint32_t* fault, uint32_t spin_limit, LevelLds& L, int first_sleeps,
                                                   During during, int j, const uint8_t* carry_in, uint64_t carry_count,
                                                   uint32_t& end_bits) {
@@ -460,7 +463,7 @@ __device__ __forceinline__ uint32_t resolve_level(uint32_t lane_map, uint64_t g,
         if (c == 0) wmap |= ((st >> 1) & 1u) << (1 + a);
         if constexpr (kBits == 3) wmap |= ((st >> 2) & 1u) << (3 + 2 * a + c);
     }
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int lane = lane_id();
     if (lane == 0) {
 #pragma unroll
         for (int i = 0; i < level_words<kBits>(); ++i) L.bw[wave][i] = bw[i];
@@ -598,11 +601,61 @@ __device__ __forceinline__ Run run_at(const HashExtent& x, uint64_t o, uint8_t* 
 
 __device__ u32x4 g_hash_zero_chunk;   // read for zero runs, so every chunk takes the same load
 
-// The lane's segment [begin, begin + len) gathered into w.  A segment in one run or two (the usual cases: inside a
-// blob, or across one page or blob boundary) issues its 16 loads at once from one or two bases; a segment over three
-// runs or more, and the payload's last partial segment, goes chunk by chunk into the payload, which the lane then reads
-// back (its own stores, after a fence).  The payload is written by store_wave below (the last partial segment only
-// here).
+// A lane's 256-byte segment from run a (its first ka chunks) and run b (the rest): 16 loads issued at once, a zero run's
+// from one zero chunk.
+__device__ __forceinline__ void load_runs(const Run& a, const Run& b, uint32_t ka, uint32_t (&w)[kFnvLaneBytes / 4]) {
+    const uint8_t* za = a.src ? a.src : reinterpret_cast<const uint8_t*>(&g_hash_zero_chunk);
+    const uint8_t* zb = b.src ? b.src : reinterpret_cast<const uint8_t*>(&g_hash_zero_chunk);
+    const uint64_t sa = a.src ? 16u : 0u, sb = b.src ? 16u : 0u;
+#pragma unroll
+    for (int k = 0; k < kFnvLaneBytes / 16; ++k) {
+        const bool in_a = uint32_t(k) < ka;
+        const uint8_t* q = in_a ? za + sa * uint64_t(k) : zb + sb * uint64_t(k - int(ka));
+        const u32x4 v = *(const gu32x4*) q;
+        w[4 * k] = v.x;
+        w[4 * k + 1] = v.y;
+        w[4 * k + 2] = v.z;
+        w[4 * k + 3] = v.w;
+    }
+}
+
+// A lane's whole segment inside extent X, where X holds the lane's whole wave and is wave-uniform (its fields stay in
+// scalar registers and no lane reads the extent table): a copy or the payload's own bytes in one run from one base, as
+// the plain hash loads, zeros without a load, pages in one run or two (across one page boundary).  False for a segment
+// over three pages or more (pages under 256 bytes), which the caller gathers chunk by chunk.
+__device__ __forceinline__ bool gather_in_extent(const HashExtent& X, uint8_t* base, uint64_t begin,
+                                                 uint32_t (&w)[kFnvLaneBytes / 4]) {
+    if (X.kind == kExtCopy) {
+        load_segment(X.src + (begin - X.off), w);
+        return true;
+    }
+    if (X.kind == kExtSelf) {
+        load_segment(base + begin, w);
+        return true;
+    }
+    if (X.kind == kExtZero) {
+#pragma unroll
+        for (int i = 0; i < kFnvLaneBytes / 4; ++i) w[i] = 0u;
+        return true;
+    }
+    const uint64_t seg_end = begin + kFnvLaneBytes;
+    const Run a = run_at(X, begin, base + begin);
+    Run b = a;
+    uint32_t ka = kFnvLaneBytes / 16;
+    if (a.end < seg_end) {
+        ka = uint32_t((a.end - begin) >> 4);
+        b = run_at(X, a.end, base + a.end);
+        if (b.end < seg_end) return false;
+    }
+    load_runs(a, b, ka, w);
+    return true;
+}
+
+// The lane's segment [begin, begin + len) gathered into w, walking the extent table from the workgroup's first extent
+// (a wave over an extent boundary, a workgroup over three extents or more, the payload's last wave).  A segment in one
+// run or two issues its 16 loads at once from one or two bases; a segment over three runs or more, and the payload's
+// last partial segment, goes chunk by chunk into the payload, which the lane then reads back (its own stores, after a
+// fence).  The payload is written by store_wave below (the last partial segment only here).
 __device__ __forceinline__ void gather_segment(const HashMapArgs& m, uint8_t* base, uint32_t e_group, uint64_t begin,
                                                uint64_t len, uint32_t (&w)[kFnvLaneBytes / 4]) {
     uint32_t e = e_group;
@@ -622,19 +675,7 @@ __device__ __forceinline__ void gather_segment(const HashMapArgs& m, uint8_t* ba
             two = b.end >= seg_end;
         }
         if (two) {
-            const uint8_t* za = a.src ? a.src : reinterpret_cast<const uint8_t*>(&g_hash_zero_chunk);
-            const uint8_t* zb = b.src ? b.src : reinterpret_cast<const uint8_t*>(&g_hash_zero_chunk);
-            const uint64_t sa = a.src ? 16u : 0u, sb = b.src ? 16u : 0u;
-#pragma unroll
-            for (int k = 0; k < kFnvLaneBytes / 16; ++k) {
-                const bool in_a = uint32_t(k) < ka;
-                const uint8_t* q = in_a ? za + sa * uint64_t(k) : zb + sb * uint64_t(k - int(ka));
-                const u32x4 v = *(const gu32x4*) q;
-                w[4 * k] = v.x;
-                w[4 * k + 1] = v.y;
-                w[4 * k + 2] = v.z;
-                w[4 * k + 3] = v.w;
-            }
+            load_runs(a, b, ka, w);
             return;
         }
         // three runs or more: walk from the workgroup's first extent again (the look-ahead above may have moved past
@@ -714,7 +755,9 @@ __global__ void __launch_bounds__(kFnvThreads) __attribute__((amdgpu_waves_per_e
     const uint64_t begin = (g * kFnvThreads + threadIdx.x) * kFnvLaneBytes;
     const bool live = begin < n;
     const uint64_t len = !live ? 0 : n - begin < kFnvLaneBytes ? n - begin : kFnvLaneBytes;
-    const bool full = aligned && len == kFnvLaneBytes;
+    // the mapped instance hashes whole lane segments only (its launch passes n rounded down to them, the closing kernel
+    // takes the rest), so every live lane is whole there and the byte-at-a-time forms below drop out of it
+    const bool full = kMapped ? live : aligned && len == kFnvLaneBytes;
     const uint8_t* p = data + begin;
     if (!kMapped && map.seg) {
         // a payload read where its segments hold it: this workgroup's 64 KiB lie in segment k
@@ -725,11 +768,34 @@ __global__ void __launch_bounds__(kFnvThreads) __attribute__((amdgpu_waves_per_e
     uint32_t w[kFnvLaneBytes / 4] = {};
     uint8_t* base = nullptr;   // mapped: `base` + o addresses payload byte o in the segment holding this workgroup's bytes
     if constexpr (kMapped) {
-        const uint64_t k = g * uint64_t(kFnvGroupBytes) / map.seg_bytes;
-        base = reinterpret_cast<uint8_t*>(reinterpret_cast<uintptr_t>(map.seg[k]) - k * map.seg_bytes);
+        // the workgroup's part of the map in one round trip: its 14 words read together through the constant address
+        // space (scalar loads; the map does not change during the launch) and held from here, rather than each field
+        // loaded in the branch that first needs it, one round trip after another
+        typedef const __attribute__((address_space(4))) uint64_t ConstWord;
+        const ConstWord* q = (const ConstWord*) (map.grp + g);
+        uint64_t h[14];
+#pragma unroll
+        for (int i = 0; i < 14; ++i) h[i] = q[i];
+        asm volatile("" ::"s"(h[0]), "s"(h[1]), "s"(h[2]), "s"(h[3]), "s"(h[4]), "s"(h[5]), "s"(h[6]), "s"(h[7]),
+                     "s"(h[8]), "s"(h[9]), "s"(h[10]), "s"(h[11]), "s"(h[12]), "s"(h[13]));
+        HashGroup hg;
+        static_assert(offsetof(HashGroup, pad) == 14 * 8, "the words read are the group's fields");
+        __builtin_memcpy(&hg, h, sizeof(h));
+        base = hg.base;
         if (begin < map.n_total) {
-            const uint64_t left = map.n_total - begin;
-            gather_segment(map, base, map.first[g], begin, left < kFnvLaneBytes ? left : kFnvLaneBytes, w);
+            const uint64_t wave_lo = (g * kFnvThreads + uint64_t(wave) * 64) * kFnvLaneBytes;
+            const uint64_t wave_hi = wave_lo + 64u * kFnvLaneBytes;
+            bool done = false;
+            if (hg.two && wave_hi <= map.n_total) {   // every lane of the wave whole, inside one of the two extents
+                if (wave_hi <= hg.x[0].end)
+                    done = gather_in_extent(hg.x[0], base, begin, w);
+                else if (wave_lo >= hg.x[0].end)
+                    done = gather_in_extent(hg.x[1], base, begin, w);
+            }
+            if (!done) {
+                const uint64_t left = map.n_total - begin;
+                gather_segment(map, base, hg.first, begin, left < kFnvLaneBytes ? left : kFnvLaneBytes, w);
+            }
         }
     } else if (full) {
         load_segment(p, w);
@@ -747,17 +813,17 @@ __global__ void __launch_bounds__(kFnvThreads) __attribute__((amdgpu_waves_per_e
     } else if (live) {
         lane_map = map3_bytes<0>(p, len, 0u);
     }
-    // the gathered payload is written while the first look-back waits (its waits are the longest: they follow the
-    // predecessors' gathers)
+    // the gathered payload is written while the last look-back waits: 2.05 ms for the 128K capture + hash, against
+    // 2.22 ms while the first waits, 2.15 ms while the second waits and 2.18 ms after the last (stores issued earlier
+    // meet the next workgroups' gathers)
     const auto store_gathered = [&] {
         if constexpr (kMapped)
             if (map.store)
                 store_wave(s_xpose[wave], w, base, (g * kFnvThreads + uint64_t(wave) * 64) * kFnvLaneBytes, n, lane);
     };
     uint32_t end_bits = 0;   // wave 0: the workgroup's end state, level by level (its carry)
-    uint32_t s = resolve_level<3>(lane_map, g, status, uint32_t(h0) & 7u, fault, spin_limit, L,
-                                  kMapped ? kFirstSleepsMapped : kFirstSleeps, store_gathered, 0, carries.in,
-                                  carry_count, end_bits);
+    uint32_t s = resolve_level<3>(wave, lane_map, g, status, uint32_t(h0) & 7u, fault, spin_limit, L,
+                                  kFirstSleeps, [] {}, 0, carries.in, carry_count, end_bits);
     uint32_t sb = apply<3>(halves & 0xFFFFu, s);
 
     lane_map = 0;
@@ -767,7 +833,7 @@ __global__ void __launch_bounds__(kFnvThreads) __attribute__((amdgpu_waves_per_e
     } else if (live) {
         lane_map = map3_bytes<3>(p, len, s);
     }
-    uint32_t st = resolve_level<3>(lane_map, g, status + stride, uint32_t(h0 >> 3) & 7u, fault, spin_limit, L,
+    uint32_t st = resolve_level<3>(wave, lane_map, g, status + stride, uint32_t(h0 >> 3) & 7u, fault, spin_limit, L,
                                    kFirstSleeps, [] {}, 3, carries.in, carry_count, end_bits);
     s |= st << 3;
     sb |= apply<3>(halves & 0xFFFFu, st) << 3;
@@ -779,8 +845,9 @@ __global__ void __launch_bounds__(kFnvThreads) __attribute__((amdgpu_waves_per_e
     } else if (live) {
         lane_map = map2_bytes<6>(p, len, s);
     }
-    st = resolve_level<2>(lane_map, g, status + 2 * stride, uint32_t(h0 >> 6) & 3u, fault, spin_limit, L, kFirstSleeps,
-                          [] {}, 6, carries.in, carry_count, end_bits);
+    st = resolve_level<2>(wave, lane_map, g, status + 2 * stride, uint32_t(h0 >> 6) & 3u, fault, spin_limit, L,
+                          kMapped ? kFirstSleepsMapped : kFirstSleeps, store_gathered, 6, carries.in, carry_count,
+                          end_bits);
     if (carries.out && threadIdx.x == 0 && g < carry_count) carries.out[g] = uint8_t(end_bits);
     s |= st << 6;
     sb |= apply<2>(halves & 0xFFFFu, st) << 6;

@@ -233,9 +233,21 @@ struct FnvCarries {
     uint8_t* out = nullptr;
 };
 constexpr uint64_t fnv_carry_count(uint64_t bytes) { return bytes ? (bytes - 1) / uint64_t(kFnvGroupBytes) : 0; }
+// One hash workgroup's part of a map, built with the map so that the workgroup reads it in one scalar load after its
+// ticket: where its payload bytes lie, the extent holding its first byte and, when all its bytes lie in at most two
+// extents (a workgroup inside one blob or across one blob boundary), those two, so that its lanes gather without
+// reading the extent table.
+struct HashGroup {
+    uint8_t* base;       // payload byte o of this workgroup is at base + o (its segment's start less the segment offset)
+    uint32_t first;      // the extent holding the workgroup's first byte
+    uint32_t two;        // 1: the workgroup's gathered bytes lie in x[0] and x[1]
+    HashExtent x[2];     // the extent `first` and the one after it (zeros past the last)
+    uint64_t pad[2];
+};
+static_assert(sizeof(HashGroup) == 128, "hash groups are 128 bytes");
 struct HashMapArgs {
     const HashExtent* ext;   // null: the plain hash of `data`
-    const uint32_t* first;   // per workgroup: the extent holding its first byte
+    const HashGroup* grp;    // per workgroup (maps that gather)
     uint8_t* const* seg;     // the payload's segments: byte o is at seg[o / seg_bytes] + o % seg_bytes
     uint64_t seg_bytes;      // a multiple of kFnvGroupBytes, so no workgroup's bytes straddle two segments
     uint64_t n_total;        // payload bytes gathered (n rounded down to whole lane segments is hashed in the kernel)
