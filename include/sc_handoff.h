@@ -325,6 +325,17 @@ int sc_park_layers_async(const sc_geometry* g, const sc_slot_layers* slot, int64
                          uint64_t image_bytes, void* stream, void* done);
 int sc_resume_layers_async(const sc_geometry* g, const void* host_image, uint64_t image_bytes, int64_t tokens,
                            const sc_slot_layers* slot, void* stream, void* done);
+/* A plan of plain device-to-device copies: `n` copies of `bytes` each (whole 16-byte chunks, both addresses 16-byte
+ * aligned, no two destinations overlapping), moved by one launch.  Its use is as a row source of a hash map
+ * (sc_hash_map_create, _segments): bytes staged in device memory once, such as a payload's head built on the host,
+ * are then written by the fused gather + hash itself instead of copied in before it.  No counterpart in the reference
+ * (its encoder writes the head and the pool with one host walk, src/core/conversation_wire.cpp:400-480). */
+typedef struct sc_copy {
+    void* dst;
+    const void* src;
+    uint64_t bytes;
+} sc_copy;
+int sc_plan_copies(const sc_copy* copies, int32_t n, sc_plan** out);
 /* Enqueue the plan on `stream` (a hipStream_t; NULL is the null stream).  Asynchronous. */
 int sc_plan_launch(const sc_plan* plan, void* stream);
 /* sc_plan_launch that moves nothing unless the 32-bit word at `gate` (device memory, written by earlier work on the

@@ -1220,6 +1220,40 @@ int sc_plan_capture(const sc_geometry* g, const sc_decode_slot* src, int64_t tok
     return guarded([&] { return page_plan(g, image, image_bytes, tokens, src, false, out); });
 }
 
+int sc_plan_copies(const sc_copy* copies, int32_t n, sc_plan** out) {
+    return guarded([&] {
+        if (!out || n < 0 || (n && !copies)) return fail(SC_EINVAL, "sc_handoff: missing copy plan argument");
+        std::vector<sc::MoveRow> rows;
+        std::vector<std::pair<uintptr_t, uintptr_t>> spans;
+        uint64_t payload = 0;
+        for (int32_t i = 0; i < n; ++i) {
+            const sc_copy& c = copies[i];
+            if (!c.bytes) continue;
+            if (!c.dst || !c.src || !aligned16(c.dst) || !aligned16(c.src) || c.bytes % 16)
+                return fail(SC_EINVAL, "sc_handoff: copies are whole 16-byte chunks between 16-byte aligned addresses");
+            sc::MoveRow r{};
+            r.kind = sc::kCopy;
+            r.src = static_cast<const uint8_t*>(c.src);
+            r.dst = static_cast<uint8_t*>(c.dst);
+            r.n = c.bytes / 16;
+            rows.push_back(r);
+            spans.push_back({reinterpret_cast<uintptr_t>(c.dst), reinterpret_cast<uintptr_t>(c.dst) + c.bytes});
+            payload += c.bytes;
+        }
+        std::sort(spans.begin(), spans.end());
+        for (size_t i = 1; i < spans.size(); ++i)
+            if (spans[i].first < spans[i - 1].second)
+                return fail(SC_EINVAL, "sc_handoff: two copies of a copy plan write the same bytes");
+        // the rows need no geometry; a unit one keeps the plan's divisors defined
+        Geo unit;
+        unit.H = unit.ps = unit.HV = 1;
+        unit.D = 8;
+        unit.S = 4;
+        unit.row_bytes = unit.page_bytes = 16;
+        return finish_plan(rows, unit, payload, out);
+    });
+}
+
 int sc_layer_blob_bytes(const sc_geometry* g, int32_t format, int32_t with_index, int64_t tokens, uint64_t* bytes) {
     return guarded([&] {
         Geo o;

@@ -320,8 +320,23 @@ __global__ void fnv_finish_kernel(const uint64_t* acc, uint64_t seed, const uint
                                   uint32_t* fault_out, bool sticky, uint64_t expected, uint32_t* verdict,
                                   const uint32_t* fault, const uint8_t* tail, uint32_t tail_len) {
     uint64_t h = start_state(seed, seed_dev) * pow_prime(n) + (acc ? acc[0] : 0u);
-    // the mapped hash leaves the payload's last partial lane segment (under 256 bytes) to this loop
-    for (uint32_t i = 0; i < tail_len; ++i) h = (h ^ tail[i]) * kFnvPrime;
+    // the mapped hash leaves the payload's last partial lane segment (under 256 bytes, whole 16-byte chunks at a 16-byte
+    // aligned address) to this thread: its chunks are loaded at once, then hashed a byte at a time from registers
+    // (a loop of byte loads took 14 us, each load waiting on the one before)
+    if (tail_len) {
+        u32x4 c[kFnvLaneBytes / 16];
+#pragma unroll
+        for (int k = 0; k < kFnvLaneBytes / 16; ++k)
+            c[k] = uint32_t(k) * 16u < tail_len ? *(const gu32x4*) (tail + 16 * k) : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int k = 0; k < kFnvLaneBytes / 16; ++k) {
+            if (uint32_t(k) * 16u >= tail_len) break;
+            const uint32_t word[4] = {c[k].x, c[k].y, c[k].z, c[k].w};
+#pragma unroll
+            for (int b = 0; b < 16; ++b)
+                if (uint32_t(k) * 16u + uint32_t(b) < tail_len) h = (h ^ ((word[b / 4] >> (8 * (b % 4))) & 0xFFu)) * kFnvPrime;
+        }
+    }
     const uint32_t bad = fault ? fault[0] : 0u;   // kFaultWait and / or kFaultCarry
     out[0] = h;
     if (fault_out) fault_out[0] = sticky ? (fault_out[0] | bad) : bad;
@@ -934,6 +949,7 @@ hipError_t launch_fnv1a64_mapped(const HashMapArgs& map, const uint8_t* tail, ui
                                  uint32_t* fault_out, void* workspace, hipStream_t stream, uint64_t expected,
                                  uint32_t* verdict, const FnvCarries& carries) {
     const uint64_t n_total = map.n_total, n_full = n_total & ~uint64_t(kFnvLaneBytes - 1);
+    if (n_total % 16) return hipErrorInvalidValue;   // maps hold whole 16-byte chunks (the closing kernel loads them)
     const FnvWorkspace w = fnv_workspace(n_total);
     uint8_t* ws = static_cast<uint8_t*>(workspace);
     uint32_t* ctl = reinterpret_cast<uint32_t*>(ws + w.off_ctl);

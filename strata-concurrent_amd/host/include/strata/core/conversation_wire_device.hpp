@@ -84,7 +84,8 @@ public:
     const WirePlan& layout() const { return plan_; }
     uint64_t bytes() const { return plan_.total_bytes; }
     /// Enqueues the whole encode on `stream` into `payload` (16-byte aligned device memory of at least bytes()): the
-    /// head copied in, then the gather fused with the payload hash (one read of the slot).  When `gathered` (a
+    /// gather fused with the payload hash (one read of the slot), which also writes the head and the small host blobs
+    /// from their device copy (or they are copied in first, for a head that is not whole 16-byte chunks).  When `gathered` (a
     /// hipEvent_t) is given the gather runs on its own first and the event is recorded once every payload byte is in
     /// place and before the hash runs, so a copy of the payload on another stream (a park) can start while the hash
     /// is computed.
@@ -133,6 +134,12 @@ private:
     std::vector<Upload> uploads_;      // the head and the small host blobs, staged in pinned memory
     uint8_t* staged_ = nullptr;        // pinned
     uint64_t staged_bytes_ = 0;
+    // The same bytes in device memory, copied once at plan time, when every upload is whole 16-byte chunks at a 16-byte
+    // offset (staged_rows_): the encode then writes them by copy rows of its gather (copies_, an sc_plan_copies plan
+    // built with the capture plans) instead of copying them in from pinned memory before it.
+    uint8_t* staged_dev_ = nullptr;
+    bool staged_rows_ = false;
+    sc_plan* copies_ = nullptr;
     void* hash_ws_ = nullptr;          // device
     uint64_t hash_ws_bytes_ = 0;
     uint64_t* hash_host_ = nullptr;    // pinned (64 B); the hash's last kernel stores the payload hash here

@@ -133,6 +133,8 @@ void WireDeviceEncoder::release() {
         if (sp.plan) sc_plan_destroy(sp.plan);
     stage_plans_.clear();
     if (capture_) sc_plan_destroy(capture_);
+    if (copies_) sc_plan_destroy(copies_);
+    copies_ = nullptr;
     if (hash_map_) sc_hash_map_destroy(hash_map_);
     hash_map_ = nullptr;
     if (seg_map_) sc_hash_map_destroy(seg_map_);
@@ -140,10 +142,13 @@ void WireDeviceEncoder::release() {
     seg_target_.clear();
     seg_bytes_ = 0;
     if (staged_) sc_host_free(staged_);
+    if (staged_dev_) sc_device_free(staged_dev_);
     if (hash_host_) sc_host_free(hash_host_);
     if (hash_ws_) sc_device_free(hash_ws_);
     capture_ = nullptr;
     staged_ = nullptr;
+    staged_dev_ = nullptr;
+    staged_rows_ = false;
     hash_host_ = nullptr;
     hash_ws_ = nullptr;
     capture_target_ = nullptr;
@@ -201,6 +206,15 @@ bool WireDeviceEncoder::stage(const SavedConversation& img, const std::vector<st
         if (!stage_host_blob(img, e->who, staged_ + at, e->bytes)) return refuse(error, "internal: a host blob of the pool was not found");
         uploads_.push_back({e->offset, up64(e->bytes), at});
         at += up64(e->bytes);
+    }
+    // a device copy of the staged bytes, written into each payload by copy rows of the gather (no copy per encode)
+    staged_rows_ = std::all_of(uploads_.begin(), uploads_.end(),
+                               [](const Upload& u) { return u.offset % 16 == 0 && u.bytes % 16 == 0; });
+    if (staged_rows_) {
+        rc = sc_device_alloc(reinterpret_cast<void**>(&staged_dev_), staged_bytes_ ? staged_bytes_ : 64);
+        if (rc == SC_OK) rc = sc_copy_async(staged_dev_, staged_, staged_bytes_, nullptr);
+        if (rc == SC_OK) rc = sc_stream_sync(nullptr);
+        if (!abi(rc, error, "device staging")) return false;
     }
     hash_ws_bytes_ = sc_fnv1a64_workspace_bytes(plan_.total_bytes);
     rc = sc_device_alloc(&hash_ws_, hash_ws_bytes_);
@@ -354,6 +368,8 @@ bool WireDeviceEncoder::encode(void* payload, uint64_t capacity, void* stream, s
     if (capture_target_ != payload) {
         if (capture_) sc_plan_destroy(capture_);
         capture_ = nullptr;
+        if (copies_) sc_plan_destroy(copies_);
+        copies_ = nullptr;
         for (StagePlan& sp : stage_plans_) {
             if (sp.plan) sc_plan_destroy(sp.plan);
             sp.plan = nullptr;
@@ -365,16 +381,19 @@ bool WireDeviceEncoder::encode(void* payload, uint64_t capacity, void* stream, s
         if (!capture_plans(payload, capacity, plans, error)) return false;
         capture_ = plans[0];
         for (size_t i = 0; i < stage_plans_.size(); ++i) stage_plans_[i].plan = plans[i + 1];
-        // the same rows as the sources of the fused gather + hash (the head and the small host blobs are copied in
-        // first and hashed as the payload holds them)
+        if (staged_rows_) copies_ = plans.back();
+        // the same rows as the sources of the fused gather + hash (with the head and the small host blobs as copy
+        // rows, or, when they are not whole 16-byte chunks, copied in first and hashed as the payload holds them)
         if (!abi(sc_hash_map_create(plans.data(), int32_t(plans.size()), payload, plan_.total_bytes, &hash_map_), error,
                  "payload hash map"))
             return false;
         capture_target_ = payload;
     }
     uint8_t* p = static_cast<uint8_t*>(payload);
-    for (const Upload& u : uploads_)
-        if (!abi(sc_copy_async(p + u.offset, staged_ + u.staged_at, u.bytes, stream), error, "head copy")) return false;
+    if (!staged_rows_)
+        for (const Upload& u : uploads_)
+            if (!abi(sc_copy_async(p + u.offset, staged_ + u.staged_at, u.bytes, stream), error, "head copy"))
+                return false;
     // the hash and its fault word go straight to pinned host memory (the last kernel's stores): no readback copy
     if (!gathered) {
         // one kernel gathers the slot's blobs into the payload and hashes the payload from its registers
@@ -390,6 +409,7 @@ bool WireDeviceEncoder::encode(void* payload, uint64_t capacity, void* stream, s
         if (!abi(sc_plan_launch(capture_, stream), error, "pool gather")) return false;
         for (const StagePlan& sp : stage_plans_)
             if (!abi(sc_plan_launch(sp.plan, stream), error, "stage gather")) return false;
+        if (copies_ && !abi(sc_plan_launch(copies_, stream), error, "head copy")) return false;
         if (!abi(sc_event_record(gathered, stream), error, "gather event")) return false;
         if (!abi(carry_ ? sc_fnv1a64_carry_async(payload, plan_.total_bytes, kWireHashSeed, hash_host_,
                                                  hash_fault_host(), carry_, hash_ws_, hash_ws_bytes_, stream)
@@ -435,6 +455,14 @@ bool WireDeviceEncoder::capture_plans(void* base, uint64_t capacity, std::vector
             return undo();
         plans.push_back(q);
     }
+    if (staged_rows_) {   // the head and the small host blobs from their device copy, last
+        std::vector<sc_copy> copies;
+        for (const Upload& u : uploads_)
+            copies.push_back({static_cast<uint8_t*>(base) + u.offset, staged_dev_ + u.staged_at, u.bytes});
+        sc_plan* q = nullptr;
+        if (!abi(sc_plan_copies(copies.data(), int32_t(copies.size()), &q), error, "head copy plan")) return undo();
+        plans.push_back(q);
+    }
     return true;
 }
 
@@ -457,8 +485,8 @@ bool WireDeviceEncoder::encode_segments(const sc_segments& into, void* stream, s
         seg_target_ = ptrs;
         seg_bytes_ = into.segment_bytes;
     }
-    // the head and the small host blobs, a piece per segment they touch
-    for (const Upload& u : uploads_)
+    // the head and the small host blobs (when the map does not write them), a piece per segment they touch
+    for (const Upload& u : staged_rows_ ? std::vector<Upload>{} : uploads_)
         for (uint64_t o = u.offset, end = u.offset + u.bytes; o < end;) {
             const uint64_t k = o / seg_bytes_, stop = std::min(end, (k + 1) * seg_bytes_);
             if (k >= ptrs.size()) return refuse(error, "the segments are smaller than the payload");

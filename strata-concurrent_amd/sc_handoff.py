@@ -151,6 +151,7 @@ _SIGS = {
     "sc_plan_gather": (C.c_int, [_GEO, C.POINTER(PrefillView), _P, _U64, C.POINTER(_P)]),
     "sc_plan_scatter": (C.c_int, [_GEO, _P, _U64, _I64, C.POINTER(DecodeSlot), C.POINTER(_P)]),
     "sc_plan_capture": (C.c_int, [_GEO, C.POINTER(DecodeSlot), _I64, _P, _U64, C.POINTER(_P)]),
+    "sc_plan_copies": (C.c_int, [_P, C.c_int32, C.POINTER(_P)]),
     "sc_plan_launch": (C.c_int, [_P, _P]),
     "sc_plan_launch_gated": (C.c_int, [_P, _P, _P]),
     "sc_batch_staging_layout": (C.c_int, [_GEO, C.POINTER(_I64), C.c_int32, C.POINTER(_U64), C.POINTER(_U64)]),
@@ -555,6 +556,18 @@ def plan_capture(geo: Geometry, slot: Slot, tokens: int, image_ptr: int, image_b
     check(lib.sc_plan_capture(C.byref(geo), C.byref(cs), tokens, image_ptr, image_bytes, C.byref(h)),
           "sc_plan_capture")
     return Plan(h.value, slot._keep)
+
+
+class CopyDesc(C.Structure):
+    _fields_ = [("dst", C.c_void_p), ("src", C.c_void_p), ("bytes", C.c_uint64)]
+
+
+def plan_copies(copies) -> Plan:
+    """A plan of device-to-device copies (sc_plan_copies): `copies` is a list of (dst_ptr, src_ptr, nbytes)."""
+    arr = (CopyDesc * max(len(copies), 1))(*[CopyDesc(d, s_, b) for d, s_, b in copies])
+    h = C.c_void_p()
+    check(lib.sc_plan_copies(C.cast(arr, C.c_void_p), len(copies), C.byref(h)), "sc_plan_copies")
+    return Plan(h.value, (arr,))
 
 
 def park_async(geo: Geometry, slot: Slot, tokens: int, host_ptr: int, host_bytes: int, stream=None,

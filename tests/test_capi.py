@@ -138,6 +138,19 @@ def test_noalloc_hash_refusals_before_any_hip_call(sc):
     assert "4-byte aligned" in sc.last_error()
 
 
+def test_copy_plan_refusals_before_any_hip_call(sc):
+    """A copy plan refuses copies that are not whole 16-byte chunks between 16-byte aligned addresses, and copies whose
+    destinations overlap, on the host (host addresses stand in: nothing is allocated or dereferenced)."""
+    base = 1 << 40
+    out = C.c_void_p()
+    for copies in ([(base + 8, base + 4096, 64)], [(base, base + 4096 + 4, 64)], [(base, base + 4096, 40)],
+                   [(base, base + 4096, 64), (base + 32, base + 8192, 64)]):
+        arr = (sc.CopyDesc * len(copies))(*[sc.CopyDesc(d, s_, b) for d, s_, b in copies])
+        assert sc.lib.sc_plan_copies(C.cast(arr, C.c_void_p), len(copies), C.byref(out)) == sc.SC_EINVAL
+    assert "same bytes" in sc.last_error()
+    assert sc.lib.sc_plan_copies(None, 1, C.byref(out)) == sc.SC_EINVAL
+
+
 def test_core_library_exports_the_wire_abi():
     """libsc_core.so exports every entry point include/sc_wire.h declares (the device payload path)."""
     import sc_wire

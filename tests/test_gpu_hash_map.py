@@ -101,6 +101,54 @@ def test_fused_map_with_head_and_offsets(sc, oracle, cuda):
         p.destroy()
 
 
+def test_copy_plan_alone_and_as_rows_of_a_map(sc, oracle, cuda):
+    """A plan of plain device copies (sc_plan_copies): launched on its own it writes exactly its copies (and nothing
+    between them); as rows of a map beside a capture plan (a head staged in device memory and two small blobs, the
+    wire encoder's use) the map writes the same payload as launching both plans, with the byte loop's hash - here with
+    no head copied in before the launch: the map's copy rows write it."""
+    geo = sc.geometry(**SMALL)
+    tokens = 53
+    case = synth.SyntheticCase(geo, tokens, seed=21)
+    slot = case.new_slot(max_cells=64)
+    case.carve_into(slot)
+    _, image = sc.image_layout(geo, tokens)
+    head, blob1, blob2 = 4096 + 48, 96, 64 * 1024 + 16
+    at1 = head + image
+    at2 = at1 + blob1 + 32          # a gap left as the payload holds it
+    total = at2 + blob2 + 48       # and a tail past the last row
+    rng = np.random.default_rng(9)
+    staged_host = rng.integers(0, 256, size=head + blob1 + blob2, dtype=np.uint8)
+    staged = sc.DeviceBuffer(staged_host.size, "uint8")
+    staged.upload(staged_host)
+    payload = sc.DeviceBuffer(total, "uint8")
+    copies = [(payload.ptr, staged.ptr, head), (payload.ptr + at1, staged.ptr + head, blob1),
+              (payload.ptr + at2, staged.ptr + head + blob1, blob2)]
+    cp = sc.plan_copies(copies)
+    assert cp.payload_bytes == head + blob1 + blob2
+    payload.fill(0x5D)
+    cp.launch()
+    sc.device_sync()
+    got = payload.numpy(total)
+    want = np.full(total, 0x5D, np.uint8)
+    want[:head] = staged_host[:head]
+    want[at1:at1 + blob1] = staged_host[head:head + blob1]
+    want[at2:at2 + blob2] = staged_host[head + blob1:]
+    assert np.array_equal(got, want), np.flatnonzero(got != want)[:8]
+    cap = sc.plan_capture(geo, slot, tokens, payload.ptr + head, image)
+    _compare(sc, oracle, [cap, cp], payload, total, 0x33)
+    # the same map over a payload whose length is not a whole lane segment, a head inside the first workgroup only
+    _compare(sc, oracle, [cp, cap], payload, at2 + blob2, 0x44)
+    cap.destroy()
+    cp.destroy()
+    # refusals: overlapping destinations, unaligned or partial chunks
+    for bad in ([(payload.ptr, staged.ptr, 64), (payload.ptr + 48, staged.ptr, 64)],
+                [(payload.ptr + 8, staged.ptr, 64)], [(payload.ptr, staged.ptr, 40)]):
+        with pytest.raises(sc.ScError):
+            sc.plan_copies(bad)
+    for b in (staged, payload):
+        b.free()
+
+
 @pytest.mark.parametrize("fmt", [1, 2, 3])
 @pytest.mark.parametrize("index", [False, True])
 @pytest.mark.parametrize("tokens", [1, 77])
