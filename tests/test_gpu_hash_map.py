@@ -149,6 +149,34 @@ def test_copy_plan_alone_and_as_rows_of_a_map(sc, oracle, cuda):
         b.free()
 
 
+def test_map_extent_boundaries_at_wave_and_workgroup_edges(sc, oracle, cuda):
+    """Copy rows whose boundaries fall exactly on a wave's edge (16 KiB), on a workgroup's edge (64 KiB), 16 bytes
+    past either, inside a lane segment, and three extents inside one workgroup, with gaps left as the payload holds
+    them: every wave that lies inside one of its workgroup's first two extents takes the uniform gather, the others
+    walk the extent table, and all give the payload the rows write and the byte loop's hash."""
+    W, G = 16 << 10, 64 << 10
+    cuts = [0, W, 2 * W + 16, G, G + 48, G + 64, 2 * G - 16, 2 * G + W, 3 * G, 3 * G + 4096, 5 * G + 256]
+    total = 5 * G + 256 + 3 * W + 80     # then a gap, and a tail that is not a whole lane segment
+    src = sc.DeviceBuffer(total, "uint8")
+    data = np.random.default_rng(17).integers(0, 256, size=total, dtype=np.uint8)
+    src.upload(data)
+    payload = sc.DeviceBuffer(total, "uint8")
+    copies = []
+    for k in range(len(cuts) - 1):
+        lo, hi = cuts[k], cuts[k + 1]
+        if k % 4 == 3:
+            continue                     # a gap: self bytes
+        # every other row reads its bytes from a shifted place of the source, so a row boundary is also a source jump
+        shift = 4096 * (k % 3)
+        copies.append((payload.ptr + lo, src.ptr + (lo + shift) % (total - (hi - lo)) // 16 * 16, hi - lo))
+    cp = sc.plan_copies(copies)
+    _compare(sc, oracle, [cp], payload, total - 80 + 64, 0x6B)
+    _compare(sc, oracle, [cp], payload, total, 0x6C)
+    cp.destroy()
+    src.free()
+    payload.free()
+
+
 @pytest.mark.parametrize("fmt", [1, 2, 3])
 @pytest.mark.parametrize("index", [False, True])
 @pytest.mark.parametrize("tokens", [1, 77])
