@@ -888,13 +888,12 @@ bool WireDeviceDecoder::restore(void* stream, SavedConversation& image, std::str
     // verdict word that gates the scatter, so a mismatch writes nothing and there is no host round trip before the
     // scatter; the host reads the hash back with the other small blobs, once, at the end.
     uint32_t* verdict = reinterpret_cast<uint32_t*>(hash_dev_ + 1);
-    // host blobs: read on the side stream once everything before this call on `stream` (the payload's arrival) is done
-    if (!abi(sc_event_record(ev_start_, stream), error, "restore start") ||
-        !abi(sc_stream_wait_event(side_, ev_start_), error, "restore start"))
-        return false;
-    for (const Download& d : downloads_)
-        if (d.bytes && !copy_payload(staged_ + d.staged_at, d.offset, d.bytes, side_, error)) return false;
-    if (!abi(sc_event_record(ev_done_, side_), error, "blob read")) return false;
+    // host blobs are read on the side stream once everything before this call on `stream` (the payload's arrival) is
+    // done: the point is marked here, and the side stream is set up after the hash is enqueued (a wait between streams
+    // and the first launch after it cost the host ~30 us, the GPU idle meanwhile); with no host blob to read there is
+    // no side stream work at all
+    const bool side = std::any_of(downloads_.begin(), downloads_.end(), [](const Download& d) { return d.bytes != 0; });
+    if (side && !abi(sc_event_record(ev_start_, stream), error, "restore start")) return false;
     // the hash itself goes straight to pinned host memory (the last kernel's store), the verdict stays on the device
     int hrc = SC_OK;
     if (expect_.check_payload_hash) {
@@ -911,6 +910,12 @@ bool WireDeviceDecoder::restore(void* stream, SavedConversation& image, std::str
                                                   hash_fault_host(), hash_ws_, hash_ws_bytes_, stream);
     }
     if (!abi(hrc, error, "payload hash")) return false;
+    if (side) {
+        if (!abi(sc_stream_wait_event(side_, ev_start_), error, "restore start")) return false;
+        for (const Download& d : downloads_)
+            if (d.bytes && !copy_payload(staged_ + d.staged_at, d.offset, d.bytes, side_, error)) return false;
+        if (!abi(sc_event_record(ev_done_, side_), error, "blob read")) return false;
+    }
     SavedConversation out = head_image_;
     // the same blobs inside the copy: re-point the downloads by position
     auto remap = [&](void* who) -> void* {
@@ -949,7 +954,7 @@ bool WireDeviceDecoder::restore(void* stream, SavedConversation& image, std::str
                                    : !abi(sc_plan_launch(scatter_, stream), error, "pool scatter"))
         return false;
     // the caller's stream covers the whole restore, the side stream's reads included
-    if (!abi(sc_stream_wait_event(stream, ev_done_), error, "restore") ||
+    if ((side && !abi(sc_stream_wait_event(stream, ev_done_), error, "restore")) ||
         !abi(sc_stream_sync(stream), error, "restore"))
         return false;
     if (expect_.check_payload_hash) {
