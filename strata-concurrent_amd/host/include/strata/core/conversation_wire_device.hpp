@@ -228,6 +228,8 @@ private:
     void* ev_start_ = nullptr;
     void* ev_done_ = nullptr;
     sc_plan* scatter_ = nullptr;
+    bool opened_ = false;   // the last open succeeded (the kept scatter plan alone does not say so: a refused open
+                            // keeps it for the next one)
     std::vector<sc_plan*> stage_scatters_;   // one per stage part, gated by the same hash verdict
     void* hash_ws_ = nullptr;
     uint64_t hash_ws_bytes_ = 0;

@@ -520,6 +520,7 @@ bool WireDeviceEncoder::payload_hash(uint64_t& hash, std::string& error) {
 WireDeviceDecoder::~WireDeviceDecoder() { release(); }
 
 void WireDeviceDecoder::drop_open() {
+    opened_ = false;
     for (sc_plan* p : stage_scatters_)
         if (p) sc_plan_destroy(p);
     stage_scatters_.clear();
@@ -661,6 +662,7 @@ bool WireDeviceDecoder::finish_open(const void* payload, uint64_t bytes, const W
     (void) payload;
     bytes_ = bytes;
     expect_ = expect;
+    opened_ = true;
     return true;
 }
 
@@ -883,7 +885,7 @@ bool WireDeviceDecoder::open_layers(const void* payload, const sc_segments* segs
 }
 
 bool WireDeviceDecoder::restore(void* stream, SavedConversation& image, std::string& error) {
-    if (!scatter_) return refuse(error, "restore before a successful open");
+    if (!opened_ || !scatter_) return refuse(error, "restore before a successful open");
     // The payload hash is checked on the device: the hash's last kernel compares it with the expected one and leaves a
     // verdict word that gates the scatter, so a mismatch writes nothing and there is no host round trip before the
     // scatter; the host reads the hash back with the other small blobs, once, at the end.

@@ -4,7 +4,8 @@ A serving engine holds one decoder per slot and re-opens it per hand-off, keepin
 place, the slot and the blob offsets are unchanged - its scatter plan.  Here every mount after a re-open must be the
 mount a fresh decoder makes: the next payload of another conversation of the same length in the same buffer (the plan
 kept), one of another length (the plan rebuilt), the same from segments, a slot in int8 with the indexer's rows, a
-wrong hash refused with the slot untouched and the decoder usable afterwards, and the refusals of the call itself.
+wrong hash refused with the slot untouched and the decoder usable afterwards, a refused re-open (corrupted head) after
+which a restore is refused with the slot untouched, and the refusals of the call itself.
 """
 import numpy as np
 import pytest
@@ -70,6 +71,21 @@ def test_reopen_contiguous(sc, wire, cuda):
     assert all(np.array_equal(before[k], after[k]) for k in before)
     dec.reopen(buf.ptr, n, h)
     dec.restore()
+    # a refused re-open (a corrupted head) leaves nothing to restore: the restore is refused with the slot untouched,
+    # though the decoder keeps its scatter plan for the next open, which then mounts
+    magic = buf.numpy(1, start=0)
+    buf.upload(magic ^ 0xFF, start=0)
+    with pytest.raises(wire.WireError):
+        dec.reopen(buf.ptr, n, h)
+    before = dst.host_state()
+    with pytest.raises(wire.WireError):
+        dec.restore()
+    after = dst.host_state()
+    assert all(np.array_equal(before[k], after[k]) for k in before)
+    buf.upload(magic, start=0)
+    dec.reopen(buf.ptr, n, h)
+    dec.restore()
+    assert _slot_equal(geo, tokens, src, dst)
     # the call's own refusals: a contiguous decoder needs a payload
     with pytest.raises(wire.WireError):
         dec.reopen(None, n, h)
