@@ -253,6 +253,10 @@ bool WireDeviceEncoder::plan(const sc_geometry& g, const sc_decode_slot& slot, i
         if (st.state.ids != conv.live.ids) return refuse(error, "a stage part's ids are not the live ids");
         if (!st.state.gdn.empty() || !st.state.imgs.empty() || !st.state.stage_parts.empty())
             return refuse(error, "a stage part's state carries only its small host buffers (its GDN rows are the slot's)");
+        // checked before anything is staged: a refusal leaves the encoder without a plan
+        if (st.slot.page_table)
+            for (int64_t j = 0; j < ss.n_qsa; ++j)
+                if (st.slot.page_table[j]) return refuse(error, "a stage slot must use identity page tables");
         ConversationStageSnapshot& part = img.stage_parts[i];
         part.layer_lo = st.layer_lo;
         part.layer_hi = st.layer_hi;
@@ -287,9 +291,6 @@ bool WireDeviceEncoder::plan(const sc_geometry& g, const sc_decode_slot& slot, i
         sp.slot.k_pool = st.slot.k_pool ? sp.k.data() : nullptr;
         sp.slot.v_pool = st.slot.v_pool ? sp.v.data() : nullptr;
         sp.slot.page_table = nullptr;
-        if (st.slot.page_table)
-            for (int64_t j = 0; j < ss.n_qsa; ++j)
-                if (st.slot.page_table[j]) return refuse(error, "a stage slot must use identity page tables");
         sp.slot.host = sp.slot.stage = nullptr;
         sp.k_off.assign(size_t(ss.n_qsa), 0);
         sp.v_off.assign(size_t(ss.n_qsa), 0);
