@@ -52,6 +52,8 @@ hipError_t launch_fnv1a64(const void* data, uint64_t n, uint64_t seed, const uin
 hipError_t launch_fnv1a64_mapped(const HashMapArgs& map, const uint8_t* tail, uint64_t seed, uint64_t* out,
                                  uint32_t* fault_out, void* workspace, hipStream_t stream, uint64_t expected = 0,
                                  uint32_t* verdict = nullptr, const FnvCarries& carries = {});
+hipError_t launch_hash_groups(const HashExtent* ext, uint32_t n_ext, uint64_t bytes, uint8_t* const* segs,
+                              uint32_t n_segs, uint64_t seg_bytes, HashGroup* grp, uint64_t groups, hipStream_t stream);
 
 static uint64_t host_mix64(uint64_t z) {
     z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
@@ -1553,29 +1555,19 @@ int segment_list(const sc_segments* s, uint64_t bytes, std::vector<uint8_t*>& se
     return SC_OK;
 }
 
-// Uploads a map: the extents, each workgroup's part (sc::HashGroup) and the segment table, in one device block.  A map
-// that only reads (no extents) is hashed by the plain kernel from the segment table alone, so it uploads nothing else.
+// Makes a map in one device block: the extents and the segment table uploaded, each workgroup's part (sc::HashGroup)
+// built from them on the device (hash_groups_kernel), waited for before the map is handed out.  A map that only reads
+// (no extents) is hashed by the plain kernel from the segment table alone, so it needs nothing else.
 int make_hash_map(const std::vector<sc::HashExtent>& ext, uint64_t bytes, const std::vector<uint8_t*>& segs,
                   uint64_t seg_bytes, bool store, sc_hash_map** out) {
     const sc::FnvWorkspace w = sc::fnv_workspace(bytes);
-    std::vector<sc::HashGroup> grp(store ? std::max<uint64_t>(w.groups, 1) : 1, sc::HashGroup{});
-    size_t e = 0;
-    for (uint64_t g = 0; store && g < w.groups; ++g) {
-        const uint64_t o = g * uint64_t(sc::kFnvGroupBytes), o_end = std::min(o + uint64_t(sc::kFnvGroupBytes), bytes);
-        while (e + 1 < ext.size() && ext[e].end <= o) ++e;
-        sc::HashGroup& h = grp[g];
-        const uint64_t k = o / seg_bytes;
-        h.base = reinterpret_cast<uint8_t*>(
-            reinterpret_cast<uintptr_t>(segs[size_t(std::min<uint64_t>(k, segs.size() - 1))]) - k * seg_bytes);
-        h.first = uint32_t(e);
-        h.x[0] = ext[e];
-        if (e + 1 < ext.size()) h.x[1] = ext[e + 1];
-        h.two = ext[e].end >= o_end || (e + 1 < ext.size() && ext[e + 1].end >= o_end) ? 1u : 0u;
-    }
+    const uint64_t n_grp = store ? std::max<uint64_t>(w.groups, 1) : 1;
+    if (ext.size() >= (uint64_t(1) << 32) || segs.empty())
+        return fail(SC_ERANGE, "sc_handoff: a hash map holds fewer than 2^32 extents and at least one segment");
     auto* m = new (std::nothrow) sc_hash_map();
     if (!m) return fail(SC_ENOMEM, "sc_handoff: hash map allocation failed");
     const uint64_t ext_bytes = round_up(ext.size() * sizeof(sc::HashExtent), 256);
-    const uint64_t grp_bytes = round_up(grp.size() * sizeof(sc::HashGroup), 256);
+    const uint64_t grp_bytes = round_up(n_grp * sizeof(sc::HashGroup), 256);
     hipError_t err = hipMalloc(reinterpret_cast<void**>(&m->ext_dev), ext_bytes + grp_bytes + segs.size() * 8);
     if (err != hipSuccess) {
         delete m;
@@ -1585,8 +1577,11 @@ int make_hash_map(const std::vector<sc::HashExtent>& ext, uint64_t bytes, const 
     m->grp_dev = reinterpret_cast<sc::HashGroup*>(block + ext_bytes);
     m->seg_dev = reinterpret_cast<uint8_t**>(block + ext_bytes + grp_bytes);
     if (!ext.empty()) err = hipMemcpy(m->ext_dev, ext.data(), ext.size() * sizeof(sc::HashExtent), hipMemcpyHostToDevice);
-    if (err == hipSuccess) err = hipMemcpy(m->grp_dev, grp.data(), grp.size() * sizeof(sc::HashGroup), hipMemcpyHostToDevice);
     if (err == hipSuccess) err = hipMemcpy(m->seg_dev, segs.data(), segs.size() * 8, hipMemcpyHostToDevice);
+    if (err == hipSuccess && store && !ext.empty())
+        err = sc::launch_hash_groups(m->ext_dev, uint32_t(ext.size()), bytes, m->seg_dev, uint32_t(segs.size()),
+                                     seg_bytes, m->grp_dev, w.groups, nullptr);
+    if (err == hipSuccess) err = hipStreamSynchronize(nullptr);
     if (err != hipSuccess) {
         (void) hipFree(m->ext_dev);
         delete m;

@@ -940,6 +940,40 @@ hipError_t launch_fnv1a64(const void* data, uint64_t n, uint64_t seed, const uin
     return hipGetLastError();
 }
 
+// Each hash workgroup's part of a map (HashGroup), one thread per workgroup: the extent holding the workgroup's first
+// byte (extents tile [0, bytes) in order, so the first whose end lies past it), that extent and the next, whether the
+// workgroup's bytes lie in those two, and where its segment puts payload byte 0.  Built on the device so that a map's
+// creation uploads its extents only (the parts are 128 bytes per 64 KiB: 6.4 MB for a 3.3 GB payload).
+__global__ void hash_groups_kernel(const HashExtent* ext, uint32_t n_ext, uint64_t bytes, uint8_t* const* segs,
+                                   uint32_t n_segs, uint64_t seg_bytes, HashGroup* grp, uint64_t groups) {
+    const uint64_t g = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (g >= groups) return;
+    const uint64_t o = g * uint64_t(kFnvGroupBytes), o_end = o + kFnvGroupBytes < bytes ? o + kFnvGroupBytes : bytes;
+    uint32_t lo = 0, hi = n_ext - 1;   // the first extent whose end lies past o (the last one at most)
+    while (lo < hi) {
+        const uint32_t mid = lo + (hi - lo) / 2;
+        if (ext[mid].end > o) hi = mid;
+        else lo = mid + 1;
+    }
+    HashGroup h{};
+    const uint64_t k = o / seg_bytes;
+    h.base = reinterpret_cast<uint8_t*>(reinterpret_cast<uintptr_t>(segs[k < n_segs ? k : n_segs - 1]) - k * seg_bytes);
+    h.first = lo;
+    h.x[0] = ext[lo];
+    if (lo + 1 < n_ext) h.x[1] = ext[lo + 1];
+    h.two = ext[lo].end >= o_end || (lo + 1 < n_ext && ext[lo + 1].end >= o_end) ? 1u : 0u;
+    grp[g] = h;
+}
+
+hipError_t launch_hash_groups(const HashExtent* ext, uint32_t n_ext, uint64_t bytes, uint8_t* const* segs,
+                              uint32_t n_segs, uint64_t seg_bytes, HashGroup* grp, uint64_t groups, hipStream_t stream) {
+    if (!groups) return hipSuccess;
+    if (!n_ext || !n_segs || !seg_bytes) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(hash_groups_kernel, dim3(unsigned((groups + 255) / 256)), dim3(256), 0, stream, ext, n_ext, bytes,
+                       segs, n_segs, seg_bytes, grp, groups);
+    return hipGetLastError();
+}
+
 // The gather fused with the hash: the payload's `map.n_total` bytes gathered into its segments and hashed, the whole
 // lane segments in the one-pass kernel and the last partial one (under 256 bytes, at `tail`) by the closing kernel,
 // which runs after every byte is in place.  With `verdict`, the closing kernel also leaves the check of the hash
