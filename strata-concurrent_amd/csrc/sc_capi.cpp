@@ -38,6 +38,8 @@ hipError_t launch_fill_uniform_f32(float* dst, uint64_t n, float lo, float hi, u
 hipError_t launch_fill_normal_f32(float* dst, uint64_t n, uint64_t seed, uint64_t sid, hipStream_t stream);
 hipError_t launch_fill_bytes(void* dst, uint8_t value, uint64_t n, hipStream_t stream);
 hipError_t launch_copy_bytes(void* dst, const void* src, uint64_t n, hipStream_t stream);
+hipError_t launch_tile_rows(const MoveRow* rows, uint32_t n_rows, uint16_t* tile_row, uint64_t n_entries, uint64_t tiles,
+                            hipStream_t stream);
 hipError_t launch_decode_probe(const void* kv, uint64_t n_bytes, uint32_t* sink, int64_t workgroups,
                                hipStream_t stream);
 hipError_t launch_batch(const BatchArgs& args, const OrderGroup* arena, uint32_t arena_blocks, int64_t grid,
@@ -407,12 +409,9 @@ int finish_plan(std::vector<sc::MoveRow>& rows, const Geo& g, uint64_t payload, 
         *out = p;
         return ok();
     }
-    // padded to an even count: the kernel reads the entries a 4-byte word (two entries) at a time
-    std::vector<uint16_t> tile_row(tiles + (tiles & 1), uint16_t(rows.size() - 1));
-    for (size_t k = 0; k < rows.size(); ++k) {
-        const uint64_t end = k + 1 < rows.size() ? rows[k + 1].tile0 : tiles;
-        std::fill(tile_row.begin() + int64_t(rows[k].tile0), tile_row.begin() + int64_t(end), uint16_t(k));
-    }
+    // padded to an even count: the kernel reads the entries a 4-byte word (two entries) at a time; the table is built
+    // on the device from the rows (tile_rows_kernel)
+    const uint64_t n_entries = tiles + (tiles & 1);
     if (const int rc = order_workspace(order, rows, p)) {
         if (p->order_ws) (void) hipFree(p->order_ws);
         delete p;
@@ -420,7 +419,7 @@ int finish_plan(std::vector<sc::MoveRow>& rows, const Geo& g, uint64_t payload, 
     }
     hipError_t e = hipMalloc(reinterpret_cast<void**>(&p->rows_dev), rows.size() * sizeof(sc::MoveRow));
     if (e == hipSuccess)
-        e = hipMalloc(reinterpret_cast<void**>(&p->tile_row_dev), tile_row.size() * sizeof(uint16_t));
+        e = hipMalloc(reinterpret_cast<void**>(&p->tile_row_dev), n_entries * sizeof(uint16_t));
     if (e != hipSuccess) {
         if (p->rows_dev) (void) hipFree(p->rows_dev);
         if (p->order_ws) (void) hipFree(p->order_ws);
@@ -429,7 +428,8 @@ int finish_plan(std::vector<sc::MoveRow>& rows, const Geo& g, uint64_t payload, 
     }
     e = hipMemcpy(p->rows_dev, rows.data(), rows.size() * sizeof(sc::MoveRow), hipMemcpyHostToDevice);
     if (e == hipSuccess)
-        e = hipMemcpy(p->tile_row_dev, tile_row.data(), tile_row.size() * sizeof(uint16_t), hipMemcpyHostToDevice);
+        e = sc::launch_tile_rows(p->rows_dev, uint32_t(rows.size()), p->tile_row_dev, n_entries, tiles, nullptr);
+    if (e == hipSuccess) e = hipStreamSynchronize(nullptr);
     if (e != hipSuccess) {
         (void) hipFree(p->rows_dev);
         (void) hipFree(p->tile_row_dev);

@@ -1243,6 +1243,38 @@ hipError_t launch_fill_normal_f32(float* dst, uint64_t n, uint64_t seed, uint64_
     return hipGetLastError();
 }
 
+// A plan's tile -> row table, one thread per entry: the last row whose first tile is at or before the entry (rows are in
+// tile order, and a row that moves nothing shares its first tile with the next, so the row that owns the tile is the
+// last of them); the padding entry past the last tile names the last row.  Built on the device from the uploaded rows
+// so that a plan's creation uploads its rows only (the table is 2 bytes per 8 KiB tile: 806 KB for the 128K slot,
+// whose upload from pageable memory took 0.35 ms).
+__global__ void tile_rows_kernel(const MoveRow* rows, uint32_t n_rows, uint16_t* tile_row, uint64_t n_entries,
+                                 uint64_t tiles) {
+    const uint64_t t = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (t >= n_entries) return;
+    uint32_t k = n_rows - 1;
+    if (t < tiles) {
+        uint32_t lo = 0, hi = n_rows - 1;   // the last row with tile0 <= t
+        while (lo < hi) {
+            const uint32_t mid = lo + (hi - lo + 1) / 2;
+            if (rows[mid].tile0 <= t) lo = mid;
+            else hi = mid - 1;
+        }
+        k = lo;
+    }
+    tile_row[t] = uint16_t(k);
+}
+
+hipError_t launch_tile_rows(const MoveRow* rows, uint32_t n_rows, uint16_t* tile_row, uint64_t n_entries, uint64_t tiles,
+                            hipStream_t stream) {
+    if (!n_entries) return hipSuccess;
+    if (!n_rows) return hipErrorInvalidValue;
+    const uint64_t blocks = (n_entries + 255) / 256;
+    hipLaunchKernelGGL(tile_rows_kernel, dim3(unsigned(blocks)), dim3(256), 0, stream, rows, n_rows, tile_row, n_entries,
+                       tiles);
+    return hipGetLastError();
+}
+
 hipError_t launch_fill_bytes(void* dst, uint8_t value, uint64_t n, hipStream_t stream) {
     if (!n) return hipSuccess;
     hipLaunchKernelGGL(fill_bytes_kernel, dim3(fill_grid(n / 16 + 16)), dim3(256), 0, stream,
