@@ -543,6 +543,9 @@ void WireDeviceDecoder::release() {
     if (hash_dev_) sc_device_free(hash_dev_);
     if (hash_host_) sc_host_free(hash_host_);
     if (staged_) sc_host_free(staged_);
+    if (head_pinned_) sc_host_free(head_pinned_);
+    head_pinned_ = nullptr;
+    head_cap_ = 0;
     if (ev_start_) sc_event_destroy(ev_start_);
     if (ev_done_) sc_event_destroy(ev_done_);
     if (side_) sc_stream_destroy(side_);
@@ -586,20 +589,34 @@ bool WireDeviceDecoder::read_head(const void* payload, const sc_segments* segs, 
     if (!payload || bytes < kWireHeaderRecordBytes) return refuse(error, "the payload is shorter than the header record");
     // the payload may still be arriving on another stream: everything enqueued before this call completes first
     if (!abi(sc_device_sync(), error, "wait for the payload")) return false;
-    std::vector<uint8_t> head(kWireHeaderRecordBytes);
-    if (!copy_payload(head.data(), 0, head.size(), nullptr, error) || !abi(sc_device_sync(), error, "head read"))
+    // the head is read into pinned memory kept across opens (plain DMA, no bounce copies)
+    auto head_room = [&](uint64_t need) {
+        if (head_cap_ >= need) return true;
+        if (head_pinned_) sc_host_free(head_pinned_);
+        head_pinned_ = nullptr;
+        head_cap_ = 0;
+        const uint64_t cap = std::max<uint64_t>(need, uint64_t(1) << 20);
+        if (!abi(sc_host_alloc(reinterpret_cast<void**>(&head_pinned_), cap), error, "head staging")) return false;
+        head_cap_ = cap;
+        return true;
+    };
+    if (!head_room(kWireHeaderRecordBytes)) return false;
+    if (!copy_payload(head_pinned_, 0, kWireHeaderRecordBytes, nullptr, error) ||
+        !abi(sc_device_sync(), error, "head read"))
         return false;
     WireHeaderRecord h{};
-    if (!conversation_wire_peek(head.data(), head.size(), h, error)) return false;
+    if (!conversation_wire_peek(head_pinned_, kWireHeaderRecordBytes, h, error)) return false;
     if (h.blob_pool_off > bytes) return refuse(error, "the blob pool starts past the end of the buffer");
-    head.resize(size_t(h.blob_pool_off));
-    if (!copy_payload(head.data(), 0, head.size(), nullptr, error) || !abi(sc_device_sync(), error, "head read"))
+    if (!head_room(h.blob_pool_off)) return false;
+    if (!copy_payload(head_pinned_, 0, h.blob_pool_off, nullptr, error) || !abi(sc_device_sync(), error, "head read"))
         return false;
+    const uint8_t* head_bytes = head_pinned_;
+    const uint64_t head_len = h.blob_pool_off;
     // every check of the host decoder, against the real buffer size
     WireExpect bounded = expect;
     if (!bounded.max_payload_bytes || bounded.max_payload_bytes > bytes) bounded.max_payload_bytes = bytes;
     head_image_ = SavedConversation{};
-    if (!detail::wire_locate(head.data(), head.size(), head_image_, info_, bounded, blobs, error)) return false;
+    if (!detail::wire_locate(head_bytes, head_len, head_image_, info_, bounded, blobs, error)) return false;
     tokens_ = info_.live_tokens;
     return true;
 }
