@@ -103,6 +103,8 @@ public:
     void set_carry(uint8_t* carry) { carry_ = carry; }
 
 private:
+    void settle();
+    bool mark_launched(void* stream, std::string& error);
     void release();
     bool stage(const SavedConversation& img, const std::vector<std::pair<const void*, uint64_t>>& sizes,
                const std::vector<const void*>& device, const WireIdentity& identity,
@@ -146,6 +148,8 @@ private:
     // and the launch's fault word right after it (1: a wait ran out and the hash is not valid)
     uint32_t* hash_fault_host() { return reinterpret_cast<uint32_t*>(hash_host_ + 1); }
     void* last_stream_ = nullptr;
+    void* done_ = nullptr;     // hipEvent_t recorded after each encode's launches; settle() waits on it before the
+    bool launched_ = false;    // plans, maps or buffers those launches read are destroyed
     sc_plan* capture_ = nullptr;
     sc_hash_map* hash_map_ = nullptr;  // the capture plans' rows fused with the payload hash (one read of the slot)
     void* capture_target_ = nullptr;   // the payload the capture plan was built for

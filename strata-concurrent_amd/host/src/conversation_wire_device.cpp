@@ -128,7 +128,26 @@ const detail::WireBlobAt* find(const std::vector<detail::WireBlobAt>& pool, cons
 
 WireDeviceEncoder::~WireDeviceEncoder() { release(); }
 
+// Waits for the last encode's launches, before anything they read is destroyed (a freed plan or map must not be in use:
+// the library does not rely on the runtime's free waiting for the device).
+void WireDeviceEncoder::settle() {
+    if (launched_ && done_) (void) sc_event_sync(done_);
+    launched_ = false;
+}
+
+// Records the encoder's event after an encode's launches (what settle() waits for).
+bool WireDeviceEncoder::mark_launched(void* stream, std::string& error) {
+    if (!done_ && !abi(sc_event_create(&done_), error, "encode event")) return false;
+    if (!abi(sc_event_record(done_, stream), error, "encode event")) return false;
+    launched_ = true;
+    return true;
+}
+
 void WireDeviceEncoder::release() {
+    settle();
+    last_stream_ = nullptr;
+    if (done_) sc_event_destroy(done_);
+    done_ = nullptr;
     for (StagePlan& sp : stage_plans_)
         if (sp.plan) sc_plan_destroy(sp.plan);
     stage_plans_.clear();
@@ -367,6 +386,7 @@ bool WireDeviceEncoder::encode(void* payload, uint64_t capacity, void* stream, s
         return refuse(error, "the payload buffer holds " + std::to_string(capacity) + " bytes and the payload needs " +
                                  std::to_string(plan_.total_bytes));
     if (capture_target_ != payload) {
+        settle();
         if (capture_) sc_plan_destroy(capture_);
         capture_ = nullptr;
         if (copies_) sc_plan_destroy(copies_);
@@ -420,7 +440,7 @@ bool WireDeviceEncoder::encode(void* payload, uint64_t capacity, void* stream, s
             return false;
     }
     last_stream_ = stream;
-    return true;
+    return mark_launched(stream, error);
 }
 
 bool WireDeviceEncoder::capture_plans(void* base, uint64_t capacity, std::vector<sc_plan*>& plans, std::string& error) {
@@ -472,6 +492,7 @@ bool WireDeviceEncoder::encode_segments(const sc_segments& into, void* stream, s
     if (into.n < 1 || !into.ptr || !into.segment_bytes) return refuse(error, "a segmented payload needs its segments");
     std::vector<void*> ptrs(into.ptr, into.ptr + into.n);
     if (!seg_map_ || ptrs != seg_target_ || into.segment_bytes != seg_bytes_) {
+        settle();
         if (seg_map_) sc_hash_map_destroy(seg_map_);
         seg_map_ = nullptr;
         seg_target_.clear();
@@ -487,16 +508,17 @@ bool WireDeviceEncoder::encode_segments(const sc_segments& into, void* stream, s
         seg_bytes_ = into.segment_bytes;
     }
     // the head and the small host blobs (when the map does not write them), a piece per segment they touch
-    for (const Upload& u : staged_rows_ ? std::vector<Upload>{} : uploads_)
-        for (uint64_t o = u.offset, end = u.offset + u.bytes; o < end;) {
-            const uint64_t k = o / seg_bytes_, stop = std::min(end, (k + 1) * seg_bytes_);
-            if (k >= ptrs.size()) return refuse(error, "the segments are smaller than the payload");
-            if (!abi(sc_copy_async(static_cast<uint8_t*>(ptrs[size_t(k)]) + (o - k * seg_bytes_),
-                                   staged_ + u.staged_at + (o - u.offset), stop - o, stream),
-                     error, "head copy"))
-                return false;
-            o = stop;
-        }
+    if (!staged_rows_)
+        for (const Upload& u : uploads_)
+            for (uint64_t o = u.offset, end = u.offset + u.bytes; o < end;) {
+                const uint64_t k = o / seg_bytes_, stop = std::min(end, (k + 1) * seg_bytes_);
+                if (k >= ptrs.size()) return refuse(error, "the segments are smaller than the payload");
+                if (!abi(sc_copy_async(static_cast<uint8_t*>(ptrs[size_t(k)]) + (o - k * seg_bytes_),
+                                       staged_ + u.staged_at + (o - u.offset), stop - o, stream),
+                         error, "head copy"))
+                    return false;
+                o = stop;
+            }
     if (!abi(carry_ ? sc_hash_map_launch_carry(seg_map_, kWireHashSeed, hash_host_, hash_fault_host(), carry_, hash_ws_,
                                                hash_ws_bytes_, stream)
                     : sc_hash_map_launch(seg_map_, kWireHashSeed, hash_host_, hash_fault_host(), hash_ws_,
@@ -504,7 +526,7 @@ bool WireDeviceEncoder::encode_segments(const sc_segments& into, void* stream, s
              error, "payload gather and hash"))
         return false;
     last_stream_ = stream;
-    return true;
+    return mark_launched(stream, error);
 }
 
 bool WireDeviceEncoder::payload_hash(uint64_t& hash, std::string& error) {
