@@ -177,6 +177,36 @@ def test_map_extent_boundaries_at_wave_and_workgroup_edges(sc, oracle, cuda):
     payload.free()
 
 
+def test_fused_map_with_large_zero_ranges(sc, oracle, cuda):
+    """Zero ranges of a capture plan large enough to hold whole waves and workgroups (the uniform gather's zero
+    extents, which write zeros without a load), one starting mid-workgroup and one across a workgroup's end, between a
+    slot's blobs and after them: the map writes the zeros and the blobs the plan writes, with the byte loop's hash."""
+    geo = sc.geometry(**SMALL)
+    fmt, index, tokens = 1, True, 77
+    pools = sc.LayerPools(geo, fmt, 96, index)
+    pools.randomize(0x5E)
+    sizes = sc.layer_blob_bytes(geo, fmt, index, tokens)
+    G = 64 << 10
+    at, offsets, zero = 896, [], []
+    for j in range(geo.n_qsa):
+        for b in range(5):
+            offsets.append(at if sizes[b] else None)
+            at += (sizes[b] + 63) // 64 * 64
+        if j == 0:   # a zero range from inside a workgroup across its end and the whole next one
+            zero += [at, 2 * G + 4096]
+            at += 2 * G + 4096
+    offsets.append(at)
+    at += (geo.n_gdn * geo.gdn_row_floats * 4 + 63) // 64 * 64
+    zero += [at, 3 * G + 48 * 16]   # after the blobs: three whole workgroups and a ragged end
+    total = at + 3 * G + 48 * 16 + 64
+    payload = sc.DeviceBuffer(total, "uint8")
+    plan = sc.plan_capture_layers(geo, pools, tokens, payload.ptr, total, offsets=offsets, zero=zero)
+    head = np.random.default_rng(3).integers(0, 256, size=896, dtype=np.uint8)
+    _compare(sc, oracle, [plan], payload, total, 0xD7, head=head)
+    plan.destroy()
+    payload.free()
+
+
 @pytest.mark.parametrize("fmt", [1, 2, 3])
 @pytest.mark.parametrize("index", [False, True])
 @pytest.mark.parametrize("tokens", [1, 77])
