@@ -77,16 +77,17 @@ int sc_wire_encoder_create_layers(const sc_geometry* g, const sc_slot_layers* sl
 /* The payload's total size (WirePlan::total_bytes) and where its blob pool starts. */
 uint64_t sc_wire_encoder_bytes(const sc_wire_encoder* e);
 uint64_t sc_wire_encoder_pool_offset(const sc_wire_encoder* e);
-/* Enqueues the encode on `stream` into 16-byte aligned device memory `payload`: the head copied in, then one kernel
- * that gathers the pool's blobs from the slot and hashes the whole payload as it writes it (sc_hash_map_launch: the
- * slot is read once and the payload never re-read).  With `gathered` (a hipEvent_t) the gather runs first on its own,
+/* Enqueues the encode on `stream` into 16-byte aligned device memory `payload`: one kernel that gathers the pool's
+ * blobs from the slot, and the head and small host blobs from their device copy (staged once by
+ * sc_wire_encoder_create), and hashes the whole payload as it writes it (sc_hash_map_launch: the slot is read once and
+ * the payload never re-read).  With `gathered` (a hipEvent_t) the gather runs first on its own,
  * the event is recorded when every payload byte is in place, then the hash: a park on another stream can wait on the
  * event and overlap the hash.  Replaces conversation_wire_encode's walk and byte-serial hash
  * (src/core/conversation_wire.cpp:400-480, 1006-1025). */
 int sc_wire_encode_async(sc_wire_encoder* e, void* payload, uint64_t capacity, void* stream, void* gathered);
 /* The encode into a payload held in segments (`into`, sc_handoff.h: the same-GPU hand-off's exported segments, each at
- * most SC_IPC_MAX_SEGMENT bytes, segment_bytes a multiple of 64 KiB): the head and small blobs copied into their
- * segments and the blobs gathered into them by the fused gather + hash, cut wherever a segment ends.  The bytes are
+ * most SC_IPC_MAX_SEGMENT bytes, segment_bytes a multiple of 64 KiB): the head, the small blobs and the slot's blobs
+ * written into them by the fused gather + hash, cut wherever a segment ends.  The bytes are
  * exactly sc_wire_encode_async's, and no contiguous copy of the payload exists at any point. */
 int sc_wire_encode_segments_async(sc_wire_encoder* e, const sc_segments* into, void* stream);
 /* The payload hash of the last encode (waits for it): WireEncoded::payload_hash.  SC_ETIMEOUT, and no hash, when the

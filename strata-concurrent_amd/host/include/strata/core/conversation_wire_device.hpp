@@ -91,9 +91,8 @@ public:
     /// is computed.
     bool encode(void* payload, uint64_t capacity, void* stream, std::string& error, void* gathered = nullptr);
     /// Enqueues the encode into a segmented payload (`into`: the same-GPU hand-off's exported segments, byte o at
-    /// into.ptr[o / segment_bytes] + o % segment_bytes, segment_bytes a multiple of 64 KiB): the head and small blobs
-    /// copied into their segments, then the gather fused with the hash writing every blob into its segments, cut
-    /// wherever a segment ends.  The payload bytes are exactly encode()'s; nothing is staged in between.
+    /// into.ptr[o / segment_bytes] + o % segment_bytes, segment_bytes a multiple of 64 KiB): the gather fused with the
+    /// hash writing the head, the small blobs and every slot blob into its segments, cut wherever a segment ends.  The payload bytes are exactly encode()'s; nothing is staged in between.
     bool encode_segments(const sc_segments& into, void* stream, std::string& error);
     /// The payload hash of the last encode; waits for it.
     bool payload_hash(uint64_t& hash, std::string& error);
